@@ -1,0 +1,174 @@
+"""ctypes front end of libckks_hip.so (the C ABI in include/ckks_engine.h).
+
+This is the Python side of the drop-in boundary: plain pointers and sizes go through; device memory
+is either allocated through the ABI (DeviceBuffer) or comes from torch tensors (data_ptr()).
+There is no CPU fallback: if the library is missing, loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libckks_hip.so")
+
+CKKS_OK = 0
+
+_vp = ctypes.c_void_p
+_u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
+_int = ctypes.c_int
+
+
+class Params(ctypes.Structure):
+    _fields_ = [("log_n", _u32), ("num_q", _u32), ("num_p", _u32), ("dnum", _u32),
+                ("q_bits", _u32), ("p_bits", _u32), ("scale", ctypes.c_double), ("device", _int)]
+
+
+# name -> (restype, argtypes); the exported C ABI (kept in step with include/ckks_engine.h)
+SIGNATURES = {
+    "ckks_last_error": (ctypes.c_char_p, []),
+    "ckks_context_create": (_int, [ctypes.POINTER(Params), ctypes.POINTER(_vp)]),
+    "ckks_context_create_from_moduli": (_int, [_u32, _vp, _u32, _vp, _u32, _u32, ctypes.c_double, _int,
+                                               ctypes.POINTER(_vp)]),
+    "ckks_context_destroy": (None, [_vp]),
+    "ckks_context_info": (_int, [_vp, _vp, _vp, _vp, _vp]),
+    "ckks_context_moduli": (_int, [_vp, _vp, _u32]),
+    "ckks_context_roots": (_int, [_vp, _vp, _u32]),
+    "ckks_set_ntt_mode": (_int, [_vp, _int]),
+    "ckks_buffer_alloc": (_int, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "ckks_buffer_free": (_int, [_vp]),
+    "ckks_memcpy_h2d": (_int, [_vp, _vp, ctypes.c_size_t]),
+    "ckks_memcpy_d2h": (_int, [_vp, _vp, ctypes.c_size_t]),
+    "ckks_device_sync": (_int, []),
+    "ckks_ntt_forward": (_int, [_vp, _vp, _u32, _u32, _vp, _vp]),
+    "ckks_ntt_inverse": (_int, [_vp, _vp, _u32, _u32, _vp, _vp]),
+}
+
+
+class CkksError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """Load the engine library (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(path):
+            raise CkksError(f"{path} is missing: build it with __graft_entry__.build() (make -C fhe-ssm_amd)")
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(lib, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != CKKS_OK:
+        raise CkksError(f"ckks error {rc}: {load().ckks_last_error().decode()}")
+
+
+def _ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_vp)
+
+
+class DeviceBuffer:
+    """A device allocation made through the ABI."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = _vp()
+        check(load().ckks_buffer_alloc(self.nbytes, ctypes.byref(p)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        check(load().ckks_memcpy_h2d(self.ptr, _ptr(a), a.nbytes))
+
+    def download(self, shape, dtype=np.uint64) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert out.nbytes <= self.nbytes
+        check(load().ckks_memcpy_d2h(_ptr(out), self.ptr, out.nbytes))
+        return out
+
+    def free(self) -> None:
+        if self.ptr:
+            check(load().ckks_buffer_free(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def sync() -> None:
+    check(load().ckks_device_sync())
+
+
+class Context:
+    """Engine context (moduli, NTT tables and key-switch constants resident on the device)."""
+
+    def __init__(self, num_q: int = 24, num_p: int = 8, dnum: int = 3, q_bits: int = 54, p_bits: int = 60,
+                 scale: float = 2.0**50, device: int = 0, log_n: int = 16, moduli=None):
+        lib = load()
+        h = _vp()
+        if moduli is None:
+            p = Params(log_n, num_q, num_p, dnum, q_bits, p_bits, scale, device)
+            check(lib.ckks_context_create(ctypes.byref(p), ctypes.byref(h)))
+        else:
+            q = np.ascontiguousarray(np.asarray(moduli[:num_q], dtype=np.uint64))
+            pp = np.ascontiguousarray(np.asarray(list(moduli[num_q:num_q + num_p]) or [0], dtype=np.uint64))
+            check(lib.ckks_context_create_from_moduli(log_n, _ptr(q), num_q, _ptr(pp), num_p, dnum, scale, device,
+                                                      ctypes.byref(h)))
+        self.h = h.value
+        n, L, K, D = _u32(), _u32(), _u32(), _u32()
+        check(lib.ckks_context_info(self.h, ctypes.byref(n), ctypes.byref(L), ctypes.byref(K), ctypes.byref(D)))
+        self.N, self.L, self.K, self.dnum = n.value, L.value, K.value, D.value
+        self.scale = scale
+        m = np.zeros(self.L + self.K, dtype=np.uint64)
+        check(lib.ckks_context_moduli(self.h, _ptr(m), len(m)))
+        self.moduli = [int(x) for x in m]
+        r = np.zeros(self.L + self.K, dtype=np.uint64)
+        check(lib.ckks_context_roots(self.h, _ptr(r), len(r)))
+        self.roots = [int(x) for x in r]
+
+    def close(self) -> None:
+        if self.h:
+            load().ckks_context_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_ntt_mode(self, mode: int) -> None:
+        check(load().ckks_set_ntt_mode(self.h, mode))
+
+    # raw stages on device pointers -------------------------------------------------------------
+    def ntt_forward(self, d_ptr: int, n_polys: int, prime_idx, stream=None) -> None:
+        pi = np.ascontiguousarray(np.asarray(prime_idx, dtype=np.uint32))
+        check(load().ckks_ntt_forward(self.h, d_ptr, n_polys, len(pi), _ptr(pi), stream))
+
+    def ntt_inverse(self, d_ptr: int, n_polys: int, prime_idx, stream=None) -> None:
+        pi = np.ascontiguousarray(np.asarray(prime_idx, dtype=np.uint32))
+        check(load().ckks_ntt_inverse(self.h, d_ptr, n_polys, len(pi), _ptr(pi), stream))

@@ -1,0 +1,198 @@
+// abi.cpp -- the extern "C" entry points declared in include/ckks_engine.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <string>
+
+#include "ckks_engine.h"
+#include "engine.hpp"
+
+namespace fhe {
+std::vector<uint64_t> ntt_primes(uint32_t bits, uint32_t count, uint64_t m, const std::vector<uint64_t>& skip);
+void context_init(Context& c, const std::vector<uint64_t>& q, const std::vector<uint64_t>& p, uint32_t dnum,
+                  double scale, int device);
+void context_release(Context& c);
+}  // namespace fhe
+
+struct ckks_context {
+    fhe::Context c;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(CKKS_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr)                                \
+    do {                                             \
+        hipError_t _e = (expr);                      \
+        if (_e != hipSuccess) return hip_fail(_e, #expr); \
+    } while (0)
+
+template <class F>
+int guarded(F&& f) {
+    try {
+        return f();
+    } catch (const std::invalid_argument& e) {
+        return fail(CKKS_EINVAL, e.what());
+    } catch (const std::bad_alloc&) {
+        return fail(CKKS_ENOMEM, "host allocation failed");
+    } catch (const std::exception& e) {
+        return fail(CKKS_EHIP, e.what());
+    }
+}
+
+int check_limbs(const ckks_context* ctx, uint32_t n_limbs, const uint32_t* prime_idx) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    if (n_limbs == 0 || n_limbs > fhe::kMaxPmap) return fail(CKKS_EINVAL, "n_limbs must be in [1, 96]");
+    if (!prime_idx) return fail(CKKS_EINVAL, "null prime_idx");
+    for (uint32_t i = 0; i < n_limbs; i++)
+        if (prime_idx[i] >= ctx->c.L + ctx->c.K) return fail(CKKS_EINVAL, "prime index out of range");
+    return CKKS_OK;
+}
+
+int ntt_entry(ckks_context* ctx, uint64_t* d, uint32_t n_polys, uint32_t n_limbs, const uint32_t* prime_idx,
+              void* stream, bool inverse) {
+    if (int rc = check_limbs(ctx, n_limbs, prime_idx)) return rc;
+    if (!d) return fail(CKKS_EINVAL, "null data");
+    if (n_polys == 0) return CKKS_OK;
+    const uint64_t jobs = (uint64_t)n_polys * n_limbs;
+    if (jobs > 0x7fffffffull) return fail(CKKS_EINVAL, "too many limbs");
+    fhe::JobSpec js{};
+    js.jobs = nullptr;
+    js.n_polys = n_polys;
+    js.period = n_limbs;
+    for (uint32_t i = 0; i < n_limbs; i++) js.pmap[i] = (uint8_t)prime_idx[i];
+    HIP_TRY(fhe::launch_ntt(ctx->c, d, js, (uint32_t)jobs, inverse, ctx->c.ntt_mode, (hipStream_t)stream));
+    return CKKS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* ckks_last_error(void) { return g_err.c_str(); }
+
+int ckks_context_create(const ckks_params* p, ckks_context** out) {
+    if (!p || !out) return fail(CKKS_EINVAL, "null argument");
+    if (p->log_n != fhe::kLogN) return fail(CKKS_ENOTSUP, "this build supports log_n = 16 only");
+    if (p->q_bits < 20 || p->q_bits > 61 || p->p_bits < 20 || p->p_bits > 61)
+        return fail(CKKS_EINVAL, "prime sizes must be in [20, 61] bits");
+    return guarded([&] {
+        const uint64_t m = 2ull * fhe::kN;
+        auto q = fhe::ntt_primes(p->q_bits, p->num_q, m, {});
+        auto pp = fhe::ntt_primes(p->p_bits, p->num_p, m, q);
+        auto* ctx = new ckks_context();
+        try {
+            fhe::context_init(ctx->c, q, pp, p->dnum, p->scale, p->device);
+        } catch (...) {
+            fhe::context_release(ctx->c);
+            delete ctx;
+            throw;
+        }
+        *out = ctx;
+        return CKKS_OK;
+    });
+}
+
+int ckks_context_create_from_moduli(uint32_t log_n, const uint64_t* q, uint32_t num_q, const uint64_t* p,
+                                    uint32_t num_p, uint32_t dnum, double scale, int device, ckks_context** out) {
+    if (!out || !q || (num_p && !p)) return fail(CKKS_EINVAL, "null argument");
+    if (log_n != fhe::kLogN) return fail(CKKS_ENOTSUP, "this build supports log_n = 16 only");
+    return guarded([&] {
+        auto* ctx = new ckks_context();
+        try {
+            fhe::context_init(ctx->c, std::vector<uint64_t>(q, q + num_q), std::vector<uint64_t>(p, p + num_p), dnum,
+                              scale, device);
+        } catch (...) {
+            fhe::context_release(ctx->c);
+            delete ctx;
+            throw;
+        }
+        *out = ctx;
+        return CKKS_OK;
+    });
+}
+
+void ckks_context_destroy(ckks_context* ctx) {
+    if (!ctx) return;
+    fhe::context_release(ctx->c);
+    delete ctx;
+}
+
+int ckks_context_info(const ckks_context* ctx, uint32_t* n, uint32_t* num_q, uint32_t* num_p, uint32_t* dnum) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    if (n) *n = fhe::kN;
+    if (num_q) *num_q = ctx->c.L;
+    if (num_p) *num_p = ctx->c.K;
+    if (dnum) *dnum = ctx->c.dnum;
+    return CKKS_OK;
+}
+
+int ckks_context_moduli(const ckks_context* ctx, uint64_t* out, uint32_t cap) {
+    if (!ctx || !out) return fail(CKKS_EINVAL, "null argument");
+    if (cap < ctx->c.moduli.size()) return fail(CKKS_EINVAL, "buffer too small");
+    std::memcpy(out, ctx->c.moduli.data(), ctx->c.moduli.size() * 8);
+    return CKKS_OK;
+}
+
+int ckks_context_roots(const ckks_context* ctx, uint64_t* out, uint32_t cap) {
+    if (!ctx || !out) return fail(CKKS_EINVAL, "null argument");
+    if (cap < ctx->c.psi.size()) return fail(CKKS_EINVAL, "buffer too small");
+    std::memcpy(out, ctx->c.psi.data(), ctx->c.psi.size() * 8);
+    return CKKS_OK;
+}
+
+int ckks_set_ntt_mode(ckks_context* ctx, int mode) {
+    if (!ctx || (mode != 0 && mode != 1)) return fail(CKKS_EINVAL, "mode must be 0 or 1");
+    ctx->c.ntt_mode = mode ? fhe::NttMode::Fused : fhe::NttMode::TwoPass;
+    return CKKS_OK;
+}
+
+int ckks_buffer_alloc(size_t bytes, void** d_out) {
+    if (!d_out) return fail(CKKS_EINVAL, "null argument");
+    HIP_TRY(hipMalloc(d_out, bytes ? bytes : 1));
+    return CKKS_OK;
+}
+
+int ckks_buffer_free(void* d) {
+    HIP_TRY(hipFree(d));
+    return CKKS_OK;
+}
+
+int ckks_memcpy_h2d(void* d_dst, const void* h_src, size_t bytes) {
+    HIP_TRY(hipMemcpy(d_dst, h_src, bytes, hipMemcpyHostToDevice));
+    return CKKS_OK;
+}
+
+int ckks_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes) {
+    HIP_TRY(hipMemcpy(h_dst, d_src, bytes, hipMemcpyDeviceToHost));
+    return CKKS_OK;
+}
+
+int ckks_device_sync(void) {
+    HIP_TRY(hipDeviceSynchronize());
+    return CKKS_OK;
+}
+
+int ckks_ntt_forward(ckks_context* ctx, uint64_t* d_data, uint32_t n_polys, uint32_t n_limbs,
+                     const uint32_t* prime_idx, void* stream) {
+    return ntt_entry(ctx, d_data, n_polys, n_limbs, prime_idx, stream, false);
+}
+
+int ckks_ntt_inverse(ckks_context* ctx, uint64_t* d_data, uint32_t n_polys, uint32_t n_limbs,
+                     const uint32_t* prime_idx, void* stream) {
+    return ntt_entry(ctx, d_data, n_polys, n_limbs, prime_idx, stream, true);
+}
+
+}  // extern "C"

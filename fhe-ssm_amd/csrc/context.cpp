@@ -1,0 +1,163 @@
+// context.cpp -- parameter generation (prime chain, roots, NTT tables) and device upload.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "ckks_engine.h"
+#include "engine.hpp"
+
+namespace fhe {
+
+using u128 = unsigned __int128;
+
+uint64_t mulmod_h(uint64_t a, uint64_t b, uint64_t q) { return (uint64_t)((u128)a * b % q); }
+
+uint64_t powmod_h(uint64_t a, uint64_t e, uint64_t q) {
+    uint64_t r = 1 % q;
+    a %= q;
+    for (; e; e >>= 1) {
+        if (e & 1) r = mulmod_h(r, a, q);
+        a = mulmod_h(a, a, q);
+    }
+    return r;
+}
+
+uint64_t invmod_h(uint64_t a, uint64_t q) { return powmod_h(a, q - 2, q); }
+
+bool is_prime_h(uint64_t n) {
+    static const uint64_t bases[] = {2, 3, 5, 7, 11, 13, 17, 19, 23, 29, 31, 37};
+    if (n < 2) return false;
+    for (uint64_t b : bases) {
+        if (n == b) return true;
+        if (n % b == 0) return false;
+    }
+    uint64_t d = n - 1;
+    int r = 0;
+    while (!(d & 1)) d >>= 1, r++;
+    for (uint64_t b : bases) {
+        uint64_t x = powmod_h(b, d, n);
+        if (x == 1 || x == n - 1) continue;
+        bool composite = true;
+        for (int i = 1; i < r && composite; i++) {
+            x = mulmod_h(x, x, n);
+            if (x == n - 1) composite = false;
+        }
+        if (composite) return false;
+    }
+    return true;
+}
+
+// largest primes below 2^bits with p = 1 mod m, excluding `skip`
+std::vector<uint64_t> ntt_primes(uint32_t bits, uint32_t count, uint64_t m, const std::vector<uint64_t>& skip) {
+    std::vector<uint64_t> out;
+    const uint64_t top = 1ull << bits;
+    uint64_t c = top - (top % m) + 1;
+    if (c >= top) c -= m;
+    for (; out.size() < count && c > m; c -= m) {
+        bool excluded = false;
+        for (uint64_t s : skip) excluded |= (s == c);
+        if (!excluded && is_prime_h(c)) out.push_back(c);
+    }
+    if (out.size() != count) throw std::runtime_error("not enough NTT primes below 2^" + std::to_string(bits));
+    return out;
+}
+
+// smallest primitive m-th root of unity mod q (m a power of two)
+uint64_t min_root_h(uint64_t q, uint64_t m) {
+    uint64_t psi = 0;
+    for (uint64_t g = 2; g < q && !psi; g++) {
+        const uint64_t x = powmod_h(g, (q - 1) / m, q);
+        if (powmod_h(x, m / 2, q) == q - 1) psi = x;
+    }
+    if (!psi) throw std::runtime_error("no primitive root");
+    uint64_t best = psi, cur = psi;
+    const uint64_t sq = mulmod_h(psi, psi, q);
+    for (uint64_t j = 1; j < m / 2; j++) {
+        cur = mulmod_h(cur, sq, q);
+        if (cur < best) best = cur;
+    }
+    return best;
+}
+
+static uint32_t brev(uint32_t v, uint32_t bits) {
+    uint32_t r = 0;
+    for (uint32_t b = 0; b < bits; b++, v >>= 1) r = (r << 1) | (v & 1);
+    return r;
+}
+
+static uint64_t shoup_companion(uint64_t w, uint64_t q) { return (uint64_t)(((u128)w << 64) / q); }
+
+PrimeInfo make_prime_info(uint64_t q) {
+    PrimeInfo p{};
+    p.q = q;
+    p.ninv = invmod_h(kN % q, q);
+    p.ninv_p = shoup_companion(p.ninv, q);
+    // mu = floor(2^128 / q) = floor((2^128 - 1) / q) for q not a power of two
+    const u128 mu = ~(u128)0 / q;
+    p.mu_hi = (uint64_t)(mu >> 64);
+    p.mu_lo = (uint64_t)mu;
+    return p;
+}
+
+void context_init(Context& c, const std::vector<uint64_t>& q, const std::vector<uint64_t>& p, uint32_t dnum,
+                  double scale, int device) {
+    if (q.empty() || dnum == 0 || dnum > q.size()) throw std::invalid_argument("bad num_q / dnum");
+    if (q.size() + p.size() > kMaxPrimes) throw std::invalid_argument("too many primes");
+    c.device = device;
+    c.L = (uint32_t)q.size();
+    c.K = (uint32_t)p.size();
+    c.dnum = dnum;
+    c.alpha = (c.L + dnum - 1) / dnum;
+    c.scale = scale;
+    c.moduli = q;
+    c.moduli.insert(c.moduli.end(), p.begin(), p.end());
+    const uint32_t T = c.L + c.K;
+    for (uint64_t m : c.moduli)
+        if (m >= (1ull << 62) || (m - 1) % (2ull * kN) != 0 || !is_prime_h(m))
+            throw std::invalid_argument("modulus is not an NTT prime below 2^62: " + std::to_string(m));
+    std::vector<TwPair> tw((size_t)T * kN), itw((size_t)T * kN);
+    c.psi.resize(T);
+    c.primes.resize(T);
+    for (uint32_t i = 0; i < T; i++) {
+        const uint64_t m = c.moduli[i];
+        const uint64_t psi = min_root_h(m, 2ull * kN), psiinv = invmod_h(psi, m);
+        c.psi[i] = psi;
+        c.primes[i] = make_prime_info(m);
+        uint64_t x = 1, y = 1;
+        TwPair* t = tw.data() + (size_t)i * kN;
+        TwPair* it = itw.data() + (size_t)i * kN;
+        for (uint32_t j = 0; j < kN; j++) {
+            const uint32_t r = brev(j, kLogN);
+            t[r] = TwPair{x, shoup_companion(x, m)};
+            it[r] = TwPair{y, shoup_companion(y, m)};
+            x = mulmod_h(x, psi, m);
+            y = mulmod_h(y, psiinv, m);
+        }
+    }
+    if (hipSetDevice(device) != hipSuccess) throw std::runtime_error("hipSetDevice failed");
+    auto up = [](void** d, const void* h, size_t bytes) {
+        if (hipMalloc(d, bytes) != hipSuccess) throw std::runtime_error("hipMalloc failed");
+        if (hipMemcpy(*d, h, bytes, hipMemcpyHostToDevice) != hipSuccess) throw std::runtime_error("hipMemcpy failed");
+    };
+    up((void**)&c.d_tw, tw.data(), tw.size() * sizeof(TwPair));
+    up((void**)&c.d_itw, itw.data(), itw.size() * sizeof(TwPair));
+    up((void**)&c.d_primes, c.primes.data(), c.primes.size() * sizeof(PrimeInfo));
+}
+
+void context_release(Context& c) {
+    (void)hipFree(c.d_tw);
+    (void)hipFree(c.d_itw);
+    (void)hipFree(c.d_primes);
+    for (auto& kv : c.job_cache) (void)hipFree(kv.second);
+    for (auto& kv : c.bconv_cache) (void)hipFree(kv.second.d_tab);
+    for (auto& s : c.scratch) (void)hipFree(s.first);
+    c.job_cache.clear();
+    c.bconv_cache.clear();
+    c.scratch.clear();
+    c.d_tw = c.d_itw = nullptr;
+    c.d_primes = nullptr;
+}
+
+}  // namespace fhe

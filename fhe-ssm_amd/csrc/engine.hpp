@@ -1,0 +1,71 @@
+// engine.hpp -- internal types of the MI355X RNS-CKKS engine (not part of the C ABI).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+namespace fhe {
+
+constexpr uint32_t kLogN = 16;
+constexpr uint32_t kN = 1u << kLogN;
+constexpr uint32_t kMaxPrimes = 96;
+constexpr uint32_t kMaxPmap = 96;
+
+struct TwPair {
+    uint64_t w, wp;  // twiddle and its Shoup companion floor(w * 2^64 / q)
+};
+
+struct PrimeInfo {
+    uint64_t q;
+    uint64_t ninv, ninv_p;   // N^-1 mod q and Shoup companion
+    uint64_t mu_hi, mu_lo;   // floor(2^128 / q)
+};
+
+// One limb to transform: offset (in units of N words) from the base pointer, and its prime index.
+struct Job {
+    uint32_t off, prime;
+};
+
+// Either an explicit device job list, or a dense [n_polys][period][N] buffer whose limb l uses
+// prime pmap[l] (enumerated prime-major).
+struct JobSpec {
+    const Job* jobs;
+    uint32_t n_polys, period;
+    uint8_t pmap[kMaxPmap];
+};
+
+enum class NttMode { TwoPass = 0, Fused = 1 };
+
+// Precomputed constants for one approximate CRT switch (BConv) from `n_in` source limbs to `n_out`
+// target limbs: y_i = [x_i * qhat_inv_i]_{q_i};  out_j = sum_i y_i * qhat_mod[i][j] mod p_j.
+struct BConvPlan {
+    uint32_t n_in = 0, n_out = 0;
+    std::vector<uint32_t> in_idx, out_idx;  // prime indices
+    uint64_t* d_tab = nullptr;  // [n_in] (qhat_inv, companion) pairs, then [n_in][n_out] qhat_mod
+};
+
+struct Context {
+    int device = 0;
+    uint32_t L = 0, K = 0, dnum = 0, alpha = 0;
+    double scale = 0.0;
+    std::vector<uint64_t> moduli;  // Q chain then P
+    std::vector<uint64_t> psi;
+    std::vector<PrimeInfo> primes;
+    TwPair* d_tw = nullptr;   // [L+K][N] forward table (brev order)
+    TwPair* d_itw = nullptr;  // [L+K][N] inverse table (brev order)
+    PrimeInfo* d_primes = nullptr;
+    NttMode ntt_mode = NttMode::Fused;
+    // cached device job lists keyed by a shape string
+    std::map<std::string, Job*> job_cache;
+    std::map<std::string, BConvPlan> bconv_cache;
+    // growable scratch
+    std::vector<std::pair<void*, size_t>> scratch;
+};
+
+hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,
+                      NttMode mode, hipStream_t st);
+
+}  // namespace fhe

@@ -1,0 +1,69 @@
+// modarith.hpp -- 64-bit modular arithmetic for gfx950 built from 32-bit VALU multiplies.
+//
+// Moduli are NTT primes q < 2^62 (54-bit Q limbs, 60-bit P limbs).  Residues live in uint64.
+// Lazy (Harvey) reduction: NTT butterflies keep values in [0, 2q) / [0, 4q) between stages and
+// reduce to [0, q) once at the end, so every value a kernel writes is canonical and results are
+// bit-identical to any other correct reduction order.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fhe {
+
+// high 64 bits of a 64x64 product
+__device__ __forceinline__ uint64_t mulhi64(uint64_t a, uint64_t b) { return __umul64hi(a, b); }
+
+// Shoup multiply by a constant w with companion wp = floor(w * 2^64 / q): result in [0, 2q) for any
+// x < 2^64 (w < q).  Same companion as hpc_gpu_port/periodic_encode.hpp:115-120.
+__device__ __forceinline__ uint64_t shoup_lazy(uint64_t x, uint64_t w, uint64_t wp, uint64_t q) {
+    const uint64_t hi = mulhi64(x, wp);
+    return x * w - hi * q;
+}
+
+__device__ __forceinline__ uint64_t csub(uint64_t x, uint64_t q) { return x >= q ? x - q : x; }
+
+__device__ __forceinline__ uint64_t shoup(uint64_t x, uint64_t w, uint64_t wp, uint64_t q) {
+    return csub(shoup_lazy(x, w, wp, q), q);
+}
+
+__device__ __forceinline__ uint64_t add_mod(uint64_t a, uint64_t b, uint64_t q) { return csub(a + b, q); }
+__device__ __forceinline__ uint64_t sub_mod(uint64_t a, uint64_t b, uint64_t q) { return a >= b ? a - b : a + q - b; }
+
+// Barrett reduction of a 128-bit value (hi:lo) with hi < q, using mu = floor(2^128 / q) split as
+// (mu_hi, mu_lo).  Result in [0, q).
+struct Barrett {
+    uint64_t q, mu_hi, mu_lo;
+};
+
+__device__ __forceinline__ uint64_t reduce128(uint64_t hi, uint64_t lo, const Barrett& b) {
+    // estimate quotient floor(x * mu / 2^128) from the top words; error < 4
+    const uint64_t q = b.q;
+    // x * mu >> 128 ~= hi*mu_hi + mulhi(hi, mu_lo) + mulhi(lo, mu_hi)
+    uint64_t t1 = mulhi64(lo, b.mu_hi);
+    uint64_t t2 = mulhi64(hi, b.mu_lo);
+    uint64_t qt = hi * b.mu_hi + t1 + t2;
+    uint64_t r = lo - qt * q;
+    r = csub(r, q);
+    r = csub(r, q);
+    r = csub(r, q);
+    return csub(r, q);
+}
+
+__device__ __forceinline__ uint64_t mul_mod(uint64_t a, uint64_t b, const Barrett& br) {
+    return reduce128(mulhi64(a, b), a * b, br);
+}
+
+// 128-bit accumulator
+struct U128 {
+    uint64_t lo, hi;
+};
+
+__device__ __forceinline__ void mac128(U128& acc, uint64_t a, uint64_t b) {
+    const uint64_t lo = a * b;
+    const uint64_t hi = mulhi64(a, b);
+    const uint64_t nlo = acc.lo + lo;
+    acc.hi += hi + (nlo < lo ? 1 : 0);
+    acc.lo = nlo;
+}
+
+}  // namespace fhe

@@ -1,0 +1,346 @@
+// ntt.hip -- batched negacyclic NTT / INTT at N = 2^16 for gfx950.
+//
+// Semantics are OpenFHE's (restated in hpc_gpu_port/periodic_encode.hpp:240-260): forward is the
+// Cooley-Tukey network over the table Table[brev(i)] = psi^i, natural order in, bit-reversed order
+// out; inverse is the Gentleman-Sande network over the psi^-1 table, bit-reversed in, natural out,
+// times N^-1.  The kernels run exactly that butterfly network, so the words they write are the
+// words the CPU loop writes.
+//
+// Decomposition: N = 256 x 256.  The 16 stages split into two passes of 8:
+//   pass A  (forward stages 0..7 / inverse stages 8..15): butterflies of stride >= 256.  Element j =
+//           c + 256 r; for a fixed column c the 256 rows are an independent 8-stage problem whose
+//           twiddles depend only on r.  A tile = 16 adjacent columns x 256 rows (32 KiB), so every
+//           global access is a run of 16 consecutive words (128 B) per row.
+//   pass B  (forward stages 8..15 / inverse 0..7): butterflies of stride < 256 inside each
+//           contiguous 256-word block.  A tile = 16 blocks.
+// Inside a tile each of 256 threads holds 16 words in registers and performs 4 stages (a radix-16
+// step) between two LDS exchanges.  Values stay lazily reduced (Harvey) in [0, 4q) between stages.
+//
+// Launch layout: a "job" is one limb (offset in units of N words + prime index).  Jobs are
+// enumerated prime-major so that concurrently running workgroups share one prime's twiddle table
+// (1 MiB) in L2.  Either both passes run as separate kernels (grid 16 x jobs, 256 threads), or the
+// fused kernel runs one limb per 512-thread workgroup (2 tiles at a time, passes separated by a
+// workgroup barrier; the intermediate stays in L2/MALL instead of making a second HBM round trip).
+#include "engine.hpp"
+#include "modarith.hpp"
+
+namespace fhe {
+
+namespace {
+
+constexpr int kTileThreads = 256;
+constexpr int kLdsWords = 16 * 272;  // one tile, padded (pass B uses 17 words per 16)
+
+__device__ __forceinline__ void job_of(const JobSpec& js, uint32_t u, uint32_t& off, uint32_t& prime) {
+    if (js.jobs) {
+        const Job j = js.jobs[u];
+        off = j.off;
+        prime = j.prime;
+    } else {
+        // prime-major enumeration of a dense [polys][period][N] buffer
+        const uint32_t l = u / js.n_polys, p = u - l * js.n_polys;
+        off = p * js.period + l;
+        prime = js.pmap[l];
+    }
+}
+
+__device__ __forceinline__ void ct_bfly(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q, uint64_t q2) {
+    const uint64_t x = X >= q2 ? X - q2 : X;
+    const uint64_t t = shoup_lazy(Y, w.w, w.wp, q);
+    X = x + t;
+    Y = x - t + q2;
+}
+
+__device__ __forceinline__ void gs_bfly(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q, uint64_t q2) {
+    uint64_t s = X + Y;
+    s = s >= q2 ? s - q2 : s;
+    const uint64_t d = X - Y + q2;
+    X = s;
+    Y = shoup_lazy(d, w.w, w.wp, q);
+}
+
+// ---------------------------------------------------------------- forward pass A (strided columns)
+// tile: columns [16*tile, 16*tile + 16).  g: thread id within the 256-thread group.
+__device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
+                                           int tile, int g, uint64_t* lds) {
+    const uint64_t q2 = q << 1;
+    const int cl = g & 15, rg = g >> 4;
+    const int col = tile * 16 + cl;
+    uint64_t x[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = a[col + 256 * (rg + 16 * k)];
+    // stages 0..3: rows r = rg + 16k, pairs differ in bit (3-s) of k; twiddle (1<<s) + (k >> (4-s))
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const int h = 8 >> s;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (k & h) continue;
+            ct_bfly(x[k], x[k + h], tw[(1 << s) + (k >> (4 - s))], q, q2);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 16; k++) lds[(rg + 16 * k) * 16 + cl] = x[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = lds[(16 * rg + k) * 16 + cl];
+    // stages 4..7: rows r = 16 rg + k, pairs differ in bit (7-s) of r; twiddle (1<<s) + (r >> (8-s))
+#pragma unroll
+    for (int s = 4; s < 8; s++) {
+        const int h = 128 >> s;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (k & h) continue;
+            ct_bfly(x[k], x[k + h], tw[(1 << s) + ((16 * rg + k) >> (8 - s))], q, q2);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 16; k++) a[col + 256 * (16 * rg + k)] = x[k];
+}
+
+// ---------------------------------------------------------------- forward pass B (256-word blocks)
+__device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
+                                           int tile, int g, uint64_t* lds) {
+    const uint64_t q2 = q << 1;
+    const int bl = g >> 4, rl = g & 15;
+    const int b = tile * 16 + bl;  // block index within the limb
+    uint64_t* blk = a + 256 * b;
+    uint64_t* L = lds + bl * 272;
+    uint64_t x[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = blk[rl + 16 * k];
+    // stages 8+s, s = 0..3: r = rl + 16k; twiddle 2^(8+s) + b 2^s + (k >> (4-s))
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const int h = 8 >> s;
+        const TwPair* t = tw + (256 << s) + (b << s);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (k & h) continue;
+            ct_bfly(x[k], x[k + h], t[k >> (4 - s)], q, q2);
+        }
+    }
+    // LDS word index of r: r + (r >> 4)
+#pragma unroll
+    for (int k = 0; k < 16; k++) L[rl + 17 * k] = x[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = L[17 * rl + k];
+    // stages 8+s, s = 4..7: r = 16 rl + k; twiddle 2^(8+s) + b 2^s + (r >> (8-s))
+#pragma unroll
+    for (int s = 4; s < 8; s++) {
+        const int h = 128 >> s;
+        const TwPair* t = tw + (256 << s) + (b << s);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (k & h) continue;
+            ct_bfly(x[k], x[k + h], t[(16 * rl + k) >> (8 - s)], q, q2);
+        }
+    }
+    // canonical [0, q), then transpose through LDS for coalesced stores
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        uint64_t v = x[k] >= q2 ? x[k] - q2 : x[k];
+        x[k] = v >= q ? v - q : v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) L[17 * rl + k] = x[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) blk[rl + 16 * k] = L[rl + 17 * k];
+}
+
+// ---------------------------------------------------------------- inverse pass B (256-word blocks)
+// GS stages with t = 2^u, u = 0..7: m = 2^(15-u), twiddle m + (j >> (u+1)), j = 256 b + r.
+__device__ __forceinline__ void inv_b_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
+                                           int tile, int g, uint64_t* lds) {
+    const uint64_t q2 = q << 1;
+    const int bl = g >> 4, rl = g & 15;
+    const int b = tile * 16 + bl;
+    uint64_t* blk = a + 256 * b;
+    uint64_t* L = lds + bl * 272;
+    uint64_t x[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) L[rl + 17 * k] = blk[rl + 16 * k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = L[17 * rl + k];
+    // u = 0..3: r = 16 rl + k, pairs differ in bit u of k
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int h = 1 << u;
+        const TwPair* t = tw + (32768 >> u) + (b << (7 - u));
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (k & h) continue;
+            gs_bfly(x[k], x[k + h], t[(16 * rl + k) >> (u + 1)], q, q2);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) L[17 * rl + k] = x[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = L[rl + 17 * k];
+    // u = 4..7: r = rl + 16k, pairs differ in bit (u-4) of k; r >> (u+1) = k >> (u-3)
+#pragma unroll
+    for (int u = 4; u < 8; u++) {
+        const int h = 1 << (u - 4);
+        const TwPair* t = tw + (32768 >> u) + (b << (7 - u));
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (k & h) continue;
+            gs_bfly(x[k], x[k + h], t[k >> (u - 3)], q, q2);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 16; k++) blk[rl + 16 * k] = x[k];
+}
+
+// ---------------------------------------------------------------- inverse pass A (strided columns)
+// GS stages with t = 2^(8+u), u = 0..7: m = 2^(7-u), twiddle m + (r >> (u+1)); then * N^-1.
+__device__ __forceinline__ void inv_a_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
+                                           TwPair ninv, int tile, int g, uint64_t* lds) {
+    const uint64_t q2 = q << 1;
+    const int cl = g & 15, rg = g >> 4;
+    const int col = tile * 16 + cl;
+    uint64_t x[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = a[col + 256 * (16 * rg + k)];
+    // u = 0..3: r = 16 rg + k, pairs differ in bit u of k
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int h = 1 << u;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (k & h) continue;
+            gs_bfly(x[k], x[k + h], tw[(128 >> u) + ((16 * rg + k) >> (u + 1))], q, q2);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 16; k++) lds[(16 * rg + k) * 16 + cl] = x[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; k++) x[k] = lds[(rg + 16 * k) * 16 + cl];
+    // u = 4..7: r = rg + 16k, pairs differ in bit (u-4) of k; r >> (u+1) = k >> (u-3)
+#pragma unroll
+    for (int u = 4; u < 8; u++) {
+        const int h = 1 << (u - 4);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (k & h) continue;
+            gs_bfly(x[k], x[k + h], tw[(128 >> u) + (k >> (u - 3))], q, q2);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 16; k++) a[col + 256 * (rg + 16 * k)] = shoup(x[k], ninv.w, ninv.wp, q);
+}
+
+// ---------------------------------------------------------------- kernels
+__global__ __launch_bounds__(kTileThreads) void k_ntt_fwd_a(uint64_t* data, JobSpec js, const TwPair* tw_all,
+                                                           const PrimeInfo* primes) {
+    __shared__ uint64_t lds[kLdsWords];
+    uint32_t off, prime;
+    job_of(js, blockIdx.y, off, prime);
+    fwd_a_tile(data + (size_t)off * kN, tw_all + (size_t)prime * kN, primes[prime].q, blockIdx.x, threadIdx.x, lds);
+}
+
+__global__ __launch_bounds__(kTileThreads) void k_ntt_fwd_b(uint64_t* data, JobSpec js, const TwPair* tw_all,
+                                                           const PrimeInfo* primes) {
+    __shared__ uint64_t lds[kLdsWords];
+    uint32_t off, prime;
+    job_of(js, blockIdx.y, off, prime);
+    fwd_b_tile(data + (size_t)off * kN, tw_all + (size_t)prime * kN, primes[prime].q, blockIdx.x, threadIdx.x, lds);
+}
+
+__global__ __launch_bounds__(kTileThreads) void k_ntt_inv_b(uint64_t* data, JobSpec js, const TwPair* tw_all,
+                                                           const PrimeInfo* primes) {
+    __shared__ uint64_t lds[kLdsWords];
+    uint32_t off, prime;
+    job_of(js, blockIdx.y, off, prime);
+    inv_b_tile(data + (size_t)off * kN, tw_all + (size_t)prime * kN, primes[prime].q, blockIdx.x, threadIdx.x, lds);
+}
+
+__global__ __launch_bounds__(kTileThreads) void k_ntt_inv_a(uint64_t* data, JobSpec js, const TwPair* tw_all,
+                                                           const PrimeInfo* primes) {
+    __shared__ uint64_t lds[kLdsWords];
+    uint32_t off, prime;
+    job_of(js, blockIdx.y, off, prime);
+    const PrimeInfo& P = primes[prime];
+    inv_a_tile(data + (size_t)off * kN, tw_all + (size_t)prime * kN, P.q, TwPair{P.ninv, P.ninv_p}, blockIdx.x,
+               threadIdx.x, lds);
+}
+
+// Fused: one limb per workgroup of 4 x 256 threads; each 256-thread group owns one LDS tile.
+constexpr int kFusedGroups = 2;
+
+__global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_fwd_fused(uint64_t* data, JobSpec js,
+                                                                              const TwPair* tw_all,
+                                                                              const PrimeInfo* primes) {
+    __shared__ uint64_t lds[kFusedGroups * kLdsWords];
+    uint32_t off, prime;
+    job_of(js, blockIdx.x, off, prime);
+    uint64_t* a = data + (size_t)off * kN;
+    const TwPair* tw = tw_all + (size_t)prime * kN;
+    const uint64_t q = primes[prime].q;
+    const int grp = threadIdx.x >> 8, g = threadIdx.x & 255;
+    uint64_t* L = lds + grp * kLdsWords;
+    for (int t = grp; t < 16; t += kFusedGroups) {
+        fwd_a_tile(a, tw, q, t, g, L);
+        __syncthreads();
+    }
+    for (int t = grp; t < 16; t += kFusedGroups) {
+        fwd_b_tile(a, tw, q, t, g, L);
+        __syncthreads();
+    }
+}
+
+__global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_inv_fused(uint64_t* data, JobSpec js,
+                                                                              const TwPair* tw_all,
+                                                                              const PrimeInfo* primes) {
+    __shared__ uint64_t lds[kFusedGroups * kLdsWords];
+    uint32_t off, prime;
+    job_of(js, blockIdx.x, off, prime);
+    uint64_t* a = data + (size_t)off * kN;
+    const TwPair* tw = tw_all + (size_t)prime * kN;
+    const PrimeInfo& P = primes[prime];
+    const int grp = threadIdx.x >> 8, g = threadIdx.x & 255;
+    uint64_t* L = lds + grp * kLdsWords;
+    for (int t = grp; t < 16; t += kFusedGroups) {
+        inv_b_tile(a, tw, P.q, t, g, L);
+        __syncthreads();
+    }
+    for (int t = grp; t < 16; t += kFusedGroups) {
+        inv_a_tile(a, tw, P.q, TwPair{P.ninv, P.ninv_p}, t, g, L);
+        __syncthreads();
+    }
+}
+
+}  // namespace
+
+hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,
+                      NttMode mode, hipStream_t st) {
+    if (n_jobs == 0) return hipSuccess;
+    const TwPair* tw = inverse ? ctx.d_itw : ctx.d_tw;
+    if (mode == NttMode::Fused) {
+        if (inverse)
+            hipLaunchKernelGGL(k_ntt_inv_fused, dim3(n_jobs), dim3(kTileThreads * kFusedGroups), 0, st, data, js, tw,
+                               ctx.d_primes);
+        else
+            hipLaunchKernelGGL(k_ntt_fwd_fused, dim3(n_jobs), dim3(kTileThreads * kFusedGroups), 0, st, data, js, tw,
+                               ctx.d_primes);
+        return hipGetLastError();
+    }
+    const dim3 grid(16, n_jobs), block(kTileThreads);
+    if (inverse) {
+        hipLaunchKernelGGL(k_ntt_inv_b, grid, block, 0, st, data, js, tw, ctx.d_primes);
+        hipLaunchKernelGGL(k_ntt_inv_a, grid, block, 0, st, data, js, tw, ctx.d_primes);
+    } else {
+        hipLaunchKernelGGL(k_ntt_fwd_a, grid, block, 0, st, data, js, tw, ctx.d_primes);
+        hipLaunchKernelGGL(k_ntt_fwd_b, grid, block, 0, st, data, js, tw, ctx.d_primes);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace fhe

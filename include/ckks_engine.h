@@ -1,0 +1,94 @@
+/*
+ * ckks_engine.h -- C ABI of the MI355X-native RNS-CKKS evaluation engine (libckks_hip.so).
+ *
+ * What it replaces.  The reference evaluates its encrypted recurrent step through FIDESlib's
+ * OpenFHE-compatible C++ class API, fideslib::CryptoContext<DCRTPoly> (hpc_gpu_port/gpu_real_model.cu:66,185);
+ * every EvalMult / RescaleInPlace / EvalRotate / EvalAdd / EvalBootstrap call of the driver goes there.
+ * This header is the drop-in boundary for that path: plain C, opaque handles, raw device pointers and
+ * sizes, status codes instead of exceptions (the reference's exceptions surface as JSON `fatal` lines,
+ * gpu_real_model.cu:924-928; here every entry point returns an int and ckks_last_error() explains).
+ *
+ * Data layout (kept from the reference, gpu_real_model.cu:1762-1790 and seeded_keys.hpp:216-256):
+ *   - a polynomial is a list of limbs, each limb N = 2^16 contiguous uint64 residues in [0, q);
+ *   - evaluation form uses OpenFHE's bit-reversed NTT order (periodic_encode.hpp:240-260);
+ *   - limb index = global prime index in chain order: 0..L-1 the Q chain, L..L+K-1 the special primes P;
+ *     limbs are dropped from the end (level l keeps Q limbs 0..l-1);
+ *   - a ciphertext batch is uint64[B][2][l][N] (B ciphertexts, polys c0,c1, l limbs);
+ *   - a key-switching key is uint64[dnum][2][L+K][N]: [j][0] = b_j, [j][1] = a_j, EVALUATION form
+ *     (EvalKeyRelinImpl{A[dnum], B[dnum]} of OpenFHE).
+ *
+ * Threading: one host thread per context issues all work; entry points are not re-entrant per
+ * context (the reference's FIDESlib usage has the same rule, gpu_real_model.cu:3017-3024).
+ * Streams: every compute entry point takes a hipStream_t (as void*); NULL is the null stream.
+ * Device pointers may come from ckks_buffer_alloc or from any HIP allocator (e.g. torch tensors).
+ */
+#ifndef CKKS_ENGINE_H
+#define CKKS_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define CKKS_OK 0
+#define CKKS_EINVAL 1   /* bad argument / shape / level */
+#define CKKS_EHIP 2     /* HIP runtime error (message in ckks_last_error) */
+#define CKKS_ENOMEM 3
+#define CKKS_ENOTSUP 4
+
+typedef struct ckks_context ckks_context;
+
+typedef struct {
+    uint32_t log_n;     /* ring dimension log2; this build supports 16 */
+    uint32_t num_q;     /* L: Q-chain limbs (multiplicative depth + 1) */
+    uint32_t num_p;     /* K: special primes for hybrid key switching */
+    uint32_t dnum;      /* digits of the hybrid key switch */
+    uint32_t q_bits;    /* bit size of the Q primes (largest primes below 2^q_bits, = 1 mod 2N) */
+    uint32_t p_bits;    /* bit size of the P primes */
+    double scale;       /* CKKS scaling factor Delta */
+    int device;         /* HIP device ordinal */
+} ckks_params;
+
+/* Last error message of the calling thread ("" when none). */
+const char* ckks_last_error(void);
+
+/* ---- context -------------------------------------------------------------------------------
+ * Replaces GenCryptoContext + the device upload of FIDESlib's LoadContext (gpu_real_model.cu:1138-1164,
+ * 1530).  Moduli: the largest primes below 2^q_bits (then 2^p_bits, skipping Q primes) with
+ * q = 1 mod 2N; root of unity per prime: the smallest primitive 2N-th root. */
+int ckks_context_create(const ckks_params* params, ckks_context** out);
+/* Same, with the moduli given explicitly (Q chain order, then P). */
+int ckks_context_create_from_moduli(uint32_t log_n, const uint64_t* q, uint32_t num_q, const uint64_t* p,
+                                    uint32_t num_p, uint32_t dnum, double scale, int device, ckks_context** out);
+void ckks_context_destroy(ckks_context* ctx);
+int ckks_context_info(const ckks_context* ctx, uint32_t* n, uint32_t* num_q, uint32_t* num_p, uint32_t* dnum);
+/* moduli (num_q + num_p) and the primitive 2N-th roots used by the NTT, chain order */
+int ckks_context_moduli(const ckks_context* ctx, uint64_t* out, uint32_t cap);
+int ckks_context_roots(const ckks_context* ctx, uint64_t* out, uint32_t cap);
+/* NTT schedule: 0 = two kernels (pass A, pass B), 1 = fused one-limb-per-workgroup (default) */
+int ckks_set_ntt_mode(ckks_context* ctx, int mode);
+
+/* ---- device memory helpers (plain HIP; any HIP allocation works with the compute calls) ---- */
+int ckks_buffer_alloc(size_t bytes, void** d_out);
+int ckks_buffer_free(void* d);
+int ckks_memcpy_h2d(void* d_dst, const void* h_src, size_t bytes);
+int ckks_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes);
+int ckks_device_sync(void);
+
+/* ---- raw stages (the hot path; all buffers device-resident, limb-major) ----------------------
+ * NTT over a dense buffer uint64[n_polys][n_limbs][N]; limb l of every poly uses prime prime_idx[l]
+ * (host array, n_limbs <= 96).  Forward: natural -> bit-reversed (OpenFHE
+ * ForwardTransformToBitReverse, periodic_encode.hpp:240-260); inverse: bit-reversed -> natural, * N^-1.
+ * Inputs must be canonical residues in [0, q); outputs are canonical. In place. */
+int ckks_ntt_forward(ckks_context* ctx, uint64_t* d_data, uint32_t n_polys, uint32_t n_limbs,
+                     const uint32_t* prime_idx, void* stream);
+int ckks_ntt_inverse(ckks_context* ctx, uint64_t* d_data, uint32_t n_polys, uint32_t n_limbs,
+                     const uint32_t* prime_idx, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,96 @@
+"""GPU parity of the batched NTT/INTT against the CPU oracle, through the C ABI.
+
+Bar: bit-exact words.  Sizes: oracle-checked batches of a few hundred limbs, plus the full config-1
+shape (64 ct x 2 polys x 24 limbs) checked on a seeded sample of limbs and by the size-independent
+round trip INTT(NTT(x)) = x over every limb.
+"""
+import numpy as np
+import pytest
+
+from engine_loader import load_ckks
+
+pytestmark = pytest.mark.gpu
+
+L, K = 24, 8
+
+
+@pytest.fixture(scope="module")
+def ckks():
+    return load_ckks()
+
+
+@pytest.fixture(scope="module")
+def ctx(ckks):
+    return ckks.Context(num_q=L, num_p=K, dnum=3, q_bits=54, p_bits=60)
+
+
+@pytest.fixture(scope="module")
+def octx(oracle, ctx):
+    return oracle.Ctx(16, ctx.moduli, L, K, 3)
+
+
+def rand_polys(moduli, n_polys, prime_idx, seed):
+    rng = np.random.default_rng(seed)
+    q = np.array([moduli[i] for i in prime_idx], dtype=np.uint64)
+    return (rng.integers(0, 2**63, (n_polys, len(prime_idx), 1 << 16), dtype=np.uint64) % q[None, :, None])
+
+
+def test_context_matches_oracle_parameters(oracle, ctx, octx):
+    q = oracle.gen_primes(54, L, 2**17)
+    p = oracle.gen_primes(60, K, 2**17, exclude=q)
+    assert ctx.moduli == q + p
+    assert ctx.roots == octx.psi
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("prime_idx", [list(range(24)), list(range(24, 32)), [3, 31, 0, 17, 24]])
+def test_ntt_forward_inverse_bit_exact(ckks, ctx, octx, mode, prime_idx):
+    ctx.set_ntt_mode(mode)
+    x = rand_polys(ctx.moduli, 3, prime_idx, seed=len(prime_idx) + mode)
+    buf = ckks.DeviceBuffer.from_array(x)
+    ctx.ntt_forward(buf.ptr, 3, prime_idx)
+    X = buf.download(x.shape)
+    want = octx.ntt_fwd(x, prime_idx)
+    assert np.array_equal(X, want)
+    ctx.ntt_inverse(buf.ptr, 3, prime_idx)
+    assert np.array_equal(buf.download(x.shape), x)
+    # inverse on its own vs the oracle inverse of random (bit-reversed-order) data
+    y = rand_polys(ctx.moduli, 3, prime_idx, seed=99)
+    buf.upload(y)
+    ctx.ntt_inverse(buf.ptr, 3, prime_idx)
+    assert np.array_equal(buf.download(y.shape), octx.ntt_inv(y, prime_idx))
+    ctx.set_ntt_mode(1)
+
+
+def test_ntt_edge_values(ckks, ctx, octx):
+    """all-zero, all q-1 and delta limbs (extremes of the lazy-reduction ranges)"""
+    pi = [0, 23, 24, 31]
+    x = np.zeros((3, 4, 1 << 16), dtype=np.uint64)
+    for j, p in enumerate(pi):
+        x[1, j, :] = ctx.moduli[p] - 1
+        x[2, j, 1] = 1
+    for mode in (0, 1):
+        ctx.set_ntt_mode(mode)
+        buf = ckks.DeviceBuffer.from_array(x)
+        ctx.ntt_forward(buf.ptr, 3, pi)
+        assert np.array_equal(buf.download(x.shape), octx.ntt_fwd(x, pi))
+        ctx.ntt_inverse(buf.ptr, 3, pi)
+        assert np.array_equal(buf.download(x.shape), x)
+    ctx.set_ntt_mode(1)
+
+
+def test_ntt_config1_full_shape(ckks, ctx, octx):
+    """64 ciphertexts x 2 polys x 24 limbs: sampled limbs vs the oracle, round trip on all limbs."""
+    n_polys = 128
+    prime_idx = list(range(L))
+    rng = np.random.default_rng(2024)
+    q = np.array(ctx.moduli[:L], dtype=np.uint64)
+    x = rng.integers(0, 2**63, (n_polys, L, 1 << 16), dtype=np.uint64) % q[None, :, None]
+    buf = ckks.DeviceBuffer.from_array(x)
+    ctx.ntt_forward(buf.ptr, n_polys, prime_idx)
+    X = buf.download(x.shape)
+    for p, l in zip(rng.integers(0, n_polys, 24), rng.permutation(L)):
+        assert np.array_equal(X[p, l], octx.ntt_fwd(x[p, l][None], [l])[0]), (p, l)
+    assert bool((X < q[None, :, None]).all())
+    ctx.ntt_inverse(buf.ptr, n_polys, prime_idx)
+    assert np.array_equal(buf.download(x.shape), x)
