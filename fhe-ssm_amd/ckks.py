@@ -45,6 +45,17 @@ SIGNATURES = {
     "ckks_device_sync": (_int, []),
     "ckks_ntt_forward": (_int, [_vp, _vp, _u32, _u32, _vp, _vp]),
     "ckks_ntt_inverse": (_int, [_vp, _vp, _u32, _u32, _vp, _vp]),
+    "ckks_modup": (_int, [_vp, _vp, _u32, _u32, _vp, _vp]),
+    "ckks_ks_inner": (_int, [_vp, _vp, _u32, _u32, _vp, _vp, _vp]),
+    "ckks_moddown": (_int, [_vp, _vp, _u32, _u32, _vp, _vp]),
+    "ckks_keyswitch": (_int, [_vp, _vp, _u32, _u32, _vp, _vp, _vp]),
+    "ckks_rescale": (_int, [_vp, _vp, _u32, _u32, _vp, _vp]),
+    "ckks_eval_mult": (_int, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp]),
+    "ckks_eval_mult_rescale": (_int, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp]),
+    "ckks_eval_add": (_int, [_vp, _vp, _vp, _u32, _u32, _vp, _vp]),
+    "ckks_rotation_index": (_u32, [ctypes.c_int64]),
+    "ckks_automorphism": (_int, [_vp, _vp, _u32, _u32, _u32, _vp, _vp]),
+    "ckks_eval_rotate": (_int, [_vp, _vp, _u32, _u32, ctypes.c_int64, _vp, _vp, _vp]),
 }
 
 
@@ -172,3 +183,41 @@ class Context:
     def ntt_inverse(self, d_ptr: int, n_polys: int, prime_idx, stream=None) -> None:
         pi = np.ascontiguousarray(np.asarray(prime_idx, dtype=np.uint32))
         check(load().ckks_ntt_inverse(self.h, d_ptr, n_polys, len(pi), _ptr(pi), stream))
+
+    def num_digits(self, level: int) -> int:
+        alpha = -(-self.L // self.dnum)
+        return -(-level // alpha)
+
+    def modup(self, d_x, batch, level, d_ext, stream=None):
+        check(load().ckks_modup(self.h, d_x, batch, level, d_ext, stream))
+
+    def ks_inner(self, d_ext, batch, level, d_evk, d_acc, stream=None):
+        check(load().ckks_ks_inner(self.h, d_ext, batch, level, d_evk, d_acc, stream))
+
+    def moddown(self, d_x, n_polys, level, d_out, stream=None):
+        check(load().ckks_moddown(self.h, d_x, n_polys, level, d_out, stream))
+
+    def keyswitch(self, d_x, batch, level, d_evk, d_out, stream=None):
+        check(load().ckks_keyswitch(self.h, d_x, batch, level, d_evk, d_out, stream))
+
+    def rescale(self, d_in, n_polys, level, d_out, stream=None):
+        check(load().ckks_rescale(self.h, d_in, n_polys, level, d_out, stream))
+
+    def eval_mult(self, d_a, d_b, batch, level, d_evk, d_out, stream=None):
+        check(load().ckks_eval_mult(self.h, d_a, d_b, batch, level, d_evk, d_out, stream))
+
+    def eval_mult_rescale(self, d_a, d_b, batch, level, d_evk, d_out, stream=None):
+        check(load().ckks_eval_mult_rescale(self.h, d_a, d_b, batch, level, d_evk, d_out, stream))
+
+    def eval_add(self, d_x, d_y, n_polys, level, d_out, stream=None):
+        check(load().ckks_eval_add(self.h, d_x, d_y, n_polys, level, d_out, stream))
+
+    def automorphism(self, d_in, n_polys, level, g, d_out, stream=None):
+        check(load().ckks_automorphism(self.h, d_in, n_polys, level, g, d_out, stream))
+
+    def eval_rotate(self, d_ct, batch, level, step, d_evk, d_out, stream=None):
+        check(load().ckks_eval_rotate(self.h, d_ct, batch, level, step, d_evk, d_out, stream))
+
+
+def rotation_index(step: int) -> int:
+    return int(load().ckks_rotation_index(step))

@@ -8,6 +8,7 @@
 
 #include "ckks_engine.h"
 #include "engine.hpp"
+#include "ops.hpp"
 
 namespace fhe {
 std::vector<uint64_t> ntt_primes(uint32_t bits, uint32_t count, uint64_t m, const std::vector<uint64_t>& skip);
@@ -75,6 +76,25 @@ int ntt_entry(ckks_context* ctx, uint64_t* d, uint32_t n_polys, uint32_t n_limbs
     for (uint32_t i = 0; i < n_limbs; i++) js.pmap[i] = (uint8_t)prime_idx[i];
     HIP_TRY(fhe::launch_ntt(ctx->c, d, js, (uint32_t)jobs, inverse, ctx->c.ntt_mode, (hipStream_t)stream));
     return CKKS_OK;
+}
+
+int check_ctx_level(const ckks_context* ctx, uint32_t level, bool need_p) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    if (level == 0 || level > ctx->c.L) return fail(CKKS_EINVAL, "level out of range [1, L]");
+    if (need_p && ctx->c.K == 0) return fail(CKKS_EINVAL, "context has no special primes");
+    return CKKS_OK;
+}
+
+uint32_t rot_index(int64_t k) {
+    const uint64_t M = 2ull * fhe::kN, ord = fhe::kN / 2;  // 5 has order N/2 in (Z/2N)^*
+    int64_t e = k % (int64_t)ord;
+    if (e < 0) e += (int64_t)ord;
+    uint64_t r = 1, b = 5;
+    for (uint64_t x = (uint64_t)e; x; x >>= 1) {
+        if (x & 1) r = r * b % M;
+        b = b * b % M;
+    }
+    return (uint32_t)r;
 }
 
 }  // namespace
@@ -193,6 +213,119 @@ int ckks_ntt_forward(ckks_context* ctx, uint64_t* d_data, uint32_t n_polys, uint
 int ckks_ntt_inverse(ckks_context* ctx, uint64_t* d_data, uint32_t n_polys, uint32_t n_limbs,
                      const uint32_t* prime_idx, void* stream) {
     return ntt_entry(ctx, d_data, n_polys, n_limbs, prime_idx, stream, true);
+}
+
+int ckks_modup(ckks_context* ctx, const uint64_t* d_x, uint32_t batch, uint32_t level, uint64_t* d_ext,
+               void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_x || !d_ext) return fail(CKKS_EINVAL, "null buffer");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::modup(ctx->c, d_x, d_ext, batch, level, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_ks_inner(ckks_context* ctx, const uint64_t* d_ext, uint32_t batch, uint32_t level, const uint64_t* d_evk,
+                  uint64_t* d_acc, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_ext || !d_evk || !d_acc) return fail(CKKS_EINVAL, "null buffer");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::ks_inner(ctx->c, d_ext, d_evk, d_acc, batch, level, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_moddown(ckks_context* ctx, uint64_t* d_x, uint32_t n_polys, uint32_t level, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_x || !d_out) return fail(CKKS_EINVAL, "null buffer");
+    if (!n_polys) return CKKS_OK;
+    return guarded([&] {
+        fhe::moddown_inplace(ctx->c, d_x, n_polys, level, nullptr, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_keyswitch(ckks_context* ctx, const uint64_t* d_x, uint32_t batch, uint32_t level, const uint64_t* d_evk,
+                   uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_x || !d_evk || !d_out) return fail(CKKS_EINVAL, "null buffer");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::keyswitch(ctx->c, d_x, batch, level, d_evk, nullptr, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_rescale(ckks_context* ctx, const uint64_t* d_in, uint32_t n_polys, uint32_t level, uint64_t* d_out,
+                 void* stream) {
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (level < 2) return fail(CKKS_EINVAL, "rescale needs level >= 2");
+    if (!d_in || !d_out || d_in == d_out) return fail(CKKS_EINVAL, "null or aliased buffer");
+    if (!n_polys) return CKKS_OK;
+    return guarded([&] {
+        fhe::rescale(ctx->c, d_in, n_polys, level, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_mult(ckks_context* ctx, const uint64_t* d_a, const uint64_t* d_b, uint32_t batch, uint32_t level,
+                   const uint64_t* d_evk, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_a || !d_b || !d_evk || !d_out) return fail(CKKS_EINVAL, "null buffer");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::hmult(ctx->c, d_a, d_b, batch, level, d_evk, d_out, false, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_mult_rescale(ckks_context* ctx, const uint64_t* d_a, const uint64_t* d_b, uint32_t batch,
+                           uint32_t level, const uint64_t* d_evk, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (level < 2) return fail(CKKS_EINVAL, "rescale needs level >= 2");
+    if (!d_a || !d_b || !d_evk || !d_out) return fail(CKKS_EINVAL, "null buffer");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::hmult(ctx->c, d_a, d_b, batch, level, d_evk, d_out, true, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_add(ckks_context* ctx, const uint64_t* d_x, const uint64_t* d_y, uint32_t n_polys, uint32_t level,
+                  uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_x || !d_y || !d_out) return fail(CKKS_EINVAL, "null buffer");
+    if (!n_polys) return CKKS_OK;
+    return guarded([&] {
+        fhe::add(ctx->c, d_x, d_y, d_out, n_polys, level, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+uint32_t ckks_rotation_index(int64_t step) { return rot_index(step); }
+
+int ckks_automorphism(ckks_context* ctx, const uint64_t* d_in, uint32_t n_polys, uint32_t level, uint32_t g,
+                      uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_in || !d_out || d_in == d_out) return fail(CKKS_EINVAL, "null or aliased buffer");
+    if (!n_polys) return CKKS_OK;
+    return guarded([&] {
+        fhe::automorph(ctx->c, d_in, d_out, n_polys, level, g, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_rotate(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level, int64_t step,
+                     const uint64_t* d_evk, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_ct || !d_evk || !d_out || d_ct == d_out) return fail(CKKS_EINVAL, "null or aliased buffer");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::rotate(ctx->c, d_ct, batch, level, rot_index(step), d_evk, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
 }
 
 }  // extern "C"

@@ -1,0 +1,334 @@
+// ops.cpp -- composition of the hot path out of the kernels: hybrid key switching (ModUp -> evk
+// inner product -> ModDown), rescale, HMult + relinearize + rescale, rotation.  Host code only: it
+// builds the per-level plans (BConv constant tables, NTT job lists), owns the workspace and issues
+// the launches on one stream.
+//
+// Semantics follow OpenFHE's HYBRID key switching and CKKS rescale as the reference uses them
+// (FIDESlib/OpenFHE calls of hpc_gpu_port/gpu_real_model.cu; key layout seeded_keys.hpp:216-256;
+// centered lift harness/boot_overflow_probe.cpp:93-94): at level l the Q limbs 0..l-1 split into
+// digits of alpha = ceil(L/dnum) limbs, digit d = [d*alpha, min((d+1)*alpha, l)); each digit is
+// brought to coefficients, switched by the approximate CRT (no correction of the overflow
+// multiple of the digit modulus) to every other limb of Q_l * P, and taken back to evaluation form.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <stdexcept>
+#include <string>
+
+#include "engine.hpp"
+#include "ops.hpp"
+
+namespace fhe {
+
+uint64_t mulmod_h(uint64_t a, uint64_t b, uint64_t q);
+uint64_t invmod_h(uint64_t a, uint64_t q);
+
+hipError_t launch_tensor(const Context& ctx, const uint64_t* a, const uint64_t* b, uint64_t* d01, uint64_t* d2,
+                         uint32_t B, uint32_t l, uint64_t* d2e, uint64_t d2e_bstride, const uint32_t* ext_off,
+                         hipStream_t st);
+hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_t* in, uint64_t in_bstride,
+                        const uint32_t* in_off, uint64_t* out, uint64_t out_bstride, const uint32_t* out_off,
+                        uint32_t B, hipStream_t st);
+hipError_t launch_ks_inner(const Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* acc, uint32_t B,
+                           uint32_t l, hipStream_t st);
+hipError_t launch_sub_scale(const Context& ctx, const uint64_t* x, uint64_t x_pstride, const uint64_t* y,
+                            uint64_t y_pstride, const uint64_t* add, uint64_t add_pstride, uint32_t add_div,
+                            uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
+                            hipStream_t st);
+hipError_t launch_lift_centered(const Context& ctx, const uint64_t* last, uint64_t last_pstride, uint64_t* tmp,
+                                uint32_t n_polys, uint32_t n_out, uint64_t ql, hipStream_t st);
+hipError_t launch_add(const Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys,
+                      uint32_t l, hipStream_t st);
+hipError_t launch_automorph(const uint64_t* in, uint64_t* out, uint32_t n_polys, uint32_t l, uint32_t g,
+                            hipStream_t st);
+
+namespace {
+
+constexpr size_t W = kN;  // words per limb
+
+#define HIPX(expr)                                                                      \
+    do {                                                                                \
+        hipError_t _e = (expr);                                                         \
+        if (_e != hipSuccess)                                                           \
+            throw std::runtime_error(std::string(#expr) + ": " + hipGetErrorString(_e)); \
+    } while (0)
+
+uint64_t shoup_companion(uint64_t w, uint64_t q) { return (uint64_t)(((unsigned __int128)w << 64) / q); }
+
+// regular JobSpec over a dense [n_polys][period][N] buffer whose limb t uses prime pmap[t]
+JobSpec regular_jobs(uint32_t n_polys, const std::vector<uint32_t>& pmap) {
+    JobSpec js{};
+    js.jobs = nullptr;
+    js.n_polys = n_polys;
+    js.period = (uint32_t)pmap.size();
+    for (size_t i = 0; i < pmap.size(); i++) js.pmap[i] = (uint8_t)pmap[i];
+    return js;
+}
+
+// explicit job list, stored once per key; ordered prime-major (jobs sharing a twiddle table adjacent)
+const Job* cached_jobs(Context& ctx, const std::string& key, std::vector<Job> jobs) {
+    auto it = ctx.job_cache.find(key);
+    if (it != ctx.job_cache.end()) return it->second;
+    std::stable_sort(jobs.begin(), jobs.end(), [](const Job& a, const Job& b) { return a.prime < b.prime; });
+    Job* d = nullptr;
+    HIPX(hipMalloc(&d, std::max<size_t>(1, jobs.size()) * sizeof(Job)));
+    HIPX(hipMemcpy(d, jobs.data(), jobs.size() * sizeof(Job), hipMemcpyHostToDevice));
+    ctx.job_cache[key] = d;
+    return d;
+}
+
+JobSpec list_jobs(const Job* d) {
+    JobSpec js{};
+    js.jobs = d;
+    return js;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ workspace
+void* ws_get(Context& ctx, uint32_t slot, size_t bytes) {
+    if (ctx.scratch.size() <= slot) ctx.scratch.resize(slot + 1, {nullptr, 0});
+    auto& s = ctx.scratch[slot];
+    if (s.second < bytes) {
+        if (s.first) HIPX(hipFree(s.first));
+        s.first = nullptr;
+        s.second = 0;
+        HIPX(hipMalloc(&s.first, bytes));
+        s.second = bytes;
+    }
+    return s.first;
+}
+
+// ------------------------------------------------------------------ BConv plans
+const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, const std::vector<uint32_t>& out_idx) {
+    std::string key = "b";
+    for (auto i : in_idx) key += ":" + std::to_string(i);
+    key += ">";
+    for (auto j : out_idx) key += ":" + std::to_string(j);
+    auto it = ctx.bconv_cache.find(key);
+    if (it != ctx.bconv_cache.end()) return it->second;
+    BConvPlan p;
+    p.n_in = (uint32_t)in_idx.size();
+    p.n_out = (uint32_t)out_idx.size();
+    p.in_idx = in_idx;
+    p.out_idx = out_idx;
+    std::vector<uint64_t> tab(2 * p.n_in + (size_t)p.n_in * p.n_out);
+    for (uint32_t i = 0; i < p.n_in; i++) {
+        const uint64_t qi = ctx.moduli[in_idx[i]];
+        uint64_t prod = 1;
+        for (uint32_t k = 0; k < p.n_in; k++)
+            if (k != i) prod = mulmod_h(prod, ctx.moduli[in_idx[k]] % qi, qi);
+        const uint64_t inv = invmod_h(prod, qi);
+        tab[2 * i] = inv;
+        tab[2 * i + 1] = shoup_companion(inv, qi);
+        for (uint32_t j = 0; j < p.n_out; j++) {
+            const uint64_t pj = ctx.moduli[out_idx[j]];
+            uint64_t m = 1;
+            for (uint32_t k = 0; k < p.n_in; k++)
+                if (k != i) m = mulmod_h(m, ctx.moduli[in_idx[k]] % pj, pj);
+            tab[2 * p.n_in + (size_t)i * p.n_out + j] = m;
+        }
+    }
+    HIPX(hipMalloc(&p.d_tab, tab.size() * 8));
+    HIPX(hipMemcpy(p.d_tab, tab.data(), tab.size() * 8, hipMemcpyHostToDevice));
+    return ctx.bconv_cache.emplace(key, std::move(p)).first->second;
+}
+
+// ------------------------------------------------------------------ level geometry
+uint32_t num_digits(const Context& ctx, uint32_t l) { return (l + ctx.alpha - 1) / ctx.alpha; }
+
+static uint32_t ext_prime(const Context& ctx, uint32_t l, uint32_t t) { return t < l ? t : ctx.L + (t - l); }
+
+static void check_level(const Context& ctx, uint32_t l) {
+    if (l == 0 || l > ctx.L) throw std::invalid_argument("level (limb count) out of range");
+    if (num_digits(ctx, l) > 8) throw std::invalid_argument("more than 8 digits");
+}
+
+// ------------------------------------------------------------------ ModUp
+// x2c: [B][l][N] coefficient form (INTT already applied) of the polynomial to extend;
+// ext: [B][D][E][N] whose digit-own limbs already hold the evaluation form.  Fills the rest.
+void modup_from_coef(Context& ctx, const uint64_t* x2c, uint64_t* ext, uint32_t B, uint32_t l, hipStream_t st) {
+    const uint32_t D = num_digits(ctx, l), E = l + ctx.K, al = ctx.alpha;
+    std::vector<Job> jobs;
+    for (uint32_t d = 0; d < D; d++) {
+        const uint32_t lo = d * al, hi = std::min(lo + al, l);
+        std::vector<uint32_t> in_idx, in_off, out_idx, out_off;
+        for (uint32_t i = lo; i < hi; i++) {
+            in_idx.push_back(i);
+            in_off.push_back(i);
+        }
+        for (uint32_t t = 0; t < E; t++) {
+            if (t >= lo && t < hi) continue;
+            out_idx.push_back(ext_prime(ctx, l, t));
+            out_off.push_back(t);
+        }
+        const BConvPlan& plan = bconv_plan(ctx, in_idx, out_idx);
+        HIPX(launch_bconv(ctx, plan, x2c, (uint64_t)l * W, in_off.data(), ext + (size_t)d * E * W,
+                          (uint64_t)D * E * W, out_off.data(), B, st));
+        for (uint32_t b = 0; b < B; b++)
+            for (uint32_t j = 0; j < out_off.size(); j++)
+                jobs.push_back(Job{(b * D + d) * E + out_off[j], out_idx[j]});
+    }
+    const Job* dj = cached_jobs(ctx, "modup:" + std::to_string(B) + ":" + std::to_string(l), std::move(jobs));
+    const uint32_t n_jobs = B * D * (E) - B * l;  // every limb of every digit except the digit's own
+    HIPX(launch_ntt(ctx, ext, list_jobs(dj), n_jobs, false, ctx.ntt_mode, st));
+}
+
+// x: [B][l][N] evaluation form -> ext [B][D][E][N] evaluation form
+void modup(Context& ctx, const uint64_t* x, uint64_t* ext, uint32_t B, uint32_t l, hipStream_t st) {
+    check_level(ctx, l);
+    const uint32_t D = num_digits(ctx, l), E = l + ctx.K, al = ctx.alpha;
+    uint64_t* xc = (uint64_t*)ws_get(ctx, WS_X2C, (size_t)B * l * W * 8);
+    HIPX(hipMemcpyAsync(xc, x, (size_t)B * l * W * 8, hipMemcpyDeviceToDevice, st));
+    for (uint32_t d = 0; d < D; d++) {
+        const uint32_t lo = d * al, hi = std::min(lo + al, l);
+        HIPX(hipMemcpy2DAsync(ext + ((size_t)d * E + lo) * W, (size_t)D * E * W * 8, x + (size_t)lo * W,
+                              (size_t)l * W * 8, (size_t)(hi - lo) * W * 8, B, hipMemcpyDeviceToDevice, st));
+    }
+    std::vector<uint32_t> pm(l);
+    for (uint32_t i = 0; i < l; i++) pm[i] = i;
+    HIPX(launch_ntt(ctx, xc, regular_jobs(B, pm), B * l, true, ctx.ntt_mode, st));
+    modup_from_coef(ctx, xc, ext, B, l, st);
+}
+
+// ------------------------------------------------------------------ inner product
+void ks_inner(Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* acc, uint32_t B, uint32_t l,
+              hipStream_t st) {
+    check_level(ctx, l);
+    HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st));
+}
+
+// ------------------------------------------------------------------ ModDown
+// x: [n_polys][E][N] evaluation form over Q_l * P (P limbs are overwritten: they are transformed to
+// coefficients in place).  out: [n_polys][l][N] = (x_Q - BConv_{P->Q}(x_P)) * P^-1 (+ add).
+void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
+                     hipStream_t st, uint32_t add_div) {
+    check_level(ctx, l);
+    const uint32_t E = l + ctx.K, K = ctx.K;
+    if (K == 0) throw std::invalid_argument("ModDown needs special primes");
+    std::vector<Job> jobs;
+    for (uint32_t pc = 0; pc < n_polys; pc++)
+        for (uint32_t k = 0; k < K; k++) jobs.push_back(Job{pc * E + l + k, ctx.L + k});
+    const Job* dj = cached_jobs(ctx, "mdP:" + std::to_string(n_polys) + ":" + std::to_string(l), std::move(jobs));
+    HIPX(launch_ntt(ctx, x, list_jobs(dj), n_polys * K, true, ctx.ntt_mode, st));
+    std::vector<uint32_t> in_idx, in_off, out_idx, out_off;
+    for (uint32_t k = 0; k < K; k++) {
+        in_idx.push_back(ctx.L + k);
+        in_off.push_back(l + k);
+    }
+    for (uint32_t i = 0; i < l; i++) {
+        out_idx.push_back(i);
+        out_off.push_back(i);
+    }
+    const BConvPlan& plan = bconv_plan(ctx, in_idx, out_idx);
+    uint64_t* conv = (uint64_t*)ws_get(ctx, WS_CONV, (size_t)n_polys * l * W * 8);
+    HIPX(launch_bconv(ctx, plan, x, (uint64_t)E * W, in_off.data(), conv, (uint64_t)l * W, out_off.data(), n_polys,
+                      st));
+    HIPX(launch_ntt(ctx, conv, regular_jobs(n_polys, out_idx), n_polys * l, false, ctx.ntt_mode, st));
+    std::vector<TwPair> pinv(l);
+    for (uint32_t i = 0; i < l; i++) {
+        const uint64_t q = ctx.moduli[i];
+        uint64_t P = 1;
+        for (uint32_t k = 0; k < K; k++) P = mulmod_h(P, ctx.moduli[ctx.L + k] % q, q);
+        const uint64_t v = invmod_h(P, q);
+        pinv[i] = TwPair{v, shoup_companion(v, q)};
+    }
+    HIPX(launch_sub_scale(ctx, x, (uint64_t)E * W, conv, (uint64_t)l * W, add, (uint64_t)add_div * l * W, add_div, out,
+                          (uint64_t)l * W, n_polys, l, pinv.data(), st));
+}
+
+// ------------------------------------------------------------------ key switch
+// x: [B][l][N] eval; evk [dnum][2][L+K][N]; out2: [B][2][l][N] (+= add [B][2][l][N] if given)
+void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
+               uint64_t* out2, hipStream_t st, uint32_t add_div) {
+    check_level(ctx, l);
+    const uint32_t D = num_digits(ctx, l), E = l + ctx.K;
+    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)B * D * E * W * 8);
+    uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)B * 2 * E * W * 8);
+    modup(ctx, x, ext, B, l, st);
+    HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st));
+    moddown_inplace(ctx, acc, 2 * B, l, add, out2, st, add_div);
+}
+
+// ------------------------------------------------------------------ rescale
+// in: [n_polys][l][N] eval -> out: [n_polys][l-1][N] eval.  in may equal neither out nor workspace.
+void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uint64_t* out, hipStream_t st) {
+    if (l < 2 || l > ctx.L) throw std::invalid_argument("rescale needs 2 <= l <= L");
+    uint64_t* last = (uint64_t*)ws_get(ctx, WS_LAST, (size_t)n_polys * W * 8);
+    uint64_t* tmp = (uint64_t*)ws_get(ctx, WS_RTMP, (size_t)n_polys * (l - 1) * W * 8);
+    HIPX(hipMemcpy2DAsync(last, W * 8, in + (size_t)(l - 1) * W, (size_t)l * W * 8, W * 8, n_polys,
+                          hipMemcpyDeviceToDevice, st));
+    HIPX(launch_ntt(ctx, last, regular_jobs(n_polys, {l - 1}), n_polys, true, ctx.ntt_mode, st));
+    HIPX(launch_lift_centered(ctx, last, W, tmp, n_polys, l - 1, ctx.moduli[l - 1], st));
+    std::vector<uint32_t> pm(l - 1);
+    for (uint32_t i = 0; i + 1 < l; i++) pm[i] = i;
+    HIPX(launch_ntt(ctx, tmp, regular_jobs(n_polys, pm), n_polys * (l - 1), false, ctx.ntt_mode, st));
+    std::vector<TwPair> s(l - 1);
+    const uint64_t ql = ctx.moduli[l - 1];
+    for (uint32_t i = 0; i + 1 < l; i++) {
+        const uint64_t q = ctx.moduli[i];
+        const uint64_t v = invmod_h(ql % q, q);
+        s[i] = TwPair{v, shoup_companion(v, q)};
+    }
+    HIPX(launch_sub_scale(ctx, in, (uint64_t)l * W, tmp, (uint64_t)(l - 1) * W, nullptr, 0, 1, out,
+                          (uint64_t)(l - 1) * W, n_polys, l - 1, s.data(), st));
+}
+
+// ------------------------------------------------------------------ HMult + relinearize (+ rescale)
+// a, b: [B][2][l][N] eval -> out: [B][2][l-1][N] (rescaled) or [B][2][l][N] (do_rescale = false)
+void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l, const uint64_t* evk,
+           uint64_t* out, bool do_rescale, hipStream_t st) {
+    check_level(ctx, l);
+    const uint32_t D = num_digits(ctx, l), E = l + ctx.K;
+    uint64_t* d01 = (uint64_t*)ws_get(ctx, WS_D01, (size_t)B * 2 * l * W * 8);
+    uint64_t* x2c = (uint64_t*)ws_get(ctx, WS_X2C, (size_t)B * l * W * 8);
+    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)B * D * E * W * 8);
+    uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)B * 2 * E * W * 8);
+    // the tensor kernel writes d2 twice: into x2c (to be taken to coefficients) and, in evaluation
+    // form, straight into each digit's own limbs of the extension buffer
+    std::vector<uint32_t> ext_off(l);
+    for (uint32_t t = 0; t < l; t++) ext_off[t] = (t / ctx.alpha) * E + t;
+    HIPX(launch_tensor(ctx, a, b, d01, x2c, B, l, ext, (uint64_t)D * E * W, ext_off.data(), st));
+    std::vector<uint32_t> pm(l);
+    for (uint32_t i = 0; i < l; i++) pm[i] = i;
+    HIPX(launch_ntt(ctx, x2c, regular_jobs(B, pm), B * l, true, ctx.ntt_mode, st));
+    modup_from_coef(ctx, x2c, ext, B, l, st);
+    HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st));
+    if (!do_rescale) {
+        moddown_inplace(ctx, acc, 2 * B, l, d01, out, st, 1);
+        return;
+    }
+    uint64_t* relin = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)B * 2 * l * W * 8);
+    moddown_inplace(ctx, acc, 2 * B, l, d01, relin, st, 1);
+    rescale(ctx, relin, 2 * B, l, out, st);
+}
+
+// ------------------------------------------------------------------ rotation
+// ct: [B][2][l][N] -> out [B][2][l][N]: KS of c1 under evk_g, add c0, then X -> X^g on both polys
+void rotate(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, uint32_t g, const uint64_t* evk, uint64_t* out,
+            hipStream_t st) {
+    check_level(ctx, l);
+    if ((g & 1) == 0 || g >= 2 * kN) throw std::invalid_argument("automorphism index must be odd and < 2N");
+    uint64_t* c1 = (uint64_t*)ws_get(ctx, WS_C1, (size_t)B * l * W * 8);
+    uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)B * 2 * l * W * 8);
+    // c1 of every ciphertext, contiguous; c0 enters as the ModDown addend of output poly 0 only
+    HIPX(hipMemcpy2DAsync(c1, (size_t)l * W * 8, ct + (size_t)l * W, (size_t)2 * l * W * 8, (size_t)l * W * 8, B,
+                          hipMemcpyDeviceToDevice, st));
+    keyswitch(ctx, c1, B, l, evk, ct, ks, st, 2);
+    HIPX(launch_automorph(ks, out, 2 * B, l, g, st));
+}
+
+void add(Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys, uint32_t l,
+         hipStream_t st) {
+    if (l == 0 || l > ctx.L) throw std::invalid_argument("level out of range");
+    HIPX(launch_add(ctx, x, y, out, n_polys, l, st));
+}
+
+void automorph(Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n_polys, uint32_t l, uint32_t g,
+               hipStream_t st) {
+    (void)ctx;
+    if ((g & 1) == 0 || g >= 2 * kN) throw std::invalid_argument("automorphism index must be odd and < 2N");
+    HIPX(launch_automorph(in, out, n_polys, l, g, st));
+}
+
+}  // namespace fhe

@@ -1,0 +1,43 @@
+// ops.hpp -- host-side composition of the hot path (see ops.cpp).
+#pragma once
+#include "engine.hpp"
+
+namespace fhe {
+
+// workspace slots (grown on demand, owned by the context)
+enum WsSlot : uint32_t {
+    WS_X2C = 0,
+    WS_EXT,
+    WS_ACC,
+    WS_CONV,
+    WS_LAST,
+    WS_RTMP,
+    WS_D01,
+    WS_RELIN,
+    WS_C1,
+    WS_COUNT
+};
+
+void* ws_get(Context& ctx, uint32_t slot, size_t bytes);
+const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, const std::vector<uint32_t>& out_idx);
+uint32_t num_digits(const Context& ctx, uint32_t l);
+
+void modup(Context& ctx, const uint64_t* x, uint64_t* ext, uint32_t B, uint32_t l, hipStream_t st);
+void ks_inner(Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* acc, uint32_t B, uint32_t l,
+              hipStream_t st);
+// add (optional): applied to output polys pc with pc % add_div == 0, at add + (pc / add_div) * add_div * l * N
+void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
+                     hipStream_t st, uint32_t add_div = 1);
+void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
+               uint64_t* out2, hipStream_t st, uint32_t add_div = 1);
+void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uint64_t* out, hipStream_t st);
+void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l, const uint64_t* evk,
+           uint64_t* out, bool do_rescale, hipStream_t st);
+void rotate(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, uint32_t g, const uint64_t* evk, uint64_t* out,
+            hipStream_t st);
+void add(Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys, uint32_t l,
+         hipStream_t st);
+void automorph(Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n_polys, uint32_t l, uint32_t g,
+               hipStream_t st);
+
+}  // namespace fhe

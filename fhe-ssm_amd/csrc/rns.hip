@@ -1,0 +1,300 @@
+// rns.hip -- limb-wise kernels of the RNS-CKKS core: tensor product, approximate CRT basis
+// conversion (BConv, the heart of ModUp / ModDown), the key-switch inner product, the ModDown and
+// rescale combines, the centered lift of rescale, additions and the evaluation-form automorphism.
+//
+// All of these are HBM-streaming elementwise kernels: one thread per coefficient index k, limbs
+// walked in registers, residues canonical in [0, q) on every store.  Products that are not by a
+// per-limb constant accumulate in 128 bits and reduce once (Barrett, mu = floor(2^128 / q)); products
+// by a per-limb constant use Shoup with a precomputed companion.
+#include "engine.hpp"
+#include "modarith.hpp"
+
+namespace fhe {
+
+namespace {
+
+__device__ __forceinline__ Barrett barrett_of(const PrimeInfo& p) { return Barrett{p.q, p.mu_hi, p.mu_lo}; }
+
+__device__ __forceinline__ uint64_t reduce_u128(const U128& x, const Barrett& b) {
+    // hi may exceed q when several products were summed; fold it once (hi < 2^6 q in our uses)
+    uint64_t hi = x.hi;
+    if (hi >= b.q) hi = hi % b.q;
+    return reduce128(hi, x.lo, b);
+}
+
+// ------------------------------------------------------------------ tensor product
+// a, b: [B][2][l][N]; d01: [B][2][l][N] (d0, d1); d2: [B][l][N]; d2e (optional): second copy of d2
+// scattered into the ModUp extension buffer: limb t of ciphertext c goes to d2e + c*d2e_bstride +
+// ext_off[t]*N.
+struct TensorArgs {
+    uint32_t l, B;
+    uint64_t* d2e;
+    uint64_t d2e_bstride;
+    uint32_t ext_off[kMaxPmap];
+};
+
+__global__ __launch_bounds__(256) void k_tensor(const uint64_t* __restrict__ a, const uint64_t* __restrict__ b,
+                                                uint64_t* __restrict__ d01, uint64_t* __restrict__ d2,
+                                                TensorArgs ta, const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t t = blockIdx.y, c = blockIdx.z;
+    const Barrett br = barrett_of(primes[t]);
+    const size_t P = (size_t)ta.l * kN;
+    const size_t o = (size_t)c * 2 * P + (size_t)t * kN + k;
+    const uint64_t a0 = a[o], a1 = a[o + P], b0 = b[o], b1 = b[o + P];
+    U128 s0{0, 0}, s1{0, 0}, s2{0, 0};
+    mac128(s0, a0, b0);
+    mac128(s1, a0, b1);
+    mac128(s1, a1, b0);
+    mac128(s2, a1, b1);
+    d01[o] = reduce_u128(s0, br);
+    d01[o + P] = reduce_u128(s1, br);
+    const uint64_t v2 = reduce_u128(s2, br);
+    d2[(size_t)c * P + (size_t)t * kN + k] = v2;
+    if (ta.d2e) ta.d2e[c * ta.d2e_bstride + (size_t)ta.ext_off[t] * kN + k] = v2;
+}
+
+// ------------------------------------------------------------------ BConv
+// out_j[k] = sum_i [x_i[k] * qhinv_i]_{q_i} * qhmod[i][j]  mod p_j
+// in  : batch c -> in + c*in_bstride, source limb i at in_off[i]*N, prime in_prime[i]
+// out : batch c -> out + c*out_bstride, target limb j at out_off[j]*N, prime out_prime[j]
+// tab : [n_in] TwPair (qhinv, companion) followed by [n_in][n_out] uint64 qhmod
+constexpr int kMaxBconvIn = 16;
+constexpr int kMaxBconvOut = 80;
+
+struct BConvArgs {
+    uint32_t n_in, n_out;
+    uint64_t in_bstride, out_bstride;
+    uint16_t in_off[kMaxBconvIn];
+    uint8_t in_prime[kMaxBconvIn];
+    uint16_t out_off[kMaxBconvOut];
+    uint8_t out_prime[kMaxBconvOut];
+};
+
+__global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
+                                               BConvArgs ba, const uint64_t* __restrict__ tab,
+                                               const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t c = blockIdx.y;
+    const uint64_t* src = in + c * ba.in_bstride + k;
+    uint64_t* dst = out + c * ba.out_bstride + k;
+    const TwPair* qhinv = reinterpret_cast<const TwPair*>(tab);
+    const uint64_t* qhmod = tab + 2 * ba.n_in;
+    uint64_t y[kMaxBconvIn];
+#pragma unroll
+    for (int i = 0; i < kMaxBconvIn; i++) {
+        if (i < (int)ba.n_in) {
+            const uint64_t q = primes[ba.in_prime[i]].q;
+            y[i] = shoup(src[(size_t)ba.in_off[i] * kN], qhinv[i].w, qhinv[i].wp, q);
+        }
+    }
+    for (uint32_t j = 0; j < ba.n_out; j++) {
+        const Barrett br = barrett_of(primes[ba.out_prime[j]]);
+        U128 acc{0, 0};
+#pragma unroll
+        for (int i = 0; i < kMaxBconvIn; i++)
+            if (i < (int)ba.n_in) mac128(acc, y[i], qhmod[(size_t)i * ba.n_out + j]);
+        dst[(size_t)ba.out_off[j] * kN] = reduce_u128(acc, br);
+    }
+}
+
+// ------------------------------------------------------------------ key-switch inner product
+// acc[c][0][t] = sum_d ext[c][d][t] * evk[d][0][prime(t)],  acc[c][1][t] = ... * evk[d][1][prime(t)]
+// One thread per (k, t); the evk words are loaded once and reused for every ciphertext of the batch.
+constexpr int kMaxDigits = 8;
+
+struct InnerArgs {
+    uint32_t D, E, T, B;
+    uint8_t prime_of[kMaxPmap];
+};
+
+__global__ __launch_bounds__(256) void k_ks_inner(const uint64_t* __restrict__ ext, const uint64_t* __restrict__ evk,
+                                                  uint64_t* __restrict__ acc, InnerArgs ia,
+                                                  const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t t = blockIdx.y;
+    const uint32_t p = ia.prime_of[t];
+    const Barrett br = barrett_of(primes[p]);
+    uint64_t kb[kMaxDigits], ka[kMaxDigits];
+#pragma unroll
+    for (int d = 0; d < kMaxDigits; d++) {
+        if (d < (int)ia.D) {
+            kb[d] = evk[(((size_t)d * 2 + 0) * ia.T + p) * kN + k];
+            ka[d] = evk[(((size_t)d * 2 + 1) * ia.T + p) * kN + k];
+        }
+    }
+    const size_t ext_b = (size_t)ia.D * ia.E * kN, acc_b = (size_t)2 * ia.E * kN;
+    for (uint32_t c = blockIdx.z; c < ia.B; c += gridDim.z) {
+        const uint64_t* x = ext + c * ext_b + (size_t)t * kN + k;
+        U128 s0{0, 0}, s1{0, 0};
+#pragma unroll
+        for (int d = 0; d < kMaxDigits; d++) {
+            if (d < (int)ia.D) {
+                const uint64_t v = x[(size_t)d * ia.E * kN];
+                mac128(s0, v, kb[d]);
+                mac128(s1, v, ka[d]);
+            }
+        }
+        uint64_t* o = acc + c * acc_b + (size_t)t * kN + k;
+        o[0] = reduce_u128(s0, br);
+        o[(size_t)ia.E * kN] = reduce_u128(s1, br);
+    }
+}
+
+// ------------------------------------------------------------------ ModDown / rescale combines
+// out[c][p][i] = (x[c][p][i] - y[c][p][i]) * s_i  (+ add[c][p][i])  mod q_i,   s_i per-limb constant
+// The addend, if any, is applied to the polys pc with pc % add_div == 0, read at add + (pc / add_div) *
+// add_pstride (add_div = 2 adds c0 of a ciphertext batch to poly 0 of each output ciphertext only).
+struct CombineArgs {
+    uint32_t l;                 // limbs per poly of out/y/add
+    uint32_t add_div;
+    uint64_t x_pstride;         // words between polys of x (x may carry extra limbs, e.g. P limbs)
+    uint64_t y_pstride, out_pstride, add_pstride;
+    TwPair s[kMaxPmap];
+};
+
+__global__ __launch_bounds__(256) void k_sub_scale(const uint64_t* __restrict__ x, const uint64_t* __restrict__ y,
+                                                   const uint64_t* __restrict__ add, uint64_t* __restrict__ out,
+                                                   CombineArgs ca, const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y, pc = blockIdx.z;  // pc = poly index over the batch
+    const uint64_t q = primes[i].q;
+    const size_t li = (size_t)i * kN + k;
+    const uint64_t d = sub_mod(x[pc * ca.x_pstride + li], y[pc * ca.y_pstride + li], q);
+    uint64_t v = shoup(d, ca.s[i].w, ca.s[i].wp, q);
+    if (add && pc % ca.add_div == 0) v = add_mod(v, add[(pc / ca.add_div) * ca.add_pstride + li], q);
+    out[pc * ca.out_pstride + li] = v;
+}
+
+// centered lift of the dropped limb (coefficient form) into limbs 0..l-2:
+// tmp[pc][i][k] = v > ql/2 ? v - ql (mod q_i) : v (mod q_i)
+__global__ __launch_bounds__(256) void k_lift_centered(const uint64_t* __restrict__ last, uint64_t last_pstride,
+                                                       uint64_t* __restrict__ tmp, uint32_t n_out, uint64_t ql,
+                                                       const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y, pc = blockIdx.z;
+    const uint64_t v = last[pc * last_pstride + k];
+    const uint64_t q = primes[i].q;
+    uint64_t r;
+    if (v > (ql >> 1)) {
+        const uint64_t neg = ql - v;  // value is -neg
+        const uint64_t m = neg >= q ? neg % q : neg;
+        r = m ? q - m : 0;
+    } else {
+        r = v >= q ? v % q : v;
+    }
+    tmp[((size_t)pc * n_out + i) * kN + k] = r;
+}
+
+// ------------------------------------------------------------------ elementwise helpers
+// out = x + y mod q over [n_polys][l][N] (limb i uses prime i)
+__global__ __launch_bounds__(256) void k_add(const uint64_t* __restrict__ x, const uint64_t* __restrict__ y,
+                                             uint64_t* __restrict__ out, uint32_t l,
+                                             const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y, pc = blockIdx.z;
+    const size_t o = ((size_t)pc * l + i) * kN + k;
+    out[o] = add_mod(x[o], y[o], primes[i].q);
+}
+
+// evaluation-form automorphism X -> X^g on [n_polys][l][N]: out[k] = in[src(k)],
+// src(k) = brev(((g (2 brev(k) + 1)) mod 2N - 1) / 2)
+__global__ __launch_bounds__(256) void k_automorph(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
+                                                   uint32_t g) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const size_t base = ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * kN;
+    const uint32_t e = (uint32_t)(((uint64_t)g * (2u * (__brev(k) >> (32 - kLogN)) + 1u)) & (2u * kN - 1u));
+    const uint32_t src = __brev((e - 1u) >> 1) >> (32 - kLogN);
+    out[base + k] = in[base + src];
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ launchers
+hipError_t launch_tensor(const Context& ctx, const uint64_t* a, const uint64_t* b, uint64_t* d01, uint64_t* d2,
+                         uint32_t B, uint32_t l, uint64_t* d2e, uint64_t d2e_bstride, const uint32_t* ext_off,
+                         hipStream_t st) {
+    TensorArgs ta{};
+    ta.l = l;
+    ta.B = B;
+    ta.d2e = d2e;
+    ta.d2e_bstride = d2e_bstride;
+    if (d2e)
+        for (uint32_t t = 0; t < l; t++) ta.ext_off[t] = ext_off[t];
+    hipLaunchKernelGGL(k_tensor, dim3(kN / 256, l, B), dim3(256), 0, st, a, b, d01, d2, ta, ctx.d_primes);
+    return hipGetLastError();
+}
+
+hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_t* in, uint64_t in_bstride,
+                        const uint32_t* in_off, uint64_t* out, uint64_t out_bstride, const uint32_t* out_off,
+                        uint32_t B, hipStream_t st) {
+    if (plan.n_in > (uint32_t)kMaxBconvIn || plan.n_out > (uint32_t)kMaxBconvOut) return hipErrorInvalidValue;
+    BConvArgs ba{};
+    ba.n_in = plan.n_in;
+    ba.n_out = plan.n_out;
+    ba.in_bstride = in_bstride;
+    ba.out_bstride = out_bstride;
+    for (uint32_t i = 0; i < plan.n_in; i++) {
+        ba.in_off[i] = (uint16_t)in_off[i];
+        ba.in_prime[i] = (uint8_t)plan.in_idx[i];
+    }
+    for (uint32_t j = 0; j < plan.n_out; j++) {
+        ba.out_off[j] = (uint16_t)out_off[j];
+        ba.out_prime[j] = (uint8_t)plan.out_idx[j];
+    }
+    hipLaunchKernelGGL(k_bconv, dim3(kN / 256, B), dim3(256), 0, st, in, out, ba, plan.d_tab, ctx.d_primes);
+    return hipGetLastError();
+}
+
+hipError_t launch_ks_inner(const Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* acc, uint32_t B,
+                           uint32_t l, hipStream_t st) {
+    InnerArgs ia{};
+    ia.E = l + ctx.K;
+    ia.D = (l + ctx.alpha - 1) / ctx.alpha;
+    ia.T = ctx.L + ctx.K;
+    ia.B = B;
+    if (ia.D > (uint32_t)kMaxDigits || ia.E > kMaxPmap) return hipErrorInvalidValue;
+    for (uint32_t t = 0; t < ia.E; t++) ia.prime_of[t] = (uint8_t)(t < l ? t : ctx.L + (t - l));
+    // split the batch over grid.z so that the grid has enough workgroups; each z-slice keeps its
+    // evk words in registers across its ciphertexts
+    const uint32_t zs = B < 8 ? B : 8;
+    hipLaunchKernelGGL(k_ks_inner, dim3(kN / 256, ia.E, zs), dim3(256), 0, st, ext, evk, acc, ia, ctx.d_primes);
+    return hipGetLastError();
+}
+
+hipError_t launch_sub_scale(const Context& ctx, const uint64_t* x, uint64_t x_pstride, const uint64_t* y,
+                            uint64_t y_pstride, const uint64_t* add, uint64_t add_pstride, uint32_t add_div,
+                            uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
+                            hipStream_t st) {
+    CombineArgs ca{};
+    ca.l = l;
+    ca.add_div = add_div ? add_div : 1;
+    ca.x_pstride = x_pstride;
+    ca.y_pstride = y_pstride;
+    ca.out_pstride = out_pstride;
+    ca.add_pstride = add_pstride;
+    for (uint32_t i = 0; i < l; i++) ca.s[i] = s[i];
+    hipLaunchKernelGGL(k_sub_scale, dim3(kN / 256, l, n_polys), dim3(256), 0, st, x, y, add, out, ca, ctx.d_primes);
+    return hipGetLastError();
+}
+
+hipError_t launch_lift_centered(const Context& ctx, const uint64_t* last, uint64_t last_pstride, uint64_t* tmp,
+                                uint32_t n_polys, uint32_t n_out, uint64_t ql, hipStream_t st) {
+    hipLaunchKernelGGL(k_lift_centered, dim3(kN / 256, n_out, n_polys), dim3(256), 0, st, last, last_pstride, tmp,
+                       n_out, ql, ctx.d_primes);
+    return hipGetLastError();
+}
+
+hipError_t launch_add(const Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys,
+                      uint32_t l, hipStream_t st) {
+    hipLaunchKernelGGL(k_add, dim3(kN / 256, l, n_polys), dim3(256), 0, st, x, y, out, l, ctx.d_primes);
+    return hipGetLastError();
+}
+
+hipError_t launch_automorph(const uint64_t* in, uint64_t* out, uint32_t n_polys, uint32_t l, uint32_t g,
+                            hipStream_t st) {
+    hipLaunchKernelGGL(k_automorph, dim3(kN / 256, l, n_polys), dim3(256), 0, st, in, out, g);
+    return hipGetLastError();
+}
+
+}  // namespace fhe

@@ -88,6 +88,46 @@ int ckks_ntt_forward(ckks_context* ctx, uint64_t* d_data, uint32_t n_polys, uint
 int ckks_ntt_inverse(ckks_context* ctx, uint64_t* d_data, uint32_t n_polys, uint32_t n_limbs,
                      const uint32_t* prime_idx, void* stream);
 
+/* ---- hybrid key switching (OpenFHE HYBRID, restated by FIDESlib's modup_ksk_moddown; the reference
+ * reaches it through every EvalMult / EvalRotate, gpu_real_model.cu:2762-2765,4627) ----------------
+ * Level l = number of active Q limbs.  D = ceil(l / alpha) digits, alpha = ceil(L / dnum); E = l + K.
+ * Extended layout [B][D][E][N]: limb t < l is Q limb t, t >= l is P limb t - l; evaluation form.
+ * ckks_modup      x [B][l][N] eval -> ext [B][D][E][N] eval
+ * ckks_ks_inner   ext, evk [dnum][2][L+K][N] -> acc [B][2][E][N]: acc[.][0] = sum_d ext_d * b_d, [1] with a_d
+ * ckks_moddown    x [n_polys][E][N] eval -> out [n_polys][l][N] = (x_Q - BConv_{P->Q}(x_P)) * P^-1;
+ *                 the P limbs of x are used as scratch (overwritten)
+ * ckks_keyswitch  x [B][l][N] -> out [B][2][l][N] (ModUp, inner product, ModDown of both polys) */
+int ckks_modup(ckks_context* ctx, const uint64_t* d_x, uint32_t batch, uint32_t level, uint64_t* d_ext, void* stream);
+int ckks_ks_inner(ckks_context* ctx, const uint64_t* d_ext, uint32_t batch, uint32_t level, const uint64_t* d_evk,
+                  uint64_t* d_acc, void* stream);
+int ckks_moddown(ckks_context* ctx, uint64_t* d_x, uint32_t n_polys, uint32_t level, uint64_t* d_out, void* stream);
+int ckks_keyswitch(ckks_context* ctx, const uint64_t* d_x, uint32_t batch, uint32_t level, const uint64_t* d_evk,
+                   uint64_t* d_out, void* stream);
+
+/* ---- evaluation operators (CryptoContext API mirror; ciphertexts are batches [B][2][l][N]) ---------
+ * ckks_rescale             RescaleInPlace: [n_polys][l][N] -> [n_polys][l-1][N] (drop the last limb,
+ *                          centered lift, * q_{l-1}^-1), in != out
+ * ckks_eval_mult           EvalMult(ct, ct) with relinearization: a, b -> out [B][2][l][N]
+ * ckks_eval_mult_rescale   EvalMult + RescaleInPlace fused: a, b -> out [B][2][l-1][N]
+ * ckks_eval_add            EvalAdd(ct, ct): elementwise over [n_polys][l][N]
+ * ckks_rotation_index      automorphism index of rotation step k: 5^k mod 2N (gpu_real_model.cu:1337-1360)
+ * ckks_automorphism        X -> X^g on [n_polys][l][N] evaluation form (a slot permutation), in != out
+ * ckks_eval_rotate         EvalRotate(ct, k) with the key of g = ckks_rotation_index(k):
+ *                          KS of c1, add c0, then X -> X^g on both polys; in != out */
+int ckks_rescale(ckks_context* ctx, const uint64_t* d_in, uint32_t n_polys, uint32_t level, uint64_t* d_out,
+                 void* stream);
+int ckks_eval_mult(ckks_context* ctx, const uint64_t* d_a, const uint64_t* d_b, uint32_t batch, uint32_t level,
+                   const uint64_t* d_evk, uint64_t* d_out, void* stream);
+int ckks_eval_mult_rescale(ckks_context* ctx, const uint64_t* d_a, const uint64_t* d_b, uint32_t batch,
+                           uint32_t level, const uint64_t* d_evk, uint64_t* d_out, void* stream);
+int ckks_eval_add(ckks_context* ctx, const uint64_t* d_x, const uint64_t* d_y, uint32_t n_polys, uint32_t level,
+                  uint64_t* d_out, void* stream);
+uint32_t ckks_rotation_index(int64_t step);
+int ckks_automorphism(ckks_context* ctx, const uint64_t* d_in, uint32_t n_polys, uint32_t level, uint32_t g,
+                      uint64_t* d_out, void* stream);
+int ckks_eval_rotate(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level, int64_t step,
+                     const uint64_t* d_evk, uint64_t* d_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,188 @@
+"""GPU parity of hybrid key switching, rescale, HMult+relin(+rescale), automorphism, rotation and add
+against the CPU oracle, through the C ABI.  BASELINE config-2 parameters: N = 2^16, L = 24 x 54-bit,
+K = 8 x 60-bit, dnum = 3.  Bar: bit-exact words.  Keys and ciphertexts are seeded uniform residues
+(every integer stage is a deterministic function of its input words, so random words exercise it
+fully; decryption-level checks with real keys are in test_gpu_ckks.py).
+"""
+import numpy as np
+import pytest
+
+from engine_loader import load_ckks
+
+pytestmark = pytest.mark.gpu
+
+L, K, DNUM = 24, 8, 3
+N = 1 << 16
+
+
+@pytest.fixture(scope="module")
+def ckks():
+    return load_ckks()
+
+
+@pytest.fixture(scope="module")
+def ctx(ckks):
+    return ckks.Context(num_q=L, num_p=K, dnum=DNUM, q_bits=54, p_bits=60)
+
+
+@pytest.fixture(scope="module")
+def octx(oracle, ctx):
+    return oracle.Ctx(16, ctx.moduli, L, K, DNUM)
+
+
+def residues(moduli, shape_prefix, prime_idx, seed):
+    rng = np.random.default_rng(seed)
+    q = np.array([moduli[i] for i in prime_idx], dtype=np.uint64)
+    x = rng.integers(0, 2**63, tuple(shape_prefix) + (len(prime_idx), N), dtype=np.uint64)
+    return x % q.reshape((1,) * len(shape_prefix) + (-1, 1))
+
+
+@pytest.fixture(scope="module")
+def evk(ctx):
+    return residues(ctx.moduli, (DNUM, 2), list(range(L + K)), seed=77)
+
+
+@pytest.fixture(scope="module")
+def d_evk(ckks, evk):
+    return ckks.DeviceBuffer.from_array(evk)
+
+
+def ext_primes(l):
+    return list(range(l)) + [L + k for k in range(K)]
+
+
+def test_modup_inner_moddown_stagewise(ckks, ctx, octx, evk, d_evk):
+    B, l = 2, 24
+    D, E = ctx.num_digits(l), l + K
+    x = residues(ctx.moduli, (B,), list(range(l)), seed=1)
+    dx = ckks.DeviceBuffer.from_array(x)
+    dext = ckks.DeviceBuffer(B * D * E * N * 8)
+    ctx.modup(dx.ptr, B, l, dext.ptr)
+    ext = dext.download((B, D, E, N))
+    for b in range(B):
+        assert np.array_equal(ext[b], octx.modup(x[b], l)), b
+    dacc = ckks.DeviceBuffer(B * 2 * E * N * 8)
+    ctx.ks_inner(dext.ptr, B, l, d_evk.ptr, dacc.ptr)
+    acc = dacc.download((B, 2, E, N))
+    for b in range(B):
+        assert np.array_equal(acc[b], octx.ks_inner(ext[b], l, evk)), b
+    dout = ckks.DeviceBuffer(B * 2 * l * N * 8)
+    ctx.moddown(dacc.ptr, 2 * B, l, dout.ptr)
+    out = dout.download((B, 2, l, N))
+    for b in range(B):
+        for p in range(2):
+            assert np.array_equal(out[b, p], octx.moddown(acc[b, p], l)), (b, p)
+
+
+@pytest.mark.parametrize("l", [24, 13, 8, 1])
+def test_keyswitch_levels(ckks, ctx, octx, evk, d_evk, l):
+    """every digit count (3, 2, 1) and a ragged last digit (13 = 8 + 5)"""
+    x = residues(ctx.moduli, (1,), list(range(l)), seed=10 + l)
+    dx = ckks.DeviceBuffer.from_array(x)
+    dout = ckks.DeviceBuffer(2 * l * N * 8)
+    ctx.keyswitch(dx.ptr, 1, l, d_evk.ptr, dout.ptr)
+    assert np.array_equal(dout.download((2, l, N)), octx.keyswitch(x[0], l, evk))
+
+
+@pytest.mark.parametrize("l", [24, 11, 2])
+def test_rescale(ckks, ctx, octx, l):
+    x = residues(ctx.moduli, (3,), list(range(l)), seed=20 + l)
+    dx = ckks.DeviceBuffer.from_array(x)
+    dout = ckks.DeviceBuffer(3 * (l - 1) * N * 8)
+    ctx.rescale(dx.ptr, 3, l, dout.ptr)
+    assert np.array_equal(dout.download((3, l - 1, N)), octx.rescale(x, l))
+    # the input is not modified
+    assert np.array_equal(dx.download(x.shape), x)
+
+
+def test_rescale_edge_values(ckks, ctx, octx):
+    """last limb at 0, q/2, q/2 + 1 and q - 1: both sides of the centered-lift threshold"""
+    l = 4
+    x = residues(ctx.moduli, (1,), list(range(l)), seed=5)
+    ql = ctx.moduli[l - 1]
+    coef = np.zeros(N, dtype=np.uint64)
+    coef[:4] = [0, ql // 2, ql // 2 + 1, ql - 1]
+    coef[4:] = (np.arange(N - 4, dtype=np.uint64) * np.uint64(7919)) % np.uint64(ql)
+    x[0, l - 1] = octx.ntt_fwd(coef[None], [l - 1])[0]
+    dx = ckks.DeviceBuffer.from_array(x)
+    dout = ckks.DeviceBuffer((l - 1) * N * 8)
+    ctx.rescale(dx.ptr, 1, l, dout.ptr)
+    assert np.array_equal(dout.download((1, l - 1, N)), octx.rescale(x, l))
+
+
+def test_eval_mult_rescale_batch(ckks, ctx, octx, evk, d_evk):
+    B, l = 2, 24
+    a = residues(ctx.moduli, (B, 2), list(range(l)), seed=31)
+    b = residues(ctx.moduli, (B, 2), list(range(l)), seed=32)
+    da, db = ckks.DeviceBuffer.from_array(a), ckks.DeviceBuffer.from_array(b)
+    dout = ckks.DeviceBuffer(B * 2 * (l - 1) * N * 8)
+    ctx.eval_mult_rescale(da.ptr, db.ptr, B, l, d_evk.ptr, dout.ptr)
+    out = dout.download((B, 2, l - 1, N))
+    for i in range(B):
+        assert np.array_equal(out[i], octx.hmult_relin_rescale(a[i], b[i], l, evk)), i
+
+
+def test_eval_mult_no_rescale(ckks, ctx, octx, evk, d_evk):
+    l = 9
+    a = residues(ctx.moduli, (1, 2), list(range(l)), seed=41)
+    b = residues(ctx.moduli, (1, 2), list(range(l)), seed=42)
+    da, db = ckks.DeviceBuffer.from_array(a), ckks.DeviceBuffer.from_array(b)
+    dout = ckks.DeviceBuffer(2 * l * N * 8)
+    ctx.eval_mult(da.ptr, db.ptr, 1, l, d_evk.ptr, dout.ptr)
+    d = octx.tensor(a[0], b[0], l)
+    ks = octx.keyswitch(d[2], l, evk)
+    q = np.array(ctx.moduli[:l], dtype=np.uint64)[:, None]
+    want = np.stack([(d[p].astype(object) + ks[p].astype(object)) % q.astype(object) for p in range(2)]).astype(np.uint64)
+    assert np.array_equal(dout.download((2, l, N)), want)
+
+
+@pytest.mark.parametrize("step", [1, 3, -7, 1024])
+def test_automorphism(ckks, ctx, octx, step):
+    l = 3
+    g = ckks.rotation_index(step)
+    assert g == octx.rot_index(step)
+    x = residues(ctx.moduli, (2,), list(range(l)), seed=50 + abs(step))
+    dx = ckks.DeviceBuffer.from_array(x)
+    dout = ckks.DeviceBuffer(x.nbytes)
+    ctx.automorphism(dx.ptr, 2, l, g, dout.ptr)
+    out = dout.download(x.shape)
+    for p in range(2):
+        assert np.array_equal(out[p], octx.automorph_eval(x[p], g))
+    # conjugation index 2N - 1
+    ctx.automorphism(dx.ptr, 2, l, 2 * N - 1, dout.ptr)
+    assert np.array_equal(dout.download(x.shape)[1], octx.automorph_eval(x[1], 2 * N - 1))
+
+
+@pytest.mark.parametrize("step", [5, -3])
+def test_eval_rotate(ckks, ctx, octx, evk, d_evk, step):
+    l = 16
+    ct = residues(ctx.moduli, (2, 2), list(range(l)), seed=60 + step)
+    dct = ckks.DeviceBuffer.from_array(ct)
+    dout = ckks.DeviceBuffer(ct.nbytes)
+    ctx.eval_rotate(dct.ptr, 2, l, step, d_evk.ptr, dout.ptr)
+    out = dout.download(ct.shape)
+    g = octx.rot_index(step)
+    for i in range(2):
+        assert np.array_equal(out[i], octx.rotate(ct[i], l, g, evk)), i
+
+
+def test_eval_add(ckks, ctx):
+    l = 5
+    x = residues(ctx.moduli, (4,), list(range(l)), seed=70)
+    y = residues(ctx.moduli, (4,), list(range(l)), seed=71)
+    dx, dy = ckks.DeviceBuffer.from_array(x), ckks.DeviceBuffer.from_array(y)
+    dout = ckks.DeviceBuffer(x.nbytes)
+    ctx.eval_add(dx.ptr, dy.ptr, 4, l, dout.ptr)
+    q = np.array(ctx.moduli[:l], dtype=np.uint64)[None, :, None]
+    want = ((x.astype(object) + y.astype(object)) % q.astype(object)).astype(np.uint64)
+    assert np.array_equal(dout.download(x.shape), want)
+
+
+def test_error_paths(ckks, ctx):
+    """bad levels and aliasing are refused with a status code, nothing is launched"""
+    lib = ckks.load()
+    assert lib.ckks_rescale(ctx.h, 1, 2, 1, 2, None) != 0
+    assert b"alias" in lib.ckks_last_error() or b"level" in lib.ckks_last_error()
+    assert lib.ckks_keyswitch(ctx.h, 1, 1, L + 1, 1, 1, None) == 1
+    assert b"level" in lib.ckks_last_error()
+    assert lib.ckks_eval_rotate(ctx.h, 8, 1, 4, 1, 8, 8, None) == 1
