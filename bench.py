@@ -1,15 +1,18 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X RNS-CKKS hot path; prints ONE JSON line.
 
-Workloads (all inputs seeded and resident in HBM before timing):
-  ntt    config 1: forward then inverse negacyclic NTT, N=2^16, 64 ct x 2 polys x 24 limbs of
-         54-bit primes.  One step = one forward + one inverse transform over the batch.
-         value = algorithmic GB/s = 6,492,782,592 B per step / step time.
+Workloads (inputs seeded and resident in HBM before the timed region):
+  hmult  config 2 (default): CKKS HMult + relinearize + rescale on 64 ciphertext pairs, N=2^16,
+         L=24 x 54-bit + K=8 x 60-bit, hybrid key switching dnum=3; ternary secret h=192, Gaussian
+         errors sigma=3.19, slots uniform in [-1,1] at scale 2^50.  One step = one batched
+         EvalMult+Rescale over the 64 pairs.  value = HMult+relin ops/s.
+  ntt    config 1: forward then inverse NTT over 64 ct x 2 polys x 24 limbs.  value = algorithmic GB/s.
 
-Roofline: the dominant kernel (the forward NTT launch) is timed with HIP events on the stream it is
-launched on; achieved = algorithmic bytes per launch / mean launch time, against the MI355X HBM peak.
-cpu_baseline: the repository's C oracle (OpenFHE-convention restatement, not OpenFHE) timed on the
-host cores over a bounded sample of the same workload, in the same unit.
+Roofline: the engine records HIP events on its launch stream around every kernel of one profiled
+step (ckks_profile_*); the dominant kernel by time is reported with achieved = algorithmic bytes per
+launch / mean launch time, against the MI355X HBM peak (8 TB/s).
+cpu_baseline: this repository's C oracle (an OpenFHE-convention restatement, not OpenFHE, which needs
+the network to build) timed on the host over a bounded sample of the same workload.
 """
 from __future__ import annotations
 
@@ -26,105 +29,209 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(REPO, "tests"))
 
 HBM_PEAK_GBS = 8000.0
-LIMB_BYTES = 65536 * 8
-TWIDDLE_BYTES_PER_PRIME = 65536 * 8 * 2  # psi table + Shoup companions (algorithmic count)
+N = 1 << 16
+LIMB_BYTES = N * 8
+TWIDDLE_BYTES_PER_PRIME = N * 16  # (w, w') pairs
+
+L2, K2, DNUM2 = 24, 8, 3
+N_PAIRS = 64
 
 
-def ntt_config():
-    L, n_ct = 24, 64
-    n_polys = 2 * n_ct
-    limbs = n_polys * L
-    bytes_dir = limbs * 2 * LIMB_BYTES + L * TWIDDLE_BYTES_PER_PRIME
-    return L, n_polys, limbs, bytes_dir
+def seed_bytes(tag: str, seed: int) -> bytes:
+    b = (tag.encode() + seed.to_bytes(8, "little")) * 4
+    return b[:32]
+
+
+def timed_steps(torch, stream, step, steps, warmup):
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    t0 = time.perf_counter()
+    ev[0].record(stream)
+    for i in range(steps):
+        step()
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    return wall, per
+
+
+def roofline_from_profile(rep: dict):
+    name, (n, ms, by) = max(rep.items(), key=lambda kv: kv[1][1])
+    achieved = by / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
+            "launches_in_profiled_step": n, "mean_launch_ms": round(ms / n, 4),
+            "algorithmic_bytes_per_launch": round(by / n)}
+
+
+def kernel_table(rep: dict):
+    return {k: {"launches": n, "total_ms": round(ms, 4), "GBps": round(by / (ms * 1e-3) / 1e9, 1)}
+            for k, (n, ms, by) in sorted(rep.items(), key=lambda kv: -kv[1][1])}
+
+
+# ----------------------------------------------------------------------------------------- config 2
+def bench_hmult(ckks, torch, steps, warmup, seed):
+    ctx = ckks.Context(num_q=L2, num_p=K2, dnum=DNUM2, q_bits=54, p_bits=60, scale=2.0**50)
+    scale = 2.0**50
+    sk = ctx.secret(seed_bytes("secret", seed), 192)
+    T = L2 + K2
+    dev = torch.device("cuda:0")
+    evk = torch.empty((DNUM2, 2, T, N), dtype=torch.int64, device=dev)
+    ctx.keygen_relin(sk, seed_bytes("relin-a", seed), seed_bytes("relin-e", seed), evk.data_ptr())
+    A = torch.empty((N_PAIRS, 2, L2, N), dtype=torch.int64, device=dev)
+    B = torch.empty_like(A)
+    OUT = torch.empty((N_PAIRS, 2, L2 - 1, N), dtype=torch.int64, device=dev)
+    pt = torch.empty((L2, N), dtype=torch.int64, device=dev)
+    rng = np.random.default_rng(seed)
+    msgs = {}
+    ct_bytes = 2 * L2 * N * 8
+    for i in range(2 * N_PAIRS):
+        z = rng.uniform(-1.0, 1.0, N // 2)
+        if i in (0, N_PAIRS, 1, N_PAIRS + 1):
+            msgs[i] = z
+        ctx.encode(z, L2, scale, pt.data_ptr())
+        dst = (A if i < N_PAIRS else B)
+        ctx.encrypt(sk, pt.data_ptr(), L2, seed_bytes("enc", seed), i,
+                    dst.data_ptr() + (i % N_PAIRS) * ct_bytes)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    sh = ctypes.c_void_p(stream.cuda_stream)
+
+    def step():
+        ctx.eval_mult_rescale(A.data_ptr(), B.data_ptr(), N_PAIRS, L2, evk.data_ptr(), OUT.data_ptr(), sh)
+
+    wall, per = timed_steps(torch, stream, step, steps, warmup)
+    step_ms = wall * 1e3 / steps
+    # decrypted check of the timed outputs: product of the inputs, scale Delta^2 / q_{L-1}
+    out_scale = scale * scale / ctx.moduli[L2 - 1]
+    errs = []
+    for i in (0, 1):
+        got = ctx.decrypt(sk, OUT.data_ptr() + i * 2 * (L2 - 1) * N * 8, L2 - 1, out_scale)
+        want = msgs[i] * msgs[N_PAIRS + i]
+        errs.append(float(np.sqrt(np.mean((got - want) ** 2)) / np.sqrt(np.mean(want ** 2))))
+    rel_err = max(errs)
+    if not rel_err < 1e-6:
+        raise SystemExit(f"HMult output does not decrypt to the product (relErrRms {rel_err:.3e}): invalid")
+    # one profiled step: per-kernel HIP events on the launch stream
+    ctx.profile_reset()
+    ctx.profile(True)
+    step()
+    torch.cuda.synchronize()
+    ctx.profile(False)
+    rep = ctx.profile_report()
+    ctx.profile_reset()
+    ops = N_PAIRS / (step_ms * 1e-3)
+    res = {
+        "metric": "HMult+relin ops/s at N=2^16",
+        "value": round(ops, 1),
+        "unit": "ops/s",
+        "ms_per_step": round(step_ms, 4),
+        "dtype": "u64",
+        "config": {"workload": "config2: HMult+relin+rescale, 64 ciphertext pairs, N=2^16, L=24x54-bit + "
+                               "K=8x60-bit, dnum=3, h=192, sigma=3.19, scale 2^50",
+                   "batch": N_PAIRS, "level_in": L2, "ntt_mode": "fused", "seed": seed,
+                   "step_ms_min": round(min(per), 4), "step_ms_max": round(max(per), 4)},
+        "check": {"decrypted_relErrRms_max": rel_err, "ciphertexts_checked": 2},
+        "kernels": kernel_table(rep),
+        "roofline": roofline_from_profile(rep),
+    }
+    return res
+
+
+def cpu_baseline_hmult(seed, budget_s=20.0):
+    """Oracle HMult+relin+rescale (single thread) on real-shaped random words of the config-2 context."""
+    from oracle import oracle as o
+    qs = o.gen_primes(54, L2, 2 * N)
+    ps = o.gen_primes(60, K2, 2 * N, exclude=qs)
+    octx = o.Ctx(16, qs + ps, L2, K2, DNUM2)
+    rng = np.random.default_rng(seed)
+    q = np.array(qs, dtype=np.uint64)[:, None]
+    T = L2 + K2
+    qp = np.array(qs + ps, dtype=np.uint64)[:, None]
+    evk = (rng.integers(0, 2**63, (DNUM2, 2, T, N), dtype=np.uint64) % qp[None, None])
+    done, t0 = 0, time.perf_counter()
+    while True:
+        a = rng.integers(0, 2**63, (2, L2, N), dtype=np.uint64) % q[None]
+        b = rng.integers(0, 2**63, (2, L2, N), dtype=np.uint64) % q[None]
+        octx.hmult_relin_rescale(a, b, L2, evk)
+        done += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or done >= 4:
+            break
+    return {"value": round(done / el, 4), "unit": "ops/s", "cores": 1, "kind": "port",
+            "sample": f"{done} HMult+relin+rescale of one config-2 pair ({el:.1f} s), C oracle, one thread"}
+
+
+# ----------------------------------------------------------------------------------------- config 1
+def ntt_bytes():
+    limbs = 2 * N_PAIRS * L2
+    return limbs, limbs * 2 * LIMB_BYTES + L2 * TWIDDLE_BYTES_PER_PRIME
 
 
 def bench_ntt(ckks, torch, steps, warmup, seed):
-    L, n_polys, limbs, bytes_dir = ntt_config()
-    ctx = ckks.Context(num_q=L, num_p=8, dnum=3, q_bits=54, p_bits=60)
-    prime_idx = list(range(L))
-    dev = torch.device("cuda:0")
-    # seeded residues, uniform in [0, q): generated on the host once, then uploaded
+    limbs, bytes_dir = ntt_bytes()
+    n_polys = 2 * N_PAIRS
+    ctx = ckks.Context(num_q=L2, num_p=K2, dnum=DNUM2, q_bits=54, p_bits=60)
+    prime_idx = list(range(L2))
     rng = np.random.default_rng(seed)
-    q = np.array(ctx.moduli[:L], dtype=np.uint64)
-    host = rng.integers(0, 2**63, (n_polys, L, 65536), dtype=np.uint64) % q[None, :, None]
-    data = torch.from_numpy(host.view(np.int64)).to(dev)
+    q = np.array(ctx.moduli[:L2], dtype=np.uint64)
+    host = rng.integers(0, 2**63, (n_polys, L2, N), dtype=np.uint64) % q[None, :, None]
+    data = torch.from_numpy(host.view(np.int64)).to("cuda:0")
+    first = host[0, 0].copy()
     del host
     stream = torch.cuda.current_stream()
     sh = ctypes.c_void_p(stream.cuda_stream)
     ptr = data.data_ptr()
 
-    def step(ev=None):
-        if ev is not None:
-            ev[0].record(stream)
+    def step():
         ctx.ntt_forward(ptr, n_polys, prime_idx, sh)
-        if ev is not None:
-            ev[1].record(stream)
         ctx.ntt_inverse(ptr, n_polys, prime_idx, sh)
-        if ev is not None:
-            ev[2].record(stream)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
-    t0 = time.perf_counter()
-    for i in range(steps):
-        step(evs[i])
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    fwd_ms = [e[0].elapsed_time(e[1]) for e in evs]
-    inv_ms = [e[1].elapsed_time(e[2]) for e in evs]
-    step_ms = wall * 1e3 / steps
-    # the data must still be a valid residue vector after fwd+inv pairs (identity)
-    back = data[:1, :1].cpu().numpy().view(np.uint64)
-    rng2 = np.random.default_rng(seed)
-    first = rng2.integers(0, 2**63, (1, 1, 65536), dtype=np.uint64) % q[None, :1, None]
-    if not np.array_equal(back, first):
+    wall, _ = timed_steps(torch, stream, step, steps, warmup)
+    if not np.array_equal(data[0, 0].cpu().numpy().view(np.uint64), first):
         raise SystemExit("NTT round trip changed the data: results invalid")
-    fwd = float(np.mean(fwd_ms))
-    inv = float(np.mean(inv_ms))
-    value = 2 * bytes_dir / (step_ms * 1e-3) / 1e9
-    achieved = bytes_dir / (fwd * 1e-3) / 1e9
-    res = {
+    ctx.profile_reset()
+    ctx.profile(True)
+    step()
+    torch.cuda.synchronize()
+    ctx.profile(False)
+    rep = ctx.profile_report()
+    step_ms = wall * 1e3 / steps
+    return {
         "metric": "NTT HBM GB/s (algorithmic bytes, forward+inverse, N=2^16)",
-        "value": round(value, 2),
+        "value": round(2 * bytes_dir / (step_ms * 1e-3) / 1e9, 2),
         "unit": "GB/s",
         "ms_per_step": round(step_ms, 4),
         "dtype": "u64",
         "config": {"workload": "config1: fwd+inv negacyclic NTT, N=2^16, 64 ct x 2 polys x L=24 54-bit limbs",
                    "limbs_per_direction": limbs, "algorithmic_bytes_per_direction": bytes_dir,
                    "ntt_mode": "fused", "seed": seed},
-        "kernels": {"ntt_fwd_ms": round(fwd, 4), "ntt_inv_ms": round(inv, 4),
-                    "ntt_fwd_GBps": round(achieved, 1),
-                    "ntt_inv_GBps": round(bytes_dir / (inv * 1e-3) / 1e9, 1)},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_ntt_fwd_fused"},
+        "kernels": kernel_table(rep),
+        "roofline": roofline_from_profile(rep),
     }
-    return res, ctx
 
 
 def cpu_baseline_ntt(seed, budget_s=12.0):
-    """Oracle NTT forward+inverse over a bounded sample of config-1 limbs, OpenMP over host cores."""
     from oracle import oracle as o
-    L, _, _, bytes_dir = ntt_config()
-    qs = o.gen_primes(54, L, 2**17)
-    ctx = o.Ctx(16, qs, L, 0, 1)
+    limbs_total, bytes_dir = ntt_bytes()
+    qs = o.gen_primes(54, L2, 2 * N)
+    octx = o.Ctx(16, qs, L2, 0, 1)
     cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     rng = np.random.default_rng(seed)
     q = np.array(qs, dtype=np.uint64)
-    n_polys = 2
-    x = rng.integers(0, 2**63, (n_polys, L, 65536), dtype=np.uint64) % q[None, :, None]
+    x = rng.integers(0, 2**63, (2, L2, N), dtype=np.uint64) % q[None, :, None]
     done, t0 = 0, time.perf_counter()
     while True:
-        y = ctx.ntt_fwd(x, list(range(L)))
-        ctx.ntt_inv(y, list(range(L)))
-        done += n_polys * L
+        y = octx.ntt_fwd(x, list(range(L2)))
+        octx.ntt_inv(y, list(range(L2)))
+        done += 2 * L2
         el = time.perf_counter() - t0
-        if el > budget_s or done >= 3072:
+        if el > budget_s or done >= limbs_total:
             break
-    per_limb_dir = bytes_dir / 3072
-    gbs = done * 2 * per_limb_dir / el / 1e9
+    gbs = done * 2 * (bytes_dir / limbs_total) / el / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
             "sample": f"{done} limbs fwd+inv of the config-1 batch ({el:.1f} s), C oracle with OpenMP"}
 
@@ -132,11 +239,12 @@ def cpu_baseline_ntt(seed, budget_s=12.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="ntt", choices=["ntt"])
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", default="hmult", choices=["hmult", "ntt"])
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ntt-line", action="store_true", help="skip the config-1 NTT figure in the hmult run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design note, "
@@ -147,14 +255,28 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     ckks = load_ckks()
-    res, _ = bench_ntt(ckks, torch, args.steps, args.warmup, args.seed)
+    if args.workload == "hmult":
+        res = bench_hmult(ckks, torch, args.steps, args.warmup, args.seed)
+        extra = {}
+        if not args.no_ntt_line:
+            n = bench_ntt(ckks, torch, max(3, args.steps // 2), 1, args.seed)
+            extra["ntt_config1"] = {"GBps": n["value"], "ms_per_step": n["ms_per_step"],
+                                    "roofline": n["roofline"]}
+        cpu = None if args.no_cpu_baseline else cpu_baseline_hmult(args.seed)
+    else:
+        res = bench_ntt(ckks, torch, args.steps, args.warmup, args.seed)
+        extra = {}
+        cpu = None if args.no_cpu_baseline else cpu_baseline_ntt(args.seed)
     out = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
-           "data": "synthetic (seeded uniform residues)", "config": res["config"],
-           "kernels": res["kernels"], "roofline": res["roofline"]}
-    if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline_ntt(args.seed)
+           "data": "synthetic (seeded)", "config": res["config"], "roofline": res["roofline"],
+           "kernels": res["kernels"]}
+    if "check" in res:
+        out["check"] = res["check"]
+    out.update(extra)
+    if cpu is not None:
+        out["cpu_baseline"] = cpu
     print(json.dumps(out), flush=True)
 
 

@@ -56,6 +56,17 @@ SIGNATURES = {
     "ckks_rotation_index": (_u32, [ctypes.c_int64]),
     "ckks_automorphism": (_int, [_vp, _vp, _u32, _u32, _u32, _vp, _vp]),
     "ckks_eval_rotate": (_int, [_vp, _vp, _u32, _u32, ctypes.c_int64, _vp, _vp, _vp]),
+    "ckks_secret_generate": (_int, [_vp, _vp, _u32, ctypes.POINTER(_vp)]),
+    "ckks_secret_destroy": (None, [_vp]),
+    "ckks_secret_coeffs": (_int, [_vp, _vp, _u32]),
+    "ckks_keygen_relin": (_int, [_vp, _vp, _vp, _vp, _vp]),
+    "ckks_keygen_automorphism": (_int, [_vp, _vp, _u32, _vp, _vp, _vp]),
+    "ckks_encode": (_int, [_vp, _vp, _vp, _u32, _u32, ctypes.c_double, _vp]),
+    "ckks_encrypt": (_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp]),
+    "ckks_decrypt_decode": (_int, [_vp, _vp, _vp, _u32, ctypes.c_double, _vp, _vp, _u32]),
+    "ckks_profile_enable": (_int, [_vp, _int]),
+    "ckks_profile_reset": (_int, [_vp]),
+    "ckks_profile_query": (_int, [_vp, _u32, ctypes.c_char_p, _u32, _vp, _vp, _vp]),
 }
 
 
@@ -217,6 +228,84 @@ class Context:
 
     def eval_rotate(self, d_ct, batch, level, step, d_evk, d_out, stream=None):
         check(load().ckks_eval_rotate(self.h, d_ct, batch, level, step, d_evk, d_out, stream))
+
+
+    # client side ------------------------------------------------------------------------------
+    def secret(self, seed: bytes, hamming_weight: int = 192) -> "Secret":
+        return Secret(self, seed, hamming_weight)
+
+    def keygen_relin(self, sk, seed: bytes, eseed: bytes, d_evk) -> None:
+        check(load().ckks_keygen_relin(self.h, sk.h, _seed(seed), _seed(eseed), d_evk))
+
+    def keygen_automorphism(self, sk, g: int, seed: bytes, eseed: bytes, d_evk) -> None:
+        check(load().ckks_keygen_automorphism(self.h, sk.h, g, _seed(seed), _seed(eseed), d_evk))
+
+    def encode(self, values, level: int, scale: float, d_pt) -> None:
+        v = np.asarray(values)
+        re = np.ascontiguousarray(v.real, dtype=np.float64)
+        im = np.ascontiguousarray(v.imag, dtype=np.float64) if np.iscomplexobj(v) else None
+        check(load().ckks_encode(self.h, _ptr(re), _ptr(im) if im is not None else None, len(re), level, scale,
+                                 d_pt))
+
+    def encrypt(self, sk, d_pt, level: int, seed: bytes, index: int, d_ct) -> None:
+        check(load().ckks_encrypt(self.h, sk.h, d_pt, level, _seed(seed), index, d_ct))
+
+    def decrypt(self, sk, d_ct, level: int, scale: float, n_slots: int = 1 << 15, complex_out: bool = False):
+        re = np.zeros(n_slots, dtype=np.float64)
+        im = np.zeros(n_slots, dtype=np.float64)
+        check(load().ckks_decrypt_decode(self.h, sk.h, d_ct, level, scale, _ptr(re), _ptr(im), n_slots))
+        return re + 1j * im if complex_out else re
+
+    # profiling ---------------------------------------------------------------------------------
+    def profile(self, on: bool) -> None:
+        check(load().ckks_profile_enable(self.h, 1 if on else 0))
+
+    def profile_reset(self) -> None:
+        check(load().ckks_profile_reset(self.h))
+
+    def profile_report(self) -> dict:
+        """{kernel name: (launches, total_ms, total_algorithmic_bytes)}"""
+        out = {}
+        i = 0
+        name = ctypes.create_string_buffer(64)
+        while True:
+            n, ms, by = ctypes.c_uint64(), ctypes.c_double(), ctypes.c_double()
+            rc = load().ckks_profile_query(self.h, i, name, 64, ctypes.byref(n), ctypes.byref(ms), ctypes.byref(by))
+            if rc != CKKS_OK:
+                break
+            out[name.value.decode()] = (n.value, ms.value, by.value)
+            i += 1
+        return out
+
+
+def _seed(seed: bytes):
+    b = bytes(seed)
+    assert len(b) == 32
+    return ctypes.c_char_p(b)
+
+
+class Secret:
+    def __init__(self, ctx: Context, seed: bytes, hamming_weight: int):
+        h = _vp()
+        check(load().ckks_secret_generate(ctx.h, _seed(seed), hamming_weight, ctypes.byref(h)))
+        self.h = h.value
+        self.ctx = ctx
+
+    def coeffs(self) -> np.ndarray:
+        out = np.zeros(1 << 16, dtype=np.int8)
+        check(load().ckks_secret_coeffs(self.h, _ptr(out), len(out)))
+        return out
+
+    def close(self):
+        if self.h:
+            load().ckks_secret_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def rotation_index(step: int) -> int:

@@ -6,7 +6,10 @@
 #include <exception>
 #include <string>
 
+#include <map>
+
 #include "ckks_engine.h"
+#include "client.hpp"
 #include "engine.hpp"
 #include "ops.hpp"
 
@@ -19,6 +22,11 @@ void context_release(Context& c);
 
 struct ckks_context {
     fhe::Context c;
+};
+
+struct ckks_secret {
+    fhe::Secret* s;
+    const ckks_context* owner;
 };
 
 namespace {
@@ -326,6 +334,140 @@ int ckks_eval_rotate(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, ui
         fhe::rotate(ctx->c, d_ct, batch, level, rot_index(step), d_evk, d_out, (hipStream_t)stream);
         return CKKS_OK;
     });
+}
+
+int ckks_secret_generate(ckks_context* ctx, const uint8_t* seed32, uint32_t hamming_weight, ckks_secret** out) {
+    if (!ctx || !seed32 || !out) return fail(CKKS_EINVAL, "null argument");
+    if (hamming_weight == 0 || hamming_weight > fhe::kN) return fail(CKKS_EINVAL, "hamming weight out of range");
+    return guarded([&] {
+        auto* sk = new ckks_secret{nullptr, ctx};
+        try {
+            sk->s = fhe::secret_create(ctx->c, seed32, hamming_weight);
+        } catch (...) {
+            delete sk;
+            throw;
+        }
+        *out = sk;
+        return CKKS_OK;
+    });
+}
+
+void ckks_secret_destroy(ckks_secret* sk) {
+    if (!sk) return;
+    fhe::secret_destroy(sk->s);
+    delete sk;
+}
+
+int ckks_secret_coeffs(const ckks_secret* sk, int8_t* out, uint32_t n) {
+    if (!sk || !out) return fail(CKKS_EINVAL, "null argument");
+    if (n < fhe::kN) return fail(CKKS_EINVAL, "buffer too small");
+    std::memcpy(out, sk->s->coeffs.data(), fhe::kN);
+    return CKKS_OK;
+}
+
+static int check_secret(const ckks_context* ctx, const ckks_secret* sk) {
+    if (!ctx || !sk) return fail(CKKS_EINVAL, "null context or secret");
+    if (sk->owner != ctx) return fail(CKKS_EINVAL, "secret belongs to another context");
+    return CKKS_OK;
+}
+
+int ckks_keygen_relin(ckks_context* ctx, const ckks_secret* sk, const uint8_t* seed32, const uint8_t* eseed32,
+                      uint64_t* d_evk) {
+    if (int rc = check_secret(ctx, sk)) return rc;
+    if (!seed32 || !eseed32 || !d_evk) return fail(CKKS_EINVAL, "null argument");
+    if (ctx->c.K == 0) return fail(CKKS_EINVAL, "context has no special primes");
+    return guarded([&] {
+        fhe::keygen_relin(ctx->c, *sk->s, seed32, eseed32, 3.19, d_evk);
+        return CKKS_OK;
+    });
+}
+
+int ckks_keygen_automorphism(ckks_context* ctx, const ckks_secret* sk, uint32_t g, const uint8_t* seed32,
+                             const uint8_t* eseed32, uint64_t* d_evk) {
+    if (int rc = check_secret(ctx, sk)) return rc;
+    if (!seed32 || !eseed32 || !d_evk) return fail(CKKS_EINVAL, "null argument");
+    if ((g & 1) == 0 || g >= 2 * fhe::kN) return fail(CKKS_EINVAL, "automorphism index must be odd and < 2N");
+    if (ctx->c.K == 0) return fail(CKKS_EINVAL, "context has no special primes");
+    return guarded([&] {
+        fhe::keygen_automorphism(ctx->c, *sk->s, g, seed32, eseed32, 3.19, d_evk);
+        return CKKS_OK;
+    });
+}
+
+int ckks_encode(ckks_context* ctx, const double* re, const double* im, uint32_t n_slots, uint32_t level, double scale,
+                uint64_t* d_pt) {
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_pt || (!re && !im)) return fail(CKKS_EINVAL, "null argument");
+    if (!(scale > 0)) return fail(CKKS_EINVAL, "scale must be positive");
+    return guarded([&] {
+        fhe::encode(ctx->c, re, im, n_slots, level, scale, d_pt);
+        return CKKS_OK;
+    });
+}
+
+int ckks_encrypt(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_pt, uint32_t level, const uint8_t* seed32,
+                 uint32_t index, uint64_t* d_ct) {
+    if (int rc = check_secret(ctx, sk)) return rc;
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_pt || !seed32 || !d_ct) return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        fhe::encrypt(ctx->c, *sk->s, d_pt, level, seed32, index, d_ct);
+        return CKKS_OK;
+    });
+}
+
+int ckks_decrypt_decode(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_ct, uint32_t level, double scale,
+                        double* re, double* im, uint32_t n_slots) {
+    if (int rc = check_secret(ctx, sk)) return rc;
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_ct || (!re && !im)) return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        fhe::decrypt_decode(ctx->c, *sk->s, d_ct, level, scale, re, im, n_slots);
+        return CKKS_OK;
+    });
+}
+
+int ckks_profile_enable(ckks_context* ctx, int on) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    ctx->c.prof_on = on != 0;
+    return CKKS_OK;
+}
+
+int ckks_profile_reset(ckks_context* ctx) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    fhe::prof_clear(ctx->c);
+    return CKKS_OK;
+}
+
+int ckks_profile_query(ckks_context* ctx, uint32_t idx, char* name, uint32_t name_cap, uint64_t* launches,
+                       double* total_ms, double* total_bytes) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    std::vector<std::string> order;
+    std::map<std::string, std::tuple<uint64_t, double, double>> agg;
+    for (auto& r : ctx->c.prof) {
+        HIP_TRY(hipEventSynchronize(r.e1));
+        float ms = 0;
+        HIP_TRY(hipEventElapsedTime(&ms, r.e0, r.e1));
+        auto it = agg.find(r.name);
+        if (it == agg.end()) {
+            order.push_back(r.name);
+            agg[r.name] = std::make_tuple(1ull, (double)ms, r.bytes);
+        } else {
+            std::get<0>(it->second) += 1;
+            std::get<1>(it->second) += ms;
+            std::get<2>(it->second) += r.bytes;
+        }
+    }
+    if (idx >= order.size()) return fail(CKKS_EINVAL, "no such profile entry");
+    const auto& a = agg[order[idx]];
+    if (name && name_cap) {
+        std::strncpy(name, order[idx].c_str(), name_cap - 1);
+        name[name_cap - 1] = 0;
+    }
+    if (launches) *launches = std::get<0>(a);
+    if (total_ms) *total_ms = std::get<1>(a);
+    if (total_bytes) *total_bytes = std::get<2>(a);
+    return CKKS_OK;
 }
 
 }  // extern "C"

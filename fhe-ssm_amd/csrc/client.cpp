@@ -1,0 +1,359 @@
+// client.cpp -- client-side operations: seeded sampling (ChaCha20 expander of
+// hpc_gpu_port/seeded_keys.hpp:28-43), key-switching-key generation (seeded_keys.hpp:216-256),
+// CKKS encode/decode (special FFT, slot j <-> evaluation at zeta^(5^j), zeta = exp(i pi / N)),
+// secret-key encryption and decryption.  Host code; the limb arithmetic runs in client.hip kernels.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <complex>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "client.hpp"
+#include "engine.hpp"
+#include "ops.hpp"
+
+namespace fhe {
+
+uint64_t mulmod_h(uint64_t a, uint64_t b, uint64_t q);
+uint64_t invmod_h(uint64_t a, uint64_t q);
+hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,
+                      NttMode mode, hipStream_t st);
+hipError_t launch_small_to_rns(const Context& ctx, const int64_t* coef, uint64_t* out, uint32_t n_polys,
+                               const std::vector<uint32_t>& pmap, hipStream_t st);
+hipError_t launch_ksk_b(const Context& ctx, const uint64_t* a, const uint64_t* s_new, const uint64_t* e,
+                        const uint64_t* s_old, uint64_t* b, uint32_t lo, uint32_t hi, const TwPair* pmod,
+                        hipStream_t st);
+hipError_t launch_encrypt(const Context& ctx, const uint64_t* m, const uint64_t* e, const uint64_t* a,
+                          const uint64_t* s, uint64_t* ct, uint32_t l, hipStream_t st);
+hipError_t launch_decrypt(const Context& ctx, const uint64_t* ct, const uint64_t* s, uint64_t* out, uint32_t l,
+                          hipStream_t st);
+hipError_t launch_mul(const Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t l,
+                      hipStream_t st);
+
+namespace {
+
+#define HIPC(expr)                                                                      \
+    do {                                                                                \
+        hipError_t _e = (expr);                                                         \
+        if (_e != hipSuccess)                                                           \
+            throw std::runtime_error(std::string(#expr) + ": " + hipGetErrorString(_e)); \
+    } while (0)
+
+constexpr uint32_t kTagKey = 0x59454b53u;   // "SKEY" (seeded_keys.hpp:32)
+constexpr uint32_t kTagSecret = 0x52434553u;  // "SECR"
+constexpr uint32_t kTagGauss = 0x53554147u;   // "GAUS"
+constexpr uint32_t kTagCtA = 0x41585443u;     // "CTXA"
+
+// ---------------------------------------------------------------- ChaCha20 (RFC 8439)
+inline uint32_t rotl(uint32_t v, int c) { return (v << c) | (v >> (32 - c)); }
+
+void chacha_block(const uint32_t key[8], uint32_t counter, const uint32_t nonce[3], uint32_t out[16]) {
+    const uint32_t init[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u, key[0], key[1],
+                               key[2],      key[3],      key[4],      key[5],      key[6], key[7],
+                               counter,     nonce[0],    nonce[1],    nonce[2]};
+    uint32_t x[16];
+    std::memcpy(x, init, sizeof(x));
+    auto qr = [&](int a, int b, int c, int d) {
+        x[a] += x[b]; x[d] = rotl(x[d] ^ x[a], 16);
+        x[c] += x[d]; x[b] = rotl(x[b] ^ x[c], 12);
+        x[a] += x[b]; x[d] = rotl(x[d] ^ x[a], 8);
+        x[c] += x[d]; x[b] = rotl(x[b] ^ x[c], 7);
+    };
+    for (int r = 0; r < 10; r++) {
+        qr(0, 4, 8, 12); qr(1, 5, 9, 13); qr(2, 6, 10, 14); qr(3, 7, 11, 15);
+        qr(0, 5, 10, 15); qr(1, 6, 11, 12); qr(2, 7, 8, 13); qr(3, 4, 9, 14);
+    }
+    for (int i = 0; i < 16; i++) out[i] = x[i] + init[i];
+}
+
+class Stream {
+public:
+    Stream(const uint8_t seed[32], uint32_t w0, uint32_t w1, uint32_t tag) {
+        for (int k = 0; k < 8; k++)
+            key_[k] = (uint32_t)seed[4 * k] | ((uint32_t)seed[4 * k + 1] << 8) | ((uint32_t)seed[4 * k + 2] << 16) |
+                      ((uint32_t)seed[4 * k + 3] << 24);
+        nonce_[0] = w0;
+        nonce_[1] = w1;
+        nonce_[2] = tag;
+    }
+    uint64_t next() {
+        if (pos_ == 8) {
+            chacha_block(key_, ctr_++, nonce_, w_);
+            pos_ = 0;
+        }
+        const uint64_t v = (uint64_t)w_[2 * pos_] | ((uint64_t)w_[2 * pos_ + 1] << 32);
+        pos_++;
+        return v;
+    }
+
+private:
+    uint32_t key_[8], nonce_[3], w_[16], ctr_ = 0;
+    int pos_ = 8;
+};
+
+void fill_uniform(const uint8_t seed[32], uint32_t w0, uint32_t w1, uint32_t tag, uint64_t q, uint64_t* out,
+                  size_t n) {
+    Stream s(seed, w0, w1, tag);
+    const uint64_t r = (0 - q) % q, lim = 0 - r;
+    for (size_t k = 0; k < n; k++) {
+        uint64_t w = s.next();
+        while (r != 0 && w >= lim) w = s.next();
+        out[k] = w % q;
+    }
+}
+
+void gauss(const uint8_t seed[32], uint32_t w0, uint32_t w1, double sigma, int64_t* e) {
+    Stream s(seed, w0, w1, kTagGauss);
+    const double two53 = 9007199254740992.0;
+    for (uint32_t k = 0; k < kN; k++) {
+        const double u1 = ((double)(s.next() >> 11) + 1.0) / two53;
+        const double u2 = (double)(s.next() >> 11) / two53;
+        const double z = std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+        e[k] = (int64_t)std::llround(sigma * z);
+    }
+}
+
+// device upload + conversion of signed coefficient polys to the given limbs, evaluation form
+struct DevBuf {
+    void* p = nullptr;
+    explicit DevBuf(size_t bytes) { HIPC(hipMalloc(&p, bytes)); }
+    ~DevBuf() { (void)hipFree(p); }
+    template <class T>
+    T* as() const { return (T*)p; }
+};
+
+void coeffs_to_eval(Context& ctx, const int64_t* h_coef, uint32_t n_polys, const std::vector<uint32_t>& pmap,
+                    uint64_t* d_out, hipStream_t st) {
+    DevBuf dc((size_t)n_polys * kN * 8);
+    HIPC(hipMemcpy(dc.p, h_coef, (size_t)n_polys * kN * 8, hipMemcpyHostToDevice));
+    HIPC(launch_small_to_rns(ctx, dc.as<int64_t>(), d_out, n_polys, pmap, st));
+    JobSpec js{};
+    js.n_polys = n_polys;
+    js.period = (uint32_t)pmap.size();
+    for (size_t i = 0; i < pmap.size(); i++) js.pmap[i] = (uint8_t)pmap[i];
+    HIPC(launch_ntt(ctx, d_out, js, n_polys * (uint32_t)pmap.size(), false, ctx.ntt_mode, st));
+    HIPC(hipStreamSynchronize(st));
+}
+
+std::vector<uint32_t> iota(uint32_t n) {
+    std::vector<uint32_t> v(n);
+    for (uint32_t i = 0; i < n; i++) v[i] = i;
+    return v;
+}
+
+// ---------------------------------------------------------------- FFT (radix 2, in place)
+void fft(std::vector<std::complex<double>>& a, int sign) {
+    const size_t n = a.size();
+    for (size_t i = 1, j = 0; i < n; i++) {
+        size_t bit = n >> 1;
+        for (; j & bit; bit >>= 1) j ^= bit;
+        j ^= bit;
+        if (i < j) std::swap(a[i], a[j]);
+    }
+    for (size_t len = 2; len <= n; len <<= 1) {
+        const size_t h = len / 2;
+        std::vector<std::complex<double>> w(h);
+        for (size_t k = 0; k < h; k++) {
+            const double ang = sign * 2.0 * M_PI * (double)k / (double)len;
+            w[k] = std::complex<double>(std::cos(ang), std::sin(ang));
+        }
+        for (size_t i = 0; i < n; i += len)
+            for (size_t k = 0; k < h; k++) {
+                const auto u = a[i + k], v = a[i + k + h] * w[k];
+                a[i + k] = u + v;
+                a[i + k + h] = u - v;
+            }
+    }
+}
+
+// t index (evaluation point zeta^(2t+1)) of slot j and of its conjugate
+void slot_points(std::vector<uint32_t>& t_of, std::vector<uint32_t>& tc_of) {
+    const uint64_t M = 2ull * kN;
+    t_of.resize(kN / 2);
+    tc_of.resize(kN / 2);
+    uint64_t e = 1;
+    for (uint32_t j = 0; j < kN / 2; j++) {
+        t_of[j] = (uint32_t)((e - 1) / 2);
+        tc_of[j] = (uint32_t)((M - e - 1) / 2);
+        e = e * 5 % M;
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- public (C++) API used by abi.cpp
+void sample_ternary(const uint8_t seed[32], uint32_t h, int8_t* s) {
+    Stream st(seed, 0, 0, kTagSecret);
+    std::memset(s, 0, kN);
+    for (uint32_t i = 0; i < h && i < kN; i++) {
+        for (;;) {
+            const uint64_t w = st.next();
+            const uint32_t p = (uint32_t)(w & (kN - 1));
+            if (s[p]) continue;
+            s[p] = (w >> 63) ? -1 : 1;
+            break;
+        }
+    }
+}
+
+Secret* secret_create(Context& ctx, const uint8_t seed[32], uint32_t h) {
+    auto* sk = new Secret();
+    sk->coeffs.resize(kN);
+    sample_ternary(seed, h, sk->coeffs.data());
+    const uint32_t T = ctx.L + ctx.K;
+    try {
+        HIPC(hipMalloc(&sk->d_eval, (size_t)T * kN * 8));
+        std::vector<int64_t> c(sk->coeffs.begin(), sk->coeffs.end());
+        coeffs_to_eval(ctx, c.data(), 1, iota(T), sk->d_eval, nullptr);
+    } catch (...) {
+        secret_destroy(sk);
+        throw;
+    }
+    return sk;
+}
+
+void secret_destroy(Secret* sk) {
+    if (!sk) return;
+    (void)hipFree(sk->d_eval);
+    delete sk;
+}
+
+// Key-switching key from s_old (device, evaluation form, Q limbs [L][N]) to s_new (signed coefficients).
+void keygen_switch(Context& ctx, const uint64_t* d_s_old, const int8_t* s_new, const uint8_t seed[32],
+                   const uint8_t eseed[32], double sigma, uint64_t* d_evk) {
+    const uint32_t T = ctx.L + ctx.K;
+    DevBuf dsn((size_t)T * kN * 8), de((size_t)T * kN * 8);
+    std::vector<int64_t> c(s_new, s_new + kN);
+    coeffs_to_eval(ctx, c.data(), 1, iota(T), dsn.as<uint64_t>(), nullptr);
+    std::vector<TwPair> pmod(T);
+    for (uint32_t i = 0; i < T; i++) {
+        const uint64_t q = ctx.moduli[i];
+        uint64_t P = 1;
+        for (uint32_t k = 0; k < ctx.K; k++) P = mulmod_h(P, ctx.moduli[ctx.L + k] % q, q);
+        pmod[i] = TwPair{P, (uint64_t)(((unsigned __int128)P << 64) / q)};
+    }
+    std::vector<uint64_t> a((size_t)T * kN);
+    std::vector<int64_t> e(kN);
+    for (uint32_t d = 0; d < ctx.dnum; d++) {
+        uint64_t* b_d = d_evk + ((size_t)d * 2 + 0) * T * kN;
+        uint64_t* a_d = d_evk + ((size_t)d * 2 + 1) * T * kN;
+        for (uint32_t i = 0; i < T; i++) fill_uniform(seed, d, i, kTagKey, ctx.moduli[i], a.data() + (size_t)i * kN, kN);
+        HIPC(hipMemcpy(a_d, a.data(), a.size() * 8, hipMemcpyHostToDevice));
+        gauss(eseed, d, 0, sigma, e.data());
+        coeffs_to_eval(ctx, e.data(), 1, iota(T), de.as<uint64_t>(), nullptr);
+        const uint32_t lo = d * ctx.alpha, hi = std::min(lo + ctx.alpha, ctx.L);
+        HIPC(launch_ksk_b(ctx, a_d, dsn.as<uint64_t>(), de.as<uint64_t>(), d_s_old, b_d, lo, hi, pmod.data(), nullptr));
+    }
+    HIPC(hipDeviceSynchronize());
+}
+
+void keygen_relin(Context& ctx, const Secret& sk, const uint8_t seed[32], const uint8_t eseed[32], double sigma,
+                  uint64_t* d_evk) {
+    DevBuf s2((size_t)ctx.L * kN * 8);
+    HIPC(launch_mul(ctx, sk.d_eval, sk.d_eval, s2.as<uint64_t>(), ctx.L, nullptr));
+    keygen_switch(ctx, s2.as<uint64_t>(), sk.coeffs.data(), seed, eseed, sigma, d_evk);
+}
+
+// EvalAutomorphismKeyGen: switch from s to tau_{g^-1}(s) (seeded_keys.hpp:159-168)
+void keygen_automorphism(Context& ctx, const Secret& sk, uint32_t g, const uint8_t seed[32], const uint8_t eseed[32],
+                         double sigma, uint64_t* d_evk) {
+    const uint64_t M = 2ull * kN;
+    // g^-1 mod 2N: the order of g in (Z/2N)^* divides N/2, so g^(N/2 - 1) = g^-1
+    uint64_t gi = 1, base = g % M;
+    for (uint64_t e = kN / 2 - 1; e; e >>= 1) {
+        if (e & 1) gi = gi * base % M;
+        base = base * base % M;
+    }
+    std::vector<int8_t> sp(kN, 0);
+    for (uint32_t j = 0; j < kN; j++) {
+        const uint64_t e = (uint64_t)j * gi % M;
+        if (e < kN) sp[e] = (int8_t)(sp[e] + sk.coeffs[j]);
+        else sp[e - kN] = (int8_t)(sp[e - kN] - sk.coeffs[j]);
+    }
+    keygen_switch(ctx, sk.d_eval, sp.data(), seed, eseed, sigma, d_evk);
+}
+
+// values (re, im may be null) of n_slots slots, replicated to N/2 when n_slots divides N/2
+void encode(Context& ctx, const double* re, const double* im, uint32_t n_slots, uint32_t l, double scale,
+            uint64_t* d_pt) {
+    if (n_slots == 0 || (kN / 2) % n_slots != 0) throw std::invalid_argument("n_slots must divide N/2");
+    std::vector<uint32_t> t_of, tc_of;
+    slot_points(t_of, tc_of);
+    std::vector<std::complex<double>> v(kN, 0.0);
+    for (uint32_t j = 0; j < kN / 2; j++) {
+        const uint32_t s = j % n_slots;
+        const std::complex<double> z(re ? re[s] : 0.0, im ? im[s] : 0.0);
+        v[t_of[j]] = z * scale;
+        v[tc_of[j]] = std::conj(z) * scale;
+    }
+    fft(v, -1);  // sum_t v_t w^(-tk)
+    std::vector<int64_t> coef(kN);
+    for (uint32_t k = 0; k < kN; k++) {
+        const double ang = -M_PI * (double)k / (double)kN;  // zeta^-k
+        const double m = (v[k] * std::complex<double>(std::cos(ang), std::sin(ang))).real() / (double)kN;
+        if (!(std::fabs(m) < 4.0e18)) throw std::invalid_argument("encoded coefficient overflows int64");
+        coef[k] = (int64_t)std::llround(m);
+    }
+    coeffs_to_eval(ctx, coef.data(), 1, iota(l), d_pt, nullptr);
+}
+
+void encrypt(Context& ctx, const Secret& sk, const uint64_t* d_pt, uint32_t l, const uint8_t seed[32],
+             uint32_t index, uint64_t* d_ct) {
+    DevBuf da((size_t)l * kN * 8), de((size_t)l * kN * 8);
+    std::vector<uint64_t> a((size_t)l * kN);
+    for (uint32_t i = 0; i < l; i++) fill_uniform(seed, index, i, kTagCtA, ctx.moduli[i], a.data() + (size_t)i * kN, kN);
+    HIPC(hipMemcpy(da.p, a.data(), a.size() * 8, hipMemcpyHostToDevice));
+    std::vector<int64_t> e(kN);
+    gauss(seed, index, 1, 3.19, e.data());
+    coeffs_to_eval(ctx, e.data(), 1, iota(l), de.as<uint64_t>(), nullptr);
+    HIPC(launch_encrypt(ctx, d_pt, de.as<uint64_t>(), da.as<uint64_t>(), sk.d_eval, d_ct, l, nullptr));
+    HIPC(hipDeviceSynchronize());
+}
+
+// decrypt (c0 + c1 s), to coefficients, CRT of the first two limbs (|m| < q0 q1 / 2), decode
+void decrypt_decode(Context& ctx, const Secret& sk, const uint64_t* d_ct, uint32_t l, double scale, double* re,
+                    double* im, uint32_t n_slots) {
+    if (n_slots == 0 || n_slots > kN / 2) throw std::invalid_argument("n_slots must be in [1, N/2]");
+    DevBuf dm((size_t)l * kN * 8);
+    HIPC(launch_decrypt(ctx, d_ct, sk.d_eval, dm.as<uint64_t>(), l, nullptr));
+    const uint32_t nl = l >= 2 ? 2 : 1;
+    JobSpec js{};
+    js.n_polys = 1;
+    js.period = nl;
+    for (uint32_t i = 0; i < nl; i++) js.pmap[i] = (uint8_t)i;
+    HIPC(launch_ntt(ctx, dm.as<uint64_t>(), js, nl, true, ctx.ntt_mode, nullptr));
+    std::vector<uint64_t> limbs((size_t)nl * kN);
+    HIPC(hipMemcpy(limbs.data(), dm.p, limbs.size() * 8, hipMemcpyDeviceToHost));
+    const uint64_t q0 = ctx.moduli[0];
+    std::vector<std::complex<double>> v(kN);
+    for (uint32_t k = 0; k < kN; k++) {
+        double m;
+        if (nl == 1) {
+            const uint64_t x = limbs[k];
+            m = x > q0 / 2 ? -(double)(q0 - x) : (double)x;
+        } else {
+            const uint64_t q1 = ctx.moduli[1];
+            const uint64_t x0 = limbs[k], x1 = limbs[kN + k];
+            const uint64_t q0inv = invmod_h(q0 % q1, q1);
+            const uint64_t d = mulmod_h((x1 + q1 - x0 % q1) % q1, q0inv, q1);
+            const unsigned __int128 Q = (unsigned __int128)q0 * q1;
+            const unsigned __int128 x = (unsigned __int128)d * q0 + x0;
+            m = x > Q / 2 ? -(double)(Q - x) : (double)x;
+        }
+        const double ang = M_PI * (double)k / (double)kN;  // zeta^k
+        v[k] = std::complex<double>(m * std::cos(ang), m * std::sin(ang));
+    }
+    fft(v, +1);
+    std::vector<uint32_t> t_of, tc_of;
+    slot_points(t_of, tc_of);
+    for (uint32_t j = 0; j < n_slots; j++) {
+        const auto z = v[t_of[j]] / scale;
+        if (re) re[j] = z.real();
+        if (im) im[j] = z.imag();
+    }
+}
+
+}  // namespace fhe

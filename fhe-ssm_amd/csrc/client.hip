@@ -1,0 +1,134 @@
+// client.hip -- limb kernels of the client-side operations (key generation, encryption, decryption):
+// small signed polynomials to RNS limbs, the key-switching-key formula, secret-key encryption and
+// the decryption inner product.  Not on the evaluation hot path; used to produce seeded keys and
+// ciphertexts on the device and to read results back.
+#include "engine.hpp"
+#include "modarith.hpp"
+
+namespace fhe {
+
+namespace {
+
+__device__ __forceinline__ Barrett barrett_c(const PrimeInfo& p) { return Barrett{p.q, p.mu_hi, p.mu_lo}; }
+
+// out[pc][l][k] = coef[pc][k] mod q_{pmap[l]} (signed coefficients)
+struct PmapArgs {
+    uint32_t n_limbs;
+    uint8_t pmap[kMaxPmap];
+};
+
+__global__ __launch_bounds__(256) void k_small_to_rns(const int64_t* __restrict__ coef, uint64_t* __restrict__ out,
+                                                      PmapArgs pa, const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t l = blockIdx.y, pc = blockIdx.z;
+    const uint64_t q = primes[pa.pmap[l]].q;
+    const int64_t c = coef[(size_t)pc * kN + k];
+    uint64_t r;
+    if (c >= 0) {
+        r = (uint64_t)c % q;
+    } else {
+        const uint64_t m = (uint64_t)(-(c + 1)) % q;  // -(c+1) >= 0 even for INT64_MIN
+        r = (m + 1 == q) ? 0 : q - 1 - m;
+    }
+    out[((size_t)pc * pa.n_limbs + l) * kN + k] = r;
+}
+
+// key-switching key of one digit over Q*P (T limbs, limb i uses prime i):
+// b[i] = -a[i] * s_new[i] + e[i] + (digit limb ? pmod_i * s_old[i] : 0)
+struct KskArgs {
+    uint32_t lo, hi;     // Q limbs of this digit
+    TwPair pmod[kMaxPmap];
+};
+
+__global__ __launch_bounds__(256) void k_ksk_b(const uint64_t* __restrict__ a, const uint64_t* __restrict__ s_new,
+                                               const uint64_t* __restrict__ e, const uint64_t* __restrict__ s_old,
+                                               uint64_t* __restrict__ b, KskArgs ka,
+                                               const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y;
+    const size_t o = (size_t)i * kN + k;
+    const Barrett br = barrett_c(primes[i]);
+    const uint64_t q = br.q;
+    const uint64_t as = mul_mod(a[o], s_new[o], br);
+    uint64_t v = sub_mod(e[o], as, q);
+    if (i >= ka.lo && i < ka.hi) v = add_mod(v, shoup(s_old[o], ka.pmod[i].w, ka.pmod[i].wp, q), q);
+    b[o] = v;
+}
+
+// secret-key encryption of l limbs: c0 = m + e - a*s, c1 = a  (ct layout [2][l][N])
+__global__ __launch_bounds__(256) void k_encrypt(const uint64_t* __restrict__ m, const uint64_t* __restrict__ e,
+                                                 const uint64_t* __restrict__ a, const uint64_t* __restrict__ s,
+                                                 uint64_t* __restrict__ ct, uint32_t l,
+                                                 const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y;
+    const size_t o = (size_t)i * kN + k;
+    const Barrett br = barrett_c(primes[i]);
+    const uint64_t as = mul_mod(a[o], s[o], br);
+    ct[o] = sub_mod(add_mod(m[o], e[o], br.q), as, br.q);
+    ct[(size_t)l * kN + o] = a[o];
+}
+
+// decryption inner product: out = c0 + c1 * s over l limbs
+__global__ __launch_bounds__(256) void k_decrypt(const uint64_t* __restrict__ ct, const uint64_t* __restrict__ s,
+                                                 uint64_t* __restrict__ out, uint32_t l,
+                                                 const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y;
+    const size_t o = (size_t)i * kN + k;
+    const Barrett br = barrett_c(primes[i]);
+    out[o] = add_mod(ct[o], mul_mod(ct[(size_t)l * kN + o], s[o], br), br.q);
+}
+
+// elementwise product over [l][N] (limb i uses prime i)
+__global__ __launch_bounds__(256) void k_mul(const uint64_t* __restrict__ x, const uint64_t* __restrict__ y,
+                                             uint64_t* __restrict__ out, const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y;
+    const size_t o = (size_t)i * kN + k;
+    out[o] = mul_mod(x[o], y[o], barrett_c(primes[i]));
+}
+
+}  // namespace
+
+hipError_t launch_small_to_rns(const Context& ctx, const int64_t* coef, uint64_t* out, uint32_t n_polys,
+                               const std::vector<uint32_t>& pmap, hipStream_t st) {
+    PmapArgs pa{};
+    pa.n_limbs = (uint32_t)pmap.size();
+    for (size_t i = 0; i < pmap.size(); i++) pa.pmap[i] = (uint8_t)pmap[i];
+    hipLaunchKernelGGL(k_small_to_rns, dim3(kN / 256, pa.n_limbs, n_polys), dim3(256), 0, st, coef, out, pa,
+                       ctx.d_primes);
+    return hipGetLastError();
+}
+
+hipError_t launch_ksk_b(const Context& ctx, const uint64_t* a, const uint64_t* s_new, const uint64_t* e,
+                        const uint64_t* s_old, uint64_t* b, uint32_t lo, uint32_t hi, const TwPair* pmod,
+                        hipStream_t st) {
+    KskArgs ka{};
+    ka.lo = lo;
+    ka.hi = hi;
+    const uint32_t T = ctx.L + ctx.K;
+    for (uint32_t i = 0; i < T; i++) ka.pmod[i] = pmod[i];
+    hipLaunchKernelGGL(k_ksk_b, dim3(kN / 256, T), dim3(256), 0, st, a, s_new, e, s_old, b, ka, ctx.d_primes);
+    return hipGetLastError();
+}
+
+hipError_t launch_encrypt(const Context& ctx, const uint64_t* m, const uint64_t* e, const uint64_t* a,
+                          const uint64_t* s, uint64_t* ct, uint32_t l, hipStream_t st) {
+    hipLaunchKernelGGL(k_encrypt, dim3(kN / 256, l), dim3(256), 0, st, m, e, a, s, ct, l, ctx.d_primes);
+    return hipGetLastError();
+}
+
+hipError_t launch_decrypt(const Context& ctx, const uint64_t* ct, const uint64_t* s, uint64_t* out, uint32_t l,
+                          hipStream_t st) {
+    hipLaunchKernelGGL(k_decrypt, dim3(kN / 256, l), dim3(256), 0, st, ct, s, out, l, ctx.d_primes);
+    return hipGetLastError();
+}
+
+hipError_t launch_mul(const Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t l,
+                      hipStream_t st) {
+    hipLaunchKernelGGL(k_mul, dim3(kN / 256, l), dim3(256), 0, st, x, y, out, ctx.d_primes);
+    return hipGetLastError();
+}
+
+}  // namespace fhe

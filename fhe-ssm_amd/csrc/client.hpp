@@ -1,0 +1,32 @@
+// client.hpp -- client-side operations (keygen, encode, encrypt, decrypt); see client.cpp.
+#pragma once
+#include <stdint.h>
+
+#include <vector>
+
+#include "engine.hpp"
+
+namespace fhe {
+
+struct Secret {
+    std::vector<int8_t> coeffs;  // ternary coefficients, length N
+    uint64_t* d_eval = nullptr;  // [L+K][N] evaluation form over Q*P
+};
+
+void sample_ternary(const uint8_t seed[32], uint32_t h, int8_t* s);
+Secret* secret_create(Context& ctx, const uint8_t seed[32], uint32_t h);
+void secret_destroy(Secret* sk);
+void keygen_switch(Context& ctx, const uint64_t* d_s_old, const int8_t* s_new, const uint8_t seed[32],
+                   const uint8_t eseed[32], double sigma, uint64_t* d_evk);
+void keygen_relin(Context& ctx, const Secret& sk, const uint8_t seed[32], const uint8_t eseed[32], double sigma,
+                  uint64_t* d_evk);
+void keygen_automorphism(Context& ctx, const Secret& sk, uint32_t g, const uint8_t seed[32], const uint8_t eseed[32],
+                         double sigma, uint64_t* d_evk);
+void encode(Context& ctx, const double* re, const double* im, uint32_t n_slots, uint32_t l, double scale,
+            uint64_t* d_pt);
+void encrypt(Context& ctx, const Secret& sk, const uint64_t* d_pt, uint32_t l, const uint8_t seed[32], uint32_t index,
+             uint64_t* d_ct);
+void decrypt_decode(Context& ctx, const Secret& sk, const uint64_t* d_ct, uint32_t l, double scale, double* re,
+                    double* im, uint32_t n_slots);
+
+}  // namespace fhe

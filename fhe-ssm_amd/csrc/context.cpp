@@ -146,11 +146,34 @@ void context_init(Context& c, const std::vector<uint64_t>& q, const std::vector<
     up((void**)&c.d_primes, c.primes.data(), c.primes.size() * sizeof(PrimeInfo));
 }
 
+int prof_begin(const Context& ctx, const char* name, double bytes, hipStream_t st) {
+    if (!ctx.prof_on) return -1;
+    ProfRec r{name, bytes, nullptr, nullptr};
+    if (hipEventCreate(&r.e0) != hipSuccess || hipEventCreate(&r.e1) != hipSuccess) return -1;
+    if (hipEventRecord(r.e0, st) != hipSuccess) return -1;
+    ctx.prof.push_back(r);
+    return (int)ctx.prof.size() - 1;
+}
+
+void prof_end(const Context& ctx, int idx, hipStream_t st) {
+    if (idx < 0 || idx >= (int)ctx.prof.size()) return;
+    (void)hipEventRecord(ctx.prof[idx].e1, st);
+}
+
+void prof_clear(const Context& ctx) {
+    for (auto& r : ctx.prof) {
+        (void)hipEventDestroy(r.e0);
+        (void)hipEventDestroy(r.e1);
+    }
+    ctx.prof.clear();
+}
+
 void context_release(Context& c) {
     (void)hipFree(c.d_tw);
     (void)hipFree(c.d_itw);
     (void)hipFree(c.d_primes);
-    for (auto& kv : c.job_cache) (void)hipFree(kv.second);
+    for (auto& kv : c.job_cache) (void)hipFree(kv.second.first);
+    prof_clear(c);
     for (auto& kv : c.bconv_cache) (void)hipFree(kv.second.d_tab);
     for (auto& s : c.scratch) (void)hipFree(s.first);
     c.job_cache.clear();

@@ -34,6 +34,7 @@ struct Job {
 struct JobSpec {
     const Job* jobs;
     uint32_t n_polys, period;
+    uint32_t n_primes;  // distinct primes among the jobs (host-side byte accounting only)
     uint8_t pmap[kMaxPmap];
 };
 
@@ -47,6 +48,14 @@ struct BConvPlan {
     uint64_t* d_tab = nullptr;  // [n_in] (qhat_inv, companion) pairs, then [n_in][n_out] qhat_mod
 };
 
+// One profiled launch: HIP events recorded on the launch stream around the kernel, plus the
+// algorithmic bytes that launch must move (inputs read once, outputs written once, shared tables once).
+struct ProfRec {
+    std::string name;
+    double bytes;
+    hipEvent_t e0, e1;
+};
+
 struct Context {
     int device = 0;
     uint32_t L = 0, K = 0, dnum = 0, alpha = 0;
@@ -58,12 +67,20 @@ struct Context {
     TwPair* d_itw = nullptr;  // [L+K][N] inverse table (brev order)
     PrimeInfo* d_primes = nullptr;
     NttMode ntt_mode = NttMode::Fused;
-    // cached device job lists keyed by a shape string
-    std::map<std::string, Job*> job_cache;
+    // cached device job lists keyed by a shape string (list, distinct primes in it)
+    std::map<std::string, std::pair<Job*, uint32_t>> job_cache;
     std::map<std::string, BConvPlan> bconv_cache;
     // growable scratch
     std::vector<std::pair<void*, size_t>> scratch;
+    // per-launch profiling (off by default)
+    bool prof_on = false;
+    mutable std::vector<ProfRec> prof;
 };
+
+// Profiling helpers: no-ops unless ctx.prof_on.
+int prof_begin(const Context& ctx, const char* name, double bytes, hipStream_t st);
+void prof_end(const Context& ctx, int idx, hipStream_t st);
+void prof_clear(const Context& ctx);
 
 hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,
                       NttMode mode, hipStream_t st);

@@ -319,10 +319,33 @@ __global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_inv_fused(ui
 
 }  // namespace
 
-hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,
+hipError_t launch_ntt_kernels(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,
+                              NttMode mode, const TwPair* tw, hipStream_t st);
+
+hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js_in, uint32_t n_jobs, bool inverse,
                       NttMode mode, hipStream_t st) {
     if (n_jobs == 0) return hipSuccess;
+    JobSpec js = js_in;
+    if (!js.jobs && js.n_primes == 0) {
+        bool seen[kMaxPrimes] = {};
+        for (uint32_t i = 0; i < js.period; i++) {
+            js.n_primes += seen[js.pmap[i]] ? 0 : 1;
+            seen[js.pmap[i]] = true;
+        }
+    }
     const TwPair* tw = inverse ? ctx.d_itw : ctx.d_tw;
+    // algorithmic bytes: every limb read and written once, each prime's table (w, w') read once
+    const double bytes = (double)n_jobs * 2.0 * kN * 8 + (double)js.n_primes * kN * sizeof(TwPair);
+    const char* name = mode == NttMode::Fused ? (inverse ? "ntt_inv_fused" : "ntt_fwd_fused")
+                                              : (inverse ? "ntt_inv_2pass" : "ntt_fwd_2pass");
+    const int pi = prof_begin(ctx, name, bytes, st);
+    hipError_t err = launch_ntt_kernels(ctx, data, js, n_jobs, inverse, mode, tw, st);
+    prof_end(ctx, pi, st);
+    return err;
+}
+
+hipError_t launch_ntt_kernels(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,
+                              NttMode mode, const TwPair* tw, hipStream_t st) {
     if (mode == NttMode::Fused) {
         if (inverse)
             hipLaunchKernelGGL(k_ntt_inv_fused, dim3(n_jobs), dim3(kTileThreads * kFusedGroups), 0, st, data, js, tw,

@@ -66,20 +66,20 @@ JobSpec regular_jobs(uint32_t n_polys, const std::vector<uint32_t>& pmap) {
 }
 
 // explicit job list, stored once per key; ordered prime-major (jobs sharing a twiddle table adjacent)
-const Job* cached_jobs(Context& ctx, const std::string& key, std::vector<Job> jobs) {
+JobSpec cached_jobs(Context& ctx, const std::string& key, std::vector<Job> jobs) {
     auto it = ctx.job_cache.find(key);
-    if (it != ctx.job_cache.end()) return it->second;
-    std::stable_sort(jobs.begin(), jobs.end(), [](const Job& a, const Job& b) { return a.prime < b.prime; });
-    Job* d = nullptr;
-    HIPX(hipMalloc(&d, std::max<size_t>(1, jobs.size()) * sizeof(Job)));
-    HIPX(hipMemcpy(d, jobs.data(), jobs.size() * sizeof(Job), hipMemcpyHostToDevice));
-    ctx.job_cache[key] = d;
-    return d;
-}
-
-JobSpec list_jobs(const Job* d) {
+    if (it == ctx.job_cache.end()) {
+        std::stable_sort(jobs.begin(), jobs.end(), [](const Job& a, const Job& b) { return a.prime < b.prime; });
+        uint32_t distinct = 0;
+        for (size_t i = 0; i < jobs.size(); i++) distinct += (i == 0 || jobs[i].prime != jobs[i - 1].prime) ? 1 : 0;
+        Job* d = nullptr;
+        HIPX(hipMalloc(&d, std::max<size_t>(1, jobs.size()) * sizeof(Job)));
+        HIPX(hipMemcpy(d, jobs.data(), jobs.size() * sizeof(Job), hipMemcpyHostToDevice));
+        it = ctx.job_cache.emplace(key, std::make_pair(d, distinct)).first;
+    }
     JobSpec js{};
-    js.jobs = d;
+    js.jobs = it->second.first;
+    js.n_primes = it->second.second;
     return js;
 }
 
@@ -169,9 +169,9 @@ void modup_from_coef(Context& ctx, const uint64_t* x2c, uint64_t* ext, uint32_t 
             for (uint32_t j = 0; j < out_off.size(); j++)
                 jobs.push_back(Job{(b * D + d) * E + out_off[j], out_idx[j]});
     }
-    const Job* dj = cached_jobs(ctx, "modup:" + std::to_string(B) + ":" + std::to_string(l), std::move(jobs));
+    const JobSpec js = cached_jobs(ctx, "modup:" + std::to_string(B) + ":" + std::to_string(l), std::move(jobs));
     const uint32_t n_jobs = B * D * (E) - B * l;  // every limb of every digit except the digit's own
-    HIPX(launch_ntt(ctx, ext, list_jobs(dj), n_jobs, false, ctx.ntt_mode, st));
+    HIPX(launch_ntt(ctx, ext, js, n_jobs, false, ctx.ntt_mode, st));
 }
 
 // x: [B][l][N] evaluation form -> ext [B][D][E][N] evaluation form
@@ -209,8 +209,8 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
     std::vector<Job> jobs;
     for (uint32_t pc = 0; pc < n_polys; pc++)
         for (uint32_t k = 0; k < K; k++) jobs.push_back(Job{pc * E + l + k, ctx.L + k});
-    const Job* dj = cached_jobs(ctx, "mdP:" + std::to_string(n_polys) + ":" + std::to_string(l), std::move(jobs));
-    HIPX(launch_ntt(ctx, x, list_jobs(dj), n_polys * K, true, ctx.ntt_mode, st));
+    const JobSpec js = cached_jobs(ctx, "mdP:" + std::to_string(n_polys) + ":" + std::to_string(l), std::move(jobs));
+    HIPX(launch_ntt(ctx, x, js, n_polys * K, true, ctx.ntt_mode, st));
     std::vector<uint32_t> in_idx, in_off, out_idx, out_off;
     for (uint32_t k = 0; k < K; k++) {
         in_idx.push_back(ctx.L + k);

@@ -221,7 +221,9 @@ hipError_t launch_tensor(const Context& ctx, const uint64_t* a, const uint64_t* 
     ta.d2e_bstride = d2e_bstride;
     if (d2e)
         for (uint32_t t = 0; t < l; t++) ta.ext_off[t] = ext_off[t];
+    const int pi = prof_begin(ctx, "tensor", (double)B * l * (4 + 3 + (d2e ? 1 : 0)) * kN * 8, st);
     hipLaunchKernelGGL(k_tensor, dim3(kN / 256, l, B), dim3(256), 0, st, a, b, d01, d2, ta, ctx.d_primes);
+    prof_end(ctx, pi, st);
     return hipGetLastError();
 }
 
@@ -242,7 +244,9 @@ hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_
         ba.out_off[j] = (uint16_t)out_off[j];
         ba.out_prime[j] = (uint8_t)plan.out_idx[j];
     }
+    const int pi = prof_begin(ctx, "bconv", (double)B * (plan.n_in + plan.n_out) * kN * 8, st);
     hipLaunchKernelGGL(k_bconv, dim3(kN / 256, B), dim3(256), 0, st, in, out, ba, plan.d_tab, ctx.d_primes);
+    prof_end(ctx, pi, st);
     return hipGetLastError();
 }
 
@@ -258,7 +262,11 @@ hipError_t launch_ks_inner(const Context& ctx, const uint64_t* ext, const uint64
     // split the batch over grid.z so that the grid has enough workgroups; each z-slice keeps its
     // evk words in registers across its ciphertexts
     const uint32_t zs = B < 8 ? B : 8;
+    // ext read once per ciphertext, acc written once, the evk limbs of the level read once
+    const double bytes = ((double)B * (ia.D * ia.E + 2 * ia.E) + 2.0 * ia.D * ia.E) * kN * 8;
+    const int pi = prof_begin(ctx, "ks_inner", bytes, st);
     hipLaunchKernelGGL(k_ks_inner, dim3(kN / 256, ia.E, zs), dim3(256), 0, st, ext, evk, acc, ia, ctx.d_primes);
+    prof_end(ctx, pi, st);
     return hipGetLastError();
 }
 
@@ -274,20 +282,27 @@ hipError_t launch_sub_scale(const Context& ctx, const uint64_t* x, uint64_t x_ps
     ca.out_pstride = out_pstride;
     ca.add_pstride = add_pstride;
     for (uint32_t i = 0; i < l; i++) ca.s[i] = s[i];
+    const double n_add = add ? (double)n_polys / ca.add_div : 0.0;
+    const int pi = prof_begin(ctx, "sub_scale", ((double)n_polys * 3 + n_add) * l * kN * 8, st);
     hipLaunchKernelGGL(k_sub_scale, dim3(kN / 256, l, n_polys), dim3(256), 0, st, x, y, add, out, ca, ctx.d_primes);
+    prof_end(ctx, pi, st);
     return hipGetLastError();
 }
 
 hipError_t launch_lift_centered(const Context& ctx, const uint64_t* last, uint64_t last_pstride, uint64_t* tmp,
                                 uint32_t n_polys, uint32_t n_out, uint64_t ql, hipStream_t st) {
+    const int pi = prof_begin(ctx, "lift_centered", (double)n_polys * (1 + n_out) * kN * 8, st);
     hipLaunchKernelGGL(k_lift_centered, dim3(kN / 256, n_out, n_polys), dim3(256), 0, st, last, last_pstride, tmp,
                        n_out, ql, ctx.d_primes);
+    prof_end(ctx, pi, st);
     return hipGetLastError();
 }
 
 hipError_t launch_add(const Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys,
                       uint32_t l, hipStream_t st) {
+    const int pi = prof_begin(ctx, "add", (double)n_polys * l * 3 * kN * 8, st);
     hipLaunchKernelGGL(k_add, dim3(kN / 256, l, n_polys), dim3(256), 0, st, x, y, out, l, ctx.d_primes);
+    prof_end(ctx, pi, st);
     return hipGetLastError();
 }
 

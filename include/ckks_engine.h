@@ -128,6 +128,39 @@ int ckks_automorphism(ckks_context* ctx, const uint64_t* d_in, uint32_t n_polys,
 int ckks_eval_rotate(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level, int64_t step,
                      const uint64_t* d_evk, uint64_t* d_out, void* stream);
 
+/* ---- client side: keys, encoding, encryption (CryptoContext KeyGen / EvalMultKeyGen /
+ * EvalRotateKeyGen / MakeCKKSPackedPlaintext / Encrypt / Decrypt, gpu_real_model.cu:1293-1336,1577-1589,
+ * 2202-2221).  Not on the evaluation hot path; used to make seeded inputs and read results.
+ * Sampling is seeded and deterministic: the uniform a_j of a key-switching key follow the ChaCha20
+ * expander of hpc_gpu_port/seeded_keys.hpp:28-43 (nonce {digit, limb, "SKEY"}); the secret (ternary,
+ * fixed Hamming weight) and the rounded-Gaussian errors use the same expander with this library's tags.
+ * Encoding: slot j <-> evaluation at zeta^(5^j), zeta = exp(i pi / N); n_slots must divide N/2 (the
+ * vector is replicated); encrypt is secret-key encryption (c0 = m + e - a s, c1 = a). */
+typedef struct ckks_secret ckks_secret;
+int ckks_secret_generate(ckks_context* ctx, const uint8_t* seed32, uint32_t hamming_weight, ckks_secret** out);
+void ckks_secret_destroy(ckks_secret* sk);
+int ckks_secret_coeffs(const ckks_secret* sk, int8_t* out, uint32_t n);
+/* evk [dnum][2][L+K][N]; relinearization key: s^2 -> s; automorphism key of index g: s -> tau_{g^-1}(s) */
+int ckks_keygen_relin(ckks_context* ctx, const ckks_secret* sk, const uint8_t* seed32, const uint8_t* eseed32,
+                      uint64_t* d_evk);
+int ckks_keygen_automorphism(ckks_context* ctx, const ckks_secret* sk, uint32_t g, const uint8_t* seed32,
+                             const uint8_t* eseed32, uint64_t* d_evk);
+int ckks_encode(ckks_context* ctx, const double* re, const double* im, uint32_t n_slots, uint32_t level, double scale,
+                uint64_t* d_pt);
+int ckks_encrypt(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_pt, uint32_t level, const uint8_t* seed32,
+                 uint32_t index, uint64_t* d_ct);
+int ckks_decrypt_decode(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_ct, uint32_t level, double scale,
+                        double* re, double* im, uint32_t n_slots);
+
+/* ---- per-launch profiling (HIP events on the launch stream) ------------------------------------
+ * enable: start recording every kernel launch (name, algorithmic bytes, start/stop events);
+ * query: aggregated per kernel name, idx = 0..; returns CKKS_EINVAL past the last name.
+ * Waits for the recorded events. */
+int ckks_profile_enable(ckks_context* ctx, int on);
+int ckks_profile_reset(ckks_context* ctx);
+int ckks_profile_query(ckks_context* ctx, uint32_t idx, char* name, uint32_t name_cap, uint64_t* launches,
+                       double* total_ms, double* total_bytes);
+
 #ifdef __cplusplus
 }
 #endif
