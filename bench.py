@@ -132,7 +132,7 @@ def bench_hmult(ckks, torch, steps, warmup, seed):
         "dtype": "u64",
         "config": {"workload": "config2: HMult+relin+rescale, 64 ciphertext pairs, N=2^16, L=24x54-bit + "
                                "K=8x60-bit, dnum=3, h=192, sigma=3.19, scale 2^50",
-                   "batch": N_PAIRS, "level_in": L2, "ntt_mode": "fused", "seed": seed,
+                   "batch": N_PAIRS, "level_in": L2, "ntt_mode": "two-pass", "seed": seed,
                    "step_ms_min": round(min(per), 4), "step_ms_max": round(max(per), 4)},
         "check": {"decrypted_relErrRms_max": rel_err, "ciphertexts_checked": 2},
         "kernels": kernel_table(rep),
@@ -208,7 +208,7 @@ def bench_ntt(ckks, torch, steps, warmup, seed):
         "dtype": "u64",
         "config": {"workload": "config1: fwd+inv negacyclic NTT, N=2^16, 64 ct x 2 polys x L=24 54-bit limbs",
                    "limbs_per_direction": limbs, "algorithmic_bytes_per_direction": bytes_dir,
-                   "ntt_mode": "fused", "seed": seed},
+                   "ntt_mode": "two-pass", "seed": seed},
         "kernels": kernel_table(rep),
         "roofline": roofline_from_profile(rep),
     }

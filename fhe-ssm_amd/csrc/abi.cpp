@@ -114,8 +114,8 @@ const char* ckks_last_error(void) { return g_err.c_str(); }
 int ckks_context_create(const ckks_params* p, ckks_context** out) {
     if (!p || !out) return fail(CKKS_EINVAL, "null argument");
     if (p->log_n != fhe::kLogN) return fail(CKKS_ENOTSUP, "this build supports log_n = 16 only");
-    if (p->q_bits < 20 || p->q_bits > 61 || p->p_bits < 20 || p->p_bits > 61)
-        return fail(CKKS_EINVAL, "prime sizes must be in [20, 61] bits");
+    if (p->q_bits < 20 || p->q_bits > 60 || p->p_bits < 20 || p->p_bits > 60)
+        return fail(CKKS_EINVAL, "prime sizes must be in [20, 60] bits");
     return guarded([&] {
         const uint64_t m = 2ull * fhe::kN;
         auto q = fhe::ntt_primes(p->q_bits, p->num_q, m, {});

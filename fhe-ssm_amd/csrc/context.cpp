@@ -89,11 +89,13 @@ static uint32_t brev(uint32_t v, uint32_t bits) {
 
 static uint64_t shoup_companion(uint64_t w, uint64_t q) { return (uint64_t)(((u128)w << 64) / q); }
 
-PrimeInfo make_prime_info(uint64_t q) {
+PrimeInfo make_prime_info(uint64_t q, uint64_t itab1) {
     PrimeInfo p{};
     p.q = q;
     p.ninv = invmod_h(kN % q, q);
     p.ninv_p = shoup_companion(p.ninv, q);
+    p.w1ninv = mulmod_h(itab1, p.ninv, q);
+    p.w1ninv_p = shoup_companion(p.w1ninv, q);
     // mu = floor(2^128 / q) = floor((2^128 - 1) / q) for q not a power of two
     const u128 mu = ~(u128)0 / q;
     p.mu_hi = (uint64_t)(mu >> 64);
@@ -115,8 +117,8 @@ void context_init(Context& c, const std::vector<uint64_t>& q, const std::vector<
     c.moduli.insert(c.moduli.end(), p.begin(), p.end());
     const uint32_t T = c.L + c.K;
     for (uint64_t m : c.moduli)
-        if (m >= (1ull << 62) || (m - 1) % (2ull * kN) != 0 || !is_prime_h(m))
-            throw std::invalid_argument("modulus is not an NTT prime below 2^62: " + std::to_string(m));
+        if (m >= (1ull << 60) || (m - 1) % (2ull * kN) != 0 || !is_prime_h(m))
+            throw std::invalid_argument("modulus is not an NTT prime below 2^60: " + std::to_string(m));
     std::vector<TwPair> tw((size_t)T * kN), itw((size_t)T * kN);
     c.psi.resize(T);
     c.primes.resize(T);
@@ -124,7 +126,6 @@ void context_init(Context& c, const std::vector<uint64_t>& q, const std::vector<
         const uint64_t m = c.moduli[i];
         const uint64_t psi = min_root_h(m, 2ull * kN), psiinv = invmod_h(psi, m);
         c.psi[i] = psi;
-        c.primes[i] = make_prime_info(m);
         uint64_t x = 1, y = 1;
         TwPair* t = tw.data() + (size_t)i * kN;
         TwPair* it = itw.data() + (size_t)i * kN;
@@ -135,6 +136,7 @@ void context_init(Context& c, const std::vector<uint64_t>& q, const std::vector<
             x = mulmod_h(x, psi, m);
             y = mulmod_h(y, psiinv, m);
         }
+        c.primes[i] = make_prime_info(m, it[1].w);
     }
     if (hipSetDevice(device) != hipSuccess) throw std::runtime_error("hipSetDevice failed");
     auto up = [](void** d, const void* h, size_t bytes) {

@@ -20,8 +20,9 @@ struct TwPair {
 
 struct PrimeInfo {
     uint64_t q;
-    uint64_t ninv, ninv_p;   // N^-1 mod q and Shoup companion
-    uint64_t mu_hi, mu_lo;   // floor(2^128 / q)
+    uint64_t ninv, ninv_p;      // N^-1 mod q and Shoup companion
+    uint64_t w1ninv, w1ninv_p;  // inverse-table entry 1 (psi^-N/2) times N^-1: the last inverse stage
+    uint64_t mu_hi, mu_lo;      // floor(2^128 / q)
 };
 
 // One limb to transform: offset (in units of N words) from the base pointer, and its prime index.
@@ -66,7 +67,7 @@ struct Context {
     TwPair* d_tw = nullptr;   // [L+K][N] forward table (brev order)
     TwPair* d_itw = nullptr;  // [L+K][N] inverse table (brev order)
     PrimeInfo* d_primes = nullptr;
-    NttMode ntt_mode = NttMode::Fused;
+    NttMode ntt_mode = NttMode::TwoPass;
     // cached device job lists keyed by a shape string (list, distinct primes in it)
     std::map<std::string, std::pair<Job*, uint32_t>> job_cache;
     std::map<std::string, BConvPlan> bconv_cache;

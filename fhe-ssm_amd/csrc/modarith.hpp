@@ -22,6 +22,29 @@ __device__ __forceinline__ uint64_t shoup_lazy(uint64_t x, uint64_t w, uint64_t 
 
 __device__ __forceinline__ uint64_t csub(uint64_t x, uint64_t q) { return x >= q ? x - q : x; }
 
+// Shoup multiply from 32-bit pieces, for q < 2^61 and any x < 2^64; result in [0, 4q).
+// The quotient H'' = x1*p1 + hi(x1*p0) + hi(x0*p1) drops the low partial product and the carries of the
+// middle terms, so H - 2 <= H'' <= H (H = floor(x * wp / 2^64), for which x*w - H*q lies in [0, 2q)).
+// The remainder is accumulated with nq = 2^64 - q so that every step is a multiply-add mod 2^64:
+// 2 mul_hi + 2 mad_u64 + 4 mul_lo + 1 mad_u64 + adds.
+__device__ __forceinline__ uint64_t shoup_lazy4(uint64_t x, uint64_t w, uint64_t wp, uint64_t nq) {
+    const uint32_t x0 = (uint32_t)x, x1 = (uint32_t)(x >> 32);
+    const uint32_t p0 = (uint32_t)wp, p1 = (uint32_t)(wp >> 32);
+    const uint64_t h = (uint64_t)x1 * p1 + ((uint64_t)__umulhi(x1, p0) + __umulhi(x0, p1));
+    const uint32_t h0 = (uint32_t)h, h1 = (uint32_t)(h >> 32);
+    const uint32_t w0 = (uint32_t)w, w1 = (uint32_t)(w >> 32);
+    const uint32_t n0 = (uint32_t)nq, n1 = (uint32_t)(nq >> 32);
+    const uint64_t t = (uint64_t)x0 * w0 + (uint64_t)h0 * n0;
+    const uint32_t hi = (uint32_t)(t >> 32) + x1 * w0 + x0 * w1 + h1 * n0 + h0 * n1;
+    return ((uint64_t)hi << 32) | (uint32_t)t;
+}
+
+// x in [0, 2c) with c < 2^62 -> [0, c): the difference is negative exactly when x < c
+__device__ __forceinline__ uint64_t csub_s(uint64_t x, uint64_t c) {
+    const uint64_t d = x - c;
+    return (int64_t)d < 0 ? x : d;
+}
+
 __device__ __forceinline__ uint64_t shoup(uint64_t x, uint64_t w, uint64_t wp, uint64_t q) {
     return csub(shoup_lazy(x, w, wp, q), q);
 }

@@ -14,7 +14,8 @@
 //   pass B  (forward stages 8..15 / inverse 0..7): butterflies of stride < 256 inside each
 //           contiguous 256-word block.  A tile = 16 blocks.
 // Inside a tile each of 256 threads holds 16 words in registers and performs 4 stages (a radix-16
-// step) between two LDS exchanges.  Values stay lazily reduced (Harvey) in [0, 4q) between stages.
+// step) between two LDS exchanges.  Values stay lazily reduced (Harvey): [0, 8q) forward, [0, 4q)
+// inverse, with the twiddle product from shoup_lazy4; N^-1 is folded into the last inverse stage.
 //
 // Launch layout: a "job" is one limb (offset in units of N words + prime index).  Jobs are
 // enumerated prime-major so that concurrently running workgroups share one prime's twiddle table
@@ -44,26 +45,35 @@ __device__ __forceinline__ void job_of(const JobSpec& js, uint32_t u, uint32_t& 
     }
 }
 
-__device__ __forceinline__ void ct_bfly(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q, uint64_t q2) {
-    const uint64_t x = X >= q2 ? X - q2 : X;
-    const uint64_t t = shoup_lazy(Y, w.w, w.wp, q);
+// Forward (Cooley-Tukey) butterfly, values kept in [0, 8q) (q < 2^60): X is brought to [0, 4q), the
+// twiddle product is in [0, 4q), so X + T and X - T + 4q stay in [0, 8q).
+__device__ __forceinline__ void ct_bfly(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q4, uint64_t nq) {
+    const uint64_t x = csub_s(X, q4);
+    const uint64_t t = shoup_lazy4(Y, w.w, w.wp, nq);
     X = x + t;
-    Y = x - t + q2;
+    Y = x + q4 - t;
 }
 
-__device__ __forceinline__ void gs_bfly(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q, uint64_t q2) {
-    uint64_t s = X + Y;
-    s = s >= q2 ? s - q2 : s;
-    const uint64_t d = X - Y + q2;
+// Inverse (Gentleman-Sande) butterfly, values kept in [0, 4q).
+__device__ __forceinline__ void gs_bfly(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q4, uint64_t nq) {
+    const uint64_t s = csub_s(X + Y, q4);
+    const uint64_t d = X + q4 - Y;
     X = s;
-    Y = shoup_lazy(d, w.w, w.wp, q);
+    Y = shoup_lazy4(d, w.w, w.wp, nq);
+}
+
+// [0, 8q) -> [0, q)
+__device__ __forceinline__ uint64_t canon8(uint64_t v, uint64_t q) {
+    v = csub_s(v, q << 2);
+    v = csub_s(v, q << 1);
+    return csub_s(v, q);
 }
 
 // ---------------------------------------------------------------- forward pass A (strided columns)
 // tile: columns [16*tile, 16*tile + 16).  g: thread id within the 256-thread group.
 __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
                                            int tile, int g, uint64_t* lds) {
-    const uint64_t q2 = q << 1;
+    const uint64_t q4 = q << 2, nq = 0 - q;
     const int cl = g & 15, rg = g >> 4;
     const int col = tile * 16 + cl;
     uint64_t x[16];
@@ -76,7 +86,7 @@ __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            ct_bfly(x[k], x[k + h], tw[(1 << s) + (k >> (4 - s))], q, q2);
+            ct_bfly(x[k], x[k + h], tw[(1 << s) + (k >> (4 - s))], q4, nq);
         }
     }
 #pragma unroll
@@ -91,7 +101,7 @@ __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            ct_bfly(x[k], x[k + h], tw[(1 << s) + ((16 * rg + k) >> (8 - s))], q, q2);
+            ct_bfly(x[k], x[k + h], tw[(1 << s) + ((16 * rg + k) >> (8 - s))], q4, nq);
         }
     }
 #pragma unroll
@@ -101,7 +111,7 @@ __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPai
 // ---------------------------------------------------------------- forward pass B (256-word blocks)
 __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
                                            int tile, int g, uint64_t* lds) {
-    const uint64_t q2 = q << 1;
+    const uint64_t q4 = q << 2, nq = 0 - q;
     const int bl = g >> 4, rl = g & 15;
     const int b = tile * 16 + bl;  // block index within the limb
     uint64_t* blk = a + 256 * b;
@@ -117,7 +127,7 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            ct_bfly(x[k], x[k + h], t[k >> (4 - s)], q, q2);
+            ct_bfly(x[k], x[k + h], t[k >> (4 - s)], q4, nq);
         }
     }
     // LDS word index of r: r + (r >> 4)
@@ -134,15 +144,12 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            ct_bfly(x[k], x[k + h], t[(16 * rl + k) >> (8 - s)], q, q2);
+            ct_bfly(x[k], x[k + h], t[(16 * rl + k) >> (8 - s)], q4, nq);
         }
     }
     // canonical [0, q), then transpose through LDS for coalesced stores
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-        uint64_t v = x[k] >= q2 ? x[k] - q2 : x[k];
-        x[k] = v >= q ? v - q : v;
-    }
+    for (int k = 0; k < 16; k++) x[k] = canon8(x[k], q);
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) L[17 * rl + k] = x[k];
@@ -155,7 +162,7 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
 // GS stages with t = 2^u, u = 0..7: m = 2^(15-u), twiddle m + (j >> (u+1)), j = 256 b + r.
 __device__ __forceinline__ void inv_b_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
                                            int tile, int g, uint64_t* lds) {
-    const uint64_t q2 = q << 1;
+    const uint64_t q4 = q << 2, nq = 0 - q;
     const int bl = g >> 4, rl = g & 15;
     const int b = tile * 16 + bl;
     uint64_t* blk = a + 256 * b;
@@ -174,7 +181,7 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            gs_bfly(x[k], x[k + h], t[(16 * rl + k) >> (u + 1)], q, q2);
+            gs_bfly(x[k], x[k + h], t[(16 * rl + k) >> (u + 1)], q4, nq);
         }
     }
     __syncthreads();
@@ -191,7 +198,7 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            gs_bfly(x[k], x[k + h], t[k >> (u - 3)], q, q2);
+            gs_bfly(x[k], x[k + h], t[k >> (u - 3)], q4, nq);
         }
     }
 #pragma unroll
@@ -201,8 +208,8 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* __restrict__ a, const TwPai
 // ---------------------------------------------------------------- inverse pass A (strided columns)
 // GS stages with t = 2^(8+u), u = 0..7: m = 2^(7-u), twiddle m + (r >> (u+1)); then * N^-1.
 __device__ __forceinline__ void inv_a_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
-                                           TwPair ninv, int tile, int g, uint64_t* lds) {
-    const uint64_t q2 = q << 1;
+                                           TwPair ninv, TwPair w1ninv, int tile, int g, uint64_t* lds) {
+    const uint64_t q4 = q << 2, nq = 0 - q;
     const int cl = g & 15, rg = g >> 4;
     const int col = tile * 16 + cl;
     uint64_t x[16];
@@ -215,7 +222,7 @@ __device__ __forceinline__ void inv_a_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            gs_bfly(x[k], x[k + h], tw[(128 >> u) + ((16 * rg + k) >> (u + 1))], q, q2);
+            gs_bfly(x[k], x[k + h], tw[(128 >> u) + ((16 * rg + k) >> (u + 1))], q4, nq);
         }
     }
 #pragma unroll
@@ -223,18 +230,28 @@ __device__ __forceinline__ void inv_a_tile(uint64_t* __restrict__ a, const TwPai
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = lds[(rg + 16 * k) * 16 + cl];
-    // u = 4..7: r = rg + 16k, pairs differ in bit (u-4) of k; r >> (u+1) = k >> (u-3)
+    // u = 4..6: r = rg + 16k, pairs differ in bit (u-4) of k; r >> (u+1) = k >> (u-3)
 #pragma unroll
-    for (int u = 4; u < 8; u++) {
+    for (int u = 4; u < 7; u++) {
         const int h = 1 << (u - 4);
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            gs_bfly(x[k], x[k + h], tw[(128 >> u) + (k >> (u - 3))], q, q2);
+            gs_bfly(x[k], x[k + h], tw[(128 >> u) + (k >> (u - 3))], q4, nq);
         }
     }
+    // u = 7 (m = 1, stride N/2) with N^-1 folded in: X' = (X + Y) N^-1, Y' = (X - Y) w_1 N^-1
 #pragma unroll
-    for (int k = 0; k < 16; k++) a[col + 256 * (rg + 16 * k)] = shoup(x[k], ninv.w, ninv.wp, q);
+    for (int k = 0; k < 8; k++) {
+        const uint64_t X = x[k], Y = x[k + 8];
+        x[k] = shoup_lazy4(X + Y, ninv.w, ninv.wp, nq);
+        x[k + 8] = shoup_lazy4(X + q4 - Y, w1ninv.w, w1ninv.wp, nq);
+    }
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        const uint64_t v = csub_s(x[k], q << 1);
+        a[col + 256 * (rg + 16 * k)] = csub_s(v, q);
+    }
 }
 
 // ---------------------------------------------------------------- kernels
@@ -268,8 +285,8 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_a(uint64_t* data, JobS
     uint32_t off, prime;
     job_of(js, blockIdx.y, off, prime);
     const PrimeInfo& P = primes[prime];
-    inv_a_tile(data + (size_t)off * kN, tw_all + (size_t)prime * kN, P.q, TwPair{P.ninv, P.ninv_p}, blockIdx.x,
-               threadIdx.x, lds);
+    inv_a_tile(data + (size_t)off * kN, tw_all + (size_t)prime * kN, P.q, TwPair{P.ninv, P.ninv_p},
+               TwPair{P.w1ninv, P.w1ninv_p}, blockIdx.x, threadIdx.x, lds);
 }
 
 // Fused: one limb per workgroup of 4 x 256 threads; each 256-thread group owns one LDS tile.
@@ -312,7 +329,7 @@ __global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_inv_fused(ui
         __syncthreads();
     }
     for (int t = grp; t < 16; t += kFusedGroups) {
-        inv_a_tile(a, tw, P.q, TwPair{P.ninv, P.ninv_p}, t, g, L);
+        inv_a_tile(a, tw, P.q, TwPair{P.ninv, P.ninv_p}, TwPair{P.w1ninv, P.w1ninv_p}, t, g, L);
         __syncthreads();
     }
 }

@@ -68,7 +68,7 @@ int ckks_context_info(const ckks_context* ctx, uint32_t* n, uint32_t* num_q, uin
 /* moduli (num_q + num_p) and the primitive 2N-th roots used by the NTT, chain order */
 int ckks_context_moduli(const ckks_context* ctx, uint64_t* out, uint32_t cap);
 int ckks_context_roots(const ckks_context* ctx, uint64_t* out, uint32_t cap);
-/* NTT schedule: 0 = two kernels (pass A, pass B), 1 = fused one-limb-per-workgroup (default) */
+/* NTT schedule: 0 = two kernels (pass A, pass B; default), 1 = fused one-limb-per-workgroup */
 int ckks_set_ntt_mode(ckks_context* ctx, int mode);
 
 /* ---- device memory helpers (plain HIP; any HIP allocation works with the compute calls) ---- */
