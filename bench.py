@@ -7,6 +7,8 @@ Workloads (inputs seeded and resident in HBM before the t
          errors sigma=3.19, slots uniform in [-1,1] at scale 2^50.  One step = one batched
          EvalMult+Rescale over the 64 pairs.  value = HMult+relin ops/s.
   ntt    config 1: forward then inverse NTT over 64 ct x 2 polys x 24 limbs.  value = algorithmic GB/s.
+  pcmm   config 3: 768x768 plaintext matrix x one ciphertext (L=16) by BSGS 28 x 28.  value = ms.
+The default run also reports the config-1 and config-3 figures beside the config-2 metric.
 
 Roofline: the engine records HIP events on its launch stream around every kernel of one profiled
 step (ckks_profile_*); the dominant kernel by time is reported with achieved = algorithmic bytes per
@@ -165,6 +167,64 @@ def cpu_baseline_hmult(seed, budget_s=20.0):
             "sample": f"{done} HMult+relin+rescale of one config-2 pair ({el:.1f} s), C oracle, one thread"}
 
 
+# ----------------------------------------------------------------------------------------- config 3
+def bench_pcmm(ckks, torch, steps_n, warmup, seed):
+    """768 x 768 plaintext weights N(0, 1/768) times one ciphertext at L=16, BSGS 28 baby x 28 giant."""
+    from pcmm_util import bsgs_diagonals, replicate, steps
+    d, bs, l = 768, 28, 16
+    ctx = ckks.Context(num_q=L2, num_p=K2, dnum=DNUM2, q_bits=54, p_bits=60, scale=2.0**50)
+    scale = 2.0**50
+    sk = ctx.secret(seed_bytes("pcmm-secret", seed), 192)
+    dev = torch.device("cuda:0")
+    bst, gst = steps(d, bs)
+    T = L2 + K2
+    keys = torch.empty((len(bst) + len(gst), DNUM2, 2, T, N), dtype=torch.int64, device=dev)
+    kb = DNUM2 * 2 * T * N * 8
+    for i, s_ in enumerate(bst + gst):
+        ctx.keygen_automorphism(sk, ckks.rotation_index(s_), seed_bytes(f"rk{i}a", seed), seed_bytes(f"rk{i}e", seed),
+                                keys.data_ptr() + i * kb)
+    bptr = [keys.data_ptr() + i * kb for i in range(len(bst))]
+    gptr = [keys.data_ptr() + (len(bst) + i) * kb for i in range(len(gst))]
+    rng = np.random.default_rng(seed)
+    W = rng.normal(0.0, np.sqrt(1.0 / d), (d, d))
+    u = rng.uniform(-1.0, 1.0, d)
+    diags = bsgs_diagonals(W, bs)
+    D = torch.empty((d, l, N), dtype=torch.int64, device=dev)
+    for k in range(d):
+        ctx.encode(diags[k], l, scale, D.data_ptr() + k * l * N * 8)
+    del diags
+    pt = torch.empty((l, N), dtype=torch.int64, device=dev)
+    ct = torch.empty((2, l, N), dtype=torch.int64, device=dev)
+    out = torch.empty((2, l - 1, N), dtype=torch.int64, device=dev)
+    ctx.encode(replicate(u), l, scale, pt.data_ptr())
+    ctx.encrypt(sk, pt.data_ptr(), l, seed_bytes("pcmm-enc", seed), 0, ct.data_ptr())
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    sh = ctypes.c_void_p(stream.cuda_stream)
+
+    def step():
+        ctx.linear_transform_bsgs(ct.data_ptr(), l, D.data_ptr(), d, bs, bptr, gptr, out.data_ptr(), sh)
+
+    wall, per = timed_steps(torch, stream, step, steps_n, warmup)
+    got = ctx.decrypt(sk, out.data_ptr(), l - 1, scale * scale / ctx.moduli[l - 1])[:d]
+    want = W @ u
+    rel = float(np.sqrt(np.mean((got - want) ** 2)) / np.sqrt(np.mean(want ** 2)))
+    ctx.profile_reset()
+    ctx.profile(True)
+    step()
+    torch.cuda.synchronize()
+    ctx.profile(False)
+    rep = ctx.profile_report()
+    ctx.profile_reset()
+    ms = wall * 1e3 / steps_n
+    # algorithmic bytes (SURVEY 8d config 3): evk 56 x 96 limbs + 768 x 16 plaintext limbs + ct in/out 62 limbs
+    alg = (56 * 96 + d * l + 62) * LIMB_BYTES
+    return {"ms_per_pcmm": round(ms, 4), "relErrRms_vs_fp64": rel, "algorithmic_GBps": round(alg / (ms * 1e-3) / 1e9, 1),
+            "kernels": kernel_table(rep), "roofline": roofline_from_profile(rep),
+            "workload": "config3: 768x768 fp64 weights N(0,1/768) x 1 ct at L=16, BSGS 28 baby x 28 giant, "
+                        "period-768 replicated layout"}
+
+
 # ----------------------------------------------------------------------------------------- config 1
 def ntt_bytes():
     limbs = 2 * N_PAIRS * L2
@@ -241,10 +301,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="hmult", choices=["hmult", "ntt"])
+    ap.add_argument("--workload", default="hmult", choices=["hmult", "ntt", "pcmm"])
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ntt-line", action="store_true", help="skip the config-1 NTT figure in the hmult run")
+    ap.add_argument("--no-pcmm-line", action="store_true", help="skip the config-3 PCMM figure in the hmult run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design note, "
@@ -262,14 +323,25 @@ def main():
             n = bench_ntt(ckks, torch, max(3, args.steps // 2), 1, args.seed)
             extra["ntt_config1"] = {"GBps": n["value"], "ms_per_step": n["ms_per_step"],
                                     "roofline": n["roofline"]}
+        if not args.no_pcmm_line:
+            p = bench_pcmm(ckks, torch, max(3, args.steps // 2), 1, args.seed)
+            extra["pcmm_config3"] = {k: p[k] for k in ("ms_per_pcmm", "relErrRms_vs_fp64", "algorithmic_GBps",
+                                                        "roofline")}
         cpu = None if args.no_cpu_baseline else cpu_baseline_hmult(args.seed)
+    elif args.workload == "pcmm":
+        p = bench_pcmm(ckks, torch, args.steps, args.warmup, args.seed)
+        res = {"metric": "PCMM ms (768x768 BSGS, N=2^16, L=16)", "value": p["ms_per_pcmm"], "unit": "ms",
+               "ms_per_step": p["ms_per_pcmm"], "dtype": "u64", "config": {"workload": p["workload"]},
+               "kernels": p["kernels"], "roofline": p["roofline"],
+               "check": {"relErrRms_vs_fp64": p["relErrRms_vs_fp64"]}}
+        extra, cpu = {}, None
     else:
         res = bench_ntt(ckks, torch, args.steps, args.warmup, args.seed)
         extra = {}
         cpu = None if args.no_cpu_baseline else cpu_baseline_ntt(args.seed)
     out = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
-           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
+           "higher_is_better": res["unit"] != "ms", "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
            "data": "synthetic (seeded)", "config": res["config"], "roofline": res["roofline"],
            "kernels": res["kernels"]}
     if "check" in res:

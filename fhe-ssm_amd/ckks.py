@@ -56,6 +56,11 @@ SIGNATURES = {
     "ckks_rotation_index": (_u32, [ctypes.c_int64]),
     "ckks_automorphism": (_int, [_vp, _vp, _u32, _u32, _u32, _vp, _vp]),
     "ckks_eval_rotate": (_int, [_vp, _vp, _u32, _u32, ctypes.c_int64, _vp, _vp, _vp]),
+    "ckks_eval_mult_plain": (_int, [_vp, _vp, _u32, _u32, _vp, _int, _vp, _vp]),
+    "ckks_eval_add_plain": (_int, [_vp, _vp, _u32, _u32, _vp, _int, _vp, _vp]),
+    "ckks_eval_rotate_hoisted": (_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp]),
+    "ckks_eval_rotate_many": (_int, [_vp, _vp, _u32, _u32, _vp, _vp, _vp, _vp]),
+    "ckks_linear_transform_bsgs": (_int, [_vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _vp]),
     "ckks_secret_generate": (_int, [_vp, _vp, _u32, ctypes.POINTER(_vp)]),
     "ckks_secret_destroy": (None, [_vp]),
     "ckks_secret_coeffs": (_int, [_vp, _vp, _u32]),
@@ -230,6 +235,27 @@ class Context:
         check(load().ckks_eval_rotate(self.h, d_ct, batch, level, step, d_evk, d_out, stream))
 
 
+    def eval_mult_plain(self, d_ct, batch, level, d_pt, d_out, pt_shared=True, stream=None):
+        check(load().ckks_eval_mult_plain(self.h, d_ct, batch, level, d_pt, 1 if pt_shared else 0, d_out, stream))
+
+    def eval_add_plain(self, d_ct, batch, level, d_pt, d_out, pt_shared=True, stream=None):
+        check(load().ckks_eval_add_plain(self.h, d_ct, batch, level, d_pt, 1 if pt_shared else 0, d_out, stream))
+
+    def eval_rotate_hoisted(self, d_ct, level, steps, d_evks, d_out, stream=None):
+        st = np.ascontiguousarray(np.asarray(steps, dtype=np.int64))
+        keys = _ptr_array(d_evks)
+        check(load().ckks_eval_rotate_hoisted(self.h, d_ct, level, _ptr(st), len(st), keys, d_out, stream))
+
+    def eval_rotate_many(self, d_cts, level, steps, d_evks, d_out, stream=None):
+        st = np.ascontiguousarray(np.asarray(steps, dtype=np.int64))
+        keys = _ptr_array(d_evks)
+        check(load().ckks_eval_rotate_many(self.h, d_cts, len(st), level, _ptr(st), keys, d_out, stream))
+
+    def linear_transform_bsgs(self, d_ct, level, d_diags, n_diag, baby_steps, baby_evks, giant_evks, d_out,
+                              stream=None):
+        check(load().ckks_linear_transform_bsgs(self.h, d_ct, level, d_diags, n_diag, baby_steps,
+                                                _ptr_array(baby_evks), _ptr_array(giant_evks), d_out, stream))
+
     # client side ------------------------------------------------------------------------------
     def secret(self, seed: bytes, hamming_weight: int = 192) -> "Secret":
         return Secret(self, seed, hamming_weight)
@@ -276,6 +302,14 @@ class Context:
             out[name.value.decode()] = (n.value, ms.value, by.value)
             i += 1
         return out
+
+
+def _ptr_array(ptrs):
+    ptrs = list(ptrs)
+    if not ptrs:
+        return None
+    arr = (_vp * len(ptrs))(*ptrs)
+    return ctypes.cast(arr, _vp)
 
 
 def _seed(seed: bytes):

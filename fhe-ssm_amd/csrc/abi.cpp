@@ -93,18 +93,6 @@ int check_ctx_level(const ckks_context* ctx, uint32_t level, bool need_p) {
     return CKKS_OK;
 }
 
-uint32_t rot_index(int64_t k) {
-    const uint64_t M = 2ull * fhe::kN, ord = fhe::kN / 2;  // 5 has order N/2 in (Z/2N)^*
-    int64_t e = k % (int64_t)ord;
-    if (e < 0) e += (int64_t)ord;
-    uint64_t r = 1, b = 5;
-    for (uint64_t x = (uint64_t)e; x; x >>= 1) {
-        if (x & 1) r = r * b % M;
-        b = b * b % M;
-    }
-    return (uint32_t)r;
-}
-
 }  // namespace
 
 extern "C" {
@@ -312,7 +300,74 @@ int ckks_eval_add(ckks_context* ctx, const uint64_t* d_x, const uint64_t* d_y, u
     });
 }
 
-uint32_t ckks_rotation_index(int64_t step) { return rot_index(step); }
+uint32_t ckks_rotation_index(int64_t step) { return fhe::rotation_index(step); }
+
+int ckks_eval_mult_plain(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level, const uint64_t* d_pt,
+                         int pt_shared, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_ct || !d_pt || !d_out) return fail(CKKS_EINVAL, "null buffer");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::mul_plain(ctx->c, d_ct, batch, level, d_pt, pt_shared != 0, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_add_plain(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level, const uint64_t* d_pt,
+                        int pt_shared, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_ct || !d_pt || !d_out) return fail(CKKS_EINVAL, "null buffer");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::add_plain(ctx->c, d_ct, batch, level, d_pt, pt_shared != 0, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_rotate_hoisted(ckks_context* ctx, const uint64_t* d_ct, uint32_t level, const int64_t* steps,
+                             uint32_t n, const uint64_t* const* d_evks, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_ct || !steps || !d_evks || !d_out) return fail(CKKS_EINVAL, "null argument");
+    for (uint32_t i = 0; i < n; i++)
+        if (!d_evks[i]) return fail(CKKS_EINVAL, "null key");
+    if (!n) return CKKS_OK;
+    return guarded([&] {
+        fhe::rotate_hoisted(ctx->c, d_ct, level, steps, n, d_evks, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_rotate_many(ckks_context* ctx, const uint64_t* d_cts, uint32_t n, uint32_t level, const int64_t* steps,
+                          const uint64_t* const* d_evks, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_cts || !steps || !d_evks || !d_out || d_cts == d_out) return fail(CKKS_EINVAL, "null or aliased argument");
+    for (uint32_t i = 0; i < n; i++)
+        if (!d_evks[i]) return fail(CKKS_EINVAL, "null key");
+    if (!n) return CKKS_OK;
+    return guarded([&] {
+        fhe::rotate_list(ctx->c, d_cts, n, level, steps, d_evks, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_linear_transform_bsgs(ckks_context* ctx, const uint64_t* d_ct, uint32_t level, const uint64_t* d_diags,
+                               uint32_t n_diag, uint32_t baby_steps, const uint64_t* const* d_baby_evks,
+                               const uint64_t* const* d_giant_evks, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_ct || !d_diags || !d_out || n_diag == 0 || baby_steps == 0) return fail(CKKS_EINVAL, "bad argument");
+    const uint32_t ng = (n_diag + baby_steps - 1) / baby_steps;
+    if (baby_steps > 1 && !d_baby_evks) return fail(CKKS_EINVAL, "null baby keys");
+    if (ng > 1 && !d_giant_evks) return fail(CKKS_EINVAL, "null giant keys");
+    for (uint32_t i = 0; i + 1 < baby_steps; i++)
+        if (!d_baby_evks[i]) return fail(CKKS_EINVAL, "null baby key");
+    for (uint32_t i = 0; i + 1 < ng; i++)
+        if (!d_giant_evks[i]) return fail(CKKS_EINVAL, "null giant key");
+    return guarded([&] {
+        fhe::bsgs_matvec(ctx->c, d_ct, level, d_diags, n_diag, baby_steps, d_baby_evks, d_giant_evks, d_out,
+                         (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
 
 int ckks_automorphism(ckks_context* ctx, const uint64_t* d_in, uint32_t n_polys, uint32_t level, uint32_t g,
                       uint64_t* d_out, void* stream) {
@@ -331,7 +386,7 @@ int ckks_eval_rotate(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, ui
     if (!d_ct || !d_evk || !d_out || d_ct == d_out) return fail(CKKS_EINVAL, "null or aliased buffer");
     if (!batch) return CKKS_OK;
     return guarded([&] {
-        fhe::rotate(ctx->c, d_ct, batch, level, rot_index(step), d_evk, d_out, (hipStream_t)stream);
+        fhe::rotate(ctx->c, d_ct, batch, level, fhe::rotation_index(step), d_evk, d_out, (hipStream_t)stream);
         return CKKS_OK;
     });
 }

@@ -41,6 +41,18 @@ hipError_t launch_add(const Context& ctx, const uint64_t* x, const uint64_t* y, 
                       uint32_t l, hipStream_t st);
 hipError_t launch_automorph(const uint64_t* in, uint64_t* out, uint32_t n_polys, uint32_t l, uint32_t g,
                             hipStream_t st);
+hipError_t launch_ks_inner_list(const Context& ctx, const uint64_t* const* ext, const uint64_t* const* evk,
+                                uint64_t* acc, uint32_t n, uint32_t l, hipStream_t st);
+hipError_t launch_automorph_list(const Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n, uint32_t l,
+                                 const uint32_t* g, hipStream_t st);
+hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* baby, const uint64_t* diag, uint64_t* out, uint32_t nb,
+                           uint32_t n_diag, uint32_t ng, uint32_t l, hipStream_t st);
+hipError_t launch_mul_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
+                            uint32_t l, uint64_t pt_bstride, hipStream_t st);
+hipError_t launch_add_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
+                            uint32_t l, uint64_t pt_bstride, hipStream_t st);
+hipError_t launch_sum_list(const Context& ctx, const uint64_t* const* in, uint32_t n, uint64_t* out, uint32_t n_polys,
+                           uint32_t l, hipStream_t st);
 
 namespace {
 
@@ -202,7 +214,7 @@ void ks_inner(Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* 
 // x: [n_polys][E][N] evaluation form over Q_l * P (P limbs are overwritten: they are transformed to
 // coefficients in place).  out: [n_polys][l][N] = (x_Q - BConv_{P->Q}(x_P)) * P^-1 (+ add).
 void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
-                     hipStream_t st, uint32_t add_div) {
+                     hipStream_t st, uint32_t add_div, int64_t add_pstride) {
     check_level(ctx, l);
     const uint32_t E = l + ctx.K, K = ctx.K;
     if (K == 0) throw std::invalid_argument("ModDown needs special primes");
@@ -233,8 +245,9 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
         const uint64_t v = invmod_h(P, q);
         pinv[i] = TwPair{v, shoup_companion(v, q)};
     }
-    HIPX(launch_sub_scale(ctx, x, (uint64_t)E * W, conv, (uint64_t)l * W, add, (uint64_t)add_div * l * W, add_div, out,
-                          (uint64_t)l * W, n_polys, l, pinv.data(), st));
+    const uint64_t aps = add_pstride < 0 ? (uint64_t)add_div * l * W : (uint64_t)add_pstride;
+    HIPX(launch_sub_scale(ctx, x, (uint64_t)E * W, conv, (uint64_t)l * W, add, aps, add_div, out, (uint64_t)l * W,
+                          n_polys, l, pinv.data(), st));
 }
 
 // ------------------------------------------------------------------ key switch
@@ -316,6 +329,109 @@ void rotate(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, uint32_t g
                           hipMemcpyDeviceToDevice, st));
     keyswitch(ctx, c1, B, l, evk, ct, ks, st, 2);
     HIPX(launch_automorph(ks, out, 2 * B, l, g, st));
+}
+
+uint32_t rotation_index(int64_t k) {
+    const uint64_t M = 2ull * kN, ord = kN / 2;  // 5 has order N/2 in (Z/2N)^*
+    int64_t e = k % (int64_t)ord;
+    if (e < 0) e += (int64_t)ord;
+    uint64_t r = 1, b = 5;
+    for (uint64_t x = (uint64_t)e; x; x >>= 1) {
+        if (x & 1) r = r * b % M;
+        b = b * b % M;
+    }
+    return (uint32_t)r;
+}
+
+// n ciphertexts [n][2][l][N], each rotated by its own step with its own key -> out [n][2][l][N]
+void rotate_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l, const int64_t* steps,
+                 const uint64_t* const* evk, uint64_t* out, hipStream_t st) {
+    check_level(ctx, l);
+    if (n == 0) return;
+    if (n > 64) throw std::invalid_argument("at most 64 rotations per call");
+    const uint32_t D = num_digits(ctx, l), E = l + ctx.K;
+    uint64_t* c1 = (uint64_t*)ws_get(ctx, WS_C1, (size_t)n * l * W * 8);
+    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)n * D * E * W * 8);
+    uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)n * 2 * E * W * 8);
+    uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)n * 2 * l * W * 8);
+    HIPX(hipMemcpy2DAsync(c1, (size_t)l * W * 8, cts + (size_t)l * W, (size_t)2 * l * W * 8, (size_t)l * W * 8, n,
+                          hipMemcpyDeviceToDevice, st));
+    modup(ctx, c1, ext, n, l, st);
+    std::vector<const uint64_t*> ep(n);
+    std::vector<uint32_t> g(n);
+    for (uint32_t c = 0; c < n; c++) {
+        ep[c] = ext + (size_t)c * D * E * W;
+        g[c] = rotation_index(steps[c]);
+    }
+    HIPX(launch_ks_inner_list(ctx, ep.data(), evk, acc, n, l, st));
+    moddown_inplace(ctx, acc, 2 * n, l, cts, ks, st, 2);
+    HIPX(launch_automorph_list(ctx, ks, out, n, l, g.data(), st));
+}
+
+// one ciphertext [2][l][N] rotated by n steps with one shared ModUp -> out [n][2][l][N]
+void rotate_hoisted(Context& ctx, const uint64_t* ct, uint32_t l, const int64_t* steps, uint32_t n,
+                    const uint64_t* const* evk, uint64_t* out, hipStream_t st) {
+    check_level(ctx, l);
+    if (n == 0) return;
+    if (n > 64) throw std::invalid_argument("at most 64 rotations per call");
+    const uint32_t E = l + ctx.K;
+    const uint32_t D = num_digits(ctx, l);
+    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)D * E * W * 8);
+    uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)n * 2 * E * W * 8);
+    uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)n * 2 * l * W * 8);
+    modup(ctx, ct + (size_t)l * W, ext, 1, l, st);
+    std::vector<const uint64_t*> ep(n, ext);
+    std::vector<uint32_t> g(n);
+    for (uint32_t c = 0; c < n; c++) g[c] = rotation_index(steps[c]);
+    HIPX(launch_ks_inner_list(ctx, ep.data(), evk, acc, n, l, st));
+    // c0 (the same for every rotation) is the ModDown addend of poly 0 of each output
+    moddown_inplace(ctx, acc, 2 * n, l, ct, ks, st, 2, 0);
+    HIPX(launch_automorph_list(ctx, ks, out, n, l, g.data(), st));
+}
+
+void mul_plain(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const uint64_t* pt, bool pt_shared,
+               uint64_t* out, hipStream_t st) {
+    check_level(ctx, l);
+    HIPX(launch_mul_plain(ctx, ct, pt, out, B, l, pt_shared ? 0 : (uint64_t)l * W, st));
+}
+
+void add_plain(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const uint64_t* pt, bool pt_shared,
+               uint64_t* out, hipStream_t st) {
+    check_level(ctx, l);
+    HIPX(launch_add_plain(ctx, ct, pt, out, B, l, pt_shared ? 0 : (uint64_t)l * W, st));
+}
+
+// Baby-step giant-step diagonal matrix-vector product (gpu_real_model.cu:2767-2823):
+// y = rescale( sum_g rot_{g*bs}( sum_j diag'_{g*bs+j} (.) rot_j(u) ) ), diagonals pre-rotated by -g*bs.
+// Babies rot_1..rot_{bs-1} share one ModUp (hoisted); the ng-1 giant rotations run as one batch.
+void bsgs_matvec(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* diags, uint32_t n_diag, uint32_t bs,
+                 const uint64_t* const* baby_evk, const uint64_t* const* giant_evk, uint64_t* out, hipStream_t st) {
+    check_level(ctx, l);
+    if (l < 2) throw std::invalid_argument("matvec consumes a level: needs l >= 2");
+    if (bs == 0 || bs > 32) throw std::invalid_argument("baby steps must be in [1, 32]");
+    const uint32_t ng = (n_diag + bs - 1) / bs;
+    if (ng == 0 || ng > 65) throw std::invalid_argument("giant steps must be in [1, 65]");
+    const size_t ctw = (size_t)2 * l * W;
+    uint64_t* baby = (uint64_t*)ws_get(ctx, WS_BABY, (size_t)bs * ctw * 8);
+    uint64_t* v = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)ng * ctw * 8);
+    uint64_t* vr = (uint64_t*)ws_get(ctx, WS_GROT, (size_t)ng * ctw * 8);
+    uint64_t* sum = (uint64_t*)ws_get(ctx, WS_SUM, ctw * 8);
+    HIPX(hipMemcpyAsync(baby, ct, ctw * 8, hipMemcpyDeviceToDevice, st));
+    if (bs > 1) {
+        std::vector<int64_t> steps(bs - 1);
+        for (uint32_t j = 1; j < bs; j++) steps[j - 1] = j;
+        rotate_hoisted(ctx, ct, l, steps.data(), bs - 1, baby_evk, baby + ctw, st);
+    }
+    HIPX(launch_bsgs_mac(ctx, baby, diags, v, bs, n_diag, ng, l, st));
+    std::vector<const uint64_t*> terms(1, v);
+    if (ng > 1) {
+        std::vector<int64_t> steps(ng - 1);
+        for (uint32_t g = 1; g < ng; g++) steps[g - 1] = (int64_t)g * bs;
+        rotate_list(ctx, v + ctw, ng - 1, l, steps.data(), giant_evk, vr, st);
+        for (uint32_t g = 1; g < ng; g++) terms.push_back(vr + (size_t)(g - 1) * ctw);
+    }
+    HIPX(launch_sum_list(ctx, terms.data(), (uint32_t)terms.size(), sum, 2, l, st));
+    rescale(ctx, sum, 2, l, out, st);
 }
 
 void add(Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys, uint32_t l,

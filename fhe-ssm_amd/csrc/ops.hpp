@@ -15,6 +15,10 @@ enum WsSlot : uint32_t {
     WS_D01,
     WS_RELIN,
     WS_C1,
+    WS_BABY,
+    WS_GIANT,
+    WS_GROT,
+    WS_SUM,
     WS_COUNT
 };
 
@@ -26,8 +30,9 @@ void modup(Context& ctx, const uint64_t* x, uint64_t* ext, uint32_t B, uint32_t 
 void ks_inner(Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* acc, uint32_t B, uint32_t l,
               hipStream_t st);
 // add (optional): applied to output polys pc with pc % add_div == 0, at add + (pc / add_div) * add_div * l * N
+// add_pstride < 0: add_div * l * N (the addend is a ciphertext batch); 0: one addend for every poly
 void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
-                     hipStream_t st, uint32_t add_div = 1);
+                     hipStream_t st, uint32_t add_div = 1, int64_t add_pstride = -1);
 void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
                uint64_t* out2, hipStream_t st, uint32_t add_div = 1);
 void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uint64_t* out, hipStream_t st);
@@ -37,6 +42,17 @@ void rotate(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, uint32_t g
             hipStream_t st);
 void add(Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys, uint32_t l,
          hipStream_t st);
+uint32_t rotation_index(int64_t k);
+void rotate_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l, const int64_t* steps,
+                 const uint64_t* const* evk, uint64_t* out, hipStream_t st);
+void rotate_hoisted(Context& ctx, const uint64_t* ct, uint32_t l, const int64_t* steps, uint32_t n,
+                    const uint64_t* const* evk, uint64_t* out, hipStream_t st);
+void mul_plain(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const uint64_t* pt, bool pt_shared,
+               uint64_t* out, hipStream_t st);
+void add_plain(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const uint64_t* pt, bool pt_shared,
+               uint64_t* out, hipStream_t st);
+void bsgs_matvec(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* diags, uint32_t n_diag, uint32_t bs,
+                 const uint64_t* const* baby_evk, const uint64_t* const* giant_evk, uint64_t* out, hipStream_t st);
 void automorph(Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n_polys, uint32_t l, uint32_t g,
                hipStream_t st);
 

@@ -208,6 +208,125 @@ __global__ __launch_bounds__(256) void k_automorph(const uint64_t* __restrict__ 
     out[base + k] = in[base + src];
 }
 
+// ------------------------------------------------------------------ list forms (one key per item)
+// acc[c][0/1][t] = sum_d ext_c[d][t] * evk_c[d][0/1][prime(t)] with per-item ext and evk pointers
+// (hoisted rotations share one ext; giant-step rotations have one ext each).
+constexpr int kMaxList = 64;
+
+struct ListPtrs {
+    const uint64_t* p[kMaxList];
+};
+
+__global__ __launch_bounds__(256) void k_ks_inner_list(ListPtrs ext, ListPtrs evk, uint64_t* __restrict__ acc,
+                                                       InnerArgs ia, const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t t = blockIdx.y, c = blockIdx.z;
+    const uint32_t p = ia.prime_of[t];
+    const Barrett br = barrett_of(primes[p]);
+    const uint64_t* x = ext.p[c] + (size_t)t * kN + k;
+    const uint64_t* e = evk.p[c] + (size_t)p * kN + k;
+    U128 s0{0, 0}, s1{0, 0};
+#pragma unroll
+    for (int d = 0; d < kMaxDigits; d++) {
+        if (d < (int)ia.D) {
+            const uint64_t v = x[(size_t)d * ia.E * kN];
+            mac128(s0, v, e[((size_t)d * 2 + 0) * ia.T * kN]);
+            mac128(s1, v, e[((size_t)d * 2 + 1) * ia.T * kN]);
+        }
+    }
+    uint64_t* o = acc + (size_t)c * 2 * ia.E * kN + (size_t)t * kN + k;
+    o[0] = reduce_u128(s0, br);
+    o[(size_t)ia.E * kN] = reduce_u128(s1, br);
+}
+
+// per-ciphertext automorphism index: [n][2][l][N], ciphertext c uses g[c]
+struct AutoList {
+    uint32_t g[kMaxList];
+};
+
+__global__ __launch_bounds__(256) void k_automorph_list(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
+                                                        uint32_t l, AutoList al) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y, pc = blockIdx.z;  // pc = 2 c + poly
+    const uint32_t g = al.g[pc >> 1];
+    const size_t base = ((size_t)pc * l + i) * kN;
+    const uint32_t e = (uint32_t)(((uint64_t)g * (2u * (__brev(k) >> (32 - kLogN)) + 1u)) & (2u * kN - 1u));
+    const uint32_t src = __brev((e - 1u) >> 1) >> (32 - kLogN);
+    out[base + k] = in[base + src];
+}
+
+// BSGS multiply-accumulate: babies [nb][2][l][N], diagonals [n_diag][l][N] (diagonal g*nb + j pairs with
+// baby j), out [ng][2][l][N]: out_g = sum_j baby_j (.) diag_{g*nb+j}.  Each thread keeps its word of every
+// baby in registers and streams the diagonals once.
+constexpr int kMaxBaby = 32;
+
+__global__ __launch_bounds__(256) void k_bsgs_mac(const uint64_t* __restrict__ baby, const uint64_t* __restrict__ diag,
+                                                  uint64_t* __restrict__ out, uint32_t nb, uint32_t n_diag, uint32_t ng,
+                                                  uint32_t l, const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y;
+    const Barrett br = barrett_of(primes[i]);
+    const size_t P = (size_t)l * kN, off = (size_t)i * kN + k;
+    uint64_t b0[kMaxBaby], b1[kMaxBaby];
+#pragma unroll
+    for (int j = 0; j < kMaxBaby; j++) {
+        if (j < (int)nb) {
+            b0[j] = baby[(size_t)j * 2 * P + off];
+            b1[j] = baby[(size_t)j * 2 * P + P + off];
+        }
+    }
+    for (uint32_t g = 0; g < ng; g++) {
+        U128 s0{0, 0}, s1{0, 0};
+#pragma unroll
+        for (int j = 0; j < kMaxBaby; j++) {
+            const uint32_t di = g * nb + j;
+            if (j < (int)nb && di < n_diag) {
+                const uint64_t m = diag[(size_t)di * P + off];
+                mac128(s0, b0[j], m);
+                mac128(s1, b1[j], m);
+            }
+        }
+        out[(size_t)g * 2 * P + off] = reduce_u128(s0, br);
+        out[(size_t)g * 2 * P + P + off] = reduce_u128(s1, br);
+    }
+}
+
+// ct (.) pt on both polys: ct [B][2][l][N], pt [B or 1][l][N] (pt_bstride 0 = shared plaintext)
+__global__ __launch_bounds__(256) void k_mul_plain(const uint64_t* __restrict__ ct, const uint64_t* __restrict__ pt,
+                                                   uint64_t* __restrict__ out, uint32_t l, uint64_t pt_bstride,
+                                                   const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y, pc = blockIdx.z;
+    const Barrett br = barrett_of(primes[i]);
+    const size_t o = ((size_t)pc * l + i) * kN + k;
+    const uint64_t m = pt[(size_t)(pc >> 1) * pt_bstride + (size_t)i * kN + k];
+    out[o] = mul_mod(ct[o], m, br);
+}
+
+// c0 + pt: ct [B][2][l][N]; out gets (c0 + m, c1)
+__global__ __launch_bounds__(256) void k_add_plain(const uint64_t* __restrict__ ct, const uint64_t* __restrict__ pt,
+                                                   uint64_t* __restrict__ out, uint32_t l, uint64_t pt_bstride,
+                                                   const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y, pc = blockIdx.z;
+    const size_t o = ((size_t)pc * l + i) * kN + k;
+    uint64_t v = ct[o];
+    if ((pc & 1) == 0) v = add_mod(v, pt[(size_t)(pc >> 1) * pt_bstride + (size_t)i * kN + k], primes[i].q);
+    out[o] = v;
+}
+
+// out = sum of n inputs, each [n_polys][l][N]
+__global__ __launch_bounds__(256) void k_sum_list(ListPtrs in, uint32_t n, uint64_t* __restrict__ out, uint32_t l,
+                                                  const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y, pc = blockIdx.z;
+    const uint64_t q = primes[i].q;
+    const size_t o = ((size_t)pc * l + i) * kN + k;
+    uint64_t acc = 0;
+    for (uint32_t j = 0; j < n; j++) acc = add_mod(acc, in.p[j][o], q);
+    out[o] = acc;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ launchers
@@ -302,6 +421,78 @@ hipError_t launch_add(const Context& ctx, const uint64_t* x, const uint64_t* y, 
                       uint32_t l, hipStream_t st) {
     const int pi = prof_begin(ctx, "add", (double)n_polys * l * 3 * kN * 8, st);
     hipLaunchKernelGGL(k_add, dim3(kN / 256, l, n_polys), dim3(256), 0, st, x, y, out, l, ctx.d_primes);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_ks_inner_list(const Context& ctx, const uint64_t* const* ext, const uint64_t* const* evk,
+                                uint64_t* acc, uint32_t n, uint32_t l, hipStream_t st) {
+    InnerArgs ia{};
+    ia.E = l + ctx.K;
+    ia.D = (l + ctx.alpha - 1) / ctx.alpha;
+    ia.T = ctx.L + ctx.K;
+    ia.B = n;
+    if (ia.D > (uint32_t)kMaxDigits || ia.E > kMaxPmap || n > (uint32_t)kMaxList) return hipErrorInvalidValue;
+    for (uint32_t t = 0; t < ia.E; t++) ia.prime_of[t] = (uint8_t)(t < l ? t : ctx.L + (t - l));
+    ListPtrs pe{}, pk{};
+    uint32_t distinct_ext = 0;
+    for (uint32_t c = 0; c < n; c++) {
+        pe.p[c] = ext[c];
+        pk.p[c] = evk[c];
+        distinct_ext += (c == 0 || ext[c] != ext[c - 1]) ? 1 : 0;
+    }
+    const double bytes = ((double)distinct_ext * ia.D * ia.E + (double)n * (2 * ia.D * ia.E + 2 * ia.E)) * kN * 8;
+    const int pi = prof_begin(ctx, "ks_inner_list", bytes, st);
+    hipLaunchKernelGGL(k_ks_inner_list, dim3(kN / 256, ia.E, n), dim3(256), 0, st, pe, pk, acc, ia, ctx.d_primes);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_automorph_list(const Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n, uint32_t l,
+                                 const uint32_t* g, hipStream_t st) {
+    if (n > (uint32_t)kMaxList) return hipErrorInvalidValue;
+    AutoList al{};
+    for (uint32_t c = 0; c < n; c++) al.g[c] = g[c];
+    const int pi = prof_begin(ctx, "automorph", (double)n * 2 * l * 2 * kN * 8, st);
+    hipLaunchKernelGGL(k_automorph_list, dim3(kN / 256, l, 2 * n), dim3(256), 0, st, in, out, l, al);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* baby, const uint64_t* diag, uint64_t* out, uint32_t nb,
+                           uint32_t n_diag, uint32_t ng, uint32_t l, hipStream_t st) {
+    if (nb == 0 || nb > (uint32_t)kMaxBaby) return hipErrorInvalidValue;
+    const double bytes = ((double)nb * 2 * l + (double)n_diag * l + (double)ng * 2 * l) * kN * 8;
+    const int pi = prof_begin(ctx, "bsgs_mac", bytes, st);
+    hipLaunchKernelGGL(k_bsgs_mac, dim3(kN / 256, l), dim3(256), 0, st, baby, diag, out, nb, n_diag, ng, l,
+                       ctx.d_primes);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_mul_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
+                            uint32_t l, uint64_t pt_bstride, hipStream_t st) {
+    const int pi = prof_begin(ctx, "mul_plain", ((double)B * 4 * l + (pt_bstride ? B : 1) * (double)l) * kN * 8, st);
+    hipLaunchKernelGGL(k_mul_plain, dim3(kN / 256, l, 2 * B), dim3(256), 0, st, ct, pt, out, l, pt_bstride,
+                       ctx.d_primes);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
+                            uint32_t l, uint64_t pt_bstride, hipStream_t st) {
+    hipLaunchKernelGGL(k_add_plain, dim3(kN / 256, l, 2 * B), dim3(256), 0, st, ct, pt, out, l, pt_bstride,
+                       ctx.d_primes);
+    return hipGetLastError();
+}
+
+hipError_t launch_sum_list(const Context& ctx, const uint64_t* const* in, uint32_t n, uint64_t* out, uint32_t n_polys,
+                           uint32_t l, hipStream_t st) {
+    if (n == 0 || n > (uint32_t)kMaxList) return hipErrorInvalidValue;
+    ListPtrs lp{};
+    for (uint32_t j = 0; j < n; j++) lp.p[j] = in[j];
+    const int pi = prof_begin(ctx, "sum_list", (double)(n + 1) * n_polys * l * kN * 8, st);
+    hipLaunchKernelGGL(k_sum_list, dim3(kN / 256, l, n_polys), dim3(256), 0, st, lp, n, out, l, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }

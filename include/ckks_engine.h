@@ -128,6 +128,29 @@ int ckks_automorphism(ckks_context* ctx, const uint64_t* d_in, uint32_t n_polys,
 int ckks_eval_rotate(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level, int64_t step,
                      const uint64_t* d_evk, uint64_t* d_out, void* stream);
 
+/* ---- plaintext operators, hoisted rotations, BSGS linear transform -----------------------------
+ * ckks_eval_mult_plain   EvalMult(ct, pt): both polys (.) pt; pt [l][N] shared by the batch (pt_shared = 1)
+ *                        or [B][l][N]; no rescale (gpu_real_model.cu:3316-3334 multiplies then rescales once)
+ * ckks_eval_add_plain    EvalAdd(ct, pt): c0 + pt
+ * ckks_eval_rotate_hoisted  EvalFastRotation: one ciphertext rotated by steps[0..n) (n <= 64) with one shared
+ *                        ModUp of c1; key i = the automorphism key of rotation steps[i]; out [n][2][l][N]
+ * ckks_eval_rotate_many  n ciphertexts [n][2][l][N], ciphertext i rotated by steps[i] with key i (n <= 64)
+ * ckks_linear_transform_bsgs  the reference's baby-step giant-step diagonal matvec (gpu_real_model.cu:2767-2823):
+ *                        out = Rescale( sum_g Rot_{g*bs}( sum_j diag[g*bs + j] (.) Rot_j(ct) ) ), diag [n_diag][l][N]
+ *                        encoded plaintexts already pre-rotated by -g*bs; baby keys for steps 1..bs-1, giant keys
+ *                        for steps bs, 2bs, ...; out [2][l-1][N] */
+int ckks_eval_mult_plain(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level, const uint64_t* d_pt,
+                         int pt_shared, uint64_t* d_out, void* stream);
+int ckks_eval_add_plain(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level, const uint64_t* d_pt,
+                        int pt_shared, uint64_t* d_out, void* stream);
+int ckks_eval_rotate_hoisted(ckks_context* ctx, const uint64_t* d_ct, uint32_t level, const int64_t* steps,
+                             uint32_t n, const uint64_t* const* d_evks, uint64_t* d_out, void* stream);
+int ckks_eval_rotate_many(ckks_context* ctx, const uint64_t* d_cts, uint32_t n, uint32_t level, const int64_t* steps,
+                          const uint64_t* const* d_evks, uint64_t* d_out, void* stream);
+int ckks_linear_transform_bsgs(ckks_context* ctx, const uint64_t* d_ct, uint32_t level, const uint64_t* d_diags,
+                               uint32_t n_diag, uint32_t baby_steps, const uint64_t* const* d_baby_evks,
+                               const uint64_t* const* d_giant_evks, uint64_t* d_out, void* stream);
+
 /* ---- client side: keys, encoding, encryption (CryptoContext KeyGen / EvalMultKeyGen /
  * EvalRotateKeyGen / MakeCKKSPackedPlaintext / Encrypt / Decrypt, gpu_real_model.cu:1293-1336,1577-1589,
  * 2202-2221).  Not on the evaluation hot path; used to make seeded inputs and read results.
