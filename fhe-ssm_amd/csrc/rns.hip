@@ -256,35 +256,38 @@ __global__ __launch_bounds__(256) void k_automorph_list(const uint64_t* __restri
 }
 
 // BSGS multiply-accumulate: babies [nb][2][l][N], diagonals [n_diag][l][N] (diagonal g*nb + j pairs with
-// baby j), out [ng][2][l][N]: out_g = sum_j baby_j (.) diag_{g*nb+j}.  Each thread keeps its word of every
-// baby in registers and streams the diagonals once.
+// baby j), out [ng][2][l][N]: out_g = sum_j baby_j (.) diag_{g*nb+j}.
+// A workgroup owns 64 coefficients of one limb: it stages those words of every baby in LDS once, then its
+// 4 wave-rows take the giant steps g = row, row + 4, ...; every diagonal word is read exactly once and each
+// wave reads 64 consecutive words (512 B) per diagonal.
 constexpr int kMaxBaby = 32;
+constexpr int kMacCoef = 64;
+constexpr int kMacRows = 4;
 
-__global__ __launch_bounds__(256) void k_bsgs_mac(const uint64_t* __restrict__ baby, const uint64_t* __restrict__ diag,
-                                                  uint64_t* __restrict__ out, uint32_t nb, uint32_t n_diag, uint32_t ng,
-                                                  uint32_t l, const PrimeInfo* __restrict__ primes) {
-    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+__global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(const uint64_t* __restrict__ baby,
+                                                                  const uint64_t* __restrict__ diag,
+                                                                  uint64_t* __restrict__ out, uint32_t nb,
+                                                                  uint32_t n_diag, uint32_t ng, uint32_t l,
+                                                                  const PrimeInfo* __restrict__ primes) {
+    __shared__ uint64_t sb[kMaxBaby * 2 * kMacCoef];
+    const uint32_t kk = threadIdx.x & (kMacCoef - 1), row = threadIdx.x / kMacCoef;
+    const uint32_t k = blockIdx.x * kMacCoef + kk;
     const uint32_t i = blockIdx.y;
     const Barrett br = barrett_of(primes[i]);
     const size_t P = (size_t)l * kN, off = (size_t)i * kN + k;
-    uint64_t b0[kMaxBaby], b1[kMaxBaby];
-#pragma unroll
-    for (int j = 0; j < kMaxBaby; j++) {
-        if (j < (int)nb) {
-            b0[j] = baby[(size_t)j * 2 * P + off];
-            b1[j] = baby[(size_t)j * 2 * P + P + off];
-        }
+    for (uint32_t jp = row; jp < 2 * nb; jp += kMacRows) {  // jp = 2 j + poly
+        const uint32_t j = jp >> 1, p = jp & 1;
+        sb[jp * kMacCoef + kk] = baby[(size_t)j * 2 * P + p * P + off];
     }
-    for (uint32_t g = 0; g < ng; g++) {
+    __syncthreads();
+    for (uint32_t g = row; g < ng; g += kMacRows) {
         U128 s0{0, 0}, s1{0, 0};
-#pragma unroll
-        for (int j = 0; j < kMaxBaby; j++) {
-            const uint32_t di = g * nb + j;
-            if (j < (int)nb && di < n_diag) {
-                const uint64_t m = diag[(size_t)di * P + off];
-                mac128(s0, b0[j], m);
-                mac128(s1, b1[j], m);
-            }
+        const uint32_t jn = min(nb, n_diag - g * nb);
+        const uint64_t* dg = diag + (size_t)g * nb * P + off;
+        for (uint32_t j = 0; j < jn; j++) {
+            const uint64_t m = dg[(size_t)j * P];
+            mac128(s0, sb[(2 * j) * kMacCoef + kk], m);
+            mac128(s1, sb[(2 * j + 1) * kMacCoef + kk], m);
         }
         out[(size_t)g * 2 * P + off] = reduce_u128(s0, br);
         out[(size_t)g * 2 * P + P + off] = reduce_u128(s1, br);
@@ -464,8 +467,8 @@ hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* baby, const uint6
     if (nb == 0 || nb > (uint32_t)kMaxBaby) return hipErrorInvalidValue;
     const double bytes = ((double)nb * 2 * l + (double)n_diag * l + (double)ng * 2 * l) * kN * 8;
     const int pi = prof_begin(ctx, "bsgs_mac", bytes, st);
-    hipLaunchKernelGGL(k_bsgs_mac, dim3(kN / 256, l), dim3(256), 0, st, baby, diag, out, nb, n_diag, ng, l,
-                       ctx.d_primes);
+    hipLaunchKernelGGL(k_bsgs_mac, dim3(kN / kMacCoef, l), dim3(kMacCoef * kMacRows), 0, st, baby, diag, out, nb,
+                       n_diag, ng, l, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
