@@ -8,7 +8,8 @@ Workloads (inputs seeded and resident in HBM before the t
          EvalMult+Rescale over the 64 pairs.  value = HMult+relin ops/s.
   ntt    config 1: forward then inverse NTT over 64 ct x 2 polys x 24 limbs.  value = algorithmic GB/s.
   pcmm   config 3: 768x768 plaintext matrix x one ciphertext (L=16) by BSGS 28 x 28.  value = ms.
-The default run also reports the config-1 and config-3 figures beside the config-2 metric.
+  bootstrap  config 4: full-slot bootstrap of a level-1 ciphertext.  value = ms; precision in bits.
+The default run also reports the config-1, -3 and -4 figures beside the config-2 metric.
 
 Roofline: the engine records HIP events on its launch stream around every kernel of one profiled
 step (ckks_profile_*); the dominant kernel by time is reported with achieved = algorithmic bytes per
@@ -225,6 +226,62 @@ def bench_pcmm(ckks, torch, steps_n, warmup, seed):
                         "period-768 replicated layout"}
 
 
+# ----------------------------------------------------------------------------------------- config 4
+def bootstrap_context(ckks):
+    """q0 60-bit, 22 x 50-bit, 3 x 60-bit CoeffToSlot primes on top; 8 x 60-bit special primes; dnum 3."""
+    big = ckks.gen_primes(60, 12)
+    qs = ckks.gen_primes(50, 22)
+    return ckks.Context(num_q=26, num_p=8, dnum=3, scale=2.0**50, moduli=big[:1] + qs + big[1:4] + big[4:])
+
+
+def bench_bootstrap(ckks, torch, steps_n, warmup, seed):
+    ctx = bootstrap_context(ckks)
+    L, K, D = ctx.L, ctx.K, ctx.dnum
+    bt = ckks.Bootstrap(ctx, K=22.0, cheb_degree=59, double_angles=2, top_scale=2.0**50, in_scale=2.0**50)
+    sk = ctx.secret(seed_bytes("boot-secret", seed), 192)
+    dev = torch.device("cuda:0")
+    kb = D * 2 * (L + K) * N * 8
+    nk = len(bt.steps) + 2
+    keys = torch.empty((nk, kb // 8), dtype=torch.int64, device=dev)
+    kp = [keys.data_ptr() + i * kb for i in range(nk)]
+    ctx.keygen_relin(sk, seed_bytes("boot-ra", seed), seed_bytes("boot-re", seed), kp[0])
+    ctx.keygen_automorphism(sk, 2 * N - 1, seed_bytes("boot-ca", seed), seed_bytes("boot-ce", seed), kp[1])
+    rot = {}
+    for i, s_ in enumerate(bt.steps):
+        ctx.keygen_automorphism(sk, ckks.rotation_index(s_), seed_bytes(f"bk{i}a", seed), seed_bytes(f"bk{i}e", seed),
+                                kp[2 + i])
+        rot[s_] = kp[2 + i]
+    rng = np.random.default_rng(seed)
+    z = rng.uniform(-1.0, 1.0, N // 2)
+    pt = torch.empty((1, N), dtype=torch.int64, device=dev)
+    ct = torch.empty((2, 1, N), dtype=torch.int64, device=dev)
+    out = torch.empty((2, bt.out_level, N), dtype=torch.int64, device=dev)
+    ctx.encode(z, 1, 2.0**50, pt.data_ptr())
+    ctx.encrypt(sk, pt.data_ptr(), 1, seed_bytes("boot-enc", seed), 0, ct.data_ptr())
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    sh = ctypes.c_void_p(stream.cuda_stream)
+
+    def step():
+        bt.run(ct.data_ptr(), kp[0], kp[1], rot, out.data_ptr(), sh)
+
+    wall, per = timed_steps(torch, stream, step, steps_n, warmup)
+    got = ctx.decrypt(sk, out.data_ptr(), bt.out_level, bt.scale(bt.out_level), N // 2, complex_out=True)
+    bits = float(-np.log2(np.max(np.abs(got - z))))
+    ctx.profile_reset()
+    ctx.profile(True)
+    step()
+    torch.cuda.synchronize()
+    ctx.profile(False)
+    rep = ctx.profile_report()
+    ctx.profile_reset()
+    return {"ms_per_bootstrap": round(wall * 1e3 / steps_n, 3), "precision_bits": round(bits, 2),
+            "levels_in_out": [1, bt.out_level], "rotation_keys": len(bt.steps),
+            "kernels": kernel_table(rep), "roofline": roofline_from_profile(rep),
+            "workload": "config4: full-slot bootstrap N=2^16, 32768 slots, CtS 3 levels, EvalMod Chebyshev 59 + 2 "
+                        "double-angle (K=22), StC 3 levels; chain q0 60 + 22x50 + 3x60 bits, P 8x60, dnum 3"}
+
+
 # ----------------------------------------------------------------------------------------- config 1
 def ntt_bytes():
     limbs = 2 * N_PAIRS * L2
@@ -301,11 +358,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="hmult", choices=["hmult", "ntt", "pcmm"])
+    ap.add_argument("--workload", default="hmult", choices=["hmult", "ntt", "pcmm", "bootstrap"])
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ntt-line", action="store_true", help="skip the config-1 NTT figure in the hmult run")
     ap.add_argument("--no-pcmm-line", action="store_true", help="skip the config-3 PCMM figure in the hmult run")
+    ap.add_argument("--no-boot-line", action="store_true", help="skip the config-4 bootstrap figure in the hmult run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design note, "
@@ -327,7 +385,18 @@ def main():
             p = bench_pcmm(ckks, torch, max(3, args.steps // 2), 1, args.seed)
             extra["pcmm_config3"] = {k: p[k] for k in ("ms_per_pcmm", "relErrRms_vs_fp64", "algorithmic_GBps",
                                                         "roofline")}
+        if not args.no_boot_line:
+            b = bench_bootstrap(ckks, torch, max(2, args.steps // 4), 1, args.seed)
+            extra["bootstrap_config4"] = {k: b[k] for k in ("ms_per_bootstrap", "precision_bits", "levels_in_out",
+                                                             "roofline")}
         cpu = None if args.no_cpu_baseline else cpu_baseline_hmult(args.seed)
+    elif args.workload == "bootstrap":
+        b = bench_bootstrap(ckks, torch, args.steps, args.warmup, args.seed)
+        res = {"metric": "bootstrap ms (full-slot, N=2^16)", "value": b["ms_per_bootstrap"], "unit": "ms",
+               "ms_per_step": b["ms_per_bootstrap"], "dtype": "u64", "config": {"workload": b["workload"]},
+               "kernels": b["kernels"], "roofline": b["roofline"],
+               "check": {"precision_bits": b["precision_bits"], "levels_in_out": b["levels_in_out"]}}
+        extra, cpu = {}, None
     elif args.workload == "pcmm":
         p = bench_pcmm(ckks, torch, args.steps, args.warmup, args.seed)
         res = {"metric": "PCMM ms (768x768 BSGS, N=2^16, L=16)", "value": p["ms_per_pcmm"], "unit": "ms",

@@ -61,6 +61,16 @@ SIGNATURES = {
     "ckks_eval_rotate_hoisted": (_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp]),
     "ckks_eval_rotate_many": (_int, [_vp, _vp, _u32, _u32, _vp, _vp, _vp, _vp]),
     "ckks_linear_transform_bsgs": (_int, [_vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _vp]),
+    "ckks_gen_primes": (_int, [_u32, _u32, _vp, _u32, _vp]),
+    "ckks_bootstrap_setup": (_int, [_vp, ctypes.c_double, _u32, _u32, ctypes.c_double, ctypes.c_double,
+                                    ctypes.POINTER(_vp)]),
+    "ckks_bootstrap_destroy": (None, [_vp]),
+    "ckks_bootstrap_steps": (_int, [_vp, _vp, _u32, ctypes.POINTER(_u32)]),
+    "ckks_bootstrap_out_level": (_u32, [_vp]),
+    "ckks_bootstrap_scale": (ctypes.c_double, [_vp, _u32]),
+    "ckks_eval_bootstrap": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _vp, _vp]),
+    "ckks_eval_bootstrap_stage": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _vp, ctypes.POINTER(_u32)]),
+    "ckks_decrypt_coeffs": (_int, [_vp, _vp, _vp, _u32, _vp]),
     "ckks_secret_generate": (_int, [_vp, _vp, _u32, ctypes.POINTER(_vp)]),
     "ckks_secret_destroy": (None, [_vp]),
     "ckks_secret_coeffs": (_int, [_vp, _vp, _u32]),
@@ -282,6 +292,11 @@ class Context:
         check(load().ckks_decrypt_decode(self.h, sk.h, d_ct, level, scale, _ptr(re), _ptr(im), n_slots))
         return re + 1j * im if complex_out else re
 
+    def decrypt_coeffs(self, sk, d_ct, level: int) -> np.ndarray:
+        out = np.zeros(self.N, dtype=np.float64)
+        check(load().ckks_decrypt_coeffs(self.h, sk.h, d_ct, level, _ptr(out)))
+        return out
+
     # profiling ---------------------------------------------------------------------------------
     def profile(self, on: bool) -> None:
         check(load().ckks_profile_enable(self.h, 1 if on else 0))
@@ -344,3 +359,54 @@ class Secret:
 
 def rotation_index(step: int) -> int:
     return int(load().ckks_rotation_index(step))
+
+
+def gen_primes(bits: int, count: int, skip=()) -> list:
+    sk = np.ascontiguousarray(np.asarray(list(skip) or [0], dtype=np.uint64))
+    out = np.zeros(count, dtype=np.uint64)
+    check(load().ckks_gen_primes(bits, count, _ptr(sk), len(skip), _ptr(out)))
+    return [int(x) for x in out]
+
+
+class Bootstrap:
+    """EvalBootstrapSetup: plan (CtS/StC diagonals, Chebyshev coefficients) resident on the device."""
+
+    def __init__(self, ctx: Context, K: float = 22.0, cheb_degree: int = 59, double_angles: int = 2,
+                 top_scale: float = 2.0**50, in_scale: float = 2.0**50):
+        h = _vp()
+        check(load().ckks_bootstrap_setup(ctx.h, K, cheb_degree, double_angles, top_scale, in_scale,
+                                          ctypes.byref(h)))
+        self.h = h.value
+        self.ctx = ctx
+        n = _u32()
+        check(load().ckks_bootstrap_steps(self.h, None, 0, ctypes.byref(n)))
+        st = np.zeros(max(1, n.value), dtype=np.int64)
+        check(load().ckks_bootstrap_steps(self.h, _ptr(st), len(st), ctypes.byref(n)))
+        self.steps = [int(x) for x in st[:n.value]]
+        self.out_level = int(load().ckks_bootstrap_out_level(self.h))
+
+    def scale(self, level: int) -> float:
+        return float(load().ckks_bootstrap_scale(self.h, level))
+
+    def run(self, d_ct_in, d_relin, d_conj, keys: dict, d_out, stream=None):
+        steps = np.ascontiguousarray(np.asarray(list(keys.keys()), dtype=np.int64))
+        check(load().ckks_eval_bootstrap(self.ctx.h, self.h, d_ct_in, d_relin, d_conj, _ptr(steps), _ptr_array(
+            list(keys.values())), len(steps), d_out, stream))
+
+    def run_stage(self, d_ct_in, d_relin, d_conj, keys: dict, stage: int, d_out) -> int:
+        steps = np.ascontiguousarray(np.asarray(list(keys.keys()), dtype=np.int64))
+        lvl = _u32()
+        check(load().ckks_eval_bootstrap_stage(self.ctx.h, self.h, d_ct_in, d_relin, d_conj, _ptr(steps), _ptr_array(
+            list(keys.values())), len(steps), stage, d_out, ctypes.byref(lvl)))
+        return lvl.value
+
+    def close(self):
+        if self.h:
+            load().ckks_bootstrap_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -8,6 +8,7 @@
 
 #include <map>
 
+#include "bootstrap.hpp"
 #include "ckks_engine.h"
 #include "client.hpp"
 #include "engine.hpp"
@@ -22,6 +23,11 @@ void context_release(Context& c);
 
 struct ckks_context {
     fhe::Context c;
+};
+
+struct ckks_bootstrap {
+    fhe::BootPlan* p;
+    const ckks_context* owner;
 };
 
 struct ckks_secret {
@@ -478,6 +484,96 @@ int ckks_decrypt_decode(ckks_context* ctx, const ckks_secret* sk, const uint64_t
     if (!d_ct || (!re && !im)) return fail(CKKS_EINVAL, "null argument");
     return guarded([&] {
         fhe::decrypt_decode(ctx->c, *sk->s, d_ct, level, scale, re, im, n_slots);
+        return CKKS_OK;
+    });
+}
+
+int ckks_gen_primes(uint32_t bits, uint32_t count, const uint64_t* skip, uint32_t n_skip, uint64_t* out) {
+    if (!out || (n_skip && !skip)) return fail(CKKS_EINVAL, "null argument");
+    if (bits < 20 || bits > 60) return fail(CKKS_EINVAL, "bits must be in [20, 60]");
+    return guarded([&] {
+        auto v = fhe::ntt_primes(bits, count, 2ull * fhe::kN, std::vector<uint64_t>(skip, skip + n_skip));
+        std::memcpy(out, v.data(), v.size() * 8);
+        return CKKS_OK;
+    });
+}
+
+int ckks_bootstrap_setup(ckks_context* ctx, double K, uint32_t cheb_degree, uint32_t double_angles, double top_scale,
+                         double in_scale, ckks_bootstrap** out) {
+    if (!ctx || !out) return fail(CKKS_EINVAL, "null argument");
+    if (!(K >= 1) || !(top_scale > 0) || !(in_scale > 0) || double_angles > 6)
+        return fail(CKKS_EINVAL, "bad bootstrap parameters");
+    return guarded([&] {
+        auto* bt = new ckks_bootstrap{nullptr, ctx};
+        try {
+            bt->p = fhe::bootstrap_plan(ctx->c, K, (int)cheb_degree, (int)double_angles, top_scale, in_scale);
+        } catch (...) {
+            delete bt;
+            throw;
+        }
+        *out = bt;
+        return CKKS_OK;
+    });
+}
+
+void ckks_bootstrap_destroy(ckks_bootstrap* bt) {
+    if (!bt) return;
+    fhe::bootstrap_plan_destroy(bt->p);
+    delete bt;
+}
+
+int ckks_bootstrap_steps(const ckks_bootstrap* bt, int64_t* steps, uint32_t cap, uint32_t* n) {
+    if (!bt || !n) return fail(CKKS_EINVAL, "null argument");
+    *n = (uint32_t)bt->p->steps.size();
+    if (steps) {
+        if (cap < *n) return fail(CKKS_EINVAL, "buffer too small");
+        std::memcpy(steps, bt->p->steps.data(), *n * 8);
+    }
+    return CKKS_OK;
+}
+
+uint32_t ckks_bootstrap_out_level(const ckks_bootstrap* bt) { return bt ? bt->p->l_out : 0; }
+
+double ckks_bootstrap_scale(const ckks_bootstrap* bt, uint32_t level) {
+    if (!bt || level == 0 || level >= bt->p->S.size()) return 0.0;
+    return (double)bt->p->S[level];
+}
+
+int ckks_eval_bootstrap(ckks_context* ctx, const ckks_bootstrap* bt, const uint64_t* d_ct_in, const uint64_t* d_relin,
+                        const uint64_t* d_conj, const int64_t* steps, const uint64_t* const* d_evks, uint32_t n_keys,
+                        uint64_t* d_out, void* stream) {
+    if (!ctx || !bt || bt->owner != ctx) return fail(CKKS_EINVAL, "null context or plan of another context");
+    if (!d_ct_in || !d_relin || !d_conj || !d_out || (n_keys && (!steps || !d_evks)))
+        return fail(CKKS_EINVAL, "null argument");
+    for (uint32_t i = 0; i < n_keys; i++)
+        if (!d_evks[i]) return fail(CKKS_EINVAL, "null key");
+    return guarded([&] {
+        fhe::bootstrap(ctx->c, *bt->p, d_ct_in, d_relin, d_conj, steps, d_evks, n_keys, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_bootstrap_stage(ckks_context* ctx, const ckks_bootstrap* bt, const uint64_t* d_ct_in,
+                              const uint64_t* d_relin, const uint64_t* d_conj, const int64_t* steps,
+                              const uint64_t* const* d_evks, uint32_t n_keys, uint32_t stage, uint64_t* d_out,
+                              uint32_t* level) {
+    if (!ctx || !bt || bt->owner != ctx || !level) return fail(CKKS_EINVAL, "bad argument");
+    if (!d_ct_in || !d_relin || !d_conj || !d_out || (n_keys && (!steps || !d_evks)))
+        return fail(CKKS_EINVAL, "null argument");
+    if (stage < 1 || stage > 6) return fail(CKKS_EINVAL, "stage must be in [1, 6]");
+    return guarded([&] {
+        *level = fhe::bootstrap(ctx->c, *bt->p, d_ct_in, d_relin, d_conj, steps, d_evks, n_keys, d_out, nullptr,
+                                stage);
+        return CKKS_OK;
+    });
+}
+
+int ckks_decrypt_coeffs(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_ct, uint32_t level, double* out) {
+    if (int rc = check_secret(ctx, sk)) return rc;
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_ct || !out) return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        fhe::decrypt_coeffs(ctx->c, *sk->s, d_ct, level, out);
         return CKKS_OK;
     });
 }

@@ -1,0 +1,35 @@
+// bootstrap.hpp -- CKKS bootstrapping plan and evaluation (see bootstrap.cpp).
+#pragma once
+#include <stdint.h>
+
+#include <vector>
+
+#include "engine.hpp"
+
+namespace fhe {
+
+// one BSGS level of CoeffToSlot or SlotToCoeff: applied at l limbs, then rescaled
+struct BootLevel {
+    uint32_t l = 0, nb = 0, ng = 0;
+    std::vector<int64_t> bsteps, gsteps;
+    uint64_t* d_diags = nullptr;  // [ng * nb][l][N], term (g, b) pre-rotated by -gsteps[g]
+};
+
+struct BootPlan {
+    double K = 0;
+    int deg = 0, r = 0;
+    double in_scale = 0;
+    std::vector<long double> S;  // S[l]: scale of a ciphertext with l limbs
+    std::vector<double> cheb;
+    std::vector<BootLevel> cts, stc;
+    std::vector<int64_t> steps;  // rotation steps whose keys evaluation needs (plus the conjugation key)
+    uint32_t l_out = 0;
+};
+
+BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scale, double in_scale);
+void bootstrap_plan_destroy(BootPlan* P);
+uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, const uint64_t* relin,
+                   const uint64_t* conj_evk, const int64_t* steps, const uint64_t* const* evks, uint32_t n_keys,
+                   uint64_t* out, hipStream_t st, uint32_t stop_stage = 0);
+
+}  // namespace fhe

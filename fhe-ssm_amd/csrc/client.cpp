@@ -313,6 +313,34 @@ void encrypt(Context& ctx, const Secret& sk, const uint64_t* d_pt, uint32_t l, c
     HIPC(hipDeviceSynchronize());
 }
 
+// decrypt (c0 + c1 s) to centered coefficients (CRT of the first two limbs, |m| < q0 q1 / 2), as doubles
+void decrypt_coeffs(Context& ctx, const Secret& sk, const uint64_t* d_ct, uint32_t l, double* out) {
+    DevBuf dm((size_t)l * kN * 8);
+    HIPC(launch_decrypt(ctx, d_ct, sk.d_eval, dm.as<uint64_t>(), l, nullptr));
+    const uint32_t nl = l >= 2 ? 2 : 1;
+    JobSpec js{};
+    js.n_polys = 1;
+    js.period = nl;
+    for (uint32_t i = 0; i < nl; i++) js.pmap[i] = (uint8_t)i;
+    HIPC(launch_ntt(ctx, dm.as<uint64_t>(), js, nl, true, ctx.ntt_mode, nullptr));
+    std::vector<uint64_t> limbs((size_t)nl * kN);
+    HIPC(hipMemcpy(limbs.data(), dm.p, limbs.size() * 8, hipMemcpyDeviceToHost));
+    const uint64_t q0 = ctx.moduli[0];
+    for (uint32_t k = 0; k < kN; k++) {
+        if (nl == 1) {
+            const uint64_t x = limbs[k];
+            out[k] = x > q0 / 2 ? -(double)(q0 - x) : (double)x;
+        } else {
+            const uint64_t q1 = ctx.moduli[1];
+            const uint64_t x0 = limbs[k], x1 = limbs[kN + k];
+            const uint64_t d = mulmod_h((x1 + q1 - x0 % q1) % q1, invmod_h(q0 % q1, q1), q1);
+            const unsigned __int128 Q = (unsigned __int128)q0 * q1;
+            const unsigned __int128 x = (unsigned __int128)d * q0 + x0;
+            out[k] = x > Q / 2 ? -(double)(Q - x) : (double)x;
+        }
+    }
+}
+
 // decrypt (c0 + c1 s), to coefficients, CRT of the first two limbs (|m| < q0 q1 / 2), decode
 void decrypt_decode(Context& ctx, const Secret& sk, const uint64_t* d_ct, uint32_t l, double scale, double* re,
                     double* im, uint32_t n_slots) {

@@ -26,6 +26,7 @@ void encode(Context& ctx, const double* re, const double* im, uint32_t n_slots, 
             uint64_t* d_pt);
 void encrypt(Context& ctx, const Secret& sk, const uint64_t* d_pt, uint32_t l, const uint8_t seed[32], uint32_t index,
              uint64_t* d_ct);
+void decrypt_coeffs(Context& ctx, const Secret& sk, const uint64_t* d_ct, uint32_t l, double* out);
 void decrypt_decode(Context& ctx, const Secret& sk, const uint64_t* d_ct, uint32_t l, double scale, double* re,
                     double* im, uint32_t n_slots);
 

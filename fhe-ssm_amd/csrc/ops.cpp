@@ -346,6 +346,14 @@ uint32_t rotation_index(int64_t k) {
 // n ciphertexts [n][2][l][N], each rotated by its own step with its own key -> out [n][2][l][N]
 void rotate_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l, const int64_t* steps,
                  const uint64_t* const* evk, uint64_t* out, hipStream_t st) {
+    std::vector<uint32_t> g(n);
+    for (uint32_t c = 0; c < n; c++) g[c] = rotation_index(steps[c]);
+    automorph_ks_list(ctx, cts, n, l, g.data(), evk, out, st);
+}
+
+// n ciphertexts, ciphertext c mapped by X -> X^g[c] with the key of g[c] (KS of c1, add c0, permute)
+void automorph_ks_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l, const uint32_t* gidx,
+                       const uint64_t* const* evk, uint64_t* out, hipStream_t st) {
     check_level(ctx, l);
     if (n == 0) return;
     if (n > 64) throw std::invalid_argument("at most 64 rotations per call");
@@ -358,14 +366,13 @@ void rotate_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l, cons
                           hipMemcpyDeviceToDevice, st));
     modup(ctx, c1, ext, n, l, st);
     std::vector<const uint64_t*> ep(n);
-    std::vector<uint32_t> g(n);
     for (uint32_t c = 0; c < n; c++) {
         ep[c] = ext + (size_t)c * D * E * W;
-        g[c] = rotation_index(steps[c]);
+        if ((gidx[c] & 1) == 0 || gidx[c] >= 2 * kN) throw std::invalid_argument("automorphism index must be odd < 2N");
     }
     HIPX(launch_ks_inner_list(ctx, ep.data(), evk, acc, n, l, st));
     moddown_inplace(ctx, acc, 2 * n, l, cts, ks, st, 2);
-    HIPX(launch_automorph_list(ctx, ks, out, n, l, g.data(), st));
+    HIPX(launch_automorph_list(ctx, ks, out, n, l, gidx, st));
 }
 
 // one ciphertext [2][l][N] rotated by n steps with one shared ModUp -> out [n][2][l][N]
@@ -432,6 +439,61 @@ void bsgs_matvec(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* d
     }
     HIPX(launch_sum_list(ctx, terms.data(), (uint32_t)terms.size(), sum, 2, l, st));
     rescale(ctx, sum, 2, l, out, st);
+}
+
+// General BSGS linear transform on one ciphertext [2][l][N]:
+//   y = sum_g Rot_{G[g]}( sum_b diag[g*nb + b] (.) Rot_{Bs[b]}(x) )   (no rescale; out [2][l][N])
+// A step of 0 is the identity (no key).  Baby rotations share one ModUp; giant rotations run as one batch.
+void bsgs_general(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* diags, uint32_t nb,
+                  const int64_t* bsteps, const uint64_t* const* bevk, uint32_t ng, const int64_t* gsteps,
+                  const uint64_t* const* gevk, uint64_t* out, hipStream_t st) {
+    check_level(ctx, l);
+    if (nb == 0 || nb > 32 || ng == 0 || ng > 64) throw std::invalid_argument("bad BSGS shape");
+    const size_t ctw = (size_t)2 * l * W;
+    uint64_t* baby = (uint64_t*)ws_get(ctx, WS_BABY, (size_t)nb * ctw * 8);
+    uint64_t* v = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)ng * ctw * 8);
+    uint64_t* vr = (uint64_t*)ws_get(ctx, WS_GROT, (size_t)ng * ctw * 8);
+    std::vector<int64_t> rs;
+    std::vector<const uint64_t*> rk;
+    std::vector<uint32_t> rpos;
+    for (uint32_t b = 0; b < nb; b++) {
+        if (bsteps[b] == 0) {
+            HIPX(hipMemcpyAsync(baby + b * ctw, ct, ctw * 8, hipMemcpyDeviceToDevice, st));
+        } else {
+            rs.push_back(bsteps[b]);
+            rk.push_back(bevk[b]);
+            rpos.push_back(b);
+        }
+    }
+    if (!rs.empty()) {
+        uint64_t* tmp = (uint64_t*)ws_get(ctx, WS_SUM, rs.size() * ctw * 8);
+        rotate_hoisted(ctx, ct, l, rs.data(), (uint32_t)rs.size(), rk.data(), tmp, st);
+        for (size_t r = 0; r < rs.size(); r++)
+            HIPX(hipMemcpyAsync(baby + rpos[r] * ctw, tmp + r * ctw, ctw * 8, hipMemcpyDeviceToDevice, st));
+    }
+    HIPX(launch_bsgs_mac(ctx, baby, diags, v, nb, nb * ng, ng, l, st));
+    std::vector<const uint64_t*> terms;
+    std::vector<int64_t> gs;
+    std::vector<const uint64_t*> gk;
+    std::vector<uint32_t> gpos;
+    for (uint32_t g = 0; g < ng; g++) {
+        if (gsteps[g] == 0) {
+            terms.push_back(v + g * ctw);
+        } else {
+            gs.push_back(gsteps[g]);
+            gk.push_back(gevk[g]);
+            gpos.push_back(g);
+        }
+    }
+    if (!gs.empty()) {
+        // the giants to rotate must be contiguous: pack them
+        uint64_t* packed = (uint64_t*)ws_get(ctx, WS_SUM, gs.size() * ctw * 8);
+        for (size_t r = 0; r < gs.size(); r++)
+            HIPX(hipMemcpyAsync(packed + r * ctw, v + gpos[r] * ctw, ctw * 8, hipMemcpyDeviceToDevice, st));
+        rotate_list(ctx, packed, (uint32_t)gs.size(), l, gs.data(), gk.data(), vr, st);
+        for (size_t r = 0; r < gs.size(); r++) terms.push_back(vr + r * ctw);
+    }
+    HIPX(launch_sum_list(ctx, terms.data(), (uint32_t)terms.size(), out, 2, l, st));
 }
 
 void add(Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys, uint32_t l,

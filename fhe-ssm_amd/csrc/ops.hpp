@@ -45,6 +45,11 @@ void add(Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint
 uint32_t rotation_index(int64_t k);
 void rotate_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l, const int64_t* steps,
                  const uint64_t* const* evk, uint64_t* out, hipStream_t st);
+void automorph_ks_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l, const uint32_t* gidx,
+                       const uint64_t* const* evk, uint64_t* out, hipStream_t st);
+void bsgs_general(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* diags, uint32_t nb,
+                  const int64_t* bsteps, const uint64_t* const* bevk, uint32_t ng, const int64_t* gsteps,
+                  const uint64_t* const* gevk, uint64_t* out, hipStream_t st);
 void rotate_hoisted(Context& ctx, const uint64_t* ct, uint32_t l, const int64_t* steps, uint32_t n,
                     const uint64_t* const* evk, uint64_t* out, hipStream_t st);
 void mul_plain(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const uint64_t* pt, bool pt_shared,

@@ -330,6 +330,53 @@ __global__ __launch_bounds__(256) void k_sum_list(ListPtrs in, uint32_t n, uint6
     out[o] = acc;
 }
 
+// Integer linear combination over ciphertext batches:
+//   out[c][p][i] = sum_t C[t][i] * x_t[c][p][i]  (+ add[i] on poly 0)   mod q_i,   i < l_out
+// Term t reads ciphertext c at x_t + c * 2 * stride_t * N (stride_t = the term's own limb count, so a term
+// at a higher level is read without copying; only its first l_out limbs are used).
+constexpr int kMaxTerms = 8;
+constexpr int kMaxLcLimbs = 40;
+
+struct LinArgs {
+    const uint64_t* x[kMaxTerms];
+    uint32_t stride[kMaxTerms];
+    uint32_t n_terms, l_out, has_add;
+    uint64_t C[kMaxTerms][kMaxLcLimbs];
+    uint64_t add[kMaxLcLimbs];
+};
+
+__global__ __launch_bounds__(256) void k_lincomb(uint64_t* __restrict__ out, LinArgs la,
+                                                 const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y, pc = blockIdx.z;  // pc = 2 c + poly
+    const uint32_t c = pc >> 1, p = pc & 1;
+    const Barrett br = barrett_of(primes[i]);
+    U128 acc{0, 0};
+    for (uint32_t t = 0; t < la.n_terms; t++) {
+        const uint64_t v = la.x[t][((size_t)(2 * c + p) * la.stride[t] + i) * kN + k];
+        mac128(acc, v, la.C[t][i]);
+    }
+    uint64_t r = reduce_u128(acc, br);
+    if (la.has_add && p == 0) r = add_mod(r, la.add[i], br.q);
+    out[((size_t)pc * la.l_out + i) * kN + k] = r;
+}
+
+// multiply by X^(N/2) (slot-wise by +-i): evaluation slot k holds a(psi^(2 brev(k)+1)); X^(N/2) there is
+// psi^(N/2 (2 brev(k)+1)) = +iq for k < N/2 and -iq for k >= N/2 (iq = psi^(N/2) = forward-table entry 1).
+// sign = 1 multiplies by X^(N/2), sign = -1 by -X^(N/2).
+__global__ __launch_bounds__(256) void k_mul_i(const uint64_t* __restrict__ in, uint64_t* __restrict__ out, uint32_t l,
+                                               int sign, const TwPair* __restrict__ tw_all,
+                                               const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y, pc = blockIdx.z;
+    const uint64_t q = primes[i].q;
+    const TwPair w = tw_all[(size_t)i * kN + 1];
+    const size_t o = ((size_t)pc * l + i) * kN + k;
+    uint64_t v = shoup(in[o], w.w, w.wp, q);
+    const bool neg = (k >= kN / 2) != (sign < 0);
+    out[o] = (neg && v) ? q - v : v;
+}
+
 }  // namespace
 
 // ------------------------------------------------------------------ launchers
@@ -497,6 +544,34 @@ hipError_t launch_sum_list(const Context& ctx, const uint64_t* const* in, uint32
     const int pi = prof_begin(ctx, "sum_list", (double)(n + 1) * n_polys * l * kN * 8, st);
     hipLaunchKernelGGL(k_sum_list, dim3(kN / 256, l, n_polys), dim3(256), 0, st, lp, n, out, l, ctx.d_primes);
     prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_lincomb(const Context& ctx, uint64_t* out, uint32_t B, uint32_t l_out, uint32_t n_terms,
+                          const uint64_t* const* x, const uint32_t* stride, const uint64_t* C /*[n_terms][l_out]*/,
+                          const uint64_t* add /*[l_out] or null*/, hipStream_t st) {
+    if (n_terms == 0 || n_terms > (uint32_t)kMaxTerms || l_out > (uint32_t)kMaxLcLimbs) return hipErrorInvalidValue;
+    LinArgs la{};
+    la.n_terms = n_terms;
+    la.l_out = l_out;
+    la.has_add = add ? 1 : 0;
+    for (uint32_t t = 0; t < n_terms; t++) {
+        la.x[t] = x[t];
+        la.stride[t] = stride[t];
+        for (uint32_t i = 0; i < l_out; i++) la.C[t][i] = C[(size_t)t * l_out + i];
+    }
+    if (add)
+        for (uint32_t i = 0; i < l_out; i++) la.add[i] = add[i];
+    const int pi = prof_begin(ctx, "lincomb", (double)B * 2 * l_out * (n_terms + 1) * kN * 8, st);
+    hipLaunchKernelGGL(k_lincomb, dim3(kN / 256, l_out, 2 * B), dim3(256), 0, st, out, la, ctx.d_primes);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_mul_i(const Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n_polys, uint32_t l, int sign,
+                        hipStream_t st) {
+    hipLaunchKernelGGL(k_mul_i, dim3(kN / 256, l, n_polys), dim3(256), 0, st, in, out, l, sign, ctx.d_tw,
+                       ctx.d_primes);
     return hipGetLastError();
 }
 

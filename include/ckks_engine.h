@@ -151,6 +151,35 @@ int ckks_linear_transform_bsgs(ckks_context* ctx, const uint64_t* d_ct, uint32_t
                                uint32_t n_diag, uint32_t baby_steps, const uint64_t* const* d_baby_evks,
                                const uint64_t* const* d_giant_evks, uint64_t* d_out, void* stream);
 
+/* ---- bootstrapping (EvalBootstrapSetup / EvalBootstrapKeyGen / EvalBootstrap, gpu_real_model.cu:1335-1336,
+ * 1444,2544) ------------------------------------------------------------------------------------------
+ * Full-slot (N/2 slots) CKKS bootstrap: ModRaise (centered q0 limb), CoeffToSlot (3 BSGS levels), EvalMod
+ * (Chebyshev interpolant of degree cheb_degree of a scaled cosine on [-1, 1], evaluated by Chebyshev
+ * division, then double_angles double-angle steps; K bounds |I| of the raised message m + q0 I), SlotToCoeff
+ * (3 BSGS levels).  Consumes 3 + 7 + double_angles + 3 levels: the input is the q0 limb [2][1][N] of a
+ * ciphertext whose message has scale in_scale; the output has ckks_bootstrap_out_level() limbs and scale
+ * S(l): S(l) = top_scale for l >= L-3 (CoeffToSlot keeps the scale: its diagonals are encoded at the prime
+ * each level drops, so the top three Q primes should be the largest), then S(l-1) = S(l)^2 / q_{l-1}.  Keys: the relinearization key, the conjugation key
+ * (automorphism 2N-1) and one automorphism key per rotation step of ckks_bootstrap_steps(). */
+typedef struct ckks_bootstrap ckks_bootstrap;
+int ckks_gen_primes(uint32_t bits, uint32_t count, const uint64_t* skip, uint32_t n_skip, uint64_t* out);
+int ckks_bootstrap_setup(ckks_context* ctx, double K, uint32_t cheb_degree, uint32_t double_angles, double top_scale,
+                         double in_scale, ckks_bootstrap** out);
+void ckks_bootstrap_destroy(ckks_bootstrap* bt);
+int ckks_bootstrap_steps(const ckks_bootstrap* bt, int64_t* steps, uint32_t cap, uint32_t* n);
+uint32_t ckks_bootstrap_out_level(const ckks_bootstrap* bt);
+double ckks_bootstrap_scale(const ckks_bootstrap* bt, uint32_t level);
+int ckks_eval_bootstrap(ckks_context* ctx, const ckks_bootstrap* bt, const uint64_t* d_ct_in, const uint64_t* d_relin,
+                        const uint64_t* d_conj, const int64_t* steps, const uint64_t* const* d_evks, uint32_t n_keys,
+                        uint64_t* d_out, void* stream);
+/* stage-wise form for testing: stops after stage 1 ModRaise, 2 CoeffToSlot, 3 split (two ciphertexts),
+ * 4 EvalMod (two ciphertexts), 5 recombination, 6 the full bootstrap; writes that ciphertext (batch) to d_out
+ * (sized for the top level) and its level to *level.  Synchronous on the null stream. */
+int ckks_eval_bootstrap_stage(ckks_context* ctx, const ckks_bootstrap* bt, const uint64_t* d_ct_in,
+                              const uint64_t* d_relin, const uint64_t* d_conj, const int64_t* steps,
+                              const uint64_t* const* d_evks, uint32_t n_keys, uint32_t stage, uint64_t* d_out,
+                              uint32_t* level);
+
 /* ---- client side: keys, encoding, encryption (CryptoContext KeyGen / EvalMultKeyGen /
  * EvalRotateKeyGen / MakeCKKSPackedPlaintext / Encrypt / Decrypt, gpu_real_model.cu:1293-1336,1577-1589,
  * 2202-2221).  Not on the evaluation hot path; used to make seeded inputs and read results.
@@ -174,6 +203,8 @@ int ckks_encrypt(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_pt,
                  uint32_t index, uint64_t* d_ct);
 int ckks_decrypt_decode(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_ct, uint32_t level, double scale,
                         double* re, double* im, uint32_t n_slots);
+/* decryption to the N centered coefficients (CRT of the first two limbs) as doubles */
+int ckks_decrypt_coeffs(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_ct, uint32_t level, double* out);
 
 /* ---- per-launch profiling (HIP events on the launch stream) ------------------------------------
  * enable: start recording every kernel launch (name, algorithmic bytes, start/stop events);
