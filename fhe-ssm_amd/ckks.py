@@ -62,6 +62,17 @@ SIGNATURES = {
     "ckks_eval_rotate_many": (_int, [_vp, _vp, _u32, _u32, _vp, _vp, _vp, _vp]),
     "ckks_linear_transform_bsgs": (_int, [_vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _vp]),
     "ckks_gen_primes": (_int, [_u32, _u32, _vp, _u32, _vp]),
+    "ckks_encode_periodic": (_int, [_vp, _vp, _vp, _u32, _u32, _u32, ctypes.c_double, _vp]),
+    "ckks_eval_mult_plain_ex": (_int, [_vp, _vp, _u32, _u32, _vp, _int, _u32, _vp, _vp]),
+    "ckks_linear_transform_general": (_int, [_vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, _u32, _vp, _vp, _vp, _vp]),
+    "ckks_linear_transform_multi": (_int, [_vp, _vp, _u32, _u32, _vp, _u32, _u32, _vp, _vp, _u32, _vp, _vp, _u32,
+                                           _int, _vp, _vp]),
+    "ckks_eval_mult_sum": (_int, [_vp, _vp, _u32, _u32, _u32, _vp, _int, _vp, _vp]),
+    "ckks_eval_rotate_masked": (_int, [_vp, _vp, _u32, _u32, _vp, _vp, _vp, _vp, _u32, _vp, _u32, _vp, _vp]),
+    "ckks_eval_automorphism_ks": (_int, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp]),
+    "ckks_eval_mul_i": (_int, [_vp, _vp, _u32, _u32, _int, _vp, _vp]),
+    "ckks_eval_lincomb": (_int, [_vp, _u32, _u32, _vp, _vp, _vp, _vp, ctypes.c_double, ctypes.c_double, _u32, _int,
+                                 _vp, _vp]),
     "ckks_bootstrap_setup": (_int, [_vp, ctypes.c_double, _u32, _u32, ctypes.c_double, ctypes.c_double,
                                     ctypes.POINTER(_vp)]),
     "ckks_bootstrap_destroy": (None, [_vp]),
@@ -265,6 +276,67 @@ class Context:
                               stream=None):
         check(load().ckks_linear_transform_bsgs(self.h, d_ct, level, d_diags, n_diag, baby_steps,
                                                 _ptr_array(baby_evks), _ptr_array(giant_evks), d_out, stream))
+
+    def encode_periodic(self, values, level: int, scale: float, d_out) -> None:
+        """values [n][period] (real or complex); out [n][level][2 period] compressed periodic plaintexts"""
+        v = np.atleast_2d(np.asarray(values))
+        re = np.ascontiguousarray(v.real, dtype=np.float64)
+        im = np.ascontiguousarray(v.imag, dtype=np.float64) if np.iscomplexobj(v) else None
+        check(load().ckks_encode_periodic(self.h, _ptr(re), _ptr(im) if im is not None else None, v.shape[0],
+                                          v.shape[1], level, scale, d_out))
+
+    def eval_mult_plain_ex(self, d_ct, batch, level, d_pt, log_rep, d_out, pt_shared=True, stream=None):
+        check(load().ckks_eval_mult_plain_ex(self.h, d_ct, batch, level, d_pt, 1 if pt_shared else 0, log_rep,
+                                             d_out, stream))
+
+    def linear_transform_general(self, d_ct, level, d_diags, log_rep, baby_steps, baby_evks, giant_steps,
+                                 giant_evks, d_out, stream=None):
+        bs = np.ascontiguousarray(np.asarray(baby_steps, dtype=np.int64))
+        gs = np.ascontiguousarray(np.asarray(giant_steps, dtype=np.int64))
+        check(load().ckks_linear_transform_general(self.h, d_ct, level, d_diags, log_rep, len(bs), _ptr(bs),
+                                                   _ptr_array([k or 0 for k in baby_evks]), len(gs), _ptr(gs),
+                                                   _ptr_array([k or 0 for k in giant_evks]), d_out, stream))
+
+    def linear_transform_multi(self, inputs, level, d_diags, log_rep, baby_steps, baby_evks, giant_steps,
+                               giant_evks, n_out, rescale, d_out, stream=None):
+        bs = np.ascontiguousarray(np.asarray(baby_steps, dtype=np.int64))
+        gs = np.ascontiguousarray(np.asarray(giant_steps, dtype=np.int64))
+        check(load().ckks_linear_transform_multi(self.h, _ptr_array(inputs), len(inputs), level, d_diags, log_rep,
+                                                 len(bs), _ptr(bs), _ptr_array([k or 0 for k in baby_evks]), len(gs),
+                                                 _ptr(gs), _ptr_array([k or 0 for k in giant_evks]), n_out,
+                                                 1 if rescale else 0, d_out, stream))
+
+    def eval_mult_sum(self, pairs, level, d_evk, d_out, rescale=True, stream=None):
+        """pairs: [batch][n_products] of (a, b) device pointers"""
+        batch, npr = len(pairs), len(pairs[0])
+        flat = [p for item in pairs for ab in item for p in ab]
+        assert len(flat) == batch * npr * 2
+        check(load().ckks_eval_mult_sum(self.h, _ptr_array(flat), npr, batch, level, d_evk, 1 if rescale else 0,
+                                        d_out, stream))
+
+    def eval_rotate_masked(self, d_ct, level, steps_lo, evks_lo, steps_hi, evks_hi, n_sets, d_pts, log_rep, d_out,
+                           stream=None):
+        lo = np.ascontiguousarray(np.asarray(steps_lo, dtype=np.int64))
+        hi = np.ascontiguousarray(np.asarray(steps_hi, dtype=np.int64))
+        check(load().ckks_eval_rotate_masked(self.h, d_ct, level, len(lo), _ptr(lo),
+                                             _ptr_array([k or 0 for k in evks_lo]), _ptr(hi),
+                                             _ptr_array([k or 0 for k in evks_hi]), n_sets, d_pts, log_rep, d_out,
+                                             stream))
+
+    def eval_automorphism_ks(self, d_ct, batch, level, g, d_evk, d_out, stream=None):
+        check(load().ckks_eval_automorphism_ks(self.h, d_ct, batch, level, g, d_evk, d_out, stream))
+
+    def eval_mul_i(self, d_in, n_polys, level, sign, d_out, stream=None):
+        check(load().ckks_eval_mul_i(self.h, d_in, n_polys, level, sign, d_out, stream))
+
+    def eval_lincomb(self, batch, terms, levels, coeffs, scales_in, scale_out, add_const, target_level, integer,
+                     d_out, stream=None):
+        lv = np.ascontiguousarray(np.asarray(levels, dtype=np.uint32))
+        cf = np.ascontiguousarray(np.asarray(coeffs, dtype=np.float64))
+        si = np.ascontiguousarray(np.asarray(scales_in if scales_in is not None else [1.0] * len(terms),
+                                             dtype=np.float64))
+        check(load().ckks_eval_lincomb(self.h, batch, len(terms), _ptr_array(terms), _ptr(lv), _ptr(cf), _ptr(si),
+                                       scale_out, add_const, target_level, 1 if integer else 0, d_out, stream))
 
     # client side ------------------------------------------------------------------------------
     def secret(self, seed: bytes, hamming_weight: int = 192) -> "Secret":

@@ -488,6 +488,148 @@ int ckks_decrypt_decode(ckks_context* ctx, const ckks_secret* sk, const uint64_t
     });
 }
 
+int ckks_encode_periodic(ckks_context* ctx, const double* re, const double* im, uint32_t n_vectors, uint32_t period,
+                         uint32_t level, double scale, uint64_t* d_out) {
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_out || (!re && !im)) return fail(CKKS_EINVAL, "null argument");
+    if (!(scale > 0)) return fail(CKKS_EINVAL, "scale must be positive");
+    if (!n_vectors) return CKKS_OK;
+    return guarded([&] {
+        fhe::encode_periodic(ctx->c, re, im, n_vectors, period, level, scale, d_out);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_mult_plain_ex(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level,
+                            const uint64_t* d_pt, int pt_shared, uint32_t log_rep, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_ct || !d_pt || !d_out) return fail(CKKS_EINVAL, "null buffer");
+    if (log_rep > 6) return fail(CKKS_EINVAL, "log_rep must be <= 6");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::mul_plain(ctx->c, d_ct, batch, level, d_pt, pt_shared != 0, d_out, (hipStream_t)stream, log_rep);
+        return CKKS_OK;
+    });
+}
+
+int ckks_linear_transform_general(ckks_context* ctx, const uint64_t* d_ct, uint32_t level, const uint64_t* d_diags,
+                                  uint32_t log_rep, uint32_t n_baby, const int64_t* baby_steps,
+                                  const uint64_t* const* d_baby_evks, uint32_t n_giant, const int64_t* giant_steps,
+                                  const uint64_t* const* d_giant_evks, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_ct || !d_diags || !d_out || !baby_steps || !giant_steps || !d_baby_evks || !d_giant_evks)
+        return fail(CKKS_EINVAL, "null argument");
+    if (n_baby == 0 || n_baby > 32 || n_giant == 0 || n_giant > 64 || log_rep > 6)
+        return fail(CKKS_EINVAL, "bad BSGS shape");
+    for (uint32_t i = 0; i < n_baby; i++)
+        if (baby_steps[i] && !d_baby_evks[i]) return fail(CKKS_EINVAL, "null baby key");
+    for (uint32_t i = 0; i < n_giant; i++)
+        if (giant_steps[i] && !d_giant_evks[i]) return fail(CKKS_EINVAL, "null giant key");
+    return guarded([&] {
+        fhe::bsgs_general(ctx->c, d_ct, level, d_diags, n_baby, baby_steps, d_baby_evks, n_giant, giant_steps,
+                          d_giant_evks, d_out, (hipStream_t)stream, log_rep);
+        return CKKS_OK;
+    });
+}
+
+int ckks_linear_transform_multi(ckks_context* ctx, const uint64_t* const* d_in, uint32_t n_in, uint32_t level,
+                                const uint64_t* d_diags, uint32_t log_rep, uint32_t n_baby, const int64_t* baby_steps,
+                                const uint64_t* const* d_baby_evks, uint32_t n_giant, const int64_t* giant_steps,
+                                const uint64_t* const* d_giant_evks, uint32_t n_out, int rescale, uint64_t* d_out,
+                                void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_in || !d_diags || !d_out || !baby_steps || !giant_steps || !d_baby_evks || !d_giant_evks)
+        return fail(CKKS_EINVAL, "null argument");
+    if (n_in == 0 || n_out == 0 || n_baby == 0 || n_in * n_baby > 256 || n_giant == 0 || n_giant > 64 || log_rep > 6)
+        return fail(CKKS_EINVAL, "bad BSGS shape");
+    if (rescale && level < 2) return fail(CKKS_EINVAL, "rescale needs level >= 2");
+    for (uint32_t i = 0; i < n_in; i++)
+        if (!d_in[i]) return fail(CKKS_EINVAL, "null input");
+    for (uint32_t i = 0; i < n_baby; i++)
+        if (baby_steps[i] && !d_baby_evks[i]) return fail(CKKS_EINVAL, "null baby key");
+    for (uint32_t i = 0; i < n_giant; i++)
+        if (giant_steps[i] && !d_giant_evks[i]) return fail(CKKS_EINVAL, "null giant key");
+    return guarded([&] {
+        fhe::bsgs_multi(ctx->c, d_in, n_in, level, d_diags, n_baby, baby_steps, d_baby_evks, n_giant, giant_steps,
+                        d_giant_evks, n_out, rescale != 0, d_out, (hipStream_t)stream, log_rep);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_mult_sum(ckks_context* ctx, const uint64_t* const* d_pairs, uint32_t n_products, uint32_t batch,
+                       uint32_t level, const uint64_t* d_evk, int rescale, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_pairs || !d_evk || !d_out) return fail(CKKS_EINVAL, "null argument");
+    if (n_products == 0 || n_products > 64) return fail(CKKS_EINVAL, "1..64 products per output");
+    if (rescale && level < 2) return fail(CKKS_EINVAL, "rescale needs level >= 2");
+    for (size_t j = 0; j < (size_t)batch * n_products * 2; j++)
+        if (!d_pairs[j]) return fail(CKKS_EINVAL, "null operand");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::hmult_sum(ctx->c, d_pairs, n_products, batch, level, d_evk, d_out, rescale != 0, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_rotate_masked(ckks_context* ctx, const uint64_t* d_ct, uint32_t level, uint32_t n,
+                            const int64_t* steps_lo, const uint64_t* const* d_evks_lo, const int64_t* steps_hi,
+                            const uint64_t* const* d_evks_hi, uint32_t n_sets, const uint64_t* d_pts,
+                            uint32_t log_rep, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_ct || !steps_lo || !steps_hi || !d_evks_lo || !d_evks_hi || !d_pts || !d_out)
+        return fail(CKKS_EINVAL, "null argument");
+    if (level < 2) return fail(CKKS_EINVAL, "the masked pairs are rescaled: level >= 2");
+    if (n == 0 || n_sets == 0 || log_rep > 6) return fail(CKKS_EINVAL, "bad shape");
+    for (uint32_t i = 0; i < n; i++)
+        if ((steps_lo[i] && !d_evks_lo[i]) || (steps_hi[i] && !d_evks_hi[i])) return fail(CKKS_EINVAL, "null key");
+    return guarded([&] {
+        fhe::rotate_masked(ctx->c, d_ct, level, n, steps_lo, d_evks_lo, steps_hi, d_evks_hi, n_sets, d_pts, log_rep,
+                           d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_automorphism_ks(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level, uint32_t g,
+                              const uint64_t* d_evk, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_ct || !d_evk || !d_out) return fail(CKKS_EINVAL, "null buffer");
+    if ((g & 1) == 0 || g >= 2u * (1u << 16)) return fail(CKKS_EINVAL, "automorphism index must be odd and < 2N");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        std::vector<uint32_t> gs(batch, g);
+        std::vector<const uint64_t*> ks(batch, d_evk);
+        fhe::automorph_ks_list(ctx->c, d_ct, batch, level, gs.data(), ks.data(), d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_mul_i(ckks_context* ctx, const uint64_t* d_in, uint32_t n_polys, uint32_t level, int sign,
+                    uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_in || !d_out) return fail(CKKS_EINVAL, "null buffer");
+    if (sign != 1 && sign != -1) return fail(CKKS_EINVAL, "sign must be +1 or -1");
+    if (!n_polys) return CKKS_OK;
+    return guarded([&] {
+        fhe::mul_i(ctx->c, d_in, n_polys, level, sign, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_lincomb(ckks_context* ctx, uint32_t batch, uint32_t n_terms, const uint64_t* const* d_terms,
+                      const uint32_t* levels, const double* coeffs, const double* scales_in, double scale_out,
+                      double add_const, uint32_t target_level, int integer_mode, uint64_t* d_out, void* stream) {
+    if (!ctx || !d_terms || !levels || !coeffs || !d_out || (!integer_mode && !scales_in))
+        return fail(CKKS_EINVAL, "null argument");
+    for (uint32_t t = 0; t < n_terms; t++)
+        if (!d_terms[t]) return fail(CKKS_EINVAL, "null term");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::lincomb(ctx->c, batch, n_terms, d_terms, levels, coeffs, scales_in, scale_out, add_const, target_level,
+                     integer_mode != 0, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
 int ckks_gen_primes(uint32_t bits, uint32_t count, const uint64_t* skip, uint32_t n_skip, uint64_t* out) {
     if (!out || (n_skip && !skip)) return fail(CKKS_EINVAL, "null argument");
     if (bits < 20 || bits > 60) return fail(CKKS_EINVAL, "bits must be in [20, 60]");

@@ -9,6 +9,9 @@
 #include <cstring>
 #include <stdexcept>
 #include <string>
+#include <algorithm>
+#include <atomic>
+#include <thread>
 #include <vector>
 
 #include "client.hpp"
@@ -18,6 +21,7 @@
 namespace fhe {
 
 uint64_t mulmod_h(uint64_t a, uint64_t b, uint64_t q);
+uint64_t powmod_h(uint64_t a, uint64_t e, uint64_t q);
 uint64_t invmod_h(uint64_t a, uint64_t q);
 hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,
                       NttMode mode, hipStream_t st);
@@ -30,6 +34,8 @@ hipError_t launch_encrypt(const Context& ctx, const uint64_t* m, const uint64_t*
                           const uint64_t* s, uint64_t* ct, uint32_t l, hipStream_t st);
 hipError_t launch_decrypt(const Context& ctx, const uint64_t* ct, const uint64_t* s, uint64_t* out, uint32_t l,
                           hipStream_t st);
+hipError_t launch_encode_small(const Context& ctx, const int64_t* coef, uint64_t* out, uint32_t n_vec, uint32_t Np,
+                               uint32_t l, const TwPair* tab, hipStream_t st);
 hipError_t launch_mul(const Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t l,
                       hipStream_t st);
 
@@ -222,6 +228,19 @@ void secret_destroy(Secret* sk) {
 }
 
 // Key-switching key from s_old (device, evaluation form, Q limbs [L][N]) to s_new (signed coefficients).
+// f(0) .. f(n-1) over up to 16 host threads (the limbs of a key are independent streams)
+template <class F>
+static void parallel_for(uint32_t n, F f) {
+    const uint32_t nt = std::min<uint32_t>(n, std::max(1u, std::min(16u, std::thread::hardware_concurrency())));
+    std::vector<std::thread> th;
+    std::atomic<uint32_t> next{0};
+    for (uint32_t t = 0; t < nt; t++)
+        th.emplace_back([&] {
+            for (uint32_t i; (i = next.fetch_add(1)) < n;) f(i);
+        });
+    for (auto& x : th) x.join();
+}
+
 void keygen_switch(Context& ctx, const uint64_t* d_s_old, const int8_t* s_new, const uint8_t seed[32],
                    const uint8_t eseed[32], double sigma, uint64_t* d_evk) {
     const uint32_t T = ctx.L + ctx.K;
@@ -240,7 +259,9 @@ void keygen_switch(Context& ctx, const uint64_t* d_s_old, const int8_t* s_new, c
     for (uint32_t d = 0; d < ctx.dnum; d++) {
         uint64_t* b_d = d_evk + ((size_t)d * 2 + 0) * T * kN;
         uint64_t* a_d = d_evk + ((size_t)d * 2 + 1) * T * kN;
-        for (uint32_t i = 0; i < T; i++) fill_uniform(seed, d, i, kTagKey, ctx.moduli[i], a.data() + (size_t)i * kN, kN);
+        parallel_for(T, [&](uint32_t i) {
+            fill_uniform(seed, d, i, kTagKey, ctx.moduli[i], a.data() + (size_t)i * kN, kN);
+        });
         HIPC(hipMemcpy(a_d, a.data(), a.size() * 8, hipMemcpyHostToDevice));
         gauss(eseed, d, 0, sigma, e.data());
         coeffs_to_eval(ctx, e.data(), 1, iota(T), de.as<uint64_t>(), nullptr);
@@ -298,6 +319,74 @@ void encode(Context& ctx, const double* re, const double* im, uint32_t n_slots, 
         coef[k] = (int64_t)std::llround(m);
     }
     coeffs_to_eval(ctx, coef.data(), 1, iota(l), d_pt, nullptr);
+}
+
+// Periodic encoding (hpc_gpu_port/periodic_encode.hpp:179-260): a slot vector of period P (replicated
+// REP = N/(2P) times) is the encoding of a polynomial in X^REP, i.e. of one period in the ring of degree
+// N' = 2P.  Its evaluation form, in the bit-reversed order of the N-point NTT, has word k equal to word
+// k >> log2(REP) of the N'-point NTT (root psi^REP) of that small polynomial, so only N' words per limb
+// are stored.  The special FFT and rounding run on the host (over threads); residues and the N'-point NTTs
+// on the GPU.  out: [n_vec][l][N'].
+void encode_periodic(Context& ctx, const double* re, const double* im, uint32_t n_vec, uint32_t P, uint32_t l,
+                     double scale, uint64_t* d_out) {
+    if (P < 2 || (P & (P - 1)) || P > 2048) throw std::invalid_argument("period must be a power of two in [2, 2048]");
+    const uint32_t Np = 2 * P;
+    uint32_t logNp = 0;
+    while ((1u << logNp) < Np) logNp++;
+    const uint32_t rep = kN / Np;
+    const uint64_t M = 2ull * Np;
+    auto it = ctx.small_ntt.find(Np);
+    if (it == ctx.small_ntt.end()) {
+        // Table[brev(j)] = psi'^j with psi' = psi^rep, per prime of the chain
+        const uint32_t T = ctx.L + ctx.K;
+        std::vector<TwPair> tabs((size_t)T * Np);
+        for (uint32_t i = 0; i < T; i++) {
+            const uint64_t q = ctx.moduli[i];
+            const uint64_t psi_p = powmod_h(ctx.psi[i], rep, q);
+            uint64_t x = 1;
+            for (uint32_t j = 0; j < Np; j++) {
+                uint32_t r = 0;
+                for (uint32_t t = 0, v = j; t < logNp; t++, v >>= 1) r = (r << 1) | (v & 1);
+                tabs[(size_t)i * Np + r] = TwPair{x, (uint64_t)(((unsigned __int128)x << 64) / q)};
+                x = mulmod_h(x, psi_p, q);
+            }
+        }
+        TwPair* d = nullptr;
+        HIPC(hipMalloc(&d, tabs.size() * sizeof(TwPair)));
+        HIPC(hipMemcpy(d, tabs.data(), tabs.size() * sizeof(TwPair), hipMemcpyHostToDevice));
+        it = ctx.small_ntt.emplace(Np, d).first;
+    }
+    std::vector<uint32_t> t_of(P), tc_of(P);
+    {
+        uint64_t e = 1;
+        for (uint32_t j = 0; j < P; j++) {
+            t_of[j] = (uint32_t)((e - 1) / 2);
+            tc_of[j] = (uint32_t)((M - e - 1) / 2);
+            e = e * 5 % M;
+        }
+    }
+    std::vector<int64_t> coef((size_t)n_vec * Np);
+    std::atomic<bool> overflow{false};
+    parallel_for(n_vec, [&](uint32_t n) {
+        std::vector<std::complex<double>> v(Np, 0.0);
+        for (uint32_t j = 0; j < P; j++) {
+            const std::complex<double> z(re ? re[(size_t)n * P + j] : 0.0, im ? im[(size_t)n * P + j] : 0.0);
+            v[t_of[j]] = z * scale;
+            v[tc_of[j]] = std::conj(z) * scale;
+        }
+        fft(v, -1);
+        for (uint32_t k = 0; k < Np; k++) {
+            const double ang = -M_PI * (double)k / (double)Np;
+            const double m = (v[k] * std::complex<double>(std::cos(ang), std::sin(ang))).real() / (double)Np;
+            if (!(std::fabs(m) < 4.0e18)) overflow = true;
+            coef[(size_t)n * Np + k] = overflow ? 0 : (int64_t)std::llround(m);
+        }
+    });
+    if (overflow) throw std::invalid_argument("encoded coefficient overflows int64");
+    DevBuf dc(coef.size() * 8);
+    HIPC(hipMemcpy(dc.p, coef.data(), coef.size() * 8, hipMemcpyHostToDevice));
+    HIPC(launch_encode_small(ctx, dc.as<int64_t>(), d_out, n_vec, Np, l, it->second, nullptr));
+    HIPC(hipDeviceSynchronize());
 }
 
 void encrypt(Context& ctx, const Secret& sk, const uint64_t* d_pt, uint32_t l, const uint8_t seed[32],

@@ -91,6 +91,47 @@ __global__ __launch_bounds__(256) void k_mul(const uint64_t* __restrict__ x, con
 
 }  // namespace
 
+// Periodic-plaintext encoder: vector n, limb i -> the N'-point negacyclic NTT (root psi^(N/N'), output in
+// bit-reversed order) of the small polynomial coef[n] mod q_i.  One workgroup per (n, i), the limb in LDS.
+constexpr int kMaxSmallN = 4096;
+
+__global__ __launch_bounds__(256) void k_encode_small(const int64_t* __restrict__ coef, uint64_t* __restrict__ out,
+                                                      uint32_t Np, uint32_t l, const TwPair* __restrict__ tab,
+                                                      const PrimeInfo* __restrict__ primes) {
+    __shared__ uint64_t a[kMaxSmallN];
+    const uint32_t n = blockIdx.x, i = blockIdx.y;
+    const uint64_t q = primes[i].q;
+    const int64_t* c = coef + (size_t)n * Np;
+    for (uint32_t k = threadIdx.x; k < Np; k += 256) {
+        const int64_t v = c[k];
+        // |v| < 2^62: the residue of a negative value is q - (|v| mod q)
+        const uint64_t r = v >= 0 ? (uint64_t)v % q : (uint64_t)(-(v + 1)) % q;
+        a[k] = v >= 0 ? r : q - 1 - r;
+    }
+    __syncthreads();
+    const TwPair* tw = tab + (size_t)i * Np;
+    for (uint32_t m = 1, t = Np >> 1; m < Np; m <<= 1, t >>= 1) {
+        for (uint32_t b = threadIdx.x; b < Np / 2; b += 256) {
+            const uint32_t grp = b / t, lo = grp * 2 * t + (b - grp * t);
+            const TwPair w = tw[m + grp];
+            const uint64_t x = shoup(a[lo + t], w.w, w.wp, q);
+            const uint64_t u = a[lo];
+            a[lo] = add_mod(u, x, q);
+            a[lo + t] = sub_mod(u, x, q);
+        }
+        __syncthreads();
+    }
+    uint64_t* o = out + ((size_t)n * l + i) * Np;
+    for (uint32_t k = threadIdx.x; k < Np; k += 256) o[k] = a[k];
+}
+
+hipError_t launch_encode_small(const Context& ctx, const int64_t* coef, uint64_t* out, uint32_t n_vec, uint32_t Np,
+                               uint32_t l, const TwPair* tab, hipStream_t st) {
+    if (Np > (uint32_t)kMaxSmallN || Np < 2) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_encode_small, dim3(n_vec, l), dim3(256), 0, st, coef, out, Np, l, tab, ctx.d_primes);
+    return hipGetLastError();
+}
+
 hipError_t launch_small_to_rns(const Context& ctx, const int64_t* coef, uint64_t* out, uint32_t n_polys,
                                const std::vector<uint32_t>& pmap, hipStream_t st) {
     PmapArgs pa{};

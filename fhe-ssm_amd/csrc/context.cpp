@@ -178,6 +178,8 @@ void context_release(Context& c) {
     prof_clear(c);
     for (auto& kv : c.bconv_cache) (void)hipFree(kv.second.d_tab);
     for (auto& s : c.scratch) (void)hipFree(s.first);
+    for (auto& kv : c.small_ntt) (void)hipFree(kv.second);
+    c.small_ntt.clear();
     c.job_cache.clear();
     c.bconv_cache.clear();
     c.scratch.clear();

@@ -73,6 +73,8 @@ struct Context {
     std::map<std::string, BConvPlan> bconv_cache;
     // growable scratch
     std::vector<std::pair<void*, size_t>> scratch;
+    // device tables [L+K][N'] of the small-ring NTTs used by periodic encoding, by ring size N'
+    std::map<uint32_t, TwPair*> small_ntt;
     // per-launch profiling (off by default)
     bool prof_on = false;
     mutable std::vector<ProfRec> prof;

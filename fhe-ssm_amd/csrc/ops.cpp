@@ -46,11 +46,21 @@ hipError_t launch_ks_inner_list(const Context& ctx, const uint64_t* const* ext, 
 hipError_t launch_automorph_list(const Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n, uint32_t l,
                                  const uint32_t* g, hipStream_t st);
 hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* baby, const uint64_t* diag, uint64_t* out, uint32_t nb,
-                           uint32_t n_diag, uint32_t ng, uint32_t l, hipStream_t st);
+                           uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st);
 hipError_t launch_mul_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
-                            uint32_t l, uint64_t pt_bstride, hipStream_t st);
+                            uint32_t l, uint64_t pt_bstride, uint32_t log_rep, hipStream_t st);
 hipError_t launch_add_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
                             uint32_t l, uint64_t pt_bstride, hipStream_t st);
+hipError_t launch_lincomb(const Context& ctx, uint64_t* out, uint32_t B, uint32_t l_out, uint32_t n_terms,
+                          const uint64_t* const* x, const uint32_t* stride, const uint64_t* C, const uint64_t* add,
+                          hipStream_t st);
+hipError_t launch_mul_i(const Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n_polys, uint32_t l, int sign,
+                        hipStream_t st);
+hipError_t launch_pair_mac(const Context& ctx, const uint64_t* R, const uint64_t* pt, uint64_t* out, uint32_t n_sets,
+                           uint32_t n, uint32_t l, uint32_t log_rep, hipStream_t st);
+hipError_t launch_tensor_sum(const Context& ctx, const uint64_t* const* d_tab, uint32_t np, uint64_t* d01,
+                             uint64_t* d2, uint32_t B, uint32_t l, uint64_t* d2e, uint64_t d2e_bstride,
+                             const uint32_t* ext_off, hipStream_t st);
 hipError_t launch_sum_list(const Context& ctx, const uint64_t* const* in, uint32_t n, uint64_t* out, uint32_t n_polys,
                            uint32_t l, hipStream_t st);
 
@@ -289,19 +299,12 @@ void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uin
 
 // ------------------------------------------------------------------ HMult + relinearize (+ rescale)
 // a, b: [B][2][l][N] eval -> out: [B][2][l-1][N] (rescaled) or [B][2][l][N] (do_rescale = false)
-void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l, const uint64_t* evk,
-           uint64_t* out, bool do_rescale, hipStream_t st) {
-    check_level(ctx, l);
-    const uint32_t D = num_digits(ctx, l), E = l + ctx.K;
-    uint64_t* d01 = (uint64_t*)ws_get(ctx, WS_D01, (size_t)B * 2 * l * W * 8);
-    uint64_t* x2c = (uint64_t*)ws_get(ctx, WS_X2C, (size_t)B * l * W * 8);
-    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)B * D * E * W * 8);
+// relinearization (+ rescale) after the tensor step: d01 [B][2][l][N], d2 in x2c (evaluation form) and in
+// each digit's own limbs of ext
+static void relin_tail(Context& ctx, uint64_t* d01, uint64_t* x2c, uint64_t* ext, uint32_t B, uint32_t l,
+                       const uint64_t* evk, uint64_t* out, bool do_rescale, hipStream_t st) {
+    const uint32_t E = l + ctx.K;
     uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)B * 2 * E * W * 8);
-    // the tensor kernel writes d2 twice: into x2c (to be taken to coefficients) and, in evaluation
-    // form, straight into each digit's own limbs of the extension buffer
-    std::vector<uint32_t> ext_off(l);
-    for (uint32_t t = 0; t < l; t++) ext_off[t] = (t / ctx.alpha) * E + t;
-    HIPX(launch_tensor(ctx, a, b, d01, x2c, B, l, ext, (uint64_t)D * E * W, ext_off.data(), st));
     std::vector<uint32_t> pm(l);
     for (uint32_t i = 0; i < l; i++) pm[i] = i;
     HIPX(launch_ntt(ctx, x2c, regular_jobs(B, pm), B * l, true, ctx.ntt_mode, st));
@@ -314,6 +317,42 @@ void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint3
     uint64_t* relin = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)B * 2 * l * W * 8);
     moddown_inplace(ctx, acc, 2 * B, l, d01, relin, st, 1);
     rescale(ctx, relin, 2 * B, l, out, st);
+}
+
+void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l, const uint64_t* evk,
+           uint64_t* out, bool do_rescale, hipStream_t st) {
+    check_level(ctx, l);
+    const uint32_t D = num_digits(ctx, l), E = l + ctx.K;
+    uint64_t* d01 = (uint64_t*)ws_get(ctx, WS_D01, (size_t)B * 2 * l * W * 8);
+    uint64_t* x2c = (uint64_t*)ws_get(ctx, WS_X2C, (size_t)B * l * W * 8);
+    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)B * D * E * W * 8);
+    // the tensor kernel writes d2 twice: into x2c (to be taken to coefficients) and, in evaluation
+    // form, straight into each digit's own limbs of the extension buffer
+    std::vector<uint32_t> ext_off(l);
+    for (uint32_t t = 0; t < l; t++) ext_off[t] = (t / ctx.alpha) * E + t;
+    HIPX(launch_tensor(ctx, a, b, d01, x2c, B, l, ext, (uint64_t)D * E * W, ext_off.data(), st));
+    relin_tail(ctx, d01, x2c, ext, B, l, evk, out, do_rescale, st);
+}
+
+// out[c] = relin( sum_j a[c][j] (x) b[c][j] ) (+ rescale): one key switch per batch item for np products.
+// pairs: [B][np][2] ciphertext pointers, each [2][l][N].
+void hmult_sum(Context& ctx, const uint64_t* const* pairs, uint32_t np, uint32_t B, uint32_t l, const uint64_t* evk,
+               uint64_t* out, bool do_rescale, hipStream_t st) {
+    check_level(ctx, l);
+    if (np == 0 || np > 64) throw std::invalid_argument("1..64 products per item");
+    const uint32_t D = num_digits(ctx, l), E = l + ctx.K;
+    uint64_t* d01 = (uint64_t*)ws_get(ctx, WS_D01, (size_t)B * 2 * l * W * 8);
+    uint64_t* x2c = (uint64_t*)ws_get(ctx, WS_X2C, (size_t)B * l * W * 8);
+    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)B * D * E * W * 8);
+    const size_t tab_bytes = (size_t)B * np * 2 * sizeof(void*);
+    auto* d_tab = (const uint64_t**)ws_get(ctx, WS_PTAB, tab_bytes);
+    HIPX(hipMemcpyAsync(d_tab, pairs, tab_bytes, hipMemcpyHostToDevice, st));
+    std::vector<uint32_t> ext_off(l);
+    for (uint32_t t = 0; t < l; t++) ext_off[t] = (t / ctx.alpha) * E + t;
+    HIPX(launch_tensor_sum(ctx, d_tab, np, d01, x2c, B, l, ext, (uint64_t)D * E * W, ext_off.data(), st));
+    // the pointer table must outlive the copy: the caller's array may be freed on return
+    HIPX(hipStreamSynchronize(st));
+    relin_tail(ctx, d01, x2c, ext, B, l, evk, out, do_rescale, st);
 }
 
 // ------------------------------------------------------------------ rotation
@@ -356,7 +395,12 @@ void automorph_ks_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l
                        const uint64_t* const* evk, uint64_t* out, hipStream_t st) {
     check_level(ctx, l);
     if (n == 0) return;
-    if (n > 64) throw std::invalid_argument("at most 64 rotations per call");
+    if (n > 64) {  // in chunks of 64 (the list kernels take 64 pointers)
+        for (uint32_t c0 = 0; c0 < n; c0 += 64)
+            automorph_ks_list(ctx, cts + (size_t)c0 * 2 * l * W, std::min(64u, n - c0), l, gidx + c0, evk + c0,
+                              out + (size_t)c0 * 2 * l * W, st);
+        return;
+    }
     const uint32_t D = num_digits(ctx, l), E = l + ctx.K;
     uint64_t* c1 = (uint64_t*)ws_get(ctx, WS_C1, (size_t)n * l * W * 8);
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)n * D * E * W * 8);
@@ -380,13 +424,25 @@ void rotate_hoisted(Context& ctx, const uint64_t* ct, uint32_t l, const int64_t*
                     const uint64_t* const* evk, uint64_t* out, hipStream_t st) {
     check_level(ctx, l);
     if (n == 0) return;
-    if (n > 64) throw std::invalid_argument("at most 64 rotations per call");
     const uint32_t E = l + ctx.K;
     const uint32_t D = num_digits(ctx, l);
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)D * E * W * 8);
+    modup(ctx, ct + (size_t)l * W, ext, 1, l, st);
+    rotate_hoisted_ext(ctx, ct, ext, l, steps, n, evk, out, st);
+}
+
+// the rotations of a hoisted set from its ModUp output ext ([D][E][N] of c1), in chunks of 64
+void rotate_hoisted_ext(Context& ctx, const uint64_t* ct, const uint64_t* ext, uint32_t l, const int64_t* steps,
+                        uint32_t n, const uint64_t* const* evk, uint64_t* out, hipStream_t st) {
+    if (n > 64) {
+        for (uint32_t c0 = 0; c0 < n; c0 += 64)
+            rotate_hoisted_ext(ctx, ct, ext, l, steps + c0, std::min(64u, n - c0), evk + c0,
+                               out + (size_t)c0 * 2 * l * W, st);
+        return;
+    }
+    const uint32_t E = l + ctx.K;
     uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)n * 2 * E * W * 8);
     uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)n * 2 * l * W * 8);
-    modup(ctx, ct + (size_t)l * W, ext, 1, l, st);
     std::vector<const uint64_t*> ep(n, ext);
     std::vector<uint32_t> g(n);
     for (uint32_t c = 0; c < n; c++) g[c] = rotation_index(steps[c]);
@@ -397,9 +453,9 @@ void rotate_hoisted(Context& ctx, const uint64_t* ct, uint32_t l, const int64_t*
 }
 
 void mul_plain(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const uint64_t* pt, bool pt_shared,
-               uint64_t* out, hipStream_t st) {
+               uint64_t* out, hipStream_t st, uint32_t log_rep) {
     check_level(ctx, l);
-    HIPX(launch_mul_plain(ctx, ct, pt, out, B, l, pt_shared ? 0 : (uint64_t)l * W, st));
+    HIPX(launch_mul_plain(ctx, ct, pt, out, B, l, pt_shared ? 0 : (uint64_t)l * (W >> log_rep), log_rep, st));
 }
 
 void add_plain(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const uint64_t* pt, bool pt_shared,
@@ -429,7 +485,7 @@ void bsgs_matvec(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* d
         for (uint32_t j = 1; j < bs; j++) steps[j - 1] = j;
         rotate_hoisted(ctx, ct, l, steps.data(), bs - 1, baby_evk, baby + ctw, st);
     }
-    HIPX(launch_bsgs_mac(ctx, baby, diags, v, bs, n_diag, ng, l, st));
+    HIPX(launch_bsgs_mac(ctx, baby, diags, v, bs, n_diag, ng, l, 0, st));
     std::vector<const uint64_t*> terms(1, v);
     if (ng > 1) {
         std::vector<int64_t> steps(ng - 1);
@@ -444,56 +500,174 @@ void bsgs_matvec(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* d
 // General BSGS linear transform on one ciphertext [2][l][N]:
 //   y = sum_g Rot_{G[g]}( sum_b diag[g*nb + b] (.) Rot_{Bs[b]}(x) )   (no rescale; out [2][l][N])
 // A step of 0 is the identity (no key).  Baby rotations share one ModUp; giant rotations run as one batch.
-void bsgs_general(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* diags, uint32_t nb,
-                  const int64_t* bsteps, const uint64_t* const* bevk, uint32_t ng, const int64_t* gsteps,
-                  const uint64_t* const* gevk, uint64_t* out, hipStream_t st) {
+// General BSGS with n_in inputs sharing the baby steps and n_out outputs sharing the babies:
+//   out_o = sum_g Rot_{G_g}( sum_{i, b} diag[o][g][i nb + b] (.) Rot_{B_b}(in_i) )   (+ rescale)
+// Step 0 is the identity (no key).  diags: [n_out][ng][n_in nb][l][N >> log_rep], term (g, i, b) pre-rotated
+// by -G_g.  The babies of each input share one ModUp; all giant rotations of all outputs run as one list.
+void bsgs_multi(Context& ctx, const uint64_t* const* in, uint32_t n_in, uint32_t l, const uint64_t* diags,
+                uint32_t nb, const int64_t* bsteps, const uint64_t* const* bevk, uint32_t ng, const int64_t* gsteps,
+                const uint64_t* const* gevk, uint32_t n_out, bool do_rescale, uint64_t* out, hipStream_t st,
+                uint32_t log_rep) {
     check_level(ctx, l);
-    if (nb == 0 || nb > 32 || ng == 0 || ng > 64) throw std::invalid_argument("bad BSGS shape");
+    if (nb == 0 || n_in == 0 || n_out == 0 || ng == 0 || ng > 64) throw std::invalid_argument("bad BSGS shape");
+    if (do_rescale && l < 2) throw std::invalid_argument("rescale needs l >= 2");
     const size_t ctw = (size_t)2 * l * W;
-    uint64_t* baby = (uint64_t*)ws_get(ctx, WS_BABY, (size_t)nb * ctw * 8);
-    uint64_t* v = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)ng * ctw * 8);
-    uint64_t* vr = (uint64_t*)ws_get(ctx, WS_GROT, (size_t)ng * ctw * 8);
+    const uint32_t nbt = n_in * nb;
+    uint64_t* baby = (uint64_t*)ws_get(ctx, WS_BABY, (size_t)nbt * ctw * 8);
+    uint64_t* v = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)n_out * ng * ctw * 8);
     std::vector<int64_t> rs;
     std::vector<const uint64_t*> rk;
     std::vector<uint32_t> rpos;
     for (uint32_t b = 0; b < nb; b++) {
-        if (bsteps[b] == 0) {
-            HIPX(hipMemcpyAsync(baby + b * ctw, ct, ctw * 8, hipMemcpyDeviceToDevice, st));
-        } else {
+        if (bsteps[b] != 0) {
             rs.push_back(bsteps[b]);
             rk.push_back(bevk[b]);
             rpos.push_back(b);
+        }
+    }
+    for (uint32_t i = 0; i < n_in; i++) {
+        for (uint32_t b = 0; b < nb; b++)
+            if (bsteps[b] == 0)
+                HIPX(hipMemcpyAsync(baby + ((size_t)i * nb + b) * ctw, in[i], ctw * 8, hipMemcpyDeviceToDevice, st));
+        if (rs.empty()) continue;
+        // contiguous runs of non-zero steps rotate straight into place; otherwise through a staging buffer
+        bool contiguous = true;
+        for (size_t r = 0; r < rpos.size(); r++) contiguous &= rpos[r] == rpos[0] + r;
+        if (contiguous) {
+            rotate_hoisted(ctx, in[i], l, rs.data(), (uint32_t)rs.size(), rk.data(),
+                           baby + ((size_t)i * nb + rpos[0]) * ctw, st);
+        } else {
+            uint64_t* tmp = (uint64_t*)ws_get(ctx, WS_SUM, rs.size() * ctw * 8);
+            rotate_hoisted(ctx, in[i], l, rs.data(), (uint32_t)rs.size(), rk.data(), tmp, st);
+            for (size_t r = 0; r < rs.size(); r++)
+                HIPX(hipMemcpyAsync(baby + ((size_t)i * nb + rpos[r]) * ctw, tmp + r * ctw, ctw * 8,
+                                    hipMemcpyDeviceToDevice, st));
+        }
+    }
+    HIPX(launch_bsgs_mac(ctx, baby, diags, v, nbt, nbt * n_out * ng, n_out * ng, l, log_rep, st));
+    // giants with a non-zero step, all outputs, packed contiguously and rotated as one list
+    std::vector<int64_t> gs;
+    std::vector<const uint64_t*> gk;
+    std::vector<uint32_t> gpos;
+    for (uint32_t o = 0; o < n_out; o++)
+        for (uint32_t g = 0; g < ng; g++)
+            if (gsteps[g] != 0) {
+                gs.push_back(gsteps[g]);
+                gk.push_back(gevk[g]);
+                gpos.push_back(o * ng + g);
+            }
+    uint64_t* vr = nullptr;
+    if (!gs.empty()) {
+        uint64_t* packed = (uint64_t*)ws_get(ctx, WS_SUM, gs.size() * ctw * 8);
+        vr = (uint64_t*)ws_get(ctx, WS_GROT, gs.size() * ctw * 8);
+        for (size_t r = 0; r < gs.size(); r++)
+            HIPX(hipMemcpyAsync(packed + r * ctw, v + (size_t)gpos[r] * ctw, ctw * 8, hipMemcpyDeviceToDevice, st));
+        rotate_list(ctx, packed, (uint32_t)gs.size(), l, gs.data(), gk.data(), vr, st);
+    }
+    uint64_t* dst = out;
+    if (do_rescale) dst = (uint64_t*)ws_get(ctx, WS_LIN, (size_t)n_out * ctw * 8);
+    size_t r = 0;
+    for (uint32_t o = 0; o < n_out; o++) {
+        std::vector<const uint64_t*> terms;
+        for (uint32_t g = 0; g < ng; g++)
+            terms.push_back(gsteps[g] == 0 ? v + ((size_t)o * ng + g) * ctw : vr + (r++) * ctw);
+        HIPX(launch_sum_list(ctx, terms.data(), (uint32_t)terms.size(), dst + (size_t)o * ctw, 2, l, st));
+    }
+    if (do_rescale) rescale(ctx, dst, 2 * n_out, l, out, st);
+}
+
+void bsgs_general(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* diags, uint32_t nb,
+                  const int64_t* bsteps, const uint64_t* const* bevk, uint32_t ng, const int64_t* gsteps,
+                  const uint64_t* const* gevk, uint64_t* out, hipStream_t st, uint32_t log_rep) {
+    bsgs_multi(ctx, &ct, 1, l, diags, nb, bsteps, bevk, ng, gsteps, gevk, 1, false, out, st, log_rep);
+}
+
+// Masked rotation pairs of one ciphertext (cyclic rotations inside blocks, assembled from two plain ones):
+//   out[s][t] = rescale( pt[s][t][0] (.) Rot_{lo_t}(ct) + pt[s][t][1] (.) Rot_{hi_t}(ct) )
+// all 2n rotations hoisted over one ModUp; pt [n_sets][n][2][l][N >> log_rep]; out [n_sets][n][2][l-1][N].
+void rotate_masked(Context& ctx, const uint64_t* ct, uint32_t l, uint32_t n, const int64_t* lo,
+                   const uint64_t* const* lo_evk, const int64_t* hi, const uint64_t* const* hi_evk, uint32_t n_sets,
+                   const uint64_t* pts, uint32_t log_rep, uint64_t* out, hipStream_t st) {
+    check_level(ctx, l);
+    if (l < 2 || n == 0 || n_sets == 0) throw std::invalid_argument("bad masked rotation shape");
+    const size_t ctw = (size_t)2 * l * W;
+    uint64_t* R = (uint64_t*)ws_get(ctx, WS_BABY, (size_t)2 * n * ctw * 8);
+    std::vector<int64_t> steps(lo, lo + n);
+    steps.insert(steps.end(), hi, hi + n);
+    std::vector<const uint64_t*> keys(lo_evk, lo_evk + n);
+    keys.insert(keys.end(), hi_evk, hi_evk + n);
+    // a zero step is the identity: rotate the others, copy the input for those
+    std::vector<int64_t> rs;
+    std::vector<const uint64_t*> rk;
+    std::vector<uint32_t> rpos;
+    for (uint32_t j = 0; j < 2 * n; j++) {
+        if (steps[j] == 0) {
+            HIPX(hipMemcpyAsync(R + j * ctw, ct, ctw * 8, hipMemcpyDeviceToDevice, st));
+        } else {
+            rs.push_back(steps[j]);
+            rk.push_back(keys[j]);
+            rpos.push_back(j);
         }
     }
     if (!rs.empty()) {
         uint64_t* tmp = (uint64_t*)ws_get(ctx, WS_SUM, rs.size() * ctw * 8);
         rotate_hoisted(ctx, ct, l, rs.data(), (uint32_t)rs.size(), rk.data(), tmp, st);
         for (size_t r = 0; r < rs.size(); r++)
-            HIPX(hipMemcpyAsync(baby + rpos[r] * ctw, tmp + r * ctw, ctw * 8, hipMemcpyDeviceToDevice, st));
+            HIPX(hipMemcpyAsync(R + (size_t)rpos[r] * ctw, tmp + r * ctw, ctw * 8, hipMemcpyDeviceToDevice, st));
     }
-    HIPX(launch_bsgs_mac(ctx, baby, diags, v, nb, nb * ng, ng, l, st));
-    std::vector<const uint64_t*> terms;
-    std::vector<int64_t> gs;
-    std::vector<const uint64_t*> gk;
-    std::vector<uint32_t> gpos;
-    for (uint32_t g = 0; g < ng; g++) {
-        if (gsteps[g] == 0) {
-            terms.push_back(v + g * ctw);
-        } else {
-            gs.push_back(gsteps[g]);
-            gk.push_back(gevk[g]);
-            gpos.push_back(g);
-        }
+    uint64_t* m = (uint64_t*)ws_get(ctx, WS_LIN, (size_t)n_sets * n * ctw * 8);
+    HIPX(launch_pair_mac(ctx, R, pts, m, n_sets, n, l, log_rep, st));
+    rescale(ctx, m, 2 * n_sets * n, l, out, st);
+}
+
+void mul_i(Context& ctx, const uint64_t* x, uint32_t n_polys, uint32_t l, int sign, uint64_t* out, hipStream_t st) {
+    check_level(ctx, l);
+    HIPX(launch_mul_i(ctx, x, out, n_polys, l, sign, st));
+}
+
+static uint64_t residue_of(long double v, uint64_t q) {
+    const bool neg = v < 0;
+    const unsigned __int128 x = (unsigned __int128)(neg ? -v : v);
+    const uint64_t r = (uint64_t)(x % q);
+    return neg ? (r ? q - r : 0) : r;
+}
+
+// Linear combination of ciphertext batches [B][2][l_t][N] (term t at level levels[t], scale scales_in[t]):
+//  integer mode: sum_t round(c_t) x_t + round(a * scale_out) at level lt (every term at lt), no rescale;
+//  scalar mode:  every term read at lt + 1 limbs, multiplied by round(c_t scale_out q_lt / scales_in[t]),
+//                round(a scale_out) q_lt added, then rescaled to lt: the result has scale scale_out.
+void lincomb(Context& ctx, uint32_t B, uint32_t n_terms, const uint64_t* const* x, const uint32_t* levels,
+             const double* coeffs, const double* scales_in, double scale_out, double add_const, uint32_t lt,
+             bool integer_mode, uint64_t* out, hipStream_t st) {
+    if (n_terms == 0 || n_terms > 8) throw std::invalid_argument("1..8 terms");
+    if (lt == 0 || lt > ctx.L) throw std::invalid_argument("target level out of range");
+    const uint32_t lo = integer_mode ? lt : lt + 1;
+    if (lo > ctx.L || lo > 40) throw std::invalid_argument("target level too high");
+    for (uint32_t t = 0; t < n_terms; t++) {
+        if (integer_mode ? levels[t] != lt : levels[t] < lo) throw std::invalid_argument("term level");
     }
-    if (!gs.empty()) {
-        // the giants to rotate must be contiguous: pack them
-        uint64_t* packed = (uint64_t*)ws_get(ctx, WS_SUM, gs.size() * ctw * 8);
-        for (size_t r = 0; r < gs.size(); r++)
-            HIPX(hipMemcpyAsync(packed + r * ctw, v + gpos[r] * ctw, ctw * 8, hipMemcpyDeviceToDevice, st));
-        rotate_list(ctx, packed, (uint32_t)gs.size(), l, gs.data(), gk.data(), vr, st);
-        for (size_t r = 0; r < gs.size(); r++) terms.push_back(vr + r * ctw);
+    std::vector<uint64_t> C((size_t)n_terms * lo), add(lo);
+    const long double qlt = (long double)ctx.moduli[integer_mode ? 0 : lt];
+    for (uint32_t t = 0; t < n_terms; t++) {
+        const long double c = integer_mode ? std::roundl((long double)coeffs[t])
+                                           : std::roundl((long double)coeffs[t] * scale_out * qlt / scales_in[t]);
+        for (uint32_t i = 0; i < lo; i++) C[(size_t)t * lo + i] = residue_of(c, ctx.moduli[i]);
     }
-    HIPX(launch_sum_list(ctx, terms.data(), (uint32_t)terms.size(), out, 2, l, st));
+    const long double a = std::roundl((long double)add_const * scale_out);
+    for (uint32_t i = 0; i < lo; i++) {
+        const uint64_t qi = ctx.moduli[i];
+        add[i] = integer_mode ? residue_of(a, qi) : mulmod_h(residue_of(a, qi), ctx.moduli[lt] % qi, qi);
+    }
+    std::vector<uint32_t> stride(levels, levels + n_terms);
+    if (integer_mode) {
+        HIPX(launch_lincomb(ctx, out, B, lo, n_terms, x, stride.data(), C.data(), add_const != 0.0 ? add.data() : nullptr,
+                            st));
+        return;
+    }
+    uint64_t* tmp = (uint64_t*)ws_get(ctx, WS_LIN, (size_t)B * 2 * lo * W * 8);
+    HIPX(launch_lincomb(ctx, tmp, B, lo, n_terms, x, stride.data(), C.data(), add_const != 0.0 ? add.data() : nullptr,
+                        st));
+    rescale(ctx, tmp, 2 * B, lo, out, st);
 }
 
 void add(Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys, uint32_t l,

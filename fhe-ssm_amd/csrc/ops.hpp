@@ -19,6 +19,8 @@ enum WsSlot : uint32_t {
     WS_GIANT,
     WS_GROT,
     WS_SUM,
+    WS_LIN,
+    WS_PTAB,
     WS_COUNT
 };
 
@@ -49,15 +51,30 @@ void automorph_ks_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l
                        const uint64_t* const* evk, uint64_t* out, hipStream_t st);
 void bsgs_general(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* diags, uint32_t nb,
                   const int64_t* bsteps, const uint64_t* const* bevk, uint32_t ng, const int64_t* gsteps,
-                  const uint64_t* const* gevk, uint64_t* out, hipStream_t st);
+                  const uint64_t* const* gevk, uint64_t* out, hipStream_t st, uint32_t log_rep = 0);
 void rotate_hoisted(Context& ctx, const uint64_t* ct, uint32_t l, const int64_t* steps, uint32_t n,
                     const uint64_t* const* evk, uint64_t* out, hipStream_t st);
+void rotate_hoisted_ext(Context& ctx, const uint64_t* ct, const uint64_t* ext, uint32_t l, const int64_t* steps,
+                        uint32_t n, const uint64_t* const* evk, uint64_t* out, hipStream_t st);
+void hmult_sum(Context& ctx, const uint64_t* const* pairs, uint32_t np, uint32_t B, uint32_t l, const uint64_t* evk,
+               uint64_t* out, bool do_rescale, hipStream_t st);
+void bsgs_multi(Context& ctx, const uint64_t* const* in, uint32_t n_in, uint32_t l, const uint64_t* diags,
+                uint32_t nb, const int64_t* bsteps, const uint64_t* const* bevk, uint32_t ng, const int64_t* gsteps,
+                const uint64_t* const* gevk, uint32_t n_out, bool do_rescale, uint64_t* out, hipStream_t st,
+                uint32_t log_rep);
+void rotate_masked(Context& ctx, const uint64_t* ct, uint32_t l, uint32_t n, const int64_t* lo,
+                   const uint64_t* const* lo_evk, const int64_t* hi, const uint64_t* const* hi_evk, uint32_t n_sets,
+                   const uint64_t* pts, uint32_t log_rep, uint64_t* out, hipStream_t st);
+void mul_i(Context& ctx, const uint64_t* x, uint32_t n_polys, uint32_t l, int sign, uint64_t* out, hipStream_t st);
 void mul_plain(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const uint64_t* pt, bool pt_shared,
-               uint64_t* out, hipStream_t st);
+               uint64_t* out, hipStream_t st, uint32_t log_rep = 0);
 void add_plain(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const uint64_t* pt, bool pt_shared,
                uint64_t* out, hipStream_t st);
 void bsgs_matvec(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* diags, uint32_t n_diag, uint32_t bs,
                  const uint64_t* const* baby_evk, const uint64_t* const* giant_evk, uint64_t* out, hipStream_t st);
+void lincomb(Context& ctx, uint32_t B, uint32_t n_terms, const uint64_t* const* x, const uint32_t* levels,
+             const double* coeffs, const double* scales_in, double scale_out, double add_const, uint32_t lt,
+             bool integer_mode, uint64_t* out, hipStream_t st);
 void automorph(Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n_polys, uint32_t l, uint32_t g,
                hipStream_t st);
 

@@ -6,6 +6,8 @@
 // walked in registers, residues canonical in [0, q) on every store.  Products that are not by a
 // per-limb constant accumulate in 128 bits and reduce once (Barrett, mu = floor(2^128 / q)); products
 // by a per-limb constant use Shoup with a precomputed companion.
+#include <algorithm>
+
 #include "engine.hpp"
 #include "modarith.hpp"
 
@@ -51,6 +53,33 @@ __global__ __launch_bounds__(256) void k_tensor(const uint64_t* __restrict__ a, 
     d01[o + P] = reduce_u128(s1, br);
     const uint64_t v2 = reduce_u128(s2, br);
     d2[(size_t)c * P + (size_t)t * kN + k] = v2;
+    if (ta.d2e) ta.d2e[c * ta.d2e_bstride + (size_t)ta.ext_off[t] * kN + k] = v2;
+}
+
+// Sum of np tensor products per batch item: tab[(c np + j) 2 + 0/1] point at ciphertexts [2][l][N];
+// d01/d2 as in k_tensor.  The 128-bit sums hold up to 2 np products below 2^120: np <= 64.
+__global__ __launch_bounds__(256) void k_tensor_sum(const uint64_t* const* __restrict__ tab, uint32_t np,
+                                                    uint64_t* __restrict__ d01, uint64_t* __restrict__ d2,
+                                                    TensorArgs ta, const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t t = blockIdx.y, c = blockIdx.z;
+    const Barrett br = barrett_of(primes[t]);
+    const size_t P = (size_t)ta.l * kN, w = (size_t)t * kN + k;
+    U128 s0{0, 0}, s1{0, 0}, s2{0, 0};
+    for (uint32_t j = 0; j < np; j++) {
+        const uint64_t* a = tab[((size_t)c * np + j) * 2];
+        const uint64_t* b = tab[((size_t)c * np + j) * 2 + 1];
+        const uint64_t a0 = a[w], a1 = a[P + w], b0 = b[w], b1 = b[P + w];
+        mac128(s0, a0, b0);
+        mac128(s1, a0, b1);
+        mac128(s1, a1, b0);
+        mac128(s2, a1, b1);
+    }
+    const size_t o = (size_t)c * 2 * P + w;
+    d01[o] = reduce_u128(s0, br);
+    d01[o + P] = reduce_u128(s1, br);
+    const uint64_t v2 = reduce_u128(s2, br);
+    d2[(size_t)c * P + w] = v2;
     if (ta.d2e) ta.d2e[c * ta.d2e_bstride + (size_t)ta.ext_off[t] * kN + k] = v2;
 }
 
@@ -260,16 +289,22 @@ __global__ __launch_bounds__(256) void k_automorph_list(const uint64_t* __restri
 // A workgroup owns 64 coefficients of one limb: it stages those words of every baby in LDS once, then its
 // 4 wave-rows take the giant steps g = row, row + 4, ...; every diagonal word is read exactly once and each
 // wave reads 64 consecutive words (512 B) per diagonal.
-constexpr int kMaxBaby = 32;
+constexpr int kMaxBaby = 64;
 constexpr int kMacCoef = 64;
 constexpr int kMacRows = 4;
 
+// log_rep > 0: the diagonals are compressed periodic plaintexts, [n_diag][l][N >> log_rep], whose
+// evaluation-form word k is comp[k >> log_rep] (the reference's store expansion, gpu_real_model.cu:145-155).
+// Babies j0 .. j0 + nb - 1 of a list of nb_total are taken (diagonal g * nb_total + j, zero from n_diag on);
+// acc != 0 adds the result to what out holds (the MAC over more babies than fit in LDS runs in baby chunks).
 __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(const uint64_t* __restrict__ baby,
                                                                   const uint64_t* __restrict__ diag,
                                                                   uint64_t* __restrict__ out, uint32_t nb,
-                                                                  uint32_t n_diag, uint32_t ng, uint32_t l,
+                                                                  uint32_t nb_total, uint32_t j0, uint32_t ng,
+                                                                  uint32_t n_diag, uint32_t l, uint32_t log_rep,
+                                                                  uint32_t acc,
                                                                   const PrimeInfo* __restrict__ primes) {
-    __shared__ uint64_t sb[kMaxBaby * 2 * kMacCoef];
+    extern __shared__ uint64_t sb[];
     const uint32_t kk = threadIdx.x & (kMacCoef - 1), row = threadIdx.x / kMacCoef;
     const uint32_t k = blockIdx.x * kMacCoef + kk;
     const uint32_t i = blockIdx.y;
@@ -277,32 +312,59 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(const uint64_t*
     const size_t P = (size_t)l * kN, off = (size_t)i * kN + k;
     for (uint32_t jp = row; jp < 2 * nb; jp += kMacRows) {  // jp = 2 j + poly
         const uint32_t j = jp >> 1, p = jp & 1;
-        sb[jp * kMacCoef + kk] = baby[(size_t)j * 2 * P + p * P + off];
+        sb[jp * kMacCoef + kk] = baby[(size_t)(j0 + j) * 2 * P + p * P + off];
     }
     __syncthreads();
+    const size_t Pd = (size_t)l * (kN >> log_rep);
     for (uint32_t g = row; g < ng; g += kMacRows) {
         U128 s0{0, 0}, s1{0, 0};
-        const uint32_t jn = min(nb, n_diag - g * nb);
-        const uint64_t* dg = diag + (size_t)g * nb * P + off;
+        const uint64_t* dg = diag + ((size_t)g * nb_total + j0) * Pd + (size_t)i * (kN >> log_rep) + (k >> log_rep);
+        // diagonals past n_diag (a short last giant step) are zero
+        const int64_t rem = (int64_t)n_diag - (int64_t)g * nb_total - j0;
+        const uint32_t jn = rem <= 0 ? 0u : (uint32_t)min<int64_t>(rem, nb);
         for (uint32_t j = 0; j < jn; j++) {
-            const uint64_t m = dg[(size_t)j * P];
+            const uint64_t m = dg[(size_t)j * Pd];
             mac128(s0, sb[(2 * j) * kMacCoef + kk], m);
             mac128(s1, sb[(2 * j + 1) * kMacCoef + kk], m);
         }
-        out[(size_t)g * 2 * P + off] = reduce_u128(s0, br);
-        out[(size_t)g * 2 * P + P + off] = reduce_u128(s1, br);
+        uint64_t r0 = reduce_u128(s0, br), r1 = reduce_u128(s1, br);
+        if (acc) {
+            r0 = add_mod(r0, out[(size_t)g * 2 * P + off], br.q);
+            r1 = add_mod(r1, out[(size_t)g * 2 * P + P + off], br.q);
+        }
+        out[(size_t)g * 2 * P + off] = r0;
+        out[(size_t)g * 2 * P + P + off] = r1;
     }
 }
 
-// ct (.) pt on both polys: ct [B][2][l][N], pt [B or 1][l][N] (pt_bstride 0 = shared plaintext)
+// Masked pairs: out[s][t] = pt[s][t][0] (.) R[t] + pt[s][t][1] (.) R[n + t] on both polys, with
+// R [2n][2][l][N] and pt [n_sets][n][2][l][N >> log_rep] compressed periodic plaintexts.
+__global__ __launch_bounds__(256) void k_pair_mac(const uint64_t* __restrict__ R, const uint64_t* __restrict__ pt,
+                                                  uint64_t* __restrict__ out, uint32_t n, uint32_t l,
+                                                  uint32_t log_rep, const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t i = blockIdx.y, z = blockIdx.z;  // z = (s n + t) 2 + poly
+    const uint32_t poly = z & 1, st = z >> 1, t = st % n;
+    const Barrett br = barrett_of(primes[i]);
+    const size_t P = (size_t)l * kN, Pc = (size_t)l * (kN >> log_rep);
+    const size_t w = (size_t)poly * P + (size_t)i * kN + k;
+    const uint64_t* p = pt + (size_t)st * 2 * Pc + (size_t)i * (kN >> log_rep) + (k >> log_rep);
+    U128 s{0, 0};
+    mac128(s, R[(size_t)t * 2 * P + w], p[0]);
+    mac128(s, R[(size_t)(n + t) * 2 * P + w], p[Pc]);
+    out[(size_t)st * 2 * P + w] = reduce_u128(s, br);
+}
+
+// ct (.) pt on both polys: ct [B][2][l][N], pt [B or 1][l][N >> log_rep] (pt_bstride 0 = shared plaintext;
+// log_rep > 0 = compressed periodic plaintext, word k of the evaluation form is comp[k >> log_rep])
 __global__ __launch_bounds__(256) void k_mul_plain(const uint64_t* __restrict__ ct, const uint64_t* __restrict__ pt,
                                                    uint64_t* __restrict__ out, uint32_t l, uint64_t pt_bstride,
-                                                   const PrimeInfo* __restrict__ primes) {
+                                                   uint32_t log_rep, const PrimeInfo* __restrict__ primes) {
     const uint32_t k = blockIdx.x * 256 + threadIdx.x;
     const uint32_t i = blockIdx.y, pc = blockIdx.z;
     const Barrett br = barrett_of(primes[i]);
     const size_t o = ((size_t)pc * l + i) * kN + k;
-    const uint64_t m = pt[(size_t)(pc >> 1) * pt_bstride + (size_t)i * kN + k];
+    const uint64_t m = pt[(size_t)(pc >> 1) * pt_bstride + (size_t)i * (kN >> log_rep) + (k >> log_rep)];
     out[o] = mul_mod(ct[o], m, br);
 }
 
@@ -510,20 +572,54 @@ hipError_t launch_automorph_list(const Context& ctx, const uint64_t* in, uint64_
 }
 
 hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* baby, const uint64_t* diag, uint64_t* out, uint32_t nb,
-                           uint32_t n_diag, uint32_t ng, uint32_t l, hipStream_t st) {
-    if (nb == 0 || nb > (uint32_t)kMaxBaby) return hipErrorInvalidValue;
-    const double bytes = ((double)nb * 2 * l + (double)n_diag * l + (double)ng * 2 * l) * kN * 8;
-    const int pi = prof_begin(ctx, "bsgs_mac", bytes, st);
-    hipLaunchKernelGGL(k_bsgs_mac, dim3(kN / kMacCoef, l), dim3(kMacCoef * kMacRows), 0, st, baby, diag, out, nb,
-                       n_diag, ng, l, ctx.d_primes);
+                           uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st) {
+    if (nb == 0 || log_rep > 6 || n_diag > nb * ng) return hipErrorInvalidValue;
+    const double bytes = ((double)nb * 2 * l + (double)n_diag * l / (1u << log_rep) + (double)ng * 2 * l) * kN * 8;
+    const int pi = prof_begin(ctx, log_rep ? "bsgs_mac_periodic" : "bsgs_mac", bytes, st);
+    for (uint32_t j0 = 0; j0 < nb; j0 += kMaxBaby) {
+        const uint32_t nbc = std::min<uint32_t>(kMaxBaby, nb - j0);
+        hipLaunchKernelGGL(k_bsgs_mac, dim3(kN / kMacCoef, l), dim3(kMacCoef * kMacRows),
+                           (size_t)nbc * 2 * kMacCoef * 8, st, baby, diag, out, nbc, nb, j0, ng, n_diag, l,
+                           log_rep, j0 ? 1u : 0u, ctx.d_primes);
+    }
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_pair_mac(const Context& ctx, const uint64_t* R, const uint64_t* pt, uint64_t* out, uint32_t n_sets,
+                           uint32_t n, uint32_t l, uint32_t log_rep, hipStream_t st) {
+    if (log_rep > 6 || n == 0) return hipErrorInvalidValue;
+    const double bytes = ((double)2 * n * 2 * l + (double)n_sets * n * 2 * l / (1u << log_rep) +
+                          (double)n_sets * n * 2 * l) * kN * 8;
+    const int pi = prof_begin(ctx, "pair_mac", bytes, st);
+    hipLaunchKernelGGL(k_pair_mac, dim3(kN / 256, l, n_sets * n * 2), dim3(256), 0, st, R, pt, out, n, l, log_rep,
+                       ctx.d_primes);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_tensor_sum(const Context& ctx, const uint64_t* const* d_tab, uint32_t np, uint64_t* d01,
+                             uint64_t* d2, uint32_t B, uint32_t l, uint64_t* d2e, uint64_t d2e_bstride,
+                             const uint32_t* ext_off, hipStream_t st) {
+    if (np == 0 || np > 64) return hipErrorInvalidValue;
+    TensorArgs ta{};
+    ta.l = l;
+    ta.B = B;
+    ta.d2e = d2e;
+    ta.d2e_bstride = d2e_bstride;
+    if (d2e)
+        for (uint32_t t = 0; t < l; t++) ta.ext_off[t] = ext_off[t];
+    const int pi = prof_begin(ctx, "tensor_sum", (double)B * l * (4.0 * np + 3 + (d2e ? 1 : 0)) * kN * 8, st);
+    hipLaunchKernelGGL(k_tensor_sum, dim3(kN / 256, l, B), dim3(256), 0, st, d_tab, np, d01, d2, ta, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
 
 hipError_t launch_mul_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
-                            uint32_t l, uint64_t pt_bstride, hipStream_t st) {
-    const int pi = prof_begin(ctx, "mul_plain", ((double)B * 4 * l + (pt_bstride ? B : 1) * (double)l) * kN * 8, st);
-    hipLaunchKernelGGL(k_mul_plain, dim3(kN / 256, l, 2 * B), dim3(256), 0, st, ct, pt, out, l, pt_bstride,
+                            uint32_t l, uint64_t pt_bstride, uint32_t log_rep, hipStream_t st) {
+    const int pi = prof_begin(ctx, "mul_plain",
+                              ((double)B * 4 * l + (pt_bstride ? B : 1) * (double)l / (1u << log_rep)) * kN * 8, st);
+    hipLaunchKernelGGL(k_mul_plain, dim3(kN / 256, l, 2 * B), dim3(256), 0, st, ct, pt, out, l, pt_bstride, log_rep,
                        ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();

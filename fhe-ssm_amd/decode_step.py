@@ -1,0 +1,448 @@
+"""The config-5 encrypted decode step: the caller that drives the engine's C ABI the way the reference's
+served step drives FIDESlib (hpc_gpu_port/gpu_real_model.cu:4674-5300: per layer rmsnorm, token shift,
+matvecBatch with shared babies, scan, gate, output projection, residual, channel mix; refresh/boot policy
+:2535-2599).  The model itself is described in rwkv_model.py.
+
+The step is written against a small backend interface (Backend below): the level/scale rules live here,
+the primitives in the backend.  HEBackend runs them on the GPU through ckks.py; the tests also run the same
+plan on a slot-vector simulator to check the packing algebra without encryption.
+
+Level rules (OpenFHE FLEXIBLEAUTO semantics, gpu_real_model.cu:1156): every ciphertext at level l carries
+the canonical scale S(l) of the bootstrapping plan (S(l-1) = S(l)^2 / q_{l-1}), except transiently the
+unpacked state (2 S(l)).  An operand above the level of its partner is brought down by a scalar
+multiplication that lands on the canonical scale (one rescale); products then land on S(l-1).
+Plaintexts applied at level l are encoded at scale S(l), which keeps the product canonical.
+
+Refresh policy: the residual stream is bootstrapped before the time mix and before the channel mix when
+fewer levels remain than the block needs; the carried WKV state is bootstrapped once per layer, packed
+two per ciphertext (D_t + i D_{t+32}) and unpacked with one conjugation.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+import rwkv_model as M
+
+# levels the two blocks consume from their input (checked by the plan at run time)
+TIME_MIX_DEPTH = 14
+CHANNEL_MIX_DEPTH = 9
+OUTPUT_DEPTH = 6
+
+
+class Backend:
+    """Level/scale rules over backend primitives.  Ciphertext handles expose .B (batch), .level, .scale."""
+
+    # -- primitives a backend provides ------------------------------------------------------------
+    def S(self, level):  # canonical scale
+        raise NotImplementedError
+
+    def _adjust(self, a, lt, coeff=1.0, const=0.0):  # scalar mode: a at level >= lt + 1 -> lt, canonical
+        raise NotImplementedError
+
+    def _lin_scalar(self, terms, coeffs, const, lt):
+        raise NotImplementedError
+
+    def _lin_int(self, terms, coeffs):  # same level and scale, integer coefficients, no level
+        raise NotImplementedError
+
+    def _mult_sum(self, pairs, level):  # pairs[b] = [(ct, idx, ct, idx), ...], all operands at level
+        raise NotImplementedError
+
+    # -- rules -------------------------------------------------------------------------------------
+    def at(self, a, lt):
+        """a at level lt with the canonical scale"""
+        if a.level == lt and self._canonical(a):
+            return a
+        if a.level < lt + 1:
+            raise ValueError(f"cannot bring a level-{a.level} ciphertext to level {lt}")
+        return self._adjust(a, lt)
+
+    def _canonical(self, a):
+        return abs(a.scale / self.S(a.level) - 1.0) < 1e-9
+
+    def add(self, a, b, sign=1):
+        m = min(a.level, b.level)
+        a2, b2 = self._align_pair(a, b, m)
+        return self._lin_int([a2, b2], [1, sign])
+
+    def _align_pair(self, a, b, m):
+        a2 = a if (a.level == m and (self._canonical(a) or b.level == m)) else self.at(a, m)
+        b2 = b if (b.level == m and (self._canonical(b) or a.level == m)) else self.at(b, m)
+        if abs(a2.scale / b2.scale - 1.0) > 1e-9:
+            # same level, different scales: both go down one level onto the canonical scale
+            a2, b2 = self.at(a2, m - 1), self.at(b2, m - 1)
+        return a2, b2
+
+    def lin(self, terms, coeffs, const=0.0, lt=None):
+        """sum_t c_t x_t + const, scalar coefficients: one level below the lowest term (or lt)"""
+        lo = min(t.level for t in terms)
+        lt = lo - 1 if lt is None else lt
+        return self._lin_scalar(terms, coeffs, const, lt)
+
+    def mul(self, a, b):
+        """a (.) b with relinearization and rescale; a batch of 1 broadcasts against a batch"""
+        B = max(a.B, b.B)
+        m = min(a.level, b.level)
+        a2 = self.at(a, m) if a.level > m else a
+        b2 = self.at(b, m) if b.level > m else b
+        pairs = [[(a2, i % a2.B, b2, i % b2.B)] for i in range(B)]
+        return self._mult_sum(pairs, m)
+
+    def mult_sum(self, pairs):
+        """pairs[b] = [(ct, idx, ct, idx), ...] summed then relinearized and rescaled; operands are brought
+        to the lowest level among them first"""
+        m = min(min(p[0].level, p[2].level) for item in pairs for p in item)
+        cache = {}
+
+        def lower(c):
+            key = id(c)
+            if key not in cache:
+                cache[key] = c if (c.level == m and self._canonical(c)) else self.at(c, m)
+            return cache[key]
+
+        pairs2 = [[(lower(a), i, lower(b), j) for (a, i, b, j) in item] for item in pairs]
+        return self._mult_sum(pairs2, m)
+
+    def poly3(self, z, c):
+        """c0 + c1 z + c2 z^2 + c3 z^3 in depth 2 (z^2 (c3 z + c2) + (c1 z + c0))"""
+        m = z.level
+        z2 = self.mul(z, z)
+        u = self.lin([z], [c[3]], c[2], lt=m - 1)
+        t = self.mul(z2, u)
+        v = self.lin([z], [c[1]], c[0], lt=m - 2)
+        return self.add(t, v)
+
+
+class DecodeStep:
+    """One encrypted decode step over all layers; the WKV state and token-shift carries persist between
+    calls (the reference's stateful serve loop, gpu_real_model.cu:4674-4720)."""
+
+    def __init__(self, be: Backend, weights: dict, n_layers: int | None = None):
+        self.be = be
+        self.W = weights
+        self.n_layers = len(weights["layers"]) if n_layers is None else n_layers
+        self.pt = {}        # (name, level) -> backend plaintext handle
+        self.state = None   # per layer: {"D": ct batch of 64, "xp_t": ct, "xp_c": ct}
+        self.stats = {"bootstraps": 0}
+
+    # -- plaintexts (encoded on first use at the level they are applied) ----------------------------
+    def _vec_pt(self, name, level, vecs):
+        key = (name, level)
+        if key not in self.pt:
+            self.pt[key] = self.be.encode_periodic(np.asarray(vecs, dtype=np.float64).reshape(-1, M.DPAD), level)
+        return self.pt[key]
+
+    def _mv_pt(self, name, level, blocks_fn):
+        key = (name, level)
+        if key not in self.pt:
+            blocks = blocks_fn()
+            self.pt[key] = self.be.encode_matvec(M.matvec_diagonals(blocks), level)
+        return self.pt[key]
+
+    # -- blocks --------------------------------------------------------------------------------------
+    def _norm(self, x, pcoef, tag):
+        """x * p(mean(x^2)) per lane"""
+        be = self.be
+        s = be.mul(x, x)
+        for k in M.NORM_UP:
+            s = be.add(s, be.rotate(s, k))
+        s = be.mul_pt(s, self._vec_pt("lane_start", s.level, M.lane_start_mask(1.0 / M.D)))
+        for k in M.NORM_DOWN:
+            s = be.add(s, be.rotate(s, k))
+        n = be.poly3(s, pcoef)
+        return be.mul(x, n)
+
+    def _refresh(self, x, need):
+        if x.level - 1 >= need:
+            return x
+        self.stats["bootstraps"] += x.B
+        return self.be.bootstrap(x)
+
+    def _time_mix(self, li, x, st):
+        be, L = self.be, self.W["layers"][li]
+        x = self._refresh(x, TIME_MIX_DEPTH)
+        xn = self._norm(x, L["p_n1"], "n1")
+        xp = st["xp_t"]
+        lv = min(xn.level, xp.level)
+
+        def tm_blocks():
+            out = []
+            for m in M.MIX_NAMES:
+                Wm = L["W_" + m]
+                out.append([Wm * (L["g1"] * (1 - L["mu_" + m]))[None, :], Wm * (L["g1"] * L["mu_" + m])[None, :]])
+            return out
+
+        proj = be.matvec([be.at(xn, lv), be.at(xp, lv)], self._mv_pt(f"tm{li}", lv, tm_blocks))
+        r, k, v, zw, za, zg = (be.item(proj, i) for i in range(6))
+        w = be.poly3(zw, L["p_w"])
+        a = be.poly3(za, L["p_a"])
+        g = be.poly3(zg, L["p_g"])
+        masks = M.wkv_masks()
+        masks_eta = M.wkv_masks(L["eta"])
+        KK = be.rotate_masked(k, self._vec_pt(f"mask_k{li}", k.level, np.concatenate([masks, masks_eta])), 2)
+        K_t, Kh_t = be.slice(KK, 0, 64), be.slice(KK, 64, 128)
+        R_t = be.rotate_masked(r, self._vec_pt("mask", r.level, masks), 1)
+        W_t = be.rotate_masked(w, self._vec_pt("mask", w.level, masks), 1)
+        ka = be.mul(k, a)
+        B_t = be.rotate_masked(ka, self._vec_pt(f"mask_eta{li}", ka.level, masks_eta), 1)
+        D = st["D"]
+        T = M.WKV_T
+        sa = be.mult_sum([[(D, t, Kh_t, t) for t in range(T)]])
+        nsa = be.at_neg(sa, min(B_t.level, W_t.level - 1, sa.level - 1))
+        Dn = be.mult_sum([[(D, t, W_t, t), (nsa, 0, B_t, t), (v, 0, K_t, t)] for t in range(T)])
+        y = be.mult_sum([[(Dn, t, R_t, t) for t in range(T)]])
+        yg = be.mul(y, g)
+        o = be.matvec([yg], self._mv_pt(f"wo{li}", yg.level, lambda: [[L["W_o"]]]))
+        st["xp_t"] = xn
+        st["Dn"] = Dn
+        return be.add(x, o)
+
+    def _channel_mix(self, li, x, st):
+        be, L = self.be, self.W["layers"][li]
+        x = self._refresh(x, CHANNEL_MIX_DEPTH)
+        xn2 = self._norm(x, L["p_n2"], "n2")
+        xp = st["xp_c"]
+        lv = min(xn2.level, xp.level)
+
+        def ck_blocks():
+            a = (L["g2"] * (1 - L["mu_c"]))[None, :]
+            b = (L["g2"] * L["mu_c"])[None, :]
+            return [[L["W_ck"][o * M.D:(o + 1) * M.D] * a, L["W_ck"][o * M.D:(o + 1) * M.D] * b] for o in range(4)]
+
+        hs = be.matvec([be.at(xn2, lv), be.at(xp, lv)], self._mv_pt(f"ck{li}", lv, ck_blocks))
+        h = be.poly3(hs, L["p_h"])
+        f = be.matvec([be.item(h, i) for i in range(4)],
+                      self._mv_pt(f"cv{li}", h.level, lambda: [[L["W_cv"][:, i * M.D:(i + 1) * M.D] for i in range(4)]]))
+        st["xp_c"] = xn2
+        return be.add(x, f)
+
+    def _refresh_state(self, st):
+        """bootstrap the new state once: pack D_t + i D_{t+32}, bootstrap 32, unpack with one conjugation"""
+        be = self.be
+        Dn = st.pop("Dn")
+        h = M.WKV_T // 2
+        lo, hi = be.slice(Dn, 0, h), be.slice(Dn, h, 2 * h)
+        packed = be.add(lo, be.mul_i(hi, 1))
+        self.stats["bootstraps"] += packed.B
+        P = be.bootstrap(packed)
+        C = be.conj(P)
+        re2 = be.add(P, C)                 # 2 Re
+        im2 = be.mul_i(be.add(C, P, -1), 1)  # i (conj - P) = 2 Im
+        st["D"] = be.halve(be.concat([re2, im2]))  # the sums hold 2 D_t: declared at twice the scale
+
+    def cold_state(self):
+        be = self.be
+        lt = be.top_level
+        return [{"D": be.zeros(M.WKV_T, lt), "xp_t": be.zeros(1, lt), "xp_c": be.zeros(1, lt)}
+                for _ in range(self.n_layers)]
+
+    def __call__(self, x):
+        """x: ciphertext of the lanes' embeddings; returns the ciphertext of the output-normed hidden state"""
+        if self.state is None:
+            self.state = self.cold_state()
+        for li in range(self.n_layers):
+            st = self.state[li]
+            x = self._time_mix(li, x, st)
+            self._refresh_state(st)
+            x = self._channel_mix(li, x, st)
+        x = self._refresh(x, OUTPUT_DEPTH)
+        xo = self._norm(x, self.W["p_o"], "out")
+        return self.be.mul_pt(xo, self._vec_pt("g_o", xo.level, M.periodic(self.W["g_o"])))
+
+
+# ======================================================================================== GPU backend
+class HECt:
+    __slots__ = ("buf", "off", "B", "level", "scale", "_pool")
+
+    def __init__(self, buf, B, level, scale, off=0, pool=None):
+        self.buf, self.B, self.level, self.scale, self.off, self._pool = buf, B, level, scale, off, pool
+
+    def ptr(self, b=0):
+        return self.buf.ptr + self.off + b * 2 * self.level * HEBackend.N * 8
+
+    @property
+    def nbytes(self):
+        return self.B * 2 * self.level * HEBackend.N * 8
+
+    def __del__(self):
+        if self._pool is not None and self.off == 0:
+            self._pool.put(self.buf)
+
+
+class _Pool:
+    """free lists of device buffers by size (a decode step allocates the same shapes every layer)"""
+
+    def __init__(self, ckks):
+        self.ckks = ckks
+        self.free = {}
+
+    def get(self, nbytes):
+        lst = self.free.get(nbytes)
+        if lst:
+            return lst.pop()
+        return self.ckks.DeviceBuffer(nbytes)
+
+    def put(self, buf):
+        self.free.setdefault(buf.nbytes, []).append(buf)
+
+
+class HEBackend(Backend):
+    """Decode-step primitives on the GPU engine (through ckks.py and the C ABI)."""
+    N = 1 << 16
+
+    def __init__(self, ckks, ctx, boot, in_scale, relin, conj, keys: dict):
+        self.ckks, self.ctx, self.boot = ckks, ctx, boot
+        self.relin, self.conj_key, self.keys = relin, conj, keys
+        self.top_level = boot.out_level
+        self.pool = _Pool(ckks)
+        self._S = {l: boot.scale(l) for l in range(1, boot.out_level + 1)}
+        self.in_scale = in_scale
+        self.moduli = ctx.moduli
+        self.boot_keys = {s: keys[s] for s in boot.steps}
+
+    def S(self, level):
+        return self._S[level]
+
+    def _new(self, B, level, scale):
+        return HECt(self.pool.get(B * 2 * level * self.N * 8), B, level, scale, pool=self.pool)
+
+    # -- client side ---------------------------------------------------------------------------------
+    def encrypt(self, sk, slots, level, seed=b"x" * 32, index=0):
+        pt = self.ckks.DeviceBuffer(level * self.N * 8)
+        self.ctx.encode(slots, level, self.S(level), pt.ptr)
+        ct = self._new(1, level, self.S(level))
+        self.ctx.encrypt(sk, pt.ptr, level, seed, index, ct.ptr())
+        return ct
+
+    def decrypt(self, sk, ct, b=0):
+        return self.ctx.decrypt(sk, ct.ptr(b), ct.level, ct.scale, 1 << 15, complex_out=True)
+
+    # -- plaintexts ----------------------------------------------------------------------------------
+    def encode_periodic(self, vecs, level):
+        vecs = np.atleast_2d(vecs)
+        n = vecs.shape[0]
+        buf = self.ckks.DeviceBuffer(n * level * (self.N >> M.LOG_REP) * 8)
+        self.ctx.encode_periodic(vecs, level, self.S(level), buf.ptr)
+        return buf
+
+    def encode_matvec(self, diags, level):
+        n_out, ng, nbt = diags.shape[:3]
+        flat = diags.reshape(-1, M.DPAD)
+        buf = self.ckks.DeviceBuffer(flat.shape[0] * level * (self.N >> M.LOG_REP) * 8)
+        step = 4096
+        per = level * (self.N >> M.LOG_REP) * 8
+        for s in range(0, flat.shape[0], step):
+            chunk = flat[s:s + step]
+            self.ctx.encode_periodic(chunk, level, self.S(level), buf.ptr + s * per)
+        return {"buf": buf, "n_out": n_out, "ng": ng, "n_in": nbt // M.MV_NB}
+
+    # -- ciphertext bookkeeping ----------------------------------------------------------------------
+    def zeros(self, B, level):
+        ct = self._new(B, level, self.S(level))
+        ct.buf.upload(np.zeros(ct.nbytes // 8, dtype=np.uint64))
+        return ct
+
+    def item(self, a, i):
+        return HECt(a.buf, 1, a.level, a.scale, off=a.off + i * 2 * a.level * self.N * 8)
+
+    def slice(self, a, i0, i1):
+        return HECt(a.buf, i1 - i0, a.level, a.scale, off=a.off + i0 * 2 * a.level * self.N * 8)
+
+    def concat(self, parts):
+        lv, sc = parts[0].level, parts[0].scale
+        out = self._new(sum(p.B for p in parts), lv, sc)
+        o = 0
+        for p in parts:
+            assert p.level == lv and p.scale == sc
+            self.ctx.eval_lincomb(p.B, [p.ptr()], [lv], [1.0], None, sc, 0.0, lv, True, out.ptr(o))
+            o += p.B
+        return out
+
+    def halve(self, a):
+        """the same ciphertext declared at twice the scale (the value halves): no arithmetic"""
+        a.scale *= 2.0
+        return a
+
+    # -- primitives ----------------------------------------------------------------------------------
+    def _adjust(self, a, lt, coeff=1.0, const=0.0):
+        out = self._new(a.B, lt, self.S(lt))
+        self.ctx.eval_lincomb(a.B, [a.ptr()], [a.level], [coeff], [a.scale], self.S(lt), const, lt, False,
+                              out.ptr())
+        return out
+
+    def at_neg(self, a, lt):
+        return self._adjust(a, lt, -1.0)
+
+    def _lin_scalar(self, terms, coeffs, const, lt):
+        B = terms[0].B
+        out = self._new(B, lt, self.S(lt))
+        self.ctx.eval_lincomb(B, [t.ptr() for t in terms], [t.level for t in terms], list(coeffs),
+                              [t.scale for t in terms], self.S(lt), const, lt, False, out.ptr())
+        return out
+
+    def _lin_int(self, terms, coeffs):
+        B, lv, sc = terms[0].B, terms[0].level, terms[0].scale
+        out = self._new(B, lv, sc)
+        self.ctx.eval_lincomb(B, [t.ptr() for t in terms], [lv] * len(terms), [float(c) for c in coeffs], None, sc,
+                              0.0, lv, True, out.ptr())
+        return out
+
+    def _mult_sum(self, pairs, level):
+        B = len(pairs)
+        a0, _, b0, _ = pairs[0][0]
+        scale = a0.scale * b0.scale / self.moduli[level - 1]
+        out = self._new(B, level - 1, scale)
+        ptrs = [[(a.ptr(i), b.ptr(j)) for (a, i, b, j) in item] for item in pairs]
+        self.ctx.eval_mult_sum(ptrs, level, self.relin, out.ptr(), rescale=True)
+        return out
+
+    def rotate(self, a, k):
+        out = self._new(a.B, a.level, a.scale)
+        self.ctx.eval_rotate(a.ptr(), a.B, a.level, k, self.keys[k], out.ptr())
+        return out
+
+    def mul_pt(self, a, pt):
+        tmp = self._new(a.B, a.level, a.scale)
+        self.ctx.eval_mult_plain_ex(a.ptr(), a.B, a.level, pt.ptr, M.LOG_REP, tmp.ptr(), pt_shared=True)
+        out = self._new(a.B, a.level - 1, a.scale * self.S(a.level) / self.moduli[a.level - 1])
+        self.ctx.rescale(tmp.ptr(), 2 * a.B, a.level, out.ptr())
+        return out
+
+    def rotate_masked(self, a, pts, n_sets):
+        assert a.B == 1
+        T = M.WKV_T
+        out = self._new(n_sets * T, a.level - 1, a.scale * self.S(a.level) / self.moduli[a.level - 1])
+        self.ctx.eval_rotate_masked(a.ptr(), a.level, M.WKV_LO, [self.keys.get(s) for s in M.WKV_LO], M.WKV_HI,
+                                    [self.keys.get(s) for s in M.WKV_HI], n_sets, pts.ptr, M.LOG_REP, out.ptr())
+        return out
+
+    def matvec(self, inputs, h):
+        lv = inputs[0].level
+        assert all(x.level == lv and x.B == 1 for x in inputs) and len(inputs) == h["n_in"]
+        out = self._new(h["n_out"], lv - 1, inputs[0].scale * self.S(lv) / self.moduli[lv - 1])
+        self.ctx.linear_transform_multi([x.ptr() for x in inputs], lv, h["buf"].ptr, M.LOG_REP, M.MV_BABIES,
+                                        [self.keys.get(s) for s in M.MV_BABIES], M.MV_GIANTS,
+                                        [self.keys.get(s) for s in M.MV_GIANTS], h["n_out"], True, out.ptr())
+        return out
+
+    def mul_i(self, a, sign):
+        out = self._new(a.B, a.level, a.scale)
+        self.ctx.eval_mul_i(a.ptr(), 2 * a.B, a.level, sign, out.ptr())
+        return out
+
+    def conj(self, a):
+        out = self._new(a.B, a.level, a.scale)
+        self.ctx.eval_automorphism_ks(a.ptr(), a.B, a.level, 2 * self.N - 1, self.conj_key, out.ptr())
+        return out
+
+    def bootstrap(self, a):
+        lo = self.at_scale(a, 1, self.in_scale)
+        out = self._new(a.B, self.top_level, self.S(self.top_level))
+        for b in range(a.B):
+            self.boot.run(lo.ptr(b), self.relin, self.conj_key, self.boot_keys, out.ptr(b))
+        return out
+
+    def at_scale(self, a, lt, scale):
+        out = self._new(a.B, lt, scale)
+        self.ctx.eval_lincomb(a.B, [a.ptr()], [a.level], [1.0], [a.scale], scale, 0.0, lt, False, out.ptr())
+        return out

@@ -1,0 +1,208 @@
+"""Shape, weights and slot layout of the config-5 decode step: an RWKV-7-0.1B-shaped polynomial recurrent
+model evaluated on 32 conversation lanes packed in the slots of one N = 2^16 ciphertext.
+
+Shape (RWKV-7 0.1B): 12 layers, d_model 768, 12 heads of size 64, channel-mix width 3072, vocabulary 65536.
+Every nonlinearity is a degree-3 polynomial p(z) = c0 + c1 z + c2 z^2 + c3 z^3 with seeded coefficients in
+[-0.5, 0.5]; weights are random-init (seeded).  Per layer and lane (x in R^768, carried state S_h in
+R^{64x64} per head, xp_t, xp_c in R^768):
+
+  time mix      n  = p_n1(mean(x^2));  xn = x n                       (RMSNorm: rsqrt -> p_n1)
+                u_m = g1 (1 - mu_m) xn + g1 mu_m xp_t,  m in {r, k, v, w, a, g}      (token shift)
+                r, k, v = W_r u_r, W_k u_k, W_v u_v
+                w, a, g = p_w(W_w u_w), p_a(W_a u_a), p_g(W_g u_g)    (decay, in-context rate, gate)
+                kh = k eta                                            (key used for removal)
+                S_h <- S_h diag(w_h) - (S_h kh_h)(kh_h a_h)^T + v_h k_h^T    (WKV-7 state update)
+                y_h = S_h r_h;  x <- x + W_o (y g);  xp_t <- xn
+  channel mix   xn2 = x p_n2(mean(x^2));  u = g2 (1 - mu_c) xn2 + g2 mu_c xp_c
+                x <- x + W_cv p_h(W_ck u);  xp_c <- xn2
+  output        xo = g_o x p_o(mean(x^2));  logits = W_head xo     (the head runs on the client)
+
+RWKV-7's LoRA pairs for w, a, g are dense 768 x 768 maps here, and its per-head L2 normalisation of kh
+and GroupNorm of y are left out (they would add two more per-head polynomial norms).  The recurrence is
+the reference model's WKV-7 step; the reference's served FHE driver (gpu_real_model.cu:4674-5300) runs
+the same sequence of norms, token shift, projections, scan, gate, output projection and channel mix.
+
+Slot layout (lane-major, gpu_real_model.cu:483-519): slot lane * 1024 + c holds channel c < 768 of lane
+lane; channels 768..1023 are zero.  Every plaintext that is the same for all lanes is 1024-periodic and
+stored compressed (N / 32 words per limb).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+N_LAYERS = 12
+D = 768
+DPAD = 1024
+HEADS = 12
+HS = 64
+FF = 3072
+VOCAB = 65536
+LANES = 32
+SLOTS = 1 << 15
+LOG_REP = 5  # 1024-periodic plaintexts: N / 2^5 words per limb
+
+MIX_NAMES = ("r", "k", "v", "w", "a", "g")
+
+
+def _poly_coeffs(rng):
+    return rng.uniform(-0.5, 0.5, 4)
+
+
+def make_weights(seed: int = 5, n_layers: int = N_LAYERS, vocab: int = VOCAB) -> dict:
+    """Seeded random-init weights.  The scales keep every activation O(1) over the 12 layers (the
+    bootstrapped values must stay well inside the EvalMod range)."""
+    rng = np.random.default_rng(seed)
+    layers = []
+    for _ in range(n_layers):
+        L = {}
+        L["g1"] = 1.0 + 0.1 * rng.standard_normal(D)
+        L["g2"] = 1.0 + 0.1 * rng.standard_normal(D)
+        for m in MIX_NAMES:
+            L["mu_" + m] = rng.uniform(0.0, 1.0, D)
+        L["mu_c"] = rng.uniform(0.0, 1.0, D)
+        for m in ("r", "k", "v"):
+            L["W_" + m] = rng.standard_normal((D, D)) / np.sqrt(D)
+        for m in ("w", "a", "g"):
+            L["W_" + m] = 0.5 * rng.standard_normal((D, D)) / np.sqrt(D)
+        L["W_o"] = 0.5 * rng.standard_normal((D, D)) / np.sqrt(D)
+        L["eta"] = rng.uniform(0.05, 0.15, D)
+        L["W_ck"] = 0.5 * rng.standard_normal((FF, D)) / np.sqrt(D)
+        L["W_cv"] = 0.5 * rng.standard_normal((D, FF)) / np.sqrt(FF)
+        for p in ("p_n1", "p_n2", "p_w", "p_a", "p_g", "p_h"):
+            L[p] = _poly_coeffs(rng)
+        layers.append(L)
+    out = {"layers": layers, "g_o": 1.0 + 0.1 * rng.standard_normal(D), "p_o": _poly_coeffs(rng)}
+    out["emb_scale"] = 1.0
+    out["head_seed"] = int(rng.integers(0, 2**31))
+    out["vocab"] = vocab
+    return out
+
+
+def head_matrix(weights: dict, rows: int | None = None) -> np.ndarray:
+    """The vocabulary head [vocab][768] (N(0, 1/768)), generated from its seed (rows: a prefix)."""
+    rng = np.random.default_rng(weights["head_seed"])
+    n = weights["vocab"] if rows is None else rows
+    return rng.standard_normal((n, D)) / np.sqrt(D)
+
+
+def embed_tokens(tokens, seed: int = 11) -> np.ndarray:
+    """Client-side embedding of one token per lane: [lanes][768], entries N(0, 1) / 2."""
+    rng = np.random.default_rng([seed] + [int(t) for t in tokens])
+    return 0.5 * rng.standard_normal((len(tokens), D))
+
+
+# ---------------------------------------------------------------- slot layout
+def pack_lanes(X: np.ndarray) -> np.ndarray:
+    """[lanes][<=1024] -> [32768] slots (lane-major, zero padded)."""
+    X = np.atleast_2d(X)
+    out = np.zeros((LANES, DPAD), dtype=X.dtype)
+    out[: X.shape[0], : X.shape[1]] = X
+    return out.reshape(-1)
+
+
+def unpack_lanes(v: np.ndarray, width: int = D) -> np.ndarray:
+    return np.asarray(v).reshape(LANES, DPAD)[:, :width]
+
+
+def periodic(vec: np.ndarray) -> np.ndarray:
+    """A per-channel vector (<= 1024 entries) as its 1024-period (zero padded)."""
+    out = np.zeros(DPAD, dtype=np.asarray(vec).dtype)
+    out[: len(vec)] = vec
+    return out
+
+
+# ---------------------------------------------------------------- BSGS diagonals (signed rotations)
+# y[i] = sum_j M[i][j] x[j] inside each lane with i, j < 768: rotation r = j - i in (-768, 768), never leaving
+# the lane.  r = 32 g + b, babies b in [0, 32), giants G_g = 32 g with g in [-24, 24).
+MV_NB = 32
+MV_GIANTS = tuple(32 * g for g in range(-24, 24))
+MV_BABIES = tuple(range(MV_NB))
+
+
+def matvec_diagonals(blocks) -> np.ndarray:
+    """blocks[o][i]: 768 x 768 matrices (output block o, input block i; None = zero).
+    Returns [n_out][n_giant][n_in * 32][1024]: the 1024-periodic diagonal for giant g, input i, baby b,
+    pre-rotated by -G_g (gpu_real_model.cu:2767-2823's pre-rotation, harness/cpu_real_model.cpp:270-318)."""
+    n_out, n_in = len(blocks), len(blocks[0])
+    ng = len(MV_GIANTS)
+    out = np.zeros((n_out, ng, n_in * MV_NB, DPAD))
+    rows = np.arange(D)
+    for o in range(n_out):
+        for i in range(n_in):
+            M = blocks[o][i]
+            if M is None:
+                continue
+            for gi, G in enumerate(MV_GIANTS):
+                for b in range(MV_NB):
+                    r = G + b
+                    cols = rows + r
+                    ok = (cols >= 0) & (cols < D)
+                    d = np.zeros(DPAD)
+                    d[rows[ok]] = M[rows[ok], cols[ok]]
+                    # pre-rotation by -G of a 1024-periodic vector: d'[p] = d[(p - G) mod 1024]
+                    out[o, gi, i * MV_NB + b] = np.roll(d, G)
+    return out
+
+
+# ---------------------------------------------------------------- WKV diagonal layout
+# D_t[lane*1024 + h*64 + i] = S_h[i][(i + t) mod 64], t = 0..63 (one ciphertext per t, all heads and lanes).
+# rot64_t(x) (cyclic rotation by t inside every 64-block) = m_lo,t (.) Rot_t(x) + m_hi,t (.) Rot_{t-64}(x).
+WKV_T = HS
+WKV_LO = tuple(range(WKV_T))
+WKV_HI = (0,) + tuple(t - HS for t in range(1, WKV_T))
+
+
+def wkv_masks(extra: np.ndarray | None = None) -> np.ndarray:
+    """[64][2][1024]: the lo/hi masks of rot64_t, optionally times rot64_t(extra) (a per-channel vector folded
+    into the same plaintext)."""
+    i = np.arange(DPAD) % HS
+    valid = np.arange(DPAD) < D
+    out = np.zeros((WKV_T, 2, DPAD))
+    e = periodic(extra) if extra is not None else None
+    for t in range(WKV_T):
+        lo = valid & (i + t < HS)
+        hi = valid & (i + t >= HS) if t else np.zeros(DPAD, dtype=bool)
+        out[t, 0] = lo
+        out[t, 1] = hi
+        if e is not None:
+            src = (np.arange(DPAD) // HS) * HS + (i + t) % HS
+            out[t, :] *= np.where(valid, e[np.minimum(src, DPAD - 1)], 0.0)[None, :]
+    return out
+
+
+def state_to_diag(S: np.ndarray) -> np.ndarray:
+    """[lanes][12][64][64] -> [64][32768] diagonal-layout slot vectors."""
+    lanes = S.shape[0]
+    out = np.zeros((WKV_T, LANES, DPAD))
+    i = np.arange(HS)
+    for t in range(WKV_T):
+        vals = S[:, :, i, (i + t) % HS]  # [lanes][12][64]
+        out[t, :lanes, :D] = vals.reshape(lanes, D)
+    return out.reshape(WKV_T, -1)
+
+
+def diag_to_state(Dg: np.ndarray, lanes: int = LANES) -> np.ndarray:
+    S = np.zeros((lanes, HEADS, HS, HS))
+    i = np.arange(HS)
+    Dg = np.asarray(Dg).reshape(WKV_T, LANES, DPAD)
+    for t in range(WKV_T):
+        S[:, :, i, (i + t) % HS] = Dg[t, :lanes, :D].reshape(lanes, HEADS, HS)
+    return S
+
+
+# ---------------------------------------------------------------- norms
+NORM_UP = tuple(1 << k for k in range(10))      # rotate-and-add: slot lane*1024 gets the lane's sum
+NORM_DOWN = tuple(-(1 << k) for k in range(10))  # broadcast the masked sum over the lane
+
+
+def lane_start_mask(scale: float = 1.0) -> np.ndarray:
+    m = np.zeros(DPAD)
+    m[0] = scale
+    return m
+
+
+def rotation_steps() -> list:
+    """Every rotation step the decode step uses (keys to generate)."""
+    s = set(MV_BABIES) | set(MV_GIANTS) | set(WKV_LO) | set(WKV_HI) | set(NORM_UP) | set(NORM_DOWN)
+    s.discard(0)
+    return sorted(s)

@@ -151,6 +151,58 @@ int ckks_linear_transform_bsgs(ckks_context* ctx, const uint64_t* d_ct, uint32_t
                                uint32_t n_diag, uint32_t baby_steps, const uint64_t* const* d_baby_evks,
                                const uint64_t* const* d_giant_evks, uint64_t* d_out, void* stream);
 
+/* ---- periodic plaintexts, general transforms, linear combinations (decode-step support) ----------
+ * ckks_encode_periodic      n_vectors slot vectors of period `period` (a power of two; replicated over the N/2
+ *                           slots) encoded in the compressed form of hpc_gpu_port/periodic_encode.hpp:179-260:
+ *                           out [n][l][2 period]; the evaluation form of limb i is comp[i][k >> log2(N/(2 period))]
+ *                           (the expansion of gpu_real_model.cu:145-155)
+ * ckks_eval_mult_plain_ex   ct (.) pt with pt [l][N >> log_rep] (log_rep = 0: full plaintext)
+ * ckks_linear_transform_general  y = sum_g Rot_{G_g}( sum_b diag[g n_baby + b] (.) Rot_{B_b}(ct) ) with explicit
+ *                           baby and giant steps (0 = identity, no key), diagonals compressed by log_rep, term
+ *                           (g, b) pre-rotated by -G_g; no rescale; out [2][l][N]
+ * ckks_linear_transform_multi  n_in inputs share the baby steps, n_out outputs share the babies:
+ *                           out_o = sum_g Rot_{G_g}( sum_{i,b} diag[o][g][i n_baby + b] (.) Rot_{B_b}(in_i) ),
+ *                           diags [n_out][n_giant][n_in n_baby][l][N >> log_rep]; rescale != 0 rescales each
+ *                           output (matvecBatchImpl with shared babies, gpu_real_model.cu:2902-3424)
+ * ckks_eval_mult_sum        out[c] = relin( sum_j a[c][j] (x) b[c][j] ) (+ rescale): one key switch for up to 64
+ *                           products; d_pairs [batch][n_products][2] pointers to ciphertexts [2][l][N]
+ * ckks_eval_rotate_masked   out[s][t] = rescale( pt[s][t][0] (.) Rot_{lo_t}(ct) + pt[s][t][1] (.) Rot_{hi_t}(ct) ),
+ *                           all 2n rotations hoisted over one ModUp; pt [n_sets][n][2][l][N >> log_rep] (cyclic
+ *                           rotations inside slot blocks built from two plain rotations and complementary masks)
+ * ckks_eval_automorphism_ks X -> X^g with the key of g on a batch (g = 2N - 1: EvalConjugate)
+ * ckks_eval_mul_i           multiply every slot by i (sign 1) or -i (sign -1): exact, no level
+ * ckks_eval_lincomb         integer mode: sum_t round(c_t) x_t + round(add_const scale_out), all terms at
+ *                           target_level, no rescale; scalar mode: terms at any level >= target_level + 1 (read
+ *                           without copying), each scaled so the result has scale scale_out after one rescale
+ *                           to target_level (FLEXIBLE scaling, gpu_real_model.cu:1156). Terms are batches
+ *                           [batch][2][l_t][N]; at most 8 terms. */
+int ckks_encode_periodic(ckks_context* ctx, const double* re, const double* im, uint32_t n_vectors, uint32_t period,
+                         uint32_t level, double scale, uint64_t* d_out);
+int ckks_eval_mult_plain_ex(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level,
+                            const uint64_t* d_pt, int pt_shared, uint32_t log_rep, uint64_t* d_out, void* stream);
+int ckks_linear_transform_general(ckks_context* ctx, const uint64_t* d_ct, uint32_t level, const uint64_t* d_diags,
+                                  uint32_t log_rep, uint32_t n_baby, const int64_t* baby_steps,
+                                  const uint64_t* const* d_baby_evks, uint32_t n_giant, const int64_t* giant_steps,
+                                  const uint64_t* const* d_giant_evks, uint64_t* d_out, void* stream);
+int ckks_linear_transform_multi(ckks_context* ctx, const uint64_t* const* d_in, uint32_t n_in, uint32_t level,
+                                const uint64_t* d_diags, uint32_t log_rep, uint32_t n_baby, const int64_t* baby_steps,
+                                const uint64_t* const* d_baby_evks, uint32_t n_giant, const int64_t* giant_steps,
+                                const uint64_t* const* d_giant_evks, uint32_t n_out, int rescale, uint64_t* d_out,
+                                void* stream);
+int ckks_eval_mult_sum(ckks_context* ctx, const uint64_t* const* d_pairs, uint32_t n_products, uint32_t batch,
+                       uint32_t level, const uint64_t* d_evk, int rescale, uint64_t* d_out, void* stream);
+int ckks_eval_rotate_masked(ckks_context* ctx, const uint64_t* d_ct, uint32_t level, uint32_t n,
+                            const int64_t* steps_lo, const uint64_t* const* d_evks_lo, const int64_t* steps_hi,
+                            const uint64_t* const* d_evks_hi, uint32_t n_sets, const uint64_t* d_pts,
+                            uint32_t log_rep, uint64_t* d_out, void* stream);
+int ckks_eval_automorphism_ks(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level, uint32_t g,
+                              const uint64_t* d_evk, uint64_t* d_out, void* stream);
+int ckks_eval_mul_i(ckks_context* ctx, const uint64_t* d_in, uint32_t n_polys, uint32_t level, int sign,
+                    uint64_t* d_out, void* stream);
+int ckks_eval_lincomb(ckks_context* ctx, uint32_t batch, uint32_t n_terms, const uint64_t* const* d_terms,
+                      const uint32_t* levels, const double* coeffs, const double* scales_in, double scale_out,
+                      double add_const, uint32_t target_level, int integer_mode, uint64_t* d_out, void* stream);
+
 /* ---- bootstrapping (EvalBootstrapSetup / EvalBootstrapKeyGen / EvalBootstrap, gpu_real_model.cu:1335-1336,
  * 1444,2544) ------------------------------------------------------------------------------------------
  * Full-slot (N/2 slots) CKKS bootstrap: ModRaise (centered q0 limb), CoeffToSlot (3 BSGS levels), EvalMod

@@ -1,0 +1,65 @@
+"""The config-5 decode step's plan on the slot-vector simulator (CPU): the encrypted driver
+(fhe-ssm_amd/decode_step.py) with every primitive applied to plain slot values must reproduce the float64
+reference model (oracle/rwkv_ref.py), which is written in matrix form without slots, diagonals or
+rotations.  This pins the packing algebra: BSGS diagonals and their pre-rotation, the lane-sum and
+broadcast of the norms, the WKV diagonal layout and its masked block rotations, the state packing
+(D_t + i D_{t+32}) and unpacking, and the token-shift carries across steps."""
+import numpy as np
+import pytest
+
+from slot_backend import DS, M, SlotBackend
+from oracle import rwkv_ref as ref
+
+
+def test_wkv_layout_roundtrip():
+    rng = np.random.default_rng(1)
+    S = rng.standard_normal((32, 12, 64, 64))
+    Dg = M.state_to_diag(S)
+    assert Dg.shape == (64, 1 << 15)
+    assert np.array_equal(M.diag_to_state(Dg), S)
+
+
+def test_masked_block_rotation():
+    """m_lo,t (.) Rot_t(x) + m_hi,t (.) Rot_{t-64}(x) is the cyclic rotation by t inside each 64-block"""
+    rng = np.random.default_rng(2)
+    x = M.pack_lanes(rng.standard_normal((32, 768)))
+    masks = M.wkv_masks()
+    for t in (0, 1, 17, 63):
+        got = np.tile(masks[t, 0], 32) * np.roll(x, -M.WKV_LO[t]) + np.tile(masks[t, 1], 32) * np.roll(x, -M.WKV_HI[t])
+        blocks = x.reshape(32, 16, 64)
+        want = np.roll(blocks, -t, axis=2).reshape(-1)
+        want.reshape(32, 1024)[:, 768:] = 0
+        assert np.allclose(got, want, atol=0), t
+
+
+def test_matvec_diagonals():
+    rng = np.random.default_rng(3)
+    A = rng.standard_normal((768, 768))
+    d = M.matvec_diagonals([[A]])
+    x = rng.standard_normal((32, 768))
+    xs = M.pack_lanes(x)
+    y = np.zeros(1 << 15)
+    for gi, G in enumerate(M.MV_GIANTS):
+        acc = sum(np.tile(d[0, gi, b], 32) * np.roll(xs, -b) for b in M.MV_BABIES)
+        y += np.roll(acc, -G)
+    assert np.allclose(M.unpack_lanes(y), x @ A.T, atol=1e-9)
+    assert np.all(y.reshape(32, 1024)[:, 768:] == 0)
+
+
+@pytest.mark.timeout(300)
+def test_decode_step_plan_matches_reference():
+    W = M.make_weights(5, n_layers=1)
+    be = SlotBackend(16)
+    step = DS.DecodeStep(be, W)
+    st = ref.init_state(32, 1)
+    for s in range(2):
+        x = M.embed_tokens(np.arange(32) + 100 * s)
+        out = step(be.encrypt(None, M.pack_lanes(x), 16))
+        xo, _ = ref.step(x, st, W)
+        got = M.unpack_lanes(be.decrypt(None, out))
+        assert np.max(np.abs(got - xo)) < 1e-12
+        assert np.max(np.abs(be.decrypt(None, out).reshape(32, 1024)[:, 768:])) == 0
+        assert np.allclose(M.diag_to_state(step.state[0]["D"].v.real), st[0]["S"], atol=1e-14)
+    # one refresh of the residual before the channel mix and the 32 packed state ciphertexts, per step
+    assert step.stats["bootstraps"] == 2 * 33
+    assert out.level == 1
