@@ -90,6 +90,10 @@ SIGNATURES = {
     "ckks_encode": (_int, [_vp, _vp, _vp, _u32, _u32, ctypes.c_double, _vp]),
     "ckks_encrypt": (_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp]),
     "ckks_decrypt_decode": (_int, [_vp, _vp, _vp, _u32, ctypes.c_double, _vp, _vp, _u32]),
+    "ckks_context_counters": (_int, [_vp, _vp, _int]),
+    "ckks_set_moddown_exact": (_int, [_vp, _int]),
+    "ckks_keygen_switch": (_int, [_vp, _vp, _vp, _vp, _vp, _u32, _vp]),
+    "ckks_bootstrap_set_sparse_keys": (_int, [_vp, _vp, _vp]),
     "ckks_profile_enable": (_int, [_vp, _int]),
     "ckks_profile_reset": (_int, [_vp]),
     "ckks_profile_query": (_int, [_vp, _u32, ctypes.c_char_p, _u32, _vp, _vp, _vp]),
@@ -345,6 +349,9 @@ class Context:
     def keygen_relin(self, sk, seed: bytes, eseed: bytes, d_evk) -> None:
         check(load().ckks_keygen_relin(self.h, sk.h, _seed(seed), _seed(eseed), d_evk))
 
+    def keygen_switch(self, sk_from, sk_to, seed: bytes, eseed: bytes, d_evk, q_limbs: int = 0) -> None:
+        check(load().ckks_keygen_switch(self.h, sk_from.h, sk_to.h, _seed(seed), _seed(eseed), q_limbs, d_evk))
+
     def keygen_automorphism(self, sk, g: int, seed: bytes, eseed: bytes, d_evk) -> None:
         check(load().ckks_keygen_automorphism(self.h, sk.h, g, _seed(seed), _seed(eseed), d_evk))
 
@@ -375,6 +382,14 @@ class Context:
 
     def profile_reset(self) -> None:
         check(load().ckks_profile_reset(self.h))
+
+    def set_moddown_exact(self, exact: bool) -> None:
+        check(load().ckks_set_moddown_exact(self.h, 1 if exact else 0))
+
+    def key_switches(self, reset: bool = False) -> int:
+        n = ctypes.c_uint64()
+        check(load().ckks_context_counters(self.h, ctypes.byref(n), 1 if reset else 0))
+        return n.value
 
     def profile_report(self) -> dict:
         """{kernel name: (launches, total_ms, total_algorithmic_bytes)}"""
@@ -459,6 +474,9 @@ class Bootstrap:
 
     def scale(self, level: int) -> float:
         return float(load().ckks_bootstrap_scale(self.h, level))
+
+    def set_sparse_keys(self, d_to_sparse, d_from_sparse) -> None:
+        check(load().ckks_bootstrap_set_sparse_keys(self.h, d_to_sparse, d_from_sparse))
 
     def run(self, d_ct_in, d_relin, d_conj, keys: dict, d_out, stream=None):
         steps = np.ascontiguousarray(np.asarray(list(keys.keys()), dtype=np.int64))

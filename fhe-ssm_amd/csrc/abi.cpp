@@ -181,6 +181,12 @@ int ckks_set_ntt_mode(ckks_context* ctx, int mode) {
     return CKKS_OK;
 }
 
+int ckks_set_moddown_exact(ckks_context* ctx, int exact) {
+    if (!ctx || (exact != 0 && exact != 1)) return fail(CKKS_EINVAL, "exact must be 0 or 1");
+    ctx->c.moddown_exact = exact != 0;
+    return CKKS_OK;
+}
+
 int ckks_buffer_alloc(size_t bytes, void** d_out) {
     if (!d_out) return fail(CKKS_EINVAL, "null argument");
     HIP_TRY(hipMalloc(d_out, bytes ? bytes : 1));
@@ -453,6 +459,26 @@ int ckks_keygen_automorphism(ckks_context* ctx, const ckks_secret* sk, uint32_t 
         fhe::keygen_automorphism(ctx->c, *sk->s, g, seed32, eseed32, 3.19, d_evk);
         return CKKS_OK;
     });
+}
+
+int ckks_keygen_switch(ckks_context* ctx, const ckks_secret* sk_from, const ckks_secret* sk_to,
+                       const uint8_t* seed32, const uint8_t* eseed32, uint32_t q_limbs, uint64_t* d_evk) {
+    if (int rc = check_secret(ctx, sk_from)) return rc;
+    if (int rc = check_secret(ctx, sk_to)) return rc;
+    if (!seed32 || !eseed32 || !d_evk) return fail(CKKS_EINVAL, "null argument");
+    if (ctx->c.K == 0) return fail(CKKS_EINVAL, "context has no special primes");
+    if (q_limbs > ctx->c.L) return fail(CKKS_EINVAL, "q_limbs exceeds the chain");
+    return guarded([&] {
+        fhe::keygen_switch_secret(ctx->c, *sk_from->s, *sk_to->s, seed32, eseed32, 3.19, q_limbs, d_evk);
+        return CKKS_OK;
+    });
+}
+
+int ckks_bootstrap_set_sparse_keys(ckks_bootstrap* bt, const uint64_t* d_to_sparse, const uint64_t* d_from_sparse) {
+    if (!bt || (!d_to_sparse) != (!d_from_sparse)) return fail(CKKS_EINVAL, "both keys or neither");
+    bt->p->sse_to = d_to_sparse;
+    bt->p->sse_from = d_from_sparse;
+    return CKKS_OK;
 }
 
 int ckks_encode(ckks_context* ctx, const double* re, const double* im, uint32_t n_slots, uint32_t level, double scale,
@@ -729,6 +755,13 @@ int ckks_profile_enable(ckks_context* ctx, int on) {
 int ckks_profile_reset(ckks_context* ctx) {
     if (!ctx) return fail(CKKS_EINVAL, "null context");
     fhe::prof_clear(ctx->c);
+    return CKKS_OK;
+}
+
+int ckks_context_counters(ckks_context* ctx, uint64_t* key_switches, int reset) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    if (key_switches) *key_switches = ctx->c.n_keyswitch;
+    if (reset) ctx->c.n_keyswitch = 0;
     return CKKS_OK;
 }
 

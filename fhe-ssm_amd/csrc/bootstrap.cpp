@@ -153,12 +153,17 @@ BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scal
     P->deg = deg;
     P->r = r;
     P->in_scale = in_scale;
-    // CoeffToSlot levels (limbs L, L-1, L-2) encode their diagonals at the prime they drop, so the scale
-    // stays top_scale through them (these primes should be the largest of the chain: the raised message
-    // is ~q0 K, and the plaintext precision is scale * |entry| ~ q_dropped / (2 q0 K) bits).  From L-3 on
-    // the FLEXIBLE rule S(l-1) = S(l)^2 / q_{l-1} applies.
+    // CoeffToSlot runs at top_scale on limbs L, L-1, L-2 (these primes should be the largest of the chain:
+    // the raised message is ~q0 K, and the absolute rounding and key-switching noise of these levels,
+    // amplified by 2 pi K in EvalMod, is what limits the precision, so top_scale should be well above the
+    // chain's scale).  Level l's diagonals are encoded at q_{l-1} S(l-1) / S(l): the first two keep the
+    // scale, the last lands on the context's scale at L-3.  From L-3 on the FLEXIBLE rule
+    // S(l-1) = S(l)^2 / q_{l-1} applies (the chain's scaling primes are chosen for it).  in_scale, the
+    // input's scale, is independent of it: EvalMod's signal is sin(2 pi m / q0), so in_scale close to q0
+    // (as OpenFHE's q0 ~ 2 Delta) keeps the signal well above EvalMod's noise.
     P->S.assign(L + 1, 0.0L);
-    for (uint32_t l = L; l >= L - 3; l--) P->S[l] = top_scale;
+    for (uint32_t l = L; l >= L - 2; l--) P->S[l] = top_scale;
+    P->S[L - 3] = ctx.scale;
     for (uint32_t l = L - 3; l >= 2; l--) P->S[l - 1] = P->S[l] * P->S[l] / (long double)ctx.moduli[l - 1];
     P->cheb = chebyshev_coeffs(deg, K, r);
     const auto rg = rot_group();
@@ -173,17 +178,33 @@ BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scal
             for (int s = s_lo; s <= s_hi; s++) D = compose(fft_layer(s, false, rg), D);
         return D;
     };
-    auto add_level = [&](std::vector<BootLevel>& dst, const Diags& D, int s_lo, uint32_t l, double pt_scale) {
+    // split: the level also separates real and imaginary parts.  With y its input, x = T(y) its output and
+    // conj commuting with rotations, 2 Re x = x + conj x = sum_g Rot_G(sum_b d (.) Rot_b(y) + conj(d) (.)
+    // Rot_b(conj y)) and 2 Im x = -i (x - conj x): one two-input, two-output BSGS over (y, conj y), whose
+    // conjugation key switch runs at this level's (high) scale instead of at the EvalMod scale.
+    auto add_level = [&](std::vector<BootLevel>& dst, const Diags& D, int s_lo, uint32_t l, double pt_scale,
+                         bool split) {
         const long delta = 1L << (s_lo - 1);
         BootLevel bl;
         bl.l = l;
         bl.nb = 8;
         bl.ng = 8;
+        bl.n_in = bl.n_out = split ? 2 : 1;
         for (uint32_t b = 0; b < bl.nb; b++) bl.bsteps.push_back((int64_t)b * delta);
         for (uint32_t g = 0; g < bl.ng; g++) bl.gsteps.push_back(((int64_t)g * bl.nb - 31) * delta);
-        HIPB(hipMalloc(&bl.d_diags, (size_t)bl.nb * bl.ng * l * W * 8));
-        HIPB(hipMemset(bl.d_diags, 0, (size_t)bl.nb * bl.ng * l * W * 8));
+        const size_t n_terms = (size_t)bl.n_out * bl.ng * bl.n_in * bl.nb;
+        HIPB(hipMalloc(&bl.d_diags, n_terms * l * W * 8));
+        HIPB(hipMemset(bl.d_diags, 0, n_terms * l * W * 8));
         std::vector<double> re(kSlots), im(kSlots);
+        auto put = [&](uint32_t o, uint32_t g, uint32_t j, const std::vector<cd>& v) {
+            for (uint32_t s = 0; s < kSlots; s++) {
+                re[s] = v[s].real();
+                im[s] = v[s].imag();
+            }
+            const size_t t = ((size_t)o * bl.ng + g) * bl.n_in * bl.nb + j;
+            encode(ctx, re.data(), im.data(), kSlots, l, pt_scale, bl.d_diags + t * l * W);
+        };
+        std::vector<cd> dr(kSlots), tmp(kSlots);
         for (auto& [off, d] : D) {
             if (off % delta) throw std::logic_error("unexpected diagonal offset");
             const long k = off / delta;
@@ -195,26 +216,34 @@ BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scal
             const uint32_t g = (uint32_t)(kp / bl.nb), b = (uint32_t)(kp % bl.nb);
             const long G = bl.gsteps[g];
             // term (g, b) is pre-rotated by -G: d'[s] = d[(s - G) mod n]
-            for (uint32_t s = 0; s < kSlots; s++) {
-                const uint32_t src = (uint32_t)((((long)s - G) % (long)kSlots + kSlots) % kSlots);
-                re[s] = d[src].real();
-                im[s] = d[src].imag();
+            for (uint32_t s = 0; s < kSlots; s++)
+                dr[s] = d[(uint32_t)((((long)s - G) % (long)kSlots + kSlots) % kSlots)];
+            if (!split) {
+                put(0, g, b, dr);
+                continue;
             }
-            encode(ctx, re.data(), im.data(), kSlots, l, pt_scale, bl.d_diags + (size_t)(g * bl.nb + b) * l * W);
+            const cd I(0.0, 1.0);
+            for (uint32_t s = 0; s < kSlots; s++) tmp[s] = std::conj(dr[s]);
+            put(0, g, b, dr);
+            put(0, g, bl.nb + b, tmp);
+            for (uint32_t s = 0; s < kSlots; s++) tmp[s] = -I * dr[s];
+            put(1, g, b, tmp);
+            for (uint32_t s = 0; s < kSlots; s++) tmp[s] = I * std::conj(dr[s]);
+            put(1, g, bl.nb + b, tmp);
         }
         dst.push_back(std::move(bl));
     };
     try {
         const double c_cts = (double)(P->S[L] / (q0 * K)) * 0.5;
-        const auto qd = [&](uint32_t l) { return (double)ctx.moduli[l - 1]; };
-        add_level(P->cts, build_group(11, 15, true, c_cts), 11, L, qd(L));
-        add_level(P->cts, build_group(6, 10, true, 1.0), 6, L - 1, qd(L - 1));
-        add_level(P->cts, build_group(1, 5, true, 1.0), 1, L - 2, qd(L - 2));
+        const auto qd = [&](uint32_t l) { return (double)((long double)ctx.moduli[l - 1] * P->S[l - 1] / P->S[l]); };
+        add_level(P->cts, build_group(11, 15, true, c_cts), 11, L, qd(L), false);
+        add_level(P->cts, build_group(6, 10, true, 1.0), 6, L - 1, qd(L - 1), false);
+        add_level(P->cts, build_group(1, 5, true, 1.0), 1, L - 2, qd(L - 2), true);
         const uint32_t l_stc = L - 3 - 7 - (uint32_t)r;
         const double c_stc = q0 / (2.0 * M_PI * in_scale);
-        add_level(P->stc, build_group(1, 5, false, c_stc), 1, l_stc, (double)P->S[l_stc]);
-        add_level(P->stc, build_group(6, 10, false, 1.0), 6, l_stc - 1, (double)P->S[l_stc - 1]);
-        add_level(P->stc, build_group(11, 15, false, 1.0), 11, l_stc - 2, (double)P->S[l_stc - 2]);
+        add_level(P->stc, build_group(1, 5, false, c_stc), 1, l_stc, (double)P->S[l_stc], false);
+        add_level(P->stc, build_group(6, 10, false, 1.0), 6, l_stc - 1, (double)P->S[l_stc - 1], false);
+        add_level(P->stc, build_group(11, 15, false, 1.0), 11, l_stc - 2, (double)P->S[l_stc - 2], false);
         P->l_out = l_stc - 3;
     } catch (...) {
         bootstrap_plan_destroy(P);
@@ -455,7 +484,16 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, const
     {
         uint64_t* last = raised.d;  // staging: the two q0 limbs, then lifted in place of the output
         HCt stage = ev1.get(1);
-        HIPB(hipMemcpyAsync(stage.d, ct_in, 2 * W * 8, hipMemcpyDeviceToDevice, st));
+        if (P.sse_to) {
+            // sparse-secret encapsulation: switch the q0 ciphertext to the sparse secret, so that the raised
+            // message m + q0 I has a small I (K bounds it), then switch back at the top level below
+            HCt c1 = ev1.get(1);
+            HIPB(hipMemcpyAsync(c1.d, ct_in + W, W * 8, hipMemcpyDeviceToDevice, st));
+            keyswitch(ctx, c1.d, 1, 1, P.sse_to, ct_in, stage.d, st, 2);
+            ev1.put(c1);
+        } else {
+            HIPB(hipMemcpyAsync(stage.d, ct_in, 2 * W * 8, hipMemcpyDeviceToDevice, st));
+        }
         JobSpec js{};
         js.n_polys = 2;
         js.period = 1;
@@ -468,6 +506,14 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, const
         for (uint32_t i = 0; i < L; i++) jl.pmap[i] = (uint8_t)i;
         HIPB(launch_ntt(ctx, raised.d, jl, 2 * L, false, ctx.ntt_mode, st));
         ev1.put(stage);
+        if (P.sse_from) {
+            HCt c1 = ev1.get(L), back = ev1.get(L);
+            HIPB(hipMemcpyAsync(c1.d, raised.d + (size_t)L * W, (size_t)L * W * 8, hipMemcpyDeviceToDevice, st));
+            keyswitch(ctx, c1.d, 1, L, P.sse_from, raised.d, back.d, st, 2);
+            ev1.put(c1);
+            ev1.put(raised);
+            raised = back;
+        }
     }
     if (stop_stage == 1) return emit(raised.d, 1, L);
     // ---- CoeffToSlot
@@ -485,38 +531,40 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, const
         return o;
     };
     HCt x = raised;
-    for (auto& bl : P.cts) {
-        HCt y = apply_level(ev1, x, bl);
+    for (size_t i = 0; i + 1 < P.cts.size(); i++) {
+        HCt y = apply_level(ev1, x, P.cts[i]);
         ev1.put(x);
         x = y;
     }
-    if (stop_stage == 2) return emit(x.d, 1, x.l);
-    // ---- split into real parts: [Re t, Im t] as one batch of two
-    const uint32_t lm = x.l;
+    // ---- last CoeffToSlot level with the split into real parts folded in: [2 Re t, 2 Im t] as a batch of
+    // two (the 1/2 is in the first level's constant)
+    const BootLevel& bs = P.cts.back();
+    if (x.l != bs.l || bs.n_in != 2 || bs.n_out != 2) throw std::logic_error("split level mismatch");
+    const uint32_t lm = bs.l - 1;
     HCt pair = ev2.get(lm);
     {
-        HCt cj = ev1.get(lm);
+        HCt cj = ev1.get(bs.l);
         const uint32_t g = 2 * kN - 1;
         const uint64_t* ck[1] = {conj_evk};
-        automorph_ks_list(ctx, x.d, 1, lm, &g, ck, cj.d, st);
-        const size_t cw = (size_t)2 * lm * W;
-        // Re: x + conj ; Im: -i (x - conj)
-        std::vector<uint64_t> C1(2 * lm), C2(2 * lm);
-        for (uint32_t i = 0; i < lm; i++) {
-            C1[i] = 1;
-            C1[lm + i] = 1;
-            C2[i] = 1;
-            C2[lm + i] = ctx.moduli[i] - 1;
-        }
-        const uint64_t* xs[2] = {x.d, cj.d};
-        const uint32_t strides[2] = {lm, lm};
-        HIPB(launch_lincomb(ctx, pair.d, 1, lm, 2, xs, strides, C1.data(), nullptr, st));
-        HCt diff = ev1.get(lm);
-        HIPB(launch_lincomb(ctx, diff.d, 1, lm, 2, xs, strides, C2.data(), nullptr, st));
-        HIPB(launch_mul_i(ctx, diff.d, pair.d + cw, 2, lm, -1, st));
-        ev1.put(diff);
+        automorph_ks_list(ctx, x.d, 1, bs.l, &g, ck, cj.d, st);
+        std::vector<const uint64_t*> bk, gk;
+        for (auto s : bs.bsteps) bk.push_back(s ? key[s] : nullptr);
+        for (auto s : bs.gsteps) gk.push_back(s ? key[s] : nullptr);
+        const uint64_t* ins[2] = {x.d, cj.d};
+        bsgs_multi(ctx, ins, 2, bs.l, bs.d_diags, bs.nb, bs.bsteps.data(), bk.data(), bs.ng, bs.gsteps.data(),
+                   gk.data(), 2, true, pair.d, st, 0);
         ev1.put(cj);
         ev1.put(x);
+    }
+    if (stop_stage == 2) {  // the CoeffToSlot output itself: Re + i Im
+        const size_t cw = (size_t)2 * lm * W;
+        HCt im = ev1.get(lm), z = ev1.get(lm);
+        HIPB(launch_mul_i(ctx, pair.d + cw, im.d, 2, lm, 1, st));
+        const uint64_t* xs[2] = {pair.d, im.d};
+        const uint32_t strides[2] = {lm, lm};
+        std::vector<uint64_t> C(2 * lm, 1);
+        HIPB(launch_lincomb(ctx, z.d, 1, lm, 2, xs, strides, C.data(), nullptr, st));
+        return emit(z.d, 1, lm);
     }
     if (stop_stage == 3) return emit(pair.d, 2, pair.l);
     // ---- EvalMod on both halves

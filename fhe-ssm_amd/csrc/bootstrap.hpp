@@ -11,8 +11,9 @@ namespace fhe {
 // one BSGS level of CoeffToSlot or SlotToCoeff: applied at l limbs, then rescaled
 struct BootLevel {
     uint32_t l = 0, nb = 0, ng = 0;
+    uint32_t n_in = 1, n_out = 1;  // the last CoeffToSlot level: inputs (y, conj y), outputs (2 Re, 2 Im)
     std::vector<int64_t> bsteps, gsteps;
-    uint64_t* d_diags = nullptr;  // [ng * nb][l][N], term (g, b) pre-rotated by -gsteps[g]
+    uint64_t* d_diags = nullptr;  // [n_out][ng][n_in nb][l][N], term (g, b) pre-rotated by -gsteps[g]
 };
 
 struct BootPlan {
@@ -24,6 +25,9 @@ struct BootPlan {
     std::vector<BootLevel> cts, stc;
     std::vector<int64_t> steps;  // rotation steps whose keys evaluation needs (plus the conjugation key)
     uint32_t l_out = 0;
+    // sparse-secret encapsulation (not owned): keys s -> s' (sparse, on q0 and P) and s' -> s
+    const uint64_t* sse_to = nullptr;
+    const uint64_t* sse_from = nullptr;
 };
 
 BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scale, double in_scale);

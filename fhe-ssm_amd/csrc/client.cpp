@@ -271,6 +271,18 @@ void keygen_switch(Context& ctx, const uint64_t* d_s_old, const int8_t* s_new, c
     HIPC(hipDeviceSynchronize());
 }
 
+// switching key from sk_from to sk_to; q_limbs > 0 keeps only Q limbs [0, q_limbs) (and P), zeroing the rest:
+// a key to a sparse secret is then published at the small modulus q_0..q_{q_limbs-1} P only
+void keygen_switch_secret(Context& ctx, const Secret& from, const Secret& to, const uint8_t seed[32],
+                          const uint8_t eseed[32], double sigma, uint32_t q_limbs, uint64_t* d_evk) {
+    keygen_switch(ctx, from.d_eval, to.coeffs.data(), seed, eseed, sigma, d_evk);
+    if (q_limbs == 0 || q_limbs >= ctx.L) return;
+    const uint32_t T = ctx.L + ctx.K;
+    for (uint32_t dp = 0; dp < 2 * ctx.dnum; dp++)
+        HIPC(hipMemset(d_evk + ((size_t)dp * T + q_limbs) * kN, 0, (size_t)(ctx.L - q_limbs) * kN * 8));
+    HIPC(hipDeviceSynchronize());
+}
+
 void keygen_relin(Context& ctx, const Secret& sk, const uint8_t seed[32], const uint8_t eseed[32], double sigma,
                   uint64_t* d_evk) {
     DevBuf s2((size_t)ctx.L * kN * 8);

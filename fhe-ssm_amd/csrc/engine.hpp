@@ -45,6 +45,7 @@ enum class NttMode { TwoPass = 0, Fused = 1 };
 // target limbs: y_i = [x_i * qhat_inv_i]_{q_i};  out_j = sum_i y_i * qhat_mod[i][j] mod p_j.
 struct BConvPlan {
     uint32_t n_in = 0, n_out = 0;
+    bool centered = false;  // exact (centered) conversion: table also holds floor(2^128/q_i) and prod mod p_j
     std::vector<uint32_t> in_idx, out_idx;  // prime indices
     uint64_t* d_tab = nullptr;  // [n_in] (qhat_inv, companion) pairs, then [n_in][n_out] qhat_mod
 };
@@ -78,6 +79,11 @@ struct Context {
     // per-launch profiling (off by default)
     bool prof_on = false;
     mutable std::vector<ProfRec> prof;
+    // key switches issued (evk inner products, one per ciphertext), always counted
+    mutable uint64_t n_keyswitch = 0;
+    // ModDown rounding: false = approximate P -> Q conversion (OpenFHE ApproxModDown, floor(x/P) - u with
+    // u in [0, K)); true = exact round(x / P) (centered conversion)
+    bool moddown_exact = false;
 };
 
 // Profiling helpers: no-ops unless ctx.prof_on.

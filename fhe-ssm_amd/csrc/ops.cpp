@@ -122,8 +122,9 @@ void* ws_get(Context& ctx, uint32_t slot, size_t bytes) {
 }
 
 // ------------------------------------------------------------------ BConv plans
-const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, const std::vector<uint32_t>& out_idx) {
-    std::string key = "b";
+const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, const std::vector<uint32_t>& out_idx,
+                            bool centered) {
+    std::string key = centered ? "c" : "b";
     for (auto i : in_idx) key += ":" + std::to_string(i);
     key += ">";
     for (auto j : out_idx) key += ":" + std::to_string(j);
@@ -134,7 +135,8 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
     p.n_out = (uint32_t)out_idx.size();
     p.in_idx = in_idx;
     p.out_idx = out_idx;
-    std::vector<uint64_t> tab(2 * p.n_in + (size_t)p.n_in * p.n_out);
+    p.centered = centered;
+    std::vector<uint64_t> tab(2 * p.n_in + (size_t)p.n_in * p.n_out + (centered ? 2 * p.n_in + p.n_out : 0));
     for (uint32_t i = 0; i < p.n_in; i++) {
         const uint64_t qi = ctx.moduli[in_idx[i]];
         uint64_t prod = 1;
@@ -149,6 +151,20 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
             for (uint32_t k = 0; k < p.n_in; k++)
                 if (k != i) m = mulmod_h(m, ctx.moduli[in_idx[k]] % pj, pj);
             tab[2 * p.n_in + (size_t)i * p.n_out + j] = m;
+        }
+    }
+    if (centered) {
+        uint64_t* cfix = tab.data() + 2 * p.n_in + (size_t)p.n_in * p.n_out;
+        for (uint32_t i = 0; i < p.n_in; i++) {
+            const unsigned __int128 c = (~(unsigned __int128)0) / ctx.moduli[in_idx[i]];  // floor(2^128 / q_i)
+            cfix[2 * i] = (uint64_t)c;
+            cfix[2 * i + 1] = (uint64_t)(c >> 64);
+        }
+        for (uint32_t j = 0; j < p.n_out; j++) {
+            const uint64_t pj = ctx.moduli[out_idx[j]];
+            uint64_t m = 1;
+            for (uint32_t k = 0; k < p.n_in; k++) m = mulmod_h(m, ctx.moduli[in_idx[k]] % pj, pj);
+            cfix[2 * p.n_in + j] = m;
         }
     }
     HIPX(hipMalloc(&p.d_tab, tab.size() * 8));
@@ -242,7 +258,7 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
         out_idx.push_back(i);
         out_off.push_back(i);
     }
-    const BConvPlan& plan = bconv_plan(ctx, in_idx, out_idx);
+    const BConvPlan& plan = bconv_plan(ctx, in_idx, out_idx, ctx.moddown_exact);
     uint64_t* conv = (uint64_t*)ws_get(ctx, WS_CONV, (size_t)n_polys * l * W * 8);
     HIPX(launch_bconv(ctx, plan, x, (uint64_t)E * W, in_off.data(), conv, (uint64_t)l * W, out_off.data(), n_polys,
                       st));

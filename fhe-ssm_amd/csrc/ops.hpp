@@ -25,7 +25,8 @@ enum WsSlot : uint32_t {
 };
 
 void* ws_get(Context& ctx, uint32_t slot, size_t bytes);
-const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, const std::vector<uint32_t>& out_idx);
+const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, const std::vector<uint32_t>& out_idx,
+                            bool centered = false);
 uint32_t num_digits(const Context& ctx, uint32_t l);
 
 void modup(Context& ctx, const uint64_t* x, uint64_t* ext, uint32_t B, uint32_t l, hipStream_t st);

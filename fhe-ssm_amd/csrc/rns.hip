@@ -93,6 +93,7 @@ constexpr int kMaxBconvOut = 80;
 
 struct BConvArgs {
     uint32_t n_in, n_out;
+    uint32_t centered;  // subtract u * (prod of input primes) with u = round(sum_i y_i / q_i)
     uint64_t in_bstride, out_bstride;
     uint16_t in_off[kMaxBconvIn];
     uint8_t in_prime[kMaxBconvIn];
@@ -117,12 +118,38 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
             y[i] = shoup(src[(size_t)ba.in_off[i] * kN], qhinv[i].w, qhinv[i].wp, q);
         }
     }
+    // centered form (exact ModDown): u = round(sum_i y_i / q_i) from the 128-bit fixed-point sum of
+    // floor(y_i * floor(2^128 / q_i) / 2^64); the table then holds [n_in] (lo, hi) words of floor(2^128 / q_i)
+    // and [n_out] (prod of the input primes) mod p_j
+    uint64_t u = 0;
+    const uint64_t* cfix = qhmod + (size_t)ba.n_in * ba.n_out;
+    const uint64_t* pmod = cfix + 2 * ba.n_in;
+    if (ba.centered) {
+        U128 F{0, 0};
+#pragma unroll
+        for (int i = 0; i < kMaxBconvIn; i++) {
+            if (i < (int)ba.n_in) {
+                mac128(F, y[i], cfix[2 * i + 1]);
+                const uint64_t h = mulhi64(y[i], cfix[2 * i]);
+                F.lo += h;
+                F.hi += (F.lo < h) ? 1 : 0;
+            }
+        }
+        const uint64_t lo = F.lo + (1ull << 63);
+        u = F.hi + (lo < F.lo ? 1 : 0);
+    }
     for (uint32_t j = 0; j < ba.n_out; j++) {
         const Barrett br = barrett_of(primes[ba.out_prime[j]]);
         U128 acc{0, 0};
 #pragma unroll
         for (int i = 0; i < kMaxBconvIn; i++)
             if (i < (int)ba.n_in) mac128(acc, y[i], qhmod[(size_t)i * ba.n_out + j]);
+        if (ba.centered) {
+            // acc - u * pmod_j, kept non-negative by adding 16 p_j (u <= n_in <= 16, pmod_j < p_j)
+            const uint64_t t = 16 * br.q - u * pmod[j];
+            acc.lo += t;
+            acc.hi += (acc.lo < t) ? 1 : 0;
+        }
         dst[(size_t)ba.out_off[j] * kN] = reduce_u128(acc, br);
     }
 }
@@ -465,6 +492,7 @@ hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_
     BConvArgs ba{};
     ba.n_in = plan.n_in;
     ba.n_out = plan.n_out;
+    ba.centered = plan.centered ? 1 : 0;
     ba.in_bstride = in_bstride;
     ba.out_bstride = out_bstride;
     for (uint32_t i = 0; i < plan.n_in; i++) {
@@ -483,6 +511,7 @@ hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_
 
 hipError_t launch_ks_inner(const Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* acc, uint32_t B,
                            uint32_t l, hipStream_t st) {
+    ctx.n_keyswitch += B;
     InnerArgs ia{};
     ia.E = l + ctx.K;
     ia.D = (l + ctx.alpha - 1) / ctx.alpha;
@@ -539,6 +568,7 @@ hipError_t launch_add(const Context& ctx, const uint64_t* x, const uint64_t* y, 
 
 hipError_t launch_ks_inner_list(const Context& ctx, const uint64_t* const* ext, const uint64_t* const* evk,
                                 uint64_t* acc, uint32_t n, uint32_t l, hipStream_t st) {
+    ctx.n_keyswitch += n;
     InnerArgs ia{};
     ia.E = l + ctx.K;
     ia.D = (l + ctx.alpha - 1) / ctx.alpha;

@@ -252,10 +252,12 @@ class DecodeStep:
 
 # ======================================================================================== GPU backend
 class HECt:
-    __slots__ = ("buf", "off", "B", "level", "scale", "_pool")
+    """a batch of B ciphertexts [B][2][level][N] in a pooled device buffer (or a view into another's)"""
+    __slots__ = ("buf", "off", "B", "level", "scale", "_pool", "base")
 
-    def __init__(self, buf, B, level, scale, off=0, pool=None):
+    def __init__(self, buf, B, level, scale, off=0, pool=None, base=None):
         self.buf, self.B, self.level, self.scale, self.off, self._pool = buf, B, level, scale, off, pool
+        self.base = base  # a view keeps the ciphertext it points into alive
 
     def ptr(self, b=0):
         return self.buf.ptr + self.off + b * 2 * self.level * HEBackend.N * 8
@@ -265,7 +267,7 @@ class HECt:
         return self.B * 2 * self.level * HEBackend.N * 8
 
     def __del__(self):
-        if self._pool is not None and self.off == 0:
+        if self._pool is not None:
             self._pool.put(self.buf)
 
 
@@ -343,10 +345,10 @@ class HEBackend(Backend):
         return ct
 
     def item(self, a, i):
-        return HECt(a.buf, 1, a.level, a.scale, off=a.off + i * 2 * a.level * self.N * 8)
+        return HECt(a.buf, 1, a.level, a.scale, off=a.off + i * 2 * a.level * self.N * 8, base=a)
 
     def slice(self, a, i0, i1):
-        return HECt(a.buf, i1 - i0, a.level, a.scale, off=a.off + i0 * 2 * a.level * self.N * 8)
+        return HECt(a.buf, i1 - i0, a.level, a.scale, off=a.off + i0 * 2 * a.level * self.N * 8, base=a)
 
     def concat(self, parts):
         lv, sc = parts[0].level, parts[0].scale
@@ -446,3 +448,95 @@ class HEBackend(Backend):
         out = self._new(a.B, lt, scale)
         self.ctx.eval_lincomb(a.B, [a.ptr()], [a.level], [1.0], [a.scale], scale, 0.0, lt, False, out.ptr())
         return out
+
+
+# ======================================================================================== set-up
+def _is_prime(n: int) -> bool:
+    """deterministic Miller-Rabin for n < 2^64"""
+    if n < 2:
+        return False
+    small = (2, 3, 5, 7, 11, 13, 17, 19, 23, 29, 31, 37)
+    for p in small:
+        if n % p == 0:
+            return n == p
+    d, r = n - 1, 0
+    while d % 2 == 0:
+        d //= 2
+        r += 1
+    for a in small:
+        x = pow(a, d, n)
+        if x in (1, n - 1):
+            continue
+        for _ in range(r - 1):
+            x = x * x % n
+            if x == n - 1:
+                break
+        else:
+            return False
+    return True
+
+
+def _nearest_ntt_prime(target: float, used: set, two_n: int = 1 << 17) -> int:
+    """the prime q = 1 mod 2N nearest to target that is not in used"""
+    k0 = int(round((target - 1) / two_n))
+    for d in range(0, 1 << 20):
+        for k in ((k0 + d, k0 - d) if d else (k0,)):
+            q = k * two_n + 1
+            if q > 1 and q not in used and _is_prime(q):
+                return q
+    raise ValueError("no prime found")
+
+
+def config5_moduli(ckks, log_scale: int = 40, n_scaling: int = 28):
+    """The config-5 chain: q0 50-bit, 28 scaling primes near 2^40, 3 x 60-bit CoeffToSlot primes on top;
+    P = 7 x 60-bit (1783 bits in all; the reference's n32 chains have 1730-1759, tests/golden/chain_moduli.json).
+
+    The scaling primes are chosen top-down so that the FLEXIBLE scales S(l-1) = S(l)^2 / q_{l-1}, which
+    double any deviation at every level, stay at 2^40: q_{l-1} is the NTT prime nearest S(l)^2 / 2^40
+    (OpenFHE picks its FLEXIBLE moduli on alternating sides of 2^p for the same reason)."""
+    big = ckks.gen_primes(60, 10)
+    q0 = ckks.gen_primes(50, 1)
+    used = set(big) | set(q0)
+    target = 2.0**log_scale
+    S = target
+    scaling = []
+    for _ in range(n_scaling):  # q_28 first (under the CoeffToSlot primes), down to q_1
+        q = _nearest_ntt_prime(S * S / target, used)
+        used.add(q)
+        scaling.append(q)
+        S = S * S / q
+    return q0 + scaling[::-1] + big[:3] + big[3:]
+
+
+def build_engine(ckks, secret_seed=b"S" * 32, n_keys_seed=7, steps=None):
+    """Context, bootstrapping plan, secret and every key the decode step uses; returns (backend, secret)."""
+    ctx = ckks.Context(num_q=32, num_p=7, dnum=4, scale=2.0**40, moduli=config5_moduli(ckks))
+    ctx.set_moddown_exact(True)  # unbiased key-switch rounding: the 2^40 chain bootstraps to ~13 bits with it
+    in_scale = 2.0**49  # bootstrap inputs enter at q0 / 2 (as OpenFHE: q0 ~ 2 Delta)
+    # sparse-secret encapsulation (h' = 32): |I| <= ~8 sigma = 8 sqrt(33/12) ~ 13, so K = 14 and two double
+    # angles suffice (EvalMod's noise grows as K^2)
+    boot = ckks.Bootstrap(ctx, K=14.0, cheb_degree=59, double_angles=2, top_scale=2.0**52, in_scale=in_scale)
+    sk = ctx.secret(secret_seed, 192)
+    sk_sparse = ctx.secret(bytes(reversed(secret_seed)), 32)
+    kb = ctx.dnum * 2 * (ctx.L + ctx.K) * ctx.N * 8
+    to_sparse = ckks.DeviceBuffer(kb)
+    ctx.keygen_switch(sk, sk_sparse, b"t" * 32, b"u" * 32, to_sparse.ptr, q_limbs=1)
+    from_sparse = ckks.DeviceBuffer(kb)
+    ctx.keygen_switch(sk_sparse, sk, b"v" * 32, b"w" * 32, from_sparse.ptr)
+    boot.set_sparse_keys(to_sparse.ptr, from_sparse.ptr)
+    relin = ckks.DeviceBuffer(kb)
+    ctx.keygen_relin(sk, b"r" * 32, b"s" * 32, relin.ptr)
+    conj = ckks.DeviceBuffer(kb)
+    ctx.keygen_automorphism(sk, 2 * ctx.N - 1, b"c" * 32, b"d" * 32, conj.ptr)
+    want = sorted(set(M.rotation_steps() if steps is None else steps) | set(boot.steps))
+    keys, bufs = {}, []
+    for i, s in enumerate(want):
+        b = ckks.DeviceBuffer(kb)
+        tag = i.to_bytes(2, "little")
+        ctx.keygen_automorphism(sk, ckks.rotation_index(s), bytes([n_keys_seed]) + tag + b"k" * 29,
+                                bytes([n_keys_seed]) + tag + b"e" * 29, b.ptr)
+        keys[s] = b.ptr
+        bufs.append(b)
+    be = HEBackend(ckks, ctx, boot, in_scale, relin.ptr, conj.ptr, keys)
+    be._owned = (relin, conj, bufs, to_sparse, from_sparse, sk_sparse)  # keep the keys alive with the backend
+    return be, sk

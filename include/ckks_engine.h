@@ -70,6 +70,12 @@ int ckks_context_moduli(const ckks_context* ctx, uint64_t* out, uint32_t cap);
 int ckks_context_roots(const ckks_context* ctx, uint64_t* out, uint32_t cap);
 /* NTT schedule: 0 = two kernels (pass A, pass B; default), 1 = fused one-limb-per-workgroup */
 int ckks_set_ntt_mode(ckks_context* ctx, int mode);
+/* ckks_set_moddown_exact: ModDown rounding.  0 (default): OpenFHE's ApproxModDown, floor(x / P) - u with
+ * u in [0, K) from the approximate P -> Q conversion (a bias of ~K/2 per coefficient, multiplied by the
+ * secret on decryption: it costs ~10 bits of bootstrapping precision at a 2^40 scale).  1: exact
+ * round(x / P): the conversion subtracts round(sum_i y_i / p_i) P, computed in 128-bit fixed point
+ * (Halevi-Polyakov-Shoup's corrected base conversion). */
+int ckks_set_moddown_exact(ckks_context* ctx, int exact);
 
 /* ---- device memory helpers (plain HIP; any HIP allocation works with the compute calls) ---- */
 int ckks_buffer_alloc(size_t bytes, void** d_out);
@@ -210,14 +216,22 @@ int ckks_eval_lincomb(ckks_context* ctx, uint32_t batch, uint32_t n_terms, const
  * division, then double_angles double-angle steps; K bounds |I| of the raised message m + q0 I), SlotToCoeff
  * (3 BSGS levels).  Consumes 3 + 7 + double_angles + 3 levels: the input is the q0 limb [2][1][N] of a
  * ciphertext whose message has scale in_scale; the output has ckks_bootstrap_out_level() limbs and scale
- * S(l): S(l) = top_scale for l >= L-3 (CoeffToSlot keeps the scale: its diagonals are encoded at the prime
- * each level drops, so the top three Q primes should be the largest), then S(l-1) = S(l)^2 / q_{l-1}.  Keys: the relinearization key, the conjugation key
+ * S(l): CoeffToSlot runs at S(l) = top_scale on l = L, L-1, L-2 (the top three Q primes should be the
+ * largest; top_scale well above the context's scale keeps its noise, which EvalMod amplifies by 2 pi K,
+ * small); its last level lands on S(L-3) = the context's scale (ckks_params.scale), then
+ * S(l-1) = S(l)^2 / q_{l-1} (the FLEXIBLE chain; the scaling primes must keep it near that scale).
+ * in_scale may exceed the context's scale: EvalMod's signal grows with in_scale / q0.  Keys: the relinearization key, the conjugation key
  * (automorphism 2N-1) and one automorphism key per rotation step of ckks_bootstrap_steps(). */
 typedef struct ckks_bootstrap ckks_bootstrap;
 int ckks_gen_primes(uint32_t bits, uint32_t count, const uint64_t* skip, uint32_t n_skip, uint64_t* out);
 int ckks_bootstrap_setup(ckks_context* ctx, double K, uint32_t cheb_degree, uint32_t double_angles, double top_scale,
                          double in_scale, ckks_bootstrap** out);
 void ckks_bootstrap_destroy(ckks_bootstrap* bt);
+/* ckks_bootstrap_set_sparse_keys: sparse-secret encapsulation (Bossuat, Troncoso-Pastoriza, Hubaux, ePrint
+ * 2022/024): the level-1 input is switched to a sparse secret s' (key s -> s', q_limbs = 1) before ModRaise and
+ * the raised ciphertext back to s (key s' -> s), so that |I| is bounded by the sparse weight: K drops from
+ * ~8 sqrt(h/12) to ~8 sqrt(h'/12), and EvalMod's noise (~K^2) with it.  The keys stay owned by the caller. */
+int ckks_bootstrap_set_sparse_keys(ckks_bootstrap* bt, const uint64_t* d_to_sparse, const uint64_t* d_from_sparse);
 int ckks_bootstrap_steps(const ckks_bootstrap* bt, int64_t* steps, uint32_t cap, uint32_t* n);
 uint32_t ckks_bootstrap_out_level(const ckks_bootstrap* bt);
 double ckks_bootstrap_scale(const ckks_bootstrap* bt, uint32_t level);
@@ -247,6 +261,10 @@ int ckks_secret_coeffs(const ckks_secret* sk, int8_t* out, uint32_t n);
 /* evk [dnum][2][L+K][N]; relinearization key: s^2 -> s; automorphism key of index g: s -> tau_{g^-1}(s) */
 int ckks_keygen_relin(ckks_context* ctx, const ckks_secret* sk, const uint8_t* seed32, const uint8_t* eseed32,
                       uint64_t* d_evk);
+/* ckks_keygen_switch: key switching from sk_from to sk_to (EvalKeySwitchGen); q_limbs > 0 publishes only Q
+ * limbs [0, q_limbs) and P (zeros elsewhere): the key to a sparse secret must live at a small modulus. */
+int ckks_keygen_switch(ckks_context* ctx, const ckks_secret* sk_from, const ckks_secret* sk_to,
+                       const uint8_t* seed32, const uint8_t* eseed32, uint32_t q_limbs, uint64_t* d_evk);
 int ckks_keygen_automorphism(ckks_context* ctx, const ckks_secret* sk, uint32_t g, const uint8_t* seed32,
                              const uint8_t* eseed32, uint64_t* d_evk);
 int ckks_encode(ckks_context* ctx, const double* re, const double* im, uint32_t n_slots, uint32_t level, double scale,
@@ -262,6 +280,8 @@ int ckks_decrypt_coeffs(ckks_context* ctx, const ckks_secret* sk, const uint64_t
  * enable: start recording every kernel launch (name, algorithmic bytes, start/stop events);
  * query: aggregated per kernel name, idx = 0..; returns CKKS_EINVAL past the last name.
  * Waits for the recorded events. */
+/* ckks_context_counters: key switches issued since the last reset (one per ciphertext key-switched) */
+int ckks_context_counters(ckks_context* ctx, uint64_t* key_switches, int reset);
 int ckks_profile_enable(ckks_context* ctx, int on);
 int ckks_profile_reset(ckks_context* ctx);
 int ckks_profile_query(ckks_context* ctx, uint32_t idx, char* name, uint32_t name_cap, uint64_t* launches,

@@ -260,6 +260,54 @@ void or_bconv(const or_ctx* c, const uint64_t* in, uint32_t n_in, const uint32_t
     free(qhmod);
 }
 
+/* Exact (centered) conversion for ModDown.  The approximate conversion above returns x_P + u P with
+ * u in [0, n_in) (u = floor(sum_i y_i / p_i)); ModDown then computes floor(x / P) - u, an error that is
+ * biased (mean ~n_in / 2 per coefficient, multiplied by the secret in decryption).  Taking
+ * u = round(sum_i y_i / p_i) instead makes the conversion the centered representative of x mod P and
+ * ModDown exactly round(x / P) (the floating-point-corrected base conversion of Halevi, Polyakov and
+ * Shoup, ePrint 2018/117, here in 128-bit fixed point so that CPU and GPU agree word for word). */
+void or_bconv_centered(const or_ctx* c, const uint64_t* in, uint32_t n_in, const uint32_t* in_idx,
+                       uint64_t* out, uint32_t n_out, const uint32_t* out_idx) {
+    typedef unsigned __int128 u128;
+    const uint32_t N = c->N;
+    or_bconv(c, in, n_in, in_idx, out, n_out, out_idx);
+    u128* cfix = (u128*)malloc(sizeof(u128) * n_in);
+    uint64_t* qhinv = (uint64_t*)malloc(sizeof(uint64_t) * n_in);
+    uint64_t* pmod = (uint64_t*)malloc(sizeof(uint64_t) * n_out);
+    for (uint32_t i = 0; i < n_in; i++) {
+        const uint64_t qi = c->q[in_idx[i]];
+        uint64_t prod = 1;
+        for (uint32_t k = 0; k < n_in; k++)
+            if (k != i) prod = or_mulmod(prod, c->q[in_idx[k]] % qi, qi);
+        qhinv[i] = or_invmod(prod, qi);
+        cfix[i] = (~(u128)0) / qi; /* floor(2^128 / q_i): q_i is odd */
+    }
+    for (uint32_t j = 0; j < n_out; j++) {
+        const uint64_t pj = c->q[out_idx[j]];
+        uint64_t m = 1;
+        for (uint32_t k = 0; k < n_in; k++) m = or_mulmod(m, c->q[in_idx[k]] % pj, pj);
+        pmod[j] = m;
+    }
+    for (uint32_t k = 0; k < N; k++) {
+        u128 F = 0;
+        for (uint32_t i = 0; i < n_in; i++) {
+            const uint64_t y = or_mulmod(in[(size_t)i * N + k], qhinv[i], c->q[in_idx[i]]);
+            const uint64_t clo = (uint64_t)cfix[i], chi = (uint64_t)(cfix[i] >> 64);
+            F += (u128)y * chi + (uint64_t)(((u128)y * clo) >> 64);
+        }
+        const uint64_t u = (uint64_t)((F + ((u128)1 << 63)) >> 64);
+        for (uint32_t j = 0; j < n_out; j++) {
+            const uint64_t pj = c->q[out_idx[j]];
+            const uint64_t t = or_mulmod(u % pj, pmod[j], pj);
+            uint64_t* o = out + (size_t)j * N + k;
+            *o = *o >= t ? *o - t : *o + pj - t;
+        }
+    }
+    free(cfix);
+    free(qhinv);
+    free(pmod);
+}
+
 /* ------------------------------------------------------------------ elementwise */
 
 void or_tensor(const or_ctx* c, const uint64_t* a, const uint64_t* b, uint32_t l, uint64_t* d) {
@@ -345,7 +393,10 @@ void or_moddown(const or_ctx* c, const uint64_t* x, uint32_t l, uint64_t* out) {
         or_ntt_inv(c, c->L + k, coef + (size_t)k * N);
     }
     for (uint32_t i = 0; i < l; i++) out_idx[i] = i;
-    or_bconv(c, coef, K, in_idx, conv, l, out_idx);
+    if (c->moddown_exact)
+        or_bconv_centered(c, coef, K, in_idx, conv, l, out_idx);
+    else
+        or_bconv(c, coef, K, in_idx, conv, l, out_idx);
     for (uint32_t i = 0; i < l; i++) {
         const uint64_t q = c->q[i];
         uint64_t pinv = 1;

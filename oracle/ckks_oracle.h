@@ -44,6 +44,7 @@ typedef struct {
     uint64_t ninv[OR_MAX_PRIMES];  /* N^{-1} mod q */
     uint64_t *tab, *tabp;          /* [L+K][N] forward table (brev order) + Shoup companions */
     uint64_t *itab, *itabp;        /* [L+K][N] inverse table (brev order) + Shoup companions */
+    uint32_t moddown_exact;        /* 0: approximate P->Q conversion (OpenFHE ApproxModDown); 1: exact rounding */
 } or_ctx;
 
 /* ---- scalar modular arithmetic ---- */
@@ -84,7 +85,11 @@ void or_tensor(const or_ctx* c, const uint64_t* a, const uint64_t* b, uint32_t l
 uint32_t or_num_digits(const or_ctx* c, uint32_t l);
 void or_modup(const or_ctx* c, const uint64_t* x, uint32_t l, uint64_t* ext);                       /* x eval [l][N] */
 void or_ks_inner(const or_ctx* c, const uint64_t* ext, uint32_t l, const uint64_t* evk, uint64_t* acc); /* evk [dnum][2][L+K][N]; acc [2][l+K][N] */
-void or_moddown(const or_ctx* c, const uint64_t* x, uint32_t l, uint64_t* out);                     /* x eval [l+K][N] -> out eval [l][N] */
+void or_moddown(const or_ctx* c, const uint64_t* x, uint32_t l, uint64_t* out);
+/* basis conversion returning the centered representative: sum_i y_i Qhat_i - u Q with u = round(sum_i y_i / q_i),
+ * u from the 128-bit fixed-point sum of floor(y_i * floor(2^128 / q_i) / 2^64) */
+void or_bconv_centered(const or_ctx* c, const uint64_t* in, uint32_t n_in, const uint32_t* in_idx,
+                       uint64_t* out, uint32_t n_out, const uint32_t* out_idx);                     /* x eval [l+K][N] -> out eval [l][N] */
 void or_keyswitch(const or_ctx* c, const uint64_t* x, uint32_t l, const uint64_t* evk, uint64_t* out2); /* out2 [2][l][N] */
 
 /* ---- rescale: in eval [n_polys][l][N] -> out eval [n_polys][l-1][N] ---- */

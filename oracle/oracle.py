@@ -31,6 +31,7 @@ class _Ctx(ctypes.Structure):
         ("psi", ctypes.c_uint64 * MAX_PRIMES),
         ("ninv", ctypes.c_uint64 * MAX_PRIMES),
         ("tab", _u64p), ("tabp", _u64p), ("itab", _u64p), ("itabp", _u64p),
+        ("moddown_exact", ctypes.c_uint32),
     ]
 
 
@@ -65,6 +66,7 @@ def lib():
             "or_ntt_fwd_batch": (None, [P, vp, u32, u32, vp]),
             "or_ntt_inv_batch": (None, [P, vp, u32, u32, vp]),
             "or_bconv": (None, [P, vp, u32, vp, vp, u32, vp]),
+            "or_bconv_centered": (None, [P, vp, u32, vp, vp, u32, vp]),
             "or_tensor": (None, [P, vp, vp, u32, vp]),
             "or_num_digits": (u32, [P, u32]),
             "or_modup": (None, [P, vp, u32, vp]),
@@ -149,12 +151,13 @@ def sample_gauss(seed: bytes, stream: int, N: int, sigma: float) -> np.ndarray:
 class Ctx:
     """Oracle context: moduli = Q chain (L) followed by P (K), dnum digits."""
 
-    def __init__(self, logN: int, moduli, L: int, K: int, dnum: int):
+    def __init__(self, logN: int, moduli, L: int, K: int, dnum: int, moddown_exact: bool = False):
         self._c = _Ctx()
         m = np.ascontiguousarray(np.asarray(moduli, dtype=np.uint64))
         rc = lib().or_ctx_init(ctypes.byref(self._c), logN, _p(m), L, K, dnum)
         if rc != 0:
             raise ValueError(f"or_ctx_init failed: {rc}")
+        self._c.moddown_exact = 1 if moddown_exact else 0
         self.logN, self.N, self.L, self.K, self.dnum = logN, 1 << logN, L, K, dnum
         self.alpha = self._c.alpha
         self.q = [int(x) for x in m]
@@ -200,6 +203,13 @@ class Ctx:
         ii, oo = _u32(in_idx), _u32(out_idx)
         out = np.zeros((len(oo), self.N), dtype=np.uint64)
         lib().or_bconv(self.ref, _p(x), len(ii), _p(ii), _p(out), len(oo), _p(oo))
+        return out
+
+    def bconv_centered(self, x: np.ndarray, in_idx, out_idx) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.uint64)
+        ii, oo = _u32(in_idx), _u32(out_idx)
+        out = np.zeros((len(oo), self.N), dtype=np.uint64)
+        lib().or_bconv_centered(self.ref, _p(x), len(ii), _p(ii), _p(out), len(oo), _p(oo))
         return out
 
     def tensor(self, a, b, l):

@@ -10,7 +10,7 @@ Precision is -log2 max|error| over all 32768 slots; the bar written here is 10 b
 import numpy as np
 import pytest
 
-from engine_loader import load_ckks
+from engine_loader import load_ckks, load_module
 
 pytestmark = pytest.mark.gpu
 
@@ -28,6 +28,29 @@ def boot_ctx(ckks):
     big = ckks.gen_primes(60, 12)
     qs = ckks.gen_primes(50, 22)
     return ckks.Context(num_q=26, num_p=8, dnum=3, scale=2.0**50, moduli=big[:1] + qs + big[1:4] + big[4:])
+
+
+def _exact(ctx):
+    ctx.set_moddown_exact(True)
+    return ctx
+
+
+# (context factory, K, Chebyshev degree, double angles, top scale, input scale)
+CHAINS = {
+    "config4": (lambda ckks: ckks.Context(num_q=26, num_p=8, dnum=3, scale=2.0**50,
+                                          moduli=ckks.gen_primes(60, 1) + ckks.gen_primes(50, 22) +
+                                          ckks.gen_primes(60, 12)[1:4] + ckks.gen_primes(60, 12)[4:]),
+                22.0, 59, 2, 2.0**50, 2.0**50),
+    "config5": (lambda ckks: _exact(ckks.Context(num_q=32, num_p=7, dnum=4, scale=2.0**40,
+                                                 moduli=load_module("decode_step").config5_moduli(ckks))),
+                32.0, 59, 3, 2.0**52, 2.0**48),
+}
+
+
+@pytest.fixture(scope="module", params=sorted(CHAINS))
+def chain(request, ckks):
+    make, K, deg, r, top, ins = CHAINS[request.param]
+    return make(ckks), K, deg, r, top, ins
 
 
 @pytest.mark.timeout(900)
@@ -75,14 +98,14 @@ def _bitrev(n):
 
 
 @pytest.mark.timeout(900)
-def test_bootstrap_stagewise(ckks, oracle, boot_ctx):
+def test_bootstrap_stagewise(ckks, oracle, chain):
     """Each stage against its mathematical expectation, computed from the secret and the input words:
-    ModRaise decrypts to m + q0 I exactly; CoeffToSlot to the bit-reversed coefficients (m'_k + i m'_{k+n})/(2 q0 K);
-    the split to their real and imaginary parts; EvalMod to sin(2 pi K t); the recombination to their sum."""
-    ctx = boot_ctx
+    ModRaise decrypts to m + q0 I exactly; CoeffToSlot (its last level split into real and imaginary parts,
+    stage 2 their recombination Re + i Im) to the bit-reversed coefficients (m'_k + i m'_{k+n})/(q0 K);
+    stage 3 to their real and imaginary parts; EvalMod to sin(2 pi K t); the recombination to their sum."""
+    ctx, Kr, deg, r, top, ins = chain
     L, K, D = ctx.L, ctx.K, ctx.dnum
-    Kr = 22.0
-    bt = ckks.Bootstrap(ctx, K=Kr, cheb_degree=59, double_angles=2, top_scale=2.0**50, in_scale=2.0**50)
+    bt = ckks.Bootstrap(ctx, K=Kr, cheb_degree=deg, double_angles=r, top_scale=top, in_scale=ins)
     sk = ctx.secret(b"T" * 32, 192)
     kb = D * 2 * (L + K) * N * 8
     relin = ckks.DeviceBuffer(kb)
@@ -99,7 +122,7 @@ def test_bootstrap_stagewise(ckks, oracle, boot_ctx):
     z = rng.uniform(-1.0, 1.0, SLOTS)
     pt = ckks.DeviceBuffer(N * 8)
     ct = ckks.DeviceBuffer(2 * N * 8)
-    ctx.encode(z, 1, 2.0**50, pt.ptr)
+    ctx.encode(z, 1, ins, pt.ptr)
     ctx.encrypt(sk, pt.ptr, 1, b"f" * 32, 0, ct.ptr)
     q0 = ctx.moduli[0]
     octx = oracle.Ctx(16, [q0], 1, 0, 1)
@@ -129,7 +152,7 @@ def test_bootstrap_stagewise(ckks, oracle, boot_ctx):
     n = SLOTS
     wprime = (mpf[:n] + 1j * mpf[n:]) / (q0 * Kr)
     v = wprime[_bitrev(n)]
-    stages = {2: [v / 2], 3: [v.real, v.imag], 4: [np.sin(2 * np.pi * Kr * v.real), np.sin(2 * np.pi * Kr * v.imag)]}
+    stages = {2: [v], 3: [v.real, v.imag], 4: [np.sin(2 * np.pi * Kr * v.real), np.sin(2 * np.pi * Kr * v.imag)]}
     stages[5] = [stages[4][0] + 1j * stages[4][1]]
     for st_ in (2, 3, 4, 5):
         lvl = bt.run_stage(ct.ptr, relin.ptr, conj.ptr, keys, st_, out.ptr)

@@ -1,0 +1,267 @@
+"""Config 5 on the GPU: the decode-step entry points bit-exact against the oracle composed from its
+stages, the config-5 chain's bootstrapping precision, and the encrypted decode step against the float64
+reference model (relErrRms <= 1e-3, the north star's bar for the full step).
+
+Chain (fhe-ssm_amd/decode_step.py): q0 50-bit, 28 scaling primes within 2^-12 of 2^40 (chosen so that the
+FLEXIBLE scales stay at 2^40), 3 x 60-bit CoeffToSlot primes, P 7 x 60-bit, dnum 4 (so K = 7 < alpha = 8:
+P only has to exceed each digit's product).
+"""
+import numpy as np
+import pytest
+
+from engine_loader import load_ckks, load_module
+
+pytestmark = pytest.mark.gpu
+
+N = 1 << 16
+SLOTS = N // 2
+LOG_REP = 5
+
+
+@pytest.fixture(scope="module")
+def ckks():
+    return load_ckks()
+
+
+@pytest.fixture(scope="module")
+def DS():
+    return load_module("decode_step")
+
+
+@pytest.fixture(scope="module")
+def M():
+    return load_module("rwkv_model")
+
+
+@pytest.fixture(scope="module")
+def ctx5(ckks, DS):
+    c = ckks.Context(num_q=32, num_p=7, dnum=4, scale=2.0**40, moduli=DS.config5_moduli(ckks))
+    c.set_moddown_exact(True)
+    return c
+
+
+@pytest.fixture(scope="module")
+def octx5(oracle, ctx5):
+    return oracle.Ctx(16, ctx5.moduli, ctx5.L, ctx5.K, ctx5.dnum, moddown_exact=True)
+
+
+@pytest.mark.parametrize("exact", [False, True])
+def test_moddown_keyswitch_bit_exact(ckks, oracle, ctx5, exact):
+    """ModDown and the full key switch in both rounding modes against the oracle (config-5 chain, K < alpha)"""
+    L, K, D = ctx5.L, ctx5.K, ctx5.dnum
+    oc = oracle.Ctx(16, ctx5.moduli, L, K, D, moddown_exact=exact)
+    ctx5.set_moddown_exact(exact)
+    try:
+        l = 13
+        x = residues(ctx5.moduli, (2,), list(range(l)) + [L + k for k in range(K)], 41)
+        dx = ckks.DeviceBuffer.from_array(x)
+        out = ckks.DeviceBuffer(2 * l * N * 8)
+        ctx5.moddown(dx.ptr, 2, l, out.ptr)
+        got = out.download((2, l, N))
+        for p in range(2):
+            assert np.array_equal(got[p], oc.moddown(x[p], l)), p
+        evk = residues(ctx5.moduli, (D, 2), list(range(L + K)), 42)
+        devk = ckks.DeviceBuffer.from_array(evk)
+        y = residues(ctx5.moduli, (1,), list(range(l)), 43)
+        dy = ckks.DeviceBuffer.from_array(y)
+        ctx5.keyswitch(dy.ptr, 1, l, devk.ptr, out.ptr)
+        assert np.array_equal(out.download((2, l, N)), oc.keyswitch(y[0], l, evk))
+    finally:
+        ctx5.set_moddown_exact(True)
+
+
+def residues(moduli, shape_prefix, prime_idx, seed):
+    rng = np.random.default_rng(seed)
+    q = np.array([moduli[i] for i in prime_idx], dtype=np.uint64)
+    x = rng.integers(0, 2**63, tuple(shape_prefix) + (len(prime_idx), N), dtype=np.uint64)
+    return x % q.reshape((1,) * len(shape_prefix) + (-1, 1))
+
+
+def qcol(ctx, l):
+    return np.array(ctx.moduli[:l], dtype=object).reshape(-1, 1)
+
+
+def expand(comp):
+    """compressed periodic plaintext [..., l, N/32] -> evaluation form [..., l, N]"""
+    return np.repeat(comp, 1 << LOG_REP, axis=-1)
+
+
+def test_chain(ctx5):
+    m = ctx5.moduli
+    assert m[0].bit_length() == 50 and all(abs(q / 2.0**40 - 1) < 2.0**-12 for q in m[1:29])
+    assert all(q.bit_length() == 60 for q in m[29:]) and len(set(m)) == 39
+    assert all(q % (1 << 17) == 1 for q in m)
+    # the FLEXIBLE scales from 2^40 at the CoeffToSlot levels down to level 1 stay within 2^+-0.001 of 2^40
+    S = 2.0**40
+    for l in range(29, 1, -1):
+        S = S * S / m[l - 1]
+        assert abs(np.log2(S) - 40) < 1e-3, l
+
+
+def test_mult_sum_bit_exact(ckks, ctx5, octx5):
+    """relin(sum_j a_j (x) b_j) + rescale == the oracle's tensors summed, key-switched, rescaled"""
+    l, B, npr = 9, 2, 3
+    L, K, D = ctx5.L, ctx5.K, ctx5.dnum
+    evk = residues(ctx5.moduli, (D, 2), list(range(L + K)), 5)
+    devk = ckks.DeviceBuffer.from_array(evk)
+    cts = residues(ctx5.moduli, (B, npr, 2, 2), list(range(l)), 6)  # [b][j][a/b][poly]
+    dc = ckks.DeviceBuffer.from_array(cts)
+    ctw = 2 * l * N * 8
+
+    def ptr(b, j, w):
+        return dc.ptr + ((b * npr + j) * 2 + w) * ctw
+
+    out = ckks.DeviceBuffer(B * 2 * (l - 1) * N * 8)
+    ctx5.eval_mult_sum([[(ptr(b, j, 0), ptr(b, j, 1)) for j in range(npr)] for b in range(B)], l, devk.ptr, out.ptr)
+    got = out.download((B, 2, l - 1, N))
+    q = qcol(ctx5, l)
+    for b in range(B):
+        acc = None
+        for j in range(npr):
+            d = octx5.tensor(cts[b, j, 0], cts[b, j, 1], l).astype(object)
+            acc = d if acc is None else acc + d
+        acc = (acc % q[None]).astype(np.uint64)
+        ks = octx5.keyswitch(acc[2], l, evk).astype(object)
+        rel = ((acc[:2].astype(object) + ks) % q[None]).astype(np.uint64)
+        assert np.array_equal(got[b], octx5.rescale(rel, l)), b
+    # one product: the same as EvalMult + rescale
+    out1 = ckks.DeviceBuffer(2 * (l - 1) * N * 8)
+    ctx5.eval_mult_sum([[(ptr(0, 0, 0), ptr(0, 0, 1))]], l, devk.ptr, out1.ptr)
+    ref = ckks.DeviceBuffer(2 * (l - 1) * N * 8)
+    ctx5.eval_mult_rescale(ptr(0, 0, 0), ptr(0, 0, 1), 1, l, devk.ptr, ref.ptr)
+    assert np.array_equal(out1.download((2, l - 1, N)), ref.download((2, l - 1, N)))
+
+
+def test_mult_plain_compressed_bit_exact(ckks, ctx5):
+    l, B = 4, 2
+    ct = residues(ctx5.moduli, (B, 2), list(range(l)), 7)
+    comp = residues(ctx5.moduli, (), list(range(l)), 8)[:, : N >> LOG_REP]
+    dct, dp = ckks.DeviceBuffer.from_array(ct), ckks.DeviceBuffer.from_array(np.ascontiguousarray(comp))
+    out = ckks.DeviceBuffer(ct.nbytes)
+    ctx5.eval_mult_plain_ex(dct.ptr, B, l, dp.ptr, LOG_REP, out.ptr)
+    full = expand(comp)
+    q = qcol(ctx5, l)
+    want = ((ct.astype(object) * full.astype(object)[None, None]) % q[None, None]).astype(np.uint64)
+    assert np.array_equal(out.download(ct.shape), want)
+
+
+def test_encode_periodic_decrypts(ckks, ctx5, M):
+    """a 1024-periodic plaintext multiplied into an encryption of x decrypts to x (.) periodic vector"""
+    l = 6
+    sk = ctx5.secret(b"Q" * 32, 192)
+    rng = np.random.default_rng(9)
+    x = rng.uniform(-1, 1, SLOTS)
+    p = rng.uniform(-1, 1, M.DPAD)
+    S = 2.0**40
+    pt = ckks.DeviceBuffer(l * N * 8)
+    ct = ckks.DeviceBuffer(2 * l * N * 8)
+    ctx5.encode(x, l, S, pt.ptr)
+    ctx5.encrypt(sk, pt.ptr, l, b"x" * 32, 0, ct.ptr)
+    comp = ckks.DeviceBuffer(l * (N >> LOG_REP) * 8)
+    ctx5.encode_periodic(p[None], l, S, comp.ptr)
+    out = ckks.DeviceBuffer(2 * l * N * 8)
+    ctx5.eval_mult_plain_ex(ct.ptr, 1, l, comp.ptr, LOG_REP, out.ptr)
+    got = ctx5.decrypt(sk, out.ptr, l, S * S)
+    assert np.max(np.abs(got - x * np.tile(p, SLOTS // M.DPAD))) < 1e-6
+
+
+def test_rotate_masked_bit_exact(ckks, ctx5, octx5):
+    l, n, n_sets = 5, 3, 2
+    L, K, D = ctx5.L, ctx5.K, ctx5.dnum
+    lo, hi = [0, 1, 5], [0, -63, -59]
+    steps = sorted(set(lo + hi) - {0})
+    evk = {s: residues(ctx5.moduli, (D, 2), list(range(L + K)), 100 + i) for i, s in enumerate(steps)}
+    dk = {s: ckks.DeviceBuffer.from_array(e) for s, e in evk.items()}
+    ct = residues(ctx5.moduli, (2,), list(range(l)), 11)
+    comp = residues(ctx5.moduli, (n_sets, n, 2), list(range(l)), 12)[..., : N >> LOG_REP]
+    dct, dp = ckks.DeviceBuffer.from_array(ct), ckks.DeviceBuffer.from_array(np.ascontiguousarray(comp))
+    out = ckks.DeviceBuffer(n_sets * n * 2 * (l - 1) * N * 8)
+    ctx5.eval_rotate_masked(dct.ptr, l, lo, [dk[s].ptr if s else None for s in lo], hi,
+                            [dk[s].ptr if s else None for s in hi], n_sets, dp.ptr, LOG_REP, out.ptr)
+    got = out.download((n_sets, n, 2, l - 1, N))
+    q = qcol(ctx5, l)
+
+    def rot(s):
+        return ct if s == 0 else octx5.rotate(ct, l, octx5.rot_index(s), evk[s])
+
+    for s in range(n_sets):
+        for t in range(n):
+            acc = rot(lo[t]).astype(object) * expand(comp[s, t, 0]).astype(object)[None] + \
+                rot(hi[t]).astype(object) * expand(comp[s, t, 1]).astype(object)[None]
+            want = octx5.rescale((acc % q[None]).astype(np.uint64), l)
+            assert np.array_equal(got[s, t], want), (s, t)
+
+
+def test_linear_transform_multi_bit_exact(ckks, ctx5, octx5):
+    """2 inputs sharing babies {0, 1, 2}, 2 outputs sharing the babies, giants {0, 3, -3}, compressed
+    diagonals, rescale: against the oracle composition"""
+    l, n_in, n_out = 4, 2, 2
+    L, K, D = ctx5.L, ctx5.K, ctx5.dnum
+    bst, gst = [0, 1, 2], [0, 3, -3]
+    nb, ng = len(bst), len(gst)
+    steps = [1, 2, 3, -3]
+    evk = {s: residues(ctx5.moduli, (D, 2), list(range(L + K)), 200 + i) for i, s in enumerate(steps)}
+    dk = {s: ckks.DeviceBuffer.from_array(e) for s, e in evk.items()}
+    xs = residues(ctx5.moduli, (n_in, 2), list(range(l)), 21)
+    diags = residues(ctx5.moduli, (n_out, ng, n_in * nb), list(range(l)), 22)[..., : N >> LOG_REP]
+    dx, dd = ckks.DeviceBuffer.from_array(xs), ckks.DeviceBuffer.from_array(np.ascontiguousarray(diags))
+    out = ckks.DeviceBuffer(n_out * 2 * (l - 1) * N * 8)
+    ctw = 2 * l * N * 8
+    ctx5.linear_transform_multi([dx.ptr + i * ctw for i in range(n_in)], l, dd.ptr, LOG_REP, bst,
+                                [dk[s].ptr if s else None for s in bst], gst,
+                                [dk[s].ptr if s else None for s in gst], n_out, True, out.ptr)
+    got = out.download((n_out, 2, l - 1, N))
+    q = qcol(ctx5, l)
+
+    def rot(c, s):
+        return c if s == 0 else octx5.rotate(c, l, octx5.rot_index(s), evk[s])
+
+    babies = [rot(xs[i], s) for i in range(n_in) for s in bst]
+    for o in range(n_out):
+        total = np.zeros((2, l, N), dtype=object)
+        for g in range(ng):
+            acc = sum(babies[j].astype(object) * expand(diags[o, g, j]).astype(object)[None] for j in range(n_in * nb))
+            total += rot((acc % q[None]).astype(np.uint64), gst[g]).astype(object)
+        want = octx5.rescale((total % q[None]).astype(np.uint64), l)
+        assert np.array_equal(got[o], want), o
+
+
+@pytest.fixture(scope="module")
+def engine(ckks, DS):
+    be, sk = DS.build_engine(ckks)
+    return be, sk
+
+
+@pytest.mark.timeout(900)
+def test_config5_chain_bootstrap(engine):
+    """sparse-secret encapsulation (h' = 32), K = 14, Chebyshev 59, 2 double angles on the config-5 chain:
+    level 17 out, precision bar 11 bits"""
+    be, sk = engine
+    assert be.top_level == 17
+    rng = np.random.default_rng(31)
+    z = rng.uniform(-1, 1, SLOTS)
+    ct = be.encrypt(sk, z, 3)
+    out = be.bootstrap(ct)
+    got = be.decrypt(sk, out)
+    err = np.abs(got - z)
+    bits = -np.log2(err.max())
+    print(f"config-5 chain bootstrap: {bits:.2f} bits (max {err.max():.3e}, rms {np.sqrt(np.mean(err**2)):.3e})")
+    assert bits > 11.0
+
+
+@pytest.mark.timeout(900)
+def test_decode_step_one_layer(engine, DS, M):
+    """one layer, two tokens with the state carried: decrypted output against the float64 model"""
+    from oracle import rwkv_ref as ref
+    be, sk = engine
+    W = M.make_weights(5, n_layers=1)
+    step = DS.DecodeStep(be, W)
+    st = ref.init_state(32, 1)
+    for s in range(2):
+        x = M.embed_tokens(np.arange(32) + 100 * s)
+        out = step(be.encrypt(sk, M.pack_lanes(x), be.top_level, seed=bytes([s]) * 32))
+        xo, _ = ref.step(x, st, W)
+        got = M.unpack_lanes(be.decrypt(sk, out).real)
+        err = np.sqrt(np.mean((got - xo) ** 2)) / np.sqrt(np.mean(xo ** 2))
+        print(f"token {s}: relErrRms {err:.3e}, bootstraps so far {step.stats['bootstraps']}")
+        assert err < 1e-3, err

@@ -268,3 +268,33 @@ def test_rotate_decrypts_to_rotated_message(oracle, small):
         else:
             want[e - N] -= m[j]
     assert np.abs(got - want).max() < 2**25
+
+
+def test_moddown_exact_is_rounded_division(oracle):
+    """exact ModDown (centered conversion) == round(X / P) per coefficient, X the integer whose residues the
+    Q and P limbs hold (closed form by big-integer CRT); the approximate form is floor(X / P) - u, u in [0, K)"""
+    N = 1 << 16
+    qs = oracle.gen_primes(40, 3, 2 * N)
+    ps = oracle.gen_primes(60, 3, 2 * N)
+    l, K = 3, 3
+    ex = oracle.Ctx(16, qs + ps, l, K, 1, moddown_exact=True)
+    ap = oracle.Ctx(16, qs + ps, l, K, 1, moddown_exact=False)
+    P = 1
+    for p in ps:
+        P *= p
+    QP = P
+    for q in qs:
+        QP *= q
+    rng = np.random.default_rng(5)
+    X = [int.from_bytes(rng.bytes(40), "little") % QP for _ in range(N)]
+    coef = np.array([[x % m for x in X] for m in qs + ps], dtype=np.uint64)
+    ev = ex.ntt_fwd(coef, list(range(l + K)))
+    got_ex = ex.ntt_inv(ex.moddown(ev, l), list(range(l)))
+    got_ap = ap.ntt_inv(ap.moddown(ev, l), list(range(l)))
+    for k in range(0, N, 331):
+        r = (X[k] + P // 2) // P  # round(X / P) (P odd: no ties)
+        f = X[k] // P
+        for i, q in enumerate(qs):
+            assert int(got_ex[i, k]) == r % q, (k, i)
+            u = (f - int(got_ap[i, k])) % q
+            assert u < K, (k, i, u)
