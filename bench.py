@@ -282,6 +282,123 @@ def bench_bootstrap(ckks, torch, steps_n, warmup, seed):
                         "double-angle (K=22), StC 3 levels; chain q0 60 + 22x50 + 3x60 bits, P 8x60, dnum 3"}
 
 
+# ----------------------------------------------------------------------------------------- config 5
+DECODE_LANES = 32
+
+
+def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12):
+    """Config 5: one encrypted decode step of the RWKV-7-0.1B-shaped polynomial model (12 layers, 32 lanes in
+    the slots, state carried across steps, state bootstrapped once per layer).  The client side (token
+    embedding + encryption before the step, decryption + the 768 x 65536 vocabulary head after it) is
+    outside the timed region and reported separately."""
+    from engine_loader import load_module
+    DS = load_module("decode_step")
+    M = load_module("rwkv_model")
+    t0 = time.perf_counter()
+    be, sk = DS.build_engine(ckks)
+    t_keys = time.perf_counter() - t0
+    log = lambda msg: print(f"[decode] {msg}", file=sys.stderr, flush=True)
+    log(f"keys ready in {t_keys:.1f} s ({len(be.keys)} rotation keys)")
+    W = M.make_weights(seed + 4, n_layers)
+    step = DS.DecodeStep(be, W)
+    ctx = be.ctx
+    tokens = lambda i: (np.arange(DECODE_LANES) * 7919 + 131 * i + seed) % M.VOCAB
+
+    def client_in(i):
+        x = M.embed_tokens(tokens(i), seed=seed)
+        return x, be.encrypt(sk, M.pack_lanes(x), be.top_level, seed=seed_bytes(f"dec{i}", seed))
+
+    xs, outs, times, ks = [], [], [], []
+    t_enc0 = time.perf_counter()
+    for i in range(warmup):  # the first step also encodes every plaintext (weights, masks) on first use
+        x, ct = client_in(i)
+        xs.append(x)
+        outs.append(step(ct))
+        torch.cuda.synchronize()
+        log(f"warmup step {i} done at {time.perf_counter() - t_enc0:.1f} s")
+    t_warm = time.perf_counter() - t_enc0
+    for i in range(warmup, warmup + steps_n):
+        x, ct = client_in(i)
+        xs.append(x)
+        torch.cuda.synchronize()
+        ctx.key_switches(reset=True)
+        t = time.perf_counter()
+        outs.append(step(ct))
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t)
+        ks.append(ctx.key_switches())
+        log(f"timed step {i}: {times[-1]:.2f} s, {ks[-1]} key switches")
+    # client side of the last step: decrypt, vocabulary head on the plaintext
+    t = time.perf_counter()
+    xo = M.unpack_lanes(be.decrypt(sk, outs[-1]).real)
+    head = M.head_matrix(W)
+    logits = xo @ head.T
+    t_client = time.perf_counter() - t
+    # one profiled step for the kernel table (state keeps carrying)
+    x, ct = client_in(warmup + steps_n)
+    xs.append(x)
+    ctx.profile_reset()
+    ctx.profile(True)
+    outs.append(step(ct))
+    torch.cuda.synchronize()
+    ctx.profile(False)
+    rep = ctx.profile_report()
+    ctx.profile_reset()
+    s_per_step = sum(times) / len(times)
+    return {"s_per_step": round(s_per_step, 3), "key_switches_per_step": int(np.mean(ks)),
+            "bootstraps_per_step": step.stats["bootstraps"] // (warmup + steps_n + 1),
+            "setup_s": {"keys": round(t_keys, 1), "first_steps_with_plaintext_encoding": round(t_warm, 1)},
+            "client_s": {"decrypt_and_vocab_head": round(t_client, 3)},
+            "kernels": kernel_table(rep), "roofline": roofline_from_profile(rep),
+            "_check": {"xs": xs, "outs": outs, "logits": logits, "logits_step": warmup + steps_n - 1, "W": W,
+                       "be": be, "sk": sk, "M": M, "n_steps": warmup + steps_n + 1},
+            "workload": f"config5: RWKV-7-0.1B-shaped decode step, {n_layers} layers, d=768, 12 heads x 64, "
+                        f"degree-3 polynomial nonlinearities (seeded coefficients in [-0.5, 0.5]), 32 lanes in "
+                        f"the slots of one N=2^16 ciphertext, WKV state carried and bootstrapped once per layer; "
+                        f"chain q0 50 + 28 x 40 + 3 x 60 bits, P 7 x 60, dnum 4; sparse-secret bootstrapping"}
+
+
+def cpu_baseline_decode(res, seed, budget_s=15.0):
+    """The oracle's key switch (ModUp + inner product + ModDown) at level 10 of the config-5 chain, single
+    thread, times the step's key-switch count: a lower bound for the step on the CPU (NTT-only, elementwise
+    and encoding work left out).  The same leg checks the decrypted step against the float64 model."""
+    from oracle import oracle as o
+    from oracle import rwkv_ref as ref
+    chk = res["_check"]
+    be = chk["be"]
+    ctx = be.ctx
+    oc = o.Ctx(16, ctx.moduli, ctx.L, ctx.K, ctx.dnum, moddown_exact=True)
+    rng = np.random.default_rng(seed)
+    l = 10
+    q = np.array(ctx.moduli[:l], dtype=np.uint64)[:, None]
+    x = rng.integers(0, 2**62, (l, N), dtype=np.uint64) % q
+    qall = np.array(ctx.moduli, dtype=np.uint64)[None, None, :, None]
+    evk = rng.integers(0, 2**62, (ctx.dnum, 2, ctx.L + ctx.K, N), dtype=np.uint64) % qall[0]
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s or n == 0:
+        oc.keyswitch(x, l, evk)
+        n += 1
+    per_ks = (time.perf_counter() - t0) / n
+    # accuracy of every decrypted step against the float64 model (state carried identically)
+    M = chk["M"]
+    st = ref.init_state(DECODE_LANES, len(chk["W"]["layers"]))
+    errs = []
+    head = M.head_matrix(chk["W"])
+    for i in range(chk["n_steps"]):
+        xo_ref, _ = ref.step(chk["xs"][i], st, chk["W"])
+        got = M.unpack_lanes(be.decrypt(chk["sk"], chk["outs"][i]).real)
+        errs.append(float(np.sqrt(np.mean((got - xo_ref) ** 2)) / np.sqrt(np.mean(xo_ref ** 2))))
+        if i == chk["logits_step"]:
+            lg_ref = xo_ref @ head.T
+    lg_err = float(np.sqrt(np.mean((chk["logits"] - lg_ref) ** 2)) / np.sqrt(np.mean(lg_ref ** 2)))
+    est = per_ks * res["key_switches_per_step"]
+    return {"value": round(est, 1), "unit": "s/step", "cores": 1, "kind": "port",
+            "sample": f"{n} oracle key switches (level 10, config-5 chain, one thread) at {per_ks:.3f} s each x "
+                      f"{res['key_switches_per_step']} key switches per step; a lower bound (leaves out the "
+                      f"NTT-only and elementwise work)"}, {"relErrRms_per_step": [round(e, 6) for e in errs],
+                                                          "logits_relErrRms_last_step": round(lg_err, 6)}
+
+
 # ----------------------------------------------------------------------------------------- config 1
 def ntt_bytes():
     limbs = 2 * N_PAIRS * L2
@@ -358,7 +475,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="hmult", choices=["hmult", "ntt", "pcmm", "bootstrap"])
+    ap.add_argument("--workload", default="hmult", choices=["hmult", "ntt", "pcmm", "bootstrap", "decode"])
+    ap.add_argument("--layers", type=int, default=12, help="decode workload: layers (12 = config 5)")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ntt-line", action="store_true", help="skip the config-1 NTT figure in the hmult run")
@@ -390,6 +508,18 @@ def main():
             extra["bootstrap_config4"] = {k: b[k] for k in ("ms_per_bootstrap", "precision_bits", "levels_in_out",
                                                              "roofline")}
         cpu = None if args.no_cpu_baseline else cpu_baseline_hmult(args.seed)
+    elif args.workload == "decode":
+        d = bench_decode(ckks, torch, args.steps, args.warmup, args.seed, args.layers)
+        res = {"metric": "s/step for 32-lane decode (config 5)", "value": d["s_per_step"], "unit": "s/step",
+               "ms_per_step": round(d["s_per_step"] * 1e3, 1), "dtype": "u64",
+               "config": {"workload": d["workload"], "lanes": DECODE_LANES, "layers": args.layers},
+               "kernels": d["kernels"], "roofline": d["roofline"],
+               "check": {k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s")}}
+        extra = {}
+        cpu = None
+        if not args.no_cpu_baseline:
+            cpu, acc = cpu_baseline_decode(d, args.seed)
+            res["check"].update(acc)
     elif args.workload == "bootstrap":
         b = bench_bootstrap(ckks, torch, args.steps, args.warmup, args.seed)
         res = {"metric": "bootstrap ms (full-slot, N=2^16)", "value": b["ms_per_bootstrap"], "unit": "ms",
@@ -410,7 +540,7 @@ def main():
         cpu = None if args.no_cpu_baseline else cpu_baseline_ntt(args.seed)
     out = {"metric": res["metric"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
-           "higher_is_better": res["unit"] != "ms", "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
+           "higher_is_better": res["unit"] not in ("ms", "s/step"), "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
            "data": "synthetic (seeded)", "config": res["config"], "roofline": res["roofline"],
            "kernels": res["kernels"]}
     if "check" in res:

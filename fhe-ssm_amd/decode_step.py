@@ -13,20 +13,19 @@ unpacked state (2 S(l)).  An operand above the level of its partner is brought d
 multiplication that lands on the canonical scale (one rescale); products then land on S(l-1).
 Plaintexts applied at level l are encoded at scale S(l), which keeps the product canonical.
 
-Refresh policy: the residual stream is bootstrapped before the time mix and before the channel mix when
-fewer levels remain than the block needs; the carried WKV state is bootstrapped once per layer, packed
-two per ciphertext (D_t + i D_{t+32}) and unpacked with one conjugation.
+Refresh policy: the residual stream x never leaves the top level.  Each block's increment (o from the time
+mix, f from the channel mix) comes out at a low level, is bootstrapped on its own and added to x there, so
+x itself is never bootstrapped: the sine of EvalMod shrinks large coefficients slightly (a coherent
+relative error ~(2 pi m / q0)^2 / 6), and the increments are ~5-100x smaller than x.  Each increment kind
+has its own bootstrapping plan whose input scale suits its magnitude (more signal over EvalMod's noise).
+The carried WKV state is bootstrapped once per layer, packed two per ciphertext (D_t + i D_{t+32}) and
+unpacked with one conjugation.  34 bootstraps per layer.
 """
 from __future__ import annotations
 
 import numpy as np
 
 import rwkv_model as M
-
-# levels the two blocks consume from their input (checked by the plan at run time)
-TIME_MIX_DEPTH = 14
-CHANNEL_MIX_DEPTH = 9
-OUTPUT_DEPTH = 6
 
 
 class Backend:
@@ -152,15 +151,13 @@ class DecodeStep:
         n = be.poly3(s, pcoef)
         return be.mul(x, n)
 
-    def _refresh(self, x, need):
-        if x.level - 1 >= need:
-            return x
+    def _boot(self, x, kind):
         self.stats["bootstraps"] += x.B
-        return self.be.bootstrap(x)
+        return self.be.bootstrap(x, kind)
 
     def _time_mix(self, li, x, st):
+        """the time-mix increment o (x + o is the layer's residual)"""
         be, L = self.be, self.W["layers"][li]
-        x = self._refresh(x, TIME_MIX_DEPTH)
         xn = self._norm(x, L["p_n1"], "n1")
         xp = st["xp_t"]
         lv = min(xn.level, xp.level)
@@ -195,11 +192,11 @@ class DecodeStep:
         o = be.matvec([yg], self._mv_pt(f"wo{li}", yg.level, lambda: [[L["W_o"]]]))
         st["xp_t"] = xn
         st["Dn"] = Dn
-        return be.add(x, o)
+        return o
 
     def _channel_mix(self, li, x, st):
+        """the channel-mix increment f"""
         be, L = self.be, self.W["layers"][li]
-        x = self._refresh(x, CHANNEL_MIX_DEPTH)
         xn2 = self._norm(x, L["p_n2"], "n2")
         xp = st["xp_c"]
         lv = min(xn2.level, xp.level)
@@ -214,7 +211,7 @@ class DecodeStep:
         f = be.matvec([be.item(h, i) for i in range(4)],
                       self._mv_pt(f"cv{li}", h.level, lambda: [[L["W_cv"][:, i * M.D:(i + 1) * M.D] for i in range(4)]]))
         st["xp_c"] = xn2
-        return be.add(x, f)
+        return f
 
     def _refresh_state(self, st):
         """bootstrap the new state once: pack D_t + i D_{t+32}, bootstrap 32, unpack with one conjugation"""
@@ -224,7 +221,7 @@ class DecodeStep:
         lo, hi = be.slice(Dn, 0, h), be.slice(Dn, h, 2 * h)
         packed = be.add(lo, be.mul_i(hi, 1))
         self.stats["bootstraps"] += packed.B
-        P = be.bootstrap(packed)
+        P = be.bootstrap(packed, "state")
         C = be.conj(P)
         re2 = be.add(P, C)                 # 2 Re
         im2 = be.mul_i(be.add(C, P, -1), 1)  # i (conj - P) = 2 Im
@@ -240,12 +237,12 @@ class DecodeStep:
         """x: ciphertext of the lanes' embeddings; returns the ciphertext of the output-normed hidden state"""
         if self.state is None:
             self.state = self.cold_state()
+        be = self.be
         for li in range(self.n_layers):
             st = self.state[li]
-            x = self._time_mix(li, x, st)
+            x = be.add(x, self._boot(self._time_mix(li, x, st), "inc_tm"))
             self._refresh_state(st)
-            x = self._channel_mix(li, x, st)
-        x = self._refresh(x, OUTPUT_DEPTH)
+            x = be.add(x, self._boot(self._channel_mix(li, x, st), "inc_cm"))
         xo = self._norm(x, self.W["p_o"], "out")
         return self.be.mul_pt(xo, self._vec_pt("g_o", xo.level, M.periodic(self.W["g_o"])))
 
@@ -292,15 +289,16 @@ class HEBackend(Backend):
     """Decode-step primitives on the GPU engine (through ckks.py and the C ABI)."""
     N = 1 << 16
 
-    def __init__(self, ckks, ctx, boot, in_scale, relin, conj, keys: dict):
-        self.ckks, self.ctx, self.boot = ckks, ctx, boot
+    def __init__(self, ckks, ctx, boots: dict, relin, conj, keys: dict):
+        """boots: refresh kind -> (bootstrapping plan, its input scale); kind "state" must be present"""
+        self.ckks, self.ctx, self.boots = ckks, ctx, boots
+        boot = boots["state"][0]
         self.relin, self.conj_key, self.keys = relin, conj, keys
         self.top_level = boot.out_level
         self.pool = _Pool(ckks)
         self._S = {l: boot.scale(l) for l in range(1, boot.out_level + 1)}
-        self.in_scale = in_scale
         self.moduli = ctx.moduli
-        self.boot_keys = {s: keys[s] for s in boot.steps}
+        self.boot_keys = {k: {s: keys[s] for s in b.steps} for k, (b, _) in boots.items()}
 
     def S(self, level):
         return self._S[level]
@@ -437,11 +435,13 @@ class HEBackend(Backend):
         self.ctx.eval_automorphism_ks(a.ptr(), a.B, a.level, 2 * self.N - 1, self.conj_key, out.ptr())
         return out
 
-    def bootstrap(self, a):
-        lo = self.at_scale(a, 1, self.in_scale)
+    def bootstrap(self, a, kind="state"):
+        boot, in_scale = self.boots.get(kind, self.boots["state"])
+        keys = self.boot_keys.get(kind, self.boot_keys["state"])
+        lo = self.at_scale(a, 1, in_scale)
         out = self._new(a.B, self.top_level, self.S(self.top_level))
         for b in range(a.B):
-            self.boot.run(lo.ptr(b), self.relin, self.conj_key, self.boot_keys, out.ptr(b))
+            boot.run(lo.ptr(b), self.relin, self.conj_key, keys, out.ptr(b))
         return out
 
     def at_scale(self, a, lt, scale):
@@ -512,10 +512,17 @@ def build_engine(ckks, secret_seed=b"S" * 32, n_keys_seed=7, steps=None):
     """Context, bootstrapping plan, secret and every key the decode step uses; returns (backend, secret)."""
     ctx = ckks.Context(num_q=32, num_p=7, dnum=4, scale=2.0**40, moduli=config5_moduli(ckks))
     ctx.set_moddown_exact(True)  # unbiased key-switch rounding: the 2^40 chain bootstraps to ~13 bits with it
-    in_scale = 2.0**49  # bootstrap inputs enter at q0 / 2 (as OpenFHE: q0 ~ 2 Delta)
     # sparse-secret encapsulation (h' = 32): |I| <= ~8 sigma = 8 sqrt(33/12) ~ 13, so K = 14 and two double
-    # angles suffice (EvalMod's noise grows as K^2)
-    boot = ckks.Bootstrap(ctx, K=14.0, cheb_degree=59, double_angles=2, top_scale=2.0**52, in_scale=in_scale)
+    # angles suffice (EvalMod's noise grows as K^2).  One plan per refresh kind, differing only in the input
+    # scale: the state and the channel-mix increment (|f| <= ~0.6) enter at q0 (m/q0 stays ~1e-3 per
+    # coefficient), the time-mix increment (|o| <= ~0.05) at 8 q0: more signal over EvalMod's noise.
+    plans = {}
+    for kind, ins in (("state", 2.0**50), ("inc_cm", 2.0**50), ("inc_tm", 2.0**53)):
+        if ins not in [v[1] for v in plans.values()]:
+            b = ckks.Bootstrap(ctx, K=14.0, cheb_degree=59, double_angles=2, top_scale=2.0**52, in_scale=ins)
+        else:
+            b = next(v[0] for v in plans.values() if v[1] == ins)
+        plans[kind] = (b, ins)
     sk = ctx.secret(secret_seed, 192)
     sk_sparse = ctx.secret(bytes(reversed(secret_seed)), 32)
     kb = ctx.dnum * 2 * (ctx.L + ctx.K) * ctx.N * 8
@@ -523,12 +530,14 @@ def build_engine(ckks, secret_seed=b"S" * 32, n_keys_seed=7, steps=None):
     ctx.keygen_switch(sk, sk_sparse, b"t" * 32, b"u" * 32, to_sparse.ptr, q_limbs=1)
     from_sparse = ckks.DeviceBuffer(kb)
     ctx.keygen_switch(sk_sparse, sk, b"v" * 32, b"w" * 32, from_sparse.ptr)
-    boot.set_sparse_keys(to_sparse.ptr, from_sparse.ptr)
+    for b, _ in plans.values():
+        b.set_sparse_keys(to_sparse.ptr, from_sparse.ptr)
     relin = ckks.DeviceBuffer(kb)
     ctx.keygen_relin(sk, b"r" * 32, b"s" * 32, relin.ptr)
     conj = ckks.DeviceBuffer(kb)
     ctx.keygen_automorphism(sk, 2 * ctx.N - 1, b"c" * 32, b"d" * 32, conj.ptr)
-    want = sorted(set(M.rotation_steps() if steps is None else steps) | set(boot.steps))
+    want = sorted(set(M.rotation_steps() if steps is None else steps) |
+                  set(s for b, _ in plans.values() for s in b.steps))
     keys, bufs = {}, []
     for i, s in enumerate(want):
         b = ckks.DeviceBuffer(kb)
@@ -537,6 +546,6 @@ def build_engine(ckks, secret_seed=b"S" * 32, n_keys_seed=7, steps=None):
                                 bytes([n_keys_seed]) + tag + b"e" * 29, b.ptr)
         keys[s] = b.ptr
         bufs.append(b)
-    be = HEBackend(ckks, ctx, boot, in_scale, relin.ptr, conj.ptr, keys)
+    be = HEBackend(ckks, ctx, plans, relin.ptr, conj.ptr, keys)
     be._owned = (relin, conj, bufs, to_sparse, from_sparse, sk_sparse)  # keep the keys alive with the backend
     return be, sk

@@ -156,7 +156,7 @@ class SlotBackend(DS.Backend):
     def conj(self, a):
         return SimCt(np.conj(a.v), a.level, a.scale)
 
-    def bootstrap(self, a):
+    def bootstrap(self, a, kind="state"):
         assert a.level >= 2
-        self.log.append(("bootstrap", a.B, a.level))
+        self.log.append(("bootstrap", kind, a.B, a.level))
         return SimCt(a.v, self.top_level)

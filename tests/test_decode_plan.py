@@ -49,17 +49,18 @@ def test_matvec_diagonals():
 @pytest.mark.timeout(300)
 def test_decode_step_plan_matches_reference():
     W = M.make_weights(5, n_layers=1)
-    be = SlotBackend(16)
+    be = SlotBackend(17)
     step = DS.DecodeStep(be, W)
     st = ref.init_state(32, 1)
     for s in range(2):
         x = M.embed_tokens(np.arange(32) + 100 * s)
-        out = step(be.encrypt(None, M.pack_lanes(x), 16))
+        out = step(be.encrypt(None, M.pack_lanes(x), 17))
         xo, _ = ref.step(x, st, W)
         got = M.unpack_lanes(be.decrypt(None, out))
         assert np.max(np.abs(got - xo)) < 1e-12
         assert np.max(np.abs(be.decrypt(None, out).reshape(32, 1024)[:, 768:])) == 0
         assert np.allclose(M.diag_to_state(step.state[0]["D"].v.real), st[0]["S"], atol=1e-14)
-    # one refresh of the residual before the channel mix and the 32 packed state ciphertexts, per step
-    assert step.stats["bootstraps"] == 2 * 33
-    assert out.level == 1
+    # per layer and step: the two increments and the 32 packed state ciphertexts; the residual stays on top
+    assert step.stats["bootstraps"] == 2 * 34
+    assert [e[1] for e in be.log[:3]] == ["inc_tm", "state", "inc_cm"]
+    assert out.level == 11

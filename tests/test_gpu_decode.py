@@ -241,7 +241,7 @@ def test_config5_chain_bootstrap(engine):
     rng = np.random.default_rng(31)
     z = rng.uniform(-1, 1, SLOTS)
     ct = be.encrypt(sk, z, 3)
-    out = be.bootstrap(ct)
+    out = be.bootstrap(ct, "state")
     got = be.decrypt(sk, out)
     err = np.abs(got - z)
     bits = -np.log2(err.max())
@@ -265,3 +265,26 @@ def test_decode_step_one_layer(engine, DS, M):
         err = np.sqrt(np.mean((got - xo) ** 2)) / np.sqrt(np.mean(xo ** 2))
         print(f"token {s}: relErrRms {err:.3e}, bootstraps so far {step.stats['bootstraps']}")
         assert err < 1e-3, err
+
+
+@pytest.mark.timeout(900)
+def test_decode_step_full_config5(engine, DS, M):
+    """the full config-5 step: 12 layers, two tokens (cold start, then the carried state); decrypted output
+    and the client's vocabulary logits against the float64 model, relErrRms <= 1e-3"""
+    from oracle import rwkv_ref as ref
+    be, sk = engine
+    W = M.make_weights(9, n_layers=12)
+    step = DS.DecodeStep(be, W)
+    st = ref.init_state(32, 12)
+    head = M.head_matrix(W, rows=4096)
+    for s in range(2):
+        x = M.embed_tokens(np.arange(32) * 3 + 1000 * s)
+        out = step(be.encrypt(sk, M.pack_lanes(x), be.top_level, seed=bytes([9, s]) * 16))
+        xo, _ = ref.step(x, st, W)
+        got = M.unpack_lanes(be.decrypt(sk, out).real)
+        err = np.sqrt(np.mean((got - xo) ** 2)) / np.sqrt(np.mean(xo ** 2))
+        lg, lg_ref = got @ head.T, xo @ head.T
+        lerr = np.sqrt(np.mean((lg - lg_ref) ** 2)) / np.sqrt(np.mean(lg_ref ** 2))
+        print(f"token {s}: relErrRms {err:.3e}, logits (4096-row slice) {lerr:.3e}")
+        assert err < 1e-3 and lerr < 1e-3, (err, lerr)
+    assert step.stats["bootstraps"] == 2 * 12 * 34
