@@ -94,6 +94,7 @@ SIGNATURES = {
     "ckks_set_moddown_exact": (_int, [_vp, _int]),
     "ckks_keygen_switch": (_int, [_vp, _vp, _vp, _vp, _vp, _u32, _vp]),
     "ckks_bootstrap_set_sparse_keys": (_int, [_vp, _vp, _vp]),
+    "ckks_eval_bootstrap_many": (_int, [_vp, _vp, _vp, _u32, _vp, _vp, _vp, _vp, _u32, _vp, _vp]),
     "ckks_profile_enable": (_int, [_vp, _int]),
     "ckks_profile_reset": (_int, [_vp]),
     "ckks_profile_query": (_int, [_vp, _u32, ctypes.c_char_p, _u32, _vp, _vp, _vp]),
@@ -482,6 +483,11 @@ class Bootstrap:
         steps = np.ascontiguousarray(np.asarray(list(keys.keys()), dtype=np.int64))
         check(load().ckks_eval_bootstrap(self.ctx.h, self.h, d_ct_in, d_relin, d_conj, _ptr(steps), _ptr_array(
             list(keys.values())), len(steps), d_out, stream))
+
+    def run_many(self, d_ct_in, batch, d_relin, d_conj, keys: dict, d_out, stream=None):
+        steps = np.ascontiguousarray(np.asarray(list(keys.keys()), dtype=np.int64))
+        check(load().ckks_eval_bootstrap_many(self.ctx.h, self.h, d_ct_in, batch, d_relin, d_conj, _ptr(steps),
+                                              _ptr_array(list(keys.values())), len(steps), d_out, stream))
 
     def run_stage(self, d_ct_in, d_relin, d_conj, keys: dict, stage: int, d_out) -> int:
         steps = np.ascontiguousarray(np.asarray(list(keys.keys()), dtype=np.int64))

@@ -716,7 +716,25 @@ int ckks_eval_bootstrap(ckks_context* ctx, const ckks_bootstrap* bt, const uint6
     for (uint32_t i = 0; i < n_keys; i++)
         if (!d_evks[i]) return fail(CKKS_EINVAL, "null key");
     return guarded([&] {
-        fhe::bootstrap(ctx->c, *bt->p, d_ct_in, d_relin, d_conj, steps, d_evks, n_keys, d_out, (hipStream_t)stream);
+        fhe::bootstrap(ctx->c, *bt->p, d_ct_in, 1, d_relin, d_conj, steps, d_evks, n_keys, d_out,
+                       (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_eval_bootstrap_many(ckks_context* ctx, const ckks_bootstrap* bt, const uint64_t* d_ct_in, uint32_t batch,
+                             const uint64_t* d_relin, const uint64_t* d_conj, const int64_t* steps,
+                             const uint64_t* const* d_evks, uint32_t n_keys, uint64_t* d_out, void* stream) {
+    if (!ctx || !bt || bt->owner != ctx) return fail(CKKS_EINVAL, "null context or plan of another context");
+    if (!d_ct_in || !d_relin || !d_conj || !d_out || (n_keys && (!steps || !d_evks)))
+        return fail(CKKS_EINVAL, "null argument");
+    if (batch > 64) return fail(CKKS_EINVAL, "at most 64 ciphertexts per call");
+    for (uint32_t i = 0; i < n_keys; i++)
+        if (!d_evks[i]) return fail(CKKS_EINVAL, "null key");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::bootstrap(ctx->c, *bt->p, d_ct_in, batch, d_relin, d_conj, steps, d_evks, n_keys, d_out,
+                       (hipStream_t)stream);
         return CKKS_OK;
     });
 }
@@ -730,7 +748,7 @@ int ckks_eval_bootstrap_stage(ckks_context* ctx, const ckks_bootstrap* bt, const
         return fail(CKKS_EINVAL, "null argument");
     if (stage < 1 || stage > 6) return fail(CKKS_EINVAL, "stage must be in [1, 6]");
     return guarded([&] {
-        *level = fhe::bootstrap(ctx->c, *bt->p, d_ct_in, d_relin, d_conj, steps, d_evks, n_keys, d_out, nullptr,
+        *level = fhe::bootstrap(ctx->c, *bt->p, d_ct_in, 1, d_relin, d_conj, steps, d_evks, n_keys, d_out, nullptr,
                                 stage);
         return CKKS_OK;
     });

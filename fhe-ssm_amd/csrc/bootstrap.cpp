@@ -463,13 +463,16 @@ private:
 }  // namespace
 
 // ct_in: [2][1][N] (the q0 limb), message scale P.in_scale.  out: [2][P.l_out][N], scale S(l_out).
-// stop_stage (testing): 1 after ModRaise, 2 after CoeffToSlot, 3 after the split (batch of 2), 4 after EvalMod
-// (batch of 2), 5 after the recombination, 0 or 6 the full bootstrap.  Returns the level of what it wrote.
-uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, const uint64_t* relin,
+// B independent ciphertexts in one pass: every kernel runs over the whole batch and reads each key and
+// plaintext diagonal once per pass.  ct_in: [B][2][1][N]; out: [B][2][l_out][N].
+// stop_stage (testing): 1 after ModRaise, 2 after CoeffToSlot (Re + i Im), 3 after the split ([Re][B], [Im][B]),
+// 4 after EvalMod (same layout), 5 after the recombination, 0 or 6 the full bootstrap.  Returns the level.
+uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint32_t B, const uint64_t* relin,
                    const uint64_t* conj_evk, const int64_t* steps, const uint64_t* const* evks, uint32_t n_keys,
                    uint64_t* out, hipStream_t st, uint32_t stop_stage) {
-    auto emit = [&](const uint64_t* src, uint32_t B, uint32_t l) {
-        HIPB(hipMemcpyAsync(out, src, (size_t)B * 2 * l * W * 8, hipMemcpyDeviceToDevice, st));
+    if (B == 0) return P.l_out;
+    auto emit = [&](const uint64_t* src, uint32_t n, uint32_t l) {
+        HIPB(hipMemcpyAsync(out, src, (size_t)n * 2 * l * W * 8, hipMemcpyDeviceToDevice, st));
         HIPB(hipStreamSynchronize(st));
         return l;
     };
@@ -478,56 +481,58 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, const
     for (uint32_t i = 0; i < n_keys; i++) key[steps[i]] = evks[i];
     for (auto s : P.steps)
         if (!key.count(s)) throw std::invalid_argument("missing rotation key for step " + std::to_string(s));
-    Eval ev1(ctx, P, 1, relin, st), ev2(ctx, P, 2, relin, st);
+    Eval ev1(ctx, P, B, relin, st), ev2(ctx, P, 2 * B, relin, st);
     // ---- ModRaise: centered q0 limb -> all L limbs
     HCt raised = ev1.get(L);
     {
         uint64_t* last = raised.d;  // staging: the two q0 limbs, then lifted in place of the output
         HCt stage = ev1.get(1);
         if (P.sse_to) {
-            // sparse-secret encapsulation: switch the q0 ciphertext to the sparse secret, so that the raised
+            // sparse-secret encapsulation: switch the q0 ciphertexts to the sparse secret, so that the raised
             // message m + q0 I has a small I (K bounds it), then switch back at the top level below
             HCt c1 = ev1.get(1);
-            HIPB(hipMemcpyAsync(c1.d, ct_in + W, W * 8, hipMemcpyDeviceToDevice, st));
-            keyswitch(ctx, c1.d, 1, 1, P.sse_to, ct_in, stage.d, st, 2);
+            HIPB(hipMemcpy2DAsync(c1.d, W * 8, ct_in + W, 2 * W * 8, W * 8, B, hipMemcpyDeviceToDevice, st));
+            keyswitch(ctx, c1.d, B, 1, P.sse_to, ct_in, stage.d, st, 2);
             ev1.put(c1);
         } else {
-            HIPB(hipMemcpyAsync(stage.d, ct_in, 2 * W * 8, hipMemcpyDeviceToDevice, st));
+            HIPB(hipMemcpyAsync(stage.d, ct_in, (size_t)B * 2 * W * 8, hipMemcpyDeviceToDevice, st));
         }
         JobSpec js{};
-        js.n_polys = 2;
+        js.n_polys = 2 * B;
         js.period = 1;
         js.pmap[0] = 0;
-        HIPB(launch_ntt(ctx, stage.d, js, 2, true, ctx.ntt_mode, st));
-        HIPB(launch_lift_centered(ctx, stage.d, W, last, 2, L, ctx.moduli[0], st));
+        HIPB(launch_ntt(ctx, stage.d, js, 2 * B, true, ctx.ntt_mode, st));
+        HIPB(launch_lift_centered(ctx, stage.d, W, last, 2 * B, L, ctx.moduli[0], st));
         JobSpec jl{};
-        jl.n_polys = 2;
+        jl.n_polys = 2 * B;
         jl.period = L;
         for (uint32_t i = 0; i < L; i++) jl.pmap[i] = (uint8_t)i;
-        HIPB(launch_ntt(ctx, raised.d, jl, 2 * L, false, ctx.ntt_mode, st));
+        HIPB(launch_ntt(ctx, raised.d, jl, 2 * B * L, false, ctx.ntt_mode, st));
         ev1.put(stage);
         if (P.sse_from) {
             HCt c1 = ev1.get(L), back = ev1.get(L);
-            HIPB(hipMemcpyAsync(c1.d, raised.d + (size_t)L * W, (size_t)L * W * 8, hipMemcpyDeviceToDevice, st));
-            keyswitch(ctx, c1.d, 1, L, P.sse_from, raised.d, back.d, st, 2);
+            HIPB(hipMemcpy2DAsync(c1.d, (size_t)L * W * 8, raised.d + (size_t)L * W, (size_t)2 * L * W * 8,
+                                  (size_t)L * W * 8, B, hipMemcpyDeviceToDevice, st));
+            keyswitch(ctx, c1.d, B, L, P.sse_from, raised.d, back.d, st, 2);
             ev1.put(c1);
             ev1.put(raised);
             raised = back;
         }
     }
-    if (stop_stage == 1) return emit(raised.d, 1, L);
-    // ---- CoeffToSlot
-    auto apply_level = [&](Eval& ev, const HCt& in, const BootLevel& bl) {
-        if (in.l != bl.l) throw std::logic_error("linear transform level mismatch");
-        std::vector<const uint64_t*> bk, gk;
+    if (stop_stage == 1) return emit(raised.d, B, L);
+    // ---- CoeffToSlot: one BSGS level per call over the batch (diagonals and keys shared), then rescale
+    auto keys_of = [&](const BootLevel& bl, std::vector<const uint64_t*>& bk, std::vector<const uint64_t*>& gk) {
         for (auto s : bl.bsteps) bk.push_back(s ? key[s] : nullptr);
         for (auto s : bl.gsteps) gk.push_back(s ? key[s] : nullptr);
-        HCt acc = ev.get(bl.l);
-        bsgs_general(ctx, in.d, bl.l, bl.d_diags, bl.nb, bl.bsteps.data(), bk.data(), bl.ng, bl.gsteps.data(),
-                     gk.data(), acc.d, st);
+    };
+    auto apply_level = [&](Eval& ev, const HCt& in, const BootLevel& bl) {
+        if (in.l != bl.l) throw std::logic_error("linear transform level mismatch");
+        std::vector<const uint64_t*> bk, gk, ins(B);
+        keys_of(bl, bk, gk);
+        for (uint32_t b = 0; b < B; b++) ins[b] = in.d + (size_t)b * 2 * bl.l * W;
         HCt o = ev.get(bl.l - 1);
-        rescale(ctx, acc.d, 2, bl.l, o.d, st);
-        ev.put(acc);
+        bsgs_multi_batch(ctx, ins.data(), B, 1, bl.l, bl.d_diags, bl.nb, bl.bsteps.data(), bk.data(), bl.ng,
+                         bl.gsteps.data(), gk.data(), 1, true, o.d, st, 0, false);
         return o;
     };
     HCt x = raised;
@@ -536,38 +541,46 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, const
         ev1.put(x);
         x = y;
     }
-    // ---- last CoeffToSlot level with the split into real parts folded in: [2 Re t, 2 Im t] as a batch of
-    // two (the 1/2 is in the first level's constant)
+    // ---- last CoeffToSlot level with the split into real parts folded in: [2 Re t][B] then [2 Im t][B] as
+    // one batch of 2B (the 1/2 is in the first level's constant)
     const BootLevel& bs = P.cts.back();
     if (x.l != bs.l || bs.n_in != 2 || bs.n_out != 2) throw std::logic_error("split level mismatch");
     const uint32_t lm = bs.l - 1;
     HCt pair = ev2.get(lm);
     {
         HCt cj = ev1.get(bs.l);
-        const uint32_t g = 2 * kN - 1;
-        const uint64_t* ck[1] = {conj_evk};
-        automorph_ks_list(ctx, x.d, 1, bs.l, &g, ck, cj.d, st);
-        std::vector<const uint64_t*> bk, gk;
-        for (auto s : bs.bsteps) bk.push_back(s ? key[s] : nullptr);
-        for (auto s : bs.gsteps) gk.push_back(s ? key[s] : nullptr);
-        const uint64_t* ins[2] = {x.d, cj.d};
-        bsgs_multi(ctx, ins, 2, bs.l, bs.d_diags, bs.nb, bs.bsteps.data(), bk.data(), bs.ng, bs.gsteps.data(),
-                   gk.data(), 2, true, pair.d, st, 0);
+        std::vector<uint32_t> g(B, 2 * kN - 1);
+        std::vector<const uint64_t*> ck(B, conj_evk);
+        automorph_ks_list(ctx, x.d, B, bs.l, g.data(), ck.data(), cj.d, st);
+        std::vector<const uint64_t*> bk, gk, ins(2 * B);
+        keys_of(bs, bk, gk);
+        for (uint32_t b = 0; b < B; b++) {
+            ins[2 * b] = x.d + (size_t)b * 2 * bs.l * W;
+            ins[2 * b + 1] = cj.d + (size_t)b * 2 * bs.l * W;
+        }
+        bsgs_multi_batch(ctx, ins.data(), B, 2, bs.l, bs.d_diags, bs.nb, bs.bsteps.data(), bk.data(), bs.ng,
+                         bs.gsteps.data(), gk.data(), 2, true, pair.d, st, 0, true);
         ev1.put(cj);
         ev1.put(x);
     }
+    // Re[b] + i Im[b] over the batch (pair holds the Re block then the Im block)
+    auto recombine = [&](const HCt& re_im, uint32_t l) {
+        const size_t half = (size_t)B * 2 * l * W;
+        HCt im = ev1.get(l), z = ev1.get(l);
+        HIPB(launch_mul_i(ctx, re_im.d + half, im.d, 2 * B, l, 1, st));
+        const uint64_t* xs[2] = {re_im.d, im.d};
+        const uint32_t strides[2] = {l, l};
+        std::vector<uint64_t> C(2 * l, 1);
+        HIPB(launch_lincomb(ctx, z.d, B, l, 2, xs, strides, C.data(), nullptr, st));
+        ev1.put(im);
+        return z;
+    };
     if (stop_stage == 2) {  // the CoeffToSlot output itself: Re + i Im
-        const size_t cw = (size_t)2 * lm * W;
-        HCt im = ev1.get(lm), z = ev1.get(lm);
-        HIPB(launch_mul_i(ctx, pair.d + cw, im.d, 2, lm, 1, st));
-        const uint64_t* xs[2] = {pair.d, im.d};
-        const uint32_t strides[2] = {lm, lm};
-        std::vector<uint64_t> C(2 * lm, 1);
-        HIPB(launch_lincomb(ctx, z.d, 1, lm, 2, xs, strides, C.data(), nullptr, st));
-        return emit(z.d, 1, lm);
+        HCt z = recombine(pair, lm);
+        return emit(z.d, B, lm);
     }
-    if (stop_stage == 3) return emit(pair.d, 2, pair.l);
-    // ---- EvalMod on both halves
+    if (stop_stage == 3) return emit(pair.d, 2 * B, pair.l);
+    // ---- EvalMod on both halves of every ciphertext
     HCt y = ev2.chebyshev(pair, P.cheb);
     ev2.put(pair);
     for (int k = 0; k < P.r; k++) {
@@ -577,31 +590,21 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, const
         ev2.put(y);
         y = z;
     }
-    if (stop_stage == 4) return emit(y.d, 2, y.l);
+    if (stop_stage == 4) return emit(y.d, 2 * B, y.l);
     // ---- recombine Re + i Im at the StC input level
     const uint32_t ls = P.stc[0].l;
     HCt ya = y.l == ls ? y : ev2.adjust(y, ls);
     if (ya.d != y.d) ev2.put(y);
-    HCt z = ev1.get(ls);
-    {
-        const size_t cw = (size_t)2 * ls * W;
-        HCt im = ev1.get(ls);
-        HIPB(launch_mul_i(ctx, ya.d + cw, im.d, 2, ls, 1, st));
-        const uint64_t* xs[2] = {ya.d, im.d};
-        const uint32_t strides[2] = {ls, ls};
-        std::vector<uint64_t> C(2 * ls, 1);
-        HIPB(launch_lincomb(ctx, z.d, 1, ls, 2, xs, strides, C.data(), nullptr, st));
-        ev1.put(im);
-        ev2.put(ya);
-    }
-    if (stop_stage == 5) return emit(z.d, 1, z.l);
+    HCt z = recombine(ya, ls);
+    ev2.put(ya);
+    if (stop_stage == 5) return emit(z.d, B, z.l);
     // ---- SlotToCoeff
     for (auto& bl : P.stc) {
         HCt w = apply_level(ev1, z, bl);
         ev1.put(z);
         z = w;
     }
-    const uint32_t lo = emit(z.d, 1, z.l);
+    const uint32_t lo = emit(z.d, B, z.l);
     ev1.put(z);
     return lo;
 }

@@ -32,7 +32,7 @@ struct BootPlan {
 
 BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scale, double in_scale);
 void bootstrap_plan_destroy(BootPlan* P);
-uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, const uint64_t* relin,
+uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint32_t B, const uint64_t* relin,
                    const uint64_t* conj_evk, const int64_t* steps, const uint64_t* const* evks, uint32_t n_keys,
                    uint64_t* out, hipStream_t st, uint32_t stop_stage = 0);
 

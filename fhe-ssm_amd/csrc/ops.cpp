@@ -34,7 +34,7 @@ hipError_t launch_ks_inner(const Context& ctx, const uint64_t* ext, const uint64
 hipError_t launch_sub_scale(const Context& ctx, const uint64_t* x, uint64_t x_pstride, const uint64_t* y,
                             uint64_t y_pstride, const uint64_t* add, uint64_t add_pstride, uint32_t add_div,
                             uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
-                            hipStream_t st);
+                            hipStream_t st, uint32_t add_group = 0);
 hipError_t launch_lift_centered(const Context& ctx, const uint64_t* last, uint64_t last_pstride, uint64_t* tmp,
                                 uint32_t n_polys, uint32_t n_out, uint64_t ql, hipStream_t st);
 hipError_t launch_add(const Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys,
@@ -240,7 +240,7 @@ void ks_inner(Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* 
 // x: [n_polys][E][N] evaluation form over Q_l * P (P limbs are overwritten: they are transformed to
 // coefficients in place).  out: [n_polys][l][N] = (x_Q - BConv_{P->Q}(x_P)) * P^-1 (+ add).
 void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
-                     hipStream_t st, uint32_t add_div, int64_t add_pstride) {
+                     hipStream_t st, uint32_t add_div, int64_t add_pstride, uint32_t add_group) {
     check_level(ctx, l);
     const uint32_t E = l + ctx.K, K = ctx.K;
     if (K == 0) throw std::invalid_argument("ModDown needs special primes");
@@ -273,7 +273,7 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
     }
     const uint64_t aps = add_pstride < 0 ? (uint64_t)add_div * l * W : (uint64_t)add_pstride;
     HIPX(launch_sub_scale(ctx, x, (uint64_t)E * W, conv, (uint64_t)l * W, add, aps, add_div, out, (uint64_t)l * W,
-                          n_polys, l, pinv.data(), st));
+                          n_polys, l, pinv.data(), st, add_group));
 }
 
 // ------------------------------------------------------------------ key switch
@@ -468,6 +468,44 @@ void rotate_hoisted_ext(Context& ctx, const uint64_t* ct, const uint64_t* ext, u
     HIPX(launch_automorph_list(ctx, ks, out, n, l, g.data(), st));
 }
 
+// n_ct ciphertexts [n_ct][2][l][N], each rotated by the same n steps over one ModUp of its own:
+// out [n_ct][n][2][l][N].  The inner products of up to 64 (ciphertext, step) pairs run as one list.
+void rotate_hoisted_multi(Context& ctx, const uint64_t* cts, uint32_t n_ct, uint32_t l, const int64_t* steps,
+                          uint32_t n, const uint64_t* const* evk, uint64_t* out, hipStream_t st) {
+    check_level(ctx, l);
+    if (n_ct == 0 || n == 0) return;
+    const size_t ctw = (size_t)2 * l * W;
+    if (n_ct == 1 || n > 64) {
+        for (uint32_t c = 0; c < n_ct; c++) rotate_hoisted(ctx, cts + c * ctw, l, steps, n, evk, out + c * n * ctw, st);
+        return;
+    }
+    const uint32_t E = l + ctx.K, D = num_digits(ctx, l);
+    uint64_t* c1 = (uint64_t*)ws_get(ctx, WS_C1, (size_t)n_ct * l * W * 8);
+    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)n_ct * D * E * W * 8);
+    HIPX(hipMemcpy2DAsync(c1, (size_t)l * W * 8, cts + (size_t)l * W, ctw * 8, (size_t)l * W * 8, n_ct,
+                          hipMemcpyDeviceToDevice, st));
+    modup(ctx, c1, ext, n_ct, l, st);
+    std::vector<uint32_t> g(n);
+    for (uint32_t s = 0; s < n; s++) g[s] = rotation_index(steps[s]);
+    const uint32_t per = 64 / n;  // ciphertexts per list (a list starts at a ciphertext boundary)
+    for (uint32_t c0 = 0; c0 < n_ct; c0 += per) {
+        const uint32_t nc = std::min(per, n_ct - c0), m = nc * n;
+        uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)m * 2 * E * W * 8);
+        uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)m * 2 * l * W * 8);
+        std::vector<const uint64_t*> ep(m), kp(m);
+        std::vector<uint32_t> gm(m);
+        for (uint32_t j = 0; j < m; j++) {
+            ep[j] = ext + (size_t)(c0 + j / n) * D * E * W;
+            kp[j] = evk[j % n];
+            gm[j] = g[j % n];
+        }
+        HIPX(launch_ks_inner_list(ctx, ep.data(), kp.data(), acc, m, l, st));
+        // c0 of ciphertext c is the addend of poly 0 of its n outputs
+        moddown_inplace(ctx, acc, 2 * m, l, cts + (size_t)c0 * ctw, ks, st, 2, (int64_t)ctw, 2 * n);
+        HIPX(launch_automorph_list(ctx, ks, out + (size_t)c0 * n * ctw, m, l, gm.data(), st));
+    }
+}
+
 void mul_plain(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const uint64_t* pt, bool pt_shared,
                uint64_t* out, hipStream_t st, uint32_t log_rep) {
     check_level(ctx, l);
@@ -516,21 +554,28 @@ void bsgs_matvec(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* d
 // General BSGS linear transform on one ciphertext [2][l][N]:
 //   y = sum_g Rot_{G[g]}( sum_b diag[g*nb + b] (.) Rot_{Bs[b]}(x) )   (no rescale; out [2][l][N])
 // A step of 0 is the identity (no key).  Baby rotations share one ModUp; giant rotations run as one batch.
-// General BSGS with n_in inputs sharing the baby steps and n_out outputs sharing the babies:
-//   out_o = sum_g Rot_{G_g}( sum_{i, b} diag[o][g][i nb + b] (.) Rot_{B_b}(in_i) )   (+ rescale)
+// General BSGS with n_in inputs sharing the baby steps and n_out outputs sharing the babies, over n_inst
+// independent instances that share the diagonals:
+//   out_{s,o} = sum_g Rot_{G_g}( sum_{i, b} diag[o][g][i nb + b] (.) Rot_{B_b}(in_{s,i}) )   (+ rescale)
 // Step 0 is the identity (no key).  diags: [n_out][ng][n_in nb][l][N >> log_rep], term (g, i, b) pre-rotated
-// by -G_g.  The babies of each input share one ModUp; all giant rotations of all outputs run as one list.
-void bsgs_multi(Context& ctx, const uint64_t* const* in, uint32_t n_in, uint32_t l, const uint64_t* diags,
-                uint32_t nb, const int64_t* bsteps, const uint64_t* const* bevk, uint32_t ng, const int64_t* gsteps,
-                const uint64_t* const* gevk, uint32_t n_out, bool do_rescale, uint64_t* out, hipStream_t st,
-                uint32_t log_rep) {
+// by -G_g.  in: [n_inst][n_in] pointers; out: [n_inst][n_out] (by_output: [n_out][n_inst]) ciphertexts.
+// Each input's babies share one ModUp; all giant rotations of all outputs and instances run as one list.
+void bsgs_multi_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uint32_t n_in, uint32_t l,
+                      const uint64_t* diags, uint32_t nb, const int64_t* bsteps, const uint64_t* const* bevk,
+                      uint32_t ng, const int64_t* gsteps, const uint64_t* const* gevk, uint32_t n_out,
+                      bool do_rescale, uint64_t* out, hipStream_t st, uint32_t log_rep, bool by_output) {
     check_level(ctx, l);
-    if (nb == 0 || n_in == 0 || n_out == 0 || ng == 0 || ng > 64) throw std::invalid_argument("bad BSGS shape");
+    if (nb == 0 || n_in == 0 || n_out == 0 || ng == 0 || ng > 64 || n_inst == 0)
+        throw std::invalid_argument("bad BSGS shape");
     if (do_rescale && l < 2) throw std::invalid_argument("rescale needs l >= 2");
     const size_t ctw = (size_t)2 * l * W;
-    const uint32_t nbt = n_in * nb;
-    uint64_t* baby = (uint64_t*)ws_get(ctx, WS_BABY, (size_t)nbt * ctw * 8);
-    uint64_t* v = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)n_out * ng * ctw * 8);
+    const uint32_t nbt = n_in * nb, n_x = n_inst * n_in;
+    uint64_t* baby = (uint64_t*)ws_get(ctx, WS_BABY, (size_t)n_inst * nbt * ctw * 8);
+    uint64_t* v = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)n_inst * n_out * ng * ctw * 8);
+    // inputs side by side, then the babies [inst][i nb + b]
+    uint64_t* X = (uint64_t*)ws_get(ctx, WS_BINP, (size_t)n_x * ctw * 8);
+    for (uint32_t x = 0; x < n_x; x++)
+        HIPX(hipMemcpyAsync(X + x * ctw, in[x], ctw * 8, hipMemcpyDeviceToDevice, st));
     std::vector<int64_t> rs;
     std::vector<const uint64_t*> rk;
     std::vector<uint32_t> rpos;
@@ -539,39 +584,34 @@ void bsgs_multi(Context& ctx, const uint64_t* const* in, uint32_t n_in, uint32_t
             rs.push_back(bsteps[b]);
             rk.push_back(bevk[b]);
             rpos.push_back(b);
+        } else {  // identity baby: the input itself, for every (instance, input)
+            HIPX(hipMemcpy2DAsync(baby + (size_t)b * ctw, (size_t)nb * ctw * 8, X, ctw * 8, ctw * 8, n_x,
+                                  hipMemcpyDeviceToDevice, st));
         }
     }
-    for (uint32_t i = 0; i < n_in; i++) {
-        for (uint32_t b = 0; b < nb; b++)
-            if (bsteps[b] == 0)
-                HIPX(hipMemcpyAsync(baby + ((size_t)i * nb + b) * ctw, in[i], ctw * 8, hipMemcpyDeviceToDevice, st));
-        if (rs.empty()) continue;
-        // contiguous runs of non-zero steps rotate straight into place; otherwise through a staging buffer
-        bool contiguous = true;
-        for (size_t r = 0; r < rpos.size(); r++) contiguous &= rpos[r] == rpos[0] + r;
-        if (contiguous) {
-            rotate_hoisted(ctx, in[i], l, rs.data(), (uint32_t)rs.size(), rk.data(),
-                           baby + ((size_t)i * nb + rpos[0]) * ctw, st);
-        } else {
-            uint64_t* tmp = (uint64_t*)ws_get(ctx, WS_SUM, rs.size() * ctw * 8);
-            rotate_hoisted(ctx, in[i], l, rs.data(), (uint32_t)rs.size(), rk.data(), tmp, st);
-            for (size_t r = 0; r < rs.size(); r++)
-                HIPX(hipMemcpyAsync(baby + ((size_t)i * nb + rpos[r]) * ctw, tmp + r * ctw, ctw * 8,
-                                    hipMemcpyDeviceToDevice, st));
-        }
+    if (!rs.empty()) {
+        const uint32_t nr = (uint32_t)rs.size();
+        uint64_t* tmp = (uint64_t*)ws_get(ctx, WS_SUM, (size_t)n_x * nr * ctw * 8);
+        rotate_hoisted_multi(ctx, X, n_x, l, rs.data(), nr, rk.data(), tmp, st);
+        for (uint32_t r = 0; r < nr; r++)
+            HIPX(hipMemcpy2DAsync(baby + (size_t)rpos[r] * ctw, (size_t)nb * ctw * 8, tmp + (size_t)r * ctw,
+                                  (size_t)nr * ctw * 8, ctw * 8, n_x, hipMemcpyDeviceToDevice, st));
     }
-    HIPX(launch_bsgs_mac(ctx, baby, diags, v, nbt, nbt * n_out * ng, n_out * ng, l, log_rep, st));
-    // giants with a non-zero step, all outputs, packed contiguously and rotated as one list
+    for (uint32_t s = 0; s < n_inst; s++)
+        HIPX(launch_bsgs_mac(ctx, baby + (size_t)s * nbt * ctw, diags, v + (size_t)s * n_out * ng * ctw, nbt,
+                             nbt * n_out * ng, n_out * ng, l, log_rep, st));
+    // giants with a non-zero step, all instances and outputs, packed contiguously and rotated as one list
     std::vector<int64_t> gs;
     std::vector<const uint64_t*> gk;
-    std::vector<uint32_t> gpos;
-    for (uint32_t o = 0; o < n_out; o++)
-        for (uint32_t g = 0; g < ng; g++)
-            if (gsteps[g] != 0) {
-                gs.push_back(gsteps[g]);
-                gk.push_back(gevk[g]);
-                gpos.push_back(o * ng + g);
-            }
+    std::vector<uint32_t> gpos;  // index into v
+    for (uint32_t s = 0; s < n_inst; s++)
+        for (uint32_t o = 0; o < n_out; o++)
+            for (uint32_t g = 0; g < ng; g++)
+                if (gsteps[g] != 0) {
+                    gs.push_back(gsteps[g]);
+                    gk.push_back(gevk[g]);
+                    gpos.push_back((s * n_out + o) * ng + g);
+                }
     uint64_t* vr = nullptr;
     if (!gs.empty()) {
         uint64_t* packed = (uint64_t*)ws_get(ctx, WS_SUM, gs.size() * ctw * 8);
@@ -581,15 +621,25 @@ void bsgs_multi(Context& ctx, const uint64_t* const* in, uint32_t n_in, uint32_t
         rotate_list(ctx, packed, (uint32_t)gs.size(), l, gs.data(), gk.data(), vr, st);
     }
     uint64_t* dst = out;
-    if (do_rescale) dst = (uint64_t*)ws_get(ctx, WS_LIN, (size_t)n_out * ctw * 8);
+    if (do_rescale) dst = (uint64_t*)ws_get(ctx, WS_LIN, (size_t)n_inst * n_out * ctw * 8);
     size_t r = 0;
-    for (uint32_t o = 0; o < n_out; o++) {
-        std::vector<const uint64_t*> terms;
-        for (uint32_t g = 0; g < ng; g++)
-            terms.push_back(gsteps[g] == 0 ? v + ((size_t)o * ng + g) * ctw : vr + (r++) * ctw);
-        HIPX(launch_sum_list(ctx, terms.data(), (uint32_t)terms.size(), dst + (size_t)o * ctw, 2, l, st));
-    }
-    if (do_rescale) rescale(ctx, dst, 2 * n_out, l, out, st);
+    for (uint32_t s = 0; s < n_inst; s++)
+        for (uint32_t o = 0; o < n_out; o++) {
+            std::vector<const uint64_t*> terms;
+            for (uint32_t g = 0; g < ng; g++)
+                terms.push_back(gsteps[g] == 0 ? v + ((size_t)(s * n_out + o) * ng + g) * ctw : vr + (r++) * ctw);
+            const size_t slot = by_output ? (size_t)o * n_inst + s : (size_t)s * n_out + o;
+            HIPX(launch_sum_list(ctx, terms.data(), (uint32_t)terms.size(), dst + slot * ctw, 2, l, st));
+        }
+    if (do_rescale) rescale(ctx, dst, 2 * n_inst * n_out, l, out, st);
+}
+
+void bsgs_multi(Context& ctx, const uint64_t* const* in, uint32_t n_in, uint32_t l, const uint64_t* diags,
+                uint32_t nb, const int64_t* bsteps, const uint64_t* const* bevk, uint32_t ng, const int64_t* gsteps,
+                const uint64_t* const* gevk, uint32_t n_out, bool do_rescale, uint64_t* out, hipStream_t st,
+                uint32_t log_rep) {
+    bsgs_multi_batch(ctx, in, 1, n_in, l, diags, nb, bsteps, bevk, ng, gsteps, gevk, n_out, do_rescale, out, st,
+                     log_rep, false);
 }
 
 void bsgs_general(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* diags, uint32_t nb,

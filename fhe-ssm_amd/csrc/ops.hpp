@@ -21,6 +21,7 @@ enum WsSlot : uint32_t {
     WS_SUM,
     WS_LIN,
     WS_PTAB,
+    WS_BINP,
     WS_COUNT
 };
 
@@ -34,8 +35,9 @@ void ks_inner(Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* 
               hipStream_t st);
 // add (optional): applied to output polys pc with pc % add_div == 0, at add + (pc / add_div) * add_div * l * N
 // add_pstride < 0: add_div * l * N (the addend is a ciphertext batch); 0: one addend for every poly
+// add_group (0 = add_div): polys pc with pc % add_div == 0 take the addend at (pc / add_group) * add_pstride
 void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
-                     hipStream_t st, uint32_t add_div = 1, int64_t add_pstride = -1);
+                     hipStream_t st, uint32_t add_div = 1, int64_t add_pstride = -1, uint32_t add_group = 0);
 void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
                uint64_t* out2, hipStream_t st, uint32_t add_div = 1);
 void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uint64_t* out, hipStream_t st);
@@ -57,6 +59,12 @@ void rotate_hoisted(Context& ctx, const uint64_t* ct, uint32_t l, const int64_t*
                     const uint64_t* const* evk, uint64_t* out, hipStream_t st);
 void rotate_hoisted_ext(Context& ctx, const uint64_t* ct, const uint64_t* ext, uint32_t l, const int64_t* steps,
                         uint32_t n, const uint64_t* const* evk, uint64_t* out, hipStream_t st);
+void rotate_hoisted_multi(Context& ctx, const uint64_t* cts, uint32_t n_ct, uint32_t l, const int64_t* steps,
+                          uint32_t n, const uint64_t* const* evk, uint64_t* out, hipStream_t st);
+void bsgs_multi_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uint32_t n_in, uint32_t l,
+                      const uint64_t* diags, uint32_t nb, const int64_t* bsteps, const uint64_t* const* bevk,
+                      uint32_t ng, const int64_t* gsteps, const uint64_t* const* gevk, uint32_t n_out,
+                      bool do_rescale, uint64_t* out, hipStream_t st, uint32_t log_rep, bool by_output);
 void hmult_sum(Context& ctx, const uint64_t* const* pairs, uint32_t np, uint32_t B, uint32_t l, const uint64_t* evk,
                uint64_t* out, bool do_rescale, hipStream_t st);
 void bsgs_multi(Context& ctx, const uint64_t* const* in, uint32_t n_in, uint32_t l, const uint64_t* diags,

@@ -203,7 +203,7 @@ __global__ __launch_bounds__(256) void k_ks_inner(const uint64_t* __restrict__ e
 // add_pstride (add_div = 2 adds c0 of a ciphertext batch to poly 0 of each output ciphertext only).
 struct CombineArgs {
     uint32_t l;                 // limbs per poly of out/y/add
-    uint32_t add_div;
+    uint32_t add_div, add_group;  // polys pc % add_div == 0 get addend (pc / add_group) * add_pstride
     uint64_t x_pstride;         // words between polys of x (x may carry extra limbs, e.g. P limbs)
     uint64_t y_pstride, out_pstride, add_pstride;
     TwPair s[kMaxPmap];
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256) void k_sub_scale(const uint64_t* __restrict__ 
     const size_t li = (size_t)i * kN + k;
     const uint64_t d = sub_mod(x[pc * ca.x_pstride + li], y[pc * ca.y_pstride + li], q);
     uint64_t v = shoup(d, ca.s[i].w, ca.s[i].wp, q);
-    if (add && pc % ca.add_div == 0) v = add_mod(v, add[(pc / ca.add_div) * ca.add_pstride + li], q);
+    if (add && pc % ca.add_div == 0) v = add_mod(v, add[(pc / ca.add_group) * ca.add_pstride + li], q);
     out[pc * ca.out_pstride + li] = v;
 }
 
@@ -533,10 +533,11 @@ hipError_t launch_ks_inner(const Context& ctx, const uint64_t* ext, const uint64
 hipError_t launch_sub_scale(const Context& ctx, const uint64_t* x, uint64_t x_pstride, const uint64_t* y,
                             uint64_t y_pstride, const uint64_t* add, uint64_t add_pstride, uint32_t add_div,
                             uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
-                            hipStream_t st) {
+                            hipStream_t st, uint32_t add_group) {
     CombineArgs ca{};
     ca.l = l;
     ca.add_div = add_div ? add_div : 1;
+    ca.add_group = add_group ? add_group : ca.add_div;
     ca.x_pstride = x_pstride;
     ca.y_pstride = y_pstride;
     ca.out_pstride = out_pstride;

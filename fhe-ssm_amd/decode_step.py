@@ -298,6 +298,7 @@ class HEBackend(Backend):
         self.pool = _Pool(ckks)
         self._S = {l: boot.scale(l) for l in range(1, boot.out_level + 1)}
         self.moduli = ctx.moduli
+        self.boot_batch = 16  # ciphertexts per batched bootstrap (bounds its workspace)
         self.boot_keys = {k: {s: keys[s] for s in b.steps} for k, (b, _) in boots.items()}
 
     def S(self, level):
@@ -440,8 +441,9 @@ class HEBackend(Backend):
         keys = self.boot_keys.get(kind, self.boot_keys["state"])
         lo = self.at_scale(a, 1, in_scale)
         out = self._new(a.B, self.top_level, self.S(self.top_level))
-        for b in range(a.B):
-            boot.run(lo.ptr(b), self.relin, self.conj_key, keys, out.ptr(b))
+        for b0 in range(0, a.B, self.boot_batch):
+            nb = min(self.boot_batch, a.B - b0)
+            boot.run_many(lo.ptr(b0), nb, self.relin, self.conj_key, keys, out.ptr(b0))
         return out
 
     def at_scale(self, a, lt, scale):

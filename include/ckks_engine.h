@@ -238,6 +238,11 @@ double ckks_bootstrap_scale(const ckks_bootstrap* bt, uint32_t level);
 int ckks_eval_bootstrap(ckks_context* ctx, const ckks_bootstrap* bt, const uint64_t* d_ct_in, const uint64_t* d_relin,
                         const uint64_t* d_conj, const int64_t* steps, const uint64_t* const* d_evks, uint32_t n_keys,
                         uint64_t* d_out, void* stream);
+/* ckks_eval_bootstrap_many: batch independent level-1 ciphertexts [batch][2][1][N] -> [batch][2][l_out][N] in
+ * one pass (every kernel over the whole batch; keys and diagonals read once per pass); batch <= 64 */
+int ckks_eval_bootstrap_many(ckks_context* ctx, const ckks_bootstrap* bt, const uint64_t* d_ct_in, uint32_t batch,
+                             const uint64_t* d_relin, const uint64_t* d_conj, const int64_t* steps,
+                             const uint64_t* const* d_evks, uint32_t n_keys, uint64_t* d_out, void* stream);
 /* stage-wise form for testing: stops after stage 1 ModRaise, 2 CoeffToSlot, 3 split (two ciphertexts),
  * 4 EvalMod (two ciphertexts), 5 recombination, 6 the full bootstrap; writes that ciphertext (batch) to d_out
  * (sized for the top level) and its level to *level.  Synchronous on the null stream. */

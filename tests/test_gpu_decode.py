@@ -250,6 +250,27 @@ def test_config5_chain_bootstrap(engine):
 
 
 @pytest.mark.timeout(900)
+def test_bootstrap_many_matches_single(engine):
+    """the batched bootstrap is the single-ciphertext bootstrap word for word, for every item of the batch"""
+    be, sk = engine
+    boot, ins = be.boots["state"]
+    keys = be.boot_keys["state"]
+    rng = np.random.default_rng(33)
+    B = 3
+    cts = [be.at_scale(be.encrypt(sk, rng.uniform(-1, 1, SLOTS), 3, seed=bytes([b]) * 32), 1, ins) for b in range(B)]
+    batch = be._new(B, 1, ins)
+    for b in range(B):
+        be.ctx.eval_lincomb(1, [cts[b].ptr()], [1], [1.0], None, ins, 0.0, 1, True, batch.ptr(b))
+    out = be._new(B, be.top_level, be.S(be.top_level))
+    boot.run_many(batch.ptr(), B, be.relin, be.conj_key, keys, out.ptr())
+    words = out.buf.download((B, 2, be.top_level, N))
+    for b in range(B):
+        one = be._new(1, be.top_level, be.S(be.top_level))
+        boot.run(cts[b].ptr(), be.relin, be.conj_key, keys, one.ptr())
+        assert np.array_equal(one.buf.download((2, be.top_level, N)), words[b]), b
+
+
+@pytest.mark.timeout(900)
 def test_decode_step_one_layer(engine, DS, M):
     """one layer, two tokens with the state carried: decrypted output against the float64 model"""
     from oracle import rwkv_ref as ref
