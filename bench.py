@@ -9,7 +9,10 @@ Workloads (inputs seeded and resident in HBM before the t
   ntt    config 1: forward then inverse NTT over 64 ct x 2 polys x 24 limbs.  value = algorithmic GB/s.
   pcmm   config 3: 768x768 plaintext matrix x one ciphertext (L=16) by BSGS 28 x 28.  value = ms.
   bootstrap  config 4: full-slot bootstrap of a level-1 ciphertext.  value = ms; precision in bits.
-The default run also reports the config-1, -3 and -4 figures beside the config-2 metric.
+  decode config 5: one encrypted decode step of the RWKV-7-0.1B-shaped model (12 layers, 32 lanes, state
+         carried, bootstrapped once per layer).  value = s/step; decrypted output and logits checked
+         against the float64 model.
+The default run also reports the config-1, -3, -4 and -5 figures beside the config-2 metric.
 
 Roofline: the engine records HIP events on its launch stream around every kernel of one profiled
 step (ckks_profile_*); the dominant kernel by time is reported with achieved = algorithmic bytes per
@@ -317,6 +320,7 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12):
         torch.cuda.synchronize()
         log(f"warmup step {i} done at {time.perf_counter() - t_enc0:.1f} s")
     t_warm = time.perf_counter() - t_enc0
+    free_b, total_b = torch.cuda.mem_get_info()
     for i in range(warmup, warmup + steps_n):
         x, ct = client_in(i)
         xs.append(x)
@@ -348,6 +352,7 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12):
     return {"s_per_step": round(s_per_step, 3), "key_switches_per_step": int(np.mean(ks)),
             "bootstraps_per_step": step.stats["bootstraps"] // (warmup + steps_n + 1),
             "setup_s": {"keys": round(t_keys, 1), "first_steps_with_plaintext_encoding": round(t_warm, 1)},
+            "device_memory_in_use_gb_after_warmup": round((total_b - free_b) / 1e9, 1),
             "client_s": {"decrypt_and_vocab_head": round(t_client, 3)},
             "kernels": kernel_table(rep), "roofline": roofline_from_profile(rep),
             "_check": {"xs": xs, "outs": outs, "logits": logits, "logits_step": warmup + steps_n - 1, "W": W,
@@ -482,6 +487,7 @@ def main():
     ap.add_argument("--no-ntt-line", action="store_true", help="skip the config-1 NTT figure in the hmult run")
     ap.add_argument("--no-pcmm-line", action="store_true", help="skip the config-3 PCMM figure in the hmult run")
     ap.add_argument("--no-boot-line", action="store_true", help="skip the config-4 bootstrap figure in the hmult run")
+    ap.add_argument("--no-decode-line", action="store_true", help="skip the config-5 decode figure in the hmult run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding is a design note, "
@@ -507,6 +513,17 @@ def main():
             b = bench_bootstrap(ckks, torch, max(2, args.steps // 4), 1, args.seed)
             extra["bootstrap_config4"] = {k: b[k] for k in ("ms_per_bootstrap", "precision_bits", "levels_in_out",
                                                              "roofline")}
+        if not args.no_decode_line:
+            d = bench_decode(ckks, torch, 1, 1, args.seed)
+            line = {"s_per_step": d["s_per_step"], "metric": "s/step for 32-lane decode (config 5)",
+                    "roofline": d["roofline"]}
+            line.update({k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s",
+                                           "device_memory_in_use_gb_after_warmup")})
+            if not args.no_cpu_baseline:
+                line["cpu_baseline"], acc = cpu_baseline_decode(d, args.seed)
+                line.update(acc)
+            extra["decode_config5"] = line
+            del d
         cpu = None if args.no_cpu_baseline else cpu_baseline_hmult(args.seed)
     elif args.workload == "decode":
         d = bench_decode(ckks, torch, args.steps, args.warmup, args.seed, args.layers)
@@ -514,7 +531,8 @@ def main():
                "ms_per_step": round(d["s_per_step"] * 1e3, 1), "dtype": "u64",
                "config": {"workload": d["workload"], "lanes": DECODE_LANES, "layers": args.layers},
                "kernels": d["kernels"], "roofline": d["roofline"],
-               "check": {k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s")}}
+               "check": {k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s",
+                                           "device_memory_in_use_gb_after_warmup")}}
         extra = {}
         cpu = None
         if not args.no_cpu_baseline:
