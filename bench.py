@@ -64,11 +64,18 @@ def timed_steps(torch, stream, step, steps, warmup):
     return wall, per
 
 
-def roofline_from_profile(rep: dict):
+# HBM bytes per launch of a workload's dominant kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the same
+# bench command (scaled by what the counters read for a copy kernel of known size: read = 2 x FETCH_SIZE KiB,
+# write = WRITE_SIZE KiB).  Measured, not computed: re-measure when the kernel or the workload changes.
+MEASURED_TRAFFIC = {("hmult", "ntt_fwd_2pass"): 7.456e9}
+
+
+def roofline_from_profile(rep: dict, workload: str = ""):
     name, (n, ms, by) = max(rep.items(), key=lambda kv: kv[1][1])
     achieved = by / (ms * 1e-3) / 1e9
+    traffic = MEASURED_TRAFFIC.get((workload, name))
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": name,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": name,
             "launches_in_profiled_step": n, "mean_launch_ms": round(ms / n, 4),
             "algorithmic_bytes_per_launch": round(by / n)}
 
@@ -142,7 +149,7 @@ def bench_hmult(ckks, torch, steps, warmup, seed):
                    "step_ms_min": round(min(per), 4), "step_ms_max": round(max(per), 4)},
         "check": {"decrypted_relErrRms_max": rel_err, "ciphertexts_checked": 2},
         "kernels": kernel_table(rep),
-        "roofline": roofline_from_profile(rep),
+        "roofline": roofline_from_profile(rep, "hmult"),
     }
     return res
 
