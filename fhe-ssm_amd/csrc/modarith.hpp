@@ -89,4 +89,32 @@ __device__ __forceinline__ void mac128(U128& acc, uint64_t a, uint64_t b) {
     acc.lo = nlo;
 }
 
+// Lazy 128-bit multiply-accumulate for operands below 2^60 (every modulus of this engine is): the four 32 x 32
+// partial products go to separate 64-bit sums -- the low products to lo with a carry into hi, the two cross
+// products (< 2^60 each) to m, the high product (< 2^56) straight into hi -- so a term costs four
+// v_mad_u64_u32 and a carry, against ~30 instructions for a full 64 x 64 -> 128 product per term.
+// m takes at most 8 terms (< 2^61 each) between folds: call fold() at least every 8 add()s.
+struct Acc {
+    uint64_t lo, hi, m;
+    __device__ __forceinline__ Acc() : lo(0), hi(0), m(0) {}
+    __device__ __forceinline__ void add(uint64_t a, uint64_t b) {
+        const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32);
+        const uint32_t b0 = (uint32_t)b, b1 = (uint32_t)(b >> 32);
+        const uint64_t t = (uint64_t)a0 * b0;
+        lo += t;
+        hi += (uint64_t)a1 * b1 + (lo < t ? 1u : 0u);
+        m += (uint64_t)a0 * b1 + (uint64_t)a1 * b0;
+    }
+    __device__ __forceinline__ void fold() {
+        const uint64_t s = m << 32;
+        lo += s;
+        hi += (m >> 32) + (lo < s ? 1u : 0u);
+        m = 0;
+    }
+    __device__ __forceinline__ U128 get() {
+        fold();
+        return U128{lo, hi};
+    }
+};
+
 }  // namespace fhe

@@ -58,6 +58,12 @@ hipError_t launch_mul_i(const Context& ctx, const uint64_t* in, uint64_t* out, u
                         hipStream_t st);
 hipError_t launch_pair_mac(const Context& ctx, const uint64_t* R, const uint64_t* pt, uint64_t* out, uint32_t n_sets,
                            uint32_t n, uint32_t l, uint32_t log_rep, hipStream_t st);
+hipError_t launch_mdr(const Context& ctx, int step, const uint64_t* x, uint64_t x_pstride, const uint64_t* add,
+                      uint64_t add_pstride, const uint64_t* addc, const uint64_t* conv, uint64_t* z, uint64_t* T,
+                      uint64_t* out, uint32_t n_polys, uint32_t l, const TwPair* pinv, const TwPair* qlinv,
+                      hipStream_t st);
+hipError_t launch_gather(const Context& ctx, const uint64_t* const* src, uint32_t n, uint64_t words, uint64_t* dst,
+                         hipStream_t st);
 hipError_t launch_tensor_sum(const Context& ctx, const uint64_t* const* d_tab, uint32_t np, uint64_t* d01,
                              uint64_t* d2, uint32_t B, uint32_t l, uint64_t* d2e, uint64_t d2e_bstride,
                              const uint32_t* ext_off, hipStream_t st);
@@ -276,6 +282,66 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
                           n_polys, l, pinv.data(), st, add_group));
 }
 
+// ModDown fused with the rescale that follows it (the same words as moddown_inplace + rescale, one forward
+// NTT of l-1 limbs fewer): x [n_polys][E][N] evaluation form over Q_l * P (its P limbs and limb l-1 are
+// transformed in place), add [n_polys][l][N] (or null) -> out [n_polys][l-1][N].
+void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
+                     hipStream_t st) {
+    check_level(ctx, l);
+    if (l < 2) throw std::invalid_argument("rescale needs l >= 2");
+    const uint32_t E = l + ctx.K, K = ctx.K;
+    if (K == 0) throw std::invalid_argument("ModDown needs special primes");
+    // P limbs and limb l-1 of x to coefficients, in place
+    std::vector<Job> jobs;
+    for (uint32_t pc = 0; pc < n_polys; pc++) {
+        jobs.push_back(Job{pc * E + l - 1, l - 1});
+        for (uint32_t k = 0; k < K; k++) jobs.push_back(Job{pc * E + l + k, ctx.L + k});
+    }
+    const JobSpec js = cached_jobs(ctx, "mdrP:" + std::to_string(n_polys) + ":" + std::to_string(l), std::move(jobs));
+    HIPX(launch_ntt(ctx, x, js, n_polys * (K + 1), true, ctx.ntt_mode, st));
+    // limb l-1 of the addend to coefficients (a copy: the addend is the caller's)
+    uint64_t* addc = nullptr;
+    if (add) {
+        addc = (uint64_t*)ws_get(ctx, WS_LAST, (size_t)n_polys * W * 8);
+        HIPX(hipMemcpy2DAsync(addc, W * 8, add + (size_t)(l - 1) * W, (size_t)l * W * 8, W * 8, n_polys,
+                              hipMemcpyDeviceToDevice, st));
+        HIPX(launch_ntt(ctx, addc, regular_jobs(n_polys, {l - 1}), n_polys, true, ctx.ntt_mode, st));
+    }
+    std::vector<uint32_t> in_idx, in_off, out_idx, out_off;
+    for (uint32_t k = 0; k < K; k++) {
+        in_idx.push_back(ctx.L + k);
+        in_off.push_back(l + k);
+    }
+    for (uint32_t i = 0; i < l; i++) {
+        out_idx.push_back(i);
+        out_off.push_back(i);
+    }
+    const BConvPlan& plan = bconv_plan(ctx, in_idx, out_idx, ctx.moddown_exact);
+    uint64_t* conv = (uint64_t*)ws_get(ctx, WS_CONV, (size_t)n_polys * l * W * 8);
+    HIPX(launch_bconv(ctx, plan, x, (uint64_t)E * W, in_off.data(), conv, (uint64_t)l * W, out_off.data(), n_polys,
+                      st));
+    std::vector<TwPair> pinv(l), qlinv(l);
+    const uint64_t ql = ctx.moduli[l - 1];
+    for (uint32_t i = 0; i < l; i++) {
+        const uint64_t q = ctx.moduli[i];
+        uint64_t P = 1;
+        for (uint32_t k = 0; k < K; k++) P = mulmod_h(P, ctx.moduli[ctx.L + k] % q, q);
+        const uint64_t v = invmod_h(P, q);
+        pinv[i] = TwPair{v, shoup_companion(v, q)};
+        const uint64_t u = i + 1 < l ? invmod_h(ql % q, q) : 0;
+        qlinv[i] = TwPair{u, i + 1 < l ? shoup_companion(u, q) : 0};
+    }
+    uint64_t* z = (uint64_t*)ws_get(ctx, WS_RTMP2, (size_t)n_polys * W * 8);
+    uint64_t* T = (uint64_t*)ws_get(ctx, WS_RTMP, (size_t)n_polys * (l - 1) * W * 8);
+    const uint64_t xps = (uint64_t)E * W, aps = (uint64_t)l * W;
+    HIPX(launch_mdr(ctx, 0, x, xps, add, aps, addc, conv, z, T, out, n_polys, l, pinv.data(), qlinv.data(), st));
+    HIPX(launch_mdr(ctx, 1, x, xps, add, aps, addc, conv, z, T, out, n_polys, l, pinv.data(), qlinv.data(), st));
+    std::vector<uint32_t> pm(l - 1);
+    for (uint32_t i = 0; i + 1 < l; i++) pm[i] = i;
+    HIPX(launch_ntt(ctx, T, regular_jobs(n_polys, pm), n_polys * (l - 1), false, ctx.ntt_mode, st));
+    HIPX(launch_mdr(ctx, 2, x, xps, add, aps, addc, conv, z, T, out, n_polys, l, pinv.data(), qlinv.data(), st));
+}
+
 // ------------------------------------------------------------------ key switch
 // x: [B][l][N] eval; evk [dnum][2][L+K][N]; out2: [B][2][l][N] (+= add [B][2][l][N] if given)
 void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
@@ -330,9 +396,7 @@ static void relin_tail(Context& ctx, uint64_t* d01, uint64_t* x2c, uint64_t* ext
         moddown_inplace(ctx, acc, 2 * B, l, d01, out, st, 1);
         return;
     }
-    uint64_t* relin = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)B * 2 * l * W * 8);
-    moddown_inplace(ctx, acc, 2 * B, l, d01, relin, st, 1);
-    rescale(ctx, relin, 2 * B, l, out, st);
+    moddown_rescale(ctx, acc, 2 * B, l, d01, out, st);
 }
 
 void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l, const uint64_t* evk,
@@ -574,8 +638,7 @@ void bsgs_multi_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, 
     uint64_t* v = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)n_inst * n_out * ng * ctw * 8);
     // inputs side by side, then the babies [inst][i nb + b]
     uint64_t* X = (uint64_t*)ws_get(ctx, WS_BINP, (size_t)n_x * ctw * 8);
-    for (uint32_t x = 0; x < n_x; x++)
-        HIPX(hipMemcpyAsync(X + x * ctw, in[x], ctw * 8, hipMemcpyDeviceToDevice, st));
+    HIPX(launch_gather(ctx, in, n_x, ctw, X, st));
     std::vector<int64_t> rs;
     std::vector<const uint64_t*> rk;
     std::vector<uint32_t> rpos;
@@ -616,8 +679,9 @@ void bsgs_multi_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, 
     if (!gs.empty()) {
         uint64_t* packed = (uint64_t*)ws_get(ctx, WS_SUM, gs.size() * ctw * 8);
         vr = (uint64_t*)ws_get(ctx, WS_GROT, gs.size() * ctw * 8);
-        for (size_t r = 0; r < gs.size(); r++)
-            HIPX(hipMemcpyAsync(packed + r * ctw, v + (size_t)gpos[r] * ctw, ctw * 8, hipMemcpyDeviceToDevice, st));
+        std::vector<const uint64_t*> src(gs.size());
+        for (size_t r = 0; r < gs.size(); r++) src[r] = v + (size_t)gpos[r] * ctw;
+        HIPX(launch_gather(ctx, src.data(), (uint32_t)src.size(), ctw, packed, st));
         rotate_list(ctx, packed, (uint32_t)gs.size(), l, gs.data(), gk.data(), vr, st);
     }
     uint64_t* dst = out;
@@ -662,24 +726,21 @@ void rotate_masked(Context& ctx, const uint64_t* ct, uint32_t l, uint32_t n, con
     steps.insert(steps.end(), hi, hi + n);
     std::vector<const uint64_t*> keys(lo_evk, lo_evk + n);
     keys.insert(keys.end(), hi_evk, hi_evk + n);
-    // a zero step is the identity: rotate the others, copy the input for those
-    std::vector<int64_t> rs;
-    std::vector<const uint64_t*> rk;
-    std::vector<uint32_t> rpos;
-    for (uint32_t j = 0; j < 2 * n; j++) {
+    // a zero step is the identity (a copy); each run of non-zero steps rotates straight into place over one
+    // shared ModUp of c1
+    const uint32_t E = l + ctx.K, D = num_digits(ctx, l);
+    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)D * E * W * 8);
+    modup(ctx, ct + (size_t)l * W, ext, 1, l, st);
+    for (uint32_t j = 0; j < 2 * n;) {
         if (steps[j] == 0) {
             HIPX(hipMemcpyAsync(R + j * ctw, ct, ctw * 8, hipMemcpyDeviceToDevice, st));
-        } else {
-            rs.push_back(steps[j]);
-            rk.push_back(keys[j]);
-            rpos.push_back(j);
+            j++;
+            continue;
         }
-    }
-    if (!rs.empty()) {
-        uint64_t* tmp = (uint64_t*)ws_get(ctx, WS_SUM, rs.size() * ctw * 8);
-        rotate_hoisted(ctx, ct, l, rs.data(), (uint32_t)rs.size(), rk.data(), tmp, st);
-        for (size_t r = 0; r < rs.size(); r++)
-            HIPX(hipMemcpyAsync(R + (size_t)rpos[r] * ctw, tmp + r * ctw, ctw * 8, hipMemcpyDeviceToDevice, st));
+        uint32_t e = j;
+        while (e < 2 * n && steps[e] != 0) e++;
+        rotate_hoisted_ext(ctx, ct, ext, l, steps.data() + j, e - j, keys.data() + j, R + j * ctw, st);
+        j = e;
     }
     uint64_t* m = (uint64_t*)ws_get(ctx, WS_LIN, (size_t)n_sets * n * ctw * 8);
     HIPX(launch_pair_mac(ctx, R, pts, m, n_sets, n, l, log_rep, st));

@@ -22,6 +22,7 @@ enum WsSlot : uint32_t {
     WS_LIN,
     WS_PTAB,
     WS_BINP,
+    WS_RTMP2,
     WS_COUNT
 };
 
@@ -38,6 +39,8 @@ void ks_inner(Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* 
 // add_group (0 = add_div): polys pc with pc % add_div == 0 take the addend at (pc / add_group) * add_pstride
 void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
                      hipStream_t st, uint32_t add_div = 1, int64_t add_pstride = -1, uint32_t add_group = 0);
+void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
+                     hipStream_t st);
 void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
                uint64_t* out2, hipStream_t st, uint32_t add_div = 1);
 void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uint64_t* out, hipStream_t st);

@@ -44,14 +44,14 @@ __global__ __launch_bounds__(256) void k_tensor(const uint64_t* __restrict__ a, 
     const size_t P = (size_t)ta.l * kN;
     const size_t o = (size_t)c * 2 * P + (size_t)t * kN + k;
     const uint64_t a0 = a[o], a1 = a[o + P], b0 = b[o], b1 = b[o + P];
-    U128 s0{0, 0}, s1{0, 0}, s2{0, 0};
-    mac128(s0, a0, b0);
-    mac128(s1, a0, b1);
-    mac128(s1, a1, b0);
-    mac128(s2, a1, b1);
-    d01[o] = reduce_u128(s0, br);
-    d01[o + P] = reduce_u128(s1, br);
-    const uint64_t v2 = reduce_u128(s2, br);
+    Acc s0, s1, s2;
+    s0.add(a0, b0);
+    s1.add(a0, b1);
+    s1.add(a1, b0);
+    s2.add(a1, b1);
+    d01[o] = reduce_u128(s0.get(), br);
+    d01[o + P] = reduce_u128(s1.get(), br);
+    const uint64_t v2 = reduce_u128(s2.get(), br);
     d2[(size_t)c * P + (size_t)t * kN + k] = v2;
     if (ta.d2e) ta.d2e[c * ta.d2e_bstride + (size_t)ta.ext_off[t] * kN + k] = v2;
 }
@@ -65,20 +65,25 @@ __global__ __launch_bounds__(256) void k_tensor_sum(const uint64_t* const* __res
     const uint32_t t = blockIdx.y, c = blockIdx.z;
     const Barrett br = barrett_of(primes[t]);
     const size_t P = (size_t)ta.l * kN, w = (size_t)t * kN + k;
-    U128 s0{0, 0}, s1{0, 0}, s2{0, 0};
+    Acc s0, s1, s2;
     for (uint32_t j = 0; j < np; j++) {
         const uint64_t* a = tab[((size_t)c * np + j) * 2];
         const uint64_t* b = tab[((size_t)c * np + j) * 2 + 1];
         const uint64_t a0 = a[w], a1 = a[P + w], b0 = b[w], b1 = b[P + w];
-        mac128(s0, a0, b0);
-        mac128(s1, a0, b1);
-        mac128(s1, a1, b0);
-        mac128(s2, a1, b1);
+        s0.add(a0, b0);
+        s1.add(a0, b1);
+        s1.add(a1, b0);
+        s2.add(a1, b1);
+        if ((j & 3) == 3) {  // s1 takes two terms per product: fold every 4 products
+            s0.fold();
+            s1.fold();
+            s2.fold();
+        }
     }
     const size_t o = (size_t)c * 2 * P + w;
-    d01[o] = reduce_u128(s0, br);
-    d01[o + P] = reduce_u128(s1, br);
-    const uint64_t v2 = reduce_u128(s2, br);
+    d01[o] = reduce_u128(s0.get(), br);
+    d01[o + P] = reduce_u128(s1.get(), br);
+    const uint64_t v2 = reduce_u128(s2.get(), br);
     d2[(size_t)c * P + w] = v2;
     if (ta.d2e) ta.d2e[c * ta.d2e_bstride + (size_t)ta.ext_off[t] * kN + k] = v2;
 }
@@ -138,12 +143,10 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         const uint64_t lo = F.lo + (1ull << 63);
         u = F.hi + (lo < F.lo ? 1 : 0);
     }
-    for (uint32_t j = 0; j < ba.n_out; j++) {
+    // two outputs per iteration: independent accumulation chains for the scheduler to interleave
+    auto finish = [&](Acc& a, uint32_t j) {
         const Barrett br = barrett_of(primes[ba.out_prime[j]]);
-        U128 acc{0, 0};
-#pragma unroll
-        for (int i = 0; i < kMaxBconvIn; i++)
-            if (i < (int)ba.n_in) mac128(acc, y[i], qhmod[(size_t)i * ba.n_out + j]);
+        U128 acc = a.get();
         if (ba.centered) {
             // acc - u * pmod_j, kept non-negative by adding 16 p_j (u <= n_in <= 16, pmod_j < p_j)
             const uint64_t t = 16 * br.q - u * pmod[j];
@@ -151,6 +154,32 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
             acc.hi += (acc.lo < t) ? 1 : 0;
         }
         dst[(size_t)ba.out_off[j] * kN] = reduce_u128(acc, br);
+    };
+    uint32_t j = 0;
+    for (; j + 1 < ba.n_out; j += 2) {
+        Acc a, b;
+#pragma unroll
+        for (int i = 0; i < kMaxBconvIn; i++) {
+            if (i < (int)ba.n_in) {
+                a.add(y[i], qhmod[(size_t)i * ba.n_out + j]);
+                b.add(y[i], qhmod[(size_t)i * ba.n_out + j + 1]);
+            }
+            if (i == 7) {
+                a.fold();
+                b.fold();
+            }
+        }
+        finish(a, j);
+        finish(b, j + 1);
+    }
+    if (j < ba.n_out) {
+        Acc a;
+#pragma unroll
+        for (int i = 0; i < kMaxBconvIn; i++) {
+            if (i < (int)ba.n_in) a.add(y[i], qhmod[(size_t)i * ba.n_out + j]);
+            if (i == 7) a.fold();
+        }
+        finish(a, j);
     }
 }
 
@@ -182,18 +211,18 @@ __global__ __launch_bounds__(256) void k_ks_inner(const uint64_t* __restrict__ e
     const size_t ext_b = (size_t)ia.D * ia.E * kN, acc_b = (size_t)2 * ia.E * kN;
     for (uint32_t c = blockIdx.z; c < ia.B; c += gridDim.z) {
         const uint64_t* x = ext + c * ext_b + (size_t)t * kN + k;
-        U128 s0{0, 0}, s1{0, 0};
+        Acc s0, s1;  // at most kMaxDigits = 8 terms: no intermediate fold
 #pragma unroll
         for (int d = 0; d < kMaxDigits; d++) {
             if (d < (int)ia.D) {
                 const uint64_t v = x[(size_t)d * ia.E * kN];
-                mac128(s0, v, kb[d]);
-                mac128(s1, v, ka[d]);
+                s0.add(v, kb[d]);
+                s1.add(v, ka[d]);
             }
         }
         uint64_t* o = acc + c * acc_b + (size_t)t * kN + k;
-        o[0] = reduce_u128(s0, br);
-        o[(size_t)ia.E * kN] = reduce_u128(s1, br);
+        o[0] = reduce_u128(s0.get(), br);
+        o[(size_t)ia.E * kN] = reduce_u128(s1.get(), br);
     }
 }
 
@@ -281,18 +310,85 @@ __global__ __launch_bounds__(256) void k_ks_inner_list(ListPtrs ext, ListPtrs ev
     const Barrett br = barrett_of(primes[p]);
     const uint64_t* x = ext.p[c] + (size_t)t * kN + k;
     const uint64_t* e = evk.p[c] + (size_t)p * kN + k;
-    U128 s0{0, 0}, s1{0, 0};
+    Acc s0, s1;  // at most kMaxDigits = 8 terms
 #pragma unroll
     for (int d = 0; d < kMaxDigits; d++) {
         if (d < (int)ia.D) {
             const uint64_t v = x[(size_t)d * ia.E * kN];
-            mac128(s0, v, e[((size_t)d * 2 + 0) * ia.T * kN]);
-            mac128(s1, v, e[((size_t)d * 2 + 1) * ia.T * kN]);
+            s0.add(v, e[((size_t)d * 2 + 0) * ia.T * kN]);
+            s1.add(v, e[((size_t)d * 2 + 1) * ia.T * kN]);
         }
     }
     uint64_t* o = acc + (size_t)c * 2 * ia.E * kN + (size_t)t * kN + k;
-    o[0] = reduce_u128(s0, br);
-    o[(size_t)ia.E * kN] = reduce_u128(s1, br);
+    o[0] = reduce_u128(s0.get(), br);
+    o[(size_t)ia.E * kN] = reduce_u128(s1.get(), br);
+}
+
+// ---------------------------------------------------------------- ModDown fused with the following rescale
+// The relinearized y_i = add_i + (x_i - NTT(conv_i)) P^-1 and its rescale out_i = (y_i - NTT(lift(z))_i) q_l^-1
+// (z the dropped limb l-1 of y in coefficient form) combine, by linearity of the NTT mod q_i, into
+//   out_i = (add_i + x_i P^-1 - NTT(T_i)) q_l^-1,  T_i = conv_i P^-1 + lift(z)_i,
+//   z = INTT(add_{l-1}) + (INTT(x_{l-1}) - conv_{l-1}) P^-1   (mod q_{l-1}):
+// the same words with one forward NTT of l-1 limbs instead of two (l for conv, l-1 for the lift).
+struct MdrArgs {
+    uint32_t l;           // limbs before the rescale
+    uint64_t x_pstride;   // words between polys of x ([E][N] each)
+    uint64_t add_pstride; // words between polys of add (0: no addend)
+    TwPair pinv[kMaxPmap];   // P^-1 mod q_i
+    TwPair qlinv[kMaxPmap];  // q_{l-1}^-1 mod q_i
+};
+
+// z[pc][k] from the coefficient forms of x's and add's limb l-1 and of conv's limb l-1
+__global__ __launch_bounds__(256) void k_mdr_last(const uint64_t* __restrict__ x, const uint64_t* __restrict__ addc,
+                                                  const uint64_t* __restrict__ conv, uint64_t* __restrict__ z,
+                                                  MdrArgs ma, const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x, pc = blockIdx.y;
+    const uint32_t i = ma.l - 1;
+    const uint64_t q = primes[i].q;
+    const uint64_t d = sub_mod(x[pc * ma.x_pstride + (size_t)i * kN + k], conv[((size_t)pc * ma.l + i) * kN + k], q);
+    uint64_t v = shoup(d, ma.pinv[i].w, ma.pinv[i].wp, q);
+    if (addc) v = add_mod(v, addc[(size_t)pc * kN + k], q);
+    z[(size_t)pc * kN + k] = v;
+}
+
+// T[pc][i][k] = conv_i P^-1 + centered lift of z, for i < l-1 (coefficient form)
+__global__ __launch_bounds__(256) void k_mdr_lift(const uint64_t* __restrict__ conv, const uint64_t* __restrict__ z,
+                                                  uint64_t* __restrict__ T, MdrArgs ma,
+                                                  const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x, i = blockIdx.y, pc = blockIdx.z;
+    const uint64_t q = primes[i].q, ql = primes[ma.l - 1].q;
+    const uint64_t v = z[(size_t)pc * kN + k];
+    uint64_t r;
+    if (v > (ql >> 1)) {
+        const uint64_t neg = ql - v;
+        const uint64_t m = neg >= q ? neg % q : neg;
+        r = m ? q - m : 0;
+    } else {
+        r = v >= q ? v % q : v;
+    }
+    const uint64_t c = shoup(conv[((size_t)pc * ma.l + i) * kN + k], ma.pinv[i].w, ma.pinv[i].wp, q);
+    T[((size_t)pc * (ma.l - 1) + i) * kN + k] = add_mod(c, r, q);
+}
+
+// out_i = (add_i + x_i P^-1 - T_i) q_{l-1}^-1 in evaluation form, i < l-1
+__global__ __launch_bounds__(256) void k_mdr_combine(const uint64_t* __restrict__ x, const uint64_t* __restrict__ add,
+                                                     const uint64_t* __restrict__ T, uint64_t* __restrict__ out,
+                                                     MdrArgs ma, const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x, i = blockIdx.y, pc = blockIdx.z;
+    const uint64_t q = primes[i].q;
+    const size_t li = (size_t)i * kN + k;
+    uint64_t v = shoup(x[pc * ma.x_pstride + li], ma.pinv[i].w, ma.pinv[i].wp, q);
+    if (add) v = add_mod(v, add[pc * ma.add_pstride + li], q);
+    v = sub_mod(v, T[(size_t)pc * (ma.l - 1) * kN + li], q);
+    out[(size_t)pc * (ma.l - 1) * kN + li] = shoup(v, ma.qlinv[i].w, ma.qlinv[i].wp, q);
+}
+
+// dst[c] = src[c] for up to 64 items of `words` words each (gathers scattered ciphertexts into one batch)
+__global__ __launch_bounds__(256) void k_gather(ListPtrs src, uint64_t* __restrict__ dst, uint64_t words) {
+    const uint32_t c = blockIdx.y;
+    const uint64_t* s = src.p[c];
+    uint64_t* d = dst + (size_t)c * words;
+    for (uint64_t w = (uint64_t)blockIdx.x * 256 + threadIdx.x; w < words; w += (uint64_t)gridDim.x * 256) d[w] = s[w];
 }
 
 // per-ciphertext automorphism index: [n][2][l][N], ciphertext c uses g[c]
@@ -349,11 +445,18 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(const uint64_t*
         // diagonals past n_diag (a short last giant step) are zero
         const int64_t rem = (int64_t)n_diag - (int64_t)g * nb_total - j0;
         const uint32_t jn = rem <= 0 ? 0u : (uint32_t)min<int64_t>(rem, nb);
+        Acc a0, a1;
         for (uint32_t j = 0; j < jn; j++) {
             const uint64_t m = dg[(size_t)j * Pd];
-            mac128(s0, sb[(2 * j) * kMacCoef + kk], m);
-            mac128(s1, sb[(2 * j + 1) * kMacCoef + kk], m);
+            a0.add(sb[(2 * j) * kMacCoef + kk], m);
+            a1.add(sb[(2 * j + 1) * kMacCoef + kk], m);
+            if ((j & 7) == 7) {
+                a0.fold();
+                a1.fold();
+            }
         }
+        s0 = a0.get();
+        s1 = a1.get();
         uint64_t r0 = reduce_u128(s0, br), r1 = reduce_u128(s1, br);
         if (acc) {
             r0 = add_mod(r0, out[(size_t)g * 2 * P + off], br.q);
@@ -376,10 +479,10 @@ __global__ __launch_bounds__(256) void k_pair_mac(const uint64_t* __restrict__ R
     const size_t P = (size_t)l * kN, Pc = (size_t)l * (kN >> log_rep);
     const size_t w = (size_t)poly * P + (size_t)i * kN + k;
     const uint64_t* p = pt + (size_t)st * 2 * Pc + (size_t)i * (kN >> log_rep) + (k >> log_rep);
-    U128 s{0, 0};
-    mac128(s, R[(size_t)t * 2 * P + w], p[0]);
-    mac128(s, R[(size_t)(n + t) * 2 * P + w], p[Pc]);
-    out[(size_t)st * 2 * P + w] = reduce_u128(s, br);
+    Acc s;
+    s.add(R[(size_t)t * 2 * P + w], p[0]);
+    s.add(R[(size_t)(n + t) * 2 * P + w], p[Pc]);
+    out[(size_t)st * 2 * P + w] = reduce_u128(s.get(), br);
 }
 
 // ct (.) pt on both polys: ct [B][2][l][N], pt [B or 1][l][N >> log_rep] (pt_bstride 0 = shared plaintext;
@@ -440,12 +543,12 @@ __global__ __launch_bounds__(256) void k_lincomb(uint64_t* __restrict__ out, Lin
     const uint32_t i = blockIdx.y, pc = blockIdx.z;  // pc = 2 c + poly
     const uint32_t c = pc >> 1, p = pc & 1;
     const Barrett br = barrett_of(primes[i]);
-    U128 acc{0, 0};
+    Acc acc;  // at most kMaxTerms = 8 terms
     for (uint32_t t = 0; t < la.n_terms; t++) {
         const uint64_t v = la.x[t][((size_t)(2 * c + p) * la.stride[t] + i) * kN + k];
-        mac128(acc, v, la.C[t][i]);
+        acc.add(v, la.C[t][i]);
     }
-    uint64_t r = reduce_u128(acc, br);
+    uint64_t r = reduce_u128(acc.get(), br);
     if (la.has_add && p == 0) r = add_mod(r, la.add[i], br.q);
     out[((size_t)pc * la.l_out + i) * kN + k] = r;
 }
@@ -626,6 +729,55 @@ hipError_t launch_pair_mac(const Context& ctx, const uint64_t* R, const uint64_t
     hipLaunchKernelGGL(k_pair_mac, dim3(kN / 256, l, n_sets * n * 2), dim3(256), 0, st, R, pt, out, n, l, log_rep,
                        ctx.d_primes);
     prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+static MdrArgs mdr_args(uint32_t l, uint64_t x_pstride, uint64_t add_pstride, const TwPair* pinv,
+                        const TwPair* qlinv) {
+    MdrArgs ma{};
+    ma.l = l;
+    ma.x_pstride = x_pstride;
+    ma.add_pstride = add_pstride;
+    for (uint32_t i = 0; i < l; i++) {
+        ma.pinv[i] = pinv[i];
+        ma.qlinv[i] = qlinv[i];
+    }
+    return ma;
+}
+
+hipError_t launch_mdr(const Context& ctx, int step, const uint64_t* x, uint64_t x_pstride, const uint64_t* add,
+                      uint64_t add_pstride, const uint64_t* addc, const uint64_t* conv, uint64_t* z, uint64_t* T,
+                      uint64_t* out, uint32_t n_polys, uint32_t l, const TwPair* pinv, const TwPair* qlinv,
+                      hipStream_t st) {
+    if (l < 2 || l > (uint32_t)kMaxPmap) return hipErrorInvalidValue;
+    const MdrArgs ma = mdr_args(l, x_pstride, add ? add_pstride : 0, pinv, qlinv);
+    if (step == 0) {
+        const int pi = prof_begin(ctx, "mdr_last", (double)n_polys * 4 * kN * 8, st);
+        hipLaunchKernelGGL(k_mdr_last, dim3(kN / 256, n_polys), dim3(256), 0, st, x, addc, conv, z, ma, ctx.d_primes);
+        prof_end(ctx, pi, st);
+    } else if (step == 1) {
+        const int pi = prof_begin(ctx, "mdr_lift", (double)n_polys * (2 * (l - 1) + 1) * kN * 8, st);
+        hipLaunchKernelGGL(k_mdr_lift, dim3(kN / 256, l - 1, n_polys), dim3(256), 0, st, conv, z, T, ma,
+                           ctx.d_primes);
+        prof_end(ctx, pi, st);
+    } else {
+        const int pi = prof_begin(ctx, "mdr_combine", (double)n_polys * (l - 1) * (add ? 4 : 3) * kN * 8, st);
+        hipLaunchKernelGGL(k_mdr_combine, dim3(kN / 256, l - 1, n_polys), dim3(256), 0, st, x, add, T, out, ma,
+                           ctx.d_primes);
+        prof_end(ctx, pi, st);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(const Context& ctx, const uint64_t* const* src, uint32_t n, uint64_t words, uint64_t* dst,
+                         hipStream_t st) {
+    for (uint32_t c0 = 0; c0 < n; c0 += kMaxList) {
+        const uint32_t m = std::min<uint32_t>(kMaxList, n - c0);
+        ListPtrs lp{};
+        for (uint32_t j = 0; j < m; j++) lp.p[j] = src[c0 + j];
+        const uint32_t bx = (uint32_t)std::min<uint64_t>((words + 255) / 256, 1024);
+        hipLaunchKernelGGL(k_gather, dim3(bx, m), dim3(256), 0, st, lp, dst + (size_t)c0 * words, words);
+    }
     return hipGetLastError();
 }
 
