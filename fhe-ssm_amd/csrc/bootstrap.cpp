@@ -281,9 +281,12 @@ class Eval {
 public:
     Eval(Context& ctx, const BootPlan& P, uint32_t B, const uint64_t* relin, hipStream_t st)
         : ctx_(ctx), P_(P), B_(B), relin_(relin), st_(st) {}
-    ~Eval() {
-        for (auto* p : all_) (void)hipFree(p);
+    ~Eval() {  // every buffer goes back to the context's pool for the next call
+        auto& pool = ctx_.buf_pool[bytes()];
+        for (auto* p : all_) pool.push_back(p);
     }
+
+    size_t bytes() const { return (size_t)B_ * 2 * ctx_.L * W * 8; }
 
     HCt get(uint32_t l) {
         uint64_t* p;
@@ -291,7 +294,13 @@ public:
             p = free_.back();
             free_.pop_back();
         } else {
-            HIPB(hipMalloc(&p, (size_t)B_ * 2 * ctx_.L * W * 8));
+            auto& pool = ctx_.buf_pool[bytes()];
+            if (!pool.empty()) {
+                p = pool.back();
+                pool.pop_back();
+            } else {
+                HIPB(hipMalloc(&p, bytes()));
+            }
             all_.push_back(p);
         }
         return HCt{p, l};

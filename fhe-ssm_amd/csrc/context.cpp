@@ -180,6 +180,9 @@ void context_release(Context& c) {
     for (auto& s : c.scratch) (void)hipFree(s.first);
     for (auto& kv : c.small_ntt) (void)hipFree(kv.second);
     c.small_ntt.clear();
+    for (auto& kv : c.buf_pool)
+        for (auto* p : kv.second) (void)hipFree(p);
+    c.buf_pool.clear();
     c.job_cache.clear();
     c.bconv_cache.clear();
     c.scratch.clear();

@@ -76,6 +76,9 @@ struct Context {
     std::vector<std::pair<void*, size_t>> scratch;
     // device tables [L+K][N'] of the small-ring NTTs used by periodic encoding, by ring size N'
     std::map<uint32_t, TwPair*> small_ntt;
+    // free device buffers by size, reused across bootstrapping calls (a call needs tens of buffers of
+    // B x 2 x L limbs; allocating them per call costs more than the smaller kernels it runs)
+    std::map<size_t, std::vector<uint64_t*>> buf_pool;
     // per-launch profiling (off by default)
     bool prof_on = false;
     mutable std::vector<ProfRec> prof;
