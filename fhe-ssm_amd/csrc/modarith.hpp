@@ -59,17 +59,15 @@ struct Barrett {
 };
 
 __device__ __forceinline__ uint64_t reduce128(uint64_t hi, uint64_t lo, const Barrett& b) {
-    // estimate quotient floor(x * mu / 2^128) from the top words; error < 4
+    // Quotient estimate qt = hi*mu_hi + floor(hi*mu_lo / 2^64) + floor(lo*mu_hi / 2^64): it drops lo*mu_lo / 2^128
+    // and two fractional parts (< 3 in all) from x*mu / 2^128, which itself is at most 1 below x / q.  So
+    // floor(x / q) - 3 <= qt <= floor(x / q) and the remainder x - qt*q lies in [0, 4q) (q < 2^62).
     const uint64_t q = b.q;
-    // x * mu >> 128 ~= hi*mu_hi + mulhi(hi, mu_lo) + mulhi(lo, mu_hi)
-    uint64_t t1 = mulhi64(lo, b.mu_hi);
-    uint64_t t2 = mulhi64(hi, b.mu_lo);
-    uint64_t qt = hi * b.mu_hi + t1 + t2;
-    uint64_t r = lo - qt * q;
-    r = csub(r, q);
-    r = csub(r, q);
-    r = csub(r, q);
-    return csub(r, q);
+    const uint64_t t1 = mulhi64(lo, b.mu_hi);
+    const uint64_t t2 = mulhi64(hi, b.mu_lo);
+    const uint64_t qt = hi * b.mu_hi + t1 + t2;
+    const uint64_t r = csub_s(lo - qt * q, q << 1);
+    return csub_s(r, q);
 }
 
 __device__ __forceinline__ uint64_t mul_mod(uint64_t a, uint64_t b, const Barrett& br) {

@@ -147,7 +147,8 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
             ct_bfly(x[k], x[k + h], t[(16 * rl + k) >> (8 - s)], q4, nq);
         }
     }
-    // canonical [0, q), then transpose through LDS for coalesced stores
+    // canonical [0, q), then transpose through LDS for coalesced stores (direct 16-byte stores of each
+    // thread's contiguous run measured slower)
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = canon8(x[k], q);
     __syncthreads();

@@ -30,7 +30,16 @@ hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_
                         const uint32_t* in_off, uint64_t* out, uint64_t out_bstride, const uint32_t* out_off,
                         uint32_t B, hipStream_t st);
 hipError_t launch_ks_inner(const Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* acc, uint32_t B,
-                           uint32_t l, hipStream_t st);
+                           uint32_t l, hipStream_t st, uint32_t t0 = 0);
+hipError_t launch_bconv_mdr(const Context& ctx, const BConvPlan& plan, const uint64_t* in, uint64_t in_bstride,
+                            const uint32_t* in_off, uint64_t* T, uint32_t n_polys, const uint64_t* xlast,
+                            uint64_t xlast_pstride, const uint64_t* addc, TwPair pinv_last, hipStream_t st);
+hipError_t launch_mdr_combine(const Context& ctx, const uint64_t* x, uint64_t x_pstride, const uint64_t* add,
+                              uint64_t add_pstride, const uint64_t* T, uint64_t* out, uint32_t n_polys, uint32_t l,
+                              const TwPair* pinv, const TwPair* qlinv, hipStream_t st);
+hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const uint64_t* evk, const uint64_t* add,
+                                 uint64_t add_pstride, const uint64_t* T, uint64_t* out, uint32_t B, uint32_t l,
+                                 const TwPair* pinv, const TwPair* qlinv, hipStream_t st);
 hipError_t launch_sub_scale(const Context& ctx, const uint64_t* x, uint64_t x_pstride, const uint64_t* y,
                             uint64_t y_pstride, const uint64_t* add, uint64_t add_pstride, uint32_t add_div,
                             uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
@@ -58,10 +67,6 @@ hipError_t launch_mul_i(const Context& ctx, const uint64_t* in, uint64_t* out, u
                         hipStream_t st);
 hipError_t launch_pair_mac(const Context& ctx, const uint64_t* R, const uint64_t* pt, uint64_t* out, uint32_t n_sets,
                            uint32_t n, uint32_t l, uint32_t log_rep, hipStream_t st);
-hipError_t launch_mdr(const Context& ctx, int step, const uint64_t* x, uint64_t x_pstride, const uint64_t* add,
-                      uint64_t add_pstride, const uint64_t* addc, const uint64_t* conv, uint64_t* z, uint64_t* T,
-                      uint64_t* out, uint32_t n_polys, uint32_t l, const TwPair* pinv, const TwPair* qlinv,
-                      hipStream_t st);
 hipError_t launch_gather(const Context& ctx, const uint64_t* const* src, uint32_t n, uint64_t words, uint64_t* dst,
                          hipStream_t st);
 hipError_t launch_tensor_sum(const Context& ctx, const uint64_t* const* d_tab, uint32_t np, uint64_t* d01,
@@ -129,11 +134,17 @@ void* ws_get(Context& ctx, uint32_t slot, size_t bytes) {
 
 // ------------------------------------------------------------------ BConv plans
 const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, const std::vector<uint32_t>& out_idx,
-                            bool centered) {
+                            bool centered, const std::vector<uint64_t>& col_scale) {
+    if (!col_scale.empty() && col_scale.size() != out_idx.size())
+        throw std::invalid_argument("one column scale per BConv output");
     std::string key = centered ? "c" : "b";
     for (auto i : in_idx) key += ":" + std::to_string(i);
     key += ">";
     for (auto j : out_idx) key += ":" + std::to_string(j);
+    if (!col_scale.empty()) {
+        key += "*";
+        for (auto f : col_scale) key += ":" + std::to_string(f);
+    }
     auto it = ctx.bconv_cache.find(key);
     if (it != ctx.bconv_cache.end()) return it->second;
     BConvPlan p;
@@ -156,7 +167,7 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
             uint64_t m = 1;
             for (uint32_t k = 0; k < p.n_in; k++)
                 if (k != i) m = mulmod_h(m, ctx.moduli[in_idx[k]] % pj, pj);
-            tab[2 * p.n_in + (size_t)i * p.n_out + j] = m;
+            tab[2 * p.n_in + (size_t)i * p.n_out + j] = col_scale.empty() ? m : mulmod_h(m, col_scale[j], pj);
         }
     }
     if (centered) {
@@ -170,7 +181,7 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
             const uint64_t pj = ctx.moduli[out_idx[j]];
             uint64_t m = 1;
             for (uint32_t k = 0; k < p.n_in; k++) m = mulmod_h(m, ctx.moduli[in_idx[k]] % pj, pj);
-            cfix[2 * p.n_in + j] = m;
+            cfix[2 * p.n_in + j] = col_scale.empty() ? m : mulmod_h(m, col_scale[j], pj);
         }
     }
     HIPX(hipMalloc(&p.d_tab, tab.size() * 8));
@@ -284,9 +295,12 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
 
 // ModDown fused with the rescale that follows it (the same words as moddown_inplace + rescale, one forward
 // NTT of l-1 limbs fewer): x [n_polys][E][N] evaluation form over Q_l * P (its P limbs and limb l-1 are
-// transformed in place), add [n_polys][l][N] (or null) -> out [n_polys][l-1][N].
+// transformed in place), add [n_polys][l][N] (or null) -> out [n_polys][l-1][N].  The BConv writes
+// T_i = conv_i P^-1 + lift(z)_i directly (P^-1 folded into its table).  With ext/evk given (a relinearization,
+// n_polys = 2B), x holds only limbs l-1.. of the evk inner product (k_ks_inner from t0 = l-1) and the combine
+// forms limbs 0..l-2 itself from ext and evk.
 void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
-                     hipStream_t st) {
+                     hipStream_t st, const uint64_t* ext, const uint64_t* evk) {
     check_level(ctx, l);
     if (l < 2) throw std::invalid_argument("rescale needs l >= 2");
     const uint32_t E = l + ctx.K, K = ctx.K;
@@ -307,20 +321,8 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
                               hipMemcpyDeviceToDevice, st));
         HIPX(launch_ntt(ctx, addc, regular_jobs(n_polys, {l - 1}), n_polys, true, ctx.ntt_mode, st));
     }
-    std::vector<uint32_t> in_idx, in_off, out_idx, out_off;
-    for (uint32_t k = 0; k < K; k++) {
-        in_idx.push_back(ctx.L + k);
-        in_off.push_back(l + k);
-    }
-    for (uint32_t i = 0; i < l; i++) {
-        out_idx.push_back(i);
-        out_off.push_back(i);
-    }
-    const BConvPlan& plan = bconv_plan(ctx, in_idx, out_idx, ctx.moddown_exact);
-    uint64_t* conv = (uint64_t*)ws_get(ctx, WS_CONV, (size_t)n_polys * l * W * 8);
-    HIPX(launch_bconv(ctx, plan, x, (uint64_t)E * W, in_off.data(), conv, (uint64_t)l * W, out_off.data(), n_polys,
-                      st));
     std::vector<TwPair> pinv(l), qlinv(l);
+    std::vector<uint64_t> col(l);
     const uint64_t ql = ctx.moduli[l - 1];
     for (uint32_t i = 0; i < l; i++) {
         const uint64_t q = ctx.moduli[i];
@@ -328,18 +330,30 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
         for (uint32_t k = 0; k < K; k++) P = mulmod_h(P, ctx.moduli[ctx.L + k] % q, q);
         const uint64_t v = invmod_h(P, q);
         pinv[i] = TwPair{v, shoup_companion(v, q)};
+        col[i] = i + 1 < l ? v : 1;  // columns 0..l-2 carry P^-1; the dropped limb's column stays plain
         const uint64_t u = i + 1 < l ? invmod_h(ql % q, q) : 0;
         qlinv[i] = TwPair{u, i + 1 < l ? shoup_companion(u, q) : 0};
     }
-    uint64_t* z = (uint64_t*)ws_get(ctx, WS_RTMP2, (size_t)n_polys * W * 8);
+    std::vector<uint32_t> in_idx, in_off, out_idx;
+    for (uint32_t k = 0; k < K; k++) {
+        in_idx.push_back(ctx.L + k);
+        in_off.push_back(l + k);
+    }
+    for (uint32_t i = 0; i < l; i++) out_idx.push_back(i);
+    const BConvPlan& plan = bconv_plan(ctx, in_idx, out_idx, ctx.moddown_exact, col);
     uint64_t* T = (uint64_t*)ws_get(ctx, WS_RTMP, (size_t)n_polys * (l - 1) * W * 8);
-    const uint64_t xps = (uint64_t)E * W, aps = (uint64_t)l * W;
-    HIPX(launch_mdr(ctx, 0, x, xps, add, aps, addc, conv, z, T, out, n_polys, l, pinv.data(), qlinv.data(), st));
-    HIPX(launch_mdr(ctx, 1, x, xps, add, aps, addc, conv, z, T, out, n_polys, l, pinv.data(), qlinv.data(), st));
+    const uint64_t xps = (uint64_t)E * W;
+    HIPX(launch_bconv_mdr(ctx, plan, x, xps, in_off.data(), T, n_polys, x + (size_t)(l - 1) * W, xps, addc,
+                          pinv[l - 1], st));
     std::vector<uint32_t> pm(l - 1);
     for (uint32_t i = 0; i + 1 < l; i++) pm[i] = i;
     HIPX(launch_ntt(ctx, T, regular_jobs(n_polys, pm), n_polys * (l - 1), false, ctx.ntt_mode, st));
-    HIPX(launch_mdr(ctx, 2, x, xps, add, aps, addc, conv, z, T, out, n_polys, l, pinv.data(), qlinv.data(), st));
+    if (ext)
+        HIPX(launch_mdr_combine_ks(ctx, ext, evk, add, (uint64_t)l * W, T, out, n_polys / 2, l, pinv.data(),
+                                   qlinv.data(), st));
+    else
+        HIPX(launch_mdr_combine(ctx, x, xps, add, (uint64_t)l * W, T, out, n_polys, l, pinv.data(), qlinv.data(),
+                                st));
 }
 
 // ------------------------------------------------------------------ key switch
@@ -391,12 +405,14 @@ static void relin_tail(Context& ctx, uint64_t* d01, uint64_t* x2c, uint64_t* ext
     for (uint32_t i = 0; i < l; i++) pm[i] = i;
     HIPX(launch_ntt(ctx, x2c, regular_jobs(B, pm), B * l, true, ctx.ntt_mode, st));
     modup_from_coef(ctx, x2c, ext, B, l, st);
-    HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st));
     if (!do_rescale) {
+        HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st));
         moddown_inplace(ctx, acc, 2 * B, l, d01, out, st, 1);
         return;
     }
-    moddown_rescale(ctx, acc, 2 * B, l, d01, out, st);
+    // inner product of limb l-1 and the P limbs only; the combine forms limbs 0..l-2
+    HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st, l - 1));
+    moddown_rescale(ctx, acc, 2 * B, l, d01, out, st, ext, evk);
 }
 
 void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l, const uint64_t* evk,

@@ -27,8 +27,10 @@ enum WsSlot : uint32_t {
 };
 
 void* ws_get(Context& ctx, uint32_t slot, size_t bytes);
+// col_scale (optional, one factor per output): every table column j (and its centered correction) is multiplied
+// by col_scale[j] mod p_j, so output j comes out as conv_j * col_scale[j]
 const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, const std::vector<uint32_t>& out_idx,
-                            bool centered = false);
+                            bool centered = false, const std::vector<uint64_t>& col_scale = {});
 uint32_t num_digits(const Context& ctx, uint32_t l);
 
 void modup(Context& ctx, const uint64_t* x, uint64_t* ext, uint32_t B, uint32_t l, hipStream_t st);
@@ -40,7 +42,7 @@ void ks_inner(Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* 
 void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
                      hipStream_t st, uint32_t add_div = 1, int64_t add_pstride = -1, uint32_t add_group = 0);
 void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
-                     hipStream_t st);
+                     hipStream_t st, const uint64_t* ext = nullptr, const uint64_t* evk = nullptr);
 void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
                uint64_t* out2, hipStream_t st, uint32_t add_div = 1);
 void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uint64_t* out, hipStream_t st);

@@ -106,9 +106,33 @@ struct BConvArgs {
     uint8_t out_prime[kMaxBconvOut];
 };
 
+// centered residue of v in [0, ql) modulo q: v > ql/2 stands for v - ql (harness/boot_overflow_probe.cpp:93-94)
+__device__ __forceinline__ uint64_t lift_centered(uint64_t v, uint64_t ql, const Barrett& br) {
+    const uint64_t q = br.q;
+    if (v > (ql >> 1)) {
+        const uint64_t neg = ql - v;  // value is -neg
+        const uint64_t m = neg >= q ? reduce128(0, neg, br) : neg;
+        return m ? q - m : 0;
+    }
+    return v >= q ? reduce128(0, v, br) : v;
+}
+
+// Extra inputs of the ModDown BConv fused with the rescale that follows (k_bconv<true>).  The plan's last
+// output column is the dropped limb l-1 (plain table); every other column j has P^-1 mod q_j folded into its
+// table, so the column sums are conv_j P^-1 directly.  Per coefficient the kernel forms
+//   z = addc + (x_{l-1} - conv_{l-1}) P^-1  (mod q_{l-1}, x_{l-1} and addc in coefficient form)
+// and writes T_j = conv_j P^-1 + [z]_{q_j} (centered lift) for j < l-1.
+struct MdrBconvArgs {
+    const uint64_t* xlast;  // limb l-1 of each input poly, coefficient form, poly stride xlast_pstride
+    uint64_t xlast_pstride;
+    const uint64_t* addc;   // [n_polys][N] coefficient form of the addend's limb l-1, or null
+    TwPair pinv_last;       // P^-1 mod q_{l-1}
+};
+
+template <bool kMdr>
 __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
                                                BConvArgs ba, const uint64_t* __restrict__ tab,
-                                               const PrimeInfo* __restrict__ primes) {
+                                               const PrimeInfo* __restrict__ primes, MdrBconvArgs mb) {
     const uint32_t k = blockIdx.x * 256 + threadIdx.x;
     const uint32_t c = blockIdx.y;
     const uint64_t* src = in + c * ba.in_bstride + k;
@@ -143,9 +167,8 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         const uint64_t lo = F.lo + (1ull << 63);
         u = F.hi + (lo < F.lo ? 1 : 0);
     }
-    // two outputs per iteration: independent accumulation chains for the scheduler to interleave
-    auto finish = [&](Acc& a, uint32_t j) {
-        const Barrett br = barrett_of(primes[ba.out_prime[j]]);
+    // column sum of output j before its final reduction, with the centered correction
+    auto column = [&](Acc& a, uint32_t j, const Barrett& br) {
         U128 acc = a.get();
         if (ba.centered) {
             // acc - u * pmod_j, kept non-negative by adding 16 p_j (u <= n_in <= 16, pmod_j < p_j)
@@ -153,10 +176,37 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
             acc.lo += t;
             acc.hi += (acc.lo < t) ? 1 : 0;
         }
+        return acc;
+    };
+    uint32_t n_main = ba.n_out;
+    uint64_t z = 0, ql = 0;
+    if constexpr (kMdr) {
+        n_main = ba.n_out - 1;
+        Acc a;
+#pragma unroll
+        for (int i = 0; i < kMaxBconvIn; i++) {
+            if (i < (int)ba.n_in) a.add(y[i], qhmod[(size_t)i * ba.n_out + n_main]);
+            if (i == 7) a.fold();
+        }
+        const Barrett bl = barrett_of(primes[ba.out_prime[n_main]]);
+        const uint64_t conv = reduce_u128(column(a, n_main, bl), bl);
+        ql = bl.q;
+        z = shoup(sub_mod(mb.xlast[c * mb.xlast_pstride + k], conv, ql), mb.pinv_last.w, mb.pinv_last.wp, ql);
+        if (mb.addc) z = add_mod(z, mb.addc[(size_t)c * kN + k], ql);
+    }
+    auto finish = [&](Acc& a, uint32_t j) {
+        const Barrett br = barrett_of(primes[ba.out_prime[j]]);
+        U128 acc = column(a, j, br);
+        if constexpr (kMdr) {
+            const uint64_t r = lift_centered(z, ql, br);
+            acc.lo += r;
+            acc.hi += (acc.lo < r) ? 1 : 0;
+        }
         dst[(size_t)ba.out_off[j] * kN] = reduce_u128(acc, br);
     };
+    // two outputs per iteration: independent accumulation chains for the scheduler to interleave
     uint32_t j = 0;
-    for (; j + 1 < ba.n_out; j += 2) {
+    for (; j + 1 < n_main; j += 2) {
         Acc a, b;
 #pragma unroll
         for (int i = 0; i < kMaxBconvIn; i++) {
@@ -172,7 +222,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         finish(a, j);
         finish(b, j + 1);
     }
-    if (j < ba.n_out) {
+    if (j < n_main) {
         Acc a;
 #pragma unroll
         for (int i = 0; i < kMaxBconvIn; i++) {
@@ -185,45 +235,37 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
 
 // ------------------------------------------------------------------ key-switch inner product
 // acc[c][0][t] = sum_d ext[c][d][t] * evk[d][0][prime(t)],  acc[c][1][t] = ... * evk[d][1][prime(t)]
-// One thread per (k, t); the evk words are loaded once and reused for every ciphertext of the batch.
+// One thread per (c, k, t), the ciphertext index fastest in the grid: the workgroups that read one evk tile run
+// back to back, so each XCD fetches the tile once into its L2 and every load of a thread is independent.
 constexpr int kMaxDigits = 8;
 
 struct InnerArgs {
     uint32_t D, E, T, B;
+    uint32_t t0;  // first extended limb computed (k_ks_inner: limbs t0..E-1)
     uint8_t prime_of[kMaxPmap];
 };
 
 __global__ __launch_bounds__(256) void k_ks_inner(const uint64_t* __restrict__ ext, const uint64_t* __restrict__ evk,
                                                   uint64_t* __restrict__ acc, InnerArgs ia,
                                                   const PrimeInfo* __restrict__ primes) {
-    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
-    const uint32_t t = blockIdx.y;
+    const uint32_t c = blockIdx.x, k = blockIdx.y * 256 + threadIdx.x;
+    const uint32_t t = ia.t0 + blockIdx.z;
     const uint32_t p = ia.prime_of[t];
     const Barrett br = barrett_of(primes[p]);
-    uint64_t kb[kMaxDigits], ka[kMaxDigits];
+    const uint64_t* x = ext + (size_t)c * ia.D * ia.E * kN + (size_t)t * kN + k;
+    const uint64_t* e = evk + (size_t)p * kN + k;
+    Acc s0, s1;  // at most kMaxDigits = 8 terms: no intermediate fold
 #pragma unroll
     for (int d = 0; d < kMaxDigits; d++) {
         if (d < (int)ia.D) {
-            kb[d] = evk[(((size_t)d * 2 + 0) * ia.T + p) * kN + k];
-            ka[d] = evk[(((size_t)d * 2 + 1) * ia.T + p) * kN + k];
+            const uint64_t v = x[(size_t)d * ia.E * kN];
+            s0.add(v, e[((size_t)d * 2 + 0) * ia.T * kN]);
+            s1.add(v, e[((size_t)d * 2 + 1) * ia.T * kN]);
         }
     }
-    const size_t ext_b = (size_t)ia.D * ia.E * kN, acc_b = (size_t)2 * ia.E * kN;
-    for (uint32_t c = blockIdx.z; c < ia.B; c += gridDim.z) {
-        const uint64_t* x = ext + c * ext_b + (size_t)t * kN + k;
-        Acc s0, s1;  // at most kMaxDigits = 8 terms: no intermediate fold
-#pragma unroll
-        for (int d = 0; d < kMaxDigits; d++) {
-            if (d < (int)ia.D) {
-                const uint64_t v = x[(size_t)d * ia.E * kN];
-                s0.add(v, kb[d]);
-                s1.add(v, ka[d]);
-            }
-        }
-        uint64_t* o = acc + c * acc_b + (size_t)t * kN + k;
-        o[0] = reduce_u128(s0.get(), br);
-        o[(size_t)ia.E * kN] = reduce_u128(s1.get(), br);
-    }
+    uint64_t* o = acc + (size_t)c * 2 * ia.E * kN + (size_t)t * kN + k;
+    o[0] = reduce_u128(s0.get(), br);
+    o[(size_t)ia.E * kN] = reduce_u128(s1.get(), br);
 }
 
 // ------------------------------------------------------------------ ModDown / rescale combines
@@ -258,17 +300,7 @@ __global__ __launch_bounds__(256) void k_lift_centered(const uint64_t* __restric
                                                        const PrimeInfo* __restrict__ primes) {
     const uint32_t k = blockIdx.x * 256 + threadIdx.x;
     const uint32_t i = blockIdx.y, pc = blockIdx.z;
-    const uint64_t v = last[pc * last_pstride + k];
-    const uint64_t q = primes[i].q;
-    uint64_t r;
-    if (v > (ql >> 1)) {
-        const uint64_t neg = ql - v;  // value is -neg
-        const uint64_t m = neg >= q ? neg % q : neg;
-        r = m ? q - m : 0;
-    } else {
-        r = v >= q ? v % q : v;
-    }
-    tmp[((size_t)pc * n_out + i) * kN + k] = r;
+    tmp[((size_t)pc * n_out + i) * kN + k] = lift_centered(last[pc * last_pstride + k], ql, barrett_of(primes[i]));
 }
 
 // ------------------------------------------------------------------ elementwise helpers
@@ -329,7 +361,9 @@ __global__ __launch_bounds__(256) void k_ks_inner_list(ListPtrs ext, ListPtrs ev
 // (z the dropped limb l-1 of y in coefficient form) combine, by linearity of the NTT mod q_i, into
 //   out_i = (add_i + x_i P^-1 - NTT(T_i)) q_l^-1,  T_i = conv_i P^-1 + lift(z)_i,
 //   z = INTT(add_{l-1}) + (INTT(x_{l-1}) - conv_{l-1}) P^-1   (mod q_{l-1}):
-// the same words with one forward NTT of l-1 limbs instead of two (l for conv, l-1 for the lift).
+// the same words with one forward NTT of l-1 limbs instead of two (l for conv, l-1 for the lift).  The BConv
+// writes T directly (k_bconv<true>); in a relinearization the evk inner product of limbs 0..l-2 is formed inside
+// the combine (k_mdr_combine_ks) and never stored.
 struct MdrArgs {
     uint32_t l;           // limbs before the rescale
     uint64_t x_pstride;   // words between polys of x ([E][N] each)
@@ -337,38 +371,6 @@ struct MdrArgs {
     TwPair pinv[kMaxPmap];   // P^-1 mod q_i
     TwPair qlinv[kMaxPmap];  // q_{l-1}^-1 mod q_i
 };
-
-// z[pc][k] from the coefficient forms of x's and add's limb l-1 and of conv's limb l-1
-__global__ __launch_bounds__(256) void k_mdr_last(const uint64_t* __restrict__ x, const uint64_t* __restrict__ addc,
-                                                  const uint64_t* __restrict__ conv, uint64_t* __restrict__ z,
-                                                  MdrArgs ma, const PrimeInfo* __restrict__ primes) {
-    const uint32_t k = blockIdx.x * 256 + threadIdx.x, pc = blockIdx.y;
-    const uint32_t i = ma.l - 1;
-    const uint64_t q = primes[i].q;
-    const uint64_t d = sub_mod(x[pc * ma.x_pstride + (size_t)i * kN + k], conv[((size_t)pc * ma.l + i) * kN + k], q);
-    uint64_t v = shoup(d, ma.pinv[i].w, ma.pinv[i].wp, q);
-    if (addc) v = add_mod(v, addc[(size_t)pc * kN + k], q);
-    z[(size_t)pc * kN + k] = v;
-}
-
-// T[pc][i][k] = conv_i P^-1 + centered lift of z, for i < l-1 (coefficient form)
-__global__ __launch_bounds__(256) void k_mdr_lift(const uint64_t* __restrict__ conv, const uint64_t* __restrict__ z,
-                                                  uint64_t* __restrict__ T, MdrArgs ma,
-                                                  const PrimeInfo* __restrict__ primes) {
-    const uint32_t k = blockIdx.x * 256 + threadIdx.x, i = blockIdx.y, pc = blockIdx.z;
-    const uint64_t q = primes[i].q, ql = primes[ma.l - 1].q;
-    const uint64_t v = z[(size_t)pc * kN + k];
-    uint64_t r;
-    if (v > (ql >> 1)) {
-        const uint64_t neg = ql - v;
-        const uint64_t m = neg >= q ? neg % q : neg;
-        r = m ? q - m : 0;
-    } else {
-        r = v >= q ? v % q : v;
-    }
-    const uint64_t c = shoup(conv[((size_t)pc * ma.l + i) * kN + k], ma.pinv[i].w, ma.pinv[i].wp, q);
-    T[((size_t)pc * (ma.l - 1) + i) * kN + k] = add_mod(c, r, q);
-}
 
 // out_i = (add_i + x_i P^-1 - T_i) q_{l-1}^-1 in evaluation form, i < l-1
 __global__ __launch_bounds__(256) void k_mdr_combine(const uint64_t* __restrict__ x, const uint64_t* __restrict__ add,
@@ -381,6 +383,41 @@ __global__ __launch_bounds__(256) void k_mdr_combine(const uint64_t* __restrict_
     if (add) v = add_mod(v, add[pc * ma.add_pstride + li], q);
     v = sub_mod(v, T[(size_t)pc * (ma.l - 1) * kN + li], q);
     out[(size_t)pc * (ma.l - 1) * kN + li] = shoup(v, ma.qlinv[i].w, ma.qlinv[i].wp, q);
+}
+
+// k_mdr_combine for the relinearization of a batch, x formed on the fly: x[c][p][i] = sum_d ext[c][d][i] *
+// evk[d][p][i] (the same sums k_ks_inner would store), then out[c][p][i] = (add + x P^-1 - T) q_{l-1}^-1 for both
+// polys p of ciphertext c.  Grid as k_ks_inner: the ciphertext index fastest.
+__global__ __launch_bounds__(256) void k_mdr_combine_ks(const uint64_t* __restrict__ ext,
+                                                        const uint64_t* __restrict__ evk,
+                                                        const uint64_t* __restrict__ add,
+                                                        const uint64_t* __restrict__ T, uint64_t* __restrict__ out,
+                                                        InnerArgs ia, MdrArgs ma,
+                                                        const PrimeInfo* __restrict__ primes) {
+    const uint32_t c = blockIdx.x, k = blockIdx.y * 256 + threadIdx.x, i = blockIdx.z;
+    const Barrett br = barrett_of(primes[i]);
+    const uint64_t q = br.q;
+    const size_t po = (size_t)(ma.l - 1) * kN, li = (size_t)i * kN + k;
+    const uint64_t* x = ext + (size_t)c * ia.D * ia.E * kN + li;
+    const uint64_t* e = evk + li;
+    Acc s0, s1;  // at most kMaxDigits = 8 terms: no intermediate fold
+#pragma unroll
+    for (int d = 0; d < kMaxDigits; d++) {
+        if (d < (int)ia.D) {
+            const uint64_t v = x[(size_t)d * ia.E * kN];
+            s0.add(v, e[((size_t)d * 2 + 0) * ia.T * kN]);
+            s1.add(v, e[((size_t)d * 2 + 1) * ia.T * kN]);
+        }
+    }
+    const uint64_t xs[2] = {reduce_u128(s0.get(), br), reduce_u128(s1.get(), br)};
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+        const size_t pc = 2 * (size_t)c + p;
+        uint64_t v = shoup(xs[p], ma.pinv[i].w, ma.pinv[i].wp, q);
+        if (add) v = add_mod(v, add[pc * ma.add_pstride + li], q);
+        v = sub_mod(v, T[pc * po + li], q);
+        out[pc * po + li] = shoup(v, ma.qlinv[i].w, ma.qlinv[i].wp, q);
+    }
 }
 
 // dst[c] = src[c] for up to 64 items of `words` words each (gathers scattered ciphertexts into one batch)
@@ -588,10 +625,8 @@ hipError_t launch_tensor(const Context& ctx, const uint64_t* a, const uint64_t* 
     return hipGetLastError();
 }
 
-hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_t* in, uint64_t in_bstride,
-                        const uint32_t* in_off, uint64_t* out, uint64_t out_bstride, const uint32_t* out_off,
-                        uint32_t B, hipStream_t st) {
-    if (plan.n_in > (uint32_t)kMaxBconvIn || plan.n_out > (uint32_t)kMaxBconvOut) return hipErrorInvalidValue;
+static BConvArgs bconv_args(const BConvPlan& plan, uint64_t in_bstride, const uint32_t* in_off, uint64_t out_bstride,
+                            const uint32_t* out_off, uint32_t n_written) {
     BConvArgs ba{};
     ba.n_in = plan.n_in;
     ba.n_out = plan.n_out;
@@ -603,32 +638,68 @@ hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_
         ba.in_prime[i] = (uint8_t)plan.in_idx[i];
     }
     for (uint32_t j = 0; j < plan.n_out; j++) {
-        ba.out_off[j] = (uint16_t)out_off[j];
+        ba.out_off[j] = (uint16_t)(j < n_written ? out_off[j] : 0);
         ba.out_prime[j] = (uint8_t)plan.out_idx[j];
     }
+    return ba;
+}
+
+hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_t* in, uint64_t in_bstride,
+                        const uint32_t* in_off, uint64_t* out, uint64_t out_bstride, const uint32_t* out_off,
+                        uint32_t B, hipStream_t st) {
+    if (plan.n_in > (uint32_t)kMaxBconvIn || plan.n_out > (uint32_t)kMaxBconvOut) return hipErrorInvalidValue;
+    const BConvArgs ba = bconv_args(plan, in_bstride, in_off, out_bstride, out_off, plan.n_out);
     const int pi = prof_begin(ctx, "bconv", (double)B * (plan.n_in + plan.n_out) * kN * 8, st);
-    hipLaunchKernelGGL(k_bconv, dim3(kN / 256, B), dim3(256), 0, st, in, out, ba, plan.d_tab, ctx.d_primes);
+    hipLaunchKernelGGL(k_bconv<false>, dim3(kN / 256, B), dim3(256), 0, st, in, out, ba, plan.d_tab, ctx.d_primes,
+                       MdrBconvArgs{});
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
 
-hipError_t launch_ks_inner(const Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* acc, uint32_t B,
-                           uint32_t l, hipStream_t st) {
-    ctx.n_keyswitch += B;
+// ModDown BConv fused with the rescale's lift (plan from bconv_plan with the P^-1 column scaling, outputs
+// 0..l-1 with l-1 last): in [n_polys] polys of stride in_bstride holding the P limbs (coefficient form) at
+// in_off; xlast = limb l-1 of the same polys (coefficient form); T [n_polys][l-1][N].
+hipError_t launch_bconv_mdr(const Context& ctx, const BConvPlan& plan, const uint64_t* in, uint64_t in_bstride,
+                            const uint32_t* in_off, uint64_t* T, uint32_t n_polys, const uint64_t* xlast,
+                            uint64_t xlast_pstride, const uint64_t* addc, TwPair pinv_last, hipStream_t st) {
+    if (plan.n_in > (uint32_t)kMaxBconvIn || plan.n_out > (uint32_t)kMaxBconvOut || plan.n_out < 2)
+        return hipErrorInvalidValue;
+    const uint32_t l = plan.n_out;
+    std::vector<uint32_t> out_off(l - 1);
+    for (uint32_t j = 0; j + 1 < l; j++) out_off[j] = j;
+    const BConvArgs ba = bconv_args(plan, in_bstride, in_off, (uint64_t)(l - 1) * kN, out_off.data(), l - 1);
+    const MdrBconvArgs mb{xlast, xlast_pstride, addc, pinv_last};
+    // P limbs + limb l-1 (+ the addend's) read, l-1 limbs written
+    const double bytes = (double)n_polys * (plan.n_in + 1 + (addc ? 1 : 0) + (l - 1)) * kN * 8;
+    const int pi = prof_begin(ctx, "bconv_mdr", bytes, st);
+    hipLaunchKernelGGL(k_bconv<true>, dim3(kN / 256, n_polys), dim3(256), 0, st, in, T, ba, plan.d_tab,
+                       ctx.d_primes, mb);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+static InnerArgs inner_args(const Context& ctx, uint32_t l, uint32_t B) {
     InnerArgs ia{};
     ia.E = l + ctx.K;
     ia.D = (l + ctx.alpha - 1) / ctx.alpha;
     ia.T = ctx.L + ctx.K;
     ia.B = B;
-    if (ia.D > (uint32_t)kMaxDigits || ia.E > kMaxPmap) return hipErrorInvalidValue;
-    for (uint32_t t = 0; t < ia.E; t++) ia.prime_of[t] = (uint8_t)(t < l ? t : ctx.L + (t - l));
-    // split the batch over grid.z so that the grid has enough workgroups; each z-slice keeps its
-    // evk words in registers across its ciphertexts
-    const uint32_t zs = B < 8 ? B : 8;
+    for (uint32_t t = 0; t < ia.E && t < kMaxPmap; t++) ia.prime_of[t] = (uint8_t)(t < l ? t : ctx.L + (t - l));
+    return ia;
+}
+
+// evk inner product of the extended limbs t0..E-1 (t0 > 0 when the combine forms the others itself)
+hipError_t launch_ks_inner(const Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* acc, uint32_t B,
+                           uint32_t l, hipStream_t st, uint32_t t0) {
+    ctx.n_keyswitch += B;
+    InnerArgs ia = inner_args(ctx, l, B);
+    if (ia.D > (uint32_t)kMaxDigits || ia.E > kMaxPmap || t0 >= ia.E) return hipErrorInvalidValue;
+    ia.t0 = t0;
+    const uint32_t nt = ia.E - t0;
     // ext read once per ciphertext, acc written once, the evk limbs of the level read once
-    const double bytes = ((double)B * (ia.D * ia.E + 2 * ia.E) + 2.0 * ia.D * ia.E) * kN * 8;
+    const double bytes = ((double)B * (ia.D * nt + 2 * nt) + 2.0 * ia.D * nt) * kN * 8;
     const int pi = prof_begin(ctx, "ks_inner", bytes, st);
-    hipLaunchKernelGGL(k_ks_inner, dim3(kN / 256, ia.E, zs), dim3(256), 0, st, ext, evk, acc, ia, ctx.d_primes);
+    hipLaunchKernelGGL(k_ks_inner, dim3(B, kN / 256, nt), dim3(256), 0, st, ext, evk, acc, ia, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
@@ -745,27 +816,34 @@ static MdrArgs mdr_args(uint32_t l, uint64_t x_pstride, uint64_t add_pstride, co
     return ma;
 }
 
-hipError_t launch_mdr(const Context& ctx, int step, const uint64_t* x, uint64_t x_pstride, const uint64_t* add,
-                      uint64_t add_pstride, const uint64_t* addc, const uint64_t* conv, uint64_t* z, uint64_t* T,
-                      uint64_t* out, uint32_t n_polys, uint32_t l, const TwPair* pinv, const TwPair* qlinv,
-                      hipStream_t st) {
+hipError_t launch_mdr_combine(const Context& ctx, const uint64_t* x, uint64_t x_pstride, const uint64_t* add,
+                              uint64_t add_pstride, const uint64_t* T, uint64_t* out, uint32_t n_polys, uint32_t l,
+                              const TwPair* pinv, const TwPair* qlinv, hipStream_t st) {
     if (l < 2 || l > (uint32_t)kMaxPmap) return hipErrorInvalidValue;
     const MdrArgs ma = mdr_args(l, x_pstride, add ? add_pstride : 0, pinv, qlinv);
-    if (step == 0) {
-        const int pi = prof_begin(ctx, "mdr_last", (double)n_polys * 4 * kN * 8, st);
-        hipLaunchKernelGGL(k_mdr_last, dim3(kN / 256, n_polys), dim3(256), 0, st, x, addc, conv, z, ma, ctx.d_primes);
-        prof_end(ctx, pi, st);
-    } else if (step == 1) {
-        const int pi = prof_begin(ctx, "mdr_lift", (double)n_polys * (2 * (l - 1) + 1) * kN * 8, st);
-        hipLaunchKernelGGL(k_mdr_lift, dim3(kN / 256, l - 1, n_polys), dim3(256), 0, st, conv, z, T, ma,
-                           ctx.d_primes);
-        prof_end(ctx, pi, st);
-    } else {
-        const int pi = prof_begin(ctx, "mdr_combine", (double)n_polys * (l - 1) * (add ? 4 : 3) * kN * 8, st);
-        hipLaunchKernelGGL(k_mdr_combine, dim3(kN / 256, l - 1, n_polys), dim3(256), 0, st, x, add, T, out, ma,
-                           ctx.d_primes);
-        prof_end(ctx, pi, st);
-    }
+    const int pi = prof_begin(ctx, "mdr_combine", (double)n_polys * (l - 1) * (add ? 4 : 3) * kN * 8, st);
+    hipLaunchKernelGGL(k_mdr_combine, dim3(kN / 256, l - 1, n_polys), dim3(256), 0, st, x, add, T, out, ma,
+                       ctx.d_primes);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+// the same combine for a relinearization of B ciphertexts (polys 2c, 2c+1), the evk inner product of limbs
+// 0..l-2 formed in the kernel from ext [B][D][E][N] and evk [dnum][2][L+K][N]
+hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const uint64_t* evk, const uint64_t* add,
+                                 uint64_t add_pstride, const uint64_t* T, uint64_t* out, uint32_t B, uint32_t l,
+                                 const TwPair* pinv, const TwPair* qlinv, hipStream_t st) {
+    if (l < 2 || l > (uint32_t)kMaxPmap) return hipErrorInvalidValue;
+    const InnerArgs ia = inner_args(ctx, l, B);
+    if (ia.D > (uint32_t)kMaxDigits || ia.E > kMaxPmap) return hipErrorInvalidValue;
+    const MdrArgs ma = mdr_args(l, 0, add ? add_pstride : 0, pinv, qlinv);
+    // per ciphertext: D ext limbs, 2 T, 2 add (if any), 2 out; the level's evk limbs once
+    const double bytes =
+        ((double)B * (ia.D + 2 + (add ? 2 : 0) + 2) + 2.0 * ia.D) * (l - 1) * kN * 8;
+    const int pi = prof_begin(ctx, "mdr_combine_ks", bytes, st);
+    hipLaunchKernelGGL(k_mdr_combine_ks, dim3(B, kN / 256, l - 1), dim3(256), 0, st, ext, evk, add, T, out, ia, ma,
+                       ctx.d_primes);
+    prof_end(ctx, pi, st);
     return hipGetLastError();
 }
 
