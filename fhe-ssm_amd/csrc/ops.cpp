@@ -51,7 +51,10 @@ hipError_t launch_add(const Context& ctx, const uint64_t* x, const uint64_t* y, 
 hipError_t launch_automorph(const uint64_t* in, uint64_t* out, uint32_t n_polys, uint32_t l, uint32_t g,
                             hipStream_t st);
 hipError_t launch_ks_inner_list(const Context& ctx, const uint64_t* const* ext, const uint64_t* const* evk,
-                                uint64_t* acc, uint32_t n, uint32_t l, hipStream_t st);
+                                uint64_t* acc, uint32_t n, uint32_t l, hipStream_t st, uint32_t t0 = 0);
+hipError_t launch_ks_sub_list(const Context& ctx, const uint64_t* const* ext, const uint64_t* const* evk,
+                              const uint64_t* conv, const uint64_t* add, uint64_t add_stride, uint32_t add_group,
+                              uint64_t* out, uint32_t n, uint32_t l, const TwPair* pinv, hipStream_t st);
 hipError_t launch_automorph_list(const Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n, uint32_t l,
                                  const uint32_t* g, hipStream_t st);
 hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* baby, const uint64_t* diag, uint64_t* out, uint32_t nb,
@@ -356,6 +359,46 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
                                 st));
 }
 
+// Key switch of a list of n <= 64 items (item c: extended digits ext[c] [D][E][N], key evk[c]) with its ModDown:
+// out [n][2][l][N] = ((sum_d ext_c[d] evk_c[d])_Q - BConv_{P->Q}(.._P)) P^-1, plus the addend's poly 0 (the
+// ciphertext at add + (c / add_group) * add_stride) on poly 0.  The inner product is stored only for the P
+// limbs; the combine forms the Q limbs itself, and P^-1 rides in the BConv table.  Same words as
+// k_ks_inner_list + moddown_inplace.
+void ks_moddown_list(Context& ctx, const uint64_t* const* ext, const uint64_t* const* evk, uint32_t n, uint32_t l,
+                     const uint64_t* add, uint64_t add_stride, uint32_t add_group, uint64_t* out, hipStream_t st) {
+    check_level(ctx, l);
+    const uint32_t E = l + ctx.K, K = ctx.K;
+    if (K == 0) throw std::invalid_argument("ModDown needs special primes");
+    uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)n * 2 * E * W * 8);
+    HIPX(launch_ks_inner_list(ctx, ext, evk, acc, n, l, st, l));
+    std::vector<Job> jobs;
+    for (uint32_t pc = 0; pc < 2 * n; pc++)
+        for (uint32_t k = 0; k < K; k++) jobs.push_back(Job{pc * E + l + k, ctx.L + k});
+    const JobSpec js = cached_jobs(ctx, "mdP:" + std::to_string(2 * n) + ":" + std::to_string(l), std::move(jobs));
+    HIPX(launch_ntt(ctx, acc, js, 2 * n * K, true, ctx.ntt_mode, st));
+    std::vector<uint32_t> in_idx, in_off, out_idx;
+    for (uint32_t k = 0; k < K; k++) {
+        in_idx.push_back(ctx.L + k);
+        in_off.push_back(l + k);
+    }
+    std::vector<TwPair> pinv(l);
+    std::vector<uint64_t> col(l);
+    for (uint32_t i = 0; i < l; i++) {
+        out_idx.push_back(i);
+        const uint64_t q = ctx.moduli[i];
+        uint64_t P = 1;
+        for (uint32_t k = 0; k < K; k++) P = mulmod_h(P, ctx.moduli[ctx.L + k] % q, q);
+        col[i] = invmod_h(P, q);
+        pinv[i] = TwPair{col[i], shoup_companion(col[i], q)};
+    }
+    const BConvPlan& plan = bconv_plan(ctx, in_idx, out_idx, ctx.moddown_exact, col);
+    uint64_t* conv = (uint64_t*)ws_get(ctx, WS_CONV, (size_t)2 * n * l * W * 8);
+    HIPX(launch_bconv(ctx, plan, acc, (uint64_t)E * W, in_off.data(), conv, (uint64_t)l * W, out_idx.data(), 2 * n,
+                      st));
+    HIPX(launch_ntt(ctx, conv, regular_jobs(2 * n, out_idx), 2 * n * l, false, ctx.ntt_mode, st));
+    HIPX(launch_ks_sub_list(ctx, ext, evk, conv, add, add_stride, add_group, out, n, l, pinv.data(), st));
+}
+
 // ------------------------------------------------------------------ key switch
 // x: [B][l][N] eval; evk [dnum][2][L+K][N]; out2: [B][2][l][N] (+= add [B][2][l][N] if given)
 void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
@@ -500,7 +543,6 @@ void automorph_ks_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l
     const uint32_t D = num_digits(ctx, l), E = l + ctx.K;
     uint64_t* c1 = (uint64_t*)ws_get(ctx, WS_C1, (size_t)n * l * W * 8);
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)n * D * E * W * 8);
-    uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)n * 2 * E * W * 8);
     uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)n * 2 * l * W * 8);
     HIPX(hipMemcpy2DAsync(c1, (size_t)l * W * 8, cts + (size_t)l * W, (size_t)2 * l * W * 8, (size_t)l * W * 8, n,
                           hipMemcpyDeviceToDevice, st));
@@ -510,8 +552,7 @@ void automorph_ks_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l
         ep[c] = ext + (size_t)c * D * E * W;
         if ((gidx[c] & 1) == 0 || gidx[c] >= 2 * kN) throw std::invalid_argument("automorphism index must be odd < 2N");
     }
-    HIPX(launch_ks_inner_list(ctx, ep.data(), evk, acc, n, l, st));
-    moddown_inplace(ctx, acc, 2 * n, l, cts, ks, st, 2);
+    ks_moddown_list(ctx, ep.data(), evk, n, l, cts, (uint64_t)2 * l * W, 1, ks, st);
     HIPX(launch_automorph_list(ctx, ks, out, n, l, gidx, st));
 }
 
@@ -536,15 +577,12 @@ void rotate_hoisted_ext(Context& ctx, const uint64_t* ct, const uint64_t* ext, u
                                out + (size_t)c0 * 2 * l * W, st);
         return;
     }
-    const uint32_t E = l + ctx.K;
-    uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)n * 2 * E * W * 8);
     uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)n * 2 * l * W * 8);
     std::vector<const uint64_t*> ep(n, ext);
     std::vector<uint32_t> g(n);
     for (uint32_t c = 0; c < n; c++) g[c] = rotation_index(steps[c]);
-    HIPX(launch_ks_inner_list(ctx, ep.data(), evk, acc, n, l, st));
     // c0 (the same for every rotation) is the ModDown addend of poly 0 of each output
-    moddown_inplace(ctx, acc, 2 * n, l, ct, ks, st, 2, 0);
+    ks_moddown_list(ctx, ep.data(), evk, n, l, ct, 0, 1, ks, st);
     HIPX(launch_automorph_list(ctx, ks, out, n, l, g.data(), st));
 }
 
@@ -570,7 +608,6 @@ void rotate_hoisted_multi(Context& ctx, const uint64_t* cts, uint32_t n_ct, uint
     const uint32_t per = 64 / n;  // ciphertexts per list (a list starts at a ciphertext boundary)
     for (uint32_t c0 = 0; c0 < n_ct; c0 += per) {
         const uint32_t nc = std::min(per, n_ct - c0), m = nc * n;
-        uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)m * 2 * E * W * 8);
         uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)m * 2 * l * W * 8);
         std::vector<const uint64_t*> ep(m), kp(m);
         std::vector<uint32_t> gm(m);
@@ -579,9 +616,8 @@ void rotate_hoisted_multi(Context& ctx, const uint64_t* cts, uint32_t n_ct, uint
             kp[j] = evk[j % n];
             gm[j] = g[j % n];
         }
-        HIPX(launch_ks_inner_list(ctx, ep.data(), kp.data(), acc, m, l, st));
         // c0 of ciphertext c is the addend of poly 0 of its n outputs
-        moddown_inplace(ctx, acc, 2 * m, l, cts + (size_t)c0 * ctw, ks, st, 2, (int64_t)ctw, 2 * n);
+        ks_moddown_list(ctx, ep.data(), kp.data(), m, l, cts + (size_t)c0 * ctw, ctw, n, ks, st);
         HIPX(launch_automorph_list(ctx, ks, out + (size_t)c0 * n * ctw, m, l, gm.data(), st));
     }
 }

@@ -336,8 +336,8 @@ struct ListPtrs {
 
 __global__ __launch_bounds__(256) void k_ks_inner_list(ListPtrs ext, ListPtrs evk, uint64_t* __restrict__ acc,
                                                        InnerArgs ia, const PrimeInfo* __restrict__ primes) {
-    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
-    const uint32_t t = blockIdx.y, c = blockIdx.z;
+    const uint32_t c = blockIdx.x, k = blockIdx.y * 256 + threadIdx.x;
+    const uint32_t t = ia.t0 + blockIdx.z;
     const uint32_t p = ia.prime_of[t];
     const Barrett br = barrett_of(primes[p]);
     const uint64_t* x = ext.p[c] + (size_t)t * kN + k;
@@ -354,6 +354,42 @@ __global__ __launch_bounds__(256) void k_ks_inner_list(ListPtrs ext, ListPtrs ev
     uint64_t* o = acc + (size_t)c * 2 * ia.E * kN + (size_t)t * kN + k;
     o[0] = reduce_u128(s0.get(), br);
     o[(size_t)ia.E * kN] = reduce_u128(s1.get(), br);
+}
+
+// ModDown combine of a key-switch list with the evk inner product of the Q limbs formed on the fly:
+//   out[c][p][i] = x P^-1 - conv[c][p][i]  (+ the addend's poly 0 for p = 0),  x = sum_d ext_c[d][i] evk_c[d][p][i]
+// conv [n][2][l][N] is the evaluation form of the P -> Q BConv with P^-1 folded into its table; item c's addend
+// is the ciphertext at add + (c / add_group) * add_stride.  Grid: item fastest (hoisted items share ext).
+struct PinvArgs {
+    TwPair pinv[kMaxPmap];  // P^-1 mod q_i
+};
+
+__global__ __launch_bounds__(256) void k_ks_sub_list(ListPtrs ext, ListPtrs evk, const uint64_t* __restrict__ conv,
+                                                     const uint64_t* __restrict__ add, uint64_t add_stride,
+                                                     uint32_t add_group, uint64_t* __restrict__ out, uint32_t l,
+                                                     InnerArgs ia, PinvArgs pa, const PrimeInfo* __restrict__ primes) {
+    const uint32_t c = blockIdx.x, k = blockIdx.y * 256 + threadIdx.x, i = blockIdx.z;
+    const Barrett br = barrett_of(primes[i]);
+    const uint64_t q = br.q;
+    const size_t li = (size_t)i * kN + k;
+    const uint64_t* x = ext.p[c] + li;
+    const uint64_t* e = evk.p[c] + li;
+    Acc s0, s1;
+#pragma unroll
+    for (int d = 0; d < kMaxDigits; d++) {
+        if (d < (int)ia.D) {
+            const uint64_t v = x[(size_t)d * ia.E * kN];
+            s0.add(v, e[((size_t)d * 2 + 0) * ia.T * kN]);
+            s1.add(v, e[((size_t)d * 2 + 1) * ia.T * kN]);
+        }
+    }
+    const size_t pw = (size_t)l * kN;  // words per poly of conv and out
+    const uint64_t* cv = conv + (size_t)c * 2 * pw + li;
+    uint64_t* o = out + (size_t)c * 2 * pw + li;
+    uint64_t v0 = sub_mod(shoup(reduce_u128(s0.get(), br), pa.pinv[i].w, pa.pinv[i].wp, q), cv[0], q);
+    if (add) v0 = add_mod(v0, add[(size_t)(c / add_group) * add_stride + li], q);
+    o[0] = v0;
+    o[pw] = sub_mod(shoup(reduce_u128(s1.get(), br), pa.pinv[i].w, pa.pinv[i].wp, q), cv[pw], q);
 }
 
 // ---------------------------------------------------------------- ModDown fused with the following rescale
@@ -742,15 +778,13 @@ hipError_t launch_add(const Context& ctx, const uint64_t* x, const uint64_t* y, 
 }
 
 hipError_t launch_ks_inner_list(const Context& ctx, const uint64_t* const* ext, const uint64_t* const* evk,
-                                uint64_t* acc, uint32_t n, uint32_t l, hipStream_t st) {
+                                uint64_t* acc, uint32_t n, uint32_t l, hipStream_t st, uint32_t t0) {
     ctx.n_keyswitch += n;
-    InnerArgs ia{};
-    ia.E = l + ctx.K;
-    ia.D = (l + ctx.alpha - 1) / ctx.alpha;
-    ia.T = ctx.L + ctx.K;
-    ia.B = n;
-    if (ia.D > (uint32_t)kMaxDigits || ia.E > kMaxPmap || n > (uint32_t)kMaxList) return hipErrorInvalidValue;
-    for (uint32_t t = 0; t < ia.E; t++) ia.prime_of[t] = (uint8_t)(t < l ? t : ctx.L + (t - l));
+    InnerArgs ia = inner_args(ctx, l, n);
+    if (ia.D > (uint32_t)kMaxDigits || ia.E > kMaxPmap || n > (uint32_t)kMaxList || t0 >= ia.E)
+        return hipErrorInvalidValue;
+    ia.t0 = t0;
+    const uint32_t nt = ia.E - t0;
     ListPtrs pe{}, pk{};
     uint32_t distinct_ext = 0;
     for (uint32_t c = 0; c < n; c++) {
@@ -758,9 +792,35 @@ hipError_t launch_ks_inner_list(const Context& ctx, const uint64_t* const* ext, 
         pk.p[c] = evk[c];
         distinct_ext += (c == 0 || ext[c] != ext[c - 1]) ? 1 : 0;
     }
-    const double bytes = ((double)distinct_ext * ia.D * ia.E + (double)n * (2 * ia.D * ia.E + 2 * ia.E)) * kN * 8;
+    const double bytes = ((double)distinct_ext * ia.D * nt + (double)n * (2 * ia.D * nt + 2 * nt)) * kN * 8;
     const int pi = prof_begin(ctx, "ks_inner_list", bytes, st);
-    hipLaunchKernelGGL(k_ks_inner_list, dim3(kN / 256, ia.E, n), dim3(256), 0, st, pe, pk, acc, ia, ctx.d_primes);
+    hipLaunchKernelGGL(k_ks_inner_list, dim3(n, kN / 256, nt), dim3(256), 0, st, pe, pk, acc, ia, ctx.d_primes);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+// out [n][2][l][N] = ModDown combine of a key-switch list (k_ks_sub_list); conv [n][2][l][N] evaluation form
+hipError_t launch_ks_sub_list(const Context& ctx, const uint64_t* const* ext, const uint64_t* const* evk,
+                              const uint64_t* conv, const uint64_t* add, uint64_t add_stride, uint32_t add_group,
+                              uint64_t* out, uint32_t n, uint32_t l, const TwPair* pinv, hipStream_t st) {
+    InnerArgs ia = inner_args(ctx, l, n);
+    if (ia.D > (uint32_t)kMaxDigits || ia.E > kMaxPmap || n > (uint32_t)kMaxList || add_group == 0)
+        return hipErrorInvalidValue;
+    ListPtrs pe{}, pk{};
+    uint32_t distinct_ext = 0;
+    for (uint32_t c = 0; c < n; c++) {
+        pe.p[c] = ext[c];
+        pk.p[c] = evk[c];
+        distinct_ext += (c == 0 || ext[c] != ext[c - 1]) ? 1 : 0;
+    }
+    PinvArgs pa{};
+    for (uint32_t i = 0; i < l; i++) pa.pinv[i] = pinv[i];
+    // ext limbs (once per distinct ext), evk, conv and out per item, addend polys once per group
+    const double bytes = ((double)distinct_ext * ia.D + (double)n * (2 * ia.D + 4) +
+                          (add ? (double)(n + add_group - 1) / add_group : 0.0)) * l * kN * 8;
+    const int pi = prof_begin(ctx, "ks_sub_list", bytes, st);
+    hipLaunchKernelGGL(k_ks_sub_list, dim3(n, kN / 256, l), dim3(256), 0, st, pe, pk, conv, add, add_stride,
+                       add_group, out, l, ia, pa, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
