@@ -117,7 +117,7 @@ __device__ __forceinline__ uint64_t lift_centered(uint64_t v, uint64_t ql, const
     return v >= q ? reduce128(0, v, br) : v;
 }
 
-// Extra inputs of the ModDown BConv fused with the rescale that follows (k_bconv<true>).  The plan's last
+// Extra inputs of the ModDown BConv fused with the rescale that follows (k_bconv<NIN, true>).  The plan's last
 // output column is the dropped limb l-1 (plain table); every other column j has P^-1 mod q_j folded into its
 // table, so the column sums are conv_j P^-1 directly.  Per coefficient the kernel forms
 //   z = addc + (x_{l-1} - conv_{l-1}) P^-1  (mod q_{l-1}, x_{l-1} and addc in coefficient form)
@@ -129,7 +129,8 @@ struct MdrBconvArgs {
     TwPair pinv_last;       // P^-1 mod q_{l-1}
 };
 
-template <bool kMdr>
+// NIN = number of input limbs (a template parameter: the term loops unroll without run-time guards)
+template <int NIN, bool kMdr>
 __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
                                                BConvArgs ba, const uint64_t* __restrict__ tab,
                                                const PrimeInfo* __restrict__ primes, MdrBconvArgs mb) {
@@ -139,13 +140,11 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
     uint64_t* dst = out + c * ba.out_bstride + k;
     const TwPair* qhinv = reinterpret_cast<const TwPair*>(tab);
     const uint64_t* qhmod = tab + 2 * ba.n_in;
-    uint64_t y[kMaxBconvIn];
+    uint64_t y[NIN];
 #pragma unroll
-    for (int i = 0; i < kMaxBconvIn; i++) {
-        if (i < (int)ba.n_in) {
-            const uint64_t q = primes[ba.in_prime[i]].q;
-            y[i] = shoup(src[(size_t)ba.in_off[i] * kN], qhinv[i].w, qhinv[i].wp, q);
-        }
+    for (int i = 0; i < NIN; i++) {
+        const uint64_t q = primes[ba.in_prime[i]].q;
+        y[i] = shoup(src[(size_t)ba.in_off[i] * kN], qhinv[i].w, qhinv[i].wp, q);
     }
     // centered form (exact ModDown): u = round(sum_i y_i / q_i) from the 128-bit fixed-point sum of
     // floor(y_i * floor(2^128 / q_i) / 2^64); the table then holds [n_in] (lo, hi) words of floor(2^128 / q_i)
@@ -156,13 +155,11 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
     if (ba.centered) {
         U128 F{0, 0};
 #pragma unroll
-        for (int i = 0; i < kMaxBconvIn; i++) {
-            if (i < (int)ba.n_in) {
-                mac128(F, y[i], cfix[2 * i + 1]);
-                const uint64_t h = mulhi64(y[i], cfix[2 * i]);
-                F.lo += h;
-                F.hi += (F.lo < h) ? 1 : 0;
-            }
+        for (int i = 0; i < NIN; i++) {
+            mac128(F, y[i], cfix[2 * i + 1]);
+            const uint64_t h = mulhi64(y[i], cfix[2 * i]);
+            F.lo += h;
+            F.hi += (F.lo < h) ? 1 : 0;
         }
         const uint64_t lo = F.lo + (1ull << 63);
         u = F.hi + (lo < F.lo ? 1 : 0);
@@ -184,8 +181,8 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         n_main = ba.n_out - 1;
         Acc a;
 #pragma unroll
-        for (int i = 0; i < kMaxBconvIn; i++) {
-            if (i < (int)ba.n_in) a.add(y[i], qhmod[(size_t)i * ba.n_out + n_main]);
+        for (int i = 0; i < NIN; i++) {
+            a.add(y[i], qhmod[(size_t)i * ba.n_out + n_main]);
             if (i == 7) a.fold();
         }
         const Barrett bl = barrett_of(primes[ba.out_prime[n_main]]);
@@ -209,11 +206,9 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
     for (; j + 1 < n_main; j += 2) {
         Acc a, b;
 #pragma unroll
-        for (int i = 0; i < kMaxBconvIn; i++) {
-            if (i < (int)ba.n_in) {
-                a.add(y[i], qhmod[(size_t)i * ba.n_out + j]);
-                b.add(y[i], qhmod[(size_t)i * ba.n_out + j + 1]);
-            }
+        for (int i = 0; i < NIN; i++) {
+            a.add(y[i], qhmod[(size_t)i * ba.n_out + j]);
+            b.add(y[i], qhmod[(size_t)i * ba.n_out + j + 1]);
             if (i == 7) {
                 a.fold();
                 b.fold();
@@ -225,11 +220,36 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
     if (j < n_main) {
         Acc a;
 #pragma unroll
-        for (int i = 0; i < kMaxBconvIn; i++) {
-            if (i < (int)ba.n_in) a.add(y[i], qhmod[(size_t)i * ba.n_out + j]);
+        for (int i = 0; i < NIN; i++) {
+            a.add(y[i], qhmod[(size_t)i * ba.n_out + j]);
             if (i == 7) a.fold();
         }
         finish(a, j);
+    }
+}
+
+// k_bconv instance for a run-time input count (1..kMaxBconvIn)
+template <bool kMdr>
+static void (*bconv_kernel(uint32_t n_in))(const uint64_t*, uint64_t*, BConvArgs, const uint64_t*, const PrimeInfo*,
+                                           MdrBconvArgs) {
+    switch (n_in) {
+        case 1: return k_bconv<1, kMdr>;
+        case 2: return k_bconv<2, kMdr>;
+        case 3: return k_bconv<3, kMdr>;
+        case 4: return k_bconv<4, kMdr>;
+        case 5: return k_bconv<5, kMdr>;
+        case 6: return k_bconv<6, kMdr>;
+        case 7: return k_bconv<7, kMdr>;
+        case 8: return k_bconv<8, kMdr>;
+        case 9: return k_bconv<9, kMdr>;
+        case 10: return k_bconv<10, kMdr>;
+        case 11: return k_bconv<11, kMdr>;
+        case 12: return k_bconv<12, kMdr>;
+        case 13: return k_bconv<13, kMdr>;
+        case 14: return k_bconv<14, kMdr>;
+        case 15: return k_bconv<15, kMdr>;
+        case 16: return k_bconv<16, kMdr>;
+        default: return nullptr;
     }
 }
 
@@ -398,7 +418,7 @@ __global__ __launch_bounds__(256) void k_ks_sub_list(ListPtrs ext, ListPtrs evk,
 //   out_i = (add_i + x_i P^-1 - NTT(T_i)) q_l^-1,  T_i = conv_i P^-1 + lift(z)_i,
 //   z = INTT(add_{l-1}) + (INTT(x_{l-1}) - conv_{l-1}) P^-1   (mod q_{l-1}):
 // the same words with one forward NTT of l-1 limbs instead of two (l for conv, l-1 for the lift).  The BConv
-// writes T directly (k_bconv<true>); in a relinearization the evk inner product of limbs 0..l-2 is formed inside
+// writes T directly (k_bconv<NIN, true>); in a relinearization the evk inner product of limbs 0..l-2 is formed inside
 // the combine (k_mdr_combine_ks) and never stored.
 struct MdrArgs {
     uint32_t l;           // limbs before the rescale
@@ -683,11 +703,12 @@ static BConvArgs bconv_args(const BConvPlan& plan, uint64_t in_bstride, const ui
 hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_t* in, uint64_t in_bstride,
                         const uint32_t* in_off, uint64_t* out, uint64_t out_bstride, const uint32_t* out_off,
                         uint32_t B, hipStream_t st) {
-    if (plan.n_in > (uint32_t)kMaxBconvIn || plan.n_out > (uint32_t)kMaxBconvOut) return hipErrorInvalidValue;
+    if (plan.n_in == 0 || plan.n_in > (uint32_t)kMaxBconvIn || plan.n_out > (uint32_t)kMaxBconvOut)
+        return hipErrorInvalidValue;
     const BConvArgs ba = bconv_args(plan, in_bstride, in_off, out_bstride, out_off, plan.n_out);
     const int pi = prof_begin(ctx, "bconv", (double)B * (plan.n_in + plan.n_out) * kN * 8, st);
-    hipLaunchKernelGGL(k_bconv<false>, dim3(kN / 256, B), dim3(256), 0, st, in, out, ba, plan.d_tab, ctx.d_primes,
-                       MdrBconvArgs{});
+    hipLaunchKernelGGL(bconv_kernel<false>(plan.n_in), dim3(kN / 256, B), dim3(256), 0, st, in, out, ba, plan.d_tab,
+                       ctx.d_primes, MdrBconvArgs{});
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
@@ -698,7 +719,7 @@ hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_
 hipError_t launch_bconv_mdr(const Context& ctx, const BConvPlan& plan, const uint64_t* in, uint64_t in_bstride,
                             const uint32_t* in_off, uint64_t* T, uint32_t n_polys, const uint64_t* xlast,
                             uint64_t xlast_pstride, const uint64_t* addc, TwPair pinv_last, hipStream_t st) {
-    if (plan.n_in > (uint32_t)kMaxBconvIn || plan.n_out > (uint32_t)kMaxBconvOut || plan.n_out < 2)
+    if (plan.n_in == 0 || plan.n_in > (uint32_t)kMaxBconvIn || plan.n_out > (uint32_t)kMaxBconvOut || plan.n_out < 2)
         return hipErrorInvalidValue;
     const uint32_t l = plan.n_out;
     std::vector<uint32_t> out_off(l - 1);
@@ -708,8 +729,8 @@ hipError_t launch_bconv_mdr(const Context& ctx, const BConvPlan& plan, const uin
     // P limbs + limb l-1 (+ the addend's) read, l-1 limbs written
     const double bytes = (double)n_polys * (plan.n_in + 1 + (addc ? 1 : 0) + (l - 1)) * kN * 8;
     const int pi = prof_begin(ctx, "bconv_mdr", bytes, st);
-    hipLaunchKernelGGL(k_bconv<true>, dim3(kN / 256, n_polys), dim3(256), 0, st, in, T, ba, plan.d_tab,
-                       ctx.d_primes, mb);
+    hipLaunchKernelGGL(bconv_kernel<true>(plan.n_in), dim3(kN / 256, n_polys), dim3(256), 0, st, in, T, ba,
+                       plan.d_tab, ctx.d_primes, mb);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
