@@ -480,9 +480,9 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint3
                    const uint64_t* conj_evk, const int64_t* steps, const uint64_t* const* evks, uint32_t n_keys,
                    uint64_t* out, hipStream_t st, uint32_t stop_stage) {
     if (B == 0) return P.l_out;
+    // stream-ordered like every call on a context: the pooled buffers go back for reuse by later work on st
     auto emit = [&](const uint64_t* src, uint32_t n, uint32_t l) {
         HIPB(hipMemcpyAsync(out, src, (size_t)n * 2 * l * W * 8, hipMemcpyDeviceToDevice, st));
-        HIPB(hipStreamSynchronize(st));
         return l;
     };
     const uint32_t L = ctx.L;

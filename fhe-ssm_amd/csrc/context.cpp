@@ -183,6 +183,11 @@ void context_release(Context& c) {
     for (auto& kv : c.buf_pool)
         for (auto* p : kv.second) (void)hipFree(p);
     c.buf_pool.clear();
+    if (c.ring_host) (void)hipHostFree(c.ring_host);
+    if (c.ring_dev) (void)hipFree(c.ring_dev);
+    for (auto& e : c.ring_ev)
+        if (e) (void)hipEventDestroy(e);
+    c.ring_host = c.ring_dev = nullptr;
     c.job_cache.clear();
     c.bconv_cache.clear();
     c.scratch.clear();

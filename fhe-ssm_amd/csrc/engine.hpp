@@ -79,6 +79,15 @@ struct Context {
     // free device buffers by size, reused across bootstrapping calls (a call needs tens of buffers of
     // B x 2 x L limbs; allocating them per call costs more than the smaller kernels it runs)
     std::map<size_t, std::vector<uint64_t*>> buf_pool;
+    // ring of pinned host + device slots for per-call tables (pointer lists) copied asynchronously; a slot is
+    // reused once the event recorded after the kernel that read it has completed
+    static constexpr uint32_t kRingSlots = 16;
+    static constexpr size_t kRingSlotBytes = 64 * 1024;
+    uint8_t* ring_host = nullptr;
+    uint8_t* ring_dev = nullptr;
+    hipEvent_t ring_ev[kRingSlots] = {};
+    bool ring_used[kRingSlots] = {};
+    uint32_t ring_next = 0;
     // per-launch profiling (off by default)
     bool prof_on = false;
     mutable std::vector<ProfRec> prof;

@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstring>
 #include <stdexcept>
 #include <string>
 
@@ -133,6 +134,27 @@ void* ws_get(Context& ctx, uint32_t slot, size_t bytes) {
         s.second = bytes;
     }
     return s.first;
+}
+
+// ------------------------------------------------------------------ pinned table ring
+// The next ring slot, waiting (rarely) for the kernel that last read it; allocates the ring on first use.
+uint32_t ring_acquire(Context& ctx) {
+    if (!ctx.ring_host) {
+        HIPX(hipHostMalloc((void**)&ctx.ring_host, Context::kRingSlots * Context::kRingSlotBytes,
+                           hipHostMallocDefault));
+        HIPX(hipMalloc((void**)&ctx.ring_dev, Context::kRingSlots * Context::kRingSlotBytes));
+        for (auto& e : ctx.ring_ev) HIPX(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    }
+    const uint32_t slot = ctx.ring_next;
+    ctx.ring_next = (ctx.ring_next + 1) % Context::kRingSlots;
+    if (ctx.ring_used[slot]) HIPX(hipEventSynchronize(ctx.ring_ev[slot]));
+    return slot;
+}
+
+// marks the slot busy until the work enqueued on st so far (the copy and the kernel reading it) completes
+void ring_release(Context& ctx, uint32_t slot, hipStream_t st) {
+    HIPX(hipEventRecord(ctx.ring_ev[slot], st));
+    ctx.ring_used[slot] = true;
 }
 
 // ------------------------------------------------------------------ BConv plans
@@ -484,13 +506,24 @@ void hmult_sum(Context& ctx, const uint64_t* const* pairs, uint32_t np, uint32_t
     uint64_t* x2c = (uint64_t*)ws_get(ctx, WS_X2C, (size_t)B * l * W * 8);
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)B * D * E * W * 8);
     const size_t tab_bytes = (size_t)B * np * 2 * sizeof(void*);
-    auto* d_tab = (const uint64_t**)ws_get(ctx, WS_PTAB, tab_bytes);
-    HIPX(hipMemcpyAsync(d_tab, pairs, tab_bytes, hipMemcpyHostToDevice, st));
     std::vector<uint32_t> ext_off(l);
     for (uint32_t t = 0; t < l; t++) ext_off[t] = (t / ctx.alpha) * E + t;
-    HIPX(launch_tensor_sum(ctx, d_tab, np, d01, x2c, B, l, ext, (uint64_t)D * E * W, ext_off.data(), st));
-    // the pointer table must outlive the copy: the caller's array may be freed on return
-    HIPX(hipStreamSynchronize(st));
+    if (tab_bytes <= Context::kRingSlotBytes) {
+        // staged through the pinned ring: the copy is asynchronous and the caller's array may go at once
+        const uint32_t slot = ring_acquire(ctx);
+        uint8_t* h = ctx.ring_host + (size_t)slot * Context::kRingSlotBytes;
+        auto* d_tab = (const uint64_t**)(ctx.ring_dev + (size_t)slot * Context::kRingSlotBytes);
+        std::memcpy(h, pairs, tab_bytes);
+        HIPX(hipMemcpyAsync(d_tab, h, tab_bytes, hipMemcpyHostToDevice, st));
+        HIPX(launch_tensor_sum(ctx, d_tab, np, d01, x2c, B, l, ext, (uint64_t)D * E * W, ext_off.data(), st));
+        ring_release(ctx, slot, st);
+    } else {
+        auto* d_tab = (const uint64_t**)ws_get(ctx, WS_PTAB, tab_bytes);
+        HIPX(hipMemcpyAsync(d_tab, pairs, tab_bytes, hipMemcpyHostToDevice, st));
+        HIPX(launch_tensor_sum(ctx, d_tab, np, d01, x2c, B, l, ext, (uint64_t)D * E * W, ext_off.data(), st));
+        // the pointer table must outlive the copy: the caller's array may be freed on return
+        HIPX(hipStreamSynchronize(st));
+    }
     relin_tail(ctx, d01, x2c, ext, B, l, evk, out, do_rescale, st);
 }
 

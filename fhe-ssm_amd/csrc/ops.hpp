@@ -27,6 +27,8 @@ enum WsSlot : uint32_t {
 };
 
 void* ws_get(Context& ctx, uint32_t slot, size_t bytes);
+uint32_t ring_acquire(Context& ctx);
+void ring_release(Context& ctx, uint32_t slot, hipStream_t st);
 // col_scale (optional, one factor per output): every table column j (and its centered correction) is multiplied
 // by col_scale[j] mod p_j, so output j comes out as conv_j * col_scale[j]
 const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, const std::vector<uint32_t>& out_idx,
