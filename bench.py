@@ -296,11 +296,12 @@ def bench_bootstrap(ckks, torch, steps_n, warmup, seed):
 DECODE_LANES = 32
 
 
-def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12):
+def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native"):
     """Config 5: one encrypted decode step of the RWKV-7-0.1B-shaped polynomial model (12 layers, 32 lanes in
     the slots, state carried across steps, state bootstrapped once per layer).  The client side (token
     embedding + encryption before the step, decryption + the 768 x 65536 vocabulary head after it) is
-    outside the timed region and reported separately."""
+    outside the timed region and reported separately.  driver: "native" runs the C++ driver
+    (libfhe_ssm_decode.so), "python" the same plan in decode_step.py (identical engine calls and words)."""
     from engine_loader import load_module
     DS = load_module("decode_step")
     M = load_module("rwkv_model")
@@ -310,7 +311,20 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12):
     log = lambda msg: print(f"[decode] {msg}", file=sys.stderr, flush=True)
     log(f"keys ready in {t_keys:.1f} s ({len(be.keys)} rotation keys)")
     W = M.make_weights(seed + 4, n_layers)
-    step = DS.DecodeStep(be, W)
+    if driver == "native":
+        ND = load_module("native_decode")
+        nat = ND.from_backend(be, n_layers)
+        nat.set_weights(W)
+
+        def step(ct):
+            out, lv, sc = nat.step(ct.ptr(), ct.level, ct.scale)
+            return DS.HECt(out, 1, lv, sc)
+
+        n_boot = lambda: nat.bootstraps
+    else:
+        py = DS.DecodeStep(be, W)
+        step = py
+        n_boot = lambda: py.stats["bootstraps"]
     ctx = be.ctx
     tokens = lambda i: (np.arange(DECODE_LANES) * 7919 + 131 * i + seed) % M.VOCAB
 
@@ -357,7 +371,7 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12):
     ctx.profile_reset()
     s_per_step = sum(times) / len(times)
     return {"s_per_step": round(s_per_step, 3), "key_switches_per_step": int(np.mean(ks)),
-            "bootstraps_per_step": step.stats["bootstraps"] // (warmup + steps_n + 1),
+            "bootstraps_per_step": n_boot() // (warmup + steps_n + 1), "driver": driver,
             "setup_s": {"keys": round(t_keys, 1), "first_steps_with_plaintext_encoding": round(t_warm, 1)},
             "device_memory_in_use_gb_after_warmup": round((total_b - free_b) / 1e9, 1),
             "client_s": {"decrypt_and_vocab_head": round(t_client, 3)},
@@ -489,6 +503,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="hmult", choices=["hmult", "ntt", "pcmm", "bootstrap", "decode"])
     ap.add_argument("--layers", type=int, default=12, help="decode workload: layers (12 = config 5)")
+    ap.add_argument("--decode-driver", default="native", choices=["native", "python"],
+                    help="decode workload: the C++ driver (default) or the same plan in Python")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ntt-line", action="store_true", help="skip the config-1 NTT figure in the hmult run")
@@ -521,11 +537,11 @@ def main():
             extra["bootstrap_config4"] = {k: b[k] for k in ("ms_per_bootstrap", "precision_bits", "levels_in_out",
                                                              "roofline")}
         if not args.no_decode_line:
-            d = bench_decode(ckks, torch, 1, 1, args.seed)
+            d = bench_decode(ckks, torch, 1, 1, args.seed, driver=args.decode_driver)
             line = {"s_per_step": d["s_per_step"], "metric": "s/step for 32-lane decode (config 5)",
                     "roofline": d["roofline"]}
             line.update({k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s",
-                                           "device_memory_in_use_gb_after_warmup")})
+                                           "device_memory_in_use_gb_after_warmup", "driver")})
             if not args.no_cpu_baseline:
                 line["cpu_baseline"], acc = cpu_baseline_decode(d, args.seed)
                 line.update(acc)
@@ -533,13 +549,13 @@ def main():
             del d
         cpu = None if args.no_cpu_baseline else cpu_baseline_hmult(args.seed)
     elif args.workload == "decode":
-        d = bench_decode(ckks, torch, args.steps, args.warmup, args.seed, args.layers)
+        d = bench_decode(ckks, torch, args.steps, args.warmup, args.seed, args.layers, args.decode_driver)
         res = {"metric": "s/step for 32-lane decode (config 5)", "value": d["s_per_step"], "unit": "s/step",
                "ms_per_step": round(d["s_per_step"] * 1e3, 1), "dtype": "u64",
                "config": {"workload": d["workload"], "lanes": DECODE_LANES, "layers": args.layers},
                "kernels": d["kernels"], "roofline": d["roofline"],
                "check": {k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s",
-                                           "device_memory_in_use_gb_after_warmup")}}
+                                           "device_memory_in_use_gb_after_warmup", "driver")}}
         extra = {}
         cpu = None
         if not args.no_cpu_baseline:

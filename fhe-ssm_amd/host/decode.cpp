@@ -1,0 +1,843 @@
+// decode.cpp -- the config-5 encrypted decode step, driven through the engine's C ABI (ckks_engine.h).
+//
+// The caller side of the hot path: the per-layer loop of the reference's served step
+// (hpc_gpu_port/gpu_real_model.cu:4674-5300) -- per layer RMSNorm, token shift, matvecBatch with shared babies
+// (:2902-3424), WKV scan, gate, output projection, residual, channel mix -- with the refresh policy of :2535-2599
+// re-decided for this engine (increments and the packed state are bootstrapped, the residual stream never is).
+// Host code only: every device operation is one ckks_* call; this file owns the level/scale bookkeeping, the
+// plaintext store and the model's slot layout.
+//
+// Model (RWKV-7-0.1B shape, every nonlinearity a degree-3 polynomial), per layer and lane:
+//   time mix      xn = x p_n1(mean(x^2));  u_m = g1 (1 - mu_m) xn + g1 mu_m xp_t  (m in r, k, v, w, a, g)
+//                 r, k, v = W u;  w, a, g = p(W u);  kh = k eta
+//                 S_h <- S_h diag(w_h) - (S_h kh_h)(kh_h a_h)^T + v_h k_h^T;  y_h = S_h r_h
+//                 x <- x + W_o (y g);  xp_t <- xn
+//   channel mix   xn2 = x p_n2(mean(x^2));  x <- x + W_cv p_h(W_ck (g2 (1 - mu_c) xn2 + g2 mu_c xp_c));  xp_c <- xn2
+//   output        g_o x p_o(mean(x^2))
+// Slots: lane-major, slot lane*1024 + channel (channels >= 768 zero); plaintexts that are the same for every
+// lane are 1024-periodic and stored compressed (N/32 words per limb).  WKV state in diagonal layout, one
+// ciphertext per t: D_t[lane*1024 + h*64 + i] = S_h[i][(i + t) mod 64].
+#include "fhe_ssm_decode.h"
+
+#include <cmath>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <tuple>
+#include <vector>
+
+namespace {
+
+constexpr uint32_t kN = 1u << 16;
+constexpr int D = 768, DPAD = 1024, HS = 64, FF = 3072, WKV_T = 64;
+constexpr uint32_t LOG_REP = 5;  // 1024-periodic plaintexts: N / 2^5 words per limb
+constexpr int MV_NB = 32;        // matvec baby steps 0..31; giant steps 32 g, g in [-24, 24)
+constexpr int MV_G0 = -24, MV_NG = 48;
+constexpr uint32_t kBootBatch = 16;  // ciphertexts per batched bootstrap (bounds its workspace)
+
+thread_local std::string g_err;
+
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+void ck(int rc, const char* what) {
+    if (rc != CKKS_OK) throw Error(rc, std::string(what) + ": " + ckks_last_error());
+}
+
+// ------------------------------------------------------------------ device buffers
+// Free lists of device buffers by size: a decode step allocates the same shapes in every layer.
+class Pool {
+   public:
+    ~Pool() {
+        for (auto& kv : free_)
+            for (auto* p : kv.second) ckks_buffer_free(p);
+    }
+    uint64_t* get(size_t bytes) {
+        auto& l = free_[bytes];
+        if (!l.empty()) {
+            uint64_t* p = l.back();
+            l.pop_back();
+            return p;
+        }
+        void* p = nullptr;
+        ck(ckks_buffer_alloc(bytes, &p), "ckks_buffer_alloc");
+        return (uint64_t*)p;
+    }
+    void put(uint64_t* p, size_t bytes) { free_[bytes].push_back(p); }
+
+   private:
+    std::map<size_t, std::vector<uint64_t*>> free_;
+};
+
+struct Buf {
+    uint64_t* d;
+    size_t bytes;
+    Pool* pool;  // null: not pooled (plaintexts, freed directly)
+    bool own;    // false: the caller's memory, never freed here
+    Buf(uint64_t* d_, size_t bytes_, Pool* pool_, bool own_ = true) : d(d_), bytes(bytes_), pool(pool_), own(own_) {}
+    Buf(const Buf&) = delete;
+    Buf& operator=(const Buf&) = delete;
+    ~Buf() {
+        if (!own) return;
+        if (pool)
+            pool->put(d, bytes);
+        else
+            ckks_buffer_free(d);
+    }
+};
+
+// a batch of B ciphertexts [B][2][level][N] in a pooled buffer, or a view into another batch's buffer
+struct Ct {
+    std::shared_ptr<Buf> buf;
+    size_t off = 0;  // words
+    uint32_t B = 0, level = 0;
+    double scale = 0.0;
+    uint64_t* ptr(uint32_t b = 0) const { return buf->d + off + (size_t)b * 2 * level * kN; }
+};
+
+using Pair = std::tuple<const Ct*, uint32_t, const Ct*, uint32_t>;  // (a, item of a, b, item of b)
+
+struct Matvec {
+    std::shared_ptr<Buf> buf;
+    uint32_t n_out = 0, n_in = 0;
+};
+
+// ------------------------------------------------------------------ the engine side (primitives + level rules)
+class Engine {
+   public:
+    Engine(ckks_context* ctx, fhe_ssm_refresh state, fhe_ssm_refresh inc_tm, fhe_ssm_refresh inc_cm,
+           const uint64_t* relin, const uint64_t* conj, const int64_t* steps, const uint64_t* const* evks,
+           uint32_t n_keys)
+        : ctx_(ctx), relin_(relin), conj_(conj) {
+        uint32_t n = 0, nq = 0, np = 0, dnum = 0;
+        ck(ckks_context_info(ctx, &n, &nq, &np, &dnum), "ckks_context_info");
+        if (n != kN) throw Error(CKKS_EINVAL, "the decoder needs N = 2^16");
+        moduli_.resize(nq + np);
+        ck(ckks_context_moduli(ctx, moduli_.data(), nq + np), "ckks_context_moduli");
+        if (!state.plan || !inc_tm.plan || !inc_cm.plan) throw Error(CKKS_EINVAL, "missing bootstrapping plan");
+        top_ = ckks_bootstrap_out_level(state.plan);
+        S_.assign(top_ + 1, 0.0);
+        for (uint32_t l = 1; l <= top_; l++) S_[l] = ckks_bootstrap_scale(state.plan, l);
+        for (uint32_t i = 0; i < n_keys; i++) keys_[steps[i]] = evks[i];
+        boots_["state"] = state;
+        boots_["inc_tm"] = inc_tm;
+        boots_["inc_cm"] = inc_cm;
+        for (auto& kv : boots_) {
+            if (ckks_bootstrap_out_level(kv.second.plan) != top_)
+                throw Error(CKKS_EINVAL, "every refresh plan must end at the state plan's level");
+            uint32_t ns = 0;
+            std::vector<int64_t> st(256);
+            ck(ckks_bootstrap_steps(kv.second.plan, st.data(), (uint32_t)st.size(), &ns), "ckks_bootstrap_steps");
+            st.resize(ns);
+            auto& bk = boot_keys_[kv.first];
+            for (auto s : st) {
+                if (!keys_.count(s)) throw Error(CKKS_EINVAL, "missing rotation key for step " + std::to_string(s));
+                bk.first.push_back(s);
+                bk.second.push_back(keys_[s]);
+            }
+        }
+    }
+
+    uint32_t top_level() const { return top_; }
+    double S(uint32_t l) const { return S_.at(l); }
+    const uint64_t* key(int64_t s) const {
+        if (s == 0) return nullptr;
+        auto it = keys_.find(s);
+        if (it == keys_.end()) throw Error(CKKS_EINVAL, "missing rotation key for step " + std::to_string(s));
+        return it->second;
+    }
+
+    Ct fresh(uint32_t B, uint32_t level, double scale) {
+        const size_t bytes = (size_t)B * 2 * level * kN * 8;
+        Ct c;
+        c.buf = std::make_shared<Buf>(pool_.get(bytes), bytes, &pool_);
+        c.B = B;
+        c.level = level;
+        c.scale = scale;
+        return c;
+    }
+    // a ciphertext batch in the caller's memory (read or written in place, never freed)
+    static Ct borrowed(const uint64_t* d, uint32_t B, uint32_t level, double scale) {
+        Ct c;
+        c.buf = std::make_shared<Buf>(const_cast<uint64_t*>(d), (size_t)B * 2 * level * kN * 8, nullptr, false);
+        c.B = B;
+        c.level = level;
+        c.scale = scale;
+        return c;
+    }
+    // dst <- a word for word (an integer combination with coefficient 1)
+    void copy_to(const Ct& a, const Ct& dst) { lincomb(a.B, {&a}, {1.0}, false, a.scale, 0.0, a.level, true, dst); }
+    Ct item(const Ct& a, uint32_t i) const { return slice(a, i, i + 1); }
+    Ct slice(const Ct& a, uint32_t i0, uint32_t i1) const {
+        Ct c = a;
+        c.off = a.off + (size_t)i0 * 2 * a.level * kN;
+        c.B = i1 - i0;
+        return c;
+    }
+    Ct zeros(uint32_t B, uint32_t level) {
+        Ct c = fresh(B, level, S(level));
+        std::vector<uint64_t> z((size_t)B * 2 * level * kN, 0);
+        ck(ckks_memcpy_h2d(c.ptr(), z.data(), z.size() * 8), "ckks_memcpy_h2d");
+        return c;
+    }
+
+    // -- level rules --------------------------------------------------------------------------------
+    bool canonical(const Ct& a) const { return std::fabs(a.scale / S(a.level) - 1.0) < 1e-9; }
+
+    Ct at(const Ct& a, uint32_t lt) {  // a at level lt with the canonical scale
+        if (a.level == lt && canonical(a)) return a;
+        if (a.level < lt + 1)
+            throw Error(CKKS_EINVAL, "cannot bring a level-" + std::to_string(a.level) + " ciphertext to level " +
+                                         std::to_string(lt));
+        return adjust(a, lt, 1.0, 0.0);
+    }
+    Ct at_neg(const Ct& a, uint32_t lt) { return adjust(a, lt, -1.0, 0.0); }
+    Ct at_scale(const Ct& a, uint32_t lt, double scale) {
+        Ct out = fresh(a.B, lt, scale);
+        lincomb(a.B, {&a}, {1.0}, true, scale, 0.0, lt, false, out);
+        return out;
+    }
+
+    Ct add(const Ct& a, const Ct& b, int sign = 1) {
+        const uint32_t m = std::min(a.level, b.level);
+        Ct a2 = (a.level == m && (canonical(a) || b.level == m)) ? a : at(a, m);
+        Ct b2 = (b.level == m && (canonical(b) || a.level == m)) ? b : at(b, m);
+        if (std::fabs(a2.scale / b2.scale - 1.0) > 1e-9) {
+            // same level, different scales: both go down one level onto the canonical scale
+            a2 = at(a2, m - 1);
+            b2 = at(b2, m - 1);
+        }
+        return lin_int({&a2, &b2}, {1.0, (double)sign});
+    }
+
+    // sum_t c_t x_t + const with scalar coefficients, landing one level below the lowest term (or at lt)
+    Ct lin(const std::vector<const Ct*>& terms, const std::vector<double>& coeffs, double cst, int lt = -1) {
+        uint32_t lo = terms[0]->level;
+        for (auto* t : terms) lo = std::min(lo, t->level);
+        const uint32_t target = lt < 0 ? lo - 1 : (uint32_t)lt;
+        Ct out = fresh(terms[0]->B, target, S(target));
+        lincomb(terms[0]->B, terms, coeffs, true, S(target), cst, target, false, out);
+        return out;
+    }
+
+    Ct lin_int(const std::vector<const Ct*>& terms, const std::vector<double>& coeffs) {
+        const Ct& t0 = *terms[0];
+        Ct out = fresh(t0.B, t0.level, t0.scale);
+        lincomb(t0.B, terms, coeffs, false, t0.scale, 0.0, t0.level, true, out);
+        return out;
+    }
+
+    Ct concat(const std::vector<Ct>& parts) {
+        const uint32_t lv = parts[0].level;
+        const double sc = parts[0].scale;
+        uint32_t B = 0;
+        for (auto& p : parts) B += p.B;
+        Ct out = fresh(B, lv, sc);
+        uint32_t o = 0;
+        for (auto& p : parts) {
+            if (p.level != lv || p.scale != sc) throw Error(CKKS_EINVAL, "concat of unlike ciphertexts");
+            Ct dst = slice(out, o, o + p.B);
+            lincomb(p.B, {&p}, {1.0}, false, sc, 0.0, lv, true, dst);
+            o += p.B;
+        }
+        return out;
+    }
+
+    Ct mul(const Ct& a, const Ct& b) {  // a (.) b, relinearized and rescaled; a batch of 1 broadcasts
+        const uint32_t B = std::max(a.B, b.B), m = std::min(a.level, b.level);
+        Ct a2 = a.level > m ? at(a, m) : a;
+        Ct b2 = b.level > m ? at(b, m) : b;
+        std::vector<std::vector<Pair>> pairs(B);
+        for (uint32_t i = 0; i < B; i++) pairs[i] = {Pair{&a2, i % a2.B, &b2, i % b2.B}};
+        return mult_sum_at(pairs, m);
+    }
+
+    // pairs[b] = products summed before one relinearization and rescale; operands go to their lowest level
+    Ct mult_sum(const std::vector<std::vector<Pair>>& pairs) {
+        uint32_t m = UINT32_MAX;
+        for (auto& item : pairs)
+            for (auto& p : item) m = std::min({m, std::get<0>(p)->level, std::get<2>(p)->level});
+        std::map<const Ct*, Ct> lowered;
+        auto lower = [&](const Ct* c) -> const Ct* {
+            auto it = lowered.find(c);
+            if (it == lowered.end())
+                it = lowered.emplace(c, (c->level == m && canonical(*c)) ? *c : at(*c, m)).first;
+            return &it->second;
+        };
+        std::vector<std::vector<Pair>> p2(pairs.size());
+        for (size_t b = 0; b < pairs.size(); b++)
+            for (auto& p : pairs[b])
+                p2[b].push_back(Pair{lower(std::get<0>(p)), std::get<1>(p), lower(std::get<2>(p)), std::get<3>(p)});
+        return mult_sum_at(p2, m);
+    }
+
+    Ct poly3(const Ct& z, const std::vector<double>& c) {  // c0 + c1 z + c2 z^2 + c3 z^3 in depth 2
+        const uint32_t m = z.level;
+        Ct z2 = mul(z, z);
+        Ct u = lin({&z}, {c[3]}, c[2], (int)m - 1);
+        Ct t = mul(z2, u);
+        Ct v = lin({&z}, {c[1]}, c[0], (int)m - 2);
+        return add(t, v);
+    }
+
+    // -- operators ------------------------------------------------------------------------------------
+    Ct rotate(const Ct& a, int64_t k) {
+        Ct out = fresh(a.B, a.level, a.scale);
+        ck(ckks_eval_rotate(ctx_, a.ptr(), a.B, a.level, k, key(k), out.ptr(), nullptr), "ckks_eval_rotate");
+        return out;
+    }
+
+    Ct mul_pt(const Ct& a, const Buf& pt) {  // a (.) compressed periodic plaintext (encoded at S(a.level)), rescaled
+        Ct tmp = fresh(a.B, a.level, a.scale);
+        ck(ckks_eval_mult_plain_ex(ctx_, a.ptr(), a.B, a.level, pt.d, 1, LOG_REP, tmp.ptr(), nullptr),
+           "ckks_eval_mult_plain_ex");
+        Ct out = fresh(a.B, a.level - 1, a.scale * S(a.level) / (double)moduli_[a.level - 1]);
+        ck(ckks_rescale(ctx_, tmp.ptr(), 2 * a.B, a.level, out.ptr(), nullptr), "ckks_rescale");
+        return out;
+    }
+
+    // the 64 cyclic block rotations rot64_t(a), t = 0..63, each masked by n_sets plaintext pairs
+    Ct rotate_masked(const Ct& a, const Buf& pts, uint32_t n_sets) {
+        if (a.B != 1) throw Error(CKKS_EINVAL, "rotate_masked takes one ciphertext");
+        std::vector<int64_t> lo(WKV_T), hi(WKV_T);
+        std::vector<const uint64_t*> klo(WKV_T), khi(WKV_T);
+        for (int t = 0; t < WKV_T; t++) {
+            lo[t] = t;
+            hi[t] = t ? t - HS : 0;
+            klo[t] = key(lo[t]);
+            khi[t] = key(hi[t]);
+        }
+        Ct out = fresh(n_sets * WKV_T, a.level - 1, a.scale * S(a.level) / (double)moduli_[a.level - 1]);
+        ck(ckks_eval_rotate_masked(ctx_, a.ptr(), a.level, WKV_T, lo.data(), klo.data(), hi.data(), khi.data(),
+                                   n_sets, pts.d, LOG_REP, out.ptr(), nullptr),
+           "ckks_eval_rotate_masked");
+        return out;
+    }
+
+    Ct matvec(const std::vector<Ct>& inputs, const Matvec& h) {
+        const uint32_t lv = inputs[0].level;
+        if (inputs.size() != h.n_in) throw Error(CKKS_EINVAL, "matvec input count");
+        std::vector<const uint64_t*> in;
+        for (auto& x : inputs) {
+            if (x.level != lv || x.B != 1) throw Error(CKKS_EINVAL, "matvec inputs must be single, same level");
+            in.push_back(x.ptr());
+        }
+        std::vector<int64_t> bs(MV_NB), gs(MV_NG);
+        std::vector<const uint64_t*> kb(MV_NB), kg(MV_NG);
+        for (int b = 0; b < MV_NB; b++) {
+            bs[b] = b;
+            kb[b] = key(b);
+        }
+        for (int g = 0; g < MV_NG; g++) {
+            gs[g] = (int64_t)MV_NB * (MV_G0 + g);
+            kg[g] = key(gs[g]);
+        }
+        Ct out = fresh(h.n_out, lv - 1, inputs[0].scale * S(lv) / (double)moduli_[lv - 1]);
+        ck(ckks_linear_transform_multi(ctx_, in.data(), h.n_in, lv, h.buf->d, LOG_REP, MV_NB, bs.data(), kb.data(),
+                                       MV_NG, gs.data(), kg.data(), h.n_out, 1, out.ptr(), nullptr),
+           "ckks_linear_transform_multi");
+        return out;
+    }
+
+    Ct mul_i(const Ct& a, int sign) {
+        Ct out = fresh(a.B, a.level, a.scale);
+        ck(ckks_eval_mul_i(ctx_, a.ptr(), 2 * a.B, a.level, sign, out.ptr(), nullptr), "ckks_eval_mul_i");
+        return out;
+    }
+
+    Ct conj(const Ct& a) {
+        Ct out = fresh(a.B, a.level, a.scale);
+        ck(ckks_eval_automorphism_ks(ctx_, a.ptr(), a.B, a.level, 2 * kN - 1, conj_, out.ptr(), nullptr),
+           "ckks_eval_automorphism_ks");
+        return out;
+    }
+
+    Ct bootstrap(const Ct& a, const std::string& kind) {
+        const fhe_ssm_refresh& r = boots_.at(kind);
+        const auto& bk = boot_keys_.at(kind);
+        Ct lo = at_scale(a, 1, r.in_scale);
+        Ct out = fresh(a.B, top_, S(top_));
+        for (uint32_t b0 = 0; b0 < a.B; b0 += kBootBatch) {
+            const uint32_t nb = std::min(kBootBatch, a.B - b0);
+            ck(ckks_eval_bootstrap_many(ctx_, r.plan, lo.ptr(b0), nb, relin_, conj_, bk.first.data(),
+                                        bk.second.data(), (uint32_t)bk.first.size(), out.ptr(b0), nullptr),
+               "ckks_eval_bootstrap_many");
+        }
+        return out;
+    }
+
+    // -- plaintexts -----------------------------------------------------------------------------------
+    std::shared_ptr<Buf> encode_periodic(const std::vector<double>& vecs, uint32_t level) {
+        const uint32_t n = (uint32_t)(vecs.size() / DPAD);
+        const size_t per = (size_t)level * (kN >> LOG_REP) * 8;
+        void* p = nullptr;
+        ck(ckks_buffer_alloc(n * per, &p), "ckks_buffer_alloc");
+        auto buf = std::make_shared<Buf>((uint64_t*)p, n * per, nullptr);
+        // in chunks (bounds the encoder's host staging)
+        for (uint32_t s = 0; s < n; s += 4096) {
+            const uint32_t m = std::min<uint32_t>(4096, n - s);
+            ck(ckks_encode_periodic(ctx_, vecs.data() + (size_t)s * DPAD, nullptr, m, DPAD, level, S(level),
+                                    (uint64_t*)((uint8_t*)p + s * per)),
+               "ckks_encode_periodic");
+        }
+        return buf;
+    }
+
+   private:
+    void lincomb(uint32_t B, const std::vector<const Ct*>& terms, const std::vector<double>& coeffs, bool scaled,
+                 double scale_out, double cst, uint32_t lt, bool integer, const Ct& out) {
+        std::vector<const uint64_t*> ptrs;
+        std::vector<uint32_t> levels;
+        std::vector<double> scales;
+        for (auto* t : terms) {
+            ptrs.push_back(t->ptr());
+            levels.push_back(t->level);
+            scales.push_back(scaled ? t->scale : 1.0);
+        }
+        ck(ckks_eval_lincomb(ctx_, B, (uint32_t)terms.size(), ptrs.data(), levels.data(), coeffs.data(),
+                             scales.data(), scale_out, cst, lt, integer ? 1 : 0, out.ptr(), nullptr),
+           "ckks_eval_lincomb");
+    }
+
+    Ct adjust(const Ct& a, uint32_t lt, double coeff, double cst) {
+        Ct out = fresh(a.B, lt, S(lt));
+        lincomb(a.B, {&a}, {coeff}, true, S(lt), cst, lt, false, out);
+        return out;
+    }
+
+    Ct mult_sum_at(const std::vector<std::vector<Pair>>& pairs, uint32_t level) {
+        const uint32_t B = (uint32_t)pairs.size(), np = (uint32_t)pairs[0].size();
+        const Ct& a0 = *std::get<0>(pairs[0][0]);
+        const Ct& b0 = *std::get<2>(pairs[0][0]);
+        Ct out = fresh(B, level - 1, a0.scale * b0.scale / (double)moduli_[level - 1]);
+        std::vector<const uint64_t*> flat;
+        for (auto& item : pairs) {
+            if (item.size() != np) throw Error(CKKS_EINVAL, "every item needs the same number of products");
+            for (auto& p : item) {
+                flat.push_back(std::get<0>(p)->ptr(std::get<1>(p)));
+                flat.push_back(std::get<2>(p)->ptr(std::get<3>(p)));
+            }
+        }
+        ck(ckks_eval_mult_sum(ctx_, flat.data(), np, B, level, relin_, 1, out.ptr(), nullptr), "ckks_eval_mult_sum");
+        return out;
+    }
+
+    ckks_context* ctx_;
+    const uint64_t *relin_, *conj_;
+    std::vector<uint64_t> moduli_;
+    uint32_t top_ = 0;
+    std::vector<double> S_;
+    std::map<int64_t, const uint64_t*> keys_;
+    std::map<std::string, fhe_ssm_refresh> boots_;
+    std::map<std::string, std::pair<std::vector<int64_t>, std::vector<const uint64_t*>>> boot_keys_;
+    Pool pool_;
+};
+
+// ------------------------------------------------------------------ slot-layout tables
+// A 768 x 768 block of a matvec: element (row, col), or absent (zero).
+using Block = std::function<double(int, int)>;
+
+// [n_out][48 giants][n_in * 32][1024]: the 1024-periodic diagonal r = G + b of every block (giant G = 32 g,
+// baby b), pre-rotated by -G (gpu_real_model.cu:2767-2823, harness/cpu_real_model.cpp:270-318):
+// d[row] = M[row][row + r] for 0 <= row + r < 768, then d'[p] = d[(p - G) mod 1024].
+std::vector<double> matvec_diagonals(const std::vector<std::vector<Block>>& blocks) {
+    const size_t n_out = blocks.size(), n_in = blocks[0].size();
+    std::vector<double> out(n_out * MV_NG * n_in * MV_NB * DPAD, 0.0);
+    std::vector<double> d(DPAD);
+    for (size_t o = 0; o < n_out; o++)
+        for (size_t i = 0; i < n_in; i++) {
+            const Block& M = blocks[o][i];
+            if (!M) continue;
+            for (int gi = 0; gi < MV_NG; gi++) {
+                const int G = MV_NB * (MV_G0 + gi);
+                for (int b = 0; b < MV_NB; b++) {
+                    const int r = G + b;
+                    std::fill(d.begin(), d.end(), 0.0);
+                    for (int row = 0; row < D; row++) {
+                        const int col = row + r;
+                        if (col >= 0 && col < D) d[row] = M(row, col);
+                    }
+                    double* dst = out.data() + (((o * MV_NG + gi) * n_in + i) * MV_NB + b) * DPAD;
+                    for (int p = 0; p < DPAD; p++) dst[p] = d[(((p - G) % DPAD) + DPAD) % DPAD];
+                }
+            }
+        }
+    return out;
+}
+
+// [64][2][1024]: the lo / hi masks of rot64_t (rot64_t(x) = m_lo (.) Rot_t(x) + m_hi (.) Rot_{t-64}(x)), optionally
+// times rot64_t(extra) (a per-channel vector folded into the same plaintext)
+std::vector<double> wkv_masks(const double* extra) {
+    std::vector<double> out((size_t)WKV_T * 2 * DPAD, 0.0);
+    for (int t = 0; t < WKV_T; t++)
+        for (int p = 0; p < DPAD; p++) {
+            const int i = p % HS;
+            const bool valid = p < D;
+            const double lo = (valid && i + t < HS) ? 1.0 : 0.0;
+            const double hi = (t && valid && i + t >= HS) ? 1.0 : 0.0;
+            double f = 1.0;
+            if (extra) {
+                const int src = (p / HS) * HS + (i + t) % HS;
+                const int s = std::min(src, DPAD - 1);
+                f = valid ? (s < D ? extra[s] : 0.0) : 0.0;
+            }
+            out[((size_t)t * 2 + 0) * DPAD + p] = extra ? lo * f : lo;
+            out[((size_t)t * 2 + 1) * DPAD + p] = extra ? hi * f : hi;
+        }
+    return out;
+}
+
+std::vector<int64_t> layer_rotation_steps() {
+    std::vector<int64_t> s;
+    for (int b = 0; b < MV_NB; b++) s.push_back(b);
+    for (int g = 0; g < MV_NG; g++) s.push_back((int64_t)MV_NB * (MV_G0 + g));
+    for (int t = 1; t < WKV_T; t++) {
+        s.push_back(t);       // rot64_t: Rot_t on the lanes' low part
+        s.push_back(t - HS);  // and Rot_{t-64} on the wrapped part
+    }
+    for (int k = 0; k < 10; k++) {
+        s.push_back(1 << k);
+        s.push_back(-(1 << k));
+    }
+    std::map<int64_t, bool> u;
+    for (auto x : s)
+        if (x) u[x] = true;
+    std::vector<int64_t> out;
+    for (auto& kv : u) out.push_back(kv.first);
+    return out;
+}
+
+// ------------------------------------------------------------------ weights
+struct LayerW {
+    std::map<std::string, std::vector<double>> v;
+    const std::vector<double>& operator[](const std::string& k) const {
+        auto it = v.find(k);
+        if (it == v.end()) throw Error(CKKS_EINVAL, "weight " + k + " not set");
+        return it->second;
+    }
+};
+
+size_t weight_count(const std::string& n) {
+    static const std::map<std::string, size_t> sizes = {
+        {"g1", D},     {"g2", D},     {"eta", D},    {"mu_r", D},       {"mu_k", D},       {"mu_v", D},
+        {"mu_w", D},   {"mu_a", D},   {"mu_g", D},   {"mu_c", D},       {"W_r", D * D},    {"W_k", D * D},
+        {"W_v", D * D}, {"W_w", D * D}, {"W_a", D * D}, {"W_g", D * D}, {"W_o", D * D},    {"W_ck", FF * D},
+        {"W_cv", D * FF}, {"p_n1", 4}, {"p_n2", 4},   {"p_w", 4},        {"p_a", 4},        {"p_g", 4},
+        {"p_h", 4}};
+    auto it = sizes.find(n);
+    return it == sizes.end() ? 0 : it->second;
+}
+
+// ------------------------------------------------------------------ the step
+struct LayerState {
+    Ct D, xp_t, xp_c, Dn;
+};
+
+class Decoder {
+   public:
+    Decoder(Engine* be, uint32_t n_layers) : be_(be), layers_(n_layers) {}
+
+    void set_weight(const std::string& name, int32_t layer, const double* data, size_t count) {
+        size_t want = 0;
+        if (layer < 0)
+            want = name == "g_o" ? D : name == "p_o" ? 4 : 0;
+        else
+            want = weight_count(name);
+        if (want == 0) throw Error(CKKS_EINVAL, "unknown weight " + name);
+        if (count != want) throw Error(CKKS_EINVAL, "weight " + name + ": " + std::to_string(want) + " values");
+        if (layer >= (int32_t)layers_.size()) throw Error(CKKS_EINVAL, "layer out of range");
+        auto& dst = layer < 0 ? model_.v[name] : layers_[layer].v[name];
+        dst.assign(data, data + count);
+    }
+
+    Ct step(const Ct& x_in) {
+        if (state_.empty()) cold_state();
+        Ct x = x_in;
+        for (uint32_t li = 0; li < layers_.size(); li++) {
+            LayerState& st = state_[li];
+            x = be_->add(x, boot(time_mix(li, x, st), "inc_tm"));
+            refresh_state(st);
+            x = be_->add(x, boot(channel_mix(li, x, st), "inc_cm"));
+        }
+        Ct xo = norm(x, model_["p_o"]);
+        std::vector<double> go(DPAD, 0.0);
+        std::copy(model_["g_o"].begin(), model_["g_o"].end(), go.begin());
+        return be_->mul_pt(xo, *vec_pt("g_o", xo.level, [&] { return go; }));
+    }
+
+    uint64_t bootstraps() const { return n_boot_; }
+
+   private:
+    // plaintexts, encoded on first use at the level they are applied
+    std::shared_ptr<Buf> vec_pt(const std::string& name, uint32_t level,
+                                const std::function<std::vector<double>()>& vecs) {
+        auto key = std::make_pair(name, level);
+        auto it = pt_.find(key);
+        if (it == pt_.end()) it = pt_.emplace(key, be_->encode_periodic(vecs(), level)).first;
+        return it->second;
+    }
+
+    const Matvec& mv_pt(const std::string& name, uint32_t level,
+                        const std::function<std::vector<std::vector<Block>>()>& blocks_fn) {
+        auto key = std::make_pair(name, level);
+        auto it = mv_.find(key);
+        if (it == mv_.end()) {
+            const auto blocks = blocks_fn();
+            Matvec m;
+            m.n_out = (uint32_t)blocks.size();
+            m.n_in = (uint32_t)blocks[0].size();
+            m.buf = be_->encode_periodic(matvec_diagonals(blocks), level);
+            it = mv_.emplace(key, std::move(m)).first;
+        }
+        return it->second;
+    }
+
+    Ct boot(const Ct& x, const char* kind) {
+        n_boot_ += x.B;
+        return be_->bootstrap(x, kind);
+    }
+
+    // x * p(mean(x^2)) per lane: rotate-and-add to the lane start, mask (times 1/768), broadcast back
+    Ct norm(const Ct& x, const std::vector<double>& pcoef) {
+        Ct s = be_->mul(x, x);
+        for (int k = 0; k < 10; k++) s = be_->add(s, be_->rotate(s, 1 << k));
+        s = be_->mul_pt(s, *vec_pt("lane_start", s.level, [] {
+            std::vector<double> m(DPAD, 0.0);
+            m[0] = 1.0 / D;
+            return m;
+        }));
+        for (int k = 0; k < 10; k++) s = be_->add(s, be_->rotate(s, -(1 << k)));
+        Ct n = be_->poly3(s, pcoef);
+        return be_->mul(x, n);
+    }
+
+    Ct time_mix(uint32_t li, const Ct& x, LayerState& st) {
+        const LayerW& L = layers_[li];
+        Ct xn = norm(x, L["p_n1"]);
+        const uint32_t lv = std::min(xn.level, st.xp_t.level);
+        static const char* mix[6] = {"r", "k", "v", "w", "a", "g"};
+        const Matvec& tm = mv_pt("tm" + std::to_string(li), lv, [&] {
+            std::vector<std::vector<Block>> out;
+            for (auto* m : mix) {
+                const auto& W = L[std::string("W_") + m];
+                const auto& mu = L[std::string("mu_") + m];
+                const auto& g1 = L["g1"];
+                auto a = std::make_shared<std::vector<double>>(D), b = std::make_shared<std::vector<double>>(D);
+                for (int c = 0; c < D; c++) {
+                    (*a)[c] = g1[c] * (1.0 - mu[c]);
+                    (*b)[c] = g1[c] * mu[c];
+                }
+                const double* w = W.data();
+                out.push_back({[w, a](int r, int c) { return w[(size_t)r * D + c] * (*a)[c]; },
+                               [w, b](int r, int c) { return w[(size_t)r * D + c] * (*b)[c]; }});
+            }
+            return out;
+        });
+        Ct proj = be_->matvec({be_->at(xn, lv), be_->at(st.xp_t, lv)}, tm);
+        Ct r = be_->item(proj, 0), k = be_->item(proj, 1), v = be_->item(proj, 2);
+        Ct w = be_->poly3(be_->item(proj, 3), L["p_w"]);
+        Ct a = be_->poly3(be_->item(proj, 4), L["p_a"]);
+        Ct g = be_->poly3(be_->item(proj, 5), L["p_g"]);
+        const double* eta = L["eta"].data();
+        auto masks = [] { return wkv_masks(nullptr); };
+        auto masks_eta = [eta] { return wkv_masks(eta); };
+        Ct KK = be_->rotate_masked(k, *vec_pt("mask_k" + std::to_string(li), k.level, [&] {
+            auto m = masks(), e = masks_eta();
+            m.insert(m.end(), e.begin(), e.end());
+            return m;
+        }), 2);
+        Ct K_t = be_->slice(KK, 0, WKV_T), Kh_t = be_->slice(KK, WKV_T, 2 * WKV_T);
+        Ct R_t = be_->rotate_masked(r, *vec_pt("mask", r.level, masks), 1);
+        Ct W_t = be_->rotate_masked(w, *vec_pt("mask", w.level, masks), 1);
+        Ct ka = be_->mul(k, a);
+        Ct B_t = be_->rotate_masked(ka, *vec_pt("mask_eta" + std::to_string(li), ka.level, masks_eta), 1);
+        const Ct& Dc = st.D;
+        std::vector<std::vector<Pair>> p1(1);
+        for (uint32_t t = 0; t < WKV_T; t++) p1[0].push_back(Pair{&Dc, t, &Kh_t, t});
+        Ct sa = be_->mult_sum(p1);
+        Ct nsa = be_->at_neg(sa, std::min({B_t.level, W_t.level - 1, sa.level - 1}));
+        std::vector<std::vector<Pair>> p2(WKV_T);
+        for (uint32_t t = 0; t < WKV_T; t++)
+            p2[t] = {Pair{&Dc, t, &W_t, t}, Pair{&nsa, 0, &B_t, t}, Pair{&v, 0, &K_t, t}};
+        Ct Dn = be_->mult_sum(p2);
+        std::vector<std::vector<Pair>> p3(1);
+        for (uint32_t t = 0; t < WKV_T; t++) p3[0].push_back(Pair{&Dn, t, &R_t, t});
+        Ct y = be_->mult_sum(p3);
+        Ct yg = be_->mul(y, g);
+        const double* wo = L["W_o"].data();
+        Ct o = be_->matvec({yg}, mv_pt("wo" + std::to_string(li), yg.level, [wo] {
+            return std::vector<std::vector<Block>>{{[wo](int r, int c) { return wo[(size_t)r * D + c]; }}};
+        }));
+        st.xp_t = xn;
+        st.Dn = Dn;
+        return o;
+    }
+
+    Ct channel_mix(uint32_t li, const Ct& x, LayerState& st) {
+        const LayerW& L = layers_[li];
+        Ct xn2 = norm(x, L["p_n2"]);
+        const uint32_t lv = std::min(xn2.level, st.xp_c.level);
+        const Matvec& ck_mv = mv_pt("ck" + std::to_string(li), lv, [&] {
+            const auto& g2 = L["g2"];
+            const auto& mu = L["mu_c"];
+            auto a = std::make_shared<std::vector<double>>(D), b = std::make_shared<std::vector<double>>(D);
+            for (int c = 0; c < D; c++) {
+                (*a)[c] = g2[c] * (1.0 - mu[c]);
+                (*b)[c] = g2[c] * mu[c];
+            }
+            const double* w = L["W_ck"].data();
+            std::vector<std::vector<Block>> out;
+            for (int o = 0; o < 4; o++) {
+                const double* wo = w + (size_t)o * D * D;
+                out.push_back({[wo, a](int r, int c) { return wo[(size_t)r * D + c] * (*a)[c]; },
+                               [wo, b](int r, int c) { return wo[(size_t)r * D + c] * (*b)[c]; }});
+            }
+            return out;
+        });
+        Ct hs = be_->matvec({be_->at(xn2, lv), be_->at(st.xp_c, lv)}, ck_mv);
+        Ct h = be_->poly3(hs, L["p_h"]);
+        const double* wcv = L["W_cv"].data();
+        const Matvec& cv = mv_pt("cv" + std::to_string(li), h.level, [wcv] {
+            std::vector<Block> row;
+            for (int i = 0; i < 4; i++)
+                row.push_back([wcv, i](int r, int c) { return wcv[(size_t)r * FF + (size_t)i * D + c]; });
+            return std::vector<std::vector<Block>>{row};
+        });
+        std::vector<Ct> hin;
+        for (uint32_t i = 0; i < 4; i++) hin.push_back(be_->item(h, i));
+        Ct f = be_->matvec(hin, cv);
+        st.xp_c = xn2;
+        return f;
+    }
+
+    // bootstrap the new state once: pack D_t + i D_{t+32}, bootstrap 32, unpack with one conjugation
+    void refresh_state(LayerState& st) {
+        Ct Dn = st.Dn;
+        st.Dn = Ct{};
+        const uint32_t h = WKV_T / 2;
+        Ct lo = be_->slice(Dn, 0, h), hi = be_->slice(Dn, h, 2 * h);
+        Ct packed = be_->add(lo, be_->mul_i(hi, 1));
+        n_boot_ += packed.B;
+        Ct P = be_->bootstrap(packed, "state");
+        Ct C = be_->conj(P);
+        Ct re2 = be_->add(P, C);                     // 2 Re
+        Ct im2 = be_->mul_i(be_->add(C, P, -1), 1);  // i (conj - P) = 2 Im
+        Ct Dnew = be_->concat({re2, im2});
+        Dnew.scale *= 2.0;  // the sums hold 2 D_t: the same words declared at twice the scale
+        st.D = Dnew;
+    }
+
+    void cold_state() {
+        const uint32_t lt = be_->top_level();
+        state_.resize(layers_.size());
+        for (auto& st : state_) {
+            st.D = be_->zeros(WKV_T, lt);
+            st.xp_t = be_->zeros(1, lt);
+            st.xp_c = be_->zeros(1, lt);
+        }
+    }
+
+    Engine* be_;
+    std::vector<LayerW> layers_;
+    LayerW model_;
+    std::vector<LayerState> state_;
+    std::map<std::pair<std::string, uint32_t>, std::shared_ptr<Buf>> pt_;
+    std::map<std::pair<std::string, uint32_t>, Matvec> mv_;
+    uint64_t n_boot_ = 0;
+};
+
+template <class F>
+int guarded(F&& f) {
+    try {
+        f();
+        g_err.clear();
+        return CKKS_OK;
+    } catch (const Error& e) {
+        g_err = e.what();
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        g_err = "out of host memory";
+        return CKKS_ENOMEM;
+    } catch (const std::exception& e) {
+        g_err = e.what();
+        return CKKS_EINVAL;
+    }
+}
+
+}  // namespace
+
+struct fhe_ssm_decoder {
+    std::unique_ptr<Engine> be;
+    std::unique_ptr<Decoder> dec;
+};
+
+extern "C" {
+
+const char* fhe_ssm_last_error(void) { return g_err.c_str(); }
+
+int fhe_ssm_rotation_steps(int64_t* steps, uint32_t cap, uint32_t* n_steps) {
+    return guarded([&] {
+        const auto s = layer_rotation_steps();
+        if (!n_steps) throw Error(CKKS_EINVAL, "n_steps is null");
+        *n_steps = (uint32_t)s.size();
+        for (uint32_t i = 0; i < s.size() && i < cap && steps; i++) steps[i] = s[i];
+    });
+}
+
+int fhe_ssm_decoder_create(ckks_context* ctx, uint32_t n_layers, fhe_ssm_refresh state, fhe_ssm_refresh inc_tm,
+                           fhe_ssm_refresh inc_cm, const uint64_t* d_relin, const uint64_t* d_conj,
+                           const int64_t* steps, const uint64_t* const* d_evks, uint32_t n_keys,
+                           fhe_ssm_decoder** out) {
+    return guarded([&] {
+        if (!ctx || !out || !d_relin || !d_conj || (n_keys && (!steps || !d_evks)) || n_layers == 0)
+            throw Error(CKKS_EINVAL, "null argument or no layers");
+        auto d = std::make_unique<fhe_ssm_decoder>();
+        d->be = std::make_unique<Engine>(ctx, state, inc_tm, inc_cm, d_relin, d_conj, steps, d_evks, n_keys);
+        for (auto s : layer_rotation_steps()) d->be->key(s);  // every layer-loop key present
+        d->dec = std::make_unique<Decoder>(d->be.get(), n_layers);
+        *out = d.release();
+    });
+}
+
+void fhe_ssm_decoder_destroy(fhe_ssm_decoder* dec) {
+    if (!dec) return;
+    dec->dec.reset();  // ciphertexts and plaintexts go back before the pool is released
+    dec->be.reset();
+    delete dec;
+}
+
+int fhe_ssm_decoder_set_weight(fhe_ssm_decoder* dec, const char* name, int32_t layer, const double* data,
+                               size_t count) {
+    return guarded([&] {
+        if (!dec || !name || !data) throw Error(CKKS_EINVAL, "null argument");
+        dec->dec->set_weight(name, layer, data, count);
+    });
+}
+
+int fhe_ssm_decoder_step(fhe_ssm_decoder* dec, const uint64_t* d_x, uint32_t level, double scale, uint64_t* d_out,
+                         uint32_t* out_level, double* out_scale) {
+    return guarded([&] {
+        if (!dec || !d_x || !d_out || !out_level || !out_scale) throw Error(CKKS_EINVAL, "null argument");
+        Engine& be = *dec->be;
+        if (level != be.top_level()) throw Error(CKKS_EINVAL, "the input must be at the plan's output level");
+        // the step reads its input in place and never writes it
+        Ct y = dec->dec->step(Engine::borrowed(d_x, 1, level, scale));
+        be.copy_to(y, Engine::borrowed(d_out, 1, y.level, y.scale));
+        *out_level = y.level;
+        *out_scale = y.scale;
+    });
+}
+
+int fhe_ssm_decoder_stats(const fhe_ssm_decoder* dec, uint64_t* bootstraps) {
+    return guarded([&] {
+        if (!dec || !bootstraps) throw Error(CKKS_EINVAL, "null argument");
+        *bootstraps = dec->dec->bootstraps();
+    });
+}
+
+}  // extern "C"

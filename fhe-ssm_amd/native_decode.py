@@ -1,0 +1,126 @@
+"""ctypes front end of libfhe_ssm_decode.so (include/fhe_ssm_decode.h): the config-5 decode step's native driver.
+
+The driver is C++ over the engine's C ABI; this module only hands it the context, the refresh plans, the keys
+and the weights, and calls one step at a time.  There is no Python fallback: if the library is missing,
+loading raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfhe_ssm_decode.so")
+
+_vp = ctypes.c_void_p
+_u32 = ctypes.c_uint32
+_int = ctypes.c_int
+
+
+class Refresh(ctypes.Structure):
+    _fields_ = [("plan", _vp), ("in_scale", ctypes.c_double)]
+
+
+SIGNATURES = {
+    "fhe_ssm_last_error": (ctypes.c_char_p, []),
+    "fhe_ssm_decoder_create": (_int, [_vp, _u32, Refresh, Refresh, Refresh, _vp, _vp, _vp, _vp, _u32,
+                                      ctypes.POINTER(_vp)]),
+    "fhe_ssm_decoder_destroy": (None, [_vp]),
+    "fhe_ssm_rotation_steps": (_int, [_vp, _u32, ctypes.POINTER(_u32)]),
+    "fhe_ssm_decoder_set_weight": (_int, [_vp, ctypes.c_char_p, ctypes.c_int32, _vp, ctypes.c_size_t]),
+    "fhe_ssm_decoder_step": (_int, [_vp, _vp, _u32, ctypes.c_double, _vp, ctypes.POINTER(_u32),
+                                    ctypes.POINTER(ctypes.c_double)]),
+    "fhe_ssm_decoder_stats": (_int, [_vp, ctypes.POINTER(ctypes.c_uint64)]),
+}
+
+LAYER_WEIGHTS = ("g1", "g2", "eta", "mu_r", "mu_k", "mu_v", "mu_w", "mu_a", "mu_g", "mu_c", "W_r", "W_k", "W_v",
+                 "W_w", "W_a", "W_g", "W_o", "W_ck", "W_cv", "p_n1", "p_n2", "p_w", "p_a", "p_g", "p_h")
+MODEL_WEIGHTS = ("g_o", "p_o")
+
+_lib = None
+
+
+def load():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise RuntimeError(f"fhe_ssm error {rc}: {load().fhe_ssm_last_error().decode()}")
+
+
+def rotation_steps() -> list:
+    n = _u32()
+    check(load().fhe_ssm_rotation_steps(None, 0, ctypes.byref(n)))
+    buf = (ctypes.c_int64 * n.value)()
+    check(load().fhe_ssm_rotation_steps(buf, n.value, ctypes.byref(n)))
+    return list(buf)
+
+
+class NativeDecoder:
+    """The decode step in C++.  boots: refresh kind ("state", "inc_tm", "inc_cm") -> (ckks.Bootstrap, in_scale);
+    keys: rotation step -> device pointer of its automorphism key (every layer step and every plan step)."""
+
+    def __init__(self, ckks, ctx, n_layers: int, boots: dict, d_relin: int, d_conj: int, keys: dict):
+        self.ckks, self.ctx, self.n_layers = ckks, ctx, n_layers
+        steps = np.ascontiguousarray(np.asarray(sorted(keys), dtype=np.int64))
+        ptrs = (_vp * len(steps))(*[keys[int(s)] for s in steps])
+        ref = {k: Refresh(boots[k][0].h, float(boots[k][1])) for k in ("state", "inc_tm", "inc_cm")}
+        h = _vp()
+        check(load().fhe_ssm_decoder_create(ctx.h, n_layers, ref["state"], ref["inc_tm"], ref["inc_cm"], d_relin,
+                                            d_conj, steps.ctypes.data, ptrs, len(steps), ctypes.byref(h)))
+        self.h = h.value
+        self._keep = (boots, steps, ptrs)
+
+    def set_weights(self, W: dict) -> None:
+        """W in the layout of rwkv_model.make_weights (first n_layers layers)"""
+        for li in range(self.n_layers):
+            for name in LAYER_WEIGHTS:
+                self._set(name, li, W["layers"][li][name])
+        for name in MODEL_WEIGHTS:
+            self._set(name, -1, W[name])
+
+    def _set(self, name: str, layer: int, arr) -> None:
+        a = np.ascontiguousarray(np.asarray(arr, dtype=np.float64)).reshape(-1)
+        check(load().fhe_ssm_decoder_set_weight(self.h, name.encode(), layer, a.ctypes.data, a.size))
+
+    def step(self, d_x: int, level: int, scale: float):
+        """one decode step; returns (DeviceBuffer [2][level][N] holding the output, its level, its scale)"""
+        out = self.ckks.DeviceBuffer(2 * level * (1 << 16) * 8)
+        lv, sc = _u32(), ctypes.c_double()
+        check(load().fhe_ssm_decoder_step(self.h, d_x, level, scale, out.ptr, ctypes.byref(lv), ctypes.byref(sc)))
+        return out, lv.value, sc.value
+
+    @property
+    def bootstraps(self) -> int:
+        n = ctypes.c_uint64()
+        check(load().fhe_ssm_decoder_stats(self.h, ctypes.byref(n)))
+        return n.value
+
+    def close(self) -> None:
+        if self.h:
+            load().fhe_ssm_decoder_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def from_backend(be, n_layers: int) -> NativeDecoder:
+    """A native decoder over the same context, plans and keys as a decode_step.HEBackend."""
+    return NativeDecoder(be.ckks, be.ctx, n_layers, be.boots, be.relin, be.conj_key, be.keys)

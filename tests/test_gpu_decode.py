@@ -289,6 +289,29 @@ def test_decode_step_one_layer(engine, DS, M):
 
 
 @pytest.mark.timeout(900)
+def test_native_decoder_matches_python_plan(engine, DS, M):
+    """the C++ driver (libfhe_ssm_decode.so) issues the same engine calls as the Python plan: one layer, two tokens
+    with the state carried, output ciphertexts equal word for word, same level, scale and bootstrap count"""
+    ND = load_module("native_decode")
+    be, sk = engine
+    W = M.make_weights(5, n_layers=1)
+    py = DS.DecodeStep(be, W)
+    nat = ND.from_backend(be, 1)
+    nat.set_weights(W)
+    for s in range(2):
+        x = M.embed_tokens(np.arange(32) + 100 * s)
+        ct = be.encrypt(sk, M.pack_lanes(x), be.top_level, seed=bytes([7, s]) * 16)
+        want = py(ct)
+        out, lv, sc = nat.step(ct.ptr(), ct.level, ct.scale)
+        assert (lv, sc) == (want.level, want.scale), (lv, sc, want.level, want.scale)
+        got = out.download((2, lv, N))
+        assert np.array_equal(got, want.buf.download((2, lv, N))), s
+        print(f"token {s}: native == python plan at level {lv}")
+    assert nat.bootstraps == py.stats["bootstraps"] == 2 * 34
+    nat.close()
+
+
+@pytest.mark.timeout(900)
 def test_decode_step_full_config5(engine, DS, M):
     """the full config-5 step: 12 layers, two tokens (cold start, then the carried state); decrypted output
     and the client's vocabulary logits against the float64 model, relErrRms <= 1e-3"""
