@@ -507,12 +507,14 @@ __global__ __launch_bounds__(256) void k_automorph_list(const uint64_t* __restri
 // wave reads 64 consecutive words (512 B) per diagonal.
 constexpr int kMaxBaby = 64;
 constexpr int kMacCoef = 64;
-constexpr int kMacRows = 4;
+constexpr int kMacRows = 8;
 
 // log_rep > 0: the diagonals are compressed periodic plaintexts, [n_diag][l][N >> log_rep], whose
 // evaluation-form word k is comp[k >> log_rep] (the reference's store expansion, gpu_real_model.cu:145-155).
 // Babies j0 .. j0 + nb - 1 of a list of nb_total are taken (diagonal g * nb_total + j, zero from n_diag on);
 // acc != 0 adds the result to what out holds (the MAC over more babies than fit in LDS runs in baby chunks).
+// A wave row takes two giant steps at a time: four independent accumulation chains per thread, and every
+// baby word read from LDS feeds two products.
 __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(const uint64_t* __restrict__ baby,
                                                                   const uint64_t* __restrict__ diag,
                                                                   uint64_t* __restrict__ out, uint32_t nb,
@@ -531,32 +533,53 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(const uint64_t*
         sb[jp * kMacCoef + kk] = baby[(size_t)(j0 + j) * 2 * P + p * P + off];
     }
     __syncthreads();
-    const size_t Pd = (size_t)l * (kN >> log_rep);
-    for (uint32_t g = row; g < ng; g += kMacRows) {
-        U128 s0{0, 0}, s1{0, 0};
-        const uint64_t* dg = diag + ((size_t)g * nb_total + j0) * Pd + (size_t)i * (kN >> log_rep) + (k >> log_rep);
-        // diagonals past n_diag (a short last giant step) are zero
+    const size_t Pd = (size_t)l * (kN >> log_rep), dk = (size_t)i * (kN >> log_rep) + (k >> log_rep);
+    // diagonals past n_diag (a short last giant step) are zero: the baby count of giant g
+    auto count = [&](uint32_t g) {
         const int64_t rem = (int64_t)n_diag - (int64_t)g * nb_total - j0;
-        const uint32_t jn = rem <= 0 ? 0u : (uint32_t)min<int64_t>(rem, nb);
-        Acc a0, a1;
-        for (uint32_t j = 0; j < jn; j++) {
-            const uint64_t m = dg[(size_t)j * Pd];
-            a0.add(sb[(2 * j) * kMacCoef + kk], m);
-            a1.add(sb[(2 * j + 1) * kMacCoef + kk], m);
-            if ((j & 7) == 7) {
-                a0.fold();
-                a1.fold();
-            }
-        }
-        s0 = a0.get();
-        s1 = a1.get();
-        uint64_t r0 = reduce_u128(s0, br), r1 = reduce_u128(s1, br);
+        return rem <= 0 ? 0u : (uint32_t)min<int64_t>(rem, nb);
+    };
+    auto store = [&](uint32_t g, Acc& a0, Acc& a1) {
+        uint64_t r0 = reduce_u128(a0.get(), br), r1 = reduce_u128(a1.get(), br);
         if (acc) {
             r0 = add_mod(r0, out[(size_t)g * 2 * P + off], br.q);
             r1 = add_mod(r1, out[(size_t)g * 2 * P + P + off], br.q);
         }
         out[(size_t)g * 2 * P + off] = r0;
         out[(size_t)g * 2 * P + P + off] = r1;
+    };
+    for (uint32_t g = row; g < ng; g += 2 * kMacRows) {
+        const uint32_t g2 = g + kMacRows;
+        const uint32_t jn1 = count(g), jn2 = g2 < ng ? count(g2) : 0u;  // jn2 <= jn1
+        const uint64_t* d1 = diag + ((size_t)g * nb_total + j0) * Pd + dk;
+        const uint64_t* d2 = diag + ((size_t)g2 * nb_total + j0) * Pd + dk;
+        Acc a0, a1, b0, b1;
+        uint32_t j = 0;
+        for (; j < jn2; j++) {
+            const uint64_t x0 = sb[(2 * j) * kMacCoef + kk], x1 = sb[(2 * j + 1) * kMacCoef + kk];
+            const uint64_t m1 = d1[(size_t)j * Pd], m2 = d2[(size_t)j * Pd];
+            a0.add(x0, m1);
+            a1.add(x1, m1);
+            b0.add(x0, m2);
+            b1.add(x1, m2);
+            if ((j & 7) == 7) {
+                a0.fold();
+                a1.fold();
+                b0.fold();
+                b1.fold();
+            }
+        }
+        for (; j < jn1; j++) {
+            const uint64_t m1 = d1[(size_t)j * Pd];
+            a0.add(sb[(2 * j) * kMacCoef + kk], m1);
+            a1.add(sb[(2 * j + 1) * kMacCoef + kk], m1);
+            if ((j & 7) == 7) {
+                a0.fold();
+                a1.fold();
+            }
+        }
+        store(g, a0, a1);
+        if (g2 < ng) store(g2, b0, b1);
     }
 }
 
