@@ -413,8 +413,9 @@ public:
         T[6] = t2(3);
         T[7] = tsum(4, 3);
         T[8] = t2(4);
-        T[16] = t2(8);
-        T[32] = t2(16);
+        int deg = (int)c.size() - 1;
+        while (deg > 0 && c[deg] == 0.0) deg--;
+        for (int n = 16; n <= deg; n *= 2) T[n] = t2(n / 2);  // the giant steps the division below uses
         std::function<HCt(const std::vector<double>&)> rec = [&](const std::vector<double>& a) -> HCt {
             int degp = (int)a.size() - 1;
             while (degp > 0 && a[degp] == 0.0) degp--;

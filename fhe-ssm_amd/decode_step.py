@@ -510,18 +510,22 @@ def config5_moduli(ckks, log_scale: int = 40, n_scaling: int = 28):
     return q0 + scaling[::-1] + big[:3] + big[3:]
 
 
-def build_engine(ckks, secret_seed=b"S" * 32, n_keys_seed=7, steps=None):
+def build_engine(ckks, secret_seed=b"S" * 32, n_keys_seed=7, steps=None, cheb_degree=47, double_angles=2):
     """Context, bootstrapping plan, secret and every key the decode step uses; returns (backend, secret)."""
     ctx = ckks.Context(num_q=32, num_p=7, dnum=4, scale=2.0**40, moduli=config5_moduli(ckks))
     ctx.set_moddown_exact(True)  # unbiased key-switch rounding: the 2^40 chain bootstraps to ~13 bits with it
-    # sparse-secret encapsulation (h' = 32): |I| <= ~8 sigma = 8 sqrt(33/12) ~ 13, so K = 14 and two double
-    # angles suffice (EvalMod's noise grows as K^2).  One plan per refresh kind, differing only in the input
-    # scale: the state and the channel-mix increment (|f| <= ~0.6) enter at q0 (m/q0 stays ~1e-3 per
-    # coefficient), the time-mix increment (|o| <= ~0.05) at 8 q0: more signal over EvalMod's noise.
+    # sparse-secret encapsulation (h' = 32): |I| <= ~8 sigma = 8 sqrt(33/12) ~ 13, so K = 14 (EvalMod's noise
+    # grows as K^2).  Degree 47 with two double angles approximates sin(2 pi K t) to ~2e-11 -- far below the
+    # noise -- in the depth of degree 59, with 14 instead of 16 products per ciphertext (degree 31 with three
+    # double angles would save more products but costs one more level).  One plan per refresh kind, differing
+    # only in the input scale: the state and the channel-mix increment (|f| <= ~0.6)
+    # enter at q0 (m/q0 stays ~1e-3 per coefficient), the time-mix increment (|o| <= ~0.05) at 8 q0: more signal
+    # over EvalMod's noise.
     plans = {}
     for kind, ins in (("state", 2.0**50), ("inc_cm", 2.0**50), ("inc_tm", 2.0**53)):
         if ins not in [v[1] for v in plans.values()]:
-            b = ckks.Bootstrap(ctx, K=14.0, cheb_degree=59, double_angles=2, top_scale=2.0**52, in_scale=ins)
+            b = ckks.Bootstrap(ctx, K=14.0, cheb_degree=cheb_degree, double_angles=double_angles,
+                               top_scale=2.0**52, in_scale=ins)
         else:
             b = next(v[0] for v in plans.values() if v[1] == ins)
         plans[kind] = (b, ins)
