@@ -500,10 +500,7 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint3
         if (P.sse_to) {
             // sparse-secret encapsulation: switch the q0 ciphertexts to the sparse secret, so that the raised
             // message m + q0 I has a small I (K bounds it), then switch back at the top level below
-            HCt c1 = ev1.get(1);
-            HIPB(hipMemcpy2DAsync(c1.d, W * 8, ct_in + W, 2 * W * 8, W * 8, B, hipMemcpyDeviceToDevice, st));
-            keyswitch(ctx, c1.d, B, 1, P.sse_to, ct_in, stage.d, st, 2);
-            ev1.put(c1);
+            keyswitch(ctx, ct_in + W, B, 1, P.sse_to, ct_in, stage.d, st, 2, 2 * W);  // c1 read in place
         } else {
             HIPB(hipMemcpyAsync(stage.d, ct_in, (size_t)B * 2 * W * 8, hipMemcpyDeviceToDevice, st));
         }
@@ -520,11 +517,8 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint3
         HIPB(launch_ntt(ctx, raised.d, jl, 2 * B * L, false, ctx.ntt_mode, st));
         ev1.put(stage);
         if (P.sse_from) {
-            HCt c1 = ev1.get(L), back = ev1.get(L);
-            HIPB(hipMemcpy2DAsync(c1.d, (size_t)L * W * 8, raised.d + (size_t)L * W, (size_t)2 * L * W * 8,
-                                  (size_t)L * W * 8, B, hipMemcpyDeviceToDevice, st));
-            keyswitch(ctx, c1.d, B, L, P.sse_from, raised.d, back.d, st, 2);
-            ev1.put(c1);
+            HCt back = ev1.get(L);
+            keyswitch(ctx, raised.d + (size_t)L * W, B, L, P.sse_from, raised.d, back.d, st, 2, (uint64_t)2 * L * W);
             ev1.put(raised);
             raised = back;
         }

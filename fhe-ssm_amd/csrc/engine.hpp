@@ -31,11 +31,15 @@ struct Job {
 };
 
 // Either an explicit device job list, or a dense [n_polys][period][N] buffer whose limb l uses
-// prime pmap[l] (enumerated prime-major).
+// prime pmap[l] (enumerated prime-major).  Inverse transforms of a dense buffer may read their input from
+// another buffer (src: limb l of poly p at src + (p * src_period + l) * N) and write the dense buffer: the
+// copy that an in-place transform of someone else's data would need is folded into the first pass.
 struct JobSpec {
     const Job* jobs;
     uint32_t n_polys, period;
     uint32_t n_primes;  // distinct primes among the jobs (host-side byte accounting only)
+    const uint64_t* src;  // out-of-place input (dense specs, inverse only), or null
+    uint32_t src_period;  // limbs between polys of src
     uint8_t pmap[kMaxPmap];
 };
 

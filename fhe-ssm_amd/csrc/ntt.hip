@@ -45,6 +45,15 @@ __device__ __forceinline__ void job_of(const JobSpec& js, uint32_t u, uint32_t& 
     }
 }
 
+// where job u reads its input: the buffer itself, or the out-of-place source of a dense spec
+__device__ __forceinline__ const uint64_t* job_src(const JobSpec& js, uint32_t u, const uint64_t* data, uint32_t off) {
+    if (js.src && !js.jobs) {
+        const uint32_t l = u / js.n_polys, p = u - l * js.n_polys;
+        return js.src + ((size_t)p * js.src_period + l) * kN;
+    }
+    return data + (size_t)off * kN;
+}
+
 // Forward (Cooley-Tukey) butterfly, values kept in [0, 8q) (q < 2^60): X is brought to [0, 4q), the
 // twiddle product is in [0, 4q), so X + T and X - T + 4q stay in [0, 8q).
 __device__ __forceinline__ void ct_bfly(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q4, uint64_t nq) {
@@ -161,16 +170,18 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
 
 // ---------------------------------------------------------------- inverse pass B (256-word blocks)
 // GS stages with t = 2^u, u = 0..7: m = 2^(15-u), twiddle m + (j >> (u+1)), j = 256 b + r.
-__device__ __forceinline__ void inv_b_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
+// in: the limb read (a itself, or the out-of-place source)
+__device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, const TwPair* __restrict__ tw, uint64_t q,
                                            int tile, int g, uint64_t* lds) {
     const uint64_t q4 = q << 2, nq = 0 - q;
     const int bl = g >> 4, rl = g & 15;
     const int b = tile * 16 + bl;
     uint64_t* blk = a + 256 * b;
+    const uint64_t* src = in + 256 * b;
     uint64_t* L = lds + bl * 272;
     uint64_t x[16];
 #pragma unroll
-    for (int k = 0; k < 16; k++) L[rl + 17 * k] = blk[rl + 16 * k];
+    for (int k = 0; k < 16; k++) L[rl + 17 * k] = src[rl + 16 * k];
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = L[17 * rl + k];
@@ -277,7 +288,8 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_b(uint64_t* data, JobS
     __shared__ uint64_t lds[kLdsWords];
     uint32_t off, prime;
     job_of(js, blockIdx.y, off, prime);
-    inv_b_tile(data + (size_t)off * kN, tw_all + (size_t)prime * kN, primes[prime].q, blockIdx.x, threadIdx.x, lds);
+    inv_b_tile(data + (size_t)off * kN, job_src(js, blockIdx.y, data, off), tw_all + (size_t)prime * kN,
+               primes[prime].q, blockIdx.x, threadIdx.x, lds);
 }
 
 __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_a(uint64_t* data, JobSpec js, const TwPair* tw_all,
@@ -325,8 +337,9 @@ __global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_inv_fused(ui
     const PrimeInfo& P = primes[prime];
     const int grp = threadIdx.x >> 8, g = threadIdx.x & 255;
     uint64_t* L = lds + grp * kLdsWords;
+    const uint64_t* in = job_src(js, blockIdx.x, data, off);
     for (int t = grp; t < 16; t += kFusedGroups) {
-        inv_b_tile(a, tw, P.q, t, g, L);
+        inv_b_tile(a, in, tw, P.q, t, g, L);
         __syncthreads();
     }
     for (int t = grp; t < 16; t += kFusedGroups) {

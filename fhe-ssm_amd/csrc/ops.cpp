@@ -73,6 +73,8 @@ hipError_t launch_pair_mac(const Context& ctx, const uint64_t* R, const uint64_t
                            uint32_t n, uint32_t l, uint32_t log_rep, hipStream_t st);
 hipError_t launch_gather(const Context& ctx, const uint64_t* const* src, uint32_t n, uint64_t words, uint64_t* dst,
                          hipStream_t st);
+hipError_t launch_scatter_limbs(const Context& ctx, const uint64_t* src, uint64_t src_bstride, uint64_t* dst,
+                                uint64_t dst_bstride, const uint32_t* off, uint32_t l, uint32_t B, hipStream_t st);
 hipError_t launch_tensor_sum(const Context& ctx, const uint64_t* const* d_tab, uint32_t np, uint64_t* d01,
                              uint64_t* d2, uint32_t B, uint32_t l, uint64_t* d2e, uint64_t d2e_bstride,
                              const uint32_t* ext_off, hipStream_t st);
@@ -254,20 +256,26 @@ void modup_from_coef(Context& ctx, const uint64_t* x2c, uint64_t* ext, uint32_t 
     HIPX(launch_ntt(ctx, ext, js, n_jobs, false, ctx.ntt_mode, st));
 }
 
-// x: [B][l][N] evaluation form -> ext [B][D][E][N] evaluation form
-void modup(Context& ctx, const uint64_t* x, uint64_t* ext, uint32_t B, uint32_t l, hipStream_t st) {
+// x: [B] polys of l limbs, x_bstride words apart (0: l * N), evaluation form -> ext [B][D][E][N] evaluation
+// form.  x is only read: its digit-own limbs are copied into ext in one launch, and the inverse NTT reads x
+// and writes the coefficient-form copy it works on (so a ciphertext's c1 is extended in place, no extraction).
+void modup(Context& ctx, const uint64_t* x, uint64_t* ext, uint32_t B, uint32_t l, hipStream_t st,
+           uint64_t x_bstride) {
     check_level(ctx, l);
     const uint32_t D = num_digits(ctx, l), E = l + ctx.K, al = ctx.alpha;
+    if (x_bstride == 0) x_bstride = (uint64_t)l * W;
+    if (x_bstride % W) throw std::invalid_argument("ModUp input stride must be whole limbs");
     uint64_t* xc = (uint64_t*)ws_get(ctx, WS_X2C, (size_t)B * l * W * 8);
-    HIPX(hipMemcpyAsync(xc, x, (size_t)B * l * W * 8, hipMemcpyDeviceToDevice, st));
-    for (uint32_t d = 0; d < D; d++) {
-        const uint32_t lo = d * al, hi = std::min(lo + al, l);
-        HIPX(hipMemcpy2DAsync(ext + ((size_t)d * E + lo) * W, (size_t)D * E * W * 8, x + (size_t)lo * W,
-                              (size_t)l * W * 8, (size_t)(hi - lo) * W * 8, B, hipMemcpyDeviceToDevice, st));
+    std::vector<uint32_t> own(l), pm(l);
+    for (uint32_t t = 0; t < l; t++) {
+        own[t] = (t / al) * E + t;
+        pm[t] = t;
     }
-    std::vector<uint32_t> pm(l);
-    for (uint32_t i = 0; i < l; i++) pm[i] = i;
-    HIPX(launch_ntt(ctx, xc, regular_jobs(B, pm), B * l, true, ctx.ntt_mode, st));
+    HIPX(launch_scatter_limbs(ctx, x, x_bstride, ext, (uint64_t)D * E * W, own.data(), l, B, st));
+    JobSpec js = regular_jobs(B, pm);
+    js.src = x;
+    js.src_period = (uint32_t)(x_bstride / W);
+    HIPX(launch_ntt(ctx, xc, js, B * l, true, ctx.ntt_mode, st));
     modup_from_coef(ctx, xc, ext, B, l, st);
 }
 
@@ -342,9 +350,10 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
     uint64_t* addc = nullptr;
     if (add) {
         addc = (uint64_t*)ws_get(ctx, WS_LAST, (size_t)n_polys * W * 8);
-        HIPX(hipMemcpy2DAsync(addc, W * 8, add + (size_t)(l - 1) * W, (size_t)l * W * 8, W * 8, n_polys,
-                              hipMemcpyDeviceToDevice, st));
-        HIPX(launch_ntt(ctx, addc, regular_jobs(n_polys, {l - 1}), n_polys, true, ctx.ntt_mode, st));
+        JobSpec ja = regular_jobs(n_polys, {l - 1});
+        ja.src = add + (size_t)(l - 1) * W;
+        ja.src_period = l;
+        HIPX(launch_ntt(ctx, addc, ja, n_polys, true, ctx.ntt_mode, st));
     }
     std::vector<TwPair> pinv(l), qlinv(l);
     std::vector<uint64_t> col(l);
@@ -423,13 +432,14 @@ void ks_moddown_list(Context& ctx, const uint64_t* const* ext, const uint64_t* c
 
 // ------------------------------------------------------------------ key switch
 // x: [B][l][N] eval; evk [dnum][2][L+K][N]; out2: [B][2][l][N] (+= add [B][2][l][N] if given)
+// x_bstride: words between the B input polys (0: l * N)
 void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
-               uint64_t* out2, hipStream_t st, uint32_t add_div) {
+               uint64_t* out2, hipStream_t st, uint32_t add_div, uint64_t x_bstride) {
     check_level(ctx, l);
     const uint32_t D = num_digits(ctx, l), E = l + ctx.K;
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)B * D * E * W * 8);
     uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)B * 2 * E * W * 8);
-    modup(ctx, x, ext, B, l, st);
+    modup(ctx, x, ext, B, l, st, x_bstride);
     HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st));
     moddown_inplace(ctx, acc, 2 * B, l, add, out2, st, add_div);
 }
@@ -440,9 +450,11 @@ void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uin
     if (l < 2 || l > ctx.L) throw std::invalid_argument("rescale needs 2 <= l <= L");
     uint64_t* last = (uint64_t*)ws_get(ctx, WS_LAST, (size_t)n_polys * W * 8);
     uint64_t* tmp = (uint64_t*)ws_get(ctx, WS_RTMP, (size_t)n_polys * (l - 1) * W * 8);
-    HIPX(hipMemcpy2DAsync(last, W * 8, in + (size_t)(l - 1) * W, (size_t)l * W * 8, W * 8, n_polys,
-                          hipMemcpyDeviceToDevice, st));
-    HIPX(launch_ntt(ctx, last, regular_jobs(n_polys, {l - 1}), n_polys, true, ctx.ntt_mode, st));
+    // the dropped limb of every poly to coefficients, read in place
+    JobSpec jl = regular_jobs(n_polys, {l - 1});
+    jl.src = in + (size_t)(l - 1) * W;
+    jl.src_period = l;
+    HIPX(launch_ntt(ctx, last, jl, n_polys, true, ctx.ntt_mode, st));
     HIPX(launch_lift_centered(ctx, last, W, tmp, n_polys, l - 1, ctx.moduli[l - 1], st));
     std::vector<uint32_t> pm(l - 1);
     for (uint32_t i = 0; i + 1 < l; i++) pm[i] = i;
@@ -533,12 +545,9 @@ void rotate(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, uint32_t g
             hipStream_t st) {
     check_level(ctx, l);
     if ((g & 1) == 0 || g >= 2 * kN) throw std::invalid_argument("automorphism index must be odd and < 2N");
-    uint64_t* c1 = (uint64_t*)ws_get(ctx, WS_C1, (size_t)B * l * W * 8);
     uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)B * 2 * l * W * 8);
-    // c1 of every ciphertext, contiguous; c0 enters as the ModDown addend of output poly 0 only
-    HIPX(hipMemcpy2DAsync(c1, (size_t)l * W * 8, ct + (size_t)l * W, (size_t)2 * l * W * 8, (size_t)l * W * 8, B,
-                          hipMemcpyDeviceToDevice, st));
-    keyswitch(ctx, c1, B, l, evk, ct, ks, st, 2);
+    // c1 of every ciphertext read in place; c0 enters as the ModDown addend of output poly 0 only
+    keyswitch(ctx, ct + (size_t)l * W, B, l, evk, ct, ks, st, 2, (uint64_t)2 * l * W);
     HIPX(launch_automorph(ks, out, 2 * B, l, g, st));
 }
 
@@ -574,12 +583,9 @@ void automorph_ks_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l
         return;
     }
     const uint32_t D = num_digits(ctx, l), E = l + ctx.K;
-    uint64_t* c1 = (uint64_t*)ws_get(ctx, WS_C1, (size_t)n * l * W * 8);
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)n * D * E * W * 8);
     uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)n * 2 * l * W * 8);
-    HIPX(hipMemcpy2DAsync(c1, (size_t)l * W * 8, cts + (size_t)l * W, (size_t)2 * l * W * 8, (size_t)l * W * 8, n,
-                          hipMemcpyDeviceToDevice, st));
-    modup(ctx, c1, ext, n, l, st);
+    modup(ctx, cts + (size_t)l * W, ext, n, l, st, (uint64_t)2 * l * W);  // the c1 polys, read in place
     std::vector<const uint64_t*> ep(n);
     for (uint32_t c = 0; c < n; c++) {
         ep[c] = ext + (size_t)c * D * E * W;
@@ -631,11 +637,8 @@ void rotate_hoisted_multi(Context& ctx, const uint64_t* cts, uint32_t n_ct, uint
         return;
     }
     const uint32_t E = l + ctx.K, D = num_digits(ctx, l);
-    uint64_t* c1 = (uint64_t*)ws_get(ctx, WS_C1, (size_t)n_ct * l * W * 8);
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)n_ct * D * E * W * 8);
-    HIPX(hipMemcpy2DAsync(c1, (size_t)l * W * 8, cts + (size_t)l * W, ctw * 8, (size_t)l * W * 8, n_ct,
-                          hipMemcpyDeviceToDevice, st));
-    modup(ctx, c1, ext, n_ct, l, st);
+    modup(ctx, cts + (size_t)l * W, ext, n_ct, l, st, ctw);  // the c1 polys, read in place
     std::vector<uint32_t> g(n);
     for (uint32_t s = 0; s < n; s++) g[s] = rotation_index(steps[s]);
     const uint32_t per = 64 / n;  // ciphertexts per list (a list starts at a ciphertext boundary)

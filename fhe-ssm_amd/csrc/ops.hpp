@@ -35,7 +35,9 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
                             bool centered = false, const std::vector<uint64_t>& col_scale = {});
 uint32_t num_digits(const Context& ctx, uint32_t l);
 
-void modup(Context& ctx, const uint64_t* x, uint64_t* ext, uint32_t B, uint32_t l, hipStream_t st);
+// x_bstride: words between the B input polys (0: l * N; 2 l N reads the c1 of a ciphertext batch in place)
+void modup(Context& ctx, const uint64_t* x, uint64_t* ext, uint32_t B, uint32_t l, hipStream_t st,
+           uint64_t x_bstride = 0);
 void ks_inner(Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* acc, uint32_t B, uint32_t l,
               hipStream_t st);
 // add (optional): applied to output polys pc with pc % add_div == 0, at add + (pc / add_div) * add_div * l * N
@@ -46,7 +48,7 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
 void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
                      hipStream_t st, const uint64_t* ext = nullptr, const uint64_t* evk = nullptr);
 void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
-               uint64_t* out2, hipStream_t st, uint32_t add_div = 1);
+               uint64_t* out2, hipStream_t st, uint32_t add_div = 1, uint64_t x_bstride = 0);
 void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uint64_t* out, hipStream_t st);
 void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l, const uint64_t* evk,
            uint64_t* out, bool do_rescale, hipStream_t st);

@@ -476,6 +476,18 @@ __global__ __launch_bounds__(256) void k_mdr_combine_ks(const uint64_t* __restri
     }
 }
 
+// limb t of batch item c: dst + c * dst_bstride + off[t] * N  <-  src + c * src_bstride + t * N (a batch of
+// polynomials copied into the digit-own limbs of the ModUp extension buffer in one launch)
+struct LimbMap {
+    uint16_t off[kMaxPmap];
+};
+
+__global__ __launch_bounds__(256) void k_scatter_limbs(const uint64_t* __restrict__ src, uint64_t src_bstride,
+                                                       uint64_t* __restrict__ dst, uint64_t dst_bstride, LimbMap lm) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y, c = blockIdx.z;
+    dst[c * dst_bstride + (size_t)lm.off[t] * kN + k] = src[c * src_bstride + (size_t)t * kN + k];
+}
+
 // dst[c] = src[c] for up to 64 items of `words` words each (gathers scattered ciphertexts into one batch)
 __global__ __launch_bounds__(256) void k_gather(ListPtrs src, uint64_t* __restrict__ dst, uint64_t words) {
     const uint32_t c = blockIdx.y;
@@ -947,6 +959,18 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
     const int pi = prof_begin(ctx, "mdr_combine_ks", bytes, st);
     hipLaunchKernelGGL(k_mdr_combine_ks, dim3(B, kN / 256, l - 1), dim3(256), 0, st, ext, evk, add, T, out, ia, ma,
                        ctx.d_primes);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+hipError_t launch_scatter_limbs(const Context& ctx, const uint64_t* src, uint64_t src_bstride, uint64_t* dst,
+                                uint64_t dst_bstride, const uint32_t* off, uint32_t l, uint32_t B, hipStream_t st) {
+    if (l == 0 || l > kMaxPmap || B == 0) return hipErrorInvalidValue;
+    LimbMap lm{};
+    for (uint32_t t = 0; t < l; t++) lm.off[t] = (uint16_t)off[t];
+    const int pi = prof_begin(ctx, "scatter_limbs", (double)B * l * 2 * kN * 8, st);
+    hipLaunchKernelGGL(k_scatter_limbs, dim3(kN / 256, l, B), dim3(256), 0, st, src, src_bstride, dst, dst_bstride,
+                       lm);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
