@@ -67,7 +67,7 @@ def timed_steps(torch, stream, step, steps, warmup):
 # HBM bytes per launch of a workload's dominant kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the same
 # bench command (scaled by what the counters read for a copy kernel of known size: read = 2 x FETCH_SIZE KiB,
 # write = WRITE_SIZE KiB).  Measured, not computed: re-measure when the kernel or the workload changes.
-MEASURED_TRAFFIC = {("hmult", "ntt_fwd_2pass"): 7.456e9}
+MEASURED_TRAFFIC = {("hmult", "ntt_fwd_2pass"): 7.950e9}
 
 
 def roofline_from_profile(rep: dict, workload: str = ""):
