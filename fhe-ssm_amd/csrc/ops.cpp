@@ -58,8 +58,8 @@ hipError_t launch_ks_sub_list(const Context& ctx, const uint64_t* const* ext, co
                               uint64_t* out, uint32_t n, uint32_t l, const TwPair* pinv, hipStream_t st);
 hipError_t launch_automorph_list(const Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n, uint32_t l,
                                  const uint32_t* g, hipStream_t st);
-hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* baby, const uint64_t* diag, uint64_t* out, uint32_t nb,
-                           uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st);
+hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* const* baby, const uint64_t* diag, uint64_t* out,
+                           uint32_t nb, uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st);
 hipError_t launch_mul_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
                             uint32_t l, uint64_t pt_bstride, uint32_t log_rep, hipStream_t st);
 hipError_t launch_add_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
@@ -691,7 +691,9 @@ void bsgs_matvec(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* d
         for (uint32_t j = 1; j < bs; j++) steps[j - 1] = j;
         rotate_hoisted(ctx, ct, l, steps.data(), bs - 1, baby_evk, baby + ctw, st);
     }
-    HIPX(launch_bsgs_mac(ctx, baby, diags, v, bs, n_diag, ng, l, 0, st));
+    std::vector<const uint64_t*> bp(bs);
+    for (uint32_t j = 0; j < bs; j++) bp[j] = baby + (size_t)j * ctw;
+    HIPX(launch_bsgs_mac(ctx, bp.data(), diags, v, bs, n_diag, ng, l, 0, st));
     std::vector<const uint64_t*> terms(1, v);
     if (ng > 1) {
         std::vector<int64_t> steps(ng - 1);
@@ -722,35 +724,36 @@ void bsgs_multi_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, 
     if (do_rescale && l < 2) throw std::invalid_argument("rescale needs l >= 2");
     const size_t ctw = (size_t)2 * l * W;
     const uint32_t nbt = n_in * nb, n_x = n_inst * n_in;
-    uint64_t* baby = (uint64_t*)ws_get(ctx, WS_BABY, (size_t)n_inst * nbt * ctw * 8);
     uint64_t* v = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)n_inst * n_out * ng * ctw * 8);
-    // inputs side by side, then the babies [inst][i nb + b]
+    // the inputs side by side (the hoisted rotations take one strided batch)
     uint64_t* X = (uint64_t*)ws_get(ctx, WS_BINP, (size_t)n_x * ctw * 8);
     HIPX(launch_gather(ctx, in, n_x, ctw, X, st));
     std::vector<int64_t> rs;
     std::vector<const uint64_t*> rk;
-    std::vector<uint32_t> rpos;
-    for (uint32_t b = 0; b < nb; b++) {
+    std::vector<int32_t> ridx(nb, -1);  // baby b -> its rotation among rs, or -1 (identity: the input itself)
+    for (uint32_t b = 0; b < nb; b++)
         if (bsteps[b] != 0) {
+            ridx[b] = (int32_t)rs.size();
             rs.push_back(bsteps[b]);
             rk.push_back(bevk[b]);
-            rpos.push_back(b);
-        } else {  // identity baby: the input itself, for every (instance, input)
-            HIPX(hipMemcpy2DAsync(baby + (size_t)b * ctw, (size_t)nb * ctw * 8, X, ctw * 8, ctw * 8, n_x,
-                                  hipMemcpyDeviceToDevice, st));
         }
-    }
-    if (!rs.empty()) {
-        const uint32_t nr = (uint32_t)rs.size();
-        uint64_t* tmp = (uint64_t*)ws_get(ctx, WS_SUM, (size_t)n_x * nr * ctw * 8);
+    const uint32_t nr = (uint32_t)rs.size();
+    uint64_t* tmp = nullptr;
+    if (nr) {
+        tmp = (uint64_t*)ws_get(ctx, WS_SUM, (size_t)n_x * nr * ctw * 8);
         rotate_hoisted_multi(ctx, X, n_x, l, rs.data(), nr, rk.data(), tmp, st);
-        for (uint32_t r = 0; r < nr; r++)
-            HIPX(hipMemcpy2DAsync(baby + (size_t)rpos[r] * ctw, (size_t)nb * ctw * 8, tmp + (size_t)r * ctw,
-                                  (size_t)nr * ctw * 8, ctw * 8, n_x, hipMemcpyDeviceToDevice, st));
     }
-    for (uint32_t s = 0; s < n_inst; s++)
-        HIPX(launch_bsgs_mac(ctx, baby + (size_t)s * nbt * ctw, diags, v + (size_t)s * n_out * ng * ctw, nbt,
-                             nbt * n_out * ng, n_out * ng, l, log_rep, st));
+    // babies [i nb + b] of instance s, read where they are (no packing copies)
+    std::vector<const uint64_t*> bp(nbt);
+    for (uint32_t s = 0; s < n_inst; s++) {
+        for (uint32_t i = 0; i < n_in; i++)
+            for (uint32_t b = 0; b < nb; b++) {
+                const size_t x = (size_t)s * n_in + i;
+                bp[i * nb + b] = ridx[b] < 0 ? X + x * ctw : tmp + (x * nr + (uint32_t)ridx[b]) * ctw;
+            }
+        HIPX(launch_bsgs_mac(ctx, bp.data(), diags, v + (size_t)s * n_out * ng * ctw, nbt, nbt * n_out * ng,
+                             n_out * ng, l, log_rep, st));
+    }
     // giants with a non-zero step, all instances and outputs, packed contiguously and rotated as one list
     std::vector<int64_t> gs;
     std::vector<const uint64_t*> gk;

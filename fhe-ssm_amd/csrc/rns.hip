@@ -523,11 +523,12 @@ constexpr int kMacRows = 8;
 
 // log_rep > 0: the diagonals are compressed periodic plaintexts, [n_diag][l][N >> log_rep], whose
 // evaluation-form word k is comp[k >> log_rep] (the reference's store expansion, gpu_real_model.cu:145-155).
-// Babies j0 .. j0 + nb - 1 of a list of nb_total are taken (diagonal g * nb_total + j, zero from n_diag on);
+// Babies j0 .. j0 + nb - 1 of a list of nb_total are taken, each a ciphertext [2][l][N] anywhere in memory (baby.p,
+// so the rotated babies are read where the rotations wrote them; diagonal g * nb_total + j, zero from n_diag on);
 // acc != 0 adds the result to what out holds (the MAC over more babies than fit in LDS runs in baby chunks).
 // A wave row takes two giant steps at a time: four independent accumulation chains per thread, and every
 // baby word read from LDS feeds two products.
-__global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(const uint64_t* __restrict__ baby,
+__global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(ListPtrs baby,
                                                                   const uint64_t* __restrict__ diag,
                                                                   uint64_t* __restrict__ out, uint32_t nb,
                                                                   uint32_t nb_total, uint32_t j0, uint32_t ng,
@@ -540,9 +541,9 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(const uint64_t*
     const uint32_t i = blockIdx.y;
     const Barrett br = barrett_of(primes[i]);
     const size_t P = (size_t)l * kN, off = (size_t)i * kN + k;
-    for (uint32_t jp = row; jp < 2 * nb; jp += kMacRows) {  // jp = 2 j + poly
+    for (uint32_t jp = row; jp < 2 * nb; jp += kMacRows) {  // jp = 2 j + poly; baby j of this chunk at baby.p[j]
         const uint32_t j = jp >> 1, p = jp & 1;
-        sb[jp * kMacCoef + kk] = baby[(size_t)(j0 + j) * 2 * P + p * P + off];
+        sb[jp * kMacCoef + kk] = baby.p[j][p * P + off];
     }
     __syncthreads();
     const size_t Pd = (size_t)l * (kN >> log_rep), dk = (size_t)i * (kN >> log_rep) + (k >> log_rep);
@@ -892,16 +893,18 @@ hipError_t launch_automorph_list(const Context& ctx, const uint64_t* in, uint64_
     return hipGetLastError();
 }
 
-hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* baby, const uint64_t* diag, uint64_t* out, uint32_t nb,
-                           uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st) {
+hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* const* baby, const uint64_t* diag, uint64_t* out,
+                           uint32_t nb, uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st) {
     if (nb == 0 || log_rep > 6 || n_diag > nb * ng) return hipErrorInvalidValue;
     const double bytes = ((double)nb * 2 * l + (double)n_diag * l / (1u << log_rep) + (double)ng * 2 * l) * kN * 8;
     const int pi = prof_begin(ctx, log_rep ? "bsgs_mac_periodic" : "bsgs_mac", bytes, st);
     for (uint32_t j0 = 0; j0 < nb; j0 += kMaxBaby) {
         const uint32_t nbc = std::min<uint32_t>(kMaxBaby, nb - j0);
+        ListPtrs bp{};
+        for (uint32_t j = 0; j < nbc; j++) bp.p[j] = baby[j0 + j];
         hipLaunchKernelGGL(k_bsgs_mac, dim3(kN / kMacCoef, l), dim3(kMacCoef * kMacRows),
-                           (size_t)nbc * 2 * kMacCoef * 8, st, baby, diag, out, nbc, nb, j0, ng, n_diag, l,
-                           log_rep, j0 ? 1u : 0u, ctx.d_primes);
+                           (size_t)nbc * 2 * kMacCoef * 8, st, bp, diag, out, nbc, nb, j0, ng, n_diag, l, log_rep,
+                           j0 ? 1u : 0u, ctx.d_primes);
     }
     prof_end(ctx, pi, st);
     return hipGetLastError();
