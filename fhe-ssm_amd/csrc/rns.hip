@@ -354,10 +354,25 @@ struct ListPtrs {
     const uint64_t* p[kMaxList];
 };
 
+// XCD-aware order of a list kernel's one-dimensional grid: workgroups go to the 8 XCDs round-robin (wg mod 8), so
+// the m items of one (coefficient tile, limb) tile are given the ids xcd + 8 (blk m + item), all on one XCD: the
+// tile's shared ext and evk words are fetched into that XCD's L2 once for all items.  The grid has m * n_tiles
+// workgroups (n_tiles a multiple of 8).
+struct ListTile {
+    uint32_t item, kt, limb;
+};
+
+__device__ __forceinline__ ListTile list_tile(uint32_t m) {
+    const uint32_t n = blockIdx.x, q = n >> 3;
+    const uint32_t tile = (q / m) * 8 + (n & 7);
+    return ListTile{q % m, tile % (kN / 256), tile / (kN / 256)};
+}
+
 __global__ __launch_bounds__(256) void k_ks_inner_list(ListPtrs ext, ListPtrs evk, uint64_t* __restrict__ acc,
                                                        InnerArgs ia, const PrimeInfo* __restrict__ primes) {
-    const uint32_t c = blockIdx.x, k = blockIdx.y * 256 + threadIdx.x;
-    const uint32_t t = ia.t0 + blockIdx.z;
+    const ListTile lt = list_tile(ia.B);
+    const uint32_t c = lt.item, k = lt.kt * 256 + threadIdx.x;
+    const uint32_t t = ia.t0 + lt.limb;
     const uint32_t p = ia.prime_of[t];
     const Barrett br = barrett_of(primes[p]);
     const uint64_t* x = ext.p[c] + (size_t)t * kN + k;
@@ -388,7 +403,8 @@ __global__ __launch_bounds__(256) void k_ks_sub_list(ListPtrs ext, ListPtrs evk,
                                                      const uint64_t* __restrict__ add, uint64_t add_stride,
                                                      uint32_t add_group, uint64_t* __restrict__ out, uint32_t l,
                                                      InnerArgs ia, PinvArgs pa, const PrimeInfo* __restrict__ primes) {
-    const uint32_t c = blockIdx.x, k = blockIdx.y * 256 + threadIdx.x, i = blockIdx.z;
+    const ListTile lt = list_tile(ia.B);
+    const uint32_t c = lt.item, k = lt.kt * 256 + threadIdx.x, i = lt.limb;
     const Barrett br = barrett_of(primes[i]);
     const uint64_t q = br.q;
     const size_t li = (size_t)i * kN + k;
@@ -851,7 +867,7 @@ hipError_t launch_ks_inner_list(const Context& ctx, const uint64_t* const* ext, 
     }
     const double bytes = ((double)distinct_ext * ia.D * nt + (double)n * (2 * ia.D * nt + 2 * nt)) * kN * 8;
     const int pi = prof_begin(ctx, "ks_inner_list", bytes, st);
-    hipLaunchKernelGGL(k_ks_inner_list, dim3(n, kN / 256, nt), dim3(256), 0, st, pe, pk, acc, ia, ctx.d_primes);
+    hipLaunchKernelGGL(k_ks_inner_list, dim3(n * (kN / 256) * nt), dim3(256), 0, st, pe, pk, acc, ia, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
@@ -876,7 +892,7 @@ hipError_t launch_ks_sub_list(const Context& ctx, const uint64_t* const* ext, co
     const double bytes = ((double)distinct_ext * ia.D + (double)n * (2 * ia.D + 4) +
                           (add ? (double)(n + add_group - 1) / add_group : 0.0)) * l * kN * 8;
     const int pi = prof_begin(ctx, "ks_sub_list", bytes, st);
-    hipLaunchKernelGGL(k_ks_sub_list, dim3(n, kN / 256, l), dim3(256), 0, st, pe, pk, conv, add, add_stride,
+    hipLaunchKernelGGL(k_ks_sub_list, dim3(n * (kN / 256) * l), dim3(256), 0, st, pe, pk, conv, add, add_stride,
                        add_group, out, l, ia, pa, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
