@@ -18,8 +18,9 @@ mix, f from the channel mix) comes out at a low level, is bootstrapped on its ow
 x itself is never bootstrapped: the sine of EvalMod shrinks large coefficients slightly (a coherent
 relative error ~(2 pi m / q0)^2 / 6), and the increments are ~5-100x smaller than x.  Each increment kind
 has its own bootstrapping plan whose input scale suits its magnitude (more signal over EvalMod's noise).
-The carried WKV state is bootstrapped once per layer, packed two per ciphertext (D_t + i D_{t+32}) and
-unpacked with one conjugation.  34 bootstraps per layer.
+The carried WKV state is bootstrapped once per layer: its 64 diagonal ciphertexts are packed 4 -> 3 into the
+lanes' unused channels (768..1023), the 48 packed two per complex ciphertext, and unpacked with one conjugation
+and three masked rotations.  26 bootstraps per layer.
 """
 from __future__ import annotations
 
@@ -121,7 +122,7 @@ class DecodeStep:
         self.W = weights
         self.n_layers = len(weights["layers"]) if n_layers is None else n_layers
         self.pt = {}        # (name, level) -> backend plaintext handle
-        self.state = None   # per layer: {"D": ct batch of 64, "xp_t": ct, "xp_c": ct}
+        self.state = None   # per layer: {"D": [(ct batch, index) of D_t] * 64, "xp_t": ct, "xp_c": ct}
         self.stats = {"bootstraps": 0}
 
     # -- plaintexts (encoded on first use at the level they are applied) ----------------------------
@@ -182,11 +183,11 @@ class DecodeStep:
         W_t = be.rotate_masked(w, self._vec_pt("mask", w.level, masks), 1)
         ka = be.mul(k, a)
         B_t = be.rotate_masked(ka, self._vec_pt(f"mask_eta{li}", ka.level, masks_eta), 1)
-        D = st["D"]
+        D = st["D"]  # (batch, index) of D_t
         T = M.WKV_T
-        sa = be.mult_sum([[(D, t, Kh_t, t) for t in range(T)]])
+        sa = be.mult_sum([[(D[t][0], D[t][1], Kh_t, t) for t in range(T)]])
         nsa = be.at_neg(sa, min(B_t.level, W_t.level - 1, sa.level - 1))
-        Dn = be.mult_sum([[(D, t, W_t, t), (nsa, 0, B_t, t), (v, 0, K_t, t)] for t in range(T)])
+        Dn = be.mult_sum([[(D[t][0], D[t][1], W_t, t), (nsa, 0, B_t, t), (v, 0, K_t, t)] for t in range(T)])
         y = be.mult_sum([[(Dn, t, R_t, t) for t in range(T)]])
         yg = be.mul(y, g)
         o = be.matvec([yg], self._mv_pt(f"wo{li}", yg.level, lambda: [[L["W_o"]]]))
@@ -214,24 +215,50 @@ class DecodeStep:
         return f
 
     def _refresh_state(self, st):
-        """bootstrap the new state once: pack D_t + i D_{t+32}, bootstrap 32, unpack with one conjugation"""
+        """bootstrap the new state once: the 64 diagonals packed 4 -> 3 into the lanes' unused channels, the 48
+        packed two per complex ciphertext (Q_j + i Q'_j), 24 bootstraps, unpacked with one conjugation and three
+        masked rotations"""
         be = self.be
         Dn = st.pop("Dn")
-        h = M.WKV_T // 2
-        lo, hi = be.slice(Dn, 0, h), be.slice(Dn, h, 2 * h)
-        packed = be.add(lo, be.mul_i(hi, 1))
-        self.stats["bootstraps"] += packed.B
-        P = be.bootstrap(packed, "state")
-        C = be.conj(P)
-        re2 = be.add(P, C)                 # 2 Re
-        im2 = be.mul_i(be.add(C, P, -1), 1)  # i (conj - P) = 2 Im
-        st["D"] = be.halve(be.concat([re2, im2]))  # the sums hold 2 D_t: declared at twice the scale
+        q = M.WKV_T // 4
+        quarter = [be.slice(Dn, k * q, (k + 1) * q) for k in range(4)]
+        # pieces of the fourth quarter into the gaps of the first three
+        packed3 = []
+        for p, g in enumerate(M.GAP_SHIFT):
+            m = self._vec_pt(f"gap_in{p}", quarter[3].level, M.channel_range_mask(256 * p, 256 * (p + 1)))
+            packed3.append(be.add(quarter[p], be.rotate(be.mul_pt(quarter[3], m), -g)))
+        A, B, C = packed3
+        h = q // 2
+        pk = be.concat([be.add(A, be.mul_i(B, 1)),
+                        be.add(be.slice(C, 0, h), be.mul_i(be.slice(C, h, q), 1))])
+        self.stats["bootstraps"] += pk.B
+        P = be.bootstrap(pk, "state")
+        Cj = be.conj(P)
+        re2 = be.halve(be.add(P, Cj))                   # 2 Re: A, C[0:8]; declared at twice the scale
+        im2 = be.halve(be.mul_i(be.add(Cj, P, -1), 1))  # i (conj - P) = 2 Im: B, C[8:16]
+        A2, B2 = be.slice(re2, 0, q), be.slice(im2, 0, q)
+        C2 = be.concat([be.slice(re2, q, q + h), be.slice(im2, q, q + h)])
+        # the fourth quarter back out of the gaps
+        terms = []
+        for p, (src, g) in enumerate(zip((A2, B2, C2), M.GAP_SHIFT)):
+            m = self._vec_pt(f"gap_out{p}", src.level, M.channel_range_mask(256 * p, 256 * (p + 1)))
+            terms.append(be.mul_pt(be.rotate(src, g), m))
+        D4 = be._lin_int(terms, [1, 1, 1])
+        st["D"] = [(A2, t) for t in range(q)] + [(B2, t) for t in range(q)] + [(C2, t) for t in range(q)] + \
+                  [(D4, t) for t in range(q)]
+
+    def state_diagonals(self, li):
+        """(ciphertext batch, index) of D_t, t = 0..63, for layer li"""
+        return self.state[li]["D"]
 
     def cold_state(self):
         be = self.be
         lt = be.top_level
-        return [{"D": be.zeros(M.WKV_T, lt), "xp_t": be.zeros(1, lt), "xp_c": be.zeros(1, lt)}
-                for _ in range(self.n_layers)]
+        out = []
+        for _ in range(self.n_layers):
+            z = be.zeros(M.WKV_T, lt)
+            out.append({"D": [(z, t) for t in range(M.WKV_T)], "xp_t": be.zeros(1, lt), "xp_c": be.zeros(1, lt)})
+        return out
 
     def __call__(self, x):
         """x: ciphertext of the lanes' embeddings; returns the ciphertext of the output-normed hidden state"""

@@ -492,6 +492,16 @@ std::vector<double> wkv_masks(const double* extra) {
     return out;
 }
 
+// channels 768..1023 of every lane are unused: piece p (channels 256p .. 256p + 255) of the fourth quarter of the
+// state diagonals is carried in the gap of quarter p, shifted by kGapShift[p]
+constexpr int kGapShift[3] = {768, 512, 256};
+
+std::vector<double> channel_range_mask(int lo, int hi) {
+    std::vector<double> m(DPAD, 0.0);
+    for (int c = lo; c < hi; c++) m[c] = 1.0;
+    return m;
+}
+
 std::vector<int64_t> layer_rotation_steps() {
     std::vector<int64_t> s;
     for (int b = 0; b < MV_NB; b++) s.push_back(b);
@@ -503,6 +513,10 @@ std::vector<int64_t> layer_rotation_steps() {
     for (int k = 0; k < 10; k++) {
         s.push_back(1 << k);
         s.push_back(-(1 << k));
+    }
+    for (int g : kGapShift) {
+        s.push_back(g);
+        s.push_back(-g);
     }
     std::map<int64_t, bool> u;
     for (auto x : s)
@@ -534,9 +548,14 @@ size_t weight_count(const std::string& n) {
 }
 
 // ------------------------------------------------------------------ the step
+// The carried state of one layer.  D_t (t = 0..63) is item Didx[t].second of the batch Dseg[Didx[t].first]: after a
+// refresh the diagonals live in four batches (the gap-packed quarters), at first in one batch of zeros.
 struct LayerState {
-    Ct D, xp_t, xp_c, Dn;
+    std::vector<Ct> Dseg;
+    std::vector<std::pair<uint32_t, uint32_t>> Didx;
+    Ct xp_t, xp_c, Dn;
 };
+
 
 class Decoder {
    public:
@@ -656,14 +675,14 @@ class Decoder {
         Ct W_t = be_->rotate_masked(w, *vec_pt("mask", w.level, masks), 1);
         Ct ka = be_->mul(k, a);
         Ct B_t = be_->rotate_masked(ka, *vec_pt("mask_eta" + std::to_string(li), ka.level, masks_eta), 1);
-        const Ct& Dc = st.D;
+        auto Dt = [&](uint32_t t) { return &st.Dseg[st.Didx[t].first]; };
         std::vector<std::vector<Pair>> p1(1);
-        for (uint32_t t = 0; t < WKV_T; t++) p1[0].push_back(Pair{&Dc, t, &Kh_t, t});
+        for (uint32_t t = 0; t < WKV_T; t++) p1[0].push_back(Pair{Dt(t), st.Didx[t].second, &Kh_t, t});
         Ct sa = be_->mult_sum(p1);
         Ct nsa = be_->at_neg(sa, std::min({B_t.level, W_t.level - 1, sa.level - 1}));
         std::vector<std::vector<Pair>> p2(WKV_T);
         for (uint32_t t = 0; t < WKV_T; t++)
-            p2[t] = {Pair{&Dc, t, &W_t, t}, Pair{&nsa, 0, &B_t, t}, Pair{&v, 0, &K_t, t}};
+            p2[t] = {Pair{Dt(t), st.Didx[t].second, &W_t, t}, Pair{&nsa, 0, &B_t, t}, Pair{&v, 0, &K_t, t}};
         Ct Dn = be_->mult_sum(p2);
         std::vector<std::vector<Pair>> p3(1);
         for (uint32_t t = 0; t < WKV_T; t++) p3[0].push_back(Pair{&Dn, t, &R_t, t});
@@ -715,28 +734,53 @@ class Decoder {
         return f;
     }
 
-    // bootstrap the new state once: pack D_t + i D_{t+32}, bootstrap 32, unpack with one conjugation
+    // bootstrap the new state once: the 64 diagonals packed 4 -> 3 into the lanes' unused channels, the 48 packed
+    // two per complex ciphertext, 24 bootstraps, unpacked with one conjugation and three masked rotations
     void refresh_state(LayerState& st) {
         Ct Dn = st.Dn;
         st.Dn = Ct{};
-        const uint32_t h = WKV_T / 2;
-        Ct lo = be_->slice(Dn, 0, h), hi = be_->slice(Dn, h, 2 * h);
-        Ct packed = be_->add(lo, be_->mul_i(hi, 1));
-        n_boot_ += packed.B;
-        Ct P = be_->bootstrap(packed, "state");
-        Ct C = be_->conj(P);
-        Ct re2 = be_->add(P, C);                     // 2 Re
-        Ct im2 = be_->mul_i(be_->add(C, P, -1), 1);  // i (conj - P) = 2 Im
-        Ct Dnew = be_->concat({re2, im2});
-        Dnew.scale *= 2.0;  // the sums hold 2 D_t: the same words declared at twice the scale
-        st.D = Dnew;
+        const uint32_t q = WKV_T / 4, h = q / 2;
+        Ct quarter[4];
+        for (uint32_t k = 0; k < 4; k++) quarter[k] = be_->slice(Dn, k * q, (k + 1) * q);
+        Ct packed3[3];
+        for (int p = 0; p < 3; p++) {
+            auto m = vec_pt("gap_in" + std::to_string(p), quarter[3].level,
+                            [p] { return channel_range_mask(256 * p, 256 * (p + 1)); });
+            packed3[p] = be_->add(quarter[p], be_->rotate(be_->mul_pt(quarter[3], *m), -kGapShift[p]));
+        }
+        const Ct &A = packed3[0], &B = packed3[1], &C = packed3[2];
+        Ct pk = be_->concat({be_->add(A, be_->mul_i(B, 1)),
+                             be_->add(be_->slice(C, 0, h), be_->mul_i(be_->slice(C, h, q), 1))});
+        n_boot_ += pk.B;
+        Ct P = be_->bootstrap(pk, "state");
+        Ct Cj = be_->conj(P);
+        Ct re2 = be_->add(P, Cj);                     // 2 Re: A, C[0:8]
+        Ct im2 = be_->mul_i(be_->add(Cj, P, -1), 1);  // i (conj - P) = 2 Im: B, C[8:16]
+        re2.scale *= 2.0;  // the sums hold 2 D_t: the same words declared at twice the scale
+        im2.scale *= 2.0;
+        Ct A2 = be_->slice(re2, 0, q), B2 = be_->slice(im2, 0, q);
+        Ct C2 = be_->concat({be_->slice(re2, q, q + h), be_->slice(im2, q, q + h)});
+        const Ct* src[3] = {&A2, &B2, &C2};
+        std::vector<Ct> terms;
+        for (int p = 0; p < 3; p++) {
+            auto m = vec_pt("gap_out" + std::to_string(p), src[p]->level,
+                            [p] { return channel_range_mask(256 * p, 256 * (p + 1)); });
+            terms.push_back(be_->mul_pt(be_->rotate(*src[p], kGapShift[p]), *m));
+        }
+        Ct D4 = be_->lin_int({&terms[0], &terms[1], &terms[2]}, {1.0, 1.0, 1.0});
+        st.Dseg = {A2, B2, C2, D4};
+        st.Didx.clear();
+        for (uint32_t k = 0; k < 4; k++)
+            for (uint32_t t = 0; t < q; t++) st.Didx.push_back({k, t});
     }
 
     void cold_state() {
         const uint32_t lt = be_->top_level();
         state_.resize(layers_.size());
         for (auto& st : state_) {
-            st.D = be_->zeros(WKV_T, lt);
+            st.Dseg = {be_->zeros(WKV_T, lt)};
+            st.Didx.clear();
+            for (uint32_t t = 0; t < (uint32_t)WKV_T; t++) st.Didx.push_back({0, t});
             st.xp_t = be_->zeros(1, lt);
             st.xp_c = be_->zeros(1, lt);
         }

@@ -201,8 +201,25 @@ def lane_start_mask(scale: float = 1.0) -> np.ndarray:
     return m
 
 
+# ---------------------------------------------------------------- gap packing of the state
+# Channels 768..1023 of every lane are unused (a quarter of the slots).  Before the state is bootstrapped, the
+# 64 diagonal ciphertexts are packed 4 -> 3: piece p (channels 256p .. 256p + 255) of D_{48+j} is moved into the gap
+# of D_{16p+j} by a rotation of -(768 - 256p); after the bootstrap it is moved back by +(768 - 256p) and masked.
+# The gaps of D_0..D_47 then hold those pieces: every use of D_t multiplies it by a masked rotation (zero on the
+# gap), so they never reach a valid channel.
+GAP_SHIFT = (768, 512, 256)  # piece p of the fourth quarter lives in the gap of quarter p, shifted by GAP_SHIFT[p]
+
+
+def channel_range_mask(lo: int, hi: int) -> np.ndarray:
+    """1 on channels lo .. hi-1 of every lane, else 0"""
+    m = np.zeros(DPAD)
+    m[lo:hi] = 1.0
+    return m
+
+
 def rotation_steps() -> list:
     """Every rotation step the decode step uses (keys to generate)."""
     s = set(MV_BABIES) | set(MV_GIANTS) | set(WKV_LO) | set(WKV_HI) | set(NORM_UP) | set(NORM_DOWN)
+    s |= set(GAP_SHIFT) | set(-g for g in GAP_SHIFT)
     s.discard(0)
     return sorted(s)

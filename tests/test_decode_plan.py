@@ -2,8 +2,8 @@
 (fhe-ssm_amd/decode_step.py) with every primitive applied to plain slot values must reproduce the float64
 reference model (oracle/rwkv_ref.py), which is written in matrix form without slots, diagonals or
 rotations.  This pins the packing algebra: BSGS diagonals and their pre-rotation, the lane-sum and
-broadcast of the norms, the WKV diagonal layout and its masked block rotations, the state packing
-(D_t + i D_{t+32}) and unpacking, and the token-shift carries across steps."""
+broadcast of the norms, the WKV diagonal layout and its masked block rotations, the state packing (4 -> 3 into the
+unused channels, then two per complex ciphertext) and unpacking, and the token-shift carries across steps."""
 import numpy as np
 import pytest
 
@@ -59,8 +59,9 @@ def test_decode_step_plan_matches_reference():
         got = M.unpack_lanes(be.decrypt(None, out))
         assert np.max(np.abs(got - xo)) < 1e-12
         assert np.max(np.abs(be.decrypt(None, out).reshape(32, 1024)[:, 768:])) == 0
-        assert np.allclose(M.diag_to_state(step.state[0]["D"].v.real), st[0]["S"], atol=1e-14)
-    # per layer and step: the two increments and the 32 packed state ciphertexts; the residual stays on top
-    assert step.stats["bootstraps"] == 2 * 34
+        Dg = np.stack([ct.v[i].real for ct, i in step.state_diagonals(0)])
+        assert np.allclose(M.diag_to_state(Dg), st[0]["S"], atol=1e-14)
+    # per layer and step: the two increments and the 24 packed state ciphertexts; the residual stays on top
+    assert step.stats["bootstraps"] == 2 * 26
     assert [e[1] for e in be.log[:3]] == ["inc_tm", "state", "inc_cm"]
     assert out.level == 11

@@ -307,7 +307,7 @@ def test_native_decoder_matches_python_plan(engine, DS, M):
         got = out.download((2, lv, N))
         assert np.array_equal(got, want.buf.download((2, lv, N))), s
         print(f"token {s}: native == python plan at level {lv}")
-    assert nat.bootstraps == py.stats["bootstraps"] == 2 * 34
+    assert nat.bootstraps == py.stats["bootstraps"] == 2 * 26
     nat.close()
 
 
@@ -331,4 +331,4 @@ def test_decode_step_full_config5(engine, DS, M):
         lerr = np.sqrt(np.mean((lg - lg_ref) ** 2)) / np.sqrt(np.mean(lg_ref ** 2))
         print(f"token {s}: relErrRms {err:.3e}, logits (4096-row slice) {lerr:.3e}")
         assert err < 1e-3 and lerr < 1e-3, (err, lerr)
-    assert step.stats["bootstraps"] == 2 * 12 * 34
+    assert step.stats["bootstraps"] == 2 * 12 * 26
