@@ -468,8 +468,11 @@ class HEBackend(Backend):
         keys = self.boot_keys.get(kind, self.boot_keys["state"])
         lo = self.at_scale(a, 1, in_scale)
         out = self._new(a.B, self.top_level, self.S(self.top_level))
-        for b0 in range(0, a.B, self.boot_batch):
-            nb = min(self.boot_batch, a.B - b0)
+        # passes of equal size (24 -> 12 + 12): one buffer shape in the bootstrap's pool
+        n_pass = -(-a.B // self.boot_batch)
+        per = -(-a.B // n_pass)
+        for b0 in range(0, a.B, per):
+            nb = min(per, a.B - b0)
             boot.run_many(lo.ptr(b0), nb, self.relin, self.conj_key, keys, out.ptr(b0))
         return out
 

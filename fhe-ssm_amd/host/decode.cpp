@@ -362,8 +362,10 @@ class Engine {
         const auto& bk = boot_keys_.at(kind);
         Ct lo = at_scale(a, 1, r.in_scale);
         Ct out = fresh(a.B, top_, S(top_));
-        for (uint32_t b0 = 0; b0 < a.B; b0 += kBootBatch) {
-            const uint32_t nb = std::min(kBootBatch, a.B - b0);
+        // passes of equal size (24 -> 12 + 12): one buffer shape in the bootstrap's pool
+        const uint32_t n_pass = (a.B + kBootBatch - 1) / kBootBatch, per = (a.B + n_pass - 1) / n_pass;
+        for (uint32_t b0 = 0; b0 < a.B; b0 += per) {
+            const uint32_t nb = std::min(per, a.B - b0);
             ck(ckks_eval_bootstrap_many(ctx_, r.plan, lo.ptr(b0), nb, relin_, conj_, bk.first.data(),
                                         bk.second.data(), (uint32_t)bk.first.size(), out.ptr(b0), nullptr),
                "ckks_eval_bootstrap_many");
