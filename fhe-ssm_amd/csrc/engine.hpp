@@ -51,7 +51,8 @@ struct BConvPlan {
     uint32_t n_in = 0, n_out = 0;
     bool centered = false;  // exact (centered) conversion: table also holds floor(2^128/q_i) and prod mod p_j
     std::vector<uint32_t> in_idx, out_idx;  // prime indices
-    uint64_t* d_tab = nullptr;  // [n_in] (qhat_inv, companion) pairs, then [n_in][n_out] qhat_mod
+    uint64_t* d_tab = nullptr;  // [n_in] (qhat_inv, companion) pairs, then [n_in][n_out] qhat_mod split into 30-bit
+                                // halves ((v >> 30) << 32 | v mod 2^30)
 };
 
 // One profiled launch: HIP events recorded on the launch stream around the kernel, plus the

@@ -115,4 +115,29 @@ struct Acc {
     }
 };
 
+// Multiply-accumulate over 30-bit halves, for sums of at most 8 products of operands below 2^60: with
+// a = a1 2^30 + a0 and b = b1 2^30 + b0 (all halves < 2^30), s0 += a0 b0, s1 += a0 b1 + a1 b0, s2 += a1 b1 are
+// each one v_mad_u64_u32 and cannot overflow (16 terms below 2^60 in s1), so a term costs exactly four
+// multiply-adds with no carry handling.  The constant operand comes packed as (b1 << 32) | b0 (pack30 on the host).
+struct Acc30 {
+    uint64_t s0, s1, s2;
+    __device__ __forceinline__ Acc30() : s0(0), s1(0), s2(0) {}
+    __device__ __forceinline__ void add(uint32_t a0, uint32_t a1, uint64_t bp) {
+        const uint32_t b0 = (uint32_t)bp, b1 = (uint32_t)(bp >> 32);
+        s0 += (uint64_t)a0 * b0;
+        s1 += (uint64_t)a0 * b1;
+        s1 += (uint64_t)a1 * b0;
+        s2 += (uint64_t)a1 * b1;
+    }
+    // the sum as 128 bits: s0 + s1 2^30 + s2 2^60
+    __device__ __forceinline__ U128 get() const {
+        const uint64_t m = s1 << 30, t = s2 << 60;
+        uint64_t lo = s0 + m;
+        uint64_t hi = (s1 >> 34) + (s2 >> 4) + (lo < m ? 1u : 0u);
+        lo += t;
+        hi += (lo < t) ? 1u : 0u;
+        return U128{lo, hi};
+    }
+};
+
 }  // namespace fhe

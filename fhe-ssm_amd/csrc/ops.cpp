@@ -194,7 +194,8 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
             uint64_t m = 1;
             for (uint32_t k = 0; k < p.n_in; k++)
                 if (k != i) m = mulmod_h(m, ctx.moduli[in_idx[k]] % pj, pj);
-            tab[2 * p.n_in + (size_t)i * p.n_out + j] = col_scale.empty() ? m : mulmod_h(m, col_scale[j], pj);
+            const uint64_t v = col_scale.empty() ? m : mulmod_h(m, col_scale[j], pj);
+            tab[2 * p.n_in + (size_t)i * p.n_out + j] = ((v >> 30) << 32) | (v & 0x3FFFFFFFull);  // pack30
         }
     }
     if (centered) {

@@ -129,7 +129,9 @@ struct MdrBconvArgs {
     TwPair pinv_last;       // P^-1 mod q_{l-1}
 };
 
-// NIN = number of input limbs (a template parameter: the term loops unroll without run-time guards)
+// NIN = number of input limbs (a template parameter: the term loops unroll without run-time guards).  The table's
+// q-hat constants are stored pre-split into 30-bit halves (pack30), the y_i are split once, and every term is four
+// multiply-adds into carry-free sums (Acc30; inputs taken in chunks of at most 8).
 template <int NIN, bool kMdr>
 __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
                                                BConvArgs ba, const uint64_t* __restrict__ tab,
@@ -139,12 +141,15 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
     const uint64_t* src = in + c * ba.in_bstride + k;
     uint64_t* dst = out + c * ba.out_bstride + k;
     const TwPair* qhinv = reinterpret_cast<const TwPair*>(tab);
-    const uint64_t* qhmod = tab + 2 * ba.n_in;
+    const uint64_t* qhmod = tab + 2 * ba.n_in;  // [n_in][n_out], pack30 form
     uint64_t y[NIN];
+    uint32_t y0[NIN], y1[NIN];
 #pragma unroll
     for (int i = 0; i < NIN; i++) {
         const uint64_t q = primes[ba.in_prime[i]].q;
         y[i] = shoup(src[(size_t)ba.in_off[i] * kN], qhinv[i].w, qhinv[i].wp, q);
+        y0[i] = (uint32_t)y[i] & 0x3FFFFFFFu;
+        y1[i] = (uint32_t)(y[i] >> 30);
     }
     // centered form (exact ModDown): u = round(sum_i y_i / q_i) from the 128-bit fixed-point sum of
     // floor(y_i * floor(2^128 / q_i) / 2^64); the table then holds [n_in] (lo, hi) words of floor(2^128 / q_i)
@@ -164,67 +169,73 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         const uint64_t lo = F.lo + (1ull << 63);
         u = F.hi + (lo < F.lo ? 1 : 0);
     }
-    // column sum of output j before its final reduction, with the centered correction
-    auto column = [&](Acc& a, uint32_t j, const Barrett& br) {
-        U128 acc = a.get();
+    // column sums of outputs j and j2 (= j when only one is wanted), before the final reduction
+    auto sums = [&](uint32_t j, uint32_t j2, U128& r, U128& r2) {
+        Acc30 a, b;
+#pragma unroll
+        for (int i = 0; i < (NIN < 8 ? NIN : 8); i++) {
+            a.add(y0[i], y1[i], qhmod[(size_t)i * ba.n_out + j]);
+            b.add(y0[i], y1[i], qhmod[(size_t)i * ba.n_out + j2]);
+        }
+        r = a.get();
+        r2 = b.get();
+        if constexpr (NIN > 8) {
+            Acc30 a2, b2;
+#pragma unroll
+            for (int i = 8; i < NIN; i++) {
+                a2.add(y0[i], y1[i], qhmod[(size_t)i * ba.n_out + j]);
+                b2.add(y0[i], y1[i], qhmod[(size_t)i * ba.n_out + j2]);
+            }
+            const U128 s = a2.get(), s2 = b2.get();
+            r.lo += s.lo;
+            r.hi += s.hi + (r.lo < s.lo ? 1u : 0u);
+            r2.lo += s2.lo;
+            r2.hi += s2.hi + (r2.lo < s2.lo ? 1u : 0u);
+        }
+    };
+    // the centered correction: acc - u * pmod_j, kept non-negative by adding 16 p_j (u <= n_in <= 16)
+    auto correct = [&](U128& acc, uint32_t j, const Barrett& br) {
         if (ba.centered) {
-            // acc - u * pmod_j, kept non-negative by adding 16 p_j (u <= n_in <= 16, pmod_j < p_j)
             const uint64_t t = 16 * br.q - u * pmod[j];
             acc.lo += t;
             acc.hi += (acc.lo < t) ? 1 : 0;
         }
-        return acc;
     };
     uint32_t n_main = ba.n_out;
     uint64_t z = 0, ql = 0;
     if constexpr (kMdr) {
         n_main = ba.n_out - 1;
-        Acc a;
-#pragma unroll
-        for (int i = 0; i < NIN; i++) {
-            a.add(y[i], qhmod[(size_t)i * ba.n_out + n_main]);
-            if (i == 7) a.fold();
-        }
+        U128 acc, unused;
+        sums(n_main, n_main, acc, unused);
         const Barrett bl = barrett_of(primes[ba.out_prime[n_main]]);
-        const uint64_t conv = reduce_u128(column(a, n_main, bl), bl);
+        correct(acc, n_main, bl);
+        const uint64_t conv = reduce_u128(acc, bl);
         ql = bl.q;
         z = shoup(sub_mod(mb.xlast[c * mb.xlast_pstride + k], conv, ql), mb.pinv_last.w, mb.pinv_last.wp, ql);
         if (mb.addc) z = add_mod(z, mb.addc[(size_t)c * kN + k], ql);
     }
-    auto finish = [&](Acc& a, uint32_t j) {
+    auto finish = [&](U128 acc, uint32_t j) {
         const Barrett br = barrett_of(primes[ba.out_prime[j]]);
-        U128 acc = column(a, j, br);
+        correct(acc, j, br);
         if constexpr (kMdr) {
             const uint64_t r = lift_centered(z, ql, br);
             acc.lo += r;
-            acc.hi += (acc.lo < r) ? 1 : 0;
+            acc.hi += (acc.lo < r) ? 1u : 0u;
         }
         dst[(size_t)ba.out_off[j] * kN] = reduce_u128(acc, br);
     };
     // two outputs per iteration: independent accumulation chains for the scheduler to interleave
     uint32_t j = 0;
     for (; j + 1 < n_main; j += 2) {
-        Acc a, b;
-#pragma unroll
-        for (int i = 0; i < NIN; i++) {
-            a.add(y[i], qhmod[(size_t)i * ba.n_out + j]);
-            b.add(y[i], qhmod[(size_t)i * ba.n_out + j + 1]);
-            if (i == 7) {
-                a.fold();
-                b.fold();
-            }
-        }
-        finish(a, j);
-        finish(b, j + 1);
+        U128 r, r2;
+        sums(j, j + 1, r, r2);
+        finish(r, j);
+        finish(r2, j + 1);
     }
     if (j < n_main) {
-        Acc a;
-#pragma unroll
-        for (int i = 0; i < NIN; i++) {
-            a.add(y[i], qhmod[(size_t)i * ba.n_out + j]);
-            if (i == 7) a.fold();
-        }
-        finish(a, j);
+        U128 r, unused;
+        sums(j, j, r, unused);
+        finish(r, j);
     }
 }
 
