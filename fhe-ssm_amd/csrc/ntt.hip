@@ -38,10 +38,12 @@ __device__ __forceinline__ void job_of(const JobSpec& js, uint32_t u, uint32_t& 
         off = j.off;
         prime = j.prime;
     } else {
-        // prime-major enumeration of a dense [polys][period][N] buffer
+        // prime-major enumeration of a dense [polys][period][N] buffer.  The prime index is read as the aligned
+        // 32-bit word holding it (a scalar load: the data loads need not wait for a vector byte load)
         const uint32_t l = u / js.n_polys, p = u - l * js.n_polys;
         off = p * js.period + l;
-        prime = js.pmap[l];
+        const uint32_t w = reinterpret_cast<const uint32_t*>(js.pmap)[l >> 2];
+        prime = (w >> (8 * (l & 3))) & 0xFFu;
     }
 }
 
