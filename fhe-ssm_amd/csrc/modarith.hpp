@@ -35,14 +35,27 @@ __device__ __forceinline__ uint64_t shoup_lazy4(uint64_t x, uint64_t w, uint64_t
     const uint32_t w0 = (uint32_t)w, w1 = (uint32_t)(w >> 32);
     const uint32_t n0 = (uint32_t)nq, n1 = (uint32_t)(nq >> 32);
     const uint64_t t = (uint64_t)x0 * w0 + (uint64_t)h0 * n0;
-    const uint32_t hi = (uint32_t)(t >> 32) + x1 * w0 + x0 * w1 + h1 * n0 + h0 * n1;
+    const uint32_t c1 = x1 * w0 + x0 * w1, c2 = h1 * n0 + h0 * n1;
+    // the high word as one 32-bit add of three terms (left to the compiler, this became 64-bit adds and moves)
+    uint32_t hi;
+    asm("v_add3_u32 %0, %1, %2, %3" : "=v"(hi) : "v"((uint32_t)(t >> 32)), "v"(c1), "v"(c2));
     return ((uint64_t)hi << 32) | (uint32_t)t;
 }
 
-// x in [0, 2c) with c < 2^62 -> [0, c): the difference is negative exactly when x < c
+// x in [0, 2c) -> [0, c): x - c, or x when the subtraction borrows (x < c).  Written as the four instructions it
+// needs (subtract with borrow out, then two selects on the borrow): the C form costs a separate 64-bit compare.
 __device__ __forceinline__ uint64_t csub_s(uint64_t x, uint64_t c) {
-    const uint64_t d = x - c;
-    return (int64_t)d < 0 ? x : d;
+    uint32_t lo = (uint32_t)x, hi = (uint32_t)(x >> 32);
+    uint32_t dlo, dhi;
+    asm(
+        "v_sub_co_u32 %0, vcc, %2, %4\n\t"
+        "v_subb_co_u32 %1, vcc, %3, %5, vcc\n\t"
+        "v_cndmask_b32 %0, %0, %2, vcc\n\t"
+        "v_cndmask_b32 %1, %1, %3, vcc"
+        : "=&v"(dlo), "=&v"(dhi)
+        : "v"(lo), "v"(hi), "v"((uint32_t)c), "v"((uint32_t)(c >> 32))
+        : "vcc");
+    return ((uint64_t)dhi << 32) | dlo;
 }
 
 __device__ __forceinline__ uint64_t shoup(uint64_t x, uint64_t w, uint64_t wp, uint64_t q) {
