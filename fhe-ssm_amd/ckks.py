@@ -67,6 +67,8 @@ SIGNATURES = {
     "ckks_linear_transform_general": (_int, [_vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, _u32, _vp, _vp, _vp, _vp]),
     "ckks_linear_transform_multi": (_int, [_vp, _vp, _u32, _u32, _vp, _u32, _u32, _vp, _vp, _u32, _vp, _vp, _u32,
                                            _int, _vp, _vp]),
+    "ckks_linear_transform_hoisted": (_int, [_vp, _vp, _u32, _u32, _vp, _u32, _vp, _vp, _u32, _vp, _vp, _u32, _vp,
+                                             _vp]),
     "ckks_eval_mult_sum": (_int, [_vp, _vp, _u32, _u32, _u32, _vp, _int, _vp, _vp]),
     "ckks_eval_rotate_masked": (_int, [_vp, _vp, _u32, _u32, _vp, _vp, _vp, _vp, _u32, _vp, _u32, _vp, _vp]),
     "ckks_eval_automorphism_ks": (_int, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp]),
@@ -310,6 +312,16 @@ class Context:
                                                  len(bs), _ptr(bs), _ptr_array([k or 0 for k in baby_evks]), len(gs),
                                                  _ptr(gs), _ptr_array([k or 0 for k in giant_evks]), n_out,
                                                  1 if rescale else 0, d_out, stream))
+
+    def linear_transform_hoisted(self, inputs, level, d_diags, baby_steps, baby_evks, giant_steps, giant_evks,
+                                 n_out, d_out, stream=None):
+        """double-hoisted BSGS with the rescale; d_diags over the primes of Q_level then P"""
+        bs = np.ascontiguousarray(np.asarray(baby_steps, dtype=np.int64))
+        gs = np.ascontiguousarray(np.asarray(giant_steps, dtype=np.int64))
+        check(load().ckks_linear_transform_hoisted(self.h, _ptr_array(inputs), len(inputs), level, d_diags, len(bs),
+                                                   _ptr(bs), _ptr_array([k or 0 for k in baby_evks]), len(gs),
+                                                   _ptr(gs), _ptr_array([k or 0 for k in giant_evks]), n_out, d_out,
+                                                   stream))
 
     def eval_mult_sum(self, pairs, level, d_evk, d_out, rescale=True, stream=None):
         """pairs: [batch][n_products] of (a, b) device pointers"""

@@ -582,6 +582,31 @@ int ckks_linear_transform_multi(ckks_context* ctx, const uint64_t* const* d_in, 
     });
 }
 
+int ckks_linear_transform_hoisted(ckks_context* ctx, const uint64_t* const* d_in, uint32_t n_in, uint32_t level,
+                                  const uint64_t* d_diags, uint32_t n_baby, const int64_t* baby_steps,
+                                  const uint64_t* const* d_baby_evks, uint32_t n_giant, const int64_t* giant_steps,
+                                  const uint64_t* const* d_giant_evks, uint32_t n_out, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_in || !d_diags || !d_out || !baby_steps || !giant_steps || !d_baby_evks || !d_giant_evks)
+        return fail(CKKS_EINVAL, "null argument");
+    if (n_in == 0 || n_out == 0 || n_baby == 0 || n_baby > 64 || n_in * n_baby > 256 || n_giant == 0 ||
+        n_giant > 64)
+        return fail(CKKS_EINVAL, "bad BSGS shape");
+    if (level < 2) return fail(CKKS_EINVAL, "rescale needs level >= 2");
+    if (ctx->c.K == 0) return fail(CKKS_EINVAL, "the extended basis needs special primes");
+    for (uint32_t i = 0; i < n_in; i++)
+        if (!d_in[i]) return fail(CKKS_EINVAL, "null input");
+    for (uint32_t i = 0; i < n_baby; i++)
+        if (baby_steps[i] && !d_baby_evks[i]) return fail(CKKS_EINVAL, "null baby key");
+    for (uint32_t i = 0; i < n_giant; i++)
+        if (giant_steps[i] && !d_giant_evks[i]) return fail(CKKS_EINVAL, "null giant key");
+    return guarded([&] {
+        fhe::bsgs_dh_batch(ctx->c, d_in, 1, n_in, level, d_diags, n_baby, baby_steps, d_baby_evks, n_giant,
+                           giant_steps, d_giant_evks, n_out, d_out, (hipStream_t)stream, false);
+        return CKKS_OK;
+    });
+}
+
 int ckks_eval_mult_sum(ckks_context* ctx, const uint64_t* const* d_pairs, uint32_t n_products, uint32_t batch,
                        uint32_t level, const uint64_t* d_evk, int rescale, uint64_t* d_out, void* stream) {
     if (int rc = check_ctx_level(ctx, level, true)) return rc;

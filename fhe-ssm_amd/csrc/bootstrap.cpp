@@ -192,9 +192,14 @@ BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scal
         bl.n_in = bl.n_out = split ? 2 : 1;
         for (uint32_t b = 0; b < bl.nb; b++) bl.bsteps.push_back((int64_t)b * delta);
         for (uint32_t g = 0; g < bl.ng; g++) bl.gsteps.push_back(((int64_t)g * bl.nb - 31) * delta);
+        // the levels run double-hoisted: their diagonals are encoded over Q_l * P
+        std::vector<uint32_t> pmap;
+        for (uint32_t i = 0; i < l; i++) pmap.push_back(i);
+        for (uint32_t k = 0; k < ctx.K; k++) pmap.push_back(ctx.L + k);
+        const size_t E = pmap.size();
         const size_t n_terms = (size_t)bl.n_out * bl.ng * bl.n_in * bl.nb;
-        HIPB(hipMalloc(&bl.d_diags, n_terms * l * W * 8));
-        HIPB(hipMemset(bl.d_diags, 0, n_terms * l * W * 8));
+        HIPB(hipMalloc(&bl.d_diags, n_terms * E * W * 8));
+        HIPB(hipMemset(bl.d_diags, 0, n_terms * E * W * 8));
         std::vector<double> re(kSlots), im(kSlots);
         auto put = [&](uint32_t o, uint32_t g, uint32_t j, const std::vector<cd>& v) {
             for (uint32_t s = 0; s < kSlots; s++) {
@@ -202,7 +207,7 @@ BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scal
                 im[s] = v[s].imag();
             }
             const size_t t = ((size_t)o * bl.ng + g) * bl.n_in * bl.nb + j;
-            encode(ctx, re.data(), im.data(), kSlots, l, pt_scale, bl.d_diags + t * l * W);
+            encode_primes(ctx, re.data(), im.data(), kSlots, pmap, pt_scale, bl.d_diags + t * E * W);
         };
         std::vector<cd> dr(kSlots), tmp(kSlots);
         for (auto& [off, d] : D) {
@@ -535,8 +540,8 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint3
         keys_of(bl, bk, gk);
         for (uint32_t b = 0; b < B; b++) ins[b] = in.d + (size_t)b * 2 * bl.l * W;
         HCt o = ev.get(bl.l - 1);
-        bsgs_multi_batch(ctx, ins.data(), B, 1, bl.l, bl.d_diags, bl.nb, bl.bsteps.data(), bk.data(), bl.ng,
-                         bl.gsteps.data(), gk.data(), 1, true, o.d, st, 0, false);
+        bsgs_dh_batch(ctx, ins.data(), B, 1, bl.l, bl.d_diags, bl.nb, bl.bsteps.data(), bk.data(), bl.ng,
+                      bl.gsteps.data(), gk.data(), 1, o.d, st, false);
         return o;
     };
     HCt x = raised;
@@ -562,8 +567,8 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint3
             ins[2 * b] = x.d + (size_t)b * 2 * bs.l * W;
             ins[2 * b + 1] = cj.d + (size_t)b * 2 * bs.l * W;
         }
-        bsgs_multi_batch(ctx, ins.data(), B, 2, bs.l, bs.d_diags, bs.nb, bs.bsteps.data(), bk.data(), bs.ng,
-                         bs.gsteps.data(), gk.data(), 2, true, pair.d, st, 0, true);
+        bsgs_dh_batch(ctx, ins.data(), B, 2, bs.l, bs.d_diags, bs.nb, bs.bsteps.data(), bk.data(), bs.ng,
+                      bs.gsteps.data(), gk.data(), 2, pair.d, st, true);
         ev1.put(cj);
         ev1.put(x);
     }

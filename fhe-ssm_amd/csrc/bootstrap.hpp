@@ -13,7 +13,9 @@ struct BootLevel {
     uint32_t l = 0, nb = 0, ng = 0;
     uint32_t n_in = 1, n_out = 1;  // the last CoeffToSlot level: inputs (y, conj y), outputs (2 Re, 2 Im)
     std::vector<int64_t> bsteps, gsteps;
-    uint64_t* d_diags = nullptr;  // [n_out][ng][n_in nb][l][N], term (g, b) pre-rotated by -gsteps[g]
+    // [n_out][ng][n_in nb][l + K][N] over the primes of Q_l * P (the levels run double-hoisted), term (g, b)
+    // pre-rotated by -gsteps[g]
+    uint64_t* d_diags = nullptr;
 };
 
 struct BootPlan {

@@ -312,6 +312,12 @@ void keygen_automorphism(Context& ctx, const Secret& sk, uint32_t g, const uint8
 // values (re, im may be null) of n_slots slots, replicated to N/2 when n_slots divides N/2
 void encode(Context& ctx, const double* re, const double* im, uint32_t n_slots, uint32_t l, double scale,
             uint64_t* d_pt) {
+    encode_primes(ctx, re, im, n_slots, iota(l), scale, d_pt);
+}
+
+// the same plaintext over the primes pmap (limb t of the output is mod prime pmap[t])
+void encode_primes(Context& ctx, const double* re, const double* im, uint32_t n_slots,
+                   const std::vector<uint32_t>& pmap, double scale, uint64_t* d_pt) {
     if (n_slots == 0 || (kN / 2) % n_slots != 0) throw std::invalid_argument("n_slots must divide N/2");
     std::vector<uint32_t> t_of, tc_of;
     slot_points(t_of, tc_of);
@@ -330,7 +336,7 @@ void encode(Context& ctx, const double* re, const double* im, uint32_t n_slots, 
         if (!(std::fabs(m) < 4.0e18)) throw std::invalid_argument("encoded coefficient overflows int64");
         coef[k] = (int64_t)std::llround(m);
     }
-    coeffs_to_eval(ctx, coef.data(), 1, iota(l), d_pt, nullptr);
+    coeffs_to_eval(ctx, coef.data(), 1, pmap, d_pt, nullptr);
 }
 
 // Periodic encoding (hpc_gpu_port/periodic_encode.hpp:179-260): a slot vector of period P (replicated

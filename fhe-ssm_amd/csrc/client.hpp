@@ -26,6 +26,8 @@ void keygen_automorphism(Context& ctx, const Secret& sk, uint32_t g, const uint8
                          double sigma, uint64_t* d_evk);
 void encode(Context& ctx, const double* re, const double* im, uint32_t n_slots, uint32_t l, double scale,
             uint64_t* d_pt);
+void encode_primes(Context& ctx, const double* re, const double* im, uint32_t n_slots,
+                   const std::vector<uint32_t>& pmap, double scale, uint64_t* d_pt);
 void encode_periodic(Context& ctx, const double* re, const double* im, uint32_t n_vec, uint32_t P, uint32_t l,
                      double scale, uint64_t* d_out);
 void encrypt(Context& ctx, const Secret& sk, const uint64_t* d_pt, uint32_t l, const uint8_t seed[32], uint32_t index,

@@ -59,7 +59,12 @@ hipError_t launch_ks_sub_list(const Context& ctx, const uint64_t* const* ext, co
 hipError_t launch_automorph_list(const Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n, uint32_t l,
                                  const uint32_t* g, hipStream_t st);
 hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* const* baby, const uint64_t* diag, uint64_t* out,
-                           uint32_t nb, uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st);
+                           uint32_t nb, uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st,
+                           uint32_t l_q = 0);
+hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
+                             uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_out,
+                             uint32_t nt, uint32_t A, uint32_t M, uint32_t l, const TwPair* pmod, uint64_t* dst,
+                             hipStream_t st, uint32_t R = 1, uint32_t c_off = 0, uint64_t s_lo = 0);
 hipError_t launch_mul_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
                             uint32_t l, uint64_t pt_bstride, uint32_t log_rep, hipStream_t st);
 hipError_t launch_add_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
@@ -788,6 +793,88 @@ void bsgs_multi_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, 
             HIPX(launch_sum_list(ctx, terms.data(), (uint32_t)terms.size(), dst + slot * ctw, 2, l, st));
         }
     if (do_rescale) rescale(ctx, dst, 2 * n_inst * n_out, l, out, st);
+}
+
+// Double-hoisted BSGS (the same transform as bsgs_multi_batch with do_rescale, over n_inst instances that share
+// the diagonals; Bossuat, Mouchet, Troncoso-Pastoriza, Hubaux, EUROCRYPT 2021, the hoisted linear transform):
+// the baby rotations stay in the extended basis Q_l * P (no ModDown: (P c0 + ks0, ks1) under Auto_b), the
+// diagonals -- encoded over Q_l * P, diags [n_out][ng][n_in nb][l + K][N] -- multiply them there, each giant's
+// inner sum is brought down once, rotated by the giant step again without its ModDown, and the giant sums are
+// brought down and rescaled together: ng + 1 ModDowns per output instead of (nb - 1) + ng.
+// out [n_inst][n_out][2][l-1][N] (by_output: [n_out][n_inst]).  The babies' key switches and automorphisms, and
+// the giants' with their sum, each run as one kernel (k_qp_rot_sum) that stores only the rotated result.
+void bsgs_dh_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uint32_t n_in, uint32_t l,
+                   const uint64_t* diags_qp, uint32_t nb, const int64_t* bsteps, const uint64_t* const* bevk,
+                   uint32_t ng, const int64_t* gsteps, const uint64_t* const* gevk, uint32_t n_out, uint64_t* out,
+                   hipStream_t st, bool by_output) {
+    check_level(ctx, l);
+    if (nb == 0 || nb > 64 || n_in == 0 || n_out == 0 || ng == 0 || ng > 64 || n_inst == 0 || l < 2)
+        throw std::invalid_argument("bad BSGS shape");
+    const uint32_t E = l + ctx.K, D = num_digits(ctx, l), K = ctx.K;
+    const size_t ctw = (size_t)2 * l * W, cte = (size_t)2 * E * W, exw = (size_t)D * E * W;
+    const uint32_t nbt = n_in * nb, n_x = n_inst * n_in, n_o = n_inst * n_out;
+    std::vector<TwPair> pmod(l);  // P mod q_t
+    for (uint32_t t = 0; t < l; t++) {
+        const uint64_t q = ctx.moduli[t];
+        uint64_t P = 1;
+        for (uint32_t k = 0; k < K; k++) P = mulmod_h(P, ctx.moduli[ctx.L + k] % q, q);
+        pmod[t] = TwPair{P, shoup_companion(P, q)};
+    }
+    // the inputs side by side (read in place when they already are), their c1 extended once
+    const uint64_t* X = in[0];
+    for (uint32_t x = 1; x < n_x; x++)
+        if (in[x] != in[0] + x * ctw) X = nullptr;
+    if (!X) {
+        uint64_t* Xg = (uint64_t*)ws_get(ctx, WS_BINP, (size_t)n_x * ctw * 8);
+        HIPX(launch_gather(ctx, in, n_x, ctw, Xg, st));
+        X = Xg;
+    }
+    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT2, (size_t)n_x * exw * 8);
+    modup(ctx, X + (size_t)l * W, ext, n_x, l, st, ctw);
+    // babies in Q_l P, BQ [n_x][nb][2][E][N]: output x nb + b is term 0 of input x with key b
+    uint64_t* BQ = (uint64_t*)ws_get(ctx, WS_BABY, (size_t)n_x * nb * cte * 8);
+    {
+        std::vector<uint32_t> g(nb);
+        for (uint32_t b = 0; b < nb; b++) g[b] = bsteps[b] ? rotation_index(bsteps[b]) : 1;
+        HIPX(launch_qp_rot_sum(ctx, ext, exw, X, ctw, bevk, g.data(), n_x * nb, 1, nb, 1, l, pmod.data(), BQ, st));
+    }
+    // inner sums in Q_l P: S [n_inst][n_out][ng][2][E][N]
+    uint64_t* S = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)n_o * ng * cte * 8);
+    std::vector<const uint64_t*> bp(nbt);
+    for (uint32_t s = 0; s < n_inst; s++) {
+        for (uint32_t i = 0; i < n_in; i++)
+            for (uint32_t b = 0; b < nb; b++) bp[i * nb + b] = BQ + (((size_t)(s * n_in + i)) * nb + b) * cte;
+        HIPX(launch_bsgs_mac(ctx, bp.data(), diags_qp, S + (size_t)s * n_out * ng * cte, nbt, nbt * n_out * ng,
+                             n_out * ng, E, 0, st, l));
+    }
+    // every inner sum down to Q_l once (its rotation needs c1 in Q_l): SQ [n_o][ng][2][l][N]
+    uint64_t* SQ = (uint64_t*)ws_get(ctx, WS_SUM, (size_t)n_o * ng * ctw * 8);
+    moddown_inplace(ctx, S, 2 * n_o * ng, l, nullptr, SQ, st);
+    // giant rotations without their ModDown, summed per output in Q_l P: T [n_o][2][E][N] (by_output: output o of
+    // instance s at slot o n_inst + s); outputs in chunks whose extensions fit a bounded buffer
+    uint64_t* T = (uint64_t*)ws_get(ctx, WS_GROT, (size_t)n_o * cte * 8);
+    std::vector<uint32_t> gg(ng);
+    uint32_t n_rot = 0;
+    for (uint32_t g = 0; g < ng; g++) {
+        gg[g] = gsteps[g] ? rotation_index(gsteps[g]) : 1;
+        n_rot += gsteps[g] ? 1 : 0;
+    }
+    const uint32_t chunk = std::max<uint32_t>(1, 32 / ng);
+    uint64_t* ext2 = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)std::min(chunk, n_o) * ng * exw * 8);
+    for (uint32_t o0 = 0; o0 < n_o; o0 += chunk) {
+        const uint32_t m = std::min(chunk, n_o - o0);
+        const uint64_t* src = SQ + (size_t)o0 * ng * ctw;
+        // identity giants are extended too (one strided ModUp over the chunk); their extension goes unread
+        if (n_rot) modup(ctx, src + (size_t)l * W, ext2, m * ng, l, st, ctw);
+        if (by_output)
+            HIPX(launch_qp_rot_sum(ctx, ext2, exw, src, ctw, gevk, gg.data(), m, ng, 1, ng, l, pmod.data(), T, st,
+                                   n_out, o0, (uint64_t)n_inst * cte));
+        else
+            HIPX(launch_qp_rot_sum(ctx, ext2, exw, src, ctw, gevk, gg.data(), m, ng, 1, ng, l, pmod.data(),
+                                   T + (size_t)o0 * cte, st));
+    }
+    // one ModDown for the giant sums, fused with the rescale
+    moddown_rescale(ctx, T, 2 * n_o, l, nullptr, out, st);
 }
 
 void bsgs_multi(Context& ctx, const uint64_t* const* in, uint32_t n_in, uint32_t l, const uint64_t* diags,

@@ -23,6 +23,7 @@ enum WsSlot : uint32_t {
     WS_PTAB,
     WS_BINP,
     WS_RTMP2,
+    WS_EXT2,  // a second ModUp extension (double-hoisted BSGS: the inputs' while the giants' is in use)
     WS_COUNT
 };
 
@@ -74,6 +75,11 @@ void bsgs_multi_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, 
                       const uint64_t* diags, uint32_t nb, const int64_t* bsteps, const uint64_t* const* bevk,
                       uint32_t ng, const int64_t* gsteps, const uint64_t* const* gevk, uint32_t n_out,
                       bool do_rescale, uint64_t* out, hipStream_t st, uint32_t log_rep, bool by_output);
+// double-hoisted bsgs_multi_batch with the rescale: diags_qp [n_out][ng][n_in nb][l + K][N] over Q_l * P
+void bsgs_dh_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uint32_t n_in, uint32_t l,
+                   const uint64_t* diags_qp, uint32_t nb, const int64_t* bsteps, const uint64_t* const* bevk,
+                   uint32_t ng, const int64_t* gsteps, const uint64_t* const* gevk, uint32_t n_out, uint64_t* out,
+                   hipStream_t st, bool by_output);
 void hmult_sum(Context& ctx, const uint64_t* const* pairs, uint32_t np, uint32_t B, uint32_t l, const uint64_t* evk,
                uint64_t* out, bool do_rescale, hipStream_t st);
 void bsgs_multi(Context& ctx, const uint64_t* const* in, uint32_t n_in, uint32_t l, const uint64_t* diags,

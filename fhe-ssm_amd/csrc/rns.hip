@@ -539,6 +539,70 @@ __global__ __launch_bounds__(256) void k_automorph_list(const uint64_t* __restri
     out[base + k] = in[base + src];
 }
 
+// Rotations kept in the extended basis Q_l * P, summed per output (double-hoisted BSGS).  Output c ([2][E][N] at
+// dst + c 2 E N) is the sum over its nt terms j of
+//   Auto_g( <ext_x, evk>_0 + P c0_x,  <ext_x, evk>_1 )    (a key-switched term: (P c0 + ks0, ks1) encrypts P m over
+//                                                          Q_l * P, the rotation without its ModDown)
+//   Auto_g( P c0_x, P c1_x )                              (an identity term, evk null: zero on the P limbs)
+// with x = (c / A) M + j the term's input (its ModUp extension [D][E][N] at ext + x ext_stride, the ciphertext
+// [2][l][N] at src + x src_stride) and key index c % A + j (evk, g).  Output c goes to dst + (u / R) s_hi + (u % R)
+// s_lo, u = c + c_off (R = 1, s_hi = 2 E N: contiguous).  The evk inner product is formed at the
+// automorphism's source word, so nothing is stored between the key switch and the automorphism; the source words
+// of a wave's 64 consecutive outputs are a permutation of one aligned 64-word block (the automorphism multiplies
+// the bit-reversed index by an odd g), so the gathers stay coalesced.
+struct QpRotArgs {
+    uint32_t l, E, L, D, T, nt, A, M;
+    uint32_t R, c_off;
+    uint64_t ext_stride, src_stride, s_hi, s_lo;
+    const uint64_t* evk[kMaxList];
+    uint32_t g[kMaxList];
+    TwPair pmod[kMaxPmap];  // P mod q_t, t < l
+};
+
+__global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__ ext,
+                                                    const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
+                                                    QpRotArgs a, const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t t = blockIdx.y, c = blockIdx.z;
+    const bool qlimb = t < a.l;
+    const uint32_t pi = qlimb ? t : a.L + (t - a.l);
+    const Barrett br = barrett_of(primes[pi]);
+    const uint64_t q = br.q;
+    uint64_t v0 = 0, v1 = 0;
+    for (uint32_t j = 0; j < a.nt; j++) {
+        const uint32_t x = (c / a.A) * a.M + j, kk = c % a.A + j;
+        const uint32_t g = a.g[kk];
+        const uint32_t e = (uint32_t)(((uint64_t)g * (2u * (__brev(k) >> (32 - kLogN)) + 1u)) & (2u * kN - 1u));
+        const uint32_t sw = __brev((e - 1u) >> 1) >> (32 - kLogN);
+        const uint64_t* sx = src + (size_t)x * a.src_stride + (size_t)t * kN + sw;
+        const uint64_t* ek = a.evk[kk];
+        if (ek) {
+            const uint64_t* xe = ext + (size_t)x * a.ext_stride + (size_t)t * kN + sw;
+            const uint64_t* ep = ek + (size_t)pi * kN + sw;
+            Acc s0, s1;  // at most kMaxDigits = 8 terms
+#pragma unroll
+            for (int d = 0; d < kMaxDigits; d++) {
+                if (d < (int)a.D) {
+                    const uint64_t v = xe[(size_t)d * a.E * kN];
+                    s0.add(v, ep[((size_t)d * 2 + 0) * a.T * kN]);
+                    s1.add(v, ep[((size_t)d * 2 + 1) * a.T * kN]);
+                }
+            }
+            uint64_t r0 = reduce_u128(s0.get(), br);
+            if (qlimb) r0 = add_mod(r0, shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q), q);
+            v0 = add_mod(v0, r0, q);
+            v1 = add_mod(v1, reduce_u128(s1.get(), br), q);
+        } else if (qlimb) {
+            v0 = add_mod(v0, shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q), q);
+            v1 = add_mod(v1, shoup(sx[(size_t)a.l * kN], a.pmod[t].w, a.pmod[t].wp, q), q);
+        }
+    }
+    const uint32_t u = c + a.c_off;
+    uint64_t* o = dst + (size_t)(u / a.R) * a.s_hi + (size_t)(u % a.R) * a.s_lo + (size_t)t * kN + k;
+    o[0] = v0;
+    o[(size_t)a.E * kN] = v1;
+}
+
 // BSGS multiply-accumulate: babies [nb][2][l][N], diagonals [n_diag][l][N] (diagonal g*nb + j pairs with
 // baby j), out [ng][2][l][N]: out_g = sum_j baby_j (.) diag_{g*nb+j}.
 // A workgroup owns 64 coefficients of one limb: it stages those words of every baby in LDS once, then its
@@ -560,13 +624,13 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(ListPtrs baby,
                                                                   uint64_t* __restrict__ out, uint32_t nb,
                                                                   uint32_t nb_total, uint32_t j0, uint32_t ng,
                                                                   uint32_t n_diag, uint32_t l, uint32_t log_rep,
-                                                                  uint32_t acc,
+                                                                  uint32_t acc, uint32_t l_q, uint32_t Lp,
                                                                   const PrimeInfo* __restrict__ primes) {
     extern __shared__ uint64_t sb[];
     const uint32_t kk = threadIdx.x & (kMacCoef - 1), row = threadIdx.x / kMacCoef;
     const uint32_t k = blockIdx.x * kMacCoef + kk;
-    const uint32_t i = blockIdx.y;
-    const Barrett br = barrett_of(primes[i]);
+    const uint32_t i = blockIdx.y;  // limb; limbs from l_q on are P limbs (prime Lp + i - l_q)
+    const Barrett br = barrett_of(primes[i < l_q ? i : Lp + (i - l_q)]);
     const size_t P = (size_t)l * kN, off = (size_t)i * kN + k;
     for (uint32_t jp = row; jp < 2 * nb; jp += kMacRows) {  // jp = 2 j + poly; baby j of this chunk at baby.p[j]
         const uint32_t j = jp >> 1, p = jp & 1;
@@ -920,8 +984,11 @@ hipError_t launch_automorph_list(const Context& ctx, const uint64_t* in, uint64_
     return hipGetLastError();
 }
 
+// l limbs per poly; with l_q < l the limbs from l_q on are the P limbs (an extended-basis MAC)
 hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* const* baby, const uint64_t* diag, uint64_t* out,
-                           uint32_t nb, uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st) {
+                           uint32_t nb, uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st,
+                           uint32_t l_q) {
+    if (l_q == 0 || l_q > l) l_q = l;
     if (nb == 0 || log_rep > 6 || n_diag > nb * ng) return hipErrorInvalidValue;
     const double bytes = ((double)nb * 2 * l + (double)n_diag * l / (1u << log_rep) + (double)ng * 2 * l) * kN * 8;
     const int pi = prof_begin(ctx, log_rep ? "bsgs_mac_periodic" : "bsgs_mac", bytes, st);
@@ -931,7 +998,7 @@ hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* const* baby, cons
         for (uint32_t j = 0; j < nbc; j++) bp.p[j] = baby[j0 + j];
         hipLaunchKernelGGL(k_bsgs_mac, dim3(kN / kMacCoef, l), dim3(kMacCoef * kMacRows),
                            (size_t)nbc * 2 * kMacCoef * 8, st, bp, diag, out, nbc, nb, j0, ng, n_diag, l, log_rep,
-                           j0 ? 1u : 0u, ctx.d_primes);
+                           j0 ? 1u : 0u, l_q, ctx.L, ctx.d_primes);
     }
     prof_end(ctx, pi, st);
     return hipGetLastError();
@@ -989,6 +1056,51 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
     const int pi = prof_begin(ctx, "mdr_combine_ks", bytes, st);
     hipLaunchKernelGGL(k_mdr_combine_ks, dim3(B, kN / 256, l - 1), dim3(256), 0, st, ext, evk, add, T, out, ia, ma,
                        ctx.d_primes);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+// n_out outputs of nt terms each (see k_qp_rot_sum); keys[i] / steps g[i], i < A + nt - 1 <= 64 (null key:
+// identity term); output c at dst + (u / R) 2 E N + (u % R) s_lo, u = c + c_off
+hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
+                             uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_out,
+                             uint32_t nt, uint32_t A, uint32_t M, uint32_t l, const TwPair* pmod, uint64_t* dst,
+                             hipStream_t st, uint32_t R, uint32_t c_off, uint64_t s_lo) {
+    const uint32_t E = l + ctx.K;
+    if (n_out == 0 || nt == 0 || A == 0 || A + nt - 1 > (uint32_t)kMaxList || E > kMaxPmap || n_out > 65535)
+        return hipErrorInvalidValue;
+    const uint32_t D = (l + ctx.alpha - 1) / ctx.alpha;
+    if (D > (uint32_t)kMaxDigits) return hipErrorInvalidValue;
+    QpRotArgs a{};
+    a.l = l;
+    a.E = E;
+    a.L = ctx.L;
+    a.D = D;
+    a.T = ctx.L + ctx.K;
+    a.nt = nt;
+    a.A = A;
+    a.M = M;
+    a.ext_stride = ext_stride;
+    a.src_stride = src_stride;
+    a.R = R ? R : 1;
+    a.c_off = c_off;
+    a.s_hi = (uint64_t)2 * E * kN;
+    a.s_lo = s_lo;
+    uint32_t n_ks = 0;
+    for (uint32_t i = 0; i < A + nt - 1; i++) {
+        a.evk[i] = keys[i];
+        a.g[i] = g[i];
+    }
+    for (uint32_t c = 0; c < A; c++)
+        for (uint32_t j = 0; j < nt; j++) n_ks += keys[c + j] ? 1 : 0;
+    for (uint32_t t = 0; t < l; t++) a.pmod[t] = pmod[t];
+    // bytes: per key-switched term ext D E + evk 2 D E + c0 l, per identity term 2 l; output 2 E
+    const double terms = (double)n_out / A;
+    const double by = ((double)n_ks * (3.0 * D * E + l) + ((double)A * nt - n_ks) * 2.0 * l) * terms +
+                      (double)n_out * 2 * E;
+    ctx.n_keyswitch += n_ks * (uint64_t)(n_out / A);
+    const int pi = prof_begin(ctx, "qp_rot_sum", by * kN * 8, st);
+    hipLaunchKernelGGL(k_qp_rot_sum, dim3(kN / 256, E, n_out), dim3(256), 0, st, ext, src, dst, a, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }

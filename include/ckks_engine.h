@@ -195,6 +195,18 @@ int ckks_linear_transform_multi(ckks_context* ctx, const uint64_t* const* d_in, 
                                 const uint64_t* const* d_baby_evks, uint32_t n_giant, const int64_t* giant_steps,
                                 const uint64_t* const* d_giant_evks, uint32_t n_out, int rescale, uint64_t* d_out,
                                 void* stream);
+/* ckks_linear_transform_hoisted  the BSGS linear transform of EvalBootstrap's CoeffToSlot / SlotToCoeff
+ *                           (gpu_real_model.cu:2544; FIDESlib's hoisted transform, an external dependency) in its
+ *                           double-hoisted form: the sum of ckks_linear_transform_multi with the rescale, but the
+ *                           babies stay in the extended basis Q_l P (no ModDown), the diagonals multiply them there,
+ *                           each giant's inner sum is brought down once, the giant rotations are summed in Q_l P and
+ *                           one ModDown, fused with the rescale, ends it.  diags [n_out][n_giant][n_in n_baby][l+K][N]
+ *                           over the primes of Q_l then P (uncompressed); out [n_out][2][l-1][N].  Decrypts like
+ *                           ckks_linear_transform_multi's output up to the key-switching rounding (different words). */
+int ckks_linear_transform_hoisted(ckks_context* ctx, const uint64_t* const* d_in, uint32_t n_in, uint32_t level,
+                                  const uint64_t* d_diags, uint32_t n_baby, const int64_t* baby_steps,
+                                  const uint64_t* const* d_baby_evks, uint32_t n_giant, const int64_t* giant_steps,
+                                  const uint64_t* const* d_giant_evks, uint32_t n_out, uint64_t* d_out, void* stream);
 int ckks_eval_mult_sum(ckks_context* ctx, const uint64_t* const* d_pairs, uint32_t n_products, uint32_t batch,
                        uint32_t level, const uint64_t* d_evk, int rescale, uint64_t* d_out, void* stream);
 int ckks_eval_rotate_masked(ckks_context* ctx, const uint64_t* d_ct, uint32_t level, uint32_t n,

@@ -226,6 +226,64 @@ def test_linear_transform_multi_bit_exact(ckks, ctx5, octx5):
         assert np.array_equal(got[o], want), o
 
 
+def test_linear_transform_hoisted_bit_exact(ckks, ctx5, octx5):
+    """Double-hoisted BSGS (the bootstrap's CoeffToSlot / SlotToCoeff form) against the oracle composed from its
+    stages: babies rotated in Q_l P without a ModDown, diagonals over Q_l P, one ModDown per giant inner sum,
+    giant rotations summed in Q_l P, ModDown then rescale.  2 inputs, 2 outputs, babies {0, 1, 2}, giants
+    {0, 3, -3}."""
+    l, n_in, n_out = 5, 2, 2
+    L, K, D = ctx5.L, ctx5.K, ctx5.dnum
+    bst, gst = [0, 1, 2], [0, 3, -3]
+    nb, ng = len(bst), len(gst)
+    steps = [1, 2, 3, -3]
+    pmap = list(range(l)) + list(range(L, L + K))
+    E = l + K
+    evk = {s: residues(ctx5.moduli, (D, 2), list(range(L + K)), 300 + i) for i, s in enumerate(steps)}
+    dk = {s: ckks.DeviceBuffer.from_array(e) for s, e in evk.items()}
+    xs = residues(ctx5.moduli, (n_in, 2), list(range(l)), 31)
+    diags = residues(ctx5.moduli, (n_out, ng, n_in * nb), pmap, 32)
+    dx, dd = ckks.DeviceBuffer.from_array(xs), ckks.DeviceBuffer.from_array(diags)
+    out = ckks.DeviceBuffer(n_out * 2 * (l - 1) * N * 8)
+    ctw = 2 * l * N * 8
+    ctx5.linear_transform_hoisted([dx.ptr + i * ctw for i in range(n_in)], l, dd.ptr, bst,
+                                  [dk[s].ptr if s else None for s in bst], gst,
+                                  [dk[s].ptr if s else None for s in gst], n_out, out.ptr)
+    got = out.download((n_out, 2, l - 1, N))
+    qe = np.array([ctx5.moduli[i] for i in pmap], dtype=object).reshape(-1, 1)
+    P = 1
+    for k in range(K):
+        P *= ctx5.moduli[L + k]
+    pq = np.array([P % ctx5.moduli[i] for i in range(l)], dtype=object).reshape(-1, 1)
+
+    def lift(c, both):
+        """(P c0, P c1) (both) or (P c0, 0) on the Q limbs, zero on the P limbs: [2][E][N] objects"""
+        r = np.zeros((2, E, N), dtype=object)
+        r[0, :l] = c[0].astype(object) * pq % qe[:l]
+        if both:
+            r[1, :l] = c[1].astype(object) * pq % qe[:l]
+        return r
+
+    def rot_qp(c, s):
+        """rotation by s kept in Q_l P: Auto(<ModUp(c1), evk> + (P c0, 0)), or (P c0, P c1) for s = 0"""
+        if s == 0:
+            return lift(c, True)
+        acc = octx5.ks_inner(octx5.modup(c[1], l), l, evk[s]).astype(object)
+        v = ((acc + lift(c, False)) % qe[None]).astype(np.uint64)
+        return octx5.automorph_eval(v, octx5.rot_index(s)).astype(object)
+
+    babies = [rot_qp(xs[i], s) for i in range(n_in) for s in bst]
+    for o in range(n_out):
+        T = np.zeros((2, E, N), dtype=object)
+        for g in range(ng):
+            S = sum(babies[j] * diags[o, g, j].astype(object)[None] for j in range(n_in * nb))
+            S = (S % qe[None]).astype(np.uint64)
+            SQ = np.stack([octx5.moddown(S[p], l) for p in range(2)])
+            T += rot_qp(SQ, gst[g])
+        T = (T % qe[None]).astype(np.uint64)
+        want = octx5.rescale(np.stack([octx5.moddown(T[p], l) for p in range(2)]), l)
+        assert np.array_equal(got[o], want), o
+
+
 @pytest.fixture(scope="module")
 def engine(ckks, DS):
     be, sk = DS.build_engine(ckks)
