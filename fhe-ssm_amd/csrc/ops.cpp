@@ -60,7 +60,7 @@ hipError_t launch_automorph_list(const Context& ctx, const uint64_t* in, uint64_
                                  const uint32_t* g, hipStream_t st);
 hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* const* baby, const uint64_t* diag, uint64_t* out,
                            uint32_t nb, uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st,
-                           uint32_t l_q = 0);
+                           uint32_t l_q = 0, uint32_t n_inst = 1, uint64_t inst_stride = 0, uint64_t out_stride = 0);
 hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
                              uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_out,
                              uint32_t nt, uint32_t A, uint32_t M, uint32_t l, const TwPair* pmod, uint64_t* dst,
@@ -840,13 +840,11 @@ void bsgs_dh_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uin
     }
     // inner sums in Q_l P: S [n_inst][n_out][ng][2][E][N]
     uint64_t* S = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)n_o * ng * cte * 8);
+    // baby j = i nb + b of instance s at BQ + (s nbt + j) cte: one MAC launch for every instance
     std::vector<const uint64_t*> bp(nbt);
-    for (uint32_t s = 0; s < n_inst; s++) {
-        for (uint32_t i = 0; i < n_in; i++)
-            for (uint32_t b = 0; b < nb; b++) bp[i * nb + b] = BQ + (((size_t)(s * n_in + i)) * nb + b) * cte;
-        HIPX(launch_bsgs_mac(ctx, bp.data(), diags_qp, S + (size_t)s * n_out * ng * cte, nbt, nbt * n_out * ng,
-                             n_out * ng, E, 0, st, l));
-    }
+    for (uint32_t j = 0; j < nbt; j++) bp[j] = BQ + (size_t)j * cte;
+    HIPX(launch_bsgs_mac(ctx, bp.data(), diags_qp, S, nbt, nbt * n_out * ng, n_out * ng, E, 0, st, l, n_inst,
+                         (uint64_t)nbt * cte, (uint64_t)n_out * ng * cte));
     // every inner sum down to Q_l once (its rotation needs c1 in Q_l): SQ [n_o][ng][2][l][N]
     uint64_t* SQ = (uint64_t*)ws_get(ctx, WS_SUM, (size_t)n_o * ng * ctw * 8);
     moddown_inplace(ctx, S, 2 * n_o * ng, l, nullptr, SQ, st);

@@ -373,10 +373,11 @@ struct ListTile {
     uint32_t item, kt, limb;
 };
 
-__device__ __forceinline__ ListTile list_tile(uint32_t m) {
+// tiles_per_limb coefficient tiles per limb (kN / 256 for 256-thread tiles)
+__device__ __forceinline__ ListTile list_tile(uint32_t m, uint32_t tiles_per_limb = kN / 256) {
     const uint32_t n = blockIdx.x, q = n >> 3;
     const uint32_t tile = (q / m) * 8 + (n & 7);
-    return ListTile{q % m, tile % (kN / 256), tile / (kN / 256)};
+    return ListTile{q % m, tile % tiles_per_limb, tile / tiles_per_limb};
 }
 
 __global__ __launch_bounds__(256) void k_ks_inner_list(ListPtrs ext, ListPtrs evk, uint64_t* __restrict__ acc,
@@ -552,7 +553,7 @@ __global__ __launch_bounds__(256) void k_automorph_list(const uint64_t* __restri
 // the bit-reversed index by an odd g), so the gathers stay coalesced.
 struct QpRotArgs {
     uint32_t l, E, L, D, T, nt, A, M;
-    uint32_t R, c_off;
+    uint32_t n_out, R, c_off;
     uint64_t ext_stride, src_stride, s_hi, s_lo;
     const uint64_t* evk[kMaxList];
     uint32_t g[kMaxList];
@@ -562,8 +563,9 @@ struct QpRotArgs {
 __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__ ext,
                                                     const uint64_t* __restrict__ src, uint64_t* __restrict__ dst,
                                                     QpRotArgs a, const PrimeInfo* __restrict__ primes) {
-    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
-    const uint32_t t = blockIdx.y, c = blockIdx.z;
+    const ListTile lt = list_tile(a.n_out);  // outputs of one tile on one XCD: their ext and evk words meet in L2
+    const uint32_t k = lt.kt * 256 + threadIdx.x;
+    const uint32_t t = lt.limb, c = lt.item;
     const bool qlimb = t < a.l;
     const uint32_t pi = qlimb ? t : a.L + (t - a.l);
     const Barrett br = barrett_of(primes[pi]);
@@ -617,6 +619,9 @@ constexpr int kMacRows = 8;
 // Babies j0 .. j0 + nb - 1 of a list of nb_total are taken, each a ciphertext [2][l][N] anywhere in memory (baby.p,
 // so the rotated babies are read where the rotations wrote them; diagonal g * nb_total + j, zero from n_diag on);
 // acc != 0 adds the result to what out holds (the MAC over more babies than fit in LDS runs in baby chunks).
+// n_inst instances share the diagonals: instance s takes its babies at baby.p[j] + s inst_stride and writes
+// out + s out_stride; the instances of one (coefficient tile, limb) run on one XCD (list_tile), so each diagonal
+// word is fetched from HBM once for all of them.
 // A wave row takes two giant steps at a time: four independent accumulation chains per thread, and every
 // baby word read from LDS feeds two products.
 __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(ListPtrs baby,
@@ -625,16 +630,21 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(ListPtrs baby,
                                                                   uint32_t nb_total, uint32_t j0, uint32_t ng,
                                                                   uint32_t n_diag, uint32_t l, uint32_t log_rep,
                                                                   uint32_t acc, uint32_t l_q, uint32_t Lp,
+                                                                  uint32_t n_inst, uint64_t inst_stride,
+                                                                  uint64_t out_stride,
                                                                   const PrimeInfo* __restrict__ primes) {
     extern __shared__ uint64_t sb[];
+    const ListTile lt = list_tile(n_inst, kN / kMacCoef);
     const uint32_t kk = threadIdx.x & (kMacCoef - 1), row = threadIdx.x / kMacCoef;
-    const uint32_t k = blockIdx.x * kMacCoef + kk;
-    const uint32_t i = blockIdx.y;  // limb; limbs from l_q on are P limbs (prime Lp + i - l_q)
+    const uint32_t k = lt.kt * kMacCoef + kk;
+    const uint32_t i = lt.limb;  // limb; limbs from l_q on are P limbs (prime Lp + i - l_q)
     const Barrett br = barrett_of(primes[i < l_q ? i : Lp + (i - l_q)]);
     const size_t P = (size_t)l * kN, off = (size_t)i * kN + k;
+    const size_t so = (size_t)lt.item * inst_stride;
+    out += (size_t)lt.item * out_stride;
     for (uint32_t jp = row; jp < 2 * nb; jp += kMacRows) {  // jp = 2 j + poly; baby j of this chunk at baby.p[j]
         const uint32_t j = jp >> 1, p = jp & 1;
-        sb[jp * kMacCoef + kk] = baby.p[j][p * P + off];
+        sb[jp * kMacCoef + kk] = baby.p[j][so + p * P + off];
     }
     __syncthreads();
     const size_t Pd = (size_t)l * (kN >> log_rep), dk = (size_t)i * (kN >> log_rep) + (k >> log_rep);
@@ -987,18 +997,19 @@ hipError_t launch_automorph_list(const Context& ctx, const uint64_t* in, uint64_
 // l limbs per poly; with l_q < l the limbs from l_q on are the P limbs (an extended-basis MAC)
 hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* const* baby, const uint64_t* diag, uint64_t* out,
                            uint32_t nb, uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st,
-                           uint32_t l_q) {
+                           uint32_t l_q, uint32_t n_inst, uint64_t inst_stride, uint64_t out_stride) {
     if (l_q == 0 || l_q > l) l_q = l;
-    if (nb == 0 || log_rep > 6 || n_diag > nb * ng) return hipErrorInvalidValue;
-    const double bytes = ((double)nb * 2 * l + (double)n_diag * l / (1u << log_rep) + (double)ng * 2 * l) * kN * 8;
+    if (nb == 0 || log_rep > 6 || n_diag > nb * ng || n_inst == 0 || n_inst > 4096) return hipErrorInvalidValue;
+    const double bytes =
+        ((double)n_inst * (nb * 2 * l + ng * 2 * l) + (double)n_diag * l / (1u << log_rep)) * kN * 8;
     const int pi = prof_begin(ctx, log_rep ? "bsgs_mac_periodic" : "bsgs_mac", bytes, st);
     for (uint32_t j0 = 0; j0 < nb; j0 += kMaxBaby) {
         const uint32_t nbc = std::min<uint32_t>(kMaxBaby, nb - j0);
         ListPtrs bp{};
         for (uint32_t j = 0; j < nbc; j++) bp.p[j] = baby[j0 + j];
-        hipLaunchKernelGGL(k_bsgs_mac, dim3(kN / kMacCoef, l), dim3(kMacCoef * kMacRows),
+        hipLaunchKernelGGL(k_bsgs_mac, dim3(n_inst * (kN / kMacCoef) * l), dim3(kMacCoef * kMacRows),
                            (size_t)nbc * 2 * kMacCoef * 8, st, bp, diag, out, nbc, nb, j0, ng, n_diag, l, log_rep,
-                           j0 ? 1u : 0u, l_q, ctx.L, ctx.d_primes);
+                           j0 ? 1u : 0u, l_q, ctx.L, n_inst, inst_stride, out_stride, ctx.d_primes);
     }
     prof_end(ctx, pi, st);
     return hipGetLastError();
@@ -1067,7 +1078,7 @@ hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t e
                              uint32_t nt, uint32_t A, uint32_t M, uint32_t l, const TwPair* pmod, uint64_t* dst,
                              hipStream_t st, uint32_t R, uint32_t c_off, uint64_t s_lo) {
     const uint32_t E = l + ctx.K;
-    if (n_out == 0 || nt == 0 || A == 0 || A + nt - 1 > (uint32_t)kMaxList || E > kMaxPmap || n_out > 65535)
+    if (n_out == 0 || nt == 0 || A == 0 || A + nt - 1 > (uint32_t)kMaxList || E > kMaxPmap || n_out > 4096)
         return hipErrorInvalidValue;
     const uint32_t D = (l + ctx.alpha - 1) / ctx.alpha;
     if (D > (uint32_t)kMaxDigits) return hipErrorInvalidValue;
@@ -1082,6 +1093,7 @@ hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t e
     a.M = M;
     a.ext_stride = ext_stride;
     a.src_stride = src_stride;
+    a.n_out = n_out;
     a.R = R ? R : 1;
     a.c_off = c_off;
     a.s_hi = (uint64_t)2 * E * kN;
@@ -1100,7 +1112,7 @@ hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t e
                       (double)n_out * 2 * E;
     ctx.n_keyswitch += n_ks * (uint64_t)(n_out / A);
     const int pi = prof_begin(ctx, "qp_rot_sum", by * kN * 8, st);
-    hipLaunchKernelGGL(k_qp_rot_sum, dim3(kN / 256, E, n_out), dim3(256), 0, st, ext, src, dst, a, ctx.d_primes);
+    hipLaunchKernelGGL(k_qp_rot_sum, dim3(n_out * (kN / 256) * E), dim3(256), 0, st, ext, src, dst, a, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
