@@ -185,13 +185,20 @@ BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scal
     auto add_level = [&](std::vector<BootLevel>& dst, const Diags& D, int s_lo, uint32_t l, double pt_scale,
                          bool split) {
         const long delta = 1L << (s_lo - 1);
+        // The level's diagonals sit at offsets k delta, |k| <= 31.  When the slot count n is at most 63 delta,
+        // offsets k and k - n / delta are the same rotation: those diagonals are summed, leaving n / delta of them
+        // at k in [0, n / delta).  Otherwise k is taken in [-32, 32).  Babies are b delta (b < nb, b = 0 the
+        // identity), giants (lo + g nb) delta, one of them 0.
+        const long n_rot = (long)kSlots / delta;
+        const bool wrap = n_rot <= 63;
+        const long lo = wrap ? 0 : -32, span = wrap ? n_rot : 64;
         BootLevel bl;
         bl.l = l;
-        bl.nb = 8;
-        bl.ng = 8;
+        bl.nb = (uint32_t)std::min<long>(16, span);
+        bl.ng = (uint32_t)(span / bl.nb);
         bl.n_in = bl.n_out = split ? 2 : 1;
         for (uint32_t b = 0; b < bl.nb; b++) bl.bsteps.push_back((int64_t)b * delta);
-        for (uint32_t g = 0; g < bl.ng; g++) bl.gsteps.push_back(((int64_t)g * bl.nb - 31) * delta);
+        for (uint32_t g = 0; g < bl.ng; g++) bl.gsteps.push_back((lo + (int64_t)g * bl.nb) * delta);
         // the levels run double-hoisted: their diagonals are encoded over Q_l * P
         std::vector<uint32_t> pmap;
         for (uint32_t i = 0; i < l; i++) pmap.push_back(i);
@@ -209,15 +216,21 @@ BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scal
             const size_t t = ((size_t)o * bl.ng + g) * bl.n_in * bl.nb + j;
             encode_primes(ctx, re.data(), im.data(), kSlots, pmap, pt_scale, bl.d_diags + t * E * W);
         };
-        std::vector<cd> dr(kSlots), tmp(kSlots);
+        std::map<long, std::vector<cd>> folded;  // k - lo -> diagonal
         for (auto& [off, d] : D) {
             if (off % delta) throw std::logic_error("unexpected diagonal offset");
-            const long k = off / delta;
+            long k = off / delta;
             if (k < -31 || k > 31) throw std::logic_error("diagonal offset out of range");
+            if (wrap) k = ((k % n_rot) + n_rot) % n_rot;
+            auto& f = folded[k - lo];
+            if (f.empty()) f.assign(kSlots, cd(0.0));
+            for (uint32_t s = 0; s < kSlots; s++) f[s] += d[s];
+        }
+        std::vector<cd> dr(kSlots), tmp(kSlots);
+        for (auto& [kp, d] : folded) {
             bool nz = false;
             for (auto& v : d) nz |= std::abs(v) > 0;
             if (!nz) continue;
-            const long kp = k + 31;
             const uint32_t g = (uint32_t)(kp / bl.nb), b = (uint32_t)(kp % bl.nb);
             const long G = bl.gsteps[g];
             // term (g, b) is pre-rotated by -G: d'[s] = d[(s - G) mod n]
