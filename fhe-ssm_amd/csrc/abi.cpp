@@ -589,7 +589,7 @@ int ckks_linear_transform_hoisted(ckks_context* ctx, const uint64_t* const* d_in
     if (int rc = check_ctx_level(ctx, level, true)) return rc;
     if (!d_in || !d_diags || !d_out || !baby_steps || !giant_steps || !d_baby_evks || !d_giant_evks)
         return fail(CKKS_EINVAL, "null argument");
-    if (n_in == 0 || n_out == 0 || n_baby == 0 || n_baby > 64 || n_in * n_baby > 256 || n_giant == 0 ||
+    if (n_in == 0 || n_out == 0 || n_baby == 0 || n_baby > 32 || n_in * n_baby > 64 || n_giant == 0 ||
         n_giant > 64)
         return fail(CKKS_EINVAL, "bad BSGS shape");
     if (level < 2) return fail(CKKS_EINVAL, "rescale needs level >= 2");

@@ -61,6 +61,10 @@ hipError_t launch_automorph_list(const Context& ctx, const uint64_t* in, uint64_
 hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* const* baby, const uint64_t* diag, uint64_t* out,
                            uint32_t nb, uint32_t n_diag, uint32_t ng, uint32_t l, uint32_t log_rep, hipStream_t st,
                            uint32_t l_q = 0, uint32_t n_inst = 1, uint64_t inst_stride = 0, uint64_t out_stride = 0);
+hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
+                              uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_inst,
+                              uint32_t n_in, uint32_t nb, const uint64_t* diag, uint32_t n_diag, uint32_t ng,
+                              uint32_t l, const TwPair* pmod, uint64_t* out, hipStream_t st);
 hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
                              uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_out,
                              uint32_t nt, uint32_t A, uint32_t M, uint32_t l, const TwPair* pmod, uint64_t* dst,
@@ -801,14 +805,16 @@ void bsgs_multi_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, 
 // diagonals -- encoded over Q_l * P, diags [n_out][ng][n_in nb][l + K][N] -- multiply them there, each giant's
 // inner sum is brought down once, rotated by the giant step again without its ModDown, and the giant sums are
 // brought down and rescaled together: ng + 1 ModDowns per output instead of (nb - 1) + ng.
-// out [n_inst][n_out][2][l-1][N] (by_output: [n_out][n_inst]).  The babies' key switches and automorphisms, and
-// the giants' with their sum, each run as one kernel (k_qp_rot_sum) that stores only the rotated result.
+// out [n_inst][n_out][2][l-1][N] (by_output: [n_out][n_inst]).  The babies are formed inside the MAC kernel
+// (k_bsgs_dh_mac: key switch and automorphism in LDS, never stored); the giants' key switches, automorphisms and
+// sum run as one kernel (k_qp_rot_sum).  nb <= 32, n_in nb <= 64.
 void bsgs_dh_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uint32_t n_in, uint32_t l,
                    const uint64_t* diags_qp, uint32_t nb, const int64_t* bsteps, const uint64_t* const* bevk,
                    uint32_t ng, const int64_t* gsteps, const uint64_t* const* gevk, uint32_t n_out, uint64_t* out,
                    hipStream_t st, bool by_output) {
     check_level(ctx, l);
-    if (nb == 0 || nb > 64 || n_in == 0 || n_out == 0 || ng == 0 || ng > 64 || n_inst == 0 || l < 2)
+    if (nb == 0 || nb > 32 || n_in * nb > 64 || n_in == 0 || n_out == 0 || ng == 0 || ng > 64 || n_inst == 0 ||
+        l < 2)
         throw std::invalid_argument("bad BSGS shape");
     const uint32_t E = l + ctx.K, D = num_digits(ctx, l), K = ctx.K;
     const size_t ctw = (size_t)2 * l * W, cte = (size_t)2 * E * W, exw = (size_t)D * E * W;
@@ -831,20 +837,14 @@ void bsgs_dh_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uin
     }
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT2, (size_t)n_x * exw * 8);
     modup(ctx, X + (size_t)l * W, ext, n_x, l, st, ctw);
-    // babies in Q_l P, BQ [n_x][nb][2][E][N]: output x nb + b is term 0 of input x with key b
-    uint64_t* BQ = (uint64_t*)ws_get(ctx, WS_BABY, (size_t)n_x * nb * cte * 8);
+    // inner sums in Q_l P, S [n_inst][n_out][ng][2][E][N], with the babies formed inside the MAC (never stored)
+    uint64_t* S = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)n_o * ng * cte * 8);
     {
         std::vector<uint32_t> g(nb);
         for (uint32_t b = 0; b < nb; b++) g[b] = bsteps[b] ? rotation_index(bsteps[b]) : 1;
-        HIPX(launch_qp_rot_sum(ctx, ext, exw, X, ctw, bevk, g.data(), n_x * nb, 1, nb, 1, l, pmod.data(), BQ, st));
+        HIPX(launch_bsgs_dh_mac(ctx, ext, exw, X, ctw, bevk, g.data(), n_inst, n_in, nb, diags_qp, nbt * n_out * ng,
+                                n_out * ng, l, pmod.data(), S, st));
     }
-    // inner sums in Q_l P: S [n_inst][n_out][ng][2][E][N]
-    uint64_t* S = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)n_o * ng * cte * 8);
-    // baby j = i nb + b of instance s at BQ + (s nbt + j) cte: one MAC launch for every instance
-    std::vector<const uint64_t*> bp(nbt);
-    for (uint32_t j = 0; j < nbt; j++) bp[j] = BQ + (size_t)j * cte;
-    HIPX(launch_bsgs_mac(ctx, bp.data(), diags_qp, S, nbt, nbt * n_out * ng, n_out * ng, E, 0, st, l, n_inst,
-                         (uint64_t)nbt * cte, (uint64_t)n_out * ng * cte));
     // every inner sum down to Q_l once (its rotation needs c1 in Q_l): SQ [n_o][ng][2][l][N]
     uint64_t* SQ = (uint64_t*)ws_get(ctx, WS_SUM, (size_t)n_o * ng * ctw * 8);
     moddown_inplace(ctx, S, 2 * n_o * ng, l, nullptr, SQ, st);

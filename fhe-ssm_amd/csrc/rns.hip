@@ -614,41 +614,15 @@ constexpr int kMaxBaby = 64;
 constexpr int kMacCoef = 64;
 constexpr int kMacRows = 8;
 
-// log_rep > 0: the diagonals are compressed periodic plaintexts, [n_diag][l][N >> log_rep], whose
-// evaluation-form word k is comp[k >> log_rep] (the reference's store expansion, gpu_real_model.cu:145-155).
-// Babies j0 .. j0 + nb - 1 of a list of nb_total are taken, each a ciphertext [2][l][N] anywhere in memory (baby.p,
-// so the rotated babies are read where the rotations wrote them; diagonal g * nb_total + j, zero from n_diag on);
-// acc != 0 adds the result to what out holds (the MAC over more babies than fit in LDS runs in baby chunks).
-// n_inst instances share the diagonals: instance s takes its babies at baby.p[j] + s inst_stride and writes
-// out + s out_stride; the instances of one (coefficient tile, limb) run on one XCD (list_tile), so each diagonal
-// word is fetched from HBM once for all of them.
-// A wave row takes two giant steps at a time: four independent accumulation chains per thread, and every
-// baby word read from LDS feeds two products.
-__global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(ListPtrs baby,
-                                                                  const uint64_t* __restrict__ diag,
-                                                                  uint64_t* __restrict__ out, uint32_t nb,
-                                                                  uint32_t nb_total, uint32_t j0, uint32_t ng,
-                                                                  uint32_t n_diag, uint32_t l, uint32_t log_rep,
-                                                                  uint32_t acc, uint32_t l_q, uint32_t Lp,
-                                                                  uint32_t n_inst, uint64_t inst_stride,
-                                                                  uint64_t out_stride,
-                                                                  const PrimeInfo* __restrict__ primes) {
-    extern __shared__ uint64_t sb[];
-    const ListTile lt = list_tile(n_inst, kN / kMacCoef);
-    const uint32_t kk = threadIdx.x & (kMacCoef - 1), row = threadIdx.x / kMacCoef;
-    const uint32_t k = lt.kt * kMacCoef + kk;
-    const uint32_t i = lt.limb;  // limb; limbs from l_q on are P limbs (prime Lp + i - l_q)
-    const Barrett br = barrett_of(primes[i < l_q ? i : Lp + (i - l_q)]);
-    const size_t P = (size_t)l * kN, off = (size_t)i * kN + k;
-    const size_t so = (size_t)lt.item * inst_stride;
-    out += (size_t)lt.item * out_stride;
-    for (uint32_t jp = row; jp < 2 * nb; jp += kMacRows) {  // jp = 2 j + poly; baby j of this chunk at baby.p[j]
-        const uint32_t j = jp >> 1, p = jp & 1;
-        sb[jp * kMacCoef + kk] = baby.p[j][so + p * P + off];
-    }
-    __syncthreads();
-    const size_t Pd = (size_t)l * (kN >> log_rep), dk = (size_t)i * (kN >> log_rep) + (k >> log_rep);
-    // diagonals past n_diag (a short last giant step) are zero: the baby count of giant g
+// The giant sums of a BSGS MAC from babies staged in LDS (sb: word kk of baby j, poly p at (2 j + p) kMacCoef + kk):
+// out_g = sum_j baby_j (.) diag[g nb_total + j0 + j] for g < ng (out [ng][2][P], diagonals Pd words apart, this
+// thread's word at dk in a diagonal and off in an output poly).  Diagonals past n_diag (a short last giant step) are
+// zero; acc != 0 adds to what out holds.  A wave row takes two giant steps at a time: four independent accumulation
+// chains per thread, and every baby word read from LDS feeds two products.
+__device__ __forceinline__ void mac_giants(const uint64_t* sb, const uint64_t* __restrict__ diag,
+                                           uint64_t* __restrict__ out, uint32_t nb, uint32_t nb_total, uint32_t j0,
+                                           uint32_t ng, uint32_t n_diag, size_t P, size_t Pd, size_t dk, size_t off,
+                                           uint32_t acc, const Barrett& br, uint32_t kk, uint32_t row) {
     auto count = [&](uint32_t g) {
         const int64_t rem = (int64_t)n_diag - (int64_t)g * nb_total - j0;
         return rem <= 0 ? 0u : (uint32_t)min<int64_t>(rem, nb);
@@ -695,6 +669,106 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(ListPtrs baby,
         store(g, a0, a1);
         if (g2 < ng) store(g2, b0, b1);
     }
+}
+
+// log_rep > 0: the diagonals are compressed periodic plaintexts, [n_diag][l][N >> log_rep], whose
+// evaluation-form word k is comp[k >> log_rep] (the reference's store expansion, gpu_real_model.cu:145-155).
+// Babies j0 .. j0 + nb - 1 of a list of nb_total are taken, each a ciphertext [2][l][N] anywhere in memory (baby.p,
+// so the rotated babies are read where the rotations wrote them; diagonal g * nb_total + j, zero from n_diag on);
+// acc != 0 adds the result to what out holds (the MAC over more babies than fit in LDS runs in baby chunks).
+// n_inst instances share the diagonals: instance s takes its babies at baby.p[j] + s inst_stride and writes
+// out + s out_stride; the instances of one (coefficient tile, limb) run on one XCD (list_tile), so each diagonal
+// word is fetched from HBM once for all of them.
+__global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(ListPtrs baby,
+                                                                  const uint64_t* __restrict__ diag,
+                                                                  uint64_t* __restrict__ out, uint32_t nb,
+                                                                  uint32_t nb_total, uint32_t j0, uint32_t ng,
+                                                                  uint32_t n_diag, uint32_t l, uint32_t log_rep,
+                                                                  uint32_t acc, uint32_t l_q, uint32_t Lp,
+                                                                  uint32_t n_inst, uint64_t inst_stride,
+                                                                  uint64_t out_stride,
+                                                                  const PrimeInfo* __restrict__ primes) {
+    extern __shared__ uint64_t sb[];
+    const ListTile lt = list_tile(n_inst, kN / kMacCoef);
+    const uint32_t kk = threadIdx.x & (kMacCoef - 1), row = threadIdx.x / kMacCoef;
+    const uint32_t k = lt.kt * kMacCoef + kk;
+    const uint32_t i = lt.limb;  // limb; limbs from l_q on are P limbs (prime Lp + i - l_q)
+    const Barrett br = barrett_of(primes[i < l_q ? i : Lp + (i - l_q)]);
+    const size_t P = (size_t)l * kN, off = (size_t)i * kN + k;
+    const size_t so = (size_t)lt.item * inst_stride;
+    out += (size_t)lt.item * out_stride;
+    for (uint32_t jp = row; jp < 2 * nb; jp += kMacRows) {  // jp = 2 j + poly; baby j of this chunk at baby.p[j]
+        const uint32_t j = jp >> 1, p = jp & 1;
+        sb[jp * kMacCoef + kk] = baby.p[j][so + p * P + off];
+    }
+    __syncthreads();
+    mac_giants(sb, diag, out, nb, nb_total, j0, ng, n_diag, P, (size_t)l * (kN >> log_rep),
+               (size_t)i * (kN >> log_rep) + (k >> log_rep), off, acc, br, kk, row);
+}
+
+// Double-hoisted BSGS MAC: the babies are formed in LDS from the inputs' ModUp extensions and never stored.  Over
+// Q_l * P (E limbs), baby j = i nb + b of instance s is the rotation of input x = s n_in + i by baby step b kept in
+// the extended basis (see k_qp_rot_sum): Auto_b(<ext_x, evk_b> + (P c0_x, 0)), or (P c0_x, P c1_x) for b's
+// identity step; then out_s [ng][2][E][N] = sum_j baby_j (.) diag[g nbt + j] as in k_bsgs_mac (diagonals
+// [n_diag][E][N], shared by the instances, whose workgroups of one tile run on one XCD).
+constexpr int kMaxDhBaby = 32;
+struct DhMacArgs {
+    uint32_t l, E, L, D, T;          // Q limbs, extended limbs, first P prime, digits, evk limbs per poly
+    uint32_t n_in, nb, ng, n_diag, n_inst;
+    uint64_t ext_stride, src_stride;  // per input x
+    uint64_t out_stride;              // per instance
+    const uint64_t* evk[kMaxDhBaby];  // per baby step (null: the identity)
+    uint32_t g[kMaxDhBaby];
+    TwPair pmod[kMaxPmap];            // P mod q_t, t < l
+};
+
+__global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64_t* __restrict__ ext,
+                                                                     const uint64_t* __restrict__ src,
+                                                                     const uint64_t* __restrict__ diag,
+                                                                     uint64_t* __restrict__ out, DhMacArgs a,
+                                                                     const PrimeInfo* __restrict__ primes) {
+    extern __shared__ uint64_t sb[];
+    const ListTile lt = list_tile(a.n_inst, kN / kMacCoef);
+    const uint32_t kk = threadIdx.x & (kMacCoef - 1), row = threadIdx.x / kMacCoef;
+    const uint32_t k = lt.kt * kMacCoef + kk, t = lt.limb, s = lt.item;
+    const bool qlimb = t < a.l;
+    const uint32_t pi = qlimb ? t : a.L + (t - a.l);
+    const Barrett br = barrett_of(primes[pi]);
+    const uint64_t q = br.q;
+    const uint32_t nbt = a.n_in * a.nb;
+    for (uint32_t j = row; j < nbt; j += kMacRows) {
+        const uint32_t i = j / a.nb, b = j - i * a.nb, x = s * a.n_in + i;
+        const uint32_t g = a.g[b];
+        const uint32_t e = (uint32_t)(((uint64_t)g * (2u * (__brev(k) >> (32 - kLogN)) + 1u)) & (2u * kN - 1u));
+        const uint32_t sw = __brev((e - 1u) >> 1) >> (32 - kLogN);
+        const uint64_t* sx = src + (size_t)x * a.src_stride + (size_t)t * kN + sw;
+        const uint64_t* ek = a.evk[b];
+        uint64_t v0 = 0, v1 = 0;
+        if (ek) {
+            const uint64_t* xe = ext + (size_t)x * a.ext_stride + (size_t)t * kN + sw;
+            const uint64_t* ep = ek + (size_t)pi * kN + sw;
+            Acc s0, s1;  // at most kMaxDigits = 8 terms
+#pragma unroll
+            for (int d = 0; d < kMaxDigits; d++) {
+                if (d < (int)a.D) {
+                    const uint64_t v = xe[(size_t)d * a.E * kN];
+                    s0.add(v, ep[((size_t)d * 2 + 0) * a.T * kN]);
+                    s1.add(v, ep[((size_t)d * 2 + 1) * a.T * kN]);
+                }
+            }
+            v0 = reduce_u128(s0.get(), br);
+            if (qlimb) v0 = add_mod(v0, shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q), q);
+            v1 = reduce_u128(s1.get(), br);
+        } else if (qlimb) {
+            v0 = shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q);
+            v1 = shoup(sx[(size_t)a.l * kN], a.pmod[t].w, a.pmod[t].wp, q);
+        }
+        sb[(2 * j) * kMacCoef + kk] = v0;
+        sb[(2 * j + 1) * kMacCoef + kk] = v1;
+    }
+    __syncthreads();
+    const size_t P = (size_t)a.E * kN, off = (size_t)t * kN + k;
+    mac_giants(sb, diag, out + (size_t)s * a.out_stride, nbt, nbt, 0, a.ng, a.n_diag, P, P, off, off, 0, br, kk, row);
 }
 
 // Masked pairs: out[s][t] = pt[s][t][0] (.) R[t] + pt[s][t][1] (.) R[n + t] on both polys, with
@@ -1011,6 +1085,49 @@ hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* const* baby, cons
                            (size_t)nbc * 2 * kMacCoef * 8, st, bp, diag, out, nbc, nb, j0, ng, n_diag, l, log_rep,
                            j0 ? 1u : 0u, l_q, ctx.L, n_inst, inst_stride, out_stride, ctx.d_primes);
     }
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
+// babies b < nb (keys[b] null: identity; g[b] its automorphism) of n_in inputs per instance, n_inst instances:
+// ext [n_inst n_in] extensions ext_stride apart, src the inputs src_stride apart; out [n_inst][ng][2][E][N]
+hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
+                              uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_inst,
+                              uint32_t n_in, uint32_t nb, const uint64_t* diag, uint32_t n_diag, uint32_t ng,
+                              uint32_t l, const TwPair* pmod, uint64_t* out, hipStream_t st) {
+    const uint32_t E = l + ctx.K, D = (l + ctx.alpha - 1) / ctx.alpha;
+    if (n_inst == 0 || n_inst > 4096 || nb == 0 || nb > (uint32_t)kMaxDhBaby || n_in * nb > (uint32_t)kMaxBaby ||
+        n_diag > n_in * nb * ng || E > kMaxPmap || D > (uint32_t)kMaxDigits)
+        return hipErrorInvalidValue;
+    DhMacArgs a{};
+    a.l = l;
+    a.E = E;
+    a.L = ctx.L;
+    a.D = D;
+    a.T = ctx.L + ctx.K;
+    a.n_in = n_in;
+    a.nb = nb;
+    a.ng = ng;
+    a.n_diag = n_diag;
+    a.n_inst = n_inst;
+    a.ext_stride = ext_stride;
+    a.src_stride = src_stride;
+    a.out_stride = (uint64_t)ng * 2 * E * kN;
+    uint32_t n_ks = 0;
+    for (uint32_t b = 0; b < nb; b++) {
+        a.evk[b] = keys[b];
+        a.g[b] = g[b];
+        n_ks += keys[b] ? 1 : 0;
+    }
+    for (uint32_t t = 0; t < l; t++) a.pmod[t] = pmod[t];
+    ctx.n_keyswitch += (uint64_t)n_ks * n_inst * n_in;
+    // bytes: each input's extension and c0 (read once per key-switched baby: different automorphism blocks), the
+    // keys and diagonals once, the giant sums written
+    const double by = (double)n_inst * n_in * (n_ks * ((double)D * E + l) + (nb - n_ks) * 2.0 * l) +
+                      (double)n_ks * 2 * D * E + (double)n_diag * E + (double)n_inst * ng * 2 * E;
+    const int pi = prof_begin(ctx, "bsgs_dh_mac", by * kN * 8, st);
+    hipLaunchKernelGGL(k_bsgs_dh_mac, dim3(n_inst * (kN / kMacCoef) * E), dim3(kMacCoef * kMacRows),
+                       (size_t)n_in * nb * 2 * kMacCoef * 8, st, ext, src, diag, out, a, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
