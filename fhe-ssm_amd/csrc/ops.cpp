@@ -63,12 +63,14 @@ hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* const* baby, cons
                            uint32_t l_q = 0, uint32_t n_inst = 1, uint64_t inst_stride = 0, uint64_t out_stride = 0);
 hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
                               uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_inst,
-                              uint32_t n_in, uint32_t nb, const uint64_t* diag, uint32_t n_diag, uint32_t ng,
-                              uint32_t l, const TwPair* pmod, uint64_t* out, hipStream_t st);
+                              uint32_t n_in, uint32_t nb, const uint64_t* diag, uint32_t n_diag, uint32_t n_out,
+                              uint32_t ngp, int32_t g0, uint32_t l, const TwPair* pmod, uint64_t* out,
+                              uint64_t* id_out, uint64_t id_inst_stride, uint64_t id_stride, hipStream_t st);
 hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
                              uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_out,
                              uint32_t nt, uint32_t A, uint32_t M, uint32_t l, const TwPair* pmod, uint64_t* dst,
-                             hipStream_t st, uint32_t R = 1, uint32_t c_off = 0, uint64_t s_lo = 0);
+                             hipStream_t st, uint32_t R = 1, uint32_t c_off = 0, uint64_t s_lo = 0,
+                             bool accumulate = false);
 hipError_t launch_mul_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
                             uint32_t l, uint64_t pt_bstride, uint32_t log_rep, hipStream_t st);
 hipError_t launch_add_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
@@ -837,39 +839,49 @@ void bsgs_dh_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uin
     }
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT2, (size_t)n_x * exw * 8);
     modup(ctx, X + (size_t)l * W, ext, n_x, l, st, ctw);
-    // inner sums in Q_l P, S [n_inst][n_out][ng][2][E][N], with the babies formed inside the MAC (never stored)
-    uint64_t* S = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)n_o * ng * cte * 8);
+    // giant sums T [n_o][2][E][N] in Q_l P (by_output: output o of instance s at slot o n_inst + s).  The MAC forms
+    // the babies itself (never stored) and writes the inner sum of the identity giant step (if any) straight into T;
+    // the other inner sums, S [n_inst][n_out][ngr][2][E][N], go down to Q_l once (the giant rotation needs c1 in
+    // Q_l) and come back rotated in Q_l P, added to T.
+    int32_t g0 = -1;
+    std::vector<const uint64_t*> rk;
+    std::vector<uint32_t> rg;
+    for (uint32_t g = 0; g < ng; g++) {
+        if (gsteps[g] == 0 && g0 < 0) {
+            g0 = (int32_t)g;
+            continue;
+        }
+        rk.push_back(gsteps[g] ? gevk[g] : nullptr);
+        rg.push_back(gsteps[g] ? rotation_index(gsteps[g]) : 1);
+    }
+    const uint32_t ngr = (uint32_t)rk.size();
+    uint64_t* T = (uint64_t*)ws_get(ctx, WS_GROT, (size_t)n_o * cte * 8);
+    uint64_t* S = ngr ? (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)n_o * ngr * cte * 8) : nullptr;
     {
         std::vector<uint32_t> g(nb);
         for (uint32_t b = 0; b < nb; b++) g[b] = bsteps[b] ? rotation_index(bsteps[b]) : 1;
+        const uint64_t id_inst = by_output ? cte : (uint64_t)n_out * cte, id_o = by_output ? (uint64_t)n_inst * cte : cte;
         HIPX(launch_bsgs_dh_mac(ctx, ext, exw, X, ctw, bevk, g.data(), n_inst, n_in, nb, diags_qp, nbt * n_out * ng,
-                                n_out * ng, l, pmod.data(), S, st));
+                                n_out, ng, g0, l, pmod.data(), S, T, id_inst, id_o, st));
     }
-    // every inner sum down to Q_l once (its rotation needs c1 in Q_l): SQ [n_o][ng][2][l][N]
-    uint64_t* SQ = (uint64_t*)ws_get(ctx, WS_SUM, (size_t)n_o * ng * ctw * 8);
-    moddown_inplace(ctx, S, 2 * n_o * ng, l, nullptr, SQ, st);
-    // giant rotations without their ModDown, summed per output in Q_l P: T [n_o][2][E][N] (by_output: output o of
-    // instance s at slot o n_inst + s); outputs in chunks whose extensions fit a bounded buffer
-    uint64_t* T = (uint64_t*)ws_get(ctx, WS_GROT, (size_t)n_o * cte * 8);
-    std::vector<uint32_t> gg(ng);
-    uint32_t n_rot = 0;
-    for (uint32_t g = 0; g < ng; g++) {
-        gg[g] = gsteps[g] ? rotation_index(gsteps[g]) : 1;
-        n_rot += gsteps[g] ? 1 : 0;
-    }
-    const uint32_t chunk = std::max<uint32_t>(1, 32 / ng);
-    uint64_t* ext2 = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)std::min(chunk, n_o) * ng * exw * 8);
-    for (uint32_t o0 = 0; o0 < n_o; o0 += chunk) {
-        const uint32_t m = std::min(chunk, n_o - o0);
-        const uint64_t* src = SQ + (size_t)o0 * ng * ctw;
-        // identity giants are extended too (one strided ModUp over the chunk); their extension goes unread
-        if (n_rot) modup(ctx, src + (size_t)l * W, ext2, m * ng, l, st, ctw);
-        if (by_output)
-            HIPX(launch_qp_rot_sum(ctx, ext2, exw, src, ctw, gevk, gg.data(), m, ng, 1, ng, l, pmod.data(), T, st,
-                                   n_out, o0, (uint64_t)n_inst * cte));
-        else
-            HIPX(launch_qp_rot_sum(ctx, ext2, exw, src, ctw, gevk, gg.data(), m, ng, 1, ng, l, pmod.data(),
-                                   T + (size_t)o0 * cte, st));
+    if (ngr) {
+        uint64_t* SQ = (uint64_t*)ws_get(ctx, WS_SUM, (size_t)n_o * ngr * ctw * 8);
+        moddown_inplace(ctx, S, 2 * n_o * ngr, l, nullptr, SQ, st);
+        // outputs in chunks whose extensions fit a bounded buffer
+        const uint32_t chunk = std::max<uint32_t>(1, 32 / ngr);
+        uint64_t* ext2 = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)std::min(chunk, n_o) * ngr * exw * 8);
+        const bool acc = g0 >= 0;
+        for (uint32_t o0 = 0; o0 < n_o; o0 += chunk) {
+            const uint32_t m = std::min(chunk, n_o - o0);
+            const uint64_t* src = SQ + (size_t)o0 * ngr * ctw;
+            modup(ctx, src + (size_t)l * W, ext2, m * ngr, l, st, ctw);
+            if (by_output)
+                HIPX(launch_qp_rot_sum(ctx, ext2, exw, src, ctw, rk.data(), rg.data(), m, ngr, 1, ngr, l, pmod.data(),
+                                       T, st, n_out, o0, (uint64_t)n_inst * cte, acc));
+            else
+                HIPX(launch_qp_rot_sum(ctx, ext2, exw, src, ctw, rk.data(), rg.data(), m, ngr, 1, ngr, l, pmod.data(),
+                                       T + (size_t)o0 * cte, st, 1, 0, 0, acc));
+        }
     }
     // one ModDown for the giant sums, fused with the rescale
     moddown_rescale(ctx, T, 2 * n_o, l, nullptr, out, st);

@@ -553,7 +553,7 @@ __global__ __launch_bounds__(256) void k_automorph_list(const uint64_t* __restri
 // the bit-reversed index by an odd g), so the gathers stay coalesced.
 struct QpRotArgs {
     uint32_t l, E, L, D, T, nt, A, M;
-    uint32_t n_out, R, c_off;
+    uint32_t n_out, R, c_off, accumulate;
     uint64_t ext_stride, src_stride, s_hi, s_lo;
     const uint64_t* evk[kMaxList];
     uint32_t g[kMaxList];
@@ -601,6 +601,10 @@ __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__
     }
     const uint32_t u = c + a.c_off;
     uint64_t* o = dst + (size_t)(u / a.R) * a.s_hi + (size_t)(u % a.R) * a.s_lo + (size_t)t * kN + k;
+    if (a.accumulate) {
+        v0 = add_mod(v0, o[0], q);
+        v1 = add_mod(v1, o[(size_t)a.E * kN], q);
+    }
     o[0] = v0;
     o[(size_t)a.E * kN] = v1;
 }
@@ -619,22 +623,40 @@ constexpr int kMacRows = 8;
 // thread's word at dk in a diagonal and off in an output poly).  Diagonals past n_diag (a short last giant step) are
 // zero; acc != 0 adds to what out holds.  A wave row takes two giant steps at a time: four independent accumulation
 // chains per thread, and every baby word read from LDS feeds two products.
+// Destinations of the giant sums: sum G goes to out + G 2 P, or, with g0 >= 0 (an identity giant step), writing
+// G = o ngp + g: sum (o, g0) to id_out + o id_stride and the others to out + (o (ngp - 1) + g - [g > g0]) 2 P.
+struct GiantMap {
+    uint32_t ngp;
+    int32_t g0;
+    uint64_t* id_out;
+    uint64_t id_stride;
+};
+
 __device__ __forceinline__ void mac_giants(const uint64_t* sb, const uint64_t* __restrict__ diag,
                                            uint64_t* __restrict__ out, uint32_t nb, uint32_t nb_total, uint32_t j0,
                                            uint32_t ng, uint32_t n_diag, size_t P, size_t Pd, size_t dk, size_t off,
-                                           uint32_t acc, const Barrett& br, uint32_t kk, uint32_t row) {
+                                           uint32_t acc, const Barrett& br, uint32_t kk, uint32_t row,
+                                           const GiantMap& gm = GiantMap{1, -1, nullptr, 0}) {
     auto count = [&](uint32_t g) {
         const int64_t rem = (int64_t)n_diag - (int64_t)g * nb_total - j0;
         return rem <= 0 ? 0u : (uint32_t)min<int64_t>(rem, nb);
     };
     auto store = [&](uint32_t g, Acc& a0, Acc& a1) {
+        uint64_t* o = out + (size_t)g * 2 * P + off;
+        if (gm.g0 >= 0) {
+            const uint32_t oi = g / gm.ngp, gi = g - oi * gm.ngp;
+            if (gi == (uint32_t)gm.g0)
+                o = gm.id_out + (size_t)oi * gm.id_stride + off;
+            else
+                o = out + ((size_t)oi * (gm.ngp - 1) + gi - (gi > (uint32_t)gm.g0 ? 1 : 0)) * 2 * P + off;
+        }
         uint64_t r0 = reduce_u128(a0.get(), br), r1 = reduce_u128(a1.get(), br);
         if (acc) {
-            r0 = add_mod(r0, out[(size_t)g * 2 * P + off], br.q);
-            r1 = add_mod(r1, out[(size_t)g * 2 * P + P + off], br.q);
+            r0 = add_mod(r0, o[0], br.q);
+            r1 = add_mod(r1, o[P], br.q);
         }
-        out[(size_t)g * 2 * P + off] = r0;
-        out[(size_t)g * 2 * P + P + off] = r1;
+        o[0] = r0;
+        o[P] = r1;
     };
     for (uint32_t g = row; g < ng; g += 2 * kMacRows) {
         const uint32_t g2 = g + kMacRows;
@@ -709,14 +731,20 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(ListPtrs baby,
 // Double-hoisted BSGS MAC: the babies are formed in LDS from the inputs' ModUp extensions and never stored.  Over
 // Q_l * P (E limbs), baby j = i nb + b of instance s is the rotation of input x = s n_in + i by baby step b kept in
 // the extended basis (see k_qp_rot_sum): Auto_b(<ext_x, evk_b> + (P c0_x, 0)), or (P c0_x, P c1_x) for b's
-// identity step; then out_s [ng][2][E][N] = sum_j baby_j (.) diag[g nbt + j] as in k_bsgs_mac (diagonals
-// [n_diag][E][N], shared by the instances, whose workgroups of one tile run on one XCD).
+// identity step; then the giant sums sum_j baby_j (.) diag[G nbt + j] as in k_bsgs_mac (diagonals [n_diag][E][N],
+// shared by the instances, whose workgroups of one tile run on one XCD), G = o ngp + g.  The sums of the identity
+// giant step g0 need no rotation: they go to id_out (where the giant rotations are later added), the others to
+// out_s [n_out][ngp - 1][2][E][N] (all ngp when g0 < 0).
 constexpr int kMaxDhBaby = 32;
 struct DhMacArgs {
     uint32_t l, E, L, D, T;          // Q limbs, extended limbs, first P prime, digits, evk limbs per poly
     uint32_t n_in, nb, ng, n_diag, n_inst;
+    uint32_t ngp;                     // giant steps per output (ng = n_out ngp)
+    int32_t g0;                       // the identity giant step (or -1): its sums go to id_out
     uint64_t ext_stride, src_stride;  // per input x
     uint64_t out_stride;              // per instance
+    uint64_t* id_out;
+    uint64_t id_inst_stride, id_stride;  // id_out: per instance, per output
     const uint64_t* evk[kMaxDhBaby];  // per baby step (null: the identity)
     uint32_t g[kMaxDhBaby];
     TwPair pmod[kMaxPmap];            // P mod q_t, t < l
@@ -768,7 +796,9 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
     }
     __syncthreads();
     const size_t P = (size_t)a.E * kN, off = (size_t)t * kN + k;
-    mac_giants(sb, diag, out + (size_t)s * a.out_stride, nbt, nbt, 0, a.ng, a.n_diag, P, P, off, off, 0, br, kk, row);
+    const GiantMap gm{a.ngp, a.g0, a.g0 >= 0 ? a.id_out + (size_t)s * a.id_inst_stride : nullptr, a.id_stride};
+    mac_giants(sb, diag, out + (size_t)s * a.out_stride, nbt, nbt, 0, a.ng, a.n_diag, P, P, off, off, 0, br, kk, row,
+               gm);
 }
 
 // Masked pairs: out[s][t] = pt[s][t][0] (.) R[t] + pt[s][t][1] (.) R[n + t] on both polys, with
@@ -1090,14 +1120,19 @@ hipError_t launch_bsgs_mac(const Context& ctx, const uint64_t* const* baby, cons
 }
 
 // babies b < nb (keys[b] null: identity; g[b] its automorphism) of n_in inputs per instance, n_inst instances:
-// ext [n_inst n_in] extensions ext_stride apart, src the inputs src_stride apart; out [n_inst][ng][2][E][N]
+// ext [n_inst n_in] extensions ext_stride apart, src the inputs src_stride apart; n_out outputs of ngp giant sums
+// each, the identity giant g0's (g0 >= 0) to id_out + s id_inst_stride + o id_stride, the others to out
+// [n_inst][n_out][ngp or ngp - 1][2][E][N]
 hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
                               uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_inst,
-                              uint32_t n_in, uint32_t nb, const uint64_t* diag, uint32_t n_diag, uint32_t ng,
-                              uint32_t l, const TwPair* pmod, uint64_t* out, hipStream_t st) {
+                              uint32_t n_in, uint32_t nb, const uint64_t* diag, uint32_t n_diag, uint32_t n_out,
+                              uint32_t ngp, int32_t g0, uint32_t l, const TwPair* pmod, uint64_t* out,
+                              uint64_t* id_out, uint64_t id_inst_stride, uint64_t id_stride, hipStream_t st) {
+    const uint32_t ng = n_out * ngp;
     const uint32_t E = l + ctx.K, D = (l + ctx.alpha - 1) / ctx.alpha;
     if (n_inst == 0 || n_inst > 4096 || nb == 0 || nb > (uint32_t)kMaxDhBaby || n_in * nb > (uint32_t)kMaxBaby ||
-        n_diag > n_in * nb * ng || E > kMaxPmap || D > (uint32_t)kMaxDigits)
+        n_diag > n_in * nb * ng || E > kMaxPmap || D > (uint32_t)kMaxDigits || g0 >= (int32_t)ngp ||
+        (g0 >= 0 && !id_out))
         return hipErrorInvalidValue;
     DhMacArgs a{};
     a.l = l;
@@ -1112,7 +1147,12 @@ hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t 
     a.n_inst = n_inst;
     a.ext_stride = ext_stride;
     a.src_stride = src_stride;
-    a.out_stride = (uint64_t)ng * 2 * E * kN;
+    a.ngp = ngp;
+    a.g0 = g0;
+    a.out_stride = (uint64_t)n_out * (g0 >= 0 ? ngp - 1 : ngp) * 2 * E * kN;
+    a.id_out = id_out;
+    a.id_inst_stride = id_inst_stride;
+    a.id_stride = id_stride;
     uint32_t n_ks = 0;
     for (uint32_t b = 0; b < nb; b++) {
         a.evk[b] = keys[b];
@@ -1189,11 +1229,11 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
 }
 
 // n_out outputs of nt terms each (see k_qp_rot_sum); keys[i] / steps g[i], i < A + nt - 1 <= 64 (null key:
-// identity term); output c at dst + (u / R) 2 E N + (u % R) s_lo, u = c + c_off
+// identity term); output c at dst + (u / R) 2 E N + (u % R) s_lo, u = c + c_off; accumulate adds to it
 hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
                              uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_out,
                              uint32_t nt, uint32_t A, uint32_t M, uint32_t l, const TwPair* pmod, uint64_t* dst,
-                             hipStream_t st, uint32_t R, uint32_t c_off, uint64_t s_lo) {
+                             hipStream_t st, uint32_t R, uint32_t c_off, uint64_t s_lo, bool accumulate) {
     const uint32_t E = l + ctx.K;
     if (n_out == 0 || nt == 0 || A == 0 || A + nt - 1 > (uint32_t)kMaxList || E > kMaxPmap || n_out > 4096)
         return hipErrorInvalidValue;
@@ -1211,6 +1251,7 @@ hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t e
     a.ext_stride = ext_stride;
     a.src_stride = src_stride;
     a.n_out = n_out;
+    a.accumulate = accumulate ? 1 : 0;
     a.R = R ? R : 1;
     a.c_off = c_off;
     a.s_hi = (uint64_t)2 * E * kN;

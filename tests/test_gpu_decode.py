@@ -226,14 +226,16 @@ def test_linear_transform_multi_bit_exact(ckks, ctx5, octx5):
         assert np.array_equal(got[o], want), o
 
 
-def test_linear_transform_hoisted_bit_exact(ckks, ctx5, octx5):
+@pytest.mark.parametrize("gst", [[0, 3, -3], [3, 0, -3], [2, 3, -3]])
+def test_linear_transform_hoisted_bit_exact(ckks, ctx5, octx5, gst):
     """Double-hoisted BSGS (the bootstrap's CoeffToSlot / SlotToCoeff form) against the oracle composed from its
     stages: babies rotated in Q_l P without a ModDown, diagonals over Q_l P, one ModDown per giant inner sum,
-    giant rotations summed in Q_l P, ModDown then rescale.  2 inputs, 2 outputs, babies {0, 1, 2}, giants
-    {0, 3, -3}."""
+    giant rotations summed in Q_l P, ModDown then rescale; the inner sum of the identity giant step (the first
+    step 0) is added in Q_l P as it is, without a ModDown.  2 inputs, 2 outputs, babies {0, 1, 2}; giants with the
+    identity first, in the middle, or absent."""
     l, n_in, n_out = 5, 2, 2
     L, K, D = ctx5.L, ctx5.K, ctx5.dnum
-    bst, gst = [0, 1, 2], [0, 3, -3]
+    bst = [0, 1, 2]
     nb, ng = len(bst), len(gst)
     steps = [1, 2, 3, -3]
     pmap = list(range(l)) + list(range(L, L + K))
@@ -272,11 +274,15 @@ def test_linear_transform_hoisted_bit_exact(ckks, ctx5, octx5):
         return octx5.automorph_eval(v, octx5.rot_index(s)).astype(object)
 
     babies = [rot_qp(xs[i], s) for i in range(n_in) for s in bst]
+    g0 = gst.index(0) if 0 in gst else -1
     for o in range(n_out):
         T = np.zeros((2, E, N), dtype=object)
         for g in range(ng):
             S = sum(babies[j] * diags[o, g, j].astype(object)[None] for j in range(n_in * nb))
             S = (S % qe[None]).astype(np.uint64)
+            if g == g0:
+                T += S.astype(object)
+                continue
             SQ = np.stack([octx5.moddown(S[p], l) for p in range(2)])
             T += rot_qp(SQ, gst[g])
         T = (T % qe[None]).astype(np.uint64)
