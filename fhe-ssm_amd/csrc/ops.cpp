@@ -65,7 +65,8 @@ hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t 
                               uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_inst,
                               uint32_t n_in, uint32_t nb, const uint64_t* diag, uint32_t n_diag, uint32_t n_out,
                               uint32_t ngp, int32_t g0, uint32_t l, const TwPair* pmod, uint64_t* out,
-                              uint64_t* id_out, uint64_t id_inst_stride, uint64_t id_stride, hipStream_t st);
+                              uint64_t* id_out, uint64_t id_inst_stride, uint64_t id_stride, uint32_t chain_delta,
+                              hipStream_t st);
 hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
                              uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_out,
                              uint32_t nt, uint32_t A, uint32_t M, uint32_t l, const TwPair* pmod, uint64_t* dst,
@@ -861,8 +862,13 @@ void bsgs_dh_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uin
         std::vector<uint32_t> g(nb);
         for (uint32_t b = 0; b < nb; b++) g[b] = bsteps[b] ? rotation_index(bsteps[b]) : 1;
         const uint64_t id_inst = by_output ? cte : (uint64_t)n_out * cte, id_o = by_output ? (uint64_t)n_inst * cte : cte;
+        // baby steps b delta (delta > 0) let the MAC order its tiles along the rotation chains
+        int64_t delta = nb > 1 ? bsteps[1] : 0;
+        for (uint32_t b = 0; b < nb; b++)
+            if (bsteps[b] != (int64_t)b * delta) delta = 0;
+        if (delta < 0 || delta >= (int64_t)(kN / 2) || (delta & (delta - 1))) delta = 0;  // a power of two
         HIPX(launch_bsgs_dh_mac(ctx, ext, exw, X, ctw, bevk, g.data(), n_inst, n_in, nb, diags_qp, nbt * n_out * ng,
-                                n_out, ng, g0, l, pmod.data(), S, T, id_inst, id_o, st));
+                                n_out, ng, g0, l, pmod.data(), S, T, id_inst, id_o, (uint32_t)delta, st));
     }
     if (ngr) {
         uint64_t* SQ = (uint64_t*)ws_get(ctx, WS_SUM, (size_t)n_o * ngr * ctw * 8);

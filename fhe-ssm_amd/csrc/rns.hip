@@ -736,11 +736,37 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(ListPtrs baby,
 // giant step g0 need no rotation: they go to id_out (where the giant rotations are later added), the others to
 // out_s [n_out][ngp - 1][2][E][N] (all ngp when g0 < 0).
 constexpr int kMaxDhBaby = 32;
+
+// Coefficient tile order for rotations by multiples of delta slots.  Tile kt (64 consecutive evaluation words) is the
+// odd residue u = 2 brev10(kt) + 1 mod 2048, and the automorphism X -> X^g maps it onto the tile of g u mod 2048
+// (the words stay in their aligned 64-word block, permuted).  With the babies' g_b = 5^(b delta), tile u reads the
+// blocks u 5^(b delta): ordering the tiles along the chains u0 5^(delta m) makes consecutive tiles read nearly the same
+// blocks (15 of 16 for 16 babies), so a baby input's words come from L2 instead of HBM.  The odd residues are
+// +-5^a (a < 512); the chains are the cosets +-5^a <5^delta>, a < min(delta, 512).  Position pos in [0, 1024) of the
+// order -> tile kt; delta = 0 keeps kt = pos.
+__device__ __forceinline__ uint32_t chain_tile(uint32_t pos, uint32_t delta) {
+    if (delta == 0) return pos;
+    const uint32_t d = delta >= 512 ? 512u : delta;         // 5 has order 512 mod 2048
+    const uint32_t len = 512u / d;                           // chain length
+    const uint32_t c = pos / len, m = pos - c * len;
+    const uint32_t per_sign = 512u / len;                    // chains per sign (= d)
+    const uint32_t neg = c / per_sign, a = c - neg * per_sign;
+    uint32_t e = (a + (uint32_t)(((uint64_t)delta * m) & 511u)) & 511u;
+    uint32_t u = 1, b = 5;
+    for (; e; e >>= 1) {
+        if (e & 1) u = (u * b) & 2047u;
+        b = (b * b) & 2047u;
+    }
+    if (neg) u = (2048u - u) & 2047u;
+    return __brev((u - 1u) >> 1) >> 22;                      // brev10((u - 1) / 2)
+}
+
 struct DhMacArgs {
     uint32_t l, E, L, D, T;          // Q limbs, extended limbs, first P prime, digits, evk limbs per poly
     uint32_t n_in, nb, ng, n_diag, n_inst;
     uint32_t ngp;                     // giant steps per output (ng = n_out ngp)
     int32_t g0;                       // the identity giant step (or -1): its sums go to id_out
+    uint32_t chain_delta;             // baby steps b chain_delta (0: not an arithmetic progression)
     uint64_t ext_stride, src_stride;  // per input x
     uint64_t out_stride;              // per instance
     uint64_t* id_out;
@@ -756,9 +782,13 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
                                                                      uint64_t* __restrict__ out, DhMacArgs a,
                                                                      const PrimeInfo* __restrict__ primes) {
     extern __shared__ uint64_t sb[];
-    const ListTile lt = list_tile(a.n_inst, kN / kMacCoef);
+    // XCD x (workgroups x mod 8) takes one contiguous run of the (limb, chain-ordered tile) sequence; the instances of
+    // a tile follow each other on it (they share the tile's keys and diagonals)
+    const uint32_t xcd = blockIdx.x & 7, qi = blockIdx.x >> 3;
+    const uint32_t s = qi % a.n_inst, seq = xcd * (a.E * (kN / kMacCoef) / 8) + qi / a.n_inst;
+    const uint32_t t = seq / (kN / kMacCoef);
     const uint32_t kk = threadIdx.x & (kMacCoef - 1), row = threadIdx.x / kMacCoef;
-    const uint32_t k = lt.kt * kMacCoef + kk, t = lt.limb, s = lt.item;
+    const uint32_t k = chain_tile(seq % (kN / kMacCoef), a.chain_delta) * kMacCoef + kk;
     const bool qlimb = t < a.l;
     const uint32_t pi = qlimb ? t : a.L + (t - a.l);
     const Barrett br = barrett_of(primes[pi]);
@@ -795,10 +825,60 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
         sb[(2 * j + 1) * kMacCoef + kk] = v1;
     }
     __syncthreads();
+    // giant sums: with fewer giants than rows, each giant's babies are split over kMacRows / ng rows (slices) whose
+    // partial sums meet in LDS, so every row works
     const size_t P = (size_t)a.E * kN, off = (size_t)t * kN + k;
-    const GiantMap gm{a.ngp, a.g0, a.g0 >= 0 ? a.id_out + (size_t)s * a.id_inst_stride : nullptr, a.id_stride};
-    mac_giants(sb, diag, out + (size_t)s * a.out_stride, nbt, nbt, 0, a.ng, a.n_diag, P, P, off, off, 0, br, kk, row,
-               gm);
+    const uint32_t slices = a.ng < (uint32_t)kMacRows ? kMacRows / a.ng : 1u;
+    uint64_t* part = sb + (size_t)2 * nbt * kMacCoef;  // [kMacRows][2][kMacCoef]
+    out += (size_t)s * a.out_stride;
+    uint64_t* id_out = a.g0 >= 0 ? a.id_out + (size_t)s * a.id_inst_stride : nullptr;
+    auto dest = [&](uint32_t G) {
+        if (a.g0 < 0) return out + (size_t)G * 2 * P + off;
+        const uint32_t oi = G / a.ngp, gi = G - oi * a.ngp;
+        if (gi == (uint32_t)a.g0) return id_out + (size_t)oi * a.id_stride + off;
+        return out + ((size_t)oi * (a.ngp - 1) + gi - (gi > (uint32_t)a.g0 ? 1 : 0)) * 2 * P + off;
+    };
+    const uint32_t per = (nbt + slices - 1) / slices;
+    for (uint32_t G0 = 0; G0 < a.ng; G0 += kMacRows / slices) {
+        const uint32_t G = G0 + row % (kMacRows / slices), sl = row / (kMacRows / slices);
+        uint64_t r0 = 0, r1 = 0;
+        if (G < a.ng) {
+            const uint32_t j_lo = sl * per, j_hi = min(nbt, j_lo + per);
+            const int64_t rem = (int64_t)a.n_diag - (int64_t)G * nbt;  // diagonals past n_diag are zero
+            const uint32_t j_end = rem <= 0 ? 0u : min<uint32_t>(j_hi, (uint32_t)min<int64_t>(rem, nbt));
+            const uint64_t* d = diag + (size_t)G * nbt * P + off;
+            Acc s0, s1;
+            for (uint32_t j = j_lo, c = 0; j < j_end; j++, c++) {
+                const uint64_t m = d[(size_t)j * P];
+                s0.add(sb[(2 * j) * kMacCoef + kk], m);
+                s1.add(sb[(2 * j + 1) * kMacCoef + kk], m);
+                if ((c & 7) == 7) {
+                    s0.fold();
+                    s1.fold();
+                }
+            }
+            r0 = reduce_u128(s0.get(), br);
+            r1 = reduce_u128(s1.get(), br);
+        }
+        if (slices > 1) {
+            part[(2 * row) * kMacCoef + kk] = r0;
+            part[(2 * row + 1) * kMacCoef + kk] = r1;
+            __syncthreads();
+            if (sl == 0 && G < a.ng) {
+                for (uint32_t o = 1; o < slices; o++) {
+                    const uint32_t rr = row + o * (kMacRows / slices);
+                    r0 = add_mod(r0, part[(2 * rr) * kMacCoef + kk], q);
+                    r1 = add_mod(r1, part[(2 * rr + 1) * kMacCoef + kk], q);
+                }
+            }
+            __syncthreads();
+        }
+        if (sl == 0 && G < a.ng) {
+            uint64_t* o = dest(G);
+            o[0] = r0;
+            o[P] = r1;
+        }
+    }
 }
 
 // Masked pairs: out[s][t] = pt[s][t][0] (.) R[t] + pt[s][t][1] (.) R[n + t] on both polys, with
@@ -1127,7 +1207,8 @@ hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t 
                               uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_inst,
                               uint32_t n_in, uint32_t nb, const uint64_t* diag, uint32_t n_diag, uint32_t n_out,
                               uint32_t ngp, int32_t g0, uint32_t l, const TwPair* pmod, uint64_t* out,
-                              uint64_t* id_out, uint64_t id_inst_stride, uint64_t id_stride, hipStream_t st) {
+                              uint64_t* id_out, uint64_t id_inst_stride, uint64_t id_stride, uint32_t chain_delta,
+                              hipStream_t st) {
     const uint32_t ng = n_out * ngp;
     const uint32_t E = l + ctx.K, D = (l + ctx.alpha - 1) / ctx.alpha;
     if (n_inst == 0 || n_inst > 4096 || nb == 0 || nb > (uint32_t)kMaxDhBaby || n_in * nb > (uint32_t)kMaxBaby ||
@@ -1149,6 +1230,7 @@ hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t 
     a.src_stride = src_stride;
     a.ngp = ngp;
     a.g0 = g0;
+    a.chain_delta = chain_delta;
     a.out_stride = (uint64_t)n_out * (g0 >= 0 ? ngp - 1 : ngp) * 2 * E * kN;
     a.id_out = id_out;
     a.id_inst_stride = id_inst_stride;
@@ -1167,7 +1249,7 @@ hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t 
                       (double)n_ks * 2 * D * E + (double)n_diag * E + (double)n_inst * ng * 2 * E;
     const int pi = prof_begin(ctx, "bsgs_dh_mac", by * kN * 8, st);
     hipLaunchKernelGGL(k_bsgs_dh_mac, dim3(n_inst * (kN / kMacCoef) * E), dim3(kMacCoef * kMacRows),
-                       (size_t)n_in * nb * 2 * kMacCoef * 8, st, ext, src, diag, out, a, ctx.d_primes);
+                       ((size_t)n_in * nb + kMacRows) * 2 * kMacCoef * 8, st, ext, src, diag, out, a, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
