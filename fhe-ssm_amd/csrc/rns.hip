@@ -776,6 +776,9 @@ struct DhMacArgs {
     TwPair pmod[kMaxPmap];            // P mod q_t, t < l
 };
 
+// ND: the digit count (a template parameter, so that a baby's extension and key loads are all issued before the
+// first product waits on them).
+template <int ND>
 __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64_t* __restrict__ ext,
                                                                      const uint64_t* __restrict__ src,
                                                                      const uint64_t* __restrict__ diag,
@@ -805,14 +808,18 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
         if (ek) {
             const uint64_t* xe = ext + (size_t)x * a.ext_stride + (size_t)t * kN + sw;
             const uint64_t* ep = ek + (size_t)pi * kN + sw;
+            uint64_t xv[ND], e0[ND], e1[ND];
+#pragma unroll
+            for (int d = 0; d < ND; d++) {
+                xv[d] = xe[(size_t)d * a.E * kN];
+                e0[d] = ep[((size_t)d * 2 + 0) * a.T * kN];
+                e1[d] = ep[((size_t)d * 2 + 1) * a.T * kN];
+            }
             Acc s0, s1;  // at most kMaxDigits = 8 terms
 #pragma unroll
-            for (int d = 0; d < kMaxDigits; d++) {
-                if (d < (int)a.D) {
-                    const uint64_t v = xe[(size_t)d * a.E * kN];
-                    s0.add(v, ep[((size_t)d * 2 + 0) * a.T * kN]);
-                    s1.add(v, ep[((size_t)d * 2 + 1) * a.T * kN]);
-                }
+            for (int d = 0; d < ND; d++) {
+                s0.add(xv[d], e0[d]);
+                s1.add(xv[d], e1[d]);
             }
             v0 = reduce_u128(s0.get(), br);
             if (qlimb) v0 = add_mod(v0, shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q), q);
@@ -848,14 +855,21 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
             const uint32_t j_end = rem <= 0 ? 0u : min<uint32_t>(j_hi, (uint32_t)min<int64_t>(rem, nbt));
             const uint64_t* d = diag + (size_t)G * nbt * P + off;
             Acc s0, s1;
-            for (uint32_t j = j_lo, c = 0; j < j_end; j++, c++) {
-                const uint64_t m = d[(size_t)j * P];
-                s0.add(sb[(2 * j) * kMacCoef + kk], m);
-                s1.add(sb[(2 * j + 1) * kMacCoef + kk], m);
-                if ((c & 7) == 7) {
-                    s0.fold();
-                    s1.fold();
+            // 8 babies at a time: their diagonal words are all requested before the first product waits
+            for (uint32_t j0 = j_lo; j0 < j_end; j0 += 8) {
+                uint64_t m[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) m[u] = j0 + u < j_end ? d[(size_t)(j0 + u) * P] : 0;
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    if (j0 + u < j_end) {
+                        const uint32_t j = j0 + u;
+                        s0.add(sb[(2 * j) * kMacCoef + kk], m[u]);
+                        s1.add(sb[(2 * j + 1) * kMacCoef + kk], m[u]);
+                    }
                 }
+                s0.fold();
+                s1.fold();
             }
             r0 = reduce_u128(s0.get(), br);
             r1 = reduce_u128(s1.get(), br);
@@ -1248,7 +1262,12 @@ hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t 
     const double by = (double)n_inst * n_in * (n_ks * ((double)D * E + l) + (nb - n_ks) * 2.0 * l) +
                       (double)n_ks * 2 * D * E + (double)n_diag * E + (double)n_inst * ng * 2 * E;
     const int pi = prof_begin(ctx, "bsgs_dh_mac", by * kN * 8, st);
-    hipLaunchKernelGGL(k_bsgs_dh_mac, dim3(n_inst * (kN / kMacCoef) * E), dim3(kMacCoef * kMacRows),
+    using MacKernel = void (*)(const uint64_t*, const uint64_t*, const uint64_t*, uint64_t*, DhMacArgs,
+                               const PrimeInfo*);
+    static constexpr MacKernel kByDigits[kMaxDigits] = {k_bsgs_dh_mac<1>, k_bsgs_dh_mac<2>, k_bsgs_dh_mac<3>,
+                                                        k_bsgs_dh_mac<4>, k_bsgs_dh_mac<5>, k_bsgs_dh_mac<6>,
+                                                        k_bsgs_dh_mac<7>, k_bsgs_dh_mac<8>};
+    hipLaunchKernelGGL(kByDigits[D - 1], dim3(n_inst * (kN / kMacCoef) * E), dim3(kMacCoef * kMacRows),
                        ((size_t)n_in * nb + kMacRows) * 2 * kMacCoef * 8, st, ext, src, diag, out, a, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();

@@ -315,12 +315,13 @@ def test_config5_chain_bootstrap(engine):
 
 @pytest.mark.timeout(900)
 def test_bootstrap_many_matches_single(engine):
-    """the batched bootstrap is the single-ciphertext bootstrap word for word, for every item of the batch"""
+    """the batched bootstrap is the single-ciphertext bootstrap word for word, for every item of the batch (4
+    items: the linear transforms' MAC then takes 4 instances per workgroup, 2 at the two-input level)"""
     be, sk = engine
     boot, ins = be.boots["state"]
     keys = be.boot_keys["state"]
     rng = np.random.default_rng(33)
-    B = 3
+    B = 4
     cts = [be.at_scale(be.encrypt(sk, rng.uniform(-1, 1, SLOTS), 3, seed=bytes([b]) * 32), 1, ins) for b in range(B)]
     batch = be._new(B, 1, ins)
     for b in range(B):
