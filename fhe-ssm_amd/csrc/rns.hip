@@ -270,6 +270,29 @@ static void (*bconv_kernel(uint32_t n_in))(const uint64_t*, uint64_t*, BConvArgs
 // back to back, so each XCD fetches the tile once into its L2 and every load of a thread is independent.
 constexpr int kMaxDigits = 8;
 
+// The evk inner product of one extended word over D <= kMaxDigits digits: s0 += sum_d x[d xs] e[2d es],
+// s1 += sum_d x[d xs] e[(2d+1) es].  Every digit's loads are issued before the first product waits on them (a
+// load-multiply loop per digit makes each digit a separate round trip to memory).
+__device__ __forceinline__ void ks_dot(const uint64_t* __restrict__ x, size_t xs, const uint64_t* __restrict__ e,
+                                       size_t es, uint32_t D, Acc& s0, Acc& s1) {
+    uint64_t xv[kMaxDigits], e0[kMaxDigits], e1[kMaxDigits];
+#pragma unroll
+    for (int d = 0; d < kMaxDigits; d++) {
+        if (d < (int)D) {
+            xv[d] = x[(size_t)d * xs];
+            e0[d] = e[((size_t)d * 2 + 0) * es];
+            e1[d] = e[((size_t)d * 2 + 1) * es];
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < kMaxDigits; d++) {
+        if (d < (int)D) {
+            s0.add(xv[d], e0[d]);
+            s1.add(xv[d], e1[d]);
+        }
+    }
+}
+
 struct InnerArgs {
     uint32_t D, E, T, B;
     uint32_t t0;  // first extended limb computed (k_ks_inner: limbs t0..E-1)
@@ -286,14 +309,7 @@ __global__ __launch_bounds__(256) void k_ks_inner(const uint64_t* __restrict__ e
     const uint64_t* x = ext + (size_t)c * ia.D * ia.E * kN + (size_t)t * kN + k;
     const uint64_t* e = evk + (size_t)p * kN + k;
     Acc s0, s1;  // at most kMaxDigits = 8 terms: no intermediate fold
-#pragma unroll
-    for (int d = 0; d < kMaxDigits; d++) {
-        if (d < (int)ia.D) {
-            const uint64_t v = x[(size_t)d * ia.E * kN];
-            s0.add(v, e[((size_t)d * 2 + 0) * ia.T * kN]);
-            s1.add(v, e[((size_t)d * 2 + 1) * ia.T * kN]);
-        }
-    }
+    ks_dot(x, (size_t)ia.E * kN, e, (size_t)ia.T * kN, ia.D, s0, s1);
     uint64_t* o = acc + (size_t)c * 2 * ia.E * kN + (size_t)t * kN + k;
     o[0] = reduce_u128(s0.get(), br);
     o[(size_t)ia.E * kN] = reduce_u128(s1.get(), br);
@@ -390,14 +406,7 @@ __global__ __launch_bounds__(256) void k_ks_inner_list(ListPtrs ext, ListPtrs ev
     const uint64_t* x = ext.p[c] + (size_t)t * kN + k;
     const uint64_t* e = evk.p[c] + (size_t)p * kN + k;
     Acc s0, s1;  // at most kMaxDigits = 8 terms
-#pragma unroll
-    for (int d = 0; d < kMaxDigits; d++) {
-        if (d < (int)ia.D) {
-            const uint64_t v = x[(size_t)d * ia.E * kN];
-            s0.add(v, e[((size_t)d * 2 + 0) * ia.T * kN]);
-            s1.add(v, e[((size_t)d * 2 + 1) * ia.T * kN]);
-        }
-    }
+    ks_dot(x, (size_t)ia.E * kN, e, (size_t)ia.T * kN, ia.D, s0, s1);
     uint64_t* o = acc + (size_t)c * 2 * ia.E * kN + (size_t)t * kN + k;
     o[0] = reduce_u128(s0.get(), br);
     o[(size_t)ia.E * kN] = reduce_u128(s1.get(), br);
@@ -423,14 +432,7 @@ __global__ __launch_bounds__(256) void k_ks_sub_list(ListPtrs ext, ListPtrs evk,
     const uint64_t* x = ext.p[c] + li;
     const uint64_t* e = evk.p[c] + li;
     Acc s0, s1;
-#pragma unroll
-    for (int d = 0; d < kMaxDigits; d++) {
-        if (d < (int)ia.D) {
-            const uint64_t v = x[(size_t)d * ia.E * kN];
-            s0.add(v, e[((size_t)d * 2 + 0) * ia.T * kN]);
-            s1.add(v, e[((size_t)d * 2 + 1) * ia.T * kN]);
-        }
-    }
+    ks_dot(x, (size_t)ia.E * kN, e, (size_t)ia.T * kN, ia.D, s0, s1);
     const size_t pw = (size_t)l * kN;  // words per poly of conv and out
     const uint64_t* cv = conv + (size_t)c * 2 * pw + li;
     uint64_t* o = out + (size_t)c * 2 * pw + li;
@@ -485,14 +487,7 @@ __global__ __launch_bounds__(256) void k_mdr_combine_ks(const uint64_t* __restri
     const uint64_t* x = ext + (size_t)c * ia.D * ia.E * kN + li;
     const uint64_t* e = evk + li;
     Acc s0, s1;  // at most kMaxDigits = 8 terms: no intermediate fold
-#pragma unroll
-    for (int d = 0; d < kMaxDigits; d++) {
-        if (d < (int)ia.D) {
-            const uint64_t v = x[(size_t)d * ia.E * kN];
-            s0.add(v, e[((size_t)d * 2 + 0) * ia.T * kN]);
-            s1.add(v, e[((size_t)d * 2 + 1) * ia.T * kN]);
-        }
-    }
+    ks_dot(x, (size_t)ia.E * kN, e, (size_t)ia.T * kN, ia.D, s0, s1);
     const uint64_t xs[2] = {reduce_u128(s0.get(), br), reduce_u128(s1.get(), br)};
 #pragma unroll
     for (int p = 0; p < 2; p++) {
@@ -582,14 +577,7 @@ __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__
             const uint64_t* xe = ext + (size_t)x * a.ext_stride + (size_t)t * kN + sw;
             const uint64_t* ep = ek + (size_t)pi * kN + sw;
             Acc s0, s1;  // at most kMaxDigits = 8 terms
-#pragma unroll
-            for (int d = 0; d < kMaxDigits; d++) {
-                if (d < (int)a.D) {
-                    const uint64_t v = xe[(size_t)d * a.E * kN];
-                    s0.add(v, ep[((size_t)d * 2 + 0) * a.T * kN]);
-                    s1.add(v, ep[((size_t)d * 2 + 1) * a.T * kN]);
-                }
-            }
+            ks_dot(xe, (size_t)a.E * kN, ep, (size_t)a.T * kN, a.D, s0, s1);
             uint64_t r0 = reduce_u128(s0.get(), br);
             if (qlimb) r0 = add_mod(r0, shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q), q);
             v0 = add_mod(v0, r0, q);
@@ -664,29 +652,47 @@ __device__ __forceinline__ void mac_giants(const uint64_t* sb, const uint64_t* _
         const uint64_t* d1 = diag + ((size_t)g * nb_total + j0) * Pd + dk;
         const uint64_t* d2 = diag + ((size_t)g2 * nb_total + j0) * Pd + dk;
         Acc a0, a1, b0, b1;
-        uint32_t j = 0;
-        for (; j < jn2; j++) {
-            const uint64_t x0 = sb[(2 * j) * kMacCoef + kk], x1 = sb[(2 * j + 1) * kMacCoef + kk];
-            const uint64_t m1 = d1[(size_t)j * Pd], m2 = d2[(size_t)j * Pd];
-            a0.add(x0, m1);
-            a1.add(x1, m1);
-            b0.add(x0, m2);
-            b1.add(x1, m2);
-            if ((j & 7) == 7) {
-                a0.fold();
-                a1.fold();
-                b0.fold();
-                b1.fold();
+        // 8 babies at a time: their diagonal words are all requested before the first product waits
+        for (uint32_t j0 = 0; j0 < jn2; j0 += 8) {
+            uint64_t m1[8], m2[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (j0 + u < jn2) {
+                    m1[u] = d1[(size_t)(j0 + u) * Pd];
+                    m2[u] = d2[(size_t)(j0 + u) * Pd];
+                }
             }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (j0 + u < jn2) {
+                    const uint32_t j = j0 + u;
+                    const uint64_t x0 = sb[(2 * j) * kMacCoef + kk], x1 = sb[(2 * j + 1) * kMacCoef + kk];
+                    a0.add(x0, m1[u]);
+                    a1.add(x1, m1[u]);
+                    b0.add(x0, m2[u]);
+                    b1.add(x1, m2[u]);
+                }
+            }
+            a0.fold();
+            a1.fold();
+            b0.fold();
+            b1.fold();
         }
-        for (; j < jn1; j++) {
-            const uint64_t m1 = d1[(size_t)j * Pd];
-            a0.add(sb[(2 * j) * kMacCoef + kk], m1);
-            a1.add(sb[(2 * j + 1) * kMacCoef + kk], m1);
-            if ((j & 7) == 7) {
-                a0.fold();
-                a1.fold();
+        for (uint32_t j0 = jn2; j0 < jn1; j0 += 8) {
+            uint64_t m1[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (j0 + u < jn1) m1[u] = d1[(size_t)(j0 + u) * Pd];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                if (j0 + u < jn1) {
+                    const uint32_t j = j0 + u;
+                    a0.add(sb[(2 * j) * kMacCoef + kk], m1[u]);
+                    a1.add(sb[(2 * j + 1) * kMacCoef + kk], m1[u]);
+                }
             }
+            a0.fold();
+            a1.fold();
         }
         store(g, a0, a1);
         if (g2 < ng) store(g2, b0, b1);
