@@ -66,19 +66,32 @@ __global__ __launch_bounds__(256) void k_tensor_sum(const uint64_t* const* __res
     const Barrett br = barrett_of(primes[t]);
     const size_t P = (size_t)ta.l * kN, w = (size_t)t * kN + k;
     Acc s0, s1, s2;
-    for (uint32_t j = 0; j < np; j++) {
-        const uint64_t* a = tab[((size_t)c * np + j) * 2];
-        const uint64_t* b = tab[((size_t)c * np + j) * 2 + 1];
-        const uint64_t a0 = a[w], a1 = a[P + w], b0 = b[w], b1 = b[P + w];
-        s0.add(a0, b0);
-        s1.add(a0, b1);
-        s1.add(a1, b0);
-        s2.add(a1, b1);
-        if ((j & 3) == 3) {  // s1 takes two terms per product: fold every 4 products
-            s0.fold();
-            s1.fold();
-            s2.fold();
+    // 4 products at a time (s1 takes two terms per product: a fold every 4), their 16 words requested together
+    for (uint32_t j0 = 0; j0 < np; j0 += 4) {
+        uint64_t a0[4], a1[4], b0[4], b1[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (j0 + u < np) {
+                const uint64_t* a = tab[((size_t)c * np + j0 + u) * 2];
+                const uint64_t* b = tab[((size_t)c * np + j0 + u) * 2 + 1];
+                a0[u] = a[w];
+                a1[u] = a[P + w];
+                b0[u] = b[w];
+                b1[u] = b[P + w];
+            }
         }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            if (j0 + u < np) {
+                s0.add(a0[u], b0[u]);
+                s1.add(a0[u], b1[u]);
+                s1.add(a1[u], b0[u]);
+                s2.add(a1[u], b1[u]);
+            }
+        }
+        s0.fold();
+        s1.fold();
+        s2.fold();
     }
     const size_t o = (size_t)c * 2 * P + w;
     d01[o] = reduce_u128(s0.get(), br);
@@ -952,7 +965,15 @@ __global__ __launch_bounds__(256) void k_sum_list(ListPtrs in, uint32_t n, uint6
     const uint64_t q = primes[i].q;
     const size_t o = ((size_t)pc * l + i) * kN + k;
     uint64_t acc = 0;
-    for (uint32_t j = 0; j < n; j++) acc = add_mod(acc, in.p[j][o], q);
+    for (uint32_t j0 = 0; j0 < n; j0 += 8) {  // 8 words requested together
+        uint64_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (j0 + u < n) v[u] = in.p[j0 + u][o];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (j0 + u < n) acc = add_mod(acc, v[u], q);
+    }
     out[o] = acc;
 }
 
@@ -978,10 +999,13 @@ __global__ __launch_bounds__(256) void k_lincomb(uint64_t* __restrict__ out, Lin
     const uint32_t c = pc >> 1, p = pc & 1;
     const Barrett br = barrett_of(primes[i]);
     Acc acc;  // at most kMaxTerms = 8 terms
-    for (uint32_t t = 0; t < la.n_terms; t++) {
-        const uint64_t v = la.x[t][((size_t)(2 * c + p) * la.stride[t] + i) * kN + k];
-        acc.add(v, la.C[t][i]);
-    }
+    uint64_t v[kMaxTerms];  // every term's word requested before the first product waits
+#pragma unroll
+    for (int t = 0; t < kMaxTerms; t++)
+        if (t < (int)la.n_terms) v[t] = la.x[t][((size_t)(2 * c + p) * la.stride[t] + i) * kN + k];
+#pragma unroll
+    for (int t = 0; t < kMaxTerms; t++)
+        if (t < (int)la.n_terms) acc.add(v[t], la.C[t][i]);
     uint64_t r = reduce_u128(acc.get(), br);
     if (la.has_add && p == 0) r = add_mod(r, la.add[i], br.q);
     out[((size_t)pc * la.l_out + i) * kN + k] = r;
