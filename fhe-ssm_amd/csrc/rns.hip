@@ -1286,7 +1286,7 @@ hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t 
         n_ks += keys[b] ? 1 : 0;
     }
     for (uint32_t t = 0; t < l; t++) a.pmod[t] = pmod[t];
-    ctx.n_keyswitch += (uint64_t)n_ks * n_inst * n_in;
+    // the babies' inner products are not counted as key switches: they have neither a ModUp nor a ModDown of their own
     // bytes: each input's extension and c0 (read once per key-switched baby: different automorphism blocks), the
     // keys and diagonals once, the giant sums written
     const double by = (double)n_inst * n_in * (n_ks * ((double)D * E + l) + (nb - n_ks) * 2.0 * l) +
