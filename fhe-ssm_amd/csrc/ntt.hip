@@ -89,7 +89,7 @@ __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPai
     const int col = tile * 16 + cl;
     uint64_t x[16];
 #pragma unroll
-    for (int k = 0; k < 16; k++) x[k] = a[col + 256 * (rg + 16 * k)];
+    for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&a[col + 256 * (rg + 16 * k)]);
     // stages 0..3: rows r = rg + 16k, pairs differ in bit (3-s) of k; twiddle (1<<s) + (k >> (4-s))
 #pragma unroll
     for (int s = 0; s < 4; s++) {
@@ -116,7 +116,7 @@ __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPai
         }
     }
 #pragma unroll
-    for (int k = 0; k < 16; k++) a[col + 256 * (16 * rg + k)] = x[k];
+    for (int k = 0; k < 16; k++) __builtin_nontemporal_store(x[k], &a[col + 256 * (16 * rg + k)]);
 }
 
 // ---------------------------------------------------------------- forward pass B (256-word blocks)
@@ -129,7 +129,7 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
     uint64_t* L = lds + bl * 272;
     uint64_t x[16];
 #pragma unroll
-    for (int k = 0; k < 16; k++) x[k] = blk[rl + 16 * k];
+    for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&blk[rl + 16 * k]);
     // stages 8+s, s = 0..3: r = rl + 16k; twiddle 2^(8+s) + b 2^s + (k >> (4-s))
 #pragma unroll
     for (int s = 0; s < 4; s++) {
@@ -167,7 +167,7 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
     for (int k = 0; k < 16; k++) L[17 * rl + k] = x[k];
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < 16; k++) blk[rl + 16 * k] = L[rl + 17 * k];
+    for (int k = 0; k < 16; k++) __builtin_nontemporal_store(L[rl + 17 * k], &blk[rl + 16 * k]);
 }
 
 // ---------------------------------------------------------------- inverse pass B (256-word blocks)
@@ -183,7 +183,7 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
     uint64_t* L = lds + bl * 272;
     uint64_t x[16];
 #pragma unroll
-    for (int k = 0; k < 16; k++) L[rl + 17 * k] = src[rl + 16 * k];
+    for (int k = 0; k < 16; k++) L[rl + 17 * k] = __builtin_nontemporal_load(&src[rl + 16 * k]);
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = L[17 * rl + k];
@@ -216,7 +216,7 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
         }
     }
 #pragma unroll
-    for (int k = 0; k < 16; k++) blk[rl + 16 * k] = x[k];
+    for (int k = 0; k < 16; k++) __builtin_nontemporal_store(x[k], &blk[rl + 16 * k]);
 }
 
 // ---------------------------------------------------------------- inverse pass A (strided columns)
@@ -228,7 +228,7 @@ __device__ __forceinline__ void inv_a_tile(uint64_t* __restrict__ a, const TwPai
     const int col = tile * 16 + cl;
     uint64_t x[16];
 #pragma unroll
-    for (int k = 0; k < 16; k++) x[k] = a[col + 256 * (16 * rg + k)];
+    for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&a[col + 256 * (16 * rg + k)]);
     // u = 0..3: r = 16 rg + k, pairs differ in bit u of k
 #pragma unroll
     for (int u = 0; u < 4; u++) {
@@ -264,7 +264,7 @@ __device__ __forceinline__ void inv_a_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
     for (int k = 0; k < 16; k++) {
         const uint64_t v = csub_s(x[k], q << 1);
-        a[col + 256 * (rg + 16 * k)] = csub_s(v, q);
+        __builtin_nontemporal_store(csub_s(v, q), &a[col + 256 * (rg + 16 * k)]);
     }
 }
 
