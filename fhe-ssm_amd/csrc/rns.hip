@@ -160,7 +160,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
 #pragma unroll
     for (int i = 0; i < NIN; i++) {
         const uint64_t q = primes[ba.in_prime[i]].q;
-        y[i] = shoup(src[(size_t)ba.in_off[i] * kN], qhinv[i].w, qhinv[i].wp, q);
+        y[i] = shoup(__builtin_nontemporal_load(&src[(size_t)ba.in_off[i] * kN]), qhinv[i].w, qhinv[i].wp, q);
         y0[i] = (uint32_t)y[i] & 0x3FFFFFFFu;
         y1[i] = (uint32_t)(y[i] >> 30);
     }
@@ -235,7 +235,8 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
             acc.lo += r;
             acc.hi += (acc.lo < r) ? 1u : 0u;
         }
-        dst[(size_t)ba.out_off[j] * kN] = reduce_u128(acc, br);
+        // streamed: read once, by the next NTT (nontemporal, so the L2 keeps what is reused)
+        __builtin_nontemporal_store(reduce_u128(acc, br), &dst[(size_t)ba.out_off[j] * kN]);
     };
     // two outputs per iteration: independent accumulation chains for the scheduler to interleave
     uint32_t j = 0;
