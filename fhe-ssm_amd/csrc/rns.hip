@@ -49,11 +49,12 @@ __global__ __launch_bounds__(256) void k_tensor(const uint64_t* __restrict__ a, 
     s1.add(a0, b1);
     s1.add(a1, b0);
     s2.add(a1, b1);
-    d01[o] = reduce_u128(s0.get(), br);
-    d01[o + P] = reduce_u128(s1.get(), br);
+    // outputs streamed (nontemporal): each is read once, by a later kernel
+    __builtin_nontemporal_store(reduce_u128(s0.get(), br), &d01[o]);
+    __builtin_nontemporal_store(reduce_u128(s1.get(), br), &d01[o + P]);
     const uint64_t v2 = reduce_u128(s2.get(), br);
-    d2[(size_t)c * P + (size_t)t * kN + k] = v2;
-    if (ta.d2e) ta.d2e[c * ta.d2e_bstride + (size_t)ta.ext_off[t] * kN + k] = v2;
+    __builtin_nontemporal_store(v2, &d2[(size_t)c * P + (size_t)t * kN + k]);
+    if (ta.d2e) __builtin_nontemporal_store(v2, &ta.d2e[c * ta.d2e_bstride + (size_t)ta.ext_off[t] * kN + k]);
 }
 
 // Sum of np tensor products per batch item: tab[(c np + j) 2 + 0/1] point at ciphertexts [2][l][N];
@@ -348,10 +349,12 @@ __global__ __launch_bounds__(256) void k_sub_scale(const uint64_t* __restrict__ 
     const uint32_t i = blockIdx.y, pc = blockIdx.z;  // pc = poly index over the batch
     const uint64_t q = primes[i].q;
     const size_t li = (size_t)i * kN + k;
-    const uint64_t d = sub_mod(x[pc * ca.x_pstride + li], y[pc * ca.y_pstride + li], q);
+    // x, y and out are streamed (nontemporal); the addend may be shared by several polys and is read normally
+    const uint64_t d = sub_mod(__builtin_nontemporal_load(&x[pc * ca.x_pstride + li]),
+                               __builtin_nontemporal_load(&y[pc * ca.y_pstride + li]), q);
     uint64_t v = shoup(d, ca.s[i].w, ca.s[i].wp, q);
     if (add && pc % ca.add_div == 0) v = add_mod(v, add[(pc / ca.add_group) * ca.add_pstride + li], q);
-    out[pc * ca.out_pstride + li] = v;
+    __builtin_nontemporal_store(v, &out[pc * ca.out_pstride + li]);
 }
 
 // centered lift of the dropped limb (coefficient form) into limbs 0..l-2:
@@ -361,7 +364,8 @@ __global__ __launch_bounds__(256) void k_lift_centered(const uint64_t* __restric
                                                        const PrimeInfo* __restrict__ primes) {
     const uint32_t k = blockIdx.x * 256 + threadIdx.x;
     const uint32_t i = blockIdx.y, pc = blockIdx.z;
-    tmp[((size_t)pc * n_out + i) * kN + k] = lift_centered(last[pc * last_pstride + k], ql, barrett_of(primes[i]));
+    __builtin_nontemporal_store(lift_centered(last[pc * last_pstride + k], ql, barrett_of(primes[i])),
+                                &tmp[((size_t)pc * n_out + i) * kN + k]);
 }
 
 // ------------------------------------------------------------------ elementwise helpers
