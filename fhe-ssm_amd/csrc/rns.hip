@@ -288,13 +288,15 @@ constexpr int kMaxDigits = 8;
 // The evk inner product of one extended word over D <= kMaxDigits digits: s0 += sum_d x[d xs] e[2d es],
 // s1 += sum_d x[d xs] e[(2d+1) es].  Every digit's loads are issued before the first product waits on them (a
 // load-multiply loop per digit makes each digit a separate round trip to memory).
+// kStreamX: the extension words are read once (no other item shares them): nontemporal loads.
+template <bool kStreamX = false>
 __device__ __forceinline__ void ks_dot(const uint64_t* __restrict__ x, size_t xs, const uint64_t* __restrict__ e,
                                        size_t es, uint32_t D, Acc& s0, Acc& s1) {
     uint64_t xv[kMaxDigits], e0[kMaxDigits], e1[kMaxDigits];
 #pragma unroll
     for (int d = 0; d < kMaxDigits; d++) {
         if (d < (int)D) {
-            xv[d] = x[(size_t)d * xs];
+            xv[d] = kStreamX ? __builtin_nontemporal_load(&x[(size_t)d * xs]) : x[(size_t)d * xs];
             e0[d] = e[((size_t)d * 2 + 0) * es];
             e1[d] = e[((size_t)d * 2 + 1) * es];
         }
@@ -505,15 +507,16 @@ __global__ __launch_bounds__(256) void k_mdr_combine_ks(const uint64_t* __restri
     const uint64_t* x = ext + (size_t)c * ia.D * ia.E * kN + li;
     const uint64_t* e = evk + li;
     Acc s0, s1;  // at most kMaxDigits = 8 terms: no intermediate fold
-    ks_dot(x, (size_t)ia.E * kN, e, (size_t)ia.T * kN, ia.D, s0, s1);
+    // ext, the addend, T and out are each touched once (nontemporal); the key is shared by the batch
+    ks_dot<true>(x, (size_t)ia.E * kN, e, (size_t)ia.T * kN, ia.D, s0, s1);
     const uint64_t xs[2] = {reduce_u128(s0.get(), br), reduce_u128(s1.get(), br)};
 #pragma unroll
     for (int p = 0; p < 2; p++) {
         const size_t pc = 2 * (size_t)c + p;
         uint64_t v = shoup(xs[p], ma.pinv[i].w, ma.pinv[i].wp, q);
-        if (add) v = add_mod(v, add[pc * ma.add_pstride + li], q);
-        v = sub_mod(v, T[pc * po + li], q);
-        out[pc * po + li] = shoup(v, ma.qlinv[i].w, ma.qlinv[i].wp, q);
+        if (add) v = add_mod(v, __builtin_nontemporal_load(&add[pc * ma.add_pstride + li]), q);
+        v = sub_mod(v, __builtin_nontemporal_load(&T[pc * po + li]), q);
+        __builtin_nontemporal_store(shoup(v, ma.qlinv[i].w, ma.qlinv[i].wp, q), &out[pc * po + li]);
     }
 }
 
@@ -526,7 +529,8 @@ struct LimbMap {
 __global__ __launch_bounds__(256) void k_scatter_limbs(const uint64_t* __restrict__ src, uint64_t src_bstride,
                                                        uint64_t* __restrict__ dst, uint64_t dst_bstride, LimbMap lm) {
     const uint32_t k = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y, c = blockIdx.z;
-    dst[c * dst_bstride + (size_t)lm.off[t] * kN + k] = src[c * src_bstride + (size_t)t * kN + k];
+    __builtin_nontemporal_store(__builtin_nontemporal_load(&src[c * src_bstride + (size_t)t * kN + k]),
+                                &dst[c * dst_bstride + (size_t)lm.off[t] * kN + k]);
 }
 
 // dst[c] = src[c] for up to 64 items of `words` words each (gathers scattered ciphertexts into one batch)
