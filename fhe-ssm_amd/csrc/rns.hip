@@ -326,10 +326,10 @@ __global__ __launch_bounds__(256) void k_ks_inner(const uint64_t* __restrict__ e
     const uint64_t* x = ext + (size_t)c * ia.D * ia.E * kN + (size_t)t * kN + k;
     const uint64_t* e = evk + (size_t)p * kN + k;
     Acc s0, s1;  // at most kMaxDigits = 8 terms: no intermediate fold
-    ks_dot(x, (size_t)ia.E * kN, e, (size_t)ia.T * kN, ia.D, s0, s1);
+    ks_dot<true>(x, (size_t)ia.E * kN, e, (size_t)ia.T * kN, ia.D, s0, s1);  // ext: one ciphertext's, read once
     uint64_t* o = acc + (size_t)c * 2 * ia.E * kN + (size_t)t * kN + k;
-    o[0] = reduce_u128(s0.get(), br);
-    o[(size_t)ia.E * kN] = reduce_u128(s1.get(), br);
+    __builtin_nontemporal_store(reduce_u128(s0.get(), br), &o[0]);
+    __builtin_nontemporal_store(reduce_u128(s1.get(), br), &o[(size_t)ia.E * kN]);
 }
 
 // ------------------------------------------------------------------ ModDown / rescale combines
@@ -389,7 +389,7 @@ __global__ __launch_bounds__(256) void k_automorph(const uint64_t* __restrict__ 
     const size_t base = ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * kN;
     const uint32_t e = (uint32_t)(((uint64_t)g * (2u * (__brev(k) >> (32 - kLogN)) + 1u)) & (2u * kN - 1u));
     const uint32_t src = __brev((e - 1u) >> 1) >> (32 - kLogN);
-    out[base + k] = in[base + src];
+    __builtin_nontemporal_store(__builtin_nontemporal_load(&in[base + src]), &out[base + k]);
 }
 
 // ------------------------------------------------------------------ list forms (one key per item)
@@ -428,8 +428,8 @@ __global__ __launch_bounds__(256) void k_ks_inner_list(ListPtrs ext, ListPtrs ev
     Acc s0, s1;  // at most kMaxDigits = 8 terms
     ks_dot(x, (size_t)ia.E * kN, e, (size_t)ia.T * kN, ia.D, s0, s1);
     uint64_t* o = acc + (size_t)c * 2 * ia.E * kN + (size_t)t * kN + k;
-    o[0] = reduce_u128(s0.get(), br);
-    o[(size_t)ia.E * kN] = reduce_u128(s1.get(), br);
+    __builtin_nontemporal_store(reduce_u128(s0.get(), br), &o[0]);
+    __builtin_nontemporal_store(reduce_u128(s1.get(), br), &o[(size_t)ia.E * kN]);
 }
 
 // ModDown combine of a key-switch list with the evk inner product of the Q limbs formed on the fly:
@@ -456,10 +456,13 @@ __global__ __launch_bounds__(256) void k_ks_sub_list(ListPtrs ext, ListPtrs evk,
     const size_t pw = (size_t)l * kN;  // words per poly of conv and out
     const uint64_t* cv = conv + (size_t)c * 2 * pw + li;
     uint64_t* o = out + (size_t)c * 2 * pw + li;
-    uint64_t v0 = sub_mod(shoup(reduce_u128(s0.get(), br), pa.pinv[i].w, pa.pinv[i].wp, q), cv[0], q);
+    uint64_t v0 = sub_mod(shoup(reduce_u128(s0.get(), br), pa.pinv[i].w, pa.pinv[i].wp, q),
+                          __builtin_nontemporal_load(&cv[0]), q);
     if (add) v0 = add_mod(v0, add[(size_t)(c / add_group) * add_stride + li], q);
-    o[0] = v0;
-    o[pw] = sub_mod(shoup(reduce_u128(s1.get(), br), pa.pinv[i].w, pa.pinv[i].wp, q), cv[pw], q);
+    __builtin_nontemporal_store(v0, &o[0]);
+    __builtin_nontemporal_store(sub_mod(shoup(reduce_u128(s1.get(), br), pa.pinv[i].w, pa.pinv[i].wp, q),
+                                        __builtin_nontemporal_load(&cv[pw]), q),
+                                &o[pw]);
 }
 
 // ---------------------------------------------------------------- ModDown fused with the following rescale
@@ -554,7 +557,7 @@ __global__ __launch_bounds__(256) void k_automorph_list(const uint64_t* __restri
     const size_t base = ((size_t)pc * l + i) * kN;
     const uint32_t e = (uint32_t)(((uint64_t)g * (2u * (__brev(k) >> (32 - kLogN)) + 1u)) & (2u * kN - 1u));
     const uint32_t src = __brev((e - 1u) >> 1) >> (32 - kLogN);
-    out[base + k] = in[base + src];
+    __builtin_nontemporal_store(__builtin_nontemporal_load(&in[base + src]), &out[base + k]);
 }
 
 // Rotations kept in the extended basis Q_l * P, summed per output (double-hoisted BSGS).  Output c ([2][E][N] at
@@ -1017,7 +1020,7 @@ __global__ __launch_bounds__(256) void k_lincomb(uint64_t* __restrict__ out, Lin
         if (t < (int)la.n_terms) acc.add(v[t], la.C[t][i]);
     uint64_t r = reduce_u128(acc.get(), br);
     if (la.has_add && p == 0) r = add_mod(r, la.add[i], br.q);
-    out[((size_t)pc * la.l_out + i) * kN + k] = r;
+    __builtin_nontemporal_store(r, &out[((size_t)pc * la.l_out + i) * kN + k]);
 }
 
 // multiply by X^(N/2) (slot-wise by +-i): evaluation slot k holds a(psi^(2 brev(k)+1)); X^(N/2) there is
