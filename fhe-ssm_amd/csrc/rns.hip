@@ -618,8 +618,8 @@ __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__
         v0 = add_mod(v0, o[0], q);
         v1 = add_mod(v1, o[(size_t)a.E * kN], q);
     }
-    o[0] = v0;
-    o[(size_t)a.E * kN] = v1;
+    __builtin_nontemporal_store(v0, &o[0]);
+    __builtin_nontemporal_store(v1, &o[(size_t)a.E * kN]);
 }
 
 // BSGS multiply-accumulate: babies [nb][2][l][N], diagonals [n_diag][l][N] (diagonal g*nb + j pairs with
@@ -668,8 +668,8 @@ __device__ __forceinline__ void mac_giants(const uint64_t* sb, const uint64_t* _
             r0 = add_mod(r0, o[0], br.q);
             r1 = add_mod(r1, o[P], br.q);
         }
-        o[0] = r0;
-        o[P] = r1;
+        __builtin_nontemporal_store(r0, &o[0]);
+        __builtin_nontemporal_store(r1, &o[P]);
     };
     for (uint32_t g = row; g < ng; g += 2 * kMacRows) {
         const uint32_t g2 = g + kMacRows;
@@ -920,8 +920,8 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
         }
         if (sl == 0 && G < a.ng) {
             uint64_t* o = dest(G);
-            o[0] = r0;
-            o[P] = r1;
+            __builtin_nontemporal_store(r0, &o[0]);
+            __builtin_nontemporal_store(r1, &o[P]);
         }
     }
 }
