@@ -27,6 +27,13 @@ class Params(ctypes.Structure):
                 ("q_bits", _u32), ("p_bits", _u32), ("scale", ctypes.c_double), ("device", _int)]
 
 
+class SeededPartHeader(ctypes.Structure):
+    """ckks_seeded_part_header: the header of a seeded key part file"""
+    _fields_ = [("version", _u32), ("expander", _u32), ("ring_dim", _u32), ("size_q", _u32), ("size_p", _u32),
+                ("num_part_q", _u32), ("num_per_part_q", _u32), ("count", _u32), ("key_tag", ctypes.c_char * 256),
+                ("moduli", _u64 * 128)]
+
+
 # name -> (restype, argtypes); the exported C ABI (kept in step with include/ckks_engine.h)
 SIGNATURES = {
     "ckks_last_error": (ctypes.c_char_p, []),
@@ -89,6 +96,10 @@ SIGNATURES = {
     "ckks_secret_coeffs": (_int, [_vp, _vp, _u32]),
     "ckks_keygen_relin": (_int, [_vp, _vp, _vp, _vp, _vp]),
     "ckks_keygen_automorphism": (_int, [_vp, _vp, _u32, _vp, _vp, _vp]),
+    "ckks_seeded_part_read_header": (_int, [ctypes.c_char_p, ctypes.POINTER(SeededPartHeader)]),
+    "ckks_seeded_part_indices": (_int, [ctypes.c_char_p, _vp, _u32, ctypes.POINTER(_u32)]),
+    "ckks_seeded_part_load_key": (_int, [_vp, ctypes.c_char_p, _u32, ctypes.POINTER(_u32), _vp]),
+    "ckks_seeded_part_write": (_int, [_vp, ctypes.c_char_p, ctypes.c_char_p, _u32, _vp, _vp, _vp]),
     "ckks_encode": (_int, [_vp, _vp, _vp, _u32, _u32, ctypes.c_double, _vp]),
     "ckks_encrypt": (_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp]),
     "ckks_decrypt_decode": (_int, [_vp, _vp, _vp, _u32, ctypes.c_double, _vp, _vp, _u32]),
@@ -368,6 +379,19 @@ class Context:
     def keygen_automorphism(self, sk, g: int, seed: bytes, eseed: bytes, d_evk) -> None:
         check(load().ckks_keygen_automorphism(self.h, sk.h, g, _seed(seed), _seed(eseed), d_evk))
 
+    def seeded_part_load_key(self, path: str, record: int, d_evk) -> int:
+        """key `record` of a seeded part file into d_evk; returns its automorphism index"""
+        idx = _u32(0)
+        check(load().ckks_seeded_part_load_key(self.h, path.encode(), record, ctypes.byref(idx), d_evk))
+        return int(idx.value)
+
+    def seeded_part_write(self, path: str, key_tag: str, indices, seeds, d_evks) -> None:
+        ix = np.ascontiguousarray(np.asarray(indices, dtype=np.uint32))
+        sd = np.frombuffer(b"".join(bytes(x) for x in seeds), dtype=np.uint8).copy()
+        assert sd.size == 32 * len(ix) and len(d_evks) == len(ix)
+        check(load().ckks_seeded_part_write(self.h, path.encode(), key_tag.encode(), len(ix), _ptr(ix) if len(ix) else None,
+                                            _ptr(sd) if len(ix) else None, _ptr_array(d_evks)))
+
     def encode(self, values, level: int, scale: float, d_pt) -> None:
         v = np.asarray(values)
         re = np.ascontiguousarray(v.real, dtype=np.float64)
@@ -425,6 +449,24 @@ def _ptr_array(ptrs):
         return None
     arr = (_vp * len(ptrs))(*ptrs)
     return ctypes.cast(arr, _vp)
+
+
+def seeded_part_header(path: str) -> dict:
+    """the header of a seeded key part file (host only: no context, no device)"""
+    h = SeededPartHeader()
+    check(load().ckks_seeded_part_read_header(path.encode(), ctypes.byref(h)))
+    n = h.size_q + h.size_p
+    return {"version": h.version, "expander": h.expander, "N": h.ring_dim, "size_q": h.size_q, "size_p": h.size_p,
+            "num_part_q": h.num_part_q, "num_per_part_q": h.num_per_part_q, "count": h.count,
+            "key_tag": h.key_tag.decode(), "moduli": [int(h.moduli[i]) for i in range(n)]}
+
+
+def seeded_part_indices(path: str) -> list:
+    count = _u32(0)
+    check(load().ckks_seeded_part_indices(path.encode(), None, 0, ctypes.byref(count)))
+    out = np.zeros(max(1, count.value), dtype=np.uint32)
+    check(load().ckks_seeded_part_indices(path.encode(), _ptr(out), count.value, ctypes.byref(count)))
+    return [int(x) for x in out[: count.value]]
 
 
 def _seed(seed: bytes):

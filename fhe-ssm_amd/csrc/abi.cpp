@@ -12,6 +12,7 @@
 #include "ckks_engine.h"
 #include "client.hpp"
 #include "engine.hpp"
+#include "keyfile.hpp"
 #include "ops.hpp"
 
 namespace fhe {
@@ -457,6 +458,64 @@ int ckks_keygen_automorphism(ckks_context* ctx, const ckks_secret* sk, uint32_t 
     if (ctx->c.K == 0) return fail(CKKS_EINVAL, "context has no special primes");
     return guarded([&] {
         fhe::keygen_automorphism(ctx->c, *sk->s, g, seed32, eseed32, 3.19, d_evk);
+        return CKKS_OK;
+    });
+}
+
+int ckks_seeded_part_read_header(const char* path, ckks_seeded_part_header* out) {
+    if (!path || !out) return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        const fhe::SeededPartHeader h = fhe::read_seeded_part_header(path);
+        if (h.key_tag.size() >= sizeof(out->key_tag)) return fail(CKKS_EINVAL, "seeded part: key tag too long");
+        if (h.moduli.size() > sizeof(out->moduli) / sizeof(out->moduli[0]))
+            return fail(CKKS_EINVAL, "seeded part: more moduli than the header struct holds");
+        std::memset(out, 0, sizeof(*out));
+        out->version = h.version;
+        out->expander = h.expander;
+        out->ring_dim = h.N;
+        out->size_q = h.size_q;
+        out->size_p = h.size_p;
+        out->num_part_q = h.num_part_q;
+        out->num_per_part_q = h.num_per_part_q;
+        out->count = h.count;
+        std::memcpy(out->key_tag, h.key_tag.data(), h.key_tag.size());
+        for (size_t i = 0; i < h.moduli.size(); i++) out->moduli[i] = h.moduli[i];
+        return CKKS_OK;
+    });
+}
+
+int ckks_seeded_part_indices(const char* path, uint32_t* indices, uint32_t cap, uint32_t* count) {
+    if (!path || !count || (cap && !indices)) return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        const std::vector<uint32_t> idx = fhe::seeded_part_indices(path);
+        *count = (uint32_t)idx.size();
+        for (size_t i = 0; i < idx.size() && i < cap; i++) indices[i] = idx[i];
+        return CKKS_OK;
+    });
+}
+
+int ckks_seeded_part_load_key(ckks_context* ctx, const char* path, uint32_t record, uint32_t* index, uint64_t* d_evk) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    if (!path || !d_evk) return fail(CKKS_EINVAL, "null argument");
+    if (ctx->c.K == 0) return fail(CKKS_EINVAL, "context has no special primes");
+    return guarded([&] {
+        fhe::load_seeded_part_key(ctx->c, path, record, index, d_evk);
+        return CKKS_OK;
+    });
+}
+
+int ckks_seeded_part_write(ckks_context* ctx, const char* path, const char* key_tag, uint32_t n_keys,
+                           const uint32_t* indices, const uint8_t* seeds, const uint64_t* const* d_evks) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    if (!path || !key_tag || (n_keys && (!indices || !seeds || !d_evks))) return fail(CKKS_EINVAL, "null argument");
+    if (ctx->c.K == 0) return fail(CKKS_EINVAL, "context has no special primes");
+    for (uint32_t i = 0; i < n_keys; i++) {
+        if (!d_evks[i]) return fail(CKKS_EINVAL, "null key");
+        if ((indices[i] & 1) == 0 || indices[i] >= 2 * fhe::kN)
+            return fail(CKKS_EINVAL, "automorphism index must be odd and < 2N");
+    }
+    return guarded([&] {
+        fhe::write_seeded_part(ctx->c, path, key_tag, n_keys, indices, seeds, d_evks);
         return CKKS_OK;
     });
 }

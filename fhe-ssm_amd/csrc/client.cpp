@@ -271,6 +271,19 @@ void keygen_switch(Context& ctx, const uint64_t* d_s_old, const int8_t* s_new, c
     HIPC(hipDeviceSynchronize());
 }
 
+// the a-halves of a key-switching key [dnum][2][L+K][N] (poly 1 of every digit) from its seed, as keygen_switch
+// draws them (seeded_keys.hpp:28-43: nonce {digit, limb, "SKEY"})
+void expand_key_a(Context& ctx, const uint8_t seed[32], uint64_t* d_evk) {
+    const uint32_t T = ctx.L + ctx.K;
+    std::vector<uint64_t> a((size_t)T * kN);
+    for (uint32_t d = 0; d < ctx.dnum; d++) {
+        parallel_for(T, [&](uint32_t i) {
+            fill_uniform(seed, d, i, kTagKey, ctx.moduli[i], a.data() + (size_t)i * kN, kN);
+        });
+        HIPC(hipMemcpy(d_evk + ((size_t)d * 2 + 1) * T * kN, a.data(), a.size() * 8, hipMemcpyHostToDevice));
+    }
+}
+
 // switching key from sk_from to sk_to; q_limbs > 0 keeps only Q limbs [0, q_limbs) (and P), zeroing the rest:
 // a key to a sparse secret is then published at the small modulus q_0..q_{q_limbs-1} P only
 void keygen_switch_secret(Context& ctx, const Secret& from, const Secret& to, const uint8_t seed[32],

@@ -16,6 +16,7 @@ struct Secret {
 void sample_ternary(const uint8_t seed[32], uint32_t h, int8_t* s);
 Secret* secret_create(Context& ctx, const uint8_t seed[32], uint32_t h);
 void secret_destroy(Secret* sk);
+void expand_key_a(Context& ctx, const uint8_t seed[32], uint64_t* d_evk);
 void keygen_switch(Context& ctx, const uint64_t* d_s_old, const int8_t* s_new, const uint8_t seed[32],
                    const uint8_t eseed[32], double sigma, uint64_t* d_evk);
 void keygen_switch_secret(Context& ctx, const Secret& from, const Secret& to, const uint8_t seed[32],

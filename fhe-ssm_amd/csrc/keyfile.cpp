@@ -1,0 +1,173 @@
+// keyfile.cpp -- seeded key-switching-key part files (the reference's "evalrot.partNNN.seeded.bin",
+// hpc_gpu_port/seeded_keys.hpp:44-51), read and written on the host.
+//
+// Layout (all integers little-endian): char[8] "FSSMSKY1"; u32 version = 1; u32 expander = 1; u32 N; u32 sizeQ;
+// u32 sizeP; u32 numPartQ; u32 numPerPartQ; u32 count; u32 keyTagLen; keyTag bytes; u64 moduli[sizeQ + sizeP];
+// then per key: u32 automorphism index; u8 seed[32]; u64 b[numPartQ][sizeQ + sizeP][N] (evaluation form).
+// A key's a-halves are not stored: they are the ChaCha20 expansion of the seed (nonce {digit, limb, "SKEY"},
+// seeded_keys.hpp:28-43), the same expander this engine's key generation uses, so a loaded key is the key that
+// was written word for word.  In device memory a key is [dnum][2][L + K][N] with b_d at poly 0 and a_d at poly 1.
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <fstream>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "client.hpp"
+#include "engine.hpp"
+#include "keyfile.hpp"
+
+namespace fhe {
+
+namespace {
+
+#define HIPC(expr)                                                                      \
+    do {                                                                                \
+        hipError_t _e = (expr);                                                         \
+        if (_e != hipSuccess) throw std::runtime_error(std::string(#expr) + ": " + hipGetErrorString(_e)); \
+    } while (0)
+
+constexpr char kMagic[8] = {'F', 'S', 'S', 'M', 'S', 'K', 'Y', '1'};
+constexpr uint32_t kVersion = 1, kExpander = 1;
+
+uint32_t get32(std::istream& is, const char* what) {
+    uint8_t b[4];
+    if (!is.read((char*)b, 4)) throw std::invalid_argument(std::string("seeded part: short ") + what);
+    return (uint32_t)b[0] | ((uint32_t)b[1] << 8) | ((uint32_t)b[2] << 16) | ((uint32_t)b[3] << 24);
+}
+
+uint64_t get64(std::istream& is, const char* what) {
+    uint8_t b[8];
+    if (!is.read((char*)b, 8)) throw std::invalid_argument(std::string("seeded part: short ") + what);
+    uint64_t v = 0;
+    for (int i = 0; i < 8; i++) v |= (uint64_t)b[i] << (8 * i);
+    return v;
+}
+
+void put32(std::ostream& os, uint32_t v) {
+    const uint8_t b[4] = {(uint8_t)v, (uint8_t)(v >> 8), (uint8_t)(v >> 16), (uint8_t)(v >> 24)};
+    os.write((const char*)b, 4);
+}
+
+void put64(std::ostream& os, uint64_t v) {
+    uint8_t b[8];
+    for (int i = 0; i < 8; i++) b[i] = (uint8_t)(v >> (8 * i));
+    os.write((const char*)b, 8);
+}
+
+uint64_t record_bytes(const SeededPartHeader& h) {
+    return 4 + 32 + (uint64_t)h.num_part_q * (h.size_q + h.size_p) * h.N * 8;
+}
+
+// the file's layout must be this context's: ring, chain, special primes and digit partition
+void check_layout(const Context& ctx, const SeededPartHeader& h) {
+    if (h.N != kN || h.size_q != ctx.L || h.size_p != ctx.K || h.num_part_q != ctx.dnum ||
+        h.num_per_part_q != ctx.alpha)
+        throw std::invalid_argument("seeded part: minted for another context (N, chain or digits differ)");
+    for (uint32_t i = 0; i < ctx.L + ctx.K; i++)
+        if (h.moduli[i] != ctx.moduli[i]) throw std::invalid_argument("seeded part: modulus chain differs");
+}
+
+}  // namespace
+
+SeededPartHeader read_seeded_part_header(const std::string& path) {
+    std::ifstream is(path, std::ios::binary);
+    if (!is.good()) throw std::invalid_argument("seeded part: cannot open " + path);
+    char magic[8];
+    if (!is.read(magic, 8) || std::memcmp(magic, kMagic, 8) != 0) throw std::invalid_argument("seeded part: bad magic");
+    SeededPartHeader h;
+    h.version = get32(is, "header");
+    h.expander = get32(is, "header");
+    if (h.version != kVersion || h.expander != kExpander)
+        throw std::invalid_argument("seeded part: unsupported version or expander");
+    h.N = get32(is, "header");
+    h.size_q = get32(is, "header");
+    h.size_p = get32(is, "header");
+    h.num_part_q = get32(is, "header");
+    h.num_per_part_q = get32(is, "header");
+    h.count = get32(is, "header");
+    const uint32_t tag_len = get32(is, "header");
+    if (tag_len > 4096) throw std::invalid_argument("seeded part: key tag too long");
+    if (h.N == 0 || (h.N & (h.N - 1)) || h.size_q + h.size_p > 4096 || h.num_part_q == 0)
+        throw std::invalid_argument("seeded part: implausible layout");
+    h.key_tag.assign(tag_len, '\0');
+    if (tag_len && !is.read(&h.key_tag[0], tag_len)) throw std::invalid_argument("seeded part: short key tag");
+    h.moduli.resize(h.size_q + h.size_p);
+    for (auto& m : h.moduli) m = get64(is, "moduli");
+    h.header_bytes = 8 + 4 * 9 + tag_len + 8 * (uint64_t)h.moduli.size();
+    // every record present
+    is.seekg(0, std::ios::end);
+    const uint64_t size = (uint64_t)is.tellg();
+    if (size < h.header_bytes + (uint64_t)h.count * record_bytes(h))
+        throw std::invalid_argument("seeded part: file shorter than its key count");
+    return h;
+}
+
+std::vector<uint32_t> seeded_part_indices(const std::string& path) {
+    const SeededPartHeader h = read_seeded_part_header(path);
+    std::ifstream is(path, std::ios::binary);
+    std::vector<uint32_t> idx(h.count);
+    for (uint32_t r = 0; r < h.count; r++) {
+        is.seekg((std::streamoff)(h.header_bytes + r * record_bytes(h)));
+        idx[r] = get32(is, "key record");
+    }
+    return idx;
+}
+
+void load_seeded_part_key(Context& ctx, const std::string& path, uint32_t record, uint32_t* index, uint64_t* d_evk) {
+    const SeededPartHeader h = read_seeded_part_header(path);
+    check_layout(ctx, h);
+    if (record >= h.count) throw std::invalid_argument("seeded part: record index past the key count");
+    std::ifstream is(path, std::ios::binary);
+    is.seekg((std::streamoff)(h.header_bytes + record * record_bytes(h)));
+    const uint32_t g = get32(is, "key record");
+    uint8_t seed[32];
+    if (!is.read((char*)seed, 32)) throw std::invalid_argument("seeded part: short seed");
+    const uint32_t T = ctx.L + ctx.K;
+    std::vector<uint64_t> b((size_t)T * kN);
+    for (uint32_t d = 0; d < ctx.dnum; d++) {
+        if (!is.read((char*)b.data(), (std::streamsize)(b.size() * 8)))
+            throw std::invalid_argument("seeded part: short b words");
+        for (uint32_t i = 0; i < T; i++)
+            for (uint32_t k = 0; k < kN; k += 4099)  // spot check: residues below their modulus
+                if (b[(size_t)i * kN + k] >= ctx.moduli[i]) throw std::invalid_argument("seeded part: b word >= q");
+        HIPC(hipMemcpy(d_evk + (size_t)d * 2 * T * kN, b.data(), b.size() * 8, hipMemcpyHostToDevice));
+    }
+    expand_key_a(ctx, seed, d_evk);
+    if (index) *index = g;
+}
+
+void write_seeded_part(Context& ctx, const std::string& path, const std::string& key_tag, uint32_t n,
+                       const uint32_t* indices, const uint8_t* seeds, const uint64_t* const* d_evks) {
+    if (key_tag.empty() || key_tag.size() > 4096) throw std::invalid_argument("seeded part: key tag length");
+    std::ofstream os(path, std::ios::binary | std::ios::trunc);
+    if (!os.good()) throw std::invalid_argument("seeded part: cannot create " + path);
+    const uint32_t T = ctx.L + ctx.K;
+    os.write(kMagic, 8);
+    put32(os, kVersion);
+    put32(os, kExpander);
+    put32(os, kN);
+    put32(os, ctx.L);
+    put32(os, ctx.K);
+    put32(os, ctx.dnum);
+    put32(os, ctx.alpha);
+    put32(os, n);
+    put32(os, (uint32_t)key_tag.size());
+    os.write(key_tag.data(), (std::streamsize)key_tag.size());
+    for (uint32_t i = 0; i < T; i++) put64(os, ctx.moduli[i]);
+    std::vector<uint64_t> b((size_t)T * kN);
+    for (uint32_t r = 0; r < n; r++) {
+        put32(os, indices[r]);
+        os.write((const char*)(seeds + 32 * (size_t)r), 32);
+        for (uint32_t d = 0; d < ctx.dnum; d++) {
+            HIPC(hipMemcpy(b.data(), d_evks[r] + (size_t)d * 2 * T * kN, b.size() * 8, hipMemcpyDeviceToHost));
+            os.write((const char*)b.data(), (std::streamsize)(b.size() * 8));
+        }
+    }
+    os.flush();
+    if (!os.good()) throw std::invalid_argument("seeded part: write failed: " + path);
+}
+
+}  // namespace fhe

@@ -285,6 +285,28 @@ int ckks_keygen_switch(ckks_context* ctx, const ckks_secret* sk_from, const ckks
                        const uint8_t* seed32, const uint8_t* eseed32, uint32_t q_limbs, uint64_t* d_evk);
 int ckks_keygen_automorphism(ckks_context* ctx, const ckks_secret* sk, uint32_t g, const uint8_t* seed32,
                              const uint8_t* eseed32, uint64_t* d_evk);
+
+/* ---- seeded key parts (the reference's evalrot.partNNN.seeded.bin, hpc_gpu_port/seeded_keys.hpp:44-51; written by
+ * writeSeededPart :302-334, read by readSeededPartHeader :338-360 and expandSeededKeys :374-415) ----------------
+ * A part file holds `count` automorphism keys as (index, 32-byte seed, b-halves); each key's a-halves are the
+ * ChaCha20 expansion of its seed (seeded_keys.hpp:28-43), so a loaded key equals the written one word for word.
+ * ckks_seeded_part_read_header  the header (host only, no context): format and truncation errors are CKKS_EINVAL
+ * ckks_seeded_part_indices      the automorphism index of each record (up to cap of them)
+ * ckks_seeded_part_load_key     record -> d_evk [dnum][2][L+K][N]; the file's N, chain, special primes and digit
+ *                               partition must be the context's (the loader's refusal of another context's parts)
+ * ckks_seeded_part_write        n keys of this context into one part file: indices, seeds [n][32] (the seed each
+ *                               key's a-halves were drawn from, the seed32 of ckks_keygen_automorphism), device keys */
+typedef struct ckks_seeded_part_header {
+    uint32_t version, expander, ring_dim, size_q, size_p, num_part_q, num_per_part_q, count;
+    char key_tag[256]; /* NUL-terminated (longer tags are refused) */
+    uint64_t moduli[128]; /* size_q + size_p of them */
+} ckks_seeded_part_header;
+int ckks_seeded_part_read_header(const char* path, ckks_seeded_part_header* out);
+int ckks_seeded_part_indices(const char* path, uint32_t* indices, uint32_t cap, uint32_t* count);
+int ckks_seeded_part_load_key(ckks_context* ctx, const char* path, uint32_t record, uint32_t* index, uint64_t* d_evk);
+int ckks_seeded_part_write(ckks_context* ctx, const char* path, const char* key_tag, uint32_t n_keys,
+                           const uint32_t* indices, const uint8_t* seeds, const uint64_t* const* d_evks);
+
 int ckks_encode(ckks_context* ctx, const double* re, const double* im, uint32_t n_slots, uint32_t level, double scale,
                 uint64_t* d_pt);
 int ckks_encrypt(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_pt, uint32_t level, const uint8_t* seed32,

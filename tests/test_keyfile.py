@@ -1,0 +1,146 @@
+"""Seeded key part files (the reference's evalrot.partNNN.seeded.bin, hpc_gpu_port/seeded_keys.hpp:44-51) through
+the C ABI.  CPU: the header reader against files written from the specification (tests/keypart_util.py), and its
+refusals.  GPU: a key loaded from such a file is b from the file and a = the ChaCha20 expansion of its seed (the
+oracle's sampler, pinned by RFC 8439 vectors in test_oracle); the engine's writer produces the specification's bytes
+for a generated key, and reading them back gives the key word for word."""
+import numpy as np
+import pytest
+
+from engine_loader import load_ckks
+from keypart_util import TAG_SKEY, part_bytes
+
+N16 = 16
+MOD16 = [97, 193, 257, 353, 449]  # any values: the header reader does not check the chain
+
+
+def _write(tmp_path, name, data):
+    p = tmp_path / name
+    p.write_bytes(data)
+    return str(p)
+
+
+def _small_records(n_keys, num_part_q=2, T=5, seed=1):
+    rng = np.random.default_rng(seed)
+    return [(int(2 * rng.integers(1, 1000) + 1), bytes(rng.integers(0, 256, 32, dtype=np.uint8)),
+             rng.integers(0, 97, (num_part_q, T, N16), dtype=np.uint64)) for _ in range(n_keys)]
+
+
+def test_header_and_indices_round_trip(tmp_path):
+    ckks = load_ckks()
+    recs = _small_records(3)
+    path = _write(tmp_path, "p.bin", part_bytes(N16, MOD16, 3, 2, 2, 2, "rot-tag", recs))
+    h = ckks.seeded_part_header(path)
+    assert (h["version"], h["expander"], h["N"], h["size_q"], h["size_p"]) == (1, 1, N16, 3, 2)
+    assert (h["num_part_q"], h["num_per_part_q"], h["count"], h["key_tag"]) == (2, 2, 3, "rot-tag")
+    assert h["moduli"] == MOD16
+    assert ckks.seeded_part_indices(path) == [r[0] for r in recs]
+
+
+def test_empty_part(tmp_path):
+    ckks = load_ckks()
+    path = _write(tmp_path, "e.bin", part_bytes(N16, MOD16, 3, 2, 2, 2, "t", []))
+    assert ckks.seeded_part_header(path)["count"] == 0
+    assert ckks.seeded_part_indices(path) == []
+
+
+@pytest.mark.parametrize("kind", ["magic", "version", "expander", "truncated", "count", "tag"])
+def test_header_refusals(tmp_path, kind):
+    ckks = load_ckks()
+    recs = _small_records(2)
+    kw = {}
+    if kind == "magic":
+        kw["magic"] = b"FSSMSKY2"
+    if kind == "version":
+        kw["version"] = 2
+    if kind == "expander":
+        kw["expander"] = 7
+    if kind == "count":
+        kw["count"] = 3  # one record more than the file holds
+    data = part_bytes(N16, MOD16, 3, 2, 2, 2, "x" * 5000 if kind == "tag" else "t", recs, **kw)
+    if kind == "truncated":
+        data = data[:-8]
+    path = _write(tmp_path, "bad.bin", data)
+    with pytest.raises(ckks.CkksError):
+        ckks.seeded_part_header(path)
+
+
+def test_missing_file(tmp_path):
+    ckks = load_ckks()
+    with pytest.raises(ckks.CkksError):
+        ckks.seeded_part_header(str(tmp_path / "nope.bin"))
+
+
+# ---------------------------------------------------------------- GPU
+N = 1 << 16
+
+
+@pytest.fixture(scope="module")
+def ckks():
+    return load_ckks()
+
+
+@pytest.fixture(scope="module")
+def ctx(ckks):
+    return ckks.Context(num_q=4, num_p=2, dnum=2, q_bits=54, p_bits=60)
+
+
+@pytest.mark.gpu
+def test_load_from_specification_file(tmp_path, ckks, ctx, oracle):
+    """b from the file, a expanded from the seed (nonce {digit, limb, "SKEY"}) -- against the oracle's sampler"""
+    T, D = ctx.L + ctx.K, ctx.dnum
+    q = np.array(ctx.moduli[:T], dtype=np.uint64)
+    rng = np.random.default_rng(7)
+    recs = []
+    for r in range(2):
+        b = rng.integers(0, 2**63, (D, T, N), dtype=np.uint64) % q[None, :, None]
+        recs.append((ckks.rotation_index(r + 1), bytes(rng.integers(0, 256, 32, dtype=np.uint8)), b))
+    path = _write(tmp_path, "k.bin", part_bytes(N, ctx.moduli[:T], ctx.L, ctx.K, D, (ctx.L + D - 1) // D, "auto",
+                                                 recs))
+    buf = ckks.DeviceBuffer(D * 2 * T * N * 8)
+    for r, (g, seed, b) in enumerate(recs):
+        assert ctx.seeded_part_load_key(path, r, buf.ptr) == g
+        got = buf.download((D, 2, T, N))
+        assert np.array_equal(got[:, 0], b)
+        for d in range(D):
+            for i in range(T):
+                assert np.array_equal(got[d, 1, i], oracle.fill_uniform(seed, d, i, TAG_SKEY, ctx.moduli[i], N)), (d, i)
+
+
+@pytest.mark.gpu
+def test_write_matches_specification_and_reloads(tmp_path, ckks, ctx):
+    T, D = ctx.L + ctx.K, ctx.dnum
+    sk = ctx.secret(b"K" * 32, 64)
+    seeds = [bytes([11 + i]) * 32 for i in range(2)]
+    gs = [ckks.rotation_index(1), ckks.rotation_index(-5)]
+    keys = []
+    for i, g in enumerate(gs):
+        k = ckks.DeviceBuffer(D * 2 * T * N * 8)
+        ctx.keygen_automorphism(sk, g, seeds[i], bytes([40 + i]) * 32, k.ptr)
+        keys.append(k)
+    path = str(tmp_path / "w.bin")
+    ctx.seeded_part_write(path, "mytag", gs, seeds, [k.ptr for k in keys])
+    words = [k.download((D, 2, T, N)) for k in keys]
+    want = part_bytes(N, ctx.moduli[:T], ctx.L, ctx.K, D, (ctx.L + D - 1) // D, "mytag",
+                      [(g, s, w[:, 0]) for g, s, w in zip(gs, seeds, words)])
+    assert open(path, "rb").read() == want
+    back = ckks.DeviceBuffer(D * 2 * T * N * 8)
+    for r in range(2):
+        assert ctx.seeded_part_load_key(path, r, back.ptr) == gs[r]
+        assert np.array_equal(back.download((D, 2, T, N)), words[r]), r
+
+
+@pytest.mark.gpu
+def test_load_refuses_another_context(tmp_path, ckks, ctx):
+    T, D = ctx.L + ctx.K, ctx.dnum
+    other = list(ctx.moduli[:T])
+    other[1] = other[2]
+    b = np.zeros((D, T, N), dtype=np.uint64)
+    path = _write(tmp_path, "o.bin", part_bytes(N, other, ctx.L, ctx.K, D, (ctx.L + D - 1) // D, "t",
+                                                 [(5, b"\0" * 32, b)]))
+    buf = ckks.DeviceBuffer(D * 2 * T * N * 8)
+    with pytest.raises(ckks.CkksError):
+        ctx.seeded_part_load_key(path, 0, buf.ptr)
+    path2 = _write(tmp_path, "o2.bin", part_bytes(N, ctx.moduli[:T], ctx.L, ctx.K, D + 1, 1, "t",
+                                                  [(5, b"\0" * 32, np.zeros((D + 1, T, N), np.uint64))]))
+    with pytest.raises(ckks.CkksError):
+        ctx.seeded_part_load_key(path2, 0, buf.ptr)
