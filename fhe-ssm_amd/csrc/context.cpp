@@ -145,6 +145,26 @@ void context_init(Context& c, const std::vector<uint64_t>& q, const std::vector<
     };
     up((void**)&c.d_tw, tw.data(), tw.size() * sizeof(TwPair));
     up((void**)&c.d_itw, itw.data(), itw.size() * sizeof(TwPair));
+    // pass B's tables: within each block of 16 * 2^m entries of a strided stage, entry rl 2^m + kk moves to kk 16 + rl
+    // (forward stages 8 + s, s = 5..7, m = s - 4, blocks of 2^s at 2^(8+s) + b 2^s; inverse t = 2^u, u = 0..2,
+    // m = 3 - u, blocks of 2^(7-u) at 2^(15-u) + b 2^(7-u))
+    std::vector<TwPair> twb(tw), itwb(itw);
+    for (uint32_t i = 0; i < T; i++) {
+        const size_t base = (size_t)i * kN;
+        for (uint32_t m = 1; m <= 3; m++) {
+            const size_t f0 = (size_t)1 << (12 + m), i0 = (size_t)1 << (12 + m);  // forward s = 4 + m; inverse u = 3 - m
+            const uint32_t bs = 16u << m;
+            for (uint32_t b = 0; b < 256; b++)
+                for (uint32_t rl = 0; rl < 16; rl++)
+                    for (uint32_t kk = 0; kk < (1u << m); kk++) {
+                        twb[base + f0 + (size_t)b * bs + kk * 16 + rl] = tw[base + f0 + (size_t)b * bs + (rl << m) + kk];
+                        itwb[base + i0 + (size_t)b * bs + kk * 16 + rl] =
+                            itw[base + i0 + (size_t)b * bs + (rl << m) + kk];
+                    }
+        }
+    }
+    up((void**)&c.d_twb, twb.data(), twb.size() * sizeof(TwPair));
+    up((void**)&c.d_itwb, itwb.data(), itwb.size() * sizeof(TwPair));
     up((void**)&c.d_primes, c.primes.data(), c.primes.size() * sizeof(PrimeInfo));
 }
 
@@ -173,6 +193,8 @@ void prof_clear(const Context& ctx) {
 void context_release(Context& c) {
     (void)hipFree(c.d_tw);
     (void)hipFree(c.d_itw);
+    (void)hipFree(c.d_twb);
+    (void)hipFree(c.d_itwb);
     (void)hipFree(c.d_primes);
     for (auto& kv : c.job_cache) (void)hipFree(kv.second.first);
     prof_clear(c);
@@ -191,7 +213,7 @@ void context_release(Context& c) {
     c.job_cache.clear();
     c.bconv_cache.clear();
     c.scratch.clear();
-    c.d_tw = c.d_itw = nullptr;
+    c.d_tw = c.d_itw = c.d_twb = c.d_itwb = nullptr;
     c.d_primes = nullptr;
 }
 

@@ -72,6 +72,10 @@ struct Context {
     std::vector<PrimeInfo> primes;
     TwPair* d_tw = nullptr;   // [L+K][N] forward table (brev order)
     TwPair* d_itw = nullptr;  // [L+K][N] inverse table (brev order)
+    // the NTT pass-B copies of d_tw / d_itw: the same pairs, the entries of pass B's strided stages (forward stages
+    // 13..15, inverse stages with t = 1, 2, 4) stored per 256-word block as [k][lane] (see ntt.hip)
+    TwPair* d_twb = nullptr;
+    TwPair* d_itwb = nullptr;
     PrimeInfo* d_primes = nullptr;
     NttMode ntt_mode = NttMode::TwoPass;
     // cached device job lists keyed by a shape string (list, distinct primes in it)

@@ -147,7 +147,9 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = L[17 * rl + k];
-    // stages 8+s, s = 4..7: r = 16 rl + k; twiddle 2^(8+s) + b 2^s + (r >> (8-s))
+    // stages 8+s, s = 4..7: r = 16 rl + k; twiddle 2^(8+s) + b 2^s + (r >> (8-s)) = ... + rl 2^(s-4) + (k >> (8-s)).
+    // Pass B's table (twb) stores each block's 2^s entries of these stages as [k >> (8-s)][rl], so the 16 lanes of a
+    // block read 16 consecutive pairs per load instead of 16 pairs 2^(s-4) apart (one cache line per lane)
 #pragma unroll
     for (int s = 4; s < 8; s++) {
         const int h = 128 >> s;
@@ -155,7 +157,7 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            ct_bfly(x[k], x[k + h], t[(16 * rl + k) >> (8 - s)], q4, nq);
+            ct_bfly(x[k], x[k + h], t[((k >> (8 - s)) << 4) + rl], q4, nq);
         }
     }
     // canonical [0, q), then transpose through LDS for coalesced stores (direct 16-byte stores of each
@@ -187,7 +189,8 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = L[17 * rl + k];
-    // u = 0..3: r = 16 rl + k, pairs differ in bit u of k
+    // u = 0..3: r = 16 rl + k, pairs differ in bit u of k; twiddle ... + (r >> (u+1)) = ... + rl 2^(3-u) + (k >> (u+1)),
+    // stored by pass B's table (twb) as [k >> (u+1)][rl] within each block (consecutive pairs for a block's lanes)
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int h = 1 << u;
@@ -195,7 +198,7 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            gs_bfly(x[k], x[k + h], t[(16 * rl + k) >> (u + 1)], q4, nq);
+            gs_bfly(x[k], x[k + h], t[((k >> (u + 1)) << 4) + rl], q4, nq);
         }
     }
     __syncthreads();
@@ -309,6 +312,7 @@ constexpr int kFusedGroups = 2;
 
 __global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_fwd_fused(uint64_t* data, JobSpec js,
                                                                               const TwPair* tw_all,
+                                                                              const TwPair* twb_all,
                                                                               const PrimeInfo* primes) {
     __shared__ uint64_t lds[kFusedGroups * kLdsWords];
     uint32_t off, prime;
@@ -323,13 +327,14 @@ __global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_fwd_fused(ui
         __syncthreads();
     }
     for (int t = grp; t < 16; t += kFusedGroups) {
-        fwd_b_tile(a, tw, q, t, g, L);
+        fwd_b_tile(a, twb_all + (size_t)prime * kN, q, t, g, L);
         __syncthreads();
     }
 }
 
 __global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_inv_fused(uint64_t* data, JobSpec js,
                                                                               const TwPair* tw_all,
+                                                                              const TwPair* twb_all,
                                                                               const PrimeInfo* primes) {
     __shared__ uint64_t lds[kFusedGroups * kLdsWords];
     uint32_t off, prime;
@@ -341,7 +346,7 @@ __global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_inv_fused(ui
     uint64_t* L = lds + grp * kLdsWords;
     const uint64_t* in = job_src(js, blockIdx.x, data, off);
     for (int t = grp; t < 16; t += kFusedGroups) {
-        inv_b_tile(a, in, tw, P.q, t, g, L);
+        inv_b_tile(a, in, twb_all + (size_t)prime * kN, P.q, t, g, L);
         __syncthreads();
     }
     for (int t = grp; t < 16; t += kFusedGroups) {
@@ -353,7 +358,7 @@ __global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_inv_fused(ui
 }  // namespace
 
 hipError_t launch_ntt_kernels(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,
-                              NttMode mode, const TwPair* tw, hipStream_t st);
+                              NttMode mode, const TwPair* tw, const TwPair* twb, hipStream_t st);
 
 hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js_in, uint32_t n_jobs, bool inverse,
                       NttMode mode, hipStream_t st) {
@@ -367,34 +372,36 @@ hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js_in, 
         }
     }
     const TwPair* tw = inverse ? ctx.d_itw : ctx.d_tw;
+    const TwPair* twb = inverse ? ctx.d_itwb : ctx.d_twb;
     // algorithmic bytes: every limb read and written once, each prime's table (w, w') read once
     const double bytes = (double)n_jobs * 2.0 * kN * 8 + (double)js.n_primes * kN * sizeof(TwPair);
     const char* name = mode == NttMode::Fused ? (inverse ? "ntt_inv_fused" : "ntt_fwd_fused")
                                               : (inverse ? "ntt_inv_2pass" : "ntt_fwd_2pass");
     const int pi = prof_begin(ctx, name, bytes, st);
-    hipError_t err = launch_ntt_kernels(ctx, data, js, n_jobs, inverse, mode, tw, st);
+    hipError_t err = launch_ntt_kernels(ctx, data, js, n_jobs, inverse, mode, tw, twb, st);
     prof_end(ctx, pi, st);
     return err;
 }
 
 hipError_t launch_ntt_kernels(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,
-                              NttMode mode, const TwPair* tw, hipStream_t st) {
+                              NttMode mode, const TwPair* tw, const TwPair* twb, hipStream_t st) {
     if (mode == NttMode::Fused) {
         if (inverse)
             hipLaunchKernelGGL(k_ntt_inv_fused, dim3(n_jobs), dim3(kTileThreads * kFusedGroups), 0, st, data, js, tw,
-                               ctx.d_primes);
+                               twb, ctx.d_primes);
         else
             hipLaunchKernelGGL(k_ntt_fwd_fused, dim3(n_jobs), dim3(kTileThreads * kFusedGroups), 0, st, data, js, tw,
-                               ctx.d_primes);
+                               twb, ctx.d_primes);
         return hipGetLastError();
     }
+    // pass B reads pass B's table (the same pairs, its last four stages' entries reordered per block)
     const dim3 grid(16, n_jobs), block(kTileThreads);
     if (inverse) {
-        hipLaunchKernelGGL(k_ntt_inv_b, grid, block, 0, st, data, js, tw, ctx.d_primes);
+        hipLaunchKernelGGL(k_ntt_inv_b, grid, block, 0, st, data, js, twb, ctx.d_primes);
         hipLaunchKernelGGL(k_ntt_inv_a, grid, block, 0, st, data, js, tw, ctx.d_primes);
     } else {
         hipLaunchKernelGGL(k_ntt_fwd_a, grid, block, 0, st, data, js, tw, ctx.d_primes);
-        hipLaunchKernelGGL(k_ntt_fwd_b, grid, block, 0, st, data, js, tw, ctx.d_primes);
+        hipLaunchKernelGGL(k_ntt_fwd_b, grid, block, 0, st, data, js, twb, ctx.d_primes);
     }
     return hipGetLastError();
 }
