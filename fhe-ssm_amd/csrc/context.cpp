@@ -163,6 +163,18 @@ void context_init(Context& c, const std::vector<uint64_t>& q, const std::vector<
                     }
         }
     }
+    // and the broadcast stages (forward s = 1..3, inverse u = 4..6): entry b 2^s + j of a region moves to j 256 + b
+    for (uint32_t i = 0; i < T; i++) {
+        const size_t base = (size_t)i * kN;
+        for (uint32_t s = 1; s <= 3; s++) {
+            const size_t r0 = (size_t)256 << s;  // forward stage 8 + s; the inverse u = 7 - s has the same region
+            for (uint32_t b = 0; b < 256; b++)
+                for (uint32_t j = 0; j < (1u << s); j++) {
+                    twb[base + r0 + (size_t)j * 256 + b] = tw[base + r0 + ((size_t)b << s) + j];
+                    itwb[base + r0 + (size_t)j * 256 + b] = itw[base + r0 + ((size_t)b << s) + j];
+                }
+        }
+    }
     up((void**)&c.d_twb, twb.data(), twb.size() * sizeof(TwPair));
     up((void**)&c.d_itwb, itwb.data(), itwb.size() * sizeof(TwPair));
     up((void**)&c.d_primes, c.primes.data(), c.primes.size() * sizeof(PrimeInfo));

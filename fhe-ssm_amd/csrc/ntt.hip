@@ -130,15 +130,16 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
     uint64_t x[16];
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&blk[rl + 16 * k]);
-    // stages 8+s, s = 0..3: r = rl + 16k; twiddle 2^(8+s) + b 2^s + (k >> (4-s))
+    // stages 8+s, s = 0..3: r = rl + 16k; twiddle 2^(8+s) + b 2^s + (k >> (4-s)), which pass B's table stores at
+    // 2^(8+s) + (k >> (4-s)) 256 + b (the four blocks of a wave read adjacent pairs)
 #pragma unroll
     for (int s = 0; s < 4; s++) {
         const int h = 8 >> s;
-        const TwPair* t = tw + (256 << s) + (b << s);
+        const TwPair* t = tw + (256 << s) + b;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            ct_bfly(x[k], x[k + h], t[k >> (4 - s)], q4, nq);
+            ct_bfly(x[k], x[k + h], t[(k >> (4 - s)) << 8], q4, nq);
         }
     }
     // LDS word index of r: r + (r >> 4)
@@ -207,15 +208,16 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = L[rl + 17 * k];
-    // u = 4..7: r = rl + 16k, pairs differ in bit (u-4) of k; r >> (u+1) = k >> (u-3)
+    // u = 4..7: r = rl + 16k, pairs differ in bit (u-4) of k; r >> (u+1) = k >> (u-3); pass B's table stores twiddle
+    // 2^(15-u) + b 2^(7-u) + j at 2^(15-u) + j 256 + b (the four blocks of a wave read adjacent pairs)
 #pragma unroll
     for (int u = 4; u < 8; u++) {
         const int h = 1 << (u - 4);
-        const TwPair* t = tw + (32768 >> u) + (b << (7 - u));
+        const TwPair* t = tw + (32768 >> u) + b;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            gs_bfly(x[k], x[k + h], t[k >> (u - 3)], q4, nq);
+            gs_bfly(x[k], x[k + h], t[(k >> (u - 3)) << 8], q4, nq);
         }
     }
 #pragma unroll
