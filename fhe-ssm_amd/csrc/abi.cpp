@@ -657,8 +657,12 @@ int ckks_linear_transform_hoisted(ckks_context* ctx, const uint64_t* const* d_in
         if (!d_in[i]) return fail(CKKS_EINVAL, "null input");
     for (uint32_t i = 0; i < n_baby; i++)
         if (baby_steps[i] && !d_baby_evks[i]) return fail(CKKS_EINVAL, "null baby key");
-    for (uint32_t i = 0; i < n_giant; i++)
+    uint32_t n_zero = 0;
+    for (uint32_t i = 0; i < n_giant; i++) {
         if (giant_steps[i] && !d_giant_evks[i]) return fail(CKKS_EINVAL, "null giant key");
+        n_zero += giant_steps[i] == 0 ? 1 : 0;
+    }
+    if (n_zero > 1) return fail(CKKS_EINVAL, "at most one giant step 0");
     return guarded([&] {
         fhe::bsgs_dh_batch(ctx->c, d_in, 1, n_in, level, d_diags, n_baby, baby_steps, d_baby_evks, n_giant,
                            giant_steps, d_giant_evks, n_out, d_out, (hipStream_t)stream, false);

@@ -69,9 +69,8 @@ hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t 
                               hipStream_t st);
 hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
                              uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_out,
-                             uint32_t nt, uint32_t A, uint32_t M, uint32_t l, const TwPair* pmod, uint64_t* dst,
-                             hipStream_t st, uint32_t R = 1, uint32_t c_off = 0, uint64_t s_lo = 0,
-                             bool accumulate = false);
+                             uint32_t nt, uint32_t A, uint32_t M, uint32_t l, uint64_t* dst, hipStream_t st,
+                             uint32_t R = 1, uint32_t c_off = 0, uint64_t s_lo = 0, bool accumulate = false);
 hipError_t launch_mul_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
                             uint32_t l, uint64_t pt_bstride, uint32_t log_rep, hipStream_t st);
 hipError_t launch_add_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
@@ -303,14 +302,18 @@ void ks_inner(Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* 
 // x: [n_polys][E][N] evaluation form over Q_l * P (P limbs are overwritten: they are transformed to
 // coefficients in place).  out: [n_polys][l][N] = (x_Q - BConv_{P->Q}(x_P)) * P^-1 (+ add).
 void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
-                     hipStream_t st, uint32_t add_div, int64_t add_pstride, uint32_t add_group) {
+                     hipStream_t st, uint32_t add_div, int64_t add_pstride, uint32_t add_group, uint32_t x_plimbs) {
     check_level(ctx, l);
     const uint32_t E = l + ctx.K, K = ctx.K;
     if (K == 0) throw std::invalid_argument("ModDown needs special primes");
+    const uint32_t xs = x_plimbs ? x_plimbs : E;  // limbs between the polys of x
+    if (xs < E) throw std::invalid_argument("ModDown: poly stride below the extended limb count");
     std::vector<Job> jobs;
     for (uint32_t pc = 0; pc < n_polys; pc++)
-        for (uint32_t k = 0; k < K; k++) jobs.push_back(Job{pc * E + l + k, ctx.L + k});
-    const JobSpec js = cached_jobs(ctx, "mdP:" + std::to_string(n_polys) + ":" + std::to_string(l), std::move(jobs));
+        for (uint32_t k = 0; k < K; k++) jobs.push_back(Job{pc * xs + l + k, ctx.L + k});
+    const JobSpec js = cached_jobs(ctx, "mdP:" + std::to_string(n_polys) + ":" + std::to_string(l) + ":" +
+                                            std::to_string(xs),
+                                   std::move(jobs));
     HIPX(launch_ntt(ctx, x, js, n_polys * K, true, ctx.ntt_mode, st));
     std::vector<uint32_t> in_idx, in_off, out_idx, out_off;
     for (uint32_t k = 0; k < K; k++) {
@@ -323,7 +326,7 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
     }
     const BConvPlan& plan = bconv_plan(ctx, in_idx, out_idx, ctx.moddown_exact);
     uint64_t* conv = (uint64_t*)ws_get(ctx, WS_CONV, (size_t)n_polys * l * W * 8);
-    HIPX(launch_bconv(ctx, plan, x, (uint64_t)E * W, in_off.data(), conv, (uint64_t)l * W, out_off.data(), n_polys,
+    HIPX(launch_bconv(ctx, plan, x, (uint64_t)xs * W, in_off.data(), conv, (uint64_t)l * W, out_off.data(), n_polys,
                       st));
     HIPX(launch_ntt(ctx, conv, regular_jobs(n_polys, out_idx), n_polys * l, false, ctx.ntt_mode, st));
     std::vector<TwPair> pinv(l);
@@ -335,7 +338,7 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
         pinv[i] = TwPair{v, shoup_companion(v, q)};
     }
     const uint64_t aps = add_pstride < 0 ? (uint64_t)add_div * l * W : (uint64_t)add_pstride;
-    HIPX(launch_sub_scale(ctx, x, (uint64_t)E * W, conv, (uint64_t)l * W, add, aps, add_div, out, (uint64_t)l * W,
+    HIPX(launch_sub_scale(ctx, x, (uint64_t)xs * W, conv, (uint64_t)l * W, add, aps, add_div, out, (uint64_t)l * W,
                           n_polys, l, pinv.data(), st, add_group));
 }
 
@@ -848,12 +851,13 @@ void bsgs_dh_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uin
     std::vector<const uint64_t*> rk;
     std::vector<uint32_t> rg;
     for (uint32_t g = 0; g < ng; g++) {
-        if (gsteps[g] == 0 && g0 < 0) {
+        if (gsteps[g] == 0) {
+            if (g0 >= 0) throw std::invalid_argument("double-hoisted BSGS: at most one giant step 0");
             g0 = (int32_t)g;
             continue;
         }
-        rk.push_back(gsteps[g] ? gevk[g] : nullptr);
-        rg.push_back(gsteps[g] ? rotation_index(gsteps[g]) : 1);
+        rk.push_back(gevk[g]);
+        rg.push_back(rotation_index(gsteps[g]));
     }
     const uint32_t ngr = (uint32_t)rk.size();
     uint64_t* T = (uint64_t*)ws_get(ctx, WS_GROT, (size_t)n_o * cte * 8);
@@ -871,21 +875,23 @@ void bsgs_dh_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uin
                                 n_out, ng, g0, l, pmod.data(), S, T, id_inst, id_o, (uint32_t)delta, st));
     }
     if (ngr) {
-        uint64_t* SQ = (uint64_t*)ws_get(ctx, WS_SUM, (size_t)n_o * ngr * ctw * 8);
-        moddown_inplace(ctx, S, 2 * n_o * ngr, l, nullptr, SQ, st);
+        // only the c1 halves come down (the key switch needs c1 in Q_l); the c0 halves join the rotations in Q_l P as
+        // they are: S0 = P SQ0 + [S0]_P, and the final ModDown divides that remainder by P
+        uint64_t* SQ1 = (uint64_t*)ws_get(ctx, WS_SUM, (size_t)n_o * ngr * l * W * 8);
+        moddown_inplace(ctx, S + (size_t)E * W, n_o * ngr, l, nullptr, SQ1, st, 1, -1, 0, 2 * E);
         // outputs in chunks whose extensions fit a bounded buffer
         const uint32_t chunk = std::max<uint32_t>(1, 32 / ngr);
         uint64_t* ext2 = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)std::min(chunk, n_o) * ngr * exw * 8);
         const bool acc = g0 >= 0;
         for (uint32_t o0 = 0; o0 < n_o; o0 += chunk) {
             const uint32_t m = std::min(chunk, n_o - o0);
-            const uint64_t* src = SQ + (size_t)o0 * ngr * ctw;
-            modup(ctx, src + (size_t)l * W, ext2, m * ngr, l, st, ctw);
+            modup(ctx, SQ1 + (size_t)o0 * ngr * l * W, ext2, m * ngr, l, st);
+            const uint64_t* src = S + (size_t)o0 * ngr * cte;
             if (by_output)
-                HIPX(launch_qp_rot_sum(ctx, ext2, exw, src, ctw, rk.data(), rg.data(), m, ngr, 1, ngr, l, pmod.data(),
-                                       T, st, n_out, o0, (uint64_t)n_inst * cte, acc));
+                HIPX(launch_qp_rot_sum(ctx, ext2, exw, src, cte, rk.data(), rg.data(), m, ngr, 1, ngr, l, T, st, n_out,
+                                       o0, (uint64_t)n_inst * cte, acc));
             else
-                HIPX(launch_qp_rot_sum(ctx, ext2, exw, src, ctw, rk.data(), rg.data(), m, ngr, 1, ngr, l, pmod.data(),
+                HIPX(launch_qp_rot_sum(ctx, ext2, exw, src, cte, rk.data(), rg.data(), m, ngr, 1, ngr, l,
                                        T + (size_t)o0 * cte, st, 1, 0, 0, acc));
         }
     }

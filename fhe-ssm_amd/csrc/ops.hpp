@@ -44,8 +44,10 @@ void ks_inner(Context& ctx, const uint64_t* ext, const uint64_t* evk, uint64_t* 
 // add (optional): applied to output polys pc with pc % add_div == 0, at add + (pc / add_div) * add_div * l * N
 // add_pstride < 0: add_div * l * N (the addend is a ciphertext batch); 0: one addend for every poly
 // add_group (0 = add_div): polys pc with pc % add_div == 0 take the addend at (pc / add_group) * add_pstride
+// x_plimbs (0 = E): limbs between consecutive polys of x (2E takes every other poly of a QP ciphertext batch)
 void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
-                     hipStream_t st, uint32_t add_div = 1, int64_t add_pstride = -1, uint32_t add_group = 0);
+                     hipStream_t st, uint32_t add_div = 1, int64_t add_pstride = -1, uint32_t add_group = 0,
+                     uint32_t x_plimbs = 0);
 void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
                      hipStream_t st, const uint64_t* ext = nullptr, const uint64_t* evk = nullptr);
 void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,

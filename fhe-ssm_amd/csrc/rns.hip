@@ -560,14 +560,16 @@ __global__ __launch_bounds__(256) void k_automorph_list(const uint64_t* __restri
     __builtin_nontemporal_store(__builtin_nontemporal_load(&in[base + src]), &out[base + k]);
 }
 
-// Rotations kept in the extended basis Q_l * P, summed per output (double-hoisted BSGS).  Output c ([2][E][N] at
-// dst + c 2 E N) is the sum over its nt terms j of
-//   Auto_g( <ext_x, evk>_0 + P c0_x,  <ext_x, evk>_1 )    (a key-switched term: (P c0 + ks0, ks1) encrypts P m over
-//                                                          Q_l * P, the rotation without its ModDown)
-//   Auto_g( P c0_x, P c1_x )                              (an identity term, evk null: zero on the P limbs)
-// with x = (c / A) M + j the term's input (its ModUp extension [D][E][N] at ext + x ext_stride, the ciphertext
-// [2][l][N] at src + x src_stride) and key index c % A + j (evk, g).  Output c goes to dst + (u / R) s_hi + (u % R)
-// s_lo, u = c + c_off (R = 1, s_hi = 2 E N: contiguous).  The evk inner product is formed at the
+// Giant rotations kept in the extended basis Q_l * P, summed per output (double-hoisted BSGS).  Each term's input is a
+// giant inner sum S_x = (S0, S1) over Q_l * P encrypting P m; its c1 came down to Q_l once (SQ1 = ModDown(S1)) and
+// was extended again (ext_x).  Output c ([2][E][N] at dst + c 2 E N) is the sum over its nt terms j of
+//   Auto_g( <ext_x, evk>_0 + S0_x,  <ext_x, evk>_1 )     (a key-switched term: S0 = P SQ0 + r with r = [S0]_P, so
+//                                                         this encrypts P Auto_g(m) plus r, which the final ModDown
+//                                                         divides by P -- S0 itself needs no ModDown)
+//   Auto_g( S0_x, S1_x )                                 (an identity term, evk null)
+// with x = (c / A) M + j the term's input (its ModUp extension [D][E][N] at ext + x ext_stride, S_x [2][E][N] at
+// src + x src_stride) and key index c % A + j (evk, g).  Output c goes to dst + (u / R) s_hi + (u % R) s_lo,
+// u = c + c_off (R = 1, s_hi = 2 E N: contiguous); accumulate adds to it.  The evk inner product is formed at the
 // automorphism's source word, so nothing is stored between the key switch and the automorphism; the source words
 // of a wave's 64 consecutive outputs are a permutation of one aligned 64-word block (the automorphism multiplies
 // the bit-reversed index by an odd g), so the gathers stay coalesced.
@@ -577,7 +579,6 @@ struct QpRotArgs {
     uint64_t ext_stride, src_stride, s_hi, s_lo;
     const uint64_t* evk[kMaxList];
     uint32_t g[kMaxList];
-    TwPair pmod[kMaxPmap];  // P mod q_t, t < l
 };
 
 __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__ ext,
@@ -586,8 +587,7 @@ __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__
     const ListTile lt = list_tile(a.n_out);  // outputs of one tile on one XCD: their ext and evk words meet in L2
     const uint32_t k = lt.kt * 256 + threadIdx.x;
     const uint32_t t = lt.limb, c = lt.item;
-    const bool qlimb = t < a.l;
-    const uint32_t pi = qlimb ? t : a.L + (t - a.l);
+    const uint32_t pi = t < a.l ? t : a.L + (t - a.l);
     const Barrett br = barrett_of(primes[pi]);
     const uint64_t q = br.q;
     uint64_t v0 = 0, v1 = 0;
@@ -603,13 +603,11 @@ __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__
             const uint64_t* ep = ek + (size_t)pi * kN + sw;
             Acc s0, s1;  // at most kMaxDigits = 8 terms
             ks_dot(xe, (size_t)a.E * kN, ep, (size_t)a.T * kN, a.D, s0, s1);
-            uint64_t r0 = reduce_u128(s0.get(), br);
-            if (qlimb) r0 = add_mod(r0, shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q), q);
-            v0 = add_mod(v0, r0, q);
+            v0 = add_mod(v0, add_mod(reduce_u128(s0.get(), br), sx[0], q), q);
             v1 = add_mod(v1, reduce_u128(s1.get(), br), q);
-        } else if (qlimb) {
-            v0 = add_mod(v0, shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q), q);
-            v1 = add_mod(v1, shoup(sx[(size_t)a.l * kN], a.pmod[t].w, a.pmod[t].wp, q), q);
+        } else {
+            v0 = add_mod(v0, sx[0], q);
+            v1 = add_mod(v1, sx[(size_t)a.E * kN], q);
         }
     }
     const uint32_t u = c + a.c_off;
@@ -1371,11 +1369,12 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
     return hipGetLastError();
 }
 
-// n_out outputs of nt terms each (see k_qp_rot_sum); keys[i] / steps g[i], i < A + nt - 1 <= 64 (null key:
-// identity term); output c at dst + (u / R) 2 E N + (u % R) s_lo, u = c + c_off; accumulate adds to it
+// n_out outputs of nt terms each (see k_qp_rot_sum; src: the terms' inner sums over Q_l * P); keys[i] / steps g[i],
+// i < A + nt - 1 <= 64 (null key: identity term); output c at dst + (u / R) 2 E N + (u % R) s_lo, u = c + c_off;
+// accumulate adds to it
 hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
                              uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_out,
-                             uint32_t nt, uint32_t A, uint32_t M, uint32_t l, const TwPair* pmod, uint64_t* dst,
+                             uint32_t nt, uint32_t A, uint32_t M, uint32_t l, uint64_t* dst,
                              hipStream_t st, uint32_t R, uint32_t c_off, uint64_t s_lo, bool accumulate) {
     const uint32_t E = l + ctx.K;
     if (n_out == 0 || nt == 0 || A == 0 || A + nt - 1 > (uint32_t)kMaxList || E > kMaxPmap || n_out > 4096)
@@ -1406,10 +1405,9 @@ hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t e
     }
     for (uint32_t c = 0; c < A; c++)
         for (uint32_t j = 0; j < nt; j++) n_ks += keys[c + j] ? 1 : 0;
-    for (uint32_t t = 0; t < l; t++) a.pmod[t] = pmod[t];
-    // bytes: per key-switched term ext D E + evk 2 D E + c0 l, per identity term 2 l; output 2 E
+    // bytes: per key-switched term ext D E + evk 2 D E + S0 E, per identity term 2 E; output 2 E
     const double terms = (double)n_out / A;
-    const double by = ((double)n_ks * (3.0 * D * E + l) + ((double)A * nt - n_ks) * 2.0 * l) * terms +
+    const double by = ((double)n_ks * (3.0 * D * E + E) + ((double)A * nt - n_ks) * 2.0 * E) * terms +
                       (double)n_out * 2 * E;
     ctx.n_keyswitch += n_ks * (uint64_t)(n_out / A);
     const int pi = prof_begin(ctx, "qp_rot_sum", by * kN * 8, st);

@@ -202,7 +202,8 @@ int ckks_linear_transform_multi(ckks_context* ctx, const uint64_t* const* d_in, 
  *                           each giant's inner sum is brought down once, the giant rotations are summed in Q_l P and
  *                           one ModDown, fused with the rescale, ends it.  diags [n_out][n_giant][n_in n_baby][l+K][N]
  *                           over the primes of Q_l then P (uncompressed); out [n_out][2][l-1][N]; n_baby <= 32,
- *                           n_in n_baby <= 64, n_giant <= 64.  Decrypts like
+ *                           n_in n_baby <= 64, n_giant <= 64, at most one giant step 0.  The giants' inner sums bring
+ *                           only their c1 down to Q_l; their c0 enter the rotations over Q_l P as they are.  Decrypts like
  *                           ckks_linear_transform_multi's output up to the key-switching rounding (different words). */
 int ckks_linear_transform_hoisted(ckks_context* ctx, const uint64_t* const* d_in, uint32_t n_in, uint32_t level,
                                   const uint64_t* d_diags, uint32_t n_baby, const int64_t* baby_steps,

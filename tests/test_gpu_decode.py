@@ -230,9 +230,10 @@ def test_linear_transform_multi_bit_exact(ckks, ctx5, octx5):
 def test_linear_transform_hoisted_bit_exact(ckks, ctx5, octx5, gst):
     """Double-hoisted BSGS (the bootstrap's CoeffToSlot / SlotToCoeff form) against the oracle composed from its
     stages: babies rotated in Q_l P without a ModDown, diagonals over Q_l P, one ModDown per giant inner sum,
-    giant rotations summed in Q_l P, ModDown then rescale; the inner sum of the identity giant step (the first
-    step 0) is added in Q_l P as it is, without a ModDown.  2 inputs, 2 outputs, babies {0, 1, 2}; giants with the
-    identity first, in the middle, or absent."""
+    giant rotations summed in Q_l P, ModDown then rescale.  A giant's inner sum S = (S0, S1) brings only S1 down to
+    Q_l (the key switch needs it there); the rotation in Q_l P is Auto(<ModUp(ModDown(S1)), evk> + (S0, 0)), and the
+    identity giant's S is added as it is.  2 inputs, 2 outputs, babies {0, 1, 2}; giants with the identity first, in
+    the middle, or absent."""
     l, n_in, n_out = 5, 2, 2
     L, K, D = ctx5.L, ctx5.K, ctx5.dnum
     bst = [0, 1, 2]
@@ -273,6 +274,13 @@ def test_linear_transform_hoisted_bit_exact(ckks, ctx5, octx5, gst):
         v = ((acc + lift(c, False)) % qe[None]).astype(np.uint64)
         return octx5.automorph_eval(v, octx5.rot_index(s)).astype(object)
 
+    def giant_qp(S, s):
+        """a giant rotation of an inner sum S over Q_l P: Auto(<ModUp(ModDown(S1)), evk> + (S0, 0))"""
+        acc = octx5.ks_inner(octx5.modup(octx5.moddown(S[1], l), l), l, evk[s]).astype(object)
+        acc[0] += S[0].astype(object)
+        v = (acc % qe[None]).astype(np.uint64)
+        return octx5.automorph_eval(v, octx5.rot_index(s)).astype(object)
+
     babies = [rot_qp(xs[i], s) for i in range(n_in) for s in bst]
     g0 = gst.index(0) if 0 in gst else -1
     for o in range(n_out):
@@ -280,11 +288,7 @@ def test_linear_transform_hoisted_bit_exact(ckks, ctx5, octx5, gst):
         for g in range(ng):
             S = sum(babies[j] * diags[o, g, j].astype(object)[None] for j in range(n_in * nb))
             S = (S % qe[None]).astype(np.uint64)
-            if g == g0:
-                T += S.astype(object)
-                continue
-            SQ = np.stack([octx5.moddown(S[p], l) for p in range(2)])
-            T += rot_qp(SQ, gst[g])
+            T += S.astype(object) if g == g0 else giant_qp(S, gst[g])
         T = (T % qe[None]).astype(np.uint64)
         want = octx5.rescale(np.stack([octx5.moddown(T[p], l) for p in range(2)]), l)
         assert np.array_equal(got[o], want), o
