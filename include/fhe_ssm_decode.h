@@ -67,7 +67,7 @@ int fhe_ssm_decoder_set_weight(fhe_ssm_decoder* dec, const char* name, int32_t l
 int fhe_ssm_decoder_step(fhe_ssm_decoder* dec, const uint64_t* d_x, uint32_t level, double scale, uint64_t* d_out,
                          uint32_t* out_level, double* out_scale);
 
-/* ciphertexts bootstrapped so far (34 per layer per step) */
+/* ciphertexts bootstrapped so far (26 per layer per step) */
 int fhe_ssm_decoder_stats(const fhe_ssm_decoder* dec, uint64_t* bootstraps);
 
 #ifdef __cplusplus
