@@ -362,7 +362,8 @@ class HEBackend(Backend):
         for s in range(0, flat.shape[0], step):
             chunk = flat[s:s + step]
             self.ctx.encode_periodic(chunk, level, self.S(level), buf.ptr + s * per)
-        return {"buf": buf, "n_out": n_out, "ng": ng, "n_in": nbt // M.MV_NB}
+        nb = M.MV_SPAN // ng
+        return {"buf": buf, "n_out": n_out, "ng": ng, "nb": nb, "n_in": nbt // nb}
 
     # -- ciphertext bookkeeping ----------------------------------------------------------------------
     def zeros(self, B, level):
@@ -448,9 +449,10 @@ class HEBackend(Backend):
         lv = inputs[0].level
         assert all(x.level == lv and x.B == 1 for x in inputs) and len(inputs) == h["n_in"]
         out = self._new(h["n_out"], lv - 1, inputs[0].scale * self.S(lv) / self.moduli[lv - 1])
-        self.ctx.linear_transform_multi([x.ptr() for x in inputs], lv, h["buf"].ptr, M.LOG_REP, M.MV_BABIES,
-                                        [self.keys.get(s) for s in M.MV_BABIES], M.MV_GIANTS,
-                                        [self.keys.get(s) for s in M.MV_GIANTS], h["n_out"], True, out.ptr())
+        bs, gs = M.mv_babies(h["nb"]), M.mv_giants(h["nb"])
+        self.ctx.linear_transform_multi([x.ptr() for x in inputs], lv, h["buf"].ptr, M.LOG_REP, bs,
+                                        [self.keys.get(s) for s in bs], gs, [self.keys.get(s) for s in gs],
+                                        h["n_out"], True, out.ptr())
         return out
 
     def mul_i(self, a, sign):

@@ -34,8 +34,11 @@ namespace {
 constexpr uint32_t kN = 1u << 16;
 constexpr int D = 768, DPAD = 1024, HS = 64, FF = 3072, WKV_T = 64;
 constexpr uint32_t LOG_REP = 5;  // 1024-periodic plaintexts: N / 2^5 words per limb
-constexpr int MV_NB = 32;        // matvec baby steps 0..31; giant steps 32 g, g in [-24, 24)
-constexpr int MV_G0 = -24, MV_NG = 48;
+// matvec BSGS: rotation r = G + b in (-768, 768) with babies b in [0, nb) and giants G = nb g, g in [-768/nb, 768/nb);
+// nb = 64 when a matvec has at least as many outputs as inputs (half the giant rotations, each a key switch per
+// output), else 32
+constexpr int MV_SPAN = 1536;
+int mv_nb(size_t n_in, size_t n_out) { return n_out >= n_in ? 64 : 32; }
 constexpr uint32_t kBootBatch = 16;  // ciphertexts per batched bootstrap (bounds its workspace)
 
 thread_local std::string g_err;
@@ -104,7 +107,7 @@ using Pair = std::tuple<const Ct*, uint32_t, const Ct*, uint32_t>;  // (a, item 
 
 struct Matvec {
     std::shared_ptr<Buf> buf;
-    uint32_t n_out = 0, n_in = 0;
+    uint32_t n_out = 0, n_in = 0, nb = 0;
 };
 
 // ------------------------------------------------------------------ the engine side (primitives + level rules)
@@ -327,19 +330,20 @@ class Engine {
             if (x.level != lv || x.B != 1) throw Error(CKKS_EINVAL, "matvec inputs must be single, same level");
             in.push_back(x.ptr());
         }
-        std::vector<int64_t> bs(MV_NB), gs(MV_NG);
-        std::vector<const uint64_t*> kb(MV_NB), kg(MV_NG);
-        for (int b = 0; b < MV_NB; b++) {
+        const int nb = (int)h.nb, ng = MV_SPAN / nb, g0 = -(MV_SPAN / 2) / nb;
+        std::vector<int64_t> bs(nb), gs(ng);
+        std::vector<const uint64_t*> kb(nb), kg(ng);
+        for (int b = 0; b < nb; b++) {
             bs[b] = b;
             kb[b] = key(b);
         }
-        for (int g = 0; g < MV_NG; g++) {
-            gs[g] = (int64_t)MV_NB * (MV_G0 + g);
+        for (int g = 0; g < ng; g++) {
+            gs[g] = (int64_t)nb * (g0 + g);
             kg[g] = key(gs[g]);
         }
         Ct out = fresh(h.n_out, lv - 1, inputs[0].scale * S(lv) / (double)moduli_[lv - 1]);
-        ck(ckks_linear_transform_multi(ctx_, in.data(), h.n_in, lv, h.buf->d, LOG_REP, MV_NB, bs.data(), kb.data(),
-                                       MV_NG, gs.data(), kg.data(), h.n_out, 1, out.ptr(), nullptr),
+        ck(ckks_linear_transform_multi(ctx_, in.data(), h.n_in, lv, h.buf->d, LOG_REP, nb, bs.data(), kb.data(), ng,
+                                       gs.data(), kg.data(), h.n_out, 1, out.ptr(), nullptr),
            "ckks_linear_transform_multi");
         return out;
     }
@@ -444,27 +448,28 @@ class Engine {
 // A 768 x 768 block of a matvec: element (row, col), or absent (zero).
 using Block = std::function<double(int, int)>;
 
-// [n_out][48 giants][n_in * 32][1024]: the 1024-periodic diagonal r = G + b of every block (giant G = 32 g,
-// baby b), pre-rotated by -G (gpu_real_model.cu:2767-2823, harness/cpu_real_model.cpp:270-318):
-// d[row] = M[row][row + r] for 0 <= row + r < 768, then d'[p] = d[(p - G) mod 1024].
+// [n_out][ng giants][n_in * nb][1024] (nb = mv_nb(n_in, n_out), ng = 1536 / nb): the 1024-periodic diagonal
+// r = G + b of every block (giant G = nb g, baby b), pre-rotated by -G (gpu_real_model.cu:2767-2823,
+// harness/cpu_real_model.cpp:270-318): d[row] = M[row][row + r] for 0 <= row + r < 768, then d'[p] = d[(p - G) mod 1024].
 std::vector<double> matvec_diagonals(const std::vector<std::vector<Block>>& blocks) {
     const size_t n_out = blocks.size(), n_in = blocks[0].size();
-    std::vector<double> out(n_out * MV_NG * n_in * MV_NB * DPAD, 0.0);
+    const int nb = mv_nb(n_in, n_out), ng = MV_SPAN / nb, g0 = -(MV_SPAN / 2) / nb;
+    std::vector<double> out(n_out * ng * n_in * nb * DPAD, 0.0);
     std::vector<double> d(DPAD);
     for (size_t o = 0; o < n_out; o++)
         for (size_t i = 0; i < n_in; i++) {
             const Block& M = blocks[o][i];
             if (!M) continue;
-            for (int gi = 0; gi < MV_NG; gi++) {
-                const int G = MV_NB * (MV_G0 + gi);
-                for (int b = 0; b < MV_NB; b++) {
+            for (int gi = 0; gi < ng; gi++) {
+                const int G = nb * (g0 + gi);
+                for (int b = 0; b < nb; b++) {
                     const int r = G + b;
                     std::fill(d.begin(), d.end(), 0.0);
                     for (int row = 0; row < D; row++) {
                         const int col = row + r;
                         if (col >= 0 && col < D) d[row] = M(row, col);
                     }
-                    double* dst = out.data() + (((o * MV_NG + gi) * n_in + i) * MV_NB + b) * DPAD;
+                    double* dst = out.data() + (((o * ng + gi) * n_in + i) * nb + b) * DPAD;
                     for (int p = 0; p < DPAD; p++) dst[p] = d[(((p - G) % DPAD) + DPAD) % DPAD];
                 }
             }
@@ -506,8 +511,10 @@ std::vector<double> channel_range_mask(int lo, int hi) {
 
 std::vector<int64_t> layer_rotation_steps() {
     std::vector<int64_t> s;
-    for (int b = 0; b < MV_NB; b++) s.push_back(b);
-    for (int g = 0; g < MV_NG; g++) s.push_back((int64_t)MV_NB * (MV_G0 + g));
+    for (int nb : {32, 64}) {
+        for (int b = 0; b < nb; b++) s.push_back(b);
+        for (int g = -(MV_SPAN / 2) / nb; g < (MV_SPAN / 2) / nb; g++) s.push_back((int64_t)nb * g);
+    }
     for (int t = 1; t < WKV_T; t++) {
         s.push_back(t);       // rot64_t: Rot_t on the lanes' low part
         s.push_back(t - HS);  // and Rot_{t-64} on the wrapped part
@@ -612,6 +619,7 @@ class Decoder {
             Matvec m;
             m.n_out = (uint32_t)blocks.size();
             m.n_in = (uint32_t)blocks[0].size();
+            m.nb = (uint32_t)mv_nb(m.n_in, m.n_out);
             m.buf = be_->encode_periodic(matvec_diagonals(blocks), level);
             it = mv_.emplace(key, std::move(m)).first;
         }

@@ -113,34 +113,48 @@ def periodic(vec: np.ndarray) -> np.ndarray:
 
 # ---------------------------------------------------------------- BSGS diagonals (signed rotations)
 # y[i] = sum_j M[i][j] x[j] inside each lane with i, j < 768: rotation r = j - i in (-768, 768), never leaving
-# the lane.  r = 32 g + b, babies b in [0, 32), giants G_g = 32 g with g in [-24, 24).
-MV_NB = 32
-MV_GIANTS = tuple(32 * g for g in range(-24, 24))
-MV_BABIES = tuple(range(MV_NB))
+# the lane.  r = G + b with babies b in [0, nb) and giants G = nb g, g in [-768/nb, 768/nb).  A matvec with at least
+# as many outputs as inputs takes nb = 64 (24 giant rotations per output instead of 48: a giant costs a key switch
+# per output, a hoisted baby about half of one per input), otherwise nb = 32.
+MV_SPAN = 1536
+
+
+def mv_nb(n_in: int, n_out: int) -> int:
+    return 64 if n_out >= n_in else 32
+
+
+def mv_babies(nb: int) -> tuple:
+    return tuple(range(nb))
+
+
+def mv_giants(nb: int) -> tuple:
+    return tuple(nb * g for g in range(-(MV_SPAN // 2) // nb, (MV_SPAN // 2) // nb))
 
 
 def matvec_diagonals(blocks) -> np.ndarray:
     """blocks[o][i]: 768 x 768 matrices (output block o, input block i; None = zero).
-    Returns [n_out][n_giant][n_in * 32][1024]: the 1024-periodic diagonal for giant g, input i, baby b,
-    pre-rotated by -G_g (gpu_real_model.cu:2767-2823's pre-rotation, harness/cpu_real_model.cpp:270-318)."""
+    Returns [n_out][n_giant][n_in * nb][1024] (nb = mv_nb(n_in, n_out)): the 1024-periodic diagonal for giant g,
+    input i, baby b, pre-rotated by -G_g (gpu_real_model.cu:2767-2823's pre-rotation,
+    harness/cpu_real_model.cpp:270-318)."""
     n_out, n_in = len(blocks), len(blocks[0])
-    ng = len(MV_GIANTS)
-    out = np.zeros((n_out, ng, n_in * MV_NB, DPAD))
+    nb = mv_nb(n_in, n_out)
+    giants = mv_giants(nb)
+    out = np.zeros((n_out, len(giants), n_in * nb, DPAD))
     rows = np.arange(D)
     for o in range(n_out):
         for i in range(n_in):
             M = blocks[o][i]
             if M is None:
                 continue
-            for gi, G in enumerate(MV_GIANTS):
-                for b in range(MV_NB):
+            for gi, G in enumerate(giants):
+                for b in range(nb):
                     r = G + b
                     cols = rows + r
                     ok = (cols >= 0) & (cols < D)
                     d = np.zeros(DPAD)
                     d[rows[ok]] = M[rows[ok], cols[ok]]
                     # pre-rotation by -G of a 1024-periodic vector: d'[p] = d[(p - G) mod 1024]
-                    out[o, gi, i * MV_NB + b] = np.roll(d, G)
+                    out[o, gi, i * nb + b] = np.roll(d, G)
     return out
 
 
@@ -219,7 +233,9 @@ def channel_range_mask(lo: int, hi: int) -> np.ndarray:
 
 def rotation_steps() -> list:
     """Every rotation step the decode step uses (keys to generate)."""
-    s = set(MV_BABIES) | set(MV_GIANTS) | set(WKV_LO) | set(WKV_HI) | set(NORM_UP) | set(NORM_DOWN)
+    s = set(WKV_LO) | set(WKV_HI) | set(NORM_UP) | set(NORM_DOWN)
+    for nb in (32, 64):
+        s |= set(mv_babies(nb)) | set(mv_giants(nb))
     s |= set(GAP_SHIFT) | set(-g for g in GAP_SHIFT)
     s.discard(0)
     return sorted(s)

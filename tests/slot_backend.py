@@ -65,8 +65,9 @@ class SlotBackend(DS.Backend):
         return SimPt(np.asarray(vecs).reshape(-1, M.DPAD), level)
 
     def encode_matvec(self, diags, level):
-        return {"d": diags, "level": level, "n_out": diags.shape[0], "ng": diags.shape[1],
-                "n_in": diags.shape[2] // M.MV_NB}
+        nb = M.MV_SPAN // diags.shape[1]
+        return {"d": diags, "level": level, "n_out": diags.shape[0], "ng": diags.shape[1], "nb": nb,
+                "n_in": diags.shape[2] // nb}
 
     # bookkeeping
     def zeros(self, B, level):
@@ -139,10 +140,10 @@ class SlotBackend(DS.Backend):
         assert all(x.level == lv and x.B == 1 for x in inputs) and h["level"] == lv and lv >= 2
         assert len(inputs) == h["n_in"]
         d = h["d"]
-        babies = [np.roll(x.v[0], -b) for x in inputs for b in M.MV_BABIES]
+        babies = [np.roll(x.v[0], -b) for x in inputs for b in M.mv_babies(h["nb"])]
         out = np.zeros((h["n_out"], SLOTS), dtype=np.complex128)
         for o in range(h["n_out"]):
-            for gi, G in enumerate(M.MV_GIANTS):
+            for gi, G in enumerate(M.mv_giants(h["nb"])):
                 acc = np.zeros(SLOTS, dtype=np.complex128)
                 for j, bv in enumerate(babies):
                     if np.any(d[o, gi, j]):

@@ -32,18 +32,24 @@ def test_masked_block_rotation():
         assert np.allclose(got, want, atol=0), t
 
 
-def test_matvec_diagonals():
+@pytest.mark.parametrize("n_in,n_out", [(1, 1), (2, 1), (1, 3)])
+def test_matvec_diagonals(n_in, n_out):
+    """the BSGS sum over the diagonals is the block matvec, for both baby/giant splits (nb = 64 when n_out >= n_in)"""
     rng = np.random.default_rng(3)
-    A = rng.standard_normal((768, 768))
-    d = M.matvec_diagonals([[A]])
-    x = rng.standard_normal((32, 768))
-    xs = M.pack_lanes(x)
-    y = np.zeros(1 << 15)
-    for gi, G in enumerate(M.MV_GIANTS):
-        acc = sum(np.tile(d[0, gi, b], 32) * np.roll(xs, -b) for b in M.MV_BABIES)
-        y += np.roll(acc, -G)
-    assert np.allclose(M.unpack_lanes(y), x @ A.T, atol=1e-9)
-    assert np.all(y.reshape(32, 1024)[:, 768:] == 0)
+    A = rng.standard_normal((n_out, n_in, 768, 768))
+    d = M.matvec_diagonals([[A[o, i] for i in range(n_in)] for o in range(n_out)])
+    nb = M.mv_nb(n_in, n_out)
+    assert d.shape == (n_out, M.MV_SPAN // nb, n_in * nb, M.DPAD) and nb == (64 if n_out >= n_in else 32)
+    x = rng.standard_normal((n_in, 32, 768))
+    xs = [M.pack_lanes(x[i]) for i in range(n_in)]
+    for o in range(n_out):
+        y = np.zeros(1 << 15)
+        for gi, G in enumerate(M.mv_giants(nb)):
+            acc = sum(np.tile(d[o, gi, i * nb + b], 32) * np.roll(xs[i], -b) for i in range(n_in) for b in range(nb))
+            y += np.roll(acc, -G)
+        want = sum(x[i] @ A[o, i].T for i in range(n_in))
+        assert np.allclose(M.unpack_lanes(y), want, atol=1e-9)
+        assert np.all(y.reshape(32, 1024)[:, 768:] == 0)
 
 
 @pytest.mark.timeout(300)
