@@ -542,7 +542,7 @@ def config5_moduli(ckks, log_scale: int = 40, n_scaling: int = 28):
     return q0 + scaling[::-1] + big[:3] + big[3:]
 
 
-def build_engine(ckks, secret_seed=b"S" * 32, n_keys_seed=7, steps=None, cheb_degree=47, double_angles=2):
+def build_engine(ckks, secret_seed=b"S" * 32, n_keys_seed=7, steps=None, cheb_degree=39, double_angles=2):
     """Context, bootstrapping plan, secret and every key the decode step uses; returns (backend, secret)."""
     ctx = ckks.Context(num_q=32, num_p=7, dnum=4, scale=2.0**40, moduli=config5_moduli(ckks))
     ctx.set_moddown_exact(True)  # unbiased key-switch rounding: the 2^40 chain bootstraps to ~13 bits with it
