@@ -30,7 +30,7 @@ namespace fhe {
 namespace {
 
 constexpr int kTileThreads = 256;
-constexpr int kLdsWords = 16 * 272;  // one tile, padded (pass B uses 17 words per 16)
+constexpr int kLdsWords = 16 * 272;  // one tile, padded to 17 words per 16 (both passes: no bank conflicts)
 
 __device__ __forceinline__ void job_of(const JobSpec& js, uint32_t u, uint32_t& off, uint32_t& prime) {
     if (js.jobs) {
@@ -101,10 +101,10 @@ __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPai
         }
     }
 #pragma unroll
-    for (int k = 0; k < 16; k++) lds[(rg + 16 * k) * 16 + cl] = x[k];
+    for (int k = 0; k < 16; k++) lds[(rg + 16 * k) * 17 + cl] = x[k];
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < 16; k++) x[k] = lds[(16 * rg + k) * 16 + cl];
+    for (int k = 0; k < 16; k++) x[k] = lds[(16 * rg + k) * 17 + cl];
     // stages 4..7: rows r = 16 rg + k, pairs differ in bit (7-s) of r; twiddle (1<<s) + (r >> (8-s))
 #pragma unroll
     for (int s = 4; s < 8; s++) {
@@ -245,10 +245,10 @@ __device__ __forceinline__ void inv_a_tile(uint64_t* __restrict__ a, const TwPai
         }
     }
 #pragma unroll
-    for (int k = 0; k < 16; k++) lds[(16 * rg + k) * 16 + cl] = x[k];
+    for (int k = 0; k < 16; k++) lds[(16 * rg + k) * 17 + cl] = x[k];
     __syncthreads();
 #pragma unroll
-    for (int k = 0; k < 16; k++) x[k] = lds[(rg + 16 * k) * 16 + cl];
+    for (int k = 0; k < 16; k++) x[k] = lds[(rg + 16 * k) * 17 + cl];
     // u = 4..6: r = rg + 16k, pairs differ in bit (u-4) of k; r >> (u+1) = k >> (u-3)
 #pragma unroll
     for (int u = 4; u < 7; u++) {
