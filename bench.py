@@ -27,6 +27,7 @@ import ctypes
 import gc
 import json
 import os
+import shutil
 import sys
 import time
 
@@ -297,7 +298,7 @@ def bench_bootstrap(ckks, torch, steps_n, warmup, seed):
 DECODE_LANES = 32
 
 
-def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native"):
+def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native", serve_requests=0):
     """Config 5: one encrypted decode step of the RWKV-7-0.1B-shaped polynomial model (12 layers, 32 lanes in
     the slots, state carried across steps, state bootstrapped once per layer).  The client side (token
     embedding + encryption before the step, decryption + the 768 x 65536 vocabulary head after it) is
@@ -371,7 +372,12 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native
     rep = ctx.profile_report()
     ctx.profile_reset()
     s_per_step = sum(times) / len(times)
-    return {"s_per_step": round(s_per_step, 3), "key_switches_per_step": int(np.mean(ks)),
+    serve = None
+    if serve_requests and driver == "native":
+        serve = bench_serve(torch, be, nat, client_in, warmup + steps_n + 1, serve_requests, log)
+        serve["step_s"] = round(s_per_step, 3)
+        serve["overhead_ms_per_request"] = round((serve["request_s"] - s_per_step) * 1e3, 1)
+    return {"s_per_step": round(s_per_step, 3), "serve": serve, "key_switches_per_step": int(np.mean(ks)),
             "bootstraps_per_step": n_boot() // (warmup + steps_n + 1), "driver": driver,
             "setup_s": {"keys": round(t_keys, 1), "first_steps_with_plaintext_encoding": round(t_warm, 1)},
             "device_memory_in_use_gb_after_warmup": round((total_b - free_b) / 1e9, 1),
@@ -383,6 +389,37 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native
                         f"degree-3 polynomial nonlinearities (seeded coefficients in [-0.5, 0.5]), 32 lanes in "
                         f"the slots of one N=2^16 ciphertext, WKV state carried and bootstrapped once per layer; "
                         f"chain q0 50 + 28 x 40 + 3 x 60 bits, P 7 x 60, dnum 4; sparse-secret bootstrapping"}
+
+
+def bench_serve(torch, be, nat, client_in, i0, n_req, log):
+    """The serve-directory protocol around the same decoder (state carried on): n_req one-token requests, each
+    timed from the client writing its ciphertext file to the answer being complete (resp.N.done present,
+    req.N.ready gone).  Both ends poll every 20 ms here (the reference's server polls every 200 ms)."""
+    import tempfile
+    import threading
+    from engine_loader import load_module
+    SC = load_module("serve_client")
+    d = tempfile.mkdtemp(prefix="fhe_serve_")
+    box = {}
+    th = threading.Thread(target=lambda: box.update(rep=nat.serve(d, timeout_sec=600, stateful=True, poll_ms=20)),
+                          daemon=True)
+    th.start()
+    times = []
+    for n in range(n_req):
+        _, ct = client_in(i0 + n)
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        SC.submit(d, n, lambda k, path: be.ctx.ct_save(path, ct.ptr(), ct.level, ct.scale), 1,
+                  SC.request_meta(1, DECODE_LANES, be.top_level))
+        resp = SC.wait(d, n, timeout=600, poll=0.02, alive=th.is_alive)
+        times.append(time.perf_counter() - t)
+        log(f"serve request {n}: {times[-1]:.2f} s ({os.path.getsize(resp + '.0') / 2**20:.1f} MiB response)")
+    SC.stop(d)
+    th.join(timeout=60)
+    in_mib = 2 * be.top_level * (1 << 16) * 8 / 2**20
+    shutil.rmtree(d, ignore_errors=True)
+    return {"requests": n_req, "request_s": round(sum(times) / len(times), 3), "poll_ms": 20,
+            "request_file_MiB": round(in_mib, 1), "served": box.get("rep", {}).get("served")}
 
 
 def cpu_baseline_decode(res, seed, budget_s=15.0):
@@ -504,6 +541,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="hmult", choices=["hmult", "ntt", "pcmm", "bootstrap", "decode"])
     ap.add_argument("--layers", type=int, default=12, help="decode workload: layers (12 = config 5)")
+    ap.add_argument("--serve-requests", type=int, default=0,
+                    help="decode workload: also time this many one-token requests through the serve protocol")
     ap.add_argument("--decode-driver", default="native", choices=["native", "python"],
                     help="decode workload: the C++ driver (default) or the same plan in Python")
     ap.add_argument("--seed", type=int, default=1)
@@ -551,13 +590,16 @@ def main():
             del d
         cpu = None if args.no_cpu_baseline else cpu_baseline_hmult(args.seed)
     elif args.workload == "decode":
-        d = bench_decode(ckks, torch, args.steps, args.warmup, args.seed, args.layers, args.decode_driver)
+        d = bench_decode(ckks, torch, args.steps, args.warmup, args.seed, args.layers, args.decode_driver,
+                         args.serve_requests)
         res = {"metric": "s/step for 32-lane decode (config 5)", "value": d["s_per_step"], "unit": "s/step",
                "ms_per_step": round(d["s_per_step"] * 1e3, 1), "dtype": "u64",
                "config": {"workload": d["workload"], "lanes": DECODE_LANES, "layers": args.layers},
                "kernels": d["kernels"], "roofline": d["roofline"],
                "check": {k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s",
                                            "device_memory_in_use_gb_after_warmup", "driver")}}
+        if d["serve"]:
+            res["check"]["serve"] = d["serve"]
         extra = {}
         cpu = None
         if not args.no_cpu_baseline:

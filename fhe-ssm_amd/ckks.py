@@ -100,6 +100,10 @@ SIGNATURES = {
     "ckks_seeded_part_indices": (_int, [ctypes.c_char_p, _vp, _u32, ctypes.POINTER(_u32)]),
     "ckks_seeded_part_load_key": (_int, [_vp, ctypes.c_char_p, _u32, ctypes.POINTER(_u32), _vp]),
     "ckks_seeded_part_write": (_int, [_vp, ctypes.c_char_p, ctypes.c_char_p, _u32, _vp, _vp, _vp]),
+    "ckks_ct_file_info": (_int, [ctypes.c_char_p, ctypes.POINTER(_u32), ctypes.POINTER(_u32),
+                                 ctypes.POINTER(ctypes.c_double)]),
+    "ckks_ct_save": (_int, [_vp, ctypes.c_char_p, _vp, _u32, ctypes.c_double]),
+    "ckks_ct_load": (_int, [_vp, ctypes.c_char_p, _u32, _vp, ctypes.POINTER(_u32), ctypes.POINTER(ctypes.c_double)]),
     "ckks_encode": (_int, [_vp, _vp, _vp, _u32, _u32, ctypes.c_double, _vp]),
     "ckks_encrypt": (_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp]),
     "ckks_decrypt_decode": (_int, [_vp, _vp, _vp, _u32, ctypes.c_double, _vp, _vp, _u32]),
@@ -392,6 +396,16 @@ class Context:
         check(load().ckks_seeded_part_write(self.h, path.encode(), key_tag.encode(), len(ix), _ptr(ix) if len(ix) else None,
                                             _ptr(sd) if len(ix) else None, _ptr_array(d_evks)))
 
+    def ct_save(self, path: str, d_ct, level: int, scale: float) -> None:
+        """a ciphertext [2][level][N] into a ciphertext file (the serve protocol's req.N.t / resp.N.t)"""
+        check(load().ckks_ct_save(self.h, path.encode(), d_ct, level, scale))
+
+    def ct_load(self, path: str, d_ct, cap_level: int):
+        """a ciphertext file into d_ct (room for cap_level limbs); returns (level, scale)"""
+        lv, sc = _u32(0), ctypes.c_double()
+        check(load().ckks_ct_load(self.h, path.encode(), cap_level, d_ct, ctypes.byref(lv), ctypes.byref(sc)))
+        return int(lv.value), float(sc.value)
+
     def encode(self, values, level: int, scale: float, d_pt) -> None:
         v = np.asarray(values)
         re = np.ascontiguousarray(v.real, dtype=np.float64)
@@ -459,6 +473,13 @@ def seeded_part_header(path: str) -> dict:
     return {"version": h.version, "expander": h.expander, "N": h.ring_dim, "size_q": h.size_q, "size_p": h.size_p,
             "num_part_q": h.num_part_q, "num_per_part_q": h.num_per_part_q, "count": h.count,
             "key_tag": h.key_tag.decode(), "moduli": [int(h.moduli[i]) for i in range(n)]}
+
+
+def ct_file_info(path: str) -> dict:
+    """the header of a ciphertext file (host only: no context, no device)"""
+    n, lv, sc = _u32(0), _u32(0), ctypes.c_double()
+    check(load().ckks_ct_file_info(path.encode(), ctypes.byref(n), ctypes.byref(lv), ctypes.byref(sc)))
+    return {"N": int(n.value), "level": int(lv.value), "scale": float(sc.value)}
 
 
 def seeded_part_indices(path: str) -> list:

@@ -520,6 +520,36 @@ int ckks_seeded_part_write(ckks_context* ctx, const char* path, const char* key_
     });
 }
 
+int ckks_ct_file_info(const char* path, uint32_t* ring_dim, uint32_t* level, double* scale) {
+    if (!path || !ring_dim || !level || !scale) return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        const fhe::CtFileHeader h = fhe::read_ct_header(path);
+        *ring_dim = h.N;
+        *level = h.level;
+        *scale = h.scale;
+        return CKKS_OK;
+    });
+}
+
+int ckks_ct_save(ckks_context* ctx, const char* path, const uint64_t* d_ct, uint32_t level, double scale) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    if (!path || !d_ct) return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        fhe::save_ct(ctx->c, path, d_ct, level, scale);
+        return CKKS_OK;
+    });
+}
+
+int ckks_ct_load(ckks_context* ctx, const char* path, uint32_t cap_level, uint64_t* d_ct, uint32_t* level,
+                 double* scale) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    if (!path || !d_ct || !level || !scale) return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        fhe::load_ct(ctx->c, path, cap_level, d_ct, level, scale);
+        return CKKS_OK;
+    });
+}
+
 int ckks_keygen_switch(ckks_context* ctx, const ckks_secret* sk_from, const ckks_secret* sk_to,
                        const uint8_t* seed32, const uint8_t* eseed32, uint32_t q_limbs, uint64_t* d_evk) {
     if (int rc = check_secret(ctx, sk_from)) return rc;

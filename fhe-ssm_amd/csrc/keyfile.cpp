@@ -7,6 +7,11 @@
 // A key's a-halves are not stored: they are the ChaCha20 expansion of the seed (nonce {digit, limb, "SKEY"},
 // seeded_keys.hpp:28-43), the same expander this engine's key generation uses, so a loaded key is the key that
 // was written word for word.  In device memory a key is [dnum][2][L + K][N] with b_d at poly 0 and a_d at poly 1.
+//
+// Ciphertext files carry the serve-directory protocol's payload (req.N.t / resp.N.t).  The reference writes
+// OpenFHE-cereal ciphertexts there (gpu_real_model.cu:2303-2324, Serial::SerializeToFile), a format only OpenFHE
+// reads; this engine's layout is flat: char[8] "FSSMCTX1"; u32 version = 1; u32 N; u32 level; u32 n_polys = 2;
+// f64 scale; u64 moduli[level] (the chain's first `level` primes); u64 words[2][level][N] (evaluation form).
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -31,6 +36,7 @@ namespace {
 
 constexpr char kMagic[8] = {'F', 'S', 'S', 'M', 'S', 'K', 'Y', '1'};
 constexpr uint32_t kVersion = 1, kExpander = 1;
+constexpr char kCtMagic[8] = {'F', 'S', 'S', 'M', 'C', 'T', 'X', '1'};
 
 uint32_t get32(std::istream& is, const char* what) {
     uint8_t b[4];
@@ -168,6 +174,75 @@ void write_seeded_part(Context& ctx, const std::string& path, const std::string&
     }
     os.flush();
     if (!os.good()) throw std::invalid_argument("seeded part: write failed: " + path);
+}
+
+CtFileHeader read_ct_header(const std::string& path) {
+    std::ifstream is(path, std::ios::binary);
+    if (!is.good()) throw std::invalid_argument("ciphertext file: cannot open " + path);
+    char magic[8];
+    if (!is.read(magic, 8) || std::memcmp(magic, kCtMagic, 8) != 0)
+        throw std::invalid_argument("ciphertext file: bad magic");
+    if (get32(is, "header") != kVersion) throw std::invalid_argument("ciphertext file: unsupported version");
+    CtFileHeader h;
+    h.N = get32(is, "header");
+    h.level = get32(is, "header");
+    h.n_polys = get32(is, "header");
+    const uint64_t sb = get64(is, "header");
+    std::memcpy(&h.scale, &sb, 8);
+    if (h.N == 0 || (h.N & (h.N - 1)) || h.level == 0 || h.level > 4096 || h.n_polys != 2 || !(h.scale > 0.0))
+        throw std::invalid_argument("ciphertext file: implausible header");
+    h.moduli.resize(h.level);
+    for (auto& m : h.moduli) m = get64(is, "moduli");
+    h.header_bytes = 8 + 4 * 4 + 8 + 8 * (uint64_t)h.level;
+    is.seekg(0, std::ios::end);
+    if ((uint64_t)is.tellg() != h.header_bytes + (uint64_t)h.n_polys * h.level * h.N * 8)
+        throw std::invalid_argument("ciphertext file: size does not match its header");
+    return h;
+}
+
+void load_ct(Context& ctx, const std::string& path, uint32_t cap_level, uint64_t* d_ct, uint32_t* level,
+             double* scale) {
+    const CtFileHeader h = read_ct_header(path);
+    if (h.N != kN) throw std::invalid_argument("ciphertext file: another ring dimension");
+    if (h.level > ctx.L) throw std::invalid_argument("ciphertext file: more limbs than the chain");
+    for (uint32_t i = 0; i < h.level; i++)
+        if (h.moduli[i] != ctx.moduli[i]) throw std::invalid_argument("ciphertext file: modulus chain differs");
+    if (h.level > cap_level) throw std::invalid_argument("ciphertext file: level above what the buffer holds");
+    std::ifstream is(path, std::ios::binary);
+    is.seekg((std::streamoff)h.header_bytes);
+    std::vector<uint64_t> w((size_t)h.n_polys * h.level * kN);
+    if (!is.read((char*)w.data(), (std::streamsize)(w.size() * 8)))
+        throw std::invalid_argument("ciphertext file: short words");
+    for (uint32_t p = 0; p < h.n_polys; p++)
+        for (uint32_t i = 0; i < h.level; i++) {
+            const uint64_t* row = w.data() + ((size_t)p * h.level + i) * kN;
+            for (uint32_t k = 0; k < kN; k++)
+                if (row[k] >= ctx.moduli[i]) throw std::invalid_argument("ciphertext file: word >= q");
+        }
+    HIPC(hipMemcpy(d_ct, w.data(), w.size() * 8, hipMemcpyHostToDevice));
+    *level = h.level;
+    *scale = h.scale;
+}
+
+void save_ct(Context& ctx, const std::string& path, const uint64_t* d_ct, uint32_t level, double scale) {
+    if (level == 0 || level > ctx.L) throw std::invalid_argument("ciphertext file: level outside the chain");
+    if (!(scale > 0.0)) throw std::invalid_argument("ciphertext file: scale must be positive");
+    std::vector<uint64_t> w((size_t)2 * level * kN);
+    HIPC(hipMemcpy(w.data(), d_ct, w.size() * 8, hipMemcpyDeviceToHost));
+    std::ofstream os(path, std::ios::binary | std::ios::trunc);
+    if (!os.good()) throw std::invalid_argument("ciphertext file: cannot create " + path);
+    os.write(kCtMagic, 8);
+    put32(os, kVersion);
+    put32(os, kN);
+    put32(os, level);
+    put32(os, 2);
+    uint64_t sb;
+    std::memcpy(&sb, &scale, 8);
+    put64(os, sb);
+    for (uint32_t i = 0; i < level; i++) put64(os, ctx.moduli[i]);
+    os.write((const char*)w.data(), (std::streamsize)(w.size() * 8));
+    os.flush();
+    if (!os.good()) throw std::invalid_argument("ciphertext file: write failed: " + path);
 }
 
 }  // namespace fhe

@@ -1,4 +1,4 @@
-// keyfile.hpp -- seeded key-switching-key part files (see keyfile.cpp).
+// keyfile.hpp -- seeded key-switching-key part files and ciphertext files (see keyfile.cpp).
 #pragma once
 #include <stdint.h>
 
@@ -25,5 +25,17 @@ void load_seeded_part_key(Context& ctx, const std::string& path, uint32_t record
 // n keys (automorphism indices, 32-byte seeds whose expansion is each key's a-half, device keys) into one part file
 void write_seeded_part(Context& ctx, const std::string& path, const std::string& key_tag, uint32_t n,
                        const uint32_t* indices, const uint8_t* seeds, const uint64_t* const* d_evks);
+
+struct CtFileHeader {
+    uint32_t N = 0, level = 0, n_polys = 0;
+    double scale = 0.0;
+    std::vector<uint64_t> moduli;  // level of them
+    uint64_t header_bytes = 0;
+};
+
+CtFileHeader read_ct_header(const std::string& path);
+// a ciphertext [2][level][N] of this context (level <= cap_level) into d_ct
+void load_ct(Context& ctx, const std::string& path, uint32_t cap_level, uint64_t* d_ct, uint32_t* level, double* scale);
+void save_ct(Context& ctx, const std::string& path, const uint64_t* d_ct, uint32_t level, double scale);
 
 }  // namespace fhe

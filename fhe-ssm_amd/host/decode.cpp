@@ -20,6 +20,7 @@
 #include "fhe_ssm_decode.h"
 
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <functional>
 #include <map>
@@ -147,6 +148,7 @@ class Engine {
     }
 
     uint32_t top_level() const { return top_; }
+    ckks_context* ctx() const { return ctx_; }
     double S(uint32_t l) const { return S_.at(l); }
     const uint64_t* key(int64_t s) const {
         if (s == 0) return nullptr;
@@ -599,6 +601,8 @@ class Decoder {
     }
 
     uint64_t bootstraps() const { return n_boot_; }
+    // the next step starts cold (zero WKV state and token-shift carries), as the first one does
+    void reset() { state_.clear(); }
 
    private:
     // plaintexts, encoded on first use at the level they are applied
@@ -830,6 +834,60 @@ struct fhe_ssm_decoder {
     std::unique_ptr<Decoder> dec;
 };
 
+namespace {
+
+// the decode step as the serve protocol's handler: one token (up to 32 lanes) per ciphertext file, run as
+// consecutive steps over the carried state; the response meta stamps the request's lanes and count
+// (gpu_real_model.cu:2332-2339, writeCtMeta)
+struct ServeState {
+    fhe_ssm_decoder* dec;
+    uint64_t* d_in;
+};
+
+int serve_step(void* user, uint32_t, const char* req_prefix, const char* resp_prefix, const char* meta, int32_t reset,
+               char* err, size_t err_cap) {
+    auto* sv = static_cast<ServeState*>(user);
+    const int rc = guarded([&] {
+        Engine& be = *sv->dec->be;
+        const uint32_t top = be.top_level();
+        auto mi = [&](const char* k, long long dflt) { return fhe_ssm_meta_int(meta, k, dflt); };
+        const long long count = mi("count", -1), tokens = mi("tokensReal", -1), lanes = mi("lanes", 1);
+        if (count != tokens) throw Error(CKKS_EINVAL, "one token per ciphertext: count must equal tokensReal");
+        if (mi("packTokens", -1) != 1 || mi("dpad", -1) != DPAD || mi("ringDim", -1) != (long long)kN ||
+            mi("interleave", 0) != 0)
+            throw Error(CKKS_EINVAL, "request layout is not this decoder's (packTokens 1, dpad 1024, ringDim 65536, "
+                                     "interleave 0)");
+        if (lanes < 1 || lanes > (long long)(kN / 2 / DPAD)) throw Error(CKKS_EINVAL, "lanes must be in [1, 32]");
+        if (mi("level", -1) != (long long)top)
+            throw Error(CKKS_EINVAL, "request level must be the state plan's output level " + std::to_string(top));
+        if (reset) sv->dec->dec->reset();
+        uint32_t out_level = 0;
+        for (long long t = 0; t < count; t++) {
+            const std::string in = std::string(req_prefix) + "." + std::to_string(t);
+            uint32_t lvl = 0;
+            double sc = 0.0;
+            ck(ckks_ct_load(be.ctx(), in.c_str(), top, sv->d_in, &lvl, &sc), "ckks_ct_load");
+            if (lvl != top) throw Error(CKKS_EINVAL, in + ": not at the state plan's output level");
+            if (std::fabs(sc / be.S(top) - 1.0) > 1e-9) throw Error(CKKS_EINVAL, in + ": scale is not S(level)");
+            Ct y = sv->dec->dec->step(Engine::borrowed(sv->d_in, 1, top, sc));
+            const std::string out = std::string(resp_prefix) + "." + std::to_string(t);
+            ck(ckks_ct_save(be.ctx(), out.c_str(), y.ptr(), y.level, y.scale), "ckks_ct_save");
+            out_level = y.level;
+        }
+        FILE* f = std::fopen((std::string(resp_prefix) + ".meta").c_str(), "w");
+        if (!f) throw Error(CKKS_EINVAL, "cannot write the response meta");
+        std::fprintf(f,
+                     "{\"count\":%lld,\"packTokens\":1,\"tokensReal\":%lld,\"dpad\":%d,\"interleave\":0,"
+                     "\"lanes\":%lld,\"ringDim\":%u,\"level\":%u}\n",
+                     count, tokens, DPAD, lanes, kN, out_level);
+        if (std::fclose(f) != 0) throw Error(CKKS_EINVAL, "cannot write the response meta");
+    });
+    if (rc != CKKS_OK && err && err_cap) std::snprintf(err, err_cap, "%s", g_err.c_str());
+    return rc;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* fhe_ssm_last_error(void) { return g_err.c_str(); }
@@ -885,6 +943,30 @@ int fhe_ssm_decoder_step(fhe_ssm_decoder* dec, const uint64_t* d_x, uint32_t lev
         *out_level = y.level;
         *out_scale = y.scale;
     });
+}
+
+int fhe_ssm_decoder_reset(fhe_ssm_decoder* dec) {
+    return guarded([&] {
+        if (!dec) throw Error(CKKS_EINVAL, "null argument");
+        dec->dec->reset();
+    });
+}
+
+int fhe_ssm_decoder_serve(fhe_ssm_decoder* dec, const char* dir, const fhe_ssm_serve_opts* opts,
+                          fhe_ssm_serve_report* report) {
+    ServeState sv{dec, nullptr};
+    int rc = guarded([&] {
+        if (!dec || !dir || !opts || !report) throw Error(CKKS_EINVAL, "null argument");
+        void* p = nullptr;
+        ck(ckks_buffer_alloc((size_t)2 * dec->be->top_level() * kN * 8, &p), "ckks_buffer_alloc");
+        sv.d_in = static_cast<uint64_t*>(p);
+    });
+    if (rc != CKKS_OK) return rc;
+    rc = fhe_ssm_serve_dir(dir, opts, serve_step, &sv, report);
+    ckks_buffer_free(sv.d_in);
+    if (rc != CKKS_OK) g_err = std::string("serve: ") + dir + " is not a directory";
+    else g_err.clear();
+    return rc;
 }
 
 int fhe_ssm_decoder_stats(const fhe_ssm_decoder* dec, uint64_t* bootstraps) {

@@ -1,12 +1,13 @@
 """ctypes front end of libfhe_ssm_decode.so (include/fhe_ssm_decode.h): the config-5 decode step's native driver.
 
 The driver is C++ over the engine's C ABI; this module only hands it the context, the refresh plans, the keys
-and the weights, and calls one step at a time.  There is no Python fallback: if the library is missing,
-loading raises.
+and the weights, and calls one step at a time -- or hands it a directory to serve (the reference's --serve DIR
+protocol, the loop in host/serve.cpp).  There is no Python fallback: if the library is missing, loading raises.
 """
 from __future__ import annotations
 
 import ctypes
+import json
 import os
 
 import numpy as np
@@ -23,6 +24,23 @@ class Refresh(ctypes.Structure):
     _fields_ = [("plan", _vp), ("in_scale", ctypes.c_double)]
 
 
+class ServeOpts(ctypes.Structure):
+    """fhe_ssm_serve_opts"""
+    _fields_ = [("timeout_sec", _u32), ("poll_ms", _u32), ("stateful", ctypes.c_int32), ("log_fd", ctypes.c_int32),
+                ("first_req", _u32)]
+
+
+class ServeReport(ctypes.Structure):
+    """fhe_ssm_serve_report"""
+    _fields_ = [("served", _u32), ("failed", _u32), ("next_req", _u32), ("exit_reason", ctypes.c_int32)]
+
+
+# int handler(void* user, uint32_t req, const char* req_prefix, const char* resp_prefix, const char* meta_json,
+#             int32_t reset, char* err, size_t err_cap)
+ServeHandler = ctypes.CFUNCTYPE(_int, _vp, _u32, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int32,
+                                _vp, ctypes.c_size_t)
+
+
 SIGNATURES = {
     "fhe_ssm_last_error": (ctypes.c_char_p, []),
     "fhe_ssm_decoder_create": (_int, [_vp, _u32, Refresh, Refresh, Refresh, _vp, _vp, _vp, _vp, _u32,
@@ -33,6 +51,11 @@ SIGNATURES = {
     "fhe_ssm_decoder_step": (_int, [_vp, _vp, _u32, ctypes.c_double, _vp, ctypes.POINTER(_u32),
                                     ctypes.POINTER(ctypes.c_double)]),
     "fhe_ssm_decoder_stats": (_int, [_vp, ctypes.POINTER(ctypes.c_uint64)]),
+    "fhe_ssm_decoder_reset": (_int, [_vp]),
+    "fhe_ssm_serve_dir": (_int, [ctypes.c_char_p, ctypes.POINTER(ServeOpts), ServeHandler, _vp,
+                                 ctypes.POINTER(ServeReport)]),
+    "fhe_ssm_decoder_serve": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ServeOpts), ctypes.POINTER(ServeReport)]),
+    "fhe_ssm_meta_int": (ctypes.c_longlong, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_longlong]),
 }
 
 LAYER_WEIGHTS = ("g1", "g2", "eta", "mu_r", "mu_k", "mu_v", "mu_w", "mu_a", "mu_g", "mu_c", "W_r", "W_k", "W_v",
@@ -103,6 +126,18 @@ class NativeDecoder:
         check(load().fhe_ssm_decoder_step(self.h, d_x, level, scale, out.ptr, ctypes.byref(lv), ctypes.byref(sc)))
         return out, lv.value, sc.value
 
+    def reset(self) -> None:
+        """drop the carried state: the next step starts cold"""
+        check(load().fhe_ssm_decoder_reset(self.h))
+
+    def serve(self, directory: str, timeout_sec: int = 3600, stateful: bool = True, log_fd: int = -1,
+              poll_ms: int = 200, first_req: int = 0) -> dict:
+        """the serve-directory protocol with this decoder's step as the handler, until `stop` or idle timeout"""
+        opts = ServeOpts(timeout_sec, poll_ms, 1 if stateful else 0, log_fd, first_req)
+        rep = ServeReport()
+        check(load().fhe_ssm_decoder_serve(self.h, directory.encode(), ctypes.byref(opts), ctypes.byref(rep)))
+        return _report(rep)
+
     @property
     def bootstraps(self) -> int:
         n = ctypes.c_uint64()
@@ -119,6 +154,36 @@ class NativeDecoder:
             self.close()
         except Exception:
             pass
+
+
+def _report(rep: ServeReport) -> dict:
+    return {"served": rep.served, "failed": rep.failed, "next_req": rep.next_req,
+            "exit_reason": "stop" if rep.exit_reason == 0 else "idleTimeout"}
+
+
+def serve_dir(directory: str, handler, timeout_sec: int = 3600, stateful: bool = True, log_fd: int = -1,
+              poll_ms: int = 200, first_req: int = 0) -> dict:
+    """the serve-directory protocol loop (host only) with a Python handler
+    handler(req, req_prefix, resp_prefix, meta: dict, reset: bool) -> None; an exception answers resp.N.error"""
+
+    def cb(user, req, req_prefix, resp_prefix, meta_json, reset, err, err_cap):
+        try:
+            handler(int(req), req_prefix.decode(), resp_prefix.decode(), json.loads(meta_json.decode()), bool(reset))
+            return 0
+        except Exception as e:  # reported through the protocol's error marker and log line
+            msg = (type(e).__name__ + ": " + str(e)).encode()[: max(0, err_cap - 1)] + b"\0"
+            ctypes.memmove(err, msg, len(msg))
+            return 1
+
+    fn = ServeHandler(cb)
+    opts = ServeOpts(timeout_sec, poll_ms, 1 if stateful else 0, log_fd, first_req)
+    rep = ServeReport()
+    check(load().fhe_ssm_serve_dir(directory.encode(), ctypes.byref(opts), fn, None, ctypes.byref(rep)))
+    return _report(rep)
+
+
+def meta_int(text: str, key: str, dflt: int = -1) -> int:
+    return int(load().fhe_ssm_meta_int(text.encode(), key.encode(), dflt))
 
 
 def from_backend(be, n_layers: int) -> NativeDecoder:

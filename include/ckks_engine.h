@@ -308,6 +308,19 @@ int ckks_seeded_part_load_key(ckks_context* ctx, const char* path, uint32_t reco
 int ckks_seeded_part_write(ckks_context* ctx, const char* path, const char* key_tag, uint32_t n_keys,
                            const uint32_t* indices, const uint8_t* seeds, const uint64_t* const* d_evks);
 
+/* ---- ciphertext files (the payload of the serve-directory protocol's req.N.t / resp.N.t; the reference serializes
+ * OpenFHE-cereal ciphertexts there, hpc_gpu_port/gpu_real_model.cu:2303-2324, a format only OpenFHE reads) ------
+ * Layout (little-endian): char[8] "FSSMCTX1"; u32 version = 1; u32 N; u32 level; u32 n_polys = 2; f64 scale;
+ * u64 moduli[level]; u64 words[2][level][N] (evaluation form, canonical residues).
+ * ckks_ct_file_info  the header (host only, no context); format and size errors are CKKS_EINVAL
+ * ckks_ct_save       d_ct [2][level][N] of this context into a file
+ * ckks_ct_load       a file into d_ct (room for cap_level limbs); its ring, moduli and words must be this
+ *                    context's (every word below its prime) */
+int ckks_ct_file_info(const char* path, uint32_t* ring_dim, uint32_t* level, double* scale);
+int ckks_ct_save(ckks_context* ctx, const char* path, const uint64_t* d_ct, uint32_t level, double scale);
+int ckks_ct_load(ckks_context* ctx, const char* path, uint32_t cap_level, uint64_t* d_ct, uint32_t* level,
+                 double* scale);
+
 int ckks_encode(ckks_context* ctx, const double* re, const double* im, uint32_t n_slots, uint32_t level, double scale,
                 uint64_t* d_pt);
 int ckks_encrypt(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_pt, uint32_t level, const uint8_t* seed32,

@@ -70,6 +70,54 @@ int fhe_ssm_decoder_step(fhe_ssm_decoder* dec, const uint64_t* d_x, uint32_t lev
 /* ciphertexts bootstrapped so far (26 per layer per step) */
 int fhe_ssm_decoder_stats(const fhe_ssm_decoder* dec, uint64_t* bootstraps);
 
+/* Drop the carried state (WKV state and both token-shift carries of every layer): the next step starts cold, as
+ * the first one did.  The serve loop's req.N.reset / stateless request (gpu_real_model.cu:4461-4465). */
+int fhe_ssm_decoder_reset(fhe_ssm_decoder* dec);
+
+/* ---- the serve-directory protocol (the reference's persistent --serve DIR loop, gpu_real_model.cu:4363-4483 and
+ * :5525-5576; its client is ml-eval/fhe_client.py:1394-1492) -------------------------------------------------
+ * Inside dir, request N: the client writes req.N.0 .. req.N.<count-1> (ciphertext files, ckks_ct_save's layout),
+ * req.N.meta -- one-line JSON {"count","packTokens","tokensReal","dpad","interleave","lanes","ringDim","level"}
+ * with integer values -- optionally req.N.reset, and req.N.ready last.  The server answers with resp.N.<t>,
+ * resp.N.meta and then resp.N.done (resp.N.error on failure), and only then removes the request's files, the
+ * ready marker last.  While waiting it keeps serve.status ({"nextReq","served","pid","stateful","storeFile"})
+ * current.  It returns on a file named `stop` or after timeout_sec idle seconds. */
+typedef struct {
+    uint32_t timeout_sec; /* idle seconds with no request before returning */
+    uint32_t poll_ms;     /* 0: 200 */
+    int32_t stateful;     /* 0: every request starts from a cold state; 1: the state carries across requests */
+    int32_t log_fd;       /* JSON log lines (waiting, request, stateReset, badRequest, served, exit) go here; -1: none */
+    uint32_t first_req;   /* the first request index (0 for a fresh client session) */
+} fhe_ssm_serve_opts;
+
+typedef struct {
+    uint32_t served;      /* requests answered (done or error) */
+    uint32_t failed;      /* of those, answered with resp.N.error (bad meta included) */
+    uint32_t next_req;    /* the index the server was waiting for when it returned */
+    int32_t exit_reason;  /* 0: stop file; 1: idle timeout */
+} fhe_ssm_serve_report;
+
+/* A request's computation: read req_prefix.<t> for t < count (count and the rest in meta_json), write
+ * resp_prefix.<t> and resp_prefix.meta; reset: drop the carried state first.  Returns 0, or nonzero with a
+ * message in err (err_cap bytes). */
+typedef int (*fhe_ssm_serve_handler)(void* user, uint32_t req, const char* req_prefix, const char* resp_prefix,
+                                     const char* meta_json, int32_t reset, char* err, size_t err_cap);
+
+/* The protocol loop over any handler (host only; no device work of its own). */
+int fhe_ssm_serve_dir(const char* dir, const fhe_ssm_serve_opts* opts, fhe_ssm_serve_handler handler, void* user,
+                      fhe_ssm_serve_report* report);
+
+/* The protocol loop with the decode step as its handler: every request holds count = tokensReal ciphertexts, one
+ * token of up to 32 lanes each (packTokens 1, dpad 1024, ringDim 65536, at the state plan's output level), run as
+ * consecutive steps; resp.N.<t> is step t's output.  A meta that does not describe this layout is answered with
+ * resp.N.error. */
+int fhe_ssm_decoder_serve(fhe_ssm_decoder* dec, const char* dir, const fhe_ssm_serve_opts* opts,
+                          fhe_ssm_serve_report* report);
+
+/* An integer value of a meta sidecar's one-line JSON (the reference's metaInt, gpu_real_model.cu:2327-2331); dflt
+ * when the key is absent. */
+long long fhe_ssm_meta_int(const char* text, const char* key, long long dflt);
+
 #ifdef __cplusplus
 }
 #endif

@@ -381,6 +381,69 @@ def test_native_decoder_matches_python_plan(engine, DS, M):
 
 
 @pytest.mark.timeout(900)
+def test_native_decoder_serves_a_directory(engine, M, tmp_path):
+    """the serve-directory protocol with the decode step as its handler (one layer): a stateful session -- two
+    tokens with the reset marker, then one more token, then a reset request -- and a request in another layout;
+    every response file equals the direct steps' output word for word (cold start, carried state, reset)"""
+    import os
+    import threading
+    ND = load_module("native_decode")
+    SC = load_module("serve_client")
+    be, sk = engine
+    W = M.make_weights(5, n_layers=1)
+    nat = ND.from_backend(be, 1)
+    nat.set_weights(W)
+    top = be.top_level
+    xs = [be.encrypt(sk, M.pack_lanes(M.embed_tokens(np.arange(32) + 100 * s)), top, seed=bytes([8, s]) * 16)
+          for s in range(3)]
+    d = str(tmp_path)
+    box = {}
+    log = open(os.path.join(d, "server.jsonl"), "w")
+
+    def run():
+        box["rep"] = nat.serve(d, timeout_sec=600, stateful=True, log_fd=log.fileno(), poll_ms=20)
+    th = threading.Thread(target=run, daemon=True)
+    th.start()
+
+    def writer(cts):
+        return lambda t, path: be.ctx.ct_save(path, cts[t].ptr(), cts[t].level, cts[t].scale)
+    SC.submit(d, 0, writer(xs[:2]), 2, SC.request_meta(2, 32, top), reset=True)
+    r0 = SC.wait(d, 0, timeout=600, alive=th.is_alive)
+    SC.submit(d, 1, writer(xs[2:]), 1, SC.request_meta(1, 32, top))
+    r1 = SC.wait(d, 1, timeout=600, alive=th.is_alive)
+    SC.submit(d, 2, writer(xs[2:]), 1, SC.request_meta(1, 32, top), reset=True)
+    r2 = SC.wait(d, 2, timeout=600, alive=th.is_alive)
+    SC.submit(d, 3, writer(xs[:1]), 1, SC.request_meta(1, 32, top, pack_tokens=2))
+    with pytest.raises(SC.ServeError):
+        SC.wait(d, 3, timeout=600, alive=th.is_alive)
+    SC.stop(d)
+    th.join(timeout=120)
+    log.close()
+    assert not th.is_alive()
+    assert box["rep"] == {"served": 4, "failed": 1, "next_req": 4, "exit_reason": "stop"}, box
+    # the same tokens as direct steps
+    want = []
+    nat.reset()
+    for s in range(3):
+        o, lv, sc = nat.step(xs[s].ptr(), top, xs[s].scale)
+        want.append((o.download((2, lv, N)), lv, sc))
+    nat.reset()
+    o, lv, sc = nat.step(xs[2].ptr(), top, xs[2].scale)
+    want.append((o.download((2, lv, N)), lv, sc))
+    ckks = load_ckks()
+    for (prefix, t), (w, lv, sc) in zip([(r0, 0), (r0, 1), (r1, 0), (r2, 0)], want):
+        path = f"{prefix}.{t}"
+        assert ckks.ct_file_info(path) == {"N": N, "level": lv, "scale": sc}
+        buf = ckks.DeviceBuffer(2 * lv * N * 8)
+        assert be.ctx.ct_load(path, buf.ptr, lv) == (lv, sc)
+        assert np.array_equal(buf.download((2, lv, N)), w), path
+    m0 = SC.response_meta(d, 0)
+    assert (m0["count"], m0["tokensReal"], m0["lanes"], m0["level"], m0["ringDim"]) == (2, 2, 32, want[0][1], N)
+    print(f"served 4 requests; responses == direct steps at level {want[0][1]}")
+    nat.close()
+
+
+@pytest.mark.timeout(900)
 def test_decode_step_full_config5(engine, DS, M):
     """the full config-5 step: 12 layers, two tokens (cold start, then the carried state); decrypted output
     and the client's vocabulary logits against the float64 model, relErrRms <= 1e-3"""

@@ -2,7 +2,13 @@
 the C ABI.  CPU: the header reader against files written from the specification (tests/keypart_util.py), and its
 refusals.  GPU: a key loaded from such a file is b from the file and a = the ChaCha20 expansion of its seed (the
 oracle's sampler, pinned by RFC 8439 vectors in test_oracle); the engine's writer produces the specification's bytes
-for a generated key, and reading them back gives the key word for word."""
+for a generated key, and reading them back gives the key word for word.
+
+Ciphertext files (the serve protocol's req.N.t / resp.N.t; the engine's own flat layout, declared in
+include/ckks_engine.h): the header reader against files written from that layout, its refusals, and on the GPU
+save == the layout's bytes, load == the saved words, refusals of another chain and of words >= q."""
+import struct
+
 import numpy as np
 import pytest
 
@@ -68,6 +74,45 @@ def test_missing_file(tmp_path):
     ckks = load_ckks()
     with pytest.raises(ckks.CkksError):
         ckks.seeded_part_header(str(tmp_path / "nope.bin"))
+
+
+def ct_bytes(n, level, scale, moduli, words, magic=b"FSSMCTX1", version=1, n_polys=2):
+    """a ciphertext file from the layout: magic, u32 version, N, level, n_polys, f64 scale, u64 moduli[level],
+    u64 words[2][level][N], little-endian"""
+    head = magic + struct.pack("<4Id", version, n, level, n_polys, scale)
+    return head + struct.pack(f"<{level}Q", *moduli[:level]) + np.asarray(words, dtype="<u8").tobytes()
+
+
+def test_ct_file_info(tmp_path):
+    ckks = load_ckks()
+    w = np.arange(2 * 3 * N16, dtype=np.uint64).reshape(2, 3, N16) % 97
+    path = _write(tmp_path, "c.bin", ct_bytes(N16, 3, 2.0 ** 40, MOD16, w))
+    assert ckks.ct_file_info(path) == {"N": N16, "level": 3, "scale": 2.0 ** 40}
+
+
+@pytest.mark.parametrize("kind", ["magic", "version", "polys", "scale", "truncated", "longer", "ring"])
+def test_ct_file_refusals(tmp_path, kind):
+    ckks = load_ckks()
+    w = np.zeros((2, 3, N16), dtype=np.uint64)
+    args = dict(n=N16, level=3, scale=2.0 ** 40, moduli=MOD16, words=w)
+    if kind == "magic":
+        args["magic"] = b"FSSMCTX2"
+    elif kind == "version":
+        args["version"] = 2
+    elif kind == "polys":
+        args["n_polys"] = 3
+    elif kind == "scale":
+        args["scale"] = 0.0
+    elif kind == "ring":
+        args["n"] = 24
+    data = ct_bytes(**args)
+    if kind == "truncated":
+        data = data[:-8]
+    elif kind == "longer":
+        data = data + b"\0" * 8
+    path = _write(tmp_path, "bad.bin", data)
+    with pytest.raises(ckks.CkksError):
+        ckks.ct_file_info(path)
 
 
 # ---------------------------------------------------------------- GPU
@@ -144,3 +189,31 @@ def test_load_refuses_another_context(tmp_path, ckks, ctx):
                                                   [(5, b"\0" * 32, np.zeros((D + 1, T, N), np.uint64))]))
     with pytest.raises(ckks.CkksError):
         ctx.seeded_part_load_key(path2, 0, buf.ptr)
+
+
+@pytest.mark.gpu
+def test_ct_save_matches_layout_and_reloads(tmp_path, ckks, ctx):
+    lv = 3
+    q = np.array(ctx.moduli[:lv], dtype=np.uint64)
+    rng = np.random.default_rng(21)
+    w = rng.integers(0, 2**63, (2, lv, N), dtype=np.uint64) % q[None, :, None]
+    buf = ckks.DeviceBuffer(2 * ctx.L * N * 8)
+    buf.upload(w)
+    path = str(tmp_path / "ct.bin")
+    ctx.ct_save(path, buf.ptr, lv, 2.0 ** 45)
+    assert open(path, "rb").read() == ct_bytes(N, lv, 2.0 ** 45, ctx.moduli, w)
+    back = ckks.DeviceBuffer(2 * ctx.L * N * 8)
+    assert ctx.ct_load(path, back.ptr, ctx.L) == (lv, 2.0 ** 45)
+    assert np.array_equal(back.download((2, lv, N)), w)
+    with pytest.raises(ckks.CkksError):          # more limbs than the destination holds
+        ctx.ct_load(path, back.ptr, lv - 1)
+    bad = w.copy()
+    bad[1, 2, 77] = q[2]                          # a word >= its prime
+    p2 = _write(tmp_path, "ge.bin", ct_bytes(N, lv, 2.0 ** 45, ctx.moduli, bad))
+    with pytest.raises(ckks.CkksError):
+        ctx.ct_load(p2, back.ptr, ctx.L)
+    other = list(ctx.moduli)
+    other[0] = other[1]
+    p3 = _write(tmp_path, "oc.bin", ct_bytes(N, lv, 2.0 ** 45, other, w))
+    with pytest.raises(ckks.CkksError):
+        ctx.ct_load(p3, back.ptr, ctx.L)
