@@ -104,9 +104,11 @@ __global__ __launch_bounds__(256) void k_tensor_sum(const uint64_t* const* __res
 
 // ------------------------------------------------------------------ BConv
 // out_j[k] = sum_i [x_i[k] * qhinv_i]_{q_i} * qhmod[i][j]  mod p_j
-// in  : batch c -> in + c*in_bstride, source limb i at in_off[i]*N, prime in_prime[i]
-// out : batch c -> out + c*out_bstride, target limb j at out_off[j]*N, prime out_prime[j]
+// in  : batch c -> in + c*in_bstride, source limb i at off(in_desc[i])*N, prime prime(in_desc[i])
+// out : batch c -> out + c*out_bstride, target limb j at off(out_desc[j])*N, prime prime(out_desc[j])
 // tab : [n_in] TwPair (qhinv, companion) followed by [n_in][n_out] uint64 qhmod
+// A limb descriptor is one dword, offset | prime << 16: the output loop indexes it with a wave-uniform j, which
+// a scalar load serves (byte or half-word arrays would be read with vector loads, one round trip per output).
 constexpr int kMaxBconvIn = 16;
 constexpr int kMaxBconvOut = 80;
 
@@ -114,11 +116,12 @@ struct BConvArgs {
     uint32_t n_in, n_out;
     uint32_t centered;  // subtract u * (prod of input primes) with u = round(sum_i y_i / q_i)
     uint64_t in_bstride, out_bstride;
-    uint16_t in_off[kMaxBconvIn];
-    uint8_t in_prime[kMaxBconvIn];
-    uint16_t out_off[kMaxBconvOut];
-    uint8_t out_prime[kMaxBconvOut];
+    uint32_t in_desc[kMaxBconvIn];
+    uint32_t out_desc[kMaxBconvOut];
 };
+
+__device__ __forceinline__ uint32_t desc_off(uint32_t d) { return d & 0xFFFFu; }
+__device__ __forceinline__ uint32_t desc_prime(uint32_t d) { return d >> 16; }
 
 // centered residue of v in [0, ql) modulo q: v > ql/2 stands for v - ql (harness/boot_overflow_probe.cpp:93-94)
 __device__ __forceinline__ uint64_t lift_centered(uint64_t v, uint64_t ql, const Barrett& br) {
@@ -160,8 +163,9 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
     uint32_t y0[NIN], y1[NIN];
 #pragma unroll
     for (int i = 0; i < NIN; i++) {
-        const uint64_t q = primes[ba.in_prime[i]].q;
-        y[i] = shoup(__builtin_nontemporal_load(&src[(size_t)ba.in_off[i] * kN]), qhinv[i].w, qhinv[i].wp, q);
+        const uint64_t q = primes[desc_prime(ba.in_desc[i])].q;
+        y[i] = shoup(__builtin_nontemporal_load(&src[(size_t)desc_off(ba.in_desc[i]) * kN]), qhinv[i].w, qhinv[i].wp,
+                     q);
         y0[i] = (uint32_t)y[i] & 0x3FFFFFFFu;
         y1[i] = (uint32_t)(y[i] >> 30);
     }
@@ -221,7 +225,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         n_main = ba.n_out - 1;
         U128 acc, unused;
         sums(n_main, n_main, acc, unused);
-        const Barrett bl = barrett_of(primes[ba.out_prime[n_main]]);
+        const Barrett bl = barrett_of(primes[desc_prime(ba.out_desc[n_main])]);
         correct(acc, n_main, bl);
         const uint64_t conv = reduce_u128(acc, bl);
         ql = bl.q;
@@ -229,7 +233,8 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         if (mb.addc) z = add_mod(z, mb.addc[(size_t)c * kN + k], ql);
     }
     auto finish = [&](U128 acc, uint32_t j) {
-        const Barrett br = barrett_of(primes[ba.out_prime[j]]);
+        const uint32_t dj = ba.out_desc[j];
+        const Barrett br = barrett_of(primes[desc_prime(dj)]);
         correct(acc, j, br);
         if constexpr (kMdr) {
             const uint64_t r = lift_centered(z, ql, br);
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
             acc.hi += (acc.lo < r) ? 1u : 0u;
         }
         // streamed: read once, by the next NTT (nontemporal, so the L2 keeps what is reused)
-        __builtin_nontemporal_store(reduce_u128(acc, br), &dst[(size_t)ba.out_off[j] * kN]);
+        __builtin_nontemporal_store(reduce_u128(acc, br), &dst[(size_t)desc_off(dj) * kN]);
     };
     // two outputs per iteration: independent accumulation chains for the scheduler to interleave
     uint32_t j = 0;
@@ -1064,14 +1069,9 @@ static BConvArgs bconv_args(const BConvPlan& plan, uint64_t in_bstride, const ui
     ba.centered = plan.centered ? 1 : 0;
     ba.in_bstride = in_bstride;
     ba.out_bstride = out_bstride;
-    for (uint32_t i = 0; i < plan.n_in; i++) {
-        ba.in_off[i] = (uint16_t)in_off[i];
-        ba.in_prime[i] = (uint8_t)plan.in_idx[i];
-    }
-    for (uint32_t j = 0; j < plan.n_out; j++) {
-        ba.out_off[j] = (uint16_t)(j < n_written ? out_off[j] : 0);
-        ba.out_prime[j] = (uint8_t)plan.out_idx[j];
-    }
+    for (uint32_t i = 0; i < plan.n_in; i++) ba.in_desc[i] = (in_off[i] & 0xFFFFu) | ((uint32_t)plan.in_idx[i] << 16);
+    for (uint32_t j = 0; j < plan.n_out; j++)
+        ba.out_desc[j] = ((j < n_written ? out_off[j] : 0u) & 0xFFFFu) | ((uint32_t)plan.out_idx[j] << 16);
     return ba;
 }
 
