@@ -142,23 +142,34 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
             ct_bfly(x[k], x[k + h], t[(k >> (4 - s)) << 8], q4, nq);
         }
     }
+    // stages 8+s, s = 4..7: r = 16 rl + k; twiddle 2^(8+s) + b 2^s + (r >> (8-s)) = ... + rl 2^(s-4) + (k >> (8-s)).
+    // Pass B's table (twb) stores each block's 2^s entries of these stages as [k >> (8-s)][rl], so the 16 lanes of a
+    // block read 16 consecutive pairs per load instead of 16 pairs 2^(s-4) apart (one cache line per lane).
+    // A thread uses 2^(s-4) of them per stage.  Stages 4..6 (7 pairs) are loaded before the LDS exchange and stage 7
+    // (8 pairs) right after it, so their latency overlaps the exchange and the earlier stages (the LDS tile already
+    // limits the kernel to 4 waves per SIMD, which leaves room for the registers).
+    TwPair tw4[7], tw7[8];
+#pragma unroll
+    for (int s = 4, n = 0; s < 7; s++)
+#pragma unroll
+        for (int i = 0; i < (1 << (s - 4)); i++, n++) tw4[n] = tw[(256 << s) + (b << s) + (i << 4) + rl];
     // LDS word index of r: r + (r >> 4)
 #pragma unroll
     for (int k = 0; k < 16; k++) L[rl + 17 * k] = x[k];
     __syncthreads();
 #pragma unroll
+    for (int i = 0; i < 8; i++) tw7[i] = tw[(256 << 7) + (b << 7) + (i << 4) + rl];
+#pragma unroll
     for (int k = 0; k < 16; k++) x[k] = L[17 * rl + k];
-    // stages 8+s, s = 4..7: r = 16 rl + k; twiddle 2^(8+s) + b 2^s + (r >> (8-s)) = ... + rl 2^(s-4) + (k >> (8-s)).
-    // Pass B's table (twb) stores each block's 2^s entries of these stages as [k >> (8-s)][rl], so the 16 lanes of a
-    // block read 16 consecutive pairs per load instead of 16 pairs 2^(s-4) apart (one cache line per lane)
 #pragma unroll
     for (int s = 4; s < 8; s++) {
         const int h = 128 >> s;
-        const TwPair* t = tw + (256 << s) + (b << s);
+        const int base = (1 << (s - 4)) - 1;  // stage s's first entry in tw4
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            ct_bfly(x[k], x[k + h], t[((k >> (8 - s)) << 4) + rl], q4, nq);
+            const int i = k >> (8 - s);
+            ct_bfly(x[k], x[k + h], s < 7 ? tw4[base + i] : tw7[i], q4, nq);
         }
     }
     // canonical [0, q), then transpose through LDS for coalesced stores (direct 16-byte stores of each
@@ -187,11 +198,22 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
     uint64_t x[16];
 #pragma unroll
     for (int k = 0; k < 16; k++) L[rl + 17 * k] = __builtin_nontemporal_load(&src[rl + 16 * k]);
+    // u = 0..3: r = 16 rl + k, pairs differ in bit u of k; twiddle ... + (r >> (u+1)) = ... + rl 2^(3-u) + (k >> (u+1)),
+    // stored by pass B's table (twb) as [k >> (u+1)][rl] within each block (consecutive pairs for a block's lanes).
+    // A thread uses 2^(3-u) of them per stage; those of u = 0, 1 (12 pairs) are loaded before the LDS exchange so
+    // that their latency overlaps it (the LDS tile limits the kernel to 4 waves per SIMD; the registers are free)
+    TwPair tw01[12];
+#pragma unroll
+    for (int u = 0, n = 0; u < 2; u++)
+#pragma unroll
+        for (int i = 0; i < (8 >> u); i++, n++) tw01[n] = tw[(32768 >> u) + (b << (7 - u)) + (i << 4) + rl];
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = L[17 * rl + k];
-    // u = 0..3: r = 16 rl + k, pairs differ in bit u of k; twiddle ... + (r >> (u+1)) = ... + rl 2^(3-u) + (k >> (u+1)),
-    // stored by pass B's table (twb) as [k >> (u+1)][rl] within each block (consecutive pairs for a block's lanes)
+    // u = 4..7 (after the second exchange): r = rl + 16k, pairs differ in bit (u-4) of k; r >> (u+1) = k >> (u-3);
+    // pass B's table stores twiddle 2^(15-u) + b 2^(7-u) + j at 2^(15-u) + j 256 + b (the four blocks of a wave read
+    // adjacent pairs).  Those of u = 4, 5 (12 pairs) are loaded once u = 0, 1 have freed their registers.
+    TwPair tw45[12];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int h = 1 << u;
@@ -199,7 +221,14 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            gs_bfly(x[k], x[k + h], t[((k >> (u + 1)) << 4) + rl], q4, nq);
+            const int i = k >> (u + 1);
+            gs_bfly(x[k], x[k + h], u == 0 ? tw01[i] : u == 1 ? tw01[8 + i] : t[(i << 4) + rl], q4, nq);
+        }
+        if (u == 1) {
+#pragma unroll
+            for (int v = 4, n = 0; v < 6; v++)
+#pragma unroll
+                for (int j = 0; j < (8 >> (v - 4)); j++, n++) tw45[n] = tw[(32768 >> v) + b + (j << 8)];
         }
     }
     __syncthreads();
@@ -208,8 +237,6 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = L[rl + 17 * k];
-    // u = 4..7: r = rl + 16k, pairs differ in bit (u-4) of k; r >> (u+1) = k >> (u-3); pass B's table stores twiddle
-    // 2^(15-u) + b 2^(7-u) + j at 2^(15-u) + j 256 + b (the four blocks of a wave read adjacent pairs)
 #pragma unroll
     for (int u = 4; u < 8; u++) {
         const int h = 1 << (u - 4);
@@ -217,7 +244,8 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            gs_bfly(x[k], x[k + h], t[(k >> (u - 3)) << 8], q4, nq);
+            const int j = k >> (u - 3);
+            gs_bfly(x[k], x[k + h], u == 4 ? tw45[j] : u == 5 ? tw45[8 + j] : t[j << 8], q4, nq);
         }
     }
 #pragma unroll
