@@ -834,6 +834,11 @@ struct fhe_ssm_decoder {
     std::unique_ptr<Decoder> dec;
 };
 
+// the library's last-error message, set from the other translation units of the library (host/serve.cpp)
+namespace fhe_ssm_detail {
+void set_error(const std::string& m) { g_err = m; }
+}  // namespace fhe_ssm_detail
+
 namespace {
 
 // the decode step as the serve protocol's handler: one token (up to 32 lanes) per ciphertext file, run as
@@ -962,10 +967,9 @@ int fhe_ssm_decoder_serve(fhe_ssm_decoder* dec, const char* dir, const fhe_ssm_s
         sv.d_in = static_cast<uint64_t*>(p);
     });
     if (rc != CKKS_OK) return rc;
-    rc = fhe_ssm_serve_dir(dir, opts, serve_step, &sv, report);
+    rc = fhe_ssm_serve_dir(dir, opts, serve_step, &sv, report);  // sets the error message itself
     ckks_buffer_free(sv.d_in);
-    if (rc != CKKS_OK) g_err = std::string("serve: ") + dir + " is not a directory";
-    else g_err.clear();
+    if (rc == CKKS_OK) g_err.clear();
     return rc;
 }
 

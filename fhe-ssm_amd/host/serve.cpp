@@ -27,6 +27,10 @@
 
 #include "fhe_ssm_decode.h"
 
+namespace fhe_ssm_detail {
+void set_error(const std::string& m);  // host/decode.cpp
+}  // namespace fhe_ssm_detail
+
 namespace {
 
 using Clock = std::chrono::steady_clock;
@@ -90,9 +94,15 @@ long long fhe_ssm_meta_int(const char* text, const char* key, long long dflt) {
 
 int fhe_ssm_serve_dir(const char* dir, const fhe_ssm_serve_opts* opts, fhe_ssm_serve_handler handler, void* user,
                       fhe_ssm_serve_report* report) {
-    if (!dir || !opts || !handler || !report) return CKKS_EINVAL;
+    if (!dir || !opts || !handler || !report) {
+        fhe_ssm_detail::set_error("serve: null argument");
+        return CKKS_EINVAL;
+    }
     const std::string D(dir);
-    if (!is_dir(D)) return CKKS_EINVAL;
+    if (!is_dir(D)) {
+        fhe_ssm_detail::set_error("serve: " + D + " is not a directory");
+        return CKKS_EINVAL;
+    }
     const int fd = opts->log_fd;
     const uint32_t poll_ms = opts->poll_ms ? opts->poll_ms : 200;
     std::memset(report, 0, sizeof(*report));

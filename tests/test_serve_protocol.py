@@ -172,7 +172,7 @@ def test_stop_file_present_at_start(tmp_path):
 
 
 def test_refuses_a_missing_directory(tmp_path):
-    with pytest.raises(RuntimeError):
+    with pytest.raises(RuntimeError, match="is not a directory"):
         ND.serve_dir(str(tmp_path / "absent"), Mock(), timeout_sec=1)
 
 
@@ -185,3 +185,14 @@ def test_meta_int_matches_whole_keys():
     assert ND.meta_int('{"count":-2}', "count") == -2
     assert json.loads(SC.request_meta(3, 32, 17)) == json.loads(text)
     assert SC.request_meta(3, 32, 17).strip() == text     # the reference's key order, no spaces
+
+
+def test_decoder_entry_points_refuse_null_arguments(tmp_path):
+    """the decoder's serve and reset entry points check their arguments before any device work"""
+    import ctypes
+    lib = ND.load()
+    opts = ND.ServeOpts(1, 10, 1, -1, 0)
+    rep = ND.ServeReport()
+    assert lib.fhe_ssm_decoder_serve(None, str(tmp_path).encode(), ctypes.byref(opts), ctypes.byref(rep)) != 0
+    assert b"null" in lib.fhe_ssm_last_error()
+    assert lib.fhe_ssm_decoder_reset(None) != 0
