@@ -162,8 +162,7 @@ int fhe_ssm_serve_dir(const char* dir, const fhe_ssm_serve_opts* opts, fhe_ssm_s
             log_line(fd, "{\"serve\":\"stateReset\",\"req\":" + std::to_string(n) + "}");
         }
         if (!opts->stateful) reset = 1;  // a stateless server starts every request from a cold state
-        log_line(fd, "{\"serve\":\"request\",\"req\":" + std::to_string(n) + ",\"tokens\":" + std::to_string(tokens) +
-                         ",\"count\":" + std::to_string(count) + "}");
+        log_line(fd, "{\"serve\":\"request\",\"req\":" + std::to_string(n) + ",\"tokens\":" + std::to_string(tokens) + "}");
         const auto t0 = Clock::now();
         char err[512] = {0};
         const int rc = handler(user, n, req.c_str(), resp.c_str(), meta.c_str(), reset, err, sizeof err);

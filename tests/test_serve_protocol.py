@@ -196,3 +196,33 @@ def test_decoder_entry_points_refuse_null_arguments(tmp_path):
     assert lib.fhe_ssm_decoder_serve(None, str(tmp_path).encode(), ctypes.byref(opts), ctypes.byref(rep)) != 0
     assert b"null" in lib.fhe_ssm_last_error()
     assert lib.fhe_ssm_decoder_reset(None) != 0
+
+
+def test_log_matches_a_reference_session(tmp_path):
+    """the log against a reference server session's (tests/golden/serve_log_reference.jsonl, extracted by
+    tests/golden/extract_serve_log.py: its first two one-token requests, the first with the reset marker, then the
+    end of the session): the same events in the same order, each carrying the reference line's keys and the same
+    request numbers, token counts, served counts and failure flags.  The reference's per-stage timing keys of the
+    served line (eval, bootstrap, layer-loop milliseconds, peak VRAM) are not produced here."""
+    from conftest import GOLDEN
+    ref = [json.loads(l) for l in open(os.path.join(GOLDEN, "serve_log_reference.jsonl"))]
+    d = tmp_path
+    th, box, log = start(d, Mock(), stateful=True, timeout_sec=60)
+    send(d, 0, np.ones((1, 2, 4)), reset=True)
+    SC.wait(str(d), 0, timeout=30)
+    send(d, 1, np.ones((1, 2, 4)))
+    SC.wait(str(d), 1, timeout=30)
+    _, events = finish(d, th, box, log)
+    want = ref[:7] + ref[-2:]  # two requests, then the waiting line that ends in `stop`, and the exit line
+    assert [e["serve"] for e in events] == [e["serve"] for e in want]
+    timing = {"reqEvalMs", "reqBootMs", "reqEncPtMs", "reqBoots", "reqNormBootMs", "reqMsPerTokenExBoot",
+              "reqLayerLoopMs", "reqLayerLoopUntimedMs", "reqStageMs", "reqHostPtEncodeMs", "reqHostPtEncodeCount",
+              "peakVramGB"}
+    for i, (ours, theirs) in enumerate(zip(events, want)):
+        keys = set(theirs) - (timing if theirs["serve"] == "served" else set())
+        assert keys <= set(ours), (ours, theirs)
+        if i < 7:
+            for k in ("req", "tokens", "failed", "served"):
+                if k in theirs:
+                    assert ours[k] == theirs[k], (k, ours, theirs)
+    assert events[-1] == {"serve": "exit", "reason": "stop", "served": 2}
