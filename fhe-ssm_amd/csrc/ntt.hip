@@ -131,15 +131,22 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&blk[rl + 16 * k]);
     // stages 8+s, s = 0..3: r = rl + 16k; twiddle 2^(8+s) + b 2^s + (k >> (4-s)), which pass B's table stores at
-    // 2^(8+s) + (k >> (4-s)) 256 + b (the four blocks of a wave read adjacent pairs)
+    // 2^(8+s) + (k >> (4-s)) 256 + b (the four blocks of a wave read adjacent pairs).  All 15 are requested with the
+    // data (left to the compiler, each stage's loads were issued just before its butterflies, one exposed L2 round
+    // trip per stage); their registers are free again for the later stages' twiddles below.
+    TwPair tw03[15];
+#pragma unroll
+    for (int s = 0, n = 0; s < 4; s++)
+#pragma unroll
+        for (int j = 0; j < (1 << s); j++, n++) tw03[n] = tw[(256 << s) + (j << 8) + b];
 #pragma unroll
     for (int s = 0; s < 4; s++) {
         const int h = 8 >> s;
-        const TwPair* t = tw + (256 << s) + b;
+        const int base = (1 << s) - 1;  // stage s's first entry in tw03
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            ct_bfly(x[k], x[k + h], t[(k >> (4 - s)) << 8], q4, nq);
+            ct_bfly(x[k], x[k + h], tw03[base + (k >> (4 - s))], q4, nq);
         }
     }
     // stages 8+s, s = 4..7: r = 16 rl + k; twiddle 2^(8+s) + b 2^s + (r >> (8-s)) = ... + rl 2^(s-4) + (k >> (8-s)).
@@ -200,11 +207,11 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
     for (int k = 0; k < 16; k++) L[rl + 17 * k] = __builtin_nontemporal_load(&src[rl + 16 * k]);
     // u = 0..3: r = 16 rl + k, pairs differ in bit u of k; twiddle ... + (r >> (u+1)) = ... + rl 2^(3-u) + (k >> (u+1)),
     // stored by pass B's table (twb) as [k >> (u+1)][rl] within each block (consecutive pairs for a block's lanes).
-    // A thread uses 2^(3-u) of them per stage; those of u = 0, 1 (12 pairs) are loaded before the LDS exchange so
-    // that their latency overlaps it (the LDS tile limits the kernel to 4 waves per SIMD; the registers are free)
-    TwPair tw01[12];
+    // A thread uses 2^(3-u) of them per stage; all 15 are loaded before the LDS exchange so that their latency
+    // overlaps it (the LDS tile limits the kernel to 4 waves per SIMD; the registers are free)
+    TwPair tw01[15];
 #pragma unroll
-    for (int u = 0, n = 0; u < 2; u++)
+    for (int u = 0, n = 0; u < 4; u++)
 #pragma unroll
         for (int i = 0; i < (8 >> u); i++, n++) tw01[n] = tw[(32768 >> u) + (b << (7 - u)) + (i << 4) + rl];
     __syncthreads();
@@ -212,21 +219,20 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
     for (int k = 0; k < 16; k++) x[k] = L[17 * rl + k];
     // u = 4..7 (after the second exchange): r = rl + 16k, pairs differ in bit (u-4) of k; r >> (u+1) = k >> (u-3);
     // pass B's table stores twiddle 2^(15-u) + b 2^(7-u) + j at 2^(15-u) + j 256 + b (the four blocks of a wave read
-    // adjacent pairs).  Those of u = 4, 5 (12 pairs) are loaded once u = 0, 1 have freed their registers.
-    TwPair tw45[12];
+    // adjacent pairs).  All 15 are loaded once u = 0, 1 have freed their registers.
+    TwPair tw45[15];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int h = 1 << u;
-        const TwPair* t = tw + (32768 >> u) + (b << (7 - u));
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
             const int i = k >> (u + 1);
-            gs_bfly(x[k], x[k + h], u == 0 ? tw01[i] : u == 1 ? tw01[8 + i] : t[(i << 4) + rl], q4, nq);
+            gs_bfly(x[k], x[k + h], tw01[16 - (16 >> u) + i], q4, nq);
         }
         if (u == 1) {
 #pragma unroll
-            for (int v = 4, n = 0; v < 6; v++)
+            for (int v = 4, n = 0; v < 8; v++)
 #pragma unroll
                 for (int j = 0; j < (8 >> (v - 4)); j++, n++) tw45[n] = tw[(32768 >> v) + b + (j << 8)];
         }
@@ -240,12 +246,11 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
 #pragma unroll
     for (int u = 4; u < 8; u++) {
         const int h = 1 << (u - 4);
-        const TwPair* t = tw + (32768 >> u) + b;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
             const int j = k >> (u - 3);
-            gs_bfly(x[k], x[k + h], u == 4 ? tw45[j] : u == 5 ? tw45[8 + j] : t[j << 8], q4, nq);
+            gs_bfly(x[k], x[k + h], tw45[16 - (16 >> (u - 4)) + j], q4, nq);
         }
     }
 #pragma unroll
@@ -262,14 +267,21 @@ __device__ __forceinline__ void inv_a_tile(uint64_t* __restrict__ a, const TwPai
     uint64_t x[16];
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&a[col + 256 * (16 * rg + k)]);
-    // u = 0..3: r = 16 rg + k, pairs differ in bit u of k
+    // u = 0..3: r = 16 rg + k, pairs differ in bit u of k; twiddle (128 >> u) + rg 2^(3-u) + (k >> (u+1)).  Those of
+    // u = 0, 1 (12 pairs) are requested with the data, not just before their butterflies
+    TwPair twa[12];
+#pragma unroll
+    for (int u = 0, n = 0; u < 2; u++)
+#pragma unroll
+        for (int i = 0; i < (8 >> u); i++, n++) twa[n] = tw[(128 >> u) + (rg << (3 - u)) + i];
 #pragma unroll
     for (int u = 0; u < 4; u++) {
         const int h = 1 << u;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            gs_bfly(x[k], x[k + h], tw[(128 >> u) + ((16 * rg + k) >> (u + 1))], q4, nq);
+            const int i = k >> (u + 1);
+            gs_bfly(x[k], x[k + h], u < 2 ? twa[(u ? 8 : 0) + i] : tw[(128 >> u) + (rg << (3 - u)) + i], q4, nq);
         }
     }
 #pragma unroll
