@@ -68,11 +68,20 @@ void log_line(int fd, const std::string& s) {
     }
 }
 
+// a JSON string literal: quote and backslash escaped, control characters as \u00XX
 std::string q(const std::string& s) {
     std::string o = "\"";
     for (char c : s) {
-        if (c == '"' || c == '\\') o += '\\';
-        o += c;
+        if (c == '"' || c == '\\') {
+            o += '\\';
+            o += c;
+        } else if ((unsigned char)c < 0x20) {
+            char buf[8];
+            std::snprintf(buf, sizeof buf, "\\u%04x", (unsigned)(unsigned char)c);
+            o += buf;
+        } else {
+            o += c;
+        }
     }
     return o + "\"";
 }

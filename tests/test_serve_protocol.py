@@ -226,3 +226,12 @@ def test_log_matches_a_reference_session(tmp_path):
                 if k in theirs:
                     assert ours[k] == theirs[k], (k, ours, theirs)
     assert events[-1] == {"serve": "exit", "reason": "stop", "served": 2}
+
+
+def test_log_lines_stay_json_for_any_directory_name(tmp_path):
+    d = tmp_path / 'odd "name"\nwith\tcontrol'
+    d.mkdir()
+    with open(tmp_path / "log.jsonl", "w") as log:
+        ND.serve_dir(str(d), Mock(), timeout_sec=0, poll_ms=10, log_fd=log.fileno())
+    events = [json.loads(l) for l in open(tmp_path / "log.jsonl")]
+    assert events[0]["dir"] == str(d) and events[-1]["reason"] == "idleTimeout"
