@@ -226,10 +226,15 @@ BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scal
             if (f.empty()) f.assign(kSlots, cd(0.0));
             for (uint32_t s = 0; s < kSlots; s++) f[s] += d[s];
         }
+        // a diagonal that holds only the float residue of exact cancellations (below 1e-12 of the level's largest
+        // entry) is zero: encoding it would refuse it (every coefficient below 1/2) or waste a baby-giant term
+        double dmax = 0.0;
+        for (auto& kv : folded)
+            for (auto& v : kv.second) dmax = std::max(dmax, std::abs(v));
         std::vector<cd> dr(kSlots), tmp(kSlots);
         for (auto& [kp, d] : folded) {
             bool nz = false;
-            for (auto& v : d) nz |= std::abs(v) > 0;
+            for (auto& v : d) nz |= std::abs(v) > 1e-12 * dmax;
             if (!nz) continue;
             const uint32_t g = (uint32_t)(kp / bl.nb), b = (uint32_t)(kp % bl.nb);
             const long G = bl.gsteps[g];

@@ -4,6 +4,7 @@
 // secret-key encryption and decryption.  Host code; the limb arithmetic runs in client.hip kernels.
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cmath>
 #include <complex>
 #include <cstring>
@@ -26,7 +27,7 @@ uint64_t invmod_h(uint64_t a, uint64_t q);
 hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,
                       NttMode mode, hipStream_t st);
 hipError_t launch_small_to_rns(const Context& ctx, const int64_t* coef, uint64_t* out, uint32_t n_polys,
-                               const std::vector<uint32_t>& pmap, hipStream_t st);
+                               const std::vector<uint32_t>& pmap, uint32_t log_approx, hipStream_t st);
 hipError_t launch_ksk_b(const Context& ctx, const uint64_t* a, const uint64_t* s_new, const uint64_t* e,
                         const uint64_t* s_old, uint64_t* b, uint32_t lo, uint32_t hi, const TwPair* pmod,
                         hipStream_t st);
@@ -34,8 +35,8 @@ hipError_t launch_encrypt(const Context& ctx, const uint64_t* m, const uint64_t*
                           const uint64_t* s, uint64_t* ct, uint32_t l, hipStream_t st);
 hipError_t launch_decrypt(const Context& ctx, const uint64_t* ct, const uint64_t* s, uint64_t* out, uint32_t l,
                           hipStream_t st);
-hipError_t launch_encode_small(const Context& ctx, const int64_t* coef, uint64_t* out, uint32_t n_vec, uint32_t Np,
-                               uint32_t l, const TwPair* tab, hipStream_t st);
+hipError_t launch_encode_small(const Context& ctx, const int64_t* coef, const int32_t* log_approx, uint64_t* out,
+                               uint32_t n_vec, uint32_t Np, uint32_t l, const TwPair* tab, hipStream_t st);
 hipError_t launch_mul(const Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t l,
                       hipStream_t st);
 
@@ -131,11 +132,12 @@ struct DevBuf {
     T* as() const { return (T*)p; }
 };
 
+// signed coefficients (times 2^log_approx) -> residues of the limbs pmap -> NTT
 void coeffs_to_eval(Context& ctx, const int64_t* h_coef, uint32_t n_polys, const std::vector<uint32_t>& pmap,
-                    uint64_t* d_out, hipStream_t st) {
+                    uint64_t* d_out, hipStream_t st, uint32_t log_approx = 0) {
     DevBuf dc((size_t)n_polys * kN * 8);
     HIPC(hipMemcpy(dc.p, h_coef, (size_t)n_polys * kN * 8, hipMemcpyHostToDevice));
-    HIPC(launch_small_to_rns(ctx, dc.as<int64_t>(), d_out, n_polys, pmap, st));
+    HIPC(launch_small_to_rns(ctx, dc.as<int64_t>(), d_out, n_polys, pmap, log_approx, st));
     JobSpec js{};
     js.n_polys = n_polys;
     js.period = (uint32_t)pmap.size();
@@ -175,6 +177,26 @@ void fft(std::vector<std::complex<double>>& a, int sign) {
     }
 }
 
+// The real coefficients m[0..Np) of the polynomial of the ring of degree Np = 2 slots whose slot j (evaluation at
+// zeta'^(5^j), zeta' = exp(i pi / Np)) is scale * (re[j] + i im[j]): the inverse special FFT, unrounded.
+void slot_coeffs(const double* re, const double* im, uint32_t slots, double scale, double* m) {
+    const uint32_t Np = 2 * slots;
+    const uint64_t M = 2ull * Np;
+    std::vector<std::complex<double>> v(Np, 0.0);
+    uint64_t e = 1;
+    for (uint32_t j = 0; j < slots; j++) {
+        const std::complex<double> z(re ? re[j] : 0.0, im ? im[j] : 0.0);
+        v[(e - 1) / 2] = z * scale;
+        v[(M - e - 1) / 2] = std::conj(z) * scale;
+        e = e * 5 % M;
+    }
+    fft(v, -1);  // sum_t v_t w^(-tk)
+    for (uint32_t k = 0; k < Np; k++) {
+        const double ang = -M_PI * (double)k / (double)Np;  // zeta'^-k
+        m[k] = (v[k] * std::complex<double>(std::cos(ang), std::sin(ang))).real() / (double)Np;
+    }
+}
+
 // t index (evaluation point zeta^(2t+1)) of slot j and of its conjugate
 void slot_points(std::vector<uint32_t>& t_of, std::vector<uint32_t>& tc_of) {
     const uint64_t M = 2ull * kN;
@@ -189,6 +211,32 @@ void slot_points(std::vector<uint32_t>& t_of, std::vector<uint32_t>& tc_of) {
 }
 
 }  // namespace
+
+// The rounding rule of encoded coefficients (OpenFHE CKKSPackedEncoding::Encode, restated in
+// hpc_gpu_port/periodic_encode.hpp:199-236): logc = the largest ceil(log2 |m_k|) over the nonzero scaled coefficients
+// (0 when all are zero; a negative logc -- every coefficient below 1/2 -- is refused as a too small scaling
+// factor); coefficients wider than MAX_BITS_IN_WORD = 61 bits are divided by approxFactor = 2^(logc - 61) before
+// llround (a quotient above 2^63 - 2^9 - 1 is refused), and the residues are multiplied back by 2^(logc - 61) mod q
+// per limb.  Returns log2(approxFactor).
+int32_t round_coeffs(const double* m, uint32_t n, int64_t* coef) {
+    int32_t logc = INT32_MIN;
+    for (uint32_t k = 0; k < n; k++) {
+        if (!std::isfinite(m[k])) throw std::invalid_argument("encode: non-finite value");
+        if (m[k] != 0.0) logc = std::max(logc, (int32_t)std::ceil(std::log2(std::fabs(m[k]))));
+    }
+    if (logc == INT32_MIN) logc = 0;
+    if (logc < 0) throw std::invalid_argument("encode: scaling factor too small (every coefficient is below 1/2)");
+    constexpr int32_t kMaxBitsInWord = 61;
+    const int32_t log_approx = logc > kMaxBitsInWord ? logc - kMaxBitsInWord : 0;
+    const double approx = std::ldexp(1.0, log_approx);
+    const double max_v = (double)(int64_t)((1ull << 63) - (1ull << 9) - 1);
+    for (uint32_t k = 0; k < n; k++) {
+        const double v = m[k] / approx;
+        if (std::fabs(v) > max_v) throw std::invalid_argument("encode: coefficient overflows after approxFactor");
+        coef[k] = (int64_t)std::llround(v);
+    }
+    return log_approx;
+}
 
 // ---------------------------------------------------------------- public (C++) API used by abi.cpp
 void sample_ternary(const uint8_t seed[32], uint32_t h, int8_t* s) {
@@ -328,28 +376,20 @@ void encode(Context& ctx, const double* re, const double* im, uint32_t n_slots, 
     encode_primes(ctx, re, im, n_slots, iota(l), scale, d_pt);
 }
 
-// the same plaintext over the primes pmap (limb t of the output is mod prime pmap[t])
+// the same plaintext over the primes pmap (limb t of the output is mod prime pmap[t]).  A vector of n_slots < N/2
+// (replicated over the N/2 slots) is sparsely packed as OpenFHE packs a batch smaller than N/2: the coefficients
+// are those of the ring of degree 2 n_slots, placed at stride N / (2 n_slots) -- the same polynomial the full
+// special FFT of the replicated vector describes, computed from one period.
 void encode_primes(Context& ctx, const double* re, const double* im, uint32_t n_slots,
                    const std::vector<uint32_t>& pmap, double scale, uint64_t* d_pt) {
     if (n_slots == 0 || (kN / 2) % n_slots != 0) throw std::invalid_argument("n_slots must divide N/2");
-    std::vector<uint32_t> t_of, tc_of;
-    slot_points(t_of, tc_of);
-    std::vector<std::complex<double>> v(kN, 0.0);
-    for (uint32_t j = 0; j < kN / 2; j++) {
-        const uint32_t s = j % n_slots;
-        const std::complex<double> z(re ? re[s] : 0.0, im ? im[s] : 0.0);
-        v[t_of[j]] = z * scale;
-        v[tc_of[j]] = std::conj(z) * scale;
-    }
-    fft(v, -1);  // sum_t v_t w^(-tk)
-    std::vector<int64_t> coef(kN);
-    for (uint32_t k = 0; k < kN; k++) {
-        const double ang = -M_PI * (double)k / (double)kN;  // zeta^-k
-        const double m = (v[k] * std::complex<double>(std::cos(ang), std::sin(ang))).real() / (double)kN;
-        if (!(std::fabs(m) < 4.0e18)) throw std::invalid_argument("encoded coefficient overflows int64");
-        coef[k] = (int64_t)std::llround(m);
-    }
-    coeffs_to_eval(ctx, coef.data(), 1, pmap, d_pt, nullptr);
+    const uint32_t Np = 2 * n_slots, rep = kN / Np;
+    std::vector<double> m(Np);
+    slot_coeffs(re, im, n_slots, scale, m.data());
+    std::vector<int64_t> small(Np), coef(kN, 0);
+    const int32_t log_approx = round_coeffs(m.data(), Np, small.data());
+    for (uint32_t k = 0; k < Np; k++) coef[(size_t)k * rep] = small[k];
+    coeffs_to_eval(ctx, coef.data(), 1, pmap, d_pt, nullptr, (uint32_t)log_approx);
 }
 
 // Periodic encoding (hpc_gpu_port/periodic_encode.hpp:179-260): a slot vector of period P (replicated
@@ -365,7 +405,6 @@ void encode_periodic(Context& ctx, const double* re, const double* im, uint32_t 
     uint32_t logNp = 0;
     while ((1u << logNp) < Np) logNp++;
     const uint32_t rep = kN / Np;
-    const uint64_t M = 2ull * Np;
     auto it = ctx.small_ntt.find(Np);
     if (it == ctx.small_ntt.end()) {
         // Table[brev(j)] = psi'^j with psi' = psi^rep, per prime of the chain
@@ -387,36 +426,24 @@ void encode_periodic(Context& ctx, const double* re, const double* im, uint32_t 
         HIPC(hipMemcpy(d, tabs.data(), tabs.size() * sizeof(TwPair), hipMemcpyHostToDevice));
         it = ctx.small_ntt.emplace(Np, d).first;
     }
-    std::vector<uint32_t> t_of(P), tc_of(P);
-    {
-        uint64_t e = 1;
-        for (uint32_t j = 0; j < P; j++) {
-            t_of[j] = (uint32_t)((e - 1) / 2);
-            tc_of[j] = (uint32_t)((M - e - 1) / 2);
-            e = e * 5 % M;
-        }
-    }
     std::vector<int64_t> coef((size_t)n_vec * Np);
-    std::atomic<bool> overflow{false};
+    std::vector<int32_t> log_approx(n_vec, 0);
+    std::vector<std::string> errs(n_vec);
     parallel_for(n_vec, [&](uint32_t n) {
-        std::vector<std::complex<double>> v(Np, 0.0);
-        for (uint32_t j = 0; j < P; j++) {
-            const std::complex<double> z(re ? re[(size_t)n * P + j] : 0.0, im ? im[(size_t)n * P + j] : 0.0);
-            v[t_of[j]] = z * scale;
-            v[tc_of[j]] = std::conj(z) * scale;
-        }
-        fft(v, -1);
-        for (uint32_t k = 0; k < Np; k++) {
-            const double ang = -M_PI * (double)k / (double)Np;
-            const double m = (v[k] * std::complex<double>(std::cos(ang), std::sin(ang))).real() / (double)Np;
-            if (!(std::fabs(m) < 4.0e18)) overflow = true;
-            coef[(size_t)n * Np + k] = overflow ? 0 : (int64_t)std::llround(m);
+        std::vector<double> m(Np);
+        slot_coeffs(re ? re + (size_t)n * P : nullptr, im ? im + (size_t)n * P : nullptr, P, scale, m.data());
+        try {
+            log_approx[n] = round_coeffs(m.data(), Np, coef.data() + (size_t)n * Np);
+        } catch (const std::exception& e) {
+            errs[n] = e.what();
         }
     });
-    if (overflow) throw std::invalid_argument("encoded coefficient overflows int64");
-    DevBuf dc(coef.size() * 8);
+    for (const auto& e : errs)
+        if (!e.empty()) throw std::invalid_argument(e);
+    DevBuf dc(coef.size() * 8), dl(log_approx.size() * 4);
     HIPC(hipMemcpy(dc.p, coef.data(), coef.size() * 8, hipMemcpyHostToDevice));
-    HIPC(launch_encode_small(ctx, dc.as<int64_t>(), d_out, n_vec, Np, l, it->second, nullptr));
+    HIPC(hipMemcpy(dl.p, log_approx.data(), log_approx.size() * 4, hipMemcpyHostToDevice));
+    HIPC(launch_encode_small(ctx, dc.as<int64_t>(), dl.as<int32_t>(), d_out, n_vec, Np, l, it->second, nullptr));
     HIPC(hipDeviceSynchronize());
 }
 

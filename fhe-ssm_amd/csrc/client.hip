@@ -11,9 +11,28 @@ namespace {
 
 __device__ __forceinline__ Barrett barrett_c(const PrimeInfo& p) { return Barrett{p.q, p.mu_hi, p.mu_lo}; }
 
-// out[pc][l][k] = coef[pc][k] mod q_{pmap[l]} (signed coefficients)
+// residue of a signed coefficient: c mod q, or q - (|c| mod q) for c < 0 (0 when q divides |c|)
+__device__ __forceinline__ uint64_t signed_residue(int64_t c, uint64_t q) {
+    if (c >= 0) return (uint64_t)c % q;
+    const uint64_t m = (uint64_t)(-(c + 1)) % q;  // -(c+1) >= 0 even for INT64_MIN
+    return (m + 1 == q) ? 0 : q - 1 - m;
+}
+
+// 2^e mod q (square and multiply)
+__device__ __forceinline__ uint64_t pow2_mod(uint32_t e, const Barrett& br) {
+    uint64_t r = 1 % br.q, b = 2 % br.q;
+    for (; e; e >>= 1) {
+        if (e & 1) r = mul_mod(r, b, br);
+        b = mul_mod(b, b, br);
+    }
+    return r;
+}
+
+// out[pc][l][k] = coef[pc][k] 2^log_approx mod q_{pmap[l]} (signed coefficients; log_approx > 0 only for plaintexts
+// whose coefficients were divided by 2^log_approx before rounding)
 struct PmapArgs {
     uint32_t n_limbs;
+    uint32_t log_approx;
     uint8_t pmap[kMaxPmap];
 };
 
@@ -21,14 +40,11 @@ __global__ __launch_bounds__(256) void k_small_to_rns(const int64_t* __restrict_
                                                       PmapArgs pa, const PrimeInfo* __restrict__ primes) {
     const uint32_t k = blockIdx.x * 256 + threadIdx.x;
     const uint32_t l = blockIdx.y, pc = blockIdx.z;
-    const uint64_t q = primes[pa.pmap[l]].q;
-    const int64_t c = coef[(size_t)pc * kN + k];
-    uint64_t r;
-    if (c >= 0) {
-        r = (uint64_t)c % q;
-    } else {
-        const uint64_t m = (uint64_t)(-(c + 1)) % q;  // -(c+1) >= 0 even for INT64_MIN
-        r = (m + 1 == q) ? 0 : q - 1 - m;
+    const PrimeInfo& P = primes[pa.pmap[l]];
+    uint64_t r = signed_residue(coef[(size_t)pc * kN + k], P.q);
+    if (pa.log_approx) {
+        const Barrett br = barrett_c(P);
+        r = mul_mod(r, pow2_mod(pa.log_approx, br), br);
     }
     out[((size_t)pc * pa.n_limbs + l) * kN + k] = r;
 }
@@ -92,21 +108,25 @@ __global__ __launch_bounds__(256) void k_mul(const uint64_t* __restrict__ x, con
 }  // namespace
 
 // Periodic-plaintext encoder: vector n, limb i -> the N'-point negacyclic NTT (root psi^(N/N'), output in
-// bit-reversed order) of the small polynomial coef[n] mod q_i.  One workgroup per (n, i), the limb in LDS.
+// bit-reversed order) of the small polynomial coef[n] 2^log_approx[n] mod q_i.  One workgroup per (n, i), the limb
+// in LDS.
 constexpr int kMaxSmallN = 4096;
 
-__global__ __launch_bounds__(256) void k_encode_small(const int64_t* __restrict__ coef, uint64_t* __restrict__ out,
-                                                      uint32_t Np, uint32_t l, const TwPair* __restrict__ tab,
+__global__ __launch_bounds__(256) void k_encode_small(const int64_t* __restrict__ coef,
+                                                      const int32_t* __restrict__ log_approx,
+                                                      uint64_t* __restrict__ out, uint32_t Np, uint32_t l,
+                                                      const TwPair* __restrict__ tab,
                                                       const PrimeInfo* __restrict__ primes) {
     __shared__ uint64_t a[kMaxSmallN];
     const uint32_t n = blockIdx.x, i = blockIdx.y;
     const uint64_t q = primes[i].q;
     const int64_t* c = coef + (size_t)n * Np;
+    const uint32_t la = (uint32_t)log_approx[n];
+    const Barrett br = barrett_c(primes[i]);
+    const uint64_t f = la ? pow2_mod(la, br) : 1;
     for (uint32_t k = threadIdx.x; k < Np; k += 256) {
-        const int64_t v = c[k];
-        // |v| < 2^62: the residue of a negative value is q - (|v| mod q)
-        const uint64_t r = v >= 0 ? (uint64_t)v % q : (uint64_t)(-(v + 1)) % q;
-        a[k] = v >= 0 ? r : q - 1 - r;
+        const uint64_t r = signed_residue(c[k], q);
+        a[k] = la ? mul_mod(r, f, br) : r;
     }
     __syncthreads();
     const TwPair* tw = tab + (size_t)i * Np;
@@ -125,17 +145,20 @@ __global__ __launch_bounds__(256) void k_encode_small(const int64_t* __restrict_
     for (uint32_t k = threadIdx.x; k < Np; k += 256) o[k] = a[k];
 }
 
-hipError_t launch_encode_small(const Context& ctx, const int64_t* coef, uint64_t* out, uint32_t n_vec, uint32_t Np,
-                               uint32_t l, const TwPair* tab, hipStream_t st) {
+hipError_t launch_encode_small(const Context& ctx, const int64_t* coef, const int32_t* log_approx, uint64_t* out,
+                               uint32_t n_vec, uint32_t Np, uint32_t l, const TwPair* tab, hipStream_t st) {
     if (Np > (uint32_t)kMaxSmallN || Np < 2) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_encode_small, dim3(n_vec, l), dim3(256), 0, st, coef, out, Np, l, tab, ctx.d_primes);
+    hipLaunchKernelGGL(k_encode_small, dim3(n_vec, l), dim3(256), 0, st, coef, log_approx, out, Np, l, tab,
+                       ctx.d_primes);
     return hipGetLastError();
 }
 
 hipError_t launch_small_to_rns(const Context& ctx, const int64_t* coef, uint64_t* out, uint32_t n_polys,
-                               const std::vector<uint32_t>& pmap, hipStream_t st) {
+                               const std::vector<uint32_t>& pmap, uint32_t log_approx, hipStream_t st) {
+    if (pmap.size() > kMaxPmap) return hipErrorInvalidValue;
     PmapArgs pa{};
     pa.n_limbs = (uint32_t)pmap.size();
+    pa.log_approx = log_approx;
     for (size_t i = 0; i < pmap.size(); i++) pa.pmap[i] = (uint8_t)pmap[i];
     hipLaunchKernelGGL(k_small_to_rns, dim3(kN / 256, pa.n_limbs, n_polys), dim3(256), 0, st, coef, out, pa,
                        ctx.d_primes);

@@ -96,7 +96,9 @@ SeededPartHeader read_seeded_part_header(const std::string& path) {
     h.count = get32(is, "header");
     const uint32_t tag_len = get32(is, "header");
     if (tag_len > 4096) throw std::invalid_argument("seeded part: key tag too long");
-    if (h.N == 0 || (h.N & (h.N - 1)) || h.size_q + h.size_p > 4096 || h.num_part_q == 0)
+    // bounds that keep record_bytes below 2^48 (N <= 2^17, at most 4096 limbs, at most one digit per limb)
+    if (h.N == 0 || (h.N & (h.N - 1)) || h.N > (1u << 17) || h.size_q + h.size_p > 4096 || h.num_part_q == 0 ||
+        h.num_part_q > h.size_q + h.size_p)
         throw std::invalid_argument("seeded part: implausible layout");
     h.key_tag.assign(tag_len, '\0');
     if (tag_len && !is.read(&h.key_tag[0], tag_len)) throw std::invalid_argument("seeded part: short key tag");
@@ -106,7 +108,8 @@ SeededPartHeader read_seeded_part_header(const std::string& path) {
     // every record present
     is.seekg(0, std::ios::end);
     const uint64_t size = (uint64_t)is.tellg();
-    if (size < h.header_bytes + (uint64_t)h.count * record_bytes(h))
+    // count records must fit (compared by division: count * record_bytes could overflow for a crafted header)
+    if (size < h.header_bytes || (size - h.header_bytes) / record_bytes(h) < h.count)
         throw std::invalid_argument("seeded part: file shorter than its key count");
     return h;
 }
@@ -116,7 +119,7 @@ std::vector<uint32_t> seeded_part_indices(const std::string& path) {
     std::ifstream is(path, std::ios::binary);
     std::vector<uint32_t> idx(h.count);
     for (uint32_t r = 0; r < h.count; r++) {
-        is.seekg((std::streamoff)(h.header_bytes + r * record_bytes(h)));
+        is.seekg((std::streamoff)(h.header_bytes + (uint64_t)r * record_bytes(h)));
         idx[r] = get32(is, "key record");
     }
     return idx;
@@ -127,7 +130,7 @@ void load_seeded_part_key(Context& ctx, const std::string& path, uint32_t record
     check_layout(ctx, h);
     if (record >= h.count) throw std::invalid_argument("seeded part: record index past the key count");
     std::ifstream is(path, std::ios::binary);
-    is.seekg((std::streamoff)(h.header_bytes + record * record_bytes(h)));
+    is.seekg((std::streamoff)(h.header_bytes + (uint64_t)record * record_bytes(h)));
     const uint32_t g = get32(is, "key record");
     uint8_t seed[32];
     if (!is.read((char*)seed, 32)) throw std::invalid_argument("seeded part: short seed");
@@ -136,9 +139,14 @@ void load_seeded_part_key(Context& ctx, const std::string& path, uint32_t record
     for (uint32_t d = 0; d < ctx.dnum; d++) {
         if (!is.read((char*)b.data(), (std::streamsize)(b.size() * 8)))
             throw std::invalid_argument("seeded part: short b words");
-        for (uint32_t i = 0; i < T; i++)
-            for (uint32_t k = 0; k < kN; k += 4099)  // spot check: residues below their modulus
-                if (b[(size_t)i * kN + k] >= ctx.moduli[i]) throw std::invalid_argument("seeded part: b word >= q");
+        // every word below its modulus: the key-switch accumulators rely on operands below 2^60
+        for (uint32_t i = 0; i < T; i++) {
+            const uint64_t q = ctx.moduli[i];
+            const uint64_t* bi = b.data() + (size_t)i * kN;
+            uint64_t bad = 0;
+            for (uint32_t k = 0; k < kN; k++) bad |= (uint64_t)(bi[k] >= q);
+            if (bad) throw std::invalid_argument("seeded part: b word >= q");
+        }
         HIPC(hipMemcpy(d_evk + (size_t)d * 2 * T * kN, b.data(), b.size() * 8, hipMemcpyHostToDevice));
     }
     expand_key_a(ctx, seed, d_evk);

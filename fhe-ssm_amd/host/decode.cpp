@@ -581,15 +581,23 @@ class Decoder {
         if (want == 0) throw Error(CKKS_EINVAL, "unknown weight " + name);
         if (count != want) throw Error(CKKS_EINVAL, "weight " + name + ": " + std::to_string(want) + " values");
         if (layer >= (int32_t)layers_.size()) throw Error(CKKS_EINVAL, "layer out of range");
+        // plaintexts and matvec diagonals are encoded from the weights on first use and cached by name and level
+        if (!pt_.empty() || !mv_.empty())
+            throw Error(CKKS_EINVAL, "weights are fixed once a step has encoded them (set every weight before the "
+                                     "first step)");
         auto& dst = layer < 0 ? model_.v[name] : layers_[layer].v[name];
         dst.assign(data, data + count);
     }
 
+    // One step over the carried state.  The step works on a copy of the state (handles: the ciphertexts are shared,
+    // never written in place) and commits it only once every layer has succeeded, so a step that throws leaves the
+    // state of the previous step untouched (the reference commits its carry after the whole pass,
+    // gpu_real_model.cu:5284-5286).
     Ct step(const Ct& x_in) {
-        if (state_.empty()) cold_state();
+        std::vector<LayerState> work = state_.empty() ? cold_state() : state_;
         Ct x = x_in;
         for (uint32_t li = 0; li < layers_.size(); li++) {
-            LayerState& st = state_[li];
+            LayerState& st = work[li];
             x = be_->add(x, boot(time_mix(li, x, st), "inc_tm"));
             refresh_state(st);
             x = be_->add(x, boot(channel_mix(li, x, st), "inc_cm"));
@@ -597,12 +605,17 @@ class Decoder {
         Ct xo = norm(x, model_["p_o"]);
         std::vector<double> go(DPAD, 0.0);
         std::copy(model_["g_o"].begin(), model_["g_o"].end(), go.begin());
-        return be_->mul_pt(xo, *vec_pt("g_o", xo.level, [&] { return go; }));
+        Ct out = be_->mul_pt(xo, *vec_pt("g_o", xo.level, [&] { return go; }));
+        state_ = std::move(work);
+        return out;
     }
 
     uint64_t bootstraps() const { return n_boot_; }
     // the next step starts cold (zero WKV state and token-shift carries), as the first one does
     void reset() { state_.clear(); }
+    // the carried state as handles (for a caller that must undo several steps, e.g. a multi-token request)
+    std::vector<LayerState> snapshot() const { return state_; }
+    void restore(std::vector<LayerState> s) { state_ = std::move(s); }
 
    private:
     // plaintexts, encoded on first use at the level they are applied
@@ -788,16 +801,17 @@ class Decoder {
             for (uint32_t t = 0; t < q; t++) st.Didx.push_back({k, t});
     }
 
-    void cold_state() {
+    std::vector<LayerState> cold_state() {
         const uint32_t lt = be_->top_level();
-        state_.resize(layers_.size());
-        for (auto& st : state_) {
+        std::vector<LayerState> state(layers_.size());
+        for (auto& st : state) {
             st.Dseg = {be_->zeros(WKV_T, lt)};
             st.Didx.clear();
             for (uint32_t t = 0; t < (uint32_t)WKV_T; t++) st.Didx.push_back({0, t});
             st.xp_t = be_->zeros(1, lt);
             st.xp_c = be_->zeros(1, lt);
         }
+        return state;
     }
 
     Engine* be_;
@@ -849,6 +863,9 @@ struct ServeState {
     uint64_t* d_in;
 };
 
+void serve_tokens(ServeState* sv, const char* req_prefix, const char* resp_prefix, long long count, long long tokens,
+                  long long lanes, bool reset);
+
 int serve_step(void* user, uint32_t, const char* req_prefix, const char* resp_prefix, const char* meta, int32_t reset,
                char* err, size_t err_cap) {
     auto* sv = static_cast<ServeState*>(user);
@@ -865,30 +882,47 @@ int serve_step(void* user, uint32_t, const char* req_prefix, const char* resp_pr
         if (lanes < 1 || lanes > (long long)(kN / 2 / DPAD)) throw Error(CKKS_EINVAL, "lanes must be in [1, 32]");
         if (mi("level", -1) != (long long)top)
             throw Error(CKKS_EINVAL, "request level must be the state plan's output level " + std::to_string(top));
-        if (reset) sv->dec->dec->reset();
-        uint32_t out_level = 0;
-        for (long long t = 0; t < count; t++) {
-            const std::string in = std::string(req_prefix) + "." + std::to_string(t);
-            uint32_t lvl = 0;
-            double sc = 0.0;
-            ck(ckks_ct_load(be.ctx(), in.c_str(), top, sv->d_in, &lvl, &sc), "ckks_ct_load");
-            if (lvl != top) throw Error(CKKS_EINVAL, in + ": not at the state plan's output level");
-            if (std::fabs(sc / be.S(top) - 1.0) > 1e-9) throw Error(CKKS_EINVAL, in + ": scale is not S(level)");
-            Ct y = sv->dec->dec->step(Engine::borrowed(sv->d_in, 1, top, sc));
-            const std::string out = std::string(resp_prefix) + "." + std::to_string(t);
-            ck(ckks_ct_save(be.ctx(), out.c_str(), y.ptr(), y.level, y.scale), "ckks_ct_save");
-            out_level = y.level;
+        // a request is all or nothing: on any failure the carried state is the one from before the request
+        // (reset included), as in the reference, which commits its carry only after the whole pass
+        // (gpu_real_model.cu:5284-5286)
+        Decoder& dec = *sv->dec->dec;
+        auto before = dec.snapshot();
+        try {
+            serve_tokens(sv, req_prefix, resp_prefix, count, tokens, lanes, reset != 0);
+        } catch (...) {
+            dec.restore(std::move(before));
+            throw;
         }
-        FILE* f = std::fopen((std::string(resp_prefix) + ".meta").c_str(), "w");
-        if (!f) throw Error(CKKS_EINVAL, "cannot write the response meta");
-        std::fprintf(f,
-                     "{\"count\":%lld,\"packTokens\":1,\"tokensReal\":%lld,\"dpad\":%d,\"interleave\":0,"
-                     "\"lanes\":%lld,\"ringDim\":%u,\"level\":%u}\n",
-                     count, tokens, DPAD, lanes, kN, out_level);
-        if (std::fclose(f) != 0) throw Error(CKKS_EINVAL, "cannot write the response meta");
     });
     if (rc != CKKS_OK && err && err_cap) std::snprintf(err, err_cap, "%s", g_err.c_str());
     return rc;
+}
+
+void serve_tokens(ServeState* sv, const char* req_prefix, const char* resp_prefix, long long count, long long tokens,
+                  long long lanes, bool reset) {
+    Engine& be = *sv->dec->be;
+    const uint32_t top = be.top_level();
+    if (reset) sv->dec->dec->reset();
+    uint32_t out_level = 0;
+    for (long long t = 0; t < count; t++) {
+        const std::string in = std::string(req_prefix) + "." + std::to_string(t);
+        uint32_t lvl = 0;
+        double sc = 0.0;
+        ck(ckks_ct_load(be.ctx(), in.c_str(), top, sv->d_in, &lvl, &sc), "ckks_ct_load");
+        if (lvl != top) throw Error(CKKS_EINVAL, in + ": not at the state plan's output level");
+        if (std::fabs(sc / be.S(top) - 1.0) > 1e-9) throw Error(CKKS_EINVAL, in + ": scale is not S(level)");
+        Ct y = sv->dec->dec->step(Engine::borrowed(sv->d_in, 1, top, sc));
+        const std::string out = std::string(resp_prefix) + "." + std::to_string(t);
+        ck(ckks_ct_save(be.ctx(), out.c_str(), y.ptr(), y.level, y.scale), "ckks_ct_save");
+        out_level = y.level;
+    }
+    FILE* f = std::fopen((std::string(resp_prefix) + ".meta").c_str(), "w");
+    if (!f) throw Error(CKKS_EINVAL, "cannot write the response meta");
+    std::fprintf(f,
+                 "{\"count\":%lld,\"packTokens\":1,\"tokensReal\":%lld,\"dpad\":%d,\"interleave\":0,"
+                 "\"lanes\":%lld,\"ringDim\":%u,\"level\":%u}\n",
+                 count, tokens, DPAD, lanes, kN, out_level);
+    if (std::fclose(f) != 0) throw Error(CKKS_EINVAL, "cannot write the response meta");
 }
 
 }  // namespace

@@ -307,3 +307,57 @@ class Ctx:
         evk = np.zeros((self.dnum, 2, T, self.N), dtype=np.uint64)
         lib().or_ksk_gen(self.ref, _p(so), _p(sn), _p(sd), _p(es), sigma, _p(evk))
         return evk
+
+
+# ---------------------------------------------------------------- CKKS encoding (float part + the reference's rule)
+def slot_coeffs(z, scale: float) -> np.ndarray:
+    """Unrounded coefficients m[0..Np) of the polynomial of the ring of degree Np = 2 len(z) whose slot j (evaluation
+    at zeta'^(5^j), zeta' = exp(i pi / Np)) is scale z_j:  m_k = (2 scale / Np) Re( sum_j z_j zeta'^(-5^j k) ).
+    Computed with numpy's FFT over the odd exponents 5^j = 2t + 1 (mod 2 Np): an independent float path, not the
+    engine's radix-2 transform."""
+    z = np.asarray(z, dtype=np.complex128)
+    slots = len(z)
+    Np = 2 * slots
+    M = 2 * Np
+    t = np.empty(slots, dtype=np.int64)
+    e = 1
+    for j in range(slots):
+        t[j] = (e - 1) // 2
+        e = e * 5 % M
+    w = np.zeros(Np, dtype=np.complex128)
+    w[t] = z
+    F = np.fft.fft(w)  # sum_t w_t exp(-2 pi i t k / Np)
+    k = np.arange(Np)
+    return (2.0 * scale / Np) * (np.exp(-1j * np.pi * k / Np) * F).real
+
+
+MAX_BITS_IN_WORD = 61
+MAX_BIT_VALUE = float((1 << 63) - (1 << 9) - 1)
+
+
+def llround(v: np.ndarray) -> np.ndarray:
+    """C llround: nearest integer, halves away from zero (|v| >= 2^52 is already integral)"""
+    v = np.asarray(v, dtype=np.float64)
+    a = np.abs(v)
+    r = np.where(a >= 2.0**52, a, np.floor(a + 0.5))
+    return (np.sign(v) * r).astype(np.int64)
+
+
+def round_rule(m):
+    """The rounding of encoded coefficients, hpc_gpu_port/periodic_encode.hpp:199-225 (OpenFHE
+    CKKSPackedEncoding::Encode): logc = max ceil(log2 |m_k|) over the nonzero m_k (0 if none); logc < 0 is refused
+    (too small a scaling factor); log_approx = max(logc - 61, 0); coef = llround(m / 2^log_approx), refused above
+    2^63 - 2^9 - 1.  Returns (coef int64 array, log_approx).  The residues of the plaintext are then
+    coef * 2^log_approx mod q (periodic_encode.hpp:228-236)."""
+    m = np.asarray(m, dtype=np.float64)
+    if not np.all(np.isfinite(m)):
+        raise ValueError("non-finite coefficient")
+    nz = m[m != 0.0]
+    logc = int(np.max(np.ceil(np.log2(np.abs(nz))))) if nz.size else 0
+    if logc < 0:
+        raise ValueError("scaling factor too small")
+    log_approx = max(logc - MAX_BITS_IN_WORD, 0)
+    v = m / 2.0**log_approx
+    if np.any(np.abs(v) > MAX_BIT_VALUE):
+        raise ValueError("coefficient overflow")
+    return llround(v), log_approx

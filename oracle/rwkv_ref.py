@@ -3,9 +3,18 @@ tests and bench.py's CPU baseline use it as the checker; the product path never 
 
 It evaluates the model described in fhe-ssm_amd/rwkv_model.py in its natural matrix form (per-head 64 x 64
 states, dense products), independent of the slot layout, diagonals and rotations the encrypted driver
-uses.  The WKV-7 update and readout follow the RWKV-7 recurrence S <- S diag(w) - (S kh)(kh a)^T + v k^T,
-y = S r (the model the reference's served step runs; gpu_real_model.cu:4674-5300 sequences the same
-stages).
+uses.  The three pieces of the RWKV-7 step are separate functions so that each can be checked on its own:
+
+  token_shift   u = (1 - mu) x + mu x_prev (times a gain g): the reference's `x + m * (last_x - x)`
+                (results/vector-d-20261104/raw/rwkv_v7_numpy.py:20 restates RWKV-7's time mixing that way)
+  wkv_update    S <- S diag(w) - (S kh)(kh a)^T + v k^T per head: the reference's
+                `S = S * w.mT - S @ kk * (kk*a).mT + v * k.mT` (rwkv_v7_numpy.py:39)
+  wkv_readout   y = S r per head: `y = S @ r` (rwkv_v7_numpy.py:40)
+
+Here S is [lanes][heads][64][64] with S[i][j] the entry of row i (value index) and column j (key index), as
+the reference's per-head S of shape (HEAD_SIZE, HEAD_SIZE) with v (HEAD_SIZE, 1) times k.mT.  The model
+differs from RWKV-7 where rwkv_model.py says (polynomial nonlinearities, dense maps for the LoRA pairs, no
+L2 normalisation of kh and no GroupNorm of y).  gpu_real_model.cu:4674-5300 sequences the same stages.
 """
 from __future__ import annotations
 
@@ -23,13 +32,34 @@ def init_state(lanes: int, n_layers: int):
             for _ in range(n_layers)]
 
 
+def token_shift(x, x_prev, mu, gain):
+    """gain ((1 - mu) x + mu x_prev), elementwise over channels"""
+    return x * (gain * (1 - mu)) + x_prev * (gain * mu)
+
+
+def heads(z):
+    """[lanes][768] -> [lanes][12][64]"""
+    return z.reshape(z.shape[0], HEADS, HS)
+
+
+def wkv_update(S, w, kh, a, v, k):
+    """S [lanes][heads][64][64]; w, kh, a, v, k [lanes][heads][64] -> the new S:
+    S diag(w) - (S kh)(kh * a)^T + v k^T (each head on its own)"""
+    sa = np.einsum("lhij,lhj->lhi", S, kh)
+    return S * w[:, :, None, :] - sa[:, :, :, None] * (kh * a)[:, :, None, :] + v[:, :, :, None] * k[:, :, None, :]
+
+
+def wkv_readout(S, r):
+    """y = S r per head: [lanes][heads][64]"""
+    return np.einsum("lhij,lhj->lhi", S, r)
+
+
 def layer(x, st, L):
     """one layer for all lanes: x [lanes][768]; st is updated in place; returns the new x"""
     lanes = x.shape[0]
     n = poly(L["p_n1"], np.mean(x * x, axis=1))
     xn = x * n[:, None]
-    u = {m: xn * (L["g1"] * (1 - L["mu_" + m])) + st["xp_t"] * (L["g1"] * L["mu_" + m])
-         for m in ("r", "k", "v", "w", "a", "g")}
+    u = {m: token_shift(xn, st["xp_t"], L["mu_" + m], L["g1"]) for m in ("r", "k", "v", "w", "a", "g")}
     r = u["r"] @ L["W_r"].T
     k = u["k"] @ L["W_k"].T
     v = u["v"] @ L["W_v"].T
@@ -37,18 +67,14 @@ def layer(x, st, L):
     a = poly(L["p_a"], u["a"] @ L["W_a"].T)
     g = poly(L["p_g"], u["g"] @ L["W_g"].T)
     kh = k * L["eta"]
-    hv = lambda z: z.reshape(lanes, HEADS, HS)
-    S = st["S"]
-    sa = np.einsum("lhij,lhj->lhi", S, hv(kh))
-    S = S * hv(w)[:, :, None, :] - sa[:, :, :, None] * hv(kh * a)[:, :, None, :] \
-        + hv(v)[:, :, :, None] * hv(k)[:, :, None, :]
-    y = np.einsum("lhij,lhj->lhi", S, hv(r)).reshape(lanes, D)
+    S = wkv_update(st["S"], heads(w), heads(kh), heads(a), heads(v), heads(k))
+    y = wkv_readout(S, heads(r)).reshape(lanes, D)
     st["S"] = S
     st["xp_t"] = xn
     x = x + (y * g) @ L["W_o"].T
     n2 = poly(L["p_n2"], np.mean(x * x, axis=1))
     xn2 = x * n2[:, None]
-    uc = xn2 * (L["g2"] * (1 - L["mu_c"])) + st["xp_c"] * (L["g2"] * L["mu_c"])
+    uc = token_shift(xn2, st["xp_c"], L["mu_c"], L["g2"])
     h = poly(L["p_h"], uc @ L["W_ck"].T)
     st["xp_c"] = xn2
     return x + h @ L["W_cv"].T

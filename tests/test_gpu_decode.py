@@ -383,7 +383,8 @@ def test_native_decoder_matches_python_plan(engine, DS, M):
 @pytest.mark.timeout(900)
 def test_native_decoder_serves_a_directory(engine, M, tmp_path):
     """the serve-directory protocol with the decode step as its handler (one layer): a stateful session -- two
-    tokens with the reset marker, then one more token, then a reset request -- and a request in another layout;
+    tokens with the reset marker, a two-token request whose second file is bad (it fails after one step; the carried
+    state must be the one from before it), one more token, then a reset request -- and a request in another layout;
     every response file equals the direct steps' output word for word (cold start, carried state, reset)"""
     import os
     import threading
@@ -407,20 +408,30 @@ def test_native_decoder_serves_a_directory(engine, M, tmp_path):
 
     def writer(cts):
         return lambda t, path: be.ctx.ct_save(path, cts[t].ptr(), cts[t].level, cts[t].scale)
+    def half_bad(t, path):
+        # token 0 is good (a whole step runs on it), token 1 is not a ciphertext file: the request fails part way
+        if t == 0:
+            return writer(xs[2:])(0, path)
+        with open(path, "wb") as f:
+            f.write(b"not a ciphertext")
     SC.submit(d, 0, writer(xs[:2]), 2, SC.request_meta(2, 32, top), reset=True)
     r0 = SC.wait(d, 0, timeout=600, alive=th.is_alive)
-    SC.submit(d, 1, writer(xs[2:]), 1, SC.request_meta(1, 32, top))
-    r1 = SC.wait(d, 1, timeout=600, alive=th.is_alive)
-    SC.submit(d, 2, writer(xs[2:]), 1, SC.request_meta(1, 32, top), reset=True)
-    r2 = SC.wait(d, 2, timeout=600, alive=th.is_alive)
-    SC.submit(d, 3, writer(xs[:1]), 1, SC.request_meta(1, 32, top, pack_tokens=2))
+    SC.submit(d, 1, half_bad, 2, SC.request_meta(2, 32, top))
     with pytest.raises(SC.ServeError):
-        SC.wait(d, 3, timeout=600, alive=th.is_alive)
+        SC.wait(d, 1, timeout=600, alive=th.is_alive)
+    # the failed request left the carried state as request 0 did: request 2 continues from there
+    SC.submit(d, 2, writer(xs[2:]), 1, SC.request_meta(1, 32, top))
+    r1 = SC.wait(d, 2, timeout=600, alive=th.is_alive)
+    SC.submit(d, 3, writer(xs[2:]), 1, SC.request_meta(1, 32, top), reset=True)
+    r2 = SC.wait(d, 3, timeout=600, alive=th.is_alive)
+    SC.submit(d, 4, writer(xs[:1]), 1, SC.request_meta(1, 32, top, pack_tokens=2))
+    with pytest.raises(SC.ServeError):
+        SC.wait(d, 4, timeout=600, alive=th.is_alive)
     SC.stop(d)
     th.join(timeout=120)
     log.close()
     assert not th.is_alive()
-    assert box["rep"] == {"served": 4, "failed": 1, "next_req": 4, "exit_reason": "stop"}, box
+    assert box["rep"] == {"served": 5, "failed": 2, "next_req": 5, "exit_reason": "stop"}, box
     # the same tokens as direct steps
     want = []
     nat.reset()

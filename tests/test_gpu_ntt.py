@@ -29,6 +29,15 @@ def octx(oracle, ctx):
     return oracle.Ctx(16, ctx.moduli, L, K, 3)
 
 
+@pytest.fixture
+def ntt_mode(ctx, request):
+    """sets the context's NTT schedule for one test and restores the default (0, two passes, the one bench.py
+    times) afterwards, whatever the test does"""
+    ctx.set_ntt_mode(request.param)
+    yield request.param
+    ctx.set_ntt_mode(0)
+
+
 def rand_polys(moduli, n_polys, prime_idx, seed):
     rng = np.random.default_rng(seed)
     q = np.array([moduli[i] for i in prime_idx], dtype=np.uint64)
@@ -42,11 +51,10 @@ def test_context_matches_oracle_parameters(oracle, ctx, octx):
     assert ctx.roots == octx.psi
 
 
-@pytest.mark.parametrize("mode", [0, 1])
+@pytest.mark.parametrize("ntt_mode", [0, 1], indirect=True)
 @pytest.mark.parametrize("prime_idx", [list(range(24)), list(range(24, 32)), [3, 31, 0, 17, 24]])
-def test_ntt_forward_inverse_bit_exact(ckks, ctx, octx, mode, prime_idx):
-    ctx.set_ntt_mode(mode)
-    x = rand_polys(ctx.moduli, 3, prime_idx, seed=len(prime_idx) + mode)
+def test_ntt_forward_inverse_bit_exact(ckks, ctx, octx, ntt_mode, prime_idx):
+    x = rand_polys(ctx.moduli, 3, prime_idx, seed=len(prime_idx) + ntt_mode)
     buf = ckks.DeviceBuffer.from_array(x)
     ctx.ntt_forward(buf.ptr, 3, prime_idx)
     X = buf.download(x.shape)
@@ -59,28 +67,27 @@ def test_ntt_forward_inverse_bit_exact(ckks, ctx, octx, mode, prime_idx):
     buf.upload(y)
     ctx.ntt_inverse(buf.ptr, 3, prime_idx)
     assert np.array_equal(buf.download(y.shape), octx.ntt_inv(y, prime_idx))
-    ctx.set_ntt_mode(1)
 
 
-def test_ntt_edge_values(ckks, ctx, octx):
+@pytest.mark.parametrize("ntt_mode", [0, 1], indirect=True)
+def test_ntt_edge_values(ckks, ctx, octx, ntt_mode):
     """all-zero, all q-1 and delta limbs (extremes of the lazy-reduction ranges)"""
     pi = [0, 23, 24, 31]
     x = np.zeros((3, 4, 1 << 16), dtype=np.uint64)
     for j, p in enumerate(pi):
         x[1, j, :] = ctx.moduli[p] - 1
         x[2, j, 1] = 1
-    for mode in (0, 1):
-        ctx.set_ntt_mode(mode)
-        buf = ckks.DeviceBuffer.from_array(x)
-        ctx.ntt_forward(buf.ptr, 3, pi)
-        assert np.array_equal(buf.download(x.shape), octx.ntt_fwd(x, pi))
-        ctx.ntt_inverse(buf.ptr, 3, pi)
-        assert np.array_equal(buf.download(x.shape), x)
-    ctx.set_ntt_mode(1)
+    buf = ckks.DeviceBuffer.from_array(x)
+    ctx.ntt_forward(buf.ptr, 3, pi)
+    assert np.array_equal(buf.download(x.shape), octx.ntt_fwd(x, pi))
+    ctx.ntt_inverse(buf.ptr, 3, pi)
+    assert np.array_equal(buf.download(x.shape), x)
 
 
-def test_ntt_config1_full_shape(ckks, ctx, octx):
-    """64 ciphertexts x 2 polys x 24 limbs: sampled limbs vs the oracle, round trip on all limbs."""
+@pytest.mark.parametrize("ntt_mode", [0, 1], indirect=True)
+def test_ntt_config1_full_shape(ckks, ctx, octx, ntt_mode):
+    """64 ciphertexts x 2 polys x 24 limbs (the shape bench.py times, in both schedules): sampled limbs vs the
+    oracle, forward and inverse each on their own, and the round trip on all limbs."""
     n_polys = 128
     prime_idx = list(range(L))
     rng = np.random.default_rng(2024)
@@ -94,3 +101,9 @@ def test_ntt_config1_full_shape(ckks, ctx, octx):
     assert bool((X < q[None, :, None]).all())
     ctx.ntt_inverse(buf.ptr, n_polys, prime_idx)
     assert np.array_equal(buf.download(x.shape), x)
+    # the inverse on its own: random bit-reversed-order input, sampled limbs vs the oracle inverse
+    buf.upload(X[::-1].copy())
+    ctx.ntt_inverse(buf.ptr, n_polys, prime_idx)
+    Y = buf.download(x.shape)
+    for p, l in zip(rng.integers(0, n_polys, 24), rng.permutation(L)):
+        assert np.array_equal(Y[p, l], octx.ntt_inv(X[n_polys - 1 - p, l][None], [l])[0]), (p, l)

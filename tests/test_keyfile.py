@@ -49,7 +49,8 @@ def test_empty_part(tmp_path):
     assert ckks.seeded_part_indices(path) == []
 
 
-@pytest.mark.parametrize("kind", ["magic", "version", "expander", "truncated", "count", "tag"])
+@pytest.mark.parametrize("kind", ["magic", "version", "expander", "truncated", "count", "tag", "count_overflow",
+                                  "digits"])
 def test_header_refusals(tmp_path, kind):
     ckks = load_ckks()
     recs = _small_records(2)
@@ -62,7 +63,13 @@ def test_header_refusals(tmp_path, kind):
         kw["expander"] = 7
     if kind == "count":
         kw["count"] = 3  # one record more than the file holds
-    data = part_bytes(N16, MOD16, 3, 2, 2, 2, "x" * 5000 if kind == "tag" else "t", recs, **kw)
+    if kind == "count_overflow":
+        # the largest count: the size check divides instead of multiplying, so no count can wrap the product
+        kw["count"] = 0xFFFFFFFF
+    num_part_q = 2
+    if kind == "digits":
+        num_part_q = 1 << 20  # more digits than limbs
+    data = part_bytes(N16, MOD16, 3, 2, num_part_q, 2, "x" * 5000 if kind == "tag" else "t", recs, **kw)
     if kind == "truncated":
         data = data[:-8]
     path = _write(tmp_path, "bad.bin", data)
