@@ -59,6 +59,7 @@ SIGNATURES = {
     "ckks_rescale": (_int, [_vp, _vp, _u32, _u32, _vp, _vp]),
     "ckks_eval_mult": (_int, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp]),
     "ckks_eval_mult_rescale": (_int, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp]),
+    "ckks_eval_mult_rescale_noalloc": (_int, [_vp, _vp, _vp, _u32, _u32, _vp, _vp, _vp]),
     "ckks_eval_add": (_int, [_vp, _vp, _vp, _u32, _u32, _vp, _vp]),
     "ckks_rotation_index": (_u32, [ctypes.c_int64]),
     "ckks_automorphism": (_int, [_vp, _vp, _u32, _u32, _u32, _vp, _vp]),
@@ -267,6 +268,9 @@ class Context:
 
     def eval_mult_rescale(self, d_a, d_b, batch, level, d_evk, d_out, stream=None):
         check(load().ckks_eval_mult_rescale(self.h, d_a, d_b, batch, level, d_evk, d_out, stream))
+
+    def eval_mult_rescale_noalloc(self, d_a, d_b, batch, level, d_evk, d_out, stream=None):
+        check(load().ckks_eval_mult_rescale_noalloc(self.h, d_a, d_b, batch, level, d_evk, d_out, stream))
 
     def eval_add(self, d_x, d_y, n_polys, level, d_out, stream=None):
         check(load().ckks_eval_add(self.h, d_x, d_y, n_polys, level, d_out, stream))

@@ -302,6 +302,18 @@ int ckks_eval_mult_rescale(ckks_context* ctx, const uint64_t* d_a, const uint64_
     });
 }
 
+int ckks_eval_mult_rescale_noalloc(ckks_context* ctx, const uint64_t* d_a, const uint64_t* d_b, uint32_t batch,
+                                   uint32_t level, const uint64_t* d_evk, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (level < 2) return fail(CKKS_EINVAL, "rescale needs level >= 2");
+    if (!d_a || !d_b || !d_evk || !d_out) return fail(CKKS_EINVAL, "null buffer");
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::hmult_rescale_noalloc(ctx->c, d_a, d_b, batch, level, d_evk, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
 int ckks_eval_add(ckks_context* ctx, const uint64_t* d_x, const uint64_t* d_y, uint32_t n_polys, uint32_t level,
                   uint64_t* d_out, void* stream) {
     if (int rc = check_ctx_level(ctx, level, false)) return rc;

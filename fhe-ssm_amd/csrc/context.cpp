@@ -139,6 +139,8 @@ void context_init(Context& c, const std::vector<uint64_t>& q, const std::vector<
         c.primes[i] = make_prime_info(m, it[1].w);
     }
     if (hipSetDevice(device) != hipSuccess) throw std::runtime_error("hipSetDevice failed");
+    // the allocation-free entry point's scratch on this device: its address resolved once, with the device current
+    if (scratch_init(device) != hipSuccess) throw std::runtime_error("device scratch address lookup failed");
     auto up = [](void** d, const void* h, size_t bytes) {
         if (hipMalloc(d, bytes) != hipSuccess) throw std::runtime_error("hipMalloc failed");
         if (hipMemcpy(*d, h, bytes, hipMemcpyHostToDevice) != hipSuccess) throw std::runtime_error("hipMemcpy failed");
@@ -181,7 +183,7 @@ void context_init(Context& c, const std::vector<uint64_t>& q, const std::vector<
 }
 
 int prof_begin(const Context& ctx, const char* name, double bytes, hipStream_t st) {
-    if (!ctx.prof_on) return -1;
+    if (!ctx.prof_on || ctx.arena) return -1;  // no events are created inside an allocation-free call
     ProfRec r{name, bytes, nullptr, nullptr};
     if (hipEventCreate(&r.e0) != hipSuccess || hipEventCreate(&r.e1) != hipSuccess) return -1;
     if (hipEventRecord(r.e0, st) != hipSuccess) return -1;

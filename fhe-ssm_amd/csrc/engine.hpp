@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <deque>
 #include <map>
 #include <string>
 #include <vector>
@@ -55,6 +56,22 @@ struct BConvPlan {
                                 // halves ((v >> 30) << 32 | v mod 2^30)
 };
 
+// Device memory lent to one call of the allocation-free entry point: the library's static scratch (scratch.hip).
+// Workspace slots and the call's own device tables (NTT job lists, BConv constants not yet in the context's caches)
+// are carved from it in request order; the tables are written into it by a kernel from its arguments (arena_put),
+// on the call's stream.  Nothing is allocated on the device.
+constexpr size_t kScratchBytes = (size_t)160 << 20;    // the scratch's size on each GPU
+constexpr size_t kScratchTableBytes = (size_t)1 << 20;  // the part kept for the call's tables
+constexpr uint32_t kArenaSlots = 32;
+
+struct Arena {
+    uint8_t* base = nullptr;
+    size_t cap = 0, used = 0;
+    hipStream_t st = nullptr;
+    size_t slot_off[kArenaSlots] = {}, slot_bytes[kArenaSlots] = {};
+    std::deque<BConvPlan> plans;  // the call's BConv plans whose tables live in the arena
+};
+
 // One profiled launch: HIP events recorded on the launch stream around the kernel, plus the
 // algorithmic bytes that launch must move (inputs read once, outputs written once, shared tables once).
 struct ProfRec {
@@ -105,12 +122,22 @@ struct Context {
     // ModDown rounding: false = approximate P -> Q conversion (OpenFHE ApproxModDown, floor(x/P) - u with
     // u in [0, K)); true = exact round(x / P) (centered conversion)
     bool moddown_exact = false;
+    // set only for the duration of an allocation-free call (workspace and new tables then come from it)
+    Arena* arena = nullptr;
+    // host copies of the BConv tables built during allocation-free calls (computed once, uploaded per call)
+    std::map<std::string, std::vector<uint64_t>> bconv_host;
 };
 
 // Profiling helpers: no-ops unless ctx.prof_on.
 int prof_begin(const Context& ctx, const char* name, double bytes, hipStream_t st);
 void prof_end(const Context& ctx, int idx, hipStream_t st);
 void prof_clear(const Context& ctx);
+
+// the scratch of the allocation-free entry point: its device address resolved once per device (with that device
+// current), then looked up; arena_put writes host words into device memory by a kernel, without staging
+hipError_t scratch_init(int device);
+uint8_t* scratch_ptr(int device);
+hipError_t arena_put(void* dst, const void* src, size_t bytes, hipStream_t st);
 
 hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,
                       NttMode mode, hipStream_t st);

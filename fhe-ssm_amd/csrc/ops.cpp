@@ -23,6 +23,7 @@ namespace fhe {
 
 uint64_t mulmod_h(uint64_t a, uint64_t b, uint64_t q);
 uint64_t invmod_h(uint64_t a, uint64_t q);
+uint8_t* arena_take(Arena& a, size_t bytes);
 
 hipError_t launch_tensor(const Context& ctx, const uint64_t* a, const uint64_t* b, uint64_t* d01, uint64_t* d2,
                          uint32_t B, uint32_t l, uint64_t* d2e, uint64_t d2e_bstride, const uint32_t* ext_off,
@@ -118,6 +119,18 @@ JobSpec regular_jobs(uint32_t n_polys, const std::vector<uint32_t>& pmap) {
 // explicit job list, stored once per key; ordered prime-major (jobs sharing a twiddle table adjacent)
 JobSpec cached_jobs(Context& ctx, const std::string& key, std::vector<Job> jobs) {
     auto it = ctx.job_cache.find(key);
+    if (it == ctx.job_cache.end() && ctx.arena) {
+        // allocation-free call: the list goes into the arena for this call only
+        std::stable_sort(jobs.begin(), jobs.end(), [](const Job& a, const Job& b) { return a.prime < b.prime; });
+        uint32_t distinct = 0;
+        for (size_t i = 0; i < jobs.size(); i++) distinct += (i == 0 || jobs[i].prime != jobs[i - 1].prime) ? 1 : 0;
+        Job* d = (Job*)arena_take(*ctx.arena, std::max<size_t>(1, jobs.size()) * sizeof(Job));
+        HIPX(arena_put(d, jobs.data(), jobs.size() * sizeof(Job), ctx.arena->st));
+        JobSpec js{};
+        js.jobs = d;
+        js.n_primes = distinct;
+        return js;
+    }
     if (it == ctx.job_cache.end()) {
         std::stable_sort(jobs.begin(), jobs.end(), [](const Job& a, const Job& b) { return a.prime < b.prime; });
         uint32_t distinct = 0;
@@ -136,7 +149,27 @@ JobSpec cached_jobs(Context& ctx, const std::string& key, std::vector<Job> jobs)
 }  // namespace
 
 // ------------------------------------------------------------------ workspace
+// bump allocation from the arena of an allocation-free call (256-byte aligned); refuses what does not fit
+uint8_t* arena_take(Arena& a, size_t bytes) {
+    const size_t off = (a.used + 255) & ~(size_t)255;
+    if (off > a.cap || bytes > a.cap - off)
+        throw std::invalid_argument("the call needs more device scratch than the allocation-free entry point's " +
+                                    std::to_string(a.cap >> 20) + " MiB");
+    a.used = off + bytes;
+    return a.base + off;
+}
+
 void* ws_get(Context& ctx, uint32_t slot, size_t bytes) {
+    if (ctx.arena) {
+        Arena& a = *ctx.arena;
+        if (slot >= kArenaSlots) throw std::logic_error("workspace slot out of range");
+        // a slot asked for again with more bytes gets a new region (as a regrown workspace buffer would)
+        if (a.slot_bytes[slot] < bytes) {
+            a.slot_off[slot] = (size_t)(arena_take(a, bytes) - a.base);
+            a.slot_bytes[slot] = bytes;
+        }
+        return a.base + a.slot_off[slot];
+    }
     if (ctx.scratch.size() <= slot) ctx.scratch.resize(slot + 1, {nullptr, 0});
     auto& s = ctx.scratch[slot];
     if (s.second < bytes) {
@@ -186,6 +219,21 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
     auto it = ctx.bconv_cache.find(key);
     if (it != ctx.bconv_cache.end()) return it->second;
     BConvPlan p;
+    if (ctx.arena) {
+        // allocation-free call: the table (host copy computed once per context) goes into the arena
+        auto ht = ctx.bconv_host.find(key);
+        if (ht != ctx.bconv_host.end()) {
+            p.n_in = (uint32_t)in_idx.size();
+            p.n_out = (uint32_t)out_idx.size();
+            p.in_idx = in_idx;
+            p.out_idx = out_idx;
+            p.centered = centered;
+            p.d_tab = (uint64_t*)arena_take(*ctx.arena, ht->second.size() * 8);
+            HIPX(arena_put(p.d_tab, ht->second.data(), ht->second.size() * 8, ctx.arena->st));
+            ctx.arena->plans.push_back(std::move(p));
+            return ctx.arena->plans.back();
+        }
+    }
     p.n_in = (uint32_t)in_idx.size();
     p.n_out = (uint32_t)out_idx.size();
     p.in_idx = in_idx;
@@ -222,6 +270,13 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
             for (uint32_t k = 0; k < p.n_in; k++) m = mulmod_h(m, ctx.moduli[in_idx[k]] % pj, pj);
             cfix[2 * p.n_in + j] = col_scale.empty() ? m : mulmod_h(m, col_scale[j], pj);
         }
+    }
+    if (ctx.arena) {
+        p.d_tab = (uint64_t*)arena_take(*ctx.arena, tab.size() * 8);
+        HIPX(arena_put(p.d_tab, tab.data(), tab.size() * 8, ctx.arena->st));
+        ctx.bconv_host.emplace(key, std::move(tab));
+        ctx.arena->plans.push_back(std::move(p));
+        return ctx.arena->plans.back();
     }
     HIPX(hipMalloc(&p.d_tab, tab.size() * 8));
     HIPX(hipMemcpy(p.d_tab, tab.data(), tab.size() * 8, hipMemcpyHostToDevice));
@@ -521,6 +576,40 @@ void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint3
     for (uint32_t t = 0; t < l; t++) ext_off[t] = (t / ctx.alpha) * E + t;
     HIPX(launch_tensor(ctx, a, b, d01, x2c, B, l, ext, (uint64_t)D * E * W, ext_off.data(), st));
     relin_tail(ctx, d01, x2c, ext, B, l, evk, out, do_rescale, st);
+}
+
+// Device workspace of hmult with the rescale (bytes): d01 2Bl, d2 Bl, extension B D E, inner product 2B E,
+// the addend's dropped limb 2B and the rescale's T 2B (l-1) limbs
+size_t hmult_rescale_scratch_bytes(const Context& ctx, uint32_t B, uint32_t l) {
+    const size_t D = num_digits(ctx, l), E = l + ctx.K;
+    const size_t limbs = (size_t)B * (2 * l + l + D * E + 2 * E + 2 + 2 * (l - 1));
+    return limbs * W * 8;
+}
+
+// hmult + rescale with every workspace buffer and per-call table in the device scratch: no device allocation.
+// Same kernels, launches and words as hmult(..., true, ...).
+void hmult_rescale_noalloc(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l,
+                           const uint64_t* evk, uint64_t* out, hipStream_t st) {
+    check_level(ctx, l);
+    if (l < 2) throw std::invalid_argument("rescale needs l >= 2");
+    uint8_t* base = scratch_ptr(ctx.device);
+    if (!base) throw std::runtime_error("device scratch not initialised for this context's device");
+    const size_t need = hmult_rescale_scratch_bytes(ctx, B, l);
+    if (need > kScratchBytes - kScratchTableBytes)
+        throw std::invalid_argument("batch " + std::to_string(B) + " at level " + std::to_string(l) + " needs " +
+                                    std::to_string(need >> 20) + " MiB of workspace; the allocation-free entry "
+                                    "point has " + std::to_string((kScratchBytes - kScratchTableBytes) >> 20) +
+                                    " MiB (use ckks_eval_mult_rescale, or a smaller batch)");
+    Arena ar;
+    ar.base = base;
+    ar.cap = kScratchBytes;
+    ar.st = st;
+    struct Reset {
+        Context& c;
+        ~Reset() { c.arena = nullptr; }
+    } reset{ctx};
+    ctx.arena = &ar;
+    hmult(ctx, a, b, B, l, evk, out, true, st);
 }
 
 // out[c] = relin( sum_j a[c][j] (x) b[c][j] ) (+ rescale): one key switch per batch item for np products.

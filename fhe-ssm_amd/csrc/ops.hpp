@@ -55,6 +55,11 @@ void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const ui
 void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uint64_t* out, hipStream_t st);
 void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l, const uint64_t* evk,
            uint64_t* out, bool do_rescale, hipStream_t st);
+// hmult with the rescale, workspace and tables in the device scratch (no allocation); refuses shapes whose
+// workspace exceeds it
+size_t hmult_rescale_scratch_bytes(const Context& ctx, uint32_t B, uint32_t l);
+void hmult_rescale_noalloc(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l,
+                           const uint64_t* evk, uint64_t* out, hipStream_t st);
 void rotate(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, uint32_t g, const uint64_t* evk, uint64_t* out,
             hipStream_t st);
 void add(Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys, uint32_t l,

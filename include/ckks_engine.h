@@ -128,6 +128,16 @@ int ckks_eval_mult_rescale(ckks_context* ctx, const uint64_t* d_a, const uint64_
                            uint32_t level, const uint64_t* d_evk, uint64_t* d_out, void* stream);
 int ckks_eval_add(ckks_context* ctx, const uint64_t* d_x, const uint64_t* d_y, uint32_t n_polys, uint32_t level,
                   uint64_t* d_out, void* stream);
+
+/* ckks_eval_mult_rescale_noalloc: ckks_eval_mult_rescale (same arguments, kernels and output words) that allocates
+ * no device memory.  It has no counterpart in the reference: it is for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Its workspace and per-call tables
+ * live in a static device array of 160 MiB per GPU that the library holds until the process ends; a call whose
+ * workspace, B * (3l + D(l+K) + 2(l+K) + 2(l-1) + 2) limbs of 512 KiB (D = ceil(l / alpha)), exceeds 159 MiB is
+ * refused with CKKS_EINVAL (config 2's shape, L=24 K=8 dnum=3, takes one pair per call).  Every call on one GPU
+ * shares that array: calls that overlap on one GPU (other streams, other host threads) race. */
+int ckks_eval_mult_rescale_noalloc(ckks_context* ctx, const uint64_t* d_a, const uint64_t* d_b, uint32_t batch,
+                                   uint32_t level, const uint64_t* d_evk, uint64_t* d_out, void* stream);
 uint32_t ckks_rotation_index(int64_t step);
 int ckks_automorphism(ckks_context* ctx, const uint64_t* d_in, uint32_t n_polys, uint32_t level, uint32_t g,
                       uint64_t* d_out, void* stream);
