@@ -100,6 +100,9 @@ PrimeInfo make_prime_info(uint64_t q, uint64_t itab1) {
     const u128 mu = ~(u128)0 / q;
     p.mu_hi = (uint64_t)(mu >> 64);
     p.mu_lo = (uint64_t)mu;
+    const uint32_t bits = 64 - (uint32_t)__builtin_clzll(q);
+    p.red_shift = bits > 25 ? bits - 25 : 0;
+    p.red_mul = (uint32_t)(((u128)1 << (32 + p.red_shift)) / q);
     return p;
 }
 

@@ -24,6 +24,9 @@ struct PrimeInfo {
     uint64_t ninv, ninv_p;      // N^-1 mod q and Shoup companion
     uint64_t w1ninv, w1ninv_p;  // inverse-table entry 1 (psi^-N/2) times N^-1: the last inverse stage
     uint64_t mu_hi, mu_lo;      // floor(2^128 / q)
+    // quotient estimate of a value v < 128 q: hi32(floor(v / 2^red_shift) * red_mul) is floor(v / q) or one less,
+    // with red_shift = max(0, bits(q) - 25), red_mul = floor(2^(32 + red_shift) / q)
+    uint32_t red_shift, red_mul;
 };
 
 // One limb to transform: offset (in units of N words) from the base pointer, and its prime index.

@@ -15,7 +15,9 @@
 //           contiguous 256-word block.  A tile = 16 blocks.
 // Inside a tile each of 256 threads holds 16 words in registers and performs 4 stages (a radix-16
 // step) between two LDS exchanges.  Values stay lazily reduced (Harvey): [0, 8q) forward, [0, 4q)
-// inverse, with the twiddle product from shoup_lazy4; N^-1 is folded into the last inverse stage.
+// inverse, with the twiddle product from shoup_lazy4; N^-1 is folded into the last inverse stage.  Forward
+// transforms of primes below 2^56 skip the per-butterfly reduction altogether (fwd_bfly<true>: the bound grows by
+// 4q a stage, to < 72q) and reduce once at the end with a quotient estimate (reduce_open).
 //
 // Launch layout: a "job" is one limb (offset in units of N words + prime index).  Jobs are
 // enumerated prime-major so that concurrently running workgroups share one prime's twiddle table
@@ -65,6 +67,32 @@ __device__ __forceinline__ void ct_bfly(uint64_t& X, uint64_t& Y, const TwPair& 
     Y = x + q4 - t;
 }
 
+// Forward butterfly for primes below 2^56, X left unreduced: the twiddle product is in [0, 4q) whatever Y is, so
+// every stage adds at most 4q to the bound (inputs below 8q leave the 16 stages below 72q < 2^63) and the values
+// are brought to [0, q) once, at the end (reduce_open).  Saves the four instructions of the conditional subtract.
+constexpr uint64_t kOpenMaxQ = 1ull << 56;
+
+template <bool kOpen>
+__device__ __forceinline__ void fwd_bfly(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q4, uint64_t nq) {
+    if (kOpen) {
+        const uint64_t x = X;
+        const uint64_t t = shoup_lazy4(Y, w.w, w.wp, nq);
+        X = x + t;
+        Y = x + q4 - t;
+    } else {
+        ct_bfly(X, Y, w, q4, nq);
+    }
+}
+
+// v < 128 q -> [0, q): k = hi32(floor(v / 2^s) M), M = floor(2^(32+s) / q), is floor(v/q) or one less (the
+// truncations lose less than 2^-24 + v / 2^(32+s) < 0.6), so v - k q lies in [0, 2q); one conditional subtract.
+__device__ __forceinline__ uint64_t reduce_open(uint64_t v, uint64_t q, uint64_t nq, uint32_t s, uint32_t M) {
+    const uint32_t k = __umulhi((uint32_t)(v >> s), M);
+    uint64_t r = (uint64_t)k * (uint32_t)nq + v;               // v + k nq (mod 2^64), nq = 2^64 - q
+    r += (uint64_t)(k * (uint32_t)(nq >> 32)) << 32;
+    return csub_s(r, q);
+}
+
 // Inverse (Gentleman-Sande) butterfly, values kept in [0, 4q).
 __device__ __forceinline__ void gs_bfly(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q4, uint64_t nq) {
     const uint64_t s = csub_s(X + Y, q4);
@@ -82,6 +110,7 @@ __device__ __forceinline__ uint64_t canon8(uint64_t v, uint64_t q) {
 
 // ---------------------------------------------------------------- forward pass A (strided columns)
 // tile: columns [16*tile, 16*tile + 16).  g: thread id within the 256-thread group.
+template <bool kOpen>
 __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
                                            int tile, int g, uint64_t* lds) {
     const uint64_t q4 = q << 2, nq = 0 - q;
@@ -97,7 +126,7 @@ __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            ct_bfly(x[k], x[k + h], tw[(1 << s) + (k >> (4 - s))], q4, nq);
+            fwd_bfly<kOpen>(x[k], x[k + h], tw[(1 << s) + (k >> (4 - s))], q4, nq);
         }
     }
 #pragma unroll
@@ -112,7 +141,7 @@ __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            ct_bfly(x[k], x[k + h], tw[(1 << s) + ((16 * rg + k) >> (8 - s))], q4, nq);
+            fwd_bfly<kOpen>(x[k], x[k + h], tw[(1 << s) + ((16 * rg + k) >> (8 - s))], q4, nq);
         }
     }
 #pragma unroll
@@ -120,8 +149,10 @@ __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPai
 }
 
 // ---------------------------------------------------------------- forward pass B (256-word blocks)
-__device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
+template <bool kOpen>
+__device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, const PrimeInfo& P,
                                            int tile, int g, uint64_t* lds) {
+    const uint64_t q = P.q;
     const uint64_t q4 = q << 2, nq = 0 - q;
     const int bl = g >> 4, rl = g & 15;
     const int b = tile * 16 + bl;  // block index within the limb
@@ -146,7 +177,7 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            ct_bfly(x[k], x[k + h], tw03[base + (k >> (4 - s))], q4, nq);
+            fwd_bfly<kOpen>(x[k], x[k + h], tw03[base + (k >> (4 - s))], q4, nq);
         }
     }
     // stages 8+s, s = 4..7: r = 16 rl + k; twiddle 2^(8+s) + b 2^s + (r >> (8-s)) = ... + rl 2^(s-4) + (k >> (8-s)).
@@ -176,13 +207,13 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
             const int i = k >> (8 - s);
-            ct_bfly(x[k], x[k + h], s < 7 ? tw4[base + i] : tw7[i], q4, nq);
+            fwd_bfly<kOpen>(x[k], x[k + h], s < 7 ? tw4[base + i] : tw7[i], q4, nq);
         }
     }
     // canonical [0, q), then transpose through LDS for coalesced stores (direct 16-byte stores of each
     // thread's contiguous run measured slower)
 #pragma unroll
-    for (int k = 0; k < 16; k++) x[k] = canon8(x[k], q);
+    for (int k = 0; k < 16; k++) x[k] = kOpen ? reduce_open(x[k], q, nq, P.red_shift, P.red_mul) : canon8(x[k], q);
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) L[17 * rl + k] = x[k];
@@ -319,7 +350,11 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_fwd_a(uint64_t* data, JobS
     __shared__ uint64_t lds[kLdsWords];
     uint32_t off, prime;
     job_of(js, blockIdx.y, off, prime);
-    fwd_a_tile(data + (size_t)off * kN, tw_all + (size_t)prime * kN, primes[prime].q, blockIdx.x, threadIdx.x, lds);
+    const uint64_t q = primes[prime].q;
+    if (q < kOpenMaxQ)
+        fwd_a_tile<true>(data + (size_t)off * kN, tw_all + (size_t)prime * kN, q, blockIdx.x, threadIdx.x, lds);
+    else
+        fwd_a_tile<false>(data + (size_t)off * kN, tw_all + (size_t)prime * kN, q, blockIdx.x, threadIdx.x, lds);
 }
 
 __global__ __launch_bounds__(kTileThreads) void k_ntt_fwd_b(uint64_t* data, JobSpec js, const TwPair* tw_all,
@@ -327,7 +362,11 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_fwd_b(uint64_t* data, JobS
     __shared__ uint64_t lds[kLdsWords];
     uint32_t off, prime;
     job_of(js, blockIdx.y, off, prime);
-    fwd_b_tile(data + (size_t)off * kN, tw_all + (size_t)prime * kN, primes[prime].q, blockIdx.x, threadIdx.x, lds);
+    const PrimeInfo& P = primes[prime];
+    if (P.q < kOpenMaxQ)
+        fwd_b_tile<true>(data + (size_t)off * kN, tw_all + (size_t)prime * kN, P, blockIdx.x, threadIdx.x, lds);
+    else
+        fwd_b_tile<false>(data + (size_t)off * kN, tw_all + (size_t)prime * kN, P, blockIdx.x, threadIdx.x, lds);
 }
 
 __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_b(uint64_t* data, JobSpec js, const TwPair* tw_all,
@@ -365,11 +404,11 @@ __global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_fwd_fused(ui
     const int grp = threadIdx.x >> 8, g = threadIdx.x & 255;
     uint64_t* L = lds + grp * kLdsWords;
     for (int t = grp; t < 16; t += kFusedGroups) {
-        fwd_a_tile(a, tw, q, t, g, L);
+        fwd_a_tile<false>(a, tw, q, t, g, L);
         __syncthreads();
     }
     for (int t = grp; t < 16; t += kFusedGroups) {
-        fwd_b_tile(a, twb_all + (size_t)prime * kN, q, t, g, L);
+        fwd_b_tile<false>(a, twb_all + (size_t)prime * kN, primes[prime], t, g, L);
         __syncthreads();
     }
 }

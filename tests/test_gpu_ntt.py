@@ -107,3 +107,29 @@ def test_ntt_config1_full_shape(ckks, ctx, octx, ntt_mode):
     Y = buf.download(x.shape)
     for p, l in zip(rng.integers(0, n_polys, 24), rng.permutation(L)):
         assert np.array_equal(Y[p, l], octx.ntt_inv(X[n_polys - 1 - p, l][None], [l])[0]), (p, l)
+
+
+def test_ntt_prime_sizes(ckks, oracle):
+    """every prime size the engine meets (20..60 bits): below 2^56 the forward transform takes the unreduced
+    butterflies and the final quotient-estimate reduction, from 2^56 the reduced ones; random and edge limbs
+    (all q-1, a delta) vs the oracle, and the round trip"""
+    moduli = []
+    for bits in (20, 30, 40, 50, 54, 55):
+        moduli += ckks.gen_primes(bits, 1, moduli)
+    p_mod = []
+    for bits in (56, 57, 60):
+        p_mod += ckks.gen_primes(bits, 1, moduli + p_mod)
+    ctx = ckks.Context(num_q=len(moduli), num_p=len(p_mod), dnum=2, moduli=moduli + p_mod)
+    allm = moduli + p_mod
+    octx = oracle.Ctx(16, allm, len(moduli), len(p_mod), 2)
+    pi = list(range(len(allm)))
+    x = rand_polys(allm, 3, pi, seed=31)
+    for j, p in enumerate(pi):
+        x[1, j, :] = allm[p] - 1
+        x[2, j, :] = 0
+        x[2, j, 1] = 1
+    buf = ckks.DeviceBuffer.from_array(x)
+    ctx.ntt_forward(buf.ptr, 3, pi)
+    assert np.array_equal(buf.download(x.shape), octx.ntt_fwd(x, pi))
+    ctx.ntt_inverse(buf.ptr, 3, pi)
+    assert np.array_equal(buf.download(x.shape), x)
