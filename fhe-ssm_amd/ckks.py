@@ -107,6 +107,8 @@ SIGNATURES = {
     "ckks_ct_load": (_int, [_vp, ctypes.c_char_p, _u32, _vp, ctypes.POINTER(_u32), ctypes.POINTER(ctypes.c_double)]),
     "ckks_encode": (_int, [_vp, _vp, _vp, _u32, _u32, ctypes.c_double, _vp]),
     "ckks_encrypt": (_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp]),
+    "ckks_keygen_public": (_int, [_vp, _vp, _vp, _vp, _vp]),
+    "ckks_encrypt_public": (_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp]),
     "ckks_decrypt_decode": (_int, [_vp, _vp, _vp, _u32, ctypes.c_double, _vp, _vp, _u32]),
     "ckks_context_counters": (_int, [_vp, _vp, _int]),
     "ckks_set_moddown_exact": (_int, [_vp, _int]),
@@ -419,6 +421,13 @@ class Context:
 
     def encrypt(self, sk, d_pt, level: int, seed: bytes, index: int, d_ct) -> None:
         check(load().ckks_encrypt(self.h, sk.h, d_pt, level, _seed(seed), index, d_ct))
+
+    def keygen_public(self, sk, seed: bytes, eseed: bytes, d_pk) -> None:
+        """public key [2][L+K][N] over Q*P: b = e - a s"""
+        check(load().ckks_keygen_public(self.h, sk.h, _seed(seed), _seed(eseed), d_pk))
+
+    def encrypt_public(self, d_pk, d_pt, level: int, seed: bytes, index: int, d_ct) -> None:
+        check(load().ckks_encrypt_public(self.h, d_pk, d_pt, level, _seed(seed), index, d_ct))
 
     def decrypt(self, sk, d_ct, level: int, scale: float, n_slots: int = 1 << 15, complex_out: bool = False):
         re = np.zeros(n_slots, dtype=np.float64)

@@ -604,6 +604,27 @@ int ckks_encrypt(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_pt,
     });
 }
 
+int ckks_keygen_public(ckks_context* ctx, const ckks_secret* sk, const uint8_t* seed32, const uint8_t* eseed32,
+                       uint64_t* d_pk) {
+    if (int rc = check_secret(ctx, sk)) return rc;
+    if (!seed32 || !eseed32 || !d_pk) return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        fhe::keygen_public(ctx->c, *sk->s, seed32, eseed32, 3.19, d_pk);
+        return CKKS_OK;
+    });
+}
+
+int ckks_encrypt_public(ckks_context* ctx, const uint64_t* d_pk, const uint64_t* d_pt, uint32_t level,
+                        const uint8_t* seed32, uint32_t index, uint64_t* d_ct) {
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_pk || !d_pt || !seed32 || !d_ct) return fail(CKKS_EINVAL, "null argument");
+    if (ctx->c.K == 0) return fail(CKKS_EINVAL, "public-key encryption needs special primes (the key is over Q*P)");
+    return guarded([&] {
+        fhe::encrypt_public(ctx->c, d_pk, d_pt, level, seed32, index, d_ct);
+        return CKKS_OK;
+    });
+}
+
 int ckks_decrypt_decode(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_ct, uint32_t level, double scale,
                         double* re, double* im, uint32_t n_slots) {
     if (int rc = check_secret(ctx, sk)) return rc;

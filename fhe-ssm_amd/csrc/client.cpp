@@ -39,6 +39,8 @@ hipError_t launch_encode_small(const Context& ctx, const int64_t* coef, const in
                                uint32_t n_vec, uint32_t Np, uint32_t l, const TwPair* tab, hipStream_t st);
 hipError_t launch_mul(const Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t l,
                       hipStream_t st);
+hipError_t launch_pk_mac(const Context& ctx, const uint64_t* pk, const uint64_t* v, const uint64_t* e, uint64_t* x,
+                         const std::vector<uint32_t>& pmap, hipStream_t st);
 
 namespace {
 
@@ -53,6 +55,8 @@ constexpr uint32_t kTagKey = 0x59454b53u;   // "SKEY" (seeded_keys.hpp:32)
 constexpr uint32_t kTagSecret = 0x52434553u;  // "SECR"
 constexpr uint32_t kTagGauss = 0x53554147u;   // "GAUS"
 constexpr uint32_t kTagCtA = 0x41585443u;     // "CTXA"
+constexpr uint32_t kTagPkA = 0x59454b50u;     // "PKEY"
+constexpr uint32_t kTagEncV = 0x56434e45u;    // "ENCV"
 
 // ---------------------------------------------------------------- ChaCha20 (RFC 8439)
 inline uint32_t rotl(uint32_t v, int c) { return (v << c) | (v >> (32 - c)); }
@@ -457,6 +461,47 @@ void encrypt(Context& ctx, const Secret& sk, const uint64_t* d_pt, uint32_t l, c
     gauss(seed, index, 1, 3.19, e.data());
     coeffs_to_eval(ctx, e.data(), 1, iota(l), de.as<uint64_t>(), nullptr);
     HIPC(launch_encrypt(ctx, d_pt, de.as<uint64_t>(), da.as<uint64_t>(), sk.d_eval, d_ct, l, nullptr));
+    HIPC(hipDeviceSynchronize());
+}
+
+// Public key over Q*P (PKEBase::KeyGenInternal, harness/boot_overflow_probe.cpp:22,139): b = e - a s, a uniform
+// (ChaCha20 "PKEY" stream, nonce {0, limb}), e rounded Gaussian (stream {0, 0} of eseed): the secret-key
+// encryption of zero over all L+K limbs.  d_pk [2][L+K][N].
+void keygen_public(Context& ctx, const Secret& sk, const uint8_t seed[32], const uint8_t eseed[32], double sigma,
+                   uint64_t* d_pk) {
+    const uint32_t T = ctx.L + ctx.K;
+    DevBuf da((size_t)T * kN * 8), de((size_t)T * kN * 8), dz((size_t)T * kN * 8);
+    std::vector<uint64_t> a((size_t)T * kN);
+    parallel_for(T, [&](uint32_t i) { fill_uniform(seed, 0, i, kTagPkA, ctx.moduli[i], a.data() + (size_t)i * kN, kN); });
+    HIPC(hipMemcpy(da.p, a.data(), a.size() * 8, hipMemcpyHostToDevice));
+    std::vector<int64_t> e(kN);
+    gauss(eseed, 0, 0, sigma, e.data());
+    coeffs_to_eval(ctx, e.data(), 1, iota(T), de.as<uint64_t>(), nullptr);
+    HIPC(hipMemset(dz.p, 0, (size_t)T * kN * 8));
+    HIPC(launch_encrypt(ctx, de.as<uint64_t>(), dz.as<uint64_t>(), da.as<uint64_t>(), sk.d_eval, d_pk, T, nullptr));
+    HIPC(hipDeviceSynchronize());
+}
+
+// Public-key encryption at level l (PKEBase::EncryptZeroCore with the key over Q*P, then ApproxModDown to Q_l):
+// x = (b v + e0, a v + e1) over Q_l * P with v uniform ternary ("ENCV" stream {index, 0}, words mod 3: 0, 1, 2 ->
+// 0, 1, -1) and e0, e1 rounded Gaussians (streams {index, 2}, {index, 3}); ct = (ModDown(x0) + m, ModDown(x1)).
+void encrypt_public(Context& ctx, const uint64_t* d_pk, const uint64_t* d_pt, uint32_t l, const uint8_t seed[32],
+                    uint32_t index, uint64_t* d_ct) {
+    const uint32_t E = l + ctx.K;
+    if (ctx.K == 0) throw std::invalid_argument("public-key encryption needs special primes (the key is over Q*P)");
+    std::vector<uint32_t> pm(E);
+    for (uint32_t t = 0; t < E; t++) pm[t] = t < l ? t : ctx.L + (t - l);
+    std::vector<int64_t> c(3 * (size_t)kN);
+    std::vector<uint64_t> u(kN);
+    fill_uniform(seed, index, 0, kTagEncV, 3, u.data(), kN);
+    for (uint32_t k = 0; k < kN; k++) c[k] = u[k] == 2 ? -1 : (int64_t)u[k];
+    gauss(seed, index, 2, 3.19, c.data() + kN);
+    gauss(seed, index, 3, 3.19, c.data() + 2 * (size_t)kN);
+    DevBuf dv((size_t)3 * E * kN * 8), dx((size_t)2 * E * kN * 8);
+    coeffs_to_eval(ctx, c.data(), 3, pm, dv.as<uint64_t>(), nullptr);  // [3][E][N]: v, e0, e1
+    uint64_t* v = dv.as<uint64_t>();
+    HIPC(launch_pk_mac(ctx, d_pk, v, v + (size_t)E * kN, dx.as<uint64_t>(), pm, nullptr));
+    moddown_inplace(ctx, dx.as<uint64_t>(), 2, l, d_pt, d_ct, nullptr, 2);
     HIPC(hipDeviceSynchronize());
 }
 

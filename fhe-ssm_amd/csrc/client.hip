@@ -2,6 +2,8 @@
 // small signed polynomials to RNS limbs, the key-switching-key formula, secret-key encryption and
 // the decryption inner product.  Not on the evaluation hot path; used to produce seeded keys and
 // ciphertexts on the device and to read results back.
+#include <vector>
+
 #include "engine.hpp"
 #include "modarith.hpp"
 
@@ -83,6 +85,19 @@ __global__ __launch_bounds__(256) void k_encrypt(const uint64_t* __restrict__ m,
     const uint64_t as = mul_mod(a[o], s[o], br);
     ct[o] = sub_mod(add_mod(m[o], e[o], br.q), as, br.q);
     ct[(size_t)l * kN + o] = a[o];
+}
+
+// public-key encryption before its ModDown: x[p][t] = pk[p][prime t] * v[t] + e[p][t] over the E limbs of Q_l * P
+// (limb t uses prime pmap[t]; pk [2][L+K][N], v [E][N], e [2][E][N], x [2][E][N])
+__global__ __launch_bounds__(256) void k_pk_mac(const uint64_t* __restrict__ pk, const uint64_t* __restrict__ v,
+                                                const uint64_t* __restrict__ e, uint64_t* __restrict__ x, PmapArgs pa,
+                                                uint32_t T, const PrimeInfo* __restrict__ primes) {
+    const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t t = blockIdx.y, p = blockIdx.z;
+    const uint32_t pi = pa.pmap[t];
+    const Barrett br = barrett_c(primes[pi]);
+    const size_t o = (size_t)t * kN + k, oe = ((size_t)p * pa.n_limbs + t) * kN + k;
+    x[oe] = add_mod(mul_mod(pk[((size_t)p * T + pi) * kN + k], v[o], br), e[oe], br.q);
 }
 
 // decryption inner product: out = c0 + c1 * s over l limbs
@@ -180,6 +195,17 @@ hipError_t launch_ksk_b(const Context& ctx, const uint64_t* a, const uint64_t* s
 hipError_t launch_encrypt(const Context& ctx, const uint64_t* m, const uint64_t* e, const uint64_t* a,
                           const uint64_t* s, uint64_t* ct, uint32_t l, hipStream_t st) {
     hipLaunchKernelGGL(k_encrypt, dim3(kN / 256, l), dim3(256), 0, st, m, e, a, s, ct, l, ctx.d_primes);
+    return hipGetLastError();
+}
+
+hipError_t launch_pk_mac(const Context& ctx, const uint64_t* pk, const uint64_t* v, const uint64_t* e, uint64_t* x,
+                         const std::vector<uint32_t>& pmap, hipStream_t st) {
+    if (pmap.empty() || pmap.size() > kMaxPmap) return hipErrorInvalidValue;
+    PmapArgs pa{};
+    pa.n_limbs = (uint32_t)pmap.size();
+    for (size_t i = 0; i < pmap.size(); i++) pa.pmap[i] = (uint8_t)pmap[i];
+    hipLaunchKernelGGL(k_pk_mac, dim3(kN / 256, pa.n_limbs, 2), dim3(256), 0, st, pk, v, e, x, pa, ctx.L + ctx.K,
+                       ctx.d_primes);
     return hipGetLastError();
 }
 

@@ -33,6 +33,10 @@ void encode_periodic(Context& ctx, const double* re, const double* im, uint32_t 
                      double scale, uint64_t* d_out);
 void encrypt(Context& ctx, const Secret& sk, const uint64_t* d_pt, uint32_t l, const uint8_t seed[32], uint32_t index,
              uint64_t* d_ct);
+void keygen_public(Context& ctx, const Secret& sk, const uint8_t seed[32], const uint8_t eseed[32], double sigma,
+                   uint64_t* d_pk);
+void encrypt_public(Context& ctx, const uint64_t* d_pk, const uint64_t* d_pt, uint32_t l, const uint8_t seed[32],
+                    uint32_t index, uint64_t* d_ct);
 void decrypt_coeffs(Context& ctx, const Secret& sk, const uint64_t* d_ct, uint32_t l, double* out);
 void decrypt_decode(Context& ctx, const Secret& sk, const uint64_t* d_ct, uint32_t l, double scale, double* re,
                     double* im, uint32_t n_slots);

@@ -56,6 +56,9 @@ SIGNATURES = {
                                  ctypes.POINTER(ServeReport)]),
     "fhe_ssm_decoder_serve": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ServeOpts), ctypes.POINTER(ServeReport)]),
     "fhe_ssm_meta_int": (ctypes.c_longlong, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_longlong]),
+    "fhe_ssm_client_encrypt_rows": (_int, [_vp, _vp, ctypes.c_char_p, _u32, _u32, _u32, _u32, _u32,
+                                           ctypes.c_double, _vp]),
+    "fhe_ssm_client_decrypt_logits": (_int, [_vp, _vp, ctypes.c_char_p, _vp, _u32, _u32, _u32]),
 }
 
 LAYER_WEIGHTS = ("g1", "g2", "eta", "mu_r", "mu_k", "mu_v", "mu_w", "mu_a", "mu_g", "mu_c", "W_r", "W_k", "W_v",
@@ -189,3 +192,20 @@ def meta_int(text: str, key: str, dflt: int = -1) -> int:
 def from_backend(be, n_layers: int) -> NativeDecoder:
     """A native decoder over the same context, plans and keys as a decode_step.HEBackend."""
     return NativeDecoder(be.ckks, be.ctx, n_layers, be.boots, be.relin, be.conj_key, be.keys)
+
+
+def client_encrypt_rows(ctx, d_pk: int, rows_path: str, tokens: int, lanes: int, d: int, dpad: int, level: int,
+                        scale: float, seed: bytes) -> None:
+    """the reference driver's --enc-in: rows_path (lanes x tokens x d float64, lane-major) -> rows_path.ct.<t> and
+    rows_path.ct.meta, encrypted under the public key d_pk"""
+    sd = (ctypes.c_uint8 * 32).from_buffer_copy(bytes(seed).ljust(32, b"\0")[:32])
+    check(load().fhe_ssm_client_encrypt_rows(ctx.h, d_pk, rows_path.encode(), tokens, lanes, d, dpad, level, scale,
+                                             sd))
+
+
+def client_decrypt_logits(ctx, sk, in_prefix: str, head: np.ndarray, dpad: int) -> None:
+    """the reference driver's --dec-out: in_prefix.meta + in_prefix.<t> -> in_prefix.logits.f64 (tokens x lanes rows
+    of vocab float64) with head (vocab x d) applied to each lane's decrypted channels"""
+    head = np.ascontiguousarray(head, dtype=np.float64)
+    check(load().fhe_ssm_client_decrypt_logits(ctx.h, sk.h, in_prefix.encode(), head.ctypes.data, head.shape[0],
+                                               head.shape[1], dpad))

@@ -335,6 +335,15 @@ int ckks_encode(ckks_context* ctx, const double* re, const double* im, uint32_t 
                 uint64_t* d_pt);
 int ckks_encrypt(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_pt, uint32_t level, const uint8_t* seed32,
                  uint32_t index, uint64_t* d_ct);
+/* public key (PKEBase::KeyGenInternal, harness/boot_overflow_probe.cpp:22,132-142: b = ns*e - a*s over the
+ * key's basis, elements {b, a}; ns = 1): d_pk [2][L+K][N] over Q*P, b = e - a s.  ckks_encrypt_public encrypts
+ * with it at any level as the client's Encrypt(publicKey, pt) does (gpu_real_model.cu:2202-2221 encCh; the
+ * client holds no secret, mac_fhe_client.cpp:570-609): ct = (ModDown(b v + e0) + m, ModDown(a v + e1)), v uniform
+ * ternary, e0/e1 Gaussian, all from seed32 and index; needs special primes. */
+int ckks_keygen_public(ckks_context* ctx, const ckks_secret* sk, const uint8_t* seed32, const uint8_t* eseed32,
+                       uint64_t* d_pk);
+int ckks_encrypt_public(ckks_context* ctx, const uint64_t* d_pk, const uint64_t* d_pt, uint32_t level,
+                        const uint8_t* seed32, uint32_t index, uint64_t* d_ct);
 int ckks_decrypt_decode(ckks_context* ctx, const ckks_secret* sk, const uint64_t* d_ct, uint32_t level, double scale,
                         double* re, double* im, uint32_t n_slots);
 /* decryption to the N centered coefficients (CRT of the first two limbs) as doubles */

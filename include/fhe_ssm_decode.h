@@ -114,6 +114,25 @@ int fhe_ssm_serve_dir(const char* dir, const fhe_ssm_serve_opts* opts, fhe_ssm_s
 int fhe_ssm_decoder_serve(fhe_ssm_decoder* dec, const char* dir, const fhe_ssm_serve_opts* opts,
                           fhe_ssm_serve_report* report);
 
+/* ---- the client's file steps (the reference driver's --enc-in and --dec-out, gpu_real_model.cu:2345-2533; the
+ * client invokes them per tick, ml-eval/fhe_client.py:1312-1328) --------------------------------------------------
+ * fhe_ssm_client_encrypt_rows   reads rows_path: lanes x tokens x d float64 little-endian rows, lane-major (lane r's
+ *   tokens rows first, fhe_client.py:206-238); token t's ciphertext holds slot rep*dpad + i = lane (rep mod lanes)
+ *   channel i for every rep < (N/2)/dpad (gpu_real_model.cu:2378-2395), encoded at level with scale and encrypted
+ *   under the public key d_pk (ckks_encrypt_public, seed32 and index t); writes rows_path.ct.<t> (ckks_ct_save
+ *   layout) and rows_path.ct.meta {"count","packTokens":1,"tokensReal","dpad","interleave":0,"lanes","ringDim",
+ *   "level"} (writeCtMeta, :2333-2340; the reference writes level 0, this engine the ciphertexts' level).  A file
+ *   shorter than the rows is refused (CKKS_EINVAL), as the reference's "short file" fatal.
+ * fhe_ssm_client_decrypt_logits reads in_prefix.meta and in_prefix.<t> for t < tokensReal, decrypts each, and
+ *   writes in_prefix.logits.f64: tokensReal * lanes rows (token-major, lane-minor) of vocab float64, row = head
+ *   (vocab x d, row-major) times the lane's first d channels (slot lane*dpad + j) (:2468-2522).  A meta whose
+ *   ringDim, dpad, interleave or packTokens differs is refused (the reference's "layout mismatch"). */
+int fhe_ssm_client_encrypt_rows(ckks_context* ctx, const uint64_t* d_pk, const char* rows_path, uint32_t tokens,
+                                uint32_t lanes, uint32_t d, uint32_t dpad, uint32_t level, double scale,
+                                const uint8_t* seed32);
+int fhe_ssm_client_decrypt_logits(ckks_context* ctx, const ckks_secret* sk, const char* in_prefix,
+                                  const double* head, uint32_t vocab, uint32_t d, uint32_t dpad);
+
 /* An integer value of a meta sidecar's one-line JSON (the reference's metaInt, gpu_real_model.cu:2327-2331); dflt
  * when the key is absent. */
 long long fhe_ssm_meta_int(const char* text, const char* key, long long dflt);

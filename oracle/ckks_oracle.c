@@ -620,10 +620,10 @@ void or_sample_ternary(const uint8_t seed[32], uint32_t N, uint32_t h, int8_t* s
     }
 }
 
-/* Rounded Gaussian: Box-Muller on two 53-bit uniforms from the "GAUS" stream (nonce word0 = stream). */
-void or_sample_gauss(const uint8_t seed[32], uint32_t stream, uint32_t N, double sigma, int32_t* e) {
+/* Rounded Gaussian: Box-Muller on two 53-bit uniforms from the "GAUS" stream (nonce words w0, w1). */
+void or_sample_gauss2(const uint8_t seed[32], uint32_t w0, uint32_t w1, uint32_t N, double sigma, int32_t* e) {
     or_stream st;
-    stream_init(&st, seed, stream, 0, 0x53554147u);
+    stream_init(&st, seed, w0, w1, 0x53554147u);
     const double two53 = 9007199254740992.0;
     for (uint32_t k = 0; k < N; k++) {
         const double u1 = ((double)(stream_next(&st) >> 11) + 1.0) / two53;
@@ -631,6 +631,10 @@ void or_sample_gauss(const uint8_t seed[32], uint32_t stream, uint32_t N, double
         const double z = sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
         e[k] = (int32_t)llround(sigma * z);
     }
+}
+
+void or_sample_gauss(const uint8_t seed[32], uint32_t stream, uint32_t N, double sigma, int32_t* e) {
+    or_sample_gauss2(seed, stream, 0, N, sigma, e);
 }
 
 void or_small_to_eval_i8(const or_ctx* c, const int8_t* s, uint32_t n_limbs, const uint32_t* prime_idx, uint64_t* out) {
@@ -684,4 +688,74 @@ void or_ksk_gen(const or_ctx* c, const uint64_t* s_old_eval, const int8_t* s_new
     free(sn);
     free(ee);
     free(e);
+}
+
+/* Public key over Q*P: pk = (b, a) with b = e - a*s (noise scale 1), as PKEBase::KeyGenInternal builds it
+ * (harness/boot_overflow_probe.cpp:22,139: b = ns*e - a*s, elements {b, a}; the key over paramsPK, which may hold
+ * more towers than Q, :132-:142).  a_i = or_fill_uniform(seed, 0, i, "PKEY"), e = or_sample_gauss2(eseed, 0, 0). */
+void or_pk_gen(const or_ctx* c, const uint64_t* s_eval, const uint8_t seed[32], const uint8_t eseed[32],
+               double sigma, uint64_t* pk) {
+    const uint32_t N = c->N, T = c->L + c->K;
+    uint32_t idx[OR_MAX_PRIMES];
+    for (uint32_t i = 0; i < T; i++) idx[i] = i;
+    uint64_t* b = pk;
+    uint64_t* a = pk + (size_t)T * N;
+    int32_t* e = (int32_t*)malloc(sizeof(int32_t) * N);
+    or_sample_gauss2(eseed, 0, 0, N, sigma, e);
+    or_small_to_eval_i32(c, e, T, idx, b);
+    for (uint32_t i = 0; i < T; i++) {
+        const uint64_t q = c->q[i];
+        or_fill_uniform(seed, 0, i, 0x59454b50u, q, a + (size_t)i * N, N);
+        for (uint32_t k = 0; k < N; k++) {
+            const size_t o = (size_t)i * N + k;
+            b[o] = (b[o] + q - or_mulmod(a[o], s_eval[o], q)) % q;
+        }
+    }
+    free(e);
+}
+
+/* Public-key encryption at level l: the key's Q_l and P limbs, x0 = b v + e0, x1 = a v + e1 over Q_l*P, then
+ * ApproxModDown of both to Q_l and the plaintext added to the first: ct = (ModDown(x0) + m, ModDown(x1)).  v is
+ * uniform ternary (or_fill_uniform(seed, index, 0, "ENCV", 3): 0, 1, 2 -> 0, 1, -1), e0 and e1 Gaussian streams
+ * (index, 2) and (index, 3) of the seed.  pk [2][L+K][N], m [l][N], ct [2][l][N]. */
+void or_pk_encrypt(const or_ctx* c, const uint64_t* pk, const uint64_t* m, uint32_t l, const uint8_t seed[32],
+                   uint32_t index, double sigma, uint64_t* ct) {
+    const uint32_t N = c->N, T = c->L + c->K, E = l + c->K;
+    uint32_t idx[OR_MAX_PRIMES];
+    for (uint32_t t = 0; t < E; t++) idx[t] = t < l ? t : c->L + (t - l);
+    uint64_t* u = (uint64_t*)malloc(sizeof(uint64_t) * N);
+    int8_t* v = (int8_t*)malloc(N);
+    int32_t* e = (int32_t*)malloc(sizeof(int32_t) * N);
+    uint64_t* ve = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)E * N);
+    uint64_t* ee = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)E * N);
+    uint64_t* x = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)E * N);
+    or_fill_uniform(seed, index, 0, 0x56434e45u, 3, u, N);
+    for (uint32_t k = 0; k < N; k++) v[k] = u[k] == 2 ? -1 : (int8_t)u[k];
+    or_small_to_eval_i8(c, v, E, idx, ve);
+    for (uint32_t p = 0; p < 2; p++) {
+        or_sample_gauss2(seed, index, 2 + p, N, sigma, e);
+        or_small_to_eval_i32(c, e, E, idx, ee);
+        for (uint32_t t = 0; t < E; t++) {
+            const uint64_t q = c->q[idx[t]];
+            const uint64_t* key = pk + ((size_t)p * T + idx[t]) * N;
+            for (uint32_t k = 0; k < N; k++) {
+                const size_t o = (size_t)t * N + k;
+                x[o] = (or_mulmod(key[k], ve[o], q) + ee[o]) % q;
+            }
+        }
+        uint64_t* out = ct + (size_t)p * l * N;
+        or_moddown(c, x, l, out);
+        if (p == 0)
+            for (uint32_t i = 0; i < l; i++)
+                for (uint32_t k = 0; k < N; k++) {
+                    const size_t o = (size_t)i * N + k;
+                    out[o] = (out[o] + m[o]) % c->q[i];
+                }
+    }
+    free(u);
+    free(v);
+    free(e);
+    free(ve);
+    free(ee);
+    free(x);
 }

@@ -119,6 +119,7 @@ void or_fill_uniform(const uint8_t seed[32], uint32_t word0, uint32_t word1, uin
 /* ---- seeded secret / noise (this repo's convention) ---- */
 void or_sample_ternary(const uint8_t seed[32], uint32_t N, uint32_t h, int8_t* s);   /* Hamming weight h */
 void or_sample_gauss(const uint8_t seed[32], uint32_t stream, uint32_t N, double sigma, int32_t* e);
+void or_sample_gauss2(const uint8_t seed[32], uint32_t w0, uint32_t w1, uint32_t N, double sigma, int32_t* e);
 
 /* small signed poly -> eval form limbs for the given primes */
 void or_small_to_eval_i8(const or_ctx* c, const int8_t* s, uint32_t n_limbs, const uint32_t* prime_idx, uint64_t* out);
@@ -129,6 +130,13 @@ void or_small_to_eval_i32(const or_ctx* c, const int32_t* e, uint32_t n_limbs, c
  * a_j: or_fill_uniform(seed, j, limb, 0x59454b53 "SKEY"), e_j: or_sample_gauss(eseed, stream j). */
 void or_ksk_gen(const or_ctx* c, const uint64_t* s_old_eval, const int8_t* s_new, const uint8_t seed[32],
                 const uint8_t eseed[32], double sigma, uint64_t* evk);
+
+/* ---- public key (b = e - a s over Q*P) and public-key encryption at level l (ModDown from Q_l*P) ----
+ * pk [2][L+K][N]; ct [2][l][N] = (ModDown(b v + e0) + m, ModDown(a v + e1)) */
+void or_pk_gen(const or_ctx* c, const uint64_t* s_eval, const uint8_t seed[32], const uint8_t eseed[32],
+               double sigma, uint64_t* pk);
+void or_pk_encrypt(const or_ctx* c, const uint64_t* pk, const uint64_t* m, uint32_t l, const uint8_t seed[32],
+                   uint32_t index, double sigma, uint64_t* ct);
 
 #ifdef __cplusplus
 }

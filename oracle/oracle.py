@@ -86,6 +86,9 @@ def lib():
             "or_small_to_eval_i8": (None, [P, vp, u32, vp, vp]),
             "or_small_to_eval_i32": (None, [P, vp, u32, vp, vp]),
             "or_ksk_gen": (None, [P, vp, vp, vp, vp, ctypes.c_double, vp]),
+            "or_sample_gauss2": (None, [vp, u32, u32, u32, ctypes.c_double, vp]),
+            "or_pk_gen": (None, [P, vp, vp, vp, ctypes.c_double, vp]),
+            "or_pk_encrypt": (None, [P, vp, vp, u32, vp, u32, ctypes.c_double, vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -145,6 +148,13 @@ def sample_gauss(seed: bytes, stream: int, N: int, sigma: float) -> np.ndarray:
     s = np.frombuffer(bytes(seed), dtype=np.uint8).copy()
     out = np.zeros(N, dtype=np.int32)
     lib().or_sample_gauss(_p(s), stream, N, sigma, _p(out))
+    return out
+
+
+def sample_gauss2(seed: bytes, w0: int, w1: int, N: int, sigma: float) -> np.ndarray:
+    s = np.frombuffer(bytes(seed), dtype=np.uint8).copy()
+    out = np.zeros(N, dtype=np.int32)
+    lib().or_sample_gauss2(_p(s), w0, w1, N, sigma, _p(out))
     return out
 
 
@@ -297,6 +307,25 @@ class Ctx:
             e = np.ascontiguousarray(s, dtype=np.int32)
             lib().or_small_to_eval_i32(self.ref, _p(e), len(pi), _p(pi), _p(out))
         return out
+
+    def pk_gen(self, s_eval, seed: bytes, eseed: bytes, sigma: float = 3.19):
+        """public key [2][L+K][N]: b = e - a s over Q*P (s_eval: the secret over all L+K limbs)"""
+        T = self.L + self.K
+        se = np.ascontiguousarray(s_eval, dtype=np.uint64)
+        sd = np.frombuffer(bytes(seed), dtype=np.uint8).copy()
+        es = np.frombuffer(bytes(eseed), dtype=np.uint8).copy()
+        pk = np.zeros((2, T, self.N), dtype=np.uint64)
+        lib().or_pk_gen(self.ref, _p(se), _p(sd), _p(es), sigma, _p(pk))
+        return pk
+
+    def pk_encrypt(self, pk, m, l: int, seed: bytes, index: int, sigma: float = 3.19):
+        """public-key encryption of the plaintext m [l][N] at level l -> [2][l][N]"""
+        pk = np.ascontiguousarray(pk, dtype=np.uint64)
+        m = np.ascontiguousarray(m, dtype=np.uint64)
+        sd = np.frombuffer(bytes(seed), dtype=np.uint8).copy()
+        ct = np.zeros((2, l, self.N), dtype=np.uint64)
+        lib().or_pk_encrypt(self.ref, _p(pk), _p(m), l, _p(sd), index, sigma, _p(ct))
+        return ct
 
     def ksk_gen(self, s_old_eval, s_new: np.ndarray, seed: bytes, eseed: bytes, sigma: float = 3.19):
         so = np.ascontiguousarray(s_old_eval, dtype=np.uint64)

@@ -196,6 +196,11 @@ def test_decoder_entry_points_refuse_null_arguments(tmp_path):
     assert lib.fhe_ssm_decoder_serve(None, str(tmp_path).encode(), ctypes.byref(opts), ctypes.byref(rep)) != 0
     assert b"null" in lib.fhe_ssm_last_error()
     assert lib.fhe_ssm_decoder_reset(None) != 0
+    seed = (ctypes.c_uint8 * 32)()
+    assert lib.fhe_ssm_client_encrypt_rows(None, None, str(tmp_path / "r").encode(), 1, 1, 4, 4, 2, 2.0**40, seed) != 0
+    assert b"null" in lib.fhe_ssm_last_error()
+    assert lib.fhe_ssm_client_decrypt_logits(None, None, str(tmp_path / "r").encode(), None, 1, 4, 4) != 0
+    assert b"null" in lib.fhe_ssm_last_error()
 
 
 def test_log_matches_a_reference_session(tmp_path):
