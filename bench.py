@@ -66,20 +66,42 @@ def timed_steps(torch, stream, step, steps, warmup):
     return wall, per
 
 
-# HBM bytes per launch of a workload's dominant kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the same
-# bench command (scaled by what the counters read for a copy kernel of known size: read = 2 x FETCH_SIZE KiB,
-# write = WRITE_SIZE KiB).  Measured, not computed: re-measure when the kernel or the workload changes.
-MEASURED_TRAFFIC = {("hmult", "ntt_fwd_2pass"): 7.950e9}
+# Counter-measured figures per launch of a workload's dominant kernel, from rocprofv3 --pmc passes over the same
+# bench command (one pass per counter group; the summaries and commands are in profiles/):
+#   traffic: HBM bytes, read = 2 x FETCH_SIZE KiB, write = WRITE_SIZE KiB (the scaling a copy kernel of known size
+#            reads off the two counters);
+#   valu:    wave64 VALU instructions issued (SQ_INSTS_VALU, all waves of the launch).
+# A "launch" is one engine call (both kernels of a two-pass NTT).  Measured, not computed: re-measure when the kernel
+# or the workload changes.
+MEASURED = {
+    ("hmult", "ntt_fwd_2pass"): {"traffic": 7.950e9, "valu_insts": 628.5e6, "source": "profiles/hmult_config2_kernels.md"},
+    ("ntt", "ntt_fwd_2pass"): {"traffic": 6.470e9, "valu_insts": 493.5e6, "source": "profiles/ntt_config1_kernel_trace.md"},
+    ("ntt", "ntt_inv_2pass"): {"traffic": 6.470e9, "valu_insts": 596.1e6, "source": "profiles/ntt_config1_kernel_trace.md"},
+}
+# int-VALU issue peak: 256 CUs x 4 SIMDs, one wave64 VALU instruction per SIMD every 4 cycles (16 lanes) at the
+# 2.4 GHz peak engine clock
+VALU_PEAK_GINSTS = 1024 * 2.4 / 4
+# the rate v_mad_u64_u32 sustains on the box (fhe-ssm_amd/microbench/valu_rate.hip: 4.94 cycles per wave64
+# instruction at the 2.4 GHz clock; profiles/valu_rates.md)
+VALU_MAD_GINSTS = 1024 * 2.4 / 4.94
 
 
 def roofline_from_profile(rep: dict, workload: str = ""):
     name, (n, ms, by) = max(rep.items(), key=lambda kv: kv[1][1])
     achieved = by / (ms * 1e-3) / 1e9
-    traffic = MEASURED_TRAFFIC.get((workload, name))
-    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": name,
-            "launches_in_profiled_step": n, "mean_launch_ms": round(ms / n, 4),
-            "algorithmic_bytes_per_launch": round(by / n)}
+    meas = MEASURED.get((workload, name), {})
+    out = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": meas.get("traffic"), "kernel": name,
+           "launches_in_profiled_step": n, "mean_launch_ms": round(ms / n, 4),
+           "algorithmic_bytes_per_launch": round(by / n)}
+    if meas.get("valu_insts"):
+        g = meas["valu_insts"] / (ms / n * 1e-3) / 1e9
+        out["valu"] = {"achieved": round(g, 1), "peak": VALU_PEAK_GINSTS, "unit": "G wave64 VALU inst/s",
+                       "frac": round(g / VALU_PEAK_GINSTS, 4), "insts_per_launch": meas["valu_insts"],
+                       "frac_of_measured_mad_rate": round(g / VALU_MAD_GINSTS, 4)}
+    if meas:
+        out["counters_source"] = meas["source"]
+    return out
 
 
 def kernel_table(rep: dict):
@@ -152,12 +174,51 @@ def bench_hmult(ckks, torch, steps, warmup, seed):
         "check": {"decrypted_relErrRms_max": rel_err, "ciphertexts_checked": 2},
         "kernels": kernel_table(rep),
         "roofline": roofline_from_profile(rep, "hmult"),
+        "ks_stage": ks_stage(rep),
     }
     return res
 
 
-def cpu_baseline_hmult(seed, budget_s=20.0):
-    """Oracle HMult+relin+rescale (single thread) on real-shaped random words of the config-2 context."""
+# SURVEY 8(d) key-switching unit per op: d2 24 limbs + evk 192 limbs + output 48 limbs
+KS_UNIT_BYTES = 138_412_032
+
+
+def ks_stage(rep: dict):
+    """the key-switching part of the profiled HMult step (every kernel but the tensor product; the rescale is fused
+    into the ModDown) against the key-switching unit"""
+    ms = sum(v[1] for k, v in rep.items() if k != "tensor")
+    gbs = N_PAIRS * KS_UNIT_BYTES / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "algorithmic_bytes": N_PAIRS * KS_UNIT_BYTES, "achieved": round(gbs, 1),
+            "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "kernels": sorted(k for k in rep if k != "tensor")}
+
+
+def host_cpu():
+    """the host's processor model and logical CPU count (recorded beside every CPU figure)"""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "nproc": os.cpu_count() or 1}
+
+
+def host_threads():
+    """threads for an all-core leg: the job's CPU share where the environment states one (OMP_NUM_THREADS), else
+    every processor"""
+    try:
+        return max(1, int(os.environ.get("OMP_NUM_THREADS", "")))
+    except ValueError:
+        return os.cpu_count() or 1
+
+
+def cpu_baseline_hmult(seed, budget_s=10.0):
+    """Oracle HMult+relin+rescale on real-shaped random words of the config-2 context: one thread, then every host
+    thread with one pair per thread (OpenMP over the pairs)."""
     from oracle import oracle as o
     qs = o.gen_primes(54, L2, 2 * N)
     ps = o.gen_primes(60, K2, 2 * N, exclude=qs)
@@ -167,17 +228,29 @@ def cpu_baseline_hmult(seed, budget_s=20.0):
     T = L2 + K2
     qp = np.array(qs + ps, dtype=np.uint64)[:, None]
     evk = (rng.integers(0, 2**63, (DNUM2, 2, T, N), dtype=np.uint64) % qp[None, None])
-    done, t0 = 0, time.perf_counter()
-    while True:
-        a = rng.integers(0, 2**63, (2, L2, N), dtype=np.uint64) % q[None]
-        b = rng.integers(0, 2**63, (2, L2, N), dtype=np.uint64) % q[None]
-        octx.hmult_relin_rescale(a, b, L2, evk)
+    pair = lambda n: rng.integers(0, 2**63, (n, 2, L2, N), dtype=np.uint64) % q[None, None]
+    done, el = 0, 0.0  # the time of the HMult calls only (input generation left out)
+    while el < budget_s and done < 4:
+        a, b = pair(1), pair(1)
+        t = time.perf_counter()
+        octx.hmult_relin_rescale(a[0], b[0], L2, evk)
+        el += time.perf_counter() - t
         done += 1
-        el = time.perf_counter() - t0
-        if el > budget_s or done >= 4:
-            break
-    return {"value": round(done / el, 4), "unit": "ops/s", "cores": 1, "kind": "port",
-            "sample": f"{done} HMult+relin+rescale of one config-2 pair ({el:.1f} s), C oracle, one thread"}
+    single = done / el
+    threads = o.set_threads(host_threads())
+    n = 2 * threads
+    a, b = pair(n), pair(n)
+    t = time.perf_counter()
+    octx.hmult_relin_rescale_batch(a, b, L2, evk)
+    el_all = time.perf_counter() - t
+    o.set_threads(0)
+    cpu = host_cpu()
+    return {"value": round(n / el_all, 4), "unit": "ops/s", "cores": threads, "kind": "port",
+            "sample": f"{n} HMult+relin+rescale of config-2 pairs over {threads} threads ({el_all:.1f} s), C oracle, "
+                      f"one pair per thread",
+            "single_thread": {"value": round(single, 4), "unit": "ops/s", "cores": 1,
+                              "sample": f"{done} pairs one after another ({el:.1f} s)"},
+            "cpu_model": cpu["model"], "nproc": cpu["nproc"]}
 
 
 # ----------------------------------------------------------------------------------------- config 3
@@ -230,8 +303,9 @@ def bench_pcmm(ckks, torch, steps_n, warmup, seed):
     rep = ctx.profile_report()
     ctx.profile_reset()
     ms = wall * 1e3 / steps_n
-    # algorithmic bytes: evk 56 x 96 limbs + 768 x 16 plaintext limbs + ct in/out 62 limbs
-    alg = (56 * 96 + d * l + 62) * LIMB_BYTES
+    # algorithmic bytes (the SURVEY 8d config-3 unit with this BSGS's key count: 27 baby + 27 giant keys of
+    # 96 limbs, not the unit's 56): keys + 768 x 16 plaintext limbs + ct in/out 62 limbs
+    alg = ((len(bst) + len(gst)) * 96 + d * l + 62) * LIMB_BYTES
     return {"ms_per_pcmm": round(ms, 4), "relErrRms_vs_fp64": rel, "algorithmic_GBps": round(alg / (ms * 1e-3) / 1e9, 1),
             "kernels": kernel_table(rep), "roofline": roofline_from_profile(rep),
             "workload": "config3: 768x768 fp64 weights N(0,1/768) x 1 ct at L=16, BSGS 28 baby x 28 giant, "
@@ -508,30 +582,41 @@ def bench_ntt(ckks, torch, steps, warmup, seed):
                    "limbs_per_direction": limbs, "algorithmic_bytes_per_direction": bytes_dir,
                    "ntt_mode": "two-pass", "seed": seed},
         "kernels": kernel_table(rep),
-        "roofline": roofline_from_profile(rep),
+        "roofline": roofline_from_profile(rep, "ntt"),
     }
 
 
-def cpu_baseline_ntt(seed, budget_s=12.0):
+def cpu_baseline_ntt(seed, budget_s=6.0):
+    """Oracle forward + inverse NTT over config-1 limbs: every host thread (OpenMP over the limbs), then one."""
     from oracle import oracle as o
     limbs_total, bytes_dir = ntt_bytes()
     qs = o.gen_primes(54, L2, 2 * N)
     octx = o.Ctx(16, qs, L2, 0, 1)
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     rng = np.random.default_rng(seed)
     q = np.array(qs, dtype=np.uint64)
     x = rng.integers(0, 2**63, (2, L2, N), dtype=np.uint64) % q[None, :, None]
-    done, t0 = 0, time.perf_counter()
-    while True:
-        y = octx.ntt_fwd(x, list(range(L2)))
-        octx.ntt_inv(y, list(range(L2)))
-        done += 2 * L2
-        el = time.perf_counter() - t0
-        if el > budget_s or done >= limbs_total:
-            break
-    gbs = done * 2 * (bytes_dir / limbs_total) / el / 1e9
+
+    def leg(threads):
+        got = o.set_threads(threads)
+        done, t0 = 0, time.perf_counter()
+        while True:
+            y = octx.ntt_fwd(x, list(range(L2)))
+            octx.ntt_inv(y, list(range(L2)))
+            done += 2 * L2
+            el = time.perf_counter() - t0
+            if el > budget_s or done >= limbs_total:
+                break
+        return got, done, el, done * 2 * (bytes_dir / limbs_total) / el / 1e9
+
+    cores, done, el, gbs = leg(host_threads())
+    _, done1, el1, gbs1 = leg(1)
+    o.set_threads(0)
+    cpu = host_cpu()
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"{done} limbs fwd+inv of the config-1 batch ({el:.1f} s), C oracle with OpenMP"}
+            "sample": f"{done} limbs fwd+inv of the config-1 batch ({el:.1f} s), C oracle with OpenMP over limbs",
+            "single_thread": {"value": round(gbs1, 3), "unit": "GB/s", "cores": 1,
+                              "sample": f"{done1} limbs fwd+inv ({el1:.1f} s)"},
+            "cpu_model": cpu["model"], "nproc": cpu["nproc"]}
 
 
 def main():
@@ -630,6 +715,8 @@ def main():
            "kernels": res["kernels"]}
     if "check" in res:
         out["check"] = res["check"]
+    if "ks_stage" in res:
+        out["ks_stage"] = res["ks_stage"]
     out.update(extra)
     if cpu is not None:
         out["cpu_baseline"] = cpu

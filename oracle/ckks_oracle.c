@@ -7,6 +7,9 @@
 #include "ckks_oracle.h"
 
 #include <math.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 #include <stdlib.h>
 #include <string.h>
 
@@ -478,6 +481,35 @@ void or_hmult_relin_rescale(const or_ctx* c, const uint64_t* a, const uint64_t* 
     or_rescale(c, d, 2, l, out);
     free(d);
     free(ks);
+}
+
+/* n_pairs independent HMult+relin+rescale calls spread over the host threads (one pair per thread at a time; the
+ * per-pair work itself stays scalar).  a, b [n_pairs][2][l][N], out [n_pairs][2][l-1][N].  For the timed CPU
+ * baseline's all-core leg. */
+void or_hmult_relin_rescale_batch(const or_ctx* c, const uint64_t* a, const uint64_t* b, uint32_t n_pairs,
+                                  uint32_t l, const uint64_t* evk, uint64_t* out) {
+    const size_t in_words = (size_t)2 * l * c->N, out_words = (size_t)2 * (l - 1) * c->N;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (long p = 0; p < (long)n_pairs; p++)
+        or_hmult_relin_rescale(c, a + (size_t)p * in_words, b + (size_t)p * in_words, l, evk,
+                               out + (size_t)p * out_words);
+}
+
+/* host threads of the OpenMP batch forms (n < 1: the runtime's default) and the count now in effect */
+void or_set_threads(int n) {
+#ifdef _OPENMP
+    omp_set_num_threads(n > 0 ? n : omp_get_num_procs());
+#else
+    (void)n;
+#endif
+}
+
+int or_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
 }
 
 /* ------------------------------------------------------------------ automorphism */

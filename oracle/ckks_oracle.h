@@ -98,6 +98,10 @@ void or_rescale(const or_ctx* c, const uint64_t* in, uint32_t n_polys, uint32_t 
 /* ---- HMult + relinearize + rescale of one pair at level l: a,b [2][l][N] -> out [2][l-1][N] ---- */
 void or_hmult_relin_rescale(const or_ctx* c, const uint64_t* a, const uint64_t* b, uint32_t l,
                             const uint64_t* evk, uint64_t* out);
+void or_hmult_relin_rescale_batch(const or_ctx* c, const uint64_t* a, const uint64_t* b, uint32_t n_pairs,
+                                  uint32_t l, const uint64_t* evk, uint64_t* out);
+void or_set_threads(int n);   /* OpenMP threads of the batch forms (n < 1: all processors) */
+int or_max_threads(void);
 
 /* ---- automorphism X -> X^g (g odd) ----
  * coefficient form: out[(j*g) mod N] = +-in[j] (negated when (j*g) mod 2N >= N)

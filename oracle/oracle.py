@@ -75,6 +75,9 @@ def lib():
             "or_keyswitch": (None, [P, vp, u32, vp, vp]),
             "or_rescale": (None, [P, vp, u32, u32, vp]),
             "or_hmult_relin_rescale": (None, [P, vp, vp, u32, vp, vp]),
+            "or_hmult_relin_rescale_batch": (None, [P, vp, vp, u32, u32, vp, vp]),
+            "or_set_threads": (None, [ctypes.c_int]),
+            "or_max_threads": (ctypes.c_int, []),
             "or_automorph_coef": (None, [P, vp, u32, vp, u32, vp]),
             "or_automorph_eval": (None, [P, vp, u32, u32, vp]),
             "or_rot_index": (u32, [P, ctypes.c_int64]),
@@ -274,6 +277,16 @@ class Ctx:
         lib().or_hmult_relin_rescale(self.ref, _p(a), _p(b), l, _p(evk), _p(out))
         return out
 
+    def hmult_relin_rescale_batch(self, a, b, l, evk):
+        """a, b [n][2][l][N] -> [n][2][l-1][N], the pairs spread over the OpenMP threads (set_threads)"""
+        a = np.ascontiguousarray(a, dtype=np.uint64)
+        b = np.ascontiguousarray(b, dtype=np.uint64)
+        evk = np.ascontiguousarray(evk, dtype=np.uint64)
+        n = a.shape[0]
+        out = np.zeros((n, 2, l - 1, self.N), dtype=np.uint64)
+        lib().or_hmult_relin_rescale_batch(self.ref, _p(a), _p(b), n, l, _p(evk), _p(out))
+        return out
+
     def automorph_coef(self, x, prime_idx, g):
         x = np.ascontiguousarray(x, dtype=np.uint64)
         pi = _u32(prime_idx)
@@ -390,3 +403,9 @@ def round_rule(m):
     if np.any(np.abs(v) > MAX_BIT_VALUE):
         raise ValueError("coefficient overflow")
     return llround(v), log_approx
+
+
+def set_threads(n: int) -> int:
+    """OpenMP threads of the oracle's batch forms (n < 1: all processors); returns the count now in effect"""
+    lib().or_set_threads(int(n))
+    return int(lib().or_max_threads())

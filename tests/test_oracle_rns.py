@@ -298,3 +298,18 @@ def test_moddown_exact_is_rounded_division(oracle):
             assert int(got_ex[i, k]) == r % q, (k, i)
             u = (f - int(got_ap[i, k])) % q
             assert u < K, (k, i, u)
+
+
+def test_hmult_batch_equals_single_calls(oracle, small):
+    """the all-core CPU baseline's batch form: the same words as one call per pair, whatever the thread count"""
+    rng = np.random.default_rng(21)
+    l, n = 6, 5
+    T = small.L + small.K
+    a = np.stack([np.stack([rand_limbs(small, range(l), rng) for _ in range(2)]) for _ in range(n)])
+    b = np.stack([np.stack([rand_limbs(small, range(l), rng) for _ in range(2)]) for _ in range(n)])
+    evk = np.stack([np.stack([rand_limbs(small, range(T), rng) for _ in range(2)]) for _ in range(3)])
+    want = np.stack([small.hmult_relin_rescale(a[i], b[i], l, evk) for i in range(n)])
+    for threads in (1, 3):
+        assert oracle.set_threads(threads) == threads
+        assert np.array_equal(small.hmult_relin_rescale_batch(a, b, l, evk), want)
+    oracle.set_threads(0)
