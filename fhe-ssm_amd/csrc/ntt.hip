@@ -101,6 +101,73 @@ __device__ __forceinline__ void gs_bfly(uint64_t& X, uint64_t& Y, const TwPair& 
     Y = shoup_lazy4(d, w.w, w.wp, nq);
 }
 
+// Inverse butterflies for primes below 2^55, the sum left unreduced.  A radix-16 group is 4 GS stages over a
+// thread's 16 values, stage s pairing k and k + 2^s.  Before stage s every value below E q has a bound that depends
+// on k's low s bits only: 4 q if bit s-1 is set (it was a stage's Shoup product), else twice its bound before stage
+// s-1 (it was a sum of two values of the same bound).  Entered below 32 q, the group leaves value 0 below 512 q
+// (< 2^64 with q < 2^55: no sum wraps) and every other value below 32 q; value 0 alone is brought back below 32 q
+// with four conditional subtracts, so every group (and both passes) can be entered below 32 q.  The difference
+// X - Y is lifted by Y's bound, X + c_Y - Y, a multiple of q; the Shoup product takes any 64-bit input.
+constexpr uint64_t kGsOpenMaxQ = 1ull << 55;
+
+struct GsBounds {
+    uint8_t lg[5][16];  // log2 of the bound (units of q) of value k before stage s (s = 4: after the group)
+};
+constexpr GsBounds make_gs_bounds() {
+    GsBounds g{};
+    uint32_t b[16] = {};
+    for (int k = 0; k < 16; k++) b[k] = 32;
+    for (int s = 0; s <= 4; s++) {
+        for (int k = 0; k < 16; k++) {
+            uint8_t l = 0;
+            while ((1u << l) < b[k]) l++;
+            g.lg[s][k] = l;
+        }
+        if (s == 4) break;
+        for (int k = 0; k < 16; k++)
+            if (!(k & (1 << s))) {
+                b[k] += b[k + (1 << s)];
+                b[k + (1 << s)] = 4;
+            }
+    }
+    return g;
+}
+constexpr GsBounds kGs = make_gs_bounds();
+constexpr bool gs_bounds_ok() {
+    // value 0 leaves a group below 512 q, every other value below 32 q; no stage's X + Y reaches 512 q
+    for (int k = 1; k < 16; k++)
+        if (kGs.lg[4][k] > 5) return false;
+    for (int s = 0; s < 4; s++)
+        for (int k = 0; k < 16; k++)
+            if (!(k & (1 << s)) && (1u << kGs.lg[s][k]) + (1u << kGs.lg[s][k + (1 << s)]) > 512) return false;
+    return kGs.lg[4][0] == 9;
+}
+static_assert(gs_bounds_ok(), "GS group bounds");
+
+// stage s of a group on the pair (X = value k, Y = value k + 2^s)
+template <bool kOpen>
+__device__ __forceinline__ void gs_step(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q, int s, int k,
+                                        uint64_t q4, uint64_t nq) {
+    if (kOpen) {
+        const uint64_t d = X + (q << kGs.lg[s][k + (1 << s)]) - Y;
+        X = X + Y;
+        Y = shoup_lazy4(d, w.w, w.wp, nq);
+    } else {
+        gs_bfly(X, Y, w, q4, nq);
+    }
+}
+
+// end of an open group: value 0 from below 512 q to below 32 q
+template <bool kOpen>
+__device__ __forceinline__ void gs_group_end(uint64_t* x, uint64_t q) {
+    if (kOpen) {
+        x[0] = csub_s(x[0], q << 8);
+        x[0] = csub_s(x[0], q << 7);
+        x[0] = csub_s(x[0], q << 6);
+        x[0] = csub_s(x[0], q << 5);
+    }
+}
+
 // [0, 8q) -> [0, q)
 __device__ __forceinline__ uint64_t canon8(uint64_t v, uint64_t q) {
     v = csub_s(v, q << 2);
@@ -225,6 +292,7 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
 // ---------------------------------------------------------------- inverse pass B (256-word blocks)
 // GS stages with t = 2^u, u = 0..7: m = 2^(15-u), twiddle m + (j >> (u+1)), j = 256 b + r.
 // in: the limb read (a itself, or the out-of-place source)
+template <bool kOpen>
 __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, const TwPair* __restrict__ tw, uint64_t q,
                                            int tile, int g, uint64_t* lds) {
     const uint64_t q4 = q << 2, nq = 0 - q;
@@ -259,7 +327,7 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
             const int i = k >> (u + 1);
-            gs_bfly(x[k], x[k + h], tw01[16 - (16 >> u) + i], q4, nq);
+            gs_step<kOpen>(x[k], x[k + h], tw01[16 - (16 >> u) + i], q, u, k, q4, nq);
         }
         if (u == 1) {
 #pragma unroll
@@ -268,6 +336,7 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
                 for (int j = 0; j < (8 >> (v - 4)); j++, n++) tw45[n] = tw[(32768 >> v) + b + (j << 8)];
         }
     }
+    gs_group_end<kOpen>(x, q);
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) L[17 * rl + k] = x[k];
@@ -281,15 +350,17 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
             const int j = k >> (u - 3);
-            gs_bfly(x[k], x[k + h], tw45[16 - (16 >> (u - 4)) + j], q4, nq);
+            gs_step<kOpen>(x[k], x[k + h], tw45[16 - (16 >> (u - 4)) + j], q, u - 4, k, q4, nq);
         }
     }
+    gs_group_end<kOpen>(x, q);  // the intermediate is stored below 32 q (below 4 q when not open)
 #pragma unroll
     for (int k = 0; k < 16; k++) __builtin_nontemporal_store(x[k], &blk[rl + 16 * k]);
 }
 
 // ---------------------------------------------------------------- inverse pass A (strided columns)
 // GS stages with t = 2^(8+u), u = 0..7: m = 2^(7-u), twiddle m + (r >> (u+1)); then * N^-1.
+template <bool kOpen>
 __device__ __forceinline__ void inv_a_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
                                            TwPair ninv, TwPair w1ninv, int tile, int g, uint64_t* lds) {
     const uint64_t q4 = q << 2, nq = 0 - q;
@@ -312,9 +383,11 @@ __device__ __forceinline__ void inv_a_tile(uint64_t* __restrict__ a, const TwPai
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
             const int i = k >> (u + 1);
-            gs_bfly(x[k], x[k + h], u < 2 ? twa[(u ? 8 : 0) + i] : tw[(128 >> u) + (rg << (3 - u)) + i], q4, nq);
+            gs_step<kOpen>(x[k], x[k + h], u < 2 ? twa[(u ? 8 : 0) + i] : tw[(128 >> u) + (rg << (3 - u)) + i], q, u,
+                           k, q4, nq);
         }
     }
+    gs_group_end<kOpen>(x, q);
 #pragma unroll
     for (int k = 0; k < 16; k++) lds[(16 * rg + k) * 17 + cl] = x[k];
     __syncthreads();
@@ -327,15 +400,16 @@ __device__ __forceinline__ void inv_a_tile(uint64_t* __restrict__ a, const TwPai
 #pragma unroll
         for (int k = 0; k < 16; k++) {
             if (k & h) continue;
-            gs_bfly(x[k], x[k + h], tw[(128 >> u) + (k >> (u - 3))], q4, nq);
+            gs_step<kOpen>(x[k], x[k + h], tw[(128 >> u) + (k >> (u - 3))], q, u - 4, k, q4, nq);
         }
     }
-    // u = 7 (m = 1, stride N/2) with N^-1 folded in: X' = (X + Y) N^-1, Y' = (X - Y) w_1 N^-1
+    // u = 7 (m = 1, stride N/2) with N^-1 folded in: X' = (X + Y) N^-1, Y' = (X - Y) w_1 N^-1.  Open: the three
+    // stages above leave value k + 8 below 2^lg[3][k+8] q and X + Y below 512 q
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const uint64_t X = x[k], Y = x[k + 8];
         x[k] = shoup_lazy4(X + Y, ninv.w, ninv.wp, nq);
-        x[k + 8] = shoup_lazy4(X + q4 - Y, w1ninv.w, w1ninv.wp, nq);
+        x[k + 8] = shoup_lazy4(X + (kOpen ? q << kGs.lg[3][k + 8] : q4) - Y, w1ninv.w, w1ninv.wp, nq);
     }
 #pragma unroll
     for (int k = 0; k < 16; k++) {
@@ -374,8 +448,13 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_b(uint64_t* data, JobS
     __shared__ uint64_t lds[kLdsWords];
     uint32_t off, prime;
     job_of(js, blockIdx.y, off, prime);
-    inv_b_tile(data + (size_t)off * kN, job_src(js, blockIdx.y, data, off), tw_all + (size_t)prime * kN,
-               primes[prime].q, blockIdx.x, threadIdx.x, lds);
+    const uint64_t q = primes[prime].q;
+    if (q < kGsOpenMaxQ)
+        inv_b_tile<true>(data + (size_t)off * kN, job_src(js, blockIdx.y, data, off), tw_all + (size_t)prime * kN, q,
+                         blockIdx.x, threadIdx.x, lds);
+    else
+        inv_b_tile<false>(data + (size_t)off * kN, job_src(js, blockIdx.y, data, off), tw_all + (size_t)prime * kN, q,
+                          blockIdx.x, threadIdx.x, lds);
 }
 
 __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_a(uint64_t* data, JobSpec js, const TwPair* tw_all,
@@ -384,8 +463,12 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_a(uint64_t* data, JobS
     uint32_t off, prime;
     job_of(js, blockIdx.y, off, prime);
     const PrimeInfo& P = primes[prime];
-    inv_a_tile(data + (size_t)off * kN, tw_all + (size_t)prime * kN, P.q, TwPair{P.ninv, P.ninv_p},
-               TwPair{P.w1ninv, P.w1ninv_p}, blockIdx.x, threadIdx.x, lds);
+    if (P.q < kGsOpenMaxQ)
+        inv_a_tile<true>(data + (size_t)off * kN, tw_all + (size_t)prime * kN, P.q, TwPair{P.ninv, P.ninv_p},
+                         TwPair{P.w1ninv, P.w1ninv_p}, blockIdx.x, threadIdx.x, lds);
+    else
+        inv_a_tile<false>(data + (size_t)off * kN, tw_all + (size_t)prime * kN, P.q, TwPair{P.ninv, P.ninv_p},
+                          TwPair{P.w1ninv, P.w1ninv_p}, blockIdx.x, threadIdx.x, lds);
 }
 
 // Fused: one limb per workgroup of 4 x 256 threads; each 256-thread group owns one LDS tile.
@@ -427,11 +510,11 @@ __global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_inv_fused(ui
     uint64_t* L = lds + grp * kLdsWords;
     const uint64_t* in = job_src(js, blockIdx.x, data, off);
     for (int t = grp; t < 16; t += kFusedGroups) {
-        inv_b_tile(a, in, twb_all + (size_t)prime * kN, P.q, t, g, L);
+        inv_b_tile<false>(a, in, twb_all + (size_t)prime * kN, P.q, t, g, L);
         __syncthreads();
     }
     for (int t = grp; t < 16; t += kFusedGroups) {
-        inv_a_tile(a, tw, P.q, TwPair{P.ninv, P.ninv_p}, TwPair{P.w1ninv, P.w1ninv_p}, t, g, L);
+        inv_a_tile<false>(a, tw, P.q, TwPair{P.ninv, P.ninv_p}, TwPair{P.w1ninv, P.w1ninv_p}, t, g, L);
         __syncthreads();
     }
 }
