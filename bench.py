@@ -8,7 +8,8 @@ Workloads (inputs seeded and resident in HBM before the t
          EvalMult+Rescale over the 64 pairs.  value = HMult+relin ops/s.
   ntt    config 1: forward then inverse NTT over 64 ct x 2 polys x 24 limbs.  value = algorithmic GB/s.
   pcmm   config 3: 768x768 plaintext matrix x one ciphertext (L=16) by BSGS 28 x 28.  value = ms.
-  bootstrap  config 4: full-slot bootstrap of a level-1 ciphertext.  value = ms; precision in bits.
+  bootstrap  config 4: full-slot bootstrap of a level-1 ciphertext (scale 2^55 under a 60-bit q0).  value = ms;
+         precision in bits.
   decode config 5: one encrypted decode step of the RWKV-7-0.1B-shaped model (12 layers, 32 lanes, state
          carried, bootstrapped once per layer).  value = s/step; decrypted output and logits checked
          against the float64 model.
@@ -313,6 +314,16 @@ def bench_pcmm(ckks, torch, steps_n, warmup, seed):
 
 
 # ----------------------------------------------------------------------------------------- config 4
+# Config-4 bootstrapping parameters.  The input's scale follows the reference's parameter rule FirstModSize =
+# min(60, ScalingModSize + 5) (hpc_gpu_port/gpu_real_model.cu:1153-1154): q0 of 60 bits over a 2^55 message, so
+# EvalMod's signal sin(2 pi m / q0) stands 2^5 below q0 (at 2^50 it stood 2^10 below, and EvalMod's absolute error
+# cost 5 bits of the result).  K = 32: the raised message's integer part I is a sum of 193 uniforms on [-1/2, 1/2]
+# per coefficient (h = 192 secret terms and c0), and a Chernoff bound on that sum puts P(some |I| > K - 1/2) below
+# 1.9e-9 per bootstrap of 2^16 coefficients; three double-angle steps keep the degree-59 interpolant of
+# cos(2 pi (K t - 1/4) / 8) far below the noise.
+BOOT_K, BOOT_DEG, BOOT_R, BOOT_TOP, BOOT_IN = 32.0, 59, 3, 2.0**55, 2.0**55
+
+
 def bootstrap_context(ckks):
     """q0 60-bit, 22 x 50-bit, 3 x 60-bit CoeffToSlot primes on top; 8 x 60-bit special primes; dnum 3."""
     big = ckks.gen_primes(60, 12)
@@ -323,7 +334,8 @@ def bootstrap_context(ckks):
 def bench_bootstrap(ckks, torch, steps_n, warmup, seed):
     ctx = bootstrap_context(ckks)
     L, K, D = ctx.L, ctx.K, ctx.dnum
-    bt = ckks.Bootstrap(ctx, K=22.0, cheb_degree=59, double_angles=2, top_scale=2.0**50, in_scale=2.0**50)
+    bt = ckks.Bootstrap(ctx, K=BOOT_K, cheb_degree=BOOT_DEG, double_angles=BOOT_R, top_scale=BOOT_TOP,
+                        in_scale=BOOT_IN)
     sk = ctx.secret(seed_bytes("boot-secret", seed), 192)
     dev = torch.device("cuda:0")
     kb = D * 2 * (L + K) * N * 8
@@ -342,7 +354,7 @@ def bench_bootstrap(ckks, torch, steps_n, warmup, seed):
     pt = torch.empty((1, N), dtype=torch.int64, device=dev)
     ct = torch.empty((2, 1, N), dtype=torch.int64, device=dev)
     out = torch.empty((2, bt.out_level, N), dtype=torch.int64, device=dev)
-    ctx.encode(z, 1, 2.0**50, pt.data_ptr())
+    ctx.encode(z, 1, BOOT_IN, pt.data_ptr())
     ctx.encrypt(sk, pt.data_ptr(), 1, seed_bytes("boot-enc", seed), 0, ct.data_ptr())
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
@@ -354,6 +366,7 @@ def bench_bootstrap(ckks, torch, steps_n, warmup, seed):
     wall, per = timed_steps(torch, stream, step, steps_n, warmup)
     got = ctx.decrypt(sk, out.data_ptr(), bt.out_level, bt.scale(bt.out_level), N // 2, complex_out=True)
     bits = float(-np.log2(np.max(np.abs(got - z))))
+    stages = bootstrap_stage_errors(ckks, ctx, bt, sk, ct, kp, rot, got, z)
     ctx.profile_reset()
     ctx.profile(True)
     step()
@@ -362,10 +375,45 @@ def bench_bootstrap(ckks, torch, steps_n, warmup, seed):
     rep = ctx.profile_report()
     ctx.profile_reset()
     return {"ms_per_bootstrap": round(wall * 1e3 / steps_n, 3), "precision_bits": round(bits, 2),
-            "levels_in_out": [1, bt.out_level], "rotation_keys": len(bt.steps),
+            "levels_in_out": [1, bt.out_level], "rotation_keys": len(bt.steps), "stage_errors": stages,
             "kernels": kernel_table(rep), "roofline": roofline_from_profile(rep),
-            "workload": "config4: full-slot bootstrap N=2^16, 32768 slots, CtS 3 levels, EvalMod Chebyshev 59 + 2 "
-                        "double-angle (K=22), StC 3 levels; chain q0 60 + 22x50 + 3x60 bits, P 8x60, dnum 3"}
+            "workload": "config4: full-slot bootstrap N=2^16, 32768 slots, level-1 input at scale 2^55 (q0 60 bits), "
+                        "CtS 3 levels, EvalMod Chebyshev 59 + 3 double-angle (K=32, P(|I| > K) < 1.9e-9 per "
+                        "bootstrap), StC 3 levels; chain q0 60 + 22x50 + 3x60 bits, P 8x60, dnum 3"}
+
+
+def bootstrap_stage_errors(ckks, ctx, bt, sk, ct, kp, rot, got, z):
+    """Error budget of one bootstrap, stage by stage (the engine stops after a stage on request): ModRaise decrypts
+    to m' = m + q0 I; after CoeffToSlot the slots hold t = (m'_k + i m'_{k+n}) / (q0 K), bit-reversed; EvalMod gives
+    sin(2 pi K t) per real part; SlotToCoeff gives z.  Each figure is the max error over the slots in the units of
+    that stage's signal, beside the signal's max (EvalMod's signal is ~2 pi m / q0: its absolute error, times
+    q0 / (2 pi scale_in), is the output's)."""
+    import torch
+    n = N // 2
+    L = ctx.L
+    buf = torch.empty((2, 2, L, N), dtype=torch.int64, device="cuda:0")
+    lvl = bt.run_stage(ct.data_ptr(), kp[0], kp[1], rot, 1, buf.data_ptr())
+    mp = ctx.decrypt_coeffs(sk, buf.data_ptr(), lvl)
+    rev = np.zeros(n, dtype=np.int64)
+    b = n.bit_length() - 1
+    for i in range(n):
+        rev[i] = int(format(i, f"0{b}b")[::-1], 2)
+    t = ((mp[:n] + 1j * mp[n:]) / (ctx.moduli[0] * BOOT_K))[rev]
+    res = {}
+    lvl = bt.run_stage(ct.data_ptr(), kp[0], kp[1], rot, 2, buf.data_ptr())
+    dec = ctx.decrypt(sk, buf.data_ptr(), lvl, bt.scale(lvl), n, complex_out=True)
+    res["coeff_to_slot"] = {"max_err": float(np.max(np.abs(dec - t))), "signal_max": float(np.max(np.abs(t))),
+                            "level": lvl}
+    lvl = bt.run_stage(ct.data_ptr(), kp[0], kp[1], rot, 4, buf.data_ptr())
+    errs, sig = [], []
+    for part, want in enumerate((np.sin(2 * np.pi * BOOT_K * t.real), np.sin(2 * np.pi * BOOT_K * t.imag))):
+        dec = ctx.decrypt(sk, buf.data_ptr() + part * 2 * lvl * N * 8, lvl, bt.scale(lvl), n, complex_out=True)
+        errs.append(float(np.max(np.abs(dec - want))))
+        sig.append(float(np.max(np.abs(want))))
+    res["eval_mod"] = {"max_err": max(errs), "signal_max": max(sig), "level": lvl}
+    res["slot_to_coeff"] = {"max_err": float(np.max(np.abs(got - z))), "signal_max": float(np.max(np.abs(z))),
+                            "level": bt.out_level}
+    return res
 
 
 # ----------------------------------------------------------------------------------------- config 5
@@ -660,7 +708,7 @@ def main():
         if not args.no_boot_line:
             b = bench_bootstrap(ckks, torch, max(2, args.steps // 4), 1, args.seed)
             extra["bootstrap_config4"] = {k: b[k] for k in ("ms_per_bootstrap", "precision_bits", "levels_in_out",
-                                                             "roofline")}
+                                                             "stage_errors", "roofline")}
         if not args.no_decode_line:
             gc.collect()  # the earlier workloads' contexts, keys and buffers go before config 5's ~230 GB
             d = bench_decode(ckks, torch, 1, 1, args.seed, driver=args.decode_driver)
@@ -695,7 +743,8 @@ def main():
         res = {"metric": "bootstrap ms (full-slot, N=2^16)", "value": b["ms_per_bootstrap"], "unit": "ms",
                "ms_per_step": b["ms_per_bootstrap"], "dtype": "u64", "config": {"workload": b["workload"]},
                "kernels": b["kernels"], "roofline": b["roofline"],
-               "check": {"precision_bits": b["precision_bits"], "levels_in_out": b["levels_in_out"]}}
+               "check": {"precision_bits": b["precision_bits"], "levels_in_out": b["levels_in_out"],
+                         "stage_errors": b["stage_errors"]}}
         extra, cpu = {}, None
     elif args.workload == "pcmm":
         p = bench_pcmm(ckks, torch, args.steps, args.warmup, args.seed)

@@ -2,10 +2,11 @@
 
 Chain: q0 60-bit, 22 x 50-bit scaling primes, 3 x 60-bit CoeffToSlot primes on top, 8 x 60-bit special
 primes, dnum 3; secret ternary with Hamming weight 192; input a level-1 ciphertext (the q0 limb only) of
-uniform slots in [-1, 1] at scale 2^50.  EvalMod: Chebyshev degree 59, 2 double-angle steps, K = 22: the
-raised message is m + q0 I with I a sum of 193 uniforms on [-1/2, 1/2] per coefficient (standard deviation
-~4.01), so |I| < 22 fails with probability ~4e-8 per coefficient (~0.3% per bootstrap of 2^16 coefficients).
-Precision is -log2 max|error| over all 32768 slots; the bar written here is 10 bits.
+uniform slots in [-1, 1] at scale 2^55 (the reference's FirstModSize = ScalingModSize + 5 rule,
+gpu_real_model.cu:1153-1154).  EvalMod: Chebyshev degree 59, 3 double-angle steps, K = 32: the raised message is
+m + q0 I with I the rounded sum of 193 uniforms on [-1/2, 1/2] per coefficient, and the Chernoff bound
+P(S >= t) <= min_l exp(-l t) (sinh(l/2) / (l/2))^193 at t = 31.5, times 2 x 2^16 coefficients, puts a failure
+(|I + m/q0| beyond K) below 1.9e-9 per bootstrap (tests/test_boot_params.py checks the figure on the CPU).  Precision is -log2 max|error| over all 32768 slots; the bar written here is 14 bits.
 """
 import numpy as np
 import pytest
@@ -40,7 +41,7 @@ CHAINS = {
     "config4": (lambda ckks: ckks.Context(num_q=26, num_p=8, dnum=3, scale=2.0**50,
                                           moduli=ckks.gen_primes(60, 1) + ckks.gen_primes(50, 22) +
                                           ckks.gen_primes(60, 12)[1:4] + ckks.gen_primes(60, 12)[4:]),
-                22.0, 59, 2, 2.0**50, 2.0**50),
+                32.0, 59, 3, 2.0**55, 2.0**55),
     "config5": (lambda ckks: _exact(ckks.Context(num_q=32, num_p=7, dnum=4, scale=2.0**40,
                                                  moduli=load_module("decode_step").config5_moduli(ckks))),
                 32.0, 59, 3, 2.0**52, 2.0**48),
@@ -57,8 +58,8 @@ def chain(request, ckks):
 def test_bootstrap_config4_precision(ckks, boot_ctx):
     ctx = boot_ctx
     L, K, D = ctx.L, ctx.K, ctx.dnum
-    bt = ckks.Bootstrap(ctx, K=22.0, cheb_degree=59, double_angles=2, top_scale=2.0**50, in_scale=2.0**50)
-    assert bt.out_level == L - 15
+    bt = ckks.Bootstrap(ctx, K=32.0, cheb_degree=59, double_angles=3, top_scale=2.0**55, in_scale=2.0**55)
+    assert bt.out_level == L - 16
     sk = ctx.secret(b"B" * 32, 192)
     kb = D * 2 * (L + K) * N * 8
     relin = ckks.DeviceBuffer(kb)
@@ -76,17 +77,17 @@ def test_bootstrap_config4_precision(ckks, boot_ctx):
     z = rng.uniform(-1.0, 1.0, SLOTS)
     pt = ckks.DeviceBuffer(1 * N * 8)
     ct = ckks.DeviceBuffer(2 * 1 * N * 8)
-    ctx.encode(z, 1, 2.0**50, pt.ptr)
+    ctx.encode(z, 1, 2.0**55, pt.ptr)
     ctx.encrypt(sk, pt.ptr, 1, b"e" * 32, 0, ct.ptr)
     # the level-1 input decrypts to z
-    assert np.max(np.abs(ctx.decrypt(sk, ct.ptr, 1, 2.0**50) - z)) < 1e-9
+    assert np.max(np.abs(ctx.decrypt(sk, ct.ptr, 1, 2.0**55) - z)) < 1e-9
     out = ckks.DeviceBuffer(2 * bt.out_level * N * 8)
     bt.run(ct.ptr, relin.ptr, conj.ptr, keys, out.ptr)
     got = ctx.decrypt(sk, out.ptr, bt.out_level, bt.scale(bt.out_level), SLOTS, complex_out=True)
     err = np.abs(got - z)
     bits = -np.log2(err.max())
     print(f"bootstrap precision: {bits:.2f} bits (max err {err.max():.3e}, mean {err.mean():.3e})")
-    assert bits > 10.0, bits
+    assert bits > 14.0, bits
 
 
 def _bitrev(n):
