@@ -105,12 +105,15 @@ SIGNATURES = {
                                  ctypes.POINTER(ctypes.c_double)]),
     "ckks_ct_save": (_int, [_vp, ctypes.c_char_p, _vp, _u32, ctypes.c_double]),
     "ckks_ct_load": (_int, [_vp, ctypes.c_char_p, _u32, _vp, ctypes.POINTER(_u32), ctypes.POINTER(ctypes.c_double)]),
+    "ckks_encode_periodic_coeffs": (_int, [_vp, _vp, _vp, _u32, _u32, ctypes.c_double, _vp, _vp]),
+    "ckks_expand_periodic": (_int, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp]),
     "ckks_encode": (_int, [_vp, _vp, _vp, _u32, _u32, ctypes.c_double, _vp]),
     "ckks_encrypt": (_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp]),
     "ckks_keygen_public": (_int, [_vp, _vp, _vp, _vp, _vp]),
     "ckks_encrypt_public": (_int, [_vp, _vp, _vp, _u32, _vp, _u32, _vp]),
     "ckks_decrypt_decode": (_int, [_vp, _vp, _vp, _u32, ctypes.c_double, _vp, _vp, _u32]),
     "ckks_context_counters": (_int, [_vp, _vp, _int]),
+    "ckks_context_memory": (_int, [_vp, _vp, _u32]),
     "ckks_set_moddown_exact": (_int, [_vp, _int]),
     "ckks_keygen_switch": (_int, [_vp, _vp, _vp, _vp, _vp, _u32, _vp]),
     "ckks_bootstrap_set_sparse_keys": (_int, [_vp, _vp, _vp]),
@@ -313,6 +316,19 @@ class Context:
         check(load().ckks_encode_periodic(self.h, _ptr(re), _ptr(im) if im is not None else None, v.shape[0],
                                           v.shape[1], level, scale, d_out))
 
+    def encode_periodic_coeffs(self, values, scale: float, d_coef, d_log_approx) -> None:
+        """the host half of encode_periodic: d_coef [n][2 period] int64, d_log_approx [n] int32 (any level)"""
+        v = np.atleast_2d(np.asarray(values))
+        re = np.ascontiguousarray(v.real, dtype=np.float64)
+        im = np.ascontiguousarray(v.imag, dtype=np.float64) if np.iscomplexobj(v) else None
+        check(load().ckks_encode_periodic_coeffs(self.h, _ptr(re), _ptr(im) if im is not None else None, v.shape[0],
+                                                 v.shape[1], scale, d_coef, d_log_approx))
+
+    def expand_periodic(self, d_coef, d_log_approx, n_vectors: int, period: int, level: int, d_out,
+                        stream=None) -> None:
+        """the device half: d_out [n][level][2 period], the words encode_periodic writes"""
+        check(load().ckks_expand_periodic(self.h, d_coef, d_log_approx, n_vectors, period, level, d_out, stream))
+
     def eval_mult_plain_ex(self, d_ct, batch, level, d_pt, log_rep, d_out, pt_shared=True, stream=None):
         check(load().ckks_eval_mult_plain_ex(self.h, d_ct, batch, level, d_pt, 1 if pt_shared else 0, log_rep,
                                              d_out, stream))
@@ -439,6 +455,12 @@ class Context:
         out = np.zeros(self.N, dtype=np.float64)
         check(load().ckks_decrypt_coeffs(self.h, sk.h, d_ct, level, _ptr(out)))
         return out
+
+    def memory(self) -> dict:
+        """device bytes the context holds itself: constant tables, key-switching workspaces, bootstrapping pool"""
+        v = np.zeros(3, dtype=np.uint64)
+        check(load().ckks_context_memory(self.h, _ptr(v), 3))
+        return {"tables": int(v[0]), "workspaces": int(v[1]), "bootstrap_pool": int(v[2])}
 
     # profiling ---------------------------------------------------------------------------------
     def profile(self, on: bool) -> None:

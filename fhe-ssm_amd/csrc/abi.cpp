@@ -648,6 +648,30 @@ int ckks_encode_periodic(ckks_context* ctx, const double* re, const double* im, 
     });
 }
 
+int ckks_encode_periodic_coeffs(ckks_context* ctx, const double* re, const double* im, uint32_t n_vectors,
+                                uint32_t period, double scale, int64_t* d_coef, int32_t* d_log_approx) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    if (!d_coef || !d_log_approx || (!re && !im)) return fail(CKKS_EINVAL, "null argument");
+    if (!(scale > 0)) return fail(CKKS_EINVAL, "scale must be positive");
+    if (!n_vectors) return CKKS_OK;
+    return guarded([&] {
+        fhe::encode_periodic_coeffs(ctx->c, re, im, n_vectors, period, scale, d_coef, d_log_approx);
+        return CKKS_OK;
+    });
+}
+
+int ckks_expand_periodic(ckks_context* ctx, const int64_t* d_coef, const int32_t* d_log_approx, uint32_t n_vectors,
+                         uint32_t period, uint32_t level, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, false)) return rc;
+    if (!d_coef || !d_log_approx || !d_out) return fail(CKKS_EINVAL, "null buffer");
+    if (!n_vectors) return CKKS_OK;
+    if (n_vectors > 0x7fffffffu) return fail(CKKS_EINVAL, "too many vectors");
+    return guarded([&] {
+        fhe::expand_periodic(ctx->c, d_coef, d_log_approx, n_vectors, period, level, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
 int ckks_eval_mult_plain_ex(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level,
                             const uint64_t* d_pt, int pt_shared, uint32_t log_rep, uint64_t* d_out, void* stream) {
     if (int rc = check_ctx_level(ctx, level, false)) return rc;
@@ -931,6 +955,20 @@ int ckks_context_counters(ckks_context* ctx, uint64_t* key_switches, int reset) 
     if (!ctx) return fail(CKKS_EINVAL, "null context");
     if (key_switches) *key_switches = ctx->c.n_keyswitch;
     if (reset) ctx->c.n_keyswitch = 0;
+    return CKKS_OK;
+}
+
+int ckks_context_memory(const ckks_context* ctx, uint64_t* bytes, uint32_t n) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    if (!bytes && n) return fail(CKKS_EINVAL, "null argument");
+    const fhe::Context& c = ctx->c;
+    const uint64_t T = c.L + c.K;
+    uint64_t v[3] = {0, 0, 0};
+    v[0] = 4 * T * fhe::kN * sizeof(fhe::TwPair) + T * sizeof(fhe::PrimeInfo);
+    for (auto& kv : c.small_ntt) v[0] += T * kv.first * sizeof(fhe::TwPair);
+    for (auto& s : c.scratch) v[1] += s.second;
+    for (auto& kv : c.buf_pool) v[2] += kv.first * kv.second.size();
+    for (uint32_t i = 0; i < n && i < 3; i++) bytes[i] = v[i];
     return CKKS_OK;
 }
 

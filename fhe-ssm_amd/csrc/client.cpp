@@ -396,23 +396,13 @@ void encode_primes(Context& ctx, const double* re, const double* im, uint32_t n_
     coeffs_to_eval(ctx, coef.data(), 1, pmap, d_pt, nullptr, (uint32_t)log_approx);
 }
 
-// Periodic encoding (hpc_gpu_port/periodic_encode.hpp:179-260): a slot vector of period P (replicated
-// REP = N/(2P) times) is the encoding of a polynomial in X^REP, i.e. of one period in the ring of degree
-// N' = 2P.  Its evaluation form, in the bit-reversed order of the N-point NTT, has word k equal to word
-// k >> log2(REP) of the N'-point NTT (root psi^REP) of that small polynomial, so only N' words per limb
-// are stored.  The special FFT and rounding run on the host (over threads); residues and the N'-point NTTs
-// on the GPU.  out: [n_vec][l][N'].
-void encode_periodic(Context& ctx, const double* re, const double* im, uint32_t n_vec, uint32_t P, uint32_t l,
-                     double scale, uint64_t* d_out) {
-    if (P < 2 || (P & (P - 1)) || P > 2048) throw std::invalid_argument("period must be a power of two in [2, 2048]");
-    const uint32_t Np = 2 * P;
-    uint32_t logNp = 0;
-    while ((1u << logNp) < Np) logNp++;
-    const uint32_t rep = kN / Np;
+// the N'-point table Table[brev(j)] = psi'^j, psi' = psi^(N/N'), per prime of the chain (made on first use)
+static const TwPair* small_table(Context& ctx, uint32_t Np) {
     auto it = ctx.small_ntt.find(Np);
     if (it == ctx.small_ntt.end()) {
-        // Table[brev(j)] = psi'^j with psi' = psi^rep, per prime of the chain
-        const uint32_t T = ctx.L + ctx.K;
+        uint32_t logNp = 0;
+        while ((1u << logNp) < Np) logNp++;
+        const uint32_t rep = kN / Np, T = ctx.L + ctx.K;
         std::vector<TwPair> tabs((size_t)T * Np);
         for (uint32_t i = 0; i < T; i++) {
             const uint64_t q = ctx.moduli[i];
@@ -430,6 +420,25 @@ void encode_periodic(Context& ctx, const double* re, const double* im, uint32_t 
         HIPC(hipMemcpy(d, tabs.data(), tabs.size() * sizeof(TwPair), hipMemcpyHostToDevice));
         it = ctx.small_ntt.emplace(Np, d).first;
     }
+    return it->second;
+}
+
+static void check_period(uint32_t P) {
+    if (P < 2 || (P & (P - 1)) || P > 2048) throw std::invalid_argument("period must be a power of two in [2, 2048]");
+}
+
+// Periodic plaintexts (hpc_gpu_port/periodic_encode.hpp:179-260).  A slot vector of period P (replicated REP = N/(2P) times) is the encoding of a polynomial in
+// X^REP, i.e. of one period in the ring of degree N' = 2P.  Its evaluation form, in the bit-reversed order of the
+// N-point NTT, has word k equal to word k >> log2(REP) of the N'-point NTT (root psi^REP) of that small polynomial,
+// so only N' words per limb are stored.  The special FFT and rounding run on the host (over threads): their result,
+// the small polynomial's integer coefficients (and each vector's approxFactor exponent), is independent of the
+// level and N' words per vector in all; the residues and the N'-point NTTs of any number of limbs follow on the GPU.
+// d_coef [n_vec][N'] int64, d_log_approx [n_vec] int32 (device memory).
+void encode_periodic_coeffs(Context& ctx, const double* re, const double* im, uint32_t n_vec, uint32_t P,
+                            double scale, int64_t* d_coef, int32_t* d_log_approx) {
+    (void)ctx;
+    check_period(P);
+    const uint32_t Np = 2 * P;
     std::vector<int64_t> coef((size_t)n_vec * Np);
     std::vector<int32_t> log_approx(n_vec, 0);
     std::vector<std::string> errs(n_vec);
@@ -444,10 +453,25 @@ void encode_periodic(Context& ctx, const double* re, const double* im, uint32_t 
     });
     for (const auto& e : errs)
         if (!e.empty()) throw std::invalid_argument(e);
-    DevBuf dc(coef.size() * 8), dl(log_approx.size() * 4);
-    HIPC(hipMemcpy(dc.p, coef.data(), coef.size() * 8, hipMemcpyHostToDevice));
-    HIPC(hipMemcpy(dl.p, log_approx.data(), log_approx.size() * 4, hipMemcpyHostToDevice));
-    HIPC(launch_encode_small(ctx, dc.as<int64_t>(), dl.as<int32_t>(), d_out, n_vec, Np, l, it->second, nullptr));
+    HIPC(hipMemcpy(d_coef, coef.data(), coef.size() * 8, hipMemcpyHostToDevice));
+    HIPC(hipMemcpy(d_log_approx, log_approx.data(), log_approx.size() * 4, hipMemcpyHostToDevice));
+}
+
+// the device half: coefficients -> [n_vec][l][N'] evaluation-form limbs, enqueued on st
+void expand_periodic(Context& ctx, const int64_t* d_coef, const int32_t* d_log_approx, uint32_t n_vec, uint32_t P,
+                     uint32_t l, uint64_t* d_out, hipStream_t st) {
+    check_period(P);
+    const TwPair* tab = small_table(ctx, 2 * P);
+    HIPC(launch_encode_small(ctx, d_coef, d_log_approx, d_out, n_vec, 2 * P, l, tab, st));
+}
+
+// both halves: out [n_vec][l][N']
+void encode_periodic(Context& ctx, const double* re, const double* im, uint32_t n_vec, uint32_t P, uint32_t l,
+                     double scale, uint64_t* d_out) {
+    check_period(P);
+    DevBuf dc((size_t)n_vec * 2 * P * 8), dl((size_t)n_vec * 4);
+    encode_periodic_coeffs(ctx, re, im, n_vec, P, scale, dc.as<int64_t>(), dl.as<int32_t>());
+    expand_periodic(ctx, dc.as<int64_t>(), dl.as<int32_t>(), n_vec, P, l, d_out, nullptr);
     HIPC(hipDeviceSynchronize());
 }
 

@@ -31,6 +31,10 @@ void encode_primes(Context& ctx, const double* re, const double* im, uint32_t n_
                    const std::vector<uint32_t>& pmap, double scale, uint64_t* d_pt);
 void encode_periodic(Context& ctx, const double* re, const double* im, uint32_t n_vec, uint32_t P, uint32_t l,
                      double scale, uint64_t* d_out);
+void encode_periodic_coeffs(Context& ctx, const double* re, const double* im, uint32_t n_vec, uint32_t P,
+                            double scale, int64_t* d_coef, int32_t* d_log_approx);
+void expand_periodic(Context& ctx, const int64_t* d_coef, const int32_t* d_log_approx, uint32_t n_vec, uint32_t P,
+                     uint32_t l, uint64_t* d_out, hipStream_t st);
 void encrypt(Context& ctx, const Secret& sk, const uint64_t* d_pt, uint32_t l, const uint8_t seed[32], uint32_t index,
              uint64_t* d_ct);
 void keygen_public(Context& ctx, const Secret& sk, const uint8_t seed[32], const uint8_t eseed[32], double sigma,

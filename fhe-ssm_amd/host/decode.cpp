@@ -25,6 +25,7 @@
 #include <functional>
 #include <map>
 #include <memory>
+#include <set>
 #include <stdexcept>
 #include <string>
 #include <tuple>
@@ -70,12 +71,15 @@ class Pool {
         }
         void* p = nullptr;
         ck(ckks_buffer_alloc(bytes, &p), "ckks_buffer_alloc");
+        total_ += bytes;
         return (uint64_t*)p;
     }
     void put(uint64_t* p, size_t bytes) { free_[bytes].push_back(p); }
+    size_t total() const { return total_; }  // every buffer allocated, in use or free
 
    private:
     std::map<size_t, std::vector<uint64_t*>> free_;
+    size_t total_ = 0;
 };
 
 struct Buf {
@@ -106,8 +110,12 @@ struct Ct {
 
 using Pair = std::tuple<const Ct*, uint32_t, const Ct*, uint32_t>;  // (a, item of a, b, item of b)
 
+// A matvec's 1024-periodic diagonals, stored as their small-ring integer coefficients (2048 int64 per diagonal
+// and one int32 approxFactor exponent, whatever the level: ~1/level of the expanded plaintexts) and expanded to
+// the level's limbs each time the matvec is applied.
 struct Matvec {
-    std::shared_ptr<Buf> buf;
+    std::shared_ptr<Buf> coef;  // [n_diag][2 DPAD] int64, then [n_diag] int32
+    uint32_t n_diag = 0, level = 0;
     uint32_t n_out = 0, n_in = 0, nb = 0;
 };
 
@@ -343,11 +351,28 @@ class Engine {
             gs[g] = (int64_t)nb * (g0 + g);
             kg[g] = key(gs[g]);
         }
+        if (h.level != lv) throw Error(CKKS_EINVAL, "matvec diagonals encoded for another level");
         Ct out = fresh(h.n_out, lv - 1, inputs[0].scale * S(lv) / (double)moduli_[lv - 1]);
-        ck(ckks_linear_transform_multi(ctx_, in.data(), h.n_in, lv, h.buf->d, LOG_REP, nb, bs.data(), kb.data(), ng,
+        ck(ckks_linear_transform_multi(ctx_, in.data(), h.n_in, lv, expand(h), LOG_REP, nb, bs.data(), kb.data(), ng,
                                        gs.data(), kg.data(), h.n_out, 1, out.ptr(), nullptr),
            "ckks_linear_transform_multi");
         return out;
+    }
+
+    // a matvec's diagonals expanded to its level's limbs in one buffer shared by every matvec (grown to the
+    // largest): the work is stream-ordered, so the previous matvec has read it before the next expansion writes
+    const uint64_t* expand(const Matvec& h) {
+        const size_t bytes = (size_t)h.n_diag * h.level * (kN >> LOG_REP) * 8;
+        if (!diag_ || diag_->bytes < bytes) {
+            diag_.reset();
+            void* p = nullptr;
+            ck(ckks_buffer_alloc(bytes, &p), "ckks_buffer_alloc");
+            diag_ = std::make_shared<Buf>((uint64_t*)p, bytes, nullptr);
+        }
+        const int64_t* c = reinterpret_cast<const int64_t*>(h.coef->d);
+        const int32_t* la = reinterpret_cast<const int32_t*>(c + (size_t)h.n_diag * (kN >> LOG_REP));
+        ck(ckks_expand_periodic(ctx_, c, la, h.n_diag, DPAD, h.level, diag_->d, nullptr), "ckks_expand_periodic");
+        return diag_->d;
     }
 
     Ct mul_i(const Ct& a, int sign) {
@@ -380,6 +405,25 @@ class Engine {
     }
 
     // -- plaintexts -----------------------------------------------------------------------------------
+    // the coefficient form of 1024-periodic vectors at level's scale: [n][2 DPAD] int64, then [n] int32
+    std::shared_ptr<Buf> encode_coeffs(const std::vector<double>& vecs, uint32_t level, uint32_t* n_out) {
+        const uint32_t n = (uint32_t)(vecs.size() / DPAD);
+        const size_t per = (size_t)(kN >> LOG_REP) * 8;
+        void* p = nullptr;
+        ck(ckks_buffer_alloc(n * (per + 4), &p), "ckks_buffer_alloc");
+        auto buf = std::make_shared<Buf>((uint64_t*)p, n * (per + 4), nullptr);
+        int64_t* c = (int64_t*)p;
+        int32_t* la = (int32_t*)(c + (size_t)n * (kN >> LOG_REP));
+        for (uint32_t s = 0; s < n; s += 4096) {  // in chunks (bounds the encoder's host staging)
+            const uint32_t m = std::min<uint32_t>(4096, n - s);
+            ck(ckks_encode_periodic_coeffs(ctx_, vecs.data() + (size_t)s * DPAD, nullptr, m, DPAD, S(level),
+                                           c + (size_t)s * (kN >> LOG_REP), la + s),
+               "ckks_encode_periodic_coeffs");
+        }
+        *n_out = n;
+        return buf;
+    }
+
     std::shared_ptr<Buf> encode_periodic(const std::vector<double>& vecs, uint32_t level) {
         const uint32_t n = (uint32_t)(vecs.size() / DPAD);
         const size_t per = (size_t)level * (kN >> LOG_REP) * 8;
@@ -444,6 +488,11 @@ class Engine {
     std::map<std::string, fhe_ssm_refresh> boots_;
     std::map<std::string, std::pair<std::vector<int64_t>, std::vector<const uint64_t*>>> boot_keys_;
     Pool pool_;
+    std::shared_ptr<Buf> diag_;  // expanded matvec diagonals (see expand)
+
+   public:
+    size_t pool_bytes() const { return pool_.total(); }
+    size_t diag_bytes() const { return diag_ ? diag_->bytes : 0; }
 };
 
 // ------------------------------------------------------------------ slot-layout tables
@@ -613,6 +662,27 @@ class Decoder {
     uint64_t bootstraps() const { return n_boot_; }
     // the next step starts cold (zero WKV state and token-shift carries), as the first one does
     void reset() { state_.clear(); }
+    // device bytes: the plaintext store, and the carried state (each buffer counted once)
+    size_t store_bytes() const {
+        size_t b = 0;
+        for (auto& kv : pt_) b += kv.second->bytes;
+        for (auto& kv : mv_) b += kv.second.coef->bytes;
+        return b;
+    }
+    size_t state_bytes() const {
+        std::set<const Buf*> seen;
+        size_t b = 0;
+        auto add = [&](const Ct& c) {
+            if (c.buf && seen.insert(c.buf.get()).second) b += c.buf->bytes;
+        };
+        for (auto& st : state_) {
+            for (auto& c : st.Dseg) add(c);
+            add(st.xp_t);
+            add(st.xp_c);
+            add(st.Dn);
+        }
+        return b;
+    }
     // the carried state as handles (for a caller that must undo several steps, e.g. a multi-token request)
     std::vector<LayerState> snapshot() const { return state_; }
     void restore(std::vector<LayerState> s) { state_ = std::move(s); }
@@ -637,7 +707,8 @@ class Decoder {
             m.n_out = (uint32_t)blocks.size();
             m.n_in = (uint32_t)blocks[0].size();
             m.nb = (uint32_t)mv_nb(m.n_in, m.n_out);
-            m.buf = be_->encode_periodic(matvec_diagonals(blocks), level);
+            m.level = level;
+            m.coef = be_->encode_coeffs(matvec_diagonals(blocks), level, &m.n_diag);
             it = mv_.emplace(key, std::move(m)).first;
         }
         return it->second;
@@ -1005,6 +1076,15 @@ int fhe_ssm_decoder_serve(fhe_ssm_decoder* dec, const char* dir, const fhe_ssm_s
     ckks_buffer_free(sv.d_in);
     if (rc == CKKS_OK) g_err.clear();
     return rc;
+}
+
+int fhe_ssm_decoder_memory(const fhe_ssm_decoder* dec, uint64_t* bytes, uint32_t n) {
+    return guarded([&] {
+        if (!dec || (!bytes && n)) throw Error(CKKS_EINVAL, "null argument");
+        const uint64_t v[4] = {dec->dec->store_bytes(), dec->be->diag_bytes(), dec->be->pool_bytes(),
+                               dec->dec->state_bytes()};
+        for (uint32_t i = 0; i < n && i < 4; i++) bytes[i] = v[i];
+    });
 }
 
 int fhe_ssm_decoder_stats(const fhe_ssm_decoder* dec, uint64_t* bootstraps) {

@@ -56,6 +56,7 @@ SIGNATURES = {
                                  ctypes.POINTER(ServeReport)]),
     "fhe_ssm_decoder_serve": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ServeOpts), ctypes.POINTER(ServeReport)]),
     "fhe_ssm_meta_int": (ctypes.c_longlong, [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_longlong]),
+    "fhe_ssm_decoder_memory": (_int, [_vp, _vp, _u32]),
     "fhe_ssm_client_encrypt_rows": (_int, [_vp, _vp, ctypes.c_char_p, _u32, _u32, _u32, _u32, _u32,
                                            ctypes.c_double, _vp]),
     "fhe_ssm_client_decrypt_logits": (_int, [_vp, _vp, ctypes.c_char_p, _vp, _u32, _u32, _u32]),
@@ -132,6 +133,14 @@ class NativeDecoder:
     def reset(self) -> None:
         """drop the carried state: the next step starts cold"""
         check(load().fhe_ssm_decoder_reset(self.h))
+
+    def memory(self) -> dict:
+        """device bytes the decoder holds: plaintext store, expanded-diagonal buffer, ciphertext pool (all it has
+        allocated), carried state (part of the pool)"""
+        v = np.zeros(4, dtype=np.uint64)
+        check(load().fhe_ssm_decoder_memory(self.h, v.ctypes.data, 4))
+        return {"plaintext_store": int(v[0]), "diagonal_buffer": int(v[1]), "ciphertext_pool": int(v[2]),
+                "carried_state": int(v[3])}
 
     def serve(self, directory: str, timeout_sec: int = 3600, stateful: bool = True, log_fd: int = -1,
               poll_ms: int = 200, first_req: int = 0) -> dict:

@@ -194,6 +194,17 @@ int ckks_linear_transform_bsgs(ckks_context* ctx, const uint64_t* d_ct, uint32_t
  *                           [batch][2][l_t][N]; at most 8 terms. */
 int ckks_encode_periodic(ckks_context* ctx, const double* re, const double* im, uint32_t n_vectors, uint32_t period,
                          uint32_t level, double scale, uint64_t* d_out);
+/* ckks_encode_periodic in two halves, so that a store of plaintexts can be kept in a level-independent form of
+ * 2 period words per vector and expanded to its limbs when it is applied (the reference keeps its compressed store
+ * on the host and streams it into a device pool, gpu_real_model.cu:1660-1706,3085-3285):
+ * ckks_encode_periodic_coeffs  the host half: special FFT, rounding (with the approxFactor rule): d_coef
+ *                              [n][2 period] int64 and d_log_approx [n] int32, device memory
+ * ckks_expand_periodic         the device half, enqueued on stream: d_out [n][level][2 period], the words
+ *                              ckks_encode_periodic writes */
+int ckks_encode_periodic_coeffs(ckks_context* ctx, const double* re, const double* im, uint32_t n_vectors,
+                                uint32_t period, double scale, int64_t* d_coef, int32_t* d_log_approx);
+int ckks_expand_periodic(ckks_context* ctx, const int64_t* d_coef, const int32_t* d_log_approx, uint32_t n_vectors,
+                         uint32_t period, uint32_t level, uint64_t* d_out, void* stream);
 int ckks_eval_mult_plain_ex(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level,
                             const uint64_t* d_pt, int pt_shared, uint32_t log_rep, uint64_t* d_out, void* stream);
 int ckks_linear_transform_general(ckks_context* ctx, const uint64_t* d_ct, uint32_t level, const uint64_t* d_diags,
@@ -355,6 +366,11 @@ int ckks_decrypt_coeffs(ckks_context* ctx, const ckks_secret* sk, const uint64_t
  * Waits for the recorded events. */
 /* ckks_context_counters: key switches issued since the last reset (one per ciphertext key-switched) */
 int ckks_context_counters(ckks_context* ctx, uint64_t* key_switches, int reset);
+/* ckks_context_memory: device bytes the context holds itself (no counterpart in the reference; for memory
+ * accounting): bytes[0] constant tables (twiddles, small-ring tables, prime data), bytes[1] the growable
+ * key-switching workspaces, bytes[2] the bootstrapping buffer pool (free buffers kept for the next call).
+ * Fills min(n, 3) entries. */
+int ckks_context_memory(const ckks_context* ctx, uint64_t* bytes, uint32_t n);
 int ckks_profile_enable(ckks_context* ctx, int on);
 int ckks_profile_reset(ckks_context* ctx);
 int ckks_profile_query(ckks_context* ctx, uint32_t idx, char* name, uint32_t name_cap, uint64_t* launches,

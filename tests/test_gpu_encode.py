@@ -133,3 +133,25 @@ def test_encode_refuses_too_small_scale(ckks, ctx5):
     comp = ckks.DeviceBuffer(4 * 2048 * 8)
     with pytest.raises(ckks.CkksError):
         ctx5.encode_periodic(np.full((1, 1024), 1e-3), 4, 1.0, comp.ptr)
+
+
+@pytest.mark.parametrize("period,scale", [(1024, 2.0**40), (2048, 2.0**52), (1024, 2.0**72)])
+def test_coefficient_store_expands_to_the_encoder_words(ckks, ctx5, period, scale):
+    """ckks_encode_periodic_coeffs + ckks_expand_periodic (a plaintext store kept as 2 period int64 per vector,
+    expanded when applied) == ckks_encode_periodic word for word, at several levels from one coefficient set,
+    including a scale that needs approxFactor (2^72)"""
+    rng = np.random.default_rng(period + int(np.log2(scale)))
+    n_vec = 5
+    z = rng.uniform(-1, 1, (n_vec, period))
+    Np = 2 * period
+    dc = ckks.DeviceBuffer(n_vec * Np * 8)
+    dl = ckks.DeviceBuffer(n_vec * 4)
+    ctx5.encode_periodic_coeffs(z, scale, dc.ptr, dl.ptr)
+    la = dl.download((n_vec,), np.int32)
+    assert np.all(la == 0) == (scale < 2.0**60), la
+    for l in (3, 17, 32):
+        want = ckks.DeviceBuffer(n_vec * l * Np * 8)
+        ctx5.encode_periodic(z, l, scale, want.ptr)
+        got = ckks.DeviceBuffer(n_vec * l * Np * 8)
+        ctx5.expand_periodic(dc.ptr, dl.ptr, n_vec, period, l, got.ptr)
+        assert np.array_equal(got.download((n_vec, l, Np)), want.download((n_vec, l, Np))), l
