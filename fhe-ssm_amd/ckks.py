@@ -83,6 +83,7 @@ SIGNATURES = {
     "ckks_eval_mul_i": (_int, [_vp, _vp, _u32, _u32, _int, _vp, _vp]),
     "ckks_eval_lincomb": (_int, [_vp, _u32, _u32, _vp, _vp, _vp, _vp, ctypes.c_double, ctypes.c_double, _u32, _int,
                                  _vp, _vp]),
+    "ckks_bootstrap_setup_shared": (_int, [_vp, _vp, ctypes.c_double, ctypes.POINTER(_vp)]),
     "ckks_bootstrap_setup": (_int, [_vp, ctypes.c_double, _u32, _u32, ctypes.c_double, ctypes.c_double,
                                     ctypes.POINTER(_vp)]),
     "ckks_bootstrap_destroy": (None, [_vp]),
@@ -570,10 +571,15 @@ class Bootstrap:
     """EvalBootstrapSetup: plan (CtS/StC diagonals, Chebyshev coefficients) resident on the device."""
 
     def __init__(self, ctx: Context, K: float = 22.0, cheb_degree: int = 59, double_angles: int = 2,
-                 top_scale: float = 2.0**50, in_scale: float = 2.0**50):
+                 top_scale: float = 2.0**50, in_scale: float = 2.0**50, share=None):
+        """share: another Bootstrap of this context whose diagonals this plan uses (its in_scale an integer
+        multiple of this one's; K, degree, double angles and top scale are then the other plan's)"""
         h = _vp()
-        check(load().ckks_bootstrap_setup(ctx.h, K, cheb_degree, double_angles, top_scale, in_scale,
-                                          ctypes.byref(h)))
+        if share is not None:
+            check(load().ckks_bootstrap_setup_shared(ctx.h, share.h, in_scale, ctypes.byref(h)))
+        else:
+            check(load().ckks_bootstrap_setup(ctx.h, K, cheb_degree, double_angles, top_scale, in_scale,
+                                              ctypes.byref(h)))
         self.h = h.value
         self.ctx = ctx
         n = _u32()

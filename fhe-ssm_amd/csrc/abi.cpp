@@ -859,6 +859,23 @@ int ckks_bootstrap_setup(ckks_context* ctx, double K, uint32_t cheb_degree, uint
     });
 }
 
+int ckks_bootstrap_setup_shared(ckks_context* ctx, const ckks_bootstrap* base, double in_scale, ckks_bootstrap** out) {
+    if (!ctx || !base || !out) return fail(CKKS_EINVAL, "null argument");
+    if (base->owner != ctx) return fail(CKKS_EINVAL, "the base plan belongs to another context");
+    if (!(in_scale > 0)) return fail(CKKS_EINVAL, "bad bootstrap parameters");
+    return guarded([&] {
+        auto* bt = new ckks_bootstrap{nullptr, ctx};
+        try {
+            bt->p = fhe::bootstrap_plan_shared(*base->p, in_scale);
+        } catch (...) {
+            delete bt;
+            throw;
+        }
+        *out = bt;
+        return CKKS_OK;
+    });
+}
+
 void ckks_bootstrap_destroy(ckks_bootstrap* bt) {
     if (!bt) return;
     fhe::bootstrap_plan_destroy(bt->p);

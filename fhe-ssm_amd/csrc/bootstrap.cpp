@@ -141,6 +141,14 @@ uint64_t mod_signed(long double v, uint64_t q) {
 }  // namespace
 
 // ------------------------------------------------------------------ plan
+// the device diagonals of a plan's levels, freed with the last plan that shares them
+struct DiagStore {
+    std::vector<uint64_t*> d;
+    ~DiagStore() {
+        for (auto* p : d) (void)hipFree(p);
+    }
+};
+
 BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scale, double in_scale) {
     if (ctx.K == 0) throw std::invalid_argument("bootstrapping needs special primes");
     if (deg < 8 || deg > 63) throw std::invalid_argument("Chebyshev degree must be in [8, 63]");
@@ -272,6 +280,11 @@ BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scal
         bootstrap_plan_destroy(P);
         throw;
     }
+    // the diagonals' owner: frees them when the last plan sharing them goes
+    auto store = std::make_shared<DiagStore>();
+    for (auto* lv : {&P->cts, &P->stc})
+        for (auto& bl : *lv) store->d.push_back(bl.d_diags);
+    P->diags_owner = store;
     std::map<int64_t, int> seen;
     for (auto* lv : {&P->cts, &P->stc})
         for (auto& bl : *lv) {
@@ -284,10 +297,21 @@ BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scal
     return P;
 }
 
+BootPlan* bootstrap_plan_shared(const BootPlan& base, double in_scale) {
+    const double f = base.in_scale / in_scale;
+    if (!(f >= 1.0) || f > 1e15 || f != std::floor(f))
+        throw std::invalid_argument("a shared plan's input scale must divide the base plan's by an integer");
+    auto* P = new BootPlan(base);  // the level descriptors, scales and coefficients; the diagonals are shared
+    P->in_scale = in_scale;
+    P->stc_factor = base.stc_factor * (uint64_t)f;
+    return P;
+}
+
 void bootstrap_plan_destroy(BootPlan* P) {
     if (!P) return;
-    for (auto* lv : {&P->cts, &P->stc})
-        for (auto& bl : *lv) (void)hipFree(bl.d_diags);
+    if (!P->diags_owner)  // a plan whose construction failed before its diagonals were handed to an owner
+        for (auto* lv : {&P->cts, &P->stc})
+            for (auto& bl : *lv) (void)hipFree(bl.d_diags);
     delete P;
 }
 
@@ -590,20 +614,22 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint3
         ev1.put(cj);
         ev1.put(x);
     }
-    // Re[b] + i Im[b] over the batch (pair holds the Re block then the Im block)
-    auto recombine = [&](const HCt& re_im, uint32_t l) {
+    // f (Re[b] + i Im[b]) over the batch (pair holds the Re block then the Im block), f a small integer
+    auto recombine = [&](const HCt& re_im, uint32_t l, uint64_t f) {
         const size_t half = (size_t)B * 2 * l * W;
         HCt im = ev1.get(l), z = ev1.get(l);
         HIPB(launch_mul_i(ctx, re_im.d + half, im.d, 2 * B, l, 1, st));
         const uint64_t* xs[2] = {re_im.d, im.d};
         const uint32_t strides[2] = {l, l};
-        std::vector<uint64_t> C(2 * l, 1);
+        std::vector<uint64_t> C(2 * l);
+        for (uint32_t t = 0; t < 2; t++)
+            for (uint32_t i = 0; i < l; i++) C[(size_t)t * l + i] = f % ctx.moduli[i];
         HIPB(launch_lincomb(ctx, z.d, B, l, 2, xs, strides, C.data(), nullptr, st));
         ev1.put(im);
         return z;
     };
     if (stop_stage == 2) {  // the CoeffToSlot output itself: Re + i Im
-        HCt z = recombine(pair, lm);
+        HCt z = recombine(pair, lm, 1);
         return emit(z.d, B, lm);
     }
     if (stop_stage == 3) return emit(pair.d, 2 * B, pair.l);
@@ -622,7 +648,7 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint3
     const uint32_t ls = P.stc[0].l;
     HCt ya = y.l == ls ? y : ev2.adjust(y, ls);
     if (ya.d != y.d) ev2.put(y);
-    HCt z = recombine(ya, ls);
+    HCt z = recombine(ya, ls, P.stc_factor);  // a shared plan's SlotToCoeff constant times its integer factor
     ev2.put(ya);
     if (stop_stage == 5) return emit(z.d, B, z.l);
     // ---- SlotToCoeff

@@ -2,6 +2,7 @@
 #pragma once
 #include <stdint.h>
 
+#include <memory>
 #include <vector>
 
 #include "engine.hpp"
@@ -30,9 +31,17 @@ struct BootPlan {
     // sparse-secret encapsulation (not owned): keys s -> s' (sparse, on q0 and P) and s' -> s
     const uint64_t* sse_to = nullptr;
     const uint64_t* sse_from = nullptr;
+    // the CoeffToSlot / SlotToCoeff diagonals are shared by the plans made from one (bootstrap_plan_shared): the
+    // last holder frees them
+    std::shared_ptr<void> diags_owner;
+    // integer factor applied to EvalMod's output in the recombination before SlotToCoeff: a plan made for a
+    // smaller input scale reuses another's SlotToCoeff diagonals (whose constant is q0 / (2 pi in_scale))
+    uint64_t stc_factor = 1;
 };
 
 BootPlan* bootstrap_plan(Context& ctx, double K, int deg, int r, double top_scale, double in_scale);
+// a plan for input scale in_scale sharing every diagonal of base: base.in_scale / in_scale must be an integer
+BootPlan* bootstrap_plan_shared(const BootPlan& base, double in_scale);
 void bootstrap_plan_destroy(BootPlan* P);
 uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint32_t B, const uint64_t* relin,
                    const uint64_t* conj_evk, const int64_t* steps, const uint64_t* const* evks, uint32_t n_keys,

@@ -553,14 +553,12 @@ def build_engine(ckks, secret_seed=b"S" * 32, n_keys_seed=7, steps=None, cheb_de
     # only in the input scale: the state and the channel-mix increment (|f| <= ~0.6)
     # enter at q0 (m/q0 stays ~1e-3 per coefficient), the time-mix increment (|o| <= ~0.05) at 8 q0: more signal
     # over EvalMod's noise.
-    plans = {}
-    for kind, ins in (("state", 2.0**50), ("inc_cm", 2.0**50), ("inc_tm", 2.0**53)):
-        if ins not in [v[1] for v in plans.values()]:
-            b = ckks.Bootstrap(ctx, K=14.0, cheb_degree=cheb_degree, double_angles=double_angles,
-                               top_scale=2.0**52, in_scale=ins)
-        else:
-            b = next(v[0] for v in plans.values() if v[1] == ins)
-        plans[kind] = (b, ins)
+    # The two input scales share one set of CoeffToSlot / SlotToCoeff diagonals (~9 GB each): the 2^50 plan is the
+    # 2^53 plan with EvalMod's output multiplied by 8 before SlotToCoeff.
+    base = ckks.Bootstrap(ctx, K=14.0, cheb_degree=cheb_degree, double_angles=double_angles, top_scale=2.0**52,
+                          in_scale=2.0**53)
+    low = ckks.Bootstrap(ctx, in_scale=2.0**50, share=base)
+    plans = {"state": (low, 2.0**50), "inc_cm": (low, 2.0**50), "inc_tm": (base, 2.0**53)}
     sk = ctx.secret(secret_seed, 192)
     sk_sparse = ctx.secret(bytes(reversed(secret_seed)), 32)
     kb = ctx.dnum * 2 * (ctx.L + ctx.K) * ctx.N * 8

@@ -262,6 +262,13 @@ int ckks_gen_primes(uint32_t bits, uint32_t count, const uint64_t* skip, uint32_
 int ckks_bootstrap_setup(ckks_context* ctx, double K, uint32_t cheb_degree, uint32_t double_angles, double top_scale,
                          double in_scale, ckks_bootstrap** out);
 void ckks_bootstrap_destroy(ckks_bootstrap* bt);
+/* ckks_bootstrap_setup_shared: a plan for inputs of scale in_scale that shares every CoeffToSlot / SlotToCoeff
+ * diagonal of base (no counterpart in the reference, whose EvalBootstrapSetup makes one plan per context; for a
+ * caller that bootstraps inputs of several scales).  base's input scale / in_scale must be an integer f >= 1:
+ * EvalMod's output is multiplied by f in the recombination before SlotToCoeff, which is what base's SlotToCoeff
+ * constant q0 / (2 pi in_scale) would have applied.  Either plan may be destroyed first.  Sparse-secret keys are
+ * copied from base at this call (set them on base first, or on the shared plan after). */
+int ckks_bootstrap_setup_shared(ckks_context* ctx, const ckks_bootstrap* base, double in_scale, ckks_bootstrap** out);
 /* ckks_bootstrap_set_sparse_keys: sparse-secret encapsulation (Bossuat, Troncoso-Pastoriza, Hubaux, ePrint
  * 2022/024): the level-1 input is switched to a sparse secret s' (key s -> s', q_limbs = 1) before ModRaise and
  * the raised ciphertext back to s (key s' -> s), so that |I| is bounded by the sparse weight: K drops from

@@ -162,3 +162,46 @@ def test_bootstrap_stagewise(ckks, oracle, chain):
             err = np.max(np.abs(got - want))
             print(f"stage {st_} part {b} level {lvl}: max err {err:.3e} (max |want| {np.max(np.abs(want)):.3e})")
             assert err < 1e-3 * max(1.0, np.max(np.abs(want))), (st_, b, err)
+
+
+@pytest.mark.timeout(900)
+def test_shared_plan_matches_a_plan_of_its_own(ckks):
+    """a plan sharing another's diagonals (ckks_bootstrap_setup_shared, input scale 8x smaller: EvalMod's output
+    times 8 before SlotToCoeff) bootstraps to the same message as a plan built for that input scale, to their own
+    precision; destroying the base plan first leaves the shared one working"""
+    make, K, deg, r, top, ins = CHAINS["config4"]
+    ctx = make(ckks)
+    L, Kp, D = ctx.L, ctx.K, ctx.dnum
+    base = ckks.Bootstrap(ctx, K=K, cheb_degree=deg, double_angles=r, top_scale=top, in_scale=ins * 8)
+    shared = ckks.Bootstrap(ctx, in_scale=ins, share=base)
+    own = ckks.Bootstrap(ctx, K=K, cheb_degree=deg, double_angles=r, top_scale=top, in_scale=ins)
+    assert shared.steps == own.steps and shared.out_level == own.out_level
+    with pytest.raises(ckks.CkksError):
+        ckks.Bootstrap(ctx, in_scale=ins * 3, share=shared)   # 8 ins / (3 ins) is not an integer
+    sk = ctx.secret(b"Q" * 32, 192)
+    kb = D * 2 * (L + Kp) * N * 8
+    relin = ckks.DeviceBuffer(kb)
+    ctx.keygen_relin(sk, b"r" * 32, b"s" * 32, relin.ptr)
+    conj = ckks.DeviceBuffer(kb)
+    ctx.keygen_automorphism(sk, 2 * N - 1, b"c" * 32, b"d" * 32, conj.ptr)
+    keys, bufs = {}, []
+    for i, s in enumerate(own.steps):
+        b = ckks.DeviceBuffer(kb)
+        ctx.keygen_automorphism(sk, ckks.rotation_index(s), bytes([9, i % 256]) * 16, bytes([10, i % 256]) * 16, b.ptr)
+        keys[s] = b.ptr
+        bufs.append(b)
+    rng = np.random.default_rng(46)
+    z = rng.uniform(-1.0, 1.0, SLOTS)
+    pt = ckks.DeviceBuffer(N * 8)
+    ct = ckks.DeviceBuffer(2 * N * 8)
+    ctx.encode(z, 1, ins, pt.ptr)
+    ctx.encrypt(sk, pt.ptr, 1, b"g" * 32, 0, ct.ptr)
+    base.close()
+    outs = {}
+    for name, bt in (("shared", shared), ("own", own)):
+        out = ckks.DeviceBuffer(2 * bt.out_level * N * 8)
+        bt.run(ct.ptr, relin.ptr, conj.ptr, keys, out.ptr)
+        outs[name] = ctx.decrypt(sk, out.ptr, bt.out_level, bt.scale(bt.out_level), SLOTS, complex_out=True)
+        bits = -np.log2(np.max(np.abs(outs[name] - z)))
+        print(f"{name} plan: {bits:.2f} bits")
+        assert bits > 14.0, (name, bits)
