@@ -494,6 +494,12 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native
     rep = ctx.profile_report()
     ctx.profile_reset()
     s_per_step = sum(times) / len(times)
+    free_b2, _ = torch.cuda.mem_get_info()
+    mem = {"device_gb_after_timed_steps": round((total_b - free_b2) / 1e9, 1)}
+    if driver == "native":
+        mem["decoder_gb"] = {k: round(v / 1e9, 2) for k, v in nat.memory().items()}
+    mem["context_gb"] = {k: round(v / 1e9, 2) for k, v in ctx.memory().items()}
+    mem["keys_gb"] = round((len(be.keys) + 4) * ctx.dnum * 2 * (ctx.L + ctx.K) * N * 8 / 1e9, 1)
     serve = None
     if serve_requests and driver == "native":
         serve = bench_serve(torch, be, nat, client_in, warmup + steps_n + 1, serve_requests, log)
@@ -502,7 +508,7 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native
     return {"s_per_step": round(s_per_step, 3), "serve": serve, "key_switches_per_step": int(np.mean(ks)),
             "bootstraps_per_step": n_boot() // (warmup + steps_n + 1), "driver": driver,
             "setup_s": {"keys": round(t_keys, 1), "first_steps_with_plaintext_encoding": round(t_warm, 1)},
-            "device_memory_in_use_gb_after_warmup": round((total_b - free_b) / 1e9, 1),
+            "device_memory_in_use_gb_after_warmup": round((total_b - free_b) / 1e9, 1), "memory": mem,
             "client_s": {"decrypt_and_vocab_head": round(t_client, 3)},
             "kernels": kernel_table(rep), "roofline": roofline_from_profile(rep),
             "_check": {"xs": xs, "outs": outs, "logits": logits, "logits_step": warmup + steps_n - 1, "W": W,
@@ -715,7 +721,7 @@ def main():
             line = {"s_per_step": d["s_per_step"], "metric": "s/step for 32-lane decode (config 5)",
                     "roofline": d["roofline"]}
             line.update({k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s",
-                                           "device_memory_in_use_gb_after_warmup", "driver")})
+                                           "device_memory_in_use_gb_after_warmup", "memory", "driver")})
             if not args.no_cpu_baseline:
                 line["cpu_baseline"], acc = cpu_baseline_decode(d, args.seed)
                 line.update(acc)
@@ -730,7 +736,7 @@ def main():
                "config": {"workload": d["workload"], "lanes": DECODE_LANES, "layers": args.layers},
                "kernels": d["kernels"], "roofline": d["roofline"],
                "check": {k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s",
-                                           "device_memory_in_use_gb_after_warmup", "driver")}}
+                                           "device_memory_in_use_gb_after_warmup", "memory", "driver")}}
         if d["serve"]:
             res["check"]["serve"] = d["serve"]
         extra = {}

@@ -106,6 +106,11 @@ SIGNATURES = {
                                  ctypes.POINTER(ctypes.c_double)]),
     "ckks_ct_save": (_int, [_vp, ctypes.c_char_p, _vp, _u32, ctypes.c_double]),
     "ckks_ct_load": (_int, [_vp, ctypes.c_char_p, _u32, _vp, ctypes.POINTER(_u32), ctypes.POINTER(ctypes.c_double)]),
+    "ckks_host_alloc": (_int, [ctypes.c_size_t, ctypes.POINTER(_vp)]),
+    "ckks_host_free": (_int, [_vp]),
+    "ckks_side_copy": (_int, [_vp, _vp, _vp, ctypes.c_size_t, _vp, ctypes.POINTER(ctypes.c_uint64)]),
+    "ckks_side_wait": (_int, [_vp, ctypes.c_uint64, _vp]),
+    "ckks_side_sync": (_int, [_vp]),
     "ckks_encode_periodic_coeffs": (_int, [_vp, _vp, _vp, _u32, _u32, ctypes.c_double, _vp, _vp]),
     "ckks_expand_periodic": (_int, [_vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp]),
     "ckks_encode": (_int, [_vp, _vp, _vp, _u32, _u32, ctypes.c_double, _vp]),

@@ -204,6 +204,59 @@ int ckks_memcpy_h2d(void* d_dst, const void* h_src, size_t bytes) {
     return CKKS_OK;
 }
 
+int ckks_host_alloc(size_t bytes, void** h_out) {
+    if (!h_out) return fail(CKKS_EINVAL, "null argument");
+    *h_out = nullptr;
+    HIP_TRY(hipHostMalloc(h_out, bytes ? bytes : 1, hipHostMallocDefault));
+    return CKKS_OK;
+}
+
+int ckks_host_free(void* h) {
+    if (h) HIP_TRY(hipHostFree(h));
+    return CKKS_OK;
+}
+
+int ckks_side_copy(ckks_context* ctx, void* dst, const void* src, size_t bytes, void* stream, uint64_t* ticket) {
+    if (!ctx || !dst || !src || !ticket) return fail(CKKS_EINVAL, "null argument");
+    fhe::Context& c = ctx->c;
+    if (!c.side) HIP_TRY(hipStreamCreateWithFlags(&c.side, hipStreamNonBlocking));
+    // after the work enqueued so far on stream
+    hipEvent_t after = nullptr, done = nullptr;
+    HIP_TRY(hipEventCreateWithFlags(&after, hipEventDisableTiming));
+    hipError_t e = hipEventRecord(after, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(c.side, after, 0);
+    if (e == hipSuccess) e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, c.side);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(done, c.side);
+    c.side_after.push_back(after);  // destroyed at the next ckks_side_sync, once the side stream has drained
+    if (e != hipSuccess) {
+        if (done) (void)hipEventDestroy(done);
+        return fail(CKKS_EHIP, std::string("side copy: ") + hipGetErrorString(e));
+    }
+    *ticket = ++c.side_next;
+    c.side_ev[*ticket] = done;
+    return CKKS_OK;
+}
+
+int ckks_side_wait(ckks_context* ctx, uint64_t ticket, void* stream) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    auto it = ctx->c.side_ev.find(ticket);
+    if (it == ctx->c.side_ev.end()) return CKKS_OK;  // already synchronized (ckks_side_sync)
+    HIP_TRY(hipStreamWaitEvent((hipStream_t)stream, it->second, 0));
+    return CKKS_OK;
+}
+
+int ckks_side_sync(ckks_context* ctx) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    fhe::Context& c = ctx->c;
+    if (c.side) HIP_TRY(hipStreamSynchronize(c.side));
+    for (auto& kv : c.side_ev) (void)hipEventDestroy(kv.second);
+    c.side_ev.clear();
+    for (auto ev : c.side_after) (void)hipEventDestroy(ev);
+    c.side_after.clear();
+    return CKKS_OK;
+}
+
 int ckks_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes) {
     HIP_TRY(hipMemcpy(h_dst, d_src, bytes, hipMemcpyDeviceToHost));
     return CKKS_OK;

@@ -433,7 +433,7 @@ static void check_period(uint32_t P) {
 // so only N' words per limb are stored.  The special FFT and rounding run on the host (over threads): their result,
 // the small polynomial's integer coefficients (and each vector's approxFactor exponent), is independent of the
 // level and N' words per vector in all; the residues and the N'-point NTTs of any number of limbs follow on the GPU.
-// d_coef [n_vec][N'] int64, d_log_approx [n_vec] int32 (device memory).
+// d_coef [n_vec][N'] int64, d_log_approx [n_vec] int32 (device memory, or pinned host memory).
 void encode_periodic_coeffs(Context& ctx, const double* re, const double* im, uint32_t n_vec, uint32_t P,
                             double scale, int64_t* d_coef, int32_t* d_log_approx) {
     (void)ctx;
@@ -453,8 +453,9 @@ void encode_periodic_coeffs(Context& ctx, const double* re, const double* im, ui
     });
     for (const auto& e : errs)
         if (!e.empty()) throw std::invalid_argument(e);
-    HIPC(hipMemcpy(d_coef, coef.data(), coef.size() * 8, hipMemcpyHostToDevice));
-    HIPC(hipMemcpy(d_log_approx, log_approx.data(), log_approx.size() * 4, hipMemcpyHostToDevice));
+    // device or pinned host destinations
+    HIPC(hipMemcpy(d_coef, coef.data(), coef.size() * 8, hipMemcpyDefault));
+    HIPC(hipMemcpy(d_log_approx, log_approx.data(), log_approx.size() * 4, hipMemcpyDefault));
 }
 
 // the device half: coefficients -> [n_vec][l][N'] evaluation-form limbs, enqueued on st

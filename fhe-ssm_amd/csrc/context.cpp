@@ -227,6 +227,13 @@ void context_release(Context& c) {
     for (auto& e : c.ring_ev)
         if (e) (void)hipEventDestroy(e);
     c.ring_host = c.ring_dev = nullptr;
+    if (c.side) (void)hipStreamSynchronize(c.side);
+    for (auto& kv : c.side_ev) (void)hipEventDestroy(kv.second);
+    c.side_ev.clear();
+    for (auto ev : c.side_after) (void)hipEventDestroy(ev);
+    c.side_after.clear();
+    if (c.side) (void)hipStreamDestroy(c.side);
+    c.side = nullptr;
     c.job_cache.clear();
     c.bconv_cache.clear();
     c.scratch.clear();

@@ -117,6 +117,12 @@ struct Context {
     hipEvent_t ring_ev[kRingSlots] = {};
     bool ring_used[kRingSlots] = {};
     uint32_t ring_next = 0;
+    // side stream for copies that overlap the work (created on first use, non-blocking, default priority) and the
+    // events of the copies issued on it, by ticket
+    hipStream_t side = nullptr;
+    uint64_t side_next = 0;
+    std::map<uint64_t, hipEvent_t> side_ev;
+    std::vector<hipEvent_t> side_after;  // the events the side copies waited on
     // per-launch profiling (off by default)
     bool prof_on = false;
     mutable std::vector<ProfRec> prof;

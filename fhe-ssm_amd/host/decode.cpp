@@ -41,9 +41,10 @@ constexpr uint32_t LOG_REP = 5;  // 1024-periodic plaintexts: N / 2^5 words per 
 // output), else 32
 constexpr int MV_SPAN = 1536;
 int mv_nb(size_t n_in, size_t n_out) { return n_out >= n_in ? 64 : 32; }
-// ciphertexts per batched bootstrap: its buffer pool and workspaces grow with it (24 state ciphertexts in passes
-// of 8 instead of 12 took 7 GB off the config-5 step's device memory at no measurable cost in time)
-constexpr uint32_t kBootBatch = 8;
+// ciphertexts per batched bootstrap: its buffer pool and workspaces grow with it (the config-5 step's 24 state
+// ciphertexts in passes of 8 instead of 12: -7 GB of device memory at no measurable cost in time; of 6: -3 GB more
+// for +1% of the step)
+constexpr uint32_t kBootBatch = 6;
 
 thread_local std::string g_err;
 
@@ -112,11 +113,22 @@ struct Ct {
 
 using Pair = std::tuple<const Ct*, uint32_t, const Ct*, uint32_t>;  // (a, item of a, b, item of b)
 
-// A matvec's 1024-periodic diagonals, stored as their small-ring integer coefficients (2048 int64 per diagonal
-// and one int32 approxFactor exponent, whatever the level: ~1/level of the expanded plaintexts) and expanded to
-// the level's limbs each time the matvec is applied.
+// pinned host memory, freed on scope exit
+struct HostBuf {
+    void* p = nullptr;
+    size_t bytes = 0;
+    explicit HostBuf(size_t b) : bytes(b) { ck(ckks_host_alloc(b, &p), "ckks_host_alloc"); }
+    ~HostBuf() { (void)ckks_host_free(p); }
+    HostBuf(const HostBuf&) = delete;
+    HostBuf& operator=(const HostBuf&) = delete;
+};
+
+// A matvec's 1024-periodic diagonals, stored in pinned host memory as their small-ring integer coefficients
+// (2048 int64 per diagonal and one int32 approxFactor exponent, whatever the level: ~1/level of the expanded
+// plaintexts) and expanded to the level's limbs each time the matvec is applied (the reference likewise keeps its
+// compressed store on the host and streams it to the device, gpu_real_model.cu:1660-1706,3085-3285).
 struct Matvec {
-    std::shared_ptr<Buf> coef;  // [n_diag][2 DPAD] int64, then [n_diag] int32
+    std::shared_ptr<HostBuf> coef;  // [n_diag][2 DPAD] int64, then [n_diag] int32
     uint32_t n_diag = 0, level = 0;
     uint32_t n_out = 0, n_in = 0, nb = 0;
 };
@@ -361,9 +373,25 @@ class Engine {
         return out;
     }
 
-    // a matvec's diagonals expanded to its level's limbs in one buffer shared by every matvec (grown to the
-    // largest): the work is stream-ordered, so the previous matvec has read it before the next expansion writes
+    // A matvec's diagonals expanded to its level's limbs in one buffer shared by every matvec (grown to the
+    // largest): the work is stream-ordered, so the previous matvec has read it before the next expansion writes.
+    // The coefficients come from one of two device staging buffers: the matvecs of a step run in the same order
+    // every step, so while one is applied the next one's coefficients are copied from the host into the other
+    // buffer on the engine's side stream (the copy starts once the work already enqueued -- this expansion and
+    // every earlier read of that buffer -- is done).
+    void begin_step() { mv_pos_ = 0; }
+
     const uint64_t* expand(const Matvec& h) {
+        if (mv_pos_ < mv_order_.size() && mv_order_[mv_pos_] != &h) mv_order_.resize(mv_pos_);  // another order
+        if (mv_pos_ == mv_order_.size()) mv_order_.push_back(&h);
+        mv_pos_++;
+        // this matvec's coefficients on the device: prefetched, or copied now
+        int s = stage_[0].holds == &h ? 0 : stage_[1].holds == &h ? 1 : -1;
+        if (s < 0) {
+            s = stage_[0].holds ? 1 : 0;
+            stage_in(s, h);
+        }
+        ck(ckks_side_wait(ctx_, stage_[s].ticket, nullptr), "ckks_side_wait");
         const size_t bytes = (size_t)h.n_diag * h.level * (kN >> LOG_REP) * 8;
         if (!diag_ || diag_->bytes < bytes) {
             diag_.reset();
@@ -371,11 +399,34 @@ class Engine {
             ck(ckks_buffer_alloc(bytes, &p), "ckks_buffer_alloc");
             diag_ = std::make_shared<Buf>((uint64_t*)p, bytes, nullptr);
         }
-        const int64_t* c = reinterpret_cast<const int64_t*>(h.coef->d);
+        const int64_t* c = reinterpret_cast<const int64_t*>(stage_[s].buf->d);
         const int32_t* la = reinterpret_cast<const int32_t*>(c + (size_t)h.n_diag * (kN >> LOG_REP));
         ck(ckks_expand_periodic(ctx_, c, la, h.n_diag, DPAD, h.level, diag_->d, nullptr), "ckks_expand_periodic");
+        stage_[s].holds = nullptr;  // consumed: the buffer may take the matvec after next
+        // the next matvec of the recorded order (the first one of the next step after the last)
+        if (mv_order_.size() > 1) {
+            const Matvec* nx = mv_order_[mv_pos_ < mv_order_.size() ? mv_pos_ : 0];
+            if (nx != &h) stage_in(1 - s, *nx);
+        }
         return diag_->d;
     }
+
+   private:
+    // copy h's coefficients into staging buffer s on the side stream
+    void stage_in(int s, const Matvec& h) {
+        auto& st = stage_[s];
+        if (!st.buf || st.buf->bytes < h.coef->bytes) {
+            if (st.buf) ck(ckks_side_sync(ctx_), "ckks_side_sync");  // no copy may still write the old buffer
+            st.buf.reset();
+            void* p = nullptr;
+            ck(ckks_buffer_alloc(h.coef->bytes, &p), "ckks_buffer_alloc");
+            st.buf = std::make_shared<Buf>((uint64_t*)p, h.coef->bytes, nullptr);
+        }
+        ck(ckks_side_copy(ctx_, st.buf->d, h.coef->p, h.coef->bytes, nullptr, &st.ticket), "ckks_side_copy");
+        st.holds = &h;
+    }
+
+   public:
 
     Ct mul_i(const Ct& a, int sign) {
         Ct out = fresh(a.B, a.level, a.scale);
@@ -407,14 +458,13 @@ class Engine {
     }
 
     // -- plaintexts -----------------------------------------------------------------------------------
-    // the coefficient form of 1024-periodic vectors at level's scale: [n][2 DPAD] int64, then [n] int32
-    std::shared_ptr<Buf> encode_coeffs(const std::vector<double>& vecs, uint32_t level, uint32_t* n_out) {
+    // the coefficient form of 1024-periodic vectors at level's scale, in pinned host memory: [n][2 DPAD] int64,
+    // then [n] int32
+    std::shared_ptr<HostBuf> encode_coeffs(const std::vector<double>& vecs, uint32_t level, uint32_t* n_out) {
         const uint32_t n = (uint32_t)(vecs.size() / DPAD);
         const size_t per = (size_t)(kN >> LOG_REP) * 8;
-        void* p = nullptr;
-        ck(ckks_buffer_alloc(n * (per + 4), &p), "ckks_buffer_alloc");
-        auto buf = std::make_shared<Buf>((uint64_t*)p, n * (per + 4), nullptr);
-        int64_t* c = (int64_t*)p;
+        auto buf = std::make_shared<HostBuf>(n * (per + 4));
+        int64_t* c = (int64_t*)buf->p;
         int32_t* la = (int32_t*)(c + (size_t)n * (kN >> LOG_REP));
         for (uint32_t s = 0; s < n; s += 4096) {  // in chunks (bounds the encoder's host staging)
             const uint32_t m = std::min<uint32_t>(4096, n - s);
@@ -491,10 +541,21 @@ class Engine {
     std::map<std::string, std::pair<std::vector<int64_t>, std::vector<const uint64_t*>>> boot_keys_;
     Pool pool_;
     std::shared_ptr<Buf> diag_;  // expanded matvec diagonals (see expand)
+    struct Stage {
+        std::shared_ptr<Buf> buf;
+        const Matvec* holds = nullptr;  // whose coefficients the buffer holds (or is receiving)
+        uint64_t ticket = 0;
+    } stage_[2];
+    std::vector<const Matvec*> mv_order_;  // the matvecs of a step, in order (recorded as they run)
+    size_t mv_pos_ = 0;
 
    public:
     size_t pool_bytes() const { return pool_.total(); }
-    size_t diag_bytes() const { return diag_ ? diag_->bytes : 0; }
+    size_t diag_bytes() const {
+        return (diag_ ? diag_->bytes : 0) + (stage_[0].buf ? stage_[0].buf->bytes : 0) +
+               (stage_[1].buf ? stage_[1].buf->bytes : 0);
+    }
+    std::shared_ptr<Buf> alloc(size_t bytes) { return std::make_shared<Buf>(pool_.get(bytes), bytes, &pool_); }
 };
 
 // ------------------------------------------------------------------ slot-layout tables
@@ -622,6 +683,14 @@ struct LayerState {
 class Decoder {
    public:
     Decoder(Engine* be, uint32_t n_layers) : be_(be), layers_(n_layers) {}
+    ~Decoder() {
+        (void)ckks_side_sync(be_->ctx());
+        for (auto& c : saved_.copies) (void)ckks_host_free(c.first);
+        for (auto& kv : host_free_)
+            for (void* p : kv.second) (void)ckks_host_free(p);
+    }
+    Decoder(const Decoder&) = delete;
+    Decoder& operator=(const Decoder&) = delete;
 
     void set_weight(const std::string& name, int32_t layer, const double* data, size_t count) {
         size_t want = 0;
@@ -642,32 +711,71 @@ class Decoder {
 
     // One step over the carried state.  The step works on a copy of the state (handles: the ciphertexts are shared,
     // never written in place) and commits it only once every layer has succeeded, so a step that throws leaves the
-    // state of the previous step untouched (the reference commits its carry after the whole pass,
-    // gpu_real_model.cu:5284-5286).
+    // state of the previous step in place (the reference commits its carry after the whole pass,
+    // gpu_real_model.cu:5284-5286).  The previous state is not kept on the device meanwhile: at the start of the
+    // step it is copied to pinned host memory on the engine's side stream (the copies overlap the first layer), and
+    // each layer's old state is released once its new state exists and its copy has landed; a step that throws
+    // puts the saved state back.  The device holds one state instead of two.
     Ct step(const Ct& x_in) {
-        std::vector<LayerState> work = state_.empty() ? cold_state() : state_;
-        Ct x = x_in;
-        for (uint32_t li = 0; li < layers_.size(); li++) {
-            LayerState& st = work[li];
-            x = be_->add(x, boot(time_mix(li, x, st), "inc_tm"));
-            refresh_state(st);
-            x = be_->add(x, boot(channel_mix(li, x, st), "inc_cm"));
+        const bool own = !saved_.active;  // a backup held by the caller (a multi-token request) is kept
+        if (own) backup();
+        be_->begin_step();
+        try {
+            std::vector<LayerState> work = state_.empty() ? cold_state() : state_;
+            Ct x = x_in;
+            for (uint32_t li = 0; li < layers_.size(); li++) {
+                LayerState& st = work[li];
+                x = be_->add(x, boot(time_mix(li, x, st), "inc_tm"));
+                refresh_state(st);
+                x = be_->add(x, boot(channel_mix(li, x, st), "inc_cm"));
+                release_layer(li);
+            }
+            Ct xo = norm(x, model_["p_o"]);
+            std::vector<double> go(DPAD, 0.0);
+            std::copy(model_["g_o"].begin(), model_["g_o"].end(), go.begin());
+            Ct out = be_->mul_pt(xo, *vec_pt("g_o", xo.level, [&] { return go; }));
+            state_ = std::move(work);
+            if (own) drop_backup();
+            reserve_backup();
+            return out;
+        } catch (...) {
+            if (own) {
+                restore_backup();
+                drop_backup();
+            }
+            throw;
         }
-        Ct xo = norm(x, model_["p_o"]);
-        std::vector<double> go(DPAD, 0.0);
-        std::copy(model_["g_o"].begin(), model_["g_o"].end(), go.begin());
-        Ct out = be_->mul_pt(xo, *vec_pt("g_o", xo.level, [&] { return go; }));
-        state_ = std::move(work);
-        return out;
+    }
+
+    // A backup the caller holds across several steps (a multi-token request is all or nothing): taken now, kept
+    // until release_held, put back by restore_held.
+    void hold_backup() {
+        if (saved_.active) drop_backup();
+        backup();
+    }
+    void restore_held() {
+        if (!saved_.active) return;
+        restore_backup();
+        drop_backup();
+    }
+    void release_held() {
+        if (saved_.active) drop_backup();
     }
 
     uint64_t bootstraps() const { return n_boot_; }
     // the next step starts cold (zero WKV state and token-shift carries), as the first one does
-    void reset() { state_.clear(); }
+    void reset() {
+        wait_backup();
+        state_.clear();
+    }
     // device bytes: the plaintext store, and the carried state (each buffer counted once)
-    size_t store_bytes() const {
+    size_t store_bytes() const {  // device: the elementwise plaintexts
         size_t b = 0;
         for (auto& kv : pt_) b += kv.second->bytes;
+        return b;
+    }
+    size_t store_host_bytes() const {  // pinned host: the matvec coefficients
+        size_t b = 0;
         for (auto& kv : mv_) b += kv.second.coef->bytes;
         return b;
     }
@@ -685,9 +793,12 @@ class Decoder {
         }
         return b;
     }
-    // the carried state as handles (for a caller that must undo several steps, e.g. a multi-token request)
-    std::vector<LayerState> snapshot() const { return state_; }
-    void restore(std::vector<LayerState> s) { state_ = std::move(s); }
+    size_t backup_host_bytes() const {
+        size_t b = 0;
+        for (auto& kv : host_free_) b += kv.first * kv.second.size();
+        for (auto& c : saved_.copies) b += c.second;
+        return b;
+    }
 
    private:
     // plaintexts, encoded on first use at the level they are applied
@@ -874,6 +985,119 @@ class Decoder {
             for (uint32_t t = 0; t < q; t++) st.Didx.push_back({k, t});
     }
 
+    // -- the host copy of the carried state ------------------------------------------------------------------
+    template <class F>
+    static void for_each_ct(LayerState& st, F&& f) {
+        for (auto& c : st.Dseg) f(c);
+        f(st.xp_t);
+        f(st.xp_c);
+        f(st.Dn);
+    }
+
+    void* host_get(size_t bytes) {
+        auto& l = host_free_[bytes];
+        if (!l.empty()) {
+            void* p = l.back();
+            l.pop_back();
+            return p;
+        }
+        void* p = nullptr;
+        ck(ckks_host_alloc(bytes, &p), "ckks_host_alloc");
+        return p;
+    }
+
+    // pinned host buffers for the next step's copy of the state, allocated now (after the step that made the state)
+    // rather than inside the next step
+    void reserve_backup() {
+        std::map<size_t, size_t> need;
+        std::set<const Buf*> seen;
+        for (auto& st : state_)
+            for_each_ct(st, [&](Ct& c) {
+                if (c.buf && seen.insert(c.buf.get()).second) need[c.buf->bytes]++;
+            });
+        for (auto& kv : need) {
+            auto& l = host_free_[kv.first];
+            while (l.size() < kv.second) {
+                void* p = nullptr;
+                ck(ckks_host_alloc(kv.first, &p), "ckks_host_alloc");
+                l.push_back(p);
+            }
+        }
+    }
+
+    // every buffer of the state copied to the host on the side stream (after the work enqueued so far)
+    void backup() {
+        saved_ = Saved{};
+        saved_.active = true;
+        saved_.meta = state_;
+        std::map<const Buf*, int> index;
+        for (auto& st : saved_.meta) {
+            std::vector<int> ids;
+            uint64_t ticket = 0;
+            for_each_ct(st, [&](Ct& c) {
+                if (!c.buf) {
+                    ids.push_back(-1);
+                    return;
+                }
+                auto it = index.find(c.buf.get());
+                if (it == index.end()) {
+                    void* h = host_get(c.buf->bytes);
+                    saved_.copies.emplace_back(h, c.buf->bytes);
+                    ck(ckks_side_copy(be_->ctx(), h, c.buf->d, c.buf->bytes, nullptr, &ticket), "ckks_side_copy");
+                    it = index.emplace(c.buf.get(), (int)saved_.copies.size() - 1).first;
+                }
+                ids.push_back(it->second);
+                c.buf.reset();  // the metadata only: the device buffer is not held by the copy
+            });
+            saved_.ids.push_back(std::move(ids));
+            saved_.ticket.push_back(ticket);
+        }
+    }
+
+    // layer li's previous state is no longer needed on the device: once its copy has landed (the wait is ordered
+    // on the work stream, before any reuse of the released buffers), let it go
+    void release_layer(uint32_t li) {
+        if (li >= state_.size()) return;
+        if (saved_.active && li < saved_.ticket.size() && saved_.ticket[li])
+            ck(ckks_side_wait(be_->ctx(), saved_.ticket[li], nullptr), "ckks_side_wait");
+        if (saved_.active) {
+            // every copy up to this layer's last one has landed: the buffers shared with later layers stay held
+            state_[li] = LayerState{};
+        }
+    }
+
+    // the device must not reuse a buffer still being copied
+    void wait_backup() {
+        if (!saved_.active) return;
+        for (auto t : saved_.ticket)
+            if (t) ck(ckks_side_wait(be_->ctx(), t, nullptr), "ckks_side_wait");
+    }
+
+    void restore_backup() {
+        ck(ckks_side_sync(be_->ctx()), "ckks_side_sync");
+        std::vector<std::shared_ptr<Buf>> bufs(saved_.copies.size());
+        for (size_t i = 0; i < bufs.size(); i++) {
+            bufs[i] = be_->alloc(saved_.copies[i].second);
+            ck(ckks_memcpy_h2d(bufs[i]->d, saved_.copies[i].first, saved_.copies[i].second), "ckks_memcpy_h2d");
+        }
+        std::vector<LayerState> st = saved_.meta;
+        for (size_t li = 0; li < st.size(); li++) {
+            size_t j = 0;
+            for_each_ct(st[li], [&](Ct& c) {
+                const int id = saved_.ids[li][j++];
+                if (id >= 0) c.buf = bufs[id];
+            });
+        }
+        state_ = std::move(st);
+    }
+
+    void drop_backup() {
+        wait_backup();
+        ck(ckks_side_sync(be_->ctx()), "ckks_side_sync");  // the host buffers go back to the free lists
+        for (auto& c : saved_.copies) host_free_[c.second].push_back(c.first);
+        saved_ = Saved{};
+    }
+
     std::vector<LayerState> cold_state() {
         const uint32_t lt = be_->top_level();
         std::vector<LayerState> state(layers_.size());
@@ -891,6 +1115,15 @@ class Decoder {
     std::vector<LayerW> layers_;
     LayerW model_;
     std::vector<LayerState> state_;
+    // the previous state on the host while a step (or a held request) may still need to put it back
+    struct Saved {
+        bool active = false;
+        std::vector<LayerState> meta;             // the state's ciphertexts without their buffers
+        std::vector<std::vector<int>> ids;        // per layer, per ciphertext (for_each_ct order): its copy, or -1
+        std::vector<std::pair<void*, size_t>> copies;  // pinned host buffer, bytes
+        std::vector<uint64_t> ticket;             // per layer: the side copy of its last new buffer (0: none)
+    } saved_;
+    std::map<size_t, std::vector<void*>> host_free_;  // pinned host buffers kept for the next backup
     std::map<std::pair<std::string, uint32_t>, std::shared_ptr<Buf>> pt_;
     std::map<std::pair<std::string, uint32_t>, Matvec> mv_;
     uint64_t n_boot_ = 0;
@@ -959,13 +1192,14 @@ int serve_step(void* user, uint32_t, const char* req_prefix, const char* resp_pr
         // (reset included), as in the reference, which commits its carry only after the whole pass
         // (gpu_real_model.cu:5284-5286)
         Decoder& dec = *sv->dec->dec;
-        auto before = dec.snapshot();
+        dec.hold_backup();  // the state from before the request, on the host until the request is done
         try {
             serve_tokens(sv, req_prefix, resp_prefix, count, tokens, lanes, reset != 0);
         } catch (...) {
-            dec.restore(std::move(before));
+            dec.restore_held();
             throw;
         }
+        dec.release_held();
     });
     if (rc != CKKS_OK && err && err_cap) std::snprintf(err, err_cap, "%s", g_err.c_str());
     return rc;
@@ -1083,9 +1317,9 @@ int fhe_ssm_decoder_serve(fhe_ssm_decoder* dec, const char* dir, const fhe_ssm_s
 int fhe_ssm_decoder_memory(const fhe_ssm_decoder* dec, uint64_t* bytes, uint32_t n) {
     return guarded([&] {
         if (!dec || (!bytes && n)) throw Error(CKKS_EINVAL, "null argument");
-        const uint64_t v[4] = {dec->dec->store_bytes(), dec->be->diag_bytes(), dec->be->pool_bytes(),
-                               dec->dec->state_bytes()};
-        for (uint32_t i = 0; i < n && i < 4; i++) bytes[i] = v[i];
+        const uint64_t v[6] = {dec->dec->store_bytes(), dec->be->diag_bytes(), dec->be->pool_bytes(),
+                               dec->dec->state_bytes(), dec->dec->backup_host_bytes(), dec->dec->store_host_bytes()};
+        for (uint32_t i = 0; i < n && i < 6; i++) bytes[i] = v[i];
     });
 }
 

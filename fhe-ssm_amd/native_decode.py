@@ -135,12 +135,13 @@ class NativeDecoder:
         check(load().fhe_ssm_decoder_reset(self.h))
 
     def memory(self) -> dict:
-        """device bytes the decoder holds: plaintext store, expanded-diagonal buffer, ciphertext pool (all it has
-        allocated), carried state (part of the pool)"""
-        v = np.zeros(4, dtype=np.uint64)
-        check(load().fhe_ssm_decoder_memory(self.h, v.ctypes.data, 4))
-        return {"plaintext_store": int(v[0]), "diagonal_buffer": int(v[1]), "ciphertext_pool": int(v[2]),
-                "carried_state": int(v[3])}
+        """bytes the decoder holds: elementwise plaintexts, diagonal staging/expansion buffers, ciphertext pool (all
+        it has allocated), carried state (part of the pool) on the device; the previous state's copy and the matvec
+        coefficients in pinned host memory"""
+        v = np.zeros(6, dtype=np.uint64)
+        check(load().fhe_ssm_decoder_memory(self.h, v.ctypes.data, 6))
+        return {"plaintexts": int(v[0]), "diagonal_buffers": int(v[1]), "ciphertext_pool": int(v[2]),
+                "carried_state": int(v[3]), "host_state_copy": int(v[4]), "host_matvec_store": int(v[5])}
 
     def serve(self, directory: str, timeout_sec: int = 3600, stateful: bool = True, log_fd: int = -1,
               poll_ms: int = 200, first_req: int = 0) -> dict:

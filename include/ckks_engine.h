@@ -82,6 +82,16 @@ int ckks_buffer_alloc(size_t bytes, void** d_out);
 int ckks_buffer_free(void* d);
 int ckks_memcpy_h2d(void* d_dst, const void* h_src, size_t bytes);
 int ckks_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes);
+/* Pinned host memory, and copies on a side stream of the context that overlap the work on the caller's stream (no
+ * counterpart in the reference; for a caller that keeps copies of device data on the host while it computes):
+ * ckks_side_copy   copies bytes (any direction) once the work enqueued so far on stream is done; returns a ticket
+ * ckks_side_wait   makes stream wait (without blocking the host) until the copy of ticket is done
+ * ckks_side_sync   blocks the host until every side copy is done and forgets the tickets */
+int ckks_host_alloc(size_t bytes, void** h_out);
+int ckks_host_free(void* h);
+int ckks_side_copy(ckks_context* ctx, void* dst, const void* src, size_t bytes, void* stream, uint64_t* ticket);
+int ckks_side_wait(ckks_context* ctx, uint64_t ticket, void* stream);
+int ckks_side_sync(ckks_context* ctx);
 int ckks_device_sync(void);
 
 /* ---- raw stages (the hot path; all buffers device-resident, limb-major) ----------------------
@@ -198,7 +208,7 @@ int ckks_encode_periodic(ckks_context* ctx, const double* re, const double* im, 
  * 2 period words per vector and expanded to its limbs when it is applied (the reference keeps its compressed store
  * on the host and streams it into a device pool, gpu_real_model.cu:1660-1706,3085-3285):
  * ckks_encode_periodic_coeffs  the host half: special FFT, rounding (with the approxFactor rule): d_coef
- *                              [n][2 period] int64 and d_log_approx [n] int32, device memory
+ *                              [n][2 period] int64 and d_log_approx [n] int32, device or pinned host memory
  * ckks_expand_periodic         the device half, enqueued on stream: d_out [n][level][2 period], the words
  *                              ckks_encode_periodic writes */
 int ckks_encode_periodic_coeffs(ckks_context* ctx, const double* re, const double* im, uint32_t n_vectors,

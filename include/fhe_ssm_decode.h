@@ -73,10 +73,11 @@ int fhe_ssm_decoder_stats(const fhe_ssm_decoder* dec, uint64_t* bootstraps);
 /* Drop the carried state (WKV state and both token-shift carries of every layer): the next step starts cold, as
  * the first one did.  The serve loop's req.N.reset / stateless request (gpu_real_model.cu:4461-4465). */
 int fhe_ssm_decoder_reset(fhe_ssm_decoder* dec);
-/* Device bytes the decoder holds (no counterpart in the reference; for memory accounting): bytes[0] the plaintext
- * store (elementwise plaintexts and the matvec diagonals' coefficients), bytes[1] the buffer the matvec diagonals
- * are expanded into, bytes[2] the ciphertext pool (every buffer it has allocated, in use or free), bytes[3] the
- * carried state (part of bytes[2]).  Fills min(n, 4) entries. */
+/* Bytes the decoder holds (no counterpart in the reference; for memory accounting): device bytes[0] the elementwise
+ * plaintexts, bytes[1] the buffers the matvec diagonals are staged and expanded in, bytes[2] the ciphertext pool
+ * (every buffer it has allocated, in use or free), bytes[3] the carried state (part of bytes[2]); pinned host
+ * bytes[4] the copy of the previous state a step puts back if it fails, bytes[5] the matvec diagonals'
+ * coefficients.  Fills min(n, 6) entries. */
 int fhe_ssm_decoder_memory(const fhe_ssm_decoder* dec, uint64_t* bytes, uint32_t n);
 
 /* ---- the serve-directory protocol (the reference's persistent --serve DIR loop, gpu_real_model.cu:4363-4483 and
