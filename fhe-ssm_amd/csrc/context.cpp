@@ -103,6 +103,10 @@ PrimeInfo make_prime_info(uint64_t q, uint64_t itab1) {
     const uint32_t bits = 64 - (uint32_t)__builtin_clzll(q);
     p.red_shift = bits > 25 ? bits - 25 : 0;
     p.red_mul = (uint32_t)(((u128)1 << (32 + p.red_shift)) / q);
+    // q^-1 mod 2^64 by Newton's iteration (q odd: x = q is correct to 3 bits, each step doubles them)
+    uint64_t x = q;
+    for (int i = 0; i < 5; i++) x *= 2 - q * x;
+    p.mont_ninv = 0 - x;
     return p;
 }
 

@@ -27,6 +27,7 @@ struct PrimeInfo {
     // quotient estimate of a value v < 128 q: hi32(floor(v / 2^red_shift) * red_mul) is floor(v / q) or one less,
     // with red_shift = max(0, bits(q) - 25), red_mul = floor(2^(32 + red_shift) / q)
     uint32_t red_shift, red_mul;
+    uint64_t mont_ninv;  // -q^-1 mod 2^64 (Montgomery reduction of a 128-bit sum, R = 2^64)
 };
 
 // One limb to transform: offset (in units of N words) from the base pointer, and its prime index.
@@ -54,6 +55,10 @@ enum class NttMode { TwoPass = 0, Fused = 1 };
 struct BConvPlan {
     uint32_t n_in = 0, n_out = 0;
     bool centered = false;  // exact (centered) conversion: table also holds floor(2^128/q_i) and prod mod p_j
+    // the output sums are reduced by Montgomery's REDC (R = 2^64) instead of Barrett: the table's qhat_mod (and
+    // prod mod p_j) columns then hold their values times R mod p_j.  Taken when sum_i q_i + 16 < 2^64, which keeps
+    // every sum below p_j R (REDC's input bound).
+    bool mont = false;
     std::vector<uint32_t> in_idx, out_idx;  // prime indices
     uint64_t* d_tab = nullptr;  // [n_in] (qhat_inv, companion) pairs, then [n_in][n_out] qhat_mod split into 30-bit
                                 // halves ((v >> 30) << 32 | v mod 2^30)

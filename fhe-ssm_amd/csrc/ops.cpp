@@ -204,6 +204,14 @@ void ring_release(Context& ctx, uint32_t slot, hipStream_t st) {
 }
 
 // ------------------------------------------------------------------ BConv plans
+// Montgomery reduction of the output sums is exact when every sum stays below p_j 2^64: a sum is at most
+// p_j (sum_i q_i) plus the centered correction (below 16 p_j)
+static bool bconv_mont(const Context& ctx, const std::vector<uint32_t>& in_idx) {
+    unsigned __int128 s = 16;
+    for (auto i : in_idx) s += ctx.moduli[i];
+    return s < ((unsigned __int128)1 << 64);
+}
+
 const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, const std::vector<uint32_t>& out_idx,
                             bool centered, const std::vector<uint64_t>& col_scale) {
     if (!col_scale.empty() && col_scale.size() != out_idx.size())
@@ -228,6 +236,7 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
             p.in_idx = in_idx;
             p.out_idx = out_idx;
             p.centered = centered;
+            p.mont = bconv_mont(ctx, in_idx);
             p.d_tab = (uint64_t*)arena_take(*ctx.arena, ht->second.size() * 8);
             HIPX(arena_put(p.d_tab, ht->second.data(), ht->second.size() * 8, ctx.arena->st));
             ctx.arena->plans.push_back(std::move(p));
@@ -239,6 +248,11 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
     p.in_idx = in_idx;
     p.out_idx = out_idx;
     p.centered = centered;
+    p.mont = bconv_mont(ctx, in_idx);
+    // R = 2^64 mod p_j: the Montgomery form of a table column
+    auto to_mont = [&](uint64_t v, uint64_t pj) {
+        return p.mont ? (uint64_t)(((unsigned __int128)v << 64) % pj) : v;
+    };
     std::vector<uint64_t> tab(2 * p.n_in + (size_t)p.n_in * p.n_out + (centered ? 2 * p.n_in + p.n_out : 0));
     for (uint32_t i = 0; i < p.n_in; i++) {
         const uint64_t qi = ctx.moduli[in_idx[i]];
@@ -253,7 +267,7 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
             uint64_t m = 1;
             for (uint32_t k = 0; k < p.n_in; k++)
                 if (k != i) m = mulmod_h(m, ctx.moduli[in_idx[k]] % pj, pj);
-            const uint64_t v = col_scale.empty() ? m : mulmod_h(m, col_scale[j], pj);
+            const uint64_t v = to_mont(col_scale.empty() ? m : mulmod_h(m, col_scale[j], pj), pj);
             tab[2 * p.n_in + (size_t)i * p.n_out + j] = ((v >> 30) << 32) | (v & 0x3FFFFFFFull);  // pack30
         }
     }
@@ -268,7 +282,7 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
             const uint64_t pj = ctx.moduli[out_idx[j]];
             uint64_t m = 1;
             for (uint32_t k = 0; k < p.n_in; k++) m = mulmod_h(m, ctx.moduli[in_idx[k]] % pj, pj);
-            cfix[2 * p.n_in + j] = col_scale.empty() ? m : mulmod_h(m, col_scale[j], pj);
+            cfix[2 * p.n_in + j] = to_mont(col_scale.empty() ? m : mulmod_h(m, col_scale[j], pj), pj);
         }
     }
     if (ctx.arena) {

@@ -24,6 +24,15 @@ __device__ __forceinline__ uint64_t reduce_u128(const U128& x, const Barrett& b)
     return reduce128(hi, x.lo, b);
 }
 
+// Montgomery's REDC with R = 2^64: x < q R -> x R^-1 mod q in [0, q).  m = x_lo (-q^-1) mod 2^64 makes x + m q a
+// multiple of R; its low word sums to R exactly when x_lo != 0, so (x + m q) / R = x_hi + hi(m q) + [x_lo != 0],
+// below 2q.
+__device__ __forceinline__ uint64_t redc(const U128& x, uint64_t q, uint64_t ninv) {
+    const uint64_t m = x.lo * ninv;
+    const uint64_t t = x.hi + mulhi64(m, q) + (x.lo != 0 ? 1u : 0u);
+    return csub_s(t, q);
+}
+
 // ------------------------------------------------------------------ tensor product
 // a, b: [B][2][l][N]; d01: [B][2][l][N] (d0, d1); d2: [B][l][N]; d2e (optional): second copy of d2
 // scattered into the ModUp extension buffer: limb t of ciphertext c goes to d2e + c*d2e_bstride +
@@ -115,6 +124,7 @@ constexpr int kMaxBconvOut = 80;
 struct BConvArgs {
     uint32_t n_in, n_out;
     uint32_t centered;  // subtract u * (prod of input primes) with u = round(sum_i y_i / q_i)
+    uint32_t mont;      // the table's columns are in Montgomery form: reduce the sums by REDC
     uint64_t in_bstride, out_bstride;
     uint32_t in_desc[kMaxBconvIn];
     uint32_t out_desc[kMaxBconvOut];
@@ -225,24 +235,33 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         n_main = ba.n_out - 1;
         U128 acc, unused;
         sums(n_main, n_main, acc, unused);
-        const Barrett bl = barrett_of(primes[desc_prime(ba.out_desc[n_main])]);
+        const PrimeInfo& pl = primes[desc_prime(ba.out_desc[n_main])];
+        const Barrett bl = barrett_of(pl);
         correct(acc, n_main, bl);
-        const uint64_t conv = reduce_u128(acc, bl);
+        const uint64_t conv = ba.mont ? redc(acc, pl.q, pl.mont_ninv) : reduce_u128(acc, bl);
         ql = bl.q;
         z = shoup(sub_mod(mb.xlast[c * mb.xlast_pstride + k], conv, ql), mb.pinv_last.w, mb.pinv_last.wp, ql);
         if (mb.addc) z = add_mod(z, mb.addc[(size_t)c * kN + k], ql);
     }
     auto finish = [&](U128 acc, uint32_t j) {
         const uint32_t dj = ba.out_desc[j];
-        const Barrett br = barrett_of(primes[desc_prime(dj)]);
+        const PrimeInfo& pj = primes[desc_prime(dj)];
+        const Barrett br = barrett_of(pj);
         correct(acc, j, br);
-        if constexpr (kMdr) {
-            const uint64_t r = lift_centered(z, ql, br);
-            acc.lo += r;
-            acc.hi += (acc.lo < r) ? 1u : 0u;
+        uint64_t v;
+        if (ba.mont) {
+            v = redc(acc, pj.q, pj.mont_ninv);
+            if constexpr (kMdr) v = add_mod(v, lift_centered(z, ql, br), pj.q);
+        } else {
+            if constexpr (kMdr) {
+                const uint64_t r = lift_centered(z, ql, br);
+                acc.lo += r;
+                acc.hi += (acc.lo < r) ? 1u : 0u;
+            }
+            v = reduce_u128(acc, br);
         }
         // streamed: read once, by the next NTT (nontemporal, so the L2 keeps what is reused)
-        __builtin_nontemporal_store(reduce_u128(acc, br), &dst[(size_t)desc_off(dj) * kN]);
+        __builtin_nontemporal_store(v, &dst[(size_t)desc_off(dj) * kN]);
     };
     // two outputs per iteration: independent accumulation chains for the scheduler to interleave
     uint32_t j = 0;
@@ -1067,6 +1086,7 @@ static BConvArgs bconv_args(const BConvPlan& plan, uint64_t in_bstride, const ui
     ba.n_in = plan.n_in;
     ba.n_out = plan.n_out;
     ba.centered = plan.centered ? 1 : 0;
+    ba.mont = plan.mont ? 1 : 0;
     ba.in_bstride = in_bstride;
     ba.out_bstride = out_bstride;
     for (uint32_t i = 0; i < plan.n_in; i++) ba.in_desc[i] = (in_off[i] & 0xFFFFu) | ((uint32_t)plan.in_idx[i] << 16);
