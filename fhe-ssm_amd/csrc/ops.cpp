@@ -27,7 +27,7 @@ uint8_t* arena_take(Arena& a, size_t bytes);
 
 hipError_t launch_tensor(const Context& ctx, const uint64_t* a, const uint64_t* b, uint64_t* d01, uint64_t* d2,
                          uint32_t B, uint32_t l, uint64_t* d2e, uint64_t d2e_bstride, const uint32_t* ext_off,
-                         hipStream_t st);
+                         hipStream_t st, bool d01_last_only = false);
 hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_t* in, uint64_t in_bstride,
                         const uint32_t* in_off, uint64_t* out, uint64_t out_bstride, const uint32_t* out_off,
                         uint32_t B, hipStream_t st);
@@ -41,7 +41,8 @@ hipError_t launch_mdr_combine(const Context& ctx, const uint64_t* x, uint64_t x_
                               const TwPair* pinv, const TwPair* qlinv, hipStream_t st);
 hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const uint64_t* evk, const uint64_t* add,
                                  uint64_t add_pstride, const uint64_t* T, uint64_t* out, uint32_t B, uint32_t l,
-                                 const TwPair* pinv, const TwPair* qlinv, hipStream_t st);
+                                 const TwPair* pinv, const TwPair* qlinv, hipStream_t st,
+                                 const uint64_t* ta = nullptr, const uint64_t* tb = nullptr);
 hipError_t launch_sub_scale(const Context& ctx, const uint64_t* x, uint64_t x_pstride, const uint64_t* y,
                             uint64_t y_pstride, const uint64_t* add, uint64_t add_pstride, uint32_t add_div,
                             uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
@@ -418,7 +419,8 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
 // n_polys = 2B), x holds only limbs l-1.. of the evk inner product (k_ks_inner from t0 = l-1) and the combine
 // forms limbs 0..l-2 itself from ext and evk.
 void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
-                     hipStream_t st, const uint64_t* ext, const uint64_t* evk) {
+                     hipStream_t st, const uint64_t* ext, const uint64_t* evk, const uint64_t* ta,
+                     const uint64_t* tb) {
     check_level(ctx, l);
     if (l < 2) throw std::invalid_argument("rescale needs l >= 2");
     const uint32_t E = l + ctx.K, K = ctx.K;
@@ -467,7 +469,10 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
     std::vector<uint32_t> pm(l - 1);
     for (uint32_t i = 0; i + 1 < l; i++) pm[i] = i;
     HIPX(launch_ntt(ctx, T, regular_jobs(n_polys, pm), n_polys * (l - 1), false, ctx.ntt_mode, st));
-    if (ext)
+    if (ext && ta)  // the addend formed from the product's inputs (add holds limb l-1 only, read above)
+        HIPX(launch_mdr_combine_ks(ctx, ext, evk, nullptr, 0, T, out, n_polys / 2, l, pinv.data(), qlinv.data(), st,
+                                   ta, tb));
+    else if (ext)
         HIPX(launch_mdr_combine_ks(ctx, ext, evk, add, (uint64_t)l * W, T, out, n_polys / 2, l, pinv.data(),
                                    qlinv.data(), st));
     else
@@ -559,8 +564,10 @@ void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uin
 // a, b: [B][2][l][N] eval -> out: [B][2][l-1][N] (rescaled) or [B][2][l][N] (do_rescale = false)
 // relinearization (+ rescale) after the tensor step: d01 [B][2][l][N], d2 in x2c (evaluation form) and in
 // each digit's own limbs of ext
+// ta, tb: the product's inputs when the tensor kernel wrote d0 and d1 for limb l-1 only (with the rescale)
 static void relin_tail(Context& ctx, uint64_t* d01, uint64_t* x2c, uint64_t* ext, uint32_t B, uint32_t l,
-                       const uint64_t* evk, uint64_t* out, bool do_rescale, hipStream_t st) {
+                       const uint64_t* evk, uint64_t* out, bool do_rescale, hipStream_t st,
+                       const uint64_t* ta = nullptr, const uint64_t* tb = nullptr) {
     const uint32_t E = l + ctx.K;
     uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)B * 2 * E * W * 8);
     std::vector<uint32_t> pm(l);
@@ -574,7 +581,7 @@ static void relin_tail(Context& ctx, uint64_t* d01, uint64_t* x2c, uint64_t* ext
     }
     // inner product of limb l-1 and the P limbs only; the combine forms limbs 0..l-2
     HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st, l - 1));
-    moddown_rescale(ctx, acc, 2 * B, l, d01, out, st, ext, evk);
+    moddown_rescale(ctx, acc, 2 * B, l, d01, out, st, ext, evk, ta, tb);
 }
 
 void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l, const uint64_t* evk,
@@ -585,11 +592,22 @@ void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint3
     uint64_t* x2c = (uint64_t*)ws_get(ctx, WS_X2C, (size_t)B * l * W * 8);
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)B * D * E * W * 8);
     // the tensor kernel writes d2 twice: into x2c (to be taken to coefficients) and, in evaluation
-    // form, straight into each digit's own limbs of the extension buffer
+    // form, straight into each digit's own limbs of the extension buffer.  With the rescale, d0 and d1 of limbs
+    // 0..l-2 are not written: the ModDown combine forms them from a and b (two limbs read per product instead of
+    // d0 and d1 written and read back)
     std::vector<uint32_t> ext_off(l);
     for (uint32_t t = 0; t < l; t++) ext_off[t] = (t / ctx.alpha) * E + t;
-    HIPX(launch_tensor(ctx, a, b, d01, x2c, B, l, ext, (uint64_t)D * E * W, ext_off.data(), st));
-    relin_tail(ctx, d01, x2c, ext, B, l, evk, out, do_rescale, st);
+    // (an output that overlaps an input keeps the d0 / d1 round trip: the combine would read a and b while writing)
+    auto overlaps = [&](const uint64_t* x) {
+        const uint64_t *xe = x + (size_t)B * 2 * l * W, *oe = out + (size_t)B * 2 * (l - 1) * W;
+        return out < xe && x < oe;
+    };
+    const bool from_inputs = do_rescale && !overlaps(a) && !overlaps(b);
+    HIPX(launch_tensor(ctx, a, b, d01, x2c, B, l, ext, (uint64_t)D * E * W, ext_off.data(), st, from_inputs));
+    if (from_inputs)
+        relin_tail(ctx, d01, x2c, ext, B, l, evk, out, true, st, a, b);
+    else
+        relin_tail(ctx, d01, x2c, ext, B, l, evk, out, do_rescale, st);
 }
 
 // Device workspace of hmult with the rescale (bytes): d01 2Bl, d2 Bl, extension B D E, inner product 2B E,

@@ -37,10 +37,14 @@ __device__ __forceinline__ uint64_t redc(const U128& x, uint64_t q, uint64_t nin
 // a, b: [B][2][l][N]; d01: [B][2][l][N] (d0, d1); d2: [B][l][N]; d2e (optional): second copy of d2
 // scattered into the ModUp extension buffer: limb t of ciphertext c goes to d2e + c*d2e_bstride +
 // ext_off[t]*N.
+// d01_last_only: d0 and d1 are written for limb l-1 only (a relinearization with its rescale forms limbs 0..l-2 of
+// them in the ModDown combine from a and b, k_mdr_combine_ks, and needs only limb l-1 here), and the other limbs
+// read a1 and b1 alone.
 struct TensorArgs {
     uint32_t l, B;
     uint64_t* d2e;
     uint64_t d2e_bstride;
+    uint32_t d01_last_only;
     uint32_t ext_off[kMaxPmap];
 };
 
@@ -52,15 +56,19 @@ __global__ __launch_bounds__(256) void k_tensor(const uint64_t* __restrict__ a, 
     const Barrett br = barrett_of(primes[t]);
     const size_t P = (size_t)ta.l * kN;
     const size_t o = (size_t)c * 2 * P + (size_t)t * kN + k;
-    const uint64_t a0 = a[o], a1 = a[o + P], b0 = b[o], b1 = b[o + P];
-    Acc s0, s1, s2;
-    s0.add(a0, b0);
-    s1.add(a0, b1);
-    s1.add(a1, b0);
+    const uint64_t a1 = a[o + P], b1 = b[o + P];
+    if (!ta.d01_last_only || t + 1 == ta.l) {
+        const uint64_t a0 = a[o], b0 = b[o];
+        Acc s0, s1;
+        s0.add(a0, b0);
+        s1.add(a0, b1);
+        s1.add(a1, b0);
+        // outputs streamed (nontemporal): each is read once, by a later kernel
+        __builtin_nontemporal_store(reduce_u128(s0.get(), br), &d01[o]);
+        __builtin_nontemporal_store(reduce_u128(s1.get(), br), &d01[o + P]);
+    }
+    Acc s2;
     s2.add(a1, b1);
-    // outputs streamed (nontemporal): each is read once, by a later kernel
-    __builtin_nontemporal_store(reduce_u128(s0.get(), br), &d01[o]);
-    __builtin_nontemporal_store(reduce_u128(s1.get(), br), &d01[o + P]);
     const uint64_t v2 = reduce_u128(s2.get(), br);
     __builtin_nontemporal_store(v2, &d2[(size_t)c * P + (size_t)t * kN + k]);
     if (ta.d2e) __builtin_nontemporal_store(v2, &ta.d2e[c * ta.d2e_bstride + (size_t)ta.ext_off[t] * kN + k]);
@@ -521,11 +529,14 @@ __global__ __launch_bounds__(256) void k_mdr_combine(const uint64_t* __restrict_
 // k_mdr_combine for the relinearization of a batch, x formed on the fly: x[c][p][i] = sum_d ext[c][d][i] *
 // evk[d][p][i] (the same sums k_ks_inner would store), then out[c][p][i] = (add + x P^-1 - T) q_{l-1}^-1 for both
 // polys p of ciphertext c.  Grid as k_ks_inner: the ciphertext index fastest.
+// ta, tb (optional, in place of add): the inputs [B][2][l][N] of the product being relinearized; the addend of
+// poly 0 is then d0 = a0 b0 and of poly 1 d1 = a0 b1 + a1 b0, formed here instead of read from the tensor kernel.
 __global__ __launch_bounds__(256) void k_mdr_combine_ks(const uint64_t* __restrict__ ext,
                                                         const uint64_t* __restrict__ evk,
                                                         const uint64_t* __restrict__ add,
                                                         const uint64_t* __restrict__ T, uint64_t* __restrict__ out,
-                                                        InnerArgs ia, MdrArgs ma,
+                                                        InnerArgs ia, MdrArgs ma, const uint64_t* __restrict__ ta,
+                                                        const uint64_t* __restrict__ tb,
                                                         const PrimeInfo* __restrict__ primes) {
     const uint32_t c = blockIdx.x, k = blockIdx.y * 256 + threadIdx.x, i = blockIdx.z;
     const Barrett br = barrett_of(primes[i]);
@@ -537,10 +548,23 @@ __global__ __launch_bounds__(256) void k_mdr_combine_ks(const uint64_t* __restri
     // ext, the addend, T and out are each touched once (nontemporal); the key is shared by the batch
     ks_dot<true>(x, (size_t)ia.E * kN, e, (size_t)ia.T * kN, ia.D, s0, s1);
     const uint64_t xs[2] = {reduce_u128(s0.get(), br), reduce_u128(s1.get(), br)};
+    uint64_t dt[2] = {0, 0};
+    if (ta) {
+        const size_t pw = (size_t)ma.l * kN, o = (size_t)c * 2 * pw + li;
+        const uint64_t a0 = __builtin_nontemporal_load(&ta[o]), a1 = __builtin_nontemporal_load(&ta[o + pw]);
+        const uint64_t b0 = __builtin_nontemporal_load(&tb[o]), b1 = __builtin_nontemporal_load(&tb[o + pw]);
+        Acc u0, u1;
+        u0.add(a0, b0);
+        u1.add(a0, b1);
+        u1.add(a1, b0);
+        dt[0] = reduce_u128(u0.get(), br);
+        dt[1] = reduce_u128(u1.get(), br);
+    }
 #pragma unroll
     for (int p = 0; p < 2; p++) {
         const size_t pc = 2 * (size_t)c + p;
         uint64_t v = shoup(xs[p], ma.pinv[i].w, ma.pinv[i].wp, q);
+        if (ta) v = add_mod(v, dt[p], q);
         if (add) v = add_mod(v, __builtin_nontemporal_load(&add[pc * ma.add_pstride + li]), q);
         v = sub_mod(v, __builtin_nontemporal_load(&T[pc * po + li]), q);
         __builtin_nontemporal_store(shoup(v, ma.qlinv[i].w, ma.qlinv[i].wp, q), &out[pc * po + li]);
@@ -1066,15 +1090,19 @@ __global__ __launch_bounds__(256) void k_mul_i(const uint64_t* __restrict__ in, 
 // ------------------------------------------------------------------ launchers
 hipError_t launch_tensor(const Context& ctx, const uint64_t* a, const uint64_t* b, uint64_t* d01, uint64_t* d2,
                          uint32_t B, uint32_t l, uint64_t* d2e, uint64_t d2e_bstride, const uint32_t* ext_off,
-                         hipStream_t st) {
+                         hipStream_t st, bool d01_last_only) {
     TensorArgs ta{};
     ta.l = l;
     ta.B = B;
     ta.d2e = d2e;
     ta.d2e_bstride = d2e_bstride;
+    ta.d01_last_only = d01_last_only ? 1 : 0;
     if (d2e)
         for (uint32_t t = 0; t < l; t++) ta.ext_off[t] = ext_off[t];
-    const int pi = prof_begin(ctx, "tensor", (double)B * l * (4 + 3 + (d2e ? 1 : 0)) * kN * 8, st);
+    // per limb: inputs read, d2 (and its copy) written; d0 and d1 for every limb or only the last
+    const double per = d01_last_only ? 2.0 + 1.0 + (d2e ? 1 : 0) : 4.0 + 3.0 + (d2e ? 1 : 0);
+    const double bytes = (double)B * (l * per + (d01_last_only ? 4.0 : 0.0)) * kN * 8;
+    const int pi = prof_begin(ctx, "tensor", bytes, st);
     hipLaunchKernelGGL(k_tensor, dim3(kN / 256, l, B), dim3(256), 0, st, a, b, d01, d2, ta, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
@@ -1374,17 +1402,18 @@ hipError_t launch_mdr_combine(const Context& ctx, const uint64_t* x, uint64_t x_
 // 0..l-2 formed in the kernel from ext [B][D][E][N] and evk [dnum][2][L+K][N]
 hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const uint64_t* evk, const uint64_t* add,
                                  uint64_t add_pstride, const uint64_t* T, uint64_t* out, uint32_t B, uint32_t l,
-                                 const TwPair* pinv, const TwPair* qlinv, hipStream_t st) {
-    if (l < 2 || l > (uint32_t)kMaxPmap) return hipErrorInvalidValue;
+                                 const TwPair* pinv, const TwPair* qlinv, hipStream_t st, const uint64_t* ta,
+                                 const uint64_t* tb) {
+    if (l < 2 || l > (uint32_t)kMaxPmap || (ta && (!tb || add))) return hipErrorInvalidValue;
     const InnerArgs ia = inner_args(ctx, l, B);
     if (ia.D > (uint32_t)kMaxDigits || ia.E > kMaxPmap) return hipErrorInvalidValue;
     const MdrArgs ma = mdr_args(l, 0, add ? add_pstride : 0, pinv, qlinv);
-    // per ciphertext: D ext limbs, 2 T, 2 add (if any), 2 out; the level's evk limbs once
+    // per ciphertext: D ext limbs, 2 T, 2 add (or the 4 product inputs), 2 out; the level's evk limbs once
     const double bytes =
-        ((double)B * (ia.D + 2 + (add ? 2 : 0) + 2) + 2.0 * ia.D) * (l - 1) * kN * 8;
+        ((double)B * (ia.D + 2 + (add ? 2 : 0) + (ta ? 4 : 0) + 2) + 2.0 * ia.D) * (l - 1) * kN * 8;
     const int pi = prof_begin(ctx, "mdr_combine_ks", bytes, st);
     hipLaunchKernelGGL(k_mdr_combine_ks, dim3(B, kN / 256, l - 1), dim3(256), 0, st, ext, evk, add, T, out, ia, ma,
-                       ctx.d_primes);
+                       ta, tb, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }

@@ -124,7 +124,7 @@ int ckks_keyswitch(ckks_context* ctx, const uint64_t* d_x, uint32_t batch, uint3
  * ckks_rescale             RescaleInPlace: [n_polys][l][N] -> [n_polys][l-1][N] (drop the last limb,
  *                          centered lift, * q_{l-1}^-1), in != out
  * ckks_eval_mult           EvalMult(ct, ct) with relinearization: a, b -> out [B][2][l][N]
- * ckks_eval_mult_rescale   EvalMult + RescaleInPlace fused: a, b -> out [B][2][l-1][N]
+ * ckks_eval_mult_rescale   EvalMult + RescaleInPlace fused: a, b -> out [B][2][l-1][N] (out may overlap a or b)
  * ckks_eval_add            EvalAdd(ct, ct): elementwise over [n_polys][l][N]
  * ckks_rotation_index      automorphism index of rotation step k: 5^k mod 2N (gpu_real_model.cu:1337-1360)
  * ckks_automorphism        X -> X^g on [n_polys][l][N] evaluation form (a slot permutation), in != out

@@ -122,6 +122,21 @@ def test_eval_mult_rescale_batch(ckks, ctx, octx, evk, d_evk):
         assert np.array_equal(out[i], octx.hmult_relin_rescale(a[i], b[i], l, evk)), i
 
 
+@pytest.mark.parametrize("alias", ["a", "b"])
+def test_eval_mult_rescale_in_place(ckks, ctx, octx, evk, d_evk, alias):
+    """The output written over an input (the product's d0 / d1 then take the tensor kernel's round trip, since the
+    ModDown combine would read the inputs while writing the output)."""
+    B, l = 2, 7
+    a = residues(ctx.moduli, (B, 2), list(range(l)), seed=33)
+    b = residues(ctx.moduli, (B, 2), list(range(l)), seed=34)
+    da, db = ckks.DeviceBuffer.from_array(a), ckks.DeviceBuffer.from_array(b)
+    dst = da if alias == "a" else db
+    ctx.eval_mult_rescale(da.ptr, db.ptr, B, l, d_evk.ptr, dst.ptr)
+    out = dst.download((B, 2, l - 1, N))
+    for i in range(B):
+        assert np.array_equal(out[i], octx.hmult_relin_rescale(a[i], b[i], l, evk)), i
+
+
 def test_eval_mult_no_rescale(ckks, ctx, octx, evk, d_evk):
     l = 9
     a = residues(ctx.moduli, (1, 2), list(range(l)), seed=41)
