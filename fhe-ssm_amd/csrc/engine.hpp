@@ -46,6 +46,14 @@ struct JobSpec {
     const uint64_t* src;  // out-of-place input (dense specs, inverse only), or null
     uint32_t src_period;  // limbs between polys of src
     uint8_t pmap[kMaxPmap];
+    // With src (two-pass mode only): src2, if set, makes the input the product src * src2 mod q, both factors read
+    // at src's layout; copy, if set, receives the input (or that product) as read, before the transform: limb l of
+    // poly p at copy + p * copy_pstride + ((l / copy_alpha) * copy_E + l) * N -- a ModUp extension buffer's
+    // digit-own limbs.
+    const uint64_t* src2;
+    uint64_t* copy;
+    uint64_t copy_pstride;
+    uint32_t copy_alpha, copy_E;
 };
 
 enum class NttMode { TwoPass = 0, Fused = 1 };

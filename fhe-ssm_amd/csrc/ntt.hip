@@ -58,6 +58,20 @@ __device__ __forceinline__ const uint64_t* job_src(const JobSpec& js, uint32_t u
     return data + (size_t)off * kN;
 }
 
+// a dense spec's second input factor and the copy destination of its input, for job u (null when unused)
+struct JobIn {
+    const uint64_t* in2;
+    uint64_t* cpy;
+};
+
+__device__ __forceinline__ JobIn job_in(const JobSpec& js, uint32_t u) {
+    JobIn r{nullptr, nullptr};
+    const uint32_t l = u / js.n_polys, p = u - l * js.n_polys;
+    if (js.src2) r.in2 = js.src2 + ((size_t)p * js.src_period + l) * kN;
+    if (js.copy) r.cpy = js.copy + p * js.copy_pstride + ((size_t)(l / js.copy_alpha) * js.copy_E + l) * kN;
+    return r;
+}
+
 // Forward (Cooley-Tukey) butterfly, values kept in [0, 8q) (q < 2^60): X is brought to [0, 4q), the
 // twiddle product is in [0, 4q), so X + T and X - T + 4q stay in [0, 8q).
 __device__ __forceinline__ void ct_bfly(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q4, uint64_t nq) {
@@ -291,10 +305,13 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
 
 // ---------------------------------------------------------------- inverse pass B (256-word blocks)
 // GS stages with t = 2^u, u = 0..7: m = 2^(15-u), twiddle m + (j >> (u+1)), j = 256 b + r.
-// in: the limb read (a itself, or the out-of-place source)
-template <bool kOpen>
-__device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, const TwPair* __restrict__ tw, uint64_t q,
-                                           int tile, int g, uint64_t* lds) {
+// in: the limb read (a itself, or the out-of-place source).  kProd: the input is in * in2 mod q (q < 2^60, both
+// factors canonical, so the product's high word is below q).  ji.cpy (optional): the input words, as read or formed,
+// are also stored there.
+template <bool kOpen, bool kProd>
+__device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, JobIn ji, const PrimeInfo& P,
+                                           const TwPair* __restrict__ tw, int tile, int g, uint64_t* lds) {
+    const uint64_t q = P.q;
     const uint64_t q4 = q << 2, nq = 0 - q;
     const int bl = g >> 4, rl = g & 15;
     const int b = tile * 16 + bl;
@@ -302,8 +319,30 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, cons
     const uint64_t* src = in + 256 * b;
     uint64_t* L = lds + bl * 272;
     uint64_t x[16];
+    if (kProd || ji.cpy) {
 #pragma unroll
-    for (int k = 0; k < 16; k++) L[rl + 17 * k] = __builtin_nontemporal_load(&src[rl + 16 * k]);
+        for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&src[rl + 16 * k]);
+        if (kProd) {
+            const uint64_t* src2 = ji.in2 + 256 * b;
+            const Barrett br{q, P.mu_hi, P.mu_lo};
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                Acc s;
+                s.add(x[k], __builtin_nontemporal_load(&src2[rl + 16 * k]));
+                const U128 v = s.get();
+                x[k] = reduce128(v.hi, v.lo, br);
+            }
+        }
+        if (ji.cpy) {
+#pragma unroll
+            for (int k = 0; k < 16; k++) __builtin_nontemporal_store(x[k], &ji.cpy[256 * b + rl + 16 * k]);
+        }
+#pragma unroll
+        for (int k = 0; k < 16; k++) L[rl + 17 * k] = x[k];
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; k++) L[rl + 17 * k] = __builtin_nontemporal_load(&src[rl + 16 * k]);
+    }
     // u = 0..3: r = 16 rl + k, pairs differ in bit u of k; twiddle ... + (r >> (u+1)) = ... + rl 2^(3-u) + (k >> (u+1)),
     // stored by pass B's table (twb) as [k >> (u+1)][rl] within each block (consecutive pairs for a block's lanes).
     // A thread uses 2^(3-u) of them per stage; all 15 are loaded before the LDS exchange so that their latency
@@ -448,13 +487,21 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_b(uint64_t* data, JobS
     __shared__ uint64_t lds[kLdsWords];
     uint32_t off, prime;
     job_of(js, blockIdx.y, off, prime);
-    const uint64_t q = primes[prime].q;
-    if (q < kGsOpenMaxQ)
-        inv_b_tile<true>(data + (size_t)off * kN, job_src(js, blockIdx.y, data, off), tw_all + (size_t)prime * kN, q,
-                         blockIdx.x, threadIdx.x, lds);
-    else
-        inv_b_tile<false>(data + (size_t)off * kN, job_src(js, blockIdx.y, data, off), tw_all + (size_t)prime * kN, q,
-                          blockIdx.x, threadIdx.x, lds);
+    const PrimeInfo& P = primes[prime];
+    uint64_t* a = data + (size_t)off * kN;
+    const uint64_t* in = job_src(js, blockIdx.y, data, off);
+    const TwPair* tw = tw_all + (size_t)prime * kN;
+    const JobIn ji = js.jobs ? JobIn{nullptr, nullptr} : job_in(js, blockIdx.y);
+    if (ji.in2) {
+        if (P.q < kGsOpenMaxQ)
+            inv_b_tile<true, true>(a, in, ji, P, tw, blockIdx.x, threadIdx.x, lds);
+        else
+            inv_b_tile<false, true>(a, in, ji, P, tw, blockIdx.x, threadIdx.x, lds);
+    } else if (P.q < kGsOpenMaxQ) {
+        inv_b_tile<true, false>(a, in, ji, P, tw, blockIdx.x, threadIdx.x, lds);
+    } else {
+        inv_b_tile<false, false>(a, in, ji, P, tw, blockIdx.x, threadIdx.x, lds);
+    }
 }
 
 __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_a(uint64_t* data, JobSpec js, const TwPair* tw_all,
@@ -510,7 +557,7 @@ __global__ __launch_bounds__(kTileThreads* kFusedGroups) void k_ntt_inv_fused(ui
     uint64_t* L = lds + grp * kLdsWords;
     const uint64_t* in = job_src(js, blockIdx.x, data, off);
     for (int t = grp; t < 16; t += kFusedGroups) {
-        inv_b_tile<false>(a, in, twb_all + (size_t)prime * kN, P.q, t, g, L);
+        inv_b_tile<false, false>(a, in, JobIn{nullptr, nullptr}, P, twb_all + (size_t)prime * kN, t, g, L);
         __syncthreads();
     }
     for (int t = grp; t < 16; t += kFusedGroups) {
@@ -535,10 +582,20 @@ hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js_in, 
             seen[js.pmap[i]] = true;
         }
     }
+    if (js.src2 || js.copy) {
+        // product / copy of the input: dense inverse specs with an out-of-place source, two-pass kernels only
+        if (js.jobs || !js.src || !inverse || (js.copy && (js.copy_alpha == 0 || js.copy_E == 0)))
+            return hipErrorInvalidValue;
+        for (uint32_t i = 0; i < js.period; i++)
+            if (js.src2 && ctx.moduli[js.pmap[i]] >= (1ull << 60)) return hipErrorInvalidValue;
+        mode = NttMode::TwoPass;
+    }
     const TwPair* tw = inverse ? ctx.d_itw : ctx.d_tw;
     const TwPair* twb = inverse ? ctx.d_itwb : ctx.d_twb;
-    // algorithmic bytes: every limb read and written once, each prime's table (w, w') read once
-    const double bytes = (double)n_jobs * 2.0 * kN * 8 + (double)js.n_primes * kN * sizeof(TwPair);
+    // algorithmic bytes: every limb read and written once (plus the second factor read and the copy written), each
+    // prime's table (w, w') read once
+    const double streams = 2.0 + (js.src2 ? 1.0 : 0.0) + (js.copy ? 1.0 : 0.0);
+    const double bytes = (double)n_jobs * streams * kN * 8 + (double)js.n_primes * kN * sizeof(TwPair);
     const char* name = mode == NttMode::Fused ? (inverse ? "ntt_inv_fused" : "ntt_fwd_fused")
                                               : (inverse ? "ntt_inv_2pass" : "ntt_fwd_2pass");
     const int pi = prof_begin(ctx, name, bytes, st);

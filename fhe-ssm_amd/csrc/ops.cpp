@@ -27,7 +27,7 @@ uint8_t* arena_take(Arena& a, size_t bytes);
 
 hipError_t launch_tensor(const Context& ctx, const uint64_t* a, const uint64_t* b, uint64_t* d01, uint64_t* d2,
                          uint32_t B, uint32_t l, uint64_t* d2e, uint64_t d2e_bstride, const uint32_t* ext_off,
-                         hipStream_t st, bool d01_last_only = false);
+                         hipStream_t st, uint32_t t0 = 0);
 hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_t* in, uint64_t in_bstride,
                         const uint32_t* in_off, uint64_t* out, uint64_t out_bstride, const uint32_t* out_off,
                         uint32_t B, hipStream_t st);
@@ -86,8 +86,6 @@ hipError_t launch_pair_mac(const Context& ctx, const uint64_t* R, const uint64_t
                            uint32_t n, uint32_t l, uint32_t log_rep, hipStream_t st);
 hipError_t launch_gather(const Context& ctx, const uint64_t* const* src, uint32_t n, uint64_t words, uint64_t* dst,
                          hipStream_t st);
-hipError_t launch_scatter_limbs(const Context& ctx, const uint64_t* src, uint64_t src_bstride, uint64_t* dst,
-                                uint64_t dst_bstride, const uint32_t* off, uint32_t l, uint32_t B, hipStream_t st);
 hipError_t launch_tensor_sum(const Context& ctx, const uint64_t* const* d_tab, uint32_t np, uint64_t* d01,
                              uint64_t* d2, uint32_t B, uint32_t l, uint64_t* d2e, uint64_t d2e_bstride,
                              const uint32_t* ext_off, hipStream_t st);
@@ -339,8 +337,9 @@ void modup_from_coef(Context& ctx, const uint64_t* x2c, uint64_t* ext, uint32_t 
 }
 
 // x: [B] polys of l limbs, x_bstride words apart (0: l * N), evaluation form -> ext [B][D][E][N] evaluation
-// form.  x is only read: its digit-own limbs are copied into ext in one launch, and the inverse NTT reads x
-// and writes the coefficient-form copy it works on (so a ciphertext's c1 is extended in place, no extraction).
+// form.  x is only read: the inverse NTT reads x, writes the coefficient-form copy it works on (so a ciphertext's
+// c1 is extended in place, no extraction) and, in its first pass, copies x's limbs into their digits' own limbs of
+// ext.
 void modup(Context& ctx, const uint64_t* x, uint64_t* ext, uint32_t B, uint32_t l, hipStream_t st,
            uint64_t x_bstride) {
     check_level(ctx, l);
@@ -348,15 +347,15 @@ void modup(Context& ctx, const uint64_t* x, uint64_t* ext, uint32_t B, uint32_t 
     if (x_bstride == 0) x_bstride = (uint64_t)l * W;
     if (x_bstride % W) throw std::invalid_argument("ModUp input stride must be whole limbs");
     uint64_t* xc = (uint64_t*)ws_get(ctx, WS_X2C, (size_t)B * l * W * 8);
-    std::vector<uint32_t> own(l), pm(l);
-    for (uint32_t t = 0; t < l; t++) {
-        own[t] = (t / al) * E + t;
-        pm[t] = t;
-    }
-    HIPX(launch_scatter_limbs(ctx, x, x_bstride, ext, (uint64_t)D * E * W, own.data(), l, B, st));
+    std::vector<uint32_t> pm(l);
+    for (uint32_t t = 0; t < l; t++) pm[t] = t;
     JobSpec js = regular_jobs(B, pm);
     js.src = x;
     js.src_period = (uint32_t)(x_bstride / W);
+    js.copy = ext;
+    js.copy_pstride = (uint64_t)D * E * W;
+    js.copy_alpha = al;
+    js.copy_E = E;
     HIPX(launch_ntt(ctx, xc, js, B * l, true, ctx.ntt_mode, st));
     modup_from_coef(ctx, xc, ext, B, l, st);
 }
@@ -565,14 +564,15 @@ void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uin
 // relinearization (+ rescale) after the tensor step: d01 [B][2][l][N], d2 in x2c (evaluation form) and in
 // each digit's own limbs of ext
 // ta, tb: the product's inputs when the tensor kernel wrote d0 and d1 for limb l-1 only (with the rescale)
+// x2c_coef: x2c already holds d2 in coefficient form (the inverse NTT formed it from the inputs)
 static void relin_tail(Context& ctx, uint64_t* d01, uint64_t* x2c, uint64_t* ext, uint32_t B, uint32_t l,
                        const uint64_t* evk, uint64_t* out, bool do_rescale, hipStream_t st,
-                       const uint64_t* ta = nullptr, const uint64_t* tb = nullptr) {
+                       const uint64_t* ta = nullptr, const uint64_t* tb = nullptr, bool x2c_coef = false) {
     const uint32_t E = l + ctx.K;
     uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)B * 2 * E * W * 8);
     std::vector<uint32_t> pm(l);
     for (uint32_t i = 0; i < l; i++) pm[i] = i;
-    HIPX(launch_ntt(ctx, x2c, regular_jobs(B, pm), B * l, true, ctx.ntt_mode, st));
+    if (!x2c_coef) HIPX(launch_ntt(ctx, x2c, regular_jobs(B, pm), B * l, true, ctx.ntt_mode, st));
     modup_from_coef(ctx, x2c, ext, B, l, st);
     if (!do_rescale) {
         HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st));
@@ -591,23 +591,32 @@ void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint3
     uint64_t* d01 = (uint64_t*)ws_get(ctx, WS_D01, (size_t)B * 2 * l * W * 8);
     uint64_t* x2c = (uint64_t*)ws_get(ctx, WS_X2C, (size_t)B * l * W * 8);
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)B * D * E * W * 8);
-    // the tensor kernel writes d2 twice: into x2c (to be taken to coefficients) and, in evaluation
-    // form, straight into each digit's own limbs of the extension buffer.  With the rescale, d0 and d1 of limbs
-    // 0..l-2 are not written: the ModDown combine forms them from a and b (two limbs read per product instead of
-    // d0 and d1 written and read back)
-    std::vector<uint32_t> ext_off(l);
-    for (uint32_t t = 0; t < l; t++) ext_off[t] = (t / ctx.alpha) * E + t;
-    // (an output that overlaps an input keeps the d0 / d1 round trip: the combine would read a and b while writing)
+    // d2 = a1 b1 is formed by the inverse NTT's first pass as it reads a1 and b1: it writes the product, in
+    // evaluation form, straight into each digit's own limbs of the extension buffer and transforms it into x2c.  The
+    // tensor kernel writes d0 and d1 only; with the rescale, only their limb l-1: the ModDown combine forms limbs
+    // 0..l-2 from a and b (two limbs read per product instead of d0 and d1 written and read back) -- unless the
+    // output overlaps an input, since the combine would then read a and b while writing.
     auto overlaps = [&](const uint64_t* x) {
-        const uint64_t *xe = x + (size_t)B * 2 * l * W, *oe = out + (size_t)B * 2 * (l - 1) * W;
+        const uint64_t *xe = x + (size_t)B * 2 * l * W, *oe = out + (size_t)B * 2 * (l - (do_rescale ? 1 : 0)) * W;
         return out < xe && x < oe;
     };
     const bool from_inputs = do_rescale && !overlaps(a) && !overlaps(b);
-    HIPX(launch_tensor(ctx, a, b, d01, x2c, B, l, ext, (uint64_t)D * E * W, ext_off.data(), st, from_inputs));
+    HIPX(launch_tensor(ctx, a, b, d01, nullptr, B, l, nullptr, 0, nullptr, st, from_inputs ? l - 1 : 0));
+    std::vector<uint32_t> pm(l);
+    for (uint32_t t = 0; t < l; t++) pm[t] = t;
+    JobSpec js = regular_jobs(B, pm);
+    js.src = a + (size_t)l * W;  // poly 1 of each ciphertext
+    js.src2 = b + (size_t)l * W;
+    js.src_period = 2 * l;
+    js.copy = ext;
+    js.copy_pstride = (uint64_t)D * E * W;
+    js.copy_alpha = ctx.alpha;
+    js.copy_E = E;
+    HIPX(launch_ntt(ctx, x2c, js, B * l, true, ctx.ntt_mode, st));
     if (from_inputs)
-        relin_tail(ctx, d01, x2c, ext, B, l, evk, out, true, st, a, b);
+        relin_tail(ctx, d01, x2c, ext, B, l, evk, out, true, st, a, b, true);
     else
-        relin_tail(ctx, d01, x2c, ext, B, l, evk, out, do_rescale, st);
+        relin_tail(ctx, d01, x2c, ext, B, l, evk, out, do_rescale, st, nullptr, nullptr, true);
 }
 
 // Device workspace of hmult with the rescale (bytes): d01 2Bl, d2 Bl, extension B D E, inner product 2B E,

@@ -37,14 +37,13 @@ __device__ __forceinline__ uint64_t redc(const U128& x, uint64_t q, uint64_t nin
 // a, b: [B][2][l][N]; d01: [B][2][l][N] (d0, d1); d2: [B][l][N]; d2e (optional): second copy of d2
 // scattered into the ModUp extension buffer: limb t of ciphertext c goes to d2e + c*d2e_bstride +
 // ext_off[t]*N.
-// d01_last_only: d0 and d1 are written for limb l-1 only (a relinearization with its rescale forms limbs 0..l-2 of
-// them in the ModDown combine from a and b, k_mdr_combine_ks, and needs only limb l-1 here), and the other limbs
-// read a1 and b1 alone.
+// Limbs t0..l-1 only (grid y = l - t0).  d2 null: d0 and d1 alone (the relinearization's inverse NTT then forms d2
+// from a1 and b1 as it reads them, and a relinearization with its rescale forms d0 and d1 of limbs 0..l-2 in the
+// ModDown combine, so it asks for limb l-1 only).
 struct TensorArgs {
-    uint32_t l, B;
+    uint32_t l, B, t0;
     uint64_t* d2e;
     uint64_t d2e_bstride;
-    uint32_t d01_last_only;
     uint32_t ext_off[kMaxPmap];
 };
 
@@ -52,21 +51,19 @@ __global__ __launch_bounds__(256) void k_tensor(const uint64_t* __restrict__ a, 
                                                 uint64_t* __restrict__ d01, uint64_t* __restrict__ d2,
                                                 TensorArgs ta, const PrimeInfo* __restrict__ primes) {
     const uint32_t k = blockIdx.x * 256 + threadIdx.x;
-    const uint32_t t = blockIdx.y, c = blockIdx.z;
+    const uint32_t t = ta.t0 + blockIdx.y, c = blockIdx.z;
     const Barrett br = barrett_of(primes[t]);
     const size_t P = (size_t)ta.l * kN;
     const size_t o = (size_t)c * 2 * P + (size_t)t * kN + k;
-    const uint64_t a1 = a[o + P], b1 = b[o + P];
-    if (!ta.d01_last_only || t + 1 == ta.l) {
-        const uint64_t a0 = a[o], b0 = b[o];
-        Acc s0, s1;
-        s0.add(a0, b0);
-        s1.add(a0, b1);
-        s1.add(a1, b0);
-        // outputs streamed (nontemporal): each is read once, by a later kernel
-        __builtin_nontemporal_store(reduce_u128(s0.get(), br), &d01[o]);
-        __builtin_nontemporal_store(reduce_u128(s1.get(), br), &d01[o + P]);
-    }
+    const uint64_t a0 = a[o], a1 = a[o + P], b0 = b[o], b1 = b[o + P];
+    Acc s0, s1;
+    s0.add(a0, b0);
+    s1.add(a0, b1);
+    s1.add(a1, b0);
+    // outputs streamed (nontemporal): each is read once, by a later kernel
+    __builtin_nontemporal_store(reduce_u128(s0.get(), br), &d01[o]);
+    __builtin_nontemporal_store(reduce_u128(s1.get(), br), &d01[o + P]);
+    if (!d2) return;
     Acc s2;
     s2.add(a1, b1);
     const uint64_t v2 = reduce_u128(s2.get(), br);
@@ -577,13 +574,6 @@ struct LimbMap {
     uint16_t off[kMaxPmap];
 };
 
-__global__ __launch_bounds__(256) void k_scatter_limbs(const uint64_t* __restrict__ src, uint64_t src_bstride,
-                                                       uint64_t* __restrict__ dst, uint64_t dst_bstride, LimbMap lm) {
-    const uint32_t k = blockIdx.x * 256 + threadIdx.x, t = blockIdx.y, c = blockIdx.z;
-    __builtin_nontemporal_store(__builtin_nontemporal_load(&src[c * src_bstride + (size_t)t * kN + k]),
-                                &dst[c * dst_bstride + (size_t)lm.off[t] * kN + k]);
-}
-
 // dst[c] = src[c] for up to 64 items of `words` words each (gathers scattered ciphertexts into one batch)
 __global__ __launch_bounds__(256) void k_gather(ListPtrs src, uint64_t* __restrict__ dst, uint64_t words) {
     const uint32_t c = blockIdx.y;
@@ -1090,20 +1080,20 @@ __global__ __launch_bounds__(256) void k_mul_i(const uint64_t* __restrict__ in, 
 // ------------------------------------------------------------------ launchers
 hipError_t launch_tensor(const Context& ctx, const uint64_t* a, const uint64_t* b, uint64_t* d01, uint64_t* d2,
                          uint32_t B, uint32_t l, uint64_t* d2e, uint64_t d2e_bstride, const uint32_t* ext_off,
-                         hipStream_t st, bool d01_last_only) {
+                         hipStream_t st, uint32_t t0) {
+    if (t0 >= l || (d2e && !d2)) return hipErrorInvalidValue;
     TensorArgs ta{};
     ta.l = l;
     ta.B = B;
+    ta.t0 = t0;
     ta.d2e = d2e;
     ta.d2e_bstride = d2e_bstride;
-    ta.d01_last_only = d01_last_only ? 1 : 0;
     if (d2e)
         for (uint32_t t = 0; t < l; t++) ta.ext_off[t] = ext_off[t];
-    // per limb: inputs read, d2 (and its copy) written; d0 and d1 for every limb or only the last
-    const double per = d01_last_only ? 2.0 + 1.0 + (d2e ? 1 : 0) : 4.0 + 3.0 + (d2e ? 1 : 0);
-    const double bytes = (double)B * (l * per + (d01_last_only ? 4.0 : 0.0)) * kN * 8;
-    const int pi = prof_begin(ctx, "tensor", bytes, st);
-    hipLaunchKernelGGL(k_tensor, dim3(kN / 256, l, B), dim3(256), 0, st, a, b, d01, d2, ta, ctx.d_primes);
+    // per limb: inputs read, d0 and d1 written, d2 (and its copy) written
+    const double per = 4.0 + 2.0 + (d2 ? 1.0 : 0.0) + (d2e ? 1.0 : 0.0);
+    const int pi = prof_begin(ctx, "tensor", (double)B * (l - t0) * per * kN * 8, st);
+    hipLaunchKernelGGL(k_tensor, dim3(kN / 256, l - t0, B), dim3(256), 0, st, a, b, d01, d2, ta, ctx.d_primes);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
@@ -1461,18 +1451,6 @@ hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t e
     ctx.n_keyswitch += n_ks * (uint64_t)(n_out / A);
     const int pi = prof_begin(ctx, "qp_rot_sum", by * kN * 8, st);
     hipLaunchKernelGGL(k_qp_rot_sum, dim3(n_out * (kN / 256) * E), dim3(256), 0, st, ext, src, dst, a, ctx.d_primes);
-    prof_end(ctx, pi, st);
-    return hipGetLastError();
-}
-
-hipError_t launch_scatter_limbs(const Context& ctx, const uint64_t* src, uint64_t src_bstride, uint64_t* dst,
-                                uint64_t dst_bstride, const uint32_t* off, uint32_t l, uint32_t B, hipStream_t st) {
-    if (l == 0 || l > kMaxPmap || B == 0) return hipErrorInvalidValue;
-    LimbMap lm{};
-    for (uint32_t t = 0; t < l; t++) lm.off[t] = (uint16_t)off[t];
-    const int pi = prof_begin(ctx, "scatter_limbs", (double)B * l * 2 * kN * 8, st);
-    hipLaunchKernelGGL(k_scatter_limbs, dim3(kN / 256, l, B), dim3(256), 0, st, src, src_bstride, dst, dst_bstride,
-                       lm);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
