@@ -24,7 +24,10 @@
 // (1 MiB) in L2.  Either both passes run as separate kernels (grid 16 x jobs, 256 threads), or the
 // fused kernel runs one limb per 512-thread workgroup (2 tiles at a time, passes separated by a
 // workgroup barrier; the intermediate stays in L2/MALL instead of making a second HBM round trip).
+#include <type_traits>
+
 #include "engine.hpp"
+#include "ks_device.hpp"
 #include "modarith.hpp"
 
 namespace fhe {
@@ -230,9 +233,16 @@ __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPai
 }
 
 // ---------------------------------------------------------------- forward pass B (256-word blocks)
-template <bool kOpen>
+// Epi: what becomes of the transformed tile, held transposed in LDS (word rl + 16 k of block b at L[rl + 17 k]) --
+// StoreLimb (the default): stored over the limb; otherwise first = epi.begin(b, rl) before the final reduction and
+// exchange (loads that do not depend on the tile), then epi.end(first, L, b, rl).
+struct StoreLimb {
+    struct First {};
+};
+
+template <bool kOpen, class Epi = StoreLimb>
 __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, const PrimeInfo& P,
-                                           int tile, int g, uint64_t* lds) {
+                                           int tile, int g, uint64_t* lds, const Epi& epi = Epi{}) {
     const uint64_t q = P.q;
     const uint64_t q4 = q << 2, nq = 0 - q;
     const int bl = g >> 4, rl = g & 15;
@@ -293,14 +303,21 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
     }
     // canonical [0, q), then transpose through LDS for coalesced stores (direct 16-byte stores of each
     // thread's contiguous run measured slower)
+    // (an epilogue's first loads are issued here, ahead of the reduction and the exchange)
+    typename Epi::First first{};
+    if constexpr (!std::is_same<Epi, StoreLimb>::value) first = epi.begin(b, rl);
 #pragma unroll
     for (int k = 0; k < 16; k++) x[k] = kOpen ? reduce_open(x[k], q, nq, P.red_shift, P.red_mul) : canon8(x[k], q);
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < 16; k++) L[17 * rl + k] = x[k];
     __syncthreads();
+    if constexpr (std::is_same<Epi, StoreLimb>::value) {
 #pragma unroll
-    for (int k = 0; k < 16; k++) __builtin_nontemporal_store(L[rl + 17 * k], &blk[rl + 16 * k]);
+        for (int k = 0; k < 16; k++) __builtin_nontemporal_store(L[rl + 17 * k], &blk[rl + 16 * k]);
+    } else {
+        epi.end(first, L, b, rl);
+    }
 }
 
 // ---------------------------------------------------------------- inverse pass B (256-word blocks)
@@ -518,6 +535,157 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_a(uint64_t* data, JobS
                           TwPair{P.w1ninv, P.w1ninv_p}, blockIdx.x, threadIdx.x, lds);
 }
 
+// ---------------------------------------------------------------- forward pass B that finishes a ModDown
+// The forward NTT of a relinearization's ModDown term T ([2B][l-1] limbs, poly 2c + p of ciphertext c) ends with the
+// combine instead of a store of T: for each word of limb i,
+//   out[2c+p][i] = (x_p P^-1 + add_p - T_p) q_{l-1}^-1,  x_p = sum_d ext[c][d][i] evk[d][p][i]  (the evk inner product),
+// add_0 = d0 = a0 b0 and add_1 = d1 = a0 b1 + a1 b0 formed from the product's inputs a, b [B][2][l][N], or read from
+// an addend [2B][..][N] (or none).  The same words as the NTT followed by k_mdr_combine_ks, without T's store and
+// reload.  A workgroup is two 256-thread groups, one per poly of ciphertext c, each transforming the same tile of its
+// poly's limb i into an LDS tile of its own; then every thread finishes 8 words of the tile for both polys, so the
+// ext digits and the inputs are read once for the two.
+struct MdrFuse {
+    const uint64_t* ext;  // [B][D][E][N]
+    const uint64_t* evk;  // [dnum][2][T][N]
+    const uint64_t* ta;   // [B][2][l][N] or null
+    const uint64_t* tb;
+    const uint64_t* add;  // [2B] polys add_pstride words apart, or null
+    uint64_t* out;        // [2B][l-1][N]
+    uint64_t add_pstride;
+    uint32_t B, l, E, T;
+    TwPair pinv[kMaxPmap], qlinv[kMaxPmap];
+};
+
+// Barrett reduction of a sum of at most 4 products of residues below q < 2^60: the high word is below q, so no fold.
+__device__ __forceinline__ uint64_t reduce_sum(Acc& s, const Barrett& br) {
+    const U128 v = s.get();
+    return reduce128(v.hi, v.lo, br);
+}
+
+// a word at a byte offset from a wave-uniform base (the global_load form with a scalar base and a 32-bit offset)
+__device__ __forceinline__ uint64_t ld_at(const uint64_t* base, uint32_t byte_off) {
+    return *reinterpret_cast<const uint64_t*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+__device__ __forceinline__ uint64_t ld_at_nt(const uint64_t* base, uint32_t byte_off) {
+    return __builtin_nontemporal_load(reinterpret_cast<const uint64_t*>(reinterpret_cast<const char*>(base) + byte_off));
+}
+
+// The combine of one thread's words (lane rl of block blk, words rl + 16 k for k = 8g .. 8g+7), after the transform.
+// kTa: the addends are formed from the product's inputs (else read from the addend).  Every pointer and constant is
+// derived from the kernel arguments and the job when needed, so that nothing of it is held in registers across the
+// transform.  Each word's loads are issued before the previous word's arithmetic (the first word's before the
+// transform's last exchange).
+template <int kD, bool kTa>
+struct MdrEpi {
+    struct First {
+        uint64_t xv[kD], e0[kD], e1[kD], u0, u1, u2, u3;
+    };
+    const MdrFuse& f;
+    const PrimeInfo& P;
+    uint32_t i, c, g;  // limb, ciphertext, the thread's group (= the poly whose tile it transformed)
+
+    __device__ __forceinline__ void load(First& B, int blk, int rl, int k) const {
+        const uint32_t bo = (256 * blk + rl + 16 * k) * 8;  // byte offset of the word within a limb
+        const size_t li = (size_t)i * kN, xs = (size_t)f.E * kN, es = (size_t)f.T * kN, pw = (size_t)f.l * kN;
+        const uint64_t* x = f.ext + (size_t)c * kD * f.E * kN + li;
+        const uint64_t* e = f.evk + li;
+#pragma unroll
+        for (int d = 0; d < kD; d++) {
+            B.xv[d] = ld_at(x + d * xs, bo);
+            B.e0[d] = ld_at(e + (2 * d) * es, bo);
+            B.e1[d] = ld_at(e + (2 * d + 1) * es, bo);
+        }
+        if (kTa) {
+            const uint64_t* a = f.ta + (size_t)c * 2 * pw + li;
+            const uint64_t* b = f.tb + (size_t)c * 2 * pw + li;
+            B.u0 = ld_at_nt(a, bo);       // a0
+            B.u1 = ld_at_nt(a + pw, bo);  // a1
+            B.u2 = ld_at_nt(b, bo);       // b0
+            B.u3 = ld_at_nt(b + pw, bo);  // b1
+        } else {
+            B.u0 = ld_at_nt(f.add + 2 * c * f.add_pstride + li, bo);
+            B.u1 = ld_at_nt(f.add + (2 * c + 1) * f.add_pstride + li, bo);
+        }
+    }
+
+    __device__ __forceinline__ First begin(int blk, int rl) const {
+        First B;
+        load(B, blk, rl, 8 * g);
+        return B;
+    }
+
+    // L: this group's tile; the tiles of polys 0 and 1 are adjacent (kLdsWords apart)
+    __device__ __forceinline__ void end(First cur, const uint64_t* L, int blk, int rl) const {
+        const uint64_t* L0 = L - g * kLdsWords;
+        const uint64_t* L1 = L0 + kLdsWords;
+        const size_t po = (size_t)(f.l - 1) * kN;
+        uint64_t* out0 = f.out + 2 * c * po + (size_t)i * kN;
+        uint64_t* out1 = out0 + po;
+        const Barrett br = barrett_of(P);
+        const uint64_t q = br.q;
+        const TwPair pinv = f.pinv[i], qlinv = f.qlinv[i];
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+            const int k = 8 * g + kk;
+            First nxt;
+            if (kk < 7) load(nxt, blk, rl, k + 1);
+            Acc s0, s1;
+#pragma unroll
+            for (int d = 0; d < kD; d++) {
+                s0.add(cur.xv[d], cur.e0[d]);
+                s1.add(cur.xv[d], cur.e1[d]);
+            }
+            uint64_t v0 = shoup(reduce_sum(s0, br), pinv.w, pinv.wp, q);
+            uint64_t v1 = shoup(reduce_sum(s1, br), pinv.w, pinv.wp, q);
+            if (kTa) {
+                Acc t0, t1;
+                t0.add(cur.u0, cur.u2);  // a0 b0
+                t1.add(cur.u0, cur.u3);  // a0 b1
+                t1.add(cur.u1, cur.u2);  // a1 b0
+                v0 = add_mod(v0, reduce_sum(t0, br), q);
+                v1 = add_mod(v1, reduce_sum(t1, br), q);
+            } else {
+                v0 = add_mod(v0, cur.u0, q);
+                v1 = add_mod(v1, cur.u1, q);
+            }
+            v0 = sub_mod(v0, L0[rl + 17 * k], q);
+            v1 = sub_mod(v1, L1[rl + 17 * k], q);
+            const uint32_t bo = (256 * blk + rl + 16 * k) * 8;
+            __builtin_nontemporal_store(shoup(v0, qlinv.w, qlinv.wp, q),
+                                        reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out0) + bo));
+            __builtin_nontemporal_store(shoup(v1, qlinv.w, qlinv.wp, q),
+                                        reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out1) + bo));
+            if (kk < 7) cur = nxt;
+        }
+    }
+};
+
+// grid (16 tiles, B (l-1) jobs), 512 threads; job v = i B + c (limb-major: a limb's evk is shared by the batch)
+template <int kD, bool kTa>
+__global__ __launch_bounds__(2 * kTileThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_ntt_fwd_b_mdr(
+    uint64_t* T, const TwPair* tw_all, const PrimeInfo* primes, MdrFuse f) {
+    __shared__ uint64_t lds[2 * kLdsWords];
+    const uint32_t i = blockIdx.y / f.B, c = blockIdx.y - i * f.B;
+    const uint32_t g = threadIdx.x >> 8, t = threadIdx.x & 255;
+    const PrimeInfo& P = primes[i];
+    const MdrEpi<kD, kTa> epi{f, P, i, c, g};
+    uint64_t* a = T + ((size_t)(2 * c + g) * (f.l - 1) + i) * kN;
+    const TwPair* tw = tw_all + (size_t)i * kN;
+    if (P.q < kOpenMaxQ)
+        fwd_b_tile<true>(a, tw, P, blockIdx.x, t, lds + g * kLdsWords, epi);
+    else
+        fwd_b_tile<false>(a, tw, P, blockIdx.x, t, lds + g * kLdsWords, epi);
+}
+
+template <int kD>
+void launch_b_mdr(dim3 grid, dim3 block, hipStream_t st, uint64_t* T, const TwPair* twb, const PrimeInfo* primes,
+                  const MdrFuse& f) {
+    if (f.ta)
+        hipLaunchKernelGGL((k_ntt_fwd_b_mdr<kD, true>), grid, block, 0, st, T, twb, primes, f);
+    else
+        hipLaunchKernelGGL((k_ntt_fwd_b_mdr<kD, false>), grid, block, 0, st, T, twb, primes, f);
+}
+
 // Fused: one limb per workgroup of 4 x 256 threads; each 256-thread group owns one LDS tile.
 constexpr int kFusedGroups = 2;
 
@@ -602,6 +770,56 @@ hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js_in, 
     hipError_t err = launch_ntt_kernels(ctx, data, js, n_jobs, inverse, mode, tw, twb, st);
     prof_end(ctx, pi, st);
     return err;
+}
+
+// Forward NTT of a relinearization's ModDown term T [2B][l-1][N] (coefficients, limb i over prime i) whose pass B
+// ends in the combine (k_ntt_fwd_b_mdr): out [2B][l-1][N] = (x P^-1 + add - NTT(T)) q_{l-1}^-1 with x the evk inner
+// product of ext [B][D][E][N] and evk, add from ta/tb (the product's inputs) or add.  T is left holding
+// the first pass's intermediate.  Digit counts 1..4 (others: hipErrorInvalidValue, the caller runs the two kernels).
+hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint32_t l, const uint64_t* ext,
+                              const uint64_t* evk, const uint64_t* ta, const uint64_t* tb, const uint64_t* add,
+                              uint64_t add_pstride, uint64_t* out, const TwPair* pinv, const TwPair* qlinv,
+                              hipStream_t st) {
+    const uint32_t D = (l + ctx.alpha - 1) / ctx.alpha, E = l + ctx.K;
+    if (l < 2 || l > kMaxPmap || B == 0 || D < 1 || D > 4 || (ta && (!tb || add)) || (!ta && !add))
+        return hipErrorInvalidValue;
+    JobSpec js{};
+    js.n_polys = 2 * B;
+    js.period = l - 1;
+    js.n_primes = l - 1;
+    for (uint32_t i = 0; i + 1 < l; i++) js.pmap[i] = (uint8_t)i;
+    MdrFuse f{};
+    f.ext = ext;
+    f.evk = evk;
+    f.ta = ta;
+    f.tb = tb;
+    f.add = add;
+    f.add_pstride = add_pstride;
+    f.out = out;
+    f.B = B;
+    f.l = l;
+    f.E = E;
+    f.T = ctx.L + ctx.K;
+    for (uint32_t i = 0; i + 1 < l; i++) {
+        f.pinv[i] = pinv[i];
+        f.qlinv[i] = qlinv[i];
+    }
+    const uint32_t n_jobs = 2 * B * (l - 1);
+    // algorithmic bytes: T read and written by pass A, read by pass B; per ciphertext and limb D ext limbs, the
+    // 4 product inputs or 2 addend limbs, 2 outputs; the level's evk limbs and the twiddle tables once
+    const double limbs = (double)n_jobs * 3 + (double)B * (l - 1) * (D + (ta ? 4 : add ? 2 : 0) + 2) +
+                         2.0 * D * (l - 1);
+    const int pi = prof_begin(ctx, "ntt_fwd_mdr", limbs * kN * 8 + (double)(l - 1) * kN * sizeof(TwPair), st);
+    hipLaunchKernelGGL(k_ntt_fwd_a, dim3(16, n_jobs), dim3(kTileThreads), 0, st, T, js, ctx.d_tw, ctx.d_primes);
+    const dim3 grid(16, B * (l - 1)), block(2 * kTileThreads);
+    switch (D) {
+        case 1: launch_b_mdr<1>(grid, block, st, T, ctx.d_twb, ctx.d_primes, f); break;
+        case 2: launch_b_mdr<2>(grid, block, st, T, ctx.d_twb, ctx.d_primes, f); break;
+        case 3: launch_b_mdr<3>(grid, block, st, T, ctx.d_twb, ctx.d_primes, f); break;
+        default: launch_b_mdr<4>(grid, block, st, T, ctx.d_twb, ctx.d_primes, f); break;
+    }
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
 }
 
 hipError_t launch_ntt_kernels(const Context& ctx, uint64_t* data, const JobSpec& js, uint32_t n_jobs, bool inverse,

@@ -43,6 +43,10 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
                                  uint64_t add_pstride, const uint64_t* T, uint64_t* out, uint32_t B, uint32_t l,
                                  const TwPair* pinv, const TwPair* qlinv, hipStream_t st,
                                  const uint64_t* ta = nullptr, const uint64_t* tb = nullptr);
+hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint32_t l, const uint64_t* ext,
+                              const uint64_t* evk, const uint64_t* ta, const uint64_t* tb, const uint64_t* add,
+                              uint64_t add_pstride, uint64_t* out, const TwPair* pinv, const TwPair* qlinv,
+                              hipStream_t st);
 hipError_t launch_sub_scale(const Context& ctx, const uint64_t* x, uint64_t x_pstride, const uint64_t* y,
                             uint64_t y_pstride, const uint64_t* add, uint64_t add_pstride, uint32_t add_div,
                             uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
@@ -467,6 +471,14 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
                           pinv[l - 1], st));
     std::vector<uint32_t> pm(l - 1);
     for (uint32_t i = 0; i + 1 < l; i++) pm[i] = i;
+    // a relinearization: T's forward NTT finishes with the combine in its second pass (the addend formed from the
+    // product's inputs, or read), so T is never stored in evaluation form
+    const uint32_t D = num_digits(ctx, l);
+    if (ext && ctx.ntt_mode == NttMode::TwoPass && D <= 4) {
+        HIPX(launch_ntt_fwd_mdr(ctx, T, n_polys / 2, l, ext, evk, ta, tb, ta ? nullptr : add, (uint64_t)l * W, out,
+                                pinv.data(), qlinv.data(), st));
+        return;
+    }
     HIPX(launch_ntt(ctx, T, regular_jobs(n_polys, pm), n_polys * (l - 1), false, ctx.ntt_mode, st));
     if (ext && ta)  // the addend formed from the product's inputs (add holds limb l-1 only, read above)
         HIPX(launch_mdr_combine_ks(ctx, ext, evk, nullptr, 0, T, out, n_polys / 2, l, pinv.data(), qlinv.data(), st,

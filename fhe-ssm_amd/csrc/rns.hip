@@ -9,20 +9,12 @@
 #include <algorithm>
 
 #include "engine.hpp"
+#include "ks_device.hpp"
 #include "modarith.hpp"
 
 namespace fhe {
 
 namespace {
-
-__device__ __forceinline__ Barrett barrett_of(const PrimeInfo& p) { return Barrett{p.q, p.mu_hi, p.mu_lo}; }
-
-__device__ __forceinline__ uint64_t reduce_u128(const U128& x, const Barrett& b) {
-    // hi may exceed q when several products were summed; fold it once (hi < 2^6 q in our uses)
-    uint64_t hi = x.hi;
-    if (hi >= b.q) hi = hi % b.q;
-    return reduce128(hi, x.lo, b);
-}
 
 // Montgomery's REDC with R = 2^64: x < q R -> x R^-1 mod q in [0, q).  m = x_lo (-q^-1) mod 2^64 makes x + m q a
 // multiple of R; its low word sums to R exactly when x_lo != 0, so (x + m q) / R = x_hi + hi(m q) + [x_lo != 0],
@@ -312,38 +304,7 @@ static void (*bconv_kernel(uint32_t n_in))(const uint64_t*, uint64_t*, BConvArgs
 // acc[c][0][t] = sum_d ext[c][d][t] * evk[d][0][prime(t)],  acc[c][1][t] = ... * evk[d][1][prime(t)]
 // One thread per (c, k, t), the ciphertext index fastest in the grid: the workgroups that read one evk tile run
 // back to back, so each XCD fetches the tile once into its L2 and every load of a thread is independent.
-constexpr int kMaxDigits = 8;
 
-// The evk inner product of one extended word over D <= kMaxDigits digits: s0 += sum_d x[d xs] e[2d es],
-// s1 += sum_d x[d xs] e[(2d+1) es].  Every digit's loads are issued before the first product waits on them (a
-// load-multiply loop per digit makes each digit a separate round trip to memory).
-// kStreamX: the extension words are read once (no other item shares them): nontemporal loads.
-template <bool kStreamX = false>
-__device__ __forceinline__ void ks_dot(const uint64_t* __restrict__ x, size_t xs, const uint64_t* __restrict__ e,
-                                       size_t es, uint32_t D, Acc& s0, Acc& s1) {
-    uint64_t xv[kMaxDigits], e0[kMaxDigits], e1[kMaxDigits];
-#pragma unroll
-    for (int d = 0; d < kMaxDigits; d++) {
-        if (d < (int)D) {
-            xv[d] = kStreamX ? __builtin_nontemporal_load(&x[(size_t)d * xs]) : x[(size_t)d * xs];
-            e0[d] = e[((size_t)d * 2 + 0) * es];
-            e1[d] = e[((size_t)d * 2 + 1) * es];
-        }
-    }
-#pragma unroll
-    for (int d = 0; d < kMaxDigits; d++) {
-        if (d < (int)D) {
-            s0.add(xv[d], e0[d]);
-            s1.add(xv[d], e1[d]);
-        }
-    }
-}
-
-struct InnerArgs {
-    uint32_t D, E, T, B;
-    uint32_t t0;  // first extended limb computed (k_ks_inner: limbs t0..E-1)
-    uint8_t prime_of[kMaxPmap];
-};
 
 __global__ __launch_bounds__(256) void k_ks_inner(const uint64_t* __restrict__ ext, const uint64_t* __restrict__ evk,
                                                   uint64_t* __restrict__ acc, InnerArgs ia,
@@ -502,13 +463,6 @@ __global__ __launch_bounds__(256) void k_ks_sub_list(ListPtrs ext, ListPtrs evk,
 // the same words with one forward NTT of l-1 limbs instead of two (l for conv, l-1 for the lift).  The BConv
 // writes T directly (k_bconv<NIN, true>); in a relinearization the evk inner product of limbs 0..l-2 is formed inside
 // the combine (k_mdr_combine_ks) and never stored.
-struct MdrArgs {
-    uint32_t l;           // limbs before the rescale
-    uint64_t x_pstride;   // words between polys of x ([E][N] each)
-    uint64_t add_pstride; // words between polys of add (0: no addend)
-    TwPair pinv[kMaxPmap];   // P^-1 mod q_i
-    TwPair qlinv[kMaxPmap];  // q_{l-1}^-1 mod q_i
-};
 
 // out_i = (add_i + x_i P^-1 - T_i) q_{l-1}^-1 in evaluation form, i < l-1
 __global__ __launch_bounds__(256) void k_mdr_combine(const uint64_t* __restrict__ x, const uint64_t* __restrict__ add,
@@ -567,12 +521,6 @@ __global__ __launch_bounds__(256) void k_mdr_combine_ks(const uint64_t* __restri
         __builtin_nontemporal_store(shoup(v, ma.qlinv[i].w, ma.qlinv[i].wp, q), &out[pc * po + li]);
     }
 }
-
-// limb t of batch item c: dst + c * dst_bstride + off[t] * N  <-  src + c * src_bstride + t * N (a batch of
-// polynomials copied into the digit-own limbs of the ModUp extension buffer in one launch)
-struct LimbMap {
-    uint16_t off[kMaxPmap];
-};
 
 // dst[c] = src[c] for up to 64 items of `words` words each (gathers scattered ciphertexts into one batch)
 __global__ __launch_bounds__(256) void k_gather(ListPtrs src, uint64_t* __restrict__ dst, uint64_t words) {
