@@ -143,7 +143,8 @@ struct Acc30 {
         s2 += (uint64_t)a1 * b1;
     }
     // the sum as 128 bits: s0 + s1 2^30 + s2 2^60
-    __device__ __forceinline__ U128 get() const {
+    __device__ __forceinline__ U128 get() const { return combine30(s0, s1, s2); }
+    __device__ __forceinline__ static U128 combine30(uint64_t s0, uint64_t s1, uint64_t s2) {
         const uint64_t m = s1 << 30, t = s2 << 60;
         uint64_t lo = s0 + m;
         uint64_t hi = (s1 >> 34) + (s2 >> 4) + (lo < m ? 1u : 0u);
@@ -151,6 +152,21 @@ struct Acc30 {
         hi += (lo < t) ? 1u : 0u;
         return U128{lo, hi};
     }
+};
+
+// Acc30 with three multiply-adds a term (Karatsuba): s0 += a0 b0, s2 += a1 b1 and sm += (a0 + a1)(b0 + b1) mod 2^64;
+// the middle sum is s1 = sm - s0 - s2 mod 2^64, exact because the true s1 is below 2^64 (the Acc30 bound).  The
+// caller passes a0 + a1 (< 2^31) with the halves; b0 + b1 of a wave-uniform constant is a scalar add.
+struct Acc30k {
+    uint64_t s0, s2, sm;
+    __device__ __forceinline__ Acc30k() : s0(0), s2(0), sm(0) {}
+    __device__ __forceinline__ void add(uint32_t a0, uint32_t a1, uint32_t as, uint64_t bp) {
+        const uint32_t b0 = (uint32_t)bp, b1 = (uint32_t)(bp >> 32);
+        s0 += (uint64_t)a0 * b0;
+        s2 += (uint64_t)a1 * b1;
+        sm += (uint64_t)as * (b0 + b1);
+    }
+    __device__ __forceinline__ U128 get() const { return Acc30::combine30(s0, sm - s0 - s2, s2); }
 };
 
 }  // namespace fhe

@@ -141,7 +141,7 @@ __device__ __forceinline__ uint64_t lift_centered(uint64_t v, uint64_t ql, const
     return v >= q ? reduce128(0, v, br) : v;
 }
 
-// Extra inputs of the ModDown BConv fused with the rescale that follows (k_bconv<NIN, true>).  The plan's last
+// Extra inputs of the ModDown BConv fused with the rescale that follows (k_bconv<NIN, true, ..>).  The plan's last
 // output column is the dropped limb l-1 (plain table); every other column j has P^-1 mod q_j folded into its
 // table, so the column sums are conv_j P^-1 directly.  Per coefficient the kernel forms
 //   z = addc + (x_{l-1} - conv_{l-1}) P^-1  (mod q_{l-1}, x_{l-1} and addc in coefficient form)
@@ -154,12 +154,15 @@ struct MdrBconvArgs {
 };
 
 // NIN = number of input limbs (a template parameter: the term loops unroll without run-time guards).  The table's
-// q-hat constants are stored pre-split into 30-bit halves (pack30), the y_i are split once, and every term is four
-// multiply-adds into carry-free sums (Acc30; inputs taken in chunks of at most 8).
-template <int NIN, bool kMdr>
+// q-hat constants are stored pre-split into 30-bit halves (pack30), the y_i are split once, and every term is three
+// multiply-adds into carry-free sums (Acc30k; inputs taken in chunks of at most 8).
+// kMont: the plan is Montgomery-reduced and not centered (ba.mont and !ba.centered known at compile time, so no
+// per-output tests of the flags).
+template <int NIN, bool kMdr, bool kMont>
 __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
                                                BConvArgs ba, const uint64_t* __restrict__ tab,
                                                const PrimeInfo* __restrict__ primes, MdrBconvArgs mb) {
+    const bool centered = kMont ? false : ba.centered != 0, mont = kMont ? true : ba.mont != 0;
     const uint32_t k = blockIdx.x * 256 + threadIdx.x;
     const uint32_t c = blockIdx.y;
     const uint64_t* src = in + c * ba.in_bstride + k;
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
     const TwPair* qhinv = reinterpret_cast<const TwPair*>(tab);
     const uint64_t* qhmod = tab + 2 * ba.n_in;  // [n_in][n_out], pack30 form
     uint64_t y[NIN];
-    uint32_t y0[NIN], y1[NIN];
+    uint32_t y0[NIN], y1[NIN], ys[NIN];
 #pragma unroll
     for (int i = 0; i < NIN; i++) {
         const uint64_t q = primes[desc_prime(ba.in_desc[i])].q;
@@ -175,6 +178,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
                      q);
         y0[i] = (uint32_t)y[i] & 0x3FFFFFFFu;
         y1[i] = (uint32_t)(y[i] >> 30);
+        ys[i] = y0[i] + y1[i];
     }
     // centered form (exact ModDown): u = round(sum_i y_i / q_i) from the 128-bit fixed-point sum of
     // floor(y_i * floor(2^128 / q_i) / 2^64); the table then holds [n_in] (lo, hi) words of floor(2^128 / q_i)
@@ -182,7 +186,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
     uint64_t u = 0;
     const uint64_t* cfix = qhmod + (size_t)ba.n_in * ba.n_out;
     const uint64_t* pmod = cfix + 2 * ba.n_in;
-    if (ba.centered) {
+    if (centered) {
         U128 F{0, 0};
 #pragma unroll
         for (int i = 0; i < NIN; i++) {
@@ -196,20 +200,20 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
     }
     // column sums of outputs j and j2 (= j when only one is wanted), before the final reduction
     auto sums = [&](uint32_t j, uint32_t j2, U128& r, U128& r2) {
-        Acc30 a, b;
+        Acc30k a, b;
 #pragma unroll
         for (int i = 0; i < (NIN < 8 ? NIN : 8); i++) {
-            a.add(y0[i], y1[i], qhmod[(size_t)i * ba.n_out + j]);
-            b.add(y0[i], y1[i], qhmod[(size_t)i * ba.n_out + j2]);
+            a.add(y0[i], y1[i], ys[i], qhmod[(size_t)i * ba.n_out + j]);
+            b.add(y0[i], y1[i], ys[i], qhmod[(size_t)i * ba.n_out + j2]);
         }
         r = a.get();
         r2 = b.get();
         if constexpr (NIN > 8) {
-            Acc30 a2, b2;
+            Acc30k a2, b2;
 #pragma unroll
             for (int i = 8; i < NIN; i++) {
-                a2.add(y0[i], y1[i], qhmod[(size_t)i * ba.n_out + j]);
-                b2.add(y0[i], y1[i], qhmod[(size_t)i * ba.n_out + j2]);
+                a2.add(y0[i], y1[i], ys[i], qhmod[(size_t)i * ba.n_out + j]);
+                b2.add(y0[i], y1[i], ys[i], qhmod[(size_t)i * ba.n_out + j2]);
             }
             const U128 s = a2.get(), s2 = b2.get();
             r.lo += s.lo;
@@ -220,7 +224,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
     };
     // the centered correction: acc - u * pmod_j, kept non-negative by adding 16 p_j (u <= n_in <= 16)
     auto correct = [&](U128& acc, uint32_t j, const Barrett& br) {
-        if (ba.centered) {
+        if (centered) {
             const uint64_t t = 16 * br.q - u * pmod[j];
             acc.lo += t;
             acc.hi += (acc.lo < t) ? 1 : 0;
@@ -235,7 +239,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         const PrimeInfo& pl = primes[desc_prime(ba.out_desc[n_main])];
         const Barrett bl = barrett_of(pl);
         correct(acc, n_main, bl);
-        const uint64_t conv = ba.mont ? redc(acc, pl.q, pl.mont_ninv) : reduce_u128(acc, bl);
+        const uint64_t conv = mont ? redc(acc, pl.q, pl.mont_ninv) : reduce_u128(acc, bl);
         ql = bl.q;
         z = shoup(sub_mod(mb.xlast[c * mb.xlast_pstride + k], conv, ql), mb.pinv_last.w, mb.pinv_last.wp, ql);
         if (mb.addc) z = add_mod(z, mb.addc[(size_t)c * kN + k], ql);
@@ -246,7 +250,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         const Barrett br = barrett_of(pj);
         correct(acc, j, br);
         uint64_t v;
-        if (ba.mont) {
+        if (mont) {
             v = redc(acc, pj.q, pj.mont_ninv);
             if constexpr (kMdr) v = add_mod(v, lift_centered(z, ql, br), pj.q);
         } else {
@@ -276,28 +280,35 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
 }
 
 // k_bconv instance for a run-time input count (1..kMaxBconvIn)
-template <bool kMdr>
-static void (*bconv_kernel(uint32_t n_in))(const uint64_t*, uint64_t*, BConvArgs, const uint64_t*, const PrimeInfo*,
-                                           MdrBconvArgs) {
+template <bool kMdr, bool kMont>
+static void (*bconv_kernel_m(uint32_t n_in))(const uint64_t*, uint64_t*, BConvArgs, const uint64_t*,
+                                             const PrimeInfo*, MdrBconvArgs) {
     switch (n_in) {
-        case 1: return k_bconv<1, kMdr>;
-        case 2: return k_bconv<2, kMdr>;
-        case 3: return k_bconv<3, kMdr>;
-        case 4: return k_bconv<4, kMdr>;
-        case 5: return k_bconv<5, kMdr>;
-        case 6: return k_bconv<6, kMdr>;
-        case 7: return k_bconv<7, kMdr>;
-        case 8: return k_bconv<8, kMdr>;
-        case 9: return k_bconv<9, kMdr>;
-        case 10: return k_bconv<10, kMdr>;
-        case 11: return k_bconv<11, kMdr>;
-        case 12: return k_bconv<12, kMdr>;
-        case 13: return k_bconv<13, kMdr>;
-        case 14: return k_bconv<14, kMdr>;
-        case 15: return k_bconv<15, kMdr>;
-        case 16: return k_bconv<16, kMdr>;
+        case 1: return k_bconv<1, kMdr, kMont>;
+        case 2: return k_bconv<2, kMdr, kMont>;
+        case 3: return k_bconv<3, kMdr, kMont>;
+        case 4: return k_bconv<4, kMdr, kMont>;
+        case 5: return k_bconv<5, kMdr, kMont>;
+        case 6: return k_bconv<6, kMdr, kMont>;
+        case 7: return k_bconv<7, kMdr, kMont>;
+        case 8: return k_bconv<8, kMdr, kMont>;
+        case 9: return k_bconv<9, kMdr, kMont>;
+        case 10: return k_bconv<10, kMdr, kMont>;
+        case 11: return k_bconv<11, kMdr, kMont>;
+        case 12: return k_bconv<12, kMdr, kMont>;
+        case 13: return k_bconv<13, kMdr, kMont>;
+        case 14: return k_bconv<14, kMdr, kMont>;
+        case 15: return k_bconv<15, kMdr, kMont>;
+        case 16: return k_bconv<16, kMdr, kMont>;
         default: return nullptr;
     }
+}
+
+template <bool kMdr>
+static void (*bconv_kernel(const BConvPlan& plan))(const uint64_t*, uint64_t*, BConvArgs, const uint64_t*,
+                                                   const PrimeInfo*, MdrBconvArgs) {
+    if (plan.mont && !plan.centered) return bconv_kernel_m<kMdr, true>(plan.n_in);
+    return bconv_kernel_m<kMdr, false>(plan.n_in);
 }
 
 // ------------------------------------------------------------------ key-switch inner product
@@ -461,7 +472,7 @@ __global__ __launch_bounds__(256) void k_ks_sub_list(ListPtrs ext, ListPtrs evk,
 //   out_i = (add_i + x_i P^-1 - NTT(T_i)) q_l^-1,  T_i = conv_i P^-1 + lift(z)_i,
 //   z = INTT(add_{l-1}) + (INTT(x_{l-1}) - conv_{l-1}) P^-1   (mod q_{l-1}):
 // the same words with one forward NTT of l-1 limbs instead of two (l for conv, l-1 for the lift).  The BConv
-// writes T directly (k_bconv<NIN, true>); in a relinearization the evk inner product of limbs 0..l-2 is formed inside
+// writes T directly (k_bconv<NIN, true, ..>); in a relinearization the evk inner product of limbs 0..l-2 is formed inside
 // the combine (k_mdr_combine_ks) and never stored.
 
 // out_i = (add_i + x_i P^-1 - T_i) q_{l-1}^-1 in evaluation form, i < l-1
@@ -1068,7 +1079,7 @@ hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_
         return hipErrorInvalidValue;
     const BConvArgs ba = bconv_args(plan, in_bstride, in_off, out_bstride, out_off, plan.n_out);
     const int pi = prof_begin(ctx, "bconv", (double)B * (plan.n_in + plan.n_out) * kN * 8, st);
-    hipLaunchKernelGGL(bconv_kernel<false>(plan.n_in), dim3(kN / 256, B), dim3(256), 0, st, in, out, ba, plan.d_tab,
+    hipLaunchKernelGGL(bconv_kernel<false>(plan), dim3(kN / 256, B), dim3(256), 0, st, in, out, ba, plan.d_tab,
                        ctx.d_primes, MdrBconvArgs{});
     prof_end(ctx, pi, st);
     return hipGetLastError();
@@ -1090,7 +1101,7 @@ hipError_t launch_bconv_mdr(const Context& ctx, const BConvPlan& plan, const uin
     // P limbs + limb l-1 (+ the addend's) read, l-1 limbs written
     const double bytes = (double)n_polys * (plan.n_in + 1 + (addc ? 1 : 0) + (l - 1)) * kN * 8;
     const int pi = prof_begin(ctx, "bconv_mdr", bytes, st);
-    hipLaunchKernelGGL(bconv_kernel<true>(plan.n_in), dim3(kN / 256, n_polys), dim3(256), 0, st, in, T, ba,
+    hipLaunchKernelGGL(bconv_kernel<true>(plan), dim3(kN / 256, n_polys), dim3(256), 0, st, in, T, ba,
                        plan.d_tab, ctx.d_primes, mb);
     prof_end(ctx, pi, st);
     return hipGetLastError();
