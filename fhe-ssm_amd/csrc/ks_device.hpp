@@ -56,4 +56,14 @@ struct MdrArgs {
     TwPair qlinv[kMaxPmap];  // q_{l-1}^-1 mod q_i
 };
 
+// ModDown combine: out = (x - y) s_i (+ the addend), over [n_polys][l][N] (k_sub_scale and the forward NTT that ends
+// in it)
+struct CombineArgs {
+    uint32_t l;                 // limbs per poly of out/y/add
+    uint32_t add_div, add_group;  // polys pc % add_div == 0 get addend (pc / add_group) * add_pstride
+    uint64_t x_pstride;         // words between polys of x (x may carry extra limbs, e.g. P limbs)
+    uint64_t y_pstride, out_pstride, add_pstride;
+    TwPair s[kMaxPmap];
+};
+
 }  // namespace fhe

@@ -686,6 +686,82 @@ void launch_b_mdr(dim3 grid, dim3 block, hipStream_t st, uint64_t* T, const TwPa
         hipLaunchKernelGGL((k_ntt_fwd_b_mdr<kD, false>), grid, block, 0, st, T, twb, primes, f);
 }
 
+// ---------------------------------------------------------------- forward pass B that finishes a plain ModDown
+// The forward NTT of a ModDown's converted P part y ([n_polys][l] limbs, dense) ends with the combine of k_sub_scale
+// instead of a store of y: out[pc][i] = (x[pc][i] - y[pc][i]) s_i (+ the addend for polys pc % add_div == 0, read at
+// (pc / add_group) add_pstride).  The same words as the NTT followed by k_sub_scale, without y's store and reload.
+struct SubEpi {
+    struct First {
+        uint64_t xv[4];
+    };
+    // the pointers and constants are derived when needed (nothing of them held in registers across the transform)
+    const CombineArgs& ca;
+    const uint64_t* xb;    // x
+    const uint64_t* addb;  // the addend, or null
+    uint64_t* outb;        // out
+    const PrimeInfo& P;
+    uint32_t i, pc;
+
+    __device__ __forceinline__ const uint64_t* xp() const { return xb + pc * ca.x_pstride + (size_t)i * kN; }
+
+    __device__ __forceinline__ First begin(int blk, int rl) const {
+        First B;
+        const uint32_t bo = (256 * blk + rl) * 8;
+        const uint64_t* x = xp();
+#pragma unroll
+        for (int k = 0; k < 4; k++) B.xv[k] = ld_at_nt(x, bo + 128 * k);
+        return B;
+    }
+
+    // words in two halves of 8, each half's x words (but the 4 loaded ahead) and addends requested together
+    __device__ __forceinline__ void end(First cur, const uint64_t* L, int blk, int rl) const {
+        const uint32_t bo = (256 * blk + rl) * 8;
+        const uint64_t* x = xp();
+        const uint64_t* add =
+            addb && pc % ca.add_div == 0 ? addb + (pc / ca.add_group) * ca.add_pstride + (size_t)i * kN : nullptr;
+        uint64_t* out = outb + pc * ca.out_pstride + (size_t)i * kN;
+        const uint64_t q = P.q;
+        const TwPair s = ca.s[i];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            uint64_t xv[8], av[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                xv[k] = (h == 0 && k < 4) ? cur.xv[k] : ld_at_nt(x, bo + 128 * (8 * h + k));
+            if (add) {
+#pragma unroll
+                for (int k = 0; k < 8; k++) av[k] = ld_at(add, bo + 128 * (8 * h + k));
+            }
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const int kk = 8 * h + k;
+                uint64_t v = shoup(sub_mod(xv[k], L[rl + 17 * kk], q), s.w, s.wp, q);
+                if (add) v = add_mod(v, av[k], q);
+                __builtin_nontemporal_store(v,
+                                            reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out) + bo + 128 * kk));
+            }
+        }
+    }
+};
+
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_ntt_fwd_b_sub(uint64_t* y, JobSpec js, const TwPair* tw_all,
+                                                               const PrimeInfo* primes, CombineArgs ca,
+                                                               const uint64_t* x, const uint64_t* add,
+                                                               uint64_t* out) {
+    __shared__ uint64_t lds[kLdsWords];
+    uint32_t off, prime;
+    job_of(js, blockIdx.y, off, prime);
+    const uint32_t i = blockIdx.y / js.n_polys, pc = blockIdx.y - i * js.n_polys;
+    const PrimeInfo& P = primes[prime];
+    const SubEpi epi{ca, x, add, out, P, i, pc};
+    uint64_t* a = y + (size_t)off * kN;
+    const TwPair* tw = tw_all + (size_t)prime * kN;
+    if (P.q < kOpenMaxQ)
+        fwd_b_tile<true>(a, tw, P, blockIdx.x, threadIdx.x, lds, epi);
+    else
+        fwd_b_tile<false>(a, tw, P, blockIdx.x, threadIdx.x, lds, epi);
+}
+
 // Fused: one limb per workgroup of 4 x 256 threads; each 256-thread group owns one LDS tile.
 constexpr int kFusedGroups = 2;
 
@@ -770,6 +846,40 @@ hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js_in, 
     hipError_t err = launch_ntt_kernels(ctx, data, js, n_jobs, inverse, mode, tw, twb, st);
     prof_end(ctx, pi, st);
     return err;
+}
+
+// Forward NTT of a ModDown's converted P part y [n_polys][l][N] (coefficients, limb i over prime i; dense) whose pass
+// B ends in k_sub_scale's combine: out[pc][i] = (x[pc][i] - NTT(y)[pc][i]) s_i (+ the addend).  y is left holding
+// the first pass's intermediate.  Same argument meaning as launch_sub_scale.
+hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x, uint64_t x_pstride,
+                              const uint64_t* add, uint64_t add_pstride, uint32_t add_div, uint32_t add_group,
+                              uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
+                              hipStream_t st) {
+    if (l == 0 || l > kMaxPmap || n_polys == 0) return hipErrorInvalidValue;
+    JobSpec js{};
+    js.n_polys = n_polys;
+    js.period = l;
+    js.n_primes = l;
+    for (uint32_t i = 0; i < l; i++) js.pmap[i] = (uint8_t)i;
+    CombineArgs ca{};
+    ca.l = l;
+    ca.add_div = add_div ? add_div : 1;
+    ca.add_group = add_group ? add_group : ca.add_div;
+    ca.x_pstride = x_pstride;
+    ca.y_pstride = (uint64_t)l * kN;
+    ca.out_pstride = out_pstride;
+    ca.add_pstride = add_pstride;
+    for (uint32_t i = 0; i < l; i++) ca.s[i] = s[i];
+    const uint32_t n_jobs = n_polys * l;
+    // algorithmic bytes: y read and written by pass A, read by pass B; x read, out written; the addends; tables
+    const double n_add = add ? (double)n_polys / ca.add_div : 0.0;
+    const double bytes = ((double)n_jobs * 5 + n_add * l) * kN * 8 + (double)l * kN * sizeof(TwPair);
+    const int pi = prof_begin(ctx, "ntt_fwd_sub", bytes, st);
+    const dim3 grid(16, n_jobs), block(kTileThreads);
+    hipLaunchKernelGGL(k_ntt_fwd_a, grid, block, 0, st, y, js, ctx.d_tw, ctx.d_primes);
+    hipLaunchKernelGGL(k_ntt_fwd_b_sub, grid, block, 0, st, y, js, ctx.d_twb, ctx.d_primes, ca, x, add, out);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
 }
 
 // Forward NTT of a relinearization's ModDown term T [2B][l-1][N] (coefficients, limb i over prime i) whose pass B

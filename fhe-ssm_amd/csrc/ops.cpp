@@ -43,6 +43,10 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
                                  uint64_t add_pstride, const uint64_t* T, uint64_t* out, uint32_t B, uint32_t l,
                                  const TwPair* pinv, const TwPair* qlinv, hipStream_t st,
                                  const uint64_t* ta = nullptr, const uint64_t* tb = nullptr);
+hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x, uint64_t x_pstride,
+                              const uint64_t* add, uint64_t add_pstride, uint32_t add_div, uint32_t add_group,
+                              uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
+                              hipStream_t st);
 hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint32_t l, const uint64_t* ext,
                               const uint64_t* evk, const uint64_t* ta, const uint64_t* tb, const uint64_t* add,
                               uint64_t add_pstride, uint64_t* out, const TwPair* pinv, const TwPair* qlinv,
@@ -401,7 +405,6 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
     uint64_t* conv = (uint64_t*)ws_get(ctx, WS_CONV, (size_t)n_polys * l * W * 8);
     HIPX(launch_bconv(ctx, plan, x, (uint64_t)xs * W, in_off.data(), conv, (uint64_t)l * W, out_off.data(), n_polys,
                       st));
-    HIPX(launch_ntt(ctx, conv, regular_jobs(n_polys, out_idx), n_polys * l, false, ctx.ntt_mode, st));
     std::vector<TwPair> pinv(l);
     for (uint32_t i = 0; i < l; i++) {
         const uint64_t q = ctx.moduli[i];
@@ -411,6 +414,13 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
         pinv[i] = TwPair{v, shoup_companion(v, q)};
     }
     const uint64_t aps = add_pstride < 0 ? (uint64_t)add_div * l * W : (uint64_t)add_pstride;
+    if (ctx.ntt_mode == NttMode::TwoPass) {
+        // the forward NTT of conv ends in the combine (conv is never stored in evaluation form)
+        HIPX(launch_ntt_fwd_sub(ctx, conv, x, (uint64_t)xs * W, add, aps, add_div, add_group, out, (uint64_t)l * W,
+                                n_polys, l, pinv.data(), st));
+        return;
+    }
+    HIPX(launch_ntt(ctx, conv, regular_jobs(n_polys, out_idx), n_polys * l, false, ctx.ntt_mode, st));
     HIPX(launch_sub_scale(ctx, x, (uint64_t)xs * W, conv, (uint64_t)l * W, add, aps, add_div, out, (uint64_t)l * W,
                           n_polys, l, pinv.data(), st, add_group));
 }

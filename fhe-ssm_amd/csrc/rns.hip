@@ -337,14 +337,6 @@ __global__ __launch_bounds__(256) void k_ks_inner(const uint64_t* __restrict__ e
 // out[c][p][i] = (x[c][p][i] - y[c][p][i]) * s_i  (+ add[c][p][i])  mod q_i,   s_i per-limb constant
 // The addend, if any, is applied to the polys pc with pc % add_div == 0, read at add + (pc / add_div) *
 // add_pstride (add_div = 2 adds c0 of a ciphertext batch to poly 0 of each output ciphertext only).
-struct CombineArgs {
-    uint32_t l;                 // limbs per poly of out/y/add
-    uint32_t add_div, add_group;  // polys pc % add_div == 0 get addend (pc / add_group) * add_pstride
-    uint64_t x_pstride;         // words between polys of x (x may carry extra limbs, e.g. P limbs)
-    uint64_t y_pstride, out_pstride, add_pstride;
-    TwPair s[kMaxPmap];
-};
-
 __global__ __launch_bounds__(256) void k_sub_scale(const uint64_t* __restrict__ x, const uint64_t* __restrict__ y,
                                                    const uint64_t* __restrict__ add, uint64_t* __restrict__ out,
                                                    CombineArgs ca, const PrimeInfo* __restrict__ primes) {
