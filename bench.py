@@ -430,6 +430,8 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native
     from engine_loader import load_module
     DS = load_module("decode_step")
     M = load_module("rwkv_model")
+    free0, total0 = torch.cuda.mem_get_info()
+    mem_before = total0 - free0  # what the process held on the device before config 5's setup
     t0 = time.perf_counter()
     be, sk = DS.build_engine(ckks)
     t_keys = time.perf_counter() - t0
@@ -496,7 +498,8 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native
     ctx.profile_reset()
     s_per_step = sum(times) / len(times)
     free_b2, _ = torch.cuda.mem_get_info()
-    mem = {"device_gb_after_timed_steps": round((total_b - free_b2) / 1e9, 1)}
+    mem = {"device_gb_after_timed_steps": round((total_b - free_b2) / 1e9, 1),
+           "device_gb_in_use_before_setup": round(mem_before / 1e9, 1)}
     if driver == "native":
         mem["decoder_gb"] = {k: round(v / 1e9, 2) for k, v in nat.memory().items()}
     mem["context_gb"] = {k: round(v / 1e9, 2) for k, v in ctx.memory().items()}
@@ -717,7 +720,10 @@ def main():
             extra["bootstrap_config4"] = {k: b[k] for k in ("ms_per_bootstrap", "precision_bits", "levels_in_out",
                                                              "stage_errors", "roofline")}
         if not args.no_decode_line:
-            gc.collect()  # the earlier workloads' contexts, keys and buffers go before config 5's ~230 GB
+            # the earlier workloads' contexts, keys and buffers go before config 5 (and torch's cache returns their
+            # tensors' memory, so the decode line's device figures are config 5's own)
+            gc.collect()
+            torch.cuda.empty_cache()
             d = bench_decode(ckks, torch, 1, 1, args.seed, driver=args.decode_driver)
             line = {"s_per_step": d["s_per_step"], "metric": "s/step for 32-lane decode (config 5)",
                     "roofline": d["roofline"]}
