@@ -724,7 +724,7 @@ def main():
             # tensors' memory, so the decode line's device figures are config 5's own)
             gc.collect()
             torch.cuda.empty_cache()
-            d = bench_decode(ckks, torch, 1, 1, args.seed, driver=args.decode_driver)
+            d = bench_decode(ckks, torch, 2, 1, args.seed, driver=args.decode_driver)  # mean of 2 timed steps
             line = {"s_per_step": d["s_per_step"], "metric": "s/step for 32-lane decode (config 5)",
                     "roofline": d["roofline"]}
             line.update({k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s",
