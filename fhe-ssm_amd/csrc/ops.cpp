@@ -567,9 +567,6 @@ void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uin
     jl.src_period = l;
     HIPX(launch_ntt(ctx, last, jl, n_polys, true, ctx.ntt_mode, st));
     HIPX(launch_lift_centered(ctx, last, W, tmp, n_polys, l - 1, ctx.moduli[l - 1], st));
-    std::vector<uint32_t> pm(l - 1);
-    for (uint32_t i = 0; i + 1 < l; i++) pm[i] = i;
-    HIPX(launch_ntt(ctx, tmp, regular_jobs(n_polys, pm), n_polys * (l - 1), false, ctx.ntt_mode, st));
     std::vector<TwPair> s(l - 1);
     const uint64_t ql = ctx.moduli[l - 1];
     for (uint32_t i = 0; i + 1 < l; i++) {
@@ -577,6 +574,15 @@ void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uin
         const uint64_t v = invmod_h(ql % q, q);
         s[i] = TwPair{v, shoup_companion(v, q)};
     }
+    if (ctx.ntt_mode == NttMode::TwoPass) {
+        // the lifted limbs' forward NTT ends in the combine (out = (in - NTT(tmp)) q_{l-1}^-1)
+        HIPX(launch_ntt_fwd_sub(ctx, tmp, in, (uint64_t)l * W, nullptr, 0, 1, 0, out, (uint64_t)(l - 1) * W, n_polys,
+                                l - 1, s.data(), st));
+        return;
+    }
+    std::vector<uint32_t> pm(l - 1);
+    for (uint32_t i = 0; i + 1 < l; i++) pm[i] = i;
+    HIPX(launch_ntt(ctx, tmp, regular_jobs(n_polys, pm), n_polys * (l - 1), false, ctx.ntt_mode, st));
     HIPX(launch_sub_scale(ctx, in, (uint64_t)l * W, tmp, (uint64_t)(l - 1) * W, nullptr, 0, 1, out,
                           (uint64_t)(l - 1) * W, n_polys, l - 1, s.data(), st));
 }

@@ -137,6 +137,28 @@ def test_eval_mult_rescale_in_place(ckks, ctx, octx, evk, d_evk, alias):
         assert np.array_equal(out[i], octx.hmult_relin_rescale(a[i], b[i], l, evk)), i
 
 
+def test_relin_and_keyswitch_fused_ntt_mode(ckks, ctx, octx, evk, d_evk):
+    """The other NTT schedule (mode 1: one limb per workgroup) takes the unfused combines (k_mdr_combine_ks with the
+    product's inputs, k_sub_scale after the NTT) in place of the NTT passes that end in them: same words."""
+    B, l = 2, 9
+    a = residues(ctx.moduli, (B, 2), list(range(l)), seed=35)
+    b = residues(ctx.moduli, (B, 2), list(range(l)), seed=36)
+    x = residues(ctx.moduli, (1,), list(range(l)), seed=37)
+    da, db, dx = (ckks.DeviceBuffer.from_array(v) for v in (a, b, x))
+    dout = ckks.DeviceBuffer(B * 2 * (l - 1) * N * 8)
+    dks = ckks.DeviceBuffer(2 * l * N * 8)
+    ctx.set_ntt_mode(1)
+    try:
+        ctx.eval_mult_rescale(da.ptr, db.ptr, B, l, d_evk.ptr, dout.ptr)
+        ctx.keyswitch(dx.ptr, 1, l, d_evk.ptr, dks.ptr)
+    finally:
+        ctx.set_ntt_mode(0)
+    out = dout.download((B, 2, l - 1, N))
+    for i in range(B):
+        assert np.array_equal(out[i], octx.hmult_relin_rescale(a[i], b[i], l, evk)), i
+    assert np.array_equal(dks.download((2, l, N)), octx.keyswitch(x[0], l, evk))
+
+
 def test_eval_mult_no_rescale(ckks, ctx, octx, evk, d_evk):
     l = 9
     a = residues(ctx.moduli, (1, 2), list(range(l)), seed=41)
