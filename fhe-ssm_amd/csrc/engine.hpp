@@ -54,6 +54,11 @@ struct JobSpec {
     uint64_t* copy;
     uint64_t copy_pstride;
     uint32_t copy_alpha, copy_E;
+    // Forward dense specs (two-pass mode only): lift, if set, is read in place of the buffer -- the input of limb l of
+    // poly p is the centered lift of lift[p * lift_pstride + k] (a residue mod lift_q, above lift_q / 2 standing for
+    // a negative value) into limb l's prime: a rescale's dropped limb spread over the kept ones.
+    const uint64_t* lift;
+    uint64_t lift_pstride, lift_q;
 };
 
 enum class NttMode { TwoPass = 0, Fused = 1 };

@@ -15,6 +15,17 @@ __device__ __forceinline__ uint64_t reduce_u128(const U128& x, const Barrett& b)
     return reduce128(hi, x.lo, b);
 }
 
+// centered residue of v in [0, ql) modulo q: v > ql/2 stands for v - ql (harness/boot_overflow_probe.cpp:93-94)
+__device__ __forceinline__ uint64_t lift_centered(uint64_t v, uint64_t ql, const Barrett& br) {
+    const uint64_t q = br.q;
+    if (v > (ql >> 1)) {
+        const uint64_t neg = ql - v;  // value is -neg
+        const uint64_t m = neg >= q ? reduce128(0, neg, br) : neg;
+        return m ? q - m : 0;
+    }
+    return v >= q ? reduce128(0, v, br) : v;
+}
+
 constexpr int kMaxDigits = 8;
 
 // The evk inner product of one extended word over D <= kMaxDigits digits: s0 += sum_d x[d xs] e[2d es],

@@ -194,15 +194,24 @@ __device__ __forceinline__ uint64_t canon8(uint64_t v, uint64_t q) {
 
 // ---------------------------------------------------------------- forward pass A (strided columns)
 // tile: columns [16*tile, 16*tile + 16).  g: thread id within the 256-thread group.
-template <bool kOpen>
+// lift (optional): the words are read from there and lifted (centered, from residues mod lq) into this prime
+template <bool kOpen, bool kLift = false>
 __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPair* __restrict__ tw, uint64_t q,
-                                           int tile, int g, uint64_t* lds) {
+                                           int tile, int g, uint64_t* lds, const uint64_t* lift = nullptr,
+                                           uint64_t lq = 0, const Barrett br = Barrett{}) {
     const uint64_t q4 = q << 2, nq = 0 - q;
     const int cl = g & 15, rg = g >> 4;
     const int col = tile * 16 + cl;
     uint64_t x[16];
+    if (kLift) {
 #pragma unroll
-    for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&a[col + 256 * (rg + 16 * k)]);
+        for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&lift[col + 256 * (rg + 16 * k)]);
+#pragma unroll
+        for (int k = 0; k < 16; k++) x[k] = lift_centered(x[k], lq, br);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&a[col + 256 * (rg + 16 * k)]);
+    }
     // stages 0..3: rows r = rg + 16k, pairs differ in bit (3-s) of k; twiddle (1<<s) + (k >> (4-s))
 #pragma unroll
     for (int s = 0; s < 4; s++) {
@@ -481,10 +490,20 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_fwd_a(uint64_t* data, JobS
     uint32_t off, prime;
     job_of(js, blockIdx.y, off, prime);
     const uint64_t q = primes[prime].q;
-    if (q < kOpenMaxQ)
-        fwd_a_tile<true>(data + (size_t)off * kN, tw_all + (size_t)prime * kN, q, blockIdx.x, threadIdx.x, lds);
-    else
-        fwd_a_tile<false>(data + (size_t)off * kN, tw_all + (size_t)prime * kN, q, blockIdx.x, threadIdx.x, lds);
+    uint64_t* a = data + (size_t)off * kN;
+    const TwPair* tw = tw_all + (size_t)prime * kN;
+    if (js.lift && !js.jobs) {
+        const uint32_t p = blockIdx.y % js.n_polys;
+        const uint64_t* src = js.lift + p * js.lift_pstride;
+        if (q < kOpenMaxQ)
+            fwd_a_tile<true, true>(a, tw, q, blockIdx.x, threadIdx.x, lds, src, js.lift_q, barrett_of(primes[prime]));
+        else
+            fwd_a_tile<false, true>(a, tw, q, blockIdx.x, threadIdx.x, lds, src, js.lift_q, barrett_of(primes[prime]));
+    } else if (q < kOpenMaxQ) {
+        fwd_a_tile<true>(a, tw, q, blockIdx.x, threadIdx.x, lds);
+    } else {
+        fwd_a_tile<false>(a, tw, q, blockIdx.x, threadIdx.x, lds);
+    }
 }
 
 __global__ __launch_bounds__(kTileThreads) void k_ntt_fwd_b(uint64_t* data, JobSpec js, const TwPair* tw_all,
@@ -834,6 +853,11 @@ hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js_in, 
             if (js.src2 && ctx.moduli[js.pmap[i]] >= (1ull << 60)) return hipErrorInvalidValue;
         mode = NttMode::TwoPass;
     }
+    if (js.lift) {
+        // a lifted input: dense forward specs, two-pass kernels only
+        if (js.jobs || inverse) return hipErrorInvalidValue;
+        mode = NttMode::TwoPass;
+    }
     const TwPair* tw = inverse ? ctx.d_itw : ctx.d_tw;
     const TwPair* twb = inverse ? ctx.d_itwb : ctx.d_twb;
     // algorithmic bytes: every limb read and written once (plus the second factor read and the copy written), each
@@ -850,17 +874,21 @@ hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js_in, 
 
 // Forward NTT of a ModDown's converted P part y [n_polys][l][N] (coefficients, limb i over prime i; dense) whose pass
 // B ends in k_sub_scale's combine: out[pc][i] = (x[pc][i] - NTT(y)[pc][i]) s_i (+ the addend).  y is left holding
-// the first pass's intermediate.  Same argument meaning as launch_sub_scale.
+// the first pass's intermediate.  Same argument meaning as launch_sub_scale.  lift (optional): y's input is instead
+// formed by the first pass from one limb per poly (JobSpec.lift).
 hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x, uint64_t x_pstride,
                               const uint64_t* add, uint64_t add_pstride, uint32_t add_div, uint32_t add_group,
                               uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
-                              hipStream_t st) {
+                              hipStream_t st, const uint64_t* lift, uint64_t lift_pstride, uint64_t lift_q) {
     if (l == 0 || l > kMaxPmap || n_polys == 0) return hipErrorInvalidValue;
     JobSpec js{};
     js.n_polys = n_polys;
     js.period = l;
     js.n_primes = l;
     for (uint32_t i = 0; i < l; i++) js.pmap[i] = (uint8_t)i;
+    js.lift = lift;
+    js.lift_pstride = lift_pstride;
+    js.lift_q = lift_q;
     CombineArgs ca{};
     ca.l = l;
     ca.add_div = add_div ? add_div : 1;
@@ -871,9 +899,11 @@ hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x
     ca.add_pstride = add_pstride;
     for (uint32_t i = 0; i < l; i++) ca.s[i] = s[i];
     const uint32_t n_jobs = n_polys * l;
-    // algorithmic bytes: y read and written by pass A, read by pass B; x read, out written; the addends; tables
+    // algorithmic bytes: y read (or the lift source, once per poly) and written by pass A, read by pass B; x read,
+    // out written; the addends; tables
     const double n_add = add ? (double)n_polys / ca.add_div : 0.0;
-    const double bytes = ((double)n_jobs * 5 + n_add * l) * kN * 8 + (double)l * kN * sizeof(TwPair);
+    const double reads_a = lift ? (double)n_polys : (double)n_jobs;
+    const double bytes = ((double)n_jobs * 4 + reads_a + n_add * l) * kN * 8 + (double)l * kN * sizeof(TwPair);
     const int pi = prof_begin(ctx, "ntt_fwd_sub", bytes, st);
     const dim3 grid(16, n_jobs), block(kTileThreads);
     hipLaunchKernelGGL(k_ntt_fwd_a, grid, block, 0, st, y, js, ctx.d_tw, ctx.d_primes);

@@ -46,7 +46,8 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
 hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x, uint64_t x_pstride,
                               const uint64_t* add, uint64_t add_pstride, uint32_t add_div, uint32_t add_group,
                               uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
-                              hipStream_t st);
+                              hipStream_t st, const uint64_t* lift = nullptr, uint64_t lift_pstride = 0,
+                              uint64_t lift_q = 0);
 hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint32_t l, const uint64_t* ext,
                               const uint64_t* evk, const uint64_t* ta, const uint64_t* tb, const uint64_t* add,
                               uint64_t add_pstride, uint64_t* out, const TwPair* pinv, const TwPair* qlinv,
@@ -566,7 +567,6 @@ void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uin
     jl.src = in + (size_t)(l - 1) * W;
     jl.src_period = l;
     HIPX(launch_ntt(ctx, last, jl, n_polys, true, ctx.ntt_mode, st));
-    HIPX(launch_lift_centered(ctx, last, W, tmp, n_polys, l - 1, ctx.moduli[l - 1], st));
     std::vector<TwPair> s(l - 1);
     const uint64_t ql = ctx.moduli[l - 1];
     for (uint32_t i = 0; i + 1 < l; i++) {
@@ -575,11 +575,13 @@ void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uin
         s[i] = TwPair{v, shoup_companion(v, q)};
     }
     if (ctx.ntt_mode == NttMode::TwoPass) {
-        // the lifted limbs' forward NTT ends in the combine (out = (in - NTT(tmp)) q_{l-1}^-1)
+        // the lift happens in the forward NTT's first pass, and its second pass ends in the combine:
+        // out = (in - NTT(lift(last))) q_{l-1}^-1
         HIPX(launch_ntt_fwd_sub(ctx, tmp, in, (uint64_t)l * W, nullptr, 0, 1, 0, out, (uint64_t)(l - 1) * W, n_polys,
-                                l - 1, s.data(), st));
+                                l - 1, s.data(), st, last, W, ql));
         return;
     }
+    HIPX(launch_lift_centered(ctx, last, W, tmp, n_polys, l - 1, ql, st));
     std::vector<uint32_t> pm(l - 1);
     for (uint32_t i = 0; i + 1 < l; i++) pm[i] = i;
     HIPX(launch_ntt(ctx, tmp, regular_jobs(n_polys, pm), n_polys * (l - 1), false, ctx.ntt_mode, st));

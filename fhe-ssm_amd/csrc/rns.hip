@@ -130,17 +130,6 @@ struct BConvArgs {
 __device__ __forceinline__ uint32_t desc_off(uint32_t d) { return d & 0xFFFFu; }
 __device__ __forceinline__ uint32_t desc_prime(uint32_t d) { return d >> 16; }
 
-// centered residue of v in [0, ql) modulo q: v > ql/2 stands for v - ql (harness/boot_overflow_probe.cpp:93-94)
-__device__ __forceinline__ uint64_t lift_centered(uint64_t v, uint64_t ql, const Barrett& br) {
-    const uint64_t q = br.q;
-    if (v > (ql >> 1)) {
-        const uint64_t neg = ql - v;  // value is -neg
-        const uint64_t m = neg >= q ? reduce128(0, neg, br) : neg;
-        return m ? q - m : 0;
-    }
-    return v >= q ? reduce128(0, v, br) : v;
-}
-
 // Extra inputs of the ModDown BConv fused with the rescale that follows (k_bconv<NIN, true, ..>).  The plan's last
 // output column is the dropped limb l-1 (plain table); every other column j has P^-1 mod q_j folded into its
 // table, so the column sums are conv_j P^-1 directly.  Per coefficient the kernel forms
