@@ -334,9 +334,16 @@ __device__ __forceinline__ void fwd_b_tile(uint64_t* __restrict__ a, const TwPai
 // in: the limb read (a itself, or the out-of-place source).  kProd: the input is in * in2 mod q (q < 2^60, both
 // factors canonical, so the product's high word is below q).  ji.cpy (optional): the input words, as read or formed,
 // are also stored there.
-template <bool kOpen, bool kProd>
+// kD > 0: the input is the evk inner product sum_d in[d xs] * ks.e[d es] of a key switch (KsIn), kD digits.
+struct KsIn {
+    const uint64_t* e;  // the job's evk limb of digit 0 (digit d at e + d es)
+    size_t xs, es;      // digit strides of the extension (in) and of the key, in words
+};
+
+template <bool kOpen, bool kProd, int kD = 0>
 __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, JobIn ji, const PrimeInfo& P,
-                                           const TwPair* __restrict__ tw, int tile, int g, uint64_t* lds) {
+                                           const TwPair* __restrict__ tw, int tile, int g, uint64_t* lds,
+                                           const KsIn ks = KsIn{}) {
     const uint64_t q = P.q;
     const uint64_t q4 = q << 2, nq = 0 - q;
     const int bl = g >> 4, rl = g & 15;
@@ -345,7 +352,31 @@ __device__ __forceinline__ void inv_b_tile(uint64_t* a, const uint64_t* in, JobI
     const uint64_t* src = in + 256 * b;
     uint64_t* L = lds + bl * 272;
     uint64_t x[16];
-    if (kProd || ji.cpy) {
+    if constexpr (kD > 0) {
+        // two words at a time, all their digit loads issued before the products (sums of kD <= 4 products of
+        // residues below q < 2^60: the high word stays below q)
+        const Barrett br{q, P.mu_hi, P.mu_lo};
+        const uint64_t* e = ks.e + 256 * b;
+#pragma unroll
+        for (int k0 = 0; k0 < 16; k0 += 2) {
+            uint64_t xv[2][kD], ev[2][kD];
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+#pragma unroll
+                for (int d = 0; d < kD; d++) {
+                    xv[j][d] = src[d * ks.xs + rl + 16 * (k0 + j)];
+                    ev[j][d] = e[d * ks.es + rl + 16 * (k0 + j)];
+                }
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                Acc s;
+#pragma unroll
+                for (int d = 0; d < kD; d++) s.add(xv[j][d], ev[j][d]);
+                const U128 v = s.get();
+                L[rl + 17 * (k0 + j)] = reduce128(v.hi, v.lo, br);
+            }
+        }
+    } else if (kProd || ji.cpy) {
 #pragma unroll
         for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&src[rl + 16 * k]);
         if (kProd) {
@@ -538,6 +569,34 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_b(uint64_t* data, JobS
     } else {
         inv_b_tile<false, false>(a, in, ji, P, tw, blockIdx.x, threadIdx.x, lds);
     }
+}
+
+// The first inverse pass over a job list of ModDown limbs (off = pc E + t of an accumulator [n_polys][E][N]) whose
+// input is the evk inner product of a key switch of ciphertext pc / 2, poly pc % 2, formed here from the extension
+// [B][kD][E][N] and the key [dnum][2][T][N] (in place of a separate inner-product launch and its stores).
+struct KsJobArgs {
+    const uint64_t* ext;
+    const uint64_t* evk;
+    uint32_t E, T;
+};
+
+template <int kD>
+__global__ __launch_bounds__(kTileThreads) void k_ntt_inv_b_ks(uint64_t* data, JobSpec js, const TwPair* tw_all,
+                                                              const PrimeInfo* primes, KsJobArgs ka) {
+    __shared__ uint64_t lds[kLdsWords];
+    uint32_t off, prime;
+    job_of(js, blockIdx.y, off, prime);
+    const uint32_t pc = off / ka.E, t = off - pc * ka.E, c = pc >> 1, p = pc & 1;
+    const PrimeInfo& P = primes[prime];
+    const uint64_t* xin = ka.ext + ((size_t)c * kD * ka.E + t) * kN;
+    const KsIn ks{ka.evk + ((size_t)p * ka.T + prime) * kN, (size_t)ka.E * kN, 2 * (size_t)ka.T * kN};
+    uint64_t* a = data + (size_t)off * kN;
+    const TwPair* tw = tw_all + (size_t)prime * kN;
+    const JobIn none{nullptr, nullptr};
+    if (P.q < kGsOpenMaxQ)
+        inv_b_tile<true, false, kD>(a, xin, none, P, tw, blockIdx.x, threadIdx.x, lds, ks);
+    else
+        inv_b_tile<false, false, kD>(a, xin, none, P, tw, blockIdx.x, threadIdx.x, lds, ks);
 }
 
 __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_a(uint64_t* data, JobSpec js, const TwPair* tw_all,
@@ -870,6 +929,29 @@ hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js_in, 
     hipError_t err = launch_ntt_kernels(ctx, data, js, n_jobs, inverse, mode, tw, twb, st);
     prof_end(ctx, pi, st);
     return err;
+}
+
+// Inverse NTT of a job list over an accumulator [n_polys][E][N] (off = pc E + t) whose input, limb t of poly pc, is
+// the evk inner product sum_d ext[pc / 2][d][t] evk[d][pc % 2][prime] (the inner product a key switch would store
+// there first).  Digit counts 1..4 (others: hipErrorInvalidValue, the caller stores the inner product first).
+hipError_t launch_ntt_inv_ks(const Context& ctx, uint64_t* acc, const JobSpec& js, uint32_t n_jobs,
+                             const uint64_t* ext, const uint64_t* evk, uint32_t D, uint32_t E, hipStream_t st) {
+    if (!js.jobs || D < 1 || D > 4 || n_jobs == 0) return hipErrorInvalidValue;
+    const KsJobArgs ka{ext, evk, E, ctx.L + ctx.K};
+    // algorithmic bytes: per job D extension limbs and D key limbs read (the key shared by the batch counts once per
+    // job here), the limb written and read back by the second pass and written again; the tables
+    const double bytes = (double)n_jobs * (2.0 * D + 3) * kN * 8 + (double)js.n_primes * kN * sizeof(TwPair);
+    const int pi = prof_begin(ctx, "ntt_inv_ks", bytes, st);
+    const dim3 grid(16, n_jobs), block(kTileThreads);
+    switch (D) {
+        case 1: hipLaunchKernelGGL(k_ntt_inv_b_ks<1>, grid, block, 0, st, acc, js, ctx.d_itwb, ctx.d_primes, ka); break;
+        case 2: hipLaunchKernelGGL(k_ntt_inv_b_ks<2>, grid, block, 0, st, acc, js, ctx.d_itwb, ctx.d_primes, ka); break;
+        case 3: hipLaunchKernelGGL(k_ntt_inv_b_ks<3>, grid, block, 0, st, acc, js, ctx.d_itwb, ctx.d_primes, ka); break;
+        default: hipLaunchKernelGGL(k_ntt_inv_b_ks<4>, grid, block, 0, st, acc, js, ctx.d_itwb, ctx.d_primes, ka); break;
+    }
+    hipLaunchKernelGGL(k_ntt_inv_a, grid, block, 0, st, acc, js, ctx.d_itw, ctx.d_primes);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
 }
 
 // Forward NTT of a ModDown's converted P part y [n_polys][l][N] (coefficients, limb i over prime i; dense) whose pass

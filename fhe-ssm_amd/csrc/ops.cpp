@@ -43,6 +43,8 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
                                  uint64_t add_pstride, const uint64_t* T, uint64_t* out, uint32_t B, uint32_t l,
                                  const TwPair* pinv, const TwPair* qlinv, hipStream_t st,
                                  const uint64_t* ta = nullptr, const uint64_t* tb = nullptr);
+hipError_t launch_ntt_inv_ks(const Context& ctx, uint64_t* acc, const JobSpec& js, uint32_t n_jobs,
+                             const uint64_t* ext, const uint64_t* evk, uint32_t D, uint32_t E, hipStream_t st);
 hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x, uint64_t x_pstride,
                               const uint64_t* add, uint64_t add_pstride, uint32_t add_div, uint32_t add_group,
                               uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
@@ -434,7 +436,7 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
 // forms limbs 0..l-2 itself from ext and evk.
 void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
                      hipStream_t st, const uint64_t* ext, const uint64_t* evk, const uint64_t* ta,
-                     const uint64_t* tb) {
+                     const uint64_t* tb, bool x_from_ext) {
     check_level(ctx, l);
     if (l < 2) throw std::invalid_argument("rescale needs l >= 2");
     const uint32_t E = l + ctx.K, K = ctx.K;
@@ -446,7 +448,10 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
         for (uint32_t k = 0; k < K; k++) jobs.push_back(Job{pc * E + l + k, ctx.L + k});
     }
     const JobSpec js = cached_jobs(ctx, "mdrP:" + std::to_string(n_polys) + ":" + std::to_string(l), std::move(jobs));
-    HIPX(launch_ntt(ctx, x, js, n_polys * (K + 1), true, ctx.ntt_mode, st));
+    if (x_from_ext)  // those limbs of x are the evk inner product, formed by the transform's first pass
+        HIPX(launch_ntt_inv_ks(ctx, x, js, n_polys * (K + 1), ext, evk, num_digits(ctx, l), E, st));
+    else
+        HIPX(launch_ntt(ctx, x, js, n_polys * (K + 1), true, ctx.ntt_mode, st));
     // limb l-1 of the addend to coefficients (a copy: the addend is the caller's)
     uint64_t* addc = nullptr;
     if (add) {
@@ -609,7 +614,13 @@ static void relin_tail(Context& ctx, uint64_t* d01, uint64_t* x2c, uint64_t* ext
         moddown_inplace(ctx, acc, 2 * B, l, d01, out, st, 1);
         return;
     }
-    // inner product of limb l-1 and the P limbs only; the combine forms limbs 0..l-2
+    // inner product of limb l-1 and the P limbs only, formed by their inverse NTT's first pass (or stored first, under
+    // the fused NTT mode or more than 4 digits); the combine forms limbs 0..l-2
+    if (ctx.ntt_mode == NttMode::TwoPass && num_digits(ctx, l) <= 4) {
+        ctx.n_keyswitch += B;
+        moddown_rescale(ctx, acc, 2 * B, l, d01, out, st, ext, evk, ta, tb, true);
+        return;
+    }
     HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st, l - 1));
     moddown_rescale(ctx, acc, 2 * B, l, d01, out, st, ext, evk, ta, tb);
 }

@@ -50,9 +50,11 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
                      uint32_t x_plimbs = 0);
 // ta, tb (with ext): the inputs [B][2][l][N] of the product being relinearized; add then holds d0 and d1 at limb
 // l-1 only and the combine forms the other limbs' d0 = a0 b0, d1 = a0 b1 + a1 b0 itself
+// x_from_ext (with ext and evk): limb l-1 and the P limbs of x are not read but formed as the evk inner product by
+// their inverse NTT (x receives them)
 void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
                      hipStream_t st, const uint64_t* ext = nullptr, const uint64_t* evk = nullptr,
-                     const uint64_t* ta = nullptr, const uint64_t* tb = nullptr);
+                     const uint64_t* ta = nullptr, const uint64_t* tb = nullptr, bool x_from_ext = false);
 void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
                uint64_t* out2, hipStream_t st, uint32_t add_div = 1, uint64_t x_bstride = 0);
 void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uint64_t* out, hipStream_t st);

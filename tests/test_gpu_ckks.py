@@ -188,7 +188,9 @@ def test_profile_records_kernels(ckks, ctx, relin):
     ctx.profile(False)
     rep = ctx.profile_report()
     ctx.profile_reset()
-    assert {"tensor", "bconv", "ks_inner"} <= set(rep)
+    assert {"tensor", "bconv"} <= set(rep)
+    # the evk inner product of the dropped limb and the P limbs is formed by their inverse NTT (two-pass schedule)
+    assert "ntt_inv_ks" in rep or "ks_inner" in rep
     # relinearization + rescale run as one fused ModDown-and-rescale: the BConv writes the lifted T, whose forward
     # NTT ends in the combine (which forms the evk inner product of the kept limbs itself) on the two-pass schedule
     assert "bconv_mdr" in rep
