@@ -107,6 +107,8 @@ PrimeInfo make_prime_info(uint64_t q, uint64_t itab1) {
     uint64_t x = q;
     for (int i = 0; i < 5; i++) x *= 2 - q * x;
     p.mont_ninv = 0 - x;
+    p.r_mod = (uint64_t)(((u128)1 << 64) % q);
+    p.r_mod_p = shoup_companion(p.r_mod, q);
     return p;
 }
 

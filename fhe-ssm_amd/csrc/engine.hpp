@@ -28,6 +28,7 @@ struct PrimeInfo {
     // with red_shift = max(0, bits(q) - 25), red_mul = floor(2^(32 + red_shift) / q)
     uint32_t red_shift, red_mul;
     uint64_t mont_ninv;  // -q^-1 mod 2^64 (Montgomery reduction of a 128-bit sum, R = 2^64)
+    uint64_t r_mod, r_mod_p;  // R = 2^64 mod q and its Shoup companion (takes an R^-1-scaled value back to plain)
 };
 
 // One limb to transform: offset (in units of N words) from the base pointer, and its prime index.

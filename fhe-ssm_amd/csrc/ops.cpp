@@ -996,11 +996,13 @@ void bsgs_dh_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uin
     const uint32_t E = l + ctx.K, D = num_digits(ctx, l), K = ctx.K;
     const size_t ctw = (size_t)2 * l * W, cte = (size_t)2 * E * W, exw = (size_t)D * E * W;
     const uint32_t nbt = n_in * nb, n_x = n_inst * n_in, n_o = n_inst * n_out;
-    std::vector<TwPair> pmod(l);  // P mod q_t
+    std::vector<TwPair> pmod(l);  // P R^-1 mod q_t (R = 2^64; the double-hoisted MAC keeps its babies R^-1-scaled)
     for (uint32_t t = 0; t < l; t++) {
         const uint64_t q = ctx.moduli[t];
         uint64_t P = 1;
         for (uint32_t k = 0; k < K; k++) P = mulmod_h(P, ctx.moduli[ctx.L + k] % q, q);
+        const uint64_t rinv = invmod_h((uint64_t)(((unsigned __int128)1 << 64) % q), q);
+        P = mulmod_h(P, rinv, q);
         pmod[t] = TwPair{P, shoup_companion(P, q)};
     }
     // the inputs side by side (read in place when they already are), their c1 extended once

@@ -145,13 +145,13 @@ struct MdrBconvArgs {
 // NIN = number of input limbs (a template parameter: the term loops unroll without run-time guards).  The table's
 // q-hat constants are stored pre-split into 30-bit halves (pack30), the y_i are split once, and every term is three
 // multiply-adds into carry-free sums (Acc30k; inputs taken in chunks of at most 8).
-// kMont: the plan is Montgomery-reduced and not centered (ba.mont and !ba.centered known at compile time, so no
-// per-output tests of the flags).
-template <int NIN, bool kMdr, bool kMont>
+// kMode: 0 = the plan's flags read at run time; 1 = Montgomery-reduced, not centered; 2 = Montgomery-reduced and
+// centered (the flags known at compile time: no per-output tests of them).
+template <int NIN, bool kMdr, int kMode>
 __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, uint64_t* __restrict__ out,
                                                BConvArgs ba, const uint64_t* __restrict__ tab,
                                                const PrimeInfo* __restrict__ primes, MdrBconvArgs mb) {
-    const bool centered = kMont ? false : ba.centered != 0, mont = kMont ? true : ba.mont != 0;
+    const bool centered = kMode == 0 ? ba.centered != 0 : kMode == 2, mont = kMode == 0 ? ba.mont != 0 : true;
     const uint32_t k = blockIdx.x * 256 + threadIdx.x;
     const uint32_t c = blockIdx.y;
     const uint64_t* src = in + c * ba.in_bstride + k;
@@ -269,26 +269,26 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
 }
 
 // k_bconv instance for a run-time input count (1..kMaxBconvIn)
-template <bool kMdr, bool kMont>
+template <bool kMdr, int kMode>
 static void (*bconv_kernel_m(uint32_t n_in))(const uint64_t*, uint64_t*, BConvArgs, const uint64_t*,
                                              const PrimeInfo*, MdrBconvArgs) {
     switch (n_in) {
-        case 1: return k_bconv<1, kMdr, kMont>;
-        case 2: return k_bconv<2, kMdr, kMont>;
-        case 3: return k_bconv<3, kMdr, kMont>;
-        case 4: return k_bconv<4, kMdr, kMont>;
-        case 5: return k_bconv<5, kMdr, kMont>;
-        case 6: return k_bconv<6, kMdr, kMont>;
-        case 7: return k_bconv<7, kMdr, kMont>;
-        case 8: return k_bconv<8, kMdr, kMont>;
-        case 9: return k_bconv<9, kMdr, kMont>;
-        case 10: return k_bconv<10, kMdr, kMont>;
-        case 11: return k_bconv<11, kMdr, kMont>;
-        case 12: return k_bconv<12, kMdr, kMont>;
-        case 13: return k_bconv<13, kMdr, kMont>;
-        case 14: return k_bconv<14, kMdr, kMont>;
-        case 15: return k_bconv<15, kMdr, kMont>;
-        case 16: return k_bconv<16, kMdr, kMont>;
+        case 1: return k_bconv<1, kMdr, kMode>;
+        case 2: return k_bconv<2, kMdr, kMode>;
+        case 3: return k_bconv<3, kMdr, kMode>;
+        case 4: return k_bconv<4, kMdr, kMode>;
+        case 5: return k_bconv<5, kMdr, kMode>;
+        case 6: return k_bconv<6, kMdr, kMode>;
+        case 7: return k_bconv<7, kMdr, kMode>;
+        case 8: return k_bconv<8, kMdr, kMode>;
+        case 9: return k_bconv<9, kMdr, kMode>;
+        case 10: return k_bconv<10, kMdr, kMode>;
+        case 11: return k_bconv<11, kMdr, kMode>;
+        case 12: return k_bconv<12, kMdr, kMode>;
+        case 13: return k_bconv<13, kMdr, kMode>;
+        case 14: return k_bconv<14, kMdr, kMode>;
+        case 15: return k_bconv<15, kMdr, kMode>;
+        case 16: return k_bconv<16, kMdr, kMode>;
         default: return nullptr;
     }
 }
@@ -296,8 +296,8 @@ static void (*bconv_kernel_m(uint32_t n_in))(const uint64_t*, uint64_t*, BConvAr
 template <bool kMdr>
 static void (*bconv_kernel(const BConvPlan& plan))(const uint64_t*, uint64_t*, BConvArgs, const uint64_t*,
                                                    const PrimeInfo*, MdrBconvArgs) {
-    if (plan.mont && !plan.centered) return bconv_kernel_m<kMdr, true>(plan.n_in);
-    return bconv_kernel_m<kMdr, false>(plan.n_in);
+    if (plan.mont) return plan.centered ? bconv_kernel_m<kMdr, 2>(plan.n_in) : bconv_kernel_m<kMdr, 1>(plan.n_in);
+    return bconv_kernel_m<kMdr, 0>(plan.n_in);
 }
 
 // ------------------------------------------------------------------ key-switch inner product
@@ -780,7 +780,9 @@ struct DhMacArgs {
     uint64_t id_inst_stride, id_stride;  // id_out: per instance, per output
     const uint64_t* evk[kMaxDhBaby];  // per baby step (null: the identity)
     uint32_t g[kMaxDhBaby];
-    TwPair pmod[kMaxPmap];            // P mod q_t, t < l
+    // P R^-1 mod q_t, t < l (R = 2^64): the babies are kept R^-1-scaled -- their inner products are Montgomery-reduced
+    // (one REDC each instead of a Barrett reduction) -- and each giant sum is scaled back by R (PrimeInfo.r_mod)
+    TwPair pmod[kMaxPmap];
 };
 
 // ND: the digit count (a template parameter, so that a baby's extension and key loads are all issued before the
@@ -802,7 +804,7 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
     const bool qlimb = t < a.l;
     const uint32_t pi = qlimb ? t : a.L + (t - a.l);
     const Barrett br = barrett_of(primes[pi]);
-    const uint64_t q = br.q;
+    const uint64_t q = br.q, ninv = primes[pi].mont_ninv;
     const uint32_t nbt = a.n_in * a.nb;
     for (uint32_t j = row; j < nbt; j += kMacRows) {
         const uint32_t i = j / a.nb, b = j - i * a.nb, x = s * a.n_in + i;
@@ -828,9 +830,10 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
                 s0.add(xv[d], e0[d]);
                 s1.add(xv[d], e1[d]);
             }
-            v0 = reduce_u128(s0.get(), br);
+            // REDC: sums of at most 8 products of residues below q < 2^60 stay below q 2^64
+            v0 = redc(s0.get(), q, ninv);
             if (qlimb) v0 = add_mod(v0, shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q), q);
-            v1 = reduce_u128(s1.get(), br);
+            v1 = redc(s1.get(), q, ninv);
         } else if (qlimb) {
             v0 = shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q);
             v1 = shoup(sx[(size_t)a.l * kN], a.pmod[t].w, a.pmod[t].wp, q);
@@ -895,9 +898,11 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
             __syncthreads();
         }
         if (sl == 0 && G < a.ng) {
+            // the babies' R^-1 taken back out
+            const uint64_t rm = primes[pi].r_mod, rmp = primes[pi].r_mod_p;
             uint64_t* o = dest(G);
-            __builtin_nontemporal_store(r0, &o[0]);
-            __builtin_nontemporal_store(r1, &o[P]);
+            __builtin_nontemporal_store(shoup(r0, rm, rmp, q), &o[0]);
+            __builtin_nontemporal_store(shoup(r1, rm, rmp, q), &o[P]);
         }
     }
 }
