@@ -999,7 +999,9 @@ __global__ __launch_bounds__(256) void k_lincomb(uint64_t* __restrict__ out, Lin
 #pragma unroll
     for (int t = 0; t < kMaxTerms; t++)
         if (t < (int)la.n_terms) acc.add(v[t], la.C[t][i]);
-    uint64_t r = reduce_u128(acc.get(), br);
+    // the coefficients carry a factor R = 2^64 (C R mod q_i), so the REDC of the sum is the combination itself;
+    // at most 8 products of residues below q < 2^60 keep the sum below q R
+    uint64_t r = redc(acc.get(), br.q, primes[i].mont_ninv);
     if (la.has_add && p == 0) r = add_mod(r, la.add[i], br.q);
     __builtin_nontemporal_store(r, &out[((size_t)pc * la.l_out + i) * kN + k]);
 }
@@ -1468,7 +1470,12 @@ hipError_t launch_lincomb(const Context& ctx, uint64_t* out, uint32_t B, uint32_
     for (uint32_t t = 0; t < n_terms; t++) {
         la.x[t] = x[t];
         la.stride[t] = stride[t];
-        for (uint32_t i = 0; i < l_out; i++) la.C[t][i] = C[(size_t)t * l_out + i];
+        for (uint32_t i = 0; i < l_out; i++) {
+            // C R mod q_i (k_lincomb reduces by REDC)
+            const uint64_t q = ctx.moduli[i];
+            const unsigned __int128 r = ((unsigned __int128)1 << 64) % q;
+            la.C[t][i] = (uint64_t)((unsigned __int128)(C[(size_t)t * l_out + i] % q) * r % q);
+        }
     }
     if (add)
         for (uint32_t i = 0; i < l_out; i++) la.add[i] = add[i];
