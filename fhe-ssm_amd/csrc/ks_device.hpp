@@ -53,6 +53,13 @@ __device__ __forceinline__ void ks_dot(const uint64_t* __restrict__ x, size_t xs
     }
 }
 
+// per-item pointers of a list launch (up to kMaxList items)
+constexpr int kMaxList = 64;
+
+struct ListPtrs {
+    const uint64_t* p[kMaxList];
+};
+
 struct InnerArgs {
     uint32_t D, E, T, B;
     uint32_t t0;  // first extended limb computed (k_ks_inner: limbs t0..E-1)

@@ -764,6 +764,99 @@ void launch_b_mdr(dim3 grid, dim3 block, hipStream_t st, uint64_t* T, const TwPa
         hipLaunchKernelGGL((k_ntt_fwd_b_mdr<kD, false>), grid, block, 0, st, T, twb, primes, f);
 }
 
+// ---------------------------------------------------------------- forward pass B that finishes a key-switch list
+// The forward NTT of a key-switch list's converted P part y ([2n][l] limbs, poly 2c + p of item c, dense) ends with the
+// combine of k_ks_sub_list instead of a store of y: for each word of limb i,
+//   out[c][p][i] = x_p P^-1 - y_p (+ the addend's poly 0 on p = 0),  x_p = sum_d ext_c[d][i] evk_c[d][p][i],
+// with per-item extensions and keys.  Workgroups as k_ntt_fwd_b_mdr: one 256-thread half per poly, then every thread
+// finishes 8 words of the tile for both polys.
+struct KslFuse {
+    ListPtrs ext, evk;    // item c: [D][E][N] and [dnum][2][T][N]
+    const uint64_t* add;  // the addend ciphertexts [2][l][N] (poly 0 used), (c / add_group) add_stride apart, or null
+    uint64_t* out;        // [n][2][l][N]
+    uint64_t add_stride;
+    uint32_t n, l, E, T, add_group;
+    TwPair pinv[kMaxPmap];
+};
+
+template <int kD>
+struct KslEpi {
+    struct First {
+        uint64_t xv[kD], e0[kD], e1[kD], u0;
+    };
+    const KslFuse& f;
+    const PrimeInfo& P;
+    uint32_t i, c, g;  // limb, item, the thread's group (= the poly whose tile it transformed)
+
+    __device__ __forceinline__ void load(First& B, int blk, int rl, int k) const {
+        const uint32_t bo = (256 * blk + rl + 16 * k) * 8;
+        const size_t li = (size_t)i * kN, xs = (size_t)f.E * kN, es = (size_t)f.T * kN;
+        const uint64_t* x = f.ext.p[c] + li;
+        const uint64_t* e = f.evk.p[c] + li;
+#pragma unroll
+        for (int d = 0; d < kD; d++) {
+            B.xv[d] = ld_at(x + d * xs, bo);
+            B.e0[d] = ld_at(e + (2 * d) * es, bo);
+            B.e1[d] = ld_at(e + (2 * d + 1) * es, bo);
+        }
+        if (f.add) B.u0 = ld_at(f.add + (size_t)(c / f.add_group) * f.add_stride + li, bo);
+    }
+
+    __device__ __forceinline__ First begin(int blk, int rl) const {
+        First B;
+        load(B, blk, rl, 8 * g);
+        return B;
+    }
+
+    // L: this group's tile; the tiles of polys 0 and 1 are adjacent (kLdsWords apart)
+    __device__ __forceinline__ void end(First cur, const uint64_t* L, int blk, int rl) const {
+        const uint64_t* L0 = L - g * kLdsWords;
+        const uint64_t* L1 = L0 + kLdsWords;
+        const size_t pw = (size_t)f.l * kN;
+        uint64_t* out0 = f.out + 2 * c * pw + (size_t)i * kN;
+        uint64_t* out1 = out0 + pw;
+        const Barrett br = barrett_of(P);
+        const uint64_t q = br.q;
+        const TwPair pinv = f.pinv[i];
+#pragma unroll
+        for (int kk = 0; kk < 8; kk++) {
+            const int k = 8 * g + kk;
+            First nxt;
+            if (kk < 7) load(nxt, blk, rl, k + 1);
+            Acc s0, s1;
+#pragma unroll
+            for (int d = 0; d < kD; d++) {
+                s0.add(cur.xv[d], cur.e0[d]);
+                s1.add(cur.xv[d], cur.e1[d]);
+            }
+            uint64_t v0 = sub_mod(shoup(reduce_sum(s0, br), pinv.w, pinv.wp, q), L0[rl + 17 * k], q);
+            const uint64_t v1 = sub_mod(shoup(reduce_sum(s1, br), pinv.w, pinv.wp, q), L1[rl + 17 * k], q);
+            if (f.add) v0 = add_mod(v0, cur.u0, q);
+            const uint32_t bo = (256 * blk + rl + 16 * k) * 8;
+            __builtin_nontemporal_store(v0, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out0) + bo));
+            __builtin_nontemporal_store(v1, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out1) + bo));
+            if (kk < 7) cur = nxt;
+        }
+    }
+};
+
+// grid (16 tiles, n l jobs), 512 threads; job v = i n + c (limb-major: a limb's tiles of all items on one XCD)
+template <int kD>
+__global__ __launch_bounds__(2 * kTileThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_ntt_fwd_b_ksl(
+    uint64_t* y, const TwPair* tw_all, const PrimeInfo* primes, KslFuse f) {
+    __shared__ uint64_t lds[2 * kLdsWords];
+    const uint32_t i = blockIdx.y / f.n, c = blockIdx.y - i * f.n;
+    const uint32_t g = threadIdx.x >> 8, t = threadIdx.x & 255;
+    const PrimeInfo& P = primes[i];
+    const KslEpi<kD> epi{f, P, i, c, g};
+    uint64_t* a = y + ((size_t)(2 * c + g) * f.l + i) * kN;
+    const TwPair* tw = tw_all + (size_t)i * kN;
+    if (P.q < kOpenMaxQ)
+        fwd_b_tile<true>(a, tw, P, blockIdx.x, t, lds + g * kLdsWords, epi);
+    else
+        fwd_b_tile<false>(a, tw, P, blockIdx.x, t, lds + g * kLdsWords, epi);
+}
+
 // ---------------------------------------------------------------- forward pass B that finishes a plain ModDown
 // The forward NTT of a ModDown's converted P part y ([n_polys][l] limbs, dense) ends with the combine of k_sub_scale
 // instead of a store of y: out[pc][i] = (x[pc][i] - y[pc][i]) s_i (+ the addend for polys pc % add_div == 0, read at
@@ -929,6 +1022,55 @@ hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js_in, 
     hipError_t err = launch_ntt_kernels(ctx, data, js, n_jobs, inverse, mode, tw, twb, st);
     prof_end(ctx, pi, st);
     return err;
+}
+
+// Forward NTT of a key-switch list's converted P part y [2n][l][N] (coefficients, limb i over prime i; dense) whose
+// pass B ends in k_ks_sub_list's combine: out [n][2][l][N] = x P^-1 - NTT(y) (+ the addend's poly 0), x the evk inner
+// product of item c's extension and key.  y is left holding the first pass's intermediate.  Digit counts 1..4
+// (others: hipErrorInvalidValue, the caller runs the NTT and k_ks_sub_list).
+hipError_t launch_ntt_fwd_ksl(const Context& ctx, uint64_t* y, const uint64_t* const* ext, const uint64_t* const* evk,
+                              const uint64_t* add, uint64_t add_stride, uint32_t add_group, uint64_t* out, uint32_t n,
+                              uint32_t l, const TwPair* pinv, hipStream_t st) {
+    const uint32_t D = (l + ctx.alpha - 1) / ctx.alpha, E = l + ctx.K;
+    if (l == 0 || l > kMaxPmap || n == 0 || n > (uint32_t)kMaxList || D < 1 || D > 4 || add_group == 0)
+        return hipErrorInvalidValue;
+    JobSpec js{};
+    js.n_polys = 2 * n;
+    js.period = l;
+    js.n_primes = l;
+    for (uint32_t i = 0; i < l; i++) js.pmap[i] = (uint8_t)i;
+    KslFuse f{};
+    uint32_t distinct_ext = 0;
+    for (uint32_t c = 0; c < n; c++) {
+        f.ext.p[c] = ext[c];
+        f.evk.p[c] = evk[c];
+        distinct_ext += (c == 0 || ext[c] != ext[c - 1]) ? 1 : 0;
+    }
+    f.add = add;
+    f.out = out;
+    f.add_stride = add_stride;
+    f.n = n;
+    f.l = l;
+    f.E = E;
+    f.T = ctx.L + ctx.K;
+    f.add_group = add_group;
+    for (uint32_t i = 0; i < l; i++) f.pinv[i] = pinv[i];
+    const uint32_t n_jobs = 2 * n * l;
+    // algorithmic bytes: y read and written by pass A, read by pass B; ext limbs once per distinct ext, the keys and
+    // out per item, addend polys once per group; tables
+    const double limbs = (double)n_jobs * 3 + ((double)distinct_ext * D + (double)n * (2.0 * D + 2) +
+                                               (add ? (double)(n + add_group - 1) / add_group : 0.0)) * l;
+    const int pi = prof_begin(ctx, "ntt_fwd_ksl", limbs * kN * 8 + (double)l * kN * sizeof(TwPair), st);
+    hipLaunchKernelGGL(k_ntt_fwd_a, dim3(16, n_jobs), dim3(kTileThreads), 0, st, y, js, ctx.d_tw, ctx.d_primes);
+    const dim3 grid(16, n * l), block(2 * kTileThreads);
+    switch (D) {
+        case 1: hipLaunchKernelGGL(k_ntt_fwd_b_ksl<1>, grid, block, 0, st, y, ctx.d_twb, ctx.d_primes, f); break;
+        case 2: hipLaunchKernelGGL(k_ntt_fwd_b_ksl<2>, grid, block, 0, st, y, ctx.d_twb, ctx.d_primes, f); break;
+        case 3: hipLaunchKernelGGL(k_ntt_fwd_b_ksl<3>, grid, block, 0, st, y, ctx.d_twb, ctx.d_primes, f); break;
+        default: hipLaunchKernelGGL(k_ntt_fwd_b_ksl<4>, grid, block, 0, st, y, ctx.d_twb, ctx.d_primes, f); break;
+    }
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
 }
 
 // Inverse NTT of a job list over an accumulator [n_polys][E][N] (off = pc E + t) whose input, limb t of poly pc, is

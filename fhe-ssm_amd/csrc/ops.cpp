@@ -43,6 +43,9 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
                                  uint64_t add_pstride, const uint64_t* T, uint64_t* out, uint32_t B, uint32_t l,
                                  const TwPair* pinv, const TwPair* qlinv, hipStream_t st,
                                  const uint64_t* ta = nullptr, const uint64_t* tb = nullptr);
+hipError_t launch_ntt_fwd_ksl(const Context& ctx, uint64_t* y, const uint64_t* const* ext, const uint64_t* const* evk,
+                              const uint64_t* add, uint64_t add_stride, uint32_t add_group, uint64_t* out, uint32_t n,
+                              uint32_t l, const TwPair* pinv, hipStream_t st);
 hipError_t launch_ntt_inv_ks(const Context& ctx, uint64_t* acc, const JobSpec& js, uint32_t n_jobs,
                              const uint64_t* ext, const uint64_t* evk, uint32_t D, uint32_t E, hipStream_t st);
 hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x, uint64_t x_pstride,
@@ -543,6 +546,11 @@ void ks_moddown_list(Context& ctx, const uint64_t* const* ext, const uint64_t* c
     uint64_t* conv = (uint64_t*)ws_get(ctx, WS_CONV, (size_t)2 * n * l * W * 8);
     HIPX(launch_bconv(ctx, plan, acc, (uint64_t)E * W, in_off.data(), conv, (uint64_t)l * W, out_idx.data(), 2 * n,
                       st));
+    if (ctx.ntt_mode == NttMode::TwoPass && num_digits(ctx, l) <= 4) {
+        // the forward NTT of conv ends in the combine (conv never stored in evaluation form)
+        HIPX(launch_ntt_fwd_ksl(ctx, conv, ext, evk, add, add_stride, add_group, out, n, l, pinv.data(), st));
+        return;
+    }
     HIPX(launch_ntt(ctx, conv, regular_jobs(2 * n, out_idx), 2 * n * l, false, ctx.ntt_mode, st));
     HIPX(launch_ks_sub_list(ctx, ext, evk, conv, add, add_stride, add_group, out, n, l, pinv.data(), st));
 }

@@ -377,11 +377,6 @@ __global__ __launch_bounds__(256) void k_automorph(const uint64_t* __restrict__ 
 // ------------------------------------------------------------------ list forms (one key per item)
 // acc[c][0/1][t] = sum_d ext_c[d][t] * evk_c[d][0/1][prime(t)] with per-item ext and evk pointers
 // (hoisted rotations share one ext; giant-step rotations have one ext each).
-constexpr int kMaxList = 64;
-
-struct ListPtrs {
-    const uint64_t* p[kMaxList];
-};
 
 // XCD-aware order of a list kernel's one-dimensional grid: workgroups go to the 8 XCDs round-robin (wg mod 8), so
 // the m items of one (coefficient tile, limb) tile are given the ids xcd + 8 (blk m + item), all on one XCD: the
@@ -454,7 +449,8 @@ __global__ __launch_bounds__(256) void k_ks_sub_list(ListPtrs ext, ListPtrs evk,
 //   z = INTT(add_{l-1}) + (INTT(x_{l-1}) - conv_{l-1}) P^-1   (mod q_{l-1}):
 // the same words with one forward NTT of l-1 limbs instead of two (l for conv, l-1 for the lift).  The BConv
 // writes T directly (k_bconv<NIN, true, ..>); in a relinearization the evk inner product of limbs 0..l-2 is formed inside
-// the combine (k_mdr_combine_ks) and never stored.
+// the combine and never stored (the forward NTT of T ends in that combine, k_ntt_fwd_b_mdr in ntt.hip; under the fused
+// NTT mode k_mdr_combine_ks follows the NTT).
 
 // out_i = (add_i + x_i P^-1 - T_i) q_{l-1}^-1 in evaluation form, i < l-1
 __global__ __launch_bounds__(256) void k_mdr_combine(const uint64_t* __restrict__ x, const uint64_t* __restrict__ add,
