@@ -599,6 +599,31 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_b_ks(uint64_t* data, J
         inv_b_tile<false, false, kD>(a, xin, none, P, tw, blockIdx.x, threadIdx.x, lds, ks);
 }
 
+// k_ntt_inv_b_ks over a key-switch list: item c = pc / 2 has its own extension [kD][E][N] and key
+struct KslJobArgs {
+    ListPtrs ext, evk;
+    uint32_t E, T;
+};
+
+template <int kD>
+__global__ __launch_bounds__(kTileThreads) void k_ntt_inv_b_ksl(uint64_t* data, JobSpec js, const TwPair* tw_all,
+                                                               const PrimeInfo* primes, KslJobArgs ka) {
+    __shared__ uint64_t lds[kLdsWords];
+    uint32_t off, prime;
+    job_of(js, blockIdx.y, off, prime);
+    const uint32_t pc = off / ka.E, t = off - pc * ka.E, c = pc >> 1, p = pc & 1;
+    const PrimeInfo& P = primes[prime];
+    const uint64_t* xin = ka.ext.p[c] + (size_t)t * kN;
+    const KsIn ks{ka.evk.p[c] + ((size_t)p * ka.T + prime) * kN, (size_t)ka.E * kN, 2 * (size_t)ka.T * kN};
+    uint64_t* a = data + (size_t)off * kN;
+    const TwPair* tw = tw_all + (size_t)prime * kN;
+    const JobIn none{nullptr, nullptr};
+    if (P.q < kGsOpenMaxQ)
+        inv_b_tile<true, false, kD>(a, xin, none, P, tw, blockIdx.x, threadIdx.x, lds, ks);
+    else
+        inv_b_tile<false, false, kD>(a, xin, none, P, tw, blockIdx.x, threadIdx.x, lds, ks);
+}
+
 __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_a(uint64_t* data, JobSpec js, const TwPair* tw_all,
                                                            const PrimeInfo* primes) {
     __shared__ uint64_t lds[kLdsWords];
@@ -1022,6 +1047,32 @@ hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js_in, 
     hipError_t err = launch_ntt_kernels(ctx, data, js, n_jobs, inverse, mode, tw, twb, st);
     prof_end(ctx, pi, st);
     return err;
+}
+
+// launch_ntt_inv_ks for a key-switch list of n items (item c: extension ext[c] [D][E][N], key evk[c])
+hipError_t launch_ntt_inv_ksl(const Context& ctx, uint64_t* acc, const JobSpec& js, uint32_t n_jobs,
+                              const uint64_t* const* ext, const uint64_t* const* evk, uint32_t n, uint32_t D,
+                              uint32_t E, hipStream_t st) {
+    if (!js.jobs || D < 1 || D > 4 || n_jobs == 0 || n == 0 || n > (uint32_t)kMaxList) return hipErrorInvalidValue;
+    KslJobArgs ka{};
+    for (uint32_t c = 0; c < n; c++) {
+        ka.ext.p[c] = ext[c];
+        ka.evk.p[c] = evk[c];
+    }
+    ka.E = E;
+    ka.T = ctx.L + ctx.K;
+    const double bytes = (double)n_jobs * (2.0 * D + 3) * kN * 8 + (double)js.n_primes * kN * sizeof(TwPair);
+    const int pi = prof_begin(ctx, "ntt_inv_ks", bytes, st);
+    const dim3 grid(16, n_jobs), block(kTileThreads);
+    switch (D) {
+        case 1: hipLaunchKernelGGL(k_ntt_inv_b_ksl<1>, grid, block, 0, st, acc, js, ctx.d_itwb, ctx.d_primes, ka); break;
+        case 2: hipLaunchKernelGGL(k_ntt_inv_b_ksl<2>, grid, block, 0, st, acc, js, ctx.d_itwb, ctx.d_primes, ka); break;
+        case 3: hipLaunchKernelGGL(k_ntt_inv_b_ksl<3>, grid, block, 0, st, acc, js, ctx.d_itwb, ctx.d_primes, ka); break;
+        default: hipLaunchKernelGGL(k_ntt_inv_b_ksl<4>, grid, block, 0, st, acc, js, ctx.d_itwb, ctx.d_primes, ka); break;
+    }
+    hipLaunchKernelGGL(k_ntt_inv_a, grid, block, 0, st, acc, js, ctx.d_itw, ctx.d_primes);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
 }
 
 // Forward NTT of a key-switch list's converted P part y [2n][l][N] (coefficients, limb i over prime i; dense) whose

@@ -46,6 +46,9 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
 hipError_t launch_ntt_fwd_ksl(const Context& ctx, uint64_t* y, const uint64_t* const* ext, const uint64_t* const* evk,
                               const uint64_t* add, uint64_t add_stride, uint32_t add_group, uint64_t* out, uint32_t n,
                               uint32_t l, const TwPair* pinv, hipStream_t st);
+hipError_t launch_ntt_inv_ksl(const Context& ctx, uint64_t* acc, const JobSpec& js, uint32_t n_jobs,
+                              const uint64_t* const* ext, const uint64_t* const* evk, uint32_t n, uint32_t D,
+                              uint32_t E, hipStream_t st);
 hipError_t launch_ntt_inv_ks(const Context& ctx, uint64_t* acc, const JobSpec& js, uint32_t n_jobs,
                              const uint64_t* ext, const uint64_t* evk, uint32_t D, uint32_t E, hipStream_t st);
 hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x, uint64_t x_pstride,
@@ -512,21 +515,29 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
 
 // Key switch of a list of n <= 64 items (item c: extended digits ext[c] [D][E][N], key evk[c]) with its ModDown:
 // out [n][2][l][N] = ((sum_d ext_c[d] evk_c[d])_Q - BConv_{P->Q}(.._P)) P^-1, plus the addend's poly 0 (the
-// ciphertext at add + (c / add_group) * add_stride) on poly 0.  The inner product is stored only for the P
-// limbs; the combine forms the Q limbs itself, and P^-1 rides in the BConv table.  Same words as
-// k_ks_inner_list + moddown_inplace.
+// ciphertext at add + (c / add_group) * add_stride) on poly 0.  The inner product of the P limbs is formed by their
+// inverse NTT's first pass (stored first under the fused NTT mode); the combine, at the end of the converted part's
+// forward NTT, forms the Q limbs' itself; P^-1 rides in the BConv table.  Same words as k_ks_inner_list +
+// moddown_inplace.
 void ks_moddown_list(Context& ctx, const uint64_t* const* ext, const uint64_t* const* evk, uint32_t n, uint32_t l,
                      const uint64_t* add, uint64_t add_stride, uint32_t add_group, uint64_t* out, hipStream_t st) {
     check_level(ctx, l);
     const uint32_t E = l + ctx.K, K = ctx.K;
     if (K == 0) throw std::invalid_argument("ModDown needs special primes");
     uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)n * 2 * E * W * 8);
-    HIPX(launch_ks_inner_list(ctx, ext, evk, acc, n, l, st, l));
+    const bool fused = ctx.ntt_mode == NttMode::TwoPass && num_digits(ctx, l) <= 4;
     std::vector<Job> jobs;
     for (uint32_t pc = 0; pc < 2 * n; pc++)
         for (uint32_t k = 0; k < K; k++) jobs.push_back(Job{pc * E + l + k, ctx.L + k});
     const JobSpec js = cached_jobs(ctx, "mdP:" + std::to_string(2 * n) + ":" + std::to_string(l), std::move(jobs));
-    HIPX(launch_ntt(ctx, acc, js, 2 * n * K, true, ctx.ntt_mode, st));
+    if (fused) {
+        // the P limbs' inner products are formed by their inverse NTT's first pass
+        ctx.n_keyswitch += n;
+        HIPX(launch_ntt_inv_ksl(ctx, acc, js, 2 * n * K, ext, evk, n, num_digits(ctx, l), E, st));
+    } else {
+        HIPX(launch_ks_inner_list(ctx, ext, evk, acc, n, l, st, l));
+        HIPX(launch_ntt(ctx, acc, js, 2 * n * K, true, ctx.ntt_mode, st));
+    }
     std::vector<uint32_t> in_idx, in_off, out_idx;
     for (uint32_t k = 0; k < K; k++) {
         in_idx.push_back(ctx.L + k);
@@ -546,7 +557,7 @@ void ks_moddown_list(Context& ctx, const uint64_t* const* ext, const uint64_t* c
     uint64_t* conv = (uint64_t*)ws_get(ctx, WS_CONV, (size_t)2 * n * l * W * 8);
     HIPX(launch_bconv(ctx, plan, acc, (uint64_t)E * W, in_off.data(), conv, (uint64_t)l * W, out_idx.data(), 2 * n,
                       st));
-    if (ctx.ntt_mode == NttMode::TwoPass && num_digits(ctx, l) <= 4) {
+    if (fused) {
         // the forward NTT of conv ends in the combine (conv never stored in evaluation form)
         HIPX(launch_ntt_fwd_ksl(ctx, conv, ext, evk, add, add_stride, add_group, out, n, l, pinv.data(), st));
         return;
