@@ -576,6 +576,14 @@ void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const ui
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)B * D * E * W * 8);
     uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)B * 2 * E * W * 8);
     modup(ctx, x, ext, B, l, st, x_bstride);
+    if (ctx.ntt_mode == NttMode::TwoPass && D <= 4 && B <= 64 && (!add || add_div == 2)) {
+        // as a key-switch list with one key (up to 64 items): the inner products are formed by the ModDown's NTTs
+        // (the addend, when given, is a ciphertext batch whose c0 goes on poly 0)
+        std::vector<const uint64_t*> pe(B), pk(B, evk);
+        for (uint32_t c = 0; c < B; c++) pe[c] = ext + (size_t)c * D * E * W;
+        ks_moddown_list(ctx, pe.data(), pk.data(), B, l, add, add ? (uint64_t)2 * l * W : 0, 1, out2, st);
+        return;
+    }
     HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st));
     moddown_inplace(ctx, acc, 2 * B, l, add, out2, st, add_div);
 }
