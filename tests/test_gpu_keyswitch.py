@@ -139,24 +139,34 @@ def test_eval_mult_rescale_in_place(ckks, ctx, octx, evk, d_evk, alias):
 
 def test_relin_and_keyswitch_fused_ntt_mode(ckks, ctx, octx, evk, d_evk):
     """The other NTT schedule (mode 1: one limb per workgroup) takes the unfused combines (k_mdr_combine_ks with the
-    product's inputs, k_sub_scale after the NTT) in place of the NTT passes that end in them: same words."""
+    product's inputs, k_ks_sub_list and k_sub_scale after the NTT, the stored inner products, the separate lift) in
+    place of the NTT passes that end in or begin with them: same words."""
     B, l = 2, 9
     a = residues(ctx.moduli, (B, 2), list(range(l)), seed=35)
     b = residues(ctx.moduli, (B, 2), list(range(l)), seed=36)
     x = residues(ctx.moduli, (1,), list(range(l)), seed=37)
-    da, db, dx = (ckks.DeviceBuffer.from_array(v) for v in (a, b, x))
+    ct = residues(ctx.moduli, (2, 2), list(range(l)), seed=38)
+    da, db, dx, dct = (ckks.DeviceBuffer.from_array(v) for v in (a, b, x, ct))
     dout = ckks.DeviceBuffer(B * 2 * (l - 1) * N * 8)
     dks = ckks.DeviceBuffer(2 * l * N * 8)
+    drot = ckks.DeviceBuffer(ct.nbytes)
+    dres = ckks.DeviceBuffer(3 * (l - 1) * N * 8)
     ctx.set_ntt_mode(1)
     try:
         ctx.eval_mult_rescale(da.ptr, db.ptr, B, l, d_evk.ptr, dout.ptr)
         ctx.keyswitch(dx.ptr, 1, l, d_evk.ptr, dks.ptr)
+        ctx.eval_rotate(dct.ptr, 2, l, 5, d_evk.ptr, drot.ptr)
+        ctx.rescale(da.ptr, 3, l, dres.ptr)
     finally:
         ctx.set_ntt_mode(0)
     out = dout.download((B, 2, l - 1, N))
     for i in range(B):
         assert np.array_equal(out[i], octx.hmult_relin_rescale(a[i], b[i], l, evk)), i
     assert np.array_equal(dks.download((2, l, N)), octx.keyswitch(x[0], l, evk))
+    rot = drot.download(ct.shape)
+    for i in range(2):
+        assert np.array_equal(rot[i], octx.rotate(ct[i], l, octx.rot_index(5), evk)), i
+    assert np.array_equal(dres.download((3, l - 1, N)), octx.rescale(a.reshape(-1, l, N)[:3], l))
 
 
 def test_eval_mult_no_rescale(ckks, ctx, octx, evk, d_evk):
