@@ -24,6 +24,12 @@
 // (1 MiB) in L2.  Either both passes run as separate kernels (grid 16 x jobs, 256 threads), or the
 // fused kernel runs one limb per 512-thread workgroup (2 tiles at a time, passes separated by a
 // workgroup barrier; the intermediate stays in L2/MALL instead of making a second HBM round trip).
+//
+// The key-switching steps around the transforms are folded into their first and last passes, so that the
+// elementwise data they would store and reload never makes the round trip: an inverse first pass may form its input
+// (a product of two limbs, an evk inner product) and copy it into a ModUp buffer; a forward first pass may lift a
+// rescale's dropped limb; a forward last pass may end in a ModDown / rescale / key-switch combine (k_ntt_fwd_b_mdr,
+// k_ntt_fwd_b_sub, k_ntt_fwd_b_ksl) instead of storing the transform.
 #include <type_traits>
 
 #include "engine.hpp"
@@ -643,7 +649,7 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_a(uint64_t* data, JobS
 // combine instead of a store of T: for each word of limb i,
 //   out[2c+p][i] = (x_p P^-1 + add_p - T_p) q_{l-1}^-1,  x_p = sum_d ext[c][d][i] evk[d][p][i]  (the evk inner product),
 // add_0 = d0 = a0 b0 and add_1 = d1 = a0 b1 + a1 b0 formed from the product's inputs a, b [B][2][l][N], or read from
-// an addend [2B][..][N] (or none).  The same words as the NTT followed by k_mdr_combine_ks, without T's store and
+// an addend [2B][..][N].  The same words as the NTT followed by k_mdr_combine_ks, without T's store and
 // reload.  A workgroup is two 256-thread groups, one per poly of ciphertext c, each transforming the same tile of its
 // poly's limb i into an LDS tile of its own; then every thread finishes 8 words of the tile for both polys, so the
 // ext digits and the inputs are read once for the two.
