@@ -219,15 +219,24 @@ int ckks_host_free(void* h) {
 int ckks_side_copy(ckks_context* ctx, void* dst, const void* src, size_t bytes, void* stream, uint64_t* ticket) {
     if (!ctx || !dst || !src || !ticket) return fail(CKKS_EINVAL, "null argument");
     fhe::Context& c = ctx->c;
-    if (!c.side) HIP_TRY(hipStreamCreateWithFlags(&c.side, hipStreamNonBlocking));
+    // copies to host memory on their own side stream: a step's run of state copies out does not hold up the
+    // prefetches into device memory queued behind it
+    hipPointerAttribute_t at{};
+    bool to_host = false;
+    if (hipPointerGetAttributes(&at, dst) == hipSuccess)
+        to_host = at.type == hipMemoryTypeHost;
+    else
+        (void)hipGetLastError();  // pageable host memory: an unregistered pointer
+    hipStream_t& side = to_host ? c.side_out : c.side;
+    if (!side) HIP_TRY(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
     // after the work enqueued so far on stream
     hipEvent_t after = nullptr, done = nullptr;
     HIP_TRY(hipEventCreateWithFlags(&after, hipEventDisableTiming));
     hipError_t e = hipEventRecord(after, (hipStream_t)stream);
-    if (e == hipSuccess) e = hipStreamWaitEvent(c.side, after, 0);
-    if (e == hipSuccess) e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, c.side);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side, after, 0);
+    if (e == hipSuccess) e = hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, side);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&done, hipEventDisableTiming);
-    if (e == hipSuccess) e = hipEventRecord(done, c.side);
+    if (e == hipSuccess) e = hipEventRecord(done, side);
     c.side_after.push_back(after);  // destroyed at the next ckks_side_sync, once the side stream has drained
     if (e != hipSuccess) {
         if (done) (void)hipEventDestroy(done);
@@ -250,6 +259,7 @@ int ckks_side_sync(ckks_context* ctx) {
     if (!ctx) return fail(CKKS_EINVAL, "null context");
     fhe::Context& c = ctx->c;
     if (c.side) HIP_TRY(hipStreamSynchronize(c.side));
+    if (c.side_out) HIP_TRY(hipStreamSynchronize(c.side_out));
     for (auto& kv : c.side_ev) (void)hipEventDestroy(kv.second);
     c.side_ev.clear();
     for (auto ev : c.side_after) (void)hipEventDestroy(ev);

@@ -234,12 +234,15 @@ void context_release(Context& c) {
         if (e) (void)hipEventDestroy(e);
     c.ring_host = c.ring_dev = nullptr;
     if (c.side) (void)hipStreamSynchronize(c.side);
+    if (c.side_out) (void)hipStreamSynchronize(c.side_out);
     for (auto& kv : c.side_ev) (void)hipEventDestroy(kv.second);
     c.side_ev.clear();
     for (auto ev : c.side_after) (void)hipEventDestroy(ev);
     c.side_after.clear();
     if (c.side) (void)hipStreamDestroy(c.side);
+    if (c.side_out) (void)hipStreamDestroy(c.side_out);
     c.side = nullptr;
+    c.side_out = nullptr;
     c.job_cache.clear();
     c.bconv_cache.clear();
     c.scratch.clear();

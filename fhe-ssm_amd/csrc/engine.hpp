@@ -136,9 +136,11 @@ struct Context {
     hipEvent_t ring_ev[kRingSlots] = {};
     bool ring_used[kRingSlots] = {};
     uint32_t ring_next = 0;
-    // side stream for copies that overlap the work (created on first use, non-blocking, default priority) and the
-    // events of the copies issued on it, by ticket
+    // side streams for copies that overlap the work (created on first use, non-blocking, default priority): copies to
+    // host memory on side_out, every other copy on side (so that a long run of copies out never delays a copy in);
+    // the events of the copies issued on them, by ticket
     hipStream_t side = nullptr;
+    hipStream_t side_out = nullptr;
     uint64_t side_next = 0;
     std::map<uint64_t, hipEvent_t> side_ev;
     std::vector<hipEvent_t> side_after;  // the events the side copies waited on

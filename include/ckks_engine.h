@@ -84,7 +84,9 @@ int ckks_memcpy_h2d(void* d_dst, const void* h_src, size_t bytes);
 int ckks_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes);
 /* Pinned host memory, and copies on a side stream of the context that overlap the work on the caller's stream (no
  * counterpart in the reference; for a caller that keeps copies of device data on the host while it computes):
- * ckks_side_copy   copies bytes (any direction) once the work enqueued so far on stream is done; returns a ticket
+ * ckks_side_copy   copies bytes (any direction) once the work enqueued so far on stream is done; returns a ticket.
+ *                  Copies to host memory run on one side stream, all others on another: copies of one kind complete
+ *                  in issue order, copies of different kinds are not ordered against each other (wait on the ticket)
  * ckks_side_wait   makes stream wait (without blocking the host) until the copy of ticket is done
  * ckks_side_sync   blocks the host until every side copy is done and forgets the tickets */
 int ckks_host_alloc(size_t bytes, void** h_out);
