@@ -120,6 +120,10 @@ struct Context {
     // cached device job lists keyed by a shape string (list, distinct primes in it)
     std::map<std::string, std::pair<Job*, uint32_t>> job_cache;
     std::map<std::string, BConvPlan> bconv_cache;
+    // per-limb constants of the Q chain with their Shoup companions, computed on first use: P^-1 mod q_i,
+    // P R^-1 mod q_i (R = 2^64), and by j the row q_j^-1 mod q_i (i < j)
+    std::vector<TwPair> tab_pinv, tab_pmodr;
+    std::map<uint32_t, std::vector<TwPair>> tab_qinv;
     // growable scratch
     std::vector<std::pair<void*, size_t>> scratch;
     // device tables [L+K][N'] of the small-ring NTTs used by periodic encoding, by ring size N'

@@ -316,6 +316,48 @@ const BConvPlan& bconv_plan(Context& ctx, const std::vector<uint32_t>& in_idx, c
 // ------------------------------------------------------------------ level geometry
 uint32_t num_digits(const Context& ctx, uint32_t l) { return (l + ctx.alpha - 1) / ctx.alpha; }
 
+// P mod q (P the product of the special primes)
+static uint64_t p_mod(const Context& ctx, uint64_t q) {
+    uint64_t P = 1;
+    for (uint32_t k = 0; k < ctx.K; k++) P = mulmod_h(P, ctx.moduli[ctx.L + k] % q, q);
+    return P;
+}
+
+// the per-limb constant tables of the context (each computed once; a call reads the first l entries)
+static const std::vector<TwPair>& pinv_tab(Context& ctx) {
+    if (ctx.tab_pinv.empty()) {
+        for (uint32_t i = 0; i < ctx.L; i++) {
+            const uint64_t q = ctx.moduli[i], v = invmod_h(p_mod(ctx, q), q);
+            ctx.tab_pinv.push_back(TwPair{v, shoup_companion(v, q)});
+        }
+    }
+    return ctx.tab_pinv;
+}
+
+static const std::vector<TwPair>& pmodr_tab(Context& ctx) {
+    if (ctx.tab_pmodr.empty()) {
+        for (uint32_t i = 0; i < ctx.L; i++) {
+            const uint64_t q = ctx.moduli[i];
+            const uint64_t rinv = invmod_h((uint64_t)(((unsigned __int128)1 << 64) % q), q);
+            const uint64_t v = mulmod_h(p_mod(ctx, q), rinv, q);
+            ctx.tab_pmodr.push_back(TwPair{v, shoup_companion(v, q)});
+        }
+    }
+    return ctx.tab_pmodr;
+}
+
+static const std::vector<TwPair>& qinv_row(Context& ctx, uint32_t j) {
+    auto it = ctx.tab_qinv.find(j);
+    if (it != ctx.tab_qinv.end()) return it->second;
+    std::vector<TwPair> row(j);
+    const uint64_t qj = ctx.moduli[j];
+    for (uint32_t i = 0; i < j; i++) {
+        const uint64_t q = ctx.moduli[i], v = invmod_h(qj % q, q);
+        row[i] = TwPair{v, shoup_companion(v, q)};
+    }
+    return ctx.tab_qinv.emplace(j, std::move(row)).first->second;
+}
+
 static uint32_t ext_prime(const Context& ctx, uint32_t l, uint32_t t) { return t < l ? t : ctx.L + (t - l); }
 
 static void check_level(const Context& ctx, uint32_t l) {
@@ -414,14 +456,7 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
     uint64_t* conv = (uint64_t*)ws_get(ctx, WS_CONV, (size_t)n_polys * l * W * 8);
     HIPX(launch_bconv(ctx, plan, x, (uint64_t)xs * W, in_off.data(), conv, (uint64_t)l * W, out_off.data(), n_polys,
                       st));
-    std::vector<TwPair> pinv(l);
-    for (uint32_t i = 0; i < l; i++) {
-        const uint64_t q = ctx.moduli[i];
-        uint64_t P = 1;
-        for (uint32_t k = 0; k < K; k++) P = mulmod_h(P, ctx.moduli[ctx.L + k] % q, q);
-        const uint64_t v = invmod_h(P, q);
-        pinv[i] = TwPair{v, shoup_companion(v, q)};
-    }
+    const std::vector<TwPair> pinv(pinv_tab(ctx).begin(), pinv_tab(ctx).begin() + l);
     const uint64_t aps = add_pstride < 0 ? (uint64_t)add_div * l * W : (uint64_t)add_pstride;
     if (ctx.ntt_mode == NttMode::TwoPass) {
         // the forward NTT of conv ends in the combine (conv is never stored in evaluation form)
@@ -467,18 +502,13 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
         ja.src_period = l;
         HIPX(launch_ntt(ctx, addc, ja, n_polys, true, ctx.ntt_mode, st));
     }
-    std::vector<TwPair> pinv(l), qlinv(l);
+    const std::vector<TwPair>& ptab = pinv_tab(ctx);
+    const std::vector<TwPair>& qrow = qinv_row(ctx, l - 1);
+    std::vector<TwPair> pinv(ptab.begin(), ptab.begin() + l), qlinv(l);
     std::vector<uint64_t> col(l);
-    const uint64_t ql = ctx.moduli[l - 1];
     for (uint32_t i = 0; i < l; i++) {
-        const uint64_t q = ctx.moduli[i];
-        uint64_t P = 1;
-        for (uint32_t k = 0; k < K; k++) P = mulmod_h(P, ctx.moduli[ctx.L + k] % q, q);
-        const uint64_t v = invmod_h(P, q);
-        pinv[i] = TwPair{v, shoup_companion(v, q)};
-        col[i] = i + 1 < l ? v : 1;  // columns 0..l-2 carry P^-1; the dropped limb's column stays plain
-        const uint64_t u = i + 1 < l ? invmod_h(ql % q, q) : 0;
-        qlinv[i] = TwPair{u, i + 1 < l ? shoup_companion(u, q) : 0};
+        col[i] = i + 1 < l ? pinv[i].w : 1;  // columns 0..l-2 carry P^-1; the dropped limb's column stays plain
+        qlinv[i] = i + 1 < l ? qrow[i] : TwPair{0, 0};
     }
     std::vector<uint32_t> in_idx, in_off, out_idx;
     for (uint32_t k = 0; k < K; k++) {
@@ -543,15 +573,11 @@ void ks_moddown_list(Context& ctx, const uint64_t* const* ext, const uint64_t* c
         in_idx.push_back(ctx.L + k);
         in_off.push_back(l + k);
     }
-    std::vector<TwPair> pinv(l);
+    const std::vector<TwPair> pinv(pinv_tab(ctx).begin(), pinv_tab(ctx).begin() + l);
     std::vector<uint64_t> col(l);
     for (uint32_t i = 0; i < l; i++) {
         out_idx.push_back(i);
-        const uint64_t q = ctx.moduli[i];
-        uint64_t P = 1;
-        for (uint32_t k = 0; k < K; k++) P = mulmod_h(P, ctx.moduli[ctx.L + k] % q, q);
-        col[i] = invmod_h(P, q);
-        pinv[i] = TwPair{col[i], shoup_companion(col[i], q)};
+        col[i] = pinv[i].w;
     }
     const BConvPlan& plan = bconv_plan(ctx, in_idx, out_idx, ctx.moddown_exact, col);
     uint64_t* conv = (uint64_t*)ws_get(ctx, WS_CONV, (size_t)2 * n * l * W * 8);
@@ -599,13 +625,8 @@ void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uin
     jl.src = in + (size_t)(l - 1) * W;
     jl.src_period = l;
     HIPX(launch_ntt(ctx, last, jl, n_polys, true, ctx.ntt_mode, st));
-    std::vector<TwPair> s(l - 1);
+    const std::vector<TwPair>& s = qinv_row(ctx, l - 1);  // q_{l-1}^-1 mod q_i, i < l-1
     const uint64_t ql = ctx.moduli[l - 1];
-    for (uint32_t i = 0; i + 1 < l; i++) {
-        const uint64_t q = ctx.moduli[i];
-        const uint64_t v = invmod_h(ql % q, q);
-        s[i] = TwPair{v, shoup_companion(v, q)};
-    }
     if (ctx.ntt_mode == NttMode::TwoPass) {
         // the lift happens in the forward NTT's first pass, and its second pass ends in the combine:
         // out = (in - NTT(lift(last))) q_{l-1}^-1
@@ -1020,18 +1041,11 @@ void bsgs_dh_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, uin
     if (nb == 0 || nb > 32 || n_in * nb > 64 || n_in == 0 || n_out == 0 || ng == 0 || ng > 64 || n_inst == 0 ||
         l < 2)
         throw std::invalid_argument("bad BSGS shape");
-    const uint32_t E = l + ctx.K, D = num_digits(ctx, l), K = ctx.K;
+    const uint32_t E = l + ctx.K, D = num_digits(ctx, l);
     const size_t ctw = (size_t)2 * l * W, cte = (size_t)2 * E * W, exw = (size_t)D * E * W;
     const uint32_t nbt = n_in * nb, n_x = n_inst * n_in, n_o = n_inst * n_out;
-    std::vector<TwPair> pmod(l);  // P R^-1 mod q_t (R = 2^64; the double-hoisted MAC keeps its babies R^-1-scaled)
-    for (uint32_t t = 0; t < l; t++) {
-        const uint64_t q = ctx.moduli[t];
-        uint64_t P = 1;
-        for (uint32_t k = 0; k < K; k++) P = mulmod_h(P, ctx.moduli[ctx.L + k] % q, q);
-        const uint64_t rinv = invmod_h((uint64_t)(((unsigned __int128)1 << 64) % q), q);
-        P = mulmod_h(P, rinv, q);
-        pmod[t] = TwPair{P, shoup_companion(P, q)};
-    }
+    // P R^-1 mod q_t (R = 2^64; the double-hoisted MAC keeps its babies R^-1-scaled)
+    const std::vector<TwPair>& pmod = pmodr_tab(ctx);
     // the inputs side by side (read in place when they already are), their c1 extended once
     const uint64_t* X = in[0];
     for (uint32_t x = 1; x < n_x; x++)

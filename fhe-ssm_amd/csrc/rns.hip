@@ -1467,10 +1467,12 @@ hipError_t launch_lincomb(const Context& ctx, uint64_t* out, uint32_t B, uint32_
         la.x[t] = x[t];
         la.stride[t] = stride[t];
         for (uint32_t i = 0; i < l_out; i++) {
-            // C R mod q_i (k_lincomb reduces by REDC)
-            const uint64_t q = ctx.moduli[i];
-            const unsigned __int128 r = ((unsigned __int128)1 << 64) % q;
-            la.C[t][i] = (uint64_t)((unsigned __int128)(C[(size_t)t * l_out + i] % q) * r % q);
+            // C R mod q_i (k_lincomb reduces by REDC), a Shoup product by the context's R mod q_i
+            const PrimeInfo& pr = ctx.primes[i];
+            const uint64_t c = C[(size_t)t * l_out + i] % pr.q;
+            const uint64_t h = (uint64_t)(((unsigned __int128)c * pr.r_mod_p) >> 64);
+            const uint64_t v = c * pr.r_mod - h * pr.q;
+            la.C[t][i] = v >= pr.q ? v - pr.q : v;
         }
     }
     if (add)
