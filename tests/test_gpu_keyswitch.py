@@ -233,3 +233,29 @@ def test_error_paths(ckks, ctx):
     assert lib.ckks_keyswitch(ctx.h, 1, 1, L + 1, 1, 1, None) == 1
     assert b"level" in lib.ckks_last_error()
     assert lib.ckks_eval_rotate(ctx.h, 8, 1, 4, 1, 8, 8, None) == 1
+
+
+def test_four_digit_key_switch(ckks, oracle):
+    """Four digits (L = 32, dnum = 4): the 4-digit instances of the kernels that form the evk inner products inside
+    the NTT passes (relinearization with rescale, key switch, rotation) against the oracle."""
+    L4, K4, D4 = 32, 8, 4
+    c4 = ckks.Context(num_q=L4, num_p=K4, dnum=D4, q_bits=54, p_bits=60)
+    o4 = oracle.Ctx(16, c4.moduli, L4, K4, D4)
+    l = L4
+    assert c4.num_digits(l) == 4
+    ev = residues(c4.moduli, (D4, 2), list(range(L4 + K4)), seed=91)
+    dev = ckks.DeviceBuffer.from_array(ev)
+    a = residues(c4.moduli, (1, 2), list(range(l)), seed=92)
+    b = residues(c4.moduli, (1, 2), list(range(l)), seed=93)
+    x = residues(c4.moduli, (1,), list(range(l)), seed=94)
+    da, db, dx = (ckks.DeviceBuffer.from_array(v) for v in (a, b, x))
+    dout = ckks.DeviceBuffer(2 * (l - 1) * N * 8)
+    c4.eval_mult_rescale(da.ptr, db.ptr, 1, l, dev.ptr, dout.ptr)
+    assert np.array_equal(dout.download((2, l - 1, N)), o4.hmult_relin_rescale(a[0], b[0], l, ev))
+    dks = ckks.DeviceBuffer(2 * l * N * 8)
+    c4.keyswitch(dx.ptr, 1, l, dev.ptr, dks.ptr)
+    assert np.array_equal(dks.download((2, l, N)), o4.keyswitch(x[0], l, ev))
+    drot = ckks.DeviceBuffer(a.nbytes)
+    c4.eval_rotate(da.ptr, 1, l, 3, dev.ptr, drot.ptr)
+    assert np.array_equal(drot.download(a.shape)[0], o4.rotate(a[0], l, o4.rot_index(3), ev))
+    c4.close()
