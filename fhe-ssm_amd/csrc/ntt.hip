@@ -807,6 +807,10 @@ struct KslFuse {
     uint64_t* out;        // [n][2][l][N]
     uint64_t add_stride;
     uint32_t n, l, E, T, add_group;
+    // auto_on: item c's output is mapped by X -> X^g_c (a rotation), ginv[c] = g_c^-1 mod 2N: the word formed at
+    // index s is stored at the index whose source s is (see KslEpi::end)
+    uint32_t auto_on;
+    uint32_t ginv[kMaxList];
     TwPair pinv[kMaxPmap];
 };
 
@@ -863,9 +867,22 @@ struct KslEpi {
             uint64_t v0 = sub_mod(shoup(reduce_sum(s0, br), pinv.w, pinv.wp, q), L0[rl + 17 * k], q);
             const uint64_t v1 = sub_mod(shoup(reduce_sum(s1, br), pinv.w, pinv.wp, q), L1[rl + 17 * k], q);
             if (f.add) v0 = add_mod(v0, cur.u0, q);
-            const uint32_t bo = (256 * blk + rl + 16 * k) * 8;
-            __builtin_nontemporal_store(v0, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out0) + bo));
-            __builtin_nontemporal_store(v1, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out1) + bo));
+            const uint32_t w = 256 * blk + rl + 16 * k;
+            if (f.auto_on) {
+                // the automorphism: out[k'] = v[src(k')] with src(k') = brev((g (2 brev(k') + 1) mod 2N - 1) / 2), so
+                // word w goes to k' = brev((g^-1 (2 brev(w) + 1) mod 2N - 1) / 2).  That index lies in one 256-word
+                // block for all w of a block (the low 8 bits of an exponent r' = g r + (g - 1) / 2 depend on those of
+                // r only), so a block's stores fill one output block: ordinary stores, which the L2 merges
+                const uint32_t r = __brev(w) >> (32 - kLogN);
+                const uint32_t e = (f.ginv[c] * (2u * r + 1u)) & (2u * kN - 1u);
+                const uint32_t dst = __brev((e - 1u) >> 1) >> (32 - kLogN);
+                out0[dst] = v0;
+                out1[dst] = v1;
+            } else {
+                const uint32_t bo = w * 8;
+                __builtin_nontemporal_store(v0, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out0) + bo));
+                __builtin_nontemporal_store(v1, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out1) + bo));
+            }
             if (kk < 7) cur = nxt;
         }
     }
@@ -1083,11 +1100,12 @@ hipError_t launch_ntt_inv_ksl(const Context& ctx, uint64_t* acc, const JobSpec& 
 
 // Forward NTT of a key-switch list's converted P part y [2n][l][N] (coefficients, limb i over prime i; dense) whose
 // pass B ends in k_ks_sub_list's combine: out [n][2][l][N] = x P^-1 - NTT(y) (+ the addend's poly 0), x the evk inner
-// product of item c's extension and key.  y is left holding the first pass's intermediate.  Digit counts 1..4
-// (others: hipErrorInvalidValue, the caller runs the NTT and k_ks_sub_list).
+// product of item c's extension and key.  gidx (optional): item c's output mapped by X -> X^gidx[c] (odd, < 2N) as it
+// is stored -- a rotation's automorphism, no separate permutation pass.  y is left holding the first pass's
+// intermediate.  Digit counts 1..4 (others: hipErrorInvalidValue, the caller runs the NTT and k_ks_sub_list).
 hipError_t launch_ntt_fwd_ksl(const Context& ctx, uint64_t* y, const uint64_t* const* ext, const uint64_t* const* evk,
                               const uint64_t* add, uint64_t add_stride, uint32_t add_group, uint64_t* out, uint32_t n,
-                              uint32_t l, const TwPair* pinv, hipStream_t st) {
+                              uint32_t l, const TwPair* pinv, hipStream_t st, const uint32_t* gidx) {
     const uint32_t D = (l + ctx.alpha - 1) / ctx.alpha, E = l + ctx.K;
     if (l == 0 || l > kMaxPmap || n == 0 || n > (uint32_t)kMaxList || D < 1 || D > 4 || add_group == 0)
         return hipErrorInvalidValue;
@@ -1112,6 +1130,16 @@ hipError_t launch_ntt_fwd_ksl(const Context& ctx, uint64_t* y, const uint64_t* c
     f.T = ctx.L + ctx.K;
     f.add_group = add_group;
     for (uint32_t i = 0; i < l; i++) f.pinv[i] = pinv[i];
+    if (gidx) {
+        f.auto_on = 1;
+        for (uint32_t c = 0; c < n; c++) {
+            if ((gidx[c] & 1u) == 0 || gidx[c] >= 2 * kN) return hipErrorInvalidValue;
+            // g^-1 mod 2N by Newton's iteration (g odd: x = g is correct to 3 bits, each step doubles them)
+            uint32_t x = gidx[c];
+            for (int it = 0; it < 4; it++) x *= 2u - gidx[c] * x;
+            f.ginv[c] = x & (2 * kN - 1);
+        }
+    }
     const uint32_t n_jobs = 2 * n * l;
     // algorithmic bytes: y read and written by pass A, read by pass B; ext limbs once per distinct ext, the keys and
     // out per item, addend polys once per group; tables

@@ -45,7 +45,7 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
                                  const uint64_t* ta = nullptr, const uint64_t* tb = nullptr);
 hipError_t launch_ntt_fwd_ksl(const Context& ctx, uint64_t* y, const uint64_t* const* ext, const uint64_t* const* evk,
                               const uint64_t* add, uint64_t add_stride, uint32_t add_group, uint64_t* out, uint32_t n,
-                              uint32_t l, const TwPair* pinv, hipStream_t st);
+                              uint32_t l, const TwPair* pinv, hipStream_t st, const uint32_t* gidx = nullptr);
 hipError_t launch_ntt_inv_ksl(const Context& ctx, uint64_t* acc, const JobSpec& js, uint32_t n_jobs,
                               const uint64_t* const* ext, const uint64_t* const* evk, uint32_t n, uint32_t D,
                               uint32_t E, hipStream_t st);
@@ -548,9 +548,11 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
 // ciphertext at add + (c / add_group) * add_stride) on poly 0.  The inner product of the P limbs is formed by their
 // inverse NTT's first pass (stored first under the fused NTT mode); the combine, at the end of the converted part's
 // forward NTT, forms the Q limbs' itself; P^-1 rides in the BConv table.  Same words as k_ks_inner_list +
-// moddown_inplace.
+// moddown_inplace.  gidx (optional): item c's output is then mapped by X -> X^gidx[c] (a rotation's automorphism),
+// applied by the combine as it stores.
 void ks_moddown_list(Context& ctx, const uint64_t* const* ext, const uint64_t* const* evk, uint32_t n, uint32_t l,
-                     const uint64_t* add, uint64_t add_stride, uint32_t add_group, uint64_t* out, hipStream_t st) {
+                     const uint64_t* add, uint64_t add_stride, uint32_t add_group, uint64_t* out, hipStream_t st,
+                     const uint32_t* gidx = nullptr) {
     check_level(ctx, l);
     const uint32_t E = l + ctx.K, K = ctx.K;
     if (K == 0) throw std::invalid_argument("ModDown needs special primes");
@@ -583,13 +585,20 @@ void ks_moddown_list(Context& ctx, const uint64_t* const* ext, const uint64_t* c
     uint64_t* conv = (uint64_t*)ws_get(ctx, WS_CONV, (size_t)2 * n * l * W * 8);
     HIPX(launch_bconv(ctx, plan, acc, (uint64_t)E * W, in_off.data(), conv, (uint64_t)l * W, out_idx.data(), 2 * n,
                       st));
+    // the combine applies the automorphisms as it stores, unless out overlaps the addends' polys 0 (a permuted store
+    // may land on words another workgroup has still to read): then the key switch goes to a workspace first
+    const uint64_t* add_end = add ? add + (size_t)((n - 1) / std::max(add_group, 1u)) * add_stride + (size_t)l * W : nullptr;
+    const bool add_overlap = add && out < add_end && add < out + (size_t)n * 2 * l * W;
+    uint64_t* ks = gidx && (!fused || add_overlap) ? (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)n * 2 * l * W * 8) : out;
     if (fused) {
         // the forward NTT of conv ends in the combine (conv never stored in evaluation form)
-        HIPX(launch_ntt_fwd_ksl(ctx, conv, ext, evk, add, add_stride, add_group, out, n, l, pinv.data(), st));
-        return;
+        HIPX(launch_ntt_fwd_ksl(ctx, conv, ext, evk, add, add_stride, add_group, ks, n, l, pinv.data(), st,
+                                ks == out ? gidx : nullptr));
+    } else {
+        HIPX(launch_ntt(ctx, conv, regular_jobs(2 * n, out_idx), 2 * n * l, false, ctx.ntt_mode, st));
+        HIPX(launch_ks_sub_list(ctx, ext, evk, conv, add, add_stride, add_group, ks, n, l, pinv.data(), st));
     }
-    HIPX(launch_ntt(ctx, conv, regular_jobs(2 * n, out_idx), 2 * n * l, false, ctx.ntt_mode, st));
-    HIPX(launch_ks_sub_list(ctx, ext, evk, conv, add, add_stride, add_group, out, n, l, pinv.data(), st));
+    if (gidx && ks != out) HIPX(launch_automorph_list(ctx, ks, out, n, l, gidx, st));
 }
 
 // ------------------------------------------------------------------ key switch
@@ -819,15 +828,13 @@ void automorph_ks_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l
     }
     const uint32_t D = num_digits(ctx, l), E = l + ctx.K;
     uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)n * D * E * W * 8);
-    uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)n * 2 * l * W * 8);
     modup(ctx, cts + (size_t)l * W, ext, n, l, st, (uint64_t)2 * l * W);  // the c1 polys, read in place
     std::vector<const uint64_t*> ep(n);
     for (uint32_t c = 0; c < n; c++) {
         ep[c] = ext + (size_t)c * D * E * W;
         if ((gidx[c] & 1) == 0 || gidx[c] >= 2 * kN) throw std::invalid_argument("automorphism index must be odd < 2N");
     }
-    ks_moddown_list(ctx, ep.data(), evk, n, l, cts, (uint64_t)2 * l * W, 1, ks, st);
-    HIPX(launch_automorph_list(ctx, ks, out, n, l, gidx, st));
+    ks_moddown_list(ctx, ep.data(), evk, n, l, cts, (uint64_t)2 * l * W, 1, out, st, gidx);
 }
 
 // one ciphertext [2][l][N] rotated by n steps with one shared ModUp -> out [n][2][l][N]
@@ -851,13 +858,11 @@ void rotate_hoisted_ext(Context& ctx, const uint64_t* ct, const uint64_t* ext, u
                                out + (size_t)c0 * 2 * l * W, st);
         return;
     }
-    uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)n * 2 * l * W * 8);
     std::vector<const uint64_t*> ep(n, ext);
     std::vector<uint32_t> g(n);
     for (uint32_t c = 0; c < n; c++) g[c] = rotation_index(steps[c]);
     // c0 (the same for every rotation) is the ModDown addend of poly 0 of each output
-    ks_moddown_list(ctx, ep.data(), evk, n, l, ct, 0, 1, ks, st);
-    HIPX(launch_automorph_list(ctx, ks, out, n, l, g.data(), st));
+    ks_moddown_list(ctx, ep.data(), evk, n, l, ct, 0, 1, out, st, g.data());
 }
 
 // n_ct ciphertexts [n_ct][2][l][N], each rotated by the same n steps over one ModUp of its own:
@@ -879,7 +884,6 @@ void rotate_hoisted_multi(Context& ctx, const uint64_t* cts, uint32_t n_ct, uint
     const uint32_t per = 64 / n;  // ciphertexts per list (a list starts at a ciphertext boundary)
     for (uint32_t c0 = 0; c0 < n_ct; c0 += per) {
         const uint32_t nc = std::min(per, n_ct - c0), m = nc * n;
-        uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)m * 2 * l * W * 8);
         std::vector<const uint64_t*> ep(m), kp(m);
         std::vector<uint32_t> gm(m);
         for (uint32_t j = 0; j < m; j++) {
@@ -888,8 +892,8 @@ void rotate_hoisted_multi(Context& ctx, const uint64_t* cts, uint32_t n_ct, uint
             gm[j] = g[j % n];
         }
         // c0 of ciphertext c is the addend of poly 0 of its n outputs
-        ks_moddown_list(ctx, ep.data(), kp.data(), m, l, cts + (size_t)c0 * ctw, ctw, n, ks, st);
-        HIPX(launch_automorph_list(ctx, ks, out + (size_t)c0 * n * ctw, m, l, gm.data(), st));
+        ks_moddown_list(ctx, ep.data(), kp.data(), m, l, cts + (size_t)c0 * ctw, ctw, n, out + (size_t)c0 * n * ctw,
+                        st, gm.data());
     }
 }
 

@@ -213,6 +213,39 @@ def test_eval_rotate(ckks, ctx, octx, evk, d_evk, step):
         assert np.array_equal(out[i], octx.rotate(ct[i], l, g, evk)), i
 
 
+def test_rotation_lists_out_of_place_and_in_place(ckks, ctx, octx, evk, d_evk):
+    """The list rotations (many, hoisted, automorphism with key switch), whose automorphism the key-switch combine
+    applies as it stores, against the oracle's rotations -- out of place, and in place, where the output overlaps
+    the ciphertext whose c0 the combine adds (the combine then writes a workspace and a permutation pass follows)."""
+    l = 12
+    cts = residues(ctx.moduli, (2, 2), list(range(l)), seed=91)
+    g1, g3, gc = octx.rot_index(1), octx.rot_index(-3), 2 * N - 1
+    r01 = octx.rotate(cts[0], l, g1, evk)
+    r03 = octx.rotate(cts[0], l, g3, evk)
+    r13 = octx.rotate(cts[1], l, g3, evk)
+    r0c = octx.rotate(cts[0], l, gc, evk)
+    keys = [d_evk.ptr, d_evk.ptr]
+    dct = ckks.DeviceBuffer.from_array(cts)
+    dout = ckks.DeviceBuffer(cts.nbytes)
+    ctx.eval_rotate_many(dct.ptr, l, [1, -3], keys, dout.ptr)
+    out = dout.download(cts.shape)
+    assert np.array_equal(out[0], r01) and np.array_equal(out[1], r13)
+    ctx.eval_rotate_hoisted(dct.ptr, l, [1, -3], keys, dout.ptr)
+    out = dout.download(cts.shape)
+    assert np.array_equal(out[0], r01) and np.array_equal(out[1], r03)
+    ctx.eval_automorphism_ks(dct.ptr, 1, l, gc, d_evk.ptr, dout.ptr)
+    assert np.array_equal(dout.download(cts[0].shape), r0c)
+    # in place: the hoisted rotations' outputs over the ciphertext itself, the conjugation of ciphertext 0 over itself
+    dbuf = ckks.DeviceBuffer.from_array(cts)
+    ctx.eval_rotate_hoisted(dbuf.ptr, l, [1, -3], keys, dbuf.ptr)
+    out = dbuf.download(cts.shape)
+    assert np.array_equal(out[0], r01) and np.array_equal(out[1], r03)
+    dbuf = ckks.DeviceBuffer.from_array(cts)
+    ctx.eval_automorphism_ks(dbuf.ptr, 1, l, gc, d_evk.ptr, dbuf.ptr)
+    out = dbuf.download(cts.shape)
+    assert np.array_equal(out[0], r0c) and np.array_equal(out[1], cts[1])
+
+
 def test_eval_add(ckks, ctx):
     l = 5
     x = residues(ctx.moduli, (4,), list(range(l)), seed=70)
