@@ -121,8 +121,8 @@ struct Context {
     std::map<std::string, std::pair<Job*, uint32_t>> job_cache;
     std::map<std::string, BConvPlan> bconv_cache;
     // per-limb constants of the Q chain with their Shoup companions, computed on first use: P^-1 mod q_i,
-    // P R^-1 mod q_i (R = 2^64), and by j the row q_j^-1 mod q_i (i < j)
-    std::vector<TwPair> tab_pinv, tab_pmodr;
+    // P R^-1 mod q_i (R = 2^64), P mod q_i, and by j the row q_j^-1 mod q_i (i < j)
+    std::vector<TwPair> tab_pinv, tab_pmodr, tab_pmod;
     std::map<uint32_t, std::vector<TwPair>> tab_qinv;
     // growable scratch
     std::vector<std::pair<void*, size_t>> scratch;

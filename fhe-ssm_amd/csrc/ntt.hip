@@ -662,7 +662,8 @@ struct MdrFuse {
     uint64_t* out;        // [2B][l-1][N]
     uint64_t add_pstride;
     uint32_t B, l, E, T;
-    TwPair pinv[kMaxPmap], qlinv[kMaxPmap];
+    TwPair pmod[kMaxPmap];  // P mod q_i
+    TwPair cfin[kMaxPmap];  // R P^-1 q_{l-1}^-1 mod q_i (R = 2^64)
 };
 
 // Barrett reduction of a sum of at most 4 products of residues below q < 2^60: the high word is below q, so no fold.
@@ -724,15 +725,20 @@ struct MdrEpi {
     }
 
     // L: this group's tile; the tiles of polys 0 and 1 are adjacent (kLdsWords apart)
+    // out_p = (x_p P^-1 + d_p - T_p) q_{l-1}^-1 as one 128-bit sum per poly, A_p = x_p + P d_p + P (q - T_p) (P a0 and
+    // P a1 formed first, so that d_p's products enter the sum already times P), then REDC(A_p) R P^-1 q_{l-1}^-1: one
+    // Montgomery reduction and one Shoup product per word instead of four Barrett reductions, two products by
+    // constants and the modular adds between them.  A_p is at most kD + 3 <= 7 products, one factor below 2q and the
+    // rest below q < 2^60: A_p < 7 q^2 < q R (REDC's input bound), and the accumulator's cross-product sum (below
+    // 2^61.6 a term) stays below 2^64.
     __device__ __forceinline__ void end(First cur, const uint64_t* L, int blk, int rl) const {
         const uint64_t* L0 = L - g * kLdsWords;
         const uint64_t* L1 = L0 + kLdsWords;
         const size_t po = (size_t)(f.l - 1) * kN;
         uint64_t* out0 = f.out + 2 * c * po + (size_t)i * kN;
         uint64_t* out1 = out0 + po;
-        const Barrett br = barrett_of(P);
-        const uint64_t q = br.q;
-        const TwPair pinv = f.pinv[i], qlinv = f.qlinv[i];
+        const uint64_t q = P.q, ninv = P.mont_ninv;
+        const TwPair pm = f.pmod[i], cf = f.cfin[i];
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
             const int k = 8 * g + kk;
@@ -744,26 +750,22 @@ struct MdrEpi {
                 s0.add(cur.xv[d], cur.e0[d]);
                 s1.add(cur.xv[d], cur.e1[d]);
             }
-            uint64_t v0 = shoup(reduce_sum(s0, br), pinv.w, pinv.wp, q);
-            uint64_t v1 = shoup(reduce_sum(s1, br), pinv.w, pinv.wp, q);
             if (kTa) {
-                Acc t0, t1;
-                t0.add(cur.u0, cur.u2);  // a0 b0
-                t1.add(cur.u0, cur.u3);  // a0 b1
-                t1.add(cur.u1, cur.u2);  // a1 b0
-                v0 = add_mod(v0, reduce_sum(t0, br), q);
-                v1 = add_mod(v1, reduce_sum(t1, br), q);
+                const uint64_t pa0 = shoup(cur.u0, pm.w, pm.wp, q), pa1 = shoup(cur.u1, pm.w, pm.wp, q);
+                s0.add(pa0, cur.u2);                     // P a0 b0
+                s1.add(pa0, cur.u3);                     // P a0 b1
+                s1.add(pa1, cur.u2);                     // P a1 b0
+                s0.add(q - L0[rl + 17 * k], pm.w);       // P (q - T0)
+                s1.add(q - L1[rl + 17 * k], pm.w);
             } else {
-                v0 = add_mod(v0, cur.u0, q);
-                v1 = add_mod(v1, cur.u1, q);
+                s0.add(cur.u0 + q - L0[rl + 17 * k], pm.w);  // P (add0 + q - T0)
+                s1.add(cur.u1 + q - L1[rl + 17 * k], pm.w);
             }
-            v0 = sub_mod(v0, L0[rl + 17 * k], q);
-            v1 = sub_mod(v1, L1[rl + 17 * k], q);
+            const uint64_t v0 = shoup(redc(s0.get(), q, ninv), cf.w, cf.wp, q);
+            const uint64_t v1 = shoup(redc(s1.get(), q, ninv), cf.w, cf.wp, q);
             const uint32_t bo = (256 * blk + rl + 16 * k) * 8;
-            __builtin_nontemporal_store(shoup(v0, qlinv.w, qlinv.wp, q),
-                                        reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out0) + bo));
-            __builtin_nontemporal_store(shoup(v1, qlinv.w, qlinv.wp, q),
-                                        reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out1) + bo));
+            __builtin_nontemporal_store(v0, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out0) + bo));
+            __builtin_nontemporal_store(v1, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out1) + bo));
             if (kk < 7) cur = nxt;
         }
     }
@@ -1223,11 +1225,13 @@ hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x
 
 // Forward NTT of a relinearization's ModDown term T [2B][l-1][N] (coefficients, limb i over prime i) whose pass B
 // ends in the combine (k_ntt_fwd_b_mdr): out [2B][l-1][N] = (x P^-1 + add - NTT(T)) q_{l-1}^-1 with x the evk inner
-// product of ext [B][D][E][N] and evk, add from ta/tb (the product's inputs) or add.  T is left holding
-// the first pass's intermediate.  Digit counts 1..4 (others: hipErrorInvalidValue, the caller runs the two kernels).
+// product of ext [B][D][E][N] and evk, add from ta/tb (the product's inputs) or add.  pmod[i] = P mod q_i and
+// cfin[i] = R P^-1 q_{l-1}^-1 mod q_i (R = 2^64), with Shoup companions, for limbs i < l-1 (primes below 2^60).  T is
+// left holding the first pass's intermediate.  Digit counts 1..4 (others: hipErrorInvalidValue, the caller runs the
+// two kernels).
 hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint32_t l, const uint64_t* ext,
                               const uint64_t* evk, const uint64_t* ta, const uint64_t* tb, const uint64_t* add,
-                              uint64_t add_pstride, uint64_t* out, const TwPair* pinv, const TwPair* qlinv,
+                              uint64_t add_pstride, uint64_t* out, const TwPair* pmod, const TwPair* cfin,
                               hipStream_t st) {
     const uint32_t D = (l + ctx.alpha - 1) / ctx.alpha, E = l + ctx.K;
     if (l < 2 || l > kMaxPmap || B == 0 || D < 1 || D > 4 || (ta && (!tb || add)) || (!ta && !add))
@@ -1250,8 +1254,9 @@ hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint3
     f.E = E;
     f.T = ctx.L + ctx.K;
     for (uint32_t i = 0; i + 1 < l; i++) {
-        f.pinv[i] = pinv[i];
-        f.qlinv[i] = qlinv[i];
+        if (ctx.moduli[i] >= (1ull << 60)) return hipErrorInvalidValue;  // the combine's sum bound
+        f.pmod[i] = pmod[i];
+        f.cfin[i] = cfin[i];
     }
     const uint32_t n_jobs = 2 * B * (l - 1);
     // algorithmic bytes: T read and written by pass A, read by pass B; per ciphertext and limb D ext limbs, the

@@ -58,7 +58,7 @@ hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x
                               uint64_t lift_q = 0);
 hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint32_t l, const uint64_t* ext,
                               const uint64_t* evk, const uint64_t* ta, const uint64_t* tb, const uint64_t* add,
-                              uint64_t add_pstride, uint64_t* out, const TwPair* pinv, const TwPair* qlinv,
+                              uint64_t add_pstride, uint64_t* out, const TwPair* pmod, const TwPair* cfin,
                               hipStream_t st);
 hipError_t launch_sub_scale(const Context& ctx, const uint64_t* x, uint64_t x_pstride, const uint64_t* y,
                             uint64_t y_pstride, const uint64_t* add, uint64_t add_pstride, uint32_t add_div,
@@ -346,6 +346,16 @@ static const std::vector<TwPair>& pmodr_tab(Context& ctx) {
     return ctx.tab_pmodr;
 }
 
+static const std::vector<TwPair>& pmod_tab(Context& ctx) {
+    if (ctx.tab_pmod.empty()) {
+        for (uint32_t i = 0; i < ctx.L; i++) {
+            const uint64_t q = ctx.moduli[i], v = p_mod(ctx, q);
+            ctx.tab_pmod.push_back(TwPair{v, shoup_companion(v, q)});
+        }
+    }
+    return ctx.tab_pmod;
+}
+
 static const std::vector<TwPair>& qinv_row(Context& ctx, uint32_t j) {
     auto it = ctx.tab_qinv.find(j);
     if (it != ctx.tab_qinv.end()) return it->second;
@@ -527,8 +537,15 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
     // product's inputs, or read), so T is never stored in evaluation form
     const uint32_t D = num_digits(ctx, l);
     if (ext && ctx.ntt_mode == NttMode::TwoPass && D <= 4) {
+        // the combine reduces one 128-bit sum by REDC and scales it by R P^-1 q_{l-1}^-1 (R = 2^64)
+        std::vector<TwPair> cfin(l - 1);
+        for (uint32_t i = 0; i + 1 < l; i++) {
+            const uint64_t q = ctx.moduli[i];
+            const uint64_t v = mulmod_h(mulmod_h(pinv[i].w, qlinv[i].w, q), ctx.primes[i].r_mod, q);
+            cfin[i] = TwPair{v, shoup_companion(v, q)};
+        }
         HIPX(launch_ntt_fwd_mdr(ctx, T, n_polys / 2, l, ext, evk, ta, tb, ta ? nullptr : add, (uint64_t)l * W, out,
-                                pinv.data(), qlinv.data(), st));
+                                pmod_tab(ctx).data(), cfin.data(), st));
         return;
     }
     HIPX(launch_ntt(ctx, T, regular_jobs(n_polys, pm), n_polys * (l - 1), false, ctx.ntt_mode, st));

@@ -16,15 +16,6 @@ namespace fhe {
 
 namespace {
 
-// Montgomery's REDC with R = 2^64: x < q R -> x R^-1 mod q in [0, q).  m = x_lo (-q^-1) mod 2^64 makes x + m q a
-// multiple of R; its low word sums to R exactly when x_lo != 0, so (x + m q) / R = x_hi + hi(m q) + [x_lo != 0],
-// below 2q.
-__device__ __forceinline__ uint64_t redc(const U128& x, uint64_t q, uint64_t ninv) {
-    const uint64_t m = x.lo * ninv;
-    const uint64_t t = x.hi + mulhi64(m, q) + (x.lo != 0 ? 1u : 0u);
-    return csub_s(t, q);
-}
-
 // ------------------------------------------------------------------ tensor product
 // a, b: [B][2][l][N]; d01: [B][2][l][N] (d0, d1); d2: [B][l][N]; d2e (optional): second copy of d2
 // scattered into the ModUp extension buffer: limb t of ciphertext c goes to d2e + c*d2e_bstride +
