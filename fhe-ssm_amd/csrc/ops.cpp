@@ -806,10 +806,10 @@ void rotate(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, uint32_t g
             hipStream_t st) {
     check_level(ctx, l);
     if ((g & 1) == 0 || g >= 2 * kN) throw std::invalid_argument("automorphism index must be odd and < 2N");
-    uint64_t* ks = (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)B * 2 * l * W * 8);
-    // c1 of every ciphertext read in place; c0 enters as the ModDown addend of output poly 0 only
-    keyswitch(ctx, ct + (size_t)l * W, B, l, evk, ct, ks, st, 2, (uint64_t)2 * l * W);
-    HIPX(launch_automorph(ks, out, 2 * B, l, g, st));
+    // a key-switch list with one key and one index: the combine applies the automorphism as it stores
+    const std::vector<uint32_t> gv(B, g);
+    const std::vector<const uint64_t*> kv(B, evk);
+    automorph_ks_list(ctx, ct, B, l, gv.data(), kv.data(), out, st);
 }
 
 uint32_t rotation_index(int64_t k) {
