@@ -147,6 +147,14 @@ void context_init(Context& c, const std::vector<uint64_t>& q, const std::vector<
         }
         c.primes[i] = make_prime_info(m, it[1].w);
     }
+    for (uint32_t i = 0; i < c.L; i++) {
+        PrimeInfo& pi = c.primes[i];
+        uint64_t pm = 1;
+        for (uint32_t k = 0; k < c.K; k++) pm = mulmod_h(pm, c.moduli[c.L + k] % pi.q, pi.q);
+        pi.pmod = pm;
+        pi.rpinv = mulmod_h(pi.r_mod, invmod_h(pm, pi.q), pi.q);
+        pi.rpinv_p = shoup_companion(pi.rpinv, pi.q);
+    }
     if (hipSetDevice(device) != hipSuccess) throw std::runtime_error("hipSetDevice failed");
     // the allocation-free entry point's scratch on this device: its address resolved once, with the device current
     if (scratch_init(device) != hipSuccess) throw std::runtime_error("device scratch address lookup failed");

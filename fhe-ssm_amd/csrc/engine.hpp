@@ -29,6 +29,9 @@ struct PrimeInfo {
     uint32_t red_shift, red_mul;
     uint64_t mont_ninv;  // -q^-1 mod 2^64 (Montgomery reduction of a 128-bit sum, R = 2^64)
     uint64_t r_mod, r_mod_p;  // R = 2^64 mod q and its Shoup companion (takes an R^-1-scaled value back to plain)
+    // Q primes: P mod q (P the product of the special primes), and R P^-1 mod q with its Shoup companion (a ModDown
+    // combine that reduces one 128-bit sum by REDC scales it by these); 0 for the special primes
+    uint64_t pmod, rpinv, rpinv_p;
 };
 
 // One limb to transform: offset (in units of N words) from the base pointer, and its prime index.

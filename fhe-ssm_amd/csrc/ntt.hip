@@ -666,12 +666,6 @@ struct MdrFuse {
     TwPair cfin[kMaxPmap];  // R P^-1 q_{l-1}^-1 mod q_i (R = 2^64)
 };
 
-// Barrett reduction of a sum of at most 4 products of residues below q < 2^60: the high word is below q, so no fold.
-__device__ __forceinline__ uint64_t reduce_sum(Acc& s, const Barrett& br) {
-    const U128 v = s.get();
-    return reduce128(v.hi, v.lo, br);
-}
-
 // a word at a byte offset from a wave-uniform base (the global_load form with a scalar base and a 32-bit offset)
 __device__ __forceinline__ uint64_t ld_at(const uint64_t* base, uint32_t byte_off) {
     return *reinterpret_cast<const uint64_t*>(reinterpret_cast<const char*>(base) + byte_off);
@@ -813,7 +807,6 @@ struct KslFuse {
     // index s is stored at the index whose source s is (see KslEpi::end)
     uint32_t auto_on;
     uint32_t ginv[kMaxList];
-    TwPair pinv[kMaxPmap];
 };
 
 template <int kD>
@@ -852,23 +845,26 @@ struct KslEpi {
         const size_t pw = (size_t)f.l * kN;
         uint64_t* out0 = f.out + 2 * c * pw + (size_t)i * kN;
         uint64_t* out1 = out0 + pw;
-        const Barrett br = barrett_of(P);
-        const uint64_t q = br.q;
-        const TwPair pinv = f.pinv[i];
+        const uint64_t q = P.q, ninv = P.mont_ninv, pm = P.pmod;
+        const TwPair rp{P.rpinv, P.rpinv_p};
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
             const int k = 8 * g + kk;
             First nxt;
             if (kk < 7) load(nxt, blk, rl, k + 1);
+            // x_p P^-1 - conv_p (+ c0 on poly 0) as one 128-bit sum per poly, A_p = x_p + P (q - conv_p [+ c0]),
+            // finished by REDC(A_p) R P^-1: at most kD + 1 <= 5 products, one factor below 2q, the others below
+            // q < 2^60, so A_p < 6 q^2 < q R and the accumulator's cross-product sum stays below 2^64
             Acc s0, s1;
 #pragma unroll
             for (int d = 0; d < kD; d++) {
                 s0.add(cur.xv[d], cur.e0[d]);
                 s1.add(cur.xv[d], cur.e1[d]);
             }
-            uint64_t v0 = sub_mod(shoup(reduce_sum(s0, br), pinv.w, pinv.wp, q), L0[rl + 17 * k], q);
-            const uint64_t v1 = sub_mod(shoup(reduce_sum(s1, br), pinv.w, pinv.wp, q), L1[rl + 17 * k], q);
-            if (f.add) v0 = add_mod(v0, cur.u0, q);
+            s0.add((f.add ? cur.u0 : 0) + q - L0[rl + 17 * k], pm);
+            s1.add(q - L1[rl + 17 * k], pm);
+            const uint64_t v0 = shoup(redc(s0.get(), q, ninv), rp.w, rp.wp, q);
+            const uint64_t v1 = shoup(redc(s1.get(), q, ninv), rp.w, rp.wp, q);
             const uint32_t w = 256 * blk + rl + 16 * k;
             if (f.auto_on) {
                 // the automorphism: out[k'] = v[src(k')] with src(k') = brev((g (2 brev(k') + 1) mod 2N - 1) / 2), so
@@ -1104,13 +1100,16 @@ hipError_t launch_ntt_inv_ksl(const Context& ctx, uint64_t* acc, const JobSpec& 
 // pass B ends in k_ks_sub_list's combine: out [n][2][l][N] = x P^-1 - NTT(y) (+ the addend's poly 0), x the evk inner
 // product of item c's extension and key.  gidx (optional): item c's output mapped by X -> X^gidx[c] (odd, < 2N) as it
 // is stored -- a rotation's automorphism, no separate permutation pass.  y is left holding the first pass's
-// intermediate.  Digit counts 1..4 (others: hipErrorInvalidValue, the caller runs the NTT and k_ks_sub_list).
+// intermediate.  Digit counts 1..4 and Q primes below 2^60 (others: hipErrorInvalidValue, the caller runs the NTT and
+// k_ks_sub_list).
 hipError_t launch_ntt_fwd_ksl(const Context& ctx, uint64_t* y, const uint64_t* const* ext, const uint64_t* const* evk,
                               const uint64_t* add, uint64_t add_stride, uint32_t add_group, uint64_t* out, uint32_t n,
-                              uint32_t l, const TwPair* pinv, hipStream_t st, const uint32_t* gidx) {
+                              uint32_t l, hipStream_t st, const uint32_t* gidx) {
     const uint32_t D = (l + ctx.alpha - 1) / ctx.alpha, E = l + ctx.K;
     if (l == 0 || l > kMaxPmap || n == 0 || n > (uint32_t)kMaxList || D < 1 || D > 4 || add_group == 0)
         return hipErrorInvalidValue;
+    for (uint32_t i = 0; i < l; i++)
+        if (ctx.moduli[i] >= (1ull << 60)) return hipErrorInvalidValue;  // the combine's sum bound
     JobSpec js{};
     js.n_polys = 2 * n;
     js.period = l;
@@ -1131,7 +1130,6 @@ hipError_t launch_ntt_fwd_ksl(const Context& ctx, uint64_t* y, const uint64_t* c
     f.E = E;
     f.T = ctx.L + ctx.K;
     f.add_group = add_group;
-    for (uint32_t i = 0; i < l; i++) f.pinv[i] = pinv[i];
     if (gidx) {
         f.auto_on = 1;
         for (uint32_t c = 0; c < n; c++) {

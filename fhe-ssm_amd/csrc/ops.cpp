@@ -45,7 +45,7 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
                                  const uint64_t* ta = nullptr, const uint64_t* tb = nullptr);
 hipError_t launch_ntt_fwd_ksl(const Context& ctx, uint64_t* y, const uint64_t* const* ext, const uint64_t* const* evk,
                               const uint64_t* add, uint64_t add_stride, uint32_t add_group, uint64_t* out, uint32_t n,
-                              uint32_t l, const TwPair* pinv, hipStream_t st, const uint32_t* gidx = nullptr);
+                              uint32_t l, hipStream_t st, const uint32_t* gidx = nullptr);
 hipError_t launch_ntt_inv_ksl(const Context& ctx, uint64_t* acc, const JobSpec& js, uint32_t n_jobs,
                               const uint64_t* const* ext, const uint64_t* const* evk, uint32_t n, uint32_t D,
                               uint32_t E, hipStream_t st);
@@ -609,7 +609,7 @@ void ks_moddown_list(Context& ctx, const uint64_t* const* ext, const uint64_t* c
     uint64_t* ks = gidx && (!fused || add_overlap) ? (uint64_t*)ws_get(ctx, WS_RELIN, (size_t)n * 2 * l * W * 8) : out;
     if (fused) {
         // the forward NTT of conv ends in the combine (conv never stored in evaluation form)
-        HIPX(launch_ntt_fwd_ksl(ctx, conv, ext, evk, add, add_stride, add_group, ks, n, l, pinv.data(), st,
+        HIPX(launch_ntt_fwd_ksl(ctx, conv, ext, evk, add, add_stride, add_group, ks, n, l, st,
                                 ks == out ? gidx : nullptr));
     } else {
         HIPX(launch_ntt(ctx, conv, regular_jobs(2 * n, out_idx), 2 * n * l, false, ctx.ntt_mode, st));
