@@ -154,13 +154,15 @@ struct Acc30 {
     }
 };
 
-// Montgomery's REDC with R = 2^64: x < q R -> x R^-1 mod q in [0, q).  m = x_lo (-q^-1) mod 2^64 makes x + m q a
-// multiple of R; its low word sums to R exactly when x_lo != 0, so (x + m q) / R = x_hi + hi(m q) + [x_lo != 0],
-// below 2q.
-__device__ __forceinline__ uint64_t redc(const U128& x, uint64_t q, uint64_t ninv) {
+// Montgomery's REDC with R = 2^64: x < q R -> x R^-1 mod q in [0, q) (redc_lazy: in [0, 2q)).  m = x_lo (-q^-1)
+// mod 2^64 makes x + m q a multiple of R; its low word sums to R exactly when x_lo != 0, so (x + m q) / R = x_hi +
+// hi(m q) + [x_lo != 0], below 2q.
+__device__ __forceinline__ uint64_t redc_lazy(const U128& x, uint64_t q, uint64_t ninv) {
     const uint64_t m = x.lo * ninv;
-    const uint64_t t = x.hi + mulhi64(m, q) + (x.lo != 0 ? 1u : 0u);
-    return csub_s(t, q);
+    return x.hi + mulhi64(m, q) + (x.lo != 0 ? 1u : 0u);
+}
+__device__ __forceinline__ uint64_t redc(const U128& x, uint64_t q, uint64_t ninv) {
+    return csub_s(redc_lazy(x, q, ninv), q);
 }
 
 // Acc30 with three multiply-adds a term (Karatsuba): s0 += a0 b0, s2 += a1 b1 and sm += (a0 + a1)(b0 + b1) mod 2^64;

@@ -3,9 +3,10 @@
 // rescale combines, the centered lift of rescale, additions and the evaluation-form automorphism.
 //
 // All of these are HBM-streaming elementwise kernels: one thread per coefficient index k, limbs
-// walked in registers, residues canonical in [0, q) on every store.  Products that are not by a
-// per-limb constant accumulate in 128 bits and reduce once (Barrett, mu = floor(2^128 / q)); products
-// by a per-limb constant use Shoup with a precomputed companion.
+// walked in registers, residues canonical in [0, q) on every store (but the BConv's, which only forward NTTs read:
+// see there).  Products that are not by a per-limb constant accumulate in 128 bits and reduce once (Barrett, mu =
+// floor(2^128 / q), or Montgomery's REDC against R-scaled constants); products by a per-limb constant use Shoup with a
+// precomputed companion.
 #include <algorithm>
 
 #include "engine.hpp"
@@ -104,6 +105,9 @@ __global__ __launch_bounds__(256) void k_tensor_sum(const uint64_t* const* __res
 // in  : batch c -> in + c*in_bstride, source limb i at off(in_desc[i])*N, prime prime(in_desc[i])
 // out : batch c -> out + c*out_bstride, target limb j at off(out_desc[j])*N, prime prime(out_desc[j])
 // tab : [n_in] TwPair (qhinv, companion) followed by [n_in][n_out] uint64 qhmod
+// Every BConv output is the input of a forward NTT, which takes words below 8q and stores canonical residues: the
+// Montgomery-reduced instances leave their outputs in [0, 2q) ([0, 3q) with the rescale's lift), skipping the final
+// conditional subtraction.
 // A limb descriptor is one dword, offset | prime << 16: the output loop indexes it with a wave-uniform j, which
 // a scalar load serves (byte or half-word arrays would be read with vector loads, one round trip per output).
 constexpr int kMaxBconvIn = 16;
@@ -231,8 +235,9 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         correct(acc, j, br);
         uint64_t v;
         if (mont) {
-            v = redc(acc, pj.q, pj.mont_ninv);
-            if constexpr (kMdr) v = add_mod(v, lift_centered(z, ql, br), pj.q);
+            // left in [0, 2q) ([0, 3q) with the lift): the consumer is a forward NTT (inputs below 8q)
+            v = redc_lazy(acc, pj.q, pj.mont_ninv);
+            if constexpr (kMdr) v += lift_centered(z, ql, br);
         } else {
             if constexpr (kMdr) {
                 const uint64_t r = lift_centered(z, ql, br);
