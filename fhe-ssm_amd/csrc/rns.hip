@@ -135,6 +135,10 @@ struct MdrBconvArgs {
     uint64_t xlast_pstride;
     const uint64_t* addc;   // [n_polys][N] coefficient form of the addend's limb l-1, or null
     TwPair pinv_last;       // P^-1 mod q_{l-1}
+    // fast_lift (set when q_{l-1} <= 2 q_j for every output j): the lift of z into q_j is z + [z > q_{l-1} / 2] dl[j]
+    // with dl[j] = -q_{l-1} mod q_j, below 3 q_j -- no reduction (the forward NTT that reads T takes words below 8q)
+    uint32_t fast_lift;
+    uint64_t dl[kMaxBconvOut];
 };
 
 // NIN = number of input limbs (a template parameter: the term loops unroll without run-time guards).  The table's
@@ -216,6 +220,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
     };
     uint32_t n_main = ba.n_out;
     uint64_t z = 0, ql = 0;
+    bool zneg = false;  // z stands for z - q_{l-1}
     if constexpr (kMdr) {
         n_main = ba.n_out - 1;
         U128 acc, unused;
@@ -227,6 +232,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         ql = bl.q;
         z = shoup(sub_mod(mb.xlast[c * mb.xlast_pstride + k], conv, ql), mb.pinv_last.w, mb.pinv_last.wp, ql);
         if (mb.addc) z = add_mod(z, mb.addc[(size_t)c * kN + k], ql);
+        zneg = z > (ql >> 1);
     }
     auto finish = [&](U128 acc, uint32_t j) {
         const uint32_t dj = ba.out_desc[j];
@@ -237,7 +243,7 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         if (mont) {
             // left in [0, 2q) ([0, 3q) with the lift): the consumer is a forward NTT (inputs below 8q)
             v = redc_lazy(acc, pj.q, pj.mont_ninv);
-            if constexpr (kMdr) v += lift_centered(z, ql, br);
+            if constexpr (kMdr) v += mb.fast_lift ? z + (zneg ? mb.dl[j] : 0) : lift_centered(z, ql, br);
         } else {
             if constexpr (kMdr) {
                 const uint64_t r = lift_centered(z, ql, br);
@@ -1077,7 +1083,18 @@ hipError_t launch_bconv_mdr(const Context& ctx, const BConvPlan& plan, const uin
     std::vector<uint32_t> out_off(l - 1);
     for (uint32_t j = 0; j + 1 < l; j++) out_off[j] = j;
     const BConvArgs ba = bconv_args(plan, in_bstride, in_off, (uint64_t)(l - 1) * kN, out_off.data(), l - 1);
-    const MdrBconvArgs mb{xlast, xlast_pstride, addc, pinv_last};
+    MdrBconvArgs mb{};
+    mb.xlast = xlast;
+    mb.xlast_pstride = xlast_pstride;
+    mb.addc = addc;
+    mb.pinv_last = pinv_last;
+    const uint64_t ql = ctx.moduli[plan.out_idx[l - 1]];
+    mb.fast_lift = 1;
+    for (uint32_t j = 0; j + 1 < l; j++) {
+        const uint64_t qj = ctx.moduli[plan.out_idx[j]];
+        if (ql > 2 * qj) mb.fast_lift = 0;
+        mb.dl[j] = (qj - ql % qj) % qj;
+    }
     // P limbs + limb l-1 (+ the addend's) read, l-1 limbs written
     const double bytes = (double)n_polys * (plan.n_in + 1 + (addc ? 1 : 0) + (l - 1)) * kN * 8;
     const int pi = prof_begin(ctx, "bconv_mdr", bytes, st);
