@@ -212,8 +212,16 @@ __device__ __forceinline__ void fwd_a_tile(uint64_t* __restrict__ a, const TwPai
     if (kLift) {
 #pragma unroll
         for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&lift[col + 256 * (rg + 16 * k)]);
+        if (lq <= 2 * q) {
+            // v > lq/2 stands for v - lq = v + dl (mod q), dl = -lq mod q: the sum is below 3q, a valid input (this
+            // pass takes words below 8q), so no reduction
+            const uint64_t lm = lq >= q ? lq - q : lq, dl = lm ? q - lm : 0;
 #pragma unroll
-        for (int k = 0; k < 16; k++) x[k] = lift_centered(x[k], lq, br);
+            for (int k = 0; k < 16; k++) x[k] += x[k] > (lq >> 1) ? dl : 0;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 16; k++) x[k] = lift_centered(x[k], lq, br);
+        }
     } else {
 #pragma unroll
         for (int k = 0; k < 16; k++) x[k] = __builtin_nontemporal_load(&a[col + 256 * (rg + 16 * k)]);
