@@ -315,14 +315,25 @@ def bench_pcmm(ckks, torch, steps_n, warmup, seed):
 
 
 # ----------------------------------------------------------------------------------------- config 4
-# Config-4 bootstrapping parameters.  The input's scale follows the reference's parameter rule FirstModSize =
-# min(60, ScalingModSize + 5) (hpc_gpu_port/gpu_real_model.cu:1153-1154): q0 of 60 bits over a 2^55 message, so
-# EvalMod's signal sin(2 pi m / q0) stands 2^5 below q0 (at 2^50 it stood 2^10 below, and EvalMod's absolute error
-# cost 5 bits of the result).  K = 32: the raised message's integer part I is a sum of 193 uniforms on [-1/2, 1/2]
-# per coefficient (h = 192 secret terms and c0), and a Chernoff bound on that sum puts P(some |I| > K - 1/2) below
-# 1.9e-9 per bootstrap of 2^16 coefficients; three double-angle steps keep the degree-59 interpolant of
+# Config-4 bootstrapping parameters, as BASELINE states them: EvalMod = Chebyshev degree 59 + 2 double-angle steps.
+# The input's scale follows the reference's parameter rule FirstModSize = min(60, ScalingModSize + 5)
+# (hpc_gpu_port/gpu_real_model.cu:1153-1154): q0 of 60 bits over a 2^55 message, so EvalMod's signal
+# sin(2 pi m / q0) stands 2^5 below q0.  The input's secret is the dense h = 192 ternary secret; before ModRaise the
+# level-1 ciphertext is switched to a sparse h' = 32 secret and the raised one back to the dense secret at the top
+# level (sparse-secret encapsulation, Bossuat-Troncoso-Pastoriza-Hubaux, ePrint 2022/024), so the raised message's
+# integer part I is the rounded sum of 33 uniforms on [-1/2, 1/2] per coefficient (c0 and 32 secret terms): the
+# Chernoff bound puts P(some |I| > K - 1/2) at 1.2e-15 per bootstrap for K = 14 (tests/test_boot_params.py), and
+# with two double angles the degree-59 interpolant covers cos(2 pi (K t - 1/4) / 4) over |K t| <= 14.
+BOOT_SPARSE_H = 32
+BOOT_K, BOOT_DEG, BOOT_R, BOOT_TOP, BOOT_IN = 14.0, 59, 2, 2.0**55, 2.0**55
+# The labelled variant: the dense secret throughout (no encapsulation), so I is a sum of 193 uniforms and K = 32
+# (Chernoff bound 1.9e-9 per bootstrap); three double angles keep the degree-59 interpolant of
 # cos(2 pi (K t - 1/4) / 8) far below the noise.
-BOOT_K, BOOT_DEG, BOOT_R, BOOT_TOP, BOOT_IN = 32.0, 59, 3, 2.0**55, 2.0**55
+BOOT_DENSE = {"K": 32.0, "deg": 59, "r": 3, "top": 2.0**55, "in": 2.0**55}
+BOOT_FORMS = {
+    "sparse_r2": {"K": BOOT_K, "deg": BOOT_DEG, "r": BOOT_R, "top": BOOT_TOP, "in": BOOT_IN, "sparse_h": BOOT_SPARSE_H},
+    "dense_r3": dict(BOOT_DENSE, sparse_h=0),
+}
 
 
 def bootstrap_context(ckks):
@@ -332,30 +343,37 @@ def bootstrap_context(ckks):
     return ckks.Context(num_q=26, num_p=8, dnum=3, scale=2.0**50, moduli=big[:1] + qs + big[1:4] + big[4:])
 
 
-def bench_bootstrap(ckks, torch, steps_n, warmup, seed):
+def bench_bootstrap(ckks, torch, steps_n, warmup, seed, form="sparse_r2", stage_errors=True):
+    f = BOOT_FORMS[form]
     ctx = bootstrap_context(ckks)
     L, K, D = ctx.L, ctx.K, ctx.dnum
-    bt = ckks.Bootstrap(ctx, K=BOOT_K, cheb_degree=BOOT_DEG, double_angles=BOOT_R, top_scale=BOOT_TOP,
-                        in_scale=BOOT_IN)
+    bt = ckks.Bootstrap(ctx, K=f["K"], cheb_degree=f["deg"], double_angles=f["r"], top_scale=f["top"],
+                        in_scale=f["in"])
     sk = ctx.secret(seed_bytes("boot-secret", seed), 192)
     dev = torch.device("cuda:0")
     kb = D * 2 * (L + K) * N * 8
-    nk = len(bt.steps) + 2
+    nk = len(bt.steps) + 4
     keys = torch.empty((nk, kb // 8), dtype=torch.int64, device=dev)
     kp = [keys.data_ptr() + i * kb for i in range(nk)]
     ctx.keygen_relin(sk, seed_bytes("boot-ra", seed), seed_bytes("boot-re", seed), kp[0])
     ctx.keygen_automorphism(sk, 2 * N - 1, seed_bytes("boot-ca", seed), seed_bytes("boot-ce", seed), kp[1])
+    sk_sparse = None
+    if f["sparse_h"]:
+        sk_sparse = ctx.secret(seed_bytes("boot-sparse", seed), f["sparse_h"])
+        ctx.keygen_switch(sk, sk_sparse, seed_bytes("boot-ta", seed), seed_bytes("boot-te", seed), kp[2], q_limbs=1)
+        ctx.keygen_switch(sk_sparse, sk, seed_bytes("boot-fa", seed), seed_bytes("boot-fe", seed), kp[3])
+        bt.set_sparse_keys(kp[2], kp[3])
     rot = {}
     for i, s_ in enumerate(bt.steps):
         ctx.keygen_automorphism(sk, ckks.rotation_index(s_), seed_bytes(f"bk{i}a", seed), seed_bytes(f"bk{i}e", seed),
-                                kp[2 + i])
-        rot[s_] = kp[2 + i]
+                                kp[4 + i])
+        rot[s_] = kp[4 + i]
     rng = np.random.default_rng(seed)
     z = rng.uniform(-1.0, 1.0, N // 2)
     pt = torch.empty((1, N), dtype=torch.int64, device=dev)
     ct = torch.empty((2, 1, N), dtype=torch.int64, device=dev)
     out = torch.empty((2, bt.out_level, N), dtype=torch.int64, device=dev)
-    ctx.encode(z, 1, BOOT_IN, pt.data_ptr())
+    ctx.encode(z, 1, f["in"], pt.data_ptr())
     ctx.encrypt(sk, pt.data_ptr(), 1, seed_bytes("boot-enc", seed), 0, ct.data_ptr())
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
@@ -367,7 +385,7 @@ def bench_bootstrap(ckks, torch, steps_n, warmup, seed):
     wall, per = timed_steps(torch, stream, step, steps_n, warmup)
     got = ctx.decrypt(sk, out.data_ptr(), bt.out_level, bt.scale(bt.out_level), N // 2, complex_out=True)
     bits = float(-np.log2(np.max(np.abs(got - z))))
-    stages = bootstrap_stage_errors(ckks, ctx, bt, sk, ct, kp, rot, got, z)
+    stages = bootstrap_stage_errors(ckks, ctx, bt, f["K"], sk, ct, kp, rot, got, z) if stage_errors else None
     ctx.profile_reset()
     ctx.profile(True)
     step()
@@ -375,15 +393,23 @@ def bench_bootstrap(ckks, torch, steps_n, warmup, seed):
     ctx.profile(False)
     rep = ctx.profile_report()
     ctx.profile_reset()
-    return {"ms_per_bootstrap": round(wall * 1e3 / steps_n, 3), "precision_bits": round(bits, 2),
+    ms = wall * 1e3 / steps_n
+    if f["sparse_h"]:
+        em = (f"EvalMod Chebyshev {f['deg']} + {f['r']} double-angle (sparse-secret encapsulation h'={f['sparse_h']}, "
+              f"K={f['K']:g}, P(|I| > K) < 1.3e-15 per bootstrap)")
+    else:
+        em = (f"EvalMod Chebyshev {f['deg']} + {f['r']} double-angle (dense secret throughout, K={f['K']:g}, "
+              f"P(|I| > K) < 1.9e-9 per bootstrap)")
+    del sk_sparse
+    return {"ms_per_bootstrap": round(ms, 3), "precision_bits": round(bits, 2),
             "levels_in_out": [1, bt.out_level], "rotation_keys": len(bt.steps), "stage_errors": stages,
-            "kernels": kernel_table(rep), "roofline": roofline_from_profile(rep),
+            "form": form, "kernels": kernel_table(rep), "_rep": rep,
             "workload": "config4: full-slot bootstrap N=2^16, 32768 slots, level-1 input at scale 2^55 (q0 60 bits), "
-                        "CtS 3 levels, EvalMod Chebyshev 59 + 3 double-angle (K=32, P(|I| > K) < 1.9e-9 per "
-                        "bootstrap), StC 3 levels; chain q0 60 + 22x50 + 3x60 bits, P 8x60, dnum 3"}
+                        f"secret h=192, CtS 3 levels, {em}, StC 3 levels; chain q0 60 + 22x50 + 3x60 bits, P 8x60, "
+                        "dnum 3"}
 
 
-def bootstrap_stage_errors(ckks, ctx, bt, sk, ct, kp, rot, got, z):
+def bootstrap_stage_errors(ckks, ctx, bt, Kr, sk, ct, kp, rot, got, z):
     """Error budget of one bootstrap, stage by stage (the engine stops after a stage on request): ModRaise decrypts
     to m' = m + q0 I; after CoeffToSlot the slots hold t = (m'_k + i m'_{k+n}) / (q0 K), bit-reversed; EvalMod gives
     sin(2 pi K t) per real part; SlotToCoeff gives z.  Each figure is the max error over the slots in the units of
@@ -399,7 +425,7 @@ def bootstrap_stage_errors(ckks, ctx, bt, sk, ct, kp, rot, got, z):
     b = n.bit_length() - 1
     for i in range(n):
         rev[i] = int(format(i, f"0{b}b")[::-1], 2)
-    t = ((mp[:n] + 1j * mp[n:]) / (ctx.moduli[0] * BOOT_K))[rev]
+    t = ((mp[:n] + 1j * mp[n:]) / (ctx.moduli[0] * Kr))[rev]
     res = {}
     lvl = bt.run_stage(ct.data_ptr(), kp[0], kp[1], rot, 2, buf.data_ptr())
     dec = ctx.decrypt(sk, buf.data_ptr(), lvl, bt.scale(lvl), n, complex_out=True)
@@ -407,7 +433,7 @@ def bootstrap_stage_errors(ckks, ctx, bt, sk, ct, kp, rot, got, z):
                             "level": lvl}
     lvl = bt.run_stage(ct.data_ptr(), kp[0], kp[1], rot, 4, buf.data_ptr())
     errs, sig = [], []
-    for part, want in enumerate((np.sin(2 * np.pi * BOOT_K * t.real), np.sin(2 * np.pi * BOOT_K * t.imag))):
+    for part, want in enumerate((np.sin(2 * np.pi * Kr * t.real), np.sin(2 * np.pi * Kr * t.imag))):
         dec = ctx.decrypt(sk, buf.data_ptr() + part * 2 * lvl * N * 8, lvl, bt.scale(lvl), n, complex_out=True)
         errs.append(float(np.max(np.abs(dec - want))))
         sig.append(float(np.max(np.abs(want))))
@@ -688,6 +714,9 @@ def main():
                     help="decode workload: also time this many one-token requests through the serve protocol")
     ap.add_argument("--decode-driver", default="native", choices=["native", "python"],
                     help="decode workload: the C++ driver (default) or the same plan in Python")
+    ap.add_argument("--boot-form", default="sparse_r2", choices=sorted(BOOT_FORMS),
+                    help="bootstrap workload: config 4 as stated (sparse_r2: sparse-secret encapsulation, K = 14, "
+                         "2 double angles) or the dense-secret variant (dense_r3: K = 32, 3 double angles)")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ntt-line", action="store_true", help="skip the config-1 NTT figure in the hmult run")
@@ -717,8 +746,13 @@ def main():
                                                         "roofline")}
         if not args.no_boot_line:
             b = bench_bootstrap(ckks, torch, max(2, args.steps // 4), 1, args.seed)
+            b["roofline"] = roofline_from_profile(b["_rep"])
             extra["bootstrap_config4"] = {k: b[k] for k in ("ms_per_bootstrap", "precision_bits", "levels_in_out",
-                                                             "stage_errors", "roofline")}
+                                                             "stage_errors", "roofline", "workload")}
+            v = bench_bootstrap(ckks, torch, max(2, args.steps // 4), 1, args.seed, form="dense_r3",
+                                stage_errors=False)
+            extra["bootstrap_config4_variant_dense_r3"] = {k: v[k] for k in ("ms_per_bootstrap", "precision_bits",
+                                                                              "levels_in_out", "workload")}
         if not args.no_decode_line:
             # the earlier workloads' contexts, keys and buffers go before config 5 (and torch's cache returns their
             # tensors' memory, so the decode line's device figures are config 5's own)
@@ -752,10 +786,10 @@ def main():
             cpu, acc = cpu_baseline_decode(d, args.seed)
             res["check"].update(acc)
     elif args.workload == "bootstrap":
-        b = bench_bootstrap(ckks, torch, args.steps, args.warmup, args.seed)
+        b = bench_bootstrap(ckks, torch, args.steps, args.warmup, args.seed, form=args.boot_form)
         res = {"metric": "bootstrap ms (full-slot, N=2^16)", "value": b["ms_per_bootstrap"], "unit": "ms",
                "ms_per_step": b["ms_per_bootstrap"], "dtype": "u64", "config": {"workload": b["workload"]},
-               "kernels": b["kernels"], "roofline": b["roofline"],
+               "kernels": b["kernels"], "roofline": roofline_from_profile(b["_rep"]),
                "check": {"precision_bits": b["precision_bits"], "levels_in_out": b["levels_in_out"],
                          "stage_errors": b["stage_errors"]}}
         extra, cpu = {}, None

@@ -6,6 +6,9 @@ weight 192).  EvalMod is exact only while |I + m/q0| <= K, so a bootstrap fails 
 Chernoff bound P(S >= t) <= exp(-l t) E[e^(l U)]^193, E[e^(l U)] = sinh(l/2) / (l/2), holds for every l > 0 (the
 minimum over a grid is still a bound); times two signs and 2^16 coefficients it bounds the failure rate of one
 bootstrap.  bench.py's config-4 K must keep it below 1e-6; the K = 22 of the earlier parameters did not.
+
+With sparse-secret encapsulation (config 4 as stated) the raised ciphertext is the level-1 input switched to a sparse
+secret of Hamming weight h', so S is a sum of h' + 1 uniforms: K = 14 at h' = 32.
 """
 import math
 import os
@@ -26,8 +29,16 @@ def failure_bound(K: float, n_terms: int = 193, n_coeffs: int = 1 << 16) -> floa
 def test_config4_k_fails_less_than_once_per_million_bootstraps():
     sys.path.insert(0, REPO)
     import bench
-    assert failure_bound(bench.BOOT_K) < 2e-9
+    sparse = bench.BOOT_FORMS["sparse_r2"]
+    assert sparse["sparse_h"] == bench.BOOT_SPARSE_H == 32 and sparse["K"] == bench.BOOT_K
+    assert sparse["r"] == 2 and sparse["deg"] == 59           # Chebyshev 59 + 2 double angles
+    assert failure_bound(bench.BOOT_K, bench.BOOT_SPARSE_H + 1) < 2e-15
+    assert failure_bound(bench.BOOT_K - 2, bench.BOOT_SPARSE_H + 1) > 1e-8   # K = 12 would be marginal
+    dense = bench.BOOT_FORMS["dense_r3"]
+    assert dense["sparse_h"] == 0
+    assert failure_bound(dense["K"]) < 2e-9
     assert failure_bound(22.0) > 1e-2          # the earlier K: a failure every few dozen bootstraps by this bound
+    assert failure_bound(bench.BOOT_K) > 0.5   # K = 14 without the encapsulation: certain failure
 
 
 def test_bound_against_exact_small_case():
