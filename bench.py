@@ -15,9 +15,12 @@ Workloads (inputs seeded and resident in HBM before the t
          against the float64 model.
 The default run also reports the config-1, -3, -4 and -5 figures beside the config-2 metric.
 
-Roofline: the engine records HIP events on its launch stream around every kernel of one profiled
-step (ckks_profile_*); the dominant kernel by time is reported with achieved = algorithmic bytes per
-launch / mean launch time, against the MI355X HBM peak (8 TB/s).
+Roofline: `roofline` is the step-level figure of SURVEY 8(d): the unit's algorithmic bytes times the units
+one timed engine call processes (config 2: 175,112,192 B x 64 pairs), over the call's mean time by HIP events
+on its stream, against the MI355X HBM peak (8 TB/s) and against the stream rate measured on the box
+(profiles/hbm_stream.md); `traffic` is the step's counter-measured HBM bytes summed over all its dispatches.
+`kernel_io` is the dominant launch of one profiled step (the engine records HIP events on its launch stream
+around every kernel, ckks_profile_*): its own I/O bytes (intermediates included) over its mean launch time.
 cpu_baseline: this repository's C oracle (an OpenFHE-convention restatement, not OpenFHE, which needs
 the network to build) timed on the host over a bounded sample of the same workload.
 """
@@ -67,16 +70,32 @@ def timed_steps(torch, stream, step, steps, warmup):
     return wall, per
 
 
-# Counter-measured figures per launch of a workload's dominant kernel, from rocprofv3 --pmc passes over the same
-# bench command (one pass per counter group; the summaries and commands are in profiles/):
+# Achievable HBM bandwidth on the box, measured by the stream kernels of fhe-ssm_amd/microbench/copy_bw.hip (8 GiB
+# read-only nontemporal stream; 4 GiB nontemporal copy, read + write bytes; the output is in profiles/hbm_stream.md).
+# A rate whose bytes are at least 10% writes is divided by the copy figure, a read-dominated one by the read figure.
+STREAM_READ_GBS = 7167.4
+STREAM_COPY_GBS = 5498.6
+STREAM_SOURCE = "profiles/hbm_stream.md"
+# engine launches whose bytes are >= 90% reads (plaintext diagonals, keys and extensions streamed, few outputs)
+READ_DOMINATED = {"bsgs_mac", "bsgs_mac_periodic", "bsgs_dh_mac", "qp_rot_sum"}
+
+
+def achievable(write_share: float) -> float:
+    return STREAM_READ_GBS if write_share < 0.1 else STREAM_COPY_GBS
+
+
+# Counter-measured figures from rocprofv3 --pmc passes over the same bench command (one pass per counter group; the
+# summaries and commands are in profiles/):
 #   traffic: HBM bytes, read = 2 x FETCH_SIZE KiB, write = WRITE_SIZE KiB (the scaling a copy kernel of known size
-#            reads off the two counters);
+#            reads off the two counters); for ("workload", "step") summed over every dispatch of one step;
 #   valu:    wave64 VALU instructions issued (SQ_INSTS_VALU, all waves of the launch).
-# A "launch" is one engine call (both kernels of a two-pass NTT).  Measured, not computed: re-measure when the kernel
-# or the workload changes.
+# A kernel "launch" is one engine call (both kernels of a two-pass NTT).  Measured, not computed: re-measure when the
+# kernel or the workload changes.
 MEASURED = {
+    ("hmult", "step"): {"traffic": 34.659e9, "source": "profiles/hmult_config2_kernels.md"},
     ("hmult", "ntt_fwd_mdr"): {"traffic": 11.689e9, "valu_insts": 878.0e6, "source": "profiles/hmult_config2_kernels.md"},
     ("hmult", "ntt_fwd_2pass"): {"traffic": 9.700e9, "valu_insts": 786.2e6, "source": "profiles/hmult_config2_kernels.md"},
+    ("ntt", "step"): {"traffic": 12.940e9, "source": "profiles/ntt_config1_kernel_trace.md"},
     ("ntt", "ntt_fwd_2pass"): {"traffic": 6.470e9, "valu_insts": 493.9e6, "source": "profiles/ntt_config1_kernel_trace.md"},
     ("ntt", "ntt_inv_2pass"): {"traffic": 6.470e9, "valu_insts": 504.9e6, "source": "profiles/ntt_config1_kernel_trace.md"},
 }
@@ -88,14 +107,34 @@ VALU_PEAK_GINSTS = 1024 * 2.4 / 4
 VALU_MAD_GINSTS = 1024 * 2.4 / 4.94
 
 
-def roofline_from_profile(rep: dict, workload: str = ""):
+def step_roofline(workload: str, alg_bytes: float, step_ms: float, write_share: float, scope: str) -> dict:
+    """The step-level HBM roofline: SURVEY 8(d)'s algorithmic bytes for one timed step (the unit times the units one
+    engine call processes) over the step's HIP-event time, against the data-sheet peak and the measured stream rate;
+    traffic = the counter-measured HBM bytes of one step summed over all its dispatches."""
+    ach = alg_bytes / (step_ms * 1e-3) / 1e9
+    stream = achievable(write_share)
+    meas = MEASURED.get((workload, "step"), {})
+    out = {"bound": "hbm", "scope": scope, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": meas.get("traffic"),
+           "algorithmic_bytes_per_step": int(round(alg_bytes)), "step_ms": round(step_ms, 4),
+           "achievable": stream, "frac_of_achievable": round(ach / stream, 4), "achievable_source": STREAM_SOURCE}
+    if meas:
+        out["traffic_over_algorithmic"] = round(meas["traffic"] / alg_bytes, 3)
+        out["traffic_GBps"] = round(meas["traffic"] / (step_ms * 1e-3) / 1e9, 1)
+        out["traffic_source"] = meas["source"]
+    return out
+
+
+def kernel_io(rep: dict, workload: str = ""):
+    """The dominant engine launch of one profiled step by time: its own I/O bytes (every array it reads or writes,
+    intermediates included, each once) over its mean launch time (HIP events on the launch stream)."""
     name, (n, ms, by) = max(rep.items(), key=lambda kv: kv[1][1])
-    achieved = by / (ms * 1e-3) / 1e9
+    rate = by / (ms * 1e-3) / 1e9
+    stream = STREAM_READ_GBS if name in READ_DOMINATED else STREAM_COPY_GBS
     meas = MEASURED.get((workload, name), {})
-    out = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-           "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": meas.get("traffic"), "kernel": name,
-           "launches_in_profiled_step": n, "mean_launch_ms": round(ms / n, 4),
-           "algorithmic_bytes_per_launch": round(by / n)}
+    out = {"kernel": name, "achieved": round(rate, 1), "unit": "GB/s", "frac": round(rate / HBM_PEAK_GBS, 4),
+           "achievable": stream, "frac_of_achievable": round(rate / stream, 4), "traffic": meas.get("traffic"),
+           "launches_in_profiled_step": n, "mean_launch_ms": round(ms / n, 4), "io_bytes_per_launch": round(by / n)}
     if meas.get("valu_insts"):
         g = meas["valu_insts"] / (ms / n * 1e-3) / 1e9
         out["valu"] = {"achieved": round(g, 1), "peak": VALU_PEAK_GINSTS, "unit": "G wave64 VALU inst/s",
@@ -109,6 +148,11 @@ def roofline_from_profile(rep: dict, workload: str = ""):
 def kernel_table(rep: dict):
     return {k: {"launches": n, "total_ms": round(ms, 4), "GBps": round(by / (ms * 1e-3) / 1e9, 1)}
             for k, (n, ms, by) in sorted(rep.items(), key=lambda kv: -kv[1][1])}
+
+
+def profile_bytes(rep: dict) -> float:
+    """the engine's algorithmic (own-I/O) bytes summed over every launch of a profiled step"""
+    return float(sum(by for (_, _, by) in rep.values()))
 
 
 # ----------------------------------------------------------------------------------------- config 2
@@ -175,23 +219,36 @@ def bench_hmult(ckks, torch, steps, warmup, seed):
                    "step_ms_min": round(min(per), 4), "step_ms_max": round(max(per), 4)},
         "check": {"decrypted_relErrRms_max": rel_err, "ciphertexts_checked": 2},
         "kernels": kernel_table(rep),
-        "roofline": roofline_from_profile(rep, "hmult"),
-        "ks_stage": ks_stage(rep),
+        "roofline": step_roofline("hmult", N_PAIRS * HMULT_UNIT_BYTES, step_ms, 46 / 334,
+                                  "step: one ckks_eval_mult_rescale call over 64 pairs; SURVEY 8(d) config-2 unit "
+                                  "175,112,192 B per op (inputs 96 + evk 192 + output 46 limbs) x 64"),
+        "kernel_io": kernel_io(rep, "hmult"),
+        "ks_stage": ks_stage(rep, step_ms),
     }
+    res["roofline"]["evk_amortised"] = step_roofline(
+        "", N_PAIRS * HMULT_EVK_AMORTISED_BYTES, step_ms, 46 / 145,
+        "the same step with the evk counted once per 64 ops: 76,021,760 B per op")
     return res
 
 
-# SURVEY 8(d) key-switching unit per op: d2 24 limbs + evk 192 limbs + output 48 limbs
+# SURVEY 8(d) config-2 units per op: HMult+relin+rescale (inputs 96 + evk 192 + output 46 limbs), the same with the
+# evk amortised over the batch (96 + 3 + 46 limbs), and the key-switching unit (d2 24 + evk 192 + output 48 limbs)
+HMULT_UNIT_BYTES = 175_112_192
+HMULT_EVK_AMORTISED_BYTES = 76_021_760
 KS_UNIT_BYTES = 138_412_032
 
 
-def ks_stage(rep: dict):
-    """the key-switching part of the profiled HMult step (every kernel but the tensor product; the rescale is fused
-    into the ModDown) against the key-switching unit"""
-    ms = sum(v[1] for k, v in rep.items() if k != "tensor")
+def ks_stage(rep: dict, step_ms: float):
+    """the key-switching part of the timed HMult step (every kernel but the tensor product; the rescale is fused into
+    the ModDown) against the key-switching unit: its time is the timed step's scaled by the key-switching kernels'
+    share of the profiled step's kernel time (per-kernel events make a profiled step longer than a timed one)"""
+    ks_ms_prof = sum(v[1] for k, v in rep.items() if k != "tensor")
+    all_ms_prof = sum(v[1] for v in rep.values())
+    ms = step_ms * ks_ms_prof / all_ms_prof
     gbs = N_PAIRS * KS_UNIT_BYTES / (ms * 1e-3) / 1e9
-    return {"ms": round(ms, 4), "algorithmic_bytes": N_PAIRS * KS_UNIT_BYTES, "achieved": round(gbs, 1),
-            "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+    return {"ms": round(ms, 4), "share_of_step": round(ks_ms_prof / all_ms_prof, 4),
+            "algorithmic_bytes": N_PAIRS * KS_UNIT_BYTES, "achieved": round(gbs, 1), "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "frac_of_achievable": round(gbs / STREAM_COPY_GBS, 4),
             "kernels": sorted(k for k in rep if k != "tensor")}
 
 
@@ -305,11 +362,15 @@ def bench_pcmm(ckks, torch, steps_n, warmup, seed):
     rep = ctx.profile_report()
     ctx.profile_reset()
     ms = wall * 1e3 / steps_n
-    # algorithmic bytes (the SURVEY 8d config-3 unit with this BSGS's key count: 27 baby + 27 giant keys of
-    # 96 limbs, not the unit's 56): keys + 768 x 16 plaintext limbs + ct in/out 62 limbs
+    # algorithmic bytes: the SURVEY 8(d) config-3 unit with this BSGS's key count (27 baby + 27 giant keys of
+    # 96 limbs -- the identity baby and giant steps need none -- not the unit's 56): keys + 768 x 16 plaintext limbs
+    # + ct in/out 62 limbs
     alg = ((len(bst) + len(gst)) * 96 + d * l + 62) * LIMB_BYTES
-    return {"ms_per_pcmm": round(ms, 4), "relErrRms_vs_fp64": rel, "algorithmic_GBps": round(alg / (ms * 1e-3) / 1e9, 1),
-            "kernels": kernel_table(rep), "roofline": roofline_from_profile(rep),
+    return {"ms_per_pcmm": round(ms, 4), "relErrRms_vs_fp64": rel,
+            "kernels": kernel_table(rep), "kernel_io": kernel_io(rep, "pcmm"),
+            "roofline": step_roofline("pcmm", alg, ms, 30 / (alg / LIMB_BYTES),
+                                      f"step: one ckks_linear_transform_bsgs call; SURVEY 8(d) config-3 unit with "
+                                      f"{len(bst) + len(gst)} keys: keys + 768 x 16 diagonal limbs + ct in/out"),
             "workload": "config3: 768x768 fp64 weights N(0,1/768) x 1 ct at L=16, BSGS 28 baby x 28 giant, "
                         "period-768 replicated layout"}
 
@@ -403,7 +464,11 @@ def bench_bootstrap(ckks, torch, steps_n, warmup, seed, form="sparse_r2", stage_
     del sk_sparse
     return {"ms_per_bootstrap": round(ms, 3), "precision_bits": round(bits, 2),
             "levels_in_out": [1, bt.out_level], "rotation_keys": len(bt.steps), "stage_errors": stages,
-            "form": form, "kernels": kernel_table(rep), "_rep": rep,
+            "form": form, "kernels": kernel_table(rep), "kernel_io": kernel_io(rep, "bootstrap"),
+            "roofline": step_roofline("bootstrap" if form == "sparse_r2" else "", profile_bytes(rep), ms, 0.5,
+                                      "step: one ckks_eval_bootstrap call; SURVEY 8(d) config-4 unit: the sum of its "
+                                      "launches' algorithmic bytes (each launch's inputs, keys, diagonals and outputs "
+                                      "once)"),
             "workload": "config4: full-slot bootstrap N=2^16, 32768 slots, level-1 input at scale 2^55 (q0 60 bits), "
                         f"secret h=192, CtS 3 levels, {em}, StC 3 levels; chain q0 60 + 22x50 + 3x60 bits, P 8x60, "
                         "dnum 3"}
@@ -540,7 +605,11 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native
             "setup_s": {"keys": round(t_keys, 1), "first_steps_with_plaintext_encoding": round(t_warm, 1)},
             "device_memory_in_use_gb_after_warmup": round((total_b - free_b) / 1e9, 1), "memory": mem,
             "client_s": {"decrypt_and_vocab_head": round(t_client, 3)},
-            "kernels": kernel_table(rep), "roofline": roofline_from_profile(rep),
+            "kernels": kernel_table(rep), "kernel_io": kernel_io(rep, "decode"),
+            "roofline": step_roofline("decode", profile_bytes(rep), s_per_step * 1e3, 0.5,
+                                      "step: one decode step of the native driver; SURVEY 8(d) config-5 unit: the sum "
+                                      "of its launches' algorithmic bytes (each launch's inputs, keys, diagonals and "
+                                      "outputs once)"),
             "_check": {"xs": xs, "outs": outs, "logits": logits, "logits_step": warmup + steps_n - 1, "W": W,
                        "be": be, "sk": sk, "M": M, "n_steps": warmup + steps_n + 1},
             "workload": f"config5: RWKV-7-0.1B-shaped decode step, {n_layers} layers, d=768, 12 heads x 64, "
@@ -666,7 +735,10 @@ def bench_ntt(ckks, torch, steps, warmup, seed):
                    "limbs_per_direction": limbs, "algorithmic_bytes_per_direction": bytes_dir,
                    "ntt_mode": "two-pass", "seed": seed},
         "kernels": kernel_table(rep),
-        "roofline": roofline_from_profile(rep, "ntt"),
+        "roofline": step_roofline("ntt", 2 * bytes_dir, step_ms, 0.5,
+                                  "step: one forward + one inverse ckks_ntt call over the 3,072 limbs; SURVEY 8(d) "
+                                  "config-1 unit 3,246,391,296 B per direction x 2"),
+        "kernel_io": kernel_io(rep, "ntt"),
     }
 
 
@@ -739,16 +811,14 @@ def main():
         if not args.no_ntt_line:
             n = bench_ntt(ckks, torch, max(3, args.steps // 2), 1, args.seed)
             extra["ntt_config1"] = {"GBps": n["value"], "ms_per_step": n["ms_per_step"],
-                                    "roofline": n["roofline"]}
+                                    "roofline": n["roofline"], "kernel_io": n["kernel_io"]}
         if not args.no_pcmm_line:
             p = bench_pcmm(ckks, torch, max(3, args.steps // 2), 1, args.seed)
-            extra["pcmm_config3"] = {k: p[k] for k in ("ms_per_pcmm", "relErrRms_vs_fp64", "algorithmic_GBps",
-                                                        "roofline")}
+            extra["pcmm_config3"] = {k: p[k] for k in ("ms_per_pcmm", "relErrRms_vs_fp64", "roofline", "kernel_io")}
         if not args.no_boot_line:
             b = bench_bootstrap(ckks, torch, max(2, args.steps // 4), 1, args.seed)
-            b["roofline"] = roofline_from_profile(b["_rep"])
             extra["bootstrap_config4"] = {k: b[k] for k in ("ms_per_bootstrap", "precision_bits", "levels_in_out",
-                                                             "stage_errors", "roofline", "workload")}
+                                                             "stage_errors", "roofline", "kernel_io", "workload")}
             v = bench_bootstrap(ckks, torch, max(2, args.steps // 4), 1, args.seed, form="dense_r3",
                                 stage_errors=False)
             extra["bootstrap_config4_variant_dense_r3"] = {k: v[k] for k in ("ms_per_bootstrap", "precision_bits",
@@ -760,7 +830,7 @@ def main():
             torch.cuda.empty_cache()
             d = bench_decode(ckks, torch, 2, 1, args.seed, driver=args.decode_driver)  # mean of 2 timed steps
             line = {"s_per_step": d["s_per_step"], "metric": "s/step for 32-lane decode (config 5)",
-                    "roofline": d["roofline"]}
+                    "roofline": d["roofline"], "kernel_io": d["kernel_io"]}
             line.update({k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s",
                                            "device_memory_in_use_gb_after_warmup", "memory", "driver")})
             if not args.no_cpu_baseline:
@@ -775,7 +845,7 @@ def main():
         res = {"metric": "s/step for 32-lane decode (config 5)", "value": d["s_per_step"], "unit": "s/step",
                "ms_per_step": round(d["s_per_step"] * 1e3, 1), "dtype": "u64",
                "config": {"workload": d["workload"], "lanes": DECODE_LANES, "layers": args.layers},
-               "kernels": d["kernels"], "roofline": d["roofline"],
+               "kernels": d["kernels"], "roofline": d["roofline"], "kernel_io": d["kernel_io"],
                "check": {k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s",
                                            "device_memory_in_use_gb_after_warmup", "memory", "driver")}}
         if d["serve"]:
@@ -789,7 +859,7 @@ def main():
         b = bench_bootstrap(ckks, torch, args.steps, args.warmup, args.seed, form=args.boot_form)
         res = {"metric": "bootstrap ms (full-slot, N=2^16)", "value": b["ms_per_bootstrap"], "unit": "ms",
                "ms_per_step": b["ms_per_bootstrap"], "dtype": "u64", "config": {"workload": b["workload"]},
-               "kernels": b["kernels"], "roofline": roofline_from_profile(b["_rep"]),
+               "kernels": b["kernels"], "roofline": b["roofline"], "kernel_io": b["kernel_io"],
                "check": {"precision_bits": b["precision_bits"], "levels_in_out": b["levels_in_out"],
                          "stage_errors": b["stage_errors"]}}
         extra, cpu = {}, None
@@ -797,7 +867,7 @@ def main():
         p = bench_pcmm(ckks, torch, args.steps, args.warmup, args.seed)
         res = {"metric": "PCMM ms (768x768 BSGS, N=2^16, L=16)", "value": p["ms_per_pcmm"], "unit": "ms",
                "ms_per_step": p["ms_per_pcmm"], "dtype": "u64", "config": {"workload": p["workload"]},
-               "kernels": p["kernels"], "roofline": p["roofline"],
+               "kernels": p["kernels"], "roofline": p["roofline"], "kernel_io": p["kernel_io"],
                "check": {"relErrRms_vs_fp64": p["relErrRms_vs_fp64"]}}
         extra, cpu = {}, None
     else:
@@ -808,7 +878,7 @@ def main():
            "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
            "higher_is_better": res["unit"] not in ("ms", "s/step"), "scaling": "weak", "vs_baseline": None, "dtype": res["dtype"],
            "data": "synthetic (seeded)", "config": res["config"], "roofline": res["roofline"],
-           "kernels": res["kernels"]}
+           "kernel_io": res["kernel_io"], "kernels": res["kernels"]}
     if "check" in res:
         out["check"] = res["check"]
     if "ks_stage" in res:

@@ -463,10 +463,12 @@ class Context:
         return out
 
     def memory(self) -> dict:
-        """device bytes the context holds itself: constant tables, key-switching workspaces, bootstrapping pool"""
-        v = np.zeros(3, dtype=np.uint64)
-        check(load().ckks_context_memory(self.h, _ptr(v), 3))
-        return {"tables": int(v[0]), "workspaces": int(v[1]), "bootstrap_pool": int(v[2])}
+        """device bytes the context holds itself: constant tables, key-switching workspaces, bootstrapping pool, and
+        the library's static scratch for the allocation-free entry point (one per GPU, shared by its contexts)"""
+        v = np.zeros(4, dtype=np.uint64)
+        check(load().ckks_context_memory(self.h, _ptr(v), 4))
+        return {"tables": int(v[0]), "workspaces": int(v[1]), "bootstrap_pool": int(v[2]),
+                "noalloc_scratch_per_gpu": int(v[3])}
 
     # profiling ---------------------------------------------------------------------------------
     def profile(self, on: bool) -> None:

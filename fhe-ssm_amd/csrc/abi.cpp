@@ -221,12 +221,14 @@ int ckks_side_copy(ckks_context* ctx, void* dst, const void* src, size_t bytes, 
     fhe::Context& c = ctx->c;
     // copies to host memory on their own side stream: a step's run of state copies out does not hold up the
     // prefetches into device memory queued behind it
+    // the destination is host memory unless the runtime reports device memory: pinned host memory reports
+    // hipMemoryTypeHost, pageable host memory fails the query or reports hipMemoryTypeUnregistered
     hipPointerAttribute_t at{};
-    bool to_host = false;
+    bool to_host = true;
     if (hipPointerGetAttributes(&at, dst) == hipSuccess)
-        to_host = at.type == hipMemoryTypeHost;
+        to_host = at.type != hipMemoryTypeDevice && at.type != hipMemoryTypeManaged && at.type != hipMemoryTypeArray;
     else
-        (void)hipGetLastError();  // pageable host memory: an unregistered pointer
+        (void)hipGetLastError();
     hipStream_t& side = to_host ? c.side_out : c.side;
     if (!side) HIP_TRY(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
     // after the work enqueued so far on stream
@@ -1043,12 +1045,15 @@ int ckks_context_memory(const ckks_context* ctx, uint64_t* bytes, uint32_t n) {
     if (!bytes && n) return fail(CKKS_EINVAL, "null argument");
     const fhe::Context& c = ctx->c;
     const uint64_t T = c.L + c.K;
-    uint64_t v[3] = {0, 0, 0};
+    uint64_t v[4] = {0, 0, 0, 0};
     v[0] = 4 * T * fhe::kN * sizeof(fhe::TwPair) + T * sizeof(fhe::PrimeInfo);
     for (auto& kv : c.small_ntt) v[0] += T * kv.first * sizeof(fhe::TwPair);
     for (auto& s : c.scratch) v[1] += s.second;
     for (auto& kv : c.buf_pool) v[2] += kv.first * kv.second.size();
-    for (uint32_t i = 0; i < n && i < 3; i++) bytes[i] = v[i];
+    // the allocation-free entry point's static scratch: held on every GPU the library has run on, whether or not
+    // that entry point is called, and shared by all contexts on that GPU (counted once per context here)
+    v[3] = fhe::kScratchBytes;
+    for (uint32_t i = 0; i < n && i < 4; i++) bytes[i] = v[i];
     return CKKS_OK;
 }
 

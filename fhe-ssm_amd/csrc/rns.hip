@@ -106,8 +106,14 @@ __global__ __launch_bounds__(256) void k_tensor_sum(const uint64_t* const* __res
 // out : batch c -> out + c*out_bstride, target limb j at off(out_desc[j])*N, prime prime(out_desc[j])
 // tab : [n_in] TwPair (qhinv, companion) followed by [n_in][n_out] uint64 qhmod
 // Every BConv output is the input of a forward NTT, which takes words below 8q and stores canonical residues: the
-// Montgomery-reduced instances leave their outputs in [0, 2q) ([0, 3q) with the rescale's lift), skipping the final
-// conditional subtraction.
+// Montgomery-reduced instances leave their outputs in [0, 2q) (redc_lazy), skipping the final conditional
+// subtraction; the ModDown+rescale instance adds the rescale's lift to that, below q (lift_centered) or below 3q (the
+// fast lift), so its outputs stay below 5q.  The bounds, in units of the output prime q:
+constexpr uint32_t kRedcLazyBound = 2;    // redc_lazy: [0, 2q)
+constexpr uint32_t kFastLiftBound = 3;    // z + [z > q_{l-1}/2] dl with z < q_{l-1} <= 2q and dl < q: [0, 3q)
+constexpr uint32_t kNttFwdInputBound = 8; // the forward NTT's first stage takes words below 8q (fwd_a_tile, ct_bfly)
+static_assert(kRedcLazyBound + kFastLiftBound <= kNttFwdInputBound,
+              "a BConv output must stay below the forward NTT's input bound");
 // A limb descriptor is one dword, offset | prime << 16: the output loop indexes it with a wave-uniform j, which
 // a scalar load serves (byte or half-word arrays would be read with vector loads, one round trip per output).
 constexpr int kMaxBconvIn = 16;
@@ -136,7 +142,8 @@ struct MdrBconvArgs {
     const uint64_t* addc;   // [n_polys][N] coefficient form of the addend's limb l-1, or null
     TwPair pinv_last;       // P^-1 mod q_{l-1}
     // fast_lift (set when q_{l-1} <= 2 q_j for every output j): the lift of z into q_j is z + [z > q_{l-1} / 2] dl[j]
-    // with dl[j] = -q_{l-1} mod q_j, below 3 q_j -- no reduction (the forward NTT that reads T takes words below 8q)
+    // with dl[j] = -q_{l-1} mod q_j, below 3 q_j -- no reduction; added to the Montgomery sum's [0, 2q_j), T_j stays
+    // below 5 q_j (the forward NTT that reads T takes words below 8q: kNttFwdInputBound)
     uint32_t fast_lift;
     uint64_t dl[kMaxBconvOut];
 };
@@ -241,7 +248,8 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         correct(acc, j, br);
         uint64_t v;
         if (mont) {
-            // left in [0, 2q) ([0, 3q) with the lift): the consumer is a forward NTT (inputs below 8q)
+            // left in [0, 2q) (plus the lift: [0, 3q) with lift_centered, [0, 5q) with the fast lift): the consumer
+            // is a forward NTT (inputs below 8q)
             v = redc_lazy(acc, pj.q, pj.mont_ninv);
             if constexpr (kMdr) v += mb.fast_lift ? z + (zneg ? mb.dl[j] : 0) : lift_centered(z, ql, br);
         } else {
@@ -1092,8 +1100,10 @@ hipError_t launch_bconv_mdr(const Context& ctx, const BConvPlan& plan, const uin
     mb.fast_lift = 1;
     for (uint32_t j = 0; j + 1 < l; j++) {
         const uint64_t qj = ctx.moduli[plan.out_idx[j]];
-        if (ql > 2 * qj) mb.fast_lift = 0;
+        if (ql > 2 * qj) mb.fast_lift = 0;  // the fast lift's [0, 3q_j) needs q_{l-1} <= 2 q_j
         mb.dl[j] = (qj - ql % qj) % qj;
+        // the NTT's 8q input bound must hold in 64 bits too: 5 q_j < 2^64
+        if (qj > (~0ull) / kNttFwdInputBound) return hipErrorInvalidValue;
     }
     // P limbs + limb l-1 (+ the addend's) read, l-1 limbs written
     const double bytes = (double)n_polys * (plan.n_in + 1 + (addc ? 1 : 0) + (l - 1)) * kN * 8;
@@ -1291,9 +1301,11 @@ hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t 
     }
     for (uint32_t t = 0; t < l; t++) a.pmod[t] = pmod[t];
     // the babies' inner products are not counted as key switches: they have neither a ModUp nor a ModDown of their own
-    // bytes: each input's extension and c0 (read once per key-switched baby: different automorphism blocks), the
-    // keys and diagonals once, the giant sums written
-    const double by = (double)n_inst * n_in * (n_ks * ((double)D * E + l) + (nb - n_ks) * 2.0 * l) +
+    // algorithmic bytes, every array once per launch: each input's extension (if a baby is key-switched) and its c0
+    // (and c1, if a baby is the identity), the keys and the diagonals, the giant sums written.  (Each baby re-reads
+    // its input's words through another automorphism, and each instance re-reads the keys and diagonals of a tile:
+    // those re-reads are served by L2 and are not counted.)
+    const double by = (double)n_inst * n_in * ((n_ks ? (double)D * E : 0.0) + (n_ks < nb ? 2.0 : 1.0) * l) +
                       (double)n_ks * 2 * D * E + (double)n_diag * E + (double)n_inst * ng * 2 * E;
     const int pi = prof_begin(ctx, "bsgs_dh_mac", by * kN * 8, st);
     using MacKernel = void (*)(const uint64_t*, const uint64_t*, const uint64_t*, uint64_t*, DhMacArgs,

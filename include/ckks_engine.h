@@ -85,10 +85,14 @@ int ckks_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes);
 /* Pinned host memory, and copies on a side stream of the context that overlap the work on the caller's stream (no
  * counterpart in the reference; for a caller that keeps copies of device data on the host while it computes):
  * ckks_side_copy   copies bytes (any direction) once the work enqueued so far on stream is done; returns a ticket.
- *                  Copies to host memory run on one side stream, all others on another: copies of one kind complete
- *                  in issue order, copies of different kinds are not ordered against each other (wait on the ticket)
+ *                  Copies to host memory (pinned or pageable: any destination the runtime does not report as device
+ *                  memory) run on one side stream, all others on another: copies of one kind complete in issue order,
+ *                  copies of different kinds are not ordered against each other (wait on the ticket).  A copy from or
+ *                  to pageable host memory is not asynchronous to the host.
  * ckks_side_wait   makes stream wait (without blocking the host) until the copy of ticket is done
- * ckks_side_sync   blocks the host until every side copy is done and forgets the tickets */
+ * ckks_side_sync   blocks the host until every side copy is done and forgets the tickets; each side copy holds two
+ *                  events until the next ckks_side_sync, so a caller that issues side copies in a loop (the decode
+ *                  driver: once per step) calls it periodically to release them */
 int ckks_host_alloc(size_t bytes, void** h_out);
 int ckks_host_free(void* h);
 int ckks_side_copy(ckks_context* ctx, void* dst, const void* src, size_t bytes, void* stream, uint64_t* ticket);
@@ -387,8 +391,10 @@ int ckks_decrypt_coeffs(ckks_context* ctx, const ckks_secret* sk, const uint64_t
 int ckks_context_counters(ckks_context* ctx, uint64_t* key_switches, int reset);
 /* ckks_context_memory: device bytes the context holds itself (no counterpart in the reference; for memory
  * accounting): bytes[0] constant tables (twiddles, small-ring tables, prime data), bytes[1] the growable
- * key-switching workspaces, bytes[2] the bootstrapping buffer pool (free buffers kept for the next call).
- * Fills min(n, 3) entries. */
+ * key-switching workspaces, bytes[2] the bootstrapping buffer pool (free buffers kept for the next call),
+ * bytes[3] the static scratch of ckks_eval_mult_rescale_noalloc (a 160 MiB device array the library holds on each
+ * GPU it runs on whether or not that entry point is called, shared by every context on the GPU).
+ * Fills min(n, 4) entries. */
 int ckks_context_memory(const ckks_context* ctx, uint64_t* bytes, uint32_t n);
 int ckks_profile_enable(ckks_context* ctx, int on);
 int ckks_profile_reset(ckks_context* ctx);

@@ -1,6 +1,6 @@
-"""bench.py's counter-measured figures (roofline.traffic and roofline.valu) are constants taken from the rocprofv3
-summaries under profiles/; this checks them against those summaries' own tables, so that a re-measured profile and
-the bench line cannot drift apart.  CPU only."""
+"""bench.py's counter-measured figures (roofline.traffic, kernel_io.traffic and kernel_io.valu) and its stream rates are
+constants taken from the rocprofv3 and stream summaries under profiles/; this checks them against those summaries' own
+tables, so that a re-measured profile and the bench line cannot drift apart.  CPU only."""
 import os
 import re
 import sys
@@ -58,3 +58,73 @@ def test_ntt_constants_match_the_profile():
         assert abs(meas["traffic"] - traffic) / traffic < 0.01, name
         valu = (r1[2] + r2[2]) * 1e6
         assert abs(meas["valu_insts"] - valu) / valu < 0.01, name
+
+
+def counter_rows_with_dispatches(path):
+    """(kernel, dispatches, read GB, write GB) for every row of a profile's per-dispatch counter table"""
+    out = []
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 6 and cells[0].startswith("k_") and re.fullmatch(r"[0-9.]+", cells[3] or "x"):
+            out.append((cells[0], int(cells[2]), float(cells[3]), float(cells[4])))
+    return out
+
+
+def test_hmult_step_traffic_is_the_sum_over_every_dispatch():
+    """roofline.traffic of config 2 = the counter-measured bytes of one HMult step summed over all its dispatches (the
+    profiled run holds 5 steps: 1 warmup, 3 timed, 1 profiled)"""
+    sys.path.insert(0, REPO)
+    import bench
+    rows = counter_rows_with_dispatches(os.path.join(REPO, "profiles", "hmult_config2_kernels.md"))
+    per_step = sum((r + w) * n for (_, n, r, w) in rows) / 5 * 1e9
+    meas = bench.MEASURED[("hmult", "step")]["traffic"]
+    assert abs(meas - per_step) / per_step < 0.01
+    # against the SURVEY 8(d) unit: the step moves about 3x the algorithmic bytes
+    ratio = meas / (bench.N_PAIRS * bench.HMULT_UNIT_BYTES)
+    assert 2.0 < ratio < 4.0
+
+
+def test_ntt_step_traffic_is_forward_plus_inverse():
+    sys.path.insert(0, REPO)
+    import bench
+    step = bench.MEASURED[("ntt", "step")]["traffic"]
+    assert abs(step - bench.MEASURED[("ntt", "ntt_fwd_2pass")]["traffic"] -
+               bench.MEASURED[("ntt", "ntt_inv_2pass")]["traffic"]) < 1e6
+
+
+def test_stream_constants_are_the_profile_maxima():
+    """the "achievable" denominators are the best read-only and nontemporal-copy rates of the committed stream table"""
+    sys.path.insert(0, REPO)
+    import bench
+    reads, copies = [], []
+    for line in open(os.path.join(REPO, "profiles", "hbm_stream.md")):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 7 and all(re.fullmatch(r"[0-9.]+", c) for c in cells):
+            reads.append(float(cells[3]))
+            copies.append(float(cells[4]))
+    assert len(reads) >= 20
+    assert bench.STREAM_READ_GBS == max(reads)
+    assert bench.STREAM_COPY_GBS == max(copies)
+    assert bench.achievable(0.0) == bench.STREAM_READ_GBS and bench.achievable(0.5) == bench.STREAM_COPY_GBS
+
+
+def test_unit_constants_follow_the_limb_counts():
+    """SURVEY 8(d)'s per-op units as limb counts (one limb = 2^16 x 8 B)"""
+    sys.path.insert(0, REPO)
+    import bench
+    assert bench.HMULT_UNIT_BYTES == (96 + 192 + 46) * bench.LIMB_BYTES
+    assert bench.HMULT_EVK_AMORTISED_BYTES == (96 + 3 + 46) * bench.LIMB_BYTES
+    assert bench.KS_UNIT_BYTES == (24 + 192 + 48) * bench.LIMB_BYTES
+    limbs, per_dir = bench.ntt_bytes()
+    assert limbs == 3072 and per_dir == 3_246_391_296
+
+
+def test_step_roofline_fields():
+    sys.path.insert(0, REPO)
+    import bench
+    r = bench.step_roofline("hmult", 64 * bench.HMULT_UNIT_BYTES, 7.6452, 46 / 334, "x")
+    assert abs(r["achieved"] - 64 * bench.HMULT_UNIT_BYTES / 7.6452e-3 / 1e9) < 0.1
+    assert r["frac"] == round(r["achieved"] / 8000.0, 4)
+    assert r["achievable"] == bench.STREAM_COPY_GBS
+    assert r["traffic"] == bench.MEASURED[("hmult", "step")]["traffic"]
+    assert 2.0 < r["traffic_over_algorithmic"] < 4.0

@@ -455,13 +455,25 @@ def test_native_decoder_serves_a_directory(engine, M, tmp_path):
 
 
 @pytest.mark.timeout(900)
-def test_decode_step_full_config5(engine, DS, M):
+@pytest.mark.parametrize("driver", ["python", "native"])
+def test_decode_step_full_config5(engine, DS, M, driver):
     """the full config-5 step: 12 layers, two tokens (cold start, then the carried state); decrypted output
-    and the client's vocabulary logits against the float64 model, relErrRms <= 1e-3"""
+    and the client's vocabulary logits against the float64 model, relErrRms <= 1e-3 -- through the Python plan and
+    through the C++ driver that bench.py times (libfhe_ssm_decode.so)"""
     from oracle import rwkv_ref as ref
     be, sk = engine
     W = M.make_weights(9, n_layers=12)
-    step = DS.DecodeStep(be, W)
+    if driver == "native":
+        nat = load_module("native_decode").from_backend(be, 12)
+        nat.set_weights(W)
+
+        def step(ct):
+            out, lv, sc = nat.step(ct.ptr(), ct.level, ct.scale)
+            return DS.HECt(out, 1, lv, sc)
+        n_boot = lambda: nat.bootstraps
+    else:
+        step = DS.DecodeStep(be, W)
+        n_boot = lambda: step.stats["bootstraps"]
     st = ref.init_state(32, 12)
     head = M.head_matrix(W, rows=4096)
     for s in range(2):
@@ -472,6 +484,8 @@ def test_decode_step_full_config5(engine, DS, M):
         err = np.sqrt(np.mean((got - xo) ** 2)) / np.sqrt(np.mean(xo ** 2))
         lg, lg_ref = got @ head.T, xo @ head.T
         lerr = np.sqrt(np.mean((lg - lg_ref) ** 2)) / np.sqrt(np.mean(lg_ref ** 2))
-        print(f"token {s}: relErrRms {err:.3e}, logits (4096-row slice) {lerr:.3e}")
+        print(f"{driver} token {s}: relErrRms {err:.3e}, logits (4096-row slice) {lerr:.3e}")
         assert err < 1e-3 and lerr < 1e-3, (err, lerr)
-    assert step.stats["bootstraps"] == 2 * 12 * 26
+    assert n_boot() == 2 * 12 * 26
+    if driver == "native":
+        nat.close()

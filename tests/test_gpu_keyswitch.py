@@ -122,6 +122,25 @@ def test_eval_mult_rescale_batch(ckks, ctx, octx, evk, d_evk):
         assert np.array_equal(out[i], octx.hmult_relin_rescale(a[i], b[i], l, evk)), i
 
 
+@pytest.mark.timeout(300)
+def test_eval_mult_rescale_config2_full_batch(ckks, ctx, octx, evk, d_evk):
+    """the shape bench.py times: 64 pairs at l = 24 in one call (launch grids 16 x 1472 for T's NTT with the combine,
+    256 x 64 for the ModUp BConvs); the first and last pair and 2 seeded ones in between word for word against the
+    oracle, every output word reduced"""
+    B, l = 64, 24
+    a = residues(ctx.moduli, (B, 2), list(range(l)), seed=35)
+    b = residues(ctx.moduli, (B, 2), list(range(l)), seed=36)
+    da, db = ckks.DeviceBuffer.from_array(a), ckks.DeviceBuffer.from_array(b)
+    dout = ckks.DeviceBuffer(B * 2 * (l - 1) * N * 8)
+    ctx.eval_mult_rescale(da.ptr, db.ptr, B, l, d_evk.ptr, dout.ptr)
+    out = dout.download((B, 2, l - 1, N))
+    q = np.array(ctx.moduli[:l - 1], dtype=np.uint64)
+    assert bool((out < q[None, None, :, None]).all())
+    rng = np.random.default_rng(37)
+    for i in [0, B - 1] + sorted(rng.choice(np.arange(1, B - 1), 2, replace=False).tolist()):
+        assert np.array_equal(out[i], octx.hmult_relin_rescale(a[i], b[i], l, evk)), i
+
+
 @pytest.mark.parametrize("alias", ["a", "b"])
 def test_eval_mult_rescale_in_place(ckks, ctx, octx, evk, d_evk, alias):
     """The output written over an input (the product's d0 / d1 then take the tensor kernel's round trip, since the

@@ -22,10 +22,22 @@ def residues(moduli, shape_prefix, prime_idx, seed):
     return x % q.reshape((1,) * len(shape_prefix) + (-1, 1))
 
 
+def hip_runtime_path():
+    """the HIP runtime the engine library itself linked: the libamdhip64 object mapped into this process once the
+    engine is loaded (whatever its soname on this ROCm)"""
+    load_ckks().load()
+    with open("/proc/self/maps") as f:
+        for line in f:
+            path = line.split()[-1]
+            if "libamdhip64.so" in path.rsplit("/", 1)[-1]:
+                return path
+    raise RuntimeError("the engine library is loaded but no libamdhip64 is mapped")
+
+
 def free_device_bytes():
     """hipMemGetInfo of the HIP runtime the engine library itself links (already loaded with it)"""
     import ctypes
-    hip = ctypes.CDLL("libamdhip64.so.7")
+    hip = ctypes.CDLL(hip_runtime_path())
     free, total = ctypes.c_size_t(), ctypes.c_size_t()
     assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
     return free.value
