@@ -30,6 +30,7 @@
 // (a product of two limbs, an evk inner product) and copy it into a ModUp buffer; a forward first pass may lift a
 // rescale's dropped limb; a forward last pass may end in a ModDown / rescale / key-switch combine (k_ntt_fwd_b_mdr,
 // k_ntt_fwd_b_sub, k_ntt_fwd_b_ksl) instead of storing the transform.
+#include <set>
 #include <type_traits>
 
 #include "engine.hpp"
@@ -1090,7 +1091,13 @@ hipError_t launch_ntt_inv_ksl(const Context& ctx, uint64_t* acc, const JobSpec& 
     }
     ka.E = E;
     ka.T = ctx.L + ctx.K;
-    const double bytes = (double)n_jobs * (2.0 * D + 3) * kN * 8 + (double)js.n_primes * kN * sizeof(TwPair);
+    // algorithmic bytes: per job the limb written, read back by the second pass and written again; per distinct
+    // extension and per distinct key D limbs for each of an item's jobs (items of a hoisted list share an extension,
+    // items of a batch a key); the tables
+    std::set<const uint64_t*> de(ext, ext + n), dk(evk, evk + n);
+    const double per_item = (double)n_jobs / n;
+    const double bytes = ((double)n_jobs * 3 + ((double)de.size() + (double)dk.size()) * per_item * D) * kN * 8 +
+                         (double)js.n_primes * kN * sizeof(TwPair);
     const int pi = prof_begin(ctx, "ntt_inv_ks", bytes, st);
     const dim3 grid(16, n_jobs), block(kTileThreads);
     switch (D) {
@@ -1173,9 +1180,10 @@ hipError_t launch_ntt_inv_ks(const Context& ctx, uint64_t* acc, const JobSpec& j
                              const uint64_t* ext, const uint64_t* evk, uint32_t D, uint32_t E, hipStream_t st) {
     if (!js.jobs || D < 1 || D > 4 || n_jobs == 0) return hipErrorInvalidValue;
     const KsJobArgs ka{ext, evk, E, ctx.L + ctx.K};
-    // algorithmic bytes: per job D extension limbs and D key limbs read (the key shared by the batch counts once per
-    // job here), the limb written and read back by the second pass and written again; the tables
-    const double bytes = (double)n_jobs * (2.0 * D + 3) * kN * 8 + (double)js.n_primes * kN * sizeof(TwPair);
+    // algorithmic bytes: per job D extension limbs read, the limb written, read back by the second pass and written
+    // again; the key shared by the batch once: D limbs for each distinct (poly half, prime) of the jobs; the tables
+    const double key_limbs = std::min<double>(n_jobs, 2.0 * js.n_primes) * D;
+    const double bytes = ((double)n_jobs * (D + 3.0) + key_limbs) * kN * 8 + (double)js.n_primes * kN * sizeof(TwPair);
     const int pi = prof_begin(ctx, "ntt_inv_ks", bytes, st);
     const dim3 grid(16, n_jobs), block(kTileThreads);
     switch (D) {

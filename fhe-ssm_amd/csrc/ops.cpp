@@ -89,7 +89,9 @@ hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t 
 hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
                              uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_out,
                              uint32_t nt, uint32_t A, uint32_t M, uint32_t l, uint64_t* dst, hipStream_t st,
-                             uint32_t R = 1, uint32_t c_off = 0, uint64_t s_lo = 0, bool accumulate = false);
+                             uint32_t R = 1, uint32_t c_off = 0, uint64_t s_lo = 0, bool accumulate = false,
+                             const TwPair* src_pmod = nullptr, const uint64_t* id_src = nullptr,
+                             uint64_t id_stride = 0);
 hipError_t launch_mul_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
                             uint32_t l, uint64_t pt_bstride, uint32_t log_rep, hipStream_t st);
 hipError_t launch_add_plain(const Context& ctx, const uint64_t* ct, const uint64_t* pt, uint64_t* out, uint32_t B,
@@ -928,7 +930,12 @@ void add_plain(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const u
 
 // Baby-step giant-step diagonal matrix-vector product (gpu_real_model.cu:2767-2823):
 // y = rescale( sum_g rot_{g*bs}( sum_j diag'_{g*bs+j} (.) rot_j(u) ) ), diagonals pre-rotated by -g*bs.
-// Babies rot_1..rot_{bs-1} share one ModUp (hoisted); the ng-1 giant rotations run as one batch.
+// Babies rot_1..rot_{bs-1} share one ModUp (hoisted).  The giant rotations share one ModDown: each rotating giant
+// sum v_g's c1 is extended (one ModUp over all of them), and sum_g Auto_g(<ext_g, evk_g> + (P c0_g, 0)) + P v_0 is
+// formed in Q_l P by one kernel (the key switches' inner products at the automorphisms' source words, the P
+// scaling of the Q_l sums on the fly), then brought down and rescaled together: ng - 1 ModDowns fewer than rotating
+// each giant on its own.  The words differ from the per-giant form's only by the key-switching rounding (one
+// ModDown's instead of the sum of ng - 1).
 void bsgs_matvec(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* diags, uint32_t n_diag, uint32_t bs,
                  const uint64_t* const* baby_evk, const uint64_t* const* giant_evk, uint64_t* out, hipStream_t st) {
     check_level(ctx, l);
@@ -939,8 +946,6 @@ void bsgs_matvec(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* d
     const size_t ctw = (size_t)2 * l * W;
     uint64_t* baby = (uint64_t*)ws_get(ctx, WS_BABY, (size_t)bs * ctw * 8);
     uint64_t* v = (uint64_t*)ws_get(ctx, WS_GIANT, (size_t)ng * ctw * 8);
-    uint64_t* vr = (uint64_t*)ws_get(ctx, WS_GROT, (size_t)ng * ctw * 8);
-    uint64_t* sum = (uint64_t*)ws_get(ctx, WS_SUM, ctw * 8);
     HIPX(hipMemcpyAsync(baby, ct, ctw * 8, hipMemcpyDeviceToDevice, st));
     if (bs > 1) {
         std::vector<int64_t> steps(bs - 1);
@@ -950,15 +955,24 @@ void bsgs_matvec(Context& ctx, const uint64_t* ct, uint32_t l, const uint64_t* d
     std::vector<const uint64_t*> bp(bs);
     for (uint32_t j = 0; j < bs; j++) bp[j] = baby + (size_t)j * ctw;
     HIPX(launch_bsgs_mac(ctx, bp.data(), diags, v, bs, n_diag, ng, l, 0, st));
-    std::vector<const uint64_t*> terms(1, v);
-    if (ng > 1) {
-        std::vector<int64_t> steps(ng - 1);
-        for (uint32_t g = 1; g < ng; g++) steps[g - 1] = (int64_t)g * bs;
-        rotate_list(ctx, v + ctw, ng - 1, l, steps.data(), giant_evk, vr, st);
-        for (uint32_t g = 1; g < ng; g++) terms.push_back(vr + (size_t)(g - 1) * ctw);
+    if (ng == 1) {
+        rescale(ctx, v, 2, l, out, st);
+        return;
     }
-    HIPX(launch_sum_list(ctx, terms.data(), (uint32_t)terms.size(), sum, 2, l, st));
-    rescale(ctx, sum, 2, l, out, st);
+    const uint32_t ngr = ng - 1, E = l + ctx.K, D = num_digits(ctx, l);
+    const size_t exw = (size_t)D * E * W;
+    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)ngr * exw * 8);
+    uint64_t* T = (uint64_t*)ws_get(ctx, WS_GROT, (size_t)2 * E * W * 8);
+    modup(ctx, v + ctw + (size_t)l * W, ext, ngr, l, st, ctw);  // the c1 halves of v_1 .. v_{ng-1}, read in place
+    std::vector<const uint64_t*> keys(ngr);
+    std::vector<uint32_t> g(ngr);
+    for (uint32_t j = 0; j < ngr; j++) {
+        keys[j] = giant_evk[j];
+        g[j] = rotation_index((int64_t)(j + 1) * bs);
+    }
+    HIPX(launch_qp_rot_sum(ctx, ext, exw, v + ctw, ctw, keys.data(), g.data(), 1, ngr, 1, ngr, l, T, st, 1, 0, 0,
+                           false, pmod_tab(ctx).data(), v, 0));
+    moddown_rescale(ctx, T, 2, l, nullptr, out, st);
 }
 
 // General BSGS linear transform on one ciphertext [2][l][N]:
@@ -1010,39 +1024,67 @@ void bsgs_multi_batch(Context& ctx, const uint64_t* const* in, uint32_t n_inst, 
         HIPX(launch_bsgs_mac(ctx, bp.data(), diags, v + (size_t)s * n_out * ng * ctw, nbt, nbt * n_out * ng,
                              n_out * ng, l, log_rep, st));
     }
-    // giants with a non-zero step, all instances and outputs, packed contiguously and rotated as one list
-    std::vector<int64_t> gs;
+    // the giant rotations share one ModDown per output: the rotating giant sums of every instance and output, packed
+    // contiguously, have their c1 extended (in chunks of outputs whose extensions fit a bounded buffer), and each
+    // output's sum_g Auto_g(<ext_g, evk_g> + (P c0_g, 0)) + P v_{g0} is formed in Q_l P by one kernel, placed at the
+    // output's slot; one ModDown (with the rescale) brings all outputs down
+    const uint32_t n_o = n_inst * n_out;
     std::vector<const uint64_t*> gk;
-    std::vector<uint32_t> gpos;  // index into v
-    for (uint32_t s = 0; s < n_inst; s++)
-        for (uint32_t o = 0; o < n_out; o++)
-            for (uint32_t g = 0; g < ng; g++)
-                if (gsteps[g] != 0) {
-                    gs.push_back(gsteps[g]);
-                    gk.push_back(gevk[g]);
-                    gpos.push_back((s * n_out + o) * ng + g);
-                }
-    uint64_t* vr = nullptr;
-    if (!gs.empty()) {
-        uint64_t* packed = (uint64_t*)ws_get(ctx, WS_SUM, gs.size() * ctw * 8);
-        vr = (uint64_t*)ws_get(ctx, WS_GROT, gs.size() * ctw * 8);
-        std::vector<const uint64_t*> src(gs.size());
-        for (size_t r = 0; r < gs.size(); r++) src[r] = v + (size_t)gpos[r] * ctw;
-        HIPX(launch_gather(ctx, src.data(), (uint32_t)src.size(), ctw, packed, st));
-        rotate_list(ctx, packed, (uint32_t)gs.size(), l, gs.data(), gk.data(), vr, st);
-    }
-    uint64_t* dst = out;
-    if (do_rescale) dst = (uint64_t*)ws_get(ctx, WS_LIN, (size_t)n_inst * n_out * ctw * 8);
-    size_t r = 0;
-    for (uint32_t s = 0; s < n_inst; s++)
-        for (uint32_t o = 0; o < n_out; o++) {
-            std::vector<const uint64_t*> terms;
-            for (uint32_t g = 0; g < ng; g++)
-                terms.push_back(gsteps[g] == 0 ? v + ((size_t)(s * n_out + o) * ng + g) * ctw : vr + (r++) * ctw);
-            const size_t slot = by_output ? (size_t)o * n_inst + s : (size_t)s * n_out + o;
-            HIPX(launch_sum_list(ctx, terms.data(), (uint32_t)terms.size(), dst + slot * ctw, 2, l, st));
+    std::vector<uint32_t> gidx;
+    int32_t g0 = -1;
+    for (uint32_t g = 0; g < ng; g++) {
+        if (gsteps[g] == 0) {
+            if (g0 >= 0) throw std::invalid_argument("BSGS: at most one giant step 0");
+            g0 = (int32_t)g;
+            continue;
         }
-    if (do_rescale) rescale(ctx, dst, 2 * n_inst * n_out, l, out, st);
+        gk.push_back(gevk[g]);
+        gidx.push_back(rotation_index(gsteps[g]));
+    }
+    const uint32_t ngr = (uint32_t)gk.size();
+    const auto slot_of = [&](uint32_t c) {  // output c = s n_out + o -> its place in out
+        return by_output ? (size_t)(c % n_out) * n_inst + c / n_out : (size_t)c;
+    };
+    if (ngr == 0) {  // the identity giant only: its sums are the outputs
+        uint64_t* dst = do_rescale ? (uint64_t*)ws_get(ctx, WS_LIN, (size_t)n_o * ctw * 8) : out;
+        for (uint32_t c = 0; c < n_o; c++) {
+            const uint64_t* term = v + ((size_t)c * ng + (uint32_t)g0) * ctw;
+            HIPX(launch_sum_list(ctx, &term, 1, dst + slot_of(c) * ctw, 2, l, st));
+        }
+        if (do_rescale) rescale(ctx, dst, 2 * n_o, l, out, st);
+        return;
+    }
+    const uint32_t E = l + ctx.K, D = num_digits(ctx, l);
+    const size_t exw = (size_t)D * E * W, cte = (size_t)2 * E * W;
+    uint64_t* packed = (uint64_t*)ws_get(ctx, WS_SUM, (size_t)n_o * ngr * ctw * 8);
+    {
+        std::vector<const uint64_t*> src;
+        src.reserve((size_t)n_o * ngr);
+        for (uint32_t c = 0; c < n_o; c++)
+            for (uint32_t g = 0; g < ng; g++)
+                if ((int32_t)g != g0) src.push_back(v + ((size_t)c * ng + g) * ctw);
+        HIPX(launch_gather(ctx, src.data(), (uint32_t)src.size(), ctw, packed, st));
+    }
+    uint64_t* T = (uint64_t*)ws_get(ctx, WS_GROT, (size_t)n_o * cte * 8);
+    const uint32_t chunk = std::max<uint32_t>(1, 32 / ngr);
+    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)std::min(chunk, n_o) * ngr * exw * 8);
+    const TwPair* pm = pmod_tab(ctx).data();
+    for (uint32_t o0 = 0; o0 < n_o; o0 += chunk) {
+        const uint32_t m = std::min(chunk, n_o - o0);
+        const uint64_t* src = packed + (size_t)o0 * ngr * ctw;
+        modup(ctx, src + (size_t)l * W, ext, m * ngr, l, st, ctw);
+        const uint64_t* id = g0 >= 0 ? v + ((size_t)o0 * ng + (uint32_t)g0) * ctw : nullptr;
+        if (by_output)
+            HIPX(launch_qp_rot_sum(ctx, ext, exw, src, ctw, gk.data(), gidx.data(), m, ngr, 1, ngr, l, T, st, n_out, o0,
+                                   (uint64_t)n_inst * cte, false, pm, id, (uint64_t)ng * ctw));
+        else
+            HIPX(launch_qp_rot_sum(ctx, ext, exw, src, ctw, gk.data(), gidx.data(), m, ngr, 1, ngr, l,
+                                   T + (size_t)o0 * cte, st, 1, 0, 0, false, pm, id, (uint64_t)ng * ctw));
+    }
+    if (do_rescale)
+        moddown_rescale(ctx, T, 2 * n_o, l, nullptr, out, st);
+    else
+        moddown_inplace(ctx, T, 2 * n_o, l, nullptr, out, st);
 }
 
 // Double-hoisted BSGS (the same transform as bsgs_multi_batch with do_rescale, over n_inst instances that share

@@ -557,12 +557,21 @@ __global__ __launch_bounds__(256) void k_automorph_list(const uint64_t* __restri
 // automorphism's source word, so nothing is stored between the key switch and the automorphism; the source words
 // of a wave's 64 consecutive outputs are a permutation of one aligned 64-word block (the automorphism multiplies
 // the bit-reversed index by an odd g), so the gathers stay coalesced.
+// Q_l sources (src_q): the terms' inner sums are ciphertexts over Q_l (a single-hoisted BSGS's giant sums), taken
+// into Q_l * P as (P c0, P c1) -- P c mod q_t by the Shoup pair pmod[t], zero on the P limbs -- so that their giant
+// rotations share one ModDown.  id_src (any mode; Q_l only with src_q): one more identity term per output c, read
+// at id_src + c id_stride (a giant step 0 kept out of the packed terms).
 struct QpRotArgs {
     uint32_t l, E, L, D, T, nt, A, M;
     uint32_t n_out, R, c_off, accumulate;
     uint64_t ext_stride, src_stride, s_hi, s_lo;
+    uint32_t src_q;
+    uint64_t src_poly;  // words between a source's c0 and c1 (E N, or l N with src_q)
+    const uint64_t* id_src;
+    uint64_t id_stride;
     const uint64_t* evk[kMaxList];
     uint32_t g[kMaxList];
+    TwPair pmod[kMaxPmap];  // P mod q_t, t < l (src_q)
 };
 
 __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__ ext,
@@ -574,6 +583,13 @@ __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__
     const uint32_t pi = t < a.l ? t : a.L + (t - a.l);
     const Barrett br = barrett_of(primes[pi]);
     const uint64_t q = br.q;
+    // a Q_l source has no words on the P limbs (P c = 0 there); on a Q limb its words are scaled by P mod q_t
+    const bool src_here = !a.src_q || t < a.l;
+    const TwPair pm = a.src_q && t < a.l ? a.pmod[t] : TwPair{0, 0};
+    auto src_word = [&](const uint64_t* p) -> uint64_t {
+        if (!src_here) return 0;
+        return a.src_q ? shoup(p[0], pm.w, pm.wp, q) : p[0];
+    };
     uint64_t v0 = 0, v1 = 0;
     for (uint32_t j = 0; j < a.nt; j++) {
         const uint32_t x = (c / a.A) * a.M + j, kk = c % a.A + j;
@@ -587,12 +603,17 @@ __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__
             const uint64_t* ep = ek + (size_t)pi * kN + sw;
             Acc s0, s1;  // at most kMaxDigits = 8 terms
             ks_dot(xe, (size_t)a.E * kN, ep, (size_t)a.T * kN, a.D, s0, s1);
-            v0 = add_mod(v0, add_mod(reduce_u128(s0.get(), br), sx[0], q), q);
+            v0 = add_mod(v0, add_mod(reduce_u128(s0.get(), br), src_word(sx), q), q);
             v1 = add_mod(v1, reduce_u128(s1.get(), br), q);
         } else {
-            v0 = add_mod(v0, sx[0], q);
-            v1 = add_mod(v1, sx[(size_t)a.E * kN], q);
+            v0 = add_mod(v0, src_word(sx), q);
+            v1 = add_mod(v1, src_word(sx + a.src_poly), q);
         }
+    }
+    if (a.id_src) {  // the identity term of output c (no automorphism)
+        const uint64_t* ix = a.id_src + (size_t)c * a.id_stride + (size_t)t * kN + k;
+        v0 = add_mod(v0, src_word(ix), q);
+        v1 = add_mod(v1, src_word(ix + a.src_poly), q);
     }
     const uint32_t u = c + a.c_off;
     uint64_t* o = dst + (size_t)(u / a.R) * a.s_hi + (size_t)(u % a.R) * a.s_lo + (size_t)t * kN + k;
@@ -1376,13 +1397,15 @@ hipError_t launch_mdr_combine_ks(const Context& ctx, const uint64_t* ext, const 
     return hipGetLastError();
 }
 
-// n_out outputs of nt terms each (see k_qp_rot_sum; src: the terms' inner sums over Q_l * P); keys[i] / steps g[i],
-// i < A + nt - 1 <= 64 (null key: identity term); output c at dst + (u / R) 2 E N + (u % R) s_lo, u = c + c_off;
-// accumulate adds to it
+// n_out outputs of nt terms each (see k_qp_rot_sum; src: the terms' inner sums over Q_l * P, or over Q_l when
+// src_pmod (P mod q_t, t < l) is given); keys[i] / steps g[i], i < A + nt - 1 <= 64 (null key: identity term);
+// id_src: one more identity term per output c at id_src + c id_stride (or null); output c at
+// dst + (u / R) 2 E N + (u % R) s_lo, u = c + c_off; accumulate adds to it
 hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t ext_stride, const uint64_t* src,
                              uint64_t src_stride, const uint64_t* const* keys, const uint32_t* g, uint32_t n_out,
                              uint32_t nt, uint32_t A, uint32_t M, uint32_t l, uint64_t* dst,
-                             hipStream_t st, uint32_t R, uint32_t c_off, uint64_t s_lo, bool accumulate) {
+                             hipStream_t st, uint32_t R, uint32_t c_off, uint64_t s_lo, bool accumulate,
+                             const TwPair* src_pmod, const uint64_t* id_src, uint64_t id_stride) {
     const uint32_t E = l + ctx.K;
     if (n_out == 0 || nt == 0 || A == 0 || A + nt - 1 > (uint32_t)kMaxList || E > kMaxPmap || n_out > 4096)
         return hipErrorInvalidValue;
@@ -1405,17 +1428,26 @@ hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t e
     a.c_off = c_off;
     a.s_hi = (uint64_t)2 * E * kN;
     a.s_lo = s_lo;
-    uint32_t n_ks = 0;
+    a.src_q = src_pmod ? 1 : 0;
+    a.src_poly = (uint64_t)(src_pmod ? l : E) * kN;
+    a.id_src = id_src;
+    a.id_stride = id_stride;
+    if (src_pmod)
+        for (uint32_t t = 0; t < l; t++) a.pmod[t] = src_pmod[t];
+    uint32_t n_ks = 0, n_keys = 0;
     for (uint32_t i = 0; i < A + nt - 1; i++) {
         a.evk[i] = keys[i];
         a.g[i] = g[i];
+        n_keys += keys[i] ? 1 : 0;
     }
     for (uint32_t c = 0; c < A; c++)
         for (uint32_t j = 0; j < nt; j++) n_ks += keys[c + j] ? 1 : 0;
-    // bytes: per key-switched term ext D E + evk 2 D E + S0 E, per identity term 2 E; output 2 E
+    // algorithmic bytes, every array once per launch: per key-switched term its extension D E and c0 (Es limbs of the
+    // source), per identity term both source polys; the distinct keys (2 D E each) once; the outputs 2 E
+    const double Es = src_pmod ? l : E;
     const double terms = (double)n_out / A;
-    const double by = ((double)n_ks * (3.0 * D * E + E) + ((double)A * nt - n_ks) * 2.0 * E) * terms +
-                      (double)n_out * 2 * E;
+    const double by = ((double)n_ks * ((double)D * E + Es) + ((double)A * nt - n_ks) * 2.0 * Es) * terms +
+                      (id_src ? (double)n_out * 2.0 * Es : 0.0) + (double)n_keys * 2 * D * E + (double)n_out * 2 * E;
     ctx.n_keyswitch += n_ks * (uint64_t)(n_out / A);
     const int pi = prof_begin(ctx, "qp_rot_sum", by * kN * 8, st);
     hipLaunchKernelGGL(k_qp_rot_sum, dim3(n_out * (kN / 256) * E), dim3(256), 0, st, ext, src, dst, a, ctx.d_primes);

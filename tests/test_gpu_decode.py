@@ -192,12 +192,15 @@ def test_rotate_masked_bit_exact(ckks, ctx5, octx5):
             assert np.array_equal(got[s, t], want), (s, t)
 
 
-def test_linear_transform_multi_bit_exact(ckks, ctx5, octx5):
-    """2 inputs sharing babies {0, 1, 2}, 2 outputs sharing the babies, giants {0, 3, -3}, compressed
-    diagonals, rescale: against the oracle composition"""
+@pytest.mark.parametrize("gst,rescale", [([0, 3, -3], True), ([3, 0, -3], False), ([3, -3], True)])
+def test_linear_transform_multi_bit_exact(ckks, ctx5, octx5, gst, rescale):
+    """2 inputs sharing babies {0, 1, 2}, 2 outputs sharing the babies, compressed diagonals, with and without the
+    rescale, the identity giant first, in the middle or absent: against the oracle composition -- babies rotated
+    (each with its own ModDown), the MAC over Q_l, then each output's giant sums rotated in Q_l P and brought down
+    once: T = (P v_{g0}) + sum_{g != g0} Auto_g(<ModUp(v_g.c1), evk_g> + (P v_g.c0, 0)), ModDown(T) (then rescale)"""
     l, n_in, n_out = 4, 2, 2
     L, K, D = ctx5.L, ctx5.K, ctx5.dnum
-    bst, gst = [0, 1, 2], [0, 3, -3]
+    bst = [0, 1, 2]
     nb, ng = len(bst), len(gst)
     steps = [1, 2, 3, -3]
     evk = {s: residues(ctx5.moduli, (D, 2), list(range(L + K)), 200 + i) for i, s in enumerate(steps)}
@@ -205,24 +208,42 @@ def test_linear_transform_multi_bit_exact(ckks, ctx5, octx5):
     xs = residues(ctx5.moduli, (n_in, 2), list(range(l)), 21)
     diags = residues(ctx5.moduli, (n_out, ng, n_in * nb), list(range(l)), 22)[..., : N >> LOG_REP]
     dx, dd = ckks.DeviceBuffer.from_array(xs), ckks.DeviceBuffer.from_array(np.ascontiguousarray(diags))
-    out = ckks.DeviceBuffer(n_out * 2 * (l - 1) * N * 8)
+    lo = l - 1 if rescale else l
+    out = ckks.DeviceBuffer(n_out * 2 * lo * N * 8)
     ctw = 2 * l * N * 8
     ctx5.linear_transform_multi([dx.ptr + i * ctw for i in range(n_in)], l, dd.ptr, LOG_REP, bst,
                                 [dk[s].ptr if s else None for s in bst], gst,
-                                [dk[s].ptr if s else None for s in gst], n_out, True, out.ptr)
-    got = out.download((n_out, 2, l - 1, N))
+                                [dk[s].ptr if s else None for s in gst], n_out, rescale, out.ptr)
+    got = out.download((n_out, 2, lo, N))
     q = qcol(ctx5, l)
+    pmap = list(range(l)) + list(range(L, L + K))
+    E = l + K
+    qe = np.array([ctx5.moduli[i] for i in pmap], dtype=object).reshape(-1, 1)
+    P = 1
+    for k in range(K):
+        P *= ctx5.moduli[L + k]
+    pq = np.array([P % ctx5.moduli[i] for i in range(l)], dtype=object).reshape(-1, 1)
 
     def rot(c, s):
         return c if s == 0 else octx5.rotate(c, l, octx5.rot_index(s), evk[s])
 
     babies = [rot(xs[i], s) for i in range(n_in) for s in bst]
     for o in range(n_out):
-        total = np.zeros((2, l, N), dtype=object)
+        T = np.zeros((2, E, N), dtype=object)
         for g in range(ng):
             acc = sum(babies[j].astype(object) * expand(diags[o, g, j]).astype(object)[None] for j in range(n_in * nb))
-            total += rot((acc % q[None]).astype(np.uint64), gst[g]).astype(object)
-        want = octx5.rescale((total % q[None]).astype(np.uint64), l)
+            v = (acc % q[None]).astype(np.uint64)
+            if gst[g] == 0:
+                T[:, :l] += v.astype(object) * pq[None]
+                continue
+            x = octx5.ks_inner(octx5.modup(v[1], l), l, evk[gst[g]]).astype(object)
+            x[0, :l] += v[0].astype(object) * pq
+            x = (x % qe[None]).astype(np.uint64)
+            T += octx5.automorph_eval(x, octx5.rot_index(gst[g])).astype(object)
+        T = (T % qe[None]).astype(np.uint64)
+        want = np.stack([octx5.moddown(T[p], l) for p in range(2)])
+        if rescale:
+            want = octx5.rescale(want, l)
         assert np.array_equal(got[o], want), o
 
 

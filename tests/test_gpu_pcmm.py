@@ -1,7 +1,8 @@
 """Hoisted rotations, plaintext operators and the BSGS diagonal matvec on the GPU.
 
 - bit-exact: hoisted rotations == individual rotations == oracle rotations; the BSGS composition against
-  the oracle composition of the same stages (rotate, ct x pt MAC, rotate, sum, rescale) at a small shape;
+  the oracle composition of the same stages (hoisted baby rotations, ct x pt MAC, giant rotations summed in Q_l P,
+  one ModDown, rescale) at small shapes;
 - decrypted: the full config-3 product (768 x 768 weights N(0, 1/768), u uniform in [-1, 1], 28 baby and
   28 giant steps, L = 16) against the float64 matvec, relErrRms <= 1e-6.
 """
@@ -84,8 +85,13 @@ def test_hoisted_and_batched_rotations_bit_exact(ckks, ctx, octx):
         assert np.array_equal(many[i], octx.rotate(cts[i], l, octx.rot_index(s), evks[i])), s
 
 
-def test_bsgs_composition_bit_exact(ckks, ctx, octx):
-    l, bs, n_diag = 5, 4, 10
+@pytest.mark.parametrize("bs,n_diag", [(4, 10), (4, 4), (2, 9)])
+def test_bsgs_composition_bit_exact(ckks, ctx, octx, bs, n_diag):
+    """ckks_linear_transform_bsgs against the oracle composed from its stages: babies rotated (hoisted, each with its
+    own ModDown), the ct x pt MAC over Q_l, then the giant sums rotated in Q_l P and brought down once --
+    T = (P v0_0, P v0_1) + sum_{g >= 1} Auto_g(<ModUp(v_g.c1), evk_g> + (P v_g.c0, 0)), ModDown(T), rescale.
+    Shapes: 3 giants with a short last one, a single giant (no rotation), 5 giants of 2 babies."""
+    l = 5
     ng = -(-n_diag // bs)
     babies_st, giants_st = list(range(1, bs)), [g * bs for g in range(1, ng)]
     bevk = [residues(ctx.moduli, (DNUM, 2), list(range(L + K)), 200 + i) for i in range(len(babies_st))]
@@ -100,7 +106,14 @@ def test_bsgs_composition_bit_exact(ckks, ctx, octx):
     # oracle composition
     babies = [ct] + [octx.rotate(ct, l, octx.rot_index(s), bevk[i]) for i, s in enumerate(babies_st)]
     q = np.array(ctx.moduli[:l], dtype=object).reshape(1, -1, 1)
-    total = None
+    pmap = list(range(l)) + list(range(L, L + K))
+    E = l + K
+    qe = np.array([ctx.moduli[i] for i in pmap], dtype=object).reshape(1, -1, 1)
+    P = 1
+    for k in range(K):
+        P *= ctx.moduli[L + k]
+    pq = np.array([P % ctx.moduli[i] for i in range(l)], dtype=object).reshape(-1, 1)
+    T = np.zeros((2, E, N), dtype=object)
     for g in range(ng):
         acc = np.zeros((2, l, N), dtype=object)
         for j in range(bs):
@@ -108,10 +121,15 @@ def test_bsgs_composition_bit_exact(ckks, ctx, octx):
             if k < n_diag:
                 acc += babies[j].astype(object) * diags[k].astype(object)[None]
         v = (acc % q).astype(np.uint64)
-        if g > 0:
-            v = octx.rotate(v, l, octx.rot_index(giants_st[g - 1]), gevk[g - 1])
-        total = v.astype(object) if total is None else total + v.astype(object)
-    want = octx.rescale((total % q).astype(np.uint64), l)
+        if g == 0:
+            T[:, :l] += v.astype(object) * pq[None]
+        else:
+            x = octx.ks_inner(octx.modup(v[1], l), l, gevk[g - 1]).astype(object)
+            x[0, :l] += v[0].astype(object) * pq
+            x = (x % qe).astype(np.uint64)
+            T += octx.automorph_eval(x, octx.rot_index(giants_st[g - 1])).astype(object)
+    T = (T % qe).astype(np.uint64)
+    want = octx.rescale(np.stack([octx.moddown(T[p], l) for p in range(2)]), l)
     assert np.array_equal(out.download((2, l - 1, N)), want)
 
 
