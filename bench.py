@@ -96,6 +96,9 @@ MEASURED = {
     ("hmult", "ntt_fwd_mdr"): {"traffic": 11.689e9, "valu_insts": 878.0e6, "source": "profiles/hmult_config2_kernels.md"},
     ("hmult", "ntt_fwd_2pass"): {"traffic": 9.700e9, "valu_insts": 786.2e6, "source": "profiles/hmult_config2_kernels.md"},
     ("ntt", "step"): {"traffic": 12.940e9, "source": "profiles/ntt_config1_kernel_trace.md"},
+    ("pcmm", "step"): {"traffic": 18.375e9, "source": "profiles/pcmm_config3_kernel_trace.md"},
+    ("pcmm", "bsgs_mac"): {"traffic": 7.382e9, "source": "profiles/pcmm_config3_kernel_trace.md"},
+    ("bootstrap", "step"): {"traffic": 58.473e9, "source": "profiles/bootstrap_config4_kernel_trace.md"},
     ("ntt", "ntt_fwd_2pass"): {"traffic": 6.470e9, "valu_insts": 493.9e6, "source": "profiles/ntt_config1_kernel_trace.md"},
     ("ntt", "ntt_inv_2pass"): {"traffic": 6.470e9, "valu_insts": 504.9e6, "source": "profiles/ntt_config1_kernel_trace.md"},
 }

@@ -34,8 +34,19 @@ class SeededPartHeader(ctypes.Structure):
                 ("moduli", _u64 * 128)]
 
 
+class DevSidecarInfo(ctypes.Structure):
+    """ckks_dev_sidecar: the flags and counts of a FIDESlib .dev sidecar"""
+    _fields_ = [("n_devices", _u32), ("devices", _u32 * 64), ("auto_load_ciphertexts", ctypes.c_int32),
+                ("auto_load_plaintexts", ctypes.c_int32), ("key_dist", ctypes.c_int32), ("n_rotations", _u32),
+                ("n_boot_slots", _u32)]
+
+
 # name -> (restype, argtypes); the exported C ABI (kept in step with include/ckks_engine.h)
 SIGNATURES = {
+    "ckks_dev_sidecar_read": (_int, [ctypes.c_char_p, _vp, _vp, _u32, _vp, _u32]),
+    "ckks_dev_sidecar_write": (_int, [ctypes.c_char_p, _vp, _u32, _vp, _u32]),
+    "ckks_rotation_keys_resolve": (_int, [ctypes.c_char_p, _vp, _u32, _vp, _vp, _vp, _u32, ctypes.POINTER(_u32)]),
+    "ckks_rotation_keys_load": (_int, [_vp, ctypes.c_char_p, _vp, _u32, _vp, _u32]),
     "ckks_last_error": (ctypes.c_char_p, []),
     "ckks_context_create": (_int, [ctypes.POINTER(Params), ctypes.POINTER(_vp)]),
     "ckks_context_create_from_moduli": (_int, [_u32, _vp, _u32, _vp, _u32, _u32, ctypes.c_double, _int,
@@ -417,6 +428,12 @@ class Context:
         check(load().ckks_seeded_part_load_key(self.h, path.encode(), record, ctypes.byref(idx), d_evk))
         return int(idx.value)
 
+    def rotation_keys_load(self, dev_path: str, part_paths, d_evks) -> None:
+        """LoadContext's rotation keys: the key of each rotation the .dev sidecar lists, from the seeded part files,
+        into d_evks (one device buffer per listed rotation, in the sidecar's order)"""
+        check(load().ckks_rotation_keys_load(self.h, dev_path.encode(), _str_array(part_paths), len(part_paths),
+                                             _ptr_array(list(d_evks)), len(d_evks)))
+
     def seeded_part_write(self, path: str, key_tag: str, indices, seeds, d_evks) -> None:
         ix = np.ascontiguousarray(np.asarray(indices, dtype=np.uint32))
         sd = np.frombuffer(b"".join(bytes(x) for x in seeds), dtype=np.uint8).copy()
@@ -516,6 +533,45 @@ def seeded_part_header(path: str) -> dict:
     return {"version": h.version, "expander": h.expander, "N": h.ring_dim, "size_q": h.size_q, "size_p": h.size_p,
             "num_part_q": h.num_part_q, "num_per_part_q": h.num_per_part_q, "count": h.count,
             "key_tag": h.key_tag.decode(), "moduli": [int(h.moduli[i]) for i in range(n)]}
+
+
+def _str_array(strs):
+    arr = (ctypes.c_char_p * max(1, len(strs)))(*[x.encode() for x in strs])
+    return ctypes.cast(arr, _vp)
+
+
+def dev_sidecar_read(path: str) -> dict:
+    """a FIDESlib .dev sidecar (host only): devices, flags, rotation amounts and bootstrap slot counts"""
+    info = DevSidecarInfo()
+    check(load().ckks_dev_sidecar_read(path.encode(), ctypes.byref(info), None, 0, None, 0))
+    rots = np.zeros(max(1, info.n_rotations), dtype=np.int32)
+    slots = np.zeros(max(1, info.n_boot_slots), dtype=np.uint32)
+    check(load().ckks_dev_sidecar_read(path.encode(), ctypes.byref(info), _ptr(rots), info.n_rotations, _ptr(slots),
+                                       info.n_boot_slots))
+    return {"devices": [int(info.devices[i]) for i in range(info.n_devices)],
+            "AutoLoadCiphertexts": int(info.auto_load_ciphertexts), "AutoLoadPlaintexts": int(info.auto_load_plaintexts),
+            "KeyDist": int(info.key_dist), "RotationIndexes": [int(x) for x in rots[: info.n_rotations]],
+            "BootstrapSlots": [int(x) for x in slots[: info.n_boot_slots]]}
+
+
+def dev_sidecar_write(path: str, rotations, boot_slots) -> None:
+    """the reference client's cryptocontext.bin.dev for these rotation amounts and bootstrap slot counts"""
+    r = np.ascontiguousarray(np.asarray(list(rotations), dtype=np.int32))
+    b = np.ascontiguousarray(np.asarray(list(boot_slots), dtype=np.uint32))
+    check(load().ckks_dev_sidecar_write(path.encode(), _ptr(r) if len(r) else None, len(r),
+                                        _ptr(b) if len(b) else None, len(b)))
+
+
+def rotation_keys_resolve(dev_path: str, part_paths) -> list:
+    """(part, record, automorphism index) holding the key of each rotation the sidecar lists (host only)"""
+    n = _u32(0)
+    check(load().ckks_rotation_keys_resolve(dev_path.encode(), _str_array(part_paths), len(part_paths), None, None,
+                                            None, 0, ctypes.byref(n)))
+    cap = n.value
+    p, r, g = (np.zeros(max(1, cap), dtype=np.uint32) for _ in range(3))
+    check(load().ckks_rotation_keys_resolve(dev_path.encode(), _str_array(part_paths), len(part_paths), _ptr(p), _ptr(r),
+                                            _ptr(g), cap, ctypes.byref(n)))
+    return [(int(p[i]), int(r[i]), int(g[i])) for i in range(n.value)]
 
 
 def ct_file_info(path: str) -> dict:

@@ -597,6 +597,78 @@ int ckks_seeded_part_write(ckks_context* ctx, const char* path, const char* key_
     });
 }
 
+int ckks_dev_sidecar_read(const char* path, ckks_dev_sidecar* info, int32_t* rotations, uint32_t rot_cap,
+                          uint32_t* boot_slots, uint32_t slot_cap) {
+    if (!path || !info || (rot_cap && !rotations) || (slot_cap && !boot_slots)) return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        const fhe::DevSidecar s = fhe::read_dev_sidecar(path);
+        std::memset(info, 0, sizeof(*info));
+        if (s.devices.size() > sizeof(info->devices) / sizeof(info->devices[0]))
+            return fail(CKKS_EINVAL, "dev sidecar: more devices than the struct holds");
+        info->n_devices = (uint32_t)s.devices.size();
+        for (size_t i = 0; i < s.devices.size(); i++) info->devices[i] = s.devices[i];
+        info->auto_load_ciphertexts = s.auto_load_ciphertexts;
+        info->auto_load_plaintexts = s.auto_load_plaintexts;
+        info->key_dist = s.key_dist;
+        info->n_rotations = (uint32_t)s.rotations.size();
+        info->n_boot_slots = (uint32_t)s.boot_slots.size();
+        for (size_t i = 0; i < s.rotations.size() && i < rot_cap; i++) rotations[i] = s.rotations[i];
+        for (size_t i = 0; i < s.boot_slots.size() && i < slot_cap; i++) boot_slots[i] = s.boot_slots[i];
+        return CKKS_OK;
+    });
+}
+
+int ckks_dev_sidecar_write(const char* path, const int32_t* rotations, uint32_t n_rotations, const uint32_t* boot_slots,
+                           uint32_t n_boot_slots) {
+    if (!path || (n_rotations && !rotations) || (n_boot_slots && !boot_slots)) return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        fhe::DevSidecar s;
+        s.rotations.assign(rotations, rotations + n_rotations);
+        s.boot_slots.assign(boot_slots, boot_slots + n_boot_slots);
+        fhe::write_dev_sidecar(path, s);
+        return CKKS_OK;
+    });
+}
+
+static std::vector<std::string> path_list(const char* const* paths, uint32_t n) {
+    std::vector<std::string> v;
+    for (uint32_t i = 0; i < n; i++) {
+        if (!paths[i]) throw std::invalid_argument("null part path");
+        v.emplace_back(paths[i]);
+    }
+    return v;
+}
+
+int ckks_rotation_keys_resolve(const char* dev_path, const char* const* part_paths, uint32_t n_parts,
+                               uint32_t* part_of, uint32_t* record_of, uint32_t* index_of, uint32_t cap, uint32_t* n) {
+    if (!dev_path || !part_paths || !n || (cap && (!part_of || !record_of || !index_of)))
+        return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        const fhe::DevSidecar s = fhe::read_dev_sidecar(dev_path);
+        const auto loc = fhe::resolve_rotation_keys(s.rotations, path_list(part_paths, n_parts));
+        *n = (uint32_t)loc.size();
+        for (size_t i = 0; i < loc.size() && i < cap; i++) {
+            part_of[i] = loc[i].part;
+            record_of[i] = loc[i].record;
+            index_of[i] = loc[i].index;
+        }
+        return CKKS_OK;
+    });
+}
+
+int ckks_rotation_keys_load(ckks_context* ctx, const char* dev_path, const char* const* part_paths, uint32_t n_parts,
+                            uint64_t* const* d_evks, uint32_t n_keys) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    if (!dev_path || !part_paths || (n_keys && !d_evks)) return fail(CKKS_EINVAL, "null argument");
+    if (ctx->c.K == 0) return fail(CKKS_EINVAL, "context has no special primes");
+    for (uint32_t i = 0; i < n_keys; i++)
+        if (!d_evks[i]) return fail(CKKS_EINVAL, "null key buffer");
+    return guarded([&] {
+        fhe::load_rotation_keys(ctx->c, dev_path, path_list(part_paths, n_parts), d_evks, n_keys);
+        return CKKS_OK;
+    });
+}
+
 int ckks_ct_file_info(const char* path, uint32_t* ring_dim, uint32_t* level, double* scale) {
     if (!path || !ring_dim || !level || !scale) return fail(CKKS_EINVAL, "null argument");
     return guarded([&] {

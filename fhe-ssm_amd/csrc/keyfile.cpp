@@ -12,8 +12,14 @@
 // OpenFHE-cereal ciphertexts there (gpu_real_model.cu:2303-2324, Serial::SerializeToFile), a format only OpenFHE
 // reads; this engine's layout is flat: char[8] "FSSMCTX1"; u32 version = 1; u32 N; u32 level; u32 n_polys = 2;
 // f64 scale; u64 moduli[level] (the chain's first `level` primes); u64 words[2][level][N] (evaluation form).
+//
+// The FIDESlib ".dev" sidecar (cryptocontext.bin.dev, hpc_gpu_port/mac_fhe_client.cpp:178-194) is read and written
+// here too, with the loader that puts the key of every rotation it lists on the device (FIDESlib's LoadContext
+// uploads GetRotationKeySwitchKey(pk, step) for each listed step, gpu_real_model.cu:1436-1529 fills its key map).
 #include <hip/hip_runtime.h>
 
+#include <climits>
+#include <iterator>
 #include <cstring>
 #include <fstream>
 #include <stdexcept>
@@ -251,6 +257,191 @@ void save_ct(Context& ctx, const std::string& path, const uint64_t* d_ct, uint32
     os.write((const char*)w.data(), (std::streamsize)(w.size() * 8));
     os.flush();
     if (!os.good()) throw std::invalid_argument("ciphertext file: write failed: " + path);
+}
+
+// ------------------------------------------------------------------ the FIDESlib .dev sidecar
+// Six lines, as writeDevSidecar writes them (hpc_gpu_port/mac_fhe_client.cpp:183-194):
+//   "<n> { <device> ... }"                 the device list ("1 { 0 }": one GPU, device 0)
+//   "AutoLoadCiphertexts: <int>"
+//   "AutoLoadPlaintexts: <int>"
+//   "RotationIndexes: { <step> ... }"      rotation amounts, each followed by one space ("{ }" when empty)
+//   "KeyDist: <int>"
+//   "BootstrapSlots: { <slots> ... }"
+// each ended by '\n'.  The reader takes exactly that: whitespace-separated tokens, one line per field in this
+// order, nothing after the sixth line.
+namespace {
+
+std::vector<std::string> split_ws(const std::string& line) {
+    std::vector<std::string> t;
+    size_t i = 0;
+    while (i < line.size()) {
+        while (i < line.size() && (line[i] == ' ' || line[i] == '\t' || line[i] == '\r')) i++;
+        size_t j = i;
+        while (j < line.size() && line[j] != ' ' && line[j] != '\t' && line[j] != '\r') j++;
+        if (j > i) t.push_back(line.substr(i, j - i));
+        i = j;
+    }
+    return t;
+}
+
+[[noreturn]] void dev_fail(int line, const std::string& why) {
+    throw std::invalid_argument("dev sidecar line " + std::to_string(line) + ": " + why);
+}
+
+int64_t dev_int(const std::string& tok, int line, int64_t lo, int64_t hi) {
+    size_t k = 0;
+    if (tok.empty()) dev_fail(line, "empty number");
+    if (tok[0] == '-' || tok[0] == '+') k = 1;
+    if (k == tok.size() || tok.size() > 12) dev_fail(line, "not an integer: '" + tok + "'");
+    for (size_t i = k; i < tok.size(); i++)
+        if (tok[i] < '0' || tok[i] > '9') dev_fail(line, "not an integer: '" + tok + "'");
+    const int64_t v = std::stoll(tok);
+    if (v < lo || v > hi) dev_fail(line, "out of range: " + tok);
+    return v;
+}
+
+// "{ a b ... }" starting at token i0 (the braces are tokens of their own); the tokens between them
+std::vector<std::string> dev_braced(const std::vector<std::string>& t, size_t i0, int line) {
+    if (t.size() < i0 + 2 || t[i0] != "{" || t.back() != "}") dev_fail(line, "expected '{ ... }'");
+    std::vector<std::string> inner(t.begin() + (long)i0 + 1, t.end() - 1);
+    for (auto& x : inner)
+        if (x == "{" || x == "}") dev_fail(line, "nested or stray brace");
+    return inner;
+}
+
+int32_t dev_flag(const std::string& line, const char* key, int n) {
+    const auto t = split_ws(line);
+    if (t.size() != 2 || t[0] != key) dev_fail(n, std::string("expected '") + key + " <int>'");
+    return (int32_t)dev_int(t[1], n, INT32_MIN, INT32_MAX);
+}
+
+uint32_t rot_index_n(int64_t k, uint32_t N) {
+    const uint64_t M = 2ull * N, ord = N / 2;  // 5 has order N/2 in (Z/2N)^*
+    int64_t e = k % (int64_t)ord;
+    if (e < 0) e += (int64_t)ord;
+    uint64_t r = 1, b = 5;
+    for (uint64_t x = (uint64_t)e; x; x >>= 1) {
+        if (x & 1) r = r * b % M;
+        b = b * b % M;
+    }
+    return (uint32_t)r;
+}
+
+}  // namespace
+
+DevSidecar read_dev_sidecar(const std::string& path) {
+    std::ifstream is(path, std::ios::binary);
+    if (!is.good()) throw std::invalid_argument("dev sidecar: cannot open " + path);
+    std::string text((std::istreambuf_iterator<char>(is)), std::istreambuf_iterator<char>());
+    if (text.size() > (1u << 20)) throw std::invalid_argument("dev sidecar: implausibly large");
+    std::vector<std::string> lines;
+    size_t a = 0;
+    while (a < text.size()) {
+        const size_t b = text.find('\n', a);
+        if (b == std::string::npos) dev_fail((int)lines.size() + 1, "no line end (truncated file)");
+        lines.push_back(text.substr(a, b - a));
+        a = b + 1;
+    }
+    if (lines.size() != 6) throw std::invalid_argument("dev sidecar: " + std::to_string(lines.size()) + " lines, not 6");
+    DevSidecar s;
+    {
+        const auto t = split_ws(lines[0]);
+        if (t.empty()) dev_fail(1, "expected '<n> { <device> ... }'");
+        const int64_t n = dev_int(t[0], 1, 1, 64);
+        const auto ids = dev_braced(t, 1, 1);
+        if ((int64_t)ids.size() != n) dev_fail(1, "device count does not match the list");
+        s.devices.clear();
+        for (auto& x : ids) s.devices.push_back((uint32_t)dev_int(x, 1, 0, 1023));
+    }
+    s.auto_load_ciphertexts = dev_flag(lines[1], "AutoLoadCiphertexts:", 2);
+    s.auto_load_plaintexts = dev_flag(lines[2], "AutoLoadPlaintexts:", 3);
+    {
+        const auto t = split_ws(lines[3]);
+        if (t.empty() || t[0] != "RotationIndexes:") dev_fail(4, "expected 'RotationIndexes: { ... }'");
+        for (auto& x : dev_braced(t, 1, 4)) s.rotations.push_back((int32_t)dev_int(x, 4, INT32_MIN + 1, INT32_MAX));
+    }
+    s.key_dist = dev_flag(lines[4], "KeyDist:", 5);
+    {
+        const auto t = split_ws(lines[5]);
+        if (t.empty() || t[0] != "BootstrapSlots:") dev_fail(6, "expected 'BootstrapSlots: { ... }'");
+        for (auto& x : dev_braced(t, 1, 6)) {
+            const int64_t v = dev_int(x, 6, 1, 1 << 30);
+            if (v & (v - 1)) dev_fail(6, "slot count not a power of two: " + x);
+            s.boot_slots.push_back((uint32_t)v);
+        }
+    }
+    return s;
+}
+
+std::string format_dev_sidecar(const DevSidecar& s) {
+    if (s.devices.empty()) throw std::invalid_argument("dev sidecar: no device");
+    std::string o = std::to_string(s.devices.size()) + " { ";
+    for (auto d : s.devices) o += std::to_string(d) + " ";
+    o += "}\nAutoLoadCiphertexts: " + std::to_string(s.auto_load_ciphertexts) + "\n";
+    o += "AutoLoadPlaintexts: " + std::to_string(s.auto_load_plaintexts) + "\n";
+    o += "RotationIndexes: { ";
+    for (auto r : s.rotations) o += std::to_string(r) + " ";
+    o += "}\nKeyDist: " + std::to_string(s.key_dist) + "\n";
+    o += "BootstrapSlots: { ";
+    for (auto b : s.boot_slots) {
+        if (b == 0 || (b & (b - 1))) throw std::invalid_argument("dev sidecar: slot count not a power of two");
+        o += std::to_string(b) + " ";
+    }
+    o += "}\n";
+    return o;
+}
+
+void write_dev_sidecar(const std::string& path, const DevSidecar& s) {
+    const std::string text = format_dev_sidecar(s);
+    std::ofstream os(path, std::ios::binary | std::ios::trunc);
+    if (!os.good()) throw std::invalid_argument("dev sidecar: cannot create " + path);
+    os.write(text.data(), (std::streamsize)text.size());
+    os.flush();
+    if (!os.good()) throw std::invalid_argument("dev sidecar: write failed: " + path);
+}
+
+std::vector<KeyLocation> resolve_rotation_keys(const std::vector<int32_t>& rotations,
+                                               const std::vector<std::string>& parts) {
+    if (parts.empty()) throw std::invalid_argument("rotation keys: no part files");
+    uint32_t N = 0;
+    std::vector<std::vector<uint32_t>> idx(parts.size());
+    for (size_t p = 0; p < parts.size(); p++) {
+        const SeededPartHeader h = read_seeded_part_header(parts[p]);
+        if (N && h.N != N) throw std::invalid_argument("rotation keys: parts of different ring dimensions");
+        N = h.N;
+        idx[p] = seeded_part_indices(parts[p]);
+    }
+    std::vector<KeyLocation> out;
+    out.reserve(rotations.size());
+    for (int32_t k : rotations) {
+        const uint32_t g = rot_index_n(k, N);
+        bool found = false;
+        for (size_t p = 0; p < parts.size() && !found; p++)
+            for (size_t r = 0; r < idx[p].size(); r++)
+                if (idx[p][r] == g) {
+                    out.push_back(KeyLocation{(uint32_t)p, (uint32_t)r, g});
+                    found = true;
+                    break;
+                }
+        if (!found)
+            throw std::invalid_argument("rotation keys: no key for rotation " + std::to_string(k) +
+                                        " (automorphism index " + std::to_string(g) + ") in the parts");
+    }
+    return out;
+}
+
+void load_rotation_keys(Context& ctx, const std::string& dev_path, const std::vector<std::string>& parts,
+                        uint64_t* const* d_evks, uint32_t n_keys) {
+    const DevSidecar s = read_dev_sidecar(dev_path);
+    if (s.rotations.size() != n_keys)
+        throw std::invalid_argument("rotation keys: the sidecar lists " + std::to_string(s.rotations.size()) +
+                                    " rotations, " + std::to_string(n_keys) + " key buffers given");
+    const std::vector<KeyLocation> loc = resolve_rotation_keys(s.rotations, parts);
+    for (uint32_t i = 0; i < n_keys; i++) {
+        uint32_t g = 0;
+        load_seeded_part_key(ctx, parts[loc[i].part], loc[i].record, &g, d_evks[i]);
+        if (g != loc[i].index) throw std::logic_error("rotation keys: record index changed under the loader");
+    }
 }
 
 }  // namespace fhe

@@ -352,6 +352,35 @@ int ckks_seeded_part_load_key(ckks_context* ctx, const char* path, uint32_t reco
 int ckks_seeded_part_write(ckks_context* ctx, const char* path, const char* key_tag, uint32_t n_keys,
                            const uint32_t* indices, const uint8_t* seeds, const uint64_t* const* d_evks);
 
+/* ---- the FIDESlib .dev sidecar (cryptocontext.bin.dev: written by the reference client's writeDevSidecar,
+ * hpc_gpu_port/mac_fhe_client.cpp:178-194; read by FIDESlib's LoadContext, which uploads the key of every listed
+ * rotation from the key map gpu_real_model.cu:1436-1529 fills) -----------------------------------------------------
+ * Six text lines: "1 { 0 }" (devices), "AutoLoadCiphertexts: 1", "AutoLoadPlaintexts: 0", "RotationIndexes: { ... }"
+ * (rotation AMOUNTS, EvalRotate steps), "KeyDist: 1", "BootstrapSlots: { ... }" (slot counts); no binary content.
+ * ckks_dev_sidecar_read       (host only) flags and counts into info, up to rot_cap rotation amounts and slot_cap
+ *                             slot counts in file order; a malformed file is CKKS_EINVAL naming the line and reason
+ * ckks_dev_sidecar_write      (host only) the reference writer's file: device 0, AutoLoadCiphertexts 1,
+ *                             AutoLoadPlaintexts 0, KeyDist 1, the rotation amounts and slot counts as given
+ * ckks_rotation_keys_resolve  (host only) for each rotation the sidecar lists (in its order): the part file (index
+ *                             into part_paths), the record and the automorphism index 5^k mod 2N of its key; a
+ *                             rotation whose key no part holds is CKKS_EINVAL (FIDESlib aborts on it: map::at)
+ * ckks_rotation_keys_load     LoadContext's rotation keys: the key of each listed rotation, from the parts, into
+ *                             d_evks[i] [dnum][2][L+K][N]; n_keys must be the sidecar's rotation count */
+typedef struct ckks_dev_sidecar {
+    uint32_t n_devices;
+    uint32_t devices[64];
+    int32_t auto_load_ciphertexts, auto_load_plaintexts, key_dist;
+    uint32_t n_rotations, n_boot_slots;
+} ckks_dev_sidecar;
+int ckks_dev_sidecar_read(const char* path, ckks_dev_sidecar* info, int32_t* rotations, uint32_t rot_cap,
+                          uint32_t* boot_slots, uint32_t slot_cap);
+int ckks_dev_sidecar_write(const char* path, const int32_t* rotations, uint32_t n_rotations, const uint32_t* boot_slots,
+                           uint32_t n_boot_slots);
+int ckks_rotation_keys_resolve(const char* dev_path, const char* const* part_paths, uint32_t n_parts,
+                               uint32_t* part_of, uint32_t* record_of, uint32_t* index_of, uint32_t cap, uint32_t* n);
+int ckks_rotation_keys_load(ckks_context* ctx, const char* dev_path, const char* const* part_paths, uint32_t n_parts,
+                            uint64_t* const* d_evks, uint32_t n_keys);
+
 /* ---- ciphertext files (the payload of the serve-directory protocol's req.N.t / resp.N.t; the reference serializes
  * OpenFHE-cereal ciphertexts there, hpc_gpu_port/gpu_real_model.cu:2303-2324, a format only OpenFHE reads) ------
  * Layout (little-endian): char[8] "FSSMCTX1"; u32 version = 1; u32 N; u32 level; u32 n_polys = 2; f64 scale;

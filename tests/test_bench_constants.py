@@ -128,3 +128,30 @@ def test_step_roofline_fields():
     assert r["achievable"] == bench.STREAM_COPY_GBS
     assert r["traffic"] == bench.MEASURED[("hmult", "step")]["traffic"]
     assert 2.0 < r["traffic_over_algorithmic"] < 4.0
+
+
+def step_total(path):
+    """(read GB, write GB) of the '**step total**' row of a profile's counter table"""
+    for line in open(path):
+        cells = [c.strip().strip("*") for c in line.strip().strip("|").split("|")]
+        if cells and cells[0] == "step total":
+            return float(cells[3]), float(cells[4])
+    raise AssertionError(f"no step total row in {path}")
+
+
+def test_pcmm_and_bootstrap_step_traffic_match_their_profiles():
+    sys.path.insert(0, REPO)
+    import bench
+    for workload, name in (("pcmm", "pcmm_config3_kernel_trace.md"), ("bootstrap", "bootstrap_config4_kernel_trace.md")):
+        path = os.path.join(REPO, "profiles", name)
+        r, w = step_total(path)
+        meas = bench.MEASURED[(workload, "step")]
+        assert meas["source"] == "profiles/" + name
+        assert abs(meas["traffic"] - (r + w) * 1e9) / meas["traffic"] < 0.002, workload
+    # the PCMM MAC row: read + write of its one dispatch
+    rows = {}
+    for line in open(os.path.join(REPO, "profiles", "pcmm_config3_kernel_trace.md")):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 5 and cells[0] == "k_bsgs_mac" and re.fullmatch(r"[0-9.]+", cells[3]):
+            rows["mac"] = float(cells[3]) + float(cells[4])
+    assert abs(bench.MEASURED[("pcmm", "bsgs_mac")]["traffic"] - rows["mac"] * 1e9) < 2e6

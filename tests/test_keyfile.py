@@ -224,3 +224,43 @@ def test_ct_save_matches_layout_and_reloads(tmp_path, ckks, ctx):
     p3 = _write(tmp_path, "oc.bin", ct_bytes(N, lv, 2.0 ** 45, other, w))
     with pytest.raises(ckks.CkksError):
         ctx.ct_load(p3, back.ptr, ctx.L)
+
+
+@pytest.mark.gpu
+def test_rotation_keys_load_follows_the_dev_sidecar(tmp_path, ckks, ctx):
+    """LoadContext's rotation keys (gpu_real_model.cu:1436-1529, FIDESlib's upload of the key of each rotation the
+    .dev sidecar lists): keys generated on the device and written into two seeded parts; the sidecar lists a subset
+    of their rotations, out of order, one of them as the other sign of a half-slot rotation; each loaded buffer holds
+    its rotation's key word for word; a rotation with no key in the parts is refused"""
+    T, D = ctx.L + ctx.K, ctx.dnum
+    sk = ctx.secret(b"R" * 32, 64)
+    steps = [1, 2, -3, 7, N // 4]
+    words = {}
+    parts = []
+    for p, chunk in enumerate((steps[:3], steps[3:])):
+        gs, seeds, bufs = [], [], []
+        for i, s in enumerate(chunk):
+            g = ckks.rotation_index(s)
+            seed = bytes([60 + 10 * p + i]) * 32
+            k = ckks.DeviceBuffer(D * 2 * T * N * 8)
+            ctx.keygen_automorphism(sk, g, seed, bytes([90 + 10 * p + i]) * 32, k.ptr)
+            gs.append(g)
+            seeds.append(seed)
+            bufs.append(k)
+            words[s] = k.download((D, 2, T, N))
+        path = str(tmp_path / f"evalrot.part{p:03d}.seeded.bin")
+        ctx.seeded_part_write(path, "rot", gs, seeds, [b.ptr for b in bufs])
+        parts.append(path)
+    listed = [7, -3, -(N // 4), 1]
+    dev = str(tmp_path / "cryptocontext.bin.dev")
+    ckks.dev_sidecar_write(dev, listed, [N // 2])
+    out = [ckks.DeviceBuffer(D * 2 * T * N * 8) for _ in listed]
+    ctx.rotation_keys_load(dev, parts, [b.ptr for b in out])
+    for s, b in zip(listed, out):
+        want = words[s if s in words else -s]
+        assert np.array_equal(b.download((D, 2, T, N)), want), s
+    with pytest.raises(ckks.CkksError, match="buffers"):
+        ctx.rotation_keys_load(dev, parts, [b.ptr for b in out[:2]])
+    ckks.dev_sidecar_write(dev, [1, 5], [])
+    with pytest.raises(ckks.CkksError, match="no key for rotation 5"):
+        ctx.rotation_keys_load(dev, parts, [b.ptr for b in out[:2]])
