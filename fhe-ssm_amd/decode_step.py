@@ -20,7 +20,8 @@ relative error ~(2 pi m / q0)^2 / 6), and the increments are ~5-100x smaller tha
 has its own bootstrapping plan whose input scale suits its magnitude (more signal over EvalMod's noise).
 The carried WKV state is bootstrapped once per layer: its 64 diagonal ciphertexts are packed 4 -> 3 into the
 lanes' unused channels (768..1023), the 48 packed two per complex ciphertext, and unpacked with one conjugation
-and three masked rotations.  26 bootstraps per layer.
+and three masked rotations.  The WKV readout y and the per-head bonus coefficient are bootstrapped together
+mid-mix: the per-head GroupNorm of y needs more levels than the scan leaves.  28 bootstraps per layer.
 """
 from __future__ import annotations
 
@@ -156,44 +157,89 @@ class DecodeStep:
         self.stats["bootstraps"] += x.B
         return self.be.bootstrap(x, kind)
 
-    def _time_mix(self, li, x, st):
-        """the time-mix increment o (x + o is the layer's residual)"""
+    def _head_sum(self, x, scale):
+        """every head's sum of x (times scale), broadcast over the head's 64 channels: rotate-and-add by 1 .. 32
+        (slot h*64 of a lane then holds head h's sum), mask the head starts (times scale), broadcast back"""
+        be = self.be
+        s = x
+        for k in M.HEAD_UP:
+            s = be.add(s, be.rotate(s, k))
+        s = be.mul_pt(s, self._vec_pt(f"head_start{scale!r}", s.level, M.head_start_mask(scale)))
+        for k in M.HEAD_DOWN:
+            s = be.add(s, be.rotate(s, k))
+        return s
+
+    def _time_mix(self, li, x, st, v0):
+        """the time-mix increment o (x + o is the layer's residual) and the first layer's value v0 (the value
+        residual of the later layers mixes toward it)"""
         be, L = self.be, self.W["layers"][li]
         xn = self._norm(x, L["p_n1"], "n1")
         xp = st["xp_t"]
         lv = min(xn.level, xp.level)
+        first = v0 is None
 
         def tm_blocks():
-            out = []
-            for m in M.MIX_NAMES:
-                Wm = L["W_" + m]
-                out.append([Wm * (L["g1"] * (1 - L["mu_" + m]))[None, :], Wm * (L["g1"] * L["mu_" + m])[None, :]])
+            def mix(Wm, mu):
+                return [Wm * (L["g1"] * (1 - mu))[None, :], Wm * (L["g1"] * mu)[None, :]]
+            out = [mix(L["W_" + m], L["mu_" + m]) for m in M.MIX_NAMES]
+            out.append(mix(L["W_k"] * L["k_k"][:, None], L["mu_k"]))      # kk = k_k (.) k
+            if not first:
+                out.append(mix(L["W_vg"], L["mu_v"]))                    # the value gate's argument
             return out
 
         proj = be.matvec([be.at(xn, lv), be.at(xp, lv)], self._mv_pt(f"tm{li}", lv, tm_blocks))
-        r, k, v, zw, za, zg = (be.item(proj, i) for i in range(6))
+        r, k, v, zw, za, zg, kk = (be.item(proj, i) for i in range(7))
         w = be.poly3(zw, L["p_w"])
         a = be.poly3(za, L["p_a"])
         g = be.poly3(zg, L["p_g"])
+        if first:
+            v0 = v
+        else:  # value residual: v + (v0 - v) p_v(W_vg u_v)
+            gate = be.poly3(be.item(proj, 7), L["p_v"])
+            v = be.add(v, be.mul(be.add(v0, v, -1), gate))
+        # the per-head L2 norm of kk enters only the removal term, as its square:
+        # (S kh)(kh a)^T = n^2 (S kk)(kk a)^T with kh = n kk, n = p_kn(|kk_h|^2)
+        nk = be.poly3(self._head_sum(be.mul(kk, kk), 1.0), L["p_kn"])
+        n2 = be.mul(nk, nk)
         masks = M.wkv_masks()
-        masks_eta = M.wkv_masks(L["eta"])
-        KK = be.rotate_masked(k, self._vec_pt(f"mask_k{li}", k.level, np.concatenate([masks, masks_eta])), 2)
-        K_t, Kh_t = be.slice(KK, 0, 64), be.slice(KK, 64, 128)
+        # k's masked rotations: rot64_t(kk) = rot64_t(k) k_k, and the key update k' = k (1 - k_a) + (k a) k_a
+        KX = be.rotate_masked(k, self._vec_pt(f"mask_k{li}", k.level, np.concatenate(
+            [M.wkv_masks(L["k_k"]), M.wkv_masks(1 - L["k_a"])])), 2)
+        KK_t, K1_t = be.slice(KX, 0, 64), be.slice(KX, 64, 128)
+        ka = be.mul(k, a)
+        KB = be.rotate_masked(ka, self._vec_pt(f"mask_ka{li}", ka.level, np.concatenate(
+            [M.wkv_masks(L["k_k"]), M.wkv_masks(L["k_a"])])), 2)
+        B_t, K2_t = be.slice(KB, 0, 64), be.slice(KB, 64, 128)
         R_t = be.rotate_masked(r, self._vec_pt("mask", r.level, masks), 1)
         W_t = be.rotate_masked(w, self._vec_pt("mask", w.level, masks), 1)
-        ka = be.mul(k, a)
-        B_t = be.rotate_masked(ka, self._vec_pt(f"mask_eta{li}", ka.level, masks_eta), 1)
         D = st["D"]  # (batch, index) of D_t
         T = M.WKV_T
-        sa = be.mult_sum([[(D[t][0], D[t][1], Kh_t, t) for t in range(T)]])
-        nsa = be.at_neg(sa, min(B_t.level, W_t.level - 1, sa.level - 1))
-        Dn = be.mult_sum([[(D[t][0], D[t][1], W_t, t), (nsa, 0, B_t, t), (v, 0, K_t, t)] for t in range(T)])
+        sa = be.mult_sum([[(D[t][0], D[t][1], KK_t, t) for t in range(T)]])
+        nsa = be.mul(be.at_neg(sa, n2.level), n2)
+        Dn = be.mult_sum([[(D[t][0], D[t][1], W_t, t), (nsa, 0, B_t, t), (v, 0, K1_t, t), (v, 0, K2_t, t)]
+                          for t in range(T)])
         y = be.mult_sum([[(Dn, t, R_t, t) for t in range(T)]])
-        yg = be.mul(y, g)
+        # the bonus coefficient per head: sum of r k' r_k = (r k) (1 - k_a) r_k + (r ka) k_a r_k
+        rk = be.add(be.mul_pt(be.mul(r, k), self._vec_pt(f"rk1_{li}", r.level - 1, M.periodic((1 - L["k_a"]) * L["r_k"]))),
+                    be.mul_pt(be.mul(r, ka), self._vec_pt(f"rk2_{li}", ka.level - 1, M.periodic(L["k_a"] * L["r_k"]))))
+        sb = self._head_sum(rk, 1.0)
+        # y and the bonus coefficient are bootstrapped together (GroupNorm needs more levels than are left)
+        m = min(y.level, sb.level)
+        yb = self._boot(be.concat([be.at(y, m), be.at(sb, m)]), "state")
+        Y, SB = be.item(yb, 0), be.item(yb, 1)
+        # GroupNorm per head: mean and mean of squares from one batch of rotations, var = E[y^2] - mean^2
+        mom = self._head_sum(be.concat([be.at(Y, Y.level - 1), be.mul(Y, Y)]), 1.0 / M.HS)
+        mu, ey2 = be.item(mom, 0), be.item(mom, 1)
+        var = be.add(ey2, be.mul(mu, mu), -1)
+        yn = be.mul(be.add(Y, mu, -1), be.poly3(var, L["p_gn"]))
+        yl = be.mul_pt(yn, self._vec_pt(f"ln_w{li}", yn.level, M.periodic(L["ln_w"])))
+        y3 = be.add(yl, be.mul(SB, v))
+        # (y3 + ln_b) g: ln_b enters as ln_b (.) g
+        yg = be.add(be.mul(y3, g), be.mul_pt(g, self._vec_pt(f"ln_b{li}", g.level, M.periodic(L["ln_b"]))))
         o = be.matvec([yg], self._mv_pt(f"wo{li}", yg.level, lambda: [[L["W_o"]]]))
         st["xp_t"] = xn
         st["Dn"] = Dn
-        return o
+        return o, v0
 
     def _channel_mix(self, li, x, st):
         """the channel-mix increment f"""
@@ -265,9 +311,11 @@ class DecodeStep:
         if self.state is None:
             self.state = self.cold_state()
         be = self.be
+        v0 = None
         for li in range(self.n_layers):
             st = self.state[li]
-            x = be.add(x, self._boot(self._time_mix(li, x, st), "inc_tm"))
+            o, v0 = self._time_mix(li, x, st, v0)
+            x = be.add(x, self._boot(o, "inc_tm"))
             self._refresh_state(st)
             x = be.add(x, self._boot(self._channel_mix(li, x, st), "inc_cm"))
         xo = self._norm(x, self.W["p_o"], "out")
@@ -378,11 +426,12 @@ class HEBackend(Backend):
         return HECt(a.buf, i1 - i0, a.level, a.scale, off=a.off + i0 * 2 * a.level * self.N * 8, base=a)
 
     def concat(self, parts):
+        """the parts side by side in one batch (same level; scales equal to 1e-9, the rule add() applies)"""
         lv, sc = parts[0].level, parts[0].scale
         out = self._new(sum(p.B for p in parts), lv, sc)
         o = 0
         for p in parts:
-            assert p.level == lv and p.scale == sc
+            assert p.level == lv and abs(p.scale / sc - 1.0) < 1e-9
             self.ctx.eval_lincomb(p.B, [p.ptr()], [lv], [1.0], None, sc, 0.0, lv, True, out.ptr(o))
             o += p.B
         return out

@@ -267,7 +267,9 @@ class Engine {
         Ct out = fresh(B, lv, sc);
         uint32_t o = 0;
         for (auto& p : parts) {
-            if (p.level != lv || p.scale != sc) throw Error(CKKS_EINVAL, "concat of unlike ciphertexts");
+            // same level; scales equal to 1e-9 (the rule add() applies)
+            if (p.level != lv || std::fabs(p.scale / sc - 1.0) > 1e-9)
+                throw Error(CKKS_EINVAL, "concat of unlike ciphertexts");
             Ct dst = slice(out, o, o + p.B);
             lincomb(p.B, {&p}, {1.0}, false, sc, 0.0, lv, true, dst);
             o += p.B;
@@ -661,11 +663,12 @@ struct LayerW {
 
 size_t weight_count(const std::string& n) {
     static const std::map<std::string, size_t> sizes = {
-        {"g1", D},     {"g2", D},     {"eta", D},    {"mu_r", D},       {"mu_k", D},       {"mu_v", D},
+        {"g1", D},     {"g2", D},     {"k_k", D},    {"mu_r", D},       {"mu_k", D},       {"mu_v", D},
         {"mu_w", D},   {"mu_a", D},   {"mu_g", D},   {"mu_c", D},       {"W_r", D * D},    {"W_k", D * D},
         {"W_v", D * D}, {"W_w", D * D}, {"W_a", D * D}, {"W_g", D * D}, {"W_o", D * D},    {"W_ck", FF * D},
         {"W_cv", D * FF}, {"p_n1", 4}, {"p_n2", 4},   {"p_w", 4},        {"p_a", 4},        {"p_g", 4},
-        {"p_h", 4}};
+        {"p_h", 4},    {"W_vg", D * D}, {"k_a", D},   {"r_k", D},        {"ln_w", D},       {"ln_b", D},
+        {"p_v", 4},    {"p_kn", 4},   {"p_gn", 4}};
     auto it = sizes.find(n);
     return it == sizes.end() ? 0 : it->second;
 }
@@ -723,9 +726,10 @@ class Decoder {
         try {
             std::vector<LayerState> work = state_.empty() ? cold_state() : state_;
             Ct x = x_in;
+            Ct v0;  // the first layer's value (the later layers' value residual mixes toward it)
             for (uint32_t li = 0; li < layers_.size(); li++) {
                 LayerState& st = work[li];
-                x = be_->add(x, boot(time_mix(li, x, st), "inc_tm"));
+                x = be_->add(x, boot(time_mix(li, x, st, v0), "inc_tm"));
                 refresh_state(st);
                 x = be_->add(x, boot(channel_mix(li, x, st), "inc_cm"));
                 release_layer(li);
@@ -846,61 +850,149 @@ class Decoder {
         return be_->mul(x, n);
     }
 
-    Ct time_mix(uint32_t li, const Ct& x, LayerState& st) {
+    // every head's sum of x (times scale), broadcast over the head's 64 channels: rotate-and-add by 1 .. 32 (slot
+    // h*64 of a lane then holds head h's sum), mask the head starts (times scale), broadcast back
+    Ct head_sum(const Ct& x, double scale) {
+        Ct s = x;
+        for (int k = 0; k < 6; k++) s = be_->add(s, be_->rotate(s, 1 << k));
+        char tag[48];
+        std::snprintf(tag, sizeof(tag), "head_start%.17g", scale);
+        s = be_->mul_pt(s, *vec_pt(tag, s.level, [scale] {
+            std::vector<double> m(DPAD, 0.0);
+            for (int c = 0; c < D; c += HS) m[c] = scale;
+            return m;
+        }));
+        for (int k = 0; k < 6; k++) s = be_->add(s, be_->rotate(s, -(1 << k)));
+        return s;
+    }
+
+    static std::vector<double> periodic_of(const std::vector<double>& v) {
+        std::vector<double> p(DPAD, 0.0);
+        std::copy(v.begin(), v.end(), p.begin());
+        return p;
+    }
+
+    // the time-mix increment o; v0: the first layer's value (set by layer 0, read by the later layers)
+    Ct time_mix(uint32_t li, const Ct& x, LayerState& st, Ct& v0) {
         const LayerW& L = layers_[li];
+        const std::string tag = std::to_string(li);
+        const bool first = li == 0;
         Ct xn = norm(x, L["p_n1"]);
         const uint32_t lv = std::min(xn.level, st.xp_t.level);
         static const char* mix[6] = {"r", "k", "v", "w", "a", "g"};
-        const Matvec& tm = mv_pt("tm" + std::to_string(li), lv, [&] {
+        const Matvec& tm = mv_pt("tm" + tag, lv, [&] {
             std::vector<std::vector<Block>> out;
-            for (auto* m : mix) {
-                const auto& W = L[std::string("W_") + m];
-                const auto& mu = L[std::string("mu_") + m];
-                const auto& g1 = L["g1"];
+            const auto& g1 = L["g1"];
+            // the token-shift pair of one projection: row scale rs (or none) times W, columns times g1 (1 - mu), g1 mu
+            auto add = [&](const std::vector<double>& W, const std::vector<double>& mu, const std::vector<double>* rs) {
                 auto a = std::make_shared<std::vector<double>>(D), b = std::make_shared<std::vector<double>>(D);
                 for (int c = 0; c < D; c++) {
                     (*a)[c] = g1[c] * (1.0 - mu[c]);
                     (*b)[c] = g1[c] * mu[c];
                 }
                 const double* w = W.data();
-                out.push_back({[w, a](int r, int c) { return w[(size_t)r * D + c] * (*a)[c]; },
-                               [w, b](int r, int c) { return w[(size_t)r * D + c] * (*b)[c]; }});
-            }
+                const double* r = rs ? rs->data() : nullptr;
+                out.push_back({[w, a, r](int i, int c) { return (r ? r[i] : 1.0) * w[(size_t)i * D + c] * (*a)[c]; },
+                               [w, b, r](int i, int c) { return (r ? r[i] : 1.0) * w[(size_t)i * D + c] * (*b)[c]; }});
+            };
+            for (auto* m : mix) add(L[std::string("W_") + m], L[std::string("mu_") + m], nullptr);
+            add(L["W_k"], L["mu_k"], &L["k_k"]);       // kk = k_k (.) k
+            if (!first) add(L["W_vg"], L["mu_v"], nullptr);  // the value gate's argument
             return out;
         });
         Ct proj = be_->matvec({be_->at(xn, lv), be_->at(st.xp_t, lv)}, tm);
-        Ct r = be_->item(proj, 0), k = be_->item(proj, 1), v = be_->item(proj, 2);
+        Ct r = be_->item(proj, 0), k = be_->item(proj, 1), v = be_->item(proj, 2), kk = be_->item(proj, 6);
         Ct w = be_->poly3(be_->item(proj, 3), L["p_w"]);
         Ct a = be_->poly3(be_->item(proj, 4), L["p_a"]);
         Ct g = be_->poly3(be_->item(proj, 5), L["p_g"]);
-        const double* eta = L["eta"].data();
-        auto masks = [] { return wkv_masks(nullptr); };
-        auto masks_eta = [eta] { return wkv_masks(eta); };
-        Ct KK = be_->rotate_masked(k, *vec_pt("mask_k" + std::to_string(li), k.level, [&] {
-            auto m = masks(), e = masks_eta();
-            m.insert(m.end(), e.begin(), e.end());
+        if (first) {
+            v0 = v;
+        } else {  // value residual: v + (v0 - v) p_v(W_vg u_v)
+            Ct gate = be_->poly3(be_->item(proj, 7), L["p_v"]);
+            Ct dv = be_->add(v0, v, -1);
+            Ct mix_v = be_->mul(dv, gate);
+            v = be_->add(v, mix_v);
+        }
+        // the per-head L2 norm of kk enters only the removal term, as its square:
+        // (S kh)(kh a)^T = n^2 (S kk)(kk a)^T with kh = n kk, n = p_kn(|kk_h|^2)
+        Ct kk2 = be_->mul(kk, kk);
+        Ct zk = head_sum(kk2, 1.0);
+        Ct nk = be_->poly3(zk, L["p_kn"]);
+        Ct n2 = be_->mul(nk, nk);
+        const std::vector<double>& kkw = L["k_k"];
+        const std::vector<double>& kaw = L["k_a"];
+        std::vector<double> one_minus_ka(D);
+        for (int c = 0; c < D; c++) one_minus_ka[c] = 1.0 - kaw[c];
+        auto masks2 = [](const double* e1, const double* e2) {
+            auto m = wkv_masks(e1), m2 = wkv_masks(e2);
+            m.insert(m.end(), m2.begin(), m2.end());
             return m;
-        }), 2);
-        Ct K_t = be_->slice(KK, 0, WKV_T), Kh_t = be_->slice(KK, WKV_T, 2 * WKV_T);
+        };
+        // k's masked rotations: rot64_t(kk) = rot64_t(k) k_k, and the key update k' = k (1 - k_a) + (k a) k_a
+        Ct KX = be_->rotate_masked(k, *vec_pt("mask_k" + tag, k.level,
+                                               [&] { return masks2(kkw.data(), one_minus_ka.data()); }), 2);
+        Ct KK_t = be_->slice(KX, 0, WKV_T), K1_t = be_->slice(KX, WKV_T, 2 * WKV_T);
+        Ct ka = be_->mul(k, a);
+        Ct KB = be_->rotate_masked(ka, *vec_pt("mask_ka" + tag, ka.level,
+                                                [&] { return masks2(kkw.data(), kaw.data()); }), 2);
+        Ct B_t = be_->slice(KB, 0, WKV_T), K2_t = be_->slice(KB, WKV_T, 2 * WKV_T);
+        auto masks = [] { return wkv_masks(nullptr); };
         Ct R_t = be_->rotate_masked(r, *vec_pt("mask", r.level, masks), 1);
         Ct W_t = be_->rotate_masked(w, *vec_pt("mask", w.level, masks), 1);
-        Ct ka = be_->mul(k, a);
-        Ct B_t = be_->rotate_masked(ka, *vec_pt("mask_eta" + std::to_string(li), ka.level, masks_eta), 1);
         auto Dt = [&](uint32_t t) { return &st.Dseg[st.Didx[t].first]; };
         std::vector<std::vector<Pair>> p1(1);
-        for (uint32_t t = 0; t < WKV_T; t++) p1[0].push_back(Pair{Dt(t), st.Didx[t].second, &Kh_t, t});
+        for (uint32_t t = 0; t < WKV_T; t++) p1[0].push_back(Pair{Dt(t), st.Didx[t].second, &KK_t, t});
         Ct sa = be_->mult_sum(p1);
-        Ct nsa = be_->at_neg(sa, std::min({B_t.level, W_t.level - 1, sa.level - 1}));
+        Ct nsa0 = be_->at_neg(sa, n2.level);
+        Ct nsa = be_->mul(nsa0, n2);
         std::vector<std::vector<Pair>> p2(WKV_T);
         for (uint32_t t = 0; t < WKV_T; t++)
-            p2[t] = {Pair{Dt(t), st.Didx[t].second, &W_t, t}, Pair{&nsa, 0, &B_t, t}, Pair{&v, 0, &K_t, t}};
+            p2[t] = {Pair{Dt(t), st.Didx[t].second, &W_t, t}, Pair{&nsa, 0, &B_t, t}, Pair{&v, 0, &K1_t, t},
+                     Pair{&v, 0, &K2_t, t}};
         Ct Dn = be_->mult_sum(p2);
         std::vector<std::vector<Pair>> p3(1);
         for (uint32_t t = 0; t < WKV_T; t++) p3[0].push_back(Pair{&Dn, t, &R_t, t});
         Ct y = be_->mult_sum(p3);
-        Ct yg = be_->mul(y, g);
+        // the bonus coefficient per head: sum of r k' r_k = (r k) (1 - k_a) r_k + (r ka) k_a r_k
+        const std::vector<double>& rkw = L["r_k"];
+        Ct rk1p = be_->mul(r, k);
+        Ct rk1 = be_->mul_pt(rk1p, *vec_pt("rk1_" + tag, rk1p.level, [&] {
+            std::vector<double> m(DPAD, 0.0);
+            for (int c = 0; c < D; c++) m[c] = (1.0 - kaw[c]) * rkw[c];
+            return m;
+        }));
+        Ct rk2p = be_->mul(r, ka);
+        Ct rk2 = be_->mul_pt(rk2p, *vec_pt("rk2_" + tag, rk2p.level, [&] {
+            std::vector<double> m(DPAD, 0.0);
+            for (int c = 0; c < D; c++) m[c] = kaw[c] * rkw[c];
+            return m;
+        }));
+        Ct rk = be_->add(rk1, rk2);
+        Ct sb = head_sum(rk, 1.0);
+        // y and the bonus coefficient are bootstrapped together (GroupNorm needs more levels than are left)
+        const uint32_t m = std::min(y.level, sb.level);
+        Ct ya = be_->at(y, m), sba = be_->at(sb, m);
+        Ct yb = boot(be_->concat({ya, sba}), "state");
+        Ct Y = be_->item(yb, 0), SB = be_->item(yb, 1);
+        // GroupNorm per head: mean and mean of squares from one batch of rotations, var = E[y^2] - mean^2
+        Ct Ylow = be_->at(Y, Y.level - 1);
+        Ct Y2 = be_->mul(Y, Y);
+        Ct mom = head_sum(be_->concat({Ylow, Y2}), 1.0 / HS);
+        Ct mu = be_->item(mom, 0), ey2 = be_->item(mom, 1);
+        Ct mu2 = be_->mul(mu, mu);
+        Ct var = be_->add(ey2, mu2, -1);
+        Ct yc = be_->add(Y, mu, -1);
+        Ct pg = be_->poly3(var, L["p_gn"]);
+        Ct yn = be_->mul(yc, pg);
+        Ct yl = be_->mul_pt(yn, *vec_pt("ln_w" + tag, yn.level, [&] { return periodic_of(L["ln_w"]); }));
+        Ct bon = be_->mul(SB, v);
+        Ct y3 = be_->add(yl, bon);
+        // (y3 + ln_b) g: ln_b enters as ln_b (.) g
+        Ct y3g = be_->mul(y3, g);
+        Ct bg = be_->mul_pt(g, *vec_pt("ln_b" + tag, g.level, [&] { return periodic_of(L["ln_b"]); }));
+        Ct yg = be_->add(y3g, bg);
         const double* wo = L["W_o"].data();
-        Ct o = be_->matvec({yg}, mv_pt("wo" + std::to_string(li), yg.level, [wo] {
+        Ct o = be_->matvec({yg}, mv_pt("wo" + tag, yg.level, [wo] {
             return std::vector<std::vector<Block>>{{[wo](int r, int c) { return wo[(size_t)r * D + c]; }}};
         }));
         st.xp_t = xn;

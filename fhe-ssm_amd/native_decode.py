@@ -62,8 +62,9 @@ SIGNATURES = {
     "fhe_ssm_client_decrypt_logits": (_int, [_vp, _vp, ctypes.c_char_p, _vp, _u32, _u32, _u32]),
 }
 
-LAYER_WEIGHTS = ("g1", "g2", "eta", "mu_r", "mu_k", "mu_v", "mu_w", "mu_a", "mu_g", "mu_c", "W_r", "W_k", "W_v",
-                 "W_w", "W_a", "W_g", "W_o", "W_ck", "W_cv", "p_n1", "p_n2", "p_w", "p_a", "p_g", "p_h")
+LAYER_WEIGHTS = ("g1", "g2", "k_k", "mu_r", "mu_k", "mu_v", "mu_w", "mu_a", "mu_g", "mu_c", "W_r", "W_k", "W_v",
+                 "W_w", "W_a", "W_g", "W_o", "W_ck", "W_cv", "p_n1", "p_n2", "p_w", "p_a", "p_g", "p_h",
+                 "W_vg", "k_a", "r_k", "ln_w", "ln_b", "p_v", "p_kn", "p_gn")
 MODEL_WEIGHTS = ("g_o", "p_o")
 
 _lib = None

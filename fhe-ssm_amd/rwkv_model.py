@@ -10,17 +10,22 @@ R^{64x64} per head, xp_t, xp_c in R^768):
                 u_m = g1 (1 - mu_m) xn + g1 mu_m xp_t,  m in {r, k, v, w, a, g}      (token shift)
                 r, k, v = W_r u_r, W_k u_k, W_v u_v
                 w, a, g = p_w(W_w u_w), p_a(W_a u_a), p_g(W_g u_g)    (decay, in-context rate, gate)
-                kh = k eta                                            (key used for removal)
+                v <- v + (v0 - v) p_v(W_vg u_v)   in layers > 0, v0 = layer 0's v      (value residual)
+                kk = k k_k;  k <- k (1 + (a - 1) k_a)                  (removal key, key update)
+                kh_h = kk_h p_kn(|kk_h|^2)                             (per-head L2 norm: 1/|kk| -> p_kn)
                 S_h <- S_h diag(w_h) - (S_h kh_h)(kh_h a_h)^T + v_h k_h^T    (WKV-7 state update)
-                y_h = S_h r_h;  x <- x + W_o (y g);  xp_t <- xn
+                y_h = S_h r_h
+                y_h <- (y_h - mean(y_h)) p_gn(var(y_h)) ln_w_h + ln_b_h   (per-head GroupNorm: rsqrt -> p_gn)
+                y_h <- y_h + (sum_i r_i k_i r_k,i)_h v_h                (bonus)
+                x <- x + W_o (y g);  xp_t <- xn
   channel mix   xn2 = x p_n2(mean(x^2));  u = g2 (1 - mu_c) xn2 + g2 mu_c xp_c
                 x <- x + W_cv p_h(W_ck u);  xp_c <- xn2
   output        xo = g_o x p_o(mean(x^2));  logits = W_head xo     (the head runs on the client)
 
-RWKV-7's LoRA pairs for w, a, g are dense 768 x 768 maps here, and its per-head L2 normalisation of kh
-and GroupNorm of y are left out (they would add two more per-head polynomial norms).  The recurrence is
-the reference model's WKV-7 step; the reference's served FHE driver (gpu_real_model.cu:4674-5300) runs
-the same sequence of norms, token shift, projections, scan, gate, output projection and channel mix.
+This is RWKV-7's time mixing step for step (results/vector-d-20261104/raw/rwkv_v7_numpy.py:13-44); its LoRA pairs
+for w, a, g and the value gate are dense 768 x 768 maps here, its sigmoid/exp/tanh and the norms' inverse square
+roots degree-3 polynomials.  The reference's served FHE driver (gpu_real_model.cu:4674-5300) runs the same sequence
+of norms, token shift, projections, scan, gate, output projection and channel mix.
 
 Slot layout (lane-major, gpu_real_model.cu:483-519): slot lane * 1024 + c holds channel c < 768 of lane
 lane; channels 768..1023 are zero.  Every plaintext that is the same for all lanes is 1024-periodic and
@@ -65,10 +70,19 @@ def make_weights(seed: int = 5, n_layers: int = N_LAYERS, vocab: int = VOCAB) ->
         for m in ("w", "a", "g"):
             L["W_" + m] = 0.5 * rng.standard_normal((D, D)) / np.sqrt(D)
         L["W_o"] = 0.5 * rng.standard_normal((D, D)) / np.sqrt(D)
-        L["eta"] = rng.uniform(0.05, 0.15, D)
+        L["k_k"] = rng.uniform(0.05, 0.15, D)
         L["W_ck"] = 0.5 * rng.standard_normal((FF, D)) / np.sqrt(D)
         L["W_cv"] = 0.5 * rng.standard_normal((D, FF)) / np.sqrt(FF)
         for p in ("p_n1", "p_n2", "p_w", "p_a", "p_g", "p_h"):
+            L[p] = _poly_coeffs(rng)
+        # the rest of RWKV-7's time mixing: the value gate (a dense map, like w, a, g), the key update, the per-head
+        # L2 norm of kk, the per-head GroupNorm of y and the bonus term
+        L["W_vg"] = 0.5 * rng.standard_normal((D, D)) / np.sqrt(D)
+        L["k_a"] = rng.uniform(0.0, 0.5, D)
+        L["r_k"] = 0.05 * rng.standard_normal(D)
+        L["ln_w"] = 1.0 + 0.1 * rng.standard_normal(D)
+        L["ln_b"] = 0.02 * rng.standard_normal(D)
+        for p in ("p_v", "p_kn", "p_gn"):
             L[p] = _poly_coeffs(rng)
         layers.append(L)
     out = {"layers": layers, "g_o": 1.0 + 0.1 * rng.standard_normal(D), "p_o": _poly_coeffs(rng)}
@@ -209,6 +223,17 @@ NORM_UP = tuple(1 << k for k in range(10))      # rotate-and-add: slot lane*1024
 NORM_DOWN = tuple(-(1 << k) for k in range(10))  # broadcast the masked sum over the lane
 
 
+HEAD_UP = tuple(1 << k for k in range(6))      # rotate-and-add: slot h*64 of a lane gets head h's sum
+HEAD_DOWN = tuple(-(1 << k) for k in range(6))  # broadcast the masked sums over their heads
+
+
+def head_start_mask(scale: float = 1.0) -> np.ndarray:
+    """scale at channel h*64 of every head h < 12, else 0"""
+    m = np.zeros(DPAD)
+    m[0:D:HS] = scale
+    return m
+
+
 def lane_start_mask(scale: float = 1.0) -> np.ndarray:
     m = np.zeros(DPAD)
     m[0] = scale
@@ -233,7 +258,7 @@ def channel_range_mask(lo: int, hi: int) -> np.ndarray:
 
 def rotation_steps() -> list:
     """Every rotation step the decode step uses (keys to generate)."""
-    s = set(WKV_LO) | set(WKV_HI) | set(NORM_UP) | set(NORM_DOWN)
+    s = set(WKV_LO) | set(WKV_HI) | set(NORM_UP) | set(NORM_DOWN) | set(HEAD_UP) | set(HEAD_DOWN)
     for nb in (32, 64):
         s |= set(mv_babies(nb)) | set(mv_giants(nb))
     s |= set(GAP_SHIFT) | set(-g for g in GAP_SHIFT)

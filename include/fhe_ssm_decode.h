@@ -53,9 +53,10 @@ void fhe_ssm_decoder_destroy(fhe_ssm_decoder* dec);
 int fhe_ssm_rotation_steps(int64_t* steps, uint32_t cap, uint32_t* n_steps);
 
 /* Weights, float64 row-major, per layer (0..n_layers-1) or model-wide (layer = -1):
- *   per layer  g1, g2, eta, mu_r, mu_k, mu_v, mu_w, mu_a, mu_g, mu_c  [768]
- *              W_r, W_k, W_v, W_w, W_a, W_g, W_o  [768][768];  W_ck [3072][768];  W_cv [768][3072]
- *              p_n1, p_n2, p_w, p_a, p_g, p_h  [4]  (polynomial c0 + c1 z + c2 z^2 + c3 z^3)
+ *   per layer  g1, g2, k_k, k_a, r_k, ln_w, ln_b, mu_r, mu_k, mu_v, mu_w, mu_a, mu_g, mu_c  [768]
+ *              W_r, W_k, W_v, W_w, W_a, W_g, W_vg, W_o  [768][768];  W_ck [3072][768];  W_cv [768][3072]
+ *              p_n1, p_n2, p_w, p_a, p_g, p_v, p_kn, p_gn, p_h  [4]  (polynomial c0 + c1 z + c2 z^2 + c3 z^3)
+ *              (W_vg and p_v, the value gate, are read in layers > 0 only; layer 0 sets the value they mix toward)
  *   model      g_o [768], p_o [4]
  * count must match.  All must be set before the first step; plaintexts are encoded on first use. */
 int fhe_ssm_decoder_set_weight(fhe_ssm_decoder* dec, const char* name, int32_t layer, const double* data,
@@ -67,7 +68,7 @@ int fhe_ssm_decoder_set_weight(fhe_ssm_decoder* dec, const char* name, int32_t l
 int fhe_ssm_decoder_step(fhe_ssm_decoder* dec, const uint64_t* d_x, uint32_t level, double scale, uint64_t* d_out,
                          uint32_t* out_level, double* out_scale);
 
-/* ciphertexts bootstrapped so far (26 per layer per step) */
+/* ciphertexts bootstrapped so far (28 per layer per step) */
 int fhe_ssm_decoder_stats(const fhe_ssm_decoder* dec, uint64_t* bootstraps);
 
 /* Drop the carried state (WKV state and both token-shift carries of every layer): the next step starts cold, as

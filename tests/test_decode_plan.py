@@ -54,10 +54,11 @@ def test_matvec_diagonals(n_in, n_out):
 
 @pytest.mark.timeout(300)
 def test_decode_step_plan_matches_reference():
-    W = M.make_weights(5, n_layers=1)
+    """two layers (the second mixes its value toward the first's), two tokens with the state carried"""
+    W = M.make_weights(5, n_layers=2)
     be = SlotBackend(17)
     step = DS.DecodeStep(be, W)
-    st = ref.init_state(32, 1)
+    st = ref.init_state(32, 2)
     for s in range(2):
         x = M.embed_tokens(np.arange(32) + 100 * s)
         out = step(be.encrypt(None, M.pack_lanes(x), 17))
@@ -65,9 +66,23 @@ def test_decode_step_plan_matches_reference():
         got = M.unpack_lanes(be.decrypt(None, out))
         assert np.max(np.abs(got - xo)) < 1e-12
         assert np.max(np.abs(be.decrypt(None, out).reshape(32, 1024)[:, 768:])) == 0
-        Dg = np.stack([ct.v[i].real for ct, i in step.state_diagonals(0)])
-        assert np.allclose(M.diag_to_state(Dg), st[0]["S"], atol=1e-14)
-    # per layer and step: the two increments and the 24 packed state ciphertexts; the residual stays on top
-    assert step.stats["bootstraps"] == 2 * 26
-    assert [e[1] for e in be.log[:3]] == ["inc_tm", "state", "inc_cm"]
+        for li in range(2):
+            Dg = np.stack([ct.v[i].real for ct, i in step.state_diagonals(li)])
+            assert np.allclose(M.diag_to_state(Dg), st[li]["S"], atol=1e-14)
+    # per layer and step: y with its bonus coefficient, the two increments and the 24 packed state ciphertexts;
+    # the residual stays on top
+    assert step.stats["bootstraps"] == 2 * 2 * 28
+    assert [e[1] for e in be.log[:4]] == ["state", "inc_tm", "state", "inc_cm"]
     assert out.level == 11
+
+
+def test_head_sum_and_masks():
+    """the per-head sums the L2 norm, GroupNorm and bonus use: rotate-and-add by 1 .. 32 within each lane, the
+    head-start mask, broadcast back; the gap channels stay zero"""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((32, 768))
+    be = SlotBackend(17)
+    step = DS.DecodeStep(be, M.make_weights(5, n_layers=1))
+    got = M.unpack_lanes(be.decrypt(None, step._head_sum(be.encrypt(None, M.pack_lanes(x), 17), 0.5)))
+    want = np.repeat(0.5 * x.reshape(32, 12, 64).sum(axis=2), 64, axis=1)
+    assert np.allclose(got.real, want, atol=1e-12)

@@ -380,13 +380,14 @@ def test_decode_step_one_layer(engine, DS, M):
 
 @pytest.mark.timeout(900)
 def test_native_decoder_matches_python_plan(engine, DS, M):
-    """the C++ driver (libfhe_ssm_decode.so) issues the same engine calls as the Python plan: one layer, two tokens
-    with the state carried, output ciphertexts equal word for word, same level, scale and bootstrap count"""
+    """the C++ driver (libfhe_ssm_decode.so) issues the same engine calls as the Python plan: two layers (the second
+    with the value residual toward the first's value), two tokens with the state carried, output ciphertexts equal
+    word for word, same level, scale and bootstrap count"""
     ND = load_module("native_decode")
     be, sk = engine
-    W = M.make_weights(5, n_layers=1)
+    W = M.make_weights(5, n_layers=2)
     py = DS.DecodeStep(be, W)
-    nat = ND.from_backend(be, 1)
+    nat = ND.from_backend(be, 2)
     nat.set_weights(W)
     for s in range(2):
         x = M.embed_tokens(np.arange(32) + 100 * s)
@@ -397,7 +398,7 @@ def test_native_decoder_matches_python_plan(engine, DS, M):
         got = out.download((2, lv, N))
         assert np.array_equal(got, want.buf.download((2, lv, N))), s
         print(f"token {s}: native == python plan at level {lv}")
-    assert nat.bootstraps == py.stats["bootstraps"] == 2 * 26
+    assert nat.bootstraps == py.stats["bootstraps"] == 2 * 2 * 28
     nat.close()
 
 
@@ -507,6 +508,6 @@ def test_decode_step_full_config5(engine, DS, M, driver):
         lerr = np.sqrt(np.mean((lg - lg_ref) ** 2)) / np.sqrt(np.mean(lg_ref ** 2))
         print(f"{driver} token {s}: relErrRms {err:.3e}, logits (4096-row slice) {lerr:.3e}")
         assert err < 1e-3 and lerr < 1e-3, (err, lerr)
-    assert n_boot() == 2 * 12 * 26
+    assert n_boot() == 2 * 12 * 28
     if driver == "native":
         nat.close()
