@@ -99,6 +99,7 @@ MEASURED = {
     ("pcmm", "step"): {"traffic": 18.375e9, "source": "profiles/pcmm_config3_kernel_trace.md"},
     ("pcmm", "bsgs_mac"): {"traffic": 7.382e9, "source": "profiles/pcmm_config3_kernel_trace.md"},
     ("bootstrap", "step"): {"traffic": 58.473e9, "source": "profiles/bootstrap_config4_kernel_trace.md"},
+    ("decode", "step"): {"traffic": 22786.5e9, "source": "profiles/decode_config5_kernel_trace.md"},
     ("ntt", "ntt_fwd_2pass"): {"traffic": 6.470e9, "valu_insts": 493.9e6, "source": "profiles/ntt_config1_kernel_trace.md"},
     ("ntt", "ntt_inv_2pass"): {"traffic": 6.470e9, "valu_insts": 504.9e6, "source": "profiles/ntt_config1_kernel_trace.md"},
 }
@@ -515,7 +516,18 @@ def bootstrap_stage_errors(ckks, ctx, bt, Kr, sk, ct, kp, rot, got, z):
 DECODE_LANES = 32
 
 
-def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native", serve_requests=0):
+def phase_table(ph: dict, step_ms: float):
+    """the profiled step by phase label (the engine's per-launch events): launches, event time, the share of the
+    step's event time scaled to the timed step, algorithmic bytes, and each label's marker-kernel id"""
+    tot = sum(v[1] for v in ph.values()) or 1.0
+    return {k: {"launches": n, "event_ms": round(ms, 3), "share": round(ms / tot, 4),
+                "ms_in_timed_step": round(step_ms * ms / tot, 2), "algorithmic_GB": round(by / 1e9, 3),
+                "marker_id": mid}
+            for k, (n, ms, by, mid) in sorted(ph.items(), key=lambda kv: -kv[1][1])}
+
+
+def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native", serve_requests=0,
+                 phase_markers=False):
     """Config 5: one encrypted decode step of the RWKV-7-0.1B-shaped polynomial model (12 layers, 32 lanes in
     the slots, state carried across steps, state bootstrapped once per layer).  The client side (token
     embedding + encryption before the step, decryption + the 768 x 65536 vocabulary head after it) is
@@ -547,6 +559,8 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native
         step = py
         n_boot = lambda: py.stats["bootstraps"]
     ctx = be.ctx
+    if phase_markers:  # an empty marker kernel at every change of phase label, for splitting a trace by phase
+        ctx.profile_phase_markers(True)
     tokens = lambda i: (np.arange(DECODE_LANES) * 7919 + 131 * i + seed) % M.VOCAB
 
     def client_in(i):
@@ -589,6 +603,8 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native
     torch.cuda.synchronize()
     ctx.profile(False)
     rep = ctx.profile_report()
+    phases = ctx.profile_phase_report()
+    marker_ids = {k: ctx.profile_phase_id(k) for k in ("step", "idle", "state_backup")} if phase_markers else {}
     ctx.profile_reset()
     s_per_step = sum(times) / len(times)
     free_b2, _ = torch.cuda.mem_get_info()
@@ -609,6 +625,7 @@ def bench_decode(ckks, torch, steps_n, warmup, seed, n_layers=12, driver="native
             "device_memory_in_use_gb_after_warmup": round((total_b - free_b) / 1e9, 1), "memory": mem,
             "client_s": {"decrypt_and_vocab_head": round(t_client, 3)},
             "kernels": kernel_table(rep), "kernel_io": kernel_io(rep, "decode"),
+            "phases": phase_table(phases, s_per_step * 1e3), "phase_marker_ids": marker_ids,
             "roofline": step_roofline("decode", profile_bytes(rep), s_per_step * 1e3, 0.5,
                                       "step: one decode step of the native driver; SURVEY 8(d) config-5 unit: the sum "
                                       "of its launches' algorithmic bytes (each launch's inputs, keys, diagonals and "
@@ -789,6 +806,9 @@ def main():
                     help="decode workload: also time this many one-token requests through the serve protocol")
     ap.add_argument("--decode-driver", default="native", choices=["native", "python"],
                     help="decode workload: the C++ driver (default) or the same plan in Python")
+    ap.add_argument("--phase-markers", action="store_true",
+                    help="decode workload: enqueue an empty marker kernel at every change of phase label (for "
+                         "splitting a rocprofv3 trace or counter pass by phase; the phase table is always reported)")
     ap.add_argument("--boot-form", default="sparse_r2", choices=sorted(BOOT_FORMS),
                     help="bootstrap workload: config 4 as stated (sparse_r2: sparse-secret encapsulation, K = 14, "
                          "2 double angles) or the dense-secret variant (dense_r3: K = 32, 3 double angles)")
@@ -833,7 +853,7 @@ def main():
             torch.cuda.empty_cache()
             d = bench_decode(ckks, torch, 2, 1, args.seed, driver=args.decode_driver)  # mean of 2 timed steps
             line = {"s_per_step": d["s_per_step"], "metric": "s/step for 32-lane decode (config 5)",
-                    "roofline": d["roofline"], "kernel_io": d["kernel_io"]}
+                    "roofline": d["roofline"], "kernel_io": d["kernel_io"], "phases": d["phases"]}
             line.update({k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s",
                                            "device_memory_in_use_gb_after_warmup", "memory", "driver")})
             if not args.no_cpu_baseline:
@@ -844,11 +864,12 @@ def main():
         cpu = None if args.no_cpu_baseline else cpu_baseline_hmult(args.seed)
     elif args.workload == "decode":
         d = bench_decode(ckks, torch, args.steps, args.warmup, args.seed, args.layers, args.decode_driver,
-                         args.serve_requests)
+                         args.serve_requests, args.phase_markers)
         res = {"metric": "s/step for 32-lane decode (config 5)", "value": d["s_per_step"], "unit": "s/step",
                "ms_per_step": round(d["s_per_step"] * 1e3, 1), "dtype": "u64",
                "config": {"workload": d["workload"], "lanes": DECODE_LANES, "layers": args.layers},
                "kernels": d["kernels"], "roofline": d["roofline"], "kernel_io": d["kernel_io"],
+               "phases": d["phases"], "phase_marker_ids": d["phase_marker_ids"],
                "check": {k: d[k] for k in ("key_switches_per_step", "bootstraps_per_step", "setup_s", "client_s",
                                            "device_memory_in_use_gb_after_warmup", "memory", "driver")}}
         if d["serve"]:
@@ -886,6 +907,9 @@ def main():
         out["check"] = res["check"]
     if "ks_stage" in res:
         out["ks_stage"] = res["ks_stage"]
+    for k in ("phases", "phase_marker_ids"):
+        if k in res:
+            out[k] = res[k]
     out.update(extra)
     if cpu is not None:
         out["cpu_baseline"] = cpu

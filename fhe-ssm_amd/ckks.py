@@ -43,6 +43,12 @@ class DevSidecarInfo(ctypes.Structure):
 
 # name -> (restype, argtypes); the exported C ABI (kept in step with include/ckks_engine.h)
 SIGNATURES = {
+    "ckks_profile_phase": (_int, [_vp, ctypes.c_char_p, _vp]),
+    "ckks_profile_phase_markers": (_int, [_vp, _int]),
+    "ckks_profile_phase_id": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int32)]),
+    "ckks_profile_phase_query": (_int, [_vp, _u32, ctypes.c_char_p, _u32, ctypes.POINTER(ctypes.c_uint64),
+                                        ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                                        ctypes.POINTER(ctypes.c_int32)]),
     "ckks_dev_sidecar_read": (_int, [ctypes.c_char_p, _vp, _vp, _u32, _vp, _u32]),
     "ckks_dev_sidecar_write": (_int, [ctypes.c_char_p, _vp, _u32, _vp, _u32]),
     "ckks_rotation_keys_resolve": (_int, [ctypes.c_char_p, _vp, _u32, _vp, _vp, _vp, _u32, ctypes.POINTER(_u32)]),
@@ -501,6 +507,34 @@ class Context:
         n = ctypes.c_uint64()
         check(load().ckks_context_counters(self.h, ctypes.byref(n), 1 if reset else 0))
         return n.value
+
+    def profile_phase(self, phase: str, stream=None) -> None:
+        """label the launches that follow (see ckks_profile_phase)"""
+        check(load().ckks_profile_phase(self.h, phase.encode(), stream))
+
+    def profile_phase_markers(self, on: bool) -> None:
+        check(load().ckks_profile_phase_markers(self.h, 1 if on else 0))
+
+    def profile_phase_id(self, phase: str) -> int:
+        """the marker id of a phase label (-1 if it was never set with markers on)"""
+        mid = ctypes.c_int32()
+        check(load().ckks_profile_phase_id(self.h, phase.encode(), ctypes.byref(mid)))
+        return int(mid.value)
+
+    def profile_phase_report(self) -> dict:
+        """{phase label: (launches, total_ms, total_algorithmic_bytes, marker id)}"""
+        out = {}
+        i = 0
+        name = ctypes.create_string_buffer(64)
+        while True:
+            n, ms, by, mid = ctypes.c_uint64(), ctypes.c_double(), ctypes.c_double(), ctypes.c_int32()
+            rc = load().ckks_profile_phase_query(self.h, i, name, 64, ctypes.byref(n), ctypes.byref(ms),
+                                                 ctypes.byref(by), ctypes.byref(mid))
+            if rc != CKKS_OK:
+                break
+            out[name.value.decode()] = (n.value, ms.value, by.value, mid.value)
+            i += 1
+        return out
 
     def profile_report(self) -> dict:
         """{kernel name: (launches, total_ms, total_algorithmic_bytes)}"""

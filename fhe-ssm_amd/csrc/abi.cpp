@@ -1099,6 +1099,61 @@ int ckks_profile_enable(ckks_context* ctx, int on) {
     return CKKS_OK;
 }
 
+int ckks_profile_phase(ckks_context* ctx, const char* phase, void* stream) {
+    if (!ctx || !phase) return fail(CKKS_EINVAL, "null argument");
+    return guarded([&] {
+        (void)fhe::set_phase(ctx->c, phase, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
+int ckks_profile_phase_markers(ckks_context* ctx, int on) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    ctx->c.phase_marks = on != 0;
+    return CKKS_OK;
+}
+
+int ckks_profile_phase_query(ckks_context* ctx, uint32_t idx, char* name, uint32_t name_cap, uint64_t* launches,
+                             double* total_ms, double* total_bytes, int32_t* marker_id) {
+    if (!ctx) return fail(CKKS_EINVAL, "null context");
+    std::vector<std::string> order;
+    std::map<std::string, std::tuple<uint64_t, double, double>> agg;
+    for (auto& r : ctx->c.prof) {
+        HIP_TRY(hipEventSynchronize(r.e1));
+        float ms = 0;
+        HIP_TRY(hipEventElapsedTime(&ms, r.e0, r.e1));
+        auto it = agg.find(r.phase);
+        if (it == agg.end()) {
+            order.push_back(r.phase);
+            it = agg.emplace(r.phase, std::make_tuple(0ull, 0.0, 0.0)).first;
+        }
+        std::get<0>(it->second) += 1;
+        std::get<1>(it->second) += ms;
+        std::get<2>(it->second) += r.bytes;
+    }
+    if (idx >= order.size()) return fail(CKKS_EINVAL, "no such phase entry");
+    const std::string& ph = order[idx];
+    if (name && name_cap) {
+        std::strncpy(name, ph.c_str(), name_cap - 1);
+        name[name_cap - 1] = '\0';
+    }
+    if (launches) *launches = std::get<0>(agg[ph]);
+    if (total_ms) *total_ms = std::get<1>(agg[ph]);
+    if (total_bytes) *total_bytes = std::get<2>(agg[ph]);
+    if (marker_id) {
+        auto it = ctx->c.phase_ids.find(ph);
+        *marker_id = it == ctx->c.phase_ids.end() ? -1 : (int32_t)it->second;
+    }
+    return CKKS_OK;
+}
+
+int ckks_profile_phase_id(const ckks_context* ctx, const char* phase, int32_t* marker_id) {
+    if (!ctx || !phase || !marker_id) return fail(CKKS_EINVAL, "null argument");
+    auto it = ctx->c.phase_ids.find(phase);
+    *marker_id = it == ctx->c.phase_ids.end() ? -1 : (int32_t)it->second;
+    return CKKS_OK;
+}
+
 int ckks_profile_reset(ckks_context* ctx) {
     if (!ctx) return fail(CKKS_EINVAL, "null context");
     fhe::prof_clear(ctx->c);

@@ -528,6 +528,14 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint3
                    const uint64_t* conj_evk, const int64_t* steps, const uint64_t* const* evks, uint32_t n_keys,
                    uint64_t* out, hipStream_t st, uint32_t stop_stage) {
     if (B == 0) return P.l_out;
+    // the stages' phase labels (profiling), the caller's label put back on every way out
+    struct PhaseGuard {
+        Context& c;
+        hipStream_t s;
+        std::string old;
+        ~PhaseGuard() { (void)set_phase(c, old, s); }
+    } phase_guard{ctx, st, ctx.prof_phase};
+    (void)set_phase(ctx, "boot_modraise", st);
     // stream-ordered like every call on a context: the pooled buffers go back for reuse by later work on st
     auto emit = [&](const uint64_t* src, uint32_t n, uint32_t l) {
         HIPB(hipMemcpyAsync(out, src, (size_t)n * 2 * l * W * 8, hipMemcpyDeviceToDevice, st));
@@ -571,6 +579,7 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint3
         }
     }
     if (stop_stage == 1) return emit(raised.d, B, L);
+    (void)set_phase(ctx, "boot_coeff_to_slot", st);
     // ---- CoeffToSlot: one BSGS level per call over the batch (diagonals and keys shared), then rescale
     auto keys_of = [&](const BootLevel& bl, std::vector<const uint64_t*>& bk, std::vector<const uint64_t*>& gk) {
         for (auto s : bl.bsteps) bk.push_back(s ? key[s] : nullptr);
@@ -634,6 +643,7 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint3
     }
     if (stop_stage == 3) return emit(pair.d, 2 * B, pair.l);
     // ---- EvalMod on both halves of every ciphertext
+    (void)set_phase(ctx, "boot_eval_mod", st);
     HCt y = ev2.chebyshev(pair, P.cheb);
     ev2.put(pair);
     for (int k = 0; k < P.r; k++) {
@@ -645,6 +655,7 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint3
     }
     if (stop_stage == 4) return emit(y.d, 2 * B, y.l);
     // ---- recombine Re + i Im at the StC input level
+    (void)set_phase(ctx, "boot_slot_to_coeff", st);
     const uint32_t ls = P.stc[0].l;
     HCt ya = y.l == ls ? y : ev2.adjust(y, ls);
     if (ya.d != y.d) ev2.put(y);

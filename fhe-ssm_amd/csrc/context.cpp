@@ -199,9 +199,21 @@ void context_init(Context& c, const std::vector<uint64_t>& q, const std::vector<
     up((void**)&c.d_primes, c.primes.data(), c.primes.size() * sizeof(PrimeInfo));
 }
 
+std::string set_phase(Context& ctx, const std::string& phase, hipStream_t st) {
+    std::string old = ctx.prof_phase;
+    if (phase == old) return old;
+    ctx.prof_phase = phase;
+    if (ctx.phase_marks && !ctx.arena) {
+        auto it = ctx.phase_ids.find(phase);
+        if (it == ctx.phase_ids.end()) it = ctx.phase_ids.emplace(phase, (uint32_t)ctx.phase_ids.size()).first;
+        (void)launch_phase_mark(it->second, st);
+    }
+    return old;
+}
+
 int prof_begin(const Context& ctx, const char* name, double bytes, hipStream_t st) {
     if (!ctx.prof_on || ctx.arena) return -1;  // no events are created inside an allocation-free call
-    ProfRec r{name, bytes, nullptr, nullptr};
+    ProfRec r{name, bytes, nullptr, nullptr, ctx.prof_phase};
     if (hipEventCreate(&r.e0) != hipSuccess || hipEventCreate(&r.e1) != hipSuccess) return -1;
     if (hipEventRecord(r.e0, st) != hipSuccess) return -1;
     ctx.prof.push_back(r);

@@ -103,6 +103,7 @@ struct ProfRec {
     std::string name;
     double bytes;
     hipEvent_t e0, e1;
+    std::string phase;  // the caller's phase label when the launch was issued (set_phase)
 };
 
 struct Context {
@@ -154,6 +155,12 @@ struct Context {
     // per-launch profiling (off by default)
     bool prof_on = false;
     mutable std::vector<ProfRec> prof;
+    // phase attribution: the label every profiled launch records; with phase_marks, each change of label also
+    // enqueues an empty marker kernel (k_phase_mark, phase_ids[label] + 1 workgroups) so that a kernel trace or a
+    // counter pass can be split by phase
+    std::string prof_phase;
+    bool phase_marks = false;
+    std::map<std::string, uint32_t> phase_ids;
     // key switches issued (evk inner products, one per ciphertext), always counted
     mutable uint64_t n_keyswitch = 0;
     // ModDown rounding: false = approximate P -> Q conversion (OpenFHE ApproxModDown, floor(x/P) - u with
@@ -167,6 +174,9 @@ struct Context {
 
 // Profiling helpers: no-ops unless ctx.prof_on.
 int prof_begin(const Context& ctx, const char* name, double bytes, hipStream_t st);
+// the phase label of the launches that follow (the marker kernel, if phase_marks, on st); returns the previous label
+std::string set_phase(Context& ctx, const std::string& phase, hipStream_t st);
+hipError_t launch_phase_mark(uint32_t id, hipStream_t st);
 void prof_end(const Context& ctx, int idx, hipStream_t st);
 void prof_clear(const Context& ctx);
 

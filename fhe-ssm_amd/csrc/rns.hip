@@ -1340,6 +1340,14 @@ hipError_t launch_bsgs_dh_mac(const Context& ctx, const uint64_t* ext, uint64_t 
     return hipGetLastError();
 }
 
+// the phase marker: no work; phase id + 1 workgroups of 64 threads make it recognizable in a trace or counter pass
+__global__ __launch_bounds__(64) void k_phase_mark(uint32_t) {}
+
+hipError_t launch_phase_mark(uint32_t id, hipStream_t st) {
+    hipLaunchKernelGGL(k_phase_mark, dim3(id + 1), dim3(64), 0, st, id);
+    return hipGetLastError();
+}
+
 hipError_t launch_pair_mac(const Context& ctx, const uint64_t* R, const uint64_t* pt, uint64_t* out, uint32_t n_sets,
                            uint32_t n, uint32_t l, uint32_t log_rep, hipStream_t st) {
     if (log_rep > 6 || n == 0) return hipErrorInvalidValue;

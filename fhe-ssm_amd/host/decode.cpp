@@ -171,6 +171,16 @@ class Engine {
 
     uint32_t top_level() const { return top_; }
     ckks_context* ctx() const { return ctx_; }
+    // the phase label of the engine launches that follow (profiling attribution; see ckks_profile_phase); returns
+    // the previous one
+    std::string set_phase(const std::string& p) {
+        std::string old = phase_;
+        if (p != phase_) {
+            (void)ckks_profile_phase(ctx_, p.c_str(), nullptr);
+            phase_ = p;
+        }
+        return old;
+    }
     double S(uint32_t l) const { return S_.at(l); }
     const uint64_t* key(int64_t s) const {
         if (s == 0) return nullptr;
@@ -349,6 +359,12 @@ class Engine {
     }
 
     Ct matvec(const std::vector<Ct>& inputs, const Matvec& h) {
+        const std::string prev = set_phase("matvec");  // (an exception leaves the label: only profiling reads it)
+        Ct out = matvec_(inputs, h);
+        set_phase(prev);
+        return out;
+    }
+    Ct matvec_(const std::vector<Ct>& inputs, const Matvec& h) {
         const uint32_t lv = inputs[0].level;
         if (inputs.size() != h.n_in) throw Error(CKKS_EINVAL, "matvec input count");
         std::vector<const uint64_t*> in;
@@ -446,6 +462,7 @@ class Engine {
     Ct bootstrap(const Ct& a, const std::string& kind) {
         const fhe_ssm_refresh& r = boots_.at(kind);
         const auto& bk = boot_keys_.at(kind);
+        const std::string prev = set_phase("boot_prep");  // the bootstrap labels its own stages
         Ct lo = at_scale(a, 1, r.in_scale);
         Ct out = fresh(a.B, top_, S(top_));
         // passes of equal size (24 -> 12 + 12): one buffer shape in the bootstrap's pool
@@ -456,6 +473,7 @@ class Engine {
                                         bk.second.data(), (uint32_t)bk.first.size(), out.ptr(b0), nullptr),
                "ckks_eval_bootstrap_many");
         }
+        set_phase(prev);
         return out;
     }
 
@@ -534,6 +552,7 @@ class Engine {
     }
 
     ckks_context* ctx_;
+    std::string phase_;
     const uint64_t *relin_, *conj_;
     std::vector<uint64_t> moduli_;
     uint32_t top_ = 0;
@@ -558,6 +577,16 @@ class Engine {
                (stage_[1].buf ? stage_[1].buf->bytes : 0);
     }
     std::shared_ptr<Buf> alloc(size_t bytes) { return std::make_shared<Buf>(pool_.get(bytes), bytes, &pool_); }
+};
+
+// a phase label for the launches of a scope, the enclosing label put back at its end
+struct PhaseScope {
+    Engine* e;
+    std::string old;
+    PhaseScope(Engine* eng, const char* p) : e(eng), old(eng->set_phase(p)) {}
+    ~PhaseScope() { e->set_phase(old); }
+    PhaseScope(const PhaseScope&) = delete;
+    PhaseScope& operator=(const PhaseScope&) = delete;
 };
 
 // ------------------------------------------------------------------ slot-layout tables
@@ -721,6 +750,8 @@ class Decoder {
     // puts the saved state back.  The device holds one state instead of two.
     Ct step(const Ct& x_in) {
         const bool own = !saved_.active;  // a backup held by the caller (a multi-token request) is kept
+        be_->set_phase("step");           // a step's launches start after this label's marker
+        be_->set_phase("state_backup");
         if (own) backup();
         be_->begin_step();
         try {
@@ -729,20 +760,29 @@ class Decoder {
             Ct v0;  // the first layer's value (the later layers' value residual mixes toward it)
             for (uint32_t li = 0; li < layers_.size(); li++) {
                 LayerState& st = work[li];
-                x = be_->add(x, boot(time_mix(li, x, st, v0), "inc_tm"));
+                be_->set_phase("elementwise");
+                Ct o = time_mix(li, x, st, v0);
+                x = be_->add(x, boot(o, "inc_tm"));
                 refresh_state(st);
-                x = be_->add(x, boot(channel_mix(li, x, st), "inc_cm"));
-                release_layer(li);
+                Ct f = channel_mix(li, x, st);
+                x = be_->add(x, boot(f, "inc_cm"));
+                {
+                    PhaseScope ps(be_, "state_backup");
+                    release_layer(li);
+                }
             }
+            be_->set_phase("elementwise");
             Ct xo = norm(x, model_["p_o"]);
             std::vector<double> go(DPAD, 0.0);
             std::copy(model_["g_o"].begin(), model_["g_o"].end(), go.begin());
             Ct out = be_->mul_pt(xo, *vec_pt("g_o", xo.level, [&] { return go; }));
+            be_->set_phase("idle");           // what the caller enqueues next is not the step's
             state_ = std::move(work);
             if (own) drop_backup();
             reserve_backup();
             return out;
         } catch (...) {
+            be_->set_phase("idle");
             if (own) {
                 restore_backup();
                 drop_backup();
@@ -838,6 +878,7 @@ class Decoder {
 
     // x * p(mean(x^2)) per lane: rotate-and-add to the lane start, mask (times 1/768), broadcast back
     Ct norm(const Ct& x, const std::vector<double>& pcoef) {
+        PhaseScope ps(be_, "norm");
         Ct s = be_->mul(x, x);
         for (int k = 0; k < 10; k++) s = be_->add(s, be_->rotate(s, 1 << k));
         s = be_->mul_pt(s, *vec_pt("lane_start", s.level, [] {
@@ -853,6 +894,7 @@ class Decoder {
     // every head's sum of x (times scale), broadcast over the head's 64 channels: rotate-and-add by 1 .. 32 (slot
     // h*64 of a lane then holds head h's sum), mask the head starts (times scale), broadcast back
     Ct head_sum(const Ct& x, double scale) {
+        PhaseScope ps(be_, "head_sum");
         Ct s = x;
         for (int k = 0; k < 6; k++) s = be_->add(s, be_->rotate(s, 1 << k));
         char tag[48];
@@ -928,6 +970,7 @@ class Decoder {
             m.insert(m.end(), m2.begin(), m2.end());
             return m;
         };
+        be_->set_phase("wkv");
         // k's masked rotations: rot64_t(kk) = rot64_t(k) k_k, and the key update k' = k (1 - k_a) + (k a) k_a
         Ct KX = be_->rotate_masked(k, *vec_pt("mask_k" + tag, k.level,
                                                [&] { return masks2(kkw.data(), one_minus_ka.data()); }), 2);
@@ -953,6 +996,7 @@ class Decoder {
         std::vector<std::vector<Pair>> p3(1);
         for (uint32_t t = 0; t < WKV_T; t++) p3[0].push_back(Pair{&Dn, t, &R_t, t});
         Ct y = be_->mult_sum(p3);
+        be_->set_phase("elementwise");
         // the bonus coefficient per head: sum of r k' r_k = (r k) (1 - k_a) r_k + (r ka) k_a r_k
         const std::vector<double>& rkw = L["r_k"];
         Ct rk1p = be_->mul(r, k);
@@ -1040,6 +1084,7 @@ class Decoder {
     // bootstrap the new state once: the 64 diagonals packed 4 -> 3 into the lanes' unused channels, the 48 packed
     // two per complex ciphertext, 24 bootstraps, unpacked with one conjugation and three masked rotations
     void refresh_state(LayerState& st) {
+        PhaseScope ps(be_, "state_pack");
         Ct Dn = st.Dn;
         st.Dn = Ct{};
         const uint32_t q = WKV_T / 4, h = q / 2;
@@ -1056,6 +1101,7 @@ class Decoder {
                              be_->add(be_->slice(C, 0, h), be_->mul_i(be_->slice(C, h, q), 1))});
         n_boot_ += pk.B;
         Ct P = be_->bootstrap(pk, "state");
+        be_->set_phase("state_unpack");
         Ct Cj = be_->conj(P);
         Ct re2 = be_->add(P, Cj);                     // 2 Re: A, C[0:8]
         Ct im2 = be_->mul_i(be_->add(Cj, P, -1), 1);  // i (conj - P) = 2 Im: B, C[8:16]

@@ -426,6 +426,18 @@ int ckks_context_counters(ckks_context* ctx, uint64_t* key_switches, int reset);
  * Fills min(n, 4) entries. */
 int ckks_context_memory(const ckks_context* ctx, uint64_t* bytes, uint32_t n);
 int ckks_profile_enable(ckks_context* ctx, int on);
+/* phase attribution (no counterpart in the reference; for measurement): ckks_profile_phase labels the launches that
+ * follow (every profiled launch records the label; the bootstrap labels its own stages boot_modraise,
+ * boot_coeff_to_slot, boot_eval_mod, boot_slot_to_coeff and restores the caller's label); with
+ * ckks_profile_phase_markers on, each change of label also enqueues on stream an empty kernel k_phase_mark of
+ * id + 1 workgroups (id: the label's marker id, in order of first use), so that a trace or a counter pass of the
+ * kernels can be split by phase.  ckks_profile_phase_query aggregates the profiled launches by label. */
+int ckks_profile_phase(ckks_context* ctx, const char* phase, void* stream);
+int ckks_profile_phase_markers(ckks_context* ctx, int on);
+int ckks_profile_phase_query(ckks_context* ctx, uint32_t idx, char* name, uint32_t name_cap, uint64_t* launches,
+                             double* total_ms, double* total_bytes, int32_t* marker_id);
+/* the marker id of a label (-1: never set while markers were on) */
+int ckks_profile_phase_id(const ckks_context* ctx, const char* phase, int32_t* marker_id);
 int ckks_profile_reset(ckks_context* ctx);
 int ckks_profile_query(ckks_context* ctx, uint32_t idx, char* name, uint32_t name_cap, uint64_t* launches,
                        double* total_ms, double* total_bytes);

@@ -155,3 +155,20 @@ def test_pcmm_and_bootstrap_step_traffic_match_their_profiles():
         if len(cells) == 5 and cells[0] == "k_bsgs_mac" and re.fullmatch(r"[0-9.]+", cells[3]):
             rows["mac"] = float(cells[3]) + float(cells[4])
     assert abs(bench.MEASURED[("pcmm", "bsgs_mac")]["traffic"] - rows["mac"] * 1e9) < 2e6
+
+
+def test_decode_step_traffic_matches_the_phase_table():
+    """config 5's roofline.traffic: the '**step**' row of the phase table (read GB + write GB)"""
+    sys.path.insert(0, REPO)
+    import bench
+    path = os.path.join(REPO, "profiles", "decode_config5_kernel_trace.md")
+    for line in open(path):
+        cells = [c.strip().strip("*") for c in line.strip().strip("|").split("|")]
+        if cells and cells[0] == "step" and len(cells) >= 6:
+            r, w = float(cells[4]), float(cells[5])
+            break
+    else:
+        raise AssertionError("no step row")
+    meas = bench.MEASURED[("decode", "step")]
+    assert meas["source"] == "profiles/decode_config5_kernel_trace.md"
+    assert abs(meas["traffic"] - (r + w) * 1e9) / meas["traffic"] < 0.001
