@@ -6,6 +6,7 @@
 
 #include "engine.hpp"
 #include "modarith.hpp"
+#include "ntt_device.hpp"
 
 namespace fhe {
 
@@ -13,11 +14,11 @@ namespace {
 
 __device__ __forceinline__ Barrett barrett_c(const PrimeInfo& p) { return Barrett{p.q, p.mu_hi, p.mu_lo}; }
 
-// residue of a signed coefficient: c mod q, or q - (|c| mod q) for c < 0 (0 when q divides |c|)
-__device__ __forceinline__ uint64_t signed_residue(int64_t c, uint64_t q) {
-    if (c >= 0) return (uint64_t)c % q;
-    const uint64_t m = (uint64_t)(-(c + 1)) % q;  // -(c+1) >= 0 even for INT64_MIN
-    return (m + 1 == q) ? 0 : q - 1 - m;
+// residue of a signed coefficient (|c| <= 2^63): c mod q, or q - (|c| mod q) for c < 0 (0 when q divides |c|);
+// |c| mod q by one Barrett reduction
+__device__ __forceinline__ uint64_t small_residue(int64_t c, const Barrett& br) {
+    const uint64_t m = reduce128(0, c >= 0 ? (uint64_t)c : 0 - (uint64_t)c, br);
+    return (c < 0 && m) ? br.q - m : m;
 }
 
 // 2^e mod q (square and multiply)
@@ -43,11 +44,9 @@ __global__ __launch_bounds__(256) void k_small_to_rns(const int64_t* __restrict_
     const uint32_t k = blockIdx.x * 256 + threadIdx.x;
     const uint32_t l = blockIdx.y, pc = blockIdx.z;
     const PrimeInfo& P = primes[pa.pmap[l]];
-    uint64_t r = signed_residue(coef[(size_t)pc * kN + k], P.q);
-    if (pa.log_approx) {
-        const Barrett br = barrett_c(P);
-        r = mul_mod(r, pow2_mod(pa.log_approx, br), br);
-    }
+    const Barrett br = barrett_c(P);
+    uint64_t r = small_residue(coef[(size_t)pc * kN + k], br);
+    if (pa.log_approx) r = mul_mod(r, pow2_mod(pa.log_approx, br), br);
     out[((size_t)pc * pa.n_limbs + l) * kN + k] = r;
 }
 
@@ -124,46 +123,90 @@ __global__ __launch_bounds__(256) void k_mul(const uint64_t* __restrict__ x, con
 
 // Periodic-plaintext encoder: vector n, limb i -> the N'-point negacyclic NTT (root psi^(N/N'), output in
 // bit-reversed order) of the small polynomial coef[n] 2^log_approx[n] mod q_i.  One workgroup per (n, i), the limb
-// in LDS.
+// in LDS (N' words of dynamic shared memory).  The Cooley-Tukey network of the table tab (stage s uses
+// Table[2^s + group]) runs up to three stages per LDS round: a thread takes the 2^R words of a unit through R stages
+// in registers, so N' = 2^11 takes four barriers.  Values stay lazily reduced (below 8q with ct_bfly; for primes below
+// 2^56 unreduced, below q + 4q L <= 49q at N' = 2^12) and are brought to [0, q) once before the store, so the words
+// are those of any exact evaluation of the network.
 constexpr int kMaxSmallN = 4096;
+
+// stages s .. s+R-1 of the network over a (N' = 2^lg words).  At stage s (2^s groups of 2t words, t = N' / 2^(s+1)) a
+// unit is the 2^R words j + k d, k < 2^R, d = 2t / 2^R, j = grp 2t + r (r < d): they stay inside one group for the R
+// stages, and at stage s + i word k belongs to group grp 2^i + (k >> (R - i)) and pairs with word k + 2^(R-1-i).
+template <int R, bool kOpen>
+__device__ __forceinline__ void encode_small_round(uint64_t* a, uint32_t Np, uint32_t lg, uint32_t s,
+                                                   const TwPair* __restrict__ tw, uint64_t q4, uint64_t nq) {
+    constexpr int U = 1 << R;
+    const uint32_t lt = lg - s - 1, sub = lt + 1 - R, d = 1u << sub;
+    for (uint32_t u = threadIdx.x; u < (Np >> R); u += 256) {
+        const uint32_t grp = u >> sub, j = (grp << (lt + 1)) + (u & (d - 1));
+        TwPair w[U - 1];  // the unit's twiddles, stage by stage, requested with its words
+#pragma unroll
+        for (int i = 0, n = 0; i < R; i++)
+#pragma unroll
+            for (int g = 0; g < (1 << i); g++, n++) w[n] = tw[((1u << s) << i) + (grp << i) + g];
+        uint64_t x[U];
+#pragma unroll
+        for (int k = 0; k < U; k++) x[k] = a[j + k * d];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const int hh = U >> (i + 1);
+#pragma unroll
+            for (int k = 0; k < U; k++) {
+                if (k & hh) continue;
+                fwd_bfly<kOpen>(x[k], x[k + hh], w[(1 << i) - 1 + (k >> (R - i))], q4, nq);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < U; k++) a[j + k * d] = x[k];
+    }
+    __syncthreads();
+}
+
+template <bool kOpen>
+__device__ __forceinline__ void encode_small_ntt(uint64_t* a, uint32_t Np, const TwPair* __restrict__ tw,
+                                                 const PrimeInfo& P) {
+    const uint64_t q = P.q, q4 = q << 2, nq = 0 - q;
+    const uint32_t lg = 31 - __builtin_clz(Np);
+    uint32_t s = 0;
+    for (; s + 3 <= lg; s += 3) encode_small_round<3, kOpen>(a, Np, lg, s, tw, q4, nq);
+    if (lg - s == 2) encode_small_round<2, kOpen>(a, Np, lg, s, tw, q4, nq);
+    if (lg - s == 1) encode_small_round<1, kOpen>(a, Np, lg, s, tw, q4, nq);
+}
 
 __global__ __launch_bounds__(256) void k_encode_small(const int64_t* __restrict__ coef,
                                                       const int32_t* __restrict__ log_approx,
                                                       uint64_t* __restrict__ out, uint32_t Np, uint32_t l,
                                                       const TwPair* __restrict__ tab,
                                                       const PrimeInfo* __restrict__ primes) {
-    __shared__ uint64_t a[kMaxSmallN];
+    extern __shared__ uint64_t a[];  // Np words
     const uint32_t n = blockIdx.x, i = blockIdx.y;
-    const uint64_t q = primes[i].q;
+    const PrimeInfo& P = primes[i];
+    const uint64_t q = P.q;
     const int64_t* c = coef + (size_t)n * Np;
     const uint32_t la = (uint32_t)log_approx[n];
-    const Barrett br = barrett_c(primes[i]);
-    const uint64_t f = la ? pow2_mod(la, br) : 1;
+    const Barrett br = barrett_c(P);
+    const uint64_t f = la == 0 ? 1 : la < 64 ? reduce128(0, 1ull << la, br) : pow2_mod(la, br);
     for (uint32_t k = threadIdx.x; k < Np; k += 256) {
-        const uint64_t r = signed_residue(c[k], q);
+        const uint64_t r = small_residue(c[k], br);
         a[k] = la ? mul_mod(r, f, br) : r;
     }
     __syncthreads();
     const TwPair* tw = tab + (size_t)i * Np;
-    for (uint32_t m = 1, t = Np >> 1; m < Np; m <<= 1, t >>= 1) {
-        for (uint32_t b = threadIdx.x; b < Np / 2; b += 256) {
-            const uint32_t grp = b / t, lo = grp * 2 * t + (b - grp * t);
-            const TwPair w = tw[m + grp];
-            const uint64_t x = shoup(a[lo + t], w.w, w.wp, q);
-            const uint64_t u = a[lo];
-            a[lo] = add_mod(u, x, q);
-            a[lo + t] = sub_mod(u, x, q);
-        }
-        __syncthreads();
-    }
+    const bool open = q < kOpenMaxQ;
+    if (open)
+        encode_small_ntt<true>(a, Np, tw, P);
+    else
+        encode_small_ntt<false>(a, Np, tw, P);
     uint64_t* o = out + ((size_t)n * l + i) * Np;
-    for (uint32_t k = threadIdx.x; k < Np; k += 256) o[k] = a[k];
+    for (uint32_t k = threadIdx.x; k < Np; k += 256)
+        o[k] = open ? reduce_open(a[k], q, 0 - q, P.red_shift, P.red_mul) : canon8(a[k], q);
 }
 
 hipError_t launch_encode_small(const Context& ctx, const int64_t* coef, const int32_t* log_approx, uint64_t* out,
                                uint32_t n_vec, uint32_t Np, uint32_t l, const TwPair* tab, hipStream_t st) {
-    if (Np > (uint32_t)kMaxSmallN || Np < 2) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_encode_small, dim3(n_vec, l), dim3(256), 0, st, coef, log_approx, out, Np, l, tab,
+    if (Np > (uint32_t)kMaxSmallN || Np < 2 || (Np & (Np - 1))) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_encode_small, dim3(n_vec, l), dim3(256), (size_t)Np * 8, st, coef, log_approx, out, Np, l, tab,
                        ctx.d_primes);
     return hipGetLastError();
 }

@@ -93,6 +93,9 @@ PrimeInfo make_prime_info(uint64_t q, uint64_t itab1) {
     PrimeInfo p{};
     p.q = q;
     p.ninv = invmod_h(kN % q, q);
+    // the last inverse NTT stage multiplies by N^-1 as a - b c with c = q - N^-1 = (q - 1) / N (q = 1 mod 2N)
+    if ((q - 1) % (2 * (uint64_t)kN) != 0 || p.ninv != q - (q - 1) / kN)
+        throw std::invalid_argument("modulus is not 1 mod 2N");
     p.ninv_p = shoup_companion(p.ninv, q);
     p.w1ninv = mulmod_h(itab1, p.ninv, q);
     p.w1ninv_p = shoup_companion(p.w1ninv, q);

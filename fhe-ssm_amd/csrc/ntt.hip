@@ -36,6 +36,7 @@
 #include "engine.hpp"
 #include "ks_device.hpp"
 #include "modarith.hpp"
+#include "ntt_device.hpp"
 
 namespace fhe {
 
@@ -80,41 +81,6 @@ __device__ __forceinline__ JobIn job_in(const JobSpec& js, uint32_t u) {
     if (js.src2) r.in2 = js.src2 + ((size_t)p * js.src_period + l) * kN;
     if (js.copy) r.cpy = js.copy + p * js.copy_pstride + ((size_t)(l / js.copy_alpha) * js.copy_E + l) * kN;
     return r;
-}
-
-// Forward (Cooley-Tukey) butterfly, values kept in [0, 8q) (q < 2^60): X is brought to [0, 4q), the
-// twiddle product is in [0, 4q), so X + T and X - T + 4q stay in [0, 8q).
-__device__ __forceinline__ void ct_bfly(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q4, uint64_t nq) {
-    const uint64_t x = csub_s(X, q4);
-    const uint64_t t = shoup_lazy4(Y, w.w, w.wp, nq);
-    X = x + t;
-    Y = x + q4 - t;
-}
-
-// Forward butterfly for primes below 2^56, X left unreduced: the twiddle product is in [0, 4q) whatever Y is, so
-// every stage adds at most 4q to the bound (inputs below 8q leave the 16 stages below 72q < 2^63) and the values
-// are brought to [0, q) once, at the end (reduce_open).  Saves the four instructions of the conditional subtract.
-constexpr uint64_t kOpenMaxQ = 1ull << 56;
-
-template <bool kOpen>
-__device__ __forceinline__ void fwd_bfly(uint64_t& X, uint64_t& Y, const TwPair& w, uint64_t q4, uint64_t nq) {
-    if (kOpen) {
-        const uint64_t x = X;
-        const uint64_t t = shoup_lazy4(Y, w.w, w.wp, nq);
-        X = x + t;
-        Y = x + q4 - t;
-    } else {
-        ct_bfly(X, Y, w, q4, nq);
-    }
-}
-
-// v < 128 q -> [0, q): k = hi32(floor(v / 2^s) M), M = floor(2^(32+s) / q), is floor(v/q) or one less (the
-// truncations lose less than 2^-24 + v / 2^(32+s) < 0.6), so v - k q lies in [0, 2q); one conditional subtract.
-__device__ __forceinline__ uint64_t reduce_open(uint64_t v, uint64_t q, uint64_t nq, uint32_t s, uint32_t M) {
-    const uint32_t k = __umulhi((uint32_t)(v >> s), M);
-    uint64_t r = (uint64_t)k * (uint32_t)nq + v;               // v + k nq (mod 2^64), nq = 2^64 - q
-    r += (uint64_t)(k * (uint32_t)(nq >> 32)) << 32;
-    return csub_s(r, q);
 }
 
 // Inverse (Gentleman-Sande) butterfly, values kept in [0, 4q).
@@ -190,13 +156,6 @@ __device__ __forceinline__ void gs_group_end(uint64_t* x, uint64_t q) {
         x[0] = csub_s(x[0], q << 6);
         x[0] = csub_s(x[0], q << 5);
     }
-}
-
-// [0, 8q) -> [0, q)
-__device__ __forceinline__ uint64_t canon8(uint64_t v, uint64_t q) {
-    v = csub_s(v, q << 2);
-    v = csub_s(v, q << 1);
-    return csub_s(v, q);
 }
 
 // ---------------------------------------------------------------- forward pass A (strided columns)
@@ -515,15 +474,23 @@ __device__ __forceinline__ void inv_a_tile(uint64_t* __restrict__ a, const TwPai
         }
     }
     // u = 7 (m = 1, stride N/2) with N^-1 folded in: X' = (X + Y) N^-1, Y' = (X - Y) w_1 N^-1.  Open: the three
-    // stages above leave value k + 8 below 2^lg[3][k+8] q and X + Y below 512 q
+    // stages above leave value k + 8 below 2^lg[3][k+8] q and X + Y below 512 q.
+    // X' without a multiply by N^-1: q = 1 + c 2^16 (q = 1 mod 2N), so N^-1 = q - c and, with v = a 2^16 + b (b < 2^16),
+    // v N^-1 = -v c = -a (q - 1) - b c = a - b c (mod q).  a + q - b c lies in (a, a + q] with b c < q and
+    // a = v / 2^16 < q / 128, so below 2q: one conditional subtract to [0, q), where the Shoup product by N^-1 took
+    // twelve instructions and left [0, 4q).
+    const uint64_t cn = q - ninv.w;  // c = (q - 1) / 2^16
 #pragma unroll
     for (int k = 0; k < 8; k++) {
         const uint64_t X = x[k], Y = x[k + 8];
-        x[k] = shoup_lazy4(X + Y, ninv.w, ninv.wp, nq);
+        const uint64_t v = X + Y;
+        x[k] = (v >> 16) + q - (uint64_t)((uint32_t)v & 0xFFFFu) * cn;
         x[k + 8] = shoup_lazy4(X + (kOpen ? q << kGs.lg[3][k + 8] : q4) - Y, w1ninv.w, w1ninv.wp, nq);
     }
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
+    for (int k = 0; k < 8; k++) __builtin_nontemporal_store(csub_s(x[k], q), &a[col + 256 * (rg + 16 * k)]);
+#pragma unroll
+    for (int k = 8; k < 16; k++) {
         const uint64_t v = csub_s(x[k], q << 1);
         __builtin_nontemporal_store(csub_s(v, q), &a[col + 256 * (rg + 16 * k)]);
     }
