@@ -39,7 +39,7 @@ hipError_t launch_lift_centered(const Context& ctx, const uint64_t* last, uint64
                                 uint32_t n_polys, uint32_t n_out, uint64_t ql, hipStream_t st);
 hipError_t launch_lincomb(const Context& ctx, uint64_t* out, uint32_t B, uint32_t l_out, uint32_t n_terms,
                           const uint64_t* const* x, const uint32_t* stride, const uint64_t* C, const uint64_t* add,
-                          hipStream_t st);
+                          hipStream_t st, uint32_t i0 = 0);
 hipError_t launch_mul_i(const Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n_polys, uint32_t l, int sign,
                         hipStream_t st);
 
@@ -403,12 +403,9 @@ public:
             const uint64_t qi = ctx_.moduli[i];
             add[i] = mulmod_h(mod_signed(a, qi), ctx_.moduli[lt] % qi, qi);
         }
-        HCt tmp = get(lo);
-        HIPB(launch_lincomb(ctx_, tmp.d, B_, lo, (uint32_t)x.size(), x.data(), stride.data(), C.data(),
-                            add_const != 0.0 ? add.data() : nullptr, st_));
         HCt out = get(lt);
-        rescale(ctx_, tmp.d, 2 * B_, lo, out.d, st_);
-        put(tmp);
+        rescale_lincomb(ctx_, B_, lo, (uint32_t)x.size(), x.data(), stride.data(), C.data(),
+                        add_const != 0.0 ? add.data() : nullptr, out.d, st_);
         return out;
     }
 
@@ -421,6 +418,23 @@ public:
         HCt o = get(a.l);
         HIPB(hipMemcpyAsync(o.d, a.d, (size_t)B_ * 2 * a.l * W * 8, hipMemcpyDeviceToDevice, st_));
         return o;
+    }
+
+    // factor * a b + add_const (the constant at the product's scale), relinearized and rescaled, a and b at one level:
+    // the affine map is applied by the product's ModDown combine (the words of mult followed by int_comb)
+    HCt mult_affine(const HCt& a, const HCt& b, long factor, double add_const) {
+        if (a.l != b.l) throw std::logic_error("mult_affine: level mismatch");
+        const long double post = std::roundl((long double)add_const * P_.S[a.l - 1]);
+        if (!(std::fabs(post) < 0x1p62L)) {
+            HCt sq = mult(a, b);
+            HCt r = int_comb({{sq, factor}}, add_const);
+            put(sq);
+            return r;
+        }
+        const Affine aff{factor, (int64_t)post};
+        HCt out = get(a.l - 1);
+        hmult(ctx_, a.d, b.d, B_, a.l, relin_, out.d, true, st_, &aff);
+        return out;
     }
 
     // product of two batches (levels aligned first), relinearized and rescaled
@@ -438,19 +452,22 @@ public:
     // Chebyshev series sum_j c_j T_j(x) for x at level l0
     HCt chebyshev(const HCt& x, const std::vector<double>& c) {
         std::map<int, HCt> T;
-        T[1] = copy(x);
-        auto t2 = [&](int j) {  // T_{2j} = 2 T_j^2 - 1
-            HCt sq = mult(T[j], T[j]);
-            HCt r = int_comb({{sq, 2}}, -1.0);
-            put(sq);
-            return r;
+        // T_j brought down to level l, made once and kept while the T_j live (the same T_j is needed at the same
+        // lower level more than once: the words are those of a fresh adjust)
+        std::map<std::pair<int, uint32_t>, HCt> Tat;
+        auto at = [&](int j, uint32_t l) -> HCt {
+            if (T[j].l == l) return T[j];
+            auto it = Tat.find({j, l});
+            if (it == Tat.end()) it = Tat.emplace(std::make_pair(j, l), adjust(T[j], l)).first;
+            return it->second;
         };
+        T[1] = copy(x);
+        auto t2 = [&](int j) { return mult_affine(T[j], T[j], 2, -1.0); };  // T_{2j} = 2 T_j^2 - 1
         auto tsum = [&](int a, int b) {  // T_{a+b} = 2 T_a T_b - T_{a-b}, a > b
-            HCt pr = mult(T[a], T[b]);
-            HCt d = adjust(T[a - b], pr.l);
-            HCt r = int_comb({{pr, 2}, {d, -1}});
+            const uint32_t l = std::min(T[a].l, T[b].l);
+            HCt pr = mult(at(a, l), at(b, l));
+            HCt r = int_comb({{pr, 2}, {at(a - b, pr.l), -1}});
             put(pr);
-            put(d);
             return r;
         };
         T[2] = t2(1);
@@ -463,6 +480,8 @@ public:
         int deg = (int)c.size() - 1;
         while (deg > 0 && c[deg] == 0.0) deg--;
         for (int n = 16; n <= deg; n *= 2) T[n] = t2(n / 2);  // the giant steps the division below uses
+        for (auto& kv : Tat) put(kv.second);  // the products above are done with their level copies
+        Tat.clear();
         std::function<HCt(const std::vector<double>&)> rec = [&](const std::vector<double>& a) -> HCt {
             int degp = (int)a.size() - 1;
             while (degp > 0 && a[degp] == 0.0) degp--;
@@ -490,7 +509,10 @@ public:
                 }
             }
             HCt hq = rec(q);
-            HCt prod = mult(hq, T[n]);
+            const uint32_t lm = std::min(hq.l, T[n].l);
+            HCt hqa = hq.l == lm ? hq : adjust(hq, lm);
+            HCt prod = mult(hqa, at(n, lm));
+            if (hqa.d != hq.d) put(hqa);
             put(hq);
             HCt hr = rec(rr);
             const uint32_t l = std::min(prod.l, hr.l);
@@ -504,6 +526,7 @@ public:
             return out;
         };
         HCt res = rec(c);
+        for (auto& kv : Tat) put(kv.second);
         for (auto& kv : T) put(kv.second);
         return res;
     }
@@ -646,10 +669,8 @@ uint32_t bootstrap(Context& ctx, const BootPlan& P, const uint64_t* ct_in, uint3
     (void)set_phase(ctx, "boot_eval_mod", st);
     HCt y = ev2.chebyshev(pair, P.cheb);
     ev2.put(pair);
-    for (int k = 0; k < P.r; k++) {
-        HCt sq = ev2.mult(y, y);
-        HCt z = ev2.int_comb({{sq, 2}}, -1.0);
-        ev2.put(sq);
+    for (int k = 0; k < P.r; k++) {  // double angle: 2 y^2 - 1
+        HCt z = ev2.mult_affine(y, y, 2, -1.0);
         ev2.put(y);
         y = z;
     }

@@ -638,8 +638,10 @@ struct MdrFuse {
     uint64_t* out;        // [2B][l-1][N]
     uint64_t add_pstride;
     uint32_t B, l, E, T;
+    int64_t post;       // with has_post: added (mod q_i) to every poly 0 word of the output
+    uint32_t has_post;
     TwPair pmod[kMaxPmap];  // P mod q_i
-    TwPair cfin[kMaxPmap];  // R P^-1 q_{l-1}^-1 mod q_i (R = 2^64)
+    TwPair cfin[kMaxPmap];  // R P^-1 q_{l-1}^-1 mod q_i (R = 2^64), times the caller's factor
 };
 
 // a word at a byte offset from a wave-uniform base (the global_load form with a scalar base and a 32-bit offset)
@@ -655,7 +657,7 @@ __device__ __forceinline__ uint64_t ld_at_nt(const uint64_t* base, uint32_t byte
 // derived from the kernel arguments and the job when needed, so that nothing of it is held in registers across the
 // transform.  Each word's loads are issued before the previous word's arithmetic (the first word's before the
 // transform's last exchange).
-template <int kD, bool kTa>
+template <int kD, bool kTa, bool kPost>
 struct MdrEpi {
     struct First {
         uint64_t xv[kD], e0[kD], e1[kD], u0, u1, u2, u3;
@@ -709,6 +711,11 @@ struct MdrEpi {
         uint64_t* out1 = out0 + po;
         const uint64_t q = P.q, ninv = P.mont_ninv;
         const TwPair pm = f.pmod[i], cf = f.cfin[i];
+        uint64_t post = 0;  // f.post mod q_i
+        if (kPost) {
+            const uint64_t m = reduce128(0, f.post >= 0 ? (uint64_t)f.post : 0 - (uint64_t)f.post, Barrett{q, P.mu_hi, P.mu_lo});
+            post = (f.post < 0 && m) ? q - m : m;
+        }
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
             const int k = 8 * g + kk;
@@ -731,8 +738,9 @@ struct MdrEpi {
                 s0.add(cur.u0 + q - L0[rl + 17 * k], pm.w);  // P (add0 + q - T0)
                 s1.add(cur.u1 + q - L1[rl + 17 * k], pm.w);
             }
-            const uint64_t v0 = shoup(redc(s0.get(), q, ninv), cf.w, cf.wp, q);
+            uint64_t v0 = shoup(redc(s0.get(), q, ninv), cf.w, cf.wp, q);
             const uint64_t v1 = shoup(redc(s1.get(), q, ninv), cf.w, cf.wp, q);
+            if (kPost) v0 = add_mod(v0, post, q);
             const uint32_t bo = (256 * blk + rl + 16 * k) * 8;
             __builtin_nontemporal_store(v0, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out0) + bo));
             __builtin_nontemporal_store(v1, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out1) + bo));
@@ -742,14 +750,14 @@ struct MdrEpi {
 };
 
 // grid (16 tiles, B (l-1) jobs), 512 threads; job v = i B + c (limb-major: a limb's evk is shared by the batch)
-template <int kD, bool kTa>
+template <int kD, bool kTa, bool kPost>
 __global__ __launch_bounds__(2 * kTileThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_ntt_fwd_b_mdr(
     uint64_t* T, const TwPair* tw_all, const PrimeInfo* primes, MdrFuse f) {
     __shared__ uint64_t lds[2 * kLdsWords];
     const uint32_t i = blockIdx.y / f.B, c = blockIdx.y - i * f.B;
     const uint32_t g = threadIdx.x >> 8, t = threadIdx.x & 255;
     const PrimeInfo& P = primes[i];
-    const MdrEpi<kD, kTa> epi{f, P, i, c, g};
+    const MdrEpi<kD, kTa, kPost> epi{f, P, i, c, g};
     uint64_t* a = T + ((size_t)(2 * c + g) * (f.l - 1) + i) * kN;
     const TwPair* tw = tw_all + (size_t)i * kN;
     if (P.q < kOpenMaxQ)
@@ -761,10 +769,15 @@ __global__ __launch_bounds__(2 * kTileThreads) __attribute__((amdgpu_waves_per_e
 template <int kD>
 void launch_b_mdr(dim3 grid, dim3 block, hipStream_t st, uint64_t* T, const TwPair* twb, const PrimeInfo* primes,
                   const MdrFuse& f) {
-    if (f.ta)
-        hipLaunchKernelGGL((k_ntt_fwd_b_mdr<kD, true>), grid, block, 0, st, T, twb, primes, f);
+    // the poly-0 constant (an affine output) is a separate instance: the plain relinearization pays nothing for it
+    if (f.ta && f.has_post)
+        hipLaunchKernelGGL((k_ntt_fwd_b_mdr<kD, true, true>), grid, block, 0, st, T, twb, primes, f);
+    else if (f.ta)
+        hipLaunchKernelGGL((k_ntt_fwd_b_mdr<kD, true, false>), grid, block, 0, st, T, twb, primes, f);
+    else if (f.has_post)
+        hipLaunchKernelGGL((k_ntt_fwd_b_mdr<kD, false, true>), grid, block, 0, st, T, twb, primes, f);
     else
-        hipLaunchKernelGGL((k_ntt_fwd_b_mdr<kD, false>), grid, block, 0, st, T, twb, primes, f);
+        hipLaunchKernelGGL((k_ntt_fwd_b_mdr<kD, false, false>), grid, block, 0, st, T, twb, primes, f);
 }
 
 // ---------------------------------------------------------------- forward pass B that finishes a key-switch list
@@ -947,6 +960,91 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(4)
     const uint32_t i = blockIdx.y / js.n_polys, pc = blockIdx.y - i * js.n_polys;
     const PrimeInfo& P = primes[prime];
     const SubEpi epi{ca, x, add, out, P, i, pc};
+    uint64_t* a = y + (size_t)off * kN;
+    const TwPair* tw = tw_all + (size_t)prime * kN;
+    if (P.q < kOpenMaxQ)
+        fwd_b_tile<true>(a, tw, P, blockIdx.x, threadIdx.x, lds, epi);
+    else
+        fwd_b_tile<false>(a, tw, P, blockIdx.x, threadIdx.x, lds, epi);
+}
+
+// ---------------------------------------------------------------- forward pass B that finishes a scalar combination
+// A rescaled linear combination: out[pc][i] = (x[pc][i] - y[pc][i]) s_i with x = sum_t C_t,i x_t + add_i (add on
+// polys 0 only) formed here from the terms, word for word as k_lincomb forms it (the sum of the products by C R mod
+// q_i reduced by one REDC, then the addend), instead of being stored by a lincomb launch and read back.
+constexpr int kLsubTerms = 8;
+constexpr int kLsubLimbs = 32;
+
+struct LinSubArgs {
+    const uint64_t* x[kLsubTerms];  // term t: [n_polys][stride_t][N], limbs 0 .. l-1 read
+    uint32_t stride[kLsubTerms];
+    uint32_t n_terms, l, has_add;
+    uint64_t out_pstride;
+    uint64_t C[kLsubTerms][kLsubLimbs];  // C_t,i R mod q_i
+    uint64_t add[kLsubLimbs];
+    TwPair s[kLsubLimbs];
+};
+
+// the workgroup's share of LinSubArgs (limb i of poly pc), read out of the kernel arguments once
+struct LinSubEpi {
+    struct First {};
+    const uint64_t* xt[kLsubTerms];  // term t's limb i of poly pc
+    uint64_t c[kLsubTerms];          // C_t,i R mod q_i
+    uint64_t addv;                   // add_i on polys 0, else 0
+    TwPair s;
+    uint64_t* out;                   // out's limb i of poly pc
+    uint64_t q, mont_ninv;
+    uint32_t n;
+
+    __device__ __forceinline__ First begin(int, int) const { return First{}; }
+
+    // kG words at a time, every term's words requested together before their products
+    static constexpr int kG = 2;
+    __device__ __forceinline__ void end(First, const uint64_t* L, int blk, int rl) const {
+        const uint32_t bo = (256 * blk + rl) * 8;
+#pragma unroll
+        for (int h = 0; h < 16 / kG; h++) {
+            uint64_t v[kLsubTerms][kG];
+#pragma unroll
+            for (int t = 0; t < kLsubTerms; t++)
+                if (t < (int)n) {
+#pragma unroll
+                    for (int k = 0; k < kG; k++) v[t][k] = ld_at_nt(xt[t], bo + 128 * (kG * h + k));
+                }
+#pragma unroll
+            for (int k = 0; k < kG; k++) {
+                Acc acc;
+#pragma unroll
+                for (int t = 0; t < kLsubTerms; t++)
+                    if (t < (int)n) acc.add(v[t][k], c[t]);
+                const uint64_t x = add_mod(redc(acc.get(), q, mont_ninv), addv, q);
+                const int kk = kG * h + k;
+                const uint64_t r = shoup(sub_mod(x, L[rl + 17 * kk], q), s.w, s.wp, q);
+                __builtin_nontemporal_store(r, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out) + bo + 128 * kk));
+            }
+        }
+    }
+};
+
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_ntt_fwd_b_lsub(
+    uint64_t* y, JobSpec js, const TwPair* tw_all, const PrimeInfo* primes, LinSubArgs la, uint64_t* out) {
+    __shared__ uint64_t lds[kLdsWords];
+    uint32_t off, prime;
+    job_of(js, blockIdx.y, off, prime);
+    const uint32_t i = blockIdx.y / js.n_polys, pc = blockIdx.y - i * js.n_polys;
+    const PrimeInfo& P = primes[prime];
+    LinSubEpi epi;
+#pragma unroll
+    for (int t = 0; t < kLsubTerms; t++) {
+        epi.xt[t] = la.x[t] + ((size_t)pc * la.stride[t] + i) * kN;
+        epi.c[t] = la.C[t][i];
+    }
+    epi.addv = la.has_add && (pc & 1) == 0 ? la.add[i] : 0;
+    epi.s = la.s[i];
+    epi.out = out + pc * la.out_pstride + (size_t)i * kN;
+    epi.q = P.q;
+    epi.mont_ninv = P.mont_ninv;
+    epi.n = la.n_terms;
     uint64_t* a = y + (size_t)off * kN;
     const TwPair* tw = tw_all + (size_t)prime * kN;
     if (P.q < kOpenMaxQ)
@@ -1164,6 +1262,59 @@ hipError_t launch_ntt_inv_ks(const Context& ctx, uint64_t* acc, const JobSpec& j
     return hipGetLastError();
 }
 
+// The rescale of a linear combination (see LinSubEpi): y [n_polys][l][N] receives the forward NTT of the lift of
+// the combination's dropped limb (lift: its coefficients, one limb per poly lift_pstride words apart, residues mod
+// lift_q); out [n_polys][..][N] (out_pstride words between polys) = (x - y) s with x formed from the terms.
+// C [n_terms][l] and add [l] (or null) are the combination's constants reduced mod q_i; s [l].
+hipError_t launch_ntt_fwd_lsub(const Context& ctx, uint64_t* y, uint32_t n_terms, const uint64_t* const* x,
+                               const uint32_t* stride, const uint64_t* C, const uint64_t* add, uint64_t* out,
+                               uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s, hipStream_t st,
+                               const uint64_t* lift, uint64_t lift_pstride, uint64_t lift_q) {
+    if (l == 0 || l > (uint32_t)kLsubLimbs || n_polys == 0 || n_terms == 0 || n_terms > (uint32_t)kLsubTerms)
+        return hipErrorInvalidValue;
+    JobSpec js{};
+    js.n_polys = n_polys;
+    js.period = l;
+    js.n_primes = l;
+    for (uint32_t i = 0; i < l; i++) js.pmap[i] = (uint8_t)i;
+    js.lift = lift;
+    js.lift_pstride = lift_pstride;
+    js.lift_q = lift_q;
+    LinSubArgs la{};
+    la.n_terms = n_terms;
+    la.l = l;
+    la.has_add = add ? 1 : 0;
+    la.out_pstride = out_pstride;
+    for (uint32_t t = 0; t < n_terms; t++) {
+        if (stride[t] < l) return hipErrorInvalidValue;
+        la.x[t] = x[t];
+        la.stride[t] = stride[t];
+        for (uint32_t i = 0; i < l; i++) {
+            // C R mod q_i (REDC of the sum gives the combination), a Shoup product by the context's R mod q_i
+            const PrimeInfo& pr = ctx.primes[i];
+            const uint64_t c = C[(size_t)t * l + i] % pr.q;
+            const uint64_t h = (uint64_t)(((unsigned __int128)c * pr.r_mod_p) >> 64);
+            const uint64_t v = c * pr.r_mod - h * pr.q;
+            la.C[t][i] = v >= pr.q ? v - pr.q : v;
+        }
+    }
+    for (uint32_t i = 0; i < l; i++) {
+        la.add[i] = add ? add[i] : 0;
+        la.s[i] = s[i];
+    }
+    const uint32_t n_jobs = n_polys * l;
+    // algorithmic bytes: the lift source once per poly, y written by pass A and read by pass B, the terms read, out
+    // written; tables
+    const double bytes = ((double)n_polys + 2.0 * n_jobs + (double)n_jobs * n_terms + n_jobs) * kN * 8 +
+                         (double)l * kN * sizeof(TwPair);
+    const int pi = prof_begin(ctx, "ntt_fwd_lsub", bytes, st);
+    const dim3 grid(16, n_jobs), block(kTileThreads);
+    hipLaunchKernelGGL(k_ntt_fwd_a, grid, block, 0, st, y, js, ctx.d_tw, ctx.d_primes);
+    hipLaunchKernelGGL(k_ntt_fwd_b_lsub, grid, block, 0, st, y, js, ctx.d_twb, ctx.d_primes, la, out);
+    prof_end(ctx, pi, st);
+    return hipGetLastError();
+}
+
 // Forward NTT of a ModDown's converted P part y [n_polys][l][N] (coefficients, limb i over prime i; dense) whose pass
 // B ends in k_sub_scale's combine: out[pc][i] = (x[pc][i] - NTT(y)[pc][i]) s_i (+ the addend).  y is left holding
 // the first pass's intermediate.  Same argument meaning as launch_sub_scale.  lift (optional): y's input is instead
@@ -1213,7 +1364,7 @@ hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x
 hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint32_t l, const uint64_t* ext,
                               const uint64_t* evk, const uint64_t* ta, const uint64_t* tb, const uint64_t* add,
                               uint64_t add_pstride, uint64_t* out, const TwPair* pmod, const TwPair* cfin,
-                              hipStream_t st) {
+                              hipStream_t st, const int64_t* post) {
     const uint32_t D = (l + ctx.alpha - 1) / ctx.alpha, E = l + ctx.K;
     if (l < 2 || l > kMaxPmap || B == 0 || D < 1 || D > 4 || (ta && (!tb || add)) || (!ta && !add))
         return hipErrorInvalidValue;
@@ -1234,6 +1385,8 @@ hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint3
     f.l = l;
     f.E = E;
     f.T = ctx.L + ctx.K;
+    f.has_post = post ? 1 : 0;
+    f.post = post ? *post : 0;
     for (uint32_t i = 0; i + 1 < l; i++) {
         if (ctx.moduli[i] >= (1ull << 60)) return hipErrorInvalidValue;  // the combine's sum bound
         f.pmod[i] = pmod[i];

@@ -56,10 +56,14 @@ hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x
                               uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
                               hipStream_t st, const uint64_t* lift = nullptr, uint64_t lift_pstride = 0,
                               uint64_t lift_q = 0);
+hipError_t launch_ntt_fwd_lsub(const Context& ctx, uint64_t* y, uint32_t n_terms, const uint64_t* const* x,
+                               const uint32_t* stride, const uint64_t* C, const uint64_t* add, uint64_t* out,
+                               uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s, hipStream_t st,
+                               const uint64_t* lift, uint64_t lift_pstride, uint64_t lift_q);
 hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint32_t l, const uint64_t* ext,
                               const uint64_t* evk, const uint64_t* ta, const uint64_t* tb, const uint64_t* add,
                               uint64_t add_pstride, uint64_t* out, const TwPair* pmod, const TwPair* cfin,
-                              hipStream_t st);
+                              hipStream_t st, const int64_t* post = nullptr);
 hipError_t launch_sub_scale(const Context& ctx, const uint64_t* x, uint64_t x_pstride, const uint64_t* y,
                             uint64_t y_pstride, const uint64_t* add, uint64_t add_pstride, uint32_t add_div,
                             uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
@@ -98,7 +102,7 @@ hipError_t launch_add_plain(const Context& ctx, const uint64_t* ct, const uint64
                             uint32_t l, uint64_t pt_bstride, hipStream_t st);
 hipError_t launch_lincomb(const Context& ctx, uint64_t* out, uint32_t B, uint32_t l_out, uint32_t n_terms,
                           const uint64_t* const* x, const uint32_t* stride, const uint64_t* C, const uint64_t* add,
-                          hipStream_t st);
+                          hipStream_t st, uint32_t i0 = 0);
 hipError_t launch_mul_i(const Context& ctx, const uint64_t* in, uint64_t* out, uint32_t n_polys, uint32_t l, int sign,
                         hipStream_t st);
 hipError_t launch_pair_mac(const Context& ctx, const uint64_t* R, const uint64_t* pt, uint64_t* out, uint32_t n_sets,
@@ -358,6 +362,14 @@ static const std::vector<TwPair>& pmod_tab(Context& ctx) {
     return ctx.tab_pmod;
 }
 
+// an integer (|v| < 2^120, carried as long double) reduced mod q
+static uint64_t residue_of(long double v, uint64_t q) {
+    const bool neg = v < 0;
+    const unsigned __int128 x = (unsigned __int128)(neg ? -v : v);
+    const uint64_t r = (uint64_t)(x % q);
+    return neg ? (r ? q - r : 0) : r;
+}
+
 static const std::vector<TwPair>& qinv_row(Context& ctx, uint32_t j) {
     auto it = ctx.tab_qinv.find(j);
     if (it != ctx.tab_qinv.end()) return it->second;
@@ -489,7 +501,8 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
 // forms limbs 0..l-2 itself from ext and evk.
 void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
                      hipStream_t st, const uint64_t* ext, const uint64_t* evk, const uint64_t* ta,
-                     const uint64_t* tb, bool x_from_ext) {
+                     const uint64_t* tb, bool x_from_ext, const Affine* aff) {
+    if (aff && !ext) throw std::invalid_argument("an affine output needs a relinearization");
     check_level(ctx, l);
     if (l < 2) throw std::invalid_argument("rescale needs l >= 2");
     const uint32_t E = l + ctx.K, K = ctx.K;
@@ -540,14 +553,16 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
     const uint32_t D = num_digits(ctx, l);
     if (ext && ctx.ntt_mode == NttMode::TwoPass && D <= 4) {
         // the combine reduces one 128-bit sum by REDC and scales it by R P^-1 q_{l-1}^-1 (R = 2^64)
+        // (times the affine factor: the combine's one Shoup product scales the word by it)
         std::vector<TwPair> cfin(l - 1);
         for (uint32_t i = 0; i + 1 < l; i++) {
             const uint64_t q = ctx.moduli[i];
-            const uint64_t v = mulmod_h(mulmod_h(pinv[i].w, qlinv[i].w, q), ctx.primes[i].r_mod, q);
+            uint64_t v = mulmod_h(mulmod_h(pinv[i].w, qlinv[i].w, q), ctx.primes[i].r_mod, q);
+            if (aff) v = mulmod_h(v, residue_of((long double)aff->factor, q), q);
             cfin[i] = TwPair{v, shoup_companion(v, q)};
         }
         HIPX(launch_ntt_fwd_mdr(ctx, T, n_polys / 2, l, ext, evk, ta, tb, ta ? nullptr : add, (uint64_t)l * W, out,
-                                pmod_tab(ctx).data(), cfin.data(), st));
+                                pmod_tab(ctx).data(), cfin.data(), st, aff ? &aff->post : nullptr));
         return;
     }
     HIPX(launch_ntt(ctx, T, regular_jobs(n_polys, pm), n_polys * (l - 1), false, ctx.ntt_mode, st));
@@ -560,6 +575,17 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
     else
         HIPX(launch_mdr_combine(ctx, x, xps, add, (uint64_t)l * W, T, out, n_polys, l, pinv.data(), qlinv.data(),
                                 st));
+    if (aff) {  // the affine map as an integer combination over the output, in place
+        const uint32_t lo = l - 1, B = n_polys / 2;
+        std::vector<uint64_t> C(lo), pa(lo);
+        for (uint32_t i = 0; i < lo; i++) {
+            C[i] = residue_of((long double)aff->factor, ctx.moduli[i]);
+            pa[i] = residue_of((long double)aff->post, ctx.moduli[i]);
+        }
+        const uint64_t* xs[1] = {out};
+        const uint32_t stride[1] = {lo};
+        HIPX(launch_lincomb(ctx, out, B, lo, 1, xs, stride, C.data(), aff->post ? pa.data() : nullptr, st));
+    }
 }
 
 // Key switch of a list of n <= 64 items (item c: extended digits ext[c] [D][E][N], key evk[c]) with its ModDown:
@@ -670,6 +696,41 @@ void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uin
                           (uint64_t)(l - 1) * W, n_polys, l - 1, s.data(), st));
 }
 
+// Rescaled linear combination of ciphertext batches: out [B][2][lo-1][N] = rescale(sum_t C_t x_t + add) with the
+// combination formed at lo limbs (term t read in place, stride[t] >= lo limbs per poly; add on poly 0).  C [n_terms][lo]
+// and add [lo] (or null) reduced mod q_i.  The same words as a lincomb launch into a buffer and its rescale: under the
+// two-pass NTT the combination is never stored -- its dropped limb alone is formed for the inverse NTT, and the other
+// limbs are formed by the rescale's combine (k_ntt_fwd_b_lsub) from the terms.
+void rescale_lincomb(Context& ctx, uint32_t B, uint32_t lo, uint32_t n_terms, const uint64_t* const* x,
+                     const uint32_t* stride, const uint64_t* C, const uint64_t* add, uint64_t* out, hipStream_t st) {
+    if (lo < 2 || lo > ctx.L) throw std::invalid_argument("rescale needs 2 <= l <= L");
+    const uint32_t n_polys = 2 * B, lt = lo - 1;
+    if (ctx.ntt_mode != NttMode::TwoPass || lt > 32 || n_terms > 8) {
+        uint64_t* tmp = (uint64_t*)ws_get(ctx, WS_LIN, (size_t)n_polys * lo * W * 8);
+        HIPX(launch_lincomb(ctx, tmp, B, lo, n_terms, x, stride, C, add, st));
+        rescale(ctx, tmp, n_polys, lo, out, st);
+        return;
+    }
+    // the dropped limb lo-1 of the combination, then to coefficients
+    uint64_t* last_in = (uint64_t*)ws_get(ctx, WS_LIN, (size_t)n_polys * W * 8);
+    std::vector<uint64_t> Cl(n_terms);
+    for (uint32_t t = 0; t < n_terms; t++) Cl[t] = C[(size_t)t * lo + lt];
+    HIPX(launch_lincomb(ctx, last_in, B, 1, n_terms, x, stride, Cl.data(), add ? add + lt : nullptr, st, lt));
+    uint64_t* last = (uint64_t*)ws_get(ctx, WS_LAST, (size_t)n_polys * W * 8);
+    JobSpec jl = regular_jobs(n_polys, {lt});
+    jl.src = last_in;
+    jl.src_period = 1;
+    HIPX(launch_ntt(ctx, last, jl, n_polys, true, ctx.ntt_mode, st));
+    // limbs 0..lo-2: (x - NTT(lift(last))) q_{lo-1}^-1 with x formed from the terms
+    uint64_t* y = (uint64_t*)ws_get(ctx, WS_RTMP, (size_t)n_polys * lt * W * 8);
+    std::vector<uint64_t> Ck((size_t)n_terms * lt);
+    for (uint32_t t = 0; t < n_terms; t++)
+        for (uint32_t i = 0; i < lt; i++) Ck[(size_t)t * lt + i] = C[(size_t)t * lo + i];
+    const std::vector<TwPair>& s = qinv_row(ctx, lt);
+    HIPX(launch_ntt_fwd_lsub(ctx, y, n_terms, x, stride, Ck.data(), add, out, (uint64_t)lt * W, n_polys, lt, s.data(),
+                             st, last, W, ctx.moduli[lt]));
+}
+
 // ------------------------------------------------------------------ HMult + relinearize (+ rescale)
 // a, b: [B][2][l][N] eval -> out: [B][2][l-1][N] (rescaled) or [B][2][l][N] (do_rescale = false)
 // relinearization (+ rescale) after the tensor step: d01 [B][2][l][N], d2 in x2c (evaluation form) and in
@@ -678,7 +739,9 @@ void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uin
 // x2c_coef: x2c already holds d2 in coefficient form (the inverse NTT formed it from the inputs)
 static void relin_tail(Context& ctx, uint64_t* d01, uint64_t* x2c, uint64_t* ext, uint32_t B, uint32_t l,
                        const uint64_t* evk, uint64_t* out, bool do_rescale, hipStream_t st,
-                       const uint64_t* ta = nullptr, const uint64_t* tb = nullptr, bool x2c_coef = false) {
+                       const uint64_t* ta = nullptr, const uint64_t* tb = nullptr, bool x2c_coef = false,
+                       const Affine* aff = nullptr) {
+    if (aff && !do_rescale) throw std::invalid_argument("an affine output needs the rescale");
     const uint32_t E = l + ctx.K;
     uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)B * 2 * E * W * 8);
     std::vector<uint32_t> pm(l);
@@ -694,15 +757,15 @@ static void relin_tail(Context& ctx, uint64_t* d01, uint64_t* x2c, uint64_t* ext
     // the fused NTT mode or more than 4 digits); the combine forms limbs 0..l-2
     if (ctx.ntt_mode == NttMode::TwoPass && num_digits(ctx, l) <= 4) {
         ctx.n_keyswitch += B;
-        moddown_rescale(ctx, acc, 2 * B, l, d01, out, st, ext, evk, ta, tb, true);
+        moddown_rescale(ctx, acc, 2 * B, l, d01, out, st, ext, evk, ta, tb, true, aff);
         return;
     }
     HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st, l - 1));
-    moddown_rescale(ctx, acc, 2 * B, l, d01, out, st, ext, evk, ta, tb);
+    moddown_rescale(ctx, acc, 2 * B, l, d01, out, st, ext, evk, ta, tb, false, aff);
 }
 
 void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l, const uint64_t* evk,
-           uint64_t* out, bool do_rescale, hipStream_t st) {
+           uint64_t* out, bool do_rescale, hipStream_t st, const Affine* aff) {
     check_level(ctx, l);
     const uint32_t D = num_digits(ctx, l), E = l + ctx.K;
     uint64_t* d01 = (uint64_t*)ws_get(ctx, WS_D01, (size_t)B * 2 * l * W * 8);
@@ -731,9 +794,9 @@ void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint3
     js.copy_E = E;
     HIPX(launch_ntt(ctx, x2c, js, B * l, true, ctx.ntt_mode, st));
     if (from_inputs)
-        relin_tail(ctx, d01, x2c, ext, B, l, evk, out, true, st, a, b, true);
+        relin_tail(ctx, d01, x2c, ext, B, l, evk, out, true, st, a, b, true, aff);
     else
-        relin_tail(ctx, d01, x2c, ext, B, l, evk, out, do_rescale, st, nullptr, nullptr, true);
+        relin_tail(ctx, d01, x2c, ext, B, l, evk, out, do_rescale, st, nullptr, nullptr, true, aff);
 }
 
 // Device workspace of hmult with the rescale (bytes): d01 2Bl, d2 Bl, extension B D E, inner product 2B E,
@@ -1230,13 +1293,6 @@ void mul_i(Context& ctx, const uint64_t* x, uint32_t n_polys, uint32_t l, int si
     HIPX(launch_mul_i(ctx, x, out, n_polys, l, sign, st));
 }
 
-static uint64_t residue_of(long double v, uint64_t q) {
-    const bool neg = v < 0;
-    const unsigned __int128 x = (unsigned __int128)(neg ? -v : v);
-    const uint64_t r = (uint64_t)(x % q);
-    return neg ? (r ? q - r : 0) : r;
-}
-
 // Linear combination of ciphertext batches [B][2][l_t][N] (term t at level levels[t], scale scales_in[t]):
 //  integer mode: sum_t round(c_t) x_t + round(a * scale_out) at level lt (every term at lt), no rescale;
 //  scalar mode:  every term read at lt + 1 limbs, multiplied by round(c_t scale_out q_lt / scales_in[t]),
@@ -1269,10 +1325,7 @@ void lincomb(Context& ctx, uint32_t B, uint32_t n_terms, const uint64_t* const* 
                             st));
         return;
     }
-    uint64_t* tmp = (uint64_t*)ws_get(ctx, WS_LIN, (size_t)B * 2 * lo * W * 8);
-    HIPX(launch_lincomb(ctx, tmp, B, lo, n_terms, x, stride.data(), C.data(), add_const != 0.0 ? add.data() : nullptr,
-                        st));
-    rescale(ctx, tmp, 2 * B, lo, out, st);
+    rescale_lincomb(ctx, B, lo, n_terms, x, stride.data(), C.data(), add_const != 0.0 ? add.data() : nullptr, out, st);
 }
 
 void add(Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys, uint32_t l,

@@ -52,14 +52,27 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
 // l-1 only and the combine forms the other limbs' d0 = a0 b0, d1 = a0 b1 + a1 b0 itself
 // x_from_ext (with ext and evk): limb l-1 and the P limbs of x are not read but formed as the evk inner product by
 // their inverse NTT (x receives them)
+// An integer affine map applied to a rescaled product as it is formed: out = factor * out + post (post on poly 0
+// only; both reduced mod q_i).  The words are those of the product followed by an integer linear combination.
+struct Affine {
+    int64_t factor;
+    int64_t post;
+};
+// aff (optional, a relinearization with ext only): the output is factor * out + post (Affine)
 void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
                      hipStream_t st, const uint64_t* ext = nullptr, const uint64_t* evk = nullptr,
-                     const uint64_t* ta = nullptr, const uint64_t* tb = nullptr, bool x_from_ext = false);
+                     const uint64_t* ta = nullptr, const uint64_t* tb = nullptr, bool x_from_ext = false,
+                     const Affine* aff = nullptr);
 void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
                uint64_t* out2, hipStream_t st, uint32_t add_div = 1, uint64_t x_bstride = 0);
 void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uint64_t* out, hipStream_t st);
+// out [B][2][lo-1][N] = rescale(sum_t C_t x_t + add): C [n_terms][lo], add [lo] or null (reduced mod q_i), term t read
+// at stride[t] limbs per poly; the combination is not stored under the two-pass NTT
+void rescale_lincomb(Context& ctx, uint32_t B, uint32_t lo, uint32_t n_terms, const uint64_t* const* x,
+                     const uint32_t* stride, const uint64_t* C, const uint64_t* add, uint64_t* out, hipStream_t st);
+// aff (with do_rescale only): the rescaled product becomes factor * product + post (Affine)
 void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint32_t l, const uint64_t* evk,
-           uint64_t* out, bool do_rescale, hipStream_t st);
+           uint64_t* out, bool do_rescale, hipStream_t st, const Affine* aff = nullptr);
 // hmult with the rescale, workspace and tables in the device scratch (no allocation); refuses shapes whose
 // workspace exceeds it
 size_t hmult_rescale_scratch_bytes(const Context& ctx, uint32_t B, uint32_t l);

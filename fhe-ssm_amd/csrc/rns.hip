@@ -1008,6 +1008,7 @@ struct LinArgs {
     const uint64_t* x[kMaxTerms];
     uint32_t stride[kMaxTerms];
     uint32_t n_terms, l_out, has_add;
+    uint32_t i0;  // limbs i0 .. i0 + l_out - 1 are formed (out holds l_out limbs per poly; C and add are per out limb)
     uint64_t C[kMaxTerms][kMaxLcLimbs];
     uint64_t add[kMaxLcLimbs];
 };
@@ -1015,7 +1016,7 @@ struct LinArgs {
 __global__ __launch_bounds__(256) void k_lincomb(uint64_t* __restrict__ out, LinArgs la,
                                                  const PrimeInfo* __restrict__ primes) {
     const uint32_t k = blockIdx.x * 256 + threadIdx.x;
-    const uint32_t i = blockIdx.y, pc = blockIdx.z;  // pc = 2 c + poly
+    const uint32_t j = blockIdx.y, i = la.i0 + j, pc = blockIdx.z;  // out limb j is limb i; pc = 2 c + poly
     const uint32_t c = pc >> 1, p = pc & 1;
     const Barrett br = barrett_of(primes[i]);
     Acc acc;  // at most kMaxTerms = 8 terms
@@ -1025,12 +1026,12 @@ __global__ __launch_bounds__(256) void k_lincomb(uint64_t* __restrict__ out, Lin
         if (t < (int)la.n_terms) v[t] = la.x[t][((size_t)(2 * c + p) * la.stride[t] + i) * kN + k];
 #pragma unroll
     for (int t = 0; t < kMaxTerms; t++)
-        if (t < (int)la.n_terms) acc.add(v[t], la.C[t][i]);
+        if (t < (int)la.n_terms) acc.add(v[t], la.C[t][j]);
     // the coefficients carry a factor R = 2^64 (C R mod q_i), so the REDC of the sum is the combination itself;
     // at most 8 products of residues below q < 2^60 keep the sum below q R
     uint64_t r = redc(acc.get(), br.q, primes[i].mont_ninv);
-    if (la.has_add && p == 0) r = add_mod(r, la.add[i], br.q);
-    __builtin_nontemporal_store(r, &out[((size_t)pc * la.l_out + i) * kN + k]);
+    if (la.has_add && p == 0) r = add_mod(r, la.add[j], br.q);
+    __builtin_nontemporal_store(r, &out[((size_t)pc * la.l_out + j) * kN + k]);
 }
 
 // multiply by X^(N/2) (slot-wise by +-i): evaluation slot k holds a(psi^(2 brev(k)+1)); X^(N/2) there is
@@ -1522,18 +1523,21 @@ hipError_t launch_sum_list(const Context& ctx, const uint64_t* const* in, uint32
 
 hipError_t launch_lincomb(const Context& ctx, uint64_t* out, uint32_t B, uint32_t l_out, uint32_t n_terms,
                           const uint64_t* const* x, const uint32_t* stride, const uint64_t* C /*[n_terms][l_out]*/,
-                          const uint64_t* add /*[l_out] or null*/, hipStream_t st) {
+                          const uint64_t* add /*[l_out] or null*/, hipStream_t st, uint32_t i0) {
     if (n_terms == 0 || n_terms > (uint32_t)kMaxTerms || l_out > (uint32_t)kMaxLcLimbs) return hipErrorInvalidValue;
+    for (uint32_t t = 0; t < n_terms; t++)
+        if (i0 + l_out > stride[t]) return hipErrorInvalidValue;
     LinArgs la{};
     la.n_terms = n_terms;
     la.l_out = l_out;
+    la.i0 = i0;
     la.has_add = add ? 1 : 0;
     for (uint32_t t = 0; t < n_terms; t++) {
         la.x[t] = x[t];
         la.stride[t] = stride[t];
         for (uint32_t i = 0; i < l_out; i++) {
             // C R mod q_i (k_lincomb reduces by REDC), a Shoup product by the context's R mod q_i
-            const PrimeInfo& pr = ctx.primes[i];
+            const PrimeInfo& pr = ctx.primes[i0 + i];
             const uint64_t c = C[(size_t)t * l_out + i] % pr.q;
             const uint64_t h = (uint64_t)(((unsigned __int128)c * pr.r_mod_p) >> 64);
             const uint64_t v = c * pr.r_mod - h * pr.q;
