@@ -222,3 +222,46 @@ def test_shared_plan_matches_a_plan_of_its_own(ckks):
         bits = -np.log2(np.max(np.abs(outs[name] - z)))
         print(f"{name} plan: {bits:.2f} bits")
         assert bits > 14.0, (name, bits)
+
+
+@pytest.mark.timeout(900)
+def test_bootstrap_words_equal_across_ntt_modes(ckks):
+    """The two-pass NTT's fused combines (a scalar combination formed inside its rescale's combine, the Chebyshev
+    doubling 2 T^2 - 1 applied by the relinearization's ModDown combine, the key-switch combines) against the fused-NTT
+    mode, which runs each of those steps as a kernel of its own (lincomb then rescale, ModDown then an integer
+    lincomb): a config-4 bootstrap and a five-term scalar combination come out word for word equal"""
+    make, Kr, deg, r, top, ins, hs = CHAINS["config4"]
+    ctx = make(ckks)
+    bt = ckks.Bootstrap(ctx, K=Kr, cheb_degree=deg, double_angles=r, top_scale=top, in_scale=ins)
+    sk = ctx.secret(b"M" * 32, 192)
+    bk = BootKeys(ckks, ctx, bt, sk, 9, hs)
+    rng = np.random.default_rng(47)
+    z = rng.uniform(-1.0, 1.0, SLOTS)
+    pt = ckks.DeviceBuffer(N * 8)
+    ct = ckks.DeviceBuffer(2 * N * 8)
+    ctx.encode(z, 1, ins, pt.ptr)
+    ctx.encrypt(sk, pt.ptr, 1, b"g" * 32, 0, ct.ptr)
+    B, lt = 2, 17
+    terms = []
+    for lv in (20, 21, 22, 23, 24):
+        t = ckks.DeviceBuffer(B * 2 * lv * N * 8)
+        q = np.array(ctx.moduli[:lv], dtype=np.uint64)[None, None, :, None]
+        t.upload(rng.integers(0, 2**62, (B, 2, lv, N), dtype=np.uint64) % q)
+        terms.append((t, lv))
+    scales = [ctx.scale * (1 + 0.001 * t) for t in range(5)]
+    words = {}
+    try:
+        for mode in (0, 1):
+            ctx.set_ntt_mode(mode)
+            out = ckks.DeviceBuffer(2 * bt.out_level * N * 8)
+            bt.run(ct.ptr, bk.relin.ptr, bk.conj.ptr, bk.keys, out.ptr)
+            lc = ckks.DeviceBuffer(B * 2 * lt * N * 8)
+            ctx.eval_lincomb(B, [t.ptr for t, _ in terms], [lv for _, lv in terms], [0.3, -1.7, 2.5, 0.01, -0.6],
+                             scales, ctx.scale, 0.25, lt, False, lc.ptr)
+            words[mode] = (out.download((2, bt.out_level, N)), lc.download((B, 2, lt, N)))
+    finally:
+        ctx.set_ntt_mode(0)
+    assert np.array_equal(words[0][0], words[1][0])
+    assert np.array_equal(words[0][1], words[1][1])
+    got = ctx.decrypt(sk, ct.ptr, 1, ins)
+    assert np.max(np.abs(got - z)) < 1e-9
