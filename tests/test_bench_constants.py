@@ -25,7 +25,7 @@ def test_hmult_constants_match_the_profile():
     rows = counter_rows(path)
     # the dominant launch: T's forward NTT, pass A over 2,944 limbs plus the pass B that ends in the combine
     a = [r for r in rows["k_ntt_fwd_a"] if abs(r[0] - 1.545) < 0.05]
-    b = rows["k_ntt_fwd_b_mdr<3, true>"][0]
+    b = rows["k_ntt_fwd_b_mdr<3, true, false>"][0]
     assert len(a) == 1
     traffic = (a[0][0] + a[0][1] + b[0] + b[1]) * 1e9
     valu = (a[0][2] + b[2]) * 1e6
