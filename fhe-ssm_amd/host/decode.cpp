@@ -26,6 +26,7 @@
 #include <map>
 #include <memory>
 #include <set>
+#include <sstream>
 #include <stdexcept>
 #include <string>
 #include <tuple>
@@ -55,6 +56,11 @@ struct Error : std::runtime_error {
 
 void ck(int rc, const char* what) {
     if (rc != CKKS_OK) throw Error(rc, std::string(what) + ": " + ckks_last_error());
+}
+
+// the store file's calls report through this library's own message
+void ck_store(int rc, const char* what) {
+    if (rc != CKKS_OK) throw Error(rc, std::string(what) + ": " + g_err);
 }
 
 // ------------------------------------------------------------------ device buffers
@@ -741,6 +747,98 @@ class Decoder {
         dst.assign(data, data + count);
     }
 
+    // ---- the matvec coefficient store in a store file (the reference's --store-file, gpu_real_model.cu:1887-2141)
+    // One entry per matvec: key (layer, op, n_out, n_in, n_diag, nb, level) with op 1 tm, 2 wo, 3 ck, 4 cv (its
+    // 1024-periodic diagonals' small-ring coefficients [n_diag][2048] int64 and their [n_diag] int32 approxFactor
+    // exponents, as 64-bit words).  The stamp names what the coefficients depend on -- ring, slot layout, the
+    // context's moduli, the plan's scale table, every weight -- so a store made for another model or chain is refused.
+    static constexpr const char* kMvOps[5] = {"", "tm", "wo", "ck", "cv"};
+
+    std::string store_stamp() const {
+        auto fnv = [](uint64_t h, uint64_t v) { return (h ^ v) * 1099511628211ULL; };
+        auto dbits = [](double d) {
+            uint64_t u;
+            std::memcpy(&u, &d, 8);
+            return u;
+        };
+        uint32_t n = 0, nq = 0, np = 0, dnum = 0;
+        ck(ckks_context_info(be_->ctx(), &n, &nq, &np, &dnum), "ckks_context_info");
+        std::vector<uint64_t> mod(2 * (nq + np));
+        ck(ckks_context_moduli(be_->ctx(), mod.data(), (uint32_t)mod.size()), "ckks_context_moduli");
+        uint64_t qh = 1469598103934665603ULL, sh = qh, wh = qh;
+        for (uint32_t i = 0; i < nq + np; i++) qh = fnv(qh, mod[i]);
+        for (uint32_t l = 1; l <= be_->top_level(); l++) sh = fnv(sh, dbits(be_->S(l)));
+        auto mix_w = [&](const LayerW& w, int32_t layer) {
+            for (const auto& kv : w.v) {
+                wh = fnv(wh, (uint64_t)(uint32_t)layer);
+                for (unsigned char ch : kv.first) wh = fnv(wh, ch);
+                for (double d : kv.second) wh = fnv(wh, dbits(d));
+            }
+        };
+        for (size_t li = 0; li < layers_.size(); li++) mix_w(layers_[li], (int32_t)li);
+        mix_w(model_, -1);
+        std::ostringstream st;
+        st << "fhe-ssm-amd-matvec-coeffs-v1|ring=" << n << "|dpad=" << DPAD << "|logRep=" << LOG_REP
+           << "|layers=" << layers_.size() << "|nq=" << nq << "|qhash=" << qh << "|scaleHash=" << sh
+           << "|weightHash=" << wh;
+        return st.str();
+    }
+
+    uint64_t store_save(const char* path) {
+        fhe_ssm_store* st = nullptr;
+        ck_store(fhe_ssm_store_create(&st), "fhe_ssm_store_create");
+        std::unique_ptr<fhe_ssm_store, void (*)(fhe_ssm_store*)> hold(st, fhe_ssm_store_destroy);
+        for (const auto& kv : mv_) {
+            const std::string& name = kv.first.first;
+            int op = 0;
+            for (int o = 1; o < 5; o++)
+                if (name.compare(0, 2, kMvOps[o]) == 0) op = o;
+            if (op == 0) throw Error(CKKS_EINVAL, "store: unknown matvec " + name);
+            const Matvec& m = kv.second;
+            const int32_t key[7] = {std::stoi(name.substr(2)), op, (int32_t)m.n_out, (int32_t)m.n_in,
+                                    (int32_t)m.n_diag, (int32_t)m.nb, (int32_t)m.level};
+            std::vector<uint64_t> w((m.coef->bytes + 7) / 8, 0);
+            std::memcpy(w.data(), m.coef->p, m.coef->bytes);
+            ck_store(fhe_ssm_store_put(st, key, w.data(), w.size()), "fhe_ssm_store_put");
+        }
+        ck_store(fhe_ssm_store_save(st, path, store_stamp().c_str()), "fhe_ssm_store_save");
+        return mv_.size();
+    }
+
+    // the matvecs of a store file (stamp checked) in place of encoding them on first use
+    uint64_t store_load(const char* path) {
+        if (!mv_.empty()) throw Error(CKKS_EINVAL, "store: the matvecs are already encoded (load before the first step)");
+        fhe_ssm_store* st = nullptr;
+        ck_store(fhe_ssm_store_create(&st), "fhe_ssm_store_create");
+        std::unique_ptr<fhe_ssm_store, void (*)(fhe_ssm_store*)> hold(st, fhe_ssm_store_destroy);
+        uint64_t n = 0;
+        ck_store(fhe_ssm_store_load(st, path, store_stamp().c_str(), 0, 0, &n), "fhe_ssm_store_load");
+        std::map<std::pair<std::string, uint32_t>, Matvec> got;
+        for (uint64_t i = 0; i < n; i++) {
+            int32_t key[7];
+            uint64_t len = 0;
+            ck_store(fhe_ssm_store_entry(st, i, key, &len), "fhe_ssm_store_entry");
+            if (key[1] < 1 || key[1] > 4 || key[0] < 0 || key[0] >= (int32_t)layers_.size() || key[4] <= 0 ||
+                key[6] <= 0 || (uint32_t)key[6] > be_->top_level())
+                throw Error(CKKS_EINVAL, "store: entry " + std::to_string(i) + " is not a matvec of this model");
+            Matvec m;
+            m.n_out = (uint32_t)key[2];
+            m.n_in = (uint32_t)key[3];
+            m.n_diag = (uint32_t)key[4];
+            m.nb = (uint32_t)key[5];
+            m.level = (uint32_t)key[6];
+            const size_t bytes = (size_t)m.n_diag * ((kN >> LOG_REP) * 8 + 4);
+            if (len != (bytes + 7) / 8) throw Error(CKKS_EINVAL, "store: entry " + std::to_string(i) + " length");
+            m.coef = std::make_shared<HostBuf>(bytes);
+            std::vector<uint64_t> w(len);
+            ck_store(fhe_ssm_store_get(st, key, w.data(), len, &len), "fhe_ssm_store_get");
+            std::memcpy(m.coef->p, w.data(), bytes);
+            got.emplace(std::make_pair(std::string(kMvOps[key[1]]) + std::to_string(key[0]), m.level), std::move(m));
+        }
+        mv_ = std::move(got);
+        return n;
+    }
+
     // One step over the carried state.  The step works on a copy of the state (handles: the ciphertexts are shared,
     // never written in place) and commits it only once every layer has succeeded, so a step that throws leaves the
     // state of the previous step in place (the reference commits its carry after the whole pass,
@@ -1412,6 +1510,22 @@ int fhe_ssm_decoder_set_weight(fhe_ssm_decoder* dec, const char* name, int32_t l
     return guarded([&] {
         if (!dec || !name || !data) throw Error(CKKS_EINVAL, "null argument");
         dec->dec->set_weight(name, layer, data, count);
+    });
+}
+
+int fhe_ssm_decoder_store_save(fhe_ssm_decoder* dec, const char* path, uint64_t* n_entries) {
+    return guarded([&] {
+        if (!dec || !path) throw Error(CKKS_EINVAL, "null argument");
+        const uint64_t n = dec->dec->store_save(path);
+        if (n_entries) *n_entries = n;
+    });
+}
+
+int fhe_ssm_decoder_store_load(fhe_ssm_decoder* dec, const char* path, uint64_t* n_entries) {
+    return guarded([&] {
+        if (!dec || !path) throw Error(CKKS_EINVAL, "null argument");
+        const uint64_t n = dec->dec->store_load(path);
+        if (n_entries) *n_entries = n;
     });
 }
 

@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(HERE, "libfhe_ssm_decode.so")
 
 _vp = ctypes.c_void_p
 _u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
 _int = ctypes.c_int
 
 
@@ -60,6 +61,20 @@ SIGNATURES = {
     "fhe_ssm_client_encrypt_rows": (_int, [_vp, _vp, ctypes.c_char_p, _u32, _u32, _u32, _u32, _u32,
                                            ctypes.c_double, _vp]),
     "fhe_ssm_client_decrypt_logits": (_int, [_vp, _vp, ctypes.c_char_p, _vp, _u32, _u32, _u32]),
+    "fhe_ssm_store_create": (_int, [ctypes.POINTER(_vp)]),
+    "fhe_ssm_store_destroy": (None, [_vp]),
+    "fhe_ssm_store_put": (_int, [_vp, _vp, _vp, _u64]),
+    "fhe_ssm_store_count": (_int, [_vp, ctypes.POINTER(_u64)]),
+    "fhe_ssm_store_entry": (_int, [_vp, _u64, _vp, ctypes.POINTER(_u64)]),
+    "fhe_ssm_store_get": (_int, [_vp, _vp, _vp, _u64, ctypes.POINTER(_u64)]),
+    "fhe_ssm_store_save": (_int, [_vp, ctypes.c_char_p, ctypes.c_char_p]),
+    "fhe_ssm_store_load": (_int, [_vp, ctypes.c_char_p, ctypes.c_char_p, _u32, _u32, ctypes.POINTER(_u64)]),
+    "fhe_ssm_store_read_stamp": (_int, [ctypes.c_char_p, _vp, _u64, ctypes.POINTER(_u64)]),
+    "fhe_ssm_store_append": (_int, [ctypes.c_char_p, _vp, _vp, _u64]),
+    "fhe_ssm_store_load_journal": (_int, [_vp, ctypes.c_char_p, _u32, _u32, ctypes.POINTER(_u64),
+                                          ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "fhe_ssm_decoder_store_save": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_u64)]),
+    "fhe_ssm_decoder_store_load": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_u64)]),
 }
 
 LAYER_WEIGHTS = ("g1", "g2", "k_k", "mu_r", "mu_k", "mu_v", "mu_w", "mu_a", "mu_g", "mu_c", "W_r", "W_k", "W_v",
@@ -134,6 +149,18 @@ class NativeDecoder:
     def reset(self) -> None:
         """drop the carried state: the next step starts cold"""
         check(load().fhe_ssm_decoder_reset(self.h))
+
+    def store_save(self, path: str) -> int:
+        """write the matvecs encoded so far to a store file; returns their number"""
+        n = _u64()
+        check(load().fhe_ssm_decoder_store_save(self.h, path.encode(), ctypes.byref(n)))
+        return n.value
+
+    def store_load(self, path: str) -> int:
+        """take the matvecs from a store file (stamp-checked) instead of encoding them; before the first step"""
+        n = _u64()
+        check(load().fhe_ssm_decoder_store_load(self.h, path.encode(), ctypes.byref(n)))
+        return n.value
 
     def memory(self) -> dict:
         """bytes the decoder holds: elementwise plaintexts, diagonal staging/expansion buffers, ciphertext pool (all
@@ -220,3 +247,89 @@ def client_decrypt_logits(ctx, sk, in_prefix: str, head: np.ndarray, dpad: int) 
     head = np.ascontiguousarray(head, dtype=np.float64)
     check(load().fhe_ssm_client_decrypt_logits(ctx.h, sk.h, in_prefix.encode(), head.ctypes.data, head.shape[0],
                                                head.shape[1], dpad))
+
+
+# ---- the store file (base + journal), host only ---------------------------------------------------------------------
+def _key7(key) -> np.ndarray:
+    k = np.ascontiguousarray(np.asarray(key, dtype=np.int32))
+    if k.shape != (7,):
+        raise ValueError("a store key has 7 fields (layer, op, chunk, rowOff, diag, half, lvl)")
+    return k
+
+
+class Store:
+    """An in-memory store of (7-field key -> uint64 words) entries, read from and written to the store file format."""
+
+    def __init__(self):
+        h = _vp()
+        check(load().fhe_ssm_store_create(ctypes.byref(h)))
+        self.h = h.value
+
+    def put(self, key, words) -> None:
+        k = _key7(key)
+        w = np.ascontiguousarray(np.asarray(words, dtype=np.uint64))
+        check(load().fhe_ssm_store_put(self.h, k.ctypes.data, w.ctypes.data if w.size else None, w.size))
+
+    def __len__(self) -> int:
+        n = _u64()
+        check(load().fhe_ssm_store_count(self.h, ctypes.byref(n)))
+        return n.value
+
+    def keys(self) -> list:
+        out = []
+        for i in range(len(self)):
+            k = np.zeros(7, dtype=np.int32)
+            n = _u64()
+            check(load().fhe_ssm_store_entry(self.h, i, k.ctypes.data, ctypes.byref(n)))
+            out.append(tuple(int(x) for x in k))
+        return out
+
+    def get(self, key) -> np.ndarray:
+        k = _key7(key)
+        n = _u64()
+        check(load().fhe_ssm_store_get(self.h, k.ctypes.data, None, 0, ctypes.byref(n)))
+        w = np.zeros(n.value, dtype=np.uint64)
+        check(load().fhe_ssm_store_get(self.h, k.ctypes.data, w.ctypes.data if w.size else None, w.size,
+                                       ctypes.byref(n)))
+        return w
+
+    def save(self, path: str, stamp: str) -> None:
+        check(load().fhe_ssm_store_save(self.h, path.encode(), stamp.encode()))
+
+    def load(self, path: str, stamp=None, depth: int = 0, comp_cw: int = 0) -> int:
+        n = _u64()
+        check(load().fhe_ssm_store_load(self.h, path.encode(), stamp.encode() if stamp is not None else None, depth,
+                                        comp_cw, ctypes.byref(n)))
+        return n.value
+
+    def load_journal(self, journal_path: str, depth: int = 0, comp_cw: int = 0) -> dict:
+        g, d, b = _u64(), _u64(), _u64()
+        check(load().fhe_ssm_store_load_journal(self.h, journal_path.encode(), depth, comp_cw, ctypes.byref(g),
+                                                ctypes.byref(d), ctypes.byref(b)))
+        return {"good": g.value, "duplicates": d.value, "dropped_bytes": b.value}
+
+    def close(self) -> None:
+        if self.h:
+            load().fhe_ssm_store_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def store_append(journal_path: str, key, words) -> None:
+    """one self-checksummed record appended to a store journal"""
+    k = _key7(key)
+    w = np.ascontiguousarray(np.asarray(words, dtype=np.uint64))
+    check(load().fhe_ssm_store_append(journal_path.encode(), k.ctypes.data, w.ctypes.data if w.size else None, w.size))
+
+
+def store_read_stamp(path: str) -> str:
+    n = _u64()
+    check(load().fhe_ssm_store_read_stamp(path.encode(), None, 0, ctypes.byref(n)))
+    buf = ctypes.create_string_buffer(n.value + 1)
+    check(load().fhe_ssm_store_read_stamp(path.encode(), ctypes.cast(buf, _vp), n.value + 1, ctypes.byref(n)))
+    return buf.value.decode()

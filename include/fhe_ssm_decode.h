@@ -81,6 +81,46 @@ int fhe_ssm_decoder_reset(fhe_ssm_decoder* dec);
  * coefficients.  Fills min(n, 6) entries. */
 int fhe_ssm_decoder_memory(const fhe_ssm_decoder* dec, uint64_t* bytes, uint32_t n);
 
+/* ---- the compressed plaintext store file (the reference's --store-file with its append journal,
+ * gpu_real_model.cu:1887-2141) ---------------------------------------------------------------------------------
+ * Base file: "FHESSMSTORE1" and 4 zero bytes, u64 stamp length (1..4096), the stamp, u64 entry count (<= 10^8), per
+ * entry 7 int32 key fields (layer, op, chunk, rowOff, diag, half, lvl), u64 word count and the words (u64), then an
+ * FNV-1a hash over 64-bit words (offset basis 1469598103934665603, prime 1099511628211) of every entry's key fields
+ * (each the u64 of its uint32), word count and words.  Written
+ * whole through PATH.tmp and a rename.  Journal (conventionally PATH.journal): appended records of key fields, word
+ * count, words and the FNV of that record; on load a record cut short or failing its hash ends the journal and the
+ * file is truncated to the good prefix (a process killed mid-append loses that record only).  Length rule (depth > 0,
+ * the reference's check): an entry's lvl lies in [0, depth] and it holds 0 (dead) or (depth + 1 - lvl) comp_cw words,
+ * the limbs of a compressed plaintext (comp_cw = N / REP words per limb; such an entry is a plaintext
+ * ckks_eval_mult_plain_ex takes with log_rep = log2 REP).  depth = 0: no length rule.
+ * fhe_ssm_store_load refuses a bad magic, a stamp other than `stamp` (null: any), a truncated file, a broken rule, a
+ * key already present and a checksum mismatch; entries are listed in key order. */
+typedef struct fhe_ssm_store fhe_ssm_store;
+int fhe_ssm_store_create(fhe_ssm_store** st);
+void fhe_ssm_store_destroy(fhe_ssm_store* st);
+int fhe_ssm_store_put(fhe_ssm_store* st, const int32_t* key7, const uint64_t* words, uint64_t n_words);
+int fhe_ssm_store_count(const fhe_ssm_store* st, uint64_t* n);
+int fhe_ssm_store_entry(const fhe_ssm_store* st, uint64_t i, int32_t* key7, uint64_t* n_words);
+/* words may be null (the length only); cap: words the buffer holds */
+int fhe_ssm_store_get(const fhe_ssm_store* st, const int32_t* key7, uint64_t* words, uint64_t cap, uint64_t* n_words);
+int fhe_ssm_store_save(const fhe_ssm_store* st, const char* path, const char* stamp);
+int fhe_ssm_store_load(fhe_ssm_store* st, const char* path, const char* stamp, uint32_t depth, uint32_t comp_cw,
+                       uint64_t* n_loaded);
+/* the stamp of a store file (*len bytes; stamp, if given, receives it NUL-terminated, cap >= *len + 1) */
+int fhe_ssm_store_read_stamp(const char* path, char* stamp, uint64_t cap, uint64_t* len);
+int fhe_ssm_store_append(const char* journal_path, const int32_t* key7, const uint64_t* words, uint64_t n_words);
+/* good: records added; duplicates: records whose key was present (skipped); dropped_bytes: the torn tail removed */
+int fhe_ssm_store_load_journal(fhe_ssm_store* st, const char* journal_path, uint32_t depth, uint32_t comp_cw,
+                               uint64_t* good, uint64_t* duplicates, uint64_t* dropped_bytes);
+
+/* The decoder's matvec store in a store file: fhe_ssm_decoder_store_save writes every matvec encoded so far (one
+ * entry each: key (layer, op 1 tm / 2 wo / 3 ck / 4 cv, n_out, n_in, n_diag, nb, level), the small-ring coefficients
+ * of its 1024-periodic diagonals and their approxFactor exponents as words); fhe_ssm_decoder_store_load, before the
+ * first step, takes them from the file instead of encoding them.  The stamp names the ring, the slot layout, the
+ * context's moduli, the plan's scales and every weight: a file made for anything else is refused. */
+int fhe_ssm_decoder_store_save(fhe_ssm_decoder* dec, const char* path, uint64_t* n_entries);
+int fhe_ssm_decoder_store_load(fhe_ssm_decoder* dec, const char* path, uint64_t* n_entries);
+
 /* ---- the serve-directory protocol (the reference's persistent --serve DIR loop, gpu_real_model.cu:4363-4483 and
  * :5525-5576; its client is ml-eval/fhe_client.py:1394-1492) -------------------------------------------------
  * Inside dir, request N: the client writes req.N.0 .. req.N.<count-1> (ciphertext files, ckks_ct_save's layout),

@@ -403,6 +403,36 @@ def test_native_decoder_matches_python_plan(engine, DS, M):
 
 
 @pytest.mark.timeout(900)
+def test_native_decoder_store_file(engine, M, tmp_path):
+    """the matvec coefficients a decoder encoded, saved to a store file and loaded by a fresh decoder with the same
+    weights: its first step (no matvec encoded) gives the first decoder's output word for word; a decoder with other
+    weights refuses the file (its stamp names them)"""
+    ND = load_module("native_decode")
+    be, sk = engine
+    W = M.make_weights(5, n_layers=1)
+    x = be.encrypt(sk, M.pack_lanes(M.embed_tokens(np.arange(32) + 3)), be.top_level, seed=bytes([9, 1]) * 16)
+    a = ND.from_backend(be, 1)
+    a.set_weights(W)
+    out_a, lv, sc = a.step(x.ptr(), x.level, x.scale)
+    path = str(tmp_path / "matvec.store")
+    n = a.store_save(path)
+    assert n >= 4  # the layer's tm, wo, ck, cv
+    assert ND.store_read_stamp(path).startswith("fhe-ssm-amd-matvec-coeffs-v1|ring=65536|dpad=1024")
+    b = ND.from_backend(be, 1)
+    b.set_weights(W)
+    assert b.store_load(path) == n
+    out_b, lv_b, sc_b = b.step(x.ptr(), x.level, x.scale)
+    assert (lv_b, sc_b) == (lv, sc)
+    assert np.array_equal(out_b.download((2, lv, N)), out_a.download((2, lv, N)))
+    c = ND.from_backend(be, 1)
+    c.set_weights(M.make_weights(6, n_layers=1))
+    with pytest.raises(RuntimeError, match="different configuration"):
+        c.store_load(path)
+    for d in (a, b, c):
+        d.close()
+
+
+@pytest.mark.timeout(900)
 def test_native_decoder_serves_a_directory(engine, M, tmp_path):
     """the serve-directory protocol with the decode step as its handler (one layer): a stateful session -- two
     tokens with the reset marker, a two-token request whose second file is bad (it fails after one step; the carried
