@@ -631,7 +631,7 @@ __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__
 // 4 wave-rows take the giant steps g = row, row + 4, ...; every diagonal word is read exactly once and each
 // wave reads 64 consecutive words (512 B) per diagonal.
 constexpr int kMaxBaby = 64;
-constexpr int kMacCoef = 64;
+constexpr int kMacCoef = 64;  // one wave64 per MAC row
 constexpr int kMacRows = 8;
 
 // The giant sums of a BSGS MAC from babies staged in LDS (sb: word kk of baby j, poly p at (2 j + p) kMacCoef + kk):
@@ -746,7 +746,9 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_mac(ListPtrs baby,
                                                                   const PrimeInfo* __restrict__ primes) {
     extern __shared__ uint64_t sb[];
     const ListTile lt = list_tile(n_inst, kN / kMacCoef);
-    const uint32_t kk = threadIdx.x & (kMacCoef - 1), row = threadIdx.x / kMacCoef;
+    // a row is one wave (kMacCoef = 64 lanes): its index, and every baby / giant index derived from it, is wave-uniform
+    // and lives in scalar registers (left to the compiler, the per-baby division and addressing ran on the VALU)
+    const uint32_t kk = threadIdx.x & (kMacCoef - 1), row = __builtin_amdgcn_readfirstlane(threadIdx.x / kMacCoef);
     const uint32_t k = lt.kt * kMacCoef + kk;
     const uint32_t i = lt.limb;  // limb; limbs from l_q on are P limbs (prime Lp + i - l_q)
     const Barrett br = barrett_of(primes[i < l_q ? i : Lp + (i - l_q)]);
@@ -826,7 +828,9 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
     const uint32_t xcd = blockIdx.x & 7, qi = blockIdx.x >> 3;
     const uint32_t s = qi % a.n_inst, seq = xcd * (a.E * (kN / kMacCoef) / 8) + qi / a.n_inst;
     const uint32_t t = seq / (kN / kMacCoef);
-    const uint32_t kk = threadIdx.x & (kMacCoef - 1), row = threadIdx.x / kMacCoef;
+    // a row is one wave (kMacCoef = 64 lanes): its index, and every baby / giant index derived from it, is wave-uniform
+    // and lives in scalar registers (left to the compiler, the per-baby division and addressing ran on the VALU)
+    const uint32_t kk = threadIdx.x & (kMacCoef - 1), row = __builtin_amdgcn_readfirstlane(threadIdx.x / kMacCoef);
     const uint32_t k = chain_tile(seq % (kN / kMacCoef), a.chain_delta) * kMacCoef + kk;
     const bool qlimb = t < a.l;
     const uint32_t pi = qlimb ? t : a.L + (t - a.l);
@@ -851,15 +855,22 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
                 e0[d] = ep[((size_t)d * 2 + 0) * a.T * kN];
                 e1[d] = ep[((size_t)d * 2 + 1) * a.T * kN];
             }
+            const uint64_t c0 = qlimb ? sx[0] : 0;
             Acc s0, s1;  // at most kMaxDigits = 8 terms
 #pragma unroll
             for (int d = 0; d < ND; d++) {
                 s0.add(xv[d], e0[d]);
                 s1.add(xv[d], e1[d]);
             }
-            // REDC: sums of at most 8 products of residues below q < 2^60 stay below q 2^64
+            // P c0 joins the poly-0 sum (P mod q_t times c0: the REDC below takes the whole sum to R^-1 scale, the
+            // baby's form), instead of a Shoup product by P R^-1 and a modular add after it.  REDC: sums of at most
+            // 9 products of residues below q < 2^60 stay below q 2^64; the accumulator folds its cross sums first
+            // when 8 terms are already in
+            if (qlimb) {
+                if (ND >= 8) s0.fold();
+                s0.add(c0, primes[pi].pmod);
+            }
             v0 = redc(s0.get(), q, ninv);
-            if (qlimb) v0 = add_mod(v0, shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q), q);
             v1 = redc(s1.get(), q, ninv);
         } else if (qlimb) {
             v0 = shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q);
