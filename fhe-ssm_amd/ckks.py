@@ -85,6 +85,7 @@ SIGNATURES = {
     "ckks_eval_add_plain": (_int, [_vp, _vp, _u32, _u32, _vp, _int, _vp, _vp]),
     "ckks_eval_rotate_hoisted": (_int, [_vp, _vp, _u32, _vp, _u32, _vp, _vp, _vp]),
     "ckks_eval_rotate_many": (_int, [_vp, _vp, _u32, _u32, _vp, _vp, _vp, _vp]),
+    "ckks_eval_rotate_sum": (_int, [_vp, _vp, _u32, _u32, _vp, _u32, _vp, _vp, _vp]),
     "ckks_linear_transform_bsgs": (_int, [_vp, _vp, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _vp]),
     "ckks_gen_primes": (_int, [_u32, _u32, _vp, _u32, _vp]),
     "ckks_encode_periodic": (_int, [_vp, _vp, _vp, _u32, _u32, _u32, ctypes.c_double, _vp]),
@@ -320,6 +321,12 @@ class Context:
         st = np.ascontiguousarray(np.asarray(steps, dtype=np.int64))
         keys = _ptr_array(d_evks)
         check(load().ckks_eval_rotate_hoisted(self.h, d_ct, level, _ptr(st), len(st), keys, d_out, stream))
+
+    def eval_rotate_sum(self, d_ct, batch, level, steps, d_evks, d_out, stream=None):
+        """out = ct + sum_i Rot_{steps[i]}(ct), the rotations hoisted over one ModUp and one ModDown"""
+        st = np.ascontiguousarray(np.asarray(steps, dtype=np.int64))
+        keys = _ptr_array(d_evks)
+        check(load().ckks_eval_rotate_sum(self.h, d_ct, batch, level, _ptr(st), len(st), keys, d_out, stream))
 
     def eval_rotate_many(self, d_cts, level, steps, d_evks, d_out, stream=None):
         st = np.ascontiguousarray(np.asarray(steps, dtype=np.int64))

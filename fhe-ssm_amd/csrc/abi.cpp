@@ -427,6 +427,22 @@ int ckks_eval_rotate_hoisted(ckks_context* ctx, const uint64_t* d_ct, uint32_t l
     });
 }
 
+int ckks_eval_rotate_sum(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level, const int64_t* steps,
+                         uint32_t n, const uint64_t* const* d_evks, uint64_t* d_out, void* stream) {
+    if (int rc = check_ctx_level(ctx, level, true)) return rc;
+    if (!d_ct || !steps || !d_evks || !d_out) return fail(CKKS_EINVAL, "null argument");
+    if (n == 0 || n > 64) return fail(CKKS_EINVAL, "1..64 rotations per sum");
+    for (uint32_t i = 0; i < n; i++) {
+        if (!d_evks[i]) return fail(CKKS_EINVAL, "null key");
+        if (fhe::rotation_index(steps[i]) == 1) return fail(CKKS_EINVAL, "a step of the identity (no key switch)");
+    }
+    if (!batch) return CKKS_OK;
+    return guarded([&] {
+        fhe::rotate_sum(ctx->c, d_ct, batch, level, steps, n, d_evks, d_out, (hipStream_t)stream);
+        return CKKS_OK;
+    });
+}
+
 int ckks_eval_rotate_many(ckks_context* ctx, const uint64_t* d_cts, uint32_t n, uint32_t level, const int64_t* steps,
                           const uint64_t* const* d_evks, uint64_t* d_out, void* stream) {
     if (int rc = check_ctx_level(ctx, level, true)) return rc;

@@ -889,6 +889,30 @@ uint32_t rotation_index(int64_t k) {
     return (uint32_t)r;
 }
 
+// out = ct + sum_j Rot_{steps[j]}(ct) for each of B ciphertexts [B][2][l][N] (a rotate-and-add window, e.g. a sum
+// over a lane's slots): the n rotations share one ModUp of c1 and are summed in Q_l P -- sum_j Auto_j(<ext, evk_j> +
+// (P c0, 0)) + P ct (k_qp_rot_sum) -- before a single ModDown, so a sum of n rotations costs one key switch's ModUp and
+// ModDown plus n inner products.  The words differ from n separate rotations only in the key-switching rounding (one
+// ModDown instead of n).
+void rotate_sum(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const int64_t* steps, uint32_t n,
+                const uint64_t* const* evk, uint64_t* out, hipStream_t st) {
+    check_level(ctx, l);
+    if (n == 0 || n > 64) throw std::invalid_argument("1..64 rotations per sum");
+    if (B == 0) return;
+    const uint32_t E = l + ctx.K, D = num_digits(ctx, l);
+    const size_t ctw = (size_t)2 * l * W, exw = (size_t)D * E * W;
+    uint64_t* ext = (uint64_t*)ws_get(ctx, WS_EXT, (size_t)B * exw * 8);
+    uint64_t* T = (uint64_t*)ws_get(ctx, WS_GROT, (size_t)B * 2 * E * W * 8);
+    modup(ctx, ct + (size_t)l * W, ext, B, l, st, ctw);  // the c1 polys, read in place
+    std::vector<uint32_t> g(n);
+    for (uint32_t j = 0; j < n; j++) g[j] = rotation_index(steps[j]);
+    for (uint32_t c = 0; c < B; c++)
+        // one output, n terms all reading ciphertext c's extension and c0 (strides 0), its identity term P ct
+        HIPX(launch_qp_rot_sum(ctx, ext + c * exw, 0, ct + c * ctw, 0, evk, g.data(), 1, n, 1, 0, l, T, st, 1, c, 0,
+                               false, pmod_tab(ctx).data(), ct + c * ctw, 0));
+    moddown_inplace(ctx, T, 2 * B, l, nullptr, out, st);
+}
+
 // n ciphertexts [n][2][l][N], each rotated by its own step with its own key -> out [n][2][l][N]
 void rotate_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l, const int64_t* steps,
                  const uint64_t* const* evk, uint64_t* out, hipStream_t st) {

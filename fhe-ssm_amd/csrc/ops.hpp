@@ -83,6 +83,8 @@ void rotate(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, uint32_t g
 void add(Context& ctx, const uint64_t* x, const uint64_t* y, uint64_t* out, uint32_t n_polys, uint32_t l,
          hipStream_t st);
 uint32_t rotation_index(int64_t k);
+void rotate_sum(Context& ctx, const uint64_t* ct, uint32_t B, uint32_t l, const int64_t* steps, uint32_t n,
+                const uint64_t* const* evk, uint64_t* out, hipStream_t st);
 void rotate_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l, const int64_t* steps,
                  const uint64_t* const* evk, uint64_t* out, hipStream_t st);
 void automorph_ks_list(Context& ctx, const uint64_t* cts, uint32_t n, uint32_t l, const uint32_t* gidx,

@@ -1463,12 +1463,16 @@ hipError_t launch_qp_rot_sum(const Context& ctx, const uint64_t* ext, uint64_t e
     for (uint32_t c = 0; c < A; c++)
         for (uint32_t j = 0; j < nt; j++) n_ks += keys[c + j] ? 1 : 0;
     // algorithmic bytes, every array once per launch: per key-switched term its extension D E and c0 (Es limbs of the
-    // source), per identity term both source polys; the distinct keys (2 D E each) once; the outputs 2 E
+    // source) -- once for all terms when they share one input (ext_stride 0: a hoisted sum of one ciphertext's
+    // rotations) --, per identity term both source polys; the distinct keys (2 D E each) once; the outputs 2 E
     const double Es = src_pmod ? l : E;
     const double terms = (double)n_out / A;
-    const double by = ((double)n_ks * ((double)D * E + Es) + ((double)A * nt - n_ks) * 2.0 * Es) * terms +
+    const double ks_in = ext_stride == 0 ? (n_ks ? 1.0 : 0.0) : (double)n_ks;
+    const double by = (ks_in * ((double)D * E + Es) + ((double)A * nt - n_ks) * 2.0 * Es) * terms +
                       (id_src ? (double)n_out * 2.0 * Es : 0.0) + (double)n_keys * 2 * D * E + (double)n_out * 2 * E;
-    ctx.n_keyswitch += n_ks * (uint64_t)(n_out / A);
+    // key switches: one per term with an extension of its own; a hoisted sum over one extension is one (its ModUp and
+    // ModDown), its other terms inner products only
+    ctx.n_keyswitch += (uint64_t)ks_in * (uint64_t)(n_out / A);
     const int pi = prof_begin(ctx, "qp_rot_sum", by * kN * 8, st);
     hipLaunchKernelGGL(k_qp_rot_sum, dim3(n_out * (kN / 256) * E), dim3(256), 0, st, ext, src, dst, a, ctx.d_primes);
     prof_end(ctx, pi, st);

@@ -145,11 +145,11 @@ class DecodeStep:
         """x * p(mean(x^2)) per lane"""
         be = self.be
         s = be.mul(x, x)
-        for k in M.NORM_UP:
-            s = be.add(s, be.rotate(s, k))
+        for w in M.NORM_UP:
+            s = be.rotate_sum(s, w)
         s = be.mul_pt(s, self._vec_pt("lane_start", s.level, M.lane_start_mask(1.0 / M.D)))
-        for k in M.NORM_DOWN:
-            s = be.add(s, be.rotate(s, k))
+        for w in M.NORM_DOWN:
+            s = be.rotate_sum(s, w)
         n = be.poly3(s, pcoef)
         return be.mul(x, n)
 
@@ -158,15 +158,15 @@ class DecodeStep:
         return self.be.bootstrap(x, kind)
 
     def _head_sum(self, x, scale):
-        """every head's sum of x (times scale), broadcast over the head's 64 channels: rotate-and-add by 1 .. 32
+        """every head's sum of x (times scale), broadcast over the head's 64 channels: a rotate-and-add window of 64
         (slot h*64 of a lane then holds head h's sum), mask the head starts (times scale), broadcast back"""
         be = self.be
         s = x
-        for k in M.HEAD_UP:
-            s = be.add(s, be.rotate(s, k))
+        for w in M.HEAD_UP:
+            s = be.rotate_sum(s, w)
         s = be.mul_pt(s, self._vec_pt(f"head_start{scale!r}", s.level, M.head_start_mask(scale)))
-        for k in M.HEAD_DOWN:
-            s = be.add(s, be.rotate(s, k))
+        for w in M.HEAD_DOWN:
+            s = be.rotate_sum(s, w)
         return s
 
     def _time_mix(self, li, x, st, v0):
@@ -477,6 +477,11 @@ class HEBackend(Backend):
     def rotate(self, a, k):
         out = self._new(a.B, a.level, a.scale)
         self.ctx.eval_rotate(a.ptr(), a.B, a.level, k, self.keys[k], out.ptr())
+        return out
+
+    def rotate_sum(self, a, steps):
+        out = self._new(a.B, a.level, a.scale)
+        self.ctx.eval_rotate_sum(a.ptr(), a.B, a.level, steps, [self.keys[k] for k in steps], out.ptr())
         return out
 
     def mul_pt(self, a, pt):

@@ -337,6 +337,17 @@ class Engine {
         return out;
     }
 
+    // a + sum_k Rot_k(a) over the window's steps, hoisted (one ModUp, one ModDown)
+    Ct rotate_sum(const Ct& a, const std::vector<int64_t>& steps) {
+        Ct out = fresh(a.B, a.level, a.scale);
+        std::vector<const uint64_t*> keys;
+        for (auto k : steps) keys.push_back(key(k));
+        ck(ckks_eval_rotate_sum(ctx_, a.ptr(), a.B, a.level, steps.data(), (uint32_t)steps.size(), keys.data(),
+                                out.ptr(), nullptr),
+           "ckks_eval_rotate_sum");
+        return out;
+    }
+
     Ct mul_pt(const Ct& a, const Buf& pt) {  // a (.) compressed periodic plaintext (encoded at S(a.level)), rescaled
         Ct tmp = fresh(a.B, a.level, a.scale);
         ck(ckks_eval_mult_plain_ex(ctx_, a.ptr(), a.B, a.level, pt.d, 1, LOG_REP, tmp.ptr(), nullptr),
@@ -660,6 +671,24 @@ std::vector<double> channel_range_mask(int lo, int hi) {
     return m;
 }
 
+// The lane and head sums as rotate-and-add windows (the reference's red = EvalAdd(red, rot(red, p)) loops,
+// gpu_real_model.cu:3524,3540), each one hoisted rotation sum: a lane's 1,024 slots as windows of 32 (steps 1..31),
+// 16 x 32 (32 .. 480) and 2 x 512; a head's 64 slots as one window of 64.  dir = -1: the same windows downwards (the
+// broadcast of a masked sum).  The same windows as rwkv_model.NORM_UP / HEAD_UP, so both drivers give the same words.
+std::vector<std::vector<int64_t>> norm_windows(int dir) {
+    std::vector<std::vector<int64_t>> w(3);
+    for (int k = 1; k < 32; k++) w[0].push_back(dir * k);
+    for (int k = 32; k < 512; k += 32) w[1].push_back(dir * k);
+    w[2].push_back(dir * 512);
+    return w;
+}
+
+std::vector<int64_t> head_window(int dir) {
+    std::vector<int64_t> w;
+    for (int k = 1; k < HS; k++) w.push_back(dir * k);
+    return w;
+}
+
 std::vector<int64_t> layer_rotation_steps() {
     std::vector<int64_t> s;
     for (int nb : {32, 64}) {
@@ -670,10 +699,12 @@ std::vector<int64_t> layer_rotation_steps() {
         s.push_back(t);       // rot64_t: Rot_t on the lanes' low part
         s.push_back(t - HS);  // and Rot_{t-64} on the wrapped part
     }
-    for (int k = 0; k < 10; k++) {
-        s.push_back(1 << k);
-        s.push_back(-(1 << k));
-    }
+    for (const auto& w : norm_windows(1))
+        for (auto k : w) s.push_back(k);
+    for (const auto& w : norm_windows(-1))
+        for (auto k : w) s.push_back(k);
+    for (auto k : head_window(1)) s.push_back(k);
+    for (auto k : head_window(-1)) s.push_back(k);
     for (int g : kGapShift) {
         s.push_back(g);
         s.push_back(-g);
@@ -974,27 +1005,26 @@ class Decoder {
         return be_->bootstrap(x, kind);
     }
 
-    // x * p(mean(x^2)) per lane: rotate-and-add to the lane start, mask (times 1/768), broadcast back
+    // x * p(mean(x^2)) per lane: rotate-and-add windows to the lane start, mask (times 1/768), broadcast back
     Ct norm(const Ct& x, const std::vector<double>& pcoef) {
         PhaseScope ps(be_, "norm");
         Ct s = be_->mul(x, x);
-        for (int k = 0; k < 10; k++) s = be_->add(s, be_->rotate(s, 1 << k));
+        for (const auto& w : norm_windows(1)) s = be_->rotate_sum(s, w);
         s = be_->mul_pt(s, *vec_pt("lane_start", s.level, [] {
             std::vector<double> m(DPAD, 0.0);
             m[0] = 1.0 / D;
             return m;
         }));
-        for (int k = 0; k < 10; k++) s = be_->add(s, be_->rotate(s, -(1 << k)));
+        for (const auto& w : norm_windows(-1)) s = be_->rotate_sum(s, w);
         Ct n = be_->poly3(s, pcoef);
         return be_->mul(x, n);
     }
 
-    // every head's sum of x (times scale), broadcast over the head's 64 channels: rotate-and-add by 1 .. 32 (slot
+    // every head's sum of x (times scale), broadcast over the head's 64 channels: a rotate-and-add window of 64 (slot
     // h*64 of a lane then holds head h's sum), mask the head starts (times scale), broadcast back
     Ct head_sum(const Ct& x, double scale) {
         PhaseScope ps(be_, "head_sum");
-        Ct s = x;
-        for (int k = 0; k < 6; k++) s = be_->add(s, be_->rotate(s, 1 << k));
+        Ct s = be_->rotate_sum(x, head_window(1));
         char tag[48];
         std::snprintf(tag, sizeof(tag), "head_start%.17g", scale);
         s = be_->mul_pt(s, *vec_pt(tag, s.level, [scale] {
@@ -1002,8 +1032,7 @@ class Decoder {
             for (int c = 0; c < D; c += HS) m[c] = scale;
             return m;
         }));
-        for (int k = 0; k < 6; k++) s = be_->add(s, be_->rotate(s, -(1 << k)));
-        return s;
+        return be_->rotate_sum(s, head_window(-1));
     }
 
     static std::vector<double> periodic_of(const std::vector<double>& v) {

@@ -219,12 +219,17 @@ def diag_to_state(Dg: np.ndarray, lanes: int = LANES) -> np.ndarray:
 
 
 # ---------------------------------------------------------------- norms
-NORM_UP = tuple(1 << k for k in range(10))      # rotate-and-add: slot lane*1024 gets the lane's sum
-NORM_DOWN = tuple(-(1 << k) for k in range(10))  # broadcast the masked sum over the lane
+# The lane and head sums are rotate-and-add windows (the reference's red = EvalAdd(red, rot(red, p)) loops,
+# gpu_real_model.cu:3524,3540), each window one hoisted rotation sum s + sum_k Rot_k(s) over a set of steps (one
+# ModUp and one ModDown for the whole set).  Slot lane*1024 gets the lane's sum from windows of 32 (steps 1..31), then
+# 16 x 32 (steps 32, 64, .., 480), then 2 x 512; the broadcast of the masked sum runs the same windows downwards.
+# Every step is one the matvecs or the WKV scan already hold a key for.
+NORM_UP = (tuple(range(1, 32)), tuple(range(32, 512, 32)), (512,))
+NORM_DOWN = tuple(tuple(-k for k in w) for w in NORM_UP)
 
 
-HEAD_UP = tuple(1 << k for k in range(6))      # rotate-and-add: slot h*64 of a lane gets head h's sum
-HEAD_DOWN = tuple(-(1 << k) for k in range(6))  # broadcast the masked sums over their heads
+HEAD_UP = (tuple(range(1, 64)),)  # slot h*64 of a lane gets head h's sum
+HEAD_DOWN = (tuple(-k for k in HEAD_UP[0]),)  # broadcast the masked sums over their heads
 
 
 def head_start_mask(scale: float = 1.0) -> np.ndarray:
@@ -258,7 +263,9 @@ def channel_range_mask(lo: int, hi: int) -> np.ndarray:
 
 def rotation_steps() -> list:
     """Every rotation step the decode step uses (keys to generate)."""
-    s = set(WKV_LO) | set(WKV_HI) | set(NORM_UP) | set(NORM_DOWN) | set(HEAD_UP) | set(HEAD_DOWN)
+    s = set(WKV_LO) | set(WKV_HI)
+    for w in NORM_UP + NORM_DOWN + HEAD_UP + HEAD_DOWN:
+        s |= set(w)
     for nb in (32, 64):
         s |= set(mv_babies(nb)) | set(mv_giants(nb))
     s |= set(GAP_SHIFT) | set(-g for g in GAP_SHIFT)

@@ -167,6 +167,12 @@ int ckks_eval_rotate(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, ui
  * ckks_eval_rotate_hoisted  EvalFastRotation: one ciphertext rotated by steps[0..n) (n <= 64) with one shared
  *                        ModUp of c1; key i = the automorphism key of rotation steps[i]; out [n][2][l][N]
  * ckks_eval_rotate_many  n ciphertexts [n][2][l][N], ciphertext i rotated by steps[i] with key i (n <= 64)
+ * ckks_eval_rotate_sum  out = ct + sum_i Rot_{steps[i]}(ct) for each of batch ciphertexts [B][2][l][N] (1 <= n <= 64,
+ *                        no identity step): the rotate-and-add loops of the reference's lane sums
+ *                        (gpu_real_model.cu:3524,3540: red = EvalAdd(red, rot(red, p))) as windows, the n rotations
+ *                        hoisted over one ModUp of c1 and summed over Q_l P before one ModDown; key i = the
+ *                        automorphism key of steps[i]; out may be ct.  Equal to the loop of single rotations up to
+ *                        the key-switching rounding (one ModDown instead of n)
  * ckks_linear_transform_bsgs  the reference's baby-step giant-step diagonal matvec (gpu_real_model.cu:2767-2823):
  *                        out = Rescale( sum_g Rot_{g*bs}( sum_j diag[g*bs + j] (.) Rot_j(ct) ) ), diag [n_diag][l][N]
  *                        encoded plaintexts already pre-rotated by -g*bs; baby keys for steps 1..bs-1, giant keys
@@ -179,6 +185,8 @@ int ckks_eval_rotate_hoisted(ckks_context* ctx, const uint64_t* d_ct, uint32_t l
                              uint32_t n, const uint64_t* const* d_evks, uint64_t* d_out, void* stream);
 int ckks_eval_rotate_many(ckks_context* ctx, const uint64_t* d_cts, uint32_t n, uint32_t level, const int64_t* steps,
                           const uint64_t* const* d_evks, uint64_t* d_out, void* stream);
+int ckks_eval_rotate_sum(ckks_context* ctx, const uint64_t* d_ct, uint32_t batch, uint32_t level, const int64_t* steps,
+                         uint32_t n, const uint64_t* const* d_evks, uint64_t* d_out, void* stream);
 int ckks_linear_transform_bsgs(ckks_context* ctx, const uint64_t* d_ct, uint32_t level, const uint64_t* d_diags,
                                uint32_t n_diag, uint32_t baby_steps, const uint64_t* const* d_baby_evks,
                                const uint64_t* const* d_giant_evks, uint64_t* d_out, void* stream);

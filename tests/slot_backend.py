@@ -119,6 +119,9 @@ class SlotBackend(DS.Backend):
     def rotate(self, a, k):
         return SimCt(np.roll(a.v, -k, axis=1), a.level, a.scale)
 
+    def rotate_sum(self, a, steps):
+        return SimCt(a.v + sum(np.roll(a.v, -k, axis=1) for k in steps), a.level, a.scale)
+
     def mul_pt(self, a, pt):
         assert pt.level == a.level and pt.vecs.shape[0] == 1 and a.level >= 2
         return SimCt(a.v * tile(pt.vecs[0])[None, :], a.level - 1, a.scale)

@@ -315,6 +315,69 @@ def test_linear_transform_hoisted_bit_exact(ckks, ctx5, octx5, gst):
         assert np.array_equal(got[o], want), o
 
 
+def test_rotate_sum_bit_exact(ckks, ctx5, octx5):
+    """ckks_eval_rotate_sum (a rotate-and-add window hoisted over one ModUp and one ModDown) against the oracle
+    composed from its stages: ModDown( (P c0, P c1) + sum_s Auto_s(<ModUp(c1), evk_s> + (P c0, 0)) ) per poly, for a
+    batch of 2 ciphertexts, in place and out of place; and a window of one step"""
+    l, B = 5, 2
+    L, K, D = ctx5.L, ctx5.K, ctx5.dnum
+    steps = [1, 2, -3, 7]
+    E = l + K
+    pmap = list(range(l)) + list(range(L, L + K))
+    evk = {s: residues(ctx5.moduli, (D, 2), list(range(L + K)), 400 + i) for i, s in enumerate(steps)}
+    dk = {s: ckks.DeviceBuffer.from_array(e) for s, e in evk.items()}
+    xs = residues(ctx5.moduli, (B, 2), list(range(l)), 41)
+    qe = np.array([ctx5.moduli[i] for i in pmap], dtype=object).reshape(-1, 1)
+    P = 1
+    for k in range(K):
+        P *= ctx5.moduli[L + k]
+    pq = np.array([P % ctx5.moduli[i] for i in range(l)], dtype=object).reshape(-1, 1)
+
+    def want(c, st):
+        T = np.zeros((2, E, N), dtype=object)
+        T[0, :l] = c[0].astype(object) * pq % qe[:l]
+        T[1, :l] = c[1].astype(object) * pq % qe[:l]
+        ext = octx5.modup(c[1], l)
+        for s in st:
+            acc = octx5.ks_inner(ext, l, evk[s]).astype(object)
+            acc[0, :l] += c[0].astype(object) * pq % qe[:l]
+            v = (acc % qe[None]).astype(np.uint64)
+            T += octx5.automorph_eval(v, octx5.rot_index(s)).astype(object)
+        T = (T % qe[None]).astype(np.uint64)
+        return np.stack([octx5.moddown(T[p], l) for p in range(2)])
+
+    for st in (steps, [-3]):
+        dx = ckks.DeviceBuffer.from_array(xs)
+        out = ckks.DeviceBuffer(B * 2 * l * N * 8)
+        ctx5.eval_rotate_sum(dx.ptr, B, l, st, [dk[s].ptr for s in st], out.ptr)
+        got = out.download((B, 2, l, N))
+        for b in range(B):
+            assert np.array_equal(got[b], want(xs[b], st)), (st, b)
+        # in place
+        ctx5.eval_rotate_sum(dx.ptr, B, l, st, [dk[s].ptr for s in st], dx.ptr)
+        assert np.array_equal(dx.download((B, 2, l, N)), got), st
+    # refusals: no steps, the identity, a missing key
+    dx = ckks.DeviceBuffer.from_array(xs)
+    for st, keys in (([], []), ([0], [dk[1].ptr]), ([1], [None])):
+        with pytest.raises(RuntimeError):
+            ctx5.eval_rotate_sum(dx.ptr, B, l, st, keys, dx.ptr)
+
+
+def test_rotate_sum_decrypts_to_the_window_sum(engine, DS):
+    """an encrypted rotate-and-add window (the norms' lane sum: windows 1..31, 32..480 by 32, 512) decrypts to the
+    sums over 1,024 consecutive slots, within the key-switching noise"""
+    be, sk = engine
+    rng = np.random.default_rng(77)
+    z = rng.uniform(-1, 1, SLOTS)
+    ct = be.encrypt(sk, z, 10)
+    s = ct
+    for w in DS.M.NORM_UP:
+        s = be.rotate_sum(s, w)
+    got = be.decrypt(sk, s)
+    want = sum(np.roll(z, -k) for k in range(1024))
+    assert np.abs(got - want).max() < 1e-4 * np.abs(want).max()
+
+
 @pytest.fixture(scope="module")
 def engine(ckks, DS):
     be, sk = DS.build_engine(ckks)
