@@ -45,6 +45,11 @@ namespace {
 constexpr int kTileThreads = 256;
 constexpr int kLdsWords = 16 * 272;  // one tile, padded to 17 words per 16 (both passes: no bank conflicts)
 
+// a workgroup-uniform quotient: the division by a kernel argument runs on the VALU (there is no scalar divide), so
+// its result is taken back into a scalar register -- the addresses and constants derived from it then stay scalar
+// instead of occupying (and, across a transform, spilling) vector registers
+__device__ __forceinline__ uint32_t uni_div(uint32_t a, uint32_t b) { return __builtin_amdgcn_readfirstlane(a / b); }
+
 __device__ __forceinline__ void job_of(const JobSpec& js, uint32_t u, uint32_t& off, uint32_t& prime) {
     if (js.jobs) {
         const Job j = js.jobs[u];
@@ -53,7 +58,7 @@ __device__ __forceinline__ void job_of(const JobSpec& js, uint32_t u, uint32_t& 
     } else {
         // prime-major enumeration of a dense [polys][period][N] buffer.  The prime index is read as the aligned
         // 32-bit word holding it (a scalar load: the data loads need not wait for a vector byte load)
-        const uint32_t l = u / js.n_polys, p = u - l * js.n_polys;
+        const uint32_t l = uni_div(u, js.n_polys), p = u - l * js.n_polys;
         off = p * js.period + l;
         const uint32_t w = reinterpret_cast<const uint32_t*>(js.pmap)[l >> 2];
         prime = (w >> (8 * (l & 3))) & 0xFFu;
@@ -63,7 +68,7 @@ __device__ __forceinline__ void job_of(const JobSpec& js, uint32_t u, uint32_t& 
 // where job u reads its input: the buffer itself, or the out-of-place source of a dense spec
 __device__ __forceinline__ const uint64_t* job_src(const JobSpec& js, uint32_t u, const uint64_t* data, uint32_t off) {
     if (js.src && !js.jobs) {
-        const uint32_t l = u / js.n_polys, p = u - l * js.n_polys;
+        const uint32_t l = uni_div(u, js.n_polys), p = u - l * js.n_polys;
         return js.src + ((size_t)p * js.src_period + l) * kN;
     }
     return data + (size_t)off * kN;
@@ -77,7 +82,7 @@ struct JobIn {
 
 __device__ __forceinline__ JobIn job_in(const JobSpec& js, uint32_t u) {
     JobIn r{nullptr, nullptr};
-    const uint32_t l = u / js.n_polys, p = u - l * js.n_polys;
+    const uint32_t l = uni_div(u, js.n_polys), p = u - l * js.n_polys;
     if (js.src2) r.in2 = js.src2 + ((size_t)p * js.src_period + l) * kN;
     if (js.copy) r.cpy = js.copy + p * js.copy_pstride + ((size_t)(l / js.copy_alpha) * js.copy_E + l) * kN;
     return r;
@@ -506,7 +511,7 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_fwd_a(uint64_t* data, JobS
     uint64_t* a = data + (size_t)off * kN;
     const TwPair* tw = tw_all + (size_t)prime * kN;
     if (js.lift && !js.jobs) {
-        const uint32_t p = blockIdx.y % js.n_polys;
+        const uint32_t p = blockIdx.y - uni_div(blockIdx.y, js.n_polys) * js.n_polys;
         const uint64_t* src = js.lift + p * js.lift_pstride;
         if (q < kOpenMaxQ)
             fwd_a_tile<true, true>(a, tw, q, blockIdx.x, threadIdx.x, lds, src, js.lift_q, barrett_of(primes[prime]));
@@ -754,7 +759,7 @@ template <int kD, bool kTa, bool kPost>
 __global__ __launch_bounds__(2 * kTileThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_ntt_fwd_b_mdr(
     uint64_t* T, const TwPair* tw_all, const PrimeInfo* primes, MdrFuse f) {
     __shared__ uint64_t lds[2 * kLdsWords];
-    const uint32_t i = blockIdx.y / f.B, c = blockIdx.y - i * f.B;
+    const uint32_t i = uni_div(blockIdx.y, f.B), c = blockIdx.y - i * f.B;
     const uint32_t g = threadIdx.x >> 8, t = threadIdx.x & 255;
     const PrimeInfo& P = primes[i];
     const MdrEpi<kD, kTa, kPost> epi{f, P, i, c, g};
@@ -880,7 +885,7 @@ template <int kD>
 __global__ __launch_bounds__(2 * kTileThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_ntt_fwd_b_ksl(
     uint64_t* y, const TwPair* tw_all, const PrimeInfo* primes, KslFuse f) {
     __shared__ uint64_t lds[2 * kLdsWords];
-    const uint32_t i = blockIdx.y / f.n, c = blockIdx.y - i * f.n;
+    const uint32_t i = uni_div(blockIdx.y, f.n), c = blockIdx.y - i * f.n;
     const uint32_t g = threadIdx.x >> 8, t = threadIdx.x & 255;
     const PrimeInfo& P = primes[i];
     const KslEpi<kD> epi{f, P, i, c, g};
@@ -957,7 +962,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(4)
     __shared__ uint64_t lds[kLdsWords];
     uint32_t off, prime;
     job_of(js, blockIdx.y, off, prime);
-    const uint32_t i = blockIdx.y / js.n_polys, pc = blockIdx.y - i * js.n_polys;
+    const uint32_t i = uni_div(blockIdx.y, js.n_polys), pc = blockIdx.y - i * js.n_polys;
     const PrimeInfo& P = primes[prime];
     const SubEpi epi{ca, x, add, out, P, i, pc};
     uint64_t* a = y + (size_t)off * kN;
@@ -1031,7 +1036,7 @@ __global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(4)
     __shared__ uint64_t lds[kLdsWords];
     uint32_t off, prime;
     job_of(js, blockIdx.y, off, prime);
-    const uint32_t i = blockIdx.y / js.n_polys, pc = blockIdx.y - i * js.n_polys;
+    const uint32_t i = uni_div(blockIdx.y, js.n_polys), pc = blockIdx.y - i * js.n_polys;
     const PrimeInfo& P = primes[prime];
     LinSubEpi epi;
 #pragma unroll
