@@ -100,6 +100,11 @@ __device__ __forceinline__ void mac128(U128& acc, uint64_t a, uint64_t b) {
     acc.lo = nlo;
 }
 
+// a workgroup-uniform quotient (both operands uniform): the division by a kernel argument runs on the VALU (there is
+// no scalar divide), so its result is taken back into a scalar register -- the addresses and constants derived from
+// it then stay scalar instead of occupying (and, across a transform, spilling) vector registers
+__device__ __forceinline__ uint32_t uni_div(uint32_t a, uint32_t b) { return __builtin_amdgcn_readfirstlane(a / b); }
+
 // Lazy 128-bit multiply-accumulate for operands below 2^60 (every modulus of this engine is): the four 32 x 32
 // partial products go to separate 64-bit sums -- the low products to lo with a carry into hi, the two cross
 // products (< 2^60 each) to m, the high product (< 2^56) straight into hi -- so a term costs four

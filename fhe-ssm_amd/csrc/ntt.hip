@@ -45,11 +45,6 @@ namespace {
 constexpr int kTileThreads = 256;
 constexpr int kLdsWords = 16 * 272;  // one tile, padded to 17 words per 16 (both passes: no bank conflicts)
 
-// a workgroup-uniform quotient: the division by a kernel argument runs on the VALU (there is no scalar divide), so
-// its result is taken back into a scalar register -- the addresses and constants derived from it then stay scalar
-// instead of occupying (and, across a transform, spilling) vector registers
-__device__ __forceinline__ uint32_t uni_div(uint32_t a, uint32_t b) { return __builtin_amdgcn_readfirstlane(a / b); }
-
 __device__ __forceinline__ void job_of(const JobSpec& js, uint32_t u, uint32_t& off, uint32_t& prime) {
     if (js.jobs) {
         const Job j = js.jobs[u];

@@ -398,9 +398,9 @@ struct ListTile {
 
 // tiles_per_limb coefficient tiles per limb (kN / 256 for 256-thread tiles)
 __device__ __forceinline__ ListTile list_tile(uint32_t m, uint32_t tiles_per_limb = kN / 256) {
-    const uint32_t n = blockIdx.x, q = n >> 3;
-    const uint32_t tile = (q / m) * 8 + (n & 7);
-    return ListTile{q % m, tile % tiles_per_limb, tile / tiles_per_limb};
+    const uint32_t n = blockIdx.x, q = n >> 3, qm = uni_div(q, m);
+    const uint32_t tile = qm * 8 + (n & 7);
+    return ListTile{q - qm * m, tile % tiles_per_limb, tile / tiles_per_limb};
 }
 
 __global__ __launch_bounds__(256) void k_ks_inner_list(ListPtrs ext, ListPtrs evk, uint64_t* __restrict__ acc,
@@ -592,7 +592,8 @@ __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__
     };
     uint64_t v0 = 0, v1 = 0;
     for (uint32_t j = 0; j < a.nt; j++) {
-        const uint32_t x = (c / a.A) * a.M + j, kk = c % a.A + j;
+        const uint32_t cA = uni_div(c, a.A);
+        const uint32_t x = cA * a.M + j, kk = c - cA * a.A + j;
         const uint32_t g = a.g[kk];
         const uint32_t e = (uint32_t)(((uint64_t)g * (2u * (__brev(k) >> (32 - kLogN)) + 1u)) & (2u * kN - 1u));
         const uint32_t sw = __brev((e - 1u) >> 1) >> (32 - kLogN);
@@ -615,8 +616,8 @@ __global__ __launch_bounds__(256) void k_qp_rot_sum(const uint64_t* __restrict__
         v0 = add_mod(v0, src_word(ix), q);
         v1 = add_mod(v1, src_word(ix + a.src_poly), q);
     }
-    const uint32_t u = c + a.c_off;
-    uint64_t* o = dst + (size_t)(u / a.R) * a.s_hi + (size_t)(u % a.R) * a.s_lo + (size_t)t * kN + k;
+    const uint32_t u = c + a.c_off, uR = uni_div(u, a.R);
+    uint64_t* o = dst + (size_t)uR * a.s_hi + (size_t)(u - uR * a.R) * a.s_lo + (size_t)t * kN + k;
     if (a.accumulate) {
         v0 = add_mod(v0, o[0], q);
         v1 = add_mod(v1, o[(size_t)a.E * kN], q);
@@ -826,7 +827,8 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
     // XCD x (workgroups x mod 8) takes one contiguous run of the (limb, chain-ordered tile) sequence; the instances of
     // a tile follow each other on it (they share the tile's keys and diagonals)
     const uint32_t xcd = blockIdx.x & 7, qi = blockIdx.x >> 3;
-    const uint32_t s = qi % a.n_inst, seq = xcd * (a.E * (kN / kMacCoef) / 8) + qi / a.n_inst;
+    const uint32_t qn = uni_div(qi, a.n_inst);
+    const uint32_t s = qi - qn * a.n_inst, seq = xcd * (a.E * (kN / kMacCoef) / 8) + qn;
     const uint32_t t = seq / (kN / kMacCoef);
     // a row is one wave (kMacCoef = 64 lanes): its index, and every baby / giant index derived from it, is wave-uniform
     // and lives in scalar registers (left to the compiler, the per-baby division and addressing ran on the VALU)
