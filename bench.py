@@ -92,16 +92,16 @@ def achievable(write_share: float) -> float:
 # A kernel "launch" is one engine call (both kernels of a two-pass NTT).  Measured, not computed: re-measure when the
 # kernel or the workload changes.
 MEASURED = {
-    ("hmult", "step"): {"traffic": 34.655e9, "source": "profiles/hmult_config2_kernels.md"},
-    ("hmult", "ntt_fwd_mdr"): {"traffic": 11.689e9, "valu_insts": 878.0e6, "source": "profiles/hmult_config2_kernels.md"},
-    ("hmult", "ntt_fwd_2pass"): {"traffic": 9.700e9, "valu_insts": 786.2e6, "source": "profiles/hmult_config2_kernels.md"},
+    ("hmult", "step"): {"traffic": 34.659e9, "source": "profiles/hmult_config2_kernels.md"},
+    ("hmult", "ntt_fwd_mdr"): {"traffic": 11.688e9, "valu_insts": 870.3e6, "source": "profiles/hmult_config2_kernels.md"},
+    ("hmult", "ntt_fwd_2pass"): {"traffic": 9.700e9, "valu_insts": 776.7e6, "source": "profiles/hmult_config2_kernels.md"},
     ("ntt", "step"): {"traffic": 12.940e9, "source": "profiles/ntt_config1_kernel_trace.md"},
-    ("pcmm", "step"): {"traffic": 18.375e9, "source": "profiles/pcmm_config3_kernel_trace.md"},
+    ("pcmm", "step"): {"traffic": 18.373e9, "source": "profiles/pcmm_config3_kernel_trace.md"},
     ("pcmm", "bsgs_mac"): {"traffic": 7.382e9, "source": "profiles/pcmm_config3_kernel_trace.md"},
-    ("bootstrap", "step"): {"traffic": 56.220e9, "source": "profiles/bootstrap_config4_kernel_trace.md"},
-    ("decode", "step"): {"traffic": 21803.9e9, "source": "profiles/decode_config5_kernel_trace.md"},
-    ("ntt", "ntt_fwd_2pass"): {"traffic": 6.470e9, "valu_insts": 495.1e6, "source": "profiles/ntt_config1_kernel_trace.md"},
-    ("ntt", "ntt_inv_2pass"): {"traffic": 6.470e9, "valu_insts": 489.2e6, "source": "profiles/ntt_config1_kernel_trace.md"},
+    ("bootstrap", "step"): {"traffic": 55.211e9, "source": "profiles/bootstrap_config4_kernel_trace.md"},
+    ("decode", "step"): {"traffic": 21811.7e9, "source": "profiles/decode_config5_kernel_trace.md"},
+    ("ntt", "ntt_fwd_2pass"): {"traffic": 6.470e9, "valu_insts": 480.5e6, "source": "profiles/ntt_config1_kernel_trace.md"},
+    ("ntt", "ntt_inv_2pass"): {"traffic": 6.470e9, "valu_insts": 482.3e6, "source": "profiles/ntt_config1_kernel_trace.md"},
 }
 # int-VALU issue peak: 256 CUs x 4 SIMDs, one wave64 VALU instruction per SIMD every 4 cycles (16 lanes) at the
 # 2.4 GHz peak engine clock
