@@ -311,3 +311,39 @@ def test_four_digit_key_switch(ckks, oracle):
     c4.eval_rotate(da.ptr, 1, l, 3, dev.ptr, drot.ptr)
     assert np.array_equal(drot.download(a.shape)[0], o4.rotate(a[0], l, o4.rot_index(3), ev))
     c4.close()
+
+
+def test_rotate_sum_of_64_rotations(ckks, oracle):
+    """ckks_eval_rotate_sum at its limit of 64 rotations (steps 1..64, each with its own key), on a small chain so
+    that the 64 keys stay small: ct + sum_s Rot_s(ct) with one ModUp and one ModDown, against the oracle composed
+    from its stages -- ModDown((P c0, P c1) + sum_s Auto_s(<ModUp(c1), evk_s> + (P c0, 0))) per poly"""
+    Ls, Ks, Ds = 2, 1, 2
+    cs = ckks.Context(num_q=Ls, num_p=Ks, dnum=Ds, q_bits=54, p_bits=60)
+    os_ = oracle.Ctx(16, cs.moduli, Ls, Ks, Ds)
+    l, E = Ls, Ls + Ks
+    steps = list(range(1, 65))
+    ev = {s: residues(cs.moduli, (Ds, 2), list(range(Ls + Ks)), seed=500 + s) for s in steps}
+    dk = {s: ckks.DeviceBuffer.from_array(e) for s, e in ev.items()}
+    x = residues(cs.moduli, (1, 2), list(range(l)), seed=95)
+    dx = ckks.DeviceBuffer.from_array(x)
+    out = ckks.DeviceBuffer(x.nbytes)
+    cs.eval_rotate_sum(dx.ptr, 1, l, steps, [dk[s].ptr for s in steps], out.ptr)
+    qe = np.array(list(cs.moduli[:l]) + list(cs.moduli[Ls:Ls + Ks]), dtype=object).reshape(-1, 1)
+    P = cs.moduli[Ls]
+    pq = np.array([P % q for q in cs.moduli[:l]], dtype=object).reshape(-1, 1)
+    c = x[0]
+    T = np.zeros((2, E, N), dtype=object)
+    T[0, :l] = c[0].astype(object) * pq % qe[:l]
+    T[1, :l] = c[1].astype(object) * pq % qe[:l]
+    ext = os_.modup(c[1], l)
+    for s in steps:
+        acc = os_.ks_inner(ext, l, ev[s]).astype(object)
+        acc[0, :l] += c[0].astype(object) * pq % qe[:l]
+        T += os_.automorph_eval((acc % qe[None]).astype(np.uint64), os_.rot_index(s)).astype(object)
+    T = (T % qe[None]).astype(np.uint64)
+    want = np.stack([os_.moddown(T[p], l) for p in range(2)])
+    assert np.array_equal(out.download(x.shape)[0], want)
+    # 65 rotations are refused
+    with pytest.raises(RuntimeError):
+        cs.eval_rotate_sum(dx.ptr, 1, l, steps + [65], [dk[1].ptr] * 65, out.ptr)
+    cs.close()
