@@ -263,19 +263,30 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         // streamed: read once, by the next NTT (nontemporal, so the L2 keeps what is reused)
         __builtin_nontemporal_store(v, &dst[(size_t)desc_off(dj) * kN]);
     };
-    // two outputs per iteration: independent accumulation chains for the scheduler to interleave
-    uint32_t j = 0;
-    for (; j + 1 < n_main; j += 2) {
+    // the outputs of this workgroup's share (grid z splits them when the batch is too small to fill the GPU), two
+    // per iteration: independent accumulation chains for the scheduler to interleave
+    const uint32_t share = ((n_main + gridDim.z - 1) / gridDim.z + 1) & ~1u;
+    const uint32_t j_end = min(n_main, (blockIdx.z + 1) * share);
+    uint32_t j = blockIdx.z * share;
+    for (; j + 1 < j_end; j += 2) {
         U128 r, r2;
         sums(j, j + 1, r, r2);
         finish(r, j);
         finish(r2, j + 1);
     }
-    if (j < n_main) {
+    if (j < j_end) {
         U128 r, unused;
         sums(j, j, r, unused);
         finish(r, j);
     }
+}
+
+// grid z of a BConv launch: with fewer than 8 workgroups of 256 coefficients per CU the outputs are split over z
+// (each share at least 4 outputs; every share converts its inputs itself)
+static uint32_t bconv_split(uint32_t n_polys, uint32_t n_out) {
+    const uint32_t wg = (kN / 256) * n_polys, want = 2048;
+    if (wg >= want) return 1;
+    return std::max(1u, std::min((want + wg - 1) / wg, n_out / 4));
 }
 
 // k_bconv instance for a run-time input count (1..kMaxBconvIn)
@@ -1108,8 +1119,8 @@ hipError_t launch_bconv(const Context& ctx, const BConvPlan& plan, const uint64_
         return hipErrorInvalidValue;
     const BConvArgs ba = bconv_args(plan, in_bstride, in_off, out_bstride, out_off, plan.n_out);
     const int pi = prof_begin(ctx, "bconv", (double)B * (plan.n_in + plan.n_out) * kN * 8, st);
-    hipLaunchKernelGGL(bconv_kernel<false>(plan), dim3(kN / 256, B), dim3(256), 0, st, in, out, ba, plan.d_tab,
-                       ctx.d_primes, MdrBconvArgs{});
+    hipLaunchKernelGGL(bconv_kernel<false>(plan), dim3(kN / 256, B, bconv_split(B, plan.n_out)), dim3(256), 0, st,
+                       in, out, ba, plan.d_tab, ctx.d_primes, MdrBconvArgs{});
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
@@ -1143,8 +1154,8 @@ hipError_t launch_bconv_mdr(const Context& ctx, const BConvPlan& plan, const uin
     // P limbs + limb l-1 (+ the addend's) read, l-1 limbs written
     const double bytes = (double)n_polys * (plan.n_in + 1 + (addc ? 1 : 0) + (l - 1)) * kN * 8;
     const int pi = prof_begin(ctx, "bconv_mdr", bytes, st);
-    hipLaunchKernelGGL(bconv_kernel<true>(plan), dim3(kN / 256, n_polys), dim3(256), 0, st, in, T, ba,
-                       plan.d_tab, ctx.d_primes, mb);
+    hipLaunchKernelGGL(bconv_kernel<true>(plan), dim3(kN / 256, n_polys, bconv_split(n_polys, l - 1)), dim3(256), 0,
+                       st, in, T, ba, plan.d_tab, ctx.d_primes, mb);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
