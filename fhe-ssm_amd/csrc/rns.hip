@@ -281,8 +281,9 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
     }
 }
 
-// grid z of a BConv launch: with fewer than 8 workgroups of 256 coefficients per CU the outputs are split over z
-// (each share at least 4 outputs; every share converts its inputs itself)
+// grid z of a ModUp BConv launch: with fewer than 8 workgroups of 256 coefficients per CU the outputs are split over
+// z (each share at least 4 outputs; every share converts its inputs itself).  The ModDown instance is not split: each
+// share would form the dropped limb's conversion and lift again, and measured slower.
 static uint32_t bconv_split(uint32_t n_polys, uint32_t n_out) {
     const uint32_t wg = (kN / 256) * n_polys, want = 2048;
     if (wg >= want) return 1;
@@ -1154,8 +1155,8 @@ hipError_t launch_bconv_mdr(const Context& ctx, const BConvPlan& plan, const uin
     // P limbs + limb l-1 (+ the addend's) read, l-1 limbs written
     const double bytes = (double)n_polys * (plan.n_in + 1 + (addc ? 1 : 0) + (l - 1)) * kN * 8;
     const int pi = prof_begin(ctx, "bconv_mdr", bytes, st);
-    hipLaunchKernelGGL(bconv_kernel<true>(plan), dim3(kN / 256, n_polys, bconv_split(n_polys, l - 1)), dim3(256), 0,
-                       st, in, T, ba, plan.d_tab, ctx.d_primes, mb);
+    hipLaunchKernelGGL(bconv_kernel<true>(plan), dim3(kN / 256, n_polys), dim3(256), 0, st, in, T, ba, plan.d_tab,
+                       ctx.d_primes, mb);
     prof_end(ctx, pi, st);
     return hipGetLastError();
 }
