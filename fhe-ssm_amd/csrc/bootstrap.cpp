@@ -482,7 +482,10 @@ public:
         for (int n = 16; n <= deg; n *= 2) T[n] = t2(n / 2);  // the giant steps the division below uses
         for (auto& kv : Tat) put(kv.second);  // the products above are done with their level copies
         Tat.clear();
-        std::function<HCt(const std::vector<double>&)> rec = [&](const std::vector<double>& a) -> HCt {
+        // want: the level the caller consumes the result at (a leaf lands there directly when that is below its own
+        // level, instead of being adjusted down by a second rescale afterwards)
+        std::function<HCt(const std::vector<double>&, uint32_t)> rec = [&](const std::vector<double>& a,
+                                                                            uint32_t want) -> HCt {
             int degp = (int)a.size() - 1;
             while (degp > 0 && a[degp] == 0.0) degp--;
             if (degp < 8) {
@@ -494,6 +497,7 @@ public:
                     lt = std::min(lt, T[j].l - 1);
                 }
                 if (terms.empty()) terms.push_back({T[1], 0.0}), lt = T[1].l - 1;
+                if (want >= 1) lt = std::min(lt, want);
                 return scal_comb(terms, a[0], lt);
             }
             int n = 8;
@@ -508,13 +512,13 @@ public:
                     rr[2 * n - j] -= a[j];
                 }
             }
-            HCt hq = rec(q);
+            HCt hq = rec(q, T[n].l);  // multiplied by T_n at T_n's level
             const uint32_t lm = std::min(hq.l, T[n].l);
             HCt hqa = hq.l == lm ? hq : adjust(hq, lm);
             HCt prod = mult(hqa, at(n, lm));
             if (hqa.d != hq.d) put(hqa);
             put(hq);
-            HCt hr = rec(rr);
+            HCt hr = rec(rr, prod.l);  // added to the product at its level
             const uint32_t l = std::min(prod.l, hr.l);
             HCt pa = prod.l == l ? prod : adjust(prod, l);
             HCt ra = hr.l == l ? hr : adjust(hr, l);
@@ -525,7 +529,7 @@ public:
             put(hr);
             return out;
         };
-        HCt res = rec(c);
+        HCt res = rec(c, 0);  // the series at its own level
         for (auto& kv : Tat) put(kv.second);
         for (auto& kv : T) put(kv.second);
         return res;
