@@ -98,8 +98,8 @@ MEASURED = {
     ("ntt", "step"): {"traffic": 12.940e9, "source": "profiles/ntt_config1_kernel_trace.md"},
     ("pcmm", "step"): {"traffic": 18.373e9, "source": "profiles/pcmm_config3_kernel_trace.md"},
     ("pcmm", "bsgs_mac"): {"traffic": 7.382e9, "source": "profiles/pcmm_config3_kernel_trace.md"},
-    ("bootstrap", "step"): {"traffic": 55.246e9, "source": "profiles/bootstrap_config4_kernel_trace.md"},
-    ("decode", "step"): {"traffic": 21811.7e9, "source": "profiles/decode_config5_kernel_trace.md"},
+    ("bootstrap", "step"): {"traffic": 54.621e9, "source": "profiles/bootstrap_config4_kernel_trace.md"},
+    ("decode", "step"): {"traffic": 21575.8e9, "source": "profiles/decode_config5_kernel_trace.md"},
     ("ntt", "ntt_fwd_2pass"): {"traffic": 6.470e9, "valu_insts": 480.5e6, "source": "profiles/ntt_config1_kernel_trace.md"},
     ("ntt", "ntt_inv_2pass"): {"traffic": 6.470e9, "valu_insts": 482.3e6, "source": "profiles/ntt_config1_kernel_trace.md"},
 }
