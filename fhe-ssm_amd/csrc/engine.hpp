@@ -53,11 +53,11 @@ struct JobSpec {
     // With src (two-pass mode only): src2, if set, makes the input the product src * src2 mod q, both factors read
     // at src's layout; copy, if set, receives the input (or that product) as read, before the transform: limb l of
     // poly p at copy + p * copy_pstride + ((l / copy_alpha) * copy_E + l) * N -- a ModUp extension buffer's
-    // digit-own limbs.
+    // digit-own limbs.  Only limbs l >= copy_from are copied (0: all).
     const uint64_t* src2;
     uint64_t* copy;
     uint64_t copy_pstride;
-    uint32_t copy_alpha, copy_E;
+    uint32_t copy_alpha, copy_E, copy_from;
     // Forward dense specs (two-pass mode only): lift, if set, is read in place of the buffer -- the input of limb l of
     // poly p is the centered lift of lift[p * lift_pstride + k] (a residue mod lift_q, above lift_q / 2 standing for
     // a negative value) into limb l's prime: a rescale's dropped limb spread over the kept ones.

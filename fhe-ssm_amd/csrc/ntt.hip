@@ -30,6 +30,7 @@
 // (a product of two limbs, an evk inner product) and copy it into a ModUp buffer; a forward first pass may lift a
 // rescale's dropped limb; a forward last pass may end in a ModDown / rescale / key-switch combine (k_ntt_fwd_b_mdr,
 // k_ntt_fwd_b_sub, k_ntt_fwd_b_ksl) instead of storing the transform.
+#include <algorithm>
 #include <set>
 #include <type_traits>
 
@@ -79,7 +80,8 @@ __device__ __forceinline__ JobIn job_in(const JobSpec& js, uint32_t u) {
     JobIn r{nullptr, nullptr};
     const uint32_t l = uni_div(u, js.n_polys), p = u - l * js.n_polys;
     if (js.src2) r.in2 = js.src2 + ((size_t)p * js.src_period + l) * kN;
-    if (js.copy) r.cpy = js.copy + p * js.copy_pstride + ((size_t)(l / js.copy_alpha) * js.copy_E + l) * kN;
+    if (js.copy && l >= js.copy_from)
+        r.cpy = js.copy + p * js.copy_pstride + ((size_t)(l / js.copy_alpha) * js.copy_E + l) * kN;
     return r;
 }
 
@@ -626,7 +628,9 @@ __global__ __launch_bounds__(kTileThreads) void k_ntt_inv_a(uint64_t* data, JobS
 //   out[2c+p][i] = (x_p P^-1 + add_p - T_p) q_{l-1}^-1,  x_p = sum_d ext[c][d][i] evk[d][p][i]  (the evk inner product),
 // add_0 = d0 = a0 b0 and add_1 = d1 = a0 b1 + a1 b0 formed from the product's inputs a, b [B][2][l][N], or read from
 // an addend [2B][..][N].  The same words as the NTT followed by k_mdr_combine_ks, without T's store and
-// reload.  A workgroup is two 256-thread groups, one per poly of ciphertext c, each transforming the same tile of its
+// reload.  With the inputs given, the extension's own-digit limbs 0..l-2 are not read (their producer need not store
+// them): the word of digit i / own_alpha at limb i, d2 = a1 b1 mod q_i, is formed here from the inputs the combine
+// reads anyway.  A workgroup is two 256-thread groups, one per poly of ciphertext c, each transforming the same tile of its
 // poly's limb i into an LDS tile of its own; then every thread finishes 8 words of the tile for both polys, so the
 // ext digits and the inputs are read once for the two.
 struct MdrFuse {
@@ -640,6 +644,7 @@ struct MdrFuse {
     uint32_t B, l, E, T;
     int64_t post;       // with has_post: added (mod q_i) to every poly 0 word of the output
     uint32_t has_post;
+    uint32_t own_alpha;  // with ta/tb: the digit size (limb i's own digit is i / own_alpha; its word is a1 b1)
     TwPair pmod[kMaxPmap];  // P mod q_i
     TwPair cfin[kMaxPmap];  // R P^-1 q_{l-1}^-1 mod q_i (R = 2^64), times the caller's factor
 };
@@ -665,17 +670,32 @@ struct MdrEpi {
     const MdrFuse& f;
     const PrimeInfo& P;
     uint32_t i, c, g;  // limb, ciphertext, the thread's group (= the poly whose tile it transformed)
+    uint32_t dn;       // kTa: the digit whose word is formed from the inputs (limb i's own), workgroup-uniform
 
     __device__ __forceinline__ void load(First& B, int blk, int rl, int k) const {
         const uint32_t bo = (256 * blk + rl + 16 * k) * 8;  // byte offset of the word within a limb
         const size_t li = (size_t)i * kN, xs = (size_t)f.E * kN, es = (size_t)f.T * kN, pw = (size_t)f.l * kN;
         const uint64_t* x = f.ext + (size_t)c * kD * f.E * kN + li;
         const uint64_t* e = f.evk + li;
+        if (kTa) {
+            // the kD - 1 stored digits in slots 0..kD-2 (slot j holds digit j + (j >= dn), a scalar index), the own
+            // digit's key in slot kD-1 (its word is formed from the inputs)
 #pragma unroll
-        for (int d = 0; d < kD; d++) {
-            B.xv[d] = ld_at(x + d * xs, bo);
-            B.e0[d] = ld_at(e + (2 * d) * es, bo);
-            B.e1[d] = ld_at(e + (2 * d + 1) * es, bo);
+            for (int j = 0; j + 1 < kD; j++) {
+                const uint32_t d = (uint32_t)j + ((uint32_t)j >= dn ? 1u : 0u);
+                B.xv[j] = ld_at(x + d * xs, bo);
+                B.e0[j] = ld_at(e + (2 * d) * es, bo);
+                B.e1[j] = ld_at(e + (2 * d + 1) * es, bo);
+            }
+            B.e0[kD - 1] = ld_at(e + (2 * dn) * es, bo);
+            B.e1[kD - 1] = ld_at(e + (2 * dn + 1) * es, bo);
+        } else {
+#pragma unroll
+            for (int d = 0; d < kD; d++) {
+                B.xv[d] = ld_at(x + d * xs, bo);
+                B.e0[d] = ld_at(e + (2 * d) * es, bo);
+                B.e1[d] = ld_at(e + (2 * d + 1) * es, bo);
+            }
         }
         if (kTa) {
             const uint64_t* a = f.ta + (size_t)c * 2 * pw + li;
@@ -719,6 +739,9 @@ struct MdrEpi {
 #pragma unroll
         for (int kk = 0; kk < 8; kk++) {
             const int k = 8 * g + kk;
+            // with the inputs: the own digit's word a1 b1 (slot kD-1), formed before the next word's loads are
+            // issued (their registers and the product's are not live together)
+            if (kTa) cur.xv[kD - 1] = mul_mod(cur.u1, cur.u3, Barrett{q, P.mu_hi, P.mu_lo});
             First nxt;
             if (kk < 7) load(nxt, blk, rl, k + 1);
             Acc s0, s1;
@@ -757,7 +780,8 @@ __global__ __launch_bounds__(2 * kTileThreads) __attribute__((amdgpu_waves_per_e
     const uint32_t i = uni_div(blockIdx.y, f.B), c = blockIdx.y - i * f.B;
     const uint32_t g = threadIdx.x >> 8, t = threadIdx.x & 255;
     const PrimeInfo& P = primes[i];
-    const MdrEpi<kD, kTa, kPost> epi{f, P, i, c, g};
+    const uint32_t dn = kTa ? uni_div(i, f.own_alpha) : (uint32_t)kD;
+    const MdrEpi<kD, kTa, kPost> epi{f, P, i, c, g, dn};
     uint64_t* a = T + ((size_t)(2 * c + g) * (f.l - 1) + i) * kN;
     const TwPair* tw = tw_all + (size_t)i * kN;
     if (P.q < kOpenMaxQ)
@@ -1134,8 +1158,9 @@ hipError_t launch_ntt(const Context& ctx, uint64_t* data, const JobSpec& js_in, 
     const TwPair* twb = inverse ? ctx.d_itwb : ctx.d_twb;
     // algorithmic bytes: every limb read and written once (plus the second factor read and the copy written), each
     // prime's table (w, w') read once
-    const double streams = 2.0 + (js.src2 ? 1.0 : 0.0) + (js.copy ? 1.0 : 0.0);
-    const double bytes = (double)n_jobs * streams * kN * 8 + (double)js.n_primes * kN * sizeof(TwPair);
+    const double streams = 2.0 + (js.src2 ? 1.0 : 0.0);
+    const double copied = js.copy ? (double)n_jobs - (double)js.n_polys * std::min(js.copy_from, js.period) : 0.0;
+    const double bytes = ((double)n_jobs * streams + copied) * kN * 8 + (double)js.n_primes * kN * sizeof(TwPair);
     const char* name = mode == NttMode::Fused ? (inverse ? "ntt_inv_fused" : "ntt_fwd_fused")
                                               : (inverse ? "ntt_inv_2pass" : "ntt_fwd_2pass");
     const int pi = prof_begin(ctx, name, bytes, st);
@@ -1360,13 +1385,15 @@ hipError_t launch_ntt_fwd_sub(const Context& ctx, uint64_t* y, const uint64_t* x
 // product of ext [B][D][E][N] and evk, add from ta/tb (the product's inputs) or add.  pmod[i] = P mod q_i and
 // cfin[i] = R P^-1 q_{l-1}^-1 mod q_i (R = 2^64), with Shoup companions, for limbs i < l-1 (primes below 2^60).  T is
 // left holding the first pass's intermediate.  Digit counts 1..4 (others: hipErrorInvalidValue, the caller runs the
-// two kernels).
+// two kernels).  own_from_inputs (required with ta, tb, and only then): ext's own-digit limbs 0..l-2 are not read;
+// each is d2 = a1 b1, formed from the inputs.
 hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint32_t l, const uint64_t* ext,
                               const uint64_t* evk, const uint64_t* ta, const uint64_t* tb, const uint64_t* add,
                               uint64_t add_pstride, uint64_t* out, const TwPair* pmod, const TwPair* cfin,
-                              hipStream_t st, const int64_t* post) {
+                              hipStream_t st, const int64_t* post, bool own_from_inputs) {
     const uint32_t D = (l + ctx.alpha - 1) / ctx.alpha, E = l + ctx.K;
-    if (l < 2 || l > kMaxPmap || B == 0 || D < 1 || D > 4 || (ta && (!tb || add)) || (!ta && !add))
+    if (l < 2 || l > kMaxPmap || B == 0 || D < 1 || D > 4 || (ta && (!tb || add)) || (!ta && !add) ||
+        own_from_inputs != (ta != nullptr) || ctx.alpha == 0)
         return hipErrorInvalidValue;
     JobSpec js{};
     js.n_polys = 2 * B;
@@ -1387,15 +1414,18 @@ hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint3
     f.T = ctx.L + ctx.K;
     f.has_post = post ? 1 : 0;
     f.post = post ? *post : 0;
+    f.own_alpha = own_from_inputs ? ctx.alpha : 0;
     for (uint32_t i = 0; i + 1 < l; i++) {
         if (ctx.moduli[i] >= (1ull << 60)) return hipErrorInvalidValue;  // the combine's sum bound
         f.pmod[i] = pmod[i];
         f.cfin[i] = cfin[i];
     }
     const uint32_t n_jobs = 2 * B * (l - 1);
-    // algorithmic bytes: T read and written by pass A, read by pass B; per ciphertext and limb D ext limbs, the
-    // 4 product inputs or 2 addend limbs, 2 outputs; the level's evk limbs and the twiddle tables once
-    const double limbs = (double)n_jobs * 3 + (double)B * (l - 1) * (D + (ta ? 4 : add ? 2 : 0) + 2) +
+    // algorithmic bytes: T read and written by pass A, read by pass B; per ciphertext and limb D ext limbs (D - 1
+    // when the own digit's word is formed from the inputs), the 4 product inputs or 2 addend limbs, 2 outputs; the
+    // level's evk limbs and the twiddle tables once
+    const double n_ext = own_from_inputs ? D - 1.0 : (double)D;
+    const double limbs = (double)n_jobs * 3 + (double)B * (l - 1) * (n_ext + (ta ? 4 : add ? 2 : 0) + 2) +
                          2.0 * D * (l - 1);
     const int pi = prof_begin(ctx, "ntt_fwd_mdr", limbs * kN * 8 + (double)(l - 1) * kN * sizeof(TwPair), st);
     hipLaunchKernelGGL(k_ntt_fwd_a, dim3(16, n_jobs), dim3(kTileThreads), 0, st, T, js, ctx.d_tw, ctx.d_primes);

@@ -63,7 +63,7 @@ hipError_t launch_ntt_fwd_lsub(const Context& ctx, uint64_t* y, uint32_t n_terms
 hipError_t launch_ntt_fwd_mdr(const Context& ctx, uint64_t* T, uint32_t B, uint32_t l, const uint64_t* ext,
                               const uint64_t* evk, const uint64_t* ta, const uint64_t* tb, const uint64_t* add,
                               uint64_t add_pstride, uint64_t* out, const TwPair* pmod, const TwPair* cfin,
-                              hipStream_t st, const int64_t* post = nullptr);
+                              hipStream_t st, const int64_t* post = nullptr, bool own_from_inputs = false);
 hipError_t launch_sub_scale(const Context& ctx, const uint64_t* x, uint64_t x_pstride, const uint64_t* y,
                             uint64_t y_pstride, const uint64_t* add, uint64_t add_pstride, uint32_t add_div,
                             uint64_t* out, uint64_t out_pstride, uint32_t n_polys, uint32_t l, const TwPair* s,
@@ -501,8 +501,10 @@ void moddown_inplace(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
 // forms limbs 0..l-2 itself from ext and evk.
 void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
                      hipStream_t st, const uint64_t* ext, const uint64_t* evk, const uint64_t* ta,
-                     const uint64_t* tb, bool x_from_ext, const Affine* aff) {
+                     const uint64_t* tb, bool x_from_ext, const Affine* aff, bool own_from_inputs) {
     if (aff && !ext) throw std::invalid_argument("an affine output needs a relinearization");
+    if (own_from_inputs && (!ext || !ta || ctx.ntt_mode != NttMode::TwoPass || num_digits(ctx, l) > 4))
+        throw std::logic_error("own-digit words from the inputs need the fused two-pass combine");
     check_level(ctx, l);
     if (l < 2) throw std::invalid_argument("rescale needs l >= 2");
     const uint32_t E = l + ctx.K, K = ctx.K;
@@ -562,7 +564,7 @@ void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, co
             cfin[i] = TwPair{v, shoup_companion(v, q)};
         }
         HIPX(launch_ntt_fwd_mdr(ctx, T, n_polys / 2, l, ext, evk, ta, tb, ta ? nullptr : add, (uint64_t)l * W, out,
-                                pmod_tab(ctx).data(), cfin.data(), st, aff ? &aff->post : nullptr));
+                                pmod_tab(ctx).data(), cfin.data(), st, aff ? &aff->post : nullptr, own_from_inputs));
         return;
     }
     HIPX(launch_ntt(ctx, T, regular_jobs(n_polys, pm), n_polys * (l - 1), false, ctx.ntt_mode, st));
@@ -737,10 +739,11 @@ void rescale_lincomb(Context& ctx, uint32_t B, uint32_t lo, uint32_t n_terms, co
 // each digit's own limbs of ext
 // ta, tb: the product's inputs when the tensor kernel wrote d0 and d1 for limb l-1 only (with the rescale)
 // x2c_coef: x2c already holds d2 in coefficient form (the inverse NTT formed it from the inputs)
+// own_from_inputs: ext's own-digit limbs hold d2 at limb l-1 only (the ModDown combine forms the others from ta, tb)
 static void relin_tail(Context& ctx, uint64_t* d01, uint64_t* x2c, uint64_t* ext, uint32_t B, uint32_t l,
                        const uint64_t* evk, uint64_t* out, bool do_rescale, hipStream_t st,
                        const uint64_t* ta = nullptr, const uint64_t* tb = nullptr, bool x2c_coef = false,
-                       const Affine* aff = nullptr) {
+                       const Affine* aff = nullptr, bool own_from_inputs = false) {
     if (aff && !do_rescale) throw std::invalid_argument("an affine output needs the rescale");
     const uint32_t E = l + ctx.K;
     uint64_t* acc = (uint64_t*)ws_get(ctx, WS_ACC, (size_t)B * 2 * E * W * 8);
@@ -757,9 +760,10 @@ static void relin_tail(Context& ctx, uint64_t* d01, uint64_t* x2c, uint64_t* ext
     // the fused NTT mode or more than 4 digits); the combine forms limbs 0..l-2
     if (ctx.ntt_mode == NttMode::TwoPass && num_digits(ctx, l) <= 4) {
         ctx.n_keyswitch += B;
-        moddown_rescale(ctx, acc, 2 * B, l, d01, out, st, ext, evk, ta, tb, true, aff);
+        moddown_rescale(ctx, acc, 2 * B, l, d01, out, st, ext, evk, ta, tb, true, aff, own_from_inputs);
         return;
     }
+    if (own_from_inputs) throw std::logic_error("own-digit words from the inputs need the fused two-pass combine");
     HIPX(launch_ks_inner(ctx, ext, evk, acc, B, l, st, l - 1));
     moddown_rescale(ctx, acc, 2 * B, l, d01, out, st, ext, evk, ta, tb, false, aff);
 }
@@ -781,6 +785,9 @@ void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint3
         return out < xe && x < oe;
     };
     const bool from_inputs = do_rescale && !overlaps(a) && !overlaps(b);
+    // with the fused two-pass combine, the digits' own limbs of d2 below l-1 are not stored either: the combine forms
+    // them as a1 b1 from the inputs it reads for d0 and d1 (limb l-1's is read by the P part's inner product)
+    const bool own = from_inputs && ctx.ntt_mode == NttMode::TwoPass && D <= 4;
     HIPX(launch_tensor(ctx, a, b, d01, nullptr, B, l, nullptr, 0, nullptr, st, from_inputs ? l - 1 : 0));
     std::vector<uint32_t> pm(l);
     for (uint32_t t = 0; t < l; t++) pm[t] = t;
@@ -792,9 +799,10 @@ void hmult(Context& ctx, const uint64_t* a, const uint64_t* b, uint32_t B, uint3
     js.copy_pstride = (uint64_t)D * E * W;
     js.copy_alpha = ctx.alpha;
     js.copy_E = E;
+    js.copy_from = own ? l - 1 : 0;
     HIPX(launch_ntt(ctx, x2c, js, B * l, true, ctx.ntt_mode, st));
     if (from_inputs)
-        relin_tail(ctx, d01, x2c, ext, B, l, evk, out, true, st, a, b, true, aff);
+        relin_tail(ctx, d01, x2c, ext, B, l, evk, out, true, st, a, b, true, aff, own);
     else
         relin_tail(ctx, d01, x2c, ext, B, l, evk, out, do_rescale, st, nullptr, nullptr, true, aff);
 }

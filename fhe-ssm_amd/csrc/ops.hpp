@@ -59,10 +59,12 @@ struct Affine {
     int64_t post;
 };
 // aff (optional, a relinearization with ext only): the output is factor * out + post (Affine)
+// own_from_inputs (with ta, tb, two-pass NTT mode, at most 4 digits): ext holds no own-digit words below limb l-1 (the
+// combine forms them as a1 b1)
 void moddown_rescale(Context& ctx, uint64_t* x, uint32_t n_polys, uint32_t l, const uint64_t* add, uint64_t* out,
                      hipStream_t st, const uint64_t* ext = nullptr, const uint64_t* evk = nullptr,
                      const uint64_t* ta = nullptr, const uint64_t* tb = nullptr, bool x_from_ext = false,
-                     const Affine* aff = nullptr);
+                     const Affine* aff = nullptr, bool own_from_inputs = false);
 void keyswitch(Context& ctx, const uint64_t* x, uint32_t B, uint32_t l, const uint64_t* evk, const uint64_t* add,
                uint64_t* out2, hipStream_t st, uint32_t add_div = 1, uint64_t x_bstride = 0);
 void rescale(Context& ctx, const uint64_t* in, uint32_t n_polys, uint32_t l, uint64_t* out, hipStream_t st);
