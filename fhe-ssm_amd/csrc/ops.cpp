@@ -391,7 +391,8 @@ static void check_level(const Context& ctx, uint32_t l) {
 
 // ------------------------------------------------------------------ ModUp
 // x2c: [B][l][N] coefficient form (INTT already applied) of the polynomial to extend;
-// ext: [B][D][E][N] whose digit-own limbs already hold the evaluation form.  Fills the rest.
+// ext: [B][D][E][N].  Fills every limb but the digits' own (neither read nor written here: the caller stores them in
+// evaluation form, or their consumer forms them).
 void modup_from_coef(Context& ctx, const uint64_t* x2c, uint64_t* ext, uint32_t B, uint32_t l, hipStream_t st) {
     const uint32_t D = num_digits(ctx, l), E = l + ctx.K, al = ctx.alpha;
     std::vector<Job> jobs;
