@@ -183,6 +183,38 @@ struct Acc30k {
         sm += (uint64_t)as * (b0 + b1);
     }
     __device__ __forceinline__ U128 get() const { return Acc30::combine30(s0, sm - s0 - s2, s2); }
+    // redc_lazy(get(), q, ninv) without the 128-bit sum in between: T = s0 + s1 2^30 + s2 2^60 (s1 = sm - s0 - s2)
+    // has low word lo = s0 + (s1 << 30) + (s2 << 60) and high word (s2 >> 4) + (s1 >> 34) + the two carries of lo;
+    // the carries go from one add straight into the next through VCC (in C each became a compare, a select, a zero
+    // extension and a 64-bit add).  REDC: (T + m q) / 2^64 = hi + hi(m q) + [lo != 0], m = lo (-q^-1) mod 2^64.
+    __device__ __forceinline__ uint64_t redc_lazy(uint64_t q, uint64_t ninv) const {
+        const uint64_t s1 = sm - s0 - s2;
+        const uint64_t sh = s1 << 30, h0 = s2 >> 4;
+        const uint32_t s1h = (uint32_t)(s1 >> 34), t = (uint32_t)s2 << 28;  // s2 2^60 touches the high word only
+        uint32_t lol, loh, hl, hh, a_hi;
+        asm("v_add_co_u32 %0, vcc, %5, %7\n\t"           // s0 + (s1 << 30): low word
+            "v_addc_co_u32 %4, vcc, %6, %8, vcc\n\t"     // its high word, carry c1
+            "v_addc_co_u32 %2, vcc, %9, %11, vcc\n\t"    // (s2 >> 4) + (s1 >> 34) + c1
+            "v_addc_co_u32_e64 %3, vcc, %10, 0, vcc\n\t"
+            "v_add_co_u32 %1, vcc, %4, %12\n\t"          // + (s2 << 60): high word only, carry c2
+            "v_addc_co_u32_e64 %2, vcc, %2, 0, vcc\n\t"  // + c2
+            "v_addc_co_u32_e64 %3, vcc, %3, 0, vcc"
+            : "=&v"(lol), "=&v"(loh), "=&v"(hl), "=&v"(hh), "=&v"(a_hi)
+            : "v"((uint32_t)s0), "v"((uint32_t)(s0 >> 32)), "v"((uint32_t)sh), "v"((uint32_t)(sh >> 32)),
+              "v"((uint32_t)h0), "v"((uint32_t)(h0 >> 32)), "v"(s1h), "v"(t)
+            : "vcc");
+        const uint64_t m = (((uint64_t)loh << 32) | lol) * ninv;
+        const uint64_t hq = mulhi64(m, q);
+        uint32_t rl, rh, nz;
+        asm("v_or_b32 %2, %3, %4\n\t"
+            "v_cmp_ne_u32 vcc, 0, %2\n\t"                // [lo != 0]
+            "v_addc_co_u32 %0, vcc, %5, %7, vcc\n\t"
+            "v_addc_co_u32 %1, vcc, %6, %8, vcc"
+            : "=&v"(rl), "=&v"(rh), "=&v"(nz)
+            : "v"(lol), "v"(loh), "v"(hl), "v"(hh), "v"((uint32_t)hq), "v"((uint32_t)(hq >> 32))
+            : "vcc");
+        return ((uint64_t)rh << 32) | rl;
+    }
 };
 
 }  // namespace fhe

@@ -263,21 +263,52 @@ __global__ __launch_bounds__(256) void k_bconv(const uint64_t* __restrict__ in, 
         // streamed: read once, by the next NTT (nontemporal, so the L2 keeps what is reused)
         __builtin_nontemporal_store(v, &dst[(size_t)desc_off(dj) * kN]);
     };
+    // Montgomery-reduced, not centered, at most 8 inputs (the ModUp and ModDown instances): each output's REDC is
+    // taken from its three Karatsuba sums directly (Acc30k::redc_lazy, the same word as through the 128-bit sum)
+    constexpr bool kFast = kMode == 1 && NIN <= 8;
+    auto terms = [&](uint32_t j, uint32_t j2, Acc30k& a, Acc30k& b) {
+#pragma unroll
+        for (int i = 0; i < (NIN < 8 ? NIN : 8); i++) {
+            a.add(y0[i], y1[i], ys[i], qhmod[(size_t)i * ba.n_out + j]);
+            b.add(y0[i], y1[i], ys[i], qhmod[(size_t)i * ba.n_out + j2]);
+        }
+    };
+    auto finish_fast = [&](const Acc30k& a, uint32_t j) {
+        const uint32_t dj = ba.out_desc[j];
+        const PrimeInfo& pj = primes[desc_prime(dj)];
+        // [0, 2q) (with the lift, as in finish)
+        uint64_t v = a.redc_lazy(pj.q, pj.mont_ninv);
+        if constexpr (kMdr) v += mb.fast_lift ? z + (zneg ? mb.dl[j] : 0) : lift_centered(z, ql, barrett_of(pj));
+        __builtin_nontemporal_store(v, &dst[(size_t)desc_off(dj) * kN]);
+    };
     // the outputs of this workgroup's share (grid z splits them when the batch is too small to fill the GPU), two
     // per iteration: independent accumulation chains for the scheduler to interleave
     const uint32_t share = ((n_main + gridDim.z - 1) / gridDim.z + 1) & ~1u;
     const uint32_t j_end = min(n_main, (blockIdx.z + 1) * share);
     uint32_t j = blockIdx.z * share;
     for (; j + 1 < j_end; j += 2) {
-        U128 r, r2;
-        sums(j, j + 1, r, r2);
-        finish(r, j);
-        finish(r2, j + 1);
+        if constexpr (kFast) {
+            Acc30k a, b;
+            terms(j, j + 1, a, b);
+            finish_fast(a, j);
+            finish_fast(b, j + 1);
+        } else {
+            U128 r, r2;
+            sums(j, j + 1, r, r2);
+            finish(r, j);
+            finish(r2, j + 1);
+        }
     }
     if (j < j_end) {
-        U128 r, unused;
-        sums(j, j, r, unused);
-        finish(r, j);
+        if constexpr (kFast) {
+            Acc30k a, b;
+            terms(j, j, a, b);
+            finish_fast(a, j);
+        } else {
+            U128 r, unused;
+            sums(j, j, r, unused);
+            finish(r, j);
+        }
     }
 }
 
