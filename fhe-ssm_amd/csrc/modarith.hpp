@@ -106,26 +106,35 @@ __device__ __forceinline__ void mac128(U128& acc, uint64_t a, uint64_t b) {
 __device__ __forceinline__ uint32_t uni_div(uint32_t a, uint32_t b) { return __builtin_amdgcn_readfirstlane(a / b); }
 
 // Lazy 128-bit multiply-accumulate for operands below 2^60 (every modulus of this engine is): the four 32 x 32
-// partial products go to separate 64-bit sums -- the low products to lo with a carry into hi, the two cross
-// products (< 2^60 each) to m, the high product (< 2^56) straight into hi -- so a term costs four
-// v_mad_u64_u32 and a carry, against ~30 instructions for a full 64 x 64 -> 128 product per term.
+// partial products go to separate 64-bit sums -- the low products to lo, the two cross products (< 2^60 each) to
+// m, the high product (< 2^56) straight into hi -- so a term costs four v_mad_u64_u32 and a carry, against ~30
+// instructions for a full 64 x 64 -> 128 product per term.  The carry out of lo is the carry-out the multiply-add
+// itself reports (its scalar destination), counted in c and added to hi at the fold; in C it had been a 64-bit
+// compare, a select, a zero extension and a 64-bit add per term.
 // m takes at most 8 terms (< 2^61 each) between folds: call fold() at least every 8 add()s.
 struct Acc {
     uint64_t lo, hi, m;
-    __device__ __forceinline__ Acc() : lo(0), hi(0), m(0) {}
+    uint32_t c;  // carries out of lo since the last fold
+    __device__ __forceinline__ Acc() : lo(0), hi(0), m(0), c(0) {}
     __device__ __forceinline__ void add(uint64_t a, uint64_t b) {
         const uint32_t a0 = (uint32_t)a, a1 = (uint32_t)(a >> 32);
         const uint32_t b0 = (uint32_t)b, b1 = (uint32_t)(b >> 32);
-        const uint64_t t = (uint64_t)a0 * b0;
-        lo += t;
-        hi += (uint64_t)a1 * b1 + (lo < t ? 1u : 0u);
-        m += (uint64_t)a0 * b1 + (uint64_t)a1 * b0;
+        uint64_t carry;  // the low product's carry-out (a scalar register pair)
+        asm("v_mad_u64_u32 %0, %4, %5, %7, %0\n\t"   // lo += a0 b0, carry out
+            "v_mad_u64_u32 %1, vcc, %6, %8, %1\n\t"  // hi += a1 b1
+            "v_mad_u64_u32 %2, vcc, %5, %8, %2\n\t"  // m += a0 b1
+            "v_mad_u64_u32 %2, vcc, %6, %7, %2\n\t"  // m += a1 b0
+            "v_addc_co_u32_e64 %3, vcc, 0, %3, %4"     // c += carry
+            : "+v"(lo), "+v"(hi), "+v"(m), "+v"(c), "=&s"(carry)
+            : "v"(a0), "v"(a1), "v"(b0), "v"(b1)
+            : "vcc");
     }
     __device__ __forceinline__ void fold() {
         const uint64_t s = m << 32;
         lo += s;
-        hi += (m >> 32) + (lo < s ? 1u : 0u);
+        hi += (m >> 32) + (lo < s ? 1u : 0u) + c;
         m = 0;
+        c = 0;
     }
     __device__ __forceinline__ U128 get() {
         fold();
