@@ -140,6 +140,36 @@ struct Acc {
         fold();
         return U128{lo, hi};
     }
+    // Montgomery's REDC (R = 2^64) of the sum, lazily: [0, 2q), the same value as redc_lazy(get(), q, ninv).  The
+    // fold's carries run through VCC from one add into the next: the low word's high half is lo_h + m_lo (carry c1),
+    // the high word hi + m_hi + c1 + c; then (T + m' q) / R = high + hi(m' q) + [low != 0], m' = low (-q^-1) mod R.
+    // Requires the sum below q R, as redc_lazy does.
+    __device__ __forceinline__ uint64_t redc_lazy(uint64_t q, uint64_t ninv) const {
+        uint32_t lh, hl, hh;
+        asm("v_add_co_u32 %0, vcc, %3, %5\n\t"
+            "v_addc_co_u32 %1, vcc, %4, %6, vcc\n\t"
+            "v_addc_co_u32_e64 %2, vcc, %7, 0, vcc\n\t"
+            "v_add_co_u32 %1, vcc, %1, %8\n\t"
+            "v_addc_co_u32_e64 %2, vcc, %2, 0, vcc"
+            : "=&v"(lh), "=&v"(hl), "=&v"(hh)
+            : "v"((uint32_t)(lo >> 32)), "v"((uint32_t)hi), "v"((uint32_t)m), "v"((uint32_t)(m >> 32)),
+              "v"((uint32_t)(hi >> 32)), "v"(c)
+            : "vcc");
+        const uint32_t ll = (uint32_t)lo;
+        const uint64_t mm = (((uint64_t)lh << 32) | ll) * ninv;
+        const uint64_t hq = mulhi64(mm, q);
+        uint32_t rl, rh, nz;
+        asm("v_or_b32 %2, %3, %4\n\t"
+            "v_cmp_ne_u32 vcc, 0, %2\n\t"
+            "v_addc_co_u32 %0, vcc, %5, %7, vcc\n\t"
+            "v_addc_co_u32 %1, vcc, %6, %8, vcc"
+            : "=&v"(rl), "=&v"(rh), "=&v"(nz)
+            : "v"(ll), "v"(lh), "v"(hl), "v"(hh), "v"((uint32_t)hq), "v"((uint32_t)(hq >> 32))
+            : "vcc");
+        return ((uint64_t)rh << 32) | rl;
+    }
+    // the canonical REDC: [0, q)
+    __device__ __forceinline__ uint64_t redc(uint64_t q, uint64_t ninv) const { return csub_s(redc_lazy(q, ninv), q); }
 };
 
 // Multiply-accumulate over 30-bit halves, for sums of at most 8 products of operands below 2^60: with

@@ -761,8 +761,9 @@ struct MdrEpi {
                 s0.add(cur.u0 + q - L0[rl + 17 * k], pm.w);  // P (add0 + q - T0)
                 s1.add(cur.u1 + q - L1[rl + 17 * k], pm.w);
             }
-            uint64_t v0 = shoup(redc(s0.get(), q, ninv), cf.w, cf.wp, q);
-            const uint64_t v1 = shoup(redc(s1.get(), q, ninv), cf.w, cf.wp, q);
+            // the Shoup product takes any word below 2^64 to [0, q): the REDC's [0, 2q) needs no subtraction first
+            uint64_t v0 = shoup(s0.redc_lazy(q, ninv), cf.w, cf.wp, q);
+            const uint64_t v1 = shoup(s1.redc_lazy(q, ninv), cf.w, cf.wp, q);
             if (kPost) v0 = add_mod(v0, post, q);
             const uint32_t bo = (256 * blk + rl + 16 * k) * 8;
             __builtin_nontemporal_store(v0, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out0) + bo));
@@ -876,8 +877,8 @@ struct KslEpi {
             }
             s0.add((f.add ? cur.u0 : 0) + q - L0[rl + 17 * k], pm);
             s1.add(q - L1[rl + 17 * k], pm);
-            const uint64_t v0 = shoup(redc(s0.get(), q, ninv), rp.w, rp.wp, q);
-            const uint64_t v1 = shoup(redc(s1.get(), q, ninv), rp.w, rp.wp, q);
+            const uint64_t v0 = shoup(s0.redc_lazy(q, ninv), rp.w, rp.wp, q);
+            const uint64_t v1 = shoup(s1.redc_lazy(q, ninv), rp.w, rp.wp, q);
             const uint32_t w = 256 * blk + rl + 16 * k;
             if (f.auto_on) {
                 // the automorphism: out[k'] = v[src(k')] with src(k') = brev((g (2 brev(k') + 1) mod 2N - 1) / 2), so
@@ -1041,7 +1042,7 @@ struct LinSubEpi {
 #pragma unroll
                 for (int t = 0; t < kLsubTerms; t++)
                     if (t < (int)n) acc.add(v[t][k], c[t]);
-                const uint64_t x = add_mod(redc(acc.get(), q, mont_ninv), addv, q);
+                const uint64_t x = add_mod(acc.redc(q, mont_ninv), addv, q);
                 const int kk = kG * h + k;
                 const uint64_t r = shoup(sub_mod(x, L[rl + 17 * kk], q), s.w, s.wp, q);
                 __builtin_nontemporal_store(r, reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(out) + bo + 128 * kk));

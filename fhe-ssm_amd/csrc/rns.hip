@@ -915,8 +915,8 @@ __global__ __launch_bounds__(kMacCoef* kMacRows) void k_bsgs_dh_mac(const uint64
                 if (ND >= 8) s0.fold();
                 s0.add(c0, primes[pi].pmod);
             }
-            v0 = redc(s0.get(), q, ninv);
-            v1 = redc(s1.get(), q, ninv);
+            v0 = s0.redc(q, ninv);
+            v1 = s1.redc(q, ninv);
         } else if (qlimb) {
             v0 = shoup(sx[0], a.pmod[t].w, a.pmod[t].wp, q);
             v1 = shoup(sx[(size_t)a.l * kN], a.pmod[t].w, a.pmod[t].wp, q);
@@ -1085,7 +1085,7 @@ __global__ __launch_bounds__(256) void k_lincomb(uint64_t* __restrict__ out, Lin
         if (t < (int)la.n_terms) acc.add(v[t], la.C[t][j]);
     // the coefficients carry a factor R = 2^64 (C R mod q_i), so the REDC of the sum is the combination itself;
     // at most 8 products of residues below q < 2^60 keep the sum below q R
-    uint64_t r = redc(acc.get(), br.q, primes[i].mont_ninv);
+    uint64_t r = acc.redc(br.q, primes[i].mont_ninv);
     if (la.has_add && p == 0) r = add_mod(r, la.add[j], br.q);
     __builtin_nontemporal_store(r, &out[((size_t)pc * la.l_out + j) * kN + k]);
 }
